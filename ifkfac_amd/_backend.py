@@ -1,0 +1,301 @@
+"""Tensor-level dispatch of the curvature path into the HIP library.
+
+Every function here takes torch tensors that live on a ROCm device, passes
+raw device pointers, sizes and the caller's current stream through the C ABI,
+and allocates outputs and workspaces with torch's caching allocator.  There
+is no second implementation: CPU tensors, a missing library or a failed call
+raise.
+
+``get_backend()`` returns the process-wide backend (the HIP one unless a test
+installed a double with ``set_backend``).
+"""
+from __future__ import annotations
+
+import math as _math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import IFK_BF16, IFK_F32, IFK_MATH_BF16, IFK_MATH_F32, IFKFACBackendError
+
+MATH_F32 = IFK_MATH_F32
+MATH_BF16 = IFK_MATH_BF16
+
+_DT = {torch.float32: IFK_F32, torch.bfloat16: IFK_BF16}
+_TORCH_DT = {IFK_F32: torch.float32, IFK_BF16: torch.bfloat16}
+
+
+def _require_device(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise IFKFACBackendError(
+            f"{what}: tensor is on {t.device}; the IFKFAC curvature kernels run only on a "
+            "ROCm GPU")
+
+
+def _mat(t: torch.Tensor, what: str) -> Tuple[torch.Tensor, int, int]:
+    """Return (t', ld, dtype code) with t' 2-D, row-major rows, fp32 or bf16."""
+    _require_device(t, what)
+    if t.dim() != 2:
+        raise IFKFACBackendError(f"{what}: expected a 2-D tensor, got shape {tuple(t.shape)}")
+    if t.dtype not in _DT:
+        t = t.float()
+    if t.stride(1) != 1 or (t.shape[0] > 1 and t.stride(0) < t.shape[1]):
+        t = t.contiguous()
+    ld = t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
+    return t, ld, _DT[t.dtype]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+class HipBackend:
+    """Dispatch to libifkfac_hip.so."""
+
+    name = "hip"
+
+    def __init__(self) -> None:
+        self.lib = _lib.load()
+
+    # -- plumbing --------------------------------------------------------------
+    @staticmethod
+    def _stream(dev: torch.device) -> int:
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    @staticmethod
+    def _ws(nbytes: int, dev: torch.device) -> torch.Tensor:
+        return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+
+    # -- streaming TSQR fold ---------------------------------------------------
+    def fold_(self, R: torch.Tensor, r_in: int, X: torch.Tensor, math: int) -> int:
+        """Fold chunk X (p x n) into R (n x n fp32 buffer, rows [0, r_in) valid) in place."""
+        _require_device(R, "tsqr_fold")
+        n = R.shape[1]
+        if R.dtype != torch.float32 or R.shape[0] != n or not R.is_contiguous():
+            raise IFKFACBackendError("tsqr_fold: R must be a contiguous n x n fp32 buffer")
+        X, ldx, xdt = _mat(X, "tsqr_fold")
+        if X.shape[1] != n:
+            raise IFKFACBackendError(f"tsqr_fold: chunk has {X.shape[1]} columns, R has {n}")
+        p = X.shape[0]
+        ws = self._ws(self.lib.ifk_tsqr_fold_workspace_size(p, n), R.device)
+        r_out = _lib.ctypes.c_int64(0)
+        with torch.cuda.device(R.device):
+            rc = self.lib.ifk_tsqr_fold(self._stream(R.device), _ptr(X), xdt, p, n, ldx, _ptr(R), n,
+                                        int(r_in), int(math), _ptr(ws), ws.numel(),
+                                        _lib.ctypes.byref(r_out))
+        _lib.check(rc, "ifk_tsqr_fold")
+        return int(r_out.value)
+
+    # -- damping / finalisation -------------------------------------------------
+    def finalize(self, R: torch.Tensor, scale: float, damping: float, out_dtype: torch.dtype,
+                 math: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Return (R_damped, finite flag int32[1]) for a square R."""
+        R, ldr, rdt = _mat(R, "finalize")
+        if rdt != IFK_F32:
+            R = R.float()
+            ldr = R.stride(0)
+        n = R.shape[1]
+        if R.shape[0] != n:
+            raise IFKFACBackendError("finalize: R must be square")
+        out = torch.empty((n, n), dtype=out_dtype, device=R.device)
+        flag = torch.empty(1, dtype=torch.int32, device=R.device)
+        ws = self._ws(self.lib.ifk_finalize_workspace_size(n), R.device)
+        with torch.cuda.device(R.device):
+            rc = self.lib.ifk_finalize(self._stream(R.device), _ptr(R), ldr, n, float(scale),
+                                       float(damping), _ptr(out), _DT[out_dtype], n, int(math),
+                                       _ptr(flag), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_finalize")
+        return out, flag
+
+    # -- preconditioning ------------------------------------------------------------
+    def tri_inverse(self, R: torch.Tensor, math: int) -> torch.Tensor:
+        R, ldr, rdt = _mat(R, "tri_inverse")
+        n = R.shape[0]
+        if R.shape[1] != n:
+            raise IFKFACBackendError("tri_inverse: R must be square")
+        Z = torch.empty((n, n), dtype=torch.float32, device=R.device)
+        ws = self._ws(self.lib.ifk_tri_inverse_workspace_size(n), R.device)
+        with torch.cuda.device(R.device):
+            rc = self.lib.ifk_tri_inverse(self._stream(R.device), _ptr(R), rdt, ldr, n, _ptr(Z), n,
+                                          int(math), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_tri_inverse")
+        return Z
+
+    def precondition(self, grad: torch.Tensor, R_X: torch.Tensor, R_G: torch.Tensor,
+                     math: int) -> torch.Tensor:
+        g, ldg, gdt = _mat(grad, "precondition")
+        if gdt != IFK_F32:
+            g = g.float()
+            ldg = g.stride(0)
+        RX, ldrx, xdt = _mat(R_X, "precondition")
+        RG, ldrg, gdt2 = _mat(R_G, "precondition")
+        if xdt != gdt2:
+            RX = RX.float()
+            RG = RG.float()
+            ldrx, ldrg, xdt = RX.stride(0), RG.stride(0), IFK_F32
+        n_out, n_in = g.shape
+        if RX.shape != (n_in, n_in) or RG.shape != (n_out, n_out):
+            raise IFKFACBackendError(
+                f"precondition: shapes grad {tuple(g.shape)}, R_X {tuple(RX.shape)}, "
+                f"R_G {tuple(RG.shape)} do not match")
+        nat = torch.empty((n_out, n_in), dtype=torch.float32, device=g.device)
+        ws = self._ws(self.lib.ifk_precondition_workspace_size(n_out, n_in, int(math)), g.device)
+        with torch.cuda.device(g.device):
+            rc = self.lib.ifk_precondition(self._stream(g.device), _ptr(g), n_out, n_in, ldg,
+                                           _ptr(RX), ldrx, _ptr(RG), ldrg, xdt, _ptr(nat), n_in,
+                                           int(math), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_precondition")
+        return nat
+
+    def precondition_apply(self, grad: torch.Tensor, Z_X: torch.Tensor, Z_G: torch.Tensor,
+                           math: int) -> torch.Tensor:
+        g, ldg, gdt = _mat(grad, "precondition_apply")
+        if gdt != IFK_F32:
+            g = g.float()
+            ldg = g.stride(0)
+        n_out, n_in = g.shape
+        ZX, ldzx, _ = _mat(Z_X, "precondition_apply")
+        ZG, ldzg, _ = _mat(Z_G, "precondition_apply")
+        if ZX.dtype != torch.float32 or ZG.dtype != torch.float32:
+            raise IFKFACBackendError("precondition_apply: inverses must be fp32")
+        if ZX.shape != (n_in, n_in) or ZG.shape != (n_out, n_out):
+            raise IFKFACBackendError("precondition_apply: shape mismatch")
+        nat = torch.empty((n_out, n_in), dtype=torch.float32, device=g.device)
+        ws = self._ws(self.lib.ifk_precondition_apply_workspace_size(n_out, n_in, int(math)),
+                      g.device)
+        with torch.cuda.device(g.device):
+            rc = self.lib.ifk_precondition_apply(self._stream(g.device), _ptr(g), n_out, n_in, ldg,
+                                                 _ptr(ZX), ldzx, _ptr(ZG), ldzg, _ptr(nat), n_in,
+                                                 int(math), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_precondition_apply")
+        return nat
+
+    def precondition_bias(self, g: torch.Tensor, Z_G: torch.Tensor) -> torch.Tensor:
+        _require_device(g, "precondition_bias")
+        gv = g.reshape(-1)
+        if gv.dtype != torch.float32:
+            gv = gv.float()
+        gv = gv.contiguous()
+        n_out = gv.numel()
+        ZG, ldzg, _ = _mat(Z_G, "precondition_bias")
+        if ZG.shape != (n_out, n_out) or ZG.dtype != torch.float32:
+            raise IFKFACBackendError("precondition_bias: shape/dtype mismatch")
+        out = torch.empty(n_out, dtype=torch.float32, device=gv.device)
+        ws = self._ws(self.lib.ifk_precondition_bias_workspace_size(n_out), gv.device)
+        with torch.cuda.device(gv.device):
+            rc = self.lib.ifk_precondition_bias(self._stream(gv.device), _ptr(gv), n_out, _ptr(ZG),
+                                                ldzg, _ptr(out), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_precondition_bias")
+        return out
+
+    def momentum_update_(self, nat: torch.Tensor, buf: Optional[torch.Tensor], W: torch.Tensor,
+                         lr: float, momentum: float, weight_decay: float, buf_init: bool) -> None:
+        _require_device(W, "momentum_update")
+        if W.dtype != torch.float32 or not W.is_contiguous():
+            raise IFKFACBackendError("momentum_update: W must be contiguous fp32")
+        natc = nat.reshape(W.shape)
+        if natc.dtype != torch.float32:
+            natc = natc.float()
+        natc = natc.contiguous()
+        if buf is not None and (buf.dtype != torch.float32 or not buf.is_contiguous()
+                                or buf.numel() != W.numel()):
+            raise IFKFACBackendError("momentum_update: buf must match W")
+        with torch.cuda.device(W.device):
+            rc = self.lib.ifk_momentum_update(self._stream(W.device), _ptr(natc), _ptr(buf),
+                                              _ptr(W), W.numel(), float(lr), float(momentum),
+                                              float(weight_decay), 1 if buf_init else 0)
+        _lib.check(rc, "ifk_momentum_update")
+
+    # -- bf16_linalg counterparts --------------------------------------------------
+    def geqrf_r(self, A: torch.Tensor, out_dtype: torch.dtype, math: int) -> torch.Tensor:
+        A, lda, adt = _mat(A, "geqrf_r")
+        m, n = A.shape
+        R = torch.empty((n, n), dtype=out_dtype, device=A.device)
+        ws = self._ws(self.lib.ifk_geqrf_r_workspace_size(m, n), A.device)
+        with torch.cuda.device(A.device):
+            rc = self.lib.ifk_geqrf_r(self._stream(A.device), _ptr(A), adt, m, n, lda, _ptr(R),
+                                      _DT[out_dtype], n, int(math), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_geqrf_r")
+        return R
+
+    def trsm(self, R: torch.Tensor, B: torch.Tensor, upper: bool, out_dtype: torch.dtype,
+             math: int) -> torch.Tensor:
+        R, ldr, rdt = _mat(R, "trsm")
+        B, ldb, bdt = _mat(B, "trsm")
+        n, k = B.shape
+        X = torch.empty((n, k), dtype=out_dtype, device=B.device)
+        ws = self._ws(self.lib.ifk_trsm_workspace_size(n, k), B.device)
+        with torch.cuda.device(B.device):
+            rc = self.lib.ifk_trsm(self._stream(B.device), _ptr(R), rdt, n, ldr, 1 if upper else 0,
+                                   _ptr(B), bdt, k, ldb, _ptr(X), _DT[out_dtype], max(k, 1),
+                                   int(math), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_trsm")
+        return X
+
+    def potrf(self, A: torch.Tensor, out_dtype: torch.dtype, math: int) -> torch.Tensor:
+        A, lda, adt = _mat(A, "potrf")
+        n = A.shape[0]
+        L = torch.empty((n, n), dtype=out_dtype, device=A.device)
+        ws = self._ws(self.lib.ifk_potrf_workspace_size(n), A.device)
+        with torch.cuda.device(A.device):
+            rc = self.lib.ifk_potrf(self._stream(A.device), _ptr(A), adt, n, lda, _ptr(L),
+                                    _DT[out_dtype], n, int(math), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_potrf")
+        return L
+
+    def inv_spd(self, A: torch.Tensor, out_dtype: torch.dtype, math: int) -> torch.Tensor:
+        A, lda, adt = _mat(A, "inv_spd")
+        n = A.shape[0]
+        X = torch.empty((n, n), dtype=out_dtype, device=A.device)
+        ws = self._ws(self.lib.ifk_inv_spd_workspace_size(n), A.device)
+        with torch.cuda.device(A.device):
+            rc = self.lib.ifk_inv_spd(self._stream(A.device), _ptr(A), adt, n, lda, _ptr(X),
+                                      _DT[out_dtype], n, int(math), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_inv_spd")
+        return X
+
+    def gemm(self, A: torch.Tensor, B: torch.Tensor, trans_a: bool = False,
+             trans_b: bool = False, math: int = MATH_F32, alpha: float = 1.0,
+             beta: float = 0.0, C: Optional[torch.Tensor] = None) -> torch.Tensor:
+        A, lda, adt = _mat(A, "gemm")
+        B, ldb, bdt = _mat(B, "gemm")
+        m = A.shape[1] if trans_a else A.shape[0]
+        k = A.shape[0] if trans_a else A.shape[1]
+        kb = B.shape[1] if trans_b else B.shape[0]
+        n = B.shape[0] if trans_b else B.shape[1]
+        if k != kb:
+            raise IFKFACBackendError("gemm: inner dimensions differ")
+        if C is None:
+            C = torch.zeros((m, n), dtype=torch.float32, device=A.device)
+        ws = self._ws(self.lib.ifk_gemm_workspace_size(m, n), A.device)
+        with torch.cuda.device(A.device):
+            rc = self.lib.ifk_gemm(self._stream(A.device), int(math), m, n, k, float(alpha),
+                                   _ptr(A), adt, lda, int(trans_a), _ptr(B), bdt, ldb,
+                                   int(trans_b), float(beta), _ptr(C), C.stride(0), _ptr(ws),
+                                   ws.numel())
+        _lib.check(rc, "ifk_gemm")
+        return C
+
+
+_BACKEND = None
+
+
+def get_backend():
+    """The active backend; loads the HIP library on first use."""
+    global _BACKEND
+    if _BACKEND is None:
+        _BACKEND = HipBackend()
+    return _BACKEND
+
+
+def set_backend(backend):
+    """Install another backend object (test doubles); returns the previous one."""
+    global _BACKEND
+    prev = _BACKEND
+    _BACKEND = backend
+    return prev
+
+
+def inv_sqrt(rows: int) -> float:
+    return 1.0 / _math.sqrt(rows)

@@ -1,0 +1,206 @@
+// extern "C" entry points declared in include/ifkfac_hip.h.  Each validates
+// what the kernels assume about shapes before anything is launched, and maps
+// every failure to a status code plus a thread-local message.
+#include "../../include/ifkfac_hip.h"
+
+#include <string>
+
+#include "gemm.h"
+#include "kernels.h"
+#include "linalg.h"
+
+namespace ifk {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string& msg) { g_err = msg; }
+const char* get_error() { return g_err.c_str(); }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    return IFK_ERR_HIP;
+  }
+  return IFK_OK;
+}
+
+static bool dt_ok(int dt) { return dt == DT_F32 || dt == DT_BF16; }
+static bool math_ok(int m) { return m == MATH_F32 || m == MATH_BF16; }
+
+}  // namespace ifk
+
+using namespace ifk;
+
+#define GUARD(cond, msg)            \
+  do {                              \
+    if (!(cond)) {                  \
+      set_error(msg);               \
+      return IFK_ERR_INVALID;       \
+    }                               \
+  } while (0)
+
+extern "C" {
+
+int ifk_abi_version(void) { return 1; }
+
+const char* ifk_last_error(void) { return get_error(); }
+
+size_t ifk_tsqr_fold_workspace_size(int64_t p, int64_t n) {
+  if (p < 0 || n < 1) return 0;
+  return fold_ws(p, n);
+}
+
+int ifk_tsqr_fold(void* stream, const void* X, int x_dtype, int64_t p, int64_t n, int64_t ldx,
+                  float* R, int64_t ldr, int64_t r_in, int math, void* workspace,
+                  size_t workspace_bytes, int64_t* r_out) {
+  GUARD(dt_ok(x_dtype) && math_ok(math), "tsqr_fold: bad dtype or math code");
+  return fold((hipStream_t)stream, X, x_dtype, p, n, ldx, R, ldr, r_in, math, workspace,
+              workspace_bytes, r_out);
+}
+
+size_t ifk_finalize_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return finalize_ws(n);
+}
+
+int ifk_finalize(void* stream, const float* R_in, int64_t ldr_in, int64_t n, float scale,
+                 float damping, void* out, int out_dtype, int64_t ldo, int math, int32_t* finite,
+                 void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(out_dtype) && math_ok(math), "finalize: bad dtype or math code");
+  return finalize((hipStream_t)stream, R_in, ldr_in, n, scale, damping, out, out_dtype, ldo, math,
+                  finite, workspace, workspace_bytes);
+}
+
+size_t ifk_tri_inverse_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return trinv_ws(n);
+}
+
+int ifk_tri_inverse(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n, float* Z,
+                    int64_t ldz, int math, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(r_dtype) && math_ok(math), "tri_inverse: bad dtype or math code");
+  return trinv((hipStream_t)stream, R, r_dtype, ldr, n, Z, ldz, math, 0, workspace,
+               workspace_bytes);
+}
+
+size_t ifk_precondition_workspace_size(int64_t n_out, int64_t n_in, int math) {
+  if (n_out < 1 || n_in < 1 || !math_ok(math)) return 0;
+  return precondition_ws(n_out, n_in, math);
+}
+
+int ifk_precondition(void* stream, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,
+                     const void* R_X, int64_t ldrx, const void* R_G, int64_t ldrg, int r_dtype,
+                     float* nat, int64_t ldn, int math, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(r_dtype) && math_ok(math), "precondition: bad dtype or math code");
+  return precondition((hipStream_t)stream, grad, n_out, n_in, ldg, R_X, ldrx, R_G, ldrg, r_dtype,
+                      nat, ldn, math, workspace, workspace_bytes);
+}
+
+size_t ifk_precondition_apply_workspace_size(int64_t n_out, int64_t n_in, int math) {
+  if (n_out < 1 || n_in < 1 || !math_ok(math)) return 0;
+  return precondition_apply_ws(n_out, n_in, math);
+}
+
+int ifk_precondition_apply(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                           int64_t ldg, const float* Z_X, int64_t ldzx, const float* Z_G,
+                           int64_t ldzg, float* nat, int64_t ldn, int math, void* workspace,
+                           size_t workspace_bytes) {
+  GUARD(math_ok(math), "precondition_apply: bad math code");
+  return precondition_apply((hipStream_t)stream, grad, n_out, n_in, ldg, Z_X, ldzx, Z_G, ldzg, nat,
+                            ldn, math, workspace, workspace_bytes);
+}
+
+size_t ifk_precondition_bias_workspace_size(int64_t n_out) {
+  if (n_out < 1) return 0;
+  return precondition_bias_ws(n_out);
+}
+
+int ifk_precondition_bias(void* stream, const float* g, int64_t n_out, const float* Z_G,
+                          int64_t ldzg, float* out, void* workspace, size_t workspace_bytes) {
+  return precondition_bias((hipStream_t)stream, g, n_out, Z_G, ldzg, out, workspace,
+                           workspace_bytes);
+}
+
+int ifk_momentum_update(void* stream, const float* nat, float* buf, float* W, int64_t numel,
+                        float lr, float momentum, float weight_decay, int buf_init) {
+  GUARD(numel >= 0, "momentum_update: negative size");
+  GUARD(numel == 0 || (nat && W), "momentum_update: null pointer");
+  return launch_momentum_update((hipStream_t)stream, nat, buf, W, numel, lr, momentum,
+                                weight_decay, buf_init);
+}
+
+size_t ifk_geqrf_r_workspace_size(int64_t m, int64_t n) {
+  if (m < n || n < 1) return 0;
+  return geqrf_r_ws(m, n);
+}
+
+int ifk_geqrf_r(void* stream, const void* A, int a_dtype, int64_t m, int64_t n, int64_t lda,
+                void* R, int r_dtype, int64_t ldr, int math, void* workspace,
+                size_t workspace_bytes) {
+  GUARD(dt_ok(a_dtype) && dt_ok(r_dtype) && math_ok(math), "geqrf_r: bad dtype or math code");
+  return geqrf_r((hipStream_t)stream, A, a_dtype, m, n, lda, R, r_dtype, ldr, math, workspace,
+                 workspace_bytes);
+}
+
+size_t ifk_trsm_workspace_size(int64_t n, int64_t k) {
+  if (n < 1 || k < 0) return 0;
+  return trsm_ws(n, k);
+}
+
+int ifk_trsm(void* stream, const void* R, int r_dtype, int64_t n, int64_t ldr, int upper,
+             const void* B, int b_dtype, int64_t k, int64_t ldb, void* X, int x_dtype, int64_t ldx,
+             int math, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(r_dtype) && dt_ok(b_dtype) && dt_ok(x_dtype) && math_ok(math),
+        "trsm: bad dtype or math code");
+  return trsm((hipStream_t)stream, R, r_dtype, n, ldr, upper, B, b_dtype, k, ldb, X, x_dtype, ldx,
+              math, workspace, workspace_bytes);
+}
+
+size_t ifk_potrf_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return potrf_ws(n);
+}
+
+int ifk_potrf(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda, void* L,
+              int l_dtype, int64_t ldl, int math, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(a_dtype) && dt_ok(l_dtype) && math_ok(math), "potrf: bad dtype or math code");
+  return potrf((hipStream_t)stream, A, a_dtype, n, lda, L, l_dtype, ldl, math, workspace,
+               workspace_bytes);
+}
+
+size_t ifk_inv_spd_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return inv_spd_ws(n);
+}
+
+int ifk_inv_spd(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda, void* X,
+                int x_dtype, int64_t ldx, int math, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(a_dtype) && dt_ok(x_dtype) && math_ok(math), "inv_spd: bad dtype or math code");
+  return inv_spd((hipStream_t)stream, A, a_dtype, n, lda, X, x_dtype, ldx, math, workspace,
+                 workspace_bytes);
+}
+
+size_t ifk_gemm_workspace_size(int64_t m, int64_t n) {
+  if (m < 1 || n < 1) return 0;
+  size_t f = (size_t)m * n * 64;
+  if (f > ((size_t)16 << 20)) f = (size_t)16 << 20;
+  return f * sizeof(float);
+}
+
+int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alpha, const void* A,
+             int a_dtype, int64_t lda, int trans_a, const void* B, int b_dtype, int64_t ldb,
+             int trans_b, float beta, float* C, int64_t ldc, void* workspace,
+             size_t workspace_bytes) {
+  GUARD(dt_ok(a_dtype) && dt_ok(b_dtype) && math_ok(math), "gemm: bad dtype or math code");
+  GUARD(m >= 0 && n >= 0 && k >= 0, "gemm: negative size");
+  GUARD(ldc >= n && (trans_a ? lda >= m : lda >= k) && (trans_b ? ldb >= k : ldb >= n),
+        "gemm: leading dimension too small");
+  GUARD((m == 0 || n == 0) || (C && (k == 0 || (A && B))), "gemm: null pointer");
+  const MatRef a = trans_a ? A_t(A, a_dtype, lda) : A_n(A, a_dtype, lda);
+  const MatRef b = trans_b ? B_t(B, b_dtype, ldb) : B_n(B, b_dtype, ldb);
+  SplitScratch sp{(float*)workspace, workspace ? workspace_bytes / sizeof(float) : 0};
+  return gemm((hipStream_t)stream, math, m, n, k, alpha, a, b, beta, out_f32(C, ldc), 1, sp);
+}
+
+}  // extern "C"

@@ -1,0 +1,329 @@
+// HBM-bound elementwise kernels: operand staging, masking, casts and the fused
+// momentum / weight update.  Grid-stride loops over 256-thread blocks.
+#include "kernels.h"
+
+namespace ifk {
+
+static inline unsigned grid_for(int64_t n) {
+  int64_t g = cdiv(n, 256);
+  if (g > 8192) g = 8192;
+  if (g < 1) g = 1;
+  return (unsigned)g;
+}
+
+template <int DT>
+__global__ void copy_to_f32_kernel(const void* src, int64_t lds, int64_t rows, int64_t cols,
+                                   float scale, float* dst, int64_t ldd) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e % cols;
+    dst[r * ldd + c] =
+        scale * Elem<DT>::load((const typename Elem<DT>::T*)src + r * lds + c);
+  }
+}
+
+int launch_copy_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
+                       int64_t cols, float scale, float* dst, int64_t ldd) {
+  if (rows * cols == 0) return IFK_OK;
+  if (sdt == DT_F32)
+    hipLaunchKernelGGL(copy_to_f32_kernel<DT_F32>, dim3(grid_for(rows * cols)), dim3(256), 0, s,
+                       src, lds, rows, cols, scale, dst, ldd);
+  else
+    hipLaunchKernelGGL(copy_to_f32_kernel<DT_BF16>, dim3(grid_for(rows * cols)), dim3(256), 0, s,
+                       src, lds, rows, cols, scale, dst, ldd);
+  return check_launch("copy_to_f32");
+}
+
+__global__ void copy_upper_kernel(const float* src, int64_t lds, int64_t n, float scale,
+                                  float* dst, int64_t ldd) {
+  const int64_t total = n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / n, c = e % n;
+    dst[r * ldd + c] = (c >= r) ? scale * src[r * lds + c] : 0.0f;
+  }
+}
+
+int launch_copy_upper(hipStream_t s, const float* src, int64_t lds, int64_t n, float scale,
+                      float* dst, int64_t ldd) {
+  if (n == 0) return IFK_OK;
+  hipLaunchKernelGGL(copy_upper_kernel, dim3(grid_for(n * n)), dim3(256), 0, s, src, lds, n, scale,
+                     dst, ldd);
+  return check_launch("copy_upper");
+}
+
+__global__ void set_diag_kernel(float* dst, int64_t ldd, int64_t n, float value) {
+  const int64_t total = n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / n, c = e % n;
+    dst[r * ldd + c] = (r == c) ? value : 0.0f;
+  }
+}
+
+int launch_set_diag(hipStream_t s, float* dst, int64_t ldd, int64_t n, float value) {
+  if (n == 0) return IFK_OK;
+  hipLaunchKernelGGL(set_diag_kernel, dim3(grid_for(n * n)), dim3(256), 0, s, dst, ldd, n, value);
+  return check_launch("set_diag");
+}
+
+__global__ void zero_block_kernel(float* dst, int64_t ldd, int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e % cols;
+    dst[r * ldd + c] = 0.0f;
+  }
+}
+
+int launch_zero_rows(hipStream_t s, float* dst, int64_t ldd, int64_t r0, int64_t r1,
+                     int64_t cols) {
+  if (r1 <= r0 || cols == 0) return IFK_OK;
+  hipLaunchKernelGGL(zero_block_kernel, dim3(grid_for((r1 - r0) * cols)), dim3(256), 0, s,
+                     dst + r0 * ldd, ldd, r1 - r0, cols);
+  return check_launch("zero_rows");
+}
+
+int launch_zero(hipStream_t s, float* dst, int64_t ldd, int64_t rows, int64_t cols) {
+  if (rows * cols == 0) return IFK_OK;
+  hipLaunchKernelGGL(zero_block_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, s, dst, ldd,
+                     rows, cols);
+  return check_launch("zero");
+}
+
+__global__ void sub_inplace_kernel(float* dst, int64_t ldd, const float* src, int64_t lds,
+                                   int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e % cols;
+    dst[r * ldd + c] -= src[r * lds + c];
+  }
+}
+
+int launch_sub_inplace(hipStream_t s, float* dst, int64_t ldd, const float* src, int64_t lds,
+                       int64_t rows, int64_t cols) {
+  if (rows * cols == 0) return IFK_OK;
+  hipLaunchKernelGGL(sub_inplace_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, s, dst, ldd,
+                     src, lds, rows, cols);
+  return check_launch("sub_inplace");
+}
+
+// One block per row (row-stride loop): read the diagonal, flip the row when
+// it is negative.  Matches _positive_diagonal_R: sign 0 counts as +1.
+__global__ void sign_normalize_kernel(float* R, int64_t ldr, int64_t r, int64_t n) {
+  for (int64_t row = blockIdx.x; row < r; row += gridDim.x) {
+    const float d = R[row * ldr + row];
+    if (d < 0.0f) {
+      for (int64_t c = threadIdx.x; c < n; c += blockDim.x) R[row * ldr + c] = -R[row * ldr + c];
+    }
+  }
+}
+
+int launch_sign_normalize(hipStream_t s, float* R, int64_t ldr, int64_t r, int64_t n) {
+  if (r == 0) return IFK_OK;
+  unsigned g = (unsigned)(r < 8192 ? r : 8192);
+  hipLaunchKernelGGL(sign_normalize_kernel, dim3(g), dim3(256), 0, s, R, ldr, r, n);
+  return check_launch("sign_normalize");
+}
+
+template <int ODT>
+__global__ void cast_upper_kernel(const float* R, int64_t ldr, int64_t n, void* out, int64_t ldo,
+                                  int* finite) {
+  const int64_t total = n * n;
+  bool ok = true;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / n, c = e % n;
+    const float v = (c >= r) ? R[r * ldr + c] : 0.0f;
+    ok = ok && isfinite(v);
+    if constexpr (ODT == DT_F32) ((float*)out)[r * ldo + c] = v;
+    else ((bf16_t*)out)[r * ldo + c] = f32_to_bf16(v);
+  }
+  if (finite && !ok) atomicAnd(finite, 0);
+}
+
+int launch_cast_upper(hipStream_t s, const float* R, int64_t ldr, int64_t n, void* out, int odt,
+                      int64_t ldo, int* finite) {
+  if (n == 0) return IFK_OK;
+  if (odt == DT_F32)
+    hipLaunchKernelGGL(cast_upper_kernel<DT_F32>, dim3(grid_for(n * n)), dim3(256), 0, s, R, ldr, n,
+                       out, ldo, finite);
+  else
+    hipLaunchKernelGGL(cast_upper_kernel<DT_BF16>, dim3(grid_for(n * n)), dim3(256), 0, s, R, ldr,
+                       n, out, ldo, finite);
+  return check_launch("cast_upper");
+}
+
+template <int ODT>
+__global__ void cast_kernel(const float* src, int64_t lds, int64_t rows, int64_t cols, void* out,
+                            int64_t ldo) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e % cols;
+    const float v = src[r * lds + c];
+    if constexpr (ODT == DT_F32) ((float*)out)[r * ldo + c] = v;
+    else ((bf16_t*)out)[r * ldo + c] = f32_to_bf16(v);
+  }
+}
+
+int launch_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols, void* out,
+                int odt, int64_t ldo) {
+  if (rows * cols == 0) return IFK_OK;
+  if (odt == DT_F32)
+    hipLaunchKernelGGL(cast_kernel<DT_F32>, dim3(grid_for(rows * cols)), dim3(256), 0, s, src, lds,
+                       rows, cols, out, ldo);
+  else
+    hipLaunchKernelGGL(cast_kernel<DT_BF16>, dim3(grid_for(rows * cols)), dim3(256), 0, s, src, lds,
+                       rows, cols, out, ldo);
+  return check_launch("cast");
+}
+
+__global__ void fill_int_kernel(int* p, int value, int count) {
+  for (int i = threadIdx.x; i < count; i += blockDim.x) p[i] = value;
+}
+
+int launch_fill_int(hipStream_t s, int* p, int value, int count) {
+  if (count <= 0) return IFK_OK;
+  hipLaunchKernelGGL(fill_int_kernel, dim3(1), dim3(64), 0, s, p, value, count);
+  return check_launch("fill_int");
+}
+
+// buf <- (buf_init ? nat : momentum * buf + nat)   [ifkfac.py:404-406]
+// W   <- W * (1 - lr * wd) - lr * buf               [ifkfac.py:411-413]
+// momentum == 0 uses nat directly and leaves buf untouched (buf may be null).
+// 16 bytes per lane per access: float4 body, scalar tail.
+__global__ void momentum_update_kernel(const float* __restrict__ nat, float* __restrict__ buf,
+                                       float* __restrict__ W, int64_t numel, float lr,
+                                       float momentum, float wd_scale, int buf_init, int use_buf,
+                                       int vec) {
+  const int64_t n4 = vec ? numel / 4 : 0;
+  const float4* nat4 = (const float4*)nat;
+  float4* buf4 = (float4*)buf;
+  float4* W4 = (float4*)W;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float4 g = nat4[i];
+    float4 d = g;
+    if (use_buf) {
+      if (buf_init) {
+        // zeros_like(nat).mul_(momentum).add_(nat): keeps torch's +0 for -0 inputs
+        const float z = 0.0f * momentum;
+        d.x = z + g.x; d.y = z + g.y; d.z = z + g.z; d.w = z + g.w;
+      } else {
+        const float4 b = buf4[i];
+        d.x = momentum * b.x + g.x;
+        d.y = momentum * b.y + g.y;
+        d.z = momentum * b.z + g.z;
+        d.w = momentum * b.w + g.w;
+      }
+      buf4[i] = d;
+    }
+    float4 w = W4[i];
+    w.x = w.x * wd_scale - lr * d.x;
+    w.y = w.y * wd_scale - lr * d.y;
+    w.z = w.z * wd_scale - lr * d.z;
+    w.w = w.w * wd_scale - lr * d.w;
+    W4[i] = w;
+  }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < numel;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float d = nat[i];
+    if (use_buf) {
+      d = (buf_init ? 0.0f * momentum : momentum * buf[i]) + d;
+      buf[i] = d;
+    }
+    W[i] = W[i] * wd_scale - lr * d;
+  }
+}
+
+int launch_momentum_update(hipStream_t s, const float* nat, float* buf, float* W, int64_t numel,
+                           float lr, float momentum, float weight_decay, int buf_init) {
+  if (numel == 0) return IFK_OK;
+  const int use_buf = momentum > 0.0f ? 1 : 0;
+  if (use_buf && !buf) {
+    set_error("momentum_update: momentum > 0 needs a buffer");
+    return IFK_ERR_INVALID;
+  }
+  const int vec = (((uintptr_t)nat | (uintptr_t)W | (uintptr_t)(use_buf ? buf : W)) % 16 == 0);
+  const float wd_scale = weight_decay > 0.0f ? 1.0f - lr * weight_decay : 1.0f;
+  unsigned g = grid_for(cdiv(numel, 4));
+  if (g > 2048) g = 2048;
+  hipLaunchKernelGGL(momentum_update_kernel, dim3(g), dim3(256), 0, s, nat, buf, W, numel, lr,
+                     momentum, wd_scale, buf_init, use_buf, vec);
+  return check_launch("momentum_update");
+}
+
+template <int ODT>
+__global__ void scale_copy_vec_kernel(const float* x, int64_t n, float alpha, void* out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = alpha * x[i];
+    if constexpr (ODT == DT_F32) ((float*)out)[i] = v;
+    else ((bf16_t*)out)[i] = f32_to_bf16(v);
+  }
+}
+
+int launch_scale_copy_vec(hipStream_t s, const float* x, int64_t n, float alpha, void* out,
+                          int odt) {
+  if (n == 0) return IFK_OK;
+  if (odt == DT_F32)
+    hipLaunchKernelGGL(scale_copy_vec_kernel<DT_F32>, dim3(grid_for(n)), dim3(256), 0, s, x, n,
+                       alpha, out);
+  else
+    hipLaunchKernelGGL(scale_copy_vec_kernel<DT_BF16>, dim3(grid_for(n)), dim3(256), 0, s, x, n,
+                       alpha, out);
+  return check_launch("scale_copy_vec");
+}
+
+template <int DT>
+__global__ void transpose_to_f32_kernel(const void* src, int64_t lds, int64_t rows, int64_t cols,
+                                        float* dst, int64_t ldd) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t c = e / rows, r = e % rows;  // dst row c, dst col r
+    dst[c * ldd + r] = Elem<DT>::load((const typename Elem<DT>::T*)src + r * lds + c);
+  }
+}
+
+int launch_transpose_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
+                            int64_t cols, float* dst, int64_t ldd) {
+  if (rows * cols == 0) return IFK_OK;
+  if (sdt == DT_F32)
+    hipLaunchKernelGGL(transpose_to_f32_kernel<DT_F32>, dim3(grid_for(rows * cols)), dim3(256), 0,
+                       s, src, lds, rows, cols, dst, ldd);
+  else
+    hipLaunchKernelGGL(transpose_to_f32_kernel<DT_BF16>, dim3(grid_for(rows * cols)), dim3(256), 0,
+                       s, src, lds, rows, cols, dst, ldd);
+  return check_launch("transpose_to_f32");
+}
+
+template <int ODT>
+__global__ void transpose_upper_kernel(const float* src, int64_t lds, int64_t n, void* out,
+                                       int64_t ldo) {
+  const int64_t total = n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / n, j = e % n;
+    const float v = (j <= i) ? src[j * lds + i] : 0.0f;
+    if constexpr (ODT == DT_F32) ((float*)out)[i * ldo + j] = v;
+    else ((bf16_t*)out)[i * ldo + j] = f32_to_bf16(v);
+  }
+}
+
+int launch_transpose_upper(hipStream_t s, const float* src, int64_t lds, int64_t n, void* out,
+                           int odt, int64_t ldo) {
+  if (n == 0) return IFK_OK;
+  if (odt == DT_F32)
+    hipLaunchKernelGGL(transpose_upper_kernel<DT_F32>, dim3(grid_for(n * n)), dim3(256), 0, s, src,
+                       lds, n, out, ldo);
+  else
+    hipLaunchKernelGGL(transpose_upper_kernel<DT_BF16>, dim3(grid_for(n * n)), dim3(256), 0, s, src,
+                       lds, n, out, ldo);
+  return check_launch("transpose_upper");
+}
+
+}  // namespace ifk

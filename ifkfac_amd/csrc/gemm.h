@@ -1,0 +1,68 @@
+// MFMA GEMM engine for gfx950: C = alpha * op(A) * op(B) + beta * C.
+//
+// op(A) is M x K and op(B) is K x N.  Each operand is described by where its
+// K index runs in memory:
+//   A.kc = true : op(A)[m][k] = A[m * ld + k]   (A stored M x K row-major)
+//   A.kc = false: op(A)[m][k] = A[k * ld + m]   (A stored K x M, used transposed)
+//   B.kc = true : op(B)[k][n] = B[n * ld + k]   (B stored N x K, used transposed)
+//   B.kc = false: op(B)[k][n] = B[k * ld + n]   (B stored K x N row-major)
+// Operands may be fp32 or bf16 in memory.  MATH_BF16 rounds them to bf16 (RNE)
+// and runs v_mfma_f32_32x32x16_bf16; MATH_F32 keeps fp32 and runs
+// v_mfma_f32_32x32x2f32.  Accumulation is fp32 in both.  A triangular flag on
+// an operand both skips the K tiles that are structurally zero and masks the
+// zero triangle on load, so the stored contents of that triangle never matter.
+#pragma once
+#include "common.h"
+
+namespace ifk {
+
+struct MatRef {
+  const void* p;
+  int dt;          // DT_F32 / DT_BF16
+  int64_t ld;
+  bool kc;         // see header comment
+  int tri;         // TRI_NONE / TRI_UPPER / TRI_LOWER, describing op(X)
+  int64_t bstride; // elements between batch entries
+};
+
+inline MatRef A_n(const void* p, int dt, int64_t ld, int tri = TRI_NONE, int64_t bs = 0) {
+  return MatRef{p, dt, ld, true, tri, bs};
+}
+inline MatRef A_t(const void* p, int dt, int64_t ld, int tri = TRI_NONE, int64_t bs = 0) {
+  return MatRef{p, dt, ld, false, tri, bs};
+}
+inline MatRef B_n(const void* p, int dt, int64_t ld, int tri = TRI_NONE, int64_t bs = 0) {
+  return MatRef{p, dt, ld, false, tri, bs};
+}
+inline MatRef B_t(const void* p, int dt, int64_t ld, int tri = TRI_NONE, int64_t bs = 0) {
+  return MatRef{p, dt, ld, true, tri, bs};
+}
+
+struct OutRef {
+  float* c;        // fp32 output (may be null if cb is set and beta == 0)
+  int64_t ldc;
+  int64_t bstride;
+  bf16_t* cb;      // optional RNE bf16 copy of the result
+  int64_t ldcb;
+  int64_t bstride_b;
+};
+
+inline OutRef out_f32(float* c, int64_t ldc, int64_t bs = 0) {
+  return OutRef{c, ldc, bs, nullptr, 0, 0};
+}
+inline OutRef out_bf16(bf16_t* cb, int64_t ld, int64_t bs = 0) {
+  return OutRef{nullptr, 0, 0, cb, ld, bs};
+}
+
+// Scratch the engine may use for split-K partial sums (fp32 elements).  When
+// it is too small the engine uses fewer splits; it never fails for lack of it.
+struct SplitScratch {
+  float* p;
+  size_t floats;
+};
+
+int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
+         const MatRef& A, const MatRef& B, float beta, const OutRef& C, int batch,
+         SplitScratch scratch);
+
+}  // namespace ifk

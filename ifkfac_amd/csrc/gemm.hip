@@ -1,0 +1,449 @@
+// MFMA GEMM engine (gfx950).  Contract in gemm.h.
+//
+// Block tile 128 x 128, 256 threads = 4 waves in a 2 x 2 grid, each wave owns a
+// 64 x 64 sub-tile computed as 2 x 2 MFMA 32x32 tiles (4 f32x16 accumulators).
+// K is staged through LDS in slabs of BK (64 for bf16, 32 for fp32) with a
+// register prefetch of the next slab while the current one feeds the MFMAs.
+// In LDS both operands are stored K-contiguous per row so every lane reads its
+// MFMA fragment with 128-bit loads; operands that are K-strided in memory are
+// transposed in registers on the way in (8 k x 4 mn micro-blocks per thread).
+#include "gemm.h"
+
+namespace ifk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int GBM = 128;
+constexpr int GBN = 128;
+constexpr int GNT = 256;
+
+template <int MATH> struct GCfg;
+template <> struct GCfg<MATH_BF16> {
+  static constexpr int BK = 64;
+  static constexpr int LDW = 72;  // LDS row stride in elements (bf16)
+  static constexpr int G = 8;     // k values per staged group
+  typedef bf16_t LT;
+};
+template <> struct GCfg<MATH_F32> {
+  static constexpr int BK = 32;
+  static constexpr int LDW = 36;  // LDS row stride in elements (fp32)
+  static constexpr int G = 4;
+  typedef float LT;
+};
+
+struct GemmParams {
+  int64_t M, N, K;
+  float alpha, beta;
+  const void* A; int64_t lda; int tria; int64_t bsa;
+  const void* B; int64_t ldb; int trib; int64_t bsb;
+  float* C; int64_t ldc; int64_t bsc;
+  bf16_t* Cb; int64_t ldcb; int64_t bscb;
+  float* part;
+  int splits;
+  int tiles_m, tiles_n;
+  int vec_a, vec_b;
+};
+
+template <int DT>
+__device__ inline float ld_elem(const void* base, int64_t idx) {
+  if constexpr (DT == DT_F32) {
+    return ((const float*)base)[idx];
+  } else {
+    return bf16_to_f32(((const bf16_t*)base)[idx]);
+  }
+}
+
+// Load `cnt` (4 or 8) consecutive elements starting at base[idx] as floats.
+// Caller guarantees alignment (idx multiple of cnt, base 16-byte aligned).
+template <int DT, int CNT>
+__device__ inline void ld_vec(const void* base, int64_t idx, float* out) {
+  if constexpr (DT == DT_F32) {
+    const float4* p = (const float4*)((const float*)base + idx);
+#pragma unroll
+    for (int c = 0; c < CNT / 4; ++c) {
+      float4 v = p[c];
+      out[4 * c + 0] = v.x; out[4 * c + 1] = v.y; out[4 * c + 2] = v.z; out[4 * c + 3] = v.w;
+    }
+  } else {
+    const bf16_t* b = (const bf16_t*)base + idx;
+    if constexpr (CNT == 8) {
+      uint4 v = *(const uint4*)b;
+      uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        out[2 * c] = bf16_to_f32((bf16_t)(w[c] & 0xffffu));
+        out[2 * c + 1] = bf16_to_f32((bf16_t)(w[c] >> 16));
+      }
+    } else {
+      uint2 v = *(const uint2*)b;
+      uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        out[2 * c] = bf16_to_f32((bf16_t)(w[c] & 0xffffu));
+        out[2 * c + 1] = bf16_to_f32((bf16_t)(w[c] >> 16));
+      }
+    }
+  }
+}
+
+// Is element (mn, k) of the operand structurally zero?  For A, mn = m of
+// op(A)[m][k]; for B, mn = n of op(B)[k][n].
+template <bool ISA>
+__device__ inline bool tri_zero(int tri, int64_t mn, int64_t k) {
+  if (tri == TRI_NONE) return false;
+  if constexpr (ISA) {
+    return tri == TRI_UPPER ? (k < mn) : (k > mn);
+  } else {
+    return tri == TRI_UPPER ? (k > mn) : (k < mn);
+  }
+}
+
+// Stage one operand slab (128 rows of mn x BK k values) into registers as 4
+// groups of G consecutive k values each.
+template <int MATH, int DT, bool KC, bool ISA>
+__device__ inline void stage_load(float (&v)[4][GCfg<MATH>::G], const void* base, int64_t ld,
+                                  int64_t MN, int64_t K, int64_t mn0, int64_t k0, int tri,
+                                  bool vec, int t) {
+  constexpr int G = GCfg<MATH>::G;
+  constexpr int BK = GCfg<MATH>::BK;
+  const bool interior = vec && (mn0 + 128 <= MN) && (k0 + BK <= K);
+  if constexpr (KC) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int g = t + GNT * q;
+      const int mn = g / (BK / G);
+      const int kk = (g % (BK / G)) * G;
+      const int64_t gm = mn0 + mn, gk = k0 + kk;
+      if (interior) {
+        ld_vec<DT, G>(base, gm * ld + gk, v[q]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < G; ++e) {
+          v[q][e] = (gm < MN && gk + e < K) ? ld_elem<DT>(base, gm * ld + gk + e) : 0.0f;
+        }
+      }
+      if (tri != TRI_NONE) {
+#pragma unroll
+        for (int e = 0; e < G; ++e)
+          if (tri_zero<ISA>(tri, gm, gk + e)) v[q][e] = 0.0f;
+      }
+    }
+  } else {
+    // micro-block: G k values x 4 mn values per thread
+    const int mnb = (t & 31) * 4;
+    const int kb = (t >> 5) * G;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int64_t gk = k0 + kb + i;
+      float w[4];
+      if (interior) {
+        ld_vec<DT, 4>(base, gk * ld + mn0 + mnb, w);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t gm = mn0 + mnb + j;
+          w[j] = (gm < MN && gk < K) ? ld_elem<DT>(base, gk * ld + gm) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j][i] = w[j];
+    }
+    if (tri != TRI_NONE) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+          if (tri_zero<ISA>(tri, mn0 + mnb + j, k0 + kb + i)) v[j][i] = 0.0f;
+    }
+  }
+}
+
+// Write staged groups into the LDS slab (row-major [mn][k], K contiguous).
+template <int MATH, bool KC>
+__device__ inline void stage_store(typename GCfg<MATH>::LT* Xs, const float (&v)[4][GCfg<MATH>::G],
+                                   int t) {
+  constexpr int G = GCfg<MATH>::G;
+  constexpr int BK = GCfg<MATH>::BK;
+  constexpr int LDW = GCfg<MATH>::LDW;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int mn, kk;
+    if constexpr (KC) {
+      const int g = t + GNT * q;
+      mn = g / (BK / G);
+      kk = (g % (BK / G)) * G;
+    } else {
+      mn = (t & 31) * 4 + q;
+      kk = (t >> 5) * G;
+    }
+    if constexpr (MATH == MATH_BF16) {
+      uint4 w;
+      w.x = pack_bf16x2(v[q][0], v[q][1]);
+      w.y = pack_bf16x2(v[q][2], v[q][3]);
+      w.z = pack_bf16x2(v[q][4], v[q][5]);
+      w.w = pack_bf16x2(v[q][6], v[q][7]);
+      *(uint4*)(&Xs[mn * LDW + kk]) = w;
+    } else {
+      // fp32 slab keeps even k in positions 0..15 and odd k in 16..31 so that a
+      // lane's operands for consecutive 32x32x2 steps are contiguous.
+      float* row = (float*)Xs + mn * LDW;
+      *(float2*)(&row[kk / 2]) = make_float2(v[q][0], v[q][2]);
+      *(float2*)(&row[16 + kk / 2]) = make_float2(v[q][1], v[q][3]);
+    }
+  }
+}
+
+template <int MATH, int ADT, bool AKC, int BDT, bool BKC>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
+  constexpr int BK = GCfg<MATH>::BK;
+  constexpr int LDW = GCfg<MATH>::LDW;
+  constexpr int G = GCfg<MATH>::G;
+  typedef typename GCfg<MATH>::LT LT;
+  __shared__ __attribute__((aligned(16))) LT As[GBM * LDW];
+  __shared__ __attribute__((aligned(16))) LT Bs[GBN * LDW];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int tile = blockIdx.x;
+  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+  const int z = blockIdx.z;
+  const int bidx = z / p.splits, split = z % p.splits;
+  const int64_t m0 = (int64_t)tm * GBM, n0 = (int64_t)tn * GBN;
+
+  const void* Ab = (const char*)p.A + (size_t)bidx * p.bsa * (ADT == DT_F32 ? 4 : 2);
+  const void* Bb = (const char*)p.B + (size_t)bidx * p.bsb * (BDT == DT_F32 ? 4 : 2);
+
+  // K range of this tile after triangular structure, then this split's share.
+  int64_t klo = 0, khi = p.K;
+  if (p.tria == TRI_UPPER) klo = max(klo, m0);
+  if (p.tria == TRI_LOWER) khi = min(khi, m0 + GBM);
+  if (p.trib == TRI_UPPER) khi = min(khi, n0 + GBN);
+  if (p.trib == TRI_LOWER) klo = max(klo, n0);
+  int64_t nkt = khi > klo ? (khi - klo + BK - 1) / BK : 0;
+  int64_t per = (nkt + p.splits - 1) / p.splits;
+  int64_t kt0 = (int64_t)split * per;
+  int64_t kt1 = min(nkt, kt0 + per);
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  float va[4][G], vb[4][G];
+  if (kt0 < kt1) {
+    stage_load<MATH, ADT, AKC, true>(va, Ab, p.lda, p.M, khi, m0, klo + kt0 * BK, p.tria,
+                                     p.vec_a, t);
+    stage_load<MATH, BDT, BKC, false>(vb, Bb, p.ldb, p.N, khi, n0, klo + kt0 * BK, p.trib,
+                                      p.vec_b, t);
+  }
+  const int h = lane >> 5;
+  const int l32 = lane & 31;
+  for (int64_t kt = kt0; kt < kt1; ++kt) {
+    stage_store<MATH, AKC>(As, va, t);
+    stage_store<MATH, BKC>(Bs, vb, t);
+    __syncthreads();
+    if (kt + 1 < kt1) {
+      const int64_t kn = klo + (kt + 1) * BK;
+      stage_load<MATH, ADT, AKC, true>(va, Ab, p.lda, p.M, khi, m0, kn, p.tria, p.vec_a, t);
+      stage_load<MATH, BDT, BKC, false>(vb, Bb, p.ldb, p.N, khi, n0, kn, p.trib, p.vec_b, t);
+    }
+    if constexpr (MATH == MATH_BF16) {
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8_t af[2], bfr[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          af[i] = *(const bf16x8_t*)(&As[(wm * 64 + i * 32 + l32) * LDW + ks * 16 + h * 8]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          bfr[j] = *(const bf16x8_t*)(&Bs[(wn * 64 + j * 32 + l32) * LDW + ks * 16 + h * 8]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+    } else {
+      float af[2][16], bfr[2][16];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float* row = (const float*)As + (wm * 64 + i * 32 + l32) * LDW + h * 16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float4 v = *(const float4*)(row + 4 * c);
+          af[i][4 * c] = v.x; af[i][4 * c + 1] = v.y; af[i][4 * c + 2] = v.z; af[i][4 * c + 3] = v.w;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float* row = (const float*)Bs + (wn * 64 + j * 32 + l32) * LDW + h * 16;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float4 v = *(const float4*)(row + 4 * c);
+          bfr[j][4 * c] = v.x; bfr[j][4 * c + 1] = v.y; bfr[j][4 * c + 2] = v.z; bfr[j][4 * c + 3] = v.w;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 16; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bfr[j][s], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue.  acc[i][j][r] holds row (r/4)*8 + h*4 + r%4, column l32 of the
+  // 32x32 tile (i, j) of this wave.
+  if (p.splits > 1) {
+    float* P = p.part + ((size_t)(bidx * p.splits + split)) * (size_t)p.M * (size_t)p.N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          const int64_t col = n0 + wn * 64 + j * 32 + l32;
+          if (row < p.M && col < p.N) P[row * p.N + col] = acc[i][j][r];
+        }
+    return;
+  }
+  float* Cp = p.C ? p.C + (size_t)bidx * p.bsc : nullptr;
+  bf16_t* Cbp = p.Cb ? p.Cb + (size_t)bidx * p.bscb : nullptr;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        const int64_t col = n0 + wn * 64 + j * 32 + l32;
+        if (row < p.M && col < p.N) {
+          float v = p.alpha * acc[i][j][r];
+          if (p.beta != 0.0f) v += p.beta * Cp[row * p.ldc + col];
+          if (Cp) Cp[row * p.ldc + col] = v;
+          if (Cbp) Cbp[row * p.ldcb + col] = f32_to_bf16(v);
+        }
+      }
+}
+
+__global__ void splitk_reduce_kernel(GemmParams p) {
+  const int64_t MN = p.M * p.N;
+  const int bidx = blockIdx.y;
+  const float* P = p.part + (size_t)bidx * p.splits * MN;
+  float* Cp = p.C ? p.C + (size_t)bidx * p.bsc : nullptr;
+  bf16_t* Cbp = p.Cb ? p.Cb + (size_t)bidx * p.bscb : nullptr;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < MN;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.0f;
+    for (int sp = 0; sp < p.splits; ++sp) s += P[(size_t)sp * MN + e];
+    const int64_t row = e / p.N, col = e % p.N;
+    float v = p.alpha * s;
+    if (p.beta != 0.0f) v += p.beta * Cp[row * p.ldc + col];
+    if (Cp) Cp[row * p.ldc + col] = v;
+    if (Cbp) Cbp[row * p.ldcb + col] = f32_to_bf16(v);
+  }
+}
+
+template <int MATH, int ADT, bool AKC, int BDT, bool BKC>
+static void launch_t(hipStream_t s, dim3 g, const GemmParams& p) {
+  hipLaunchKernelGGL((gemm_kernel<MATH, ADT, AKC, BDT, BKC>), g, dim3(GNT), 0, s, p);
+}
+
+template <int MATH, int ADT, bool AKC>
+static void launch_b(hipStream_t s, dim3 g, const GemmParams& p, int bdt, bool bkc) {
+  if (bdt == DT_F32) {
+    if (bkc) launch_t<MATH, ADT, AKC, DT_F32, true>(s, g, p);
+    else launch_t<MATH, ADT, AKC, DT_F32, false>(s, g, p);
+  } else {
+    if (bkc) launch_t<MATH, ADT, AKC, DT_BF16, true>(s, g, p);
+    else launch_t<MATH, ADT, AKC, DT_BF16, false>(s, g, p);
+  }
+}
+
+template <int MATH>
+static void launch_a(hipStream_t s, dim3 g, const GemmParams& p, int adt, bool akc, int bdt,
+                     bool bkc) {
+  if (adt == DT_F32) {
+    if (akc) launch_b<MATH, DT_F32, true>(s, g, p, bdt, bkc);
+    else launch_b<MATH, DT_F32, false>(s, g, p, bdt, bkc);
+  } else {
+    if (akc) launch_b<MATH, DT_BF16, true>(s, g, p, bdt, bkc);
+    else launch_b<MATH, DT_BF16, false>(s, g, p, bdt, bkc);
+  }
+}
+
+static bool vec_ok(const MatRef& X) {
+  const uintptr_t a = (uintptr_t)X.p;
+  return (a % 16 == 0) && (X.ld % 8 == 0) && (X.bstride % 8 == 0);
+}
+
+int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, const MatRef& A,
+         const MatRef& B, float beta, const OutRef& C, int batch, SplitScratch scratch) {
+  if (M < 0 || N < 0 || K < 0 || batch < 1) {
+    set_error("gemm: negative size or batch < 1");
+    return IFK_ERR_INVALID;
+  }
+  if (M == 0 || N == 0) return IFK_OK;
+  if (!C.c && !C.cb) {
+    set_error("gemm: no output");
+    return IFK_ERR_INVALID;
+  }
+  if (beta != 0.0f && !C.c) {
+    set_error("gemm: beta != 0 needs an fp32 output to read");
+    return IFK_ERR_INVALID;
+  }
+  if (M > (int64_t)1 << 30 || N > (int64_t)1 << 30) {
+    set_error("gemm: dimension too large");
+    return IFK_ERR_INVALID;
+  }
+  GemmParams p;
+  p.M = M; p.N = N; p.K = K; p.alpha = alpha; p.beta = beta;
+  p.A = A.p; p.lda = A.ld; p.tria = A.tri; p.bsa = A.bstride;
+  p.B = B.p; p.ldb = B.ld; p.trib = B.tri; p.bsb = B.bstride;
+  p.C = C.c; p.ldc = C.ldc; p.bsc = C.bstride;
+  p.Cb = C.cb; p.ldcb = C.ldcb; p.bscb = C.bstride_b;
+  p.tiles_m = (int)cdiv(M, GBM);
+  p.tiles_n = (int)cdiv(N, GBN);
+  p.vec_a = vec_ok(A);
+  p.vec_b = vec_ok(B);
+  const int BK = math == MATH_BF16 ? GCfg<MATH_BF16>::BK : GCfg<MATH_F32>::BK;
+  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
+  const int64_t nkt = cdiv(K, BK);
+  int splits = 1;
+  if (tiles < 192 && nkt >= 8) {
+    int64_t want = cdiv(384, tiles);
+    want = std::min<int64_t>(want, nkt / 4);
+    want = std::min<int64_t>(want, 64);
+    while (want > 1 && (size_t)(want * batch) * (size_t)(M * N) > scratch.floats) --want;
+    if (want > 1 && scratch.p) splits = (int)want;
+  }
+  p.splits = splits;
+  p.part = splits > 1 ? scratch.p : nullptr;
+  if (tiles * splits > 0x7fffffffLL || (int64_t)batch * splits > 65535) {
+    set_error("gemm: grid too large");
+    return IFK_ERR_INVALID;
+  }
+  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * splits));
+  if (math == MATH_BF16) launch_a<MATH_BF16>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
+  else launch_a<MATH_F32>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
+  int rc = check_launch("gemm");
+  if (rc) return rc;
+  if (splits > 1) {
+    int64_t MN = M * N;
+    unsigned gx = (unsigned)std::min<int64_t>(cdiv(MN, 256), 4096);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(gx, batch), dim3(256), 0, s, p);
+    rc = check_launch("gemm splitk reduce");
+  }
+  return rc;
+}
+
+}  // namespace ifk

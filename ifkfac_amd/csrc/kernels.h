@@ -1,0 +1,57 @@
+// Host-side launchers of the single-purpose kernels (small.hip, elementwise.hip).
+#pragma once
+#include "common.h"
+
+namespace ifk {
+
+// --- panel kernels (small.hip); b <= 64 -------------------------------------
+int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t ldr, int b,
+                      float tol, float* M1, float* Q1, int* flag);
+int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, int b, float* N, int* flag);
+int launch_panel_hh_fallback(hipStream_t s, const float* Ptop, int64_t ldr, const float* Xp,
+                             int64_t ldx, int64_t pe, int b, float* Y, const int* flag);
+int launch_panel_finish(hipStream_t s, const float* YtY, const float* YtX, float* R, int64_t ldr,
+                        int b, float* T);
+int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
+int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
+                      float* Z, int64_t ldz, int safe);
+
+// --- elementwise kernels (elementwise.hip) -----------------------------------
+// dst (rows x cols, ldd, fp32) = scale * src (dtype sdt, lds)
+int launch_copy_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
+                       int64_t cols, float scale, float* dst, int64_t ldd);
+// dst = scale * src restricted to the upper triangle (strict lower part set 0)
+int launch_copy_upper(hipStream_t s, const float* src, int64_t lds, int64_t n, float scale,
+                      float* dst, int64_t ldd);
+// dst (n x n) = diag(value)
+int launch_set_diag(hipStream_t s, float* dst, int64_t ldd, int64_t n, float value);
+// rows [r0, r1) of dst (cols wide) set to zero
+int launch_zero_rows(hipStream_t s, float* dst, int64_t ldd, int64_t r0, int64_t r1, int64_t cols);
+// zero a rows x cols block
+int launch_zero(hipStream_t s, float* dst, int64_t ldd, int64_t rows, int64_t cols);
+// dst -= src (rows x cols)
+int launch_sub_inplace(hipStream_t s, float* dst, int64_t ldd, const float* src, int64_t lds,
+                       int64_t rows, int64_t cols);
+// negate rows i < r whose diagonal entry is negative (sign(0) counts as +)
+int launch_sign_normalize(hipStream_t s, float* R, int64_t ldr, int64_t r, int64_t n);
+// out (dtype odt) = R upper triangle (RNE for bf16); *finite &= all finite
+int launch_cast_upper(hipStream_t s, const float* R, int64_t ldr, int64_t n, void* out, int odt,
+                      int64_t ldo, int* finite);
+// out (odt) = src (fp32), full matrix
+int launch_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols, void* out,
+                int odt, int64_t ldo);
+// *flag = 1 (a one-thread fill, safe to capture in a graph)
+int launch_fill_int(hipStream_t s, int* p, int value, int count);
+// heavy-ball momentum + decoupled weight decay + SGD step
+int launch_momentum_update(hipStream_t s, const float* nat, float* buf, float* W, int64_t numel,
+                           float lr, float momentum, float weight_decay, int buf_init);
+// dst (cols x rows, fp32) = src^T (src rows x cols, dtype sdt)
+int launch_transpose_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
+                            int64_t cols, float* dst, int64_t ldd);
+// out (odt, n x n) = lower triangle of src^T, i.e. out[i][j] = src[j][i] for j <= i, else 0
+int launch_transpose_upper(hipStream_t s, const float* src, int64_t lds, int64_t n, void* out,
+                           int odt, int64_t ldo);
+// out (dt) = alpha * x (fp32) with optional bf16 output
+int launch_scale_copy_vec(hipStream_t s, const float* x, int64_t n, float alpha, void* out, int odt);
+
+}  // namespace ifk

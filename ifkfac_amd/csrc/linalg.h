@@ -1,0 +1,63 @@
+// Host orchestration of the curvature path.  Every routine enqueues work on
+// the given stream, takes all scratch memory from the caller's workspace and
+// returns IFK_OK or a negative status with the message in get_error().
+#pragma once
+#include "common.h"
+
+namespace ifk {
+
+constexpr int PANEL_B = 64;   // column panel width of the fold
+constexpr int TRINV_NB = 64;  // diagonal block of the triangular inverse
+
+// streaming_tsqr_update: R (n x n buffer, rows [0, r_in) valid) absorbs X (p x n).
+size_t fold_ws(int64_t p, int64_t n);
+int fold(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx, float* R,
+         int64_t ldr, int64_t r_in, int math, void* ws, size_t ws_bytes, int64_t* r_out);
+
+// finalize_R with the 1/sqrt(rows) scale: out = R_damped of [scale * R_in; sqrt(damping) I].
+size_t finalize_ws(int64_t n);
+int finalize(hipStream_t s, const float* R_in, int64_t ldr_in, int64_t n, float scale,
+             float damping, void* out, int odt, int64_t ldo, int math, int* finite, void* ws,
+             size_t ws_bytes);
+
+// Z = R^{-1} for upper-triangular R (dtype rdt); Z fp32 upper triangular.
+size_t trinv_ws(int64_t n);
+int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,
+          int math, int safe, void* ws, size_t ws_bytes);
+
+// nat = Z_G Z_G^T grad Z_X Z_X^T, with Z_X = R_X^{-1}, Z_G = R_G^{-1} given.
+size_t precondition_apply_ws(int64_t n_out, int64_t n_in, int math);
+int precondition_apply(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,
+                       const float* ZX, int64_t ldzx, const float* ZG, int64_t ldzg, float* nat,
+                       int64_t ldn, int math, void* ws, size_t ws_bytes);
+
+// All four solves from the factors themselves (inverses formed internally).
+size_t precondition_ws(int64_t n_out, int64_t n_in, int math);
+int precondition(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,
+                 const void* RX, int64_t ldrx, const void* RG, int64_t ldrg, int rdt, float* nat,
+                 int64_t ldn, int math, void* ws, size_t ws_bytes);
+
+// out = Z_G Z_G^T g for a bias gradient g (n_out).
+size_t precondition_bias_ws(int64_t n_out);
+int precondition_bias(hipStream_t s, const float* g, int64_t n_out, const float* ZG, int64_t ldzg,
+                      float* out, void* ws, size_t ws_bytes);
+
+// bf16_linalg counterparts ------------------------------------------------------
+size_t geqrf_r_ws(int64_t m, int64_t n);
+int geqrf_r(hipStream_t s, const void* A, int adt, int64_t m, int64_t n, int64_t lda, void* R,
+            int rdt, int64_t ldr, int math, void* ws, size_t ws_bytes);
+
+size_t trsm_ws(int64_t n, int64_t k);
+int trsm(hipStream_t s, const void* R, int rdt, int64_t n, int64_t ldr, int upper, const void* B,
+         int bdt, int64_t k, int64_t ldb, void* X, int xdt, int64_t ldx, int math, void* ws,
+         size_t ws_bytes);
+
+size_t potrf_ws(int64_t n);
+int potrf(hipStream_t s, const void* A, int adt, int64_t n, int64_t lda, void* L, int ldt,
+          int64_t ldl, int math, void* ws, size_t ws_bytes);
+
+size_t inv_spd_ws(int64_t n);
+int inv_spd(hipStream_t s, const void* A, int adt, int64_t n, int64_t lda, void* X, int xdt,
+            int64_t ldx, int math, void* ws, size_t ws_bytes);
+
+}  // namespace ifk

@@ -1,0 +1,186 @@
+/*
+ * ifkfac_hip.h -- C ABI of the MI355X (gfx950) IFKFAC curvature library.
+ *
+ * The library implements, as hand-written HIP kernels, the numerical seams of
+ * the reference package (Gsend/ifkfac) that its Python optimizer calls on the
+ * curvature hot path.  Each entry point below names the reference function it
+ * replaces (file:line in the reference tree).
+ *
+ * Conventions shared by every entry point
+ *   - Matrices are row-major.  `ld*` is the leading dimension in elements.
+ *   - Pointers are device pointers (HBM); the library never allocates device
+ *     memory and never frees caller memory.  Scratch space comes from the
+ *     caller through (workspace, workspace_bytes); the matching
+ *     *_workspace_size() function returns how many bytes a call needs.
+ *   - `stream` is a hipStream_t.  All work is enqueued on it; no entry point
+ *     synchronises the device or the stream.
+ *   - Return value: IFK_OK (0) or a negative IFK_ERR_* code.  The message of
+ *     the last failure on the calling thread is available from
+ *     ifk_last_error().  Nothing throws across this boundary.
+ *   - dtype codes: IFK_F32, IFK_BF16.  math codes: IFK_MATH_F32 runs the
+ *     contractions on fp32 MFMA; IFK_MATH_BF16 rounds operands to bf16 (RNE)
+ *     and runs bf16 MFMA, always with fp32 accumulation.
+ */
+#ifndef IFKFAC_HIP_H
+#define IFKFAC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IFK_OK 0
+#define IFK_ERR_INVALID (-1)
+#define IFK_ERR_WORKSPACE (-2)
+#define IFK_ERR_HIP (-3)
+
+#define IFK_F32 0
+#define IFK_BF16 1
+
+#define IFK_MATH_F32 0
+#define IFK_MATH_BF16 1
+
+/* Version of this ABI (bumped on any signature change). */
+int ifk_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ifk_last_error(void);
+
+/*
+ * Streaming TSQR fold -- replaces streaming_tsqr_update(running_R, new_chunk)
+ * (ifkfac/triangular.py:246-307) as called from the hooks
+ * (ifkfac/activation_hooks.py:579, :642).
+ *
+ * R is an n x n fp32 buffer (ldr >= n) whose first r_in rows hold the running
+ * factor (upper trapezoidal, r_in = 0 for "no data yet"); rows [r_in, n) are
+ * overwritten.  X is the p x n chunk (dtype x_dtype, ldx >= n).  On return
+ * rows [0, *r_out) of R hold the factor of [R_old; X] with a positive
+ * diagonal, *r_out = min(r_in + p, n) -- the shape torch.linalg.qr(mode=
+ * "reduced") gives the reference -- and the remaining rows are zero.
+ * X is not modified.
+ */
+size_t ifk_tsqr_fold_workspace_size(int64_t p, int64_t n);
+int ifk_tsqr_fold(void* stream, const void* X, int x_dtype, int64_t p, int64_t n, int64_t ldx,
+                  float* R, int64_t ldr, int64_t r_in, int math, void* workspace,
+                  size_t workspace_bytes, int64_t* r_out);
+
+/*
+ * Damped finalisation -- replaces the `R_raw / sqrt(rows)` scaling and
+ * finalize_R(R, damping) of get_factors (ifkfac/activation_hooks.py:328-332,
+ * ifkfac/triangular.py:386-421) and, with out_dtype = IFK_BF16, the RNE cast
+ * of _update_factors (ifkfac/ifkfac.py:292-294).
+ *
+ * out (n x n, ldo) = R_d with R_d^T R_d = scale^2 R_in^T R_in + damping I,
+ * upper triangular with positive diagonal.  If `finite` is non-null, *finite
+ * is set to 1 if every entry of R_d is finite and 0 otherwise (the check of
+ * ifkfac/ifkfac.py:232), written on the stream.
+ */
+size_t ifk_finalize_workspace_size(int64_t n);
+int ifk_finalize(void* stream, const float* R_in, int64_t ldr_in, int64_t n, float scale,
+                 float damping, void* out, int out_dtype, int64_t ldo, int math, int32_t* finite,
+                 void* workspace, size_t workspace_bytes);
+
+/*
+ * Triangular inverse Z = R^{-1} of an upper-triangular n x n factor (dtype
+ * r_dtype) into fp32 Z (ldz).  The four solves of apply_vered are applied as
+ * products with Z; this is the factor-side half of them.
+ */
+size_t ifk_tri_inverse_workspace_size(int64_t n);
+int ifk_tri_inverse(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n, float* Z,
+                    int64_t ldz, int math, void* workspace, size_t workspace_bytes);
+
+/*
+ * Four triangular solves -- replaces apply_vered(grad_W, R_X, R_G)
+ * (ifkfac/triangular.py:551-656) and the per-entry body of
+ * apply_vered_batched (ifkfac/triangular.py:430-451, :506-544):
+ *   nat = (R_G^T R_G)^{-1} grad (R_X^T R_X)^{-1}
+ * grad and nat are n_out x n_in fp32.  ifk_precondition takes the factors;
+ * ifk_precondition_apply takes their inverses from ifk_tri_inverse, which
+ * lets a caller reuse them for every step between factor updates.
+ */
+size_t ifk_precondition_workspace_size(int64_t n_out, int64_t n_in, int math);
+int ifk_precondition(void* stream, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,
+                     const void* R_X, int64_t ldrx, const void* R_G, int64_t ldrg, int r_dtype,
+                     float* nat, int64_t ldn, int math, void* workspace, size_t workspace_bytes);
+
+size_t ifk_precondition_apply_workspace_size(int64_t n_out, int64_t n_in, int math);
+int ifk_precondition_apply(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                           int64_t ldg, const float* Z_X, int64_t ldzx, const float* Z_G,
+                           int64_t ldzg, float* nat, int64_t ldn, int math, void* workspace,
+                           size_t workspace_bytes);
+
+/*
+ * Bias preconditioning -- replaces apply_vered_bias(grad_b, R_G)
+ * (ifkfac/triangular.py:659-705): out = (R_G^T R_G)^{-1} g, given Z_G.
+ */
+size_t ifk_precondition_bias_workspace_size(int64_t n_out);
+int ifk_precondition_bias(void* stream, const float* g, int64_t n_out, const float* Z_G,
+                          int64_t ldzg, float* out, void* workspace, size_t workspace_bytes);
+
+/*
+ * Momentum and weight update -- replaces the per-layer update of
+ * _apply_preconditioner_bucketed (ifkfac/ifkfac.py:402-413) and
+ * _apply_preconditioner (ifkfac/ifkfac.py:500-510) as one pass:
+ *   buf = buf_init ? nat : momentum * buf + nat      (momentum > 0 only)
+ *   W   = W * (1 - lr * weight_decay) - lr * (momentum > 0 ? buf : nat)
+ * (the decay factor only when weight_decay > 0).  All arrays fp32, numel
+ * elements; buf may be null when momentum == 0.
+ */
+int ifk_momentum_update(void* stream, const float* nat, float* buf, float* W, int64_t numel,
+                        float lr, float momentum, float weight_decay, int buf_init);
+
+/*
+ * R factor of a tall matrix -- replaces block_householder_qr_bf16 and
+ * householder_qr_bf16 (ifkfac/bf16_linalg.py:64-153, :158-183).
+ * A is m x n (m >= n); R (n x n, r_dtype) is upper triangular with a positive
+ * diagonal.
+ */
+size_t ifk_geqrf_r_workspace_size(int64_t m, int64_t n);
+int ifk_geqrf_r(void* stream, const void* A, int a_dtype, int64_t m, int64_t n, int64_t lda,
+                void* R, int r_dtype, int64_t ldr, int math, void* workspace,
+                size_t workspace_bytes);
+
+/*
+ * Triangular solve -- replaces solve_triangular_bf16(R, B, upper)
+ * (ifkfac/bf16_linalg.py:188-242): X = R^{-1} B (upper != 0) or L^{-1} B,
+ * R n x n, B and X n x k.  Diagonal divisors follow _safe_div
+ * (ifkfac/bf16_linalg.py:44-59).
+ */
+size_t ifk_trsm_workspace_size(int64_t n, int64_t k);
+int ifk_trsm(void* stream, const void* R, int r_dtype, int64_t n, int64_t ldr, int upper,
+             const void* B, int b_dtype, int64_t k, int64_t ldb, void* X, int x_dtype, int64_t ldx,
+             int math, void* workspace, size_t workspace_bytes);
+
+/*
+ * Cholesky -- replaces cholesky_bf16(A) (ifkfac/bf16_linalg.py:247-267):
+ * L lower with L L^T = A, pivots clamped at 1e-7 as the reference does.
+ */
+size_t ifk_potrf_workspace_size(int64_t n);
+int ifk_potrf(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda, void* L,
+              int l_dtype, int64_t ldl, int math, void* workspace, size_t workspace_bytes);
+
+/*
+ * SPD inverse -- replaces inv_spd_bf16(A) (ifkfac/bf16_linalg.py:272-280).
+ */
+size_t ifk_inv_spd_workspace_size(int64_t n);
+int ifk_inv_spd(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda, void* X,
+                int x_dtype, int64_t ldx, int math, void* workspace, size_t workspace_bytes);
+
+/*
+ * General MFMA matrix product C = alpha op(A) op(B) + beta C, exposed for
+ * tests and for callers that compose the path themselves.  trans_a/trans_b
+ * select op(X) = X^T; C is fp32.
+ */
+size_t ifk_gemm_workspace_size(int64_t m, int64_t n);
+int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alpha, const void* A,
+             int a_dtype, int64_t lda, int trans_a, const void* B, int b_dtype, int64_t ldb,
+             int trans_b, float beta, float* C, int64_t ldc, void* workspace,
+             size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IFKFAC_HIP_H */
