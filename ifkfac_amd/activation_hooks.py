@@ -1,0 +1,333 @@
+"""Forward/backward hooks that keep each layer's streaming R factors.
+
+Counterpart of ``RawActivationHooks`` (ifkfac/activation_hooks.py:87-653): the
+same constructor, modes (streaming, ``batched``, ``deferred``), row
+subsampling, Conv2d im2col, bias augmentation, skip rules and public methods.
+The numerical work goes to the HIP fold kernel: each tracked layer owns two
+persistent ``n x n`` fp32 buffers (input side X, output-gradient side G) that
+the fold updates in place, and ``_R_X[module]`` / ``_R_G[module]`` are views
+of the valid rows, shaped ``(min(rows, n), n)`` exactly as the reference's
+running factors are.
+"""
+from __future__ import annotations
+
+import logging
+import math
+import warnings
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ._backend import MATH_F32, get_backend
+from .gram_estimator import GramMatrixEstimator
+
+logger = logging.getLogger(__name__)
+
+warnings.filterwarnings("ignore", message="Full backward hook is firing", category=UserWarning)
+
+
+class IFKFACRankError(RuntimeError):
+    """Raised when a layer has fewer accumulated rows than columns (p < n)."""
+
+
+def _module_tag(module: nn.Module) -> str:
+    if isinstance(module, nn.Linear):
+        return f"Linear({module.in_features}→{module.out_features})"
+    if isinstance(module, nn.Conv2d):
+        return f"Conv2d({module.in_channels}→{module.out_channels}, k={module.kernel_size})"
+    return type(module).__name__
+
+
+class RawActivationHooks(GramMatrixEstimator):
+    """Streaming-TSQR factor capture for every Linear / Conv2d layer of a model.
+
+    Parameters match the reference (activation_hooks.py:128-139).  ``math``
+    selects the MFMA arithmetic of the fold (``IFKFAC`` sets bf16 when
+    ``use_true_bf16`` is on).
+    """
+
+    _SEQ_SUBSAMPLE: int = 2048
+
+    def __init__(
+        self,
+        model: nn.Module,
+        damping: float = 1e-2,
+        max_out_dim: int = 0,
+        augment_bias: bool = False,
+        max_conv_rows: int = 512,
+        max_seq_rows: Optional[int] = None,
+        batched: bool = False,
+        deferred: bool = False,
+        deferred_window: int = 5,
+        math: int = MATH_F32,
+    ):
+        self.model = model
+        self.damping = damping
+        self.augment_bias = augment_bias
+        self.max_conv_rows = max_conv_rows
+        self.max_seq_rows = self._SEQ_SUBSAMPLE if max_seq_rows is None else max_seq_rows
+        self.batched = batched
+        self.deferred = deferred
+        self.deferred_window = deferred_window
+        self.math = math
+        self.chunk_transform_X = None
+        self.chunk_transform_G = None
+        if batched and deferred:
+            raise ValueError("batched and deferred modes are mutually exclusive")
+
+        self._handles: List[torch.utils.hooks.RemovableHandle] = []
+        self._enabled = False
+        self._R_X: Dict[nn.Module, Optional[torch.Tensor]] = {}
+        self._R_G: Dict[nn.Module, Optional[torch.Tensor]] = {}
+        self._n_rows_X: Dict[nn.Module, int] = {}
+        self._n_rows_G: Dict[nn.Module, int] = {}
+        self._pending_X: Dict[nn.Module, List[torch.Tensor]] = {}
+        self._pending_G: Dict[nn.Module, List[torch.Tensor]] = {}
+        self._raw_X: Dict[nn.Module, List[torch.Tensor]] = {}
+        self._raw_G: Dict[nn.Module, List[torch.Tensor]] = {}
+        # persistent fold buffers (n x n fp32), reused across windows
+        self._buf_X: Dict[nn.Module, torch.Tensor] = {}
+        self._buf_G: Dict[nn.Module, torch.Tensor] = {}
+        self._linear_layers: List[nn.Module] = []
+
+        for module in model.modules():
+            if not isinstance(module, (nn.Linear, nn.Conv2d)):
+                continue
+            if max_out_dim > 0:
+                out_dim = (module.out_features if isinstance(module, nn.Linear)
+                           else module.out_channels)
+                if out_dim > max_out_dim:
+                    continue
+            self._linear_layers.append(module)
+            self._R_X[module] = None
+            self._R_G[module] = None
+            self._n_rows_X[module] = 0
+            self._n_rows_G[module] = 0
+            self._pending_X[module] = []
+            self._pending_G[module] = []
+            self._raw_X[module] = []
+            self._raw_G[module] = []
+
+    # ------------------------------------------------------------------ lifecycle
+    @property
+    def linear_layers(self) -> List[nn.Module]:
+        return self._linear_layers
+
+    @property
+    def is_enabled(self) -> bool:
+        return self._enabled
+
+    def enable(self):
+        if self._enabled:
+            return
+        for module in self._linear_layers:
+            self._handles.append(module.register_forward_hook(self._forward_hook))
+            self._handles.append(module.register_full_backward_hook(self._backward_hook))
+        self._enabled = True
+
+    def clear(self):
+        for module in self._linear_layers:
+            self._R_X[module] = None
+            self._R_G[module] = None
+            self._n_rows_X[module] = 0
+            self._n_rows_G[module] = 0
+            self._pending_X[module] = []
+            self._pending_G[module] = []
+            self._raw_X[module] = []
+            self._raw_G[module] = []
+
+    def remove(self):
+        for h in self._handles:
+            h.remove()
+        self._handles.clear()
+        self._enabled = False
+        self.clear()
+        self._buf_X.clear()
+        self._buf_G.clear()
+
+    def n_samples_accumulated(self, module: Optional[nn.Module] = None) -> int:
+        target = module or (self._linear_layers[0] if self._linear_layers else None)
+        if target is None:
+            return 0
+        return self._n_rows_X.get(target, 0)
+
+    # ------------------------------------------------------------------ folding
+    def _fold(self, side: str, module: nn.Module, chunk: torch.Tensor,
+              full_rank_shape: bool = False) -> None:
+        """Fold ``chunk`` into the running factor of ``module`` on ``side``."""
+        Rd = self._R_X if side == "X" else self._R_G
+        bufs = self._buf_X if side == "X" else self._buf_G
+        n = chunk.shape[1]
+        cur = Rd.get(module)
+        buf = bufs.get(module)
+        if buf is None or buf.shape[0] != n or buf.device != chunk.device:
+            buf = torch.zeros((n, n), dtype=torch.float32, device=chunk.device)
+            bufs[module] = buf
+        if cur is None:
+            r_in = n if full_rank_shape else 0
+            if full_rank_shape:
+                buf.zero_()
+        else:
+            r_in = cur.shape[0]
+            if cur.data_ptr() != buf.data_ptr():
+                buf[:r_in].copy_(cur)
+        r_new = get_backend().fold_(buf, r_in, chunk, self.math)
+        Rd[module] = buf[:r_new]
+
+    def _finalize(self, R_raw: torch.Tensor, rows: int, out_dtype: torch.dtype):
+        return get_backend().finalize(R_raw, 1.0 / math.sqrt(rows), self.damping, out_dtype,
+                                      self.math)
+
+    # ------------------------------------------------------------------ factors
+    def get_factors(self) -> Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]]:
+        """Damped factors (R_X, R_G) of every layer with enough data (fp32)."""
+        factors, _ = self._collect_factors(torch.float32)
+        return factors
+
+    def _collect_factors(self, out_dtype: torch.dtype):
+        """get_factors with the output dtype chosen and the finite flags returned."""
+        if self.deferred:
+            self._drain_deferred()
+        factors: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        flags: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        for module in self._linear_layers:
+            R_X_raw = self._R_X.get(module)
+            R_G_raw = self._R_G.get(module)
+            if R_X_raw is None or R_G_raw is None:
+                continue
+            rows_X = self._n_rows_X[module]
+            rows_G = self._n_rows_G[module]
+            if R_X_raw.shape[0] != R_X_raw.shape[1]:
+                logger.debug("get_factors() [%s]: skipped — X factor partial-rank",
+                             _module_tag(module))
+                continue
+            if R_G_raw.shape[0] != R_G_raw.shape[1]:
+                logger.debug("get_factors() [%s]: skipped — G factor partial-rank",
+                             _module_tag(module))
+                continue
+            if self.batched:
+                if rows_X < R_X_raw.shape[1]:
+                    raise IFKFACRankError(
+                        f"Layer {module}: accumulated {rows_X} rows for X, "
+                        f"but need >= n_in={R_X_raw.shape[1]} (batched mode).")
+                if rows_G < R_G_raw.shape[1]:
+                    raise IFKFACRankError(
+                        f"Layer {module}: accumulated {rows_G} rows for δ, "
+                        f"but need >= n_out={R_G_raw.shape[1]} (batched mode).")
+            R_X, fX = self._finalize(R_X_raw, rows_X, out_dtype)
+            R_G, fG = self._finalize(R_G_raw, rows_G, out_dtype)
+            factors[module] = (R_X, R_G)
+            flags[module] = (fX, fG)
+        return factors, flags
+
+    # ------------------------------------------------------------------ modes
+    def _drain_deferred(self):
+        for module in self._linear_layers:
+            if self._raw_X.get(module):
+                X = torch.cat(self._raw_X[module], dim=0)
+                self._fold("X", module, X)
+                self._raw_X[module] = []
+            if self._raw_G.get(module):
+                G = torch.cat(self._raw_G[module], dim=0)
+                self._fold("G", module, G)
+                self._raw_G[module] = []
+
+    def flush(self):
+        """Fold the chunks buffered in batched mode (no-op otherwise).
+
+        Like the reference's bucketed flush (activation_hooks.py:370-457) the
+        result is always an ``n x n`` factor: layers without data start from a
+        zero factor, and zero rows contribute nothing.
+        """
+        if not self.batched:
+            return
+        for side, pending in (("X", self._pending_X), ("G", self._pending_G)):
+            for module in list(pending.keys()):
+                chunks = pending[module]
+                if not chunks:
+                    continue
+                X = chunks[0] if len(chunks) == 1 else torch.cat(chunks, dim=0)
+                self._fold(side, module, X, full_rank_shape=True)
+                pending[module] = []
+
+    # ------------------------------------------------------------------ conv helpers
+    @staticmethod
+    def _unfold_conv_input(x: torch.Tensor, module: nn.Conv2d) -> torch.Tensor:
+        x_unf = F.unfold(x, kernel_size=module.kernel_size, dilation=module.dilation,
+                         padding=module.padding, stride=module.stride)
+        B, C_kk, L = x_unf.shape
+        return x_unf.permute(0, 2, 1).reshape(B * L, C_kk)
+
+    @staticmethod
+    def _reshape_conv_grad(delta: torch.Tensor) -> torch.Tensor:
+        B, C_out, H_out, W_out = delta.shape
+        return delta.permute(0, 2, 3, 1).reshape(B * H_out * W_out, C_out)
+
+    # ------------------------------------------------------------------ hooks
+    def _forward_hook(self, module: nn.Module, input: Tuple[torch.Tensor, ...],
+                      output: torch.Tensor):
+        if not self._enabled:
+            return
+        x = input[0].detach()
+        if isinstance(module, nn.Conv2d):
+            x = self._unfold_conv_input(x, module)
+            if self.max_conv_rows > 0 and x.shape[0] > self.max_conv_rows:
+                idx = torch.randperm(x.shape[0], device=x.device)[:self.max_conv_rows]
+                x = x[idx]
+        elif x.ndim > 2:
+            x = x.reshape(-1, x.shape[-1])
+            if self.max_seq_rows > 0 and x.shape[0] > self.max_seq_rows:
+                idx = torch.randperm(x.shape[0], device=x.device)[:self.max_seq_rows]
+                x = x[idx]
+        if self.augment_bias and isinstance(module, nn.Linear) and module.bias is not None:
+            ones = torch.ones(x.shape[0], 1, device=x.device, dtype=x.dtype)
+            x = torch.cat([x, ones], dim=1)
+        if self.chunk_transform_X is not None:
+            x = self.chunk_transform_X(x)
+
+        if self.deferred:
+            self._raw_X[module].append(x)
+            self._n_rows_X[module] += x.shape[0]
+            if len(self._raw_X[module]) >= self.deferred_window:
+                Xc = torch.cat(self._raw_X[module], dim=0)
+                self._fold("X", module, Xc)
+                self._raw_X[module] = []
+            return
+        if self.batched:
+            self._pending_X[module].append(x)
+            self._n_rows_X[module] += x.shape[0]
+            return
+        self._fold("X", module, x)
+        self._n_rows_X[module] += x.shape[0]
+
+    def _backward_hook(self, module: nn.Module, grad_input: Tuple[torch.Tensor, ...],
+                       grad_output: Tuple[torch.Tensor, ...]):
+        if not self._enabled:
+            return
+        delta = grad_output[0].detach()
+        if isinstance(module, nn.Conv2d):
+            delta = self._reshape_conv_grad(delta)
+        elif delta.ndim > 2:
+            delta = delta.reshape(-1, delta.shape[-1])
+            if self.max_seq_rows > 0 and delta.shape[0] > self.max_seq_rows:
+                idx = torch.randperm(delta.shape[0], device=delta.device)[:self.max_seq_rows]
+                delta = delta[idx]
+        if self.chunk_transform_G is not None:
+            delta = self.chunk_transform_G(delta)
+
+        if self.deferred:
+            self._raw_G[module].append(delta)
+            self._n_rows_G[module] += delta.shape[0]
+            if len(self._raw_G[module]) >= self.deferred_window:
+                Gc = torch.cat(self._raw_G[module], dim=0)
+                self._fold("G", module, Gc)
+                self._raw_G[module] = []
+            return
+        if self.batched:
+            self._pending_G[module].append(delta)
+            self._n_rows_G[module] += delta.shape[0]
+            return
+        self._fold("G", module, delta)
+        self._n_rows_G[module] += delta.shape[0]

@@ -1,0 +1,335 @@
+"""IFKFAC optimizer on the MI355X curvature kernels.
+
+Counterpart of ``IFKFAC`` (ifkfac/ifkfac.py:78-642): same constructor, param
+groups, step schedule, factor-refresh rules (skip / clear / non-finite drop /
+exact EMA blend / bf16 storage), layer classification and per-layer update
+(gradient clipping, heavy-ball momentum, decoupled weight decay, bias through
+the G factor only).  What changes is where the arithmetic happens:
+
+* factor refresh: ``ifk_finalize`` damps, sign-normalises and (with
+  ``use_true_bf16``) rounds each factor to bf16 in one pass and reports
+  finiteness on the device; one host read per refresh collects all flags;
+* after each refresh the factor inverses ``Z = R^{-1}`` are formed once
+  (``ifk_tri_inverse``) and every step applies the four solves as MFMA
+  products with them (``ifk_precondition_apply``);
+* momentum, decay and the weight step are one fused pass
+  (``ifk_momentum_update``).
+"""
+from __future__ import annotations
+
+import logging
+import math
+import time
+import warnings
+from collections import deque
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from ._backend import MATH_BF16, MATH_F32, get_backend
+from .activation_hooks import IFKFACRankError, RawActivationHooks
+from .triangular import solve_math_for
+
+logger = logging.getLogger(__name__)
+
+
+class IFKFAC(torch.optim.Optimizer):
+    """K-FAC with QR-based factors and triangular solves (no explicit Gram inverse).
+
+    Parameters are those of the reference (ifkfac/ifkfac.py:119-136).
+    """
+
+    def __init__(
+        self,
+        model: nn.Module,
+        lr: float = 1e-3,
+        damping: float = 1e-2,
+        factor_update_freq: int = 10,
+        weight_decay: float = 0.0,
+        momentum: float = 0.9,
+        grad_clip: Optional[float] = None,
+        gamma: float = 0.0,
+        max_out_dim: int = 0,
+        augment_bias: bool = False,
+        max_conv_rows: int = 512,
+        max_seq_rows: Optional[int] = None,
+        batched_qr: bool = False,
+        deferred_qr: bool = False,
+        use_true_bf16: bool = False,
+    ):
+        self.use_true_bf16 = use_true_bf16
+        params = []
+        for module in model.modules():
+            if isinstance(module, (nn.Linear, nn.Conv2d)):
+                params.append({"params": list(module.parameters())})
+        defaults = dict(lr=lr, weight_decay=weight_decay, momentum=momentum)
+        super().__init__(params, defaults)
+
+        self.model = model
+        self.damping = damping
+        self.factor_update_freq = factor_update_freq
+        self.grad_clip = grad_clip
+        self.gamma = gamma
+        self.augment_bias = augment_bias
+        self._math = MATH_BF16 if use_true_bf16 else MATH_F32
+
+        self.hooks = RawActivationHooks(
+            model,
+            damping=damping,
+            max_out_dim=max_out_dim,
+            augment_bias=augment_bias,
+            max_conv_rows=max_conv_rows,
+            max_seq_rows=max_seq_rows,
+            batched=batched_qr,
+            deferred=deferred_qr,
+            math=self._math,
+        )
+        self.hooks.enable()
+
+        self._factors: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        self._inverses: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        self._classic_fallback: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        self._momentum_buffers: Dict[nn.Module, torch.Tensor] = {}
+        self._step_count = 0
+
+        _maxlen = 1000
+        self.timing: Dict[str, deque] = {
+            "factor_compute": deque(maxlen=_maxlen),
+            "precondition": deque(maxlen=_maxlen),
+            "total_step": deque(maxlen=_maxlen),
+        }
+
+    # ------------------------------------------------------------------ factors
+    def _blend(self, R_old: torch.Tensor, R_new: torch.Tensor) -> torch.Tensor:
+        """Factor of [sqrt(g) R_old; sqrt(1-g) R_new] (ifkfac/ifkfac.py:270-278)."""
+        n = R_new.shape[0]
+        buf = (math.sqrt(self.gamma) * R_old.float()).contiguous()
+        X = (math.sqrt(1.0 - self.gamma) * R_new.float()).contiguous()
+        get_backend().fold_(buf, n, X, self._math)
+        return buf
+
+    def _update_factors(self):
+        t0 = time.perf_counter()
+        blend = self.gamma > 0.0 and bool(self._factors)
+        out_dtype = torch.bfloat16 if (self.use_true_bf16 and not blend) else torch.float32
+        try:
+            new_factors, flags = self.hooks._collect_factors(out_dtype)
+        except IFKFACRankError as e:
+            logger.warning("IFKFAC: factor update skipped — %s", e)
+            self.timing["factor_compute"].append(time.perf_counter() - t0)
+            return
+
+        self.hooks.clear()
+
+        clean: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        if new_factors:
+            mods = list(new_factors.keys())
+            ok = torch.cat([torch.cat(flags[m]) for m in mods]).view(-1, 2).cpu()
+            for i, module in enumerate(mods):
+                if not bool(ok[i].all()):
+                    logger.warning("IFKFAC: non-finite R for layer %s — skipping.",
+                                   type(module).__name__)
+                    continue
+                clean[module] = new_factors[module]
+
+        if blend:
+            blended = {}
+            for module, (R_X_new, R_G_new) in clean.items():
+                if module in self._factors:
+                    R_X_old, R_G_old = self._factors[module]
+                    blended[module] = (self._blend(R_X_old, R_X_new),
+                                       self._blend(R_G_old, R_G_new))
+                else:
+                    blended[module] = (R_X_new, R_G_new)
+            clean = blended
+            if self.use_true_bf16:
+                clean = {m: (a.to(torch.bfloat16), b.to(torch.bfloat16))
+                         for m, (a, b) in clean.items()}
+
+        self._factors = clean
+        be = get_backend()
+        self._inverses = {}
+        for module, (R_X, R_G) in clean.items():
+            m = solve_math_for(R_X.dtype)
+            self._inverses[module] = (be.tri_inverse(R_X, m), be.tri_inverse(R_G, m))
+        self.timing["factor_compute"].append(time.perf_counter() - t0)
+
+    # ------------------------------------------------------------------ apply
+    def _get_module_hp(self, module):
+        for group in self.param_groups:
+            if any(p is module.weight for p in group["params"]):
+                return group["lr"], group["weight_decay"], group["momentum"]
+        return None, None, None
+
+    def _nat_grad(self, module: nn.Module, grad_w: torch.Tensor, trim: bool) -> torch.Tensor:
+        Z_X, Z_G = self._inverses[module]
+        if trim:
+            Z_X = Z_X[:-1, :-1]
+        R_X = self._factors[module][0]
+        return get_backend().precondition_apply(grad_w, Z_X, Z_G, solve_math_for(R_X.dtype))
+
+    def _update_param(self, param: torch.Tensor, nat: torch.Tensor, lr: float, wd: float,
+                      mom: float, module: Optional[nn.Module]) -> None:
+        """Clip (if set), momentum (module given and mom > 0), decay, step."""
+        if self.grad_clip is not None:
+            gnorm = nat.norm()
+            if gnorm > self.grad_clip:
+                nat = nat * (self.grad_clip / gnorm)
+        buf = None
+        init = False
+        if module is not None and mom > 0:
+            buf = self._momentum_buffers.get(module)
+            if buf is None:
+                buf = torch.zeros_like(param.data, dtype=torch.float32)
+                self._momentum_buffers[module] = buf
+                init = True
+        W = param.data
+        if W.dtype == torch.float32 and W.is_contiguous():
+            get_backend().momentum_update_(nat, buf, W, lr, mom if buf is not None else 0.0, wd,
+                                           init)
+        else:
+            # non-fp32 or strided parameters: the reference's own tensor ops
+            nat = nat.reshape(W.shape)
+            if buf is not None:
+                buf.mul_(mom).add_(nat)
+                nat = buf
+            if wd > 0:
+                W.mul_(1.0 - lr * wd)
+            W.add_(nat.to(W.dtype), alpha=-lr)
+
+    def _update_bias(self, module: nn.Module, lr: float, wd: float) -> None:
+        if module.bias is None or module.bias.grad is None:
+            return
+        Z_G = self._inverses[module][1]
+        nat_b = get_backend().precondition_bias(module.bias.grad, Z_G)
+        self._update_param(module.bias, nat_b, lr, wd, 0.0, None)
+
+    def _apply_preconditioner_bucketed(self):
+        fast: Dict[tuple, list] = {}
+        slow_modules = []
+        for module in self.hooks.linear_layers:
+            if module.weight.grad is None:
+                continue
+            lr, wd, mom = self._get_module_hp(module)
+            if lr is None:
+                continue
+            if module not in self._factors:
+                slow_modules.append((module, lr, wd, mom))
+                continue
+            R_X, R_G = self._factors[module]
+            weight = module.weight
+            is_linear_2d = isinstance(module, nn.Linear) and weight.dim() == 2
+            needs_trim = self.augment_bias and module.bias is not None
+            if not is_linear_2d or needs_trim:
+                slow_modules.append((module, lr, wd, mom))
+                continue
+            key = (R_X.shape[0], R_G.shape[0], weight.dtype, weight.device)
+            fast.setdefault(key, []).append((module, lr, wd, mom))
+
+        for module, lr, wd, mom in slow_modules:
+            self._apply_preconditioner(module, lr=lr, weight_decay=wd, momentum=mom)
+
+        for (n_in, n_out, _, _), entries in fast.items():
+            try:
+                nats = [self._nat_grad(m, m.weight.grad, False) for m, _, _, _ in entries]
+            except Exception as e:  # same recovery as the reference's bucket failure
+                logger.warning(
+                    "IFKFAC: apply_vered_batched failed for bucket (n_in=%d, n_out=%d, B=%d): "
+                    "%s — falling back to per-layer.", n_in, n_out, len(entries), e)
+                for m, lr, wd, mom in entries:
+                    self._apply_preconditioner(m, lr=lr, weight_decay=wd, momentum=mom)
+                continue
+            for (m, lr, wd, mom), nat in zip(entries, nats):
+                self._update_param(m.weight, nat, lr, wd, mom, m)
+                self._update_bias(m, lr, wd)
+
+    def _apply_preconditioner(self, module: nn.Module, lr: float, weight_decay: float,
+                              momentum: float):
+        weight = module.weight
+        if weight.grad is None:
+            return
+        if module not in self._factors:
+            # plain SGD with decoupled decay; bias untouched (ifkfac/ifkfac.py:443-448)
+            self._update_param(weight, weight.grad, lr, weight_decay, 0.0, None)
+            return
+        grad_w = weight.grad
+        trim = self.augment_bias and module.bias is not None
+        orig_shape = grad_w.shape
+        if grad_w.dim() > 2:
+            grad_w = grad_w.reshape(orig_shape[0], -1)
+        try:
+            nat = self._nat_grad(module, grad_w, trim)
+        except Exception as e:
+            logger.warning("IFKFAC: apply_vered failed for %s (%s) — using raw gradient.",
+                           type(module).__name__, e)
+            nat = grad_w
+        nat = nat.reshape(orig_shape)
+        self._update_param(weight, nat, lr, weight_decay, momentum, module)
+        self._update_bias(module, lr, weight_decay)
+
+    # ------------------------------------------------------------------ step
+    @torch.no_grad()
+    def step(self, closure=None):
+        t_total = time.perf_counter()
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+
+        self._step_count += 1
+        _verbose = self._step_count <= 20
+        if _verbose:
+            print(f"    [IFKFAC step={self._step_count}] entry", flush=True)
+        self.hooks.flush()
+        if _verbose:
+            print(f"    [IFKFAC step={self._step_count}] hooks.flush done", flush=True)
+
+        if self.factor_update_freq == 1:
+            self._update_factors()
+        elif (self._step_count >= self.factor_update_freq
+              and self._step_count % self.factor_update_freq == 0):
+            self._update_factors()
+
+        t_precond = time.perf_counter()
+        self._apply_preconditioner_bucketed()
+        self.timing["precondition"].append(time.perf_counter() - t_precond)
+        self.timing["total_step"].append(time.perf_counter() - t_total)
+        return loss
+
+    # ------------------------------------------------------------------ utilities
+    def get_timing_stats(self) -> Dict[str, Dict[str, float]]:
+        stats: Dict[str, Dict[str, float]] = {}
+        for key, times in self.timing.items():
+            if times:
+                arr = np.array(list(times))
+                stats[key] = {
+                    "mean_ms": float(arr.mean() * 1000),
+                    "p50_ms": float(np.percentile(arr, 50) * 1000),
+                    "p99_ms": float(np.percentile(arr, 99) * 1000),
+                    "total_s": float(arr.sum()),
+                    "count": len(times),
+                }
+        return stats
+
+    def capture(self):
+        return self.hooks.capture()
+
+    def pause_capture(self):
+        self.hooks.pause()
+
+    def resume_capture(self):
+        self.hooks.resume()
+
+    def cleanup(self):
+        self.hooks.remove()
+        self._factors.clear()
+        self._inverses.clear()
+        self._classic_fallback.clear()
+        self._momentum_buffers.clear()
+
+    def __repr__(self) -> str:
+        return (f"IFKFAC(damping={self.damping}, factor_update_freq={self.factor_update_freq}, "
+                f"gamma={self.gamma}, augment_bias={self.augment_bias}, "
+                f"n_layers={len(self.hooks.linear_layers)})")

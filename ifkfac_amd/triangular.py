@@ -1,0 +1,140 @@
+"""Numerical seams of the IFKFAC curvature path, dispatched to the HIP library.
+
+Same functions, argument meaning and fallback behaviour as the reference's
+``ifkfac/triangular.py``; the arithmetic runs in the kernels behind
+include/ifkfac_hip.h:
+
+* ``streaming_tsqr_update`` (triangular.py:246-307) -> ``ifk_tsqr_fold``
+* ``finalize_R``            (triangular.py:386-421) -> ``ifk_finalize``
+* ``apply_vered``           (triangular.py:551-656) -> ``ifk_precondition``
+* ``apply_vered_batched``   (triangular.py:506-544) -> per entry, same kernels
+* ``apply_vered_bias``      (triangular.py:659-705) -> ``ifk_tri_inverse`` +
+  ``ifk_precondition_bias``
+* ``batched_streaming_tsqr_update`` (triangular.py:331-379) and ``tsqr``
+  (triangular.py:150-227) -> ``ifk_tsqr_fold``
+
+Arithmetic modes: fp32 factors are handled with fp32 MFMA.  bf16 factors (the
+``use_true_bf16`` storage) are handled with bf16 MFMA and fp32 accumulation
+unless ``IFKFAC_BF16_SOLVE_MATH=f32`` is set in the environment, which keeps
+fp32 arithmetic on the bf16-valued factors as the reference does.
+"""
+from __future__ import annotations
+
+import logging
+import os
+from typing import Optional
+
+import torch
+
+from ._backend import MATH_BF16, MATH_F32, get_backend
+
+logger = logging.getLogger(__name__)
+
+
+def _bf16_solve_math() -> int:
+    return MATH_F32 if os.environ.get("IFKFAC_BF16_SOLVE_MATH", "").lower() == "f32" else MATH_BF16
+
+
+def solve_math_for(dtype: torch.dtype) -> int:
+    """MFMA arithmetic used for factors of this storage dtype."""
+    return _bf16_solve_math() if dtype == torch.bfloat16 else MATH_F32
+
+
+def _positive_diagonal_R(R: torch.Tensor) -> torch.Tensor:
+    """Scale each row of R by the sign of its diagonal entry (sign 0 -> +1)."""
+    signs = R.diagonal().sign()
+    signs = torch.where(signs == 0, torch.ones_like(signs), signs)
+    return R * signs.unsqueeze(1)
+
+
+def streaming_tsqr_update(running_R: Optional[torch.Tensor], new_chunk: torch.Tensor, *,
+                          math: int = MATH_F32) -> torch.Tensor:
+    """Fold one chunk of rows into the running R factor.
+
+    ``running_R`` is None (no data yet) or the ``(r, n)`` upper-trapezoidal
+    factor from earlier calls; ``new_chunk`` is ``(p_i, n)``.  Returns the
+    ``(min(r + p_i, n), n)`` factor of ``[running_R; new_chunk]`` with a
+    positive diagonal (a fresh tensor, fp32).
+    """
+    p, n = new_chunk.shape
+    buf = torch.zeros((n, n), dtype=torch.float32, device=new_chunk.device)
+    r_in = 0
+    if running_R is not None:
+        r_in = running_R.shape[0]
+        if running_R.shape[1] != n:
+            raise ValueError(f"running_R has {running_R.shape[1]} columns, chunk has {n}")
+        buf[:r_in].copy_(running_R)
+    r_new = get_backend().fold_(buf, r_in, new_chunk, math)
+    return buf[:r_new]
+
+
+def batched_streaming_tsqr_update(running_R: torch.Tensor, new_chunks: torch.Tensor, *,
+                                  math: int = MATH_F32) -> torch.Tensor:
+    """Fold ``new_chunks[i]`` into ``running_R[i]`` for every layer of a bucket.
+
+    ``running_R`` is ``(B, n, n)`` (zeros for layers without data); chunks are
+    ``(B, p, n)``, zero-padded along p.  Zero rows contribute nothing.
+    """
+    B, p, n = new_chunks.shape
+    assert running_R.shape == (B, n, n), \
+        f"running_R shape {tuple(running_R.shape)} != ({B}, {n}, {n})"
+    be = get_backend()
+    out = torch.empty((B, n, n), dtype=torch.float32, device=new_chunks.device)
+    for i in range(B):
+        out[i].copy_(running_R[i])
+        be.fold_(out[i], n, new_chunks[i], math)
+    return out
+
+
+def tsqr(M: torch.Tensor, tile_size: int = 512) -> torch.Tensor:
+    """R factor (positive diagonal) of a tall ``(p, n)`` matrix, ``p >= n``."""
+    p, n = M.shape
+    if p < n:
+        raise ValueError(
+            f"tsqr requires p >= n (got p={p}, n={n}).  "
+            "IFKFAC needs batch_size × seq_len >= layer_input_dim.")
+    buf = torch.zeros((n, n), dtype=torch.float32, device=M.device)
+    get_backend().fold_(buf, 0, M, MATH_F32)
+    return buf
+
+
+def finalize_R(running_R: torch.Tensor, damping: float, *, math: int = MATH_F32) -> torch.Tensor:
+    """Return R_d with R_d^T R_d = running_R^T running_R + damping * I."""
+    R, _ = get_backend().finalize(running_R, 1.0, damping, torch.float32, math)
+    return R
+
+
+def apply_vered(grad_W: torch.Tensor, R_X: torch.Tensor, R_G: torch.Tensor) -> torch.Tensor:
+    """Natural gradient ``(R_G^T R_G)^{-1} grad_W (R_X^T R_X)^{-1}``."""
+    if R_X.dtype == torch.bfloat16 or R_G.dtype == torch.bfloat16:
+        if R_X.shape[0] != R_X.shape[1]:
+            print(f"[apply_vered bf16] SKIP — R_X non-square: "
+                  f"shape={tuple(R_X.shape)}.  Returning raw gradient.", flush=True)
+            return grad_W
+        if R_G.shape[0] != R_G.shape[1]:
+            print(f"[apply_vered bf16] SKIP — R_G non-square: "
+                  f"shape={tuple(R_G.shape)}.  Returning raw gradient.", flush=True)
+            return grad_W
+        nat = get_backend().precondition(grad_W, R_X, R_G, _bf16_solve_math())
+        return nat.to(grad_W.dtype)
+    nat = get_backend().precondition(grad_W, R_X, R_G, MATH_F32)
+    return nat if nat.dtype == grad_W.dtype else nat.to(grad_W.dtype)
+
+
+def apply_vered_batched(grad_W: torch.Tensor, R_X: torch.Tensor, R_G: torch.Tensor) -> torch.Tensor:
+    """``apply_vered`` over a bucket: grad_W (B, n_out, n_in), factors (B, n, n)."""
+    B = grad_W.shape[0]
+    assert R_X.shape[0] == B and R_G.shape[0] == B, \
+        f"batch dims mismatch: grad_W={grad_W.shape[0]}, R_X={R_X.shape[0]}, R_G={R_G.shape[0]}"
+    return torch.stack([apply_vered(grad_W[i], R_X[i], R_G[i]) for i in range(B)], dim=0)
+
+
+def apply_vered_bias(grad_b: torch.Tensor, R_G: torch.Tensor) -> torch.Tensor:
+    """``(R_G^T R_G)^{-1} grad_b`` for a bias gradient of length n_out."""
+    if R_G.dtype == torch.bfloat16 and R_G.shape[0] != R_G.shape[1]:
+        print(f"[apply_vered_bias bf16] SKIP — R_G non-square: "
+              f"shape={tuple(R_G.shape)}.  Returning raw bias gradient.", flush=True)
+        return grad_b
+    be = get_backend()
+    Z_G = be.tri_inverse(R_G, MATH_F32)
+    return be.precondition_bias(grad_b, Z_G).to(grad_b.dtype)

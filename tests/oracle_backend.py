@@ -1,0 +1,71 @@
+"""Test double of ifkfac_amd's backend built on the CPU oracle.
+
+Lets the CPU test suite drive the real host logic of ifkfac_amd (hooks,
+schedule, skip/clear rules, classification, updates) without a GPU.  It is
+installed only by tests (``_backend.set_backend``); the product never
+constructs it.  Each method mirrors the HIP backend's contract on CPU tensors
+and counts its calls so tests can assert how often each seam was used.
+"""
+from __future__ import annotations
+
+import collections
+
+import numpy as np
+import torch
+
+from oracle import ifk_oracle as O
+
+
+def _np(t):
+    return t.detach().to(torch.float64).cpu().numpy()
+
+
+class OracleBackend:
+    name = "oracle"
+
+    def __init__(self):
+        self.calls = collections.Counter()
+
+    def fold_(self, R, r_in, X, math):
+        self.calls["fold"] += 1
+        n = R.shape[1]
+        old = None if r_in == 0 else _np(R[:r_in])
+        new = O.streaming_tsqr_update(old, _np(X))
+        r_new = new.shape[0]
+        R.zero_()
+        R[:r_new] = torch.from_numpy(new).to(R.dtype)
+        return r_new
+
+    def finalize(self, R, scale, damping, out_dtype, math):
+        self.calls["finalize"] += 1
+        Rd = O.finalize_R(_np(R) * scale, damping)
+        out = torch.from_numpy(Rd).float().to(out_dtype)
+        flag = torch.tensor([1 if np.all(np.isfinite(Rd)) else 0], dtype=torch.int32)
+        return out, flag
+
+    def tri_inverse(self, R, math):
+        self.calls["tri_inverse"] += 1
+        return torch.from_numpy(np.linalg.inv(_np(R))).float()
+
+    def precondition(self, grad, R_X, R_G, math):
+        self.calls["precondition"] += 1
+        return torch.from_numpy(O.apply_vered(_np(grad), _np(R_X), _np(R_G))).float()
+
+    def precondition_apply(self, grad, Z_X, Z_G, math):
+        self.calls["precondition_apply"] += 1
+        g, zx, zg = _np(grad), _np(Z_X), _np(Z_G)
+        return torch.from_numpy(zg @ (zg.T @ g) @ zx @ zx.T).float()
+
+    def precondition_bias(self, g, Z_G):
+        self.calls["precondition_bias"] += 1
+        zg = _np(Z_G)
+        return torch.from_numpy(zg @ (zg.T @ _np(g).reshape(-1))).float()
+
+    def momentum_update_(self, nat, buf, W, lr, momentum, weight_decay, buf_init):
+        self.calls["momentum_update"] += 1
+        b = None if (buf is None or buf_init) else buf.detach().cpu().numpy()
+        Wn, bn = O.momentum_step(nat.detach().reshape(W.shape).cpu().float().numpy(), b,
+                                 W.detach().cpu().numpy(), lr, momentum, weight_decay)
+        W.copy_(torch.from_numpy(Wn))
+        if buf is not None and bn is not None:
+            buf.copy_(torch.from_numpy(bn))

@@ -1,0 +1,393 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle.
+
+Tolerances (stated per test):
+  factors   ||R^T R - R_o^T R_o||_F / ||R_o^T R_o||_F <= 4 * kappa(R_o) * eps(storage)
+            (fp32 eps = 1.19e-7).  For bf16 arithmetic the stated bound
+            4 kappa eps_bf16 is vacuous at kappa ~ 1e2, so the test also holds
+            the result to a tighter measured regression bound.
+  nat grad  relative error <= 1e-5 (fp32 mode), <= 2e-2 (bf16 mode), against the
+            oracle's solves on the same factors.
+Inputs are seeded; the kappa-controlled matrices use U diag(s) V^T with Haar
+U, V and log-spaced s (tests/test_bf16_stability.py:23-29 of the reference).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ifk_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+EPS32 = 1.1920929e-07
+EPS_BF16 = 7.8125e-03
+DEV = "cuda"
+
+
+def _gram_rel(R, Ro):
+    R = R.double().cpu().numpy() if isinstance(R, torch.Tensor) else R
+    a = R.T @ R
+    b = Ro.T @ Ro
+    return np.linalg.norm(a - b) / np.linalg.norm(b)
+
+
+def _kappa(Ro):
+    s = np.linalg.svd(Ro, compute_uv=False)
+    return s[0] / max(s[-1], 1e-300)
+
+
+def _rel(a, b):
+    a = a.double().cpu().numpy() if isinstance(a, torch.Tensor) else a
+    return np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300)
+
+
+# --------------------------------------------------------------------------- GEMM engine
+
+
+@pytest.mark.parametrize("math_", [0, 1])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,n,k", [(128, 128, 64), (200, 130, 77), (64, 1000, 4096), (1, 37, 1000)])
+def test_gemm_engine(hip, math_, ta, tb, m, n, k):
+    g = torch.Generator(device=DEV).manual_seed(m * 7 + n + k)
+    A = torch.randn((k, m) if ta else (m, k), device=DEV, generator=g)
+    B = torch.randn((n, k) if tb else (k, n), device=DEV, generator=g).to(torch.bfloat16)
+    opA = A.t() if ta else A
+    opB = B.t() if tb else B
+    if math_ == 1:
+        ref = opA.bfloat16().double() @ opB.double()
+    else:
+        ref = opA.double() @ opB.double()
+    C = hip.gemm(A, B, ta, tb, math_)
+    assert _rel(C, ref.cpu().numpy()) < 2e-6
+
+
+# --------------------------------------------------------------------------- fold
+
+
+def _fold_chunks(hip, chunks, n, math_=0):
+    R = torch.zeros(n, n, device=DEV)
+    r = 0
+    for X in chunks:
+        r = hip.fold_(R, r, X, math_)
+    return R, r
+
+
+@pytest.mark.parametrize("chunks,n", [
+    ([256], 128), ([256], 256), ([256], 10),            # demo MLP layer shapes
+    ([64, 64], 40), ([30, 30, 100], 50), ([5, 7, 3], 20),  # trapezoid growth
+    ([300], 200), ([2000], 256), ([1, 1, 1], 2), ([1], 1),
+    ([512] * 3, 1024), ([100, 1000], 333),
+])
+def test_fold_matches_oracle_fp32(hip, chunks, n):
+    g = torch.Generator(device=DEV).manual_seed(sum(chunks) + n)
+    Xs = [torch.randn(p, n, device=DEV, generator=g) for p in chunks]
+    R, r = _fold_chunks(hip, Xs, n)
+    Ro = None
+    for X in Xs:
+        Ro = O.streaming_tsqr_update(Ro, X.double().cpu().numpy())
+    assert r == Ro.shape[0]
+    Rg = R[:r].double().cpu().numpy()
+    assert np.all(np.diag(Rg) >= 0)
+    assert np.array_equal(np.tril(Rg, -1), np.zeros_like(np.tril(Rg, -1)))
+    assert torch.count_nonzero(R[r:]).item() == 0
+    if r == n:
+        kap = _kappa(Ro)
+        assert _gram_rel(Rg, Ro) <= 4 * kap * EPS32
+        assert np.abs(Rg - Ro).max() / np.abs(Ro).max() < 1e-4
+    else:  # trapezoid: compare the rows directly
+        assert np.abs(Rg - Ro).max() / np.abs(Ro).max() < 1e-4
+
+
+def test_fold_rank_deficient_and_zero_columns(hip):
+    g = torch.Generator(device=DEV).manual_seed(11)
+    X = torch.randn(100, 30, device=DEV, generator=g)
+    X[:, 5] = 0
+    X[:, 17] = 0
+    X[:, 20] = X[:, 3]          # duplicated column
+    R, r = _fold_chunks(hip, [X], 30)
+    Xd = X.double().cpu().numpy()
+    G = Xd.T @ Xd
+    Rg = R.double().cpu().numpy()
+    assert np.linalg.norm(Rg.T @ Rg - G) / np.linalg.norm(G) < 1e-6
+
+
+def test_fold_nan_gives_nonfinite_flag(hip):
+    X = torch.randn(64, 16, device=DEV)
+    X[3, 4] = float("nan")
+    R, r = _fold_chunks(hip, [X], 16)
+    Rd, flag = hip.finalize(R, 1 / 8.0, 1e-2, torch.float32, 0)
+    assert flag.item() == 0
+    X[3, 4] = 1.0
+    R, r = _fold_chunks(hip, [X], 16)
+    Rd, flag = hip.finalize(R, 1 / 8.0, 1e-2, torch.float32, 0)
+    assert flag.item() == 1
+
+
+def test_fold_is_deterministic(hip):
+    X = torch.randn(3000, 700, device=DEV)
+    R1, _ = _fold_chunks(hip, [X], 700, 1)
+    R2, _ = _fold_chunks(hip, [X], 700, 1)
+    assert torch.equal(R1, R2)
+
+
+def test_fold_bf16_math_regression_bound(hip):
+    g = torch.Generator(device=DEV).manual_seed(3)
+    X = torch.randn(4096, 1024, device=DEV, generator=g)
+    R, _ = _fold_chunks(hip, [X], 1024, 1)
+    Ro = O.streaming_tsqr_update(None, X.double().cpu().numpy())
+    e = _gram_rel(R, Ro)
+    assert e <= 4 * _kappa(Ro) * EPS_BF16
+    assert e < 2e-3   # measured regression bound for bf16 MFMA trailing updates
+
+
+# --------------------------------------------------------------------------- finalize
+
+
+@pytest.mark.parametrize("p,n,lam", [(500, 300, 1e-2), (4096, 1024, 1e-2), (64, 64, 1e-3)])
+def test_finalize_matches_closed_form(hip, p, n, lam):
+    g = torch.Generator(device=DEV).manual_seed(p + n)
+    X = torch.randn(p, n, device=DEV, generator=g)
+    R, r = _fold_chunks(hip, [X], n)
+    Rd, flag = hip.finalize(R, 1 / math.sqrt(p), lam, torch.float32, 0)
+    want = O.chol_factor([X.double().cpu().numpy()], p, lam)
+    assert flag.item() == 1
+    assert _gram_rel(Rd, want) <= 4 * _kappa(want) * EPS32
+    Rb, _ = hip.finalize(R, 1 / math.sqrt(p), lam, torch.bfloat16, 0)
+    assert torch.equal(Rb, Rd.to(torch.bfloat16))   # RNE cast of the same fp32 result
+
+
+# --------------------------------------------------------------------------- preconditioning
+
+
+def _factors(p, n, lam, kappa, seed):
+    rng = np.random.default_rng(seed)
+    X = O.kappa_matrix(p, n, kappa, rng)
+    return O.get_factor(O.streaming_tsqr_update(None, X), p, lam)
+
+
+@pytest.mark.parametrize("n_out,n_in", [(32, 16), (256, 128), (1024, 1024), (300, 700), (10, 256)])
+def test_precondition_fp32(hip, n_out, n_in):
+    R_X = _factors(4 * n_in, n_in, 1e-2, 1e2, 1)
+    R_G = _factors(4 * n_out, n_out, 1e-2, 1e1, 2)
+    g = np.random.default_rng(3).normal(0, 0.1, (n_out, n_in))
+    want = O.apply_vered(g, R_X, R_G)
+    nat = hip.precondition(torch.tensor(g, dtype=torch.float32, device=DEV),
+                           torch.tensor(R_X, dtype=torch.float32, device=DEV),
+                           torch.tensor(R_G, dtype=torch.float32, device=DEV), 0)
+    assert _rel(nat, want) <= 1e-5
+
+
+@pytest.mark.parametrize("n_out,n_in", [(32, 16), (256, 128), (1024, 1024), (300, 700)])
+def test_precondition_bf16(hip, n_out, n_in):
+    R_X = O.bf16_round(_factors(4 * n_in, n_in, 1e-2, 1e2, 1).astype(np.float32))
+    R_G = O.bf16_round(_factors(4 * n_out, n_out, 1e-2, 1e1, 2).astype(np.float32))
+    g = np.random.default_rng(3).normal(0, 0.1, (n_out, n_in)).astype(np.float32)
+    want = O.apply_vered(g.astype(np.float64), R_X.astype(np.float64), R_G.astype(np.float64))
+    nat = hip.precondition(torch.tensor(g, device=DEV),
+                           torch.tensor(R_X, device=DEV).to(torch.bfloat16),
+                           torch.tensor(R_G, device=DEV).to(torch.bfloat16), 1)
+    assert _rel(nat, want) <= 2e-2
+    nat32 = hip.precondition(torch.tensor(g, device=DEV),
+                             torch.tensor(R_X, device=DEV).to(torch.bfloat16),
+                             torch.tensor(R_G, device=DEV).to(torch.bfloat16), 0)
+    assert _rel(nat32, want) <= 1e-5     # fp32 arithmetic on bf16 factors: reference regime
+
+
+def test_precondition_kappa_exposed(hip):
+    """kappa(R_damped) ~ kappa(X): X scaled by sqrt(p), lambda below sigma_min^2 / 10."""
+    n, p = 256, 1024
+    rng = np.random.default_rng(7)
+    X = O.kappa_matrix(p, n, 1e2, rng) * math.sqrt(p)
+    R_X = O.get_factor(O.streaming_tsqr_update(None, X), p, 1e-5)
+    R_G = R_X.copy()
+    kap = _kappa(R_X)
+    assert kap > 50
+    g = rng.normal(0, 0.1, (n, n))
+    want = O.apply_vered(g, R_X, R_G)
+    nat = hip.precondition(torch.tensor(g, dtype=torch.float32, device=DEV),
+                           torch.tensor(R_X, dtype=torch.float32, device=DEV),
+                           torch.tensor(R_G, dtype=torch.float32, device=DEV), 0)
+    # forward error of four solves scales with kappa(R)^4 eps in the worst case
+    assert _rel(nat, want) <= 4 * kap ** 2 * EPS32
+
+
+def test_precondition_bias(hip):
+    R_G = _factors(512, 128, 1e-2, 10.0, 5)
+    g = np.random.default_rng(6).standard_normal(128)
+    want = O.apply_vered_bias(g, R_G)
+    Z = hip.tri_inverse(torch.tensor(R_G, dtype=torch.float32, device=DEV), 0)
+    out = hip.precondition_bias(torch.tensor(g, dtype=torch.float32, device=DEV), Z)
+    assert _rel(out, want) <= 1e-5
+
+
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 300, 1000, 2049])
+def test_tri_inverse(hip, n):
+    rng = np.random.default_rng(n)
+    R = np.triu(rng.standard_normal((n, n))) / math.sqrt(n) + 2 * np.eye(n)
+    Z = hip.tri_inverse(torch.tensor(R, dtype=torch.float32, device=DEV), 0)
+    want = np.linalg.inv(R)
+    assert _rel(Z, want) <= 1e-5
+    assert np.all(np.tril(Z.cpu().numpy(), -1) == 0)
+
+
+# --------------------------------------------------------------------------- update
+
+
+@pytest.mark.parametrize("mom,wd,init", [(0.9, 0.0, True), (0.9, 0.01, False), (0.0, 0.1, False)])
+def test_momentum_update(hip, mom, wd, init):
+    rng = np.random.default_rng(8)
+    W = rng.standard_normal((1000, 37)).astype(np.float32)
+    nat = rng.standard_normal((1000, 37)).astype(np.float32)
+    buf = rng.standard_normal((1000, 37)).astype(np.float32)
+    Wt, bt, nt = (torch.tensor(a, device=DEV) for a in (W, buf, nat))
+    hip.momentum_update_(nt, bt if mom > 0 else None, Wt, 0.05, mom, wd, init)
+    Wo, bo = O.momentum_step(nat, None if init else buf, W, 0.05, mom, wd)
+    assert np.allclose(Wt.cpu().numpy(), Wo, rtol=2e-7, atol=2e-7)
+    if mom > 0:
+        assert np.allclose(bt.cpu().numpy(), bo, rtol=2e-7, atol=2e-7)
+
+
+# --------------------------------------------------------------------------- config: Linear 1024->1024
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_config_linear_1024_streaming_path(hip, mode):
+    """8 chunks of X and delta (512 x 1024, stored bf16; kappa 1e2 / 1e1), damping 1e-2,
+    gradient ~ N(0, 1e-2): fold, finalize, four solves; each stage against the oracle."""
+    rng = np.random.default_rng(0)
+    n, p, lam = 1024, 512, 1e-2
+    Xs = [O.bf16_round(O.kappa_matrix(p, n, 1e2, rng).astype(np.float32)) for _ in range(8)]
+    Ds = [O.bf16_round(O.kappa_matrix(p, n, 1e1, rng).astype(np.float32)) for _ in range(8)]
+    grad = rng.normal(0, math.sqrt(1e-2), (n, n)).astype(np.float32)
+    math_ = 0 if mode == "fp32" else 1
+    RX = torch.zeros(n, n, device=DEV)
+    RG = torch.zeros(n, n, device=DEV)
+    rx = rg = 0
+    RXo = RGo = None
+    for X, D in zip(Xs, Ds):
+        rx = hip.fold_(RX, rx, torch.tensor(X, device=DEV).to(torch.bfloat16), math_)
+        rg = hip.fold_(RG, rg, torch.tensor(D, device=DEV).to(torch.bfloat16), math_)
+        RXo = O.streaming_tsqr_update(RXo, X.astype(np.float64))
+        RGo = O.streaming_tsqr_update(RGo, D.astype(np.float64))
+        assert rx == RXo.shape[0] and rg == RGo.shape[0]
+    tol_fold = 4 * _kappa(RXo) * (EPS32 if mode == "fp32" else EPS_BF16)
+    assert _gram_rel(RX, RXo) <= tol_fold
+    out_dt = torch.float32 if mode == "fp32" else torch.bfloat16
+    FX, _ = hip.finalize(RX, 1 / math.sqrt(8 * p), lam, out_dt, math_)
+    FG, _ = hip.finalize(RG, 1 / math.sqrt(8 * p), lam, out_dt, math_)
+    FXo = O.get_factor(RXo, 8 * p, lam)
+    FGo = O.get_factor(RGo, 8 * p, lam)
+    st = EPS32 if mode == "fp32" else EPS_BF16
+    assert _gram_rel(FX.float(), FXo) <= 4 * _kappa(FXo) * st
+    nat = hip.precondition(torch.tensor(grad, device=DEV), FX, FG, math_)
+    if mode == "fp32":
+        want = O.apply_vered(grad.astype(np.float64), FXo, FGo)
+        assert _rel(nat, want) <= 1e-5
+    else:
+        want = O.apply_vered(grad.astype(np.float64), O.bf16_round(FXo.astype(np.float32)).astype(np.float64),
+                             O.bf16_round(FGo.astype(np.float32)).astype(np.float64))
+        assert _rel(nat, want) <= 2e-2
+
+
+# --------------------------------------------------------------------------- bf16_linalg
+
+
+@pytest.mark.parametrize("n", [8, 32, 64, 256, 1000])
+def test_bf16_qr_vs_cholesky_of_gram(hip, n):
+    from ifkfac_amd import bf16_linalg as B
+    g = torch.Generator(device=DEV).manual_seed(n)
+    A = torch.randn(2 * n, n, device=DEV, generator=g).to(torch.bfloat16)
+    R = B.block_householder_qr_bf16(A)
+    assert R.dtype == torch.bfloat16 and R.shape == (n, n)
+    Ad = A.double().cpu().numpy()
+    want = np.linalg.cholesky(Ad.T @ Ad).T
+    assert _rel(R, want) < 2e-2
+    if n <= 32:   # the reference's own algorithm, restated
+        Ro = O.positive_diagonal(O.householder_qr_bf16(Ad.astype(np.float32)).astype(np.float64))
+        assert _rel(R, Ro) < 5e-2
+
+
+@pytest.mark.parametrize("n", [8, 32, 64, 200])
+def test_bf16_trsm_chol_inv(hip, n):
+    from ifkfac_amd import bf16_linalg as B
+    rng = np.random.default_rng(n)
+    R = np.triu(rng.standard_normal((n, n))).astype(np.float32)
+    R += np.diag(np.sign(np.diag(R)))
+    Rb = O.bf16_round(R)
+    Bm = O.bf16_round(rng.standard_normal((n, 4)).astype(np.float32))
+    for upper in (True, False):
+        T = Rb if upper else np.ascontiguousarray(Rb.T)
+        X = B.solve_triangular_bf16(torch.tensor(T, device=DEV).bfloat16(),
+                                    torch.tensor(Bm, device=DEV).bfloat16(), upper=upper)
+        want = np.linalg.solve(T.astype(np.float64), Bm.astype(np.float64))
+        assert _rel(X, want) < 5e-2
+    Z = rng.standard_normal((2 * n, n)).astype(np.float32)
+    S = O.bf16_round(Z.T @ Z + np.eye(n, dtype=np.float32))
+    L = B.cholesky_bf16(torch.tensor(S, device=DEV).bfloat16()).double().cpu().numpy()
+    assert np.linalg.norm(L @ L.T - S) / np.linalg.norm(S) < 2e-2
+    assert np.all(np.triu(L, 1) == 0)
+    Si = B.inv_spd_bf16(torch.tensor(S, device=DEV).bfloat16())
+    assert _rel(Si, np.linalg.inv(S.astype(np.float64))) < 5e-2
+
+
+def test_bf16_linalg_guards(hip):
+    from ifkfac_amd import bf16_linalg as B
+    with pytest.raises(TypeError):
+        B.solve_triangular_bf16(torch.eye(4, device=DEV), torch.ones(4, 1, device=DEV).bfloat16())
+    with pytest.raises(ValueError):
+        B.solve_triangular_bf16(torch.ones(4, 3, device=DEV).bfloat16(),
+                                torch.ones(4, 1, device=DEV).bfloat16())
+    with pytest.raises(AssertionError):
+        B.block_householder_qr_bf16(torch.randn(3, 5, device=DEV).bfloat16())
+
+
+# --------------------------------------------------------------------------- full sizes
+
+
+@pytest.mark.parametrize("p,n,dt", [(16384, 4096, torch.bfloat16), (16384, 11008, torch.bfloat16),
+                                    (8192, 4096, torch.float32)])
+def test_full_size_fold_properties(hip, p, n, dt):
+    """At full layer sizes: for random probes v, ||R v|| = ||X v|| (R^T R = X^T X),
+    R upper triangular with positive diagonal, finalize gives R_d^T R_d = R^T R/p + lam I."""
+    g = torch.Generator(device=DEV).manual_seed(n)
+    X = torch.randn(p, n, device=DEV, generator=g).to(dt)
+    R = torch.zeros(n, n, device=DEV)
+    r = hip.fold_(R, 0, X, 1 if dt == torch.bfloat16 else 0)
+    assert r == n
+    V = torch.randn(n, 16, device=DEV, generator=g, dtype=torch.float64)
+    lhs = (R.double() @ V).norm(dim=0)
+    rhs = (X.double() @ V).norm(dim=0)
+    tol = 2e-3 if dt == torch.bfloat16 else 1e-5
+    assert ((lhs - rhs).abs() / rhs).max().item() < tol
+    d = torch.diagonal(R)
+    assert bool((d > 0).all())
+    assert torch.count_nonzero(torch.tril(R, -1)).item() == 0
+    Rd, flag = hip.finalize(R, 1 / math.sqrt(p), 1e-2, torch.float32, 1)
+    assert flag.item() == 1
+    l2 = (Rd.double() @ V).norm(dim=0) ** 2
+    r2 = (R.double() @ V).norm(dim=0) ** 2 / p + 1e-2 * (V ** 2).sum(0)
+    assert ((l2 - r2).abs() / r2).max().item() < tol
+
+
+def test_full_size_precondition_residual(hip):
+    """4096 -> 11008 layer: R_G^T R_G nat R_X^T R_X reproduces grad.  The factors are
+    damped factors of random data (kappa(R) ~ 5), built by the fold + finalize."""
+    n_in, n_out = 4096, 11008
+    g = torch.Generator(device=DEV).manual_seed(0)
+
+    def factor(n):
+        X = torch.randn(2 * n, n, device=DEV, generator=g)
+        R = torch.zeros(n, n, device=DEV)
+        hip.fold_(R, 0, X, 0)
+        Rd, _ = hip.finalize(R, 1 / math.sqrt(2 * n), 1e-2, torch.float32, 0)
+        return Rd
+
+    RX, RG = factor(n_in), factor(n_out)
+    grad = torch.randn(n_out, n_in, device=DEV, generator=g) * 0.1
+    for math_, dt, tol in ((0, torch.float32, 1e-5), (1, torch.bfloat16, 2e-2)):
+        rx, rg = RX.to(dt), RG.to(dt)
+        nat = hip.precondition(grad, rx, rg, math_)
+        rxd, rgd = rx.double(), rg.double()
+        back = rgd.t() @ (rgd @ nat.double() @ rxd.t()) @ rxd
+        assert ((back - grad.double()).norm() / grad.double().norm()).item() < tol

@@ -1,0 +1,356 @@
+"""Host logic of ifkfac_amd on the CPU, with the oracle-backed test double.
+
+The real IFKFAC / RawActivationHooks code runs; only the numerical seams are
+answered by the oracle (tests/oracle_backend.py).  These tests pin the
+reference's control flow: the factor schedule (ifkfac.py:560-564), skip and
+clear rules (activation_hooks.py:262-311, ifkfac.py:209-237), layer
+classification and per-layer update (ifkfac.py:330-423, :443-519), capture
+controls, batched / deferred modes and the EMA blend (ifkfac.py:261-285).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import ifk_oracle as O
+from oracle_backend import OracleBackend
+
+
+@pytest.fixture
+def be():
+    from ifkfac_amd import _backend
+    b = OracleBackend()
+    prev = _backend.set_backend(b)
+    yield b
+    _backend.set_backend(prev)
+
+
+def _mlp(seed=0, bias=True):
+    torch.manual_seed(seed)
+    return nn.Sequential(nn.Linear(8, 16, bias=bias), nn.ReLU(), nn.Linear(16, 4, bias=bias))
+
+
+def _capture(model, X):
+    """Inputs and output-gradients of every Linear, recorded independently."""
+    acts, grads = {}, {}
+    hs = []
+    for m in model.modules():
+        if isinstance(m, nn.Linear):
+            hs.append(m.register_forward_hook(lambda mod, i, o: acts.__setitem__(mod, i[0].detach().clone())))
+            hs.append(m.register_full_backward_hook(lambda mod, gi, go: grads.__setitem__(mod, go[0].detach().clone())))
+    return acts, grads, hs
+
+
+def test_single_step_matches_oracle(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    X = torch.randn(64, 8, generator=torch.Generator().manual_seed(1))
+    Y = torch.randint(0, 4, (64,), generator=torch.Generator().manual_seed(2))
+    lr, lam = 1e-2, 1e-2
+    opt = IFKFAC(model, lr=lr, damping=lam, factor_update_freq=1, momentum=0.9)
+    acts, grads, hs = _capture(model, X)
+    W0 = {m: (m.weight.detach().clone(), m.bias.detach().clone()) for m in opt.hooks.linear_layers}
+    loss = F.cross_entropy(model(X), Y)
+    opt.zero_grad()
+    loss.backward()
+    gW = {m: (m.weight.grad.clone(), m.bias.grad.clone()) for m in opt.hooks.linear_layers}
+    opt.step()
+    for h in hs:
+        h.remove()
+    for m in opt.hooks.linear_layers:
+        x = acts[m].double().numpy()
+        d = grads[m].double().numpy()
+        R_X = O.get_factor(O.streaming_tsqr_update(None, x), x.shape[0], lam)
+        R_G = O.get_factor(O.streaming_tsqr_update(None, d), d.shape[0], lam)
+        nat = O.apply_vered(gW[m][0].double().numpy(), R_X, R_G)
+        nat_b = O.apply_vered_bias(gW[m][1].double().numpy(), R_G)
+        want_W = W0[m][0].double().numpy() - lr * nat      # momentum buffer starts at nat
+        want_b = W0[m][1].double().numpy() - lr * nat_b    # bias: no momentum
+        assert np.abs(m.weight.detach().double().numpy() - want_W).max() < 1e-5
+        assert np.abs(m.bias.detach().double().numpy() - want_b).max() < 1e-5
+
+
+def test_schedule_every_freq_steps(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=10)
+    X = torch.randn(64, 8)
+    for step in range(1, 26):
+        opt.zero_grad()
+        model(X).pow(2).mean().backward()
+        before = be.calls["finalize"]
+        opt.step()
+        fired = be.calls["finalize"] > before
+        assert fired == O.should_update_factors(step, 10), step
+
+
+def test_narrow_batch_layer_is_skipped_and_gets_plain_sgd(be):
+    """p < n: layer skipped, plain SGD without momentum and without bias update."""
+    from ifkfac_amd import IFKFAC
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(64, 8), nn.ReLU(), nn.Linear(8, 4))
+    opt = IFKFAC(model, lr=0.1, factor_update_freq=1, momentum=0.9)
+    X = torch.randn(16, 64)          # 16 rows < n_in = 64 for the first layer
+    first, second = model[0], model[2]
+    for _ in range(3):
+        W = first.weight.detach().clone()
+        b = first.bias.detach().clone()
+        opt.zero_grad()
+        model(X).pow(2).mean().backward()
+        g = first.weight.grad.clone()
+        opt.step()
+        assert first not in opt._factors and second in opt._factors
+        assert torch.allclose(first.weight, W - 0.1 * g, atol=1e-7)
+        assert torch.equal(first.bias, b)                 # not updated
+        assert first not in opt._momentum_buffers
+        # hooks.clear() after the successful update wiped the partial factor
+        assert opt.hooks._R_X[first] is None
+
+
+def test_non_finite_factor_is_dropped(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=1)
+    X = torch.randn(64, 8)
+    X[3, 2] = float("nan")
+    opt.zero_grad()
+    model(X).pow(2).mean().backward()
+    opt.step()
+    assert model[0] not in opt._factors
+
+
+def test_momentum_and_weight_decay_two_steps(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp(bias=False)
+    lr, mu, wd, lam = 5e-2, 0.9, 0.1, 1e-2
+    opt = IFKFAC(model, lr=lr, damping=lam, factor_update_freq=1, momentum=mu, weight_decay=wd)
+    X = torch.randn(64, 8, generator=torch.Generator().manual_seed(3))
+    layer = model[2]
+    buf = None
+    W = layer.weight.detach().double().numpy().copy()
+    for _ in range(2):
+        acts, grads, hs = _capture(model, X)
+        opt.zero_grad()
+        model(X).pow(2).mean().backward()
+        g = layer.weight.grad.double().numpy()
+        opt.step()
+        for h in hs:
+            h.remove()
+        x, d = acts[layer].double().numpy(), grads[layer].double().numpy()
+        R_X = O.get_factor(O.streaming_tsqr_update(None, x), 64, lam)
+        R_G = O.get_factor(O.streaming_tsqr_update(None, d), 64, lam)
+        nat = O.apply_vered(g, R_X, R_G)
+        buf = nat if buf is None else mu * buf + nat
+        W = W * (1 - lr * wd) - lr * buf
+        assert np.abs(layer.weight.detach().double().numpy() - W).max() < 1e-5
+
+
+def test_grad_clip_scales_natural_gradient(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp(bias=False)
+    opt = IFKFAC(model, lr=1.0, factor_update_freq=1, momentum=0.0, grad_clip=1e-3)
+    X = torch.randn(64, 8)
+    W = [m.weight.detach().clone() for m in opt.hooks.linear_layers]
+    opt.zero_grad()
+    model(X).pow(2).mean().backward()
+    opt.step()
+    for m, w in zip(opt.hooks.linear_layers, W):
+        step = (m.weight.detach() - w).norm().item()
+        assert step == pytest.approx(1e-3, rel=1e-4)
+
+
+def test_capture_controls(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=100)
+    X = torch.randn(64, 8)
+    opt.pause_capture()
+    model(X).sum().backward()
+    assert be.calls["fold"] == 0
+    with opt.capture():
+        model(X).sum().backward()
+    assert be.calls["fold"] == 4           # 2 layers x (X, G)
+    model(X).sum().backward()
+    assert be.calls["fold"] == 4           # paused again after the block
+    opt.resume_capture()
+    model(X).sum().backward()
+    assert be.calls["fold"] == 8
+
+
+def test_max_out_dim_layers_untracked_and_never_updated(be):
+    from ifkfac_amd import IFKFAC
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(8, 16), nn.ReLU(), nn.Linear(16, 40))
+    opt = IFKFAC(model, lr=1e-2, factor_update_freq=1, max_out_dim=32)
+    assert opt.hooks.linear_layers == [model[0]]
+    W = model[2].weight.detach().clone()
+    model(torch.randn(64, 8)).pow(2).mean().backward()
+    opt.step()
+    assert torch.equal(model[2].weight, W)
+
+
+def _factors_for_mode(be, **kw):
+    from ifkfac_amd import RawActivationHooks
+    model = _mlp(seed=4)
+    hooks = RawActivationHooks(model, damping=1e-2, **kw)
+    hooks.enable()
+    g = torch.Generator().manual_seed(5)
+    for _ in range(3):
+        model(torch.randn(16, 8, generator=g)).pow(2).mean().backward()
+    hooks.flush()
+    return {i: f for i, f in enumerate(hooks.get_factors().values())}
+
+
+def test_modes_agree(be):
+    a = _factors_for_mode(be)
+    b = _factors_for_mode(be, batched=True)
+    c = _factors_for_mode(be, deferred=True, deferred_window=2)
+    assert a.keys() == b.keys() == c.keys() and len(a) == 2
+    for i in a:
+        for k in range(2):
+            assert torch.allclose(a[i][k], b[i][k], atol=1e-5)
+            assert torch.allclose(a[i][k], c[i][k], atol=1e-5)
+
+
+def test_batched_and_deferred_are_exclusive(be):
+    from ifkfac_amd import RawActivationHooks
+    with pytest.raises(ValueError):
+        RawActivationHooks(_mlp(), batched=True, deferred=True)
+
+
+def test_batched_rank_error_keeps_state(be):
+    from ifkfac_amd import IFKFAC
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(32, 8))
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=1, batched_qr=True)
+    model(torch.randn(8, 32)).pow(2).mean().backward()
+    opt.step()                                 # 8 rows < 32: IFKFACRankError -> skipped
+    assert opt._factors == {}
+    assert opt.hooks._n_rows_X[model[0]] == 8  # state kept for the next window
+
+
+def test_gamma_blend_is_exact(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp(bias=False)
+    opt = IFKFAC(model, lr=0.0, factor_update_freq=1, gamma=0.5)
+    X1, X2 = torch.randn(64, 8), torch.randn(64, 8)
+    model(X1).pow(2).mean().backward()
+    opt.step()
+    old = {m: f[0].double() for m, f in opt._factors.items()}
+    opt.zero_grad()
+    model(X2).pow(2).mean().backward()
+    fresh = {i: f[0].double() for i, f in enumerate(opt.hooks.get_factors().values())}
+    opt.step()
+    for i, (m, f) in enumerate(opt._factors.items()):
+        R_b = f[0].double()
+        want = 0.5 * old[m].T @ old[m] + 0.5 * fresh[i].T @ fresh[i]
+        assert torch.allclose(R_b.T @ R_b, want, atol=1e-5)
+
+
+def test_true_bf16_stores_rne_bf16_factors(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=1, use_true_bf16=True)
+    X = torch.randn(64, 8)
+    model(X).pow(2).mean().backward()
+    fp32 = {i: f for i, f in enumerate(opt.hooks.get_factors().values())}
+    opt.step()
+    for i, (m, (R_X, R_G)) in enumerate(opt._factors.items()):
+        assert R_X.dtype == torch.bfloat16 and R_G.dtype == torch.bfloat16
+        assert torch.equal(R_X, fp32[i][0].to(torch.bfloat16))
+
+
+def test_conv2d_layer_uses_im2col_rows(be):
+    from ifkfac_amd import IFKFAC
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Conv2d(3, 4, 3), nn.ReLU(), nn.Flatten(), nn.Linear(4 * 6 * 6, 5))
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=1, max_conv_rows=0)
+    model(torch.randn(8, 3, 8, 8)).pow(2).mean().backward()
+    assert opt.hooks._n_rows_X[model[0]] == 8 * 36
+    assert opt.hooks._R_X[model[0]].shape == (27, 27)
+    W = model[0].weight.detach().clone()
+    opt.step()
+    assert model[0] in opt._factors
+    assert model[0].weight.shape == W.shape and not torch.equal(model[0].weight, W)
+
+
+def test_augment_bias_factor_has_extra_column(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=1, augment_bias=True)
+    model(torch.randn(64, 8)).pow(2).mean().backward()
+    opt.step()
+    R_X, _ = opt._factors[model[0]]
+    assert R_X.shape == (9, 9)
+
+
+def test_sequence_inputs_are_subsampled(be):
+    from ifkfac_amd import RawActivationHooks
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(8, 8))
+    hooks = RawActivationHooks(model, max_seq_rows=50)
+    hooks.enable()
+    model(torch.randn(4, 30, 8)).pow(2).mean().backward()
+    assert hooks._n_rows_X[model[0]] == 50 and hooks._n_rows_G[model[0]] == 50
+
+
+def test_timing_and_repr(be):
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=1)
+    model(torch.randn(64, 8)).pow(2).mean().backward()
+    opt.step()
+    stats = opt.get_timing_stats()
+    assert set(stats) == {"factor_compute", "precondition", "total_step"}
+    assert stats["total_step"]["count"] == 1
+    assert repr(opt).startswith("IFKFAC(damping=0.01, factor_update_freq=1")
+    opt.cleanup()
+    assert opt._factors == {} and not opt.hooks.is_enabled
+
+
+# --------------------------------------------------------------------------- reference trajectories
+
+
+def _golden():
+    import os
+    return np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_trajectories.npz"))
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_demo_trajectory_matches_reference_run(be, mode):
+    """Host logic + oracle numerics reproduce the reference's own 100-step run
+    (tests/golden/make_reference_trajectories.py)."""
+    import sys, os, contextlib, io
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import make_reference_trajectories as M
+    from ifkfac_amd import IFKFAC
+    ref = _golden()
+    with contextlib.redirect_stdout(io.StringIO()):
+        losses, final, *_ = M.demo(IFKFAC, mode == "bf16")
+    want = ref[f"demo_{mode}_losses"]
+    assert np.all(np.abs(losses - want) <= 2e-3 * np.abs(want) + 1e-7)
+    assert np.all(np.abs(losses[:10] - want[:10]) <= 1e-5 * np.abs(want[:10]))
+    if mode == "fp32":
+        for i, w in enumerate(final):
+            rw = ref[f"demo_fp32_final_{i}"]
+            assert np.linalg.norm(w - rw) / np.linalg.norm(rw) < 1e-5
+
+
+@pytest.mark.parametrize("name", ["canary", "canary_bias"])
+def test_canary_runs_match_reference_including_divergence(be, name):
+    """The reference's own canary configurations diverge on this torch version;
+    the same host logic reproduces the trajectory up to and including that."""
+    import sys, os, contextlib, io
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import make_reference_trajectories as M
+    from ifkfac_amd import IFKFAC
+    want = _golden()[f"{name}_losses"]
+    with contextlib.redirect_stdout(io.StringIO()), np.errstate(all="ignore"):
+        got = getattr(M, name)(IFKFAC)
+    ok = np.isfinite(want) & (np.abs(want) < 1e3)
+    assert ok.sum() >= 10
+    assert np.all(np.abs(got[ok] - want[ok]) <= 1e-4 * np.abs(want[ok]))
+    assert not np.isfinite(got[-1]) and not np.isfinite(want[-1])

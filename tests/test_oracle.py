@@ -1,0 +1,261 @@
+"""Pins the CPU oracle (oracle/ifk_oracle.py) before anything is checked against it.
+
+Each oracle function is checked against what the mathematics fixes (closed
+forms, uniqueness of the positive-diagonal R factor, exact rational
+arithmetic on tiny inputs, hand-computed rounding cases) and against the
+recipe tests the reference itself ships (tests/test_equivalence.py,
+tests/test_bf16_stability.py of the reference, restated on the oracle).
+A few tests plant a plausible mistake in a copy of an oracle function and
+assert that the same check rejects it, so the checks are shown to bite.
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ifk_oracle as O
+
+# --------------------------------------------------------------------------- bf16
+
+
+def test_bf16_round_hand_cases():
+    one = np.float32(1.0)
+    ulp = np.float32(2.0 ** -7)       # bf16 spacing at 1.0
+    half = np.float32(2.0 ** -8)
+    cases = {
+        1.0: 1.0,
+        float(one + half): 1.0,                      # tie -> even (mantissa 0)
+        float(one + ulp + half): float(one + 2 * ulp),  # tie -> even (mantissa 2)
+        float(one + half + np.float32(2.0 ** -20)): float(one + ulp),  # above the tie
+        -0.0: -0.0,
+        float("inf"): float("inf"),
+        3.4028234663852886e38: float("inf"),         # max fp32 rounds up past bf16 max
+        3.3895313892515355e38: 3.3895313892515355e38,  # bf16 max is exact
+    }
+    for x, want in cases.items():
+        got = float(O.bf16_round(np.array([x], np.float32))[0])
+        assert got == want or (math.isnan(got) and math.isnan(want)), (x, got, want)
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32))[0])
+    assert np.signbit(O.bf16_round(np.array([-0.0], np.float32))[0])
+
+
+def test_bf16_round_matches_torch_bitwise():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * (10.0 ** rng.integers(-30, 30, 100000)),
+                        np.array([1e-40, -1e-41, 6e-39], np.float32)]).astype(np.float32)
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = O.bf16_round(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# --------------------------------------------------------------------------- R factors
+
+
+def test_positive_diagonal_hand_case():
+    R = np.array([[-2.0, 1.0, 3.0], [0.0, 0.0, -5.0], [0.0, 0.0, -1.0]])
+    want = np.array([[2.0, -1.0, -3.0], [0.0, 0.0, -5.0], [0.0, 0.0, 1.0]])
+    assert np.array_equal(O.positive_diagonal(R), want)
+
+
+def _gs_exact(A):
+    """R of Gram-Schmidt in exact rationals, returned as R^T R (sqrt-free form):
+    the Gram matrix A^T A itself, built from Fractions."""
+    m, n = len(A), len(A[0])
+    return [[sum(Fraction(A[k][i]) * Fraction(A[k][j]) for k in range(m)) for j in range(n)]
+            for i in range(n)]
+
+
+def test_fold_tiny_integer_exact_gram():
+    A = [[1, 2, 0], [3, -1, 4], [0, 5, 1], [2, 2, -3], [1, 0, 0]]
+    X = np.array(A, dtype=np.float64)
+    R = O.streaming_tsqr_update(O.streaming_tsqr_update(None, X[:2]), X[2:])
+    G = _gs_exact(A)
+    RtR = R.T @ R
+    for i in range(3):
+        for j in range(3):
+            assert abs(RtR[i, j] - float(G[i][j])) < 1e-12
+    assert np.all(np.diag(R) > 0)
+    assert np.allclose(np.tril(R, -1), 0)
+
+
+@pytest.mark.parametrize("chunks,n", [([64, 64], 40), ([30, 30, 100], 50), ([5, 7, 3], 20),
+                                      ([512] * 3, 96)])
+def test_fold_equals_cholesky_of_gram(chunks, n):
+    rng = np.random.default_rng(1)
+    R = None
+    Xs = []
+    for p in chunks:
+        X = rng.standard_normal((p, n))
+        Xs.append(X)
+        R = O.streaming_tsqr_update(R, X)
+        rows = sum(x.shape[0] for x in Xs)
+        assert R.shape == (min(rows, n), n)
+        if rows >= n:
+            want = O.chol_factor(Xs, 1, 0.0)
+            assert np.abs(R - want).max() < 1e-10 * np.abs(want).max()
+
+
+def test_fold_check_rejects_planted_mistakes():
+    rng = np.random.default_rng(2)
+    X1, X2 = rng.standard_normal((50, 20)), rng.standard_normal((50, 20))
+    want = O.chol_factor([X1, X2], 1, 0.0)
+
+    def no_sign(Rold, X):  # forgets the positive-diagonal normalisation
+        Rn = np.linalg.qr(X, mode="r")
+        return Rn if Rold is None else np.linalg.qr(np.vstack([Rold, Rn]), mode="r")
+
+    def drops_old(Rold, X):  # merges without the running factor
+        return O.positive_diagonal(np.linalg.qr(X, mode="r"))
+
+    for bad in (no_sign, drops_old):
+        R = bad(bad(None, X1), X2)
+        assert np.abs(R - want).max() > 1e-3
+
+
+def test_finalize_and_get_factor_closed_form():
+    rng = np.random.default_rng(3)
+    Xs = [rng.standard_normal((100, 30)) for _ in range(3)]
+    R = None
+    for X in Xs:
+        R = O.streaming_tsqr_update(R, X)
+    lam = 1e-2
+    got = O.get_factor(R, 300, lam)
+    want = O.chol_factor(Xs, 300, lam)
+    assert np.abs(got - want).max() < 1e-12
+    # the check fails for a plausible mistake: damping added as lambda^2
+    bad = O.positive_diagonal(np.linalg.qr(np.vstack([R / math.sqrt(300), lam * np.eye(30)]),
+                                           mode="r"))
+    assert np.abs(bad - want).max() > 1e-4
+    assert O.get_factor(R[:20], 300, lam) is None       # non-square: skipped
+    assert O.get_factor(None, 0, lam) is None
+
+
+# --------------------------------------------------------------------------- solves
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_apply_vered_matches_classic_fp64(seed):
+    """Restates the reference's test_ifkfac_matches_classic_fp64 on the oracle."""
+    rng = np.random.default_rng(seed)
+    p, n_in, n_out, lam = 128, 16, 32, 1e-2
+    X = rng.standard_normal((p, n_in))
+    dY = rng.standard_normal((p, n_out))
+    g = rng.standard_normal((n_out, n_in))
+    R_X = O.get_factor(O.streaming_tsqr_update(None, X), p, lam)
+    R_G = O.get_factor(O.streaming_tsqr_update(None, dY), p, lam)
+    got = O.apply_vered(g, R_X, R_G)
+    want = O.natgrad_closed_form(X, dY, g, lam)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-10
+    # planted mistakes: swapped factor sides, or one transpose dropped
+    bad1 = O.apply_vered(g.T, R_G, R_X).T if n_in == n_out else None
+    bad2 = np.linalg.solve(R_G.T, g) @ np.linalg.inv(R_X.T @ R_X)
+    assert np.linalg.norm(bad2 - want) / np.linalg.norm(want) > 1e-2
+    del bad1
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_apply_vered_fp32_recipe(seed):
+    rng = np.random.default_rng(seed)
+    p, n_in, n_out, lam = 256, 16, 32, 1e-2
+    X = rng.standard_normal((p, n_in)).astype(np.float32)
+    dY = rng.standard_normal((p, n_out)).astype(np.float32)
+    g = rng.standard_normal((n_out, n_in)).astype(np.float32)
+    R_X = O.get_factor(O.streaming_tsqr_update(None, X), p, lam).astype(np.float32)
+    R_G = O.get_factor(O.streaming_tsqr_update(None, dY), p, lam).astype(np.float32)
+    got = O.apply_vered(g, R_X, R_G)
+    want = O.natgrad_closed_form(X.astype(np.float64), dY.astype(np.float64), g.astype(np.float64), lam)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-3
+
+
+def test_bf16_kappa_contrast():
+    """Restates the reference's test_ifkfac_beats_classic_at_bf16_high_kappa."""
+    rng = np.random.default_rng(0)
+    p, n, kappa, lam = 1024, 16, 100.0, 1e-3
+    U = O.haar(p, n, rng)
+    V = O.haar(n, n, rng)
+    s = np.logspace(0, math.log10(kappa), n)
+    X = (U * s) @ V.T
+    dY = rng.standard_normal((p, n))
+    g = rng.standard_normal((n, n))
+    ref = O.natgrad_closed_form(X, dY, g, lam)
+    A = O.bf16_round((X.T @ X / p).astype(np.float32)).astype(np.float64)
+    G = O.bf16_round((dY.T @ dY / p).astype(np.float32)).astype(np.float64)
+    classic = np.linalg.solve(G + lam * np.eye(n), g) @ np.linalg.inv(A + lam * np.eye(n))
+    Xb = O.bf16_round(X.astype(np.float32)).astype(np.float64)
+    Db = O.bf16_round(dY.astype(np.float32)).astype(np.float64)
+    R_X = O.bf16_round(O.get_factor(O.streaming_tsqr_update(None, Xb), p, lam).astype(np.float32))
+    R_G = O.bf16_round(O.get_factor(O.streaming_tsqr_update(None, Db), p, lam).astype(np.float32))
+    ifk = O.apply_vered(g, R_X.astype(np.float64), R_G.astype(np.float64))
+    e_c = np.linalg.norm(classic - ref) / np.linalg.norm(ref)
+    e_i = np.linalg.norm(ifk - ref) / np.linalg.norm(ref)
+    assert e_c > 5 * e_i
+
+
+def test_apply_vered_bias_closed_form():
+    rng = np.random.default_rng(4)
+    D = rng.standard_normal((200, 12))
+    lam = 1e-2
+    R_G = O.get_factor(O.streaming_tsqr_update(None, D), 200, lam)
+    g = rng.standard_normal(12)
+    want = np.linalg.solve(D.T @ D / 200 + lam * np.eye(12), g)
+    assert np.abs(O.apply_vered_bias(g, R_G) - want).max() < 1e-10
+
+
+# --------------------------------------------------------------------------- update rules
+
+
+def test_momentum_step_unrolled():
+    W0 = np.array([1.0, -2.0, 0.5], np.float32)
+    n1 = np.array([0.1, 0.2, -0.3], np.float32)
+    n2 = np.array([-0.5, 0.0, 1.0], np.float32)
+    lr, mu, wd = 0.1, 0.9, 0.01
+    W1, b1 = O.momentum_step(n1, None, W0, lr, mu, wd)
+    W2, b2 = O.momentum_step(n2, b1, W1, lr, mu, wd)
+    # by hand: b1 = n1; W1 = W0 (1 - lr wd) - lr b1; b2 = mu b1 + n2; W2 = W1 (1 - lr wd) - lr b2
+    assert np.allclose(b1, n1, atol=0)
+    assert np.allclose(W1, W0 * (1 - lr * wd) - lr * n1, rtol=1e-6)
+    assert np.allclose(b2, mu * n1 + n2, rtol=1e-6)
+    assert np.allclose(W2, W1 * (1 - lr * wd) - lr * (mu * n1 + n2), rtol=1e-6)
+    # no momentum: plain SGD, no buffer
+    W, b = O.momentum_step(n1, None, W0, lr, 0.0, 0.0)
+    assert b is None and np.allclose(W, W0 - lr * n1, rtol=1e-7)
+
+
+def test_schedule():
+    assert all(O.should_update_factors(s, 1) for s in range(1, 30))
+    hits = [s for s in range(1, 41) if O.should_update_factors(s, 10)]
+    assert hits == [10, 20, 30, 40]
+
+
+# --------------------------------------------------------------------------- bf16_linalg
+
+
+@pytest.mark.parametrize("n", [8, 16])
+def test_bf16_linalg_restatements_tolerance(n):
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((2 * n, n)).astype(np.float32)
+    R = O.householder_qr_bf16(A)
+    Rt = np.linalg.cholesky(A.astype(np.float64).T @ A.astype(np.float64)).T
+    Rn = O.positive_diagonal(R.astype(np.float64))
+    assert np.linalg.norm(Rn - Rt) / np.linalg.norm(Rt) < 5e-2
+    S = A.T @ A + np.eye(n, dtype=np.float32)
+    L = O.cholesky_bf16(S)
+    assert np.linalg.norm(L @ L.T - S) / np.linalg.norm(S) < 5e-2
+    Rtri = np.triu(rng.standard_normal((n, n))).astype(np.float32)
+    Rtri += np.diag(np.sign(np.diag(Rtri)))
+    B = rng.standard_normal((n, 3)).astype(np.float32)
+    X = O.solve_triangular_bf16(Rtri, B, upper=True)
+    Xt = np.linalg.solve(Rtri.astype(np.float64), B)
+    assert np.linalg.norm(X - Xt) / np.linalg.norm(Xt) < 1e-1
+    Ai = O.inv_spd_bf16(S)
+    St = np.linalg.inv(S.astype(np.float64))
+    assert np.linalg.norm(Ai - St) / np.linalg.norm(St) < 1e-1
+
+
+def test_kappa_matrix_condition():
+    rng = np.random.default_rng(6)
+    X = O.kappa_matrix(512, 256, 100.0, rng)
+    s = np.linalg.svd(X, compute_uv=False)
+    assert abs(s[0] - 1.0) < 1e-10 and abs(s[-1] - 0.01) < 1e-12
