@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""Benchmark of the IFKFAC curvature hot path on one MI355X.
+
+One step = one factor update plus one preconditioned weight update for a
+single Linear layer, exactly the work IFKFAC.step does for that layer with
+factor_update_freq=1 in bf16 mode:
+
+  fold X (p x n_in) and delta (p x n_out) into fresh R factors   (hooks)
+  finalize both: scale 1/sqrt(p), damping, positive diagonal, bf16 (get_factors)
+  triangular inverses of both bf16 factors                       (solve setup)
+  nat = (R_G^T R_G)^-1 grad (R_X^T R_X)^-1                       (four solves)
+  heavy-ball momentum + weight step                              (update)
+
+Default workload: Linear 4096 -> 11008 at p = 16384 rows, inputs resident in
+HBM.  value = algorithmic TFLOP/s of the step, with the algorithmic count
+2 p (n_in^2 + n_out^2) + 2 n_out n_in (n_in + n_out).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+METRIC = "ms per factor-update + precond step per layer; bf16 TFLOP/s vs MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (n_in, n_out, p)
+    "linear_4096x11008_p16384": (4096, 11008, 16384),
+    "linear_4096x4096_p8192": (4096, 4096, 8192),
+    "linear_1024x1024_p4096": (1024, 1024, 4096),
+}
+
+
+def algorithmic_flops(n_in: int, n_out: int, p: int) -> float:
+    return 2.0 * p * (n_in ** 2 + n_out ** 2) + 2.0 * n_out * n_in * (n_in + n_out)
+
+
+def kappa_matrix(p: int, n: int, kappa: float, seed: int, dtype):
+    """p x n with singular values log-spaced from 1 to 1/kappa (Haar-like U, V by
+    CholeskyQR of Gaussian matrices in fp64 on the GPU); setup only."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    k = min(p, n)
+
+    def orth(m):
+        G = torch.randn(m, k, device="cuda", dtype=torch.float64, generator=g)
+        L = torch.linalg.cholesky(G.t() @ G)
+        return torch.linalg.solve_triangular(L, G.t(), upper=False).t()
+
+    U = orth(p)
+    V = orth(n)
+    s = torch.logspace(0, -math.log10(kappa), k, device="cuda", dtype=torch.float64)
+    X = (U * s) @ V.t()
+    del U, V
+    return X.to(dtype).contiguous()
+
+
+def cpu_baseline(sample: str, threads: int):
+    """The reference's CPU call sequence (oracle/ref_recipe.py) timed on host cores."""
+    import torch
+    from oracle import ref_recipe
+    n_in, n_out, p = WORKLOADS[sample]
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(p, n_in, generator=g)
+    D = torch.randn(p, n_out, generator=g)
+    grad = torch.randn(n_out, n_in, generator=g) * 0.1
+    W = torch.randn(n_out, n_in, generator=g) * 0.01
+    t0 = time.perf_counter()
+    ref_recipe.factor_update_precond_step([X], [D], grad, W, None, 1e-3, 0.9, 1e-2, True)
+    dt = time.perf_counter() - t0
+    fl = algorithmic_flops(n_in, n_out, p)
+    return {
+        "value": round(fl / dt / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "ms_per_step": round(dt * 1e3, 1),
+        "sample": (f"one factor-update + precondition step of Linear {n_in}->{n_out} at "
+                   f"p={p} (bf16 factors) through the reference's torch-CPU call sequence "
+                   f"(LAPACK qr/solve_triangular), {threads} threads, "
+                   f"torch {torch.__version__}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="linear_4096x11008_p16384", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", default="linear_4096x4096_p8192", choices=sorted(WORKLOADS))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the curvature path is "
+              "benchmarked on a single MI355X); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from ifkfac_amd import _backend, _lib
+    from ifkfac_amd._backend import MATH_BF16
+
+    be = _backend.get_backend()
+    lib = be.lib
+    n_in, n_out, p = WORKLOADS[args.workload]
+    lam, lr, mom = 1e-2, 1e-3, 0.9
+    torch.cuda.set_device(0)
+
+    X = kappa_matrix(p, n_in, 1e2, 1, torch.bfloat16)
+    D = kappa_matrix(p, n_out, 1e1, 2, torch.bfloat16)
+    gg = torch.Generator(device="cuda").manual_seed(3)
+    grad = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.1
+    W = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.01
+    buf = torch.zeros_like(W)
+    R_X = torch.zeros(n_in, n_in, device="cuda")
+    R_G = torch.zeros(n_out, n_out, device="cuda")
+    scale = 1.0 / math.sqrt(p)
+    phase_names = ["fold_X", "fold_G", "finalize", "tri_inverse", "precondition", "update"]
+
+    def step(first: bool, events=None):
+        def mark(i):
+            if events is not None:
+                events[i].record()
+        mark(0)
+        be.fold_(R_X, 0, X, MATH_BF16)
+        mark(1)
+        be.fold_(R_G, 0, D, MATH_BF16)
+        mark(2)
+        FX, _ = be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16)
+        FG, _ = be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16)
+        mark(3)
+        ZX = be.tri_inverse(FX, MATH_BF16)
+        ZG = be.tri_inverse(FG, MATH_BF16)
+        mark(4)
+        nat = be.precondition_apply(grad, ZX, ZG, MATH_BF16)
+        mark(5)
+        be.momentum_update_(nat, buf, W, lr, mom, 0.0, first)
+        mark(6)
+
+    for i in range(args.warmup):
+        step(i == 0)
+    torch.cuda.synchronize()
+
+    # one untimed step with every GEMM launch bracketed by events: find the
+    # dominant GEMM variant and the per-phase split
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(7)]
+    _lib.check(lib.ifk_profile_begin(-2), "profile_begin")
+    step(False, ev)
+    n = _lib.ctypes.c_int64(0)
+    _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
+    torch.cuda.synchronize()
+    phases = {phase_names[i]: round(ev[i].elapsed_time(ev[i + 1]), 3) for i in range(6)}
+
+    def read_profile(count):
+        recs = []
+        v = _lib.ctypes.c_int(0)
+        ms = _lib.ctypes.c_float(0)
+        fl = _lib.ctypes.c_double(0)
+        by = _lib.ctypes.c_double(0)
+        m_ = _lib.ctypes.c_int64(0)
+        n_ = _lib.ctypes.c_int64(0)
+        k_ = _lib.ctypes.c_int64(0)
+        for i in range(count):
+            _lib.check(lib.ifk_profile_get(i, *(_lib.ctypes.byref(x) for x in
+                                                 (v, ms, fl, by, m_, n_, k_))), "profile_get")
+            recs.append((v.value, ms.value, fl.value, by.value))
+        return recs
+
+    survey = read_profile(n.value)
+    per_variant = {}
+    for vid, ms, fl, by in survey:
+        a = per_variant.setdefault(vid, [0.0, 0, 0.0, 0.0])
+        a[0] += ms
+        a[1] += 1
+        a[2] += fl
+        a[3] += by
+    dominant = max(per_variant, key=lambda k: per_variant[k][0])
+
+    # timed region: the dominant variant's launches carry event pairs
+    torch.cuda.synchronize()
+    _lib.check(lib.ifk_profile_begin(dominant), "profile_begin")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(False)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
+    recs = read_profile(n.value)
+
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    flops = algorithmic_flops(n_in, n_out, p)
+    value = flops / (ms_per_step * 1e-3) / 1e12
+
+    tot_ms = sum(r[1] for r in recs)
+    tot_fl = sum(r[2] for r in recs)
+    tot_by = sum(r[3] for r in recs)
+    math_bf16 = (dominant >> 4) & 1
+    peak_flops = PEAK_BF16_TFLOPS if math_bf16 else PEAK_F32_TFLOPS
+    intensity = tot_fl / max(tot_by, 1.0)
+    ridge = peak_flops * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if intensity < ridge:
+        achieved = tot_by / (tot_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    else:
+        achieved = tot_fl / (tot_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak_flops,
+                "unit": "TFLOP/s", "frac": round(achieved / peak_flops, 4)}
+    variant_name = ("gemm_kernel<math=%s, A=%s%s, B=%s%s>" % (
+        "bf16" if math_bf16 else "f32", "f32" if not (dominant >> 3) & 1 else "bf16",
+        "(k-contig)" if (dominant >> 2) & 1 else "(mn-contig)",
+        "f32" if not (dominant >> 1) & 1 else "bf16",
+        "(k-contig)" if dominant & 1 else "(mn-contig)"))
+    roof.update({
+        "traffic": None,
+        "kernel": variant_name,
+        "variant_id": dominant,
+        "launches_per_step": round(len(recs) / args.steps, 1),
+        "avg_launch_ms": round(tot_ms / max(len(recs), 1), 4),
+        "share_of_step": round(tot_ms / args.steps / ms_per_step, 3),
+        "algorithmic_flops_per_launch": round(tot_fl / max(len(recs), 1)),
+        "algorithmic_bytes_per_launch": round(tot_by / max(len(recs), 1)),
+    })
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded; X kappa=1e2 and delta kappa=1e1 log-spaced singular values, "
+                "grad ~ N(0, 0.01))",
+        "config": {
+            "workload": f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, "
+                        f"p={p} rows, bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9",
+            "n_in": n_in, "n_out": n_out, "p": p, "algorithmic_gflop_per_step": round(flops / 1e9, 1),
+            "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
+        },
+        "phases_ms": phases,
+        "roofline": roof,
+        "gemm_variants_ms_per_step": {str(k): round(v[0], 3) for k, v in
+                                      sorted(per_variant.items(), key=lambda kv: -kv[1][0])},
+    }
+    if not args.no_cpu_baseline:
+        threads = min(os.cpu_count() or 1, 16)
+        out["cpu_baseline"] = cpu_baseline(args.cpu_sample, threads)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -75,6 +75,11 @@ SIGNATURES = {
     "ifk_gemm": (_c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_f, _c_vp, _c_int, _c_i64,
                           _c_int, _c_vp, _c_int, _c_i64, _c_int, _c_f, _c_vp, _c_i64, _c_vp,
                           _c_sz]),
+    "ifk_profile_begin": (_c_int, [_c_int]),
+    "ifk_profile_end": (_c_int, [_c_i64p]),
+    "ifk_profile_get": (_c_int, [_c_i64, ctypes.POINTER(_c_int), ctypes.POINTER(_c_f),
+                                 ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                 _c_i64p, _c_i64p, _c_i64p]),
 }
 
 _lock = threading.Lock()

@@ -203,4 +203,14 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
   return gemm((hipStream_t)stream, math, m, n, k, alpha, a, b, beta, out_f32(C, ldc), 1, sp);
 }
 
+int ifk_profile_begin(int variant) { return profile_begin(variant); }
+
+int ifk_profile_end(int64_t* n_launches) { return profile_end(n_launches); }
+
+int ifk_profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
+                    int64_t* n, int64_t* k) {
+  GUARD(variant && ms && flops && bytes && m && n && k, "profile_get: null pointer");
+  return profile_get(i, variant, ms, flops, bytes, m, n, k);
+}
+
 }  // extern "C"

@@ -61,6 +61,13 @@ struct SplitScratch {
   size_t floats;
 };
 
+// Launch profiler (see gemm.hip).  variant: gemm_variant_id(), -2 all, -1 off.
+int gemm_variant_id(int math, int adt, bool akc, int bdt, bool bkc);
+int profile_begin(int variant);
+int profile_end(int64_t* n_launches);
+int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
+                int64_t* n, int64_t* k);
+
 int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
          const MatRef& A, const MatRef& B, float beta, const OutRef& C, int batch,
          SplitScratch scratch);

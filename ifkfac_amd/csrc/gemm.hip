@@ -9,7 +9,88 @@
 // transposed in registers on the way in (8 k x 4 mn micro-blocks per thread).
 #include "gemm.h"
 
+#include <mutex>
+#include <vector>
+
 namespace ifk {
+
+// ---------------------------------------------------------------------------
+// Opt-in launch profiler: when armed for a GEMM variant (or for all), each
+// launch of that variant is bracketed by a pair of HIP events recorded on the
+// launching stream, and its algorithmic flops and bytes are kept.  Disarmed,
+// the cost is one integer compare per GEMM call.
+// ---------------------------------------------------------------------------
+struct ProfRec {
+  hipEvent_t beg, end;
+  int variant;
+  int64_t m, n, k;
+  double flops, bytes;
+};
+
+static std::mutex g_prof_mu;
+static int g_prof_variant = -1;  // -1 off, -2 all variants
+static std::vector<ProfRec> g_prof;
+static size_t g_prof_used = 0;
+
+int gemm_variant_id(int math, int adt, bool akc, int bdt, bool bkc) {
+  return (math << 4) | (adt << 3) | ((akc ? 1 : 0) << 2) | (bdt << 1) | (bkc ? 1 : 0);
+}
+
+int profile_begin(int variant) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  g_prof_variant = variant;
+  g_prof_used = 0;
+  return IFK_OK;
+}
+
+int profile_end(int64_t* n_launches) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  g_prof_variant = -1;
+  for (size_t i = 0; i < g_prof_used; ++i) {
+    if (hipEventSynchronize(g_prof[i].end) != hipSuccess) {
+      set_error("profile_end: event synchronisation failed");
+      return IFK_ERR_HIP;
+    }
+  }
+  if (n_launches) *n_launches = (int64_t)g_prof_used;
+  return IFK_OK;
+}
+
+int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
+                int64_t* n, int64_t* k) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  if (i < 0 || (size_t)i >= g_prof_used) {
+    set_error("profile_get: index out of range");
+    return IFK_ERR_INVALID;
+  }
+  const ProfRec& r = g_prof[i];
+  float t = 0.0f;
+  if (hipEventElapsedTime(&t, r.beg, r.end) != hipSuccess) {
+    set_error("profile_get: elapsed time unavailable");
+    return IFK_ERR_HIP;
+  }
+  *variant = r.variant;
+  *ms = t;
+  *flops = r.flops;
+  *bytes = r.bytes;
+  *m = r.m;
+  *n = r.n;
+  *k = r.k;
+  return IFK_OK;
+}
+
+static ProfRec* prof_slot(int vid) {
+  if (g_prof_variant == -1) return nullptr;
+  if (g_prof_variant != -2 && g_prof_variant != vid) return nullptr;
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  if (g_prof_used == g_prof.size()) {
+    ProfRec r{};
+    if (hipEventCreate(&r.beg) != hipSuccess || hipEventCreate(&r.end) != hipSuccess)
+      return nullptr;
+    g_prof.push_back(r);
+  }
+  return &g_prof[g_prof_used++];
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -433,8 +514,25 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     return IFK_ERR_INVALID;
   }
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * splits));
+  const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc);
+  ProfRec* pr = prof_slot(vid);
+  if (pr) {
+    // algorithmic work: 2 M N K (M N K when one operand is triangular), and the
+    // minimal traffic: each operand read once, C read (beta != 0) and written once
+    const double tri = (A.tri != TRI_NONE || B.tri != TRI_NONE) ? 0.5 : 1.0;
+    pr->variant = vid;
+    pr->m = M;
+    pr->n = N;
+    pr->k = K;
+    pr->flops = 2.0 * tri * (double)M * (double)N * (double)K * batch;
+    const double sa = A.dt == DT_F32 ? 4 : 2, sb = B.dt == DT_F32 ? 4 : 2;
+    double cb = (C.c ? 4.0 : 0.0) + (C.cb ? 2.0 : 0.0) + (beta != 0.0f ? 4.0 : 0.0);
+    pr->bytes = ((double)M * K * sa + (double)K * N * sb + (double)M * N * cb) * batch;
+    hipEventRecord(pr->beg, s);
+  }
   if (math == MATH_BF16) launch_a<MATH_BF16>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   else launch_a<MATH_F32>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
+  if (pr) hipEventRecord(pr->end, s);
   int rc = check_launch("gemm");
   if (rc) return rc;
   if (splits > 1) {

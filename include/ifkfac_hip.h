@@ -179,6 +179,21 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
              int trans_b, float beta, float* C, int64_t ldc, void* workspace,
              size_t workspace_bytes);
 
+/*
+ * Measurement support (no counterpart in the reference; used by bench.py).
+ * ifk_profile_begin(v) arms the GEMM launch profiler for GEMM variant v
+ * (v = (math << 4) | (a_dtype << 3) | (a_k_contiguous << 2) | (b_dtype << 1) |
+ * b_k_contiguous), or for every variant with v = -2; v = -1 disarms.  Each
+ * armed launch is bracketed by two HIP events on its own stream.
+ * ifk_profile_end() disarms, waits for the events and returns the number of
+ * launches recorded; ifk_profile_get(i, ...) returns launch i's variant,
+ * duration (ms), algorithmic flops and bytes, and its m, n, k.
+ */
+int ifk_profile_begin(int variant);
+int ifk_profile_end(int64_t* n_launches);
+int ifk_profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
+                    int64_t* n, int64_t* k);
+
 #ifdef __cplusplus
 }
 #endif

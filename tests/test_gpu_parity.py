@@ -372,7 +372,10 @@ def test_full_size_fold_properties(hip, p, n, dt):
 
 def test_full_size_precondition_residual(hip):
     """4096 -> 11008 layer: R_G^T R_G nat R_X^T R_X reproduces grad.  The factors are
-    damped factors of random data (kappa(R) ~ 5), built by the fold + finalize."""
+    damped factors of random data with p = 2n rows, so kappa(A) = kappa(R)^2 <= 30
+    (Marchenko-Pastur edges (1 -+ 1/sqrt(2))^2 plus damping).  A backward-stable
+    solve leaves a residual of order kappa(A) kappa(G) eps_fp32 ~ 1e-4 in fp32
+    arithmetic; bf16 arithmetic is held to the 2e-2 natural-gradient bound."""
     n_in, n_out = 4096, 11008
     g = torch.Generator(device=DEV).manual_seed(0)
 
@@ -385,7 +388,7 @@ def test_full_size_precondition_residual(hip):
 
     RX, RG = factor(n_in), factor(n_out)
     grad = torch.randn(n_out, n_in, device=DEV, generator=g) * 0.1
-    for math_, dt, tol in ((0, torch.float32, 1e-5), (1, torch.bfloat16, 2e-2)):
+    for math_, dt, tol in ((0, torch.float32, 1e-4), (1, torch.bfloat16, 2e-2)):
         rx, rg = RX.to(dt), RG.to(dt)
         nat = hip.precondition(grad, rx, rg, math_)
         rxd, rgd = rx.double(), rg.double()
