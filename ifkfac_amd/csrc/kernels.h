@@ -6,12 +6,15 @@ namespace ifk {
 
 // --- panel kernels (small.hip); b <= 64 -------------------------------------
 int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t ldr, int b,
-                      float tol, float* M1, float* Q1, int* flag);
-int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, int b, float* N, int* flag);
-int launch_panel_hh_fallback(hipStream_t s, const float* Ptop, int64_t ldr, const float* Xp,
-                             int64_t ldx, int64_t pe, int b, float* Y, const int* flag);
-int launch_panel_finish(hipStream_t s, const float* YtY, const float* YtX, float* R, int64_t ldr,
-                        int b, float* T);
+                      float tol, float* U1, float* M1, float* Q1, int* flag);
+int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, const float* U1, int b,
+                      float* N, float* NT, float* T, float* R, int64_t ldr, int* flag);
+int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* Xp, int64_t ldx,
+                             int64_t pe, int b, float* Y, int64_t ldy, float* Yt, float* T,
+                             const int* flag);
+// Tinv = striu(G) + diag(1 + diag G) / 2 (UT transform of a reflector Gram matrix)
+int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,
+                   int64_t ldt);
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
 int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
                       float* Z, int64_t ldz, int safe);

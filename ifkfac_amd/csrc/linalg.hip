@@ -7,8 +7,11 @@
 //   panel's b rows of R and the rows of X, V = [I; Y].  Panel reflectors come
 //   from CholeskyQR2 + Householder reconstruction (parallel over the p rows),
 //   with a column-by-column Householder fallback for panels whose Gram
-//   pivots collapse.  T is always the UT transform of Y, so every applied
-//   block transform is exactly a product of reflectors.  The trailing update
+//   pivots collapse.  Panels are grouped into 512-column outer blocks: a
+//   panel updates the rest of its outer block, and a finished outer block is
+//   applied to all columns beyond it as one block reflector whose T is the UT
+//   transform of the outer Y (exactly a product of the reflectors it holds).
+//   Every block update
 //     W = T^T (R_blk + Y^T C)   R_blk -= W   C -= Y W
 //   runs on MFMA (bf16 operands with fp32 accumulation in MATH_BF16).
 //   A chunk with r_in + p < n leaves an upper-trapezoidal R of r_in + p rows,
@@ -39,6 +42,7 @@ namespace ifk {
   } while (0)
 
 static constexpr float HR_TOL = 1e-6f;
+static constexpr int64_t OUTER_B = 512;
 
 static size_t split_floats(int64_t b, int64_t n) {
   size_t f = (size_t)64 * b * n;
@@ -51,84 +55,125 @@ static size_t split_floats(int64_t b, int64_t n) {
 // ----------------------------------------------------------------------------
 // Fold
 // ----------------------------------------------------------------------------
+static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
+                      int64_t ldz, int math, int safe, float* tmp, SplitScratch sp);
+
 struct FoldWs {
-  float* C;
-  float* Yb;
-  float* Q2;
-  float* Yt;
-  float* W;
-  float* G;
+  float* C;      // p x n working copy of the chunk
+  float* Yo;     // p x OUTER_B: reflector X parts of the current outer block
+  float* Yto;    // p x OUTER_B: Y T of the current inner panel, then of the outer block
+  float* Q2;     // p x b
+  float* W;      // OUTER_B x n
+  float* G1;     // b x b panel scratch
+  float* G2;
+  float* U1;
   float* M1;
   float* Q1;
   float* N;
+  float* NT;
   float* T;
-  float* YtY;
-  float* YtX;
+  float* Go;     // OUTER_B x OUTER_B: Gram of the outer reflectors
+  float* Tio;    // OUTER_B x OUTER_B: UT transform T^{-1}
+  float* To;     // OUTER_B x OUTER_B: T of the outer block
+  float* ttmp;   // triangular-inverse scratch for To
+  SplitScratch tsp;
   int* flag;
   SplitScratch split;
 };
 
 static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
-  const int64_t b = PANEL_B;
+  const int64_t b = PANEL_B, B = OUTER_B;
   w.C = need_C ? a.take<float>((size_t)p * n) : nullptr;
-  w.Yb = a.take<float>((size_t)p * b);
+  w.Yo = a.take<float>((size_t)p * B);
+  w.Yto = a.take<float>((size_t)p * B);
   w.Q2 = a.take<float>((size_t)p * b);
-  w.Yt = a.take<float>((size_t)p * b);
-  w.W = a.take<float>((size_t)b * n);
-  w.G = a.take<float>(b * b);
+  w.W = a.take<float>((size_t)B * n);
+  w.G1 = a.take<float>(b * b);
+  w.G2 = a.take<float>(b * b);
+  w.U1 = a.take<float>(b * b);
   w.M1 = a.take<float>(b * b);
   w.Q1 = a.take<float>(b * b);
   w.N = a.take<float>(b * b);
+  w.NT = a.take<float>(b * b);
   w.T = a.take<float>(b * b);
-  w.YtY = a.take<float>(b * b);
-  w.YtX = a.take<float>(b * b);
+  w.Go = a.take<float>(B * B);
+  w.Tio = a.take<float>(B * B);
+  w.To = a.take<float>(B * B);
+  w.ttmp = a.take<float>((size_t)B * B / 2 + (size_t)TRINV_NB * TRINV_NB * 4);
+  w.tsp.floats = split_floats(TRINV_NB, B);
+  w.tsp.p = a.take<float>(w.tsp.floats);
   w.flag = a.take<int>(64);
-  w.split.floats = split_floats(b, n);
+  w.split.floats = split_floats(B, n);
   w.split.p = a.take<float>(w.split.floats);
 }
 
-// Core of the fold on an fp32 working copy C (p x n, ldc).  R rows
-// [0, r_new) receive the result; with x_tri, C is upper triangular and panel
-// k only involves C rows [0, c1).
+// Apply the block reflector (Y, T) of rows [r0, r0 + kb) to columns [c1, c2):
+//   W = Yt^T C + T^T R_blk,  R_blk -= W,  C -= Y W
+// with Yt = Y T given, Y and Yt of ld ldy, pe rows of C involved.
+static int apply_block(hipStream_t s, int math, const float* Y, const float* Yt, int64_t ldy,
+                       const float* T, int64_t ldt, int64_t kb, float* C, int64_t ldc,
+                       int64_t pe, float* R, int64_t ldr, int64_t r0, int64_t c1, int64_t c2,
+                       FoldWs& w) {
+  const int64_t nt = c2 - c1;
+  if (nt <= 0) return IFK_OK;
+  float* Rb = R + r0 * ldr + c1;
+  RC(gemm(s, math, kb, nt, pe, 1.0f, A_t(Yt, DT_F32, ldy), B_n(C + c1, DT_F32, ldc), 0.0f,
+          out_f32(w.W, nt), 1, w.split));
+  RC(gemm(s, kb > PANEL_B ? math : MATH_F32, kb, nt, kb, 1.0f, A_t(T, DT_F32, ldt, TRI_LOWER),
+          B_n(Rb, DT_F32, ldr), 1.0f, out_f32(w.W, nt), 1, w.split));
+  RC(launch_sub_inplace(s, Rb, ldr, w.W, nt, kb, nt));
+  return gemm(s, math, pe, nt, kb, -1.0f, A_n(Y, DT_F32, ldy), B_n(w.W, DT_F32, nt), 1.0f,
+              out_f32(C + c1, ldc), 1, w.split);
+}
+
+// Core of the fold on an fp32 working copy C (p x n, ldc).  R rows [0, r_new)
+// receive the result.  Two-level blocking: 64-column panels inside 512-column
+// outer blocks; a panel's reflectors update only the rest of its outer block,
+// and each finished outer block is applied to the columns beyond it as one
+// block reflector whose T is the UT transform of the outer Y.  With x_tri, C
+// is upper triangular and a panel ending at column c1 involves C rows [0, c1).
 static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n, float* R,
                      int64_t ldr, int64_t r_new, bool x_tri, int math, FoldWs& w) {
-  for (int64_t c0 = 0; c0 < r_new; c0 += PANEL_B) {
-    const int bk = (int)std::min<int64_t>(PANEL_B, r_new - c0);
-    const int64_t c1 = c0 + bk;
-    const int64_t pe = x_tri ? std::min<int64_t>(p, c1) : p;
-    float* Ptop = R + c0 * ldr + c0;
-    float* Xp = C + c0;
-    // --- panel: CholeskyQR2 + Householder reconstruction ---------------------
-    RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(Xp, DT_F32, ldc), B_n(Xp, DT_F32, ldc), 0.0f,
-            out_f32(w.G, bk), 1, w.split));
-    RC(launch_panel_hr_a(s, w.G, Ptop, ldr, bk, HR_TOL, w.M1, w.Q1, w.flag));
-    RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(Xp, DT_F32, ldc), B_n(w.M1, DT_F32, bk, TRI_UPPER),
-            0.0f, out_f32(w.Q2, bk), 1, w.split));
-    RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(w.Q2, DT_F32, bk), B_n(w.Q2, DT_F32, bk), 0.0f,
-            out_f32(w.G, bk), 1, w.split));
-    RC(launch_panel_hr_b(s, w.G, w.Q1, bk, w.N, w.flag));
-    RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(w.Q2, DT_F32, bk), B_n(w.N, DT_F32, bk, TRI_UPPER),
-            0.0f, out_f32(w.Yb, bk), 1, w.split));
-    RC(launch_panel_hh_fallback(s, Ptop, ldr, Xp, ldc, pe, bk, w.Yb, w.flag));
-    // --- T by the UT transform, new diagonal block ----------------------------
-    RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(w.Yb, DT_F32, bk), B_n(w.Yb, DT_F32, bk), 0.0f,
-            out_f32(w.YtY, bk), 1, w.split));
-    RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(w.Yb, DT_F32, bk), B_n(Xp, DT_F32, ldc), 0.0f,
-            out_f32(w.YtX, bk), 1, w.split));
-    RC(launch_panel_finish(s, w.YtY, w.YtX, Ptop, ldr, bk, w.T));
-    // --- trailing update -------------------------------------------------------
-    const int64_t nt = n - c1;
-    if (nt > 0) {
-      float* Rb = R + c0 * ldr + c1;
-      RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(w.Yb, DT_F32, bk),
-              B_n(w.T, DT_F32, bk, TRI_UPPER), 0.0f, out_f32(w.Yt, bk), 1, w.split));
-      RC(gemm(s, math, bk, nt, pe, 1.0f, A_t(w.Yt, DT_F32, bk), B_n(C + c1, DT_F32, ldc), 0.0f,
-              out_f32(w.W, nt), 1, w.split));
-      RC(gemm(s, MATH_F32, bk, nt, bk, 1.0f, A_t(w.T, DT_F32, bk, TRI_LOWER),
-              B_n(Rb, DT_F32, ldr), 1.0f, out_f32(w.W, nt), 1, w.split));
-      RC(launch_sub_inplace(s, Rb, ldr, w.W, nt, bk, nt));
-      RC(gemm(s, math, pe, nt, bk, -1.0f, A_n(w.Yb, DT_F32, bk), B_n(w.W, DT_F32, nt), 1.0f,
-              out_f32(C + c1, ldc), 1, w.split));
+  const int64_t B = OUTER_B;
+  for (int64_t K0 = 0; K0 < r_new; K0 += B) {
+    const int64_t K1 = std::min<int64_t>(K0 + B, r_new);
+    const int64_t KB = K1 - K0;
+    const int64_t pe_o = x_tri ? std::min<int64_t>(p, K1) : p;
+    if (x_tri) RC(launch_zero(s, w.Yo, B, pe_o, KB));
+    for (int64_t c0 = K0; c0 < K1; c0 += PANEL_B) {
+      const int bk = (int)std::min<int64_t>(PANEL_B, K1 - c0);
+      const int64_t c1 = c0 + bk;
+      const int64_t pe = x_tri ? std::min<int64_t>(p, c1) : p;
+      float* Ptop = R + c0 * ldr + c0;
+      float* Xp = C + c0;
+      float* Y = w.Yo + (c0 - K0);
+      float* Yt = w.Yto + (c0 - K0);
+      // panel: CholeskyQR2 + Householder reconstruction, fallback if flagged
+      RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(Xp, DT_F32, ldc), B_n(Xp, DT_F32, ldc), 0.0f,
+              out_f32(w.G1, bk), 1, w.split));
+      RC(launch_panel_hr_a(s, w.G1, Ptop, ldr, bk, HR_TOL, w.U1, w.M1, w.Q1, w.flag));
+      RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(Xp, DT_F32, ldc),
+              B_n(w.M1, DT_F32, bk, TRI_UPPER), 0.0f, out_f32(w.Q2, bk), 1, w.split));
+      RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(w.Q2, DT_F32, bk), B_n(w.Q2, DT_F32, bk), 0.0f,
+              out_f32(w.G2, bk), 1, w.split));
+      RC(launch_panel_hr_b(s, w.G2, w.Q1, w.U1, bk, w.N, w.NT, w.T, Ptop, ldr, w.flag));
+      RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(w.Q2, DT_F32, bk),
+              B_n(w.N, DT_F32, bk, TRI_UPPER), 0.0f, out_f32(Y, B), 1, w.split));
+      RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(w.Q2, DT_F32, bk),
+              B_n(w.NT, DT_F32, bk, TRI_UPPER), 0.0f, out_f32(Yt, B), 1, w.split));
+      RC(launch_panel_hh_fallback(s, Ptop, ldr, Xp, ldc, pe, bk, Y, B, Yt, w.T, w.flag));
+      // rest of the outer block
+      RC(apply_block(s, math, Y, Yt, B, w.T, bk, bk, C, ldc, pe, R, ldr, c0, c1, K1, w));
+    }
+    if (K1 < n) {
+      // T of the whole outer block from the UT transform of its Gram matrix
+      RC(gemm(s, math, KB, KB, pe_o, 1.0f, A_t(w.Yo, DT_F32, B), B_n(w.Yo, DT_F32, B), 0.0f,
+              out_f32(w.Go, KB), 1, w.split));
+      RC(launch_ut_tinv(s, w.Go, KB, KB, w.Tio, KB));
+      RC(trinv_core(s, w.Tio, DT_F32, KB, KB, w.To, KB, MATH_F32, 0, w.ttmp, w.tsp));
+      RC(gemm(s, math, pe_o, KB, KB, 1.0f, A_n(w.Yo, DT_F32, B), B_n(w.To, DT_F32, KB, TRI_UPPER),
+              0.0f, out_f32(w.Yto, B), 1, w.split));
+      RC(apply_block(s, math, w.Yo, w.Yto, B, w.To, KB, KB, C, ldc, pe_o, R, ldr, K0, K1, n, w));
     }
   }
   return launch_sign_normalize(s, R, ldr, r_new, n);

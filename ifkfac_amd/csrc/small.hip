@@ -1,24 +1,27 @@
 // Single-workgroup kernels on b x b (b <= 64) matrices held in LDS, used by the
 // panel factorisation of the streaming fold and by the blocked triangular
-// inverse.  All matrices are fp32 in LDS with row stride SLD.
+// inverse and Cholesky.  Matrices are fp32, padded to 64 x 64 with the
+// identity beyond b, row stride SLD.  Dense 64-wide work is blocked in 16 x 16
+// tiles: a diagonal tile is factored or inverted in registers by 16 lanes of
+// one wave (values exchanged with v_readlane broadcasts), off-diagonal tiles
+// by LDS products, so a 64 x 64 Cholesky or inverse needs about a dozen
+// workgroup barriers instead of one or more per column.
 //
 // Panel of the fold (columns [c0, c0+b) of the stacked [R; X]):
 //   P = [P_top; X_p], P_top the b x b upper-triangular diagonal block of R,
 //   X_p the p_e x b block of the working X.
-// Reflectors are generated by CholeskyQR2 plus Householder reconstruction:
-//   G1 = P^T P = U1^T U1, M1 = U1^{-1}, Q = P M1           (panel_hr_a + GEMMs)
-//   G2 = Q^T Q = U2^T U2, M2 = U2^{-1}, Q_f = Q M2
-//   S = diag(-sign(Q_f,top)_jj), T_hr = I - Q_f,top S
-//   Y = X_p-part of the reflectors = Q_bottom * N,  N = -M2 S T_hr^{-1}   (panel_hr_b)
-// which gives the unit-diagonal-free TPQRT form V = [I; Y].  When a Cholesky
-// pivot collapses (rank-deficient or ill-conditioned panel) a flag is raised
-// and panel_hh_fallback recomputes Y with column-by-column Householder
-// reflections (LAPACK dlarfg convention), which never breaks down.
-// Either way panel_finish derives T from Y by the UT transform
-//   T^{-1} = striu(V^T V) + diag(V^T V)/2,  V^T V = I + Y^T Y,
-// which makes I - V T V^T exactly the product of the reflectors defined by
-// the columns of V, and forms the new diagonal block
-//   R_new = P_top - T^T (P_top + Y^T X_p).
+// Reflectors come from CholeskyQR2 plus Householder reconstruction:
+//   G1 = P^T P = U1^T U1, M1 = U1^{-1}, Q = P M1                 (panel_hr_a)
+//   G2 = Q^T Q = U2^T U2, M2 = U2^{-1}, Q_f = Q M2               (panel_hr_b)
+//   S = diag(-sign((Q_f,top)_jj)), T = I - Q_f,top S (upper triangular)
+//   Y = Q_bottom N with N = -M2 S T^{-1},  Y T = Q_bottom (-M2 S)
+//   R_new = S U2 U1
+// which is the TPQRT form: V = [I; Y], block reflector I - V T V^T.  When a
+// Cholesky pivot collapses (rank-deficient or ill-conditioned panel) a flag
+// is raised, panel_hr_b leaves R untouched, and panel_hh_fallback recomputes
+// the panel by column-by-column Householder reflections (LAPACK dlarfg
+// convention, never breaks down), with T from the UT transform
+//   T^{-1} = striu(V^T V) + diag(V^T V) / 2,  V^T V = I + Y^T Y.
 #include "common.h"
 #include "kernels.h"
 
@@ -27,32 +30,71 @@ namespace ifk {
 constexpr int SB = 64;        // max panel / block width
 constexpr int SLD = SB + 1;   // LDS row stride (floats)
 constexpr int SNT = 256;
+constexpr int TB = 16;        // register tile
+
+__device__ inline float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
 
 // ---------------------------------------------------------------------------
-// LDS building blocks (called by all SNT threads; contain barriers)
+// LDS building blocks (all called by the whole 256-thread workgroup)
 // ---------------------------------------------------------------------------
 
-// Cholesky with a relative pivot test: a pivot below tol * (original diagonal)
-// flags the panel as unsafe for CholeskyQR.
-__device__ void sm_chol_upper_checked(float* A, int b, float tol, int* bad, float* dg) {
-  const int t = threadIdx.x;
-  for (int j = t; j < b; j += SNT) dg[j] = A[j * SLD + j];
+// Load a b x b block (row stride ld) into a padded 64 x 64 LDS matrix.  With
+// upper set, the strict lower part is zeroed.  The pad beyond b is pad * I.
+__device__ __forceinline__ void sm_load_pad(float* S, const float* g, int64_t ld, int b, bool upper,
+                            float pad = 1.0f) {
+  for (int e = threadIdx.x; e < SB * SB; e += SNT) {
+    const int r = e >> 6, c = e & 63;
+    float v;
+    if (r < b && c < b) v = (upper && r > c) ? 0.0f : g[(int64_t)r * ld + c];
+    else v = (r == c) ? pad : 0.0f;
+    S[r * SLD + c] = v;
+  }
   __syncthreads();
-  for (int j = 0; j < b; ++j) {
-    const float d = A[j * SLD + j];
-    const float sd = sqrtf(fmaxf(d, 1e-30f));
-    if (t == 0) {
-      if (!(d > tol * dg[j]) || !isfinite(d) || !(dg[j] > 0.0f)) *bad = 1;
-    }
-    __syncthreads();
-    for (int c = j + t; c < b; c += SNT) A[j * SLD + c] = (c == j) ? sd : A[j * SLD + c] / sd;
-    __syncthreads();
-    const int rem = b - j - 1;
-    for (int e = t; e < rem * rem; e += SNT) {
-      const int r = j + 1 + e / rem, c = j + 1 + e % rem;
-      if (c >= r) A[r * SLD + c] -= A[j * SLD + r] * A[j * SLD + c];
-    }
-    __syncthreads();
+}
+
+// C = alpha * op(A) op(B) (+ C if acc) for padded 64 x 64 LDS matrices, with
+// op(X) = X^T when the flag is set, on fp32 MFMA: wave w computes the 32 x 32
+// quadrant (w >> 1, w & 1) of C with 32 v_mfma_f32_32x32x2f32 (lane (l32, h)
+// supplies k = 32 h + s to step s).  Zeros of triangular operands are
+// multiplied like any other value.  C may alias A or B: every read completes
+// before the first write.
+template <bool TA, bool TBt>
+__device__ __forceinline__ void sm_gemm64(const float* A, const float* B, float* C, float alpha,
+                                          bool acc) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int r = (wave >> 1) * 32 + l32;   // row of op(A) this lane supplies
+  const int c = (wave & 1) * 32 + l32;    // column of op(B) this lane supplies
+  f32x16 d;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 32; ++s) {
+    const int k = 32 * h + s;
+    const float a = TA ? A[k * SLD + r] : A[r * SLD + k];
+    const float b = TBt ? B[c * SLD + k] : B[k * SLD + c];
+    d = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, d, 0, 0, 0);
+  }
+  __syncthreads();
+  const int row0 = (wave >> 1) * 32, col = (wave & 1) * 32 + l32;
+  float cur[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    cur[i] = acc ? C[(row0 + (i >> 2) * 8 + h * 4 + (i & 3)) * SLD + col] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    C[(row0 + (i >> 2) * 8 + h * 4 + (i & 3)) * SLD + col] = cur[i] + alpha * d[i];
+  __syncthreads();
+}
+
+__device__ __forceinline__ void sm_store(const float* S, float* g, int64_t ld, int b) {
+  for (int e = threadIdx.x; e < b * b; e += SNT) {
+    const int r = e / b, c = e - r * b;
+    g[(int64_t)r * ld + c] = S[r * SLD + c];
   }
 }
 
@@ -62,175 +104,332 @@ __device__ inline float safe_divisor(float d) {
   return fabsf(d) < 1e-7f ? (d < 0.0f ? -1e-7f : 1e-7f) : d;
 }
 
-// Z = U^{-1} for upper-triangular U (b x b); Z's strict lower part is zeroed.
-// One thread per column, back substitution down the column.  With safe set,
-// diagonal divisors follow safe_divisor.
-__device__ void sm_trinv_upper(const float* U, float* Z, int b, bool safe = false) {
+// Upper Cholesky in place (A = U^T U, upper triangle read, strict lower
+// zeroed on exit).  mode 0: a pivot below tol * (its diagonal on entry) or not
+// finite raises *bad (the factorisation continues on a clamped pivot so every
+// thread runs the same steps); mode 1: the pivot rule of cholesky_bf16,
+// max(pivot, 1e-7).
+//
+// Right-looking, blocked by CB = 8 columns.  Every thread factors the 8 x 8
+// diagonal block and inverts it redundantly in registers (no cross-lane
+// traffic on the sequential chain), then owns one column of the block row
+// (U_kr = W_kk^T A_kr with W_kk = U_kk^{-1}) and finally a column of the
+// rank-8 trailing update.  Three barriers per block.
+__device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode) {
+  constexpr int CB = 8;
   const int t = threadIdx.x;
-  for (int e = t; e < b * b; e += SNT) {
-    const int r = e / b, c = e % b;
-    if (r > c) Z[r * SLD + c] = 0.0f;
-  }
-  for (int c = t; c < b; c += SNT) {
-    const float dc = safe ? safe_divisor(U[c * SLD + c]) : U[c * SLD + c];
-    Z[c * SLD + c] = 1.0f / dc;
-    for (int i = c - 1; i >= 0; --i) {
-      float s = 0.0f;
-      for (int k = i + 1; k <= c; ++k) s += U[i * SLD + k] * Z[k * SLD + c];
-      const float di = safe ? safe_divisor(U[i * SLD + i]) : U[i * SLD + i];
-      Z[i * SLD + c] = -s / di;
+  const int lane = t & 63, wave = t >> 6;
+  __shared__ float dg[SB];
+  for (int j = t; j < SB; j += SNT) dg[j] = A[j * SLD + j];
+  __syncthreads();
+  int flag = 0;
+  for (int kb = 0; kb < SB / CB; ++kb) {
+    const int o = kb * CB;
+    float u[CB][CB], w[CB][CB];
+#pragma unroll
+    for (int i = 0; i < CB; ++i)
+#pragma unroll
+      for (int j = i; j < CB; ++j) u[i][j] = A[(o + i) * SLD + o + j];
+    __syncthreads();  // every read of the diagonal block precedes its overwrite
+#pragma unroll
+    for (int k = 0; k < CB; ++k) {
+      const float piv = u[k][k];
+      float pv, rs;
+      if (mode == 0) {
+        if (!(piv > tol * dg[o + k]) || !isfinite(piv)) flag = 1;
+        pv = fmaxf(piv, 1e-30f);
+        rs = __builtin_amdgcn_rsqf(pv);
+        u[k][k] = pv * rs;
+      } else {
+        pv = fmaxf(piv, 1e-7f);
+        u[k][k] = sqrtf(pv);
+        rs = 1.0f / u[k][k];
+      }
+      w[k][k] = rs;
+#pragma unroll
+      for (int j = k + 1; j < CB; ++j) u[k][j] *= rs;
+#pragma unroll
+      for (int i = k + 1; i < CB; ++i)
+#pragma unroll
+        for (int j = i; j < CB; ++j) u[i][j] = fmaf(-u[k][i], u[k][j], u[i][j]);
     }
+    // W = U_kk^{-1}, column by column (upper triangular)
+#pragma unroll
+    for (int j = 1; j < CB; ++j)
+#pragma unroll
+      for (int i = j - 1; i >= 0; --i) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = i + 1; k <= j; ++k) s = fmaf(u[i][k], w[k][j], s);
+        w[i][j] = -s * w[i][i];
+      }
+    if (t < CB * CB) {
+      const int i = t / CB, j = t % CB;
+      float v = 0.0f;
+#pragma unroll
+      for (int a = 0; a < CB; ++a)
+#pragma unroll
+        for (int b = a; b < CB; ++b)
+          if (a == i && b == j) v = u[a][b];
+      A[(o + i) * SLD + o + j] = v;
+    }
+    // block row: U[o:o+CB, c] = W^T A[o:o+CB, c]
+    const int c = o + CB + t;
+    if (c < SB) {
+      float x[CB];
+#pragma unroll
+      for (int i = 0; i < CB; ++i) x[i] = A[(o + i) * SLD + c];
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {
+        float s = 0.0f;
+#pragma unroll
+        for (int m = 0; m <= i; ++m) s = fmaf(w[m][i], x[m], s);
+        A[(o + i) * SLD + c] = s;
+      }
+    }
+    __syncthreads();
+    // rank-CB trailing update A[r][c] -= sum_k U[o+k][r] U[o+k][c] for
+    // r, c >= o + CB on fp32 MFMA: wave w takes the 32 x 32 quadrant
+    // (w >> 1, w & 1); lane (l32, h) supplies k = 4 h + s to step s.  The
+    // strictly lower quadrant and quadrants left of the block are skipped;
+    // within a quadrant the lower-triangle results are discarded.
+    {
+      typedef float f32x16 __attribute__((ext_vector_type(16)));
+      const int lo = o + CB;
+      const int q0 = (wave >> 1) * 32, q1 = (wave & 1) * 32;
+      if (wave != 2 && q0 + 31 >= lo && q1 + 31 >= lo) {
+        const int l32 = lane & 31, h = lane >> 5;
+        const int r = q0 + l32, c = q1 + l32;
+        f32x16 d;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < CB / 2; ++s2) {
+          const int k = o + (CB / 2) * h + s2;
+          const float a = (r >= lo) ? A[k * SLD + r] : 0.0f;
+          const float b = (c >= lo) ? A[k * SLD + c] : 0.0f;
+          d = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, d, 0, 0, 0);
+        }
+        // all reads before any write, so the 16 updates share one LDS latency
+        float cur[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) cur[i] = A[(q0 + (i >> 2) * 8 + h * 4 + (i & 3)) * SLD + c];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int row = q0 + (i >> 2) * 8 + h * 4 + (i & 3);
+          if (row >= lo && c >= row) A[row * SLD + c] = cur[i] - d[i];
+        }
+      }
+    }
+    __syncthreads();
   }
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int r = e >> 6, cc = e & 63;
+    if (r > cc) A[r * SLD + cc] = 0.0f;
+  }
+  if (t == 0 && flag && bad) *bad = 1;
   __syncthreads();
 }
 
-// C = A * B for upper-triangular A and B (result upper).  C must not alias.
-__device__ void sm_mul_uu(const float* A, const float* B, float* C, int b) {
+// Z = U^{-1} for a padded 64 x 64 upper-triangular U (Z strict lower = 0).
+// Tmp: LDS scratch of 32 * 32 floats.  With safe set, diagonal divisors follow
+// safe_divisor.
+__device__ __forceinline__ void sm_trinv64(const float* U, float* Z, float* Tmp, bool safe = false) {
   const int t = threadIdx.x;
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
+  const int lane = t & 63, wave = t >> 6;
+  for (int e = t; e < SB * SB; e += SNT) Z[(e >> 6) * SLD + (e & 63)] = 0.0f;
+  __syncthreads();
+  // 1) the four diagonal 16 x 16 tiles, one wave each, one lane per column
+  {
+    const int o = wave * TB;
+    if (lane < TB) {
+      float z[TB], rd[TB];
+#pragma unroll
+      for (int i = 0; i < TB; ++i) {
+        const float d = U[(o + i) * SLD + o + i];
+        rd[i] = 1.0f / (safe ? safe_divisor(d) : d);  // independent of the chain below
+      }
+#pragma unroll
+      for (int i = TB - 1; i >= 0; --i) {
+        float s = (i == lane) ? 1.0f : 0.0f;
+#pragma unroll
+        for (int k = i + 1; k < TB; ++k) s = fmaf(-U[(o + i) * SLD + o + k], z[k], s);
+        z[i] = s * rd[i];
+      }
+#pragma unroll
+      for (int i = 0; i < TB; ++i) Z[(o + i) * SLD + o + lane] = z[i];
+    }
+  }
+  __syncthreads();
+  // 2) level 16: Z_01 = -Z_00 U_01 Z_11 for tile pairs (0,1) and (2,3)
+  for (int e = t; e < 2 * TB * TB; e += SNT) {
+    const int pr = e / (TB * TB), w = e % (TB * TB);
+    const int i = w / TB, j = w % TB;
+    const int o0 = pr * 2 * TB, o1 = o0 + TB;
     float s = 0.0f;
-    if (i <= j)
-      for (int k = i; k <= j; ++k) s += A[i * SLD + k] * B[k * SLD + j];
-    C[i * SLD + j] = s;
+#pragma unroll
+    for (int k = 0; k < TB; ++k) s += U[(o0 + i) * SLD + o1 + k] * Z[(o1 + k) * SLD + o1 + j];
+    Tmp[pr * TB * TB + i * TB + j] = s;
   }
   __syncthreads();
-}
-
-// G[i][j] += sum_k A[k][i] * A[k][j] over k <= min(i, j) for upper A (i.e.
-// G += A^T A); only G's upper triangle is updated.
-__device__ void sm_add_utu(float* G, const float* A, int b) {
-  const int t = threadIdx.x;
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
-    if (i <= j) {
-      float s = 0.0f;
-      for (int k = 0; k <= i; ++k) s += A[k * SLD + i] * A[k * SLD + j];
-      G[i * SLD + j] += s;
-    }
+  for (int e = t; e < 2 * TB * TB; e += SNT) {
+    const int pr = e / (TB * TB), w = e % (TB * TB);
+    const int i = w / TB, j = w % TB;
+    const int o0 = pr * 2 * TB, o1 = o0 + TB;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < TB; ++k) s += Z[(o0 + i) * SLD + o0 + k] * Tmp[pr * TB * TB + k * TB + j];
+    Z[(o0 + i) * SLD + o1 + j] = -s;
   }
   __syncthreads();
-}
-
-__device__ void sm_load(float* S, const float* g, int64_t ld, int b) {
-  for (int e = threadIdx.x; e < b * b; e += SNT) {
-    const int r = e / b, c = e % b;
-    S[r * SLD + c] = g[(int64_t)r * ld + c];
+  // 3) level 32: Z[0:32, 32:64] = -Z[0:32, 0:32] U[0:32, 32:64] Z[32:64, 32:64]
+  // (the zero lower triangles are part of the unrolled products)
+  for (int e = t; e < 32 * 32; e += SNT) {
+    const int i = e >> 5, j = e & 31;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) s = fmaf(U[i * SLD + 32 + k], Z[(32 + k) * SLD + 32 + j], s);
+    Tmp[i * 32 + j] = s;
   }
   __syncthreads();
-}
-
-__device__ void sm_load_upper(float* S, const float* g, int64_t ld, int b) {
-  for (int e = threadIdx.x; e < b * b; e += SNT) {
-    const int r = e / b, c = e % b;
-    S[r * SLD + c] = (r <= c) ? g[(int64_t)r * ld + c] : 0.0f;
+  for (int e = t; e < 32 * 32; e += SNT) {
+    const int i = e >> 5, j = e & 31;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) s = fmaf(Z[i * SLD + k], Tmp[k * 32 + j], s);
+    Z[i * SLD + 32 + j] = -s;
   }
   __syncthreads();
-}
-
-__device__ void sm_store(const float* S, float* g, int64_t ld, int b) {
-  for (int e = threadIdx.x; e < b * b; e += SNT) {
-    const int r = e / b, c = e % b;
-    g[(int64_t)r * ld + c] = S[r * SLD + c];
-  }
 }
 
 // ---------------------------------------------------------------------------
 // Panel kernels
 // ---------------------------------------------------------------------------
 
-// In: G (b x b, = X_p^T X_p from the GEMM), P_top (in R at ldr).
-// Out: M1 = U1^{-1} (b x b, ld b), Q1 = P_top M1 (b x b, ld b); flag on breakdown.
+// In: G (b x b, = X_p^T X_p), P_top (in R at ldr).
+// Out: U1 (Cholesky factor of P^T P), M1 = U1^{-1}, Q1 = P_top M1 (b x b, ld b);
+//      *flag = 1 on a collapsed pivot, else 0.
 __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G, const float* Ptop,
                                                           int64_t ldr, int b, float tol,
-                                                          float* M1, float* Q1, int* flag) {
+                                                          float* U1, float* M1, float* Q1,
+                                                          int* flag) {
   __shared__ float sG[SB * SLD];
   __shared__ float sP[SB * SLD];
   __shared__ float sM[SB * SLD];
-  __shared__ float dg[SB];
+  __shared__ float sT[32 * 32];
   __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
-  sm_load(sG, G, b, b);
-  sm_load_upper(sP, Ptop, ldr, b);
-  sm_add_utu(sG, sP, b);
-  sm_chol_upper_checked(sG, b, tol, &bad, dg);
-  sm_trinv_upper(sG, sM, b);
+  sm_load_pad(sG, G, b, b, false);
+  sm_load_pad(sP, Ptop, ldr, b, true, 0.0f);
+  sm_gemm64<true, false>(sP, sP, sG, 1.0f, true);  // sG = X_p^T X_p + P_top^T P_top
+  sm_chol64(sG, tol, &bad, 0);                     // sG = U1
+  sm_store(sG, U1, b, b);
+  sm_trinv64(sG, sM, sT);                          // sM = M1
   sm_store(sM, M1, b, b);
-  // Q1 = P_top * M1 (upper * upper) -> reuse sG as output
-  sm_mul_uu(sP, sM, sG, b);
+  sm_gemm64<false, false>(sP, sM, sG, 1.0f, false);  // sG = Q1 = P_top M1
   sm_store(sG, Q1, b, b);
   __syncthreads();
   if (threadIdx.x == 0) *flag = bad;
 }
 
-// In: G2 (b x b, = Q2^T Q2 from the GEMM), Q1 (b x b).
-// Out: N (b x b) with Y = Q2 N; flag raised on breakdown (keeps an earlier flag).
-__global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const float* Q1, int b,
-                                                          float* N, int* flag) {
+// In: G2 (b x b, = Q2^T Q2 with Q2 = X_p M1), Q1, U1.
+// Out: N (Y = Q2 N), NT (Y T = Q2 NT), T (b x b, ld b); R's diagonal block
+// <- S U2 U1 unless the panel is flagged (flag kept once raised).
+__global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const float* Q1,
+                                                          const float* U1, int b, float* N,
+                                                          float* NT, float* T, float* R,
+                                                          int64_t ldr, int* flag) {
   __shared__ float sG[SB * SLD];
   __shared__ float sQ[SB * SLD];
   __shared__ float sM[SB * SLD];
-  __shared__ float dg[SB];
+  __shared__ float sX[SB * SLD];
+  __shared__ float sTmp[32 * 32];
   __shared__ float sgn[SB];
   __shared__ int bad;
-  if (threadIdx.x == 0) bad = 0;
-  sm_load(sG, G2, b, b);
-  sm_load_upper(sQ, Q1, b, b);
-  sm_add_utu(sG, sQ, b);
+  const int t = threadIdx.x;
+  if (t == 0) bad = 0;
+  sm_load_pad(sG, G2, b, b, false);
+  sm_load_pad(sQ, Q1, b, b, true, 0.0f);
+  sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
   // G2 should be close to I; a pivot below 1/4 means the first pass lost too
   // much orthogonality for the reconstruction to be trusted.
-  sm_chol_upper_checked(sG, b, 0.25f, &bad, dg);
-  sm_trinv_upper(sG, sM, b);          // sM = M2
-  sm_mul_uu(sQ, sM, sG, b);           // sG = Q1f = Q1 M2
-  for (int j = threadIdx.x; j < b; j += SNT) sgn[j] = (sG[j * SLD + j] >= 0.0f) ? -1.0f : 1.0f;
+  sm_chol64(sG, 0.25f, &bad, 0);                   // sG = U2
+  sm_trinv64(sG, sM, sTmp);                        // sM = M2
+  sm_gemm64<false, false>(sQ, sM, sX, 1.0f, false);  // sX = Q1f = Q1 M2
+  for (int j = t; j < SB; j += SNT) sgn[j] = (sX[j * SLD + j] >= 0.0f) ? -1.0f : 1.0f;
   __syncthreads();
-  // T_hr = I - Q1f S (in place in sG, upper triangular)
-  for (int e = threadIdx.x; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
-    float v = (i <= j) ? -sG[i * SLD + j] * sgn[j] : 0.0f;
-    if (i == j) v += 1.0f;
-    sG[i * SLD + j] = v;
+  // sX <- T = I - Q1f S (upper triangular; identity in the pad)
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    float v = (i == j) ? 1.0f : 0.0f;
+    if (i < b && j < b && i <= j) v -= sX[i * SLD + j] * sgn[j];
+    sX[i * SLD + j] = v;
   }
   __syncthreads();
-  sm_trinv_upper(sG, sQ, b);          // sQ = T_hr^{-1}
-  // N = -M2 S T_hr^{-1}
-  for (int e = threadIdx.x; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
-    float s = 0.0f;
-    if (i <= j)
-      for (int k = i; k <= j; ++k) s += sM[i * SLD + k] * sgn[k] * sQ[k * SLD + j];
-    N[(int64_t)i * b + j] = -s;
+  // A panel flagged by panel_hr_a keeps R untouched here: the fallback reads
+  // the original diagonal block of R.
+  const bool ok = (bad == 0) && (*flag == 0);
+  __syncthreads();
+  if (t == 0 && bad) *flag = 1;
+  for (int e = t; e < b * b; e += SNT) {
+    const int i = e / b, j = e - i * b;
+    T[e] = sX[i * SLD + j];
+    NT[e] = -sM[i * SLD + j] * sgn[j];
+  }
+  sm_trinv64(sX, sQ, sTmp);                        // sQ = T^{-1}
+  for (int e = t; e < SB * SB; e += SNT) {         // sQ <- S T^{-1}
+    const int k = e >> 6, j = e & 63;
+    sQ[k * SLD + j] *= sgn[k];
   }
   __syncthreads();
-  if (threadIdx.x == 0 && bad) *flag = 1;
+  sm_gemm64<false, false>(sM, sQ, sX, -1.0f, false);  // sX = N = -M2 S T^{-1}
+  for (int e = t; e < b * b; e += SNT) {
+    const int i = e / b, j = e - i * b;
+    N[e] = sX[i * SLD + j];
+  }
+  __syncthreads();
+  sm_load_pad(sQ, U1, b, b, true);
+  sm_gemm64<false, false>(sG, sQ, sX, 1.0f, false);  // sX = U2 U1
+  if (ok) {
+    for (int e = t; e < b * b; e += SNT) {         // R_new = S U2 U1
+      const int i = e / b, j = e - i * b;
+      R[(int64_t)i * ldr + j] = (i <= j) ? sgn[i] * sX[i * SLD + j] : 0.0f;
+    }
+  }
 }
 
 // Robust TPQRT panel by Householder reflections, run only when *flag is set.
-// Y (p_e x b, ld b) is overwritten: it is first loaded with X_p and then
-// reduced in place, column j ending up as the X-part y_j of reflector j.
-__global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(const float* Ptop, int64_t ldr,
+// Overwrites Y (p_e x b, ld ldy) with the reflectors' X parts, Yt with Y T,
+// T (b x b) with the UT-transform T of Y, and R's diagonal block with R_new.
+__global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(float* Ptop, int64_t ldr,
                                                                  const float* Xp, int64_t ldx,
                                                                  int64_t pe, int b, float* Y,
+                                                                 int64_t ldy, float* Yt, float* T,
                                                                  const int* flag) {
   if (*flag == 0) return;
   __shared__ float sP[SB * SLD];
+  __shared__ float sA[SB * SLD];
+  __shared__ float sT[SB * SLD];
+  __shared__ float sTmp[32 * 32];
   __shared__ float red[4][SB];
   __shared__ float wv[SB];
   __shared__ float scal[3];
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  sm_load_upper(sP, Ptop, ldr, b);
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int r = e >> 6, c = e & 63;
+    sP[r * SLD + c] = (r < b && c < b && r <= c) ? Ptop[(int64_t)r * ldr + c] : 0.0f;
+  }
   for (int64_t e = t; e < pe * b; e += SNT) {
     const int64_t r = e / b;
     const int c = (int)(e % b);
-    Y[r * b + c] = Xp[r * ldx + c];
+    Y[r * ldy + c] = Xp[r * ldx + c];
   }
   __syncthreads();
   for (int j = 0; j < b; ++j) {
-    // squared norm of the X part of column j
     float part = 0.0f;
     for (int64_t r = t; r < pe; r += SNT) {
-      const float v = Y[r * b + j];
+      const float v = Y[r * ldy + j];
       part += v * v;
     }
     for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
@@ -240,9 +439,11 @@ __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(const float* Pto
       const float xn2 = red[0][0] + red[1][0] + red[2][0] + red[3][0];
       const float alpha = sP[j * SLD + j];
       if (!(xn2 > 0.0f)) {
-        scal[0] = 0.0f;  // tau
-        scal[1] = 0.0f;  // scale for y
-        scal[2] = alpha;
+        // Nothing below the diagonal: reflect row j alone (v = e_j, tau = 2),
+        // which is what the UT transform of a zero y_j encodes (T_jj = 2).
+        scal[0] = 2.0f;
+        scal[1] = 0.0f;
+        scal[2] = -alpha;
       } else {
         const float nrm = sqrtf(alpha * alpha + xn2);
         const float beta = (alpha >= 0.0f) ? -nrm : nrm;
@@ -253,17 +454,16 @@ __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(const float* Pto
     }
     __syncthreads();
     const float tau = scal[0], sc = scal[1];
-    for (int64_t r = t; r < pe; r += SNT) Y[r * b + j] *= sc;
+    for (int64_t r = t; r < pe; r += SNT) Y[r * ldy + j] *= sc;
     __syncthreads();
-    // w_c = P_top[j][c] + y_j^T X_p[:, c] for c > j
     float acc[SB];
 #pragma unroll
     for (int c = 0; c < SB; ++c) acc[c] = 0.0f;
     for (int64_t r = t; r < pe; r += SNT) {
-      const float y = Y[r * b + j];
+      const float y = Y[r * ldy + j];
 #pragma unroll
       for (int c = 0; c < SB; ++c)
-        if (c > j && c < b) acc[c] += y * Y[r * b + c];
+        if (c > j && c < b) acc[c] += y * Y[r * ldy + c];
     }
 #pragma unroll
     for (int c = 0; c < SB; ++c) {
@@ -281,157 +481,159 @@ __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(const float* Pto
     for (int64_t e = t; e < pe * (b - j - 1); e += SNT) {
       const int64_t r = e / (b - j - 1);
       const int c = j + 1 + (int)(e % (b - j - 1));
-      Y[r * b + c] -= tau * wv[c] * Y[r * b + j];
+      Y[r * ldy + c] -= tau * wv[c] * Y[r * ldy + j];
     }
     if (t == 0) sP[j * SLD + j] = scal[2];
     __syncthreads();
   }
-  // Columns of Y to the right of each reflector hold reduced X values, which
-  // are ~0 after their own step; Y's column j is y_j.  Nothing else to do.
-}
-
-// T from the UT transform of Y and the new diagonal block of R.
-// In: YtY = Y^T Y, YtX = Y^T X_p (b x b each, ld b), P_top in R.
-// Out: T (b x b, ld b); R's diagonal block replaced by R_new (strict lower zeroed).
-__global__ __launch_bounds__(SNT) void panel_finish_kernel(const float* YtY, const float* YtX,
-                                                            float* R, int64_t ldr, int b, float* T) {
-  __shared__ float sA[SB * SLD];
-  __shared__ float sT[SB * SLD];
-  __shared__ float sB[SB * SLD];
-  const int t = threadIdx.x;
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
+  // T from the UT transform of Y
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, c = e & 63;
     float v = 0.0f;
-    if (i < j) v = YtY[i * b + j];
-    else if (i == j) v = 0.5f * (1.0f + YtY[i * b + i]);
-    sA[i * SLD + j] = v;
+    if (i < b && c < b && i <= c) {
+      for (int64_t r = 0; r < pe; ++r) v += Y[r * ldy + i] * Y[r * ldy + c];
+      if (i == c) v = 0.5f * (1.0f + v);
+    } else if (i == c) {
+      v = 1.0f;
+    }
+    sA[i * SLD + c] = v;
   }
   __syncthreads();
-  sm_trinv_upper(sA, sT, b);
-  sm_store(sT, T, b, b);
-  // sA = P_top + Y^T X_p
+  sm_trinv64(sA, sT, sTmp);
   for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
-    const float ptop = (i <= j) ? R[(int64_t)i * ldr + j] : 0.0f;
-    sA[i * SLD + j] = ptop + YtX[i * b + j];
+    const int i = e / b, c = e - i * b;
+    T[e] = sT[i * SLD + c];
+    Ptop[(int64_t)i * ldr + c] = (i <= c) ? sP[i * SLD + c] : 0.0f;
   }
-  __syncthreads();
-  // R_new = P_top - T^T sA  (T upper => T^T lower: (T^T sA)[i][j] = sum_{k<=i} T[k][i] sA[k][j])
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
-    float s = 0.0f;
-    for (int k = 0; k <= i; ++k) s += sT[k * SLD + i] * sA[k * SLD + j];
-    sB[i * SLD + j] = s;
-  }
-  __syncthreads();
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e % b;
-    float* dst = &R[(int64_t)i * ldr + j];
-    if (i <= j) *dst = *dst - sB[i * SLD + j];
-    else *dst = 0.0f;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Diagonal blocks of a blocked triangular inverse: Z_kk = R_kk^{-1} for every
-// nb x nb block on the diagonal of an upper-triangular R (last block may be
-// ragged).  One workgroup per block.  Z's blocks below the diagonal block row
-// are not touched.
-// ---------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t ldr, int64_t n,
-                                                         int nb, float* Z, int64_t ldz, int safe) {
-  __shared__ float sU[SB * SLD];
-  __shared__ float sZ[SB * SLD];
-  const int64_t k0 = (int64_t)blockIdx.x * nb;
-  const int b = (int)((n - k0) < nb ? (n - k0) : nb);
-  for (int e = threadIdx.x; e < b * b; e += SNT) {
-    const int r = e / b, c = e % b;
-    float v = 0.0f;
-    if (r <= c) v = Elem<DT>::load((const typename Elem<DT>::T*)R + (k0 + r) * ldr + k0 + c);
-    sU[r * SLD + c] = v;
-  }
-  __syncthreads();
-  sm_trinv_upper(sU, sZ, b, safe != 0);
-  for (int e = threadIdx.x; e < b * b; e += SNT) {
-    const int r = e / b, c = e % b;
-    Z[(k0 + r) * ldz + k0 + c] = sZ[r * SLD + c];
+  // Yt = Y T, row by row
+  for (int64_t r = t; r < pe; r += SNT) {
+    float yr[SB];
+#pragma unroll
+    for (int c = 0; c < SB; ++c) yr[c] = (c < b) ? Y[r * ldy + c] : 0.0f;
+    for (int c = 0; c < b; ++c) {
+      float s = 0.0f;
+#pragma unroll
+      for (int k = 0; k < SB; ++k)
+        if (k <= c) s += yr[k] * sT[k * SLD + c];
+      Yt[r * ldy + c] = s;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // Diagonal block of a blocked upper Cholesky (bf16_linalg.cholesky_bf16 pivot
 // rule, bf16_linalg.py:258-260): U_jj = sqrt(max(A_jj - sum_k U_kj^2, 1e-7)).
-// In place on an nb x nb block at A (ld), only the upper triangle is read;
-// on exit the block holds U (strict lower part zeroed).
+// In place on a b x b block at A (ld); only the upper triangle is read; on
+// exit the block holds U (strict lower part zeroed).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(SNT) void chol_block_kernel(float* A, int64_t ld, int b) {
   __shared__ float sA[SB * SLD];
-  const int t = threadIdx.x;
-  sm_load_upper(sA, A, ld, b);
-  for (int j = 0; j < b; ++j) {
-    const float d = fmaxf(sA[j * SLD + j], 1e-7f);
-    const float sd = sqrtf(d);
-    __syncthreads();
-    for (int c = j + t; c < b; c += SNT) sA[j * SLD + c] = (c == j) ? sd : sA[j * SLD + c] / sd;
-    __syncthreads();
-    const int rem = b - j - 1;
-    for (int e = t; e < rem * rem; e += SNT) {
-      const int r = j + 1 + e / rem, c = j + 1 + e % rem;
-      if (c >= r) sA[r * SLD + c] -= sA[j * SLD + r] * sA[j * SLD + c];
-    }
-    __syncthreads();
-  }
-  for (int e = t; e < b * b; e += SNT) {
-    const int r = e / b, c = e % b;
+  sm_load_pad(sA, A, ld, b, true);
+  sm_chol64(sA, 0.0f, nullptr, 1);
+  for (int e = threadIdx.x; e < b * b; e += SNT) {
+    const int r = e / b, c = e - r * b;
     A[(int64_t)r * ld + c] = (r <= c) ? sA[r * SLD + c] : 0.0f;
+  }
+}
+
+// UT transform: T^{-1} = striu(G) + diag(1 + diag G) / 2 for a Gram matrix G.
+__global__ void ut_tinv_kernel(const float* G, int64_t ldg, int64_t n, float* Tinv, int64_t ldt) {
+  const int64_t total = n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / n, j = e % n;
+    float v = 0.0f;
+    if (i < j) v = G[i * ldg + j];
+    else if (i == j) v = 0.5f * (1.0f + G[i * ldg + i]);
+    Tinv[i * ldt + j] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Diagonal blocks of a blocked triangular inverse: Z_kk = R_kk^{-1} for every
+// nb x nb block on the diagonal of an upper-triangular R (last block may be
+// ragged).  One workgroup per block.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t ldr, int64_t n,
+                                                         int nb, float* Z, int64_t ldz, int safe) {
+  __shared__ float sU[SB * SLD];
+  __shared__ float sZ[SB * SLD];
+  __shared__ float sT[32 * 32];
+  const int64_t k0 = (int64_t)blockIdx.x * nb;
+  const int b = (int)((n - k0) < nb ? (n - k0) : nb);
+  for (int e = threadIdx.x; e < SB * SB; e += SNT) {
+    const int r = e >> 6, c = e & 63;
+    float v;
+    if (r < b && c < b)
+      v = (r <= c) ? Elem<DT>::load((const typename Elem<DT>::T*)R + (k0 + r) * ldr + k0 + c)
+                   : 0.0f;
+    else
+      v = (r == c) ? 1.0f : 0.0f;
+    sU[r * SLD + c] = v;
+  }
+  __syncthreads();
+  sm_trinv64(sU, sZ, sT, safe != 0);
+  for (int e = threadIdx.x; e < b * b; e += SNT) {
+    const int r = e / b, c = e - r * b;
+    Z[(k0 + r) * ldz + k0 + c] = sZ[r * SLD + c];
   }
 }
 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
+static int check_b(int b, const char* what) {
+  if (b > SB || b < 1) {
+    set_error(std::string(what) + ": block size out of range");
+    return IFK_ERR_INVALID;
+  }
+  return IFK_OK;
+}
+
 int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t ldr, int b,
-                      float tol, float* M1, float* Q1, int* flag) {
-  hipLaunchKernelGGL(panel_hr_a_kernel, dim3(1), dim3(SNT), 0, s, G, Ptop, ldr, b, tol, M1, Q1,
-                     flag);
+                      float tol, float* U1, float* M1, float* Q1, int* flag) {
+  if (int rc = check_b(b, "panel_hr_a")) return rc;
+  hipLaunchKernelGGL(panel_hr_a_kernel, dim3(1), dim3(SNT), 0, s, G, Ptop, ldr, b, tol, U1, M1,
+                     Q1, flag);
   return check_launch("panel_hr_a");
 }
 
-int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, int b, float* N,
-                      int* flag) {
-  hipLaunchKernelGGL(panel_hr_b_kernel, dim3(1), dim3(SNT), 0, s, G2, Q1, b, N, flag);
+int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, const float* U1, int b,
+                      float* N, float* NT, float* T, float* R, int64_t ldr, int* flag) {
+  if (int rc = check_b(b, "panel_hr_b")) return rc;
+  hipLaunchKernelGGL(panel_hr_b_kernel, dim3(1), dim3(SNT), 0, s, G2, Q1, U1, b, N, NT, T, R, ldr,
+                     flag);
   return check_launch("panel_hr_b");
 }
 
-int launch_panel_hh_fallback(hipStream_t s, const float* Ptop, int64_t ldr, const float* Xp,
-                             int64_t ldx, int64_t pe, int b, float* Y, const int* flag) {
-  hipLaunchKernelGGL(panel_hh_fallback_kernel, dim3(1), dim3(SNT), 0, s, Ptop, ldr, Xp, ldx, pe,
-                     b, Y, flag);
+int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* Xp, int64_t ldx,
+                             int64_t pe, int b, float* Y, int64_t ldy, float* Yt, float* T,
+                             const int* flag) {
+  if (int rc = check_b(b, "panel_hh_fallback")) return rc;
+  hipLaunchKernelGGL(panel_hh_fallback_kernel, dim3(1), dim3(SNT), 0, s, Ptop, ldr, Xp, ldx, pe, b,
+                     Y, ldy, Yt, T, flag);
   return check_launch("panel_hh_fallback");
 }
 
-int launch_panel_finish(hipStream_t s, const float* YtY, const float* YtX, float* R, int64_t ldr,
-                        int b, float* T) {
-  hipLaunchKernelGGL(panel_finish_kernel, dim3(1), dim3(SNT), 0, s, YtY, YtX, R, ldr, b, T);
-  return check_launch("panel_finish");
-}
-
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b) {
-  if (b > SB || b < 1) {
-    set_error("chol_block: block size out of range");
-    return IFK_ERR_INVALID;
-  }
+  if (int rc = check_b(b, "chol_block")) return rc;
   hipLaunchKernelGGL(chol_block_kernel, dim3(1), dim3(SNT), 0, s, A, ld, b);
   return check_launch("chol_block");
 }
 
+int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,
+                   int64_t ldt) {
+  if (n == 0) return IFK_OK;
+  int64_t g = cdiv(n * n, 256);
+  if (g > 4096) g = 4096;
+  hipLaunchKernelGGL(ut_tinv_kernel, dim3((unsigned)g), dim3(256), 0, s, G, ldg, n, Tinv, ldt);
+  return check_launch("ut_tinv");
+}
+
 int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
                       float* Z, int64_t ldz, int safe) {
-  if (nb > SB || nb < 1) {
-    set_error("trinv_diag: block size out of range");
-    return IFK_ERR_INVALID;
-  }
+  if (int rc = check_b(nb, "trinv_diag")) return rc;
   const unsigned nblk = (unsigned)cdiv(n, nb);
   if (rdt == DT_F32)
     hipLaunchKernelGGL(trinv_diag_kernel<DT_F32>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, nb, Z,

@@ -19,7 +19,9 @@ torch.linalg on CPU).  How each function is pinned (tests/test_oracle.py):
   bf16_round                 hand-computed RNE ties, NaN/Inf, subnormals
   momentum_step              the recurrence unrolled by hand for 3 steps
   bf16_linalg restatements   tolerance-level only: R vs chol(A^T A), L L^T vs A,
-                             R X vs B (bit-level: parity unpinned)
+                             R X vs B.  Bit-level parity: unpinned (the reference's
+                             bf16 matmul rounding and accumulation order are not
+                             fixed by any fixture the reference holds)
 """
 from __future__ import annotations
 

@@ -112,6 +112,34 @@ def test_fold_rank_deficient_and_zero_columns(hip):
     assert np.linalg.norm(Rg.T @ Rg - G) / np.linalg.norm(G) < 1e-6
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_fold_rows_summing_to_zero(hip, seed):
+    """Output-layer deltas of a softmax cross-entropy (softmax - onehot) sum to
+    zero over the classes, so a 256 x 10 chunk has rank 9.  Two chunks are
+    folded in turn (the second onto a full R, as on every later step): the
+    running R must keep R^T R = sum X_i^T X_i and match the oracle on its
+    leading full-rank rows."""
+    g = torch.Generator(device=DEV).manual_seed(100 + seed)
+    chunks = []
+    for _ in range(2):
+        logits = torch.randn(256, 10, device=DEV, generator=g) * 2
+        onehot = torch.nn.functional.one_hot(
+            torch.randint(0, 10, (256,), device=DEV, generator=g), 10).float()
+        chunks.append((torch.softmax(logits, -1) - onehot) / 256)
+    R = torch.zeros(10, 10, device=DEV)
+    r = 0
+    G = np.zeros((10, 10))
+    R_or = None
+    for X in chunks:
+        r = hip.fold_(R, r, X, 0)
+        Xd = X.double().cpu().numpy()
+        G += Xd.T @ Xd
+        R_or = O.streaming_tsqr_update(R_or, Xd)
+        Rg = R.double().cpu().numpy()
+        assert np.linalg.norm(Rg.T @ Rg - G) / np.linalg.norm(G) < 1e-5
+        assert np.abs(Rg[:9] - R_or[:9]).max() / np.abs(R_or).max() < 1e-4
+
+
 def test_fold_nan_gives_nonfinite_flag(hip):
     X = torch.randn(64, 16, device=DEV)
     X[3, 4] = float("nan")
@@ -363,7 +391,8 @@ def test_full_size_fold_properties(hip, p, n, dt):
     d = torch.diagonal(R)
     assert bool((d > 0).all())
     assert torch.count_nonzero(torch.tril(R, -1)).item() == 0
-    Rd, flag = hip.finalize(R, 1 / math.sqrt(p), 1e-2, torch.float32, 1)
+    Rd, flag = hip.finalize(R, 1 / math.sqrt(p), 1e-2, torch.float32,
+                            1 if dt == torch.bfloat16 else 0)
     assert flag.item() == 1
     l2 = (Rd.double() @ V).norm(dim=0) ** 2
     r2 = (R.double() @ V).norm(dim=0) ** 2 / p + 1e-2 * (V ** 2).sum(0)
