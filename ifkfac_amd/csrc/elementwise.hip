@@ -92,6 +92,22 @@ int launch_zero(hipStream_t s, float* dst, int64_t ldd, int64_t rows, int64_t co
   return check_launch("zero");
 }
 
+__global__ void zero_block_bf16_kernel(bf16_t* dst, int64_t ldd, int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e % cols;
+    dst[r * ldd + c] = 0;
+  }
+}
+
+int launch_zero_bf16(hipStream_t s, bf16_t* dst, int64_t ldd, int64_t rows, int64_t cols) {
+  if (rows * cols == 0) return IFK_OK;
+  hipLaunchKernelGGL(zero_block_bf16_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, s, dst,
+                     ldd, rows, cols);
+  return check_launch("zero_bf16");
+}
+
 __global__ void sub_inplace_kernel(float* dst, int64_t ldd, const float* src, int64_t lds,
                                    int64_t rows, int64_t cols) {
   const int64_t total = rows * cols;

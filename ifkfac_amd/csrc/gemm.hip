@@ -7,7 +7,7 @@
 // In LDS both operands are stored K-contiguous per row so every lane reads its
 // MFMA fragment with 128-bit loads; operands that are K-strided in memory are
 // transposed in registers on the way in (8 k x 4 mn micro-blocks per thread).
-#include "gemm.h"
+#include "gemm_impl.h"
 
 #include <mutex>
 #include <vector>
@@ -111,19 +111,6 @@ template <> struct GCfg<MATH_F32> {
   static constexpr int LDW = 36;  // LDS row stride in elements (fp32)
   static constexpr int G = 4;
   typedef float LT;
-};
-
-struct GemmParams {
-  int64_t M, N, K;
-  float alpha, beta;
-  const void* A; int64_t lda; int tria; int64_t bsa;
-  const void* B; int64_t ldb; int trib; int64_t bsb;
-  float* C; int64_t ldc; int64_t bsc;
-  bf16_t* Cb; int64_t ldcb; int64_t bscb;
-  float* part;
-  int splits;
-  int tiles_m, tiles_n;
-  int vec_a, vec_b;
 };
 
 template <int DT>
@@ -492,16 +479,23 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   p.B = B.p; p.ldb = B.ld; p.trib = B.tri; p.bsb = B.bstride;
   p.C = C.c; p.ldc = C.ldc; p.bsc = C.bstride;
   p.Cb = C.cb; p.ldcb = C.ldcb; p.bscb = C.bstride_b;
-  p.tiles_m = (int)cdiv(M, GBM);
-  p.tiles_n = (int)cdiv(N, GBN);
   p.vec_a = vec_ok(A);
   p.vec_b = vec_ok(B);
-  const int BK = math == MATH_BF16 ? GCfg<MATH_BF16>::BK : GCfg<MATH_F32>::BK;
+  // The 256 x 256 bf16 kernel takes the large contractions; small or fp32
+  // ones stay on the 128 x 128 engine.
+  const bool big = math == MATH_BF16 && M >= 192 && N >= 192 &&
+                   (double)M * (double)N * (double)K * batch >= 1e9;
+  const int TM = big ? gemm_big_tile_m() : GBM, TN = big ? gemm_big_tile_n() : GBN;
+  p.tiles_m = (int)cdiv(M, TM);
+  p.tiles_n = (int)cdiv(N, TN);
+  const int BK = big ? gemm_big_bk()
+                     : (math == MATH_BF16 ? GCfg<MATH_BF16>::BK : GCfg<MATH_F32>::BK);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
   const int64_t nkt = cdiv(K, BK);
   int splits = 1;
-  if (tiles < 192 && nkt >= 8) {
-    int64_t want = cdiv(384, tiles);
+  const int64_t full = big ? 160 : 192;  // fewer tiles than this leave CUs idle
+  if (tiles < full && nkt >= 8) {
+    int64_t want = cdiv(2 * full, tiles);
     want = std::min<int64_t>(want, nkt / 4);
     want = std::min<int64_t>(want, 64);
     while (want > 1 && (size_t)(want * batch) * (size_t)(M * N) > scratch.floats) --want;
@@ -530,7 +524,8 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     pr->bytes = ((double)M * K * sa + (double)K * N * sb + (double)M * N * cb) * batch;
     hipEventRecord(pr->beg, s);
   }
-  if (math == MATH_BF16) launch_a<MATH_BF16>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
+  if (big) launch_gemm_big(s, grid, p, A.dt, A.kc, B.dt, B.kc);
+  else if (math == MATH_BF16) launch_a<MATH_BF16>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   else launch_a<MATH_F32>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   if (pr) hipEventRecord(pr->end, s);
   int rc = check_launch("gemm");

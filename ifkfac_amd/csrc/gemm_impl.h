@@ -1,0 +1,28 @@
+// Internal interface between the two GEMM kernels (gemm.hip, gemm_big.hip).
+#pragma once
+#include "gemm.h"
+
+namespace ifk {
+
+struct GemmParams {
+  int64_t M, N, K;
+  float alpha, beta;
+  const void* A; int64_t lda; int tria; int64_t bsa;
+  const void* B; int64_t ldb; int trib; int64_t bsb;
+  float* C; int64_t ldc; int64_t bsc;
+  bf16_t* Cb; int64_t ldcb; int64_t bscb;
+  float* part;
+  int splits;
+  int tiles_m, tiles_n;
+  int vec_a, vec_b;
+};
+
+// 256 x 256 x 32 bf16 kernel (gemm_big.hip); grid.x = tiles_m * tiles_n of
+// its tile, grid.z = batch * splits.
+int gemm_big_tile_m();
+int gemm_big_tile_n();
+int gemm_big_bk();
+void launch_gemm_big(hipStream_t s, dim3 grid, const GemmParams& p, int adt, bool akc, int bdt,
+                     bool bkc);
+
+}  // namespace ifk

@@ -1,17 +1,47 @@
-// Host-side launchers of the single-purpose kernels (small.hip, elementwise.hip).
+// Host-side launchers of the single-purpose kernels (small.hip, panel.hip,
+// elementwise.hip).
 #pragma once
 #include "common.h"
 
 namespace ifk {
 
-// --- panel kernels (small.hip); b <= 64 -------------------------------------
+// --- panel step of the fold (small.hip, panel.hip); b <= 64 ------------------
+// Gram matrices over row slabs: part[(s * ncb + cb) * 4096] (64 x 64 each)
+// for gram_slabs(pe) 128-row slabs s and 64-column blocks cb (at most
+// PANEL_MAX_CB), reduced in slab order into G[cb * 4096].
+constexpr int PANEL_MAX_CB = 8;
+int gram_slabs(int64_t pe);
+// G = A^T [B0 | B1] over the pe rows (A at most 64 wide, B0 optional and at
+// most 64 wide, B1 w1 wide); *ncb_out = number of 64-column blocks of G.
+int launch_gram(hipStream_t s, const float* A, int64_t lda, int ka, const float* B0, int64_t ldb0,
+                int w0, const float* B1, int64_t ldb1, int w1, int64_t pe, float* part, float* G,
+                int* ncb_out);
+// CholeskyQR pass 1: G1 (+ P_top^T P_top) = U1^T U1, M1 = U1^{-1},
+// Q1 = P_top M1; *flag = 1 when a pivot falls below tol * its diagonal.
 int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t ldr, int b,
                       float tol, float* U1, float* M1, float* Q1, int* flag);
+// Householder TPQRT of [P_top; X_p] when *flag is set: reflectors into Q2
+// (ld 64, columns >= b zero), P_top <- R_new.
+int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* Xp, int64_t ldx,
+                             int64_t pe, int b, float* Q2, const int* flag);
+// Q2 = X_p M1 unless *flag is set
+int launch_apply_m(hipStream_t s, const float* X, int64_t ldx, int64_t pe, int b, const float* M,
+                   float* Q2, const int* flag);
+// CholeskyQR pass 2 + Householder reconstruction (T, N, NT, R_new) from G2
+// (+ Q1^T Q1); for a flagged panel T from the UT transform of Y^T Y, N = I,
+// NT = T.
 int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, const float* U1, int b,
                       float* N, float* NT, float* T, float* R, int64_t ldr, int* flag);
-int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* Xp, int64_t ldx,
-                             int64_t pe, int b, float* Y, int64_t ldy, float* Yt, float* T,
-                             const int* flag);
+// For each 64-column block of C_rest (nr columns; G block 1 + cb = Q2^T C):
+// W = NT^T (Q2^T C) + T^T R_rest, R_rest -= W, NW = N W (ld ldnw).
+int launch_panel_wcomp(hipStream_t s, const float* G, int ncb, int b, const float* N,
+                       const float* NT, const float* T, float* Rrest, int64_t ldr, int nr, float* NW,
+                       int64_t ldnw);
+// Y = Q2 N (ld ldy; also RNE bf16 into Yb, same ld, when Yb is given) and
+// C_rest -= Q2 NW
+int launch_panel_update(hipStream_t s, const float* Q2, int64_t pe, int b, const float* N,
+                        float* Y, int64_t ldy, bf16_t* Yb, const float* NW, int64_t ldnw, float* C,
+                        int64_t ldc, int nr);
 // Tinv = striu(G) + diag(1 + diag G) / 2 (UT transform of a reflector Gram matrix)
 int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,
                    int64_t ldt);
@@ -32,6 +62,7 @@ int launch_set_diag(hipStream_t s, float* dst, int64_t ldd, int64_t n, float val
 int launch_zero_rows(hipStream_t s, float* dst, int64_t ldd, int64_t r0, int64_t r1, int64_t cols);
 // zero a rows x cols block
 int launch_zero(hipStream_t s, float* dst, int64_t ldd, int64_t rows, int64_t cols);
+int launch_zero_bf16(hipStream_t s, bf16_t* dst, int64_t ldd, int64_t rows, int64_t cols);
 // dst -= src (rows x cols)
 int launch_sub_inplace(hipStream_t s, float* dst, int64_t ldd, const float* src, int64_t lds,
                        int64_t rows, int64_t cols);

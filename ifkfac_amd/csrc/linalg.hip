@@ -41,7 +41,11 @@ namespace ifk {
     if (_rc) return _rc;      \
   } while (0)
 
-static constexpr float HR_TOL = 1e-6f;
+// First-pass pivot threshold relative to the pivot's diagonal: panels with a
+// smaller pivot (rank-deficient or kappa^2 beyond ~1e4) take the Householder
+// fallback, so the second CholeskyQR pass always starts from a Q whose loss
+// of orthogonality is far below its own 1/4 pivot threshold.
+static constexpr float HR_TOL = 1e-4f;
 static constexpr int64_t OUTER_B = 512;
 
 static size_t split_floats(int64_t b, int64_t n) {
@@ -61,12 +65,16 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
 struct FoldWs {
   float* C;      // p x n working copy of the chunk
   float* Yo;     // p x OUTER_B: reflector X parts of the current outer block
-  float* Yto;    // p x OUTER_B: Y T of the current inner panel, then of the outer block
-  float* Q2;     // p x b
+  float* Yto;    // p x OUTER_B: Y T of the outer block (fp32 arithmetic)
+  bf16_t* Yob;   // bf16 copies of Yo, Y T and W for bf16 arithmetic (the
+  bf16_t* Ytob;  // products round their operands to bf16 anyway)
+  bf16_t* Wb;
+  float* Q2;     // p x 64: X_p M1, or the fallback's reflectors
   float* W;      // OUTER_B x n
-  float* G1;     // b x b panel scratch
-  float* G2;
-  float* U1;
+  float* part;   // per-slab Gram matrices of the panel kernels
+  float* Gp;     // their sum: PANEL_MAX_CB blocks of 64 x 64
+  float* NW;     // 64 x OUTER_B: N W of the panel
+  float* U1;     // 64 x 64 panel scratch
   float* M1;
   float* Q1;
   float* N;
@@ -86,10 +94,14 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   w.C = need_C ? a.take<float>((size_t)p * n) : nullptr;
   w.Yo = a.take<float>((size_t)p * B);
   w.Yto = a.take<float>((size_t)p * B);
+  w.Yob = a.take<bf16_t>((size_t)p * B);
+  w.Ytob = a.take<bf16_t>((size_t)p * B);
+  w.Wb = a.take<bf16_t>((size_t)B * n);
   w.Q2 = a.take<float>((size_t)p * b);
   w.W = a.take<float>((size_t)B * n);
-  w.G1 = a.take<float>(b * b);
-  w.G2 = a.take<float>(b * b);
+  w.part = a.take<float>((size_t)gram_slabs(p) * PANEL_MAX_CB * b * b);
+  w.Gp = a.take<float>((size_t)PANEL_MAX_CB * b * b);
+  w.NW = a.take<float>((size_t)b * B);
   w.U1 = a.take<float>(b * b);
   w.M1 = a.take<float>(b * b);
   w.Q1 = a.take<float>(b * b);
@@ -107,23 +119,34 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   w.split.p = a.take<float>(w.split.floats);
 }
 
-// Apply the block reflector (Y, T) of rows [r0, r0 + kb) to columns [c1, c2):
-//   W = Yt^T C + T^T R_blk,  R_blk -= W,  C -= Y W
-// with Yt = Y T given, Y and Yt of ld ldy, pe rows of C involved.
-static int apply_block(hipStream_t s, int math, const float* Y, const float* Yt, int64_t ldy,
-                       const float* T, int64_t ldt, int64_t kb, float* C, int64_t ldc,
-                       int64_t pe, float* R, int64_t ldr, int64_t r0, int64_t c1, int64_t c2,
-                       FoldWs& w) {
-  const int64_t nt = c2 - c1;
-  if (nt <= 0) return IFK_OK;
-  float* Rb = R + r0 * ldr + c1;
-  RC(gemm(s, math, kb, nt, pe, 1.0f, A_t(Yt, DT_F32, ldy), B_n(C + c1, DT_F32, ldc), 0.0f,
-          out_f32(w.W, nt), 1, w.split));
-  RC(gemm(s, kb > PANEL_B ? math : MATH_F32, kb, nt, kb, 1.0f, A_t(T, DT_F32, ldt, TRI_LOWER),
-          B_n(Rb, DT_F32, ldr), 1.0f, out_f32(w.W, nt), 1, w.split));
-  RC(launch_sub_inplace(s, Rb, ldr, w.W, nt, kb, nt));
-  return gemm(s, math, pe, nt, kb, -1.0f, A_n(Y, DT_F32, ldy), B_n(w.W, DT_F32, nt), 1.0f,
-              out_f32(C + c1, ldc), 1, w.split);
+// Apply the finished outer block (reflectors Yo of columns [K0, K1), pe rows)
+// to the columns [K1, n):
+//   T^{-1} = striu(Yo^T Yo) + diag(1 + diag(Yo^T Yo)) / 2   (UT transform)
+//   W = (Yo T)^T C + T^T R_blk,  R_blk -= W,  C -= Yo W
+// In bf16 arithmetic every product reads the bf16 copies (Yob, Ytob, Wb),
+// which hold exactly the RNE roundings the MFMA operands would get; W and R
+// stay fp32.
+static int outer_update(hipStream_t s, int math, FoldWs& w, float* C, int64_t ldc, int64_t pe,
+                        float* R, int64_t ldr, int64_t K0, int64_t K1, int64_t n) {
+  const int64_t B = OUTER_B, KB = K1 - K0, nt = n - K1;
+  const bool bf = math == MATH_BF16;
+  const MatRef YoT = bf ? A_t(w.Yob, DT_BF16, B) : A_t(w.Yo, DT_F32, B);
+  const MatRef YoB = bf ? B_n(w.Yob, DT_BF16, B) : B_n(w.Yo, DT_F32, B);
+  RC(gemm(s, math, KB, KB, pe, 1.0f, YoT, YoB, 0.0f, out_f32(w.Go, KB), 1, w.split));
+  RC(launch_ut_tinv(s, w.Go, KB, KB, w.Tio, KB));
+  RC(trinv_core(s, w.Tio, DT_F32, KB, KB, w.To, KB, MATH_F32, 0, w.ttmp, w.tsp));
+  const MatRef YoA = bf ? A_n(w.Yob, DT_BF16, B) : A_n(w.Yo, DT_F32, B);
+  RC(gemm(s, math, pe, KB, KB, 1.0f, YoA, B_n(w.To, DT_F32, KB, TRI_UPPER), 0.0f,
+          bf ? out_bf16(w.Ytob, B) : out_f32(w.Yto, B), 1, w.split));
+  float* Rb = R + K0 * ldr + K1;
+  const MatRef YtoT = bf ? A_t(w.Ytob, DT_BF16, B) : A_t(w.Yto, DT_F32, B);
+  RC(gemm(s, math, KB, nt, pe, 1.0f, YtoT, B_n(C + K1, DT_F32, ldc), 0.0f, out_f32(w.W, nt), 1,
+          w.split));
+  RC(gemm(s, math, KB, nt, KB, 1.0f, A_t(w.To, DT_F32, KB, TRI_LOWER), B_n(Rb, DT_F32, ldr), 1.0f,
+          bf ? out_both(w.W, nt, w.Wb, nt) : out_f32(w.W, nt), 1, w.split));
+  RC(launch_sub_inplace(s, Rb, ldr, w.W, nt, KB, nt));
+  const MatRef WB = bf ? B_n(w.Wb, DT_BF16, nt) : B_n(w.W, DT_F32, nt);
+  return gemm(s, math, pe, nt, KB, -1.0f, YoA, WB, 1.0f, out_f32(C + K1, ldc), 1, w.split);
 }
 
 // Core of the fold on an fp32 working copy C (p x n, ldc).  R rows [0, r_new)
@@ -139,42 +162,34 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     const int64_t K1 = std::min<int64_t>(K0 + B, r_new);
     const int64_t KB = K1 - K0;
     const int64_t pe_o = x_tri ? std::min<int64_t>(p, K1) : p;
-    if (x_tri) RC(launch_zero(s, w.Yo, B, pe_o, KB));
+    if (x_tri) {
+      RC(launch_zero(s, w.Yo, B, pe_o, KB));
+      if (math == MATH_BF16) RC(launch_zero_bf16(s, w.Yob, B, pe_o, KB));
+    }
     for (int64_t c0 = K0; c0 < K1; c0 += PANEL_B) {
       const int bk = (int)std::min<int64_t>(PANEL_B, K1 - c0);
       const int64_t c1 = c0 + bk;
+      const int nr = (int)(K1 - c1);
       const int64_t pe = x_tri ? std::min<int64_t>(p, c1) : p;
       float* Ptop = R + c0 * ldr + c0;
       float* Xp = C + c0;
-      float* Y = w.Yo + (c0 - K0);
-      float* Yt = w.Yto + (c0 - K0);
-      // panel: CholeskyQR2 + Householder reconstruction, fallback if flagged
-      RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(Xp, DT_F32, ldc), B_n(Xp, DT_F32, ldc), 0.0f,
-              out_f32(w.G1, bk), 1, w.split));
-      RC(launch_panel_hr_a(s, w.G1, Ptop, ldr, bk, HR_TOL, w.U1, w.M1, w.Q1, w.flag));
-      RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(Xp, DT_F32, ldc),
-              B_n(w.M1, DT_F32, bk, TRI_UPPER), 0.0f, out_f32(w.Q2, bk), 1, w.split));
-      RC(gemm(s, MATH_F32, bk, bk, pe, 1.0f, A_t(w.Q2, DT_F32, bk), B_n(w.Q2, DT_F32, bk), 0.0f,
-              out_f32(w.G2, bk), 1, w.split));
-      RC(launch_panel_hr_b(s, w.G2, w.Q1, w.U1, bk, w.N, w.NT, w.T, Ptop, ldr, w.flag));
-      RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(w.Q2, DT_F32, bk),
-              B_n(w.N, DT_F32, bk, TRI_UPPER), 0.0f, out_f32(Y, B), 1, w.split));
-      RC(gemm(s, MATH_F32, pe, bk, bk, 1.0f, A_n(w.Q2, DT_F32, bk),
-              B_n(w.NT, DT_F32, bk, TRI_UPPER), 0.0f, out_f32(Yt, B), 1, w.split));
-      RC(launch_panel_hh_fallback(s, Ptop, ldr, Xp, ldc, pe, bk, Y, B, Yt, w.T, w.flag));
-      // rest of the outer block
-      RC(apply_block(s, math, Y, Yt, B, w.T, bk, bk, C, ldc, pe, R, ldr, c0, c1, K1, w));
+      int ncb;
+      // pass 1: G1 = X_p^T X_p (+ P_top^T P_top), U1, M1 -- or the fallback
+      RC(launch_gram(s, Xp, ldc, bk, nullptr, 0, 0, Xp, ldc, bk, pe, w.part, w.Gp, &ncb));
+      RC(launch_panel_hr_a(s, w.Gp, Ptop, ldr, bk, HR_TOL, w.U1, w.M1, w.Q1, w.flag));
+      RC(launch_panel_hh_fallback(s, Ptop, ldr, Xp, ldc, pe, bk, w.Q2, w.flag));
+      // pass 2: Q2 = X_p M1, G2 = Q2^T Q2 and Q2^T C_rest in one sweep
+      RC(launch_apply_m(s, Xp, ldc, pe, bk, w.M1, w.Q2, w.flag));
+      RC(launch_gram(s, w.Q2, PANEL_B, PANEL_B, w.Q2, PANEL_B, PANEL_B, C + c1, ldc, nr, pe, w.part,
+                     w.Gp, &ncb));
+      RC(launch_panel_hr_b(s, w.Gp, w.Q1, w.U1, bk, w.N, w.NT, w.T, Ptop, ldr, w.flag));
+      // rest of the outer block: R_rest and C_rest, Y into the outer store
+      RC(launch_panel_wcomp(s, w.Gp, ncb, bk, w.N, w.NT, w.T, Ptop + bk, ldr, nr, w.NW, OUTER_B));
+      RC(launch_panel_update(s, w.Q2, pe, bk, w.N, w.Yo + (c0 - K0), OUTER_B,
+                             math == MATH_BF16 ? w.Yob + (c0 - K0) : nullptr, w.NW, OUTER_B,
+                             C + c1, ldc, nr));
     }
-    if (K1 < n) {
-      // T of the whole outer block from the UT transform of its Gram matrix
-      RC(gemm(s, math, KB, KB, pe_o, 1.0f, A_t(w.Yo, DT_F32, B), B_n(w.Yo, DT_F32, B), 0.0f,
-              out_f32(w.Go, KB), 1, w.split));
-      RC(launch_ut_tinv(s, w.Go, KB, KB, w.Tio, KB));
-      RC(trinv_core(s, w.Tio, DT_F32, KB, KB, w.To, KB, MATH_F32, 0, w.ttmp, w.tsp));
-      RC(gemm(s, math, pe_o, KB, KB, 1.0f, A_n(w.Yo, DT_F32, B), B_n(w.To, DT_F32, KB, TRI_UPPER),
-              0.0f, out_f32(w.Yto, B), 1, w.split));
-      RC(apply_block(s, math, w.Yo, w.Yto, B, w.To, KB, KB, C, ldc, pe_o, R, ldr, K0, K1, n, w));
-    }
+    if (K1 < n) RC(outer_update(s, math, w, C, ldc, pe_o, R, ldr, K0, K1, n));
   }
   return launch_sign_normalize(s, R, ldr, r_new, n);
 }

@@ -17,11 +17,12 @@
 //   Y = Q_bottom N with N = -M2 S T^{-1},  Y T = Q_bottom (-M2 S)
 //   R_new = S U2 U1
 // which is the TPQRT form: V = [I; Y], block reflector I - V T V^T.  When a
-// Cholesky pivot collapses (rank-deficient or ill-conditioned panel) a flag
-// is raised, panel_hr_b leaves R untouched, and panel_hh_fallback recomputes
-// the panel by column-by-column Householder reflections (LAPACK dlarfg
-// convention, never breaks down), with T from the UT transform
+// first-pass Cholesky pivot collapses (rank-deficient or ill-conditioned
+// panel) a flag is raised and panel_hh_fallback computes the reflectors by
+// column-by-column Householder reflections (LAPACK dlarfg convention, never
+// breaks down); panel_hr_b then takes T from the UT transform
 //   T^{-1} = striu(V^T V) + diag(V^T V) / 2,  V^T V = I + Y^T Y.
+// The partial Gram matrices over row slabs come from panel.hip.
 #include "common.h"
 #include "kernels.h"
 
@@ -306,20 +307,21 @@ __device__ __forceinline__ void sm_trinv64(const float* U, float* Z, float* Tmp,
 // Panel kernels
 // ---------------------------------------------------------------------------
 
-// In: G (b x b, = X_p^T X_p), P_top (in R at ldr).
-// Out: U1 (Cholesky factor of P^T P), M1 = U1^{-1}, Q1 = P_top M1 (b x b, ld b);
-//      *flag = 1 on a collapsed pivot, else 0.
-__global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G, const float* Ptop,
-                                                          int64_t ldr, int b, float tol,
-                                                          float* U1, float* M1, float* Q1,
-                                                          int* flag) {
+// CholeskyQR pass 1.  In: G = X_p^T X_p (64 x 64, ld 64), P_top (in R at ldr).
+// Out: U1 (Cholesky factor of P^T P), M1 = U1^{-1}, Q1 = P_top M1 (b x b,
+// ld b); *flag = 1 when a pivot falls below tol times its diagonal (the
+// panel then goes to the Householder fallback), else 0.
+__global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
+                                                          const float* Ptop, int64_t ldr, int b,
+                                                          float tol, float* U1, float* M1,
+                                                          float* Q1, int* flag) {
   __shared__ float sG[SB * SLD];
   __shared__ float sP[SB * SLD];
   __shared__ float sM[SB * SLD];
   __shared__ float sT[32 * 32];
   __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
-  sm_load_pad(sG, G, b, b, false);
+  sm_load_pad(sG, G, SB, b, false);
   sm_load_pad(sP, Ptop, ldr, b, true, 0.0f);
   sm_gemm64<true, false>(sP, sP, sG, 1.0f, true);  // sG = X_p^T X_p + P_top^T P_top
   sm_chol64(sG, tol, &bad, 0);                     // sG = U1
@@ -332,12 +334,17 @@ __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G, const f
   if (threadIdx.x == 0) *flag = bad;
 }
 
-// In: G2 (b x b, = Q2^T Q2 with Q2 = X_p M1), Q1, U1.
-// Out: N (Y = Q2 N), NT (Y T = Q2 NT), T (b x b, ld b); R's diagonal block
-// <- S U2 U1 unless the panel is flagged (flag kept once raised).
-__global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const float* Q1,
-                                                          const float* U1, int b, float* N,
-                                                          float* NT, float* T, float* R,
+// CholeskyQR pass 2 and Householder reconstruction.  In: G2 = Q2^T Q2
+// (64 x 64, ld 64; Q2 = X_p M1), Q1, U1.
+// Out: T (b x b, ld b), N (Y = Q2 N) and NT (Y T = Q2 NT); R's diagonal block
+// <- R_new = S U2 U1.
+// For a panel flagged by pass 1, Q2 holds the fallback's reflectors Y and R
+// already holds R_new: T comes from the UT transform of Y^T Y, N = I, NT = T.
+// A second-pass pivot below 1/4 (the first pass lost too much orthogonality
+// for the reconstruction to be exact) poisons R's block with NaN, which the
+// finite check of finalize reports.
+__global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const float* Q1, const float* U1, int b,
+                                                          float* N, float* NT, float* T, float* R,
                                                           int64_t ldr, int* flag) {
   __shared__ float sG[SB * SLD];
   __shared__ float sQ[SB * SLD];
@@ -348,11 +355,34 @@ __global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const 
   __shared__ int bad;
   const int t = threadIdx.x;
   if (t == 0) bad = 0;
-  sm_load_pad(sG, G2, b, b, false);
+  const bool flagged = (*flag != 0);
+  sm_load_pad(sG, G2, SB, b, false);
+  if (flagged) {
+    // UT transform: T^{-1} = striu(Y^T Y) + diag(1 + diag(Y^T Y)) / 2
+    for (int e = t; e < SB * SB; e += SNT) {
+      const int i = e >> 6, j = e & 63;
+      float v = 0.0f;
+      if (i < b && j < b) {
+        if (i < j) v = sG[i * SLD + j];
+        else if (i == j) v = 0.5f * (1.0f + sG[i * SLD + i]);
+      } else if (i == j) {
+        v = 1.0f;
+      }
+      sX[i * SLD + j] = v;
+    }
+    __syncthreads();
+    sm_trinv64(sX, sQ, sTmp);                      // sQ = T
+    for (int e = t; e < b * b; e += SNT) {
+      const int i = e / b, j = e - i * b;
+      const float v = sQ[i * SLD + j];
+      T[e] = v;
+      NT[e] = v;
+      N[e] = (i == j) ? 1.0f : 0.0f;
+    }
+    return;
+  }
   sm_load_pad(sQ, Q1, b, b, true, 0.0f);
   sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
-  // G2 should be close to I; a pivot below 1/4 means the first pass lost too
-  // much orthogonality for the reconstruction to be trusted.
   sm_chol64(sG, 0.25f, &bad, 0);                   // sG = U2
   sm_trinv64(sG, sM, sTmp);                        // sM = M2
   sm_gemm64<false, false>(sQ, sM, sX, 1.0f, false);  // sX = Q1f = Q1 M2
@@ -366,11 +396,7 @@ __global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const 
     sX[i * SLD + j] = v;
   }
   __syncthreads();
-  // A panel flagged by panel_hr_a keeps R untouched here: the fallback reads
-  // the original diagonal block of R.
-  const bool ok = (bad == 0) && (*flag == 0);
-  __syncthreads();
-  if (t == 0 && bad) *flag = 1;
+  const bool ok = (bad == 0);
   for (int e = t; e < b * b; e += SNT) {
     const int i = e / b, j = e - i * b;
     T[e] = sX[i * SLD + j];
@@ -390,27 +416,26 @@ __global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const 
   __syncthreads();
   sm_load_pad(sQ, U1, b, b, true);
   sm_gemm64<false, false>(sG, sQ, sX, 1.0f, false);  // sX = U2 U1
-  if (ok) {
-    for (int e = t; e < b * b; e += SNT) {         // R_new = S U2 U1
-      const int i = e / b, j = e - i * b;
-      R[(int64_t)i * ldr + j] = (i <= j) ? sgn[i] * sX[i * SLD + j] : 0.0f;
-    }
+  const float nan = __int_as_float(0x7fc00000);
+  for (int e = t; e < b * b; e += SNT) {           // R_new = S U2 U1
+    const int i = e / b, j = e - i * b;
+    R[(int64_t)i * ldr + j] = !ok ? nan : ((i <= j) ? sgn[i] * sX[i * SLD + j] : 0.0f);
   }
+  if (t == 0 && !ok) *flag = 1;
 }
 
-// Robust TPQRT panel by Householder reflections, run only when *flag is set.
-// Overwrites Y (p_e x b, ld ldy) with the reflectors' X parts, Yt with Y T,
-// T (b x b) with the UT-transform T of Y, and R's diagonal block with R_new.
+// Robust TPQRT panel by Householder reflections (LAPACK dlarfg convention),
+// run only when *flag is set: the reflectors' X parts go to Q2 (p_e x 64,
+// columns >= b zero) and R's diagonal block is replaced by R_new.  One
+// workgroup walks the b columns; norms and dot products over the p_e rows
+// are wave-shuffle reductions.
 __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(float* Ptop, int64_t ldr,
                                                                  const float* Xp, int64_t ldx,
                                                                  int64_t pe, int b, float* Y,
-                                                                 int64_t ldy, float* Yt, float* T,
                                                                  const int* flag) {
   if (*flag == 0) return;
+  constexpr int64_t ldy = SB;
   __shared__ float sP[SB * SLD];
-  __shared__ float sA[SB * SLD];
-  __shared__ float sT[SB * SLD];
-  __shared__ float sTmp[32 * 32];
   __shared__ float red[4][SB];
   __shared__ float wv[SB];
   __shared__ float scal[3];
@@ -420,10 +445,10 @@ __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(float* Ptop, int
     const int r = e >> 6, c = e & 63;
     sP[r * SLD + c] = (r < b && c < b && r <= c) ? Ptop[(int64_t)r * ldr + c] : 0.0f;
   }
-  for (int64_t e = t; e < pe * b; e += SNT) {
-    const int64_t r = e / b;
-    const int c = (int)(e % b);
-    Y[r * ldy + c] = Xp[r * ldx + c];
+  for (int64_t e = t; e < pe * SB; e += SNT) {
+    const int64_t r = e / SB;
+    const int c = (int)(e % SB);
+    Y[r * ldy + c] = (c < b) ? Xp[r * ldx + c] : 0.0f;
   }
   __syncthreads();
   for (int j = 0; j < b; ++j) {
@@ -486,37 +511,48 @@ __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(float* Ptop, int
     if (t == 0) sP[j * SLD + j] = scal[2];
     __syncthreads();
   }
-  // T from the UT transform of Y
-  for (int e = t; e < SB * SB; e += SNT) {
-    const int i = e >> 6, c = e & 63;
-    float v = 0.0f;
-    if (i < b && c < b && i <= c) {
-      for (int64_t r = 0; r < pe; ++r) v += Y[r * ldy + i] * Y[r * ldy + c];
-      if (i == c) v = 0.5f * (1.0f + v);
-    } else if (i == c) {
-      v = 1.0f;
-    }
-    sA[i * SLD + c] = v;
-  }
-  __syncthreads();
-  sm_trinv64(sA, sT, sTmp);
   for (int e = t; e < b * b; e += SNT) {
     const int i = e / b, c = e - i * b;
-    T[e] = sT[i * SLD + c];
     Ptop[(int64_t)i * ldr + c] = (i <= c) ? sP[i * SLD + c] : 0.0f;
   }
-  // Yt = Y T, row by row
-  for (int64_t r = t; r < pe; r += SNT) {
-    float yr[SB];
-#pragma unroll
-    for (int c = 0; c < SB; ++c) yr[c] = (c < b) ? Y[r * ldy + c] : 0.0f;
-    for (int c = 0; c < b; ++c) {
-      float s = 0.0f;
-#pragma unroll
-      for (int k = 0; k < SB; ++k)
-        if (k <= c) s += yr[k] * sT[k * SLD + c];
-      Yt[r * ldy + c] = s;
-    }
+}
+
+// Block cb of the rest of the outer block (64 columns of C_rest, w of them
+// real): from QC = block 1 + cb of the reduced Grams (Q2^T C_rest, ld 64),
+//   W = NT^T (Q2^T C) + T^T R_rest,  R_rest -= W,  NW = N W
+// which applies the panel's block reflector to R_rest and leaves the X-side
+// update C_rest -= Q2 NW to panel_update.
+__global__ __launch_bounds__(SNT) void panel_wcomp_kernel(const float* G, int b, const float* N, const float* NT,
+                                                           const float* T, float* Rrest,
+                                                           int64_t ldr, int nr, float* NW,
+                                                           int64_t ldnw) {
+  __shared__ float sA[SB * SLD];
+  __shared__ float sB[SB * SLD];
+  __shared__ float sW[SB * SLD];
+  __shared__ float sR[SB * SLD];
+  const int t = threadIdx.x;
+  const int cb = blockIdx.x;
+  const int c0 = cb * SB;
+  const int w = (nr - c0) < SB ? (nr - c0) : SB;
+  sm_load_pad(sA, G + (size_t)(1 + cb) * SB * SB, SB, SB, false);  // Q2^T C block (zero beyond b, w)
+  sm_load_pad(sB, NT, b, b, false, 0.0f);
+  sm_gemm64<true, false>(sB, sA, sW, 1.0f, false);      // W = NT^T (Q2^T C)
+  sm_load_pad(sB, T, b, b, true, 0.0f);
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    sR[i * SLD + j] = (i < b && j < w) ? Rrest[(int64_t)i * ldr + c0 + j] : 0.0f;
+  }
+  __syncthreads();
+  sm_gemm64<true, false>(sB, sR, sW, 1.0f, true);       // W += T^T R_rest
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    if (i < b && j < w) Rrest[(int64_t)i * ldr + c0 + j] = sR[i * SLD + j] - sW[i * SLD + j];
+  }
+  sm_load_pad(sB, N, b, b, false, 0.0f);
+  sm_gemm64<false, false>(sB, sW, sA, 1.0f, false);     // NW = N W
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    NW[(int64_t)i * ldnw + c0 + j] = sA[i * SLD + j];
   }
 }
 
@@ -594,8 +630,8 @@ static int check_b(int b, const char* what) {
 int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t ldr, int b,
                       float tol, float* U1, float* M1, float* Q1, int* flag) {
   if (int rc = check_b(b, "panel_hr_a")) return rc;
-  hipLaunchKernelGGL(panel_hr_a_kernel, dim3(1), dim3(SNT), 0, s, G, Ptop, ldr, b, tol, U1, M1,
-                     Q1, flag);
+  hipLaunchKernelGGL(panel_hr_a_kernel, dim3(1), dim3(SNT), 0, s, G, Ptop, ldr, b, tol, U1, M1, Q1,
+                     flag);
   return check_launch("panel_hr_a");
 }
 
@@ -608,12 +644,26 @@ int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, const flo
 }
 
 int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* Xp, int64_t ldx,
-                             int64_t pe, int b, float* Y, int64_t ldy, float* Yt, float* T,
-                             const int* flag) {
+                             int64_t pe, int b, float* Q2, const int* flag) {
   if (int rc = check_b(b, "panel_hh_fallback")) return rc;
   hipLaunchKernelGGL(panel_hh_fallback_kernel, dim3(1), dim3(SNT), 0, s, Ptop, ldr, Xp, ldx, pe, b,
-                     Y, ldy, Yt, T, flag);
+                     Q2, flag);
   return check_launch("panel_hh_fallback");
+}
+
+int launch_panel_wcomp(hipStream_t s, const float* G, int ncb, int b, const float* N,
+                       const float* NT, const float* T, float* Rrest, int64_t ldr, int nr, float* NW,
+                       int64_t ldnw) {
+  if (int rc = check_b(b, "panel_wcomp")) return rc;
+  if (nr <= 0) return IFK_OK;
+  const int nblk = (int)cdiv((int64_t)nr, (int64_t)SB);
+  if (ncb != nblk + 1 || ldnw < (int64_t)nblk * SB) {
+    set_error("panel_wcomp: column blocks do not match the partial Grams");
+    return IFK_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(panel_wcomp_kernel, dim3(nblk), dim3(SNT), 0, s, G, b, N, NT, T, Rrest, ldr,
+                     nr, NW, ldnw);
+  return check_launch("panel_wcomp");
 }
 
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b) {

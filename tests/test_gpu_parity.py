@@ -62,6 +62,23 @@ def test_gemm_engine(hip, math_, ta, tb, m, n, k):
     assert _rel(C, ref.cpu().numpy()) < 2e-6
 
 
+@pytest.mark.parametrize("adt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("m,n,k", [(1100, 900, 1100), (700, 1300, 1500), (2048, 2560, 512)])
+def test_gemm_engine_large_tiles(hip, adt, ta, tb, m, n, k):
+    """Shapes that take the 256 x 256 bf16 kernel (ragged edges, split-K for
+    the first two, full tiles for the last), against an fp64 product of the
+    bf16-rounded operands."""
+    g = torch.Generator(device=DEV).manual_seed(m + 3 * n + 7 * k)
+    A = torch.randn((k, m) if ta else (m, k), device=DEV, generator=g).to(adt)
+    B = torch.randn((n, k) if tb else (k, n), device=DEV, generator=g).to(adt)
+    opA = A.t() if ta else A
+    opB = B.t() if tb else B
+    ref = opA.bfloat16().double() @ opB.bfloat16().double()
+    C = hip.gemm(A, B, ta, tb, 1)
+    assert _rel(C, ref.cpu().numpy()) < 2e-6
+
+
 # --------------------------------------------------------------------------- fold
 
 
