@@ -109,7 +109,7 @@ def main() -> int:
     import torch
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from ifkfac_amd import _backend, _lib
-    from ifkfac_amd._backend import MATH_BF16
+    from ifkfac_amd._backend import MATH_BF16, run_pair
 
     be = _backend.get_backend()
     lib = be.lib
@@ -137,11 +137,13 @@ def main() -> int:
         mark(1)
         be.fold_(R_G, 0, D, MATH_BF16)
         mark(2)
-        FX, _ = be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16)
-        FG, _ = be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16)
+        # input and output sides are independent, as in IFKFAC._update_factors
+        (FX, _), (FG, _) = run_pair(R_X.device,
+                                    lambda: be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16),
+                                    lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16))
         mark(3)
-        ZX = be.tri_inverse(FX, MATH_BF16)
-        ZG = be.tri_inverse(FG, MATH_BF16)
+        ZX, ZG = run_pair(R_X.device, lambda: be.tri_inverse(FX, MATH_BF16),
+                          lambda: be.tri_inverse(FG, MATH_BF16))
         mark(4)
         nat = be.precondition_apply(grad, ZX, ZG, MATH_BF16)
         mark(5)

@@ -297,5 +297,47 @@ def set_backend(backend):
     return prev
 
 
+_SIDE_STREAMS = {}
+
+
+def _side_streams(device: torch.device):
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _SIDE_STREAMS:
+        with torch.cuda.device(idx):
+            _SIDE_STREAMS[idx] = (torch.cuda.Stream(), torch.cuda.Stream())  # default priority
+    return _SIDE_STREAMS[idx]
+
+
+def _tensors(obj):
+    if isinstance(obj, torch.Tensor):
+        yield obj
+    elif isinstance(obj, (tuple, list)):
+        for o in obj:
+            yield from _tensors(o)
+
+
+def run_pair(device: torch.device, fa, fb):
+    """Run fa() and fb() concurrently on two side streams of `device`, after the
+    current stream's pending work; the current stream then waits for both.
+    Used for the independent input-side and output-side factor work (finalize,
+    triangular inverse).  On a CPU device the two calls simply run in order."""
+    if device.type != "cuda":
+        return fa(), fb()
+    main = torch.cuda.current_stream(device)
+    s1, s2 = _side_streams(device)
+    s1.wait_stream(main)
+    s2.wait_stream(main)
+    with torch.cuda.stream(s1):
+        ra = fa()
+    with torch.cuda.stream(s2):
+        rb = fb()
+    main.wait_stream(s1)
+    main.wait_stream(s2)
+    for t in list(_tensors(ra)) + list(_tensors(rb)):
+        if t.is_cuda:
+            t.record_stream(main)
+    return ra, rb
+
+
 def inv_sqrt(rows: int) -> float:
     return 1.0 / _math.sqrt(rows)

@@ -20,7 +20,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ._backend import MATH_F32, get_backend
+from ._backend import MATH_F32, get_backend, run_pair
 from .gram_estimator import GramMatrixEstimator
 
 logger = logging.getLogger(__name__)
@@ -216,8 +216,11 @@ class RawActivationHooks(GramMatrixEstimator):
                     raise IFKFACRankError(
                         f"Layer {module}: accumulated {rows_G} rows for δ, "
                         f"but need >= n_out={R_G_raw.shape[1]} (batched mode).")
-            R_X, fX = self._finalize(R_X_raw, rows_X, out_dtype)
-            R_G, fG = self._finalize(R_G_raw, rows_G, out_dtype)
+            # the two sides are independent: finalize them concurrently
+            (R_X, fX), (R_G, fG) = run_pair(
+                R_X_raw.device,
+                lambda: self._finalize(R_X_raw, rows_X, out_dtype),
+                lambda: self._finalize(R_G_raw, rows_G, out_dtype))
             factors[module] = (R_X, R_G)
             flags[module] = (fX, fG)
         return factors, flags

@@ -54,10 +54,12 @@ template <int DT> struct Elem;
 template <> struct Elem<DT_F32> {
   typedef float T;
   __device__ static inline float load(const float* p) { return *p; }
+  __device__ static inline void store(float* p, float v) { *p = v; }
 };
 template <> struct Elem<DT_BF16> {
   typedef bf16_t T;
   __device__ static inline float load(const bf16_t* p) { return bf16_to_f32(*p); }
+  __device__ static inline void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
 };
 
 // ---------------------------------------------------------------------------

@@ -108,6 +108,36 @@ int launch_zero_bf16(hipStream_t s, bf16_t* dst, int64_t ldd, int64_t rows, int6
   return check_launch("zero_bf16");
 }
 
+// R[i][j] -= WT[j][i] over a rows x cols block, through a 32 x 32 LDS tile so
+// both the read of WT and the update of R are coalesced.
+__global__ void sub_transposed_kernel(float* R, int64_t ldr, const float* WT, int64_t ldw,
+                                      int64_t rows, int64_t cols) {
+  __shared__ float tile[32][33];
+  const int64_t i0 = (int64_t)blockIdx.y * 32, j0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t j = j0 + k, i = i0 + tx;
+    tile[k][tx] = (j < cols && i < rows) ? WT[j * ldw + i] : 0.0f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t i = i0 + k, j = j0 + tx;
+    if (i < rows && j < cols) R[i * ldr + j] -= tile[tx][k];
+  }
+}
+
+int launch_sub_transposed(hipStream_t s, float* R, int64_t ldr, const float* WT, int64_t ldw,
+                          int64_t rows, int64_t cols) {
+  if (rows * cols == 0) return IFK_OK;
+  if (cdiv(rows, 32) > 65535) {
+    set_error("sub_transposed: too many rows");
+    return IFK_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(sub_transposed_kernel, dim3((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32)),
+                     dim3(256), 0, s, R, ldr, WT, ldw, rows, cols);
+  return check_launch("sub_transposed");
+}
+
 __global__ void sub_inplace_kernel(float* dst, int64_t ldd, const float* src, int64_t lds,
                                    int64_t rows, int64_t cols) {
   const int64_t total = rows * cols;
@@ -294,26 +324,41 @@ int launch_scale_copy_vec(hipStream_t s, const float* x, int64_t n, float alpha,
   return check_launch("scale_copy_vec");
 }
 
+// dst (cols x rows, fp32) = src^T through a 32 x 32 LDS tile: the read of
+// src and the write of dst are both coalesced.
 template <int DT>
 __global__ void transpose_to_f32_kernel(const void* src, int64_t lds, int64_t rows, int64_t cols,
                                         float* dst, int64_t ldd) {
-  const int64_t total = rows * cols;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t c = e / rows, r = e % rows;  // dst row c, dst col r
-    dst[c * ldd + r] = Elem<DT>::load((const typename Elem<DT>::T*)src + r * lds + c);
+  __shared__ float tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    tile[k][tx] = (r < rows && c < cols)
+                      ? Elem<DT>::load((const typename Elem<DT>::T*)src + r * lds + c)
+                      : 0.0f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (c < cols && r < rows) dst[c * ldd + r] = tile[tx][k];
   }
 }
 
 int launch_transpose_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
                             int64_t cols, float* dst, int64_t ldd) {
   if (rows * cols == 0) return IFK_OK;
+  if (cdiv(rows, 32) > 65535) {
+    set_error("transpose_to_f32: too many rows");
+    return IFK_ERR_INVALID;
+  }
+  const dim3 grid((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32));
   if (sdt == DT_F32)
-    hipLaunchKernelGGL(transpose_to_f32_kernel<DT_F32>, dim3(grid_for(rows * cols)), dim3(256), 0,
-                       s, src, lds, rows, cols, dst, ldd);
+    hipLaunchKernelGGL(transpose_to_f32_kernel<DT_F32>, grid, dim3(256), 0, s, src, lds, rows, cols,
+                       dst, ldd);
   else
-    hipLaunchKernelGGL(transpose_to_f32_kernel<DT_BF16>, dim3(grid_for(rows * cols)), dim3(256), 0,
-                       s, src, lds, rows, cols, dst, ldd);
+    hipLaunchKernelGGL(transpose_to_f32_kernel<DT_BF16>, grid, dim3(256), 0, s, src, lds, rows,
+                       cols, dst, ldd);
   return check_launch("transpose_to_f32");
 }
 
@@ -340,6 +385,46 @@ int launch_transpose_upper(hipStream_t s, const float* src, int64_t lds, int64_t
     hipLaunchKernelGGL(transpose_upper_kernel<DT_BF16>, dim3(grid_for(n * n)), dim3(256), 0, s, src,
                        lds, n, out, ldo);
   return check_launch("transpose_upper");
+}
+
+
+// out[c][r] (dtype ODT) = src[r][c] for a rows x cols fp32 block, batched over
+// blockIdx.z (element strides bss / bso), through a 32 x 32 LDS tile.
+template <int ODT>
+__global__ void transpose_cast_kernel(const float* src, int64_t lds, int64_t bss, int64_t rows,
+                                      int64_t cols, void* out, int64_t ldo, int64_t bso) {
+  __shared__ float tile[32][33];
+  const float* S = src + (int64_t)blockIdx.z * bss;
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    tile[k][tx] = (r < rows && c < cols) ? S[r * lds + c] : 0.0f;
+  }
+  __syncthreads();
+  typedef typename Elem<ODT>::T OT;
+  OT* O = (OT*)out + (int64_t)blockIdx.z * bso;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (c < cols && r < rows) Elem<ODT>::store(O + c * ldo + r, tile[tx][k]);
+  }
+}
+
+int launch_transpose_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
+                          void* out, int odt, int64_t ldo, int batch, int64_t bss, int64_t bso) {
+  if (rows * cols == 0 || batch == 0) return IFK_OK;
+  if (cdiv(rows, 32) > 65535 || batch > 65535) {
+    set_error("transpose_cast: grid too large");
+    return IFK_ERR_INVALID;
+  }
+  const dim3 grid((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32), (unsigned)batch);
+  if (odt == DT_F32)
+    hipLaunchKernelGGL(transpose_cast_kernel<DT_F32>, grid, dim3(256), 0, s, src, lds, bss, rows,
+                       cols, out, ldo, bso);
+  else
+    hipLaunchKernelGGL(transpose_cast_kernel<DT_BF16>, grid, dim3(256), 0, s, src, lds, bss, rows,
+                       cols, out, ldo, bso);
+  return check_launch("transpose_cast");
 }
 
 }  // namespace ifk

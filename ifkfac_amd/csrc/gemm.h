@@ -71,8 +71,10 @@ int profile_end(int64_t* n_launches);
 int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
                 int64_t* n, int64_t* k);
 
+// max_wgs > 0 caps the number of workgroups of a large-tile launch (tiles are
+// then visited grid-stride), leaving CUs free for work on other streams.
 int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
          const MatRef& A, const MatRef& B, float beta, const OutRef& C, int batch,
-         SplitScratch scratch);
+         SplitScratch scratch, int max_wgs = 0);
 
 }  // namespace ifk

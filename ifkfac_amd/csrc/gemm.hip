@@ -455,7 +455,8 @@ static bool vec_ok(const MatRef& X) {
 }
 
 int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, const MatRef& A,
-         const MatRef& B, float beta, const OutRef& C, int batch, SplitScratch scratch) {
+         const MatRef& B, float beta, const OutRef& C, int batch, SplitScratch scratch,
+         int max_wgs) {
   if (M < 0 || N < 0 || K < 0 || batch < 1) {
     set_error("gemm: negative size or batch < 1");
     return IFK_ERR_INVALID;
@@ -507,7 +508,12 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     set_error("gemm: grid too large");
     return IFK_ERR_INVALID;
   }
-  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * splits));
+  unsigned gx = (unsigned)(p.tiles_m * p.tiles_n);
+  if (big && max_wgs > 0) {
+    const int64_t per_z = std::max<int64_t>(1, max_wgs / std::max<int64_t>(1, batch * splits));
+    gx = (unsigned)std::min<int64_t>(gx, per_z);
+  }
+  dim3 grid(gx, 1, (unsigned)(batch * splits));
   const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc);
   ProfRec* pr = prof_slot(vid);
   if (pr) {

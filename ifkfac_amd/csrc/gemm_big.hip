@@ -64,10 +64,20 @@ struct Slab {
   bool fast;
 };
 
+// Does the 32-wide K slab starting at k0 cross the structural-zero triangle of
+// a triangular operand over its rows [mn0, mn0 + ROWS)?  Only such slabs are
+// masked element by element (see tri0).
+template <bool ISA, int ROWS>
+__device__ inline bool slab_crosses(int tri, int64_t mn0, int64_t k0) {
+  if (tri == TRI_NONE) return false;
+  const bool zero_low_k = ISA ? tri == TRI_UPPER : tri == TRI_LOWER;  // zero where k < mn
+  return zero_low_k ? (k0 < mn0 + ROWS - 1) : (k0 + BK - 1 > mn0);
+}
+
 template <int DT, bool KC, bool ISA, int ROWS>
 __device__ inline void load(Slab<DT, ROWS>& S, const void* base, int64_t ld, int64_t MN, int64_t K,
                             int64_t mn0, int64_t k0, int tri, bool vec, int t) {
-  S.fast = vec && tri == TRI_NONE && (mn0 + ROWS <= MN) && (k0 + BK <= K);
+  S.fast = vec && (mn0 + ROWS <= MN) && (k0 + BK <= K);
   if (S.fast) {
     if constexpr (KC) {
 #pragma unroll
@@ -148,8 +158,12 @@ __device__ inline void load(Slab<DT, ROWS>& S, const void* base, int64_t ld, int
   }
 }
 
-template <int DT, bool KC, int ROWS>
-__device__ inline void put(bf16_t* L, const Slab<DT, ROWS>& S, int t) {
+template <int DT, bool KC, bool ISA, int ROWS>
+__device__ inline void put(bf16_t* L, const Slab<DT, ROWS>& S, int t, int tri, int64_t mn0,
+                           int64_t k0) {
+  // fast slabs that cross the triangle are masked here (the edge path masked
+  // on load)
+  const bool mask = S.fast && slab_crosses<ISA, ROWS>(tri, mn0, k0);
 #pragma unroll
   for (int q = 0; q < ROWS / 64; ++q) {
     int mn, kk;
@@ -185,19 +199,26 @@ __device__ inline void put(bf16_t* L, const Slab<DT, ROWS>& S, int t) {
         }
       }
     }
+    if (mask) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (tri0<ISA>(tri, mn0 + mn, k0 + kk + 2 * c)) w[c] &= 0xffff0000u;
+        if (tri0<ISA>(tri, mn0 + mn, k0 + kk + 2 * c + 1)) w[c] &= 0x0000ffffu;
+      }
+    }
     *(uint4*)(&L[mn * LW + kk]) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
+// One output tile (tile index `tile` of grid z) of the product.
 template <int ADT, bool AKC, int BDT, bool BKC>
-__global__ __launch_bounds__(NTH, 2) void gemm_big_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LW];
-  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * LW];
+__device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int tile, bf16_t (&As)[2][BM * LW],
+                                              bf16_t (&Bs)[2][BN * LW]) {
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, h = lane >> 5;
-  const int tm = blockIdx.x % p.tiles_m, tn = blockIdx.x / p.tiles_m;
+  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
   const int z = blockIdx.z;
   const int bidx = z / p.splits, split = z % p.splits;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -229,8 +250,8 @@ __global__ __launch_bounds__(NTH, 2) void gemm_big_kernel(GemmParams p) {
     const int64_t k0 = klo + kt0 * BK;
     load<ADT, AKC, true, BM>(sa, Ab, p.lda, p.M, khi, m0, k0, p.tria, p.vec_a, t);
     load<BDT, BKC, false, BN>(sb, Bb, p.ldb, p.N, khi, n0, k0, p.trib, p.vec_b, t);
-    put<ADT, AKC, BM>(As[0], sa, t);
-    put<BDT, BKC, BN>(Bs[0], sb, t);
+    put<ADT, AKC, true, BM>(As[0], sa, t, p.tria, m0, k0);
+    put<BDT, BKC, false, BN>(Bs[0], sb, t, p.trib, n0, k0);
   }
   __syncthreads();
   for (int64_t kt = kt0; kt < kt1; ++kt) {
@@ -259,8 +280,9 @@ __global__ __launch_bounds__(NTH, 2) void gemm_big_kernel(GemmParams p) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
     if (more) {
-      put<ADT, AKC, BM>(As[cur ^ 1], sa, t);
-      put<BDT, BKC, BN>(Bs[cur ^ 1], sb, t);
+      const int64_t k0 = klo + (kt + 1) * BK;
+      put<ADT, AKC, true, BM>(As[cur ^ 1], sa, t, p.tria, m0, k0);
+      put<BDT, BKC, false, BN>(Bs[cur ^ 1], sb, t, p.trib, n0, k0);
     }
     __syncthreads();
   }
@@ -306,6 +328,19 @@ __global__ __launch_bounds__(NTH, 2) void gemm_big_kernel(GemmParams p) {
         }
       }
     }
+}
+
+// Tiles are visited grid-stride, so a launch may use fewer workgroups than
+// tiles (leaving CUs to kernels on other streams).
+template <int ADT, bool AKC, int BDT, bool BKC>
+__global__ __launch_bounds__(NTH, 2) void gemm_big_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LW];
+  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * LW];
+  const int tiles = p.tiles_m * p.tiles_n;
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    gemm_big_tile<ADT, AKC, BDT, BKC>(p, tile, As, Bs);
+    __syncthreads();   // the LDS slabs are reused by the next tile
+  }
 }
 
 template <int ADT, bool AKC, int BDT, bool BKC>

@@ -11,21 +11,22 @@ namespace ifk {
 // PANEL_MAX_CB), reduced in slab order into G[cb * 4096].
 constexpr int PANEL_MAX_CB = 8;
 int gram_slabs(int64_t pe);
-// G = A^T [B0 | B1] over the pe rows (A at most 64 wide, B0 optional and at
-// most 64 wide, B1 w1 wide); *ncb_out = number of 64-column blocks of G.
-int launch_gram(hipStream_t s, const float* A, int64_t lda, int ka, const float* B0, int64_t ldb0,
-                int w0, const float* B1, int64_t ldb1, int w1, int64_t pe, float* part, float* G,
-                int* ncb_out);
+// G = A^T [B0 | B1] over the pe rows: A (at most 64 wide) stored transposed
+// when a_ts (else row-major), B0 optional, row-major and at most 64 wide, B1
+// (w1 wide) stored transposed; *ncb_out = number of 64-column blocks of G.
+int launch_gram(hipStream_t s, const float* A, int64_t lda, int ka, bool a_ts, const float* B0,
+                int64_t ldb0, int w0, const float* B1, int64_t ldb1, int w1, int64_t pe,
+                float* part, float* G, int* ncb_out);
 // CholeskyQR pass 1: G1 (+ P_top^T P_top) = U1^T U1, M1 = U1^{-1},
 // Q1 = P_top M1; *flag = 1 when a pivot falls below tol * its diagonal.
 int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t ldr, int b,
                       float tol, float* U1, float* M1, float* Q1, int* flag);
-// Householder TPQRT of [P_top; X_p] when *flag is set: reflectors into Q2
-// (ld 64, columns >= b zero), P_top <- R_new.
-int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* Xp, int64_t ldx,
-                             int64_t pe, int b, float* Q2, const int* flag);
-// Q2 = X_p M1 unless *flag is set
-int launch_apply_m(hipStream_t s, const float* X, int64_t ldx, int64_t pe, int b, const float* M,
+// Householder TPQRT of [P_top; X_p] when *flag is set (X_p given transposed,
+// XpT b x pe): reflectors into Q2 (ld 64, columns >= b zero), P_top <- R_new.
+int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* XpT,
+                             int64_t ldx, int64_t pe, int b, float* Q2, const int* flag);
+// Q2 = X_p M1 (X_p given transposed, XT b x pe) unless *flag is set
+int launch_apply_m(hipStream_t s, const float* XT, int64_t ldx, int64_t pe, int b, const float* M,
                    float* Q2, const int* flag);
 // CholeskyQR pass 2 + Householder reconstruction (T, N, NT, R_new) from G2
 // (+ Q1^T Q1); for a flagged panel T from the UT transform of Y^T Y, N = I,
@@ -38,10 +39,13 @@ int launch_panel_wcomp(hipStream_t s, const float* G, int ncb, int b, const floa
                        const float* NT, const float* T, float* Rrest, int64_t ldr, int nr, float* NW,
                        int64_t ldnw);
 // Y = Q2 N (ld ldy; also RNE bf16 into Yb, same ld, when Yb is given) and
-// C_rest -= Q2 NW
+// CT_rest -= (Q2 NW)^T on the transposed working matrix (nr rows of ld ldc)
 int launch_panel_update(hipStream_t s, const float* Q2, int64_t pe, int b, const float* N,
-                        float* Y, int64_t ldy, bf16_t* Yb, const float* NW, int64_t ldnw, float* C,
-                        int64_t ldc, int nr);
+                        float* Y, int64_t ldy, bf16_t* Yb, const float* NW, int64_t ldnw,
+                        float* CT, int64_t ldc, int nr);
+// R_blk (rows x cols, ldr) -= WT^T (WT cols x rows, ldw)
+int launch_sub_transposed(hipStream_t s, float* R, int64_t ldr, const float* WT, int64_t ldw,
+                          int64_t rows, int64_t cols);
 // Tinv = striu(G) + diag(1 + diag G) / 2 (UT transform of a reflector Gram matrix)
 int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,
                    int64_t ldt);
@@ -85,6 +89,11 @@ int launch_transpose_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds
 // out (odt, n x n) = lower triangle of src^T, i.e. out[i][j] = src[j][i] for j <= i, else 0
 int launch_transpose_upper(hipStream_t s, const float* src, int64_t lds, int64_t n, void* out,
                            int odt, int64_t ldo);
+// out[c][r] (odt) = src[r][c] for a rows x cols fp32 block; batched with
+// element strides bss (src) and bso (out)
+int launch_transpose_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
+                          void* out, int odt, int64_t ldo, int batch = 1, int64_t bss = 0,
+                          int64_t bso = 0);
 // out (dt) = alpha * x (fp32) with optional bf16 output
 int launch_scale_copy_vec(hipStream_t s, const float* x, int64_t n, float alpha, void* out, int odt);
 

@@ -27,6 +27,8 @@
 //   Z12 = -Z11 R12 Z22 with batched MFMA GEMMs, log2(n/64) levels), then
 //   nat = Z_G (Z_G^T grad) Z_X Z_X^T as four triangular MFMA products.
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <cmath>
 
 #include "gemm.h"
@@ -47,6 +49,10 @@ namespace ifk {
 // of orthogonality is far below its own 1/4 pivot threshold.
 static constexpr float HR_TOL = 1e-4f;
 static constexpr int64_t OUTER_B = 512;
+// Workgroup cap of the far-column products on the helper stream: one per CU
+// on 192 of the 256 CUs, so the panel kernels of the next outer block keep
+// CUs (and LDS) of their own.
+static constexpr int FAR_MAX_WGS = 192;
 
 static size_t split_floats(int64_t b, int64_t n) {
   size_t f = (size_t)64 * b * n;
@@ -63,42 +69,50 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
                       int64_t ldz, int math, int safe, float* tmp, SplitScratch sp);
 
 struct FoldWs {
-  float* C;      // p x n working copy of the chunk
-  float* Yo;     // p x OUTER_B: reflector X parts of the current outer block
-  float* Yto;    // p x OUTER_B: Y T of the outer block (fp32 arithmetic)
-  bf16_t* Yob;   // bf16 copies of Yo, Y T and W for bf16 arithmetic (the
-  bf16_t* Ytob;  // products round their operands to bf16 anyway)
-  bf16_t* Wb;
-  float* Q2;     // p x 64: X_p M1, or the fallback's reflectors
-  float* W;      // OUTER_B x n
-  float* part;   // per-slab Gram matrices of the panel kernels
-  float* Gp;     // their sum: PANEL_MAX_CB blocks of 64 x 64
-  float* NW;     // 64 x OUTER_B: N W of the panel
-  float* U1;     // 64 x 64 panel scratch
+  float* C;       // n x p: the chunk, transposed (CT = C^T; see fold_core)
+  float* Yo[2];   // p x OUTER_B: reflector X parts of an outer block (by block parity)
+  float* Yto[2];  // OUTER_B x p: (Y T)^T of an outer block (fp32 arithmetic)
+  bf16_t* Yob[2];   // bf16 copies of Yo and (Y T)^T for bf16 arithmetic (the
+  bf16_t* Ytob[2];  // products round their operands to bf16 anyway)
+  float* Wn;      // OUTER_B x OUTER_B: W^T of the near columns (critical stream)
+  float* Wf;      // n x OUTER_B: W^T of the far columns (helper stream)
+  bf16_t* Wnb;
+  bf16_t* Wfb;
+  float* Q2;      // p x 64: X_p M1, or the fallback's reflectors
+  float* part;    // per-slab Gram matrices of the panel kernels
+  float* Gp;      // their sum: PANEL_MAX_CB blocks of 64 x 64
+  float* NW;      // 64 x OUTER_B: N W of the panel
+  float* U1;      // 64 x 64 panel scratch
   float* M1;
   float* Q1;
   float* N;
   float* NT;
   float* T;
-  float* Go;     // OUTER_B x OUTER_B: Gram of the outer reflectors
-  float* Tio;    // OUTER_B x OUTER_B: UT transform T^{-1}
-  float* To;     // OUTER_B x OUTER_B: T of the outer block
-  float* ttmp;   // triangular-inverse scratch for To
+  float* Go;      // OUTER_B x OUTER_B: Gram of the outer reflectors
+  float* Tio;     // OUTER_B x OUTER_B: UT transform T^{-1}
+  float* To[2];   // OUTER_B x OUTER_B: T of an outer block (by block parity)
+  float* ttmp;    // triangular-inverse scratch for To
   SplitScratch tsp;
   int* flag;
-  SplitScratch split;
+  SplitScratch split;   // split-K scratch of the critical stream
+  SplitScratch split2;  // ... and of the helper stream
 };
 
 static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   const int64_t b = PANEL_B, B = OUTER_B;
   w.C = need_C ? a.take<float>((size_t)p * n) : nullptr;
-  w.Yo = a.take<float>((size_t)p * B);
-  w.Yto = a.take<float>((size_t)p * B);
-  w.Yob = a.take<bf16_t>((size_t)p * B);
-  w.Ytob = a.take<bf16_t>((size_t)p * B);
-  w.Wb = a.take<bf16_t>((size_t)B * n);
+  for (int i = 0; i < 2; ++i) {
+    w.Yo[i] = a.take<float>((size_t)p * B);
+    w.Yto[i] = a.take<float>((size_t)p * B);
+    w.Yob[i] = a.take<bf16_t>((size_t)p * B);
+    w.Ytob[i] = a.take<bf16_t>((size_t)p * B);
+    w.To[i] = a.take<float>(B * B);
+  }
+  w.Wn = a.take<float>((size_t)B * B);
+  w.Wf = a.take<float>((size_t)B * n);
+  w.Wnb = a.take<bf16_t>((size_t)B * B);
+  w.Wfb = a.take<bf16_t>((size_t)B * n);
   w.Q2 = a.take<float>((size_t)p * b);
-  w.W = a.take<float>((size_t)B * n);
   w.part = a.take<float>((size_t)gram_slabs(p) * PANEL_MAX_CB * b * b);
   w.Gp = a.take<float>((size_t)PANEL_MAX_CB * b * b);
   w.NW = a.take<float>((size_t)b * B);
@@ -110,61 +124,141 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   w.T = a.take<float>(b * b);
   w.Go = a.take<float>(B * B);
   w.Tio = a.take<float>(B * B);
-  w.To = a.take<float>(B * B);
   w.ttmp = a.take<float>((size_t)B * B / 2 + (size_t)TRINV_NB * TRINV_NB * 4);
   w.tsp.floats = split_floats(TRINV_NB, B);
   w.tsp.p = a.take<float>(w.tsp.floats);
   w.flag = a.take<int>(64);
   w.split.floats = split_floats(B, n);
   w.split.p = a.take<float>(w.split.floats);
+  w.split2.floats = split_floats(B, n);
+  w.split2.p = a.take<float>(w.split2.floats);
 }
 
-// Apply the finished outer block (reflectors Yo of columns [K0, K1), pe rows)
-// to the columns [K1, n):
-//   T^{-1} = striu(Yo^T Yo) + diag(1 + diag(Yo^T Yo)) / 2   (UT transform)
-//   W = (Yo T)^T C + T^T R_blk,  R_blk -= W,  C -= Yo W
-// In bf16 arithmetic every product reads the bf16 copies (Yob, Ytob, Wb),
-// which hold exactly the RNE roundings the MFMA operands would get; W and R
-// stay fp32.
-static int outer_update(hipStream_t s, int math, FoldWs& w, float* C, int64_t ldc, int64_t pe,
-                        float* R, int64_t ldr, int64_t K0, int64_t K1, int64_t n) {
-  const int64_t B = OUTER_B, KB = K1 - K0, nt = n - K1;
+// ----------------------------------------------------------------------------
+// Helper stream and events of the look-ahead (one set per device, created on
+// first use; a fold holds the device's lock while it enqueues).
+// ----------------------------------------------------------------------------
+struct LookAhead {
+  std::mutex mu;
+  hipStream_t s2 = nullptr;
+  hipEvent_t ready[2] = {nullptr, nullptr};
+  hipEvent_t far[2] = {nullptr, nullptr};
+};
+
+static LookAhead* look_ahead(int* rc) {
+  static std::mutex g_mu;
+  static std::map<int, LookAhead*> g_la;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("tsqr_fold: hipGetDevice failed");
+    *rc = IFK_ERR_HIP;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(g_mu);
+  LookAhead*& la = g_la[dev];
+  if (!la) {
+    LookAhead* x = new LookAhead();
+    bool ok = hipStreamCreateWithFlags(&x->s2, hipStreamNonBlocking) == hipSuccess;
+    for (int i = 0; i < 2 && ok; ++i)
+      ok = hipEventCreateWithFlags(&x->ready[i], hipEventDisableTiming) == hipSuccess &&
+           hipEventCreateWithFlags(&x->far[i], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+      set_error("tsqr_fold: cannot create the helper stream or its events");
+      *rc = IFK_ERR_HIP;
+      return nullptr;
+    }
+    la = x;
+  }
+  *rc = IFK_OK;
+  return la;
+}
+
+#define HIPRC(x, what)              \
+  do {                              \
+    if ((x) != hipSuccess) {        \
+      set_error(what);              \
+      return IFK_ERR_HIP;           \
+    }                               \
+  } while (0)
+
+// Outer block k (reflectors Yo of columns [K0, K1), pe rows, buffers of
+// parity k2): T from the UT transform
+//   T^{-1} = striu(Yo^T Yo) + diag(1 + diag(Yo^T Yo)) / 2
+// and Y T.  In bf16 arithmetic every product reads the bf16 copies (Yob,
+// Ytob, W bf16), which hold exactly the RNE roundings the MFMA operands would
+// get; T, W and R stay fp32.
+static int outer_prepare(hipStream_t s, int math, FoldWs& w, int k2, int64_t pe, int64_t KB) {
+  const int64_t B = OUTER_B;
   const bool bf = math == MATH_BF16;
-  const MatRef YoT = bf ? A_t(w.Yob, DT_BF16, B) : A_t(w.Yo, DT_F32, B);
-  const MatRef YoB = bf ? B_n(w.Yob, DT_BF16, B) : B_n(w.Yo, DT_F32, B);
+  const MatRef YoT = bf ? A_t(w.Yob[k2], DT_BF16, B) : A_t(w.Yo[k2], DT_F32, B);
+  const MatRef YoB = bf ? B_n(w.Yob[k2], DT_BF16, B) : B_n(w.Yo[k2], DT_F32, B);
   RC(gemm(s, math, KB, KB, pe, 1.0f, YoT, YoB, 0.0f, out_f32(w.Go, KB), 1, w.split));
   RC(launch_ut_tinv(s, w.Go, KB, KB, w.Tio, KB));
-  RC(trinv_core(s, w.Tio, DT_F32, KB, KB, w.To, KB, MATH_F32, 0, w.ttmp, w.tsp));
-  const MatRef YoA = bf ? A_n(w.Yob, DT_BF16, B) : A_n(w.Yo, DT_F32, B);
-  RC(gemm(s, math, pe, KB, KB, 1.0f, YoA, B_n(w.To, DT_F32, KB, TRI_UPPER), 0.0f,
-          bf ? out_bf16(w.Ytob, B) : out_f32(w.Yto, B), 1, w.split));
-  float* Rb = R + K0 * ldr + K1;
-  const MatRef YtoT = bf ? A_t(w.Ytob, DT_BF16, B) : A_t(w.Yto, DT_F32, B);
-  RC(gemm(s, math, KB, nt, pe, 1.0f, YtoT, B_n(C + K1, DT_F32, ldc), 0.0f, out_f32(w.W, nt), 1,
-          w.split));
-  RC(gemm(s, math, KB, nt, KB, 1.0f, A_t(w.To, DT_F32, KB, TRI_LOWER), B_n(Rb, DT_F32, ldr), 1.0f,
-          bf ? out_both(w.W, nt, w.Wb, nt) : out_f32(w.W, nt), 1, w.split));
-  RC(launch_sub_inplace(s, Rb, ldr, w.W, nt, KB, nt));
-  const MatRef WB = bf ? B_n(w.Wb, DT_BF16, nt) : B_n(w.W, DT_F32, nt);
-  return gemm(s, math, pe, nt, KB, -1.0f, YoA, WB, 1.0f, out_f32(C + K1, ldc), 1, w.split);
+  RC(trinv_core(s, w.Tio, DT_F32, KB, KB, w.To[k2], KB, MATH_F32, 0, w.ttmp, w.tsp));
+  // (Y T)^T = T^T Y^T, K-contiguous in both operands
+  const MatRef YoBt = bf ? B_t(w.Yob[k2], DT_BF16, B) : B_t(w.Yo[k2], DT_F32, B);
+  return gemm(s, math, KB, pe, KB, 1.0f, A_t(w.To[k2], DT_F32, KB, TRI_LOWER), YoBt, 0.0f,
+              bf ? out_bf16(w.Ytob[k2], pe) : out_f32(w.Yto[k2], pe), 1, w.split);
 }
 
-// Core of the fold on an fp32 working copy C (p x n, ldc).  R rows [0, r_new)
-// receive the result.  Two-level blocking: 64-column panels inside 512-column
+// Apply outer block k to the columns [c_lo, c_hi) of C, i.e. the rows
+// [c_lo, c_hi) of the transposed working matrix CT (ld ldc):
+//   W^T = CT_cols (Y T) + R_blk^T T,  R_blk -= (W^T)^T,  CT_cols -= W^T Y^T
+// The two large products read K-contiguous operands only.  W^T is nt x KB.
+static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, int64_t ldc,
+                       int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1, int64_t c_lo,
+                       int64_t c_hi, float* W, bf16_t* Wb, SplitScratch sp, int max_wgs) {
+  const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
+  if (nt <= 0) return IFK_OK;
+  const bool bf = math == MATH_BF16;
+  float* Rb = R + K0 * ldr + c_lo;
+  float* Cr = CT + c_lo * ldc;
+  const MatRef YtoTB = bf ? B_t(w.Ytob[k2], DT_BF16, pe) : B_t(w.Yto[k2], DT_F32, pe);
+  RC(gemm(s, math, nt, KB, pe, 1.0f, A_n(Cr, DT_F32, ldc), YtoTB, 0.0f, out_f32(W, KB), 1, sp,
+          max_wgs));
+  RC(gemm(s, math, nt, KB, KB, 1.0f, A_t(Rb, DT_F32, ldr), B_n(w.To[k2], DT_F32, KB, TRI_UPPER),
+          1.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB), 1, sp));
+  RC(launch_sub_transposed(s, Rb, ldr, W, KB, KB, nt));
+  const MatRef WA = bf ? A_n(Wb, DT_BF16, KB) : A_n(W, DT_F32, KB);
+  const MatRef YoBt = bf ? B_t(w.Yob[k2], DT_BF16, B) : B_t(w.Yo[k2], DT_F32, B);
+  return gemm(s, math, nt, pe, KB, -1.0f, WA, YoBt, 1.0f, out_f32(Cr, ldc), 1, sp, max_wgs);
+}
+
+// Core of the fold on the transposed fp32 working copy CT = C^T (n x p, row
+// stride ldc; a panel X_p = C[:, c0:c1] is the contiguous row block
+// CT[c0:c1, :]).  R rows [0, r_new) receive the result.  Two-level blocking: 64-column panels inside 512-column
 // outer blocks; a panel's reflectors update only the rest of its outer block,
 // and each finished outer block is applied to the columns beyond it as one
-// block reflector whose T is the UT transform of the outer Y.  With x_tri, C
-// is upper triangular and a panel ending at column c1 involves C rows [0, c1).
+// block reflector.  Look-ahead: of that application only the next outer
+// block's columns stay on the critical stream s; the columns beyond run on
+// the device's helper stream and overlap the next block's panels (which are
+// latency-bound on a few CUs).  Buffers a far update still reads are double
+// buffered by block parity, and events order
+//   prepare(k) -> far(k);  far(k-1) -> near(k);  far(last) -> end of fold.
+// With x_tri, C is upper triangular and a panel ending at column c1
+// involves C rows [0, c1).
 static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n, float* R,
                      int64_t ldr, int64_t r_new, bool x_tri, int math, FoldWs& w) {
   const int64_t B = OUTER_B;
-  for (int64_t K0 = 0; K0 < r_new; K0 += B) {
+  int rc = IFK_OK;
+  LookAhead* la = nullptr;
+  if (std::min<int64_t>(B, r_new) + B < n) {  // some block has columns beyond the next one
+    la = look_ahead(&rc);
+    if (!la) return rc;
+  }
+  std::unique_lock<std::mutex> lock;
+  if (la) lock = std::unique_lock<std::mutex>(la->mu);
+  int far_pending = -1;  // parity of the last far update not yet joined
+  int k = 0;
+  for (int64_t K0 = 0; K0 < r_new; K0 += B, ++k) {
+    const int k2 = k & 1;
     const int64_t K1 = std::min<int64_t>(K0 + B, r_new);
     const int64_t KB = K1 - K0;
     const int64_t pe_o = x_tri ? std::min<int64_t>(p, K1) : p;
+    const bool bf = math == MATH_BF16;
     if (x_tri) {
-      RC(launch_zero(s, w.Yo, B, pe_o, KB));
-      if (math == MATH_BF16) RC(launch_zero_bf16(s, w.Yob, B, pe_o, KB));
+      RC(launch_zero(s, w.Yo[k2], B, pe_o, KB));
+      if (bf) RC(launch_zero_bf16(s, w.Yob[k2], B, pe_o, KB));
     }
     for (int64_t c0 = K0; c0 < K1; c0 += PANEL_B) {
       const int bk = (int)std::min<int64_t>(PANEL_B, K1 - c0);
@@ -172,25 +266,51 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
       const int nr = (int)(K1 - c1);
       const int64_t pe = x_tri ? std::min<int64_t>(p, c1) : p;
       float* Ptop = R + c0 * ldr + c0;
-      float* Xp = C + c0;
+      float* XpT = C + c0 * ldc;
       int ncb;
       // pass 1: G1 = X_p^T X_p (+ P_top^T P_top), U1, M1 -- or the fallback
-      RC(launch_gram(s, Xp, ldc, bk, nullptr, 0, 0, Xp, ldc, bk, pe, w.part, w.Gp, &ncb));
+      RC(launch_gram(s, XpT, ldc, bk, true, nullptr, 0, 0, XpT, ldc, bk, pe, w.part, w.Gp, &ncb));
       RC(launch_panel_hr_a(s, w.Gp, Ptop, ldr, bk, HR_TOL, w.U1, w.M1, w.Q1, w.flag));
-      RC(launch_panel_hh_fallback(s, Ptop, ldr, Xp, ldc, pe, bk, w.Q2, w.flag));
+      RC(launch_panel_hh_fallback(s, Ptop, ldr, XpT, ldc, pe, bk, w.Q2, w.flag));
       // pass 2: Q2 = X_p M1, G2 = Q2^T Q2 and Q2^T C_rest in one sweep
-      RC(launch_apply_m(s, Xp, ldc, pe, bk, w.M1, w.Q2, w.flag));
-      RC(launch_gram(s, w.Q2, PANEL_B, PANEL_B, w.Q2, PANEL_B, PANEL_B, C + c1, ldc, nr, pe, w.part,
-                     w.Gp, &ncb));
+      RC(launch_apply_m(s, XpT, ldc, pe, bk, w.M1, w.Q2, w.flag));
+      RC(launch_gram(s, w.Q2, PANEL_B, PANEL_B, false, w.Q2, PANEL_B, PANEL_B, C + c1 * ldc, ldc,
+                     nr, pe, w.part, w.Gp, &ncb));
       RC(launch_panel_hr_b(s, w.Gp, w.Q1, w.U1, bk, w.N, w.NT, w.T, Ptop, ldr, w.flag));
       // rest of the outer block: R_rest and C_rest, Y into the outer store
       RC(launch_panel_wcomp(s, w.Gp, ncb, bk, w.N, w.NT, w.T, Ptop + bk, ldr, nr, w.NW, OUTER_B));
-      RC(launch_panel_update(s, w.Q2, pe, bk, w.N, w.Yo + (c0 - K0), OUTER_B,
-                             math == MATH_BF16 ? w.Yob + (c0 - K0) : nullptr, w.NW, OUTER_B,
-                             C + c1, ldc, nr));
+      RC(launch_panel_update(s, w.Q2, pe, bk, w.N, w.Yo[k2] + (c0 - K0), OUTER_B,
+                             bf ? w.Yob[k2] + (c0 - K0) : nullptr, w.NW, OUTER_B, C + c1 * ldc,
+                             ldc, nr));
     }
-    if (K1 < n) RC(outer_update(s, math, w, C, ldc, pe_o, R, ldr, K0, K1, n));
+    if (K1 >= n) continue;
+    RC(outer_prepare(s, math, w, k2, pe_o, KB));
+    const int64_t near_hi = std::min<int64_t>(K1 + B, n);
+    if (la && near_hi < n) {
+      // far columns on the helper stream, as soon as T and Y T are ready
+      HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
+      HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
+      RC(outer_apply(la->s2, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, near_hi, n, w.Wf, w.Wfb,
+                     w.split2, FAR_MAX_WGS));
+    }
+    // near columns wait for the previous block's far update, which covers them
+    if (far_pending >= 0) {
+      HIPRC(hipStreamWaitEvent(s, la->far[far_pending], 0), "tsqr_fold: stream wait failed");
+      far_pending = -1;
+    }
+    if (la && near_hi < n) {
+      HIPRC(hipEventRecord(la->far[k2], la->s2), "tsqr_fold: event record failed");
+      far_pending = k2;
+    }
+    if (la)
+      RC(outer_apply(s, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wn, w.Wnb,
+                     w.split, 0));
+    else
+      RC(outer_apply(s, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wf, w.Wfb, w.split,
+                     0));
   }
+  if (far_pending >= 0)
+    HIPRC(hipStreamWaitEvent(s, la->far[far_pending], 0), "tsqr_fold: stream wait failed");
   return launch_sign_normalize(s, R, ldr, r_new, n);
 }
 
@@ -226,8 +346,8 @@ int fold(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ld
   plan_fold(a, p, n, true, w);
   RC(check_ws(a, "tsqr_fold"));
   RC(launch_zero_rows(s, R, ldr, r_in, n, n));
-  RC(launch_copy_to_f32(s, X, xdt, ldx, p, n, 1.0f, w.C, n));
-  RC(fold_core(s, w.C, n, p, n, R, ldr, r_new, false, math, w));
+  RC(launch_transpose_to_f32(s, X, xdt, ldx, p, n, w.C, p));
+  RC(fold_core(s, w.C, p, p, n, R, ldr, r_new, false, math, w));
   if (r_out) *r_out = r_new;
   return IFK_OK;
 }
@@ -277,11 +397,18 @@ static void plan_trinv(Arena& a, int64_t n, float** tmp, SplitScratch* sp) {
   sp->p = a.take<float>(sp->floats);
 }
 
+// ... plus the transposed bf16 copy of Z used by bf16 arithmetic
+static void plan_trinv(Arena& a, int64_t n, float** tmp, bf16_t** zt, SplitScratch* sp) {
+  plan_trinv(a, n, tmp, sp);
+  *zt = a.take<bf16_t>((size_t)n * n);
+}
+
 size_t trinv_ws(int64_t n) {
   Arena a(nullptr, 0);
   float* tmp;
+  bf16_t* zt;
   SplitScratch sp;
-  plan_trinv(a, n, &tmp, &sp);
+  plan_trinv(a, n, &tmp, &zt, &sp);
   return a.used;
 }
 
@@ -317,6 +444,57 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
   return IFK_OK;
 }
 
+// bf16-arithmetic triangular inverse that keeps a transposed bf16 copy ZT of
+// Z (n x n, ld n) next to it, so every product reads K-contiguous operands:
+// per doubling level, for the diagonal pair (Z11, Z22) and the block R12,
+//   TmpT = ZT22 R12^T,   Z12 = -Z11 TmpT^T,   ZT21 = Z12^T.
+// tmpT: n^2 / 2 + 4 * 64^2 bf16 elements.
+static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
+                        int64_t ldz, int safe, bf16_t* ZT, bf16_t* tmpT, SplitScratch sp) {
+  const size_t esz = rdt == DT_F32 ? 4 : 2;
+  const char* Rc = (const char*)R;
+  const int64_t NB = TRINV_NB;
+  RC(launch_zero(s, Z, ldz, n, n));
+  RC(launch_zero_bf16(s, ZT, n, n, n));
+  RC(launch_trinv_diag(s, R, rdt, ldr, n, NB, Z, ldz, safe));
+  const int64_t nbf = n / NB;
+  if (nbf > 0)
+    RC(launch_transpose_cast(s, Z, ldz, NB, NB, ZT, DT_BF16, n, (int)nbf, NB * (ldz + 1),
+                             NB * (n + 1)));
+  if (nbf * NB < n) {
+    const int64_t i0 = nbf * NB, r = n - i0;
+    RC(launch_transpose_cast(s, Z + i0 * ldz + i0, ldz, r, r, ZT + i0 * n + i0, DT_BF16, n));
+  }
+  for (int64_t w = NB; w < n; w *= 2) {
+    const int64_t step = 2 * w;
+    const int64_t nfull = n / step;
+    if (nfull > 0) {
+      const void* R12 = Rc + (size_t)w * esz;  // block (0, w) of pair 0
+      RC(gemm(s, MATH_BF16, w, w, w, 1.0f, A_n(ZT + w * n + w, DT_BF16, n, TRI_LOWER, step * (n + 1)),
+              B_t(R12, rdt, ldr, TRI_NONE, step * (ldr + 1)), 0.0f, out_bf16(tmpT, w, w * w),
+              (int)nfull, sp));
+      RC(gemm(s, MATH_BF16, w, w, w, -1.0f, A_n(Z, DT_F32, ldz, TRI_UPPER, step * (ldz + 1)),
+              B_t(tmpT, DT_BF16, w, TRI_NONE, w * w), 0.0f, out_f32(Z + w, ldz, step * (ldz + 1)),
+              (int)nfull, sp));
+      RC(launch_transpose_cast(s, Z + w, ldz, w, w, ZT + w * n, DT_BF16, n, (int)nfull,
+                               step * (ldz + 1), step * (n + 1)));
+    }
+    const int64_t i0 = nfull * step;
+    if (i0 + w < n) {
+      const int64_t w2 = n - i0 - w;
+      const void* R12 = Rc + ((size_t)i0 * ldr + i0 + w) * esz;  // w x w2
+      RC(gemm(s, MATH_BF16, w2, w, w2, 1.0f,
+              A_n(ZT + (i0 + w) * n + i0 + w, DT_BF16, n, TRI_LOWER), B_t(R12, rdt, ldr), 0.0f,
+              out_bf16(tmpT, w), 1, sp));
+      RC(gemm(s, MATH_BF16, w, w2, w, -1.0f, A_n(Z + i0 * ldz + i0, DT_F32, ldz, TRI_UPPER),
+              B_t(tmpT, DT_BF16, w), 0.0f, out_f32(Z + i0 * ldz + i0 + w, ldz), 1, sp));
+      RC(launch_transpose_cast(s, Z + i0 * ldz + i0 + w, ldz, w, w2, ZT + (i0 + w) * n + i0,
+                               DT_BF16, n));
+    }
+  }
+  return IFK_OK;
+}
+
 int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,
           int math, int safe, void* ws, size_t ws_bytes) {
   if (n < 1 || ldr < n || ldz < n || !R || !Z || (rdt != DT_F32 && rdt != DT_BF16)) {
@@ -325,9 +503,12 @@ int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* 
   }
   Arena a(ws, ws_bytes);
   float* tmp;
+  bf16_t* zt;
   SplitScratch sp;
-  plan_trinv(a, n, &tmp, &sp);
+  plan_trinv(a, n, &tmp, &zt, &sp);
   RC(check_ws(a, "tri_inverse"));
+  if (math == MATH_BF16)
+    return trinv_core_t(s, R, rdt, ldr, n, Z, ldz, safe, zt, (bf16_t*)tmp, sp);
   return trinv_core(s, R, rdt, ldr, n, Z, ldz, math, safe, tmp, sp);
 }
 
@@ -335,11 +516,13 @@ int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* 
 // Preconditioning
 // ----------------------------------------------------------------------------
 static void plan_apply(Arena& a, int64_t n_out, int64_t n_in, int math, void** T1, void** T2,
-                       SplitScratch* sp) {
+                       bf16_t** cv, SplitScratch* sp) {
   const size_t e = (size_t)n_out * n_in;
+  *cv = nullptr;
   if (math == MATH_BF16) {
     *T1 = a.take<bf16_t>(e);
     *T2 = a.take<bf16_t>(e);
+    *cv = a.take<bf16_t>(e + 2 * (size_t)n_out * n_out + 2 * (size_t)n_in * n_in);
   } else {
     *T1 = a.take<float>(e);
     *T2 = a.take<float>(e);
@@ -351,15 +534,44 @@ static void plan_apply(Arena& a, int64_t n_out, int64_t n_in, int math, void** T
 size_t precondition_apply_ws(int64_t n_out, int64_t n_in, int math) {
   Arena a(nullptr, 0);
   void *T1, *T2;
+  bf16_t* cv;
   SplitScratch sp;
-  plan_apply(a, n_out, n_in, math, &T1, &T2, &sp);
+  plan_apply(a, n_out, n_in, math, &T1, &T2, &cv, &sp);
   return a.used;
 }
 
 static int apply_core(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,
                       const float* ZX, int64_t ldzx, const float* ZG, int64_t ldzg, float* nat,
-                      int64_t ldn, int math, void* T1, void* T2, SplitScratch sp) {
-  const int tdt = math == MATH_BF16 ? DT_BF16 : DT_F32;
+                      int64_t ldn, int math, void* T1, void* T2, bf16_t* cv, SplitScratch sp) {
+  if (math == MATH_BF16) {
+    // bf16 copies (the RNE roundings the MFMA operands get anyway) of grad^T,
+    // Z_G, Z_G^T, Z_X, Z_X^T make every product K-contiguous in both operands
+    bf16_t* gT = cv;                                   // n_in x n_out
+    bf16_t* ZGb = gT + (size_t)n_in * n_out;           // n_out x n_out
+    bf16_t* ZGt = ZGb + (size_t)n_out * n_out;
+    bf16_t* ZXb = ZGt + (size_t)n_out * n_out;         // n_in x n_in
+    bf16_t* ZXt = ZXb + (size_t)n_in * n_in;
+    RC(launch_transpose_cast(s, grad, ldg, n_out, n_in, gT, DT_BF16, n_out));
+    RC(launch_cast(s, ZG, ldzg, n_out, n_out, ZGb, DT_BF16, n_out));
+    RC(launch_transpose_cast(s, ZG, ldzg, n_out, n_out, ZGt, DT_BF16, n_out));
+    RC(launch_cast(s, ZX, ldzx, n_in, n_in, ZXb, DT_BF16, n_in));
+    RC(launch_transpose_cast(s, ZX, ldzx, n_in, n_in, ZXt, DT_BF16, n_in));
+    bf16_t* T1T = (bf16_t*)T1;   // n_in x n_out
+    bf16_t* Tb = (bf16_t*)T2;    // n_out x n_in
+    // T1^T = grad^T Z_G          (T1 = Z_G^T grad: R_G^T T1 = grad, triangular.py:632)
+    RC(gemm(s, math, n_in, n_out, n_out, 1.0f, A_n(gT, DT_BF16, n_out),
+            B_t(ZGt, DT_BF16, n_out, TRI_UPPER), 0.0f, out_bf16(T1T, n_out), 1, sp));
+    // T2 = Z_G T1                (R_G T2 = T1, triangular.py:636)
+    RC(gemm(s, math, n_out, n_in, n_out, 1.0f, A_n(ZGb, DT_BF16, n_out, TRI_UPPER),
+            B_t(T1T, DT_BF16, n_out), 0.0f, out_bf16(Tb, n_in), 1, sp));
+    // T3 = T2 Z_X                (R_X^T T3^T = T2^T, triangular.py:645), into T1's buffer
+    RC(gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(Tb, DT_BF16, n_in),
+            B_t(ZXt, DT_BF16, n_in, TRI_UPPER), 0.0f, out_bf16(T1T, n_in), 1, sp));
+    // nat = T3 Z_X^T             (R_X T4^T = T3^T, triangular.py:649)
+    return gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(T1T, DT_BF16, n_in),
+                B_t(ZXb, DT_BF16, n_in, TRI_LOWER), 0.0f, out_f32(nat, ldn), 1, sp);
+  }
+  const int tdt = DT_F32;
   auto out_t = [&](void* p, int64_t ld) {
     return tdt == DT_BF16 ? out_bf16((bf16_t*)p, ld) : out_f32((float*)p, ld);
   };
@@ -388,26 +600,29 @@ int precondition_apply(hipStream_t s, const float* grad, int64_t n_out, int64_t 
   }
   Arena a(ws, ws_bytes);
   void *T1, *T2;
+  bf16_t* cv;
   SplitScratch sp;
-  plan_apply(a, n_out, n_in, math, &T1, &T2, &sp);
+  plan_apply(a, n_out, n_in, math, &T1, &T2, &cv, &sp);
   RC(check_ws(a, "precondition_apply"));
-  return apply_core(s, grad, n_out, n_in, ldg, ZX, ldzx, ZG, ldzg, nat, ldn, math, T1, T2, sp);
+  return apply_core(s, grad, n_out, n_in, ldg, ZX, ldzx, ZG, ldzg, nat, ldn, math, T1, T2, cv, sp);
 }
 
 static void plan_prec(Arena& a, int64_t n_out, int64_t n_in, int math, float** ZX, float** ZG,
-                      float** tmp, SplitScratch* tsp, void** T1, void** T2, SplitScratch* asp) {
+                      float** tmp, bf16_t** zt, SplitScratch* tsp, void** T1, void** T2,
+                      bf16_t** cv, SplitScratch* asp) {
   *ZX = a.take<float>((size_t)n_in * n_in);
   *ZG = a.take<float>((size_t)n_out * n_out);
-  plan_trinv(a, std::max(n_in, n_out), tmp, tsp);
-  plan_apply(a, n_out, n_in, math, T1, T2, asp);
+  plan_trinv(a, std::max(n_in, n_out), tmp, zt, tsp);
+  plan_apply(a, n_out, n_in, math, T1, T2, cv, asp);
 }
 
 size_t precondition_ws(int64_t n_out, int64_t n_in, int math) {
   Arena a(nullptr, 0);
   float *ZX, *ZG, *tmp;
+  bf16_t *zt, *cv;
   void *T1, *T2;
   SplitScratch tsp, asp;
-  plan_prec(a, n_out, n_in, math, &ZX, &ZG, &tmp, &tsp, &T1, &T2, &asp);
+  plan_prec(a, n_out, n_in, math, &ZX, &ZG, &tmp, &zt, &tsp, &T1, &T2, &cv, &asp);
   return a.used;
 }
 
@@ -421,13 +636,20 @@ int precondition(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, 
   }
   Arena a(ws, ws_bytes);
   float *ZX, *ZG, *tmp;
+  bf16_t *zt, *cv;
   void *T1, *T2;
   SplitScratch tsp, asp;
-  plan_prec(a, n_out, n_in, math, &ZX, &ZG, &tmp, &tsp, &T1, &T2, &asp);
+  plan_prec(a, n_out, n_in, math, &ZX, &ZG, &tmp, &zt, &tsp, &T1, &T2, &cv, &asp);
   RC(check_ws(a, "precondition"));
-  RC(trinv_core(s, RX, rdt, ldrx, n_in, ZX, n_in, math, 0, tmp, tsp));
-  RC(trinv_core(s, RG, rdt, ldrg, n_out, ZG, n_out, math, 0, tmp, tsp));
-  return apply_core(s, grad, n_out, n_in, ldg, ZX, n_in, ZG, n_out, nat, ldn, math, T1, T2, asp);
+  if (math == MATH_BF16) {
+    RC(trinv_core_t(s, RX, rdt, ldrx, n_in, ZX, n_in, 0, zt, (bf16_t*)tmp, tsp));
+    RC(trinv_core_t(s, RG, rdt, ldrg, n_out, ZG, n_out, 0, zt, (bf16_t*)tmp, tsp));
+  } else {
+    RC(trinv_core(s, RX, rdt, ldrx, n_in, ZX, n_in, math, 0, tmp, tsp));
+    RC(trinv_core(s, RG, rdt, ldrg, n_out, ZG, n_out, math, 0, tmp, tsp));
+  }
+  return apply_core(s, grad, n_out, n_in, ldg, ZX, n_in, ZG, n_out, nat, ldn, math, T1, T2, cv,
+                    asp);
 }
 
 size_t precondition_bias_ws(int64_t n_out) {
@@ -482,8 +704,8 @@ int geqrf_r(hipStream_t s, const void* A, int adt, int64_t m, int64_t n, int64_t
   plan_fold(a, m, n, true, w);
   RC(check_ws(a, "geqrf_r"));
   RC(launch_zero(s, Rw, n, n, n));
-  RC(launch_copy_to_f32(s, A, adt, lda, m, n, 1.0f, w.C, n));
-  RC(fold_core(s, w.C, n, m, n, Rw, n, n, false, math, w));
+  RC(launch_transpose_to_f32(s, A, adt, lda, m, n, w.C, m));
+  RC(fold_core(s, w.C, m, m, n, Rw, n, n, false, math, w));
   return launch_cast_upper(s, Rw, n, n, R, rdt, ldr, nullptr);
 }
 

@@ -426,11 +426,12 @@ __global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const 
 
 // Robust TPQRT panel by Householder reflections (LAPACK dlarfg convention),
 // run only when *flag is set: the reflectors' X parts go to Q2 (p_e x 64,
-// columns >= b zero) and R's diagonal block is replaced by R_new.  One
+// columns >= b zero) and R's diagonal block is replaced by R_new.  The panel
+// X_p is read from the transposed working matrix (XpT: b x p_e, ld ldx).  One
 // workgroup walks the b columns; norms and dot products over the p_e rows
 // are wave-shuffle reductions.
 __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(float* Ptop, int64_t ldr,
-                                                                 const float* Xp, int64_t ldx,
+                                                                 const float* XpT, int64_t ldx,
                                                                  int64_t pe, int b, float* Y,
                                                                  const int* flag) {
   if (*flag == 0) return;
@@ -448,7 +449,7 @@ __global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(float* Ptop, int
   for (int64_t e = t; e < pe * SB; e += SNT) {
     const int64_t r = e / SB;
     const int c = (int)(e % SB);
-    Y[r * ldy + c] = (c < b) ? Xp[r * ldx + c] : 0.0f;
+    Y[r * ldy + c] = (c < b) ? XpT[(int64_t)c * ldx + r] : 0.0f;
   }
   __syncthreads();
   for (int j = 0; j < b; ++j) {
@@ -643,11 +644,11 @@ int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, const flo
   return check_launch("panel_hr_b");
 }
 
-int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* Xp, int64_t ldx,
-                             int64_t pe, int b, float* Q2, const int* flag) {
+int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* XpT,
+                             int64_t ldx, int64_t pe, int b, float* Q2, const int* flag) {
   if (int rc = check_b(b, "panel_hh_fallback")) return rc;
-  hipLaunchKernelGGL(panel_hh_fallback_kernel, dim3(1), dim3(SNT), 0, s, Ptop, ldr, Xp, ldx, pe, b,
-                     Q2, flag);
+  hipLaunchKernelGGL(panel_hh_fallback_kernel, dim3(1), dim3(SNT), 0, s, Ptop, ldr, XpT, ldx, pe,
+                     b, Q2, flag);
   return check_launch("panel_hh_fallback");
 }
 

@@ -28,7 +28,7 @@ import numpy as np
 import torch
 import torch.nn as nn
 
-from ._backend import MATH_BF16, MATH_F32, get_backend
+from ._backend import MATH_BF16, MATH_F32, get_backend, run_pair
 from .activation_hooks import IFKFACRankError, RawActivationHooks
 from .triangular import solve_math_for
 
@@ -153,7 +153,9 @@ class IFKFAC(torch.optim.Optimizer):
         self._inverses = {}
         for module, (R_X, R_G) in clean.items():
             m = solve_math_for(R_X.dtype)
-            self._inverses[module] = (be.tri_inverse(R_X, m), be.tri_inverse(R_G, m))
+            self._inverses[module] = run_pair(R_X.device,
+                                              lambda R=R_X: be.tri_inverse(R, m),
+                                              lambda R=R_G: be.tri_inverse(R, m))
         self.timing["factor_compute"].append(time.perf_counter() - t0)
 
     # ------------------------------------------------------------------ apply

@@ -95,6 +95,8 @@ def _fold_chunks(hip, chunks, n, math_=0):
     ([64, 64], 40), ([30, 30, 100], 50), ([5, 7, 3], 20),  # trapezoid growth
     ([300], 200), ([2000], 256), ([1, 1, 1], 2), ([1], 1),
     ([512] * 3, 1024), ([100, 1000], 333),
+    # several outer blocks, so the far columns run on the helper stream
+    ([3000], 1600), ([700, 2500], 1600), ([400, 300], 1700), ([1200, 1200], 2100),
 ])
 def test_fold_matches_oracle_fp32(hip, chunks, n):
     g = torch.Generator(device=DEV).manual_seed(sum(chunks) + n)
@@ -189,7 +191,8 @@ def test_fold_bf16_math_regression_bound(hip):
 # --------------------------------------------------------------------------- finalize
 
 
-@pytest.mark.parametrize("p,n,lam", [(500, 300, 1e-2), (4096, 1024, 1e-2), (64, 64, 1e-3)])
+@pytest.mark.parametrize("p,n,lam", [(500, 300, 1e-2), (4096, 1024, 1e-2), (64, 64, 1e-3),
+                                      (3000, 1700, 1e-2)])
 def test_finalize_matches_closed_form(hip, p, n, lam):
     g = torch.Generator(device=DEV).manual_seed(p + n)
     X = torch.randn(p, n, device=DEV, generator=g)
@@ -273,6 +276,19 @@ def test_tri_inverse(hip, n):
     Z = hip.tri_inverse(torch.tensor(R, dtype=torch.float32, device=DEV), 0)
     want = np.linalg.inv(R)
     assert _rel(Z, want) <= 1e-5
+    assert np.all(np.tril(Z.cpu().numpy(), -1) == 0)
+
+
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 300, 1000, 2049])
+def test_tri_inverse_bf16(hip, n):
+    """bf16 factor and bf16 arithmetic (the transposed-copy doubling): Z against
+    the fp64 inverse of the same bf16 matrix, at bf16 accuracy."""
+    rng = np.random.default_rng(n + 7)
+    R = np.triu(rng.standard_normal((n, n))) / math.sqrt(n) + 2 * np.eye(n)
+    Rb = torch.tensor(R, dtype=torch.float32, device=DEV).to(torch.bfloat16)
+    Z = hip.tri_inverse(Rb, 1)
+    want = np.linalg.inv(Rb.double().cpu().numpy())
+    assert _rel(Z, want) <= 2e-2
     assert np.all(np.tril(Z.cpu().numpy(), -1) == 0)
 
 
