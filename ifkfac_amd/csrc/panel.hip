@@ -40,35 +40,59 @@ constexpr int LG = GSLAB + 1; // column stride of a slab tile in LDS (floats)
 constexpr int LT = PT + 1;    // column stride of a 64-row tile in LDS
 constexpr int TLD = PT + 4;   // row stride of a row-major 64 x 64 LDS tile
 
-// Rows [r0, r0 + nr) of a p x 64 operand view into LDS as S[c * ldS + r];
+// Rows [r0, r0 + NR) of a p x 64 operand view into LDS as S[c * ldS + r];
 // columns >= w and rows >= rmax read as zero.  TS: the operand is stored
 // transposed (element (r, c) at g[c * ld + r], the working matrix); else
-// row-major (g[r * ld + c]).
-template <bool TS>
+// row-major (g[r * ld + c]).  All loads of a thread are issued before the
+// first LDS write (one memory latency per tile, not one per element).
+template <bool TS, int NR>
 __device__ __forceinline__ void load_cm(float* S, int ldS, const float* g, int64_t ld, int64_t r0,
-                                        int nr, int64_t rmax, int w) {
-  for (int e = threadIdx.x; e < nr * PT; e += PNT) {
+                                        int64_t rmax, int w) {
+  constexpr int PER = NR * PT / PNT;
+  float v[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + PNT * q;
     int r, c;
     if constexpr (TS) {
-      c = e / nr;
-      r = e - c * nr;
+      c = e / NR;
+      r = e - c * NR;
     } else {
       r = e >> 6;
       c = e & 63;
     }
     const int64_t gr = r0 + r;
-    float v = 0.0f;
-    if (gr < rmax && c < w) v = TS ? g[(int64_t)c * ld + gr] : g[gr * ld + c];
-    S[c * ldS + r] = v;
+    v[q] = (gr < rmax && c < w) ? (TS ? g[(int64_t)c * ld + gr] : g[gr * ld + c]) : 0.0f;
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + PNT * q;
+    int r, c;
+    if constexpr (TS) {
+      c = e / NR;
+      r = e - c * NR;
+    } else {
+      r = e >> 6;
+      c = e & 63;
+    }
+    S[c * ldS + r] = v[q];
   }
 }
 
 // Row-major 64 x 64 tile (M b x b in ld, or a 64-column block) into LDS with
 // row stride TLD; rows >= rows_ok and columns >= w read as zero.
 __device__ __forceinline__ void load_rm(float* S, const float* g, int64_t ld, int rows_ok, int w) {
-  for (int e = threadIdx.x; e < PT * PT; e += PNT) {
-    const int r = e >> 6, c = e & 63;
-    S[r * TLD + c] = (r < rows_ok && c < w) ? g[(int64_t)r * ld + c] : 0.0f;
+  constexpr int PER = PT * PT / PNT;
+  float v[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + PNT * q, r = e >> 6, c = e & 63;
+    v[q] = (r < rows_ok && c < w) ? g[(int64_t)r * ld + c] : 0.0f;
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + PNT * q;
+    S[(e >> 6) * TLD + (e & 63)] = v[q];
   }
 }
 
@@ -103,12 +127,12 @@ __global__ __launch_bounds__(PNT) void gram_partial_kernel(const float* A, int64
   __shared__ float sB[PT * LG];
   const int s = blockIdx.x, cb = blockIdx.y;
   const int64_t r0 = (int64_t)s * GSLAB;
-  load_cm<A_TS>(sA, LG, A, lda, r0, GSLAB, pe, ka);
+  load_cm<A_TS, GSLAB>(sA, LG, A, lda, r0, pe, ka);
   if (B0 != nullptr && cb == 0) {
-    load_cm<false>(sB, LG, B0, ldb0, r0, GSLAB, pe, w0);
+    load_cm<false, GSLAB>(sB, LG, B0, ldb0, r0, pe, w0);
   } else {
     const int blk = cb - (B0 != nullptr ? 1 : 0);
-    load_cm<true>(sB, LG, B1 + (int64_t)blk * PT * ldb1, ldb1, r0, GSLAB, pe, w1 - blk * PT);
+    load_cm<true, GSLAB>(sB, LG, B1 + (int64_t)blk * PT * ldb1, ldb1, r0, pe, w1 - blk * PT);
   }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -158,7 +182,7 @@ __global__ __launch_bounds__(PNT) void apply_m_kernel(const float* XT, int64_t l
   __shared__ float sX[PT * LT];
   __shared__ float sM[PT * TLD];
   const int64_t r0 = (int64_t)blockIdx.x * PT;
-  load_cm<true>(sX, LT, XT, ldx, r0, PT, pe, b);
+  load_cm<true, PT>(sX, LT, XT, ldx, r0, pe, b);
   load_rm(sM, M, b, b, b);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -198,7 +222,7 @@ __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int6
   const int l32 = lane & 31, h = lane >> 5;
   const int mq = (wave >> 1) * 32 + l32, nq = (wave & 1) * 32 + l32;
   const int jc = acc_col();
-  load_cm<false>(sQ, LT, Q2, PT, r0, PT, pe, PT);
+  load_cm<false, PT>(sQ, LT, Q2, PT, r0, pe, PT);
   const int nblk = (nr + PT - 1) / PT;
   for (int cb = 0; cb <= nblk; ++cb) {
     int w;

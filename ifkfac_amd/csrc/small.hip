@@ -44,13 +44,22 @@ __device__ inline float bcast(float v, int lane) {
 // Load a b x b block (row stride ld) into a padded 64 x 64 LDS matrix.  With
 // upper set, the strict lower part is zeroed.  The pad beyond b is pad * I.
 __device__ __forceinline__ void sm_load_pad(float* S, const float* g, int64_t ld, int b, bool upper,
-                            float pad = 1.0f) {
-  for (int e = threadIdx.x; e < SB * SB; e += SNT) {
+                                            float pad = 1.0f) {
+  // every load of the thread is issued before the first LDS write, so the
+  // 16 loads share one memory latency
+  constexpr int PER = SB * SB / SNT;
+  float v[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + SNT * q;
     const int r = e >> 6, c = e & 63;
-    float v;
-    if (r < b && c < b) v = (upper && r > c) ? 0.0f : g[(int64_t)r * ld + c];
-    else v = (r == c) ? pad : 0.0f;
-    S[r * SLD + c] = v;
+    if (r < b && c < b) v[q] = (upper && r > c) ? 0.0f : g[(int64_t)r * ld + c];
+    else v[q] = (r == c) ? pad : 0.0f;
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + SNT * q;
+    S[(e >> 6) * SLD + (e & 63)] = v[q];
   }
   __syncthreads();
 }
@@ -539,9 +548,18 @@ __global__ __launch_bounds__(SNT) void panel_wcomp_kernel(const float* G, int b,
   sm_load_pad(sB, NT, b, b, false, 0.0f);
   sm_gemm64<true, false>(sB, sA, sW, 1.0f, false);      // W = NT^T (Q2^T C)
   sm_load_pad(sB, T, b, b, true, 0.0f);
-  for (int e = t; e < SB * SB; e += SNT) {
-    const int i = e >> 6, j = e & 63;
-    sR[i * SLD + j] = (i < b && j < w) ? Rrest[(int64_t)i * ldr + c0 + j] : 0.0f;
+  {
+    float v[SB * SB / SNT];
+#pragma unroll
+    for (int q = 0; q < SB * SB / SNT; ++q) {
+      const int e = t + SNT * q, i = e >> 6, j = e & 63;
+      v[q] = (i < b && j < w) ? Rrest[(int64_t)i * ldr + c0 + j] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < SB * SB / SNT; ++q) {
+      const int e = t + SNT * q;
+      sR[(e >> 6) * SLD + (e & 63)] = v[q];
+    }
   }
   __syncthreads();
   sm_gemm64<true, false>(sB, sR, sW, 1.0f, true);       // W += T^T R_rest
@@ -599,15 +617,23 @@ __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t 
   __shared__ float sT[32 * 32];
   const int64_t k0 = (int64_t)blockIdx.x * nb;
   const int b = (int)((n - k0) < nb ? (n - k0) : nb);
-  for (int e = threadIdx.x; e < SB * SB; e += SNT) {
-    const int r = e >> 6, c = e & 63;
-    float v;
-    if (r < b && c < b)
-      v = (r <= c) ? Elem<DT>::load((const typename Elem<DT>::T*)R + (k0 + r) * ldr + k0 + c)
+  {
+    float v[SB * SB / SNT];
+#pragma unroll
+    for (int q = 0; q < SB * SB / SNT; ++q) {
+      const int e = threadIdx.x + SNT * q, r = e >> 6, c = e & 63;
+      if (r < b && c < b)
+        v[q] = (r <= c)
+                   ? Elem<DT>::load((const typename Elem<DT>::T*)R + (k0 + r) * ldr + k0 + c)
                    : 0.0f;
-    else
-      v = (r == c) ? 1.0f : 0.0f;
-    sU[r * SLD + c] = v;
+      else
+        v[q] = (r == c) ? 1.0f : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < SB * SB / SNT; ++q) {
+      const int e = threadIdx.x + SNT * q;
+      sU[(e >> 6) * SLD + (e & 63)] = v[q];
+    }
   }
   __syncthreads();
   sm_trinv64(sU, sZ, sT, safe != 0);
