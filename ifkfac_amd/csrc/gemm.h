@@ -64,7 +64,9 @@ struct SplitScratch {
   size_t floats;
 };
 
-// Launch profiler (see gemm.hip).  variant: gemm_variant_id(), -2 all, -1 off.
+// Launch profiler (see gemm.hip).  variant: gemm_variant_id() (bit 5 set for
+// the 256 x 128 kernel), -2 all, -3 all of the 256 x 128 kernel, -4 all of the
+// 128 x 128 kernel, -1 off.
 int gemm_variant_id(int math, int adt, bool akc, int bdt, bool bkc);
 int profile_begin(int variant);
 int profile_end(int64_t* n_launches);

@@ -79,9 +79,14 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
   return IFK_OK;
 }
 
+// Armed variant: >= 0 one variant id, -2 every launch, -3 every launch of the
+// 256 x 128 kernel (variant bit 5), -4 every launch of the 128 x 128 kernel.
 static ProfRec* prof_slot(int vid) {
-  if (g_prof_variant == -1) return nullptr;
-  if (g_prof_variant != -2 && g_prof_variant != vid) return nullptr;
+  const int a = g_prof_variant;
+  if (a == -1) return nullptr;
+  const bool big = (vid >> 5) & 1;
+  if (a >= 0 && a != vid) return nullptr;
+  if ((a == -3 && !big) || (a == -4 && big)) return nullptr;
   std::lock_guard<std::mutex> g(g_prof_mu);
   if (g_prof_used == g_prof.size()) {
     ProfRec r{};
@@ -514,7 +519,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     gx = (unsigned)std::min<int64_t>(gx, per_z);
   }
   dim3 grid(gx, 1, (unsigned)(batch * splits));
-  const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc);
+  const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | ((big ? 1 : 0) << 5);
   ProfRec* pr = prof_slot(vid);
   if (pr) {
     // algorithmic work: 2 M N K (M N K when one operand is triangular), and the

@@ -182,9 +182,12 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
 /*
  * Measurement support (no counterpart in the reference; used by bench.py).
  * ifk_profile_begin(v) arms the GEMM launch profiler for GEMM variant v
- * (v = (math << 4) | (a_dtype << 3) | (a_k_contiguous << 2) | (b_dtype << 1) |
- * b_k_contiguous), or for every variant with v = -2; v = -1 disarms.  Each
- * armed launch is bracketed by two HIP events on its own stream.
+ * (v = (large_tile << 5) | (math << 4) | (a_dtype << 3) | (a_k_contiguous << 2)
+ * | (b_dtype << 1) | b_k_contiguous; large_tile marks the 256 x 128 kernel
+ * gemm_big_kernel, else gemm_kernel), for every variant with v = -2, for every
+ * launch of gemm_big_kernel with v = -3 or of gemm_kernel with v = -4;
+ * v = -1 disarms.  Each armed launch is bracketed by two HIP events on its
+ * own stream.
  * ifk_profile_end() disarms, waits for the events and returns the number of
  * launches recorded; ifk_profile_get(i, ...) returns launch i's variant,
  * duration (ms), algorithmic flops and bytes, and its m, n, k.
