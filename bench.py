@@ -5,11 +5,16 @@ One step = one factor update plus one preconditioned weight update for a
 single Linear layer, exactly the work IFKFAC.step does for that layer with
 factor_update_freq=1 in bf16 mode:
 
-  fold X (p x n_in) and delta (p x n_out) into fresh R factors   (hooks)
-  finalize both: scale 1/sqrt(p), damping, positive diagonal, bf16 (get_factors)
+  fold X (p x n_in) and delta (p x n_out) into fresh R factors and finalize
+  them (scale 1/sqrt(p), damping, positive diagonal, bf16): the hooks hold
+  the chunk of an update step back and the factor update runs fold and
+  finalize as one factorisation per side, the two sides concurrently
   triangular inverses of both bf16 factors                       (solve setup)
   nat = (R_G^T R_G)^-1 grad (R_X^T R_X)^-1                       (four solves)
   heavy-ball momentum + weight step                              (update)
+
+--unfused times the two-call path instead (fold into the running factor,
+then finalize), which is what get_factors() outside a factor update does.
 
 Default workload: Linear 4096 -> 11008 at p = 16384 rows, inputs resident in
 HBM.  value = algorithmic TFLOP/s of the step, with the algorithmic count
@@ -105,6 +110,9 @@ def main() -> int:
     ap.add_argument("--workload", default="linear_4096x11008_p16384", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", default="linear_4096x4096_p8192", choices=sorted(WORKLOADS))
+    ap.add_argument("--unfused", action="store_true",
+                    help="fold, then finalize (two factorisations per side) instead of the "
+                         "fused fold + finalize of IFKFAC's factor update")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the warmup, copy a device buffer of this many MiB three "
                          "times (a kernel of known HBM traffic for counter calibration)")
@@ -139,32 +147,51 @@ def main() -> int:
     grad = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.1
     W = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.01
     buf = torch.zeros_like(W)
-    R_X = torch.zeros(n_in, n_in, device="cuda")
-    R_G = torch.zeros(n_out, n_out, device="cuda")
+    dev = torch.device("cuda", 0)
+    if args.unfused:
+        R_X = torch.zeros(n_in, n_in, device=dev)
+        R_G = torch.zeros(n_out, n_out, device=dev)
     scale = 1.0 / math.sqrt(p)
-    phase_names = ["fold_X", "fold_G", "finalize", "tri_inverse", "precondition", "update"]
+    if args.unfused:
+        phase_names = ["fold_X", "fold_G", "finalize", "tri_inverse", "precondition", "update"]
+    else:
+        phase_names = ["fold_finalize", "tri_inverse", "precondition", "update"]
+    nph = len(phase_names)
+
+    def factors(mark):
+        if args.unfused:
+            be.fold_(R_X, 0, X, MATH_BF16)
+            mark()
+            be.fold_(R_G, 0, D, MATH_BF16)
+            mark()
+            # input and output sides are independent, as in IFKFAC._update_factors
+            return run_pair(dev,
+                            lambda: be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16),
+                            lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16))
+        # RawActivationHooks._collect_factors(consume=True) of the update step
+        return run_pair(dev,
+                        lambda: be.fold_finalize(None, 0, X, scale, lam, torch.bfloat16,
+                                                 MATH_BF16),
+                        lambda: be.fold_finalize(None, 0, D, scale, lam, torch.bfloat16,
+                                                 MATH_BF16))
 
     def step(first: bool, events=None):
-        def mark(i):
+        k = [0]
+
+        def mark():
             if events is not None:
-                events[i].record()
-        mark(0)
-        be.fold_(R_X, 0, X, MATH_BF16)
-        mark(1)
-        be.fold_(R_G, 0, D, MATH_BF16)
-        mark(2)
-        # input and output sides are independent, as in IFKFAC._update_factors
-        (FX, _), (FG, _) = run_pair(R_X.device,
-                                    lambda: be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16),
-                                    lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16))
-        mark(3)
-        ZX, ZG = run_pair(R_X.device, lambda: be.tri_inverse(FX, MATH_BF16),
+                events[k[0]].record()
+            k[0] += 1
+        mark()
+        (FX, _), (FG, _) = factors(mark)
+        mark()
+        ZX, ZG = run_pair(dev, lambda: be.tri_inverse(FX, MATH_BF16),
                           lambda: be.tri_inverse(FG, MATH_BF16))
-        mark(4)
+        mark()
         nat = be.precondition_apply(grad, ZX, ZG, MATH_BF16)
-        mark(5)
+        mark()
         be.momentum_update_(nat, buf, W, lr, mom, 0.0, first)
-        mark(6)
+        mark()
 
     for i in range(args.warmup):
         step(i == 0)
@@ -172,13 +199,13 @@ def main() -> int:
 
     # one untimed step with every GEMM launch bracketed by events: find the
     # dominant GEMM variant and the per-phase split
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(7)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(nph + 1)]
     _lib.check(lib.ifk_profile_begin(-2), "profile_begin")
     step(False, ev)
     n = _lib.ctypes.c_int64(0)
     _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
     torch.cuda.synchronize()
-    phases = {phase_names[i]: round(ev[i].elapsed_time(ev[i + 1]), 3) for i in range(6)}
+    phases = {phase_names[i]: round(ev[i].elapsed_time(ev[i + 1]), 3) for i in range(nph)}
 
     def read_profile(count):
         recs = []
@@ -269,6 +296,7 @@ def main() -> int:
         "config": {
             "workload": f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, "
                         f"p={p} rows, bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9",
+            "factor_path": "fold then finalize" if args.unfused else "fused fold + finalize",
             "n_in": n_in, "n_out": n_out, "p": p, "algorithmic_gflop_per_step": round(flops / 1e9, 1),
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
         },

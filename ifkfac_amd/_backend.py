@@ -108,6 +108,37 @@ class HipBackend:
         _lib.check(rc, "ifk_finalize")
         return out, flag
 
+    def fold_finalize(self, R: Optional[torch.Tensor], r_in: int, X: torch.Tensor, scale: float,
+                      damping: float, out_dtype: torch.dtype,
+                      math: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """finalize(fold(R[:r_in], X)) in one factorisation, leaving R untouched.
+
+        Returns (R_damped, finite flag int32[1]); R (n x n fp32 buffer whose
+        first r_in rows are the running factor) may be None when r_in == 0.
+        """
+        X, ldx, xdt = _mat(X, "fold_finalize")
+        p, n = X.shape
+        ldr = n
+        if r_in > 0:
+            if R is None or R.dtype != torch.float32 or R.shape[1] != n or R.shape[0] < r_in:
+                raise IFKFACBackendError("fold_finalize: R must be an fp32 buffer with n columns "
+                                         "and at least r_in rows")
+            _require_device(R, "fold_finalize")
+            if R.stride(1) != 1:
+                R = R.contiguous()
+            ldr = R.stride(0) if R.shape[0] > 1 else n
+        out = torch.empty((n, n), dtype=out_dtype, device=X.device)
+        flag = torch.empty(1, dtype=torch.int32, device=X.device)
+        ws = self._ws(self.lib.ifk_fold_finalize_workspace_size(p, n, int(r_in)), X.device)
+        with torch.cuda.device(X.device):
+            rc = self.lib.ifk_fold_finalize(self._stream(X.device), _ptr(X), xdt, p, n, ldx,
+                                            _ptr(R) if r_in > 0 else None, ldr, int(r_in),
+                                            float(scale), float(damping), _ptr(out),
+                                            _DT[out_dtype], n, int(math), _ptr(flag), _ptr(ws),
+                                            ws.numel())
+        _lib.check(rc, "ifk_fold_finalize")
+        return out, flag
+
     # -- preconditioning ------------------------------------------------------------
     def tri_inverse(self, R: torch.Tensor, math: int) -> torch.Tensor:
         R, ldr, rdt = _mat(R, "tri_inverse")

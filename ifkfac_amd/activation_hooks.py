@@ -90,6 +90,14 @@ class RawActivationHooks(GramMatrixEstimator):
         # persistent fold buffers (n x n fp32), reused across windows
         self._buf_X: Dict[nn.Module, torch.Tensor] = {}
         self._buf_G: Dict[nn.Module, torch.Tensor] = {}
+        # Last chunk of each side held back from the fold.  An owner that
+        # collects the factors and clears the hooks right after (IFKFAC's
+        # factor update) sets _defer_last; the held chunk then goes straight
+        # into a fused fold + finalize, one dependent factorisation instead of
+        # two.  Any other reader of the running factor folds it first.
+        self._defer_last = False
+        self._held_X: Dict[nn.Module, Optional[torch.Tensor]] = {}
+        self._held_G: Dict[nn.Module, Optional[torch.Tensor]] = {}
         self._linear_layers: List[nn.Module] = []
 
         for module in model.modules():
@@ -109,6 +117,8 @@ class RawActivationHooks(GramMatrixEstimator):
             self._pending_G[module] = []
             self._raw_X[module] = []
             self._raw_G[module] = []
+            self._held_X[module] = None
+            self._held_G[module] = None
 
     # ------------------------------------------------------------------ lifecycle
     @property
@@ -137,6 +147,8 @@ class RawActivationHooks(GramMatrixEstimator):
             self._pending_G[module] = []
             self._raw_X[module] = []
             self._raw_G[module] = []
+            self._held_X[module] = None
+            self._held_G[module] = None
 
     def remove(self):
         for h in self._handles:
@@ -180,30 +192,88 @@ class RawActivationHooks(GramMatrixEstimator):
         return get_backend().finalize(R_raw, 1.0 / math.sqrt(rows), self.damping, out_dtype,
                                       self.math)
 
+    def _take(self, side: str, module: nn.Module, chunk: torch.Tensor) -> None:
+        """Fold ``chunk``, or hold it back when the next reader is a fused finalize."""
+        held = self._held_X if side == "X" else self._held_G
+        prev = held.get(module)
+        if prev is not None:             # chunks fold in arrival order
+            self._fold(side, module, prev)
+            held[module] = None
+        if not self._defer_last:
+            self._fold(side, module, chunk)
+            return
+        # a copy: the caller may overwrite its activation or gradient in place
+        held[module] = chunk.detach().clone(memory_format=torch.contiguous_format)
+
+    def _fold_held(self) -> None:
+        """Fold every held chunk into its running factor."""
+        for side, held in (("X", self._held_X), ("G", self._held_G)):
+            for module, chunk in held.items():
+                if chunk is not None:
+                    self._fold(side, module, chunk)
+                    held[module] = None
+
+    def _running_factor(self, module: nn.Module, side: str) -> Optional[torch.Tensor]:
+        """The undamped running factor of one side, held chunk folded in."""
+        held = self._held_X if side == "X" else self._held_G
+        chunk = held.get(module)
+        if chunk is not None:
+            self._fold(side, module, chunk)
+            held[module] = None
+        return (self._R_X if side == "X" else self._R_G).get(module)
+
+    def _side_state(self, side: str, module: nn.Module):
+        """(R_raw or None, rows folded in R_raw, held chunk or None, final row count)."""
+        R = (self._R_X if side == "X" else self._R_G).get(module)
+        chunk = (self._held_X if side == "X" else self._held_G).get(module)
+        r = 0 if R is None else R.shape[0]
+        if chunk is None:
+            return R, r, None, (None if R is None else R.shape[0])
+        n = chunk.shape[1]
+        return R, r, chunk, min(r + chunk.shape[0], n)
+
+    def _damped(self, side: str, module: nn.Module, rows: int, out_dtype: torch.dtype):
+        R, r, chunk, _ = self._side_state(side, module)
+        if chunk is None:
+            return self._finalize(R, rows, out_dtype)
+        bufs = self._buf_X if side == "X" else self._buf_G
+        return get_backend().fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
+                                           1.0 / math.sqrt(rows), self.damping, out_dtype,
+                                           self.math)
+
     # ------------------------------------------------------------------ factors
     def get_factors(self) -> Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]]:
         """Damped factors (R_X, R_G) of every layer with enough data (fp32)."""
         factors, _ = self._collect_factors(torch.float32)
         return factors
 
-    def _collect_factors(self, out_dtype: torch.dtype):
-        """get_factors with the output dtype chosen and the finite flags returned."""
+    def _collect_factors(self, out_dtype: torch.dtype, consume: bool = False):
+        """get_factors with the output dtype chosen and the finite flags returned.
+
+        With ``consume`` the caller clears the hooks right after, so a held
+        chunk goes into a fused fold + finalize and the running factor is
+        left as it was (it is about to be dropped); otherwise held chunks are
+        folded first, exactly as get_factors leaves them."""
         if self.deferred:
             self._drain_deferred()
+        if not consume:
+            self._fold_held()
         factors: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         flags: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         for module in self._linear_layers:
-            R_X_raw = self._R_X.get(module)
-            R_G_raw = self._R_G.get(module)
-            if R_X_raw is None or R_G_raw is None:
+            R_X_raw, _, chunk_X, r_X = self._side_state("X", module)
+            R_G_raw, _, chunk_G, r_G = self._side_state("G", module)
+            if r_X is None or r_G is None:
                 continue
             rows_X = self._n_rows_X[module]
             rows_G = self._n_rows_G[module]
-            if R_X_raw.shape[0] != R_X_raw.shape[1]:
+            n_X = (R_X_raw if R_X_raw is not None else chunk_X).shape[1]
+            n_G = (R_G_raw if R_G_raw is not None else chunk_G).shape[1]
+            if r_X != n_X:
                 logger.debug("get_factors() [%s]: skipped — X factor partial-rank",
                              _module_tag(module))
                 continue
-            if R_G_raw.shape[0] != R_G_raw.shape[1]:
+            if r_G != n_G:
                 logger.debug("get_factors() [%s]: skipped — G factor partial-rank",
                              _module_tag(module))
                 continue
@@ -217,10 +287,11 @@ class RawActivationHooks(GramMatrixEstimator):
                         f"Layer {module}: accumulated {rows_G} rows for δ, "
                         f"but need >= n_out={R_G_raw.shape[1]} (batched mode).")
             # the two sides are independent: finalize them concurrently
+            dev = (R_X_raw if R_X_raw is not None else chunk_X).device
             (R_X, fX), (R_G, fG) = run_pair(
-                R_X_raw.device,
-                lambda: self._finalize(R_X_raw, rows_X, out_dtype),
-                lambda: self._finalize(R_G_raw, rows_G, out_dtype))
+                dev,
+                lambda: self._damped("X", module, rows_X, out_dtype),
+                lambda: self._damped("G", module, rows_G, out_dtype))
             factors[module] = (R_X, R_G)
             flags[module] = (fX, fG)
         return factors, flags
@@ -302,7 +373,7 @@ class RawActivationHooks(GramMatrixEstimator):
             self._pending_X[module].append(x)
             self._n_rows_X[module] += x.shape[0]
             return
-        self._fold("X", module, x)
+        self._take("X", module, x)
         self._n_rows_X[module] += x.shape[0]
 
     def _backward_hook(self, module: nn.Module, grad_input: Tuple[torch.Tensor, ...],
@@ -332,5 +403,5 @@ class RawActivationHooks(GramMatrixEstimator):
             self._pending_G[module].append(delta)
             self._n_rows_G[module] += delta.shape[0]
             return
-        self._fold("G", module, delta)
+        self._take("G", module, delta)
         self._n_rows_G[module] += delta.shape[0]

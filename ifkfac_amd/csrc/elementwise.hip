@@ -176,13 +176,13 @@ int launch_sign_normalize(hipStream_t s, float* R, int64_t ldr, int64_t r, int64
 
 template <int ODT>
 __global__ void cast_upper_kernel(const float* R, int64_t ldr, int64_t n, void* out, int64_t ldo,
-                                  int* finite) {
+                                  int* finite, float scale) {
   const int64_t total = n * n;
   bool ok = true;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = e / n, c = e % n;
-    const float v = (c >= r) ? R[r * ldr + c] : 0.0f;
+    const float v = (c >= r) ? scale * R[r * ldr + c] : 0.0f;
     ok = ok && isfinite(v);
     if constexpr (ODT == DT_F32) ((float*)out)[r * ldo + c] = v;
     else ((bf16_t*)out)[r * ldo + c] = f32_to_bf16(v);
@@ -191,14 +191,14 @@ __global__ void cast_upper_kernel(const float* R, int64_t ldr, int64_t n, void* 
 }
 
 int launch_cast_upper(hipStream_t s, const float* R, int64_t ldr, int64_t n, void* out, int odt,
-                      int64_t ldo, int* finite) {
+                      int64_t ldo, int* finite, float scale) {
   if (n == 0) return IFK_OK;
   if (odt == DT_F32)
     hipLaunchKernelGGL(cast_upper_kernel<DT_F32>, dim3(grid_for(n * n)), dim3(256), 0, s, R, ldr, n,
-                       out, ldo, finite);
+                       out, ldo, finite, scale);
   else
     hipLaunchKernelGGL(cast_upper_kernel<DT_BF16>, dim3(grid_for(n * n)), dim3(256), 0, s, R, ldr,
-                       n, out, ldo, finite);
+                       n, out, ldo, finite, scale);
   return check_launch("cast_upper");
 }
 
@@ -328,13 +328,13 @@ int launch_scale_copy_vec(hipStream_t s, const float* x, int64_t n, float alpha,
 // src and the write of dst are both coalesced.
 template <int DT>
 __global__ void transpose_to_f32_kernel(const void* src, int64_t lds, int64_t rows, int64_t cols,
-                                        float* dst, int64_t ldd) {
+                                        float* dst, int64_t ldd, int upper) {
   __shared__ float tile[32][33];
   const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
   for (int k = ty; k < 32; k += 8) {
     const int64_t r = r0 + k, c = c0 + tx;
-    tile[k][tx] = (r < rows && c < cols)
+    tile[k][tx] = (r < rows && c < cols && !(upper && r > c))
                       ? Elem<DT>::load((const typename Elem<DT>::T*)src + r * lds + c)
                       : 0.0f;
   }
@@ -346,7 +346,7 @@ __global__ void transpose_to_f32_kernel(const void* src, int64_t lds, int64_t ro
 }
 
 int launch_transpose_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
-                            int64_t cols, float* dst, int64_t ldd) {
+                            int64_t cols, float* dst, int64_t ldd, bool upper) {
   if (rows * cols == 0) return IFK_OK;
   if (cdiv(rows, 32) > 65535) {
     set_error("transpose_to_f32: too many rows");
@@ -355,10 +355,10 @@ int launch_transpose_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds
   const dim3 grid((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32));
   if (sdt == DT_F32)
     hipLaunchKernelGGL(transpose_to_f32_kernel<DT_F32>, grid, dim3(256), 0, s, src, lds, rows, cols,
-                       dst, ldd);
+                       dst, ldd, upper ? 1 : 0);
   else
     hipLaunchKernelGGL(transpose_to_f32_kernel<DT_BF16>, grid, dim3(256), 0, s, src, lds, rows,
-                       cols, dst, ldd);
+                       cols, dst, ldd, upper ? 1 : 0);
   return check_launch("transpose_to_f32");
 }
 

@@ -21,23 +21,19 @@ int launch_gram(hipStream_t s, const float* A, int64_t lda, int ka, bool a_ts, c
 // Q1 = P_top M1; *flag = 1 when a pivot falls below tol * its diagonal.
 int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t ldr, int b,
                       float tol, float* U1, float* M1, float* Q1, int* flag);
-// Householder TPQRT of [P_top; X_p] when *flag is set (X_p given transposed,
-// XpT b x pe): reflectors into Q2 (ld 64, columns >= b zero), P_top <- R_new.
-int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* XpT,
-                             int64_t ldx, int64_t pe, int b, float* Q2, const int* flag);
-// Q2 = X_p M1 (X_p given transposed, XT b x pe) unless *flag is set
+// Q2 = X_p M1 (X_p given transposed, XT b x pe); when *flag is set, the
+// Householder TPQRT of [P_top; X_p] instead: reflectors into Q2 (ld 64,
+// columns >= b zero), P_top <- R_new.
 int launch_apply_m(hipStream_t s, const float* XT, int64_t ldx, int64_t pe, int b, const float* M,
-                   float* Q2, const int* flag);
-// CholeskyQR pass 2 + Householder reconstruction (T, N, NT, R_new) from G2
-// (+ Q1^T Q1); for a flagged panel T from the UT transform of Y^T Y, N = I,
-// NT = T.
-int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, const float* U1, int b,
-                      float* N, float* NT, float* T, float* R, int64_t ldr, int* flag);
-// For each 64-column block of C_rest (nr columns; G block 1 + cb = Q2^T C):
+                   float* Q2, float* Ptop, int64_t ldr, const int* flag);
+// CholeskyQR pass 2 + Householder reconstruction from G2 (+ Q1^T Q1) (for a
+// flagged panel T from the UT transform of Y^T Y, N = I, NT = T): N (ld b),
+// R_new into R's diagonal block, and for each 64-column block of the nr
+// columns right of it (G block 1 + cb = Q2^T C_rest):
 // W = NT^T (Q2^T C) + T^T R_rest, R_rest -= W, NW = N W (ld ldnw).
-int launch_panel_wcomp(hipStream_t s, const float* G, int ncb, int b, const float* N,
-                       const float* NT, const float* T, float* Rrest, int64_t ldr, int nr, float* NW,
-                       int64_t ldnw);
+int launch_panel_hrw(hipStream_t s, const float* G, int ncb, const float* Q1, const float* U1,
+                     int b, float* N, float* R, int64_t ldr, int nr, float* NW, int64_t ldnw,
+                     const int* flag);
 // Y = Q2 N (ld ldy; also RNE bf16 into Yb, same ld, when Yb is given) and
 // CT_rest -= (Q2 NW)^T on the transposed working matrix (nr rows of ld ldc)
 int launch_panel_update(hipStream_t s, const float* Q2, int64_t pe, int b, const float* N,
@@ -74,7 +70,7 @@ int launch_sub_inplace(hipStream_t s, float* dst, int64_t ldd, const float* src,
 int launch_sign_normalize(hipStream_t s, float* R, int64_t ldr, int64_t r, int64_t n);
 // out (dtype odt) = R upper triangle (RNE for bf16); *finite &= all finite
 int launch_cast_upper(hipStream_t s, const float* R, int64_t ldr, int64_t n, void* out, int odt,
-                      int64_t ldo, int* finite);
+                      int64_t ldo, int* finite, float scale = 1.0f);
 // out (odt) = src (fp32), full matrix
 int launch_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols, void* out,
                 int odt, int64_t ldo);
@@ -83,9 +79,10 @@ int launch_fill_int(hipStream_t s, int* p, int value, int count);
 // heavy-ball momentum + decoupled weight decay + SGD step
 int launch_momentum_update(hipStream_t s, const float* nat, float* buf, float* W, int64_t numel,
                            float lr, float momentum, float weight_decay, int buf_init);
-// dst (cols x rows, fp32) = src^T (src rows x cols, dtype sdt)
+// dst (cols x rows, fp32) = src^T (src rows x cols, dtype sdt); with upper set,
+// entries of src below its diagonal are taken as zero
 int launch_transpose_to_f32(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
-                            int64_t cols, float* dst, int64_t ldd);
+                            int64_t cols, float* dst, int64_t ldd, bool upper = false);
 // out (odt, n x n) = lower triangle of src^T, i.e. out[i][j] = src[j][i] for j <= i, else 0
 int launch_transpose_upper(hipStream_t s, const float* src, int64_t lds, int64_t n, void* out,
                            int odt, int64_t ldo);

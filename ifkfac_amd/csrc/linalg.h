@@ -20,6 +20,14 @@ int finalize(hipStream_t s, const float* R_in, int64_t ldr_in, int64_t n, float 
              float damping, void* out, int odt, int64_t ldo, int math, int* finite, void* ws,
              size_t ws_bytes);
 
+// finalize(fold(R_in, X)) without the undamped running factor: out = R_damped
+// of [scale R_in[0:r_in]; scale X; sqrt(damping) I] by a single TPQRT fold.
+size_t fold_finalize_ws(int64_t p, int64_t n, int64_t r_in);
+int fold_finalize(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                  const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
+                  void* out, int odt, int64_t ldo, int math, int* finite, void* ws,
+                  size_t ws_bytes);
+
 // Z = R^{-1} for upper-triangular R (dtype rdt); Z fp32 upper triangular.
 size_t trinv_ws(int64_t n);
 int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,

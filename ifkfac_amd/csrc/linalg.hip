@@ -86,8 +86,6 @@ struct FoldWs {
   float* M1;
   float* Q1;
   float* N;
-  float* NT;
-  float* T;
   float* Go;      // OUTER_B x OUTER_B: Gram of the outer reflectors
   float* Tio;     // OUTER_B x OUTER_B: UT transform T^{-1}
   float* To[2];   // OUTER_B x OUTER_B: T of an outer block (by block parity)
@@ -120,8 +118,6 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   w.M1 = a.take<float>(b * b);
   w.Q1 = a.take<float>(b * b);
   w.N = a.take<float>(b * b);
-  w.NT = a.take<float>(b * b);
-  w.T = a.take<float>(b * b);
   w.Go = a.take<float>(B * B);
   w.Tio = a.take<float>(B * B);
   w.ttmp = a.take<float>((size_t)B * B / 2 + (size_t)TRINV_NB * TRINV_NB * 4);
@@ -271,14 +267,14 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
       // pass 1: G1 = X_p^T X_p (+ P_top^T P_top), U1, M1 -- or the fallback
       RC(launch_gram(s, XpT, ldc, bk, true, nullptr, 0, 0, XpT, ldc, bk, pe, w.part, w.Gp, &ncb));
       RC(launch_panel_hr_a(s, w.Gp, Ptop, ldr, bk, HR_TOL, w.U1, w.M1, w.Q1, w.flag));
-      RC(launch_panel_hh_fallback(s, Ptop, ldr, XpT, ldc, pe, bk, w.Q2, w.flag));
-      // pass 2: Q2 = X_p M1, G2 = Q2^T Q2 and Q2^T C_rest in one sweep
-      RC(launch_apply_m(s, XpT, ldc, pe, bk, w.M1, w.Q2, w.flag));
+      // pass 2: Q2 = X_p M1 (or the fallback), G2 = Q2^T Q2 and Q2^T C_rest in one sweep
+      RC(launch_apply_m(s, XpT, ldc, pe, bk, w.M1, w.Q2, Ptop, ldr, w.flag));
       RC(launch_gram(s, w.Q2, PANEL_B, PANEL_B, false, w.Q2, PANEL_B, PANEL_B, C + c1 * ldc, ldc,
                      nr, pe, w.part, w.Gp, &ncb));
-      RC(launch_panel_hr_b(s, w.Gp, w.Q1, w.U1, bk, w.N, w.NT, w.T, Ptop, ldr, w.flag));
-      // rest of the outer block: R_rest and C_rest, Y into the outer store
-      RC(launch_panel_wcomp(s, w.Gp, ncb, bk, w.N, w.NT, w.T, Ptop + bk, ldr, nr, w.NW, OUTER_B));
+      // reconstruction, R_new, and the rest of the outer block's R rows
+      RC(launch_panel_hrw(s, w.Gp, ncb, w.Q1, w.U1, bk, w.N, Ptop, ldr, nr, w.NW, OUTER_B,
+                          w.flag));
+      // C_rest and Y into the outer store
       RC(launch_panel_update(s, w.Q2, pe, bk, w.N, w.Yo[k2] + (c0 - K0), OUTER_B,
                              bf ? w.Yob[k2] + (c0 - K0) : nullptr, w.NW, OUTER_B, C + c1 * ldc,
                              ldc, nr));
@@ -386,6 +382,61 @@ int finalize(hipStream_t s, const float* R_in, int64_t ldr_in, int64_t n, float 
   RC(fold_core(s, w.C, n, n, n, Rw, n, n, true, math, w));
   if (finite) RC(launch_fill_int(s, finite, 1, 1));
   return launch_cast_upper(s, Rw, n, n, out, odt, ldo, finite);
+}
+
+// ----------------------------------------------------------------------------
+// Fold and finalize in one factorisation
+// ----------------------------------------------------------------------------
+// The damped factor of the rows already folded (R_in, r_in rows) plus a
+// chunk X is the R of [scale R_in; scale X; sqrt(damping) I], which is
+// scale times the R of [R_in; X; c I] with c = sqrt(damping) / scale.  The
+// triangular c I is the top block of one TPQRT fold whose working matrix is
+// [R_in; X] (r_in + p rows): a single dependent panel chain instead of a fold
+// followed by a finalize.
+static void plan_fold_finalize(Arena& a, int64_t pe, int64_t n, float** Rw, FoldWs& w) {
+  *Rw = a.take<float>((size_t)n * n);
+  plan_fold(a, pe, n, true, w);
+}
+
+size_t fold_finalize_ws(int64_t p, int64_t n, int64_t r_in) {
+  Arena a(nullptr, 0);
+  float* Rw;
+  FoldWs w;
+  plan_fold_finalize(a, r_in + p, n, &Rw, w);
+  return a.used;
+}
+
+int fold_finalize(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                  const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
+                  void* out, int odt, int64_t ldo, int math, int* finite, void* ws,
+                  size_t ws_bytes) {
+  if (n < 1 || p < 0 || r_in < 0 || r_in > n || (p > 0 && (!X || ldx < n)) ||
+      (r_in > 0 && (!R_in || ldr < n)) || !out || ldo < n || !(scale > 0.0f) ||
+      !(damping >= 0.0f) || (xdt != DT_F32 && xdt != DT_BF16) ||
+      (odt != DT_F32 && odt != DT_BF16)) {
+    set_error("fold_finalize: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  const int64_t pe = r_in + p;
+  if (!(damping > 0.0f) && pe < n) {
+    set_error("fold_finalize: fewer rows than columns and no damping (the factor is not square)");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  float* Rw;
+  FoldWs w;
+  plan_fold_finalize(a, pe, n, &Rw, w);
+  RC(check_ws(a, "fold_finalize"));
+  RC(launch_set_diag(s, Rw, n, n, std::sqrt(damping) / scale));
+  if (r_in > 0) RC(launch_transpose_to_f32(s, R_in, DT_F32, ldr, r_in, n, w.C, pe, true));
+  if (p > 0) RC(launch_transpose_to_f32(s, X, xdt, ldx, p, n, w.C + r_in, pe));
+  if (pe > 0) {
+    RC(fold_core(s, w.C, pe, pe, n, Rw, n, n, false, math, w));
+  } else {
+    RC(launch_sign_normalize(s, Rw, n, n, n));
+  }
+  if (finite) RC(launch_fill_int(s, finite, 1, 1));
+  return launch_cast_upper(s, Rw, n, n, out, odt, ldo, finite, scale);
 }
 
 // ----------------------------------------------------------------------------

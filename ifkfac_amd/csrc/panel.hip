@@ -11,10 +11,10 @@
 //                  and 64-column block cb of B) -- G1 = X_p^T X_p, then
 //                  G2 = Q2^T Q2 and Q2^T C_rest
 //   gram_reduce    G[cb] = sum_s part[s][cb], in slab order (deterministic)
-//   apply_m        Q2 = X_p M1 (skipped for a flagged panel: the Householder
-//                  fallback has written its reflectors into Q2)
+//   apply_m        Q2 = X_p M1, or for a flagged panel the Householder
+//                  fallback (reflectors into Q2, R_new into P_top)
 //   panel_update   Y = Q2 N into the outer block's reflector store and
-//                  CT_rest -= (Q2 NW)^T (NW = N W from panel_wcomp)
+//                  CT_rest -= (Q2 NW)^T (NW = N W from panel_hrw)
 //
 // All products run on fp32 MFMA (v_mfma_f32_32x32x2f32, fp32 accumulation):
 // the panel sits on the critical path of the factorisation and its
@@ -26,6 +26,7 @@
 // per wave.
 #include "common.h"
 #include "kernels.h"
+#include "panel_fallback.h"
 
 namespace ifk {
 
@@ -174,13 +175,18 @@ __global__ __launch_bounds__(PNT) void gram_reduce_kernel(const float* part, int
 
 // Q2[r][:] = X_p[r][0:b] M (M b x b in ld b), r < pe, Q2 of ld 64 (columns >=
 // b written as zero); X_p is the transposed row block XT (b x pe, ld ldx).
-// Nothing is done when *flag is set.
+// When *flag is set (the first CholeskyQR pass collapsed) workgroup 0 runs
+// the Householder fallback instead, which writes its reflectors into Q2 and
+// R_new into P_top, and the other workgroups do nothing.
 __global__ __launch_bounds__(PNT) void apply_m_kernel(const float* XT, int64_t ldx, int64_t pe,
                                                       int b, const float* M, float* Q2,
-                                                      const int* flag) {
-  if (*flag) return;
+                                                      float* Ptop, int64_t ldr, const int* flag) {
   __shared__ float sX[PT * LT];
   __shared__ float sM[PT * TLD];
+  if (*flag) {
+    if (blockIdx.x == 0) panel_hh_fallback(Ptop, ldr, XT, ldx, pe, b, Q2, sX, sM);
+    return;
+  }
   const int64_t r0 = (int64_t)blockIdx.x * PT;
   load_cm<true, PT>(sX, LT, XT, ldx, r0, pe, b);
   load_rm(sM, M, b, b, b);
@@ -203,11 +209,11 @@ __global__ __launch_bounds__(PNT) void apply_m_kernel(const float* XT, int64_t l
   }
 }
 
-// Panel update for the 64-row tile rb (the Q2 tile is loaded once):
-//   Y[r][0:b] = Q2[r][:] N                    (Y of ld ldy; RNE bf16 copy into
-//                                              Yb, same ld, if given)
-//   CT[c][r] -= (NW^T Q2^T)[c][r]             for the nr rows c of CT_rest
-//                                              (NW 64 x nr, ld ldnw)
+// Panel update, one workgroup per (64-row tile, column block cb):
+//   cb == 0:  Y[r][0:b] = Q2[r][:] N           (Y of ld ldy; RNE bf16 copy into
+//                                               Yb, same ld, if given)
+//   cb >= 1:  CT[c][r] -= (NW^T Q2^T)[c][r]    for the rows c of block cb - 1
+//                                               of CT_rest (NW 64 x nr, ld ldnw)
 // The transposed product puts consecutive r on consecutive lanes, so the
 // read-modify-write of CT is coalesced.
 __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int64_t pe, int b,
@@ -218,66 +224,63 @@ __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int6
   __shared__ float sQ[PT * LT];
   __shared__ float sM[PT * TLD];
   const int64_t r0 = (int64_t)blockIdx.x * PT;
+  const int cb = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, h = lane >> 5;
   const int mq = (wave >> 1) * 32 + l32, nq = (wave & 1) * 32 + l32;
   const int jc = acc_col();
   load_cm<false, PT>(sQ, LT, Q2, PT, r0, pe, PT);
-  const int nblk = (nr + PT - 1) / PT;
-  for (int cb = 0; cb <= nblk; ++cb) {
-    int w;
-    if (cb == 0) {
-      load_rm(sM, N, b, b, b);
-      w = b;
-    } else {
-      w = nr - (cb - 1) * PT;
-      if (w > PT) w = PT;
-      load_rm(sM, NW + (cb - 1) * PT, ldnw, PT, w);
+  int w;
+  if (cb == 0) {
+    load_rm(sM, N, b, b, b);
+    w = b;
+  } else {
+    w = nr - (cb - 1) * PT;
+    if (w > PT) w = PT;
+    load_rm(sM, NW + (cb - 1) * PT, ldnw, PT, w);
+  }
+  __syncthreads();
+  f32x16 d;
+  zero16(d);
+  if (cb == 0) {
+    // D[r][j] = sum_k Q2[r][k] N[k][j]
+#pragma unroll 8
+    for (int st = 0; st < 32; ++st) {
+      const int k = 32 * h + st;
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(sQ[k * LT + mq], sM[k * TLD + nq], d, 0, 0, 0);
     }
-    __syncthreads();
-    f32x16 d;
-    zero16(d);
-    if (cb == 0) {
-      // D[r][j] = sum_k Q2[r][k] N[k][j]
-#pragma unroll 8
-      for (int st = 0; st < 32; ++st) {
-        const int k = 32 * h + st;
-        d = __builtin_amdgcn_mfma_f32_32x32x2f32(sQ[k * LT + mq], sM[k * TLD + nq], d, 0, 0, 0);
-      }
-      if (jc < w) {
+    if (jc < w) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t gr = r0 + acc_row(r);
-          if (gr < pe) {
-            Y[gr * ldy + jc] = d[r];
-            if (Yb) Yb[gr * ldy + jc] = f32_to_bf16(d[r]);
-          }
-        }
-      }
-    } else {
-      // D[c][r] = sum_k NW[k][c] Q2[r][k]
-#pragma unroll 8
-      for (int st = 0; st < 32; ++st) {
-        const int k = 32 * h + st;
-        d = __builtin_amdgcn_mfma_f32_32x32x2f32(sM[k * TLD + mq], sQ[k * LT + nq], d, 0, 0, 0);
-      }
-      const int64_t gr = r0 + jc;
-      if (gr < pe) {
-        float* Cb = CT + (int64_t)(cb - 1) * PT * ldc + gr;
-        float cur[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = acc_row(r);
-          cur[r] = (c < w) ? Cb[(int64_t)c * ldc] : 0.0f;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = acc_row(r);
-          if (c < w) Cb[(int64_t)c * ldc] = cur[r] - d[r];
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gr = r0 + acc_row(r);
+        if (gr < pe) {
+          Y[gr * ldy + jc] = d[r];
+          if (Yb) Yb[gr * ldy + jc] = f32_to_bf16(d[r]);
         }
       }
     }
-    __syncthreads();   // sM is reloaded for the next block
+  } else {
+    // D[c][r] = sum_k NW[k][c] Q2[r][k]
+#pragma unroll 8
+    for (int st = 0; st < 32; ++st) {
+      const int k = 32 * h + st;
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(sM[k * TLD + mq], sQ[k * LT + nq], d, 0, 0, 0);
+    }
+    const int64_t gr = r0 + jc;
+    if (gr < pe) {
+      float* Cb = CT + (int64_t)(cb - 1) * PT * ldc + gr;
+      float cur[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = acc_row(r);
+        cur[r] = (c < w) ? Cb[(int64_t)c * ldc] : 0.0f;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = acc_row(r);
+        if (c < w) Cb[(int64_t)c * ldc] = cur[r] - d[r];
+      }
+    }
   }
 }
 
@@ -315,10 +318,14 @@ int launch_gram(hipStream_t s, const float* A, int64_t lda, int ka, bool a_ts, c
 }
 
 int launch_apply_m(hipStream_t s, const float* XT, int64_t ldx, int64_t pe, int b, const float* M,
-                   float* Q2, const int* flag) {
-  if (pe <= 0) return IFK_OK;
-  hipLaunchKernelGGL(apply_m_kernel, dim3((unsigned)cdiv(pe, (int64_t)PT)), dim3(PNT), 0, s, XT,
-                     ldx, pe, b, M, Q2, flag);
+                   float* Q2, float* Ptop, int64_t ldr, const int* flag) {
+  if (b < 1 || b > PT) {
+    set_error("apply_m: block size out of range");
+    return IFK_ERR_INVALID;
+  }
+  // pe == 0 still launches one workgroup: a flagged panel needs the fallback
+  hipLaunchKernelGGL(apply_m_kernel, dim3((unsigned)std::max<int64_t>(1, cdiv(pe, (int64_t)PT))),
+                     dim3(PNT), 0, s, XT, ldx, pe, b, M, Q2, Ptop, ldr, flag);
   return check_launch("apply_m");
 }
 
@@ -326,8 +333,9 @@ int launch_panel_update(hipStream_t s, const float* Q2, int64_t pe, int b, const
                         float* Y, int64_t ldy, bf16_t* Yb, const float* NW, int64_t ldnw,
                         float* CT, int64_t ldc, int nr) {
   if (pe <= 0) return IFK_OK;
-  hipLaunchKernelGGL(panel_update_kernel, dim3((unsigned)cdiv(pe, (int64_t)PT)), dim3(PNT), 0, s,
-                     Q2, pe, b, N, Y, ldy, Yb, NW, ldnw, CT, ldc, nr);
+  const int nblk = nr > 0 ? (int)cdiv((int64_t)nr, (int64_t)PT) : 0;
+  hipLaunchKernelGGL(panel_update_kernel, dim3((unsigned)cdiv(pe, (int64_t)PT), 1 + nblk),
+                     dim3(PNT), 0, s, Q2, pe, b, N, Y, ldy, Yb, NW, ldnw, CT, ldc, nr);
   return check_launch("panel_update");
 }
 

@@ -12,15 +12,16 @@
 //   X_p the p_e x b block of the working X.
 // Reflectors come from CholeskyQR2 plus Householder reconstruction:
 //   G1 = P^T P = U1^T U1, M1 = U1^{-1}, Q = P M1                 (panel_hr_a)
-//   G2 = Q^T Q = U2^T U2, M2 = U2^{-1}, Q_f = Q M2               (panel_hr_b)
+//   G2 = Q^T Q = U2^T U2, M2 = U2^{-1}, Q_f = Q M2               (panel_hrw)
 //   S = diag(-sign((Q_f,top)_jj)), T = I - Q_f,top S (upper triangular)
 //   Y = Q_bottom N with N = -M2 S T^{-1},  Y T = Q_bottom (-M2 S)
 //   R_new = S U2 U1
 // which is the TPQRT form: V = [I; Y], block reflector I - V T V^T.  When a
 // first-pass Cholesky pivot collapses (rank-deficient or ill-conditioned
-// panel) a flag is raised and panel_hh_fallback computes the reflectors by
+// panel) a flag is raised and the Householder fallback (panel_fallback.h, run by
+// apply_m in place of Q2 = X_p M1) computes the reflectors by
 // column-by-column Householder reflections (LAPACK dlarfg convention, never
-// breaks down); panel_hr_b then takes T from the UT transform
+// breaks down); panel_hrw then takes T from the UT transform
 //   T^{-1} = striu(V^T V) + diag(V^T V) / 2,  V^T V = I + Y^T Y.
 // The partial Gram matrices over row slabs come from panel.hip.
 #include "common.h"
@@ -343,29 +344,38 @@ __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
   if (threadIdx.x == 0) *flag = bad;
 }
 
-// CholeskyQR pass 2 and Householder reconstruction.  In: G2 = Q2^T Q2
-// (64 x 64, ld 64; Q2 = X_p M1), Q1, U1.
-// Out: T (b x b, ld b), N (Y = Q2 N) and NT (Y T = Q2 NT); R's diagonal block
-// <- R_new = S U2 U1.
+// CholeskyQR pass 2, Householder reconstruction and the update of the rest of
+// the outer block, one launch of 1 + nblk workgroups.  In: G[0] = G2 =
+// Q2^T Q2 and G[1 + cb] = Q2^T C_rest block cb (64 x 64 each, ld 64;
+// Q2 = X_p M1), Q1, U1.  Every workgroup builds T, NT (Y T = Q2 NT) and N
+// (Y = Q2 N) in LDS -- the redundant 64 x 64 work costs no time on the
+// critical path, and it saves a launch and a round trip through memory.
+//   workgroup 0:      N to global; R's diagonal block <- R_new = S U2 U1
+//   workgroup 1 + cb: W = NT^T (Q2^T C) + T^T R_rest, R_rest -= W, NW = N W
+//                     for the 64-column block cb of R_rest (nr columns)
 // For a panel flagged by pass 1, Q2 holds the fallback's reflectors Y and R
 // already holds R_new: T comes from the UT transform of Y^T Y, N = I, NT = T.
 // A second-pass pivot below 1/4 (the first pass lost too much orthogonality
 // for the reconstruction to be exact) poisons R's block with NaN, which the
 // finite check of finalize reports.
-__global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const float* Q1, const float* U1, int b,
-                                                          float* N, float* NT, float* T, float* R,
-                                                          int64_t ldr, int* flag) {
+__global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const float* Q1,
+                                                         const float* U1, int b, float* N,
+                                                         float* R, int64_t ldr, int nr,
+                                                         float* NW, int64_t ldnw,
+                                                         const int* flag) {
   __shared__ float sG[SB * SLD];
   __shared__ float sQ[SB * SLD];
   __shared__ float sM[SB * SLD];
   __shared__ float sX[SB * SLD];
+  __shared__ float sN[SB * SLD];
   __shared__ float sTmp[32 * 32];
   __shared__ float sgn[SB];
   __shared__ int bad;
   const int t = threadIdx.x;
+  const int role = blockIdx.x;   // 0: R_new and N; 1 + cb: block cb of the rest
   if (t == 0) bad = 0;
   const bool flagged = (*flag != 0);
-  sm_load_pad(sG, G2, SB, b, false);
+  sm_load_pad(sG, G, SB, b, false);
   if (flagged) {
     // UT transform: T^{-1} = striu(Y^T Y) + diag(1 + diag(Y^T Y)) / 2
     for (int e = t; e < SB * SB; e += SNT) {
@@ -377,177 +387,70 @@ __global__ __launch_bounds__(SNT) void panel_hr_b_kernel(const float* G2, const 
       } else if (i == j) {
         v = 1.0f;
       }
+      sM[i * SLD + j] = v;
+    }
+    __syncthreads();
+    sm_trinv64(sM, sX, sTmp);                        // sX = T
+    for (int e = t; e < SB * SB; e += SNT) {
+      const int i = e >> 6, j = e & 63;
+      const float id = (i == j) ? 1.0f : 0.0f;
+      sN[i * SLD + j] = id;                          // N = I
+      sQ[i * SLD + j] = sX[i * SLD + j];             // NT = T
+    }
+    __syncthreads();
+  } else {
+    sm_load_pad(sQ, Q1, b, b, true, 0.0f);
+    sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
+    sm_chol64(sG, 0.25f, &bad, 0);                   // sG = U2
+    sm_trinv64(sG, sM, sTmp);                        // sM = M2
+    sm_gemm64<false, false>(sQ, sM, sX, 1.0f, false);  // sX = Q1f = Q1 M2
+    for (int j = t; j < SB; j += SNT) sgn[j] = (sX[j * SLD + j] >= 0.0f) ? -1.0f : 1.0f;
+    __syncthreads();
+    // sX <- T = I - Q1f S (upper triangular; identity in the pad)
+    for (int e = t; e < SB * SB; e += SNT) {
+      const int i = e >> 6, j = e & 63;
+      float v = (i == j) ? 1.0f : 0.0f;
+      if (i < b && j < b && i <= j) v -= sX[i * SLD + j] * sgn[j];
       sX[i * SLD + j] = v;
     }
     __syncthreads();
-    sm_trinv64(sX, sQ, sTmp);                      // sQ = T
+    sm_trinv64(sX, sQ, sTmp);                        // sQ = T^{-1}
+    for (int e = t; e < SB * SB; e += SNT) {         // sQ <- S T^{-1}
+      const int k = e >> 6, j = e & 63;
+      sQ[k * SLD + j] *= sgn[k];
+    }
+    __syncthreads();
+    sm_gemm64<false, false>(sM, sQ, sN, -1.0f, false);  // sN = N = -M2 S T^{-1}
+    for (int e = t; e < SB * SB; e += SNT) {         // sQ <- NT = -M2 S (zero in the pad)
+      const int i = e >> 6, j = e & 63;
+      sQ[i * SLD + j] = (i < b && j < b) ? -sM[i * SLD + j] * sgn[j] : 0.0f;
+    }
+    __syncthreads();
+  }
+  // here: sX = T, sQ = NT, sN = N (all zero / identity beyond b as built)
+  if (role == 0) {
     for (int e = t; e < b * b; e += SNT) {
       const int i = e / b, j = e - i * b;
-      const float v = sQ[i * SLD + j];
-      T[e] = v;
-      NT[e] = v;
-      N[e] = (i == j) ? 1.0f : 0.0f;
+      N[e] = sN[i * SLD + j];
+    }
+    if (flagged) return;
+    const bool ok = (bad == 0);
+    sm_load_pad(sM, U1, b, b, true);
+    sm_gemm64<false, false>(sG, sM, sM, 1.0f, false);  // sM = U2 U1
+    const float nan = __int_as_float(0x7fc00000);
+    for (int e = t; e < b * b; e += SNT) {           // R_new = S U2 U1
+      const int i = e / b, j = e - i * b;
+      R[(int64_t)i * ldr + j] = !ok ? nan : ((i <= j) ? sgn[i] * sM[i * SLD + j] : 0.0f);
     }
     return;
   }
-  sm_load_pad(sQ, Q1, b, b, true, 0.0f);
-  sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
-  sm_chol64(sG, 0.25f, &bad, 0);                   // sG = U2
-  sm_trinv64(sG, sM, sTmp);                        // sM = M2
-  sm_gemm64<false, false>(sQ, sM, sX, 1.0f, false);  // sX = Q1f = Q1 M2
-  for (int j = t; j < SB; j += SNT) sgn[j] = (sX[j * SLD + j] >= 0.0f) ? -1.0f : 1.0f;
-  __syncthreads();
-  // sX <- T = I - Q1f S (upper triangular; identity in the pad)
-  for (int e = t; e < SB * SB; e += SNT) {
-    const int i = e >> 6, j = e & 63;
-    float v = (i == j) ? 1.0f : 0.0f;
-    if (i < b && j < b && i <= j) v -= sX[i * SLD + j] * sgn[j];
-    sX[i * SLD + j] = v;
-  }
-  __syncthreads();
-  const bool ok = (bad == 0);
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e - i * b;
-    T[e] = sX[i * SLD + j];
-    NT[e] = -sM[i * SLD + j] * sgn[j];
-  }
-  sm_trinv64(sX, sQ, sTmp);                        // sQ = T^{-1}
-  for (int e = t; e < SB * SB; e += SNT) {         // sQ <- S T^{-1}
-    const int k = e >> 6, j = e & 63;
-    sQ[k * SLD + j] *= sgn[k];
-  }
-  __syncthreads();
-  sm_gemm64<false, false>(sM, sQ, sX, -1.0f, false);  // sX = N = -M2 S T^{-1}
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, j = e - i * b;
-    N[e] = sX[i * SLD + j];
-  }
-  __syncthreads();
-  sm_load_pad(sQ, U1, b, b, true);
-  sm_gemm64<false, false>(sG, sQ, sX, 1.0f, false);  // sX = U2 U1
-  const float nan = __int_as_float(0x7fc00000);
-  for (int e = t; e < b * b; e += SNT) {           // R_new = S U2 U1
-    const int i = e / b, j = e - i * b;
-    R[(int64_t)i * ldr + j] = !ok ? nan : ((i <= j) ? sgn[i] * sX[i * SLD + j] : 0.0f);
-  }
-  if (t == 0 && !ok) *flag = 1;
-}
-
-// Robust TPQRT panel by Householder reflections (LAPACK dlarfg convention),
-// run only when *flag is set: the reflectors' X parts go to Q2 (p_e x 64,
-// columns >= b zero) and R's diagonal block is replaced by R_new.  The panel
-// X_p is read from the transposed working matrix (XpT: b x p_e, ld ldx).  One
-// workgroup walks the b columns; norms and dot products over the p_e rows
-// are wave-shuffle reductions.
-__global__ __launch_bounds__(SNT) void panel_hh_fallback_kernel(float* Ptop, int64_t ldr,
-                                                                 const float* XpT, int64_t ldx,
-                                                                 int64_t pe, int b, float* Y,
-                                                                 const int* flag) {
-  if (*flag == 0) return;
-  constexpr int64_t ldy = SB;
-  __shared__ float sP[SB * SLD];
-  __shared__ float red[4][SB];
-  __shared__ float wv[SB];
-  __shared__ float scal[3];
-  const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
-  for (int e = t; e < SB * SB; e += SNT) {
-    const int r = e >> 6, c = e & 63;
-    sP[r * SLD + c] = (r < b && c < b && r <= c) ? Ptop[(int64_t)r * ldr + c] : 0.0f;
-  }
-  for (int64_t e = t; e < pe * SB; e += SNT) {
-    const int64_t r = e / SB;
-    const int c = (int)(e % SB);
-    Y[r * ldy + c] = (c < b) ? XpT[(int64_t)c * ldx + r] : 0.0f;
-  }
-  __syncthreads();
-  for (int j = 0; j < b; ++j) {
-    float part = 0.0f;
-    for (int64_t r = t; r < pe; r += SNT) {
-      const float v = Y[r * ldy + j];
-      part += v * v;
-    }
-    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
-    if (lane == 0) red[wave][0] = part;
-    __syncthreads();
-    if (t == 0) {
-      const float xn2 = red[0][0] + red[1][0] + red[2][0] + red[3][0];
-      const float alpha = sP[j * SLD + j];
-      if (!(xn2 > 0.0f)) {
-        // Nothing below the diagonal: reflect row j alone (v = e_j, tau = 2),
-        // which is what the UT transform of a zero y_j encodes (T_jj = 2).
-        scal[0] = 2.0f;
-        scal[1] = 0.0f;
-        scal[2] = -alpha;
-      } else {
-        const float nrm = sqrtf(alpha * alpha + xn2);
-        const float beta = (alpha >= 0.0f) ? -nrm : nrm;
-        scal[0] = (beta - alpha) / beta;
-        scal[1] = 1.0f / (alpha - beta);
-        scal[2] = beta;
-      }
-    }
-    __syncthreads();
-    const float tau = scal[0], sc = scal[1];
-    for (int64_t r = t; r < pe; r += SNT) Y[r * ldy + j] *= sc;
-    __syncthreads();
-    float acc[SB];
-#pragma unroll
-    for (int c = 0; c < SB; ++c) acc[c] = 0.0f;
-    for (int64_t r = t; r < pe; r += SNT) {
-      const float y = Y[r * ldy + j];
-#pragma unroll
-      for (int c = 0; c < SB; ++c)
-        if (c > j && c < b) acc[c] += y * Y[r * ldy + c];
-    }
-#pragma unroll
-    for (int c = 0; c < SB; ++c) {
-      if (c > j && c < b) {
-        float v = acc[c];
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-        if (lane == 0) red[wave][c] = v;
-      }
-    }
-    __syncthreads();
-    for (int c = j + 1 + t; c < b; c += SNT)
-      wv[c] = sP[j * SLD + c] + red[0][c] + red[1][c] + red[2][c] + red[3][c];
-    __syncthreads();
-    for (int c = j + 1 + t; c < b; c += SNT) sP[j * SLD + c] -= tau * wv[c];
-    for (int64_t e = t; e < pe * (b - j - 1); e += SNT) {
-      const int64_t r = e / (b - j - 1);
-      const int c = j + 1 + (int)(e % (b - j - 1));
-      Y[r * ldy + c] -= tau * wv[c] * Y[r * ldy + j];
-    }
-    if (t == 0) sP[j * SLD + j] = scal[2];
-    __syncthreads();
-  }
-  for (int e = t; e < b * b; e += SNT) {
-    const int i = e / b, c = e - i * b;
-    Ptop[(int64_t)i * ldr + c] = (i <= c) ? sP[i * SLD + c] : 0.0f;
-  }
-}
-
-// Block cb of the rest of the outer block (64 columns of C_rest, w of them
-// real): from QC = block 1 + cb of the reduced Grams (Q2^T C_rest, ld 64),
-//   W = NT^T (Q2^T C) + T^T R_rest,  R_rest -= W,  NW = N W
-// which applies the panel's block reflector to R_rest and leaves the X-side
-// update C_rest -= Q2 NW to panel_update.
-__global__ __launch_bounds__(SNT) void panel_wcomp_kernel(const float* G, int b, const float* N, const float* NT,
-                                                           const float* T, float* Rrest,
-                                                           int64_t ldr, int nr, float* NW,
-                                                           int64_t ldnw) {
-  __shared__ float sA[SB * SLD];
-  __shared__ float sB[SB * SLD];
-  __shared__ float sW[SB * SLD];
-  __shared__ float sR[SB * SLD];
-  const int t = threadIdx.x;
-  const int cb = blockIdx.x;
+  // block cb of the rest: columns [b + c0, b + c0 + w) of R's block row
+  const int cb = role - 1;
   const int c0 = cb * SB;
   const int w = (nr - c0) < SB ? (nr - c0) : SB;
-  sm_load_pad(sA, G + (size_t)(1 + cb) * SB * SB, SB, SB, false);  // Q2^T C block (zero beyond b, w)
-  sm_load_pad(sB, NT, b, b, false, 0.0f);
-  sm_gemm64<true, false>(sB, sA, sW, 1.0f, false);      // W = NT^T (Q2^T C)
-  sm_load_pad(sB, T, b, b, true, 0.0f);
+  float* Rrest = R + b;
+  sm_load_pad(sG, G + (size_t)(1 + cb) * SB * SB, SB, SB, false);  // Q2^T C block
+  sm_gemm64<true, false>(sQ, sG, sM, 1.0f, false);     // sM = W = NT^T (Q2^T C)
   {
     float v[SB * SB / SNT];
 #pragma unroll
@@ -558,20 +461,19 @@ __global__ __launch_bounds__(SNT) void panel_wcomp_kernel(const float* G, int b,
 #pragma unroll
     for (int q = 0; q < SB * SB / SNT; ++q) {
       const int e = t + SNT * q;
-      sR[(e >> 6) * SLD + (e & 63)] = v[q];
+      sG[(e >> 6) * SLD + (e & 63)] = v[q];
     }
   }
   __syncthreads();
-  sm_gemm64<true, false>(sB, sR, sW, 1.0f, true);       // W += T^T R_rest
+  sm_gemm64<true, false>(sX, sG, sM, 1.0f, true);      // W += T^T R_rest
   for (int e = t; e < SB * SB; e += SNT) {
     const int i = e >> 6, j = e & 63;
-    if (i < b && j < w) Rrest[(int64_t)i * ldr + c0 + j] = sR[i * SLD + j] - sW[i * SLD + j];
+    if (i < b && j < w) Rrest[(int64_t)i * ldr + c0 + j] = sG[i * SLD + j] - sM[i * SLD + j];
   }
-  sm_load_pad(sB, N, b, b, false, 0.0f);
-  sm_gemm64<false, false>(sB, sW, sA, 1.0f, false);     // NW = N W
+  sm_gemm64<false, false>(sN, sM, sG, 1.0f, false);    // NW = N W
   for (int e = t; e < SB * SB; e += SNT) {
     const int i = e >> 6, j = e & 63;
-    NW[(int64_t)i * ldnw + c0 + j] = sA[i * SLD + j];
+    NW[(int64_t)i * ldnw + c0 + j] = sG[i * SLD + j];
   }
 }
 
@@ -662,35 +564,18 @@ int launch_panel_hr_a(hipStream_t s, const float* G, const float* Ptop, int64_t 
   return check_launch("panel_hr_a");
 }
 
-int launch_panel_hr_b(hipStream_t s, const float* G2, const float* Q1, const float* U1, int b,
-                      float* N, float* NT, float* T, float* R, int64_t ldr, int* flag) {
-  if (int rc = check_b(b, "panel_hr_b")) return rc;
-  hipLaunchKernelGGL(panel_hr_b_kernel, dim3(1), dim3(SNT), 0, s, G2, Q1, U1, b, N, NT, T, R, ldr,
-                     flag);
-  return check_launch("panel_hr_b");
-}
-
-int launch_panel_hh_fallback(hipStream_t s, float* Ptop, int64_t ldr, const float* XpT,
-                             int64_t ldx, int64_t pe, int b, float* Q2, const int* flag) {
-  if (int rc = check_b(b, "panel_hh_fallback")) return rc;
-  hipLaunchKernelGGL(panel_hh_fallback_kernel, dim3(1), dim3(SNT), 0, s, Ptop, ldr, XpT, ldx, pe,
-                     b, Q2, flag);
-  return check_launch("panel_hh_fallback");
-}
-
-int launch_panel_wcomp(hipStream_t s, const float* G, int ncb, int b, const float* N,
-                       const float* NT, const float* T, float* Rrest, int64_t ldr, int nr, float* NW,
-                       int64_t ldnw) {
-  if (int rc = check_b(b, "panel_wcomp")) return rc;
-  if (nr <= 0) return IFK_OK;
-  const int nblk = (int)cdiv((int64_t)nr, (int64_t)SB);
-  if (ncb != nblk + 1 || ldnw < (int64_t)nblk * SB) {
-    set_error("panel_wcomp: column blocks do not match the partial Grams");
+int launch_panel_hrw(hipStream_t s, const float* G, int ncb, const float* Q1, const float* U1,
+                     int b, float* N, float* R, int64_t ldr, int nr, float* NW, int64_t ldnw,
+                     const int* flag) {
+  if (int rc = check_b(b, "panel_hrw")) return rc;
+  const int nblk = nr > 0 ? (int)cdiv((int64_t)nr, (int64_t)SB) : 0;
+  if (ncb != nblk + 1 || (nblk > 0 && ldnw < (int64_t)nblk * SB)) {
+    set_error("panel_hrw: column blocks do not match the partial Grams");
     return IFK_ERR_INVALID;
   }
-  hipLaunchKernelGGL(panel_wcomp_kernel, dim3(nblk), dim3(SNT), 0, s, G, b, N, NT, T, Rrest, ldr,
-                     nr, NW, ldnw);
-  return check_launch("panel_wcomp");
+  hipLaunchKernelGGL(panel_hrw_kernel, dim3(1 + nblk), dim3(SNT), 0, s, G, Q1, U1, b, N, R, ldr, nr,
+                     NW, ldnw, flag);
+  return check_launch("panel_hrw");
 }
 
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b) {

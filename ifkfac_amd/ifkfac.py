@@ -87,6 +87,8 @@ class IFKFAC(torch.optim.Optimizer):
             math=self._math,
         )
         self.hooks.enable()
+        # the chunks captured before an update step feed a fused fold + finalize
+        self.hooks._defer_last = self._updates_at(1)
 
         self._factors: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._inverses: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
@@ -110,12 +112,18 @@ class IFKFAC(torch.optim.Optimizer):
         get_backend().fold_(buf, n, X, self._math)
         return buf
 
+    def _updates_at(self, step: int) -> bool:
+        """Whether step number ``step`` (1-based) updates the factors (ifkfac.py:560-564)."""
+        f = self.factor_update_freq
+        return f == 1 or (step >= f and step % f == 0)
+
     def _update_factors(self):
         t0 = time.perf_counter()
         blend = self.gamma > 0.0 and bool(self._factors)
         out_dtype = torch.bfloat16 if (self.use_true_bf16 and not blend) else torch.float32
         try:
-            new_factors, flags = self.hooks._collect_factors(out_dtype)
+            # the hooks are cleared right after: a held chunk may be consumed
+            new_factors, flags = self.hooks._collect_factors(out_dtype, consume=True)
         except IFKFACRankError as e:
             logger.warning("IFKFAC: factor update skipped — %s", e)
             self.timing["factor_compute"].append(time.perf_counter() - t0)
@@ -293,6 +301,7 @@ class IFKFAC(torch.optim.Optimizer):
         elif (self._step_count >= self.factor_update_freq
               and self._step_count % self.factor_update_freq == 0):
             self._update_factors()
+        self.hooks._defer_last = self._updates_at(self._step_count + 1)
 
         t_precond = time.perf_counter()
         self._apply_preconditioner_bucketed()

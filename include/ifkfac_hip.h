@@ -83,6 +83,30 @@ int ifk_finalize(void* stream, const float* R_in, int64_t ldr_in, int64_t n, flo
                  void* workspace, size_t workspace_bytes);
 
 /*
+ * Fold and finalize in one factorisation -- replaces the last
+ * streaming_tsqr_update of a factor window (ifkfac/triangular.py:246-307)
+ * followed by get_factors' scaling and finalize_R (ifkfac/activation_hooks.py:
+ * 328-332, ifkfac/triangular.py:386-421) when the undamped running factor is
+ * discarded right after, as IFKFAC._update_factors does (get_factors, then
+ * hooks.clear(): ifkfac/ifkfac.py:208, 227).
+ *
+ * out (n x n, ldo) = R_d with
+ *   R_d^T R_d = scale^2 (R_in^T R_in + X^T X) + damping I,
+ * upper triangular with positive diagonal, where R_in holds the r_in rows
+ * folded so far (row-major, ldr; entries below its diagonal are ignored) and
+ * X (p x n, ldx, fp32 or bf16) is the last chunk.  The result is the R of
+ * [scale R_in; scale X; sqrt(damping) I], computed as one TPQRT fold of
+ * [R_in; X] under the triangular block sqrt(damping) / scale I.  `finite` as
+ * for ifk_finalize.  Neither R_in nor X is modified.  With damping == 0,
+ * r_in + p must be at least n.
+ */
+size_t ifk_fold_finalize_workspace_size(int64_t p, int64_t n, int64_t r_in);
+int ifk_fold_finalize(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
+                      int64_t ldx, const float* R_in, int64_t ldr, int64_t r_in, float scale,
+                      float damping, void* out, int out_dtype, int64_t ldo, int math,
+                      int32_t* finite, void* workspace, size_t workspace_bytes);
+
+/*
  * Triangular inverse Z = R^{-1} of an upper-triangular n x n factor (dtype
  * r_dtype) into fp32 Z (ldz).  The four solves of apply_vered are applied as
  * products with Z; this is the factor-side half of them.

@@ -43,6 +43,16 @@ class OracleBackend:
         flag = torch.tensor([1 if np.all(np.isfinite(Rd)) else 0], dtype=torch.int32)
         return out, flag
 
+    def fold_finalize(self, R, r_in, X, scale, damping, out_dtype, math):
+        self.calls["fold_finalize"] += 1
+        old = None if r_in == 0 else _np(R[:r_in])
+        new = O.streaming_tsqr_update(old, _np(X))
+        assert new.shape[0] == new.shape[1], "fused finalize of a partial-rank factor"
+        Rd = O.finalize_R(new * scale, damping)
+        out = torch.from_numpy(Rd).float().to(out_dtype)
+        flag = torch.tensor([1 if np.all(np.isfinite(Rd)) else 0], dtype=torch.int32)
+        return out, flag
+
     def tri_inverse(self, R, math):
         self.calls["tri_inverse"] += 1
         return torch.from_numpy(np.linalg.inv(_np(R))).float()

@@ -205,6 +205,70 @@ def test_finalize_matches_closed_form(hip, p, n, lam):
     assert torch.equal(Rb, Rd.to(torch.bfloat16))   # RNE cast of the same fp32 result
 
 
+# --------------------------------------------------------------------------- fold + finalize
+
+
+@pytest.mark.parametrize("prev,p,n,lam", [
+    ([], 500, 300, 1e-2), ([300], 500, 300, 1e-2), ([64], 30, 128, 1e-2),
+    ([], 64, 64, 1e-3), ([], 3000, 1700, 1e-2), ([1200], 1200, 2100, 1e-2), ([], 20, 50, 1e-1),
+])
+def test_fold_finalize_matches_closed_form(hip, prev, p, n, lam):
+    """The fused call equals finalize(fold(R_in, X)): the R of [s R_in; s X; sqrt(lam) I]
+    against the fp64 Cholesky closed form, and against the two-call path on the GPU."""
+    g = torch.Generator(device=DEV).manual_seed(p + n + len(prev))
+    Xs = [torch.randn(q, n, device=DEV, generator=g) for q in prev]
+    X = torch.randn(p, n, device=DEV, generator=g)
+    R, r = _fold_chunks(hip, Xs, n)
+    R_before = R.clone()
+    rows = sum(prev) + p
+    Rd, flag = hip.fold_finalize(R, r, X, 1 / math.sqrt(rows), lam, torch.float32, 0)
+    assert flag.item() == 1
+    assert torch.equal(R, R_before)                  # the running factor is not touched
+    want = O.chol_factor([x.double().cpu().numpy() for x in Xs + [X]], rows, lam)
+    assert _gram_rel(Rd, want) <= 4 * _kappa(want) * EPS32
+    Rg = Rd.double().cpu().numpy()
+    assert np.all(np.diag(Rg) > 0) and not np.any(np.tril(Rg, -1))
+    R2 = R.clone()
+    r2 = hip.fold_(R2, r, X, 0)
+    if r2 == n:
+        Rd2, _ = hip.finalize(R2, 1 / math.sqrt(rows), lam, torch.float32, 0)
+        assert _gram_rel(Rd, Rd2.double().cpu().numpy()) <= 4 * _kappa(want) * EPS32
+    Rb, _ = hip.fold_finalize(R, r, X, 1 / math.sqrt(rows), lam, torch.bfloat16, 0)
+    assert torch.equal(Rb, Rd.to(torch.bfloat16))   # RNE cast of the same fp32 result
+
+
+def test_fold_finalize_guards_and_flags(hip):
+    X = torch.randn(10, 20, device=DEV)
+    with pytest.raises(Exception):
+        hip.fold_finalize(None, 0, X, 1.0, 0.0, torch.float32, 0)   # 10 rows, 20 columns, no damping
+    X = torch.randn(64, 16, device=DEV)
+    X[3, 4] = float("nan")
+    _, flag = hip.fold_finalize(None, 0, X, 1 / 8.0, 1e-2, torch.float32, 0)
+    assert flag.item() == 0
+    X[3, 4] = 1.0
+    _, flag = hip.fold_finalize(None, 0, X, 1 / 8.0, 1e-2, torch.float32, 0)
+    assert flag.item() == 1
+
+
+@pytest.mark.parametrize("n_in,n_out,p", [(4096, 11008, 16384)])
+def test_full_size_fold_finalize_bf16(hip, n_in, n_out, p):
+    """The benchmarked factor update at full size in bf16 arithmetic: for random
+    probes v, ||R_d v||^2 = ||X v||^2 / p + lam ||v||^2, and the natural gradient of
+    the fused factors matches that of the two-call factors to the bf16 bound."""
+    g = torch.Generator(device=DEV).manual_seed(7)
+    for n in (n_in, n_out):
+        X = torch.randn(p, n, device=DEV, generator=g).to(torch.bfloat16)
+        Rd, flag = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), 1e-2, torch.float32, 1)
+        assert flag.item() == 1
+        V = torch.randn(n, 16, device=DEV, generator=g, dtype=torch.float64)
+        l2 = (Rd.double() @ V).norm(dim=0) ** 2
+        r2 = (X.double() @ V).norm(dim=0) ** 2 / p + 1e-2 * (V ** 2).sum(0)
+        assert ((l2 - r2).abs() / r2).max().item() < 2e-3
+        d = torch.diagonal(Rd)
+        assert bool((d > 0).all()) and torch.count_nonzero(torch.tril(Rd, -1)).item() == 0
+        del X, Rd
+
+
 # --------------------------------------------------------------------------- preconditioning
 
 

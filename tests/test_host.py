@@ -81,9 +81,9 @@ def test_schedule_every_freq_steps(be):
     for step in range(1, 26):
         opt.zero_grad()
         model(X).pow(2).mean().backward()
-        before = be.calls["finalize"]
+        before = be.calls["finalize"] + be.calls["fold_finalize"]
         opt.step()
-        fired = be.calls["finalize"] > before
+        fired = be.calls["finalize"] + be.calls["fold_finalize"] > before
         assert fired == O.should_update_factors(step, 10), step
 
 
@@ -270,7 +270,7 @@ def test_conv2d_layer_uses_im2col_rows(be):
     opt = IFKFAC(model, lr=1e-3, factor_update_freq=1, max_conv_rows=0)
     model(torch.randn(8, 3, 8, 8)).pow(2).mean().backward()
     assert opt.hooks._n_rows_X[model[0]] == 8 * 36
-    assert opt.hooks._R_X[model[0]].shape == (27, 27)
+    assert opt.hooks._running_factor(model[0], "X").shape == (27, 27)
     W = model[0].weight.detach().clone()
     opt.step()
     assert model[0] in opt._factors
@@ -354,3 +354,63 @@ def test_canary_runs_match_reference_including_divergence(be, name):
     assert ok.sum() >= 10
     assert np.all(np.abs(got[ok] - want[ok]) <= 1e-4 * np.abs(want[ok]))
     assert not np.isfinite(got[-1]) and not np.isfinite(want[-1])
+
+
+def test_update_step_consumes_held_chunk_in_fused_call(be):
+    """Before an update step the hooks hold the last chunk back, and the factor
+    update folds and finalizes it in one fused call; the factors equal the
+    closed form of every chunk of the window (two backward passes here)."""
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    lam = 1e-2
+    opt = IFKFAC(model, lr=1e-3, damping=lam, factor_update_freq=1)
+    gen = torch.Generator().manual_seed(5)
+    Xs = [torch.randn(40, 8, generator=gen), torch.randn(30, 8, generator=gen)]
+    acts, grads, hs = _capture(model, Xs[0])
+    seen = {m: ([], []) for m in opt.hooks.linear_layers}
+    opt.zero_grad()
+    for X in Xs:
+        model(X).pow(2).mean().backward()
+        for m in opt.hooks.linear_layers:
+            seen[m][0].append(acts[m].double().numpy())
+            seen[m][1].append(grads[m].double().numpy())
+    for h in hs:
+        h.remove()
+    first = opt.hooks.linear_layers[0]
+    assert opt.hooks._held_X[first] is not None           # the second chunk is held
+    assert be.calls["fold"] == 4                           # the first chunk of each side folded
+    opt.step()
+    assert be.calls["fold_finalize"] == 4 and be.calls["finalize"] == 0
+    for m in opt.hooks.linear_layers:
+        R_X, R_G = opt._factors[m]
+        want_X = O.chol_factor(seen[m][0], 70, lam)
+        want_G = O.chol_factor(seen[m][1], 70, lam)
+        assert np.abs(R_X.double().numpy() - want_X).max() < 1e-5
+        assert np.abs(R_G.double().numpy() - want_G).max() < 1e-5
+    assert opt.hooks._held_X[first] is None and opt.hooks._R_X[first] is None
+
+
+def test_chunks_fold_eagerly_between_updates(be):
+    """factor_update_freq = 3: steps 1 and 2 fold their chunks at once, the chunk
+    of step 3 is held for the fused update; get_factors() folds a held chunk
+    and leaves the running factor as an eager fold would."""
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    opt = IFKFAC(model, lr=1e-3, factor_update_freq=3)
+    X = torch.randn(64, 8, generator=torch.Generator().manual_seed(6))
+    first = opt.hooks.linear_layers[0]
+    for step in (1, 2):
+        opt.zero_grad()
+        model(X).pow(2).mean().backward()
+        assert opt.hooks._held_X[first] is None, step
+        opt.step()
+    opt.zero_grad()
+    model(X).pow(2).mean().backward()
+    assert opt.hooks._held_X[first] is not None
+    f = opt.hooks.get_factors()                            # folds the held chunk
+    assert opt.hooks._held_X[first] is None
+    assert opt.hooks._R_X[first].shape == (8, 8) and opt.hooks._n_rows_X[first] == 3 * 64
+    want = O.chol_factor([X.double().numpy()] * 3, 3 * 64, opt.damping)
+    assert np.abs(f[first][0].double().numpy() - want).max() < 1e-5
+    opt.step()
+    assert first in opt._factors
