@@ -138,12 +138,16 @@ struct LookAhead {
   std::mutex mu;
   hipStream_t s2 = nullptr;
   hipEvent_t ready[2] = {nullptr, nullptr};
-  hipEvent_t far[2] = {nullptr, nullptr};
+  hipEvent_t far[2] = {nullptr, nullptr};   // the next outer block's columns are done
+  hipEvent_t fall[2] = {nullptr, nullptr};  // all of the block's far update is done
+  hipEvent_t done = nullptr;                // everything queued on s2 so far
 };
 
-static LookAhead* look_ahead(int* rc) {
+// One helper stream per (device, calling stream): folds issued on different
+// streams (the two sides of a layer) keep independent far updates.
+static LookAhead* look_ahead(hipStream_t s, int* rc) {
   static std::mutex g_mu;
-  static std::map<int, LookAhead*> g_la;
+  static std::map<std::pair<int, hipStream_t>, LookAhead*> g_la;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     set_error("tsqr_fold: hipGetDevice failed");
@@ -151,13 +155,15 @@ static LookAhead* look_ahead(int* rc) {
     return nullptr;
   }
   std::lock_guard<std::mutex> g(g_mu);
-  LookAhead*& la = g_la[dev];
+  LookAhead*& la = g_la[std::make_pair(dev, s)];
   if (!la) {
     LookAhead* x = new LookAhead();
-    bool ok = hipStreamCreateWithFlags(&x->s2, hipStreamNonBlocking) == hipSuccess;
+    bool ok = hipStreamCreateWithFlags(&x->s2, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreateWithFlags(&x->done, hipEventDisableTiming) == hipSuccess;
     for (int i = 0; i < 2 && ok; ++i)
       ok = hipEventCreateWithFlags(&x->ready[i], hipEventDisableTiming) == hipSuccess &&
-           hipEventCreateWithFlags(&x->far[i], hipEventDisableTiming) == hipSuccess;
+           hipEventCreateWithFlags(&x->far[i], hipEventDisableTiming) == hipSuccess &&
+           hipEventCreateWithFlags(&x->fall[i], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
       set_error("tsqr_fold: cannot create the helper stream or its events");
       *rc = IFK_ERR_HIP;
@@ -239,12 +245,13 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
   int rc = IFK_OK;
   LookAhead* la = nullptr;
   if (std::min<int64_t>(B, r_new) + B < n) {  // some block has columns beyond the next one
-    la = look_ahead(&rc);
+    la = look_ahead(s, &rc);
     if (!la) return rc;
   }
   std::unique_lock<std::mutex> lock;
   if (la) lock = std::unique_lock<std::mutex>(la->mu);
-  int far_pending = -1;  // parity of the last far update not yet joined
+  int far_pending = -1;              // parity of the last far update not yet joined
+  bool fall_pending[2] = {false, false};   // a far update still reads parity buffers
   int k = 0;
   for (int64_t K0 = 0; K0 < r_new; K0 += B, ++k) {
     const int k2 = k & 1;
@@ -252,6 +259,11 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     const int64_t KB = K1 - K0;
     const int64_t pe_o = x_tri ? std::min<int64_t>(p, K1) : p;
     const bool bf = math == MATH_BF16;
+    // block k - 2's far update reads this parity's reflector store
+    if (fall_pending[k2]) {
+      HIPRC(hipStreamWaitEvent(s, la->fall[k2], 0), "tsqr_fold: stream wait failed");
+      fall_pending[k2] = false;
+    }
     if (x_tri) {
       RC(launch_zero(s, w.Yo[k2], B, pe_o, KB));
       if (bf) RC(launch_zero_bf16(s, w.Yob[k2], B, pe_o, KB));
@@ -282,21 +294,27 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     if (K1 >= n) continue;
     RC(outer_prepare(s, math, w, k2, pe_o, KB));
     const int64_t near_hi = std::min<int64_t>(K1 + B, n);
-    if (la && near_hi < n) {
-      // far columns on the helper stream, as soon as T and Y T are ready
-      HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
-      HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
-      RC(outer_apply(la->s2, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, near_hi, n, w.Wf, w.Wfb,
-                     w.split2, FAR_MAX_WGS));
-    }
-    // near columns wait for the previous block's far update, which covers them
+    // near columns wait for the previous block's far update of them
     if (far_pending >= 0) {
       HIPRC(hipStreamWaitEvent(s, la->far[far_pending], 0), "tsqr_fold: stream wait failed");
       far_pending = -1;
     }
     if (la && near_hi < n) {
+      // far columns on the helper stream, as soon as T and Y T are ready:
+      // first the block after next (the next block's near columns, so its
+      // wait above is short), then everything beyond
+      const int64_t mid = std::min<int64_t>(near_hi + B, n);
+      HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
+      HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
+      RC(outer_apply(la->s2, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wf,
+                     w.Wfb, w.split2, FAR_MAX_WGS));
       HIPRC(hipEventRecord(la->far[k2], la->s2), "tsqr_fold: event record failed");
       far_pending = k2;
+      RC(outer_apply(la->s2, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wf, w.Wfb,
+                     w.split2, FAR_MAX_WGS));
+      HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
+      fall_pending[k2] = true;
+      HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
     }
     if (la)
       RC(outer_apply(s, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wn, w.Wnb,
@@ -305,8 +323,7 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
       RC(outer_apply(s, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wf, w.Wfb, w.split,
                      0));
   }
-  if (far_pending >= 0)
-    HIPRC(hipStreamWaitEvent(s, la->far[far_pending], 0), "tsqr_fold: stream wait failed");
+  if (la) HIPRC(hipStreamWaitEvent(s, la->done, 0), "tsqr_fold: stream wait failed");
   return launch_sign_normalize(s, R, ldr, r_new, n);
 }
 

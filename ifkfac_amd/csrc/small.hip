@@ -1,11 +1,13 @@
 // Single-workgroup kernels on b x b (b <= 64) matrices held in LDS, used by the
 // panel factorisation of the streaming fold and by the blocked triangular
 // inverse and Cholesky.  Matrices are fp32, padded to 64 x 64 with the
-// identity beyond b, row stride SLD.  Dense 64-wide work is blocked in 16 x 16
-// tiles: a diagonal tile is factored or inverted in registers by 16 lanes of
-// one wave (values exchanged with v_readlane broadcasts), off-diagonal tiles
-// by LDS products, so a 64 x 64 Cholesky or inverse needs about a dozen
-// workgroup barriers instead of one or more per column.
+// identity beyond b, row stride SLD.  Dense 64-wide work is blocked: diagonal
+// blocks are factored or inverted in registers (the Cholesky leaf redundantly
+// in every lane, the inverse leaf one column per lane), off-diagonal blocks
+// and products run on fp32 MFMA, so a 64 x 64 Cholesky or inverse needs a
+// few workgroup barriers instead of one or more per column.  The second
+// CholeskyQR pass factors a Gram matrix close to the identity with MFMA
+// fixed-point sweeps instead (sm_chol_near_id, sm_inv_near_id).
 //
 // Panel of the fold (columns [c0, c0+b) of the stacked [R; X]):
 //   P = [P_top; X_p], P_top the b x b upper-triangular diagonal block of R,
@@ -33,6 +35,7 @@ constexpr int SB = 64;        // max panel / block width
 constexpr int SLD = SB + 1;   // LDS row stride (floats)
 constexpr int SNT = 256;
 constexpr int TB = 16;        // register tile
+constexpr int TRINV_TMP = 2048; // LDS scratch of sm_trinv64 (floats)
 
 __device__ inline float bcast(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
@@ -121,196 +124,335 @@ __device__ inline float safe_divisor(float d) {
 // thread runs the same steps); mode 1: the pivot rule of cholesky_bf16,
 // max(pivot, 1e-7).
 //
-// Right-looking, blocked by CB = 8 columns.  Every thread factors the 8 x 8
-// diagonal block and inverts it redundantly in registers (no cross-lane
-// traffic on the sequential chain), then owns one column of the block row
-// (U_kr = W_kk^T A_kr with W_kk = U_kk^{-1}) and finally a column of the
-// rank-8 trailing update.  Three barriers per block.
+// Right-looking, blocked by CB columns.  Wave 0 factors each CB x CB diagonal
+// block redundantly in every lane's registers (no cross-lane traffic on the
+// pivot chain), then lane l solves the block-row column o + CB + l against it
+// by forward substitution, so the whole block row is finished by one wave
+// with no barrier.  The rank-CB trailing update runs on fp32 MFMA across the
+// four waves.  Two barriers per block.  CB = 8 measured fastest (the 16 x 16
+// register leaf costs more than the extra barriers it saves).
+template <int CB = 8>
 __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode) {
-  constexpr int CB = 8;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  __shared__ float dg[SB];
-  for (int j = t; j < SB; j += SNT) dg[j] = A[j * SLD + j];
+  __shared__ float dgs[SB];   // diagonal on entry, for the pivot test
+  if (t < SB) dgs[t] = A[t * SLD + t];
   __syncthreads();
   int flag = 0;
+#pragma unroll 1
   for (int kb = 0; kb < SB / CB; ++kb) {
     const int o = kb * CB;
-    float u[CB][CB], w[CB][CB];
-#pragma unroll
-    for (int i = 0; i < CB; ++i)
-#pragma unroll
-      for (int j = i; j < CB; ++j) u[i][j] = A[(o + i) * SLD + o + j];
-    __syncthreads();  // every read of the diagonal block precedes its overwrite
-#pragma unroll
-    for (int k = 0; k < CB; ++k) {
-      const float piv = u[k][k];
-      float pv, rs;
-      if (mode == 0) {
-        if (!(piv > tol * dg[o + k]) || !isfinite(piv)) flag = 1;
-        pv = fmaxf(piv, 1e-30f);
-        rs = __builtin_amdgcn_rsqf(pv);
-        u[k][k] = pv * rs;
-      } else {
-        pv = fmaxf(piv, 1e-7f);
-        u[k][k] = sqrtf(pv);
-        rs = 1.0f / u[k][k];
-      }
-      w[k][k] = rs;
-#pragma unroll
-      for (int j = k + 1; j < CB; ++j) u[k][j] *= rs;
-#pragma unroll
-      for (int i = k + 1; i < CB; ++i)
-#pragma unroll
-        for (int j = i; j < CB; ++j) u[i][j] = fmaf(-u[k][i], u[k][j], u[i][j]);
-    }
-    // W = U_kk^{-1}, column by column (upper triangular)
-#pragma unroll
-    for (int j = 1; j < CB; ++j)
-#pragma unroll
-      for (int i = j - 1; i >= 0; --i) {
-        float s = 0.0f;
-#pragma unroll
-        for (int k = i + 1; k <= j; ++k) s = fmaf(u[i][k], w[k][j], s);
-        w[i][j] = -s * w[i][i];
-      }
-    if (t < CB * CB) {
-      const int i = t / CB, j = t % CB;
-      float v = 0.0f;
-#pragma unroll
-      for (int a = 0; a < CB; ++a)
-#pragma unroll
-        for (int b = a; b < CB; ++b)
-          if (a == i && b == j) v = u[a][b];
-      A[(o + i) * SLD + o + j] = v;
-    }
-    // block row: U[o:o+CB, c] = W^T A[o:o+CB, c]
-    const int c = o + CB + t;
-    if (c < SB) {
-      float x[CB];
-#pragma unroll
-      for (int i = 0; i < CB; ++i) x[i] = A[(o + i) * SLD + c];
+    if (wave == 0) {
+      const int c = o + CB + lane;             // block-row column of this lane
+      float u[CB][CB], x[CB], ri[CB];
 #pragma unroll
       for (int i = 0; i < CB; ++i) {
-        float s = 0.0f;
 #pragma unroll
-        for (int m = 0; m <= i; ++m) s = fmaf(w[m][i], x[m], s);
-        A[(o + i) * SLD + c] = s;
+        for (int j = i; j < CB; ++j) u[i][j] = A[(o + i) * SLD + o + j];
+        x[i] = (c < SB) ? A[(o + i) * SLD + c] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < CB; ++k) {
+        const float piv = u[k][k];
+        float pv, rs;
+        if (mode == 0) {
+          if (!(piv > tol * dgs[o + k]) || !isfinite(piv)) flag = 1;
+          pv = fmaxf(piv, 1e-30f);
+          rs = __builtin_amdgcn_rsqf(pv);
+          u[k][k] = pv * rs;
+        } else {
+          pv = fmaxf(piv, 1e-7f);
+          u[k][k] = sqrtf(pv);
+          rs = 1.0f / u[k][k];
+        }
+        ri[k] = rs;
+#pragma unroll
+        for (int j = k + 1; j < CB; ++j) u[k][j] *= rs;
+#pragma unroll
+        for (int i = k + 1; i < CB; ++i)
+#pragma unroll
+          for (int j = i; j < CB; ++j) u[i][j] = fmaf(-u[k][i], u[k][j], u[i][j]);
+      }
+      // block row: U_kk^T x = a (forward substitution)
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {
+        float acc = x[i];
+#pragma unroll
+        for (int m = 0; m < i; ++m) acc = fmaf(-u[m][i], x[m], acc);
+        x[i] = acc * ri[i];
+      }
+      if (lane < CB) {
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+          float v = 0.0f;
+#pragma unroll
+          for (int j = i; j < CB; ++j)
+            if (j == lane) v = u[i][j];
+          A[(o + i) * SLD + o + lane] = v;
+        }
+      }
+      if (c < SB) {
+#pragma unroll
+        for (int i = 0; i < CB; ++i) A[(o + i) * SLD + c] = x[i];
       }
     }
     __syncthreads();
-    // rank-CB trailing update A[r][c] -= sum_k U[o+k][r] U[o+k][c] for
-    // r, c >= o + CB on fp32 MFMA: wave w takes the 32 x 32 quadrant
-    // (w >> 1, w & 1); lane (l32, h) supplies k = 4 h + s to step s.  The
-    // strictly lower quadrant and quadrants left of the block are skipped;
-    // within a quadrant the lower-triangle results are discarded.
-    {
+    const int lo = o + CB;
+    if (lo < SB) {
       typedef float f32x16 __attribute__((ext_vector_type(16)));
-      const int lo = o + CB;
       const int q0 = (wave >> 1) * 32, q1 = (wave & 1) * 32;
       if (wave != 2 && q0 + 31 >= lo && q1 + 31 >= lo) {
         const int l32 = lane & 31, h = lane >> 5;
-        const int r = q0 + l32, c = q1 + l32;
-        f32x16 d;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+        const int r = q0 + l32, cc = q1 + l32;
+        float av[CB / 2], bv[CB / 2];
 #pragma unroll
         for (int s2 = 0; s2 < CB / 2; ++s2) {
           const int k = o + (CB / 2) * h + s2;
-          const float a = (r >= lo) ? A[k * SLD + r] : 0.0f;
-          const float b = (c >= lo) ? A[k * SLD + c] : 0.0f;
-          d = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, d, 0, 0, 0);
+          av[s2] = (r >= lo) ? A[k * SLD + r] : 0.0f;
+          bv[s2] = (cc >= lo) ? A[k * SLD + cc] : 0.0f;
         }
-        // all reads before any write, so the 16 updates share one LDS latency
         float cur[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) cur[i] = A[(q0 + (i >> 2) * 8 + h * 4 + (i & 3)) * SLD + c];
+        for (int i = 0; i < 16; ++i) cur[i] = A[(q0 + (i >> 2) * 8 + h * 4 + (i & 3)) * SLD + cc];
+        f32x16 dd;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dd[i] = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < CB / 2; ++s2)
+          dd = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s2], bv[s2], dd, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int row = q0 + (i >> 2) * 8 + h * 4 + (i & 3);
-          if (row >= lo && c >= row) A[row * SLD + c] = cur[i] - d[i];
+          if (row >= lo && cc >= row) A[row * SLD + cc] = cur[i] - dd[i];
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
   for (int e = t; e < SB * SB; e += SNT) {
     const int r = e >> 6, cc = e & 63;
     if (r > cc) A[r * SLD + cc] = 0.0f;
   }
-  if (t == 0 && flag && bad) *bad = 1;
+  if (wave == 0 && flag && bad) *bad = 1;
   __syncthreads();
 }
 
 // Z = U^{-1} for a padded 64 x 64 upper-triangular U (Z strict lower = 0).
-// Tmp: LDS scratch of 32 * 32 floats.  With safe set, diagonal divisors follow
-// safe_divisor.
-__device__ __forceinline__ void sm_trinv64(const float* U, float* Z, float* Tmp, bool safe = false) {
+// With safe set, diagonal divisors follow safe_divisor.  Wave w inverts the
+// 16 x 16 diagonal block w (lane j holds
+// column j; back substitution with the row of U read from LDS as a broadcast),
+// then the off-diagonal blocks follow by recursive doubling,
+// Z_12 = -Z_11 U_12 Z_22, at 16 and 32 on fp32 MFMA (32 x 32 tiles, zero
+// padded at level 16).  Tmp: LDS scratch of TRINV_TMP floats.
+__device__ __forceinline__ void sm_trinv64(const float* U, float* Z, float* Tmp,
+                                             bool safe = false) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
   for (int e = t; e < SB * SB; e += SNT) Z[(e >> 6) * SLD + (e & 63)] = 0.0f;
   __syncthreads();
-  // 1) the four diagonal 16 x 16 tiles, one wave each, one lane per column
   {
     const int o = wave * TB;
+    float z[TB], rd[TB];
+#pragma unroll
+    for (int i = 0; i < TB; ++i) {
+      const float dv = U[(o + i) * SLD + o + i];
+      rd[i] = 1.0f / (safe ? safe_divisor(dv) : dv);
+    }
+#pragma unroll
+    for (int i = TB - 1; i >= 0; --i) {
+      float s = (i == lane) ? 1.0f : 0.0f;
+#pragma unroll
+      for (int k = i + 1; k < TB; ++k) s = fmaf(-U[(o + i) * SLD + o + k], z[k], s);
+      z[i] = s * rd[i];
+    }
     if (lane < TB) {
-      float z[TB], rd[TB];
-#pragma unroll
-      for (int i = 0; i < TB; ++i) {
-        const float d = U[(o + i) * SLD + o + i];
-        rd[i] = 1.0f / (safe ? safe_divisor(d) : d);  // independent of the chain below
-      }
-#pragma unroll
-      for (int i = TB - 1; i >= 0; --i) {
-        float s = (i == lane) ? 1.0f : 0.0f;
-#pragma unroll
-        for (int k = i + 1; k < TB; ++k) s = fmaf(-U[(o + i) * SLD + o + k], z[k], s);
-        z[i] = s * rd[i];
-      }
 #pragma unroll
       for (int i = 0; i < TB; ++i) Z[(o + i) * SLD + o + lane] = z[i];
     }
   }
   __syncthreads();
-  // 2) level 16: Z_01 = -Z_00 U_01 Z_11 for tile pairs (0,1) and (2,3)
-  for (int e = t; e < 2 * TB * TB; e += SNT) {
-    const int pr = e / (TB * TB), w = e % (TB * TB);
-    const int i = w / TB, j = w % TB;
-    const int o0 = pr * 2 * TB, o1 = o0 + TB;
-    float s = 0.0f;
+  // level 16: for pair pr (waves 0, 1), blocks (o0, o1) = (32 pr, 32 pr + 16):
+  // Tmp_pr = U[o0:o0+16, o1:o1+16] Z[o1.., o1..], then Z[o0.., o1..] = -Z[o0.., o0..] Tmp_pr.
+  // A 32 x 32 MFMA tile with rows / columns >= 16 and k >= 16 zero.
+  if (wave < 2) {
+    const int o0 = 32 * wave, o1 = o0 + 16;
+    f32x16 d;
 #pragma unroll
-    for (int k = 0; k < TB; ++k) s += U[(o0 + i) * SLD + o1 + k] * Z[(o1 + k) * SLD + o1 + j];
-    Tmp[pr * TB * TB + i * TB + j] = s;
+    for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < 8; ++s2) {
+      const int k = 8 * h + s2;    // 0..15
+      const float a = (l32 < 16) ? U[(o0 + l32) * SLD + o1 + k] : 0.0f;
+      const float b = (l32 < 16) ? Z[(o1 + k) * SLD + o1 + l32] : 0.0f;
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, d, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = (i >> 2) * 8 + h * 4 + (i & 3);
+      if (row < 16 && l32 < 16) Tmp[wave * 256 + row * 16 + l32] = d[i];
+    }
   }
   __syncthreads();
-  for (int e = t; e < 2 * TB * TB; e += SNT) {
-    const int pr = e / (TB * TB), w = e % (TB * TB);
-    const int i = w / TB, j = w % TB;
-    const int o0 = pr * 2 * TB, o1 = o0 + TB;
-    float s = 0.0f;
+  if (wave < 2) {
+    const int o0 = 32 * wave, o1 = o0 + 16;
+    f32x16 d;
 #pragma unroll
-    for (int k = 0; k < TB; ++k) s += Z[(o0 + i) * SLD + o0 + k] * Tmp[pr * TB * TB + k * TB + j];
-    Z[(o0 + i) * SLD + o1 + j] = -s;
+    for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < 8; ++s2) {
+      const int k = 8 * h + s2;
+      const float a = (l32 < 16) ? Z[(o0 + l32) * SLD + o0 + k] : 0.0f;
+      const float b = (l32 < 16) ? Tmp[wave * 256 + k * 16 + l32] : 0.0f;
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, d, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = (i >> 2) * 8 + h * 4 + (i & 3);
+      if (row < 16 && l32 < 16) Z[(o0 + row) * SLD + o1 + l32] = -d[i];
+    }
   }
   __syncthreads();
-  // 3) level 32: Z[0:32, 32:64] = -Z[0:32, 0:32] U[0:32, 32:64] Z[32:64, 32:64]
-  // (the zero lower triangles are part of the unrolled products)
-  for (int e = t; e < 32 * 32; e += SNT) {
-    const int i = e >> 5, j = e & 31;
-    float s = 0.0f;
+  // level 32: Tmp = U[0:32, 32:64] Z[32:64, 32:64], Z[0:32, 32:64] = -Z[0:32, 0:32] Tmp,
+  // one 32 x 32 tile, K = 32 split over two waves (partial sums added in LDS).
+  if (wave < 2) {
+    f32x16 d;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) s = fmaf(U[i * SLD + 32 + k], Z[(32 + k) * SLD + 32 + j], s);
-    Tmp[i * 32 + j] = s;
+    for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < 8; ++s2) {
+      const int k = 16 * wave + 8 * h + s2;   // 0..31
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(U[l32 * SLD + 32 + k], Z[(32 + k) * SLD + 32 + l32],
+                                               d, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = (i >> 2) * 8 + h * 4 + (i & 3);
+      Tmp[wave * 1024 + row * 32 + l32] = d[i];
+    }
   }
   __syncthreads();
-  for (int e = t; e < 32 * 32; e += SNT) {
-    const int i = e >> 5, j = e & 31;
-    float s = 0.0f;
+  f32x16 d2;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) s = fmaf(Z[i * SLD + k], Tmp[k * 32 + j], s);
-    Z[i * SLD + 32 + j] = -s;
+  for (int i = 0; i < 16; ++i) d2[i] = 0.0f;
+  if (wave < 2) {
+#pragma unroll
+    for (int s2 = 0; s2 < 8; ++s2) {
+      const int k = 16 * wave + 8 * h + s2;
+      const float b = Tmp[k * 32 + l32] + Tmp[1024 + k * 32 + l32];
+      d2 = __builtin_amdgcn_mfma_f32_32x32x2f32(Z[l32 * SLD + k], b, d2, 0, 0, 0);
+    }
+  }
+  __syncthreads();   // every read of Tmp precedes the partial sum written below
+  if (wave == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = (i >> 2) * 8 + h * 4 + (i & 3);
+      Tmp[row * 32 + l32] = d2[i];
+    }
   }
   __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = (i >> 2) * 8 + h * 4 + (i & 3);
+      Z[row * SLD + 32 + l32] = -(d2[i] + Tmp[row * 32 + l32]);
+    }
+  }
+  __syncthreads();
+}
+
+// max over the padded 64 x 64 matrix of |A_ij - d * delta_ij|, returned to
+// every thread.  red: LDS scratch of 4 floats.
+__device__ __forceinline__ float sm_maxabs(const float* A, float d, float* red) {
+  const int t = threadIdx.x;
+  float m = 0.0f;
+#pragma unroll
+  for (int q = 0; q < SB * SB / SNT; ++q) {
+    const int e = t + SNT * q, i = e >> 6, j = e & 63;
+    m = fmaxf(m, fabsf(A[i * SLD + j] - (i == j ? d : 0.0f)));
+  }
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __syncthreads();   // red may still be read by a previous call
+  if ((t & 63) == 0) red[t >> 6] = m;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Upper Cholesky factor of a matrix close to the identity, A = I + E with E
+// small (the Gram matrix of the second CholeskyQR pass).  With U = I + F and
+// F upper triangular, U^T U = A is the fixed point
+//   F = up(E - F^T F),  up(X) = strict upper part of X + diag(X) / 2,
+// which contracts at a rate of about 2 ||F|| from F_0 = up(E); each sweep is
+// one 64 x 64 MFMA product.  On success A holds U (strict lower part zero)
+// and the function returns true; when the sweeps have not settled below
+// 2^-26 after maxit (E not small enough) A is left unchanged and it returns
+// false.  F, P: LDS scratch (padded 64 x 64), red: 4 floats.
+__device__ __forceinline__ bool sm_chol_near_id(float* A, float* F, float* P, float* red,
+                                                int maxit) {
+  const int t = threadIdx.x;
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    const float x = A[i * SLD + j] - (i == j ? 1.0f : 0.0f);
+    F[i * SLD + j] = (i < j) ? x : (i == j ? 0.5f * x : 0.0f);
+  }
+  __syncthreads();
+  bool done = false;
+  for (int it = 0; it < maxit && !done; ++it) {
+    sm_gemm64<true, false>(F, F, P, 1.0f, false);      // P = F^T F
+    float dmax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < SB * SB / SNT; ++q) {
+      const int e = t + SNT * q, i = e >> 6, j = e & 63;
+      if (i <= j) {
+        const float x = A[i * SLD + j] - (i == j ? 1.0f : 0.0f) - P[i * SLD + j];
+        const float f = (i < j) ? x : 0.5f * x;
+        dmax = fmaxf(dmax, fabsf(f - F[i * SLD + j]));
+        F[i * SLD + j] = f;
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) dmax = fmaxf(dmax, __shfl_xor(dmax, o));
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = dmax;
+    __syncthreads();
+    done = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) <= 1.4901161e-8f;
+  }
+  if (!done) return false;
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    A[i * SLD + j] = (i <= j) ? F[i * SLD + j] + (i == j ? 1.0f : 0.0f) : 0.0f;
+  }
+  __syncthreads();
+  return true;
+}
+
+// Z = U^{-1} for U = I + F with F upper triangular and small (padded 64 x 64):
+// the Neumann series I - F + F^2 - ..., one MFMA product per term, stopped
+// once a term is below 2^-30 in every entry.  Returns false (Z undefined)
+// when maxit terms do not get there.  Tm, P: LDS scratch, red: 4 floats.
+__device__ __forceinline__ bool sm_inv_near_id(const float* U, float* Z, float* Tm, float* P,
+                                               float* red, int maxit) {
+  const int t = threadIdx.x;
+  // F = U - I into P, Z = I - F, Tm = -F (the current term)
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    const float f = U[i * SLD + j] - (i == j ? 1.0f : 0.0f);
+    P[i * SLD + j] = f;
+    Tm[i * SLD + j] = -f;
+    Z[i * SLD + j] = (i == j ? 1.0f : 0.0f) - f;
+  }
+  __syncthreads();
+  for (int it = 0; it < maxit; ++it) {
+    if (sm_maxabs(Tm, 0.0f, red) <= 9.3132257e-10f) return true;
+    sm_gemm64<false, false>(Tm, P, Tm, -1.0f, false);   // term <- -term F
+    for (int e = t; e < SB * SB; e += SNT) {
+      const int i = e >> 6, j = e & 63;
+      Z[i * SLD + j] += Tm[i * SLD + j];
+    }
+    __syncthreads();
+  }
+  return sm_maxabs(Tm, 0.0f, red) <= 9.3132257e-10f;
 }
 
 // ---------------------------------------------------------------------------
@@ -328,7 +470,7 @@ __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
   __shared__ float sG[SB * SLD];
   __shared__ float sP[SB * SLD];
   __shared__ float sM[SB * SLD];
-  __shared__ float sT[32 * 32];
+  __shared__ float sT[TRINV_TMP];
   __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
   sm_load_pad(sG, G, SB, b, false);
@@ -368,7 +510,7 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
   __shared__ float sM[SB * SLD];
   __shared__ float sX[SB * SLD];
   __shared__ float sN[SB * SLD];
-  __shared__ float sTmp[32 * 32];
+  __shared__ float sTmp[TRINV_TMP];
   __shared__ float sgn[SB];
   __shared__ int bad;
   const int t = threadIdx.x;
@@ -401,8 +543,12 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
   } else {
     sm_load_pad(sQ, Q1, b, b, true, 0.0f);
     sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
-    sm_chol64(sG, 0.25f, &bad, 0);                   // sG = U2
-    sm_trinv64(sG, sM, sTmp);                        // sM = M2
+    // after the first pass sG is I + E with E small: a few MFMA sweeps give U2
+    // and M2; the general Cholesky / inverse are the fallback
+    const bool near = sm_chol_near_id(sG, sX, sM, sgn, 8);   // sG = U2
+    if (!near) sm_chol64(sG, 0.25f, &bad, 0);
+    if (!(near && sm_inv_near_id(sG, sM, sX, sN, sgn, 8)))   // sM = M2
+      sm_trinv64(sG, sM, sTmp);
     sm_gemm64<false, false>(sQ, sM, sX, 1.0f, false);  // sX = Q1f = Q1 M2
     for (int j = t; j < SB; j += SNT) sgn[j] = (sX[j * SLD + j] >= 0.0f) ? -1.0f : 1.0f;
     __syncthreads();
@@ -516,7 +662,7 @@ __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t 
                                                          int nb, float* Z, int64_t ldz, int safe) {
   __shared__ float sU[SB * SLD];
   __shared__ float sZ[SB * SLD];
-  __shared__ float sT[32 * 32];
+  __shared__ float sT[TRINV_TMP];
   const int64_t k0 = (int64_t)blockIdx.x * nb;
   const int b = (int)((n - k0) < nb ? (n - k0) : nb);
   {

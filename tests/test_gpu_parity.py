@@ -159,6 +159,22 @@ def test_fold_rows_summing_to_zero(hip, seed):
         assert np.abs(Rg[:9] - R_or[:9]).max() / np.abs(R_or).max() < 1e-4
 
 
+@pytest.mark.parametrize("kappa,n", [(1e2, 300), (1e3, 300), (1e4, 200), (1e3, 700)])
+def test_fold_ill_conditioned_columns(hip, kappa, n):
+    """Graded and correlated columns (X = U diag(s) V^T D with log-spaced s and a
+    column scaling D over four decades): panels whose first CholeskyQR pass
+    leaves the second-pass Gram far from the identity, or collapses, take the
+    general Cholesky / inverse or the Householder fallback.  R^T R must stay
+    within 4 kappa eps of X^T X."""
+    rng = np.random.default_rng(int(kappa) + n)
+    X = O.kappa_matrix(3 * n, n, kappa, rng) * np.logspace(0, -4, n)[rng.permutation(n)]
+    Xt = torch.from_numpy(X).float().to(DEV)
+    R, r = _fold_chunks(hip, [Xt], n)
+    Ro = O.streaming_tsqr_update(None, Xt.double().cpu().numpy())
+    assert r == n
+    assert _gram_rel(R, Ro) <= 4 * _kappa(Ro) * EPS32
+
+
 def test_fold_nan_gives_nonfinite_flag(hip):
     X = torch.randn(64, 16, device=DEV)
     X[3, 4] = float("nan")
