@@ -230,13 +230,16 @@ def main() -> int:
         a[1] += 1
         a[2] += fl
         a[3] += by
-    # dominant GEMM kernel (family: the 256 x 128 kernel or the 128 x 128 one,
-    # as rocprofv3 reports kernels), timed over all of its launches
-    fam_ms = {1: 0.0, 0: 0.0}
+    # dominant GEMM kernel (family as rocprofv3 reports kernels: 0 gemm_kernel,
+    # 1 gemm_big_kernel, 2 gemm_bb_kernel), timed over all of its launches
+    def family(vid):
+        return 2 if (vid >> 6) & 1 else (vid >> 5) & 1
+    fam_ms = {0: 0.0, 1: 0.0, 2: 0.0}
     for vid, a in per_variant.items():
-        fam_ms[(vid >> 5) & 1] += a[0]
-    big = fam_ms[1] >= fam_ms[0]
-    arm = -3 if big else -4
+        fam_ms[family(vid)] += a[0]
+    fam = max(fam_ms, key=fam_ms.get)
+    arm = {0: -4, 1: -3, 2: -5}[fam]
+    kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel"}[fam]
     torch.cuda.synchronize()
     _lib.check(lib.ifk_profile_begin(arm), "profile_begin")
     torch.cuda.synchronize()
@@ -268,9 +271,9 @@ def main() -> int:
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak_flops,
                 "unit": "TFLOP/s", "frac": round(achieved / peak_flops, 4)}
     roof.update({
-        "traffic": TRAFFIC.get((args.workload, "gemm_big_kernel" if big else "gemm_kernel")),
-        "kernel": ("gemm_big_kernel (256x128x32 bf16 MFMA)" if big
-                   else "gemm_kernel (128x128 MFMA)"),
+        "traffic": TRAFFIC.get((args.workload, kname)),
+        "kernel": kname + {0: " (128x128 MFMA)", 1: " (256x128x32 bf16 MFMA, register staged)",
+                           2: " (256x128x32 bf16 MFMA, direct-to-LDS ring)"}[fam],
         "bf16_share_of_flops": round(bf16_share, 3),
         "launches_per_step": round(len(recs) / args.steps, 1),
         "avg_launch_ms": round(tot_ms / max(len(recs), 1), 4),

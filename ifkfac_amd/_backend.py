@@ -288,7 +288,10 @@ class HipBackend:
 
     def gemm(self, A: torch.Tensor, B: torch.Tensor, trans_a: bool = False,
              trans_b: bool = False, math: int = MATH_F32, alpha: float = 1.0,
-             beta: float = 0.0, C: Optional[torch.Tensor] = None) -> torch.Tensor:
+             beta: float = 0.0, C: Optional[torch.Tensor] = None, tri_a: int = 0,
+             tri_b: int = 0) -> torch.Tensor:
+        """C = alpha op(A) op(B) + beta C; tri_x = 1 / 2 declares op(X) upper /
+        lower triangular (its other triangle is not read)."""
         A, lda, adt = _mat(A, "gemm")
         B, ldb, bdt = _mat(B, "gemm")
         m = A.shape[1] if trans_a else A.shape[0]
@@ -302,9 +305,9 @@ class HipBackend:
         ws = self._ws(self.lib.ifk_gemm_workspace_size(m, n), A.device)
         with torch.cuda.device(A.device):
             rc = self.lib.ifk_gemm(self._stream(A.device), int(math), m, n, k, float(alpha),
-                                   _ptr(A), adt, lda, int(trans_a), _ptr(B), bdt, ldb,
-                                   int(trans_b), float(beta), _ptr(C), C.stride(0), _ptr(ws),
-                                   ws.numel())
+                                   _ptr(A), adt, lda, int(trans_a) | (int(tri_a) << 1),
+                                   _ptr(B), bdt, ldb, int(trans_b) | (int(tri_b) << 1),
+                                   float(beta), _ptr(C), C.stride(0), _ptr(ws), ws.numel())
         _lib.check(rc, "ifk_gemm")
         return C
 

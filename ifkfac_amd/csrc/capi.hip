@@ -209,11 +209,17 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
              size_t workspace_bytes) {
   GUARD(dt_ok(a_dtype) && dt_ok(b_dtype) && math_ok(math), "gemm: bad dtype or math code");
   GUARD(m >= 0 && n >= 0 && k >= 0, "gemm: negative size");
-  GUARD(ldc >= n && (trans_a ? lda >= m : lda >= k) && (trans_b ? ldb >= k : ldb >= n),
+  GUARD(trans_a >= 0 && trans_a < 6 && trans_b >= 0 && trans_b < 6,
+        "gemm: trans flags out of range");
+  const bool ta = trans_a & 1, tb = trans_b & 1;
+  const int tra = trans_a >> 1, trb = trans_b >> 1;   // 0 none, 1 upper, 2 lower
+  GUARD((tra == 0 || m == k) && (trb == 0 || k == n), "gemm: triangular operand not square");
+  GUARD(ldc >= n && (ta ? lda >= m : lda >= k) && (tb ? ldb >= k : ldb >= n),
         "gemm: leading dimension too small");
   GUARD((m == 0 || n == 0) || (C && (k == 0 || (A && B))), "gemm: null pointer");
-  const MatRef a = trans_a ? A_t(A, a_dtype, lda) : A_n(A, a_dtype, lda);
-  const MatRef b = trans_b ? B_t(B, b_dtype, ldb) : B_n(B, b_dtype, ldb);
+  const int tri_code[3] = {TRI_NONE, TRI_UPPER, TRI_LOWER};
+  const MatRef a = ta ? A_t(A, a_dtype, lda, tri_code[tra]) : A_n(A, a_dtype, lda, tri_code[tra]);
+  const MatRef b = tb ? B_t(B, b_dtype, ldb, tri_code[trb]) : B_n(B, b_dtype, ldb, tri_code[trb]);
   SplitScratch sp{(float*)workspace, workspace ? workspace_bytes / sizeof(float) : 0};
   return gemm((hipStream_t)stream, math, m, n, k, alpha, a, b, beta, out_f32(C, ldc), 1, sp);
 }

@@ -79,14 +79,19 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
   return IFK_OK;
 }
 
-// Armed variant: >= 0 one variant id, -2 every launch, -3 every launch of the
-// 256 x 128 kernel (variant bit 5), -4 every launch of the 128 x 128 kernel.
+// Kernel family of a variant id: 0 the 128 x 128 kernel, 1 the 256 x 128
+// register-staged kernel (bit 5), 2 the 256 x 128 direct-to-LDS kernel (bits
+// 5 and 6).
+static int gemm_family(int vid) { return ((vid >> 6) & 1) ? 2 : ((vid >> 5) & 1); }
+
+// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 every
+// launch of family 1 / 0 / 2.
 static ProfRec* prof_slot(int vid) {
   const int a = g_prof_variant;
   if (a == -1) return nullptr;
-  const bool big = (vid >> 5) & 1;
   if (a >= 0 && a != vid) return nullptr;
-  if ((a == -3 && !big) || (a == -4 && big)) return nullptr;
+  const int fam = gemm_family(vid);
+  if ((a == -3 && fam != 1) || (a == -4 && fam != 0) || (a == -5 && fam != 2)) return nullptr;
   std::lock_guard<std::mutex> g(g_prof_mu);
   if (g_prof_used == g_prof.size()) {
     ProfRec r{};
@@ -491,16 +496,26 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   // ones stay on the 128 x 128 engine.
   const bool big = math == MATH_BF16 && M >= 192 && N >= 192 &&
                    (double)M * (double)N * (double)K * batch >= 1e9;
-  const int TM = big ? gemm_big_tile_m() : GBM, TN = big ? gemm_big_tile_n() : GBN;
+  // bf16 operands with K contiguous and 16-byte chunks: the direct-to-LDS
+  // kernel (same 256 x 128 tile and split-K layout as the large-tile one)
+  const bool bb = big && A.dt == DT_BF16 && A.kc && B.dt == DT_BF16 && B.kc && p.vec_a &&
+                  p.vec_b && K % 8 == 0 && A.ld < ((int64_t)1 << 21) &&
+                  B.ld < ((int64_t)1 << 21);
+  const int TM = bb ? gemm_bb_tile_m() : (big ? gemm_big_tile_m() : GBM);
+  const int TN = bb ? gemm_bb_tile_n() : (big ? gemm_big_tile_n() : GBN);
   p.tiles_m = (int)cdiv(M, TM);
   p.tiles_n = (int)cdiv(N, TN);
-  const int BK = big ? gemm_big_bk()
-                     : (math == MATH_BF16 ? GCfg<MATH_BF16>::BK : GCfg<MATH_F32>::BK);
+  const int BK = bb ? gemm_bb_bk()
+                    : big ? gemm_big_bk()
+                          : (math == MATH_BF16 ? GCfg<MATH_BF16>::BK : GCfg<MATH_F32>::BK);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
   const int64_t nkt = cdiv(K, BK);
   int splits = 1;
-  const int64_t full = big ? 160 : 192;  // fewer tiles than this leave CUs idle
-  if (tiles < full && nkt >= 8) {
+  // fewer tiles than this leave CUs idle (the direct-to-LDS kernel runs one
+  // workgroup per CU, the others two)
+  const int64_t full = bb ? 224 : (big ? 160 : 192);
+  // (the direct-to-LDS kernel needs a longer K per split to fill its ring)
+  if (tiles < full && nkt >= (bb ? 32 : 8)) {
     int64_t want = cdiv(2 * full, tiles);
     want = std::min<int64_t>(want, nkt / 4);
     want = std::min<int64_t>(want, 64);
@@ -519,7 +534,8 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     gx = (unsigned)std::min<int64_t>(gx, per_z);
   }
   dim3 grid(gx, 1, (unsigned)(batch * splits));
-  const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | ((big ? 1 : 0) << 5);
+  const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | ((big ? 1 : 0) << 5) |
+                  ((bb ? 1 : 0) << 6);
   ProfRec* pr = prof_slot(vid);
   if (pr) {
     // algorithmic work: 2 M N K (M N K when one operand is triangular), and the
@@ -535,7 +551,8 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     pr->bytes = ((double)M * K * sa + (double)K * N * sb + (double)M * N * cb) * batch;
     hipEventRecord(pr->beg, s);
   }
-  if (big) launch_gemm_big(s, grid, p, A.dt, A.kc, B.dt, B.kc);
+  if (bb) launch_gemm_bb(s, grid, p);
+  else if (big) launch_gemm_big(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   else if (math == MATH_BF16) launch_a<MATH_BF16>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   else launch_a<MATH_F32>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   if (pr) hipEventRecord(pr->end, s);

@@ -1,0 +1,260 @@
+// bf16 x bf16 GEMM for operands whose K index is contiguous in memory:
+//   C = alpha * A B^T + beta * C,  A[m][k] (lda), B[n][k] (ldb), fp32 accumulation,
+// fp32 C and/or an RNE bf16 copy, batched and split-K like the rest of the
+// engine (gemm.h).  This is the kernel of the fold's outer-block updates and
+// of the preconditioner's products.
+//
+// Tile 256 x 256 x 32, eight waves of 128 x 64 (4 x 2 v_mfma_f32_32x32x16_bf16
+// tiles each, 128 fp32 accumulators per lane), one workgroup per CU.  The
+// square tile halves the operand bytes per flop of a 256 x 128 tile, which
+// matters because the kernel is bound by how fast slabs reach LDS, not by
+// LDS bandwidth (no bank conflicts, LDS about 10 % busy).  Operand slabs go
+// from global memory straight into LDS (buffer_load_dwordx4 ... lds), so
+// staging costs no registers and the workgroup keeps a ring of four slabs
+// (128 KB): the loads of slabs k + 1 .. k + 3 are in flight while slab k is
+// multiplied.  Buffer
+// descriptors bound each operand, so rows past M / N read as zero without a
+// branch.  The 64-byte rows of a slab are stored with their four 16-byte
+// chunks XOR-swizzled by bits 2-3 of the row, which makes the MFMA fragment
+// reads (ds_read_b128 of 16 rows x one chunk) bank-conflict free.
+//
+// Requirements checked by the dispatcher: K, lda, ldb multiples of 8 and
+// 16-byte aligned operand pointers (a 16-byte chunk never straddles K).
+// Triangular operands: the K range of a tile is trimmed to the structurally
+// non-zero part, and slabs that cross the diagonal are masked after the
+// fragment reads.
+#include "common.h"
+#include "gemm_impl.h"
+
+namespace ifk {
+
+namespace {
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int BM = 256, BN = 256, BK = 32, NTH = 512, NWAVE = NTH / 64, STAGES = 4;
+constexpr int SLAB_A = BM * BK, SLAB_B = BN * BK;   // bf16 elements per slab (16 KB each)
+constexpr int STAGE = SLAB_A + SLAB_B;
+constexpr int LOADS_A = SLAB_A * 2 / 16 / NTH;      // 16-byte loads per thread (2)
+constexpr int LOADS_B = SLAB_B * 2 / 16 / NTH;      // (2)
+constexpr int LOADS = LOADS_A + LOADS_B;            // per thread per slab pair (4)
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int nrec = bytes > 0x7ffffff0LL ? 0x7ffffff0 : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nrec, 0x00020000);
+}
+
+// Issue the loads of one operand slab (NL * NWAVE * 16 rows from row r0 of
+// the operand view whose buffer descriptor starts at row r0, K chunk kt) into
+// LDS S.  Wave w, instruction i fills slots (NWAVE i + w) * 64 .. + 63; lane
+// l's slot s = (row, q) holds the logical chunk q ^ ((row >> 2) & 3) of that
+// row.
+template <int NL>
+__device__ __forceinline__ void issue_slab(__amdgpu_buffer_rsrc_t rs, bf16_t* S, int64_t ld,
+                                           int64_t kt, int64_t kmax) {
+  // the LDS destination (M0) must be wave-uniform: take the wave index from
+  // a scalar register so the compiler knows it
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int slot0 = (i * NWAVE + wave) * 64;
+    const int slot = slot0 + lane;
+    const int row = slot >> 2, q = slot & 3;
+    const int c = q ^ ((row >> 2) & 3);
+    const int64_t k = kt * BK + 8 * c;
+    // chunks at or past K read as zero (the offset is beyond the buffer)
+    const unsigned off = (k < kmax) ? (unsigned)(((int64_t)row * ld + k) * 2) : 0x80000000u;
+    lds_void* dst = (lds_void*)(uintptr_t)(S + slot0 * 8);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, off, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ bf16x8_t frag(const bf16_t* S, int row, int c) {
+  return *(const bf16x8_t*)(S + row * BK + ((c ^ ((row >> 2) & 3)) << 3));
+}
+
+// Zero the entries of an 8-element fragment (row index mn, k = k0 .. k0 + 7)
+// that lie in the structurally zero triangle: op(X)[mn][k] for A-side (ISA)
+// or op(X)[k][mn] for B-side operands.
+template <bool ISA>
+__device__ __forceinline__ bf16x8_t mask_frag(bf16x8_t v, int tri, int64_t mn, int64_t k0) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t k = k0 + e;
+    bool zero;
+    if (ISA) zero = (tri == TRI_UPPER) ? (k < mn) : (k > mn);
+    else zero = (tri == TRI_UPPER) ? (k > mn) : (k < mn);
+    if (zero) v[e] = (__bf16)0.0f;
+  }
+  return v;
+}
+
+// Whether the diagonal k == mn passes through the slab [mn0, mn0 + ext) x
+// [k0, k0 + 32) of a triangular operand (else the slab is all structural
+// non-zeros: the K range of the tile already excludes the all-zero slabs).
+__device__ __forceinline__ bool slab_crosses(int tri, int64_t mn0, int ext, int64_t k0) {
+  if (tri == TRI_NONE) return false;
+  return k0 < mn0 + ext && k0 + BK > mn0;
+}
+
+// Wait until the loads of this slab have landed, leaving those of the
+// `ahead` later slabs already issued (0, 1 or 2: LOADS each) in flight.
+__device__ __forceinline__ void wait_vm(int ahead) {
+  static_assert(LOADS == 4, "vmcnt immediates below");
+  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x0f78);     // vmcnt(8)
+  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0f74); // vmcnt(4)
+  else __builtin_amdgcn_s_waitcnt(0x0f70);                // vmcnt(0)
+}
+
+__device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* smem) {
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 2, wn = wave & 3;      // 2 x 4 waves of 128 x 64
+  const int l32 = lane & 31, h = lane >> 5;
+  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
+  const int z = blockIdx.z;
+  const int bidx = z / p.splits, split = z % p.splits;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+  int64_t klo = 0, khi = p.K;
+  if (p.tria == TRI_UPPER) klo = max(klo, m0);
+  if (p.tria == TRI_LOWER) khi = min(khi, m0 + BM);
+  if (p.trib == TRI_UPPER) khi = min(khi, n0 + BN);
+  if (p.trib == TRI_LOWER) klo = max(klo, n0);
+  const int64_t kt_lo = klo / BK;
+  const int64_t nkt = khi > kt_lo * BK ? (khi - kt_lo * BK + BK - 1) / BK : 0;
+  const int64_t per = (nkt + p.splits - 1) / p.splits;
+  const int64_t kt0 = kt_lo + (int64_t)split * per;
+  const int64_t kt1 = min(kt_lo + nkt, kt0 + per);
+  const int n_it = (int)max((int64_t)0, kt1 - kt0);
+
+  const bf16_t* Ab = (const bf16_t*)p.A + (size_t)bidx * p.bsa + m0 * p.lda;
+  const bf16_t* Bb = (const bf16_t*)p.B + (size_t)bidx * p.bsb + n0 * p.ldb;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ab, (p.M - m0) * p.lda * 2);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb, (p.N - n0) * p.ldb * 2);
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // prologue: slabs 0 .. STAGES - 2
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) {
+    if (s < n_it) {
+      issue_slab<LOADS_A>(ra, smem + s * STAGE, p.lda, kt0 + s, p.K);
+      issue_slab<LOADS_B>(rb, smem + s * STAGE + SLAB_A, p.ldb, kt0 + s, p.K);
+    }
+  }
+  for (int it = 0; it < n_it; ++it) {
+    wait_vm(min(n_it - 1 - it, STAGES - 2));    // this slab landed (later ones may fly)
+    // every wave's loads of this slab are in LDS and slab it - 1 is free
+    // again.  A bare s_barrier: __syncthreads() would also wait for the next
+    // slab's loads (its fence drains vmcnt).
+    __builtin_amdgcn_s_barrier();
+    if (it + STAGES - 1 < n_it) {
+      const int sn = (it + STAGES - 1) % STAGES;
+      issue_slab<LOADS_A>(ra, smem + sn * STAGE, p.lda, kt0 + it + STAGES - 1, p.K);
+      issue_slab<LOADS_B>(rb, smem + sn * STAGE + SLAB_A, p.ldb, kt0 + it + STAGES - 1, p.K);
+    }
+    const bf16_t* As = smem + (it % STAGES) * STAGE;
+    const bf16_t* Bs = As + SLAB_A;
+    const int64_t kbase = (kt0 + it) * BK;
+    const bool xa = slab_crosses(p.tria, m0, BM, kbase);
+    const bool xb = slab_crosses(p.trib, n0, BN, kbase);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8_t af[4], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = frag(As, wm * 128 + i * 32 + l32, 2 * ks + h);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bfr[j] = frag(Bs, wn * 64 + j * 32 + l32, 2 * ks + h);
+      if (xa) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          af[i] = mask_frag<true>(af[i], p.tria, m0 + wm * 128 + i * 32 + l32, kbase + ks * 16 + h * 8);
+      }
+      if (xb) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          bfr[j] = mask_frag<false>(bfr[j], p.trib, n0 + wn * 64 + j * 32 + l32, kbase + ks * 16 + h * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // acc[i][j][r]: row (r / 4) * 8 + h * 4 + r % 4, column l32 of 32 x 32 tile (i, j)
+  if (p.splits > 1) {
+    float* P = p.part + ((size_t)(bidx * p.splits + split)) * (size_t)p.M * (size_t)p.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          const int64_t col = n0 + wn * 64 + j * 32 + l32;
+          if (row < p.M && col < p.N) P[row * p.N + col] = acc[i][j][r];
+        }
+    return;
+  }
+  float* Cp = p.C ? p.C + (size_t)bidx * p.bsc : nullptr;
+  bf16_t* Cbp = p.Cb ? p.Cb + (size_t)bidx * p.bscb : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + wn * 64 + j * 32 + l32;
+      float old[16];
+      if (p.beta != 0.0f) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          old[r] = (row < p.M && col < p.N) ? Cp[row * p.ldc + col] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        if (row < p.M && col < p.N) {
+          float v = p.alpha * acc[i][j][r];
+          if (p.beta != 0.0f) v += p.beta * old[r];
+          if (Cp) Cp[row * p.ldc + col] = v;
+          if (Cbp) Cbp[row * p.ldcb + col] = f32_to_bf16(v);
+        }
+      }
+    }
+}
+
+// Tiles visited grid-stride (a launch may use fewer workgroups than tiles).
+__global__ __launch_bounds__(NTH, 1) void gemm_bb_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem_bb[STAGES * STAGE];   // 128 KB
+  const int tiles = p.tiles_m * p.tiles_n;
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    bb_tile(p, tile, smem_bb);
+    __syncthreads();   // the LDS ring is reused by the next tile
+  }
+}
+
+}  // namespace
+
+int gemm_bb_tile_m() { return BM; }
+int gemm_bb_tile_n() { return BN; }
+int gemm_bb_bk() { return BK; }
+
+void launch_gemm_bb(hipStream_t s, dim3 grid, const GemmParams& p) {
+  hipLaunchKernelGGL(gemm_bb_kernel, grid, dim3(NTH), 0, s, p);
+}
+
+}  // namespace ifk

@@ -25,4 +25,12 @@ int gemm_big_bk();
 void launch_gemm_big(hipStream_t s, dim3 grid, const GemmParams& p, int adt, bool akc, int bdt,
                      bool bkc);
 
+// 256 x 256 x 32 bf16 x bf16 kernel for K-contiguous operands with a
+// four-slab direct-to-LDS ring (gemm_bb.hip); grid.x = tiles, grid.z =
+// batch * splits.
+int gemm_bb_tile_m();
+int gemm_bb_tile_n();
+int gemm_bb_bk();
+void launch_gemm_bb(hipStream_t s, dim3 grid, const GemmParams& p);
+
 }  // namespace ifk

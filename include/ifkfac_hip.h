@@ -194,8 +194,9 @@ int ifk_inv_spd(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda
 
 /*
  * General MFMA matrix product C = alpha op(A) op(B) + beta C, exposed for
- * tests and for callers that compose the path themselves.  trans_a/trans_b
- * select op(X) = X^T; C is fp32.
+ * tests and for callers that compose the path themselves.  Bit 0 of
+ * trans_a/trans_b selects op(X) = X^T; bits 1-2 declare op(X) upper (1) or
+ * lower (2) triangular, whose other triangle is then never read.  C is fp32.
  */
 size_t ifk_gemm_workspace_size(int64_t m, int64_t n);
 int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alpha, const void* A,
@@ -206,12 +207,13 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
 /*
  * Measurement support (no counterpart in the reference; used by bench.py).
  * ifk_profile_begin(v) arms the GEMM launch profiler for GEMM variant v
- * (v = (large_tile << 5) | (math << 4) | (a_dtype << 3) | (a_k_contiguous << 2)
- * | (b_dtype << 1) | b_k_contiguous; large_tile marks the 256 x 128 kernel
- * gemm_big_kernel, else gemm_kernel), for every variant with v = -2, for every
- * launch of gemm_big_kernel with v = -3 or of gemm_kernel with v = -4;
- * v = -1 disarms.  Each armed launch is bracketed by two HIP events on its
- * own stream.
+ * (v = (direct << 6) | (large_tile << 5) | (math << 4) | (a_dtype << 3) |
+ * (a_k_contiguous << 2) | (b_dtype << 1) | b_k_contiguous; large_tile marks the
+ * 256 x 128 kernels, direct the one that loads operands straight into LDS,
+ * gemm_bb_kernel, large_tile alone gemm_big_kernel, neither gemm_kernel), for
+ * every variant with v = -2, for every launch of gemm_big_kernel with v = -3,
+ * of gemm_kernel with v = -4, of gemm_bb_kernel with v = -5; v = -1 disarms.
+ * Each armed launch is bracketed by two HIP events on its own stream.
  * ifk_profile_end() disarms, waits for the events and returns the number of
  * launches recorded; ifk_profile_get(i, ...) returns launch i's variant,
  * duration (ms), algorithmic flops and bytes, and its m, n, k.

@@ -79,6 +79,45 @@ def test_gemm_engine_large_tiles(hip, adt, ta, tb, m, n, k):
     assert _rel(C, ref.cpu().numpy()) < 2e-6
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 2560, 512), (600, 520, 4096), (1000, 700, 2048),
+                                   (512, 512, 8192), (256, 384, 16384)])
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_gemm_direct_lds_kernel(hip, m, n, k, beta):
+    """bf16 operands with K contiguous take the direct-to-LDS kernel: ragged M
+    and N (rows past the operand read as zero through the buffer bounds),
+    split-K for few tiles, alpha / beta, against an fp64 product."""
+    g = torch.Generator(device=DEV).manual_seed(m + 5 * n + 3 * k)
+    A = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    B = torch.randn(n, k, device=DEV, generator=g).to(torch.bfloat16)
+    C0 = torch.randn(m, n, device=DEV, generator=g)
+    ref = -0.5 * (A.double() @ B.double().t()) + beta * C0.double()
+    C = hip.gemm(A, B, False, True, 1, -0.5, beta, C0.clone())
+    assert _rel(C, ref.cpu().numpy()) < 2e-6
+
+
+@pytest.mark.parametrize("tri", ["upper_a", "lower_b"])
+def test_gemm_direct_lds_triangular(hip, tri):
+    """Triangular bf16 operands (as in the preconditioner) through the
+    direct-to-LDS kernel: the stored zero triangle is filled with garbage,
+    which the kernel must ignore."""
+    n = 1280
+    g = torch.Generator(device=DEV).manual_seed(42)
+    Z = torch.randn(n, n, device=DEV, generator=g)
+    G = torch.randn(1100, n, device=DEV, generator=g).to(torch.bfloat16)
+    Zt = torch.triu(Z).to(torch.bfloat16)
+    noisy = (Zt.float() + torch.tril(torch.randn(n, n, device=DEV, generator=g), -1)).to(
+        torch.bfloat16)
+    if tri == "upper_a":
+        # C = U G^T: op(A) = U upper triangular, B = G stored (n_rows x K)
+        ref = Zt.double() @ G.double().t()
+        C = hip.gemm(noisy, G, False, True, 1, tri_a=1)
+    else:
+        # C = G U^T: op(B) = U^T lower triangular, given as B[n][k] = U
+        ref = G.double() @ Zt.double().t()
+        C = hip.gemm(G, noisy, False, True, 1, tri_b=2)
+    assert _rel(C, ref.cpu().numpy()) < 2e-6
+
+
 # --------------------------------------------------------------------------- fold
 
 
