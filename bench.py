@@ -32,6 +32,20 @@ import os
 import sys
 import time
 
+# HIP maps streams onto a pool of hardware queues (GPU_MAX_HW_QUEUES, 4 by
+# default), and streams that share a queue run in submission order.  The step
+# runs on five streams: the main one, one per factor side, and one look-ahead
+# helper per side; with 4 queues the two helpers share one and the output
+# side's far updates wait behind the input side's.  HIP reads the variable
+# when it initialises, so it is raised here, before torch touches the GPU
+# (a larger setting is kept).
+try:
+    _queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "0"))
+except ValueError:
+    _queues = 0
+if _queues < 8:
+    os.environ["GPU_MAX_HW_QUEUES"] = "8"
+
 METRIC = "ms per factor-update + precond step per layer; bf16 TFLOP/s vs MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_F32_TFLOPS = 157.3
@@ -167,13 +181,15 @@ def main() -> int:
             # input and output sides are independent, as in IFKFAC._update_factors
             return run_pair(dev,
                             lambda: be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16),
-                            lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16))
+                            lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16),
+                            b_first=n_out > n_in)
         # RawActivationHooks._collect_factors(consume=True) of the update step
         return run_pair(dev,
                         lambda: be.fold_finalize(None, 0, X, scale, lam, torch.bfloat16,
                                                  MATH_BF16),
                         lambda: be.fold_finalize(None, 0, D, scale, lam, torch.bfloat16,
-                                                 MATH_BF16))
+                                                 MATH_BF16),
+                        b_first=n_out > n_in)
 
     def step(first: bool, events=None):
         k = [0]
@@ -186,7 +202,7 @@ def main() -> int:
         (FX, _), (FG, _) = factors(mark)
         mark()
         ZX, ZG = run_pair(dev, lambda: be.tri_inverse(FX, MATH_BF16),
-                          lambda: be.tri_inverse(FG, MATH_BF16))
+                          lambda: be.tri_inverse(FG, MATH_BF16), b_first=n_out > n_in)
         mark()
         nat = be.precondition_apply(grad, ZX, ZG, MATH_BF16)
         mark()
@@ -273,7 +289,7 @@ def main() -> int:
     roof.update({
         "traffic": TRAFFIC.get((args.workload, kname)),
         "kernel": kname + {0: " (128x128 MFMA)", 1: " (256x128x32 bf16 MFMA, register staged)",
-                           2: " (256x128x32 bf16 MFMA, direct-to-LDS ring)"}[fam],
+                           2: " (256x256x32 bf16 MFMA, direct-to-LDS ring)"}[fam],
         "bf16_share_of_flops": round(bf16_share, 3),
         "launches_per_step": round(len(recs) / args.steps, 1),
         "avg_launch_ms": round(tot_ms / max(len(recs), 1), 4),

@@ -350,21 +350,29 @@ def _tensors(obj):
             yield from _tensors(o)
 
 
-def run_pair(device: torch.device, fa, fb):
+def run_pair(device: torch.device, fa, fb, b_first: bool = False):
     """Run fa() and fb() concurrently on two side streams of `device`, after the
     current stream's pending work; the current stream then waits for both.
-    Used for the independent input-side and output-side factor work (finalize,
-    triangular inverse).  On a CPU device the two calls simply run in order."""
+    Used for the independent input-side and output-side factor work (fold +
+    finalize, triangular inverse).  b_first enqueues fb() before fa() (the
+    longer call first, so its GPU work starts while the host enqueues the
+    other).  On a CPU device the two calls simply run in order."""
     if device.type != "cuda":
         return fa(), fb()
     main = torch.cuda.current_stream(device)
     s1, s2 = _side_streams(device)
     s1.wait_stream(main)
     s2.wait_stream(main)
-    with torch.cuda.stream(s1):
-        ra = fa()
-    with torch.cuda.stream(s2):
-        rb = fb()
+    if b_first:
+        with torch.cuda.stream(s2):
+            rb = fb()
+        with torch.cuda.stream(s1):
+            ra = fa()
+    else:
+        with torch.cuda.stream(s1):
+            ra = fa()
+        with torch.cuda.stream(s2):
+            rb = fb()
     main.wait_stream(s1)
     main.wait_stream(s2)
     for t in list(_tensors(ra)) + list(_tensors(rb)):

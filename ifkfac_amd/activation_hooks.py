@@ -286,12 +286,14 @@ class RawActivationHooks(GramMatrixEstimator):
                     raise IFKFACRankError(
                         f"Layer {module}: accumulated {rows_G} rows for δ, "
                         f"but need >= n_out={R_G_raw.shape[1]} (batched mode).")
-            # the two sides are independent: finalize them concurrently
+            # the two sides are independent: finalize them concurrently, the
+            # wider (longer) one enqueued first
             dev = (R_X_raw if R_X_raw is not None else chunk_X).device
             (R_X, fX), (R_G, fG) = run_pair(
                 dev,
                 lambda: self._damped("X", module, rows_X, out_dtype),
-                lambda: self._damped("G", module, rows_G, out_dtype))
+                lambda: self._damped("G", module, rows_G, out_dtype),
+                b_first=n_G > n_X)
             factors[module] = (R_X, R_G)
             flags[module] = (fX, fG)
         return factors, flags

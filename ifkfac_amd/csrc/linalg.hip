@@ -71,6 +71,8 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
 
 struct FoldWs {
   float* C;       // n x p: the chunk, transposed (CT = C^T; see fold_core)
+  bf16_t* Cb;     // n x p: RNE bf16 shadow of C for bf16 arithmetic (the rows of
+                  // columns beyond the current outer block are kept current)
   float* Yo[2];   // p x OUTER_B: reflector X parts of an outer block (by block parity)
   float* Yto[2];  // OUTER_B x p: (Y T)^T of an outer block (fp32 arithmetic)
   bf16_t* Yob[2];   // bf16 copies of Yo and (Y T)^T for bf16 arithmetic (the
@@ -100,6 +102,7 @@ struct FoldWs {
 static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   const int64_t b = PANEL_B, B = OUTER_B;
   w.C = need_C ? a.take<float>((size_t)p * n) : nullptr;
+  w.Cb = need_C ? a.take<bf16_t>((size_t)p * n) : nullptr;
   for (int i = 0; i < 2; ++i) {
     w.Yo[i] = a.take<float>((size_t)p * B);
     w.Yto[i] = a.take<float>((size_t)p * B);
@@ -208,23 +211,26 @@ static int outer_prepare(hipStream_t s, int math, FoldWs& w, int k2, int64_t pe,
 // [c_lo, c_hi) of the transposed working matrix CT (ld ldc):
 //   W^T = CT_cols (Y T) + R_blk^T T,  R_blk -= (W^T)^T,  CT_cols -= W^T Y^T
 // The two large products read K-contiguous operands only.  W^T is nt x KB.
-static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, int64_t ldc,
-                       int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1, int64_t c_lo,
-                       int64_t c_hi, float* W, bf16_t* Wb, SplitScratch sp, int max_wgs) {
+static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
+                       int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1,
+                       int64_t c_lo, int64_t c_hi, float* W, bf16_t* Wb, SplitScratch sp,
+                       int max_wgs) {
   const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
   if (nt <= 0) return IFK_OK;
   const bool bf = math == MATH_BF16;
   float* Rb = R + K0 * ldr + c_lo;
   float* Cr = CT + c_lo * ldc;
+  bf16_t* Crb = CTb ? CTb + c_lo * ldc : nullptr;   // bf16 shadow (bf16 arithmetic)
   const MatRef YtoTB = bf ? B_t(w.Ytob[k2], DT_BF16, pe) : B_t(w.Yto[k2], DT_F32, pe);
-  RC(gemm(s, math, nt, KB, pe, 1.0f, A_n(Cr, DT_F32, ldc), YtoTB, 0.0f, out_f32(W, KB), 1, sp,
-          max_wgs));
+  const MatRef CA = Crb ? A_n(Crb, DT_BF16, ldc) : A_n(Cr, DT_F32, ldc);
+  RC(gemm(s, math, nt, KB, pe, 1.0f, CA, YtoTB, 0.0f, out_f32(W, KB), 1, sp, max_wgs));
   RC(gemm(s, math, nt, KB, KB, 1.0f, A_t(Rb, DT_F32, ldr), B_n(w.To[k2], DT_F32, KB, TRI_UPPER),
           1.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB), 1, sp));
   RC(launch_sub_transposed(s, Rb, ldr, W, KB, KB, nt));
   const MatRef WA = bf ? A_n(Wb, DT_BF16, KB) : A_n(W, DT_F32, KB);
   const MatRef YoBt = bf ? B_t(w.Yob[k2], DT_BF16, B) : B_t(w.Yo[k2], DT_F32, B);
-  return gemm(s, math, nt, pe, KB, -1.0f, WA, YoBt, 1.0f, out_f32(Cr, ldc), 1, sp, max_wgs);
+  return gemm(s, math, nt, pe, KB, -1.0f, WA, YoBt, 1.0f,
+              Crb ? out_both(Cr, ldc, Crb, ldc) : out_f32(Cr, ldc), 1, sp, max_wgs);
 }
 
 // Core of the fold on the transposed fp32 working copy CT = C^T (n x p, row
@@ -251,6 +257,12 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
   }
   std::unique_lock<std::mutex> lock;
   if (la) lock = std::unique_lock<std::mutex>(la->mu);
+  // bf16 arithmetic: the outer-block products read a bf16 shadow of C (the
+  // exact values their operand staging would round to), which the C updates
+  // keep current; it is seeded here once
+  bf16_t* Cb = (math == MATH_BF16 && w.Cb && std::min<int64_t>(OUTER_B, r_new) < n) ? w.Cb
+                                                                                   : nullptr;
+  if (Cb) RC(launch_cast(s, C, ldc, n, p, Cb, DT_BF16, ldc));
   int far_pending = -1;              // parity of the last far update not yet joined
   bool fall_pending[2] = {false, false};   // a far update still reads parity buffers
   int k = 0;
@@ -307,21 +319,21 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
       const int64_t mid = std::min<int64_t>(near_hi + B, n);
       HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
       HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
-      RC(outer_apply(la->s2, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wf,
+      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wf,
                      w.Wfb, w.split2, FAR_MAX_WGS));
       HIPRC(hipEventRecord(la->far[k2], la->s2), "tsqr_fold: event record failed");
       far_pending = k2;
-      RC(outer_apply(la->s2, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wf, w.Wfb,
+      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wf, w.Wfb,
                      w.split2, FAR_MAX_WGS));
       HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
       fall_pending[k2] = true;
       HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
     }
     if (la)
-      RC(outer_apply(s, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wn, w.Wnb,
+      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wn, w.Wnb,
                      w.split, 0));
     else
-      RC(outer_apply(s, math, w, k2, C, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wf, w.Wfb, w.split,
+      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wf, w.Wfb, w.split,
                      0));
   }
   if (la) HIPRC(hipStreamWaitEvent(s, la->done, 0), "tsqr_fold: stream wait failed");

@@ -163,7 +163,8 @@ class IFKFAC(torch.optim.Optimizer):
             m = solve_math_for(R_X.dtype)
             self._inverses[module] = run_pair(R_X.device,
                                               lambda R=R_X: be.tri_inverse(R, m),
-                                              lambda R=R_G: be.tri_inverse(R, m))
+                                              lambda R=R_G: be.tri_inverse(R, m),
+                                              b_first=R_G.shape[0] > R_X.shape[0])
         self.timing["factor_compute"].append(time.perf_counter() - t0)
 
     # ------------------------------------------------------------------ apply
