@@ -247,15 +247,19 @@ def main() -> int:
         a[2] += fl
         a[3] += by
     # dominant GEMM kernel (family as rocprofv3 reports kernels: 0 gemm_kernel,
-    # 1 gemm_big_kernel, 2 gemm_bb_kernel), timed over all of its launches
+    # 1 gemm_big_kernel, 2 / 3 gemm_bb_kernel with its 256 / 128 tile), timed
+    # over all of its launches
     def family(vid):
-        return 2 if (vid >> 6) & 1 else (vid >> 5) & 1
-    fam_ms = {0: 0.0, 1: 0.0, 2: 0.0}
+        if (vid >> 6) & 1:
+            return 3 if (vid >> 7) & 1 else 2
+        return (vid >> 5) & 1
+    fam_ms = {0: 0.0, 1: 0.0, 2: 0.0, 3: 0.0}
     for vid, a in per_variant.items():
         fam_ms[family(vid)] += a[0]
     fam = max(fam_ms, key=fam_ms.get)
-    arm = {0: -4, 1: -3, 2: -5}[fam]
-    kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel"}[fam]
+    arm = {0: -4, 1: -3, 2: -5, 3: -6}[fam]
+    kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1>>",
+             3: "gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2>>"}[fam]
     torch.cuda.synchronize()
     _lib.check(lib.ifk_profile_begin(arm), "profile_begin")
     torch.cuda.synchronize()
@@ -289,7 +293,8 @@ def main() -> int:
     roof.update({
         "traffic": TRAFFIC.get((args.workload, kname)),
         "kernel": kname + {0: " (128x128 MFMA)", 1: " (256x128x32 bf16 MFMA, register staged)",
-                           2: " (256x256x32 bf16 MFMA, direct-to-LDS ring)"}[fam],
+                           2: " (256x256x32 bf16 MFMA, direct-to-LDS ring)",
+                           3: " (128x128x32 bf16 MFMA, direct-to-LDS ring)"}[fam],
         "bf16_share_of_flops": round(bf16_share, 3),
         "launches_per_step": round(len(recs) / args.steps, 1),
         "avg_launch_ms": round(tot_ms / max(len(recs), 1), 4),

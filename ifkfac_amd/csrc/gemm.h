@@ -65,9 +65,10 @@ struct SplitScratch {
 };
 
 // Launch profiler (see gemm.hip).  variant: gemm_variant_id() (bit 5 set for
-// the 256 x 128 kernels, bit 6 as well for the direct-to-LDS one), -2 all,
-// -3 all of the register-staged 256 x 128 kernel, -4 all of the 128 x 128
-// kernel, -5 all of the direct-to-LDS kernel, -1 off.
+// the large-tile bf16 kernels, bit 6 as well for the direct-to-LDS one, bit 7
+// for its 128 x 128 tile), -2 all, -3 all of the register-staged 256 x 128
+// kernel, -4 all of the 128 x 128 kernel, -5 / -6 all of the direct-to-LDS
+// kernel with its 256 / 128 tile, -1 off.
 int gemm_variant_id(int math, int adt, bool akc, int bdt, bool bkc);
 int profile_begin(int variant);
 int profile_end(int64_t* n_launches);

@@ -80,18 +80,23 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
 }
 
 // Kernel family of a variant id: 0 the 128 x 128 kernel, 1 the 256 x 128
-// register-staged kernel (bit 5), 2 the 256 x 128 direct-to-LDS kernel (bits
-// 5 and 6).
-static int gemm_family(int vid) { return ((vid >> 6) & 1) ? 2 : ((vid >> 5) & 1); }
+// register-staged kernel (bit 5), 2 / 3 the direct-to-LDS kernel with its 256
+// / 128 tile (bits 5 and 6, and bit 7 for the 128 tile).
+static int gemm_family(int vid) {
+  if ((vid >> 6) & 1) return ((vid >> 7) & 1) ? 3 : 2;
+  return (vid >> 5) & 1;
+}
 
-// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 every
-// launch of family 1 / 0 / 2.
+// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 / -6
+// every launch of family 1 / 0 / 2 / 3.
 static ProfRec* prof_slot(int vid) {
   const int a = g_prof_variant;
   if (a == -1) return nullptr;
   if (a >= 0 && a != vid) return nullptr;
   const int fam = gemm_family(vid);
-  if ((a == -3 && fam != 1) || (a == -4 && fam != 0) || (a == -5 && fam != 2)) return nullptr;
+  if ((a == -3 && fam != 1) || (a == -4 && fam != 0) || (a == -5 && fam != 2) ||
+      (a == -6 && fam != 3))
+    return nullptr;
   std::lock_guard<std::mutex> g(g_prof_mu);
   if (g_prof_used == g_prof.size()) {
     ProfRec r{};
@@ -497,31 +502,62 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   const bool big = math == MATH_BF16 && M >= 192 && N >= 192 &&
                    (double)M * (double)N * (double)K * batch >= 1e9;
   // bf16 operands with K contiguous and 16-byte chunks: the direct-to-LDS
-  // kernel (same 256 x 128 tile and split-K layout as the large-tile one)
+  // kernel, with its 256 tile when that alone gives most CUs a tile, else
+  // with its 128 tile (four times the tiles, a quarter of the split-K
+  // partials per tile)
   const bool bb = big && A.dt == DT_BF16 && A.kc && B.dt == DT_BF16 && B.kc && p.vec_a &&
                   p.vec_b && K % 8 == 0 && A.ld < ((int64_t)1 << 21) &&
                   B.ld < ((int64_t)1 << 21);
-  const int TM = bb ? gemm_bb_tile_m() : (big ? gemm_big_tile_m() : GBM);
-  const int TN = bb ? gemm_bb_tile_n() : (big ? gemm_big_tile_n() : GBN);
+  // split-K factor for a tile of TM x TN with BK-deep slabs
+  auto split_for = [&](int TM, int TN, int BK, bool mid_tile) -> int {
+    const int64_t tiles = cdiv(M, (int64_t)TM) * cdiv(N, (int64_t)TN) * batch;
+    const int64_t nkt = cdiv(K, (int64_t)BK);
+    int64_t want = 1;
+    if (mid_tile) {
+      // one workgroup per CU, at least eight K slabs per split
+      if (tiles < 256 && nkt >= 16) want = std::min<int64_t>(cdiv(256, tiles), nkt / 8);
+    } else {
+      // fewer tiles than this leave CUs idle (the direct-to-LDS kernel runs
+      // one workgroup per CU, the others two); the direct-to-LDS kernel needs
+      // a longer K per split to fill its ring
+      const int64_t full = bb ? 224 : (big ? 160 : 192);
+      if (tiles < full && nkt >= (bb ? 32 : 8))
+        want = std::min<int64_t>(cdiv(2 * full, tiles), nkt / 4);
+    }
+    want = std::min<int64_t>(want, 64);
+    while (want > 1 && (size_t)(want * batch) * (size_t)(M * N) > scratch.floats) --want;
+    return (want > 1 && scratch.p) ? (int)want : 1;
+  };
+  // Direct-to-LDS tile: 256 when that alone gives most CUs a tile; else
+  // whichever of 256 and 128 has the smaller estimated time -- the MFMA time
+  // at the share of CUs its workgroups keep busy (the 128 tile runs at about
+  // 0.55 of the 256 tile's rate per CU) plus its split-K partials (fp32,
+  // written and read once).  Rates: 1.0e15 flop/s, 4e12 B/s.
+  bool mid = false;
+  if (bb) {
+    const int T2 = gemm_bb_tile(false), T1 = gemm_bb_tile(true), bk = gemm_bb_bk();
+    const int64_t t256 = cdiv(M, (int64_t)T2) * cdiv(N, (int64_t)T2) * batch;
+    if (t256 < 224) {
+      const double fl = 2.0 * (double)M * (double)N * (double)K * batch;
+      auto est = [&](int T, bool mt, double rate) {
+        const int sp = split_for(T, T, bk, mt);
+        const double wgs = (double)(cdiv(M, (int64_t)T) * cdiv(N, (int64_t)T) * batch) * sp;
+        const double util = std::min(1.0, wgs / 256.0);
+        const double part = sp > 1 ? (double)sp * (double)M * (double)N * batch * 8.0 : 0.0;
+        return fl / (1.0e15 * rate * util) + part / 4.0e12;
+      };
+      mid = est(T1, true, 0.55) < est(T2, false, 1.0);
+    }
+  }
+  const int TM = bb ? gemm_bb_tile(mid) : (big ? gemm_big_tile_m() : GBM);
+  const int TN = bb ? gemm_bb_tile(mid) : (big ? gemm_big_tile_n() : GBN);
   p.tiles_m = (int)cdiv(M, TM);
   p.tiles_n = (int)cdiv(N, TN);
   const int BK = bb ? gemm_bb_bk()
                     : big ? gemm_big_bk()
                           : (math == MATH_BF16 ? GCfg<MATH_BF16>::BK : GCfg<MATH_F32>::BK);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
-  const int64_t nkt = cdiv(K, BK);
-  int splits = 1;
-  // fewer tiles than this leave CUs idle (the direct-to-LDS kernel runs one
-  // workgroup per CU, the others two)
-  const int64_t full = bb ? 224 : (big ? 160 : 192);
-  // (the direct-to-LDS kernel needs a longer K per split to fill its ring)
-  if (tiles < full && nkt >= (bb ? 32 : 8)) {
-    int64_t want = cdiv(2 * full, tiles);
-    want = std::min<int64_t>(want, nkt / 4);
-    want = std::min<int64_t>(want, 64);
-    while (want > 1 && (size_t)(want * batch) * (size_t)(M * N) > scratch.floats) --want;
-    if (want > 1 && scratch.p) splits = (int)want;
-  }
+  const int splits = split_for(TM, TN, BK, mid);
   p.splits = splits;
   p.part = splits > 1 ? scratch.p : nullptr;
   if (tiles * splits > 0x7fffffffLL || (int64_t)batch * splits > 65535) {
@@ -535,7 +571,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   }
   dim3 grid(gx, 1, (unsigned)(batch * splits));
   const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | ((big ? 1 : 0) << 5) |
-                  ((bb ? 1 : 0) << 6);
+                  ((bb ? 1 : 0) << 6) | ((mid ? 1 : 0) << 7);
   ProfRec* pr = prof_slot(vid);
   if (pr) {
     // algorithmic work: 2 M N K (M N K when one operand is triangular), and the
@@ -551,7 +587,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     pr->bytes = ((double)M * K * sa + (double)K * N * sb + (double)M * N * cb) * batch;
     hipEventRecord(pr->beg, s);
   }
-  if (bb) launch_gemm_bb(s, grid, p);
+  if (bb) launch_gemm_bb(s, grid, p, mid);
   else if (big) launch_gemm_big(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   else if (math == MATH_BF16) launch_a<MATH_BF16>(s, grid, p, A.dt, A.kc, B.dt, B.kc);
   else launch_a<MATH_F32>(s, grid, p, A.dt, A.kc, B.dt, B.kc);

@@ -4,15 +4,20 @@
 // engine (gemm.h).  This is the kernel of the fold's outer-block updates and
 // of the preconditioner's products.
 //
-// Tile 256 x 256 x 32, eight waves of 128 x 64 (4 x 2 v_mfma_f32_32x32x16_bf16
-// tiles each, 128 fp32 accumulators per lane), one workgroup per CU.  The
-// square tile halves the operand bytes per flop of a 256 x 128 tile, which
-// matters because the kernel is bound by how fast slabs reach LDS, not by
-// LDS bandwidth (no bank conflicts, LDS about 10 % busy).  Operand slabs go
-// from global memory straight into LDS (buffer_load_dwordx4 ... lds), so
-// staging costs no registers and the workgroup keeps a ring of four slabs
-// (128 KB): the loads of slabs k + 1 .. k + 3 are in flight while slab k is
-// multiplied.  Buffer
+// Two tiles share the code.  The large one, 256 x 256 x 32 with eight waves
+// of 128 x 64 (4 x 2 v_mfma_f32_32x32x16_bf16 tiles each, 128 fp32
+// accumulators per lane) and one workgroup per CU, takes products with many
+// output tiles: the square tile halves the operand bytes per flop of a
+// 256 x 128 tile, which matters because the kernel is bound by how fast
+// slabs reach LDS, not by LDS bandwidth (no bank conflicts, LDS about 10 %
+// busy).  The mid one, 128 x 128 x 32 with four waves of 64 x 64 and two
+// workgroups per CU, takes products with few output rows or columns (the
+// fold's 512-wide outer-block products): four times the tiles fill the CUs
+// without split-K, or with a quarter of the split-K partial traffic.
+// Operand slabs go from global memory straight into LDS
+// (buffer_load_dwordx4 ... lds), so staging costs no registers and the
+// workgroup keeps a ring of four slabs (128 / 64 KB): the loads of slabs
+// k + 1 .. k + 3 are in flight while slab k is multiplied.  Buffer
 // descriptors bound each operand, so rows past M / N read as zero without a
 // branch.  The 64-byte rows of a slab are stored with their four 16-byte
 // chunks XOR-swizzled by bits 2-3 of the row, which makes the MFMA fragment
@@ -33,12 +38,24 @@ namespace {
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int BM = 256, BN = 256, BK = 32, NTH = 512, NWAVE = NTH / 64, STAGES = 4;
-constexpr int SLAB_A = BM * BK, SLAB_B = BN * BK;   // bf16 elements per slab (16 KB each)
-constexpr int STAGE = SLAB_A + SLAB_B;
-constexpr int LOADS_A = SLAB_A * 2 / 16 / NTH;      // 16-byte loads per thread (2)
-constexpr int LOADS_B = SLAB_B * 2 / 16 / NTH;      // (2)
-constexpr int LOADS = LOADS_A + LOADS_B;            // per thread per slab pair (4)
+constexpr int BK = 32, STAGES = 4;
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int OCC_>
+struct BbCfg {
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, OCC = OCC_;
+  static constexpr int NWAVE = WAVES_M * WAVES_N, NTH = NWAVE * 64;
+  static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;   // wave tile
+  static constexpr int FM = WTM / 32, FN = WTN / 32;             // 32 x 32 MFMA tiles per wave
+  static constexpr int SLAB_A = BM * BK, SLAB_B = BN * BK;       // bf16 elements per slab
+  static constexpr int STAGE = SLAB_A + SLAB_B;
+  static constexpr int LOADS_A = SLAB_A * 2 / 16 / NTH;          // 16-byte loads per thread
+  static constexpr int LOADS_B = SLAB_B * 2 / 16 / NTH;
+  static constexpr int LOADS = LOADS_A + LOADS_B;                // per thread per slab pair
+  static_assert(LOADS == 4, "wait_vm immediates assume four loads per slab pair");
+  static_assert(SLAB_A * 2 % (16 * NTH) == 0 && SLAB_B * 2 % (16 * NTH) == 0, "slab split");
+};
+using BigCfg = BbCfg<256, 256, 2, 4, 1>;   // 512 threads, 128 KB ring, one workgroup per CU
+using MidCfg = BbCfg<128, 128, 2, 2, 2>;   // 256 threads, 64 KB ring, two workgroups per CU
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -52,7 +69,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 // LDS S.  Wave w, instruction i fills slots (NWAVE i + w) * 64 .. + 63; lane
 // l's slot s = (row, q) holds the logical chunk q ^ ((row >> 2) & 3) of that
 // row.
-template <int NL>
+template <int NWAVE, int NL>
 __device__ __forceinline__ void issue_slab(__amdgpu_buffer_rsrc_t rs, bf16_t* S, int64_t ld,
                                            int64_t kt, int64_t kmax) {
   // the LDS destination (M0) must be wave-uniform: take the wave index from
@@ -102,18 +119,20 @@ __device__ __forceinline__ bool slab_crosses(int tri, int64_t mn0, int ext, int6
 }
 
 // Wait until the loads of this slab have landed, leaving those of the
-// `ahead` later slabs already issued (0, 1 or 2: LOADS each) in flight.
+// `ahead` later slabs already issued (0, 1 or 2: four loads each) in flight.
 __device__ __forceinline__ void wait_vm(int ahead) {
-  static_assert(LOADS == 4, "vmcnt immediates below");
   if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x0f78);     // vmcnt(8)
   else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0f74); // vmcnt(4)
   else __builtin_amdgcn_s_waitcnt(0x0f70);                // vmcnt(0)
 }
 
+template <class CF>
 __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* smem) {
+  constexpr int BM = CF::BM, BN = CF::BN, FM = CF::FM, FN = CF::FN;
+  constexpr int STAGE = CF::STAGE, SLAB_A = CF::SLAB_A;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 2, wn = wave & 3;      // 2 x 4 waves of 128 x 64
+  const int wm = wave / CF::WAVES_N, wn = wave % CF::WAVES_N;
   const int l32 = lane & 31, h = lane >> 5;
   const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
   const int z = blockIdx.z;
@@ -137,11 +156,11 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ab, (p.M - m0) * p.lda * 2);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb, (p.N - n0) * p.ldb * 2);
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -149,8 +168,8 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s) {
     if (s < n_it) {
-      issue_slab<LOADS_A>(ra, smem + s * STAGE, p.lda, kt0 + s, p.K);
-      issue_slab<LOADS_B>(rb, smem + s * STAGE + SLAB_A, p.ldb, kt0 + s, p.K);
+      issue_slab<CF::NWAVE, CF::LOADS_A>(ra, smem + s * STAGE, p.lda, kt0 + s, p.K);
+      issue_slab<CF::NWAVE, CF::LOADS_B>(rb, smem + s * STAGE + SLAB_A, p.ldb, kt0 + s, p.K);
     }
   }
   for (int it = 0; it < n_it; ++it) {
@@ -161,8 +180,10 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
     __builtin_amdgcn_s_barrier();
     if (it + STAGES - 1 < n_it) {
       const int sn = (it + STAGES - 1) % STAGES;
-      issue_slab<LOADS_A>(ra, smem + sn * STAGE, p.lda, kt0 + it + STAGES - 1, p.K);
-      issue_slab<LOADS_B>(rb, smem + sn * STAGE + SLAB_A, p.ldb, kt0 + it + STAGES - 1, p.K);
+      issue_slab<CF::NWAVE, CF::LOADS_A>(ra, smem + sn * STAGE, p.lda, kt0 + it + STAGES - 1,
+                                         p.K);
+      issue_slab<CF::NWAVE, CF::LOADS_B>(rb, smem + sn * STAGE + SLAB_A, p.ldb,
+                                         kt0 + it + STAGES - 1, p.K);
     }
     const bf16_t* As = smem + (it % STAGES) * STAGE;
     const bf16_t* Bs = As + SLAB_A;
@@ -171,25 +192,27 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
     const bool xb = slab_crosses(p.trib, n0, BN, kbase);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8_t af[4], bfr[2];
+      bf16x8_t af[FM], bfr[FN];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = frag(As, wm * 128 + i * 32 + l32, 2 * ks + h);
+      for (int i = 0; i < FM; ++i) af[i] = frag(As, wm * CF::WTM + i * 32 + l32, 2 * ks + h);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bfr[j] = frag(Bs, wn * 64 + j * 32 + l32, 2 * ks + h);
+      for (int j = 0; j < FN; ++j) bfr[j] = frag(Bs, wn * CF::WTN + j * 32 + l32, 2 * ks + h);
       if (xa) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          af[i] = mask_frag<true>(af[i], p.tria, m0 + wm * 128 + i * 32 + l32, kbase + ks * 16 + h * 8);
+        for (int i = 0; i < FM; ++i)
+          af[i] = mask_frag<true>(af[i], p.tria, m0 + wm * CF::WTM + i * 32 + l32,
+                                  kbase + ks * 16 + h * 8);
       }
       if (xb) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          bfr[j] = mask_frag<false>(bfr[j], p.trib, n0 + wn * 64 + j * 32 + l32, kbase + ks * 16 + h * 8);
+        for (int j = 0; j < FN; ++j)
+          bfr[j] = mask_frag<false>(bfr[j], p.trib, n0 + wn * CF::WTN + j * 32 + l32,
+                                    kbase + ks * 16 + h * 8);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
   }
@@ -198,13 +221,13 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
   if (p.splits > 1) {
     float* P = p.part + ((size_t)(bidx * p.splits + split)) * (size_t)p.M * (size_t)p.N;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-          const int64_t col = n0 + wn * 64 + j * 32 + l32;
+          const int64_t row = m0 + wm * CF::WTM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          const int64_t col = n0 + wn * CF::WTN + j * 32 + l32;
           if (row < p.M && col < p.N) P[row * p.N + col] = acc[i][j][r];
         }
     return;
@@ -212,21 +235,21 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
   float* Cp = p.C ? p.C + (size_t)bidx * p.bsc : nullptr;
   bf16_t* Cbp = p.Cb ? p.Cb + (size_t)bidx * p.bscb : nullptr;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + l32;
+    for (int j = 0; j < FN; ++j) {
+      const int64_t col = n0 + wn * CF::WTN + j * 32 + l32;
       float old[16];
       if (p.beta != 0.0f) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          const int64_t row = m0 + wm * CF::WTM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
           old[r] = (row < p.M && col < p.N) ? Cp[row * p.ldc + col] : 0.0f;
         }
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        const int64_t row = m0 + wm * CF::WTM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
         if (row < p.M && col < p.N) {
           float v = p.alpha * acc[i][j][r];
           if (p.beta != 0.0f) v += p.beta * old[r];
@@ -238,23 +261,26 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
 }
 
 // Tiles visited grid-stride (a launch may use fewer workgroups than tiles).
-__global__ __launch_bounds__(NTH, 1) void gemm_bb_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) bf16_t smem_bb[STAGES * STAGE];   // 128 KB
+template <class CF>
+__global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem_bb[STAGES * CF::STAGE];
   const int tiles = p.tiles_m * p.tiles_n;
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    bb_tile(p, tile, smem_bb);
+    bb_tile<CF>(p, tile, smem_bb);
     __syncthreads();   // the LDS ring is reused by the next tile
   }
 }
 
 }  // namespace
 
-int gemm_bb_tile_m() { return BM; }
-int gemm_bb_tile_n() { return BN; }
+int gemm_bb_tile(bool mid) { return mid ? MidCfg::BM : BigCfg::BM; }
 int gemm_bb_bk() { return BK; }
 
-void launch_gemm_bb(hipStream_t s, dim3 grid, const GemmParams& p) {
-  hipLaunchKernelGGL(gemm_bb_kernel, grid, dim3(NTH), 0, s, p);
+void launch_gemm_bb(hipStream_t s, dim3 grid, const GemmParams& p, bool mid) {
+  if (mid)
+    hipLaunchKernelGGL(gemm_bb_kernel<MidCfg>, grid, dim3(MidCfg::NTH), 0, s, p);
+  else
+    hipLaunchKernelGGL(gemm_bb_kernel<BigCfg>, grid, dim3(BigCfg::NTH), 0, s, p);
 }
 
 }  // namespace ifk

@@ -25,12 +25,11 @@ int gemm_big_bk();
 void launch_gemm_big(hipStream_t s, dim3 grid, const GemmParams& p, int adt, bool akc, int bdt,
                      bool bkc);
 
-// 256 x 256 x 32 bf16 x bf16 kernel for K-contiguous operands with a
-// four-slab direct-to-LDS ring (gemm_bb.hip); grid.x = tiles, grid.z =
-// batch * splits.
-int gemm_bb_tile_m();
-int gemm_bb_tile_n();
+// bf16 x bf16 kernel for K-contiguous operands with a four-slab
+// direct-to-LDS ring (gemm_bb.hip), square tile 256 (mid = false) or 128
+// (mid = true), BK 32; grid.x = tiles, grid.z = batch * splits.
+int gemm_bb_tile(bool mid);
 int gemm_bb_bk();
-void launch_gemm_bb(hipStream_t s, dim3 grid, const GemmParams& p);
+void launch_gemm_bb(hipStream_t s, dim3 grid, const GemmParams& p, bool mid);
 
 }  // namespace ifk

@@ -34,11 +34,12 @@ int launch_apply_m(hipStream_t s, const float* XT, int64_t ldx, int64_t pe, int 
 int launch_panel_hrw(hipStream_t s, const float* G, int ncb, const float* Q1, const float* U1,
                      int b, float* N, float* R, int64_t ldr, int nr, float* NW, int64_t ldnw,
                      const int* flag);
-// Y = Q2 N (ld ldy; also RNE bf16 into Yb, same ld, when Yb is given) and
+// Y = Q2 N (ld ldy; also RNE bf16 into Yb, same ld, when Yb is given, and
+// into YbT transposed, b rows of ld ldt >= pe, when YbT is given) and
 // CT_rest -= (Q2 NW)^T on the transposed working matrix (nr rows of ld ldc)
 int launch_panel_update(hipStream_t s, const float* Q2, int64_t pe, int b, const float* N,
-                        float* Y, int64_t ldy, bf16_t* Yb, const float* NW, int64_t ldnw,
-                        float* CT, int64_t ldc, int nr);
+                        float* Y, int64_t ldy, bf16_t* Yb, bf16_t* YbT, int64_t ldt,
+                        const float* NW, int64_t ldnw, float* CT, int64_t ldc, int nr);
 // R_blk (rows x cols, ldr) -= WT^T (WT cols x rows, ldw)
 int launch_sub_transposed(hipStream_t s, float* R, int64_t ldr, const float* WT, int64_t ldw,
                           int64_t rows, int64_t cols);
@@ -48,6 +49,14 @@ int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float*
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
 int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
                       float* Z, int64_t ldz, int safe);
+// Diagonal nb x nb blocks of T = (striu(G) + diag(1 + diag G) / 2)^{-1}, the T
+// factor of a block of reflectors [I; Y] from their Gram matrix G = Y^T Y
+int launch_ut_trinv_diag(hipStream_t s, const float* G, int64_t ldg, int64_t n, int nb, float* T,
+                         int64_t ldt);
+// C_b = alpha A_b B_b, fp32 row-major, 64 x 64 tiles (small products)
+int launch_gemm64(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                  int64_t lda, int64_t bsa, int tria, const float* B, int64_t ldb, int64_t bsb,
+                  int trib, float* C, int64_t ldc, int64_t bsc, int batch);
 
 // --- elementwise kernels (elementwise.hip) -----------------------------------
 // dst (rows x cols, ldd, fp32) = scale * src (dtype sdt, lds)

@@ -67,16 +67,19 @@ static size_t split_floats(int64_t b, int64_t n) {
 // Fold
 // ----------------------------------------------------------------------------
 static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
-                      int64_t ldz, int math, int safe, float* tmp, SplitScratch sp);
+                      int64_t ldz, int math, int safe, float* tmp, SplitScratch sp,
+                      bool ut = false);
 
 struct FoldWs {
   float* C;       // n x p: the chunk, transposed (CT = C^T; see fold_core)
   bf16_t* Cb;     // n x p: RNE bf16 shadow of C for bf16 arithmetic (the rows of
                   // columns beyond the current outer block are kept current)
   float* Yo[2];   // p x OUTER_B: reflector X parts of an outer block (by block parity)
-  float* Yto[2];  // OUTER_B x p: (Y T)^T of an outer block (fp32 arithmetic)
-  bf16_t* Yob[2];   // bf16 copies of Yo and (Y T)^T for bf16 arithmetic (the
-  bf16_t* Ytob[2];  // products round their operands to bf16 anyway)
+  bf16_t* Yob[2];   // bf16 copies of Yo, row-major and transposed (OUTER_B x p),
+  bf16_t* YobT[2];  // for bf16 arithmetic (the products round their operands
+                    // to bf16 anyway)
+  float* Wpn;     // OUTER_B x OUTER_B: CT_cols Y + R_blk^T of the near columns
+  float* Wpf;     // n x OUTER_B: ... of the far columns
   float* Wn;      // OUTER_B x OUTER_B: W^T of the near columns (critical stream)
   float* Wf;      // n x OUTER_B: W^T of the far columns (helper stream)
   bf16_t* Wnb;
@@ -89,8 +92,7 @@ struct FoldWs {
   float* M1;
   float* Q1;
   float* N;
-  float* Go;      // OUTER_B x OUTER_B: Gram of the outer reflectors
-  float* Tio;     // OUTER_B x OUTER_B: UT transform T^{-1}
+  float* Go;      // OUTER_B x OUTER_B: Gram of the outer reflectors (upper part)
   float* To[2];   // OUTER_B x OUTER_B: T of an outer block (by block parity)
   float* ttmp;    // triangular-inverse scratch for To
   SplitScratch tsp;
@@ -105,11 +107,12 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   w.Cb = need_C ? a.take<bf16_t>((size_t)p * n) : nullptr;
   for (int i = 0; i < 2; ++i) {
     w.Yo[i] = a.take<float>((size_t)p * B);
-    w.Yto[i] = a.take<float>((size_t)p * B);
     w.Yob[i] = a.take<bf16_t>((size_t)p * B);
-    w.Ytob[i] = a.take<bf16_t>((size_t)p * B);
+    w.YobT[i] = a.take<bf16_t>((size_t)p * B);
     w.To[i] = a.take<float>(B * B);
   }
+  w.Wpn = a.take<float>((size_t)B * B);
+  w.Wpf = a.take<float>((size_t)B * n);
   w.Wn = a.take<float>((size_t)B * B);
   w.Wf = a.take<float>((size_t)B * n);
   w.Wnb = a.take<bf16_t>((size_t)B * B);
@@ -123,7 +126,6 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   w.Q1 = a.take<float>(b * b);
   w.N = a.take<float>(b * b);
   w.Go = a.take<float>(B * B);
-  w.Tio = a.take<float>(B * B);
   w.ttmp = a.take<float>((size_t)B * B / 2 + (size_t)TRINV_NB * TRINV_NB * 4);
   w.tsp.floats = split_floats(TRINV_NB, B);
   w.tsp.p = a.take<float>(w.tsp.floats);
@@ -135,16 +137,18 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
 }
 
 // ----------------------------------------------------------------------------
-// Helper stream and events of the look-ahead (one set per device, created on
-// first use; a fold holds the device's lock while it enqueues).
+// Helper streams and events of the look-ahead (one set per device and
+// calling stream, created on first use; a fold holds the set's lock while it
+// enqueues).
 // ----------------------------------------------------------------------------
 struct LookAhead {
   std::mutex mu;
-  hipStream_t s2 = nullptr;
+  hipStream_t s2 = nullptr;                 // far updates
   hipEvent_t ready[2] = {nullptr, nullptr};
   hipEvent_t far[2] = {nullptr, nullptr};   // the next outer block's columns are done
   hipEvent_t fall[2] = {nullptr, nullptr};  // all of the block's far update is done
   hipEvent_t done = nullptr;                // everything queued on s2 so far
+  hipEvent_t tready[2] = {nullptr, nullptr};  // T of the outer block is complete
 };
 
 // One helper stream per (device, calling stream): folds issued on different
@@ -167,7 +171,8 @@ static LookAhead* look_ahead(hipStream_t s, int* rc) {
     for (int i = 0; i < 2 && ok; ++i)
       ok = hipEventCreateWithFlags(&x->ready[i], hipEventDisableTiming) == hipSuccess &&
            hipEventCreateWithFlags(&x->far[i], hipEventDisableTiming) == hipSuccess &&
-           hipEventCreateWithFlags(&x->fall[i], hipEventDisableTiming) == hipSuccess;
+           hipEventCreateWithFlags(&x->fall[i], hipEventDisableTiming) == hipSuccess &&
+           hipEventCreateWithFlags(&x->tready[i], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
       set_error("tsqr_fold: cannot create the helper stream or its events");
       *rc = IFK_ERR_HIP;
@@ -187,45 +192,46 @@ static LookAhead* look_ahead(hipStream_t s, int* rc) {
     }                               \
   } while (0)
 
-// Outer block k (reflectors Yo of columns [K0, K1), pe rows, buffers of
-// parity k2): T from the UT transform
-//   T^{-1} = striu(Yo^T Yo) + diag(1 + diag(Yo^T Yo)) / 2
-// and Y T.  In bf16 arithmetic every product reads the bf16 copies (Yob,
-// Ytob, W bf16), which hold exactly the RNE roundings the MFMA operands would
-// get; T, W and R stay fp32.
-static int outer_prepare(hipStream_t s, int math, FoldWs& w, int k2, int64_t pe, int64_t KB) {
+// T of outer block k (reflectors V = [I; Y] of columns [K0, K1), pe rows,
+// buffers of parity k2).  The UT transform gives
+//   T^{-1} = striu(V^T V) + diag(V^T V) / 2,   V^T V = I + Go,  Go = Y^T Y,
+// and T is its triangular inverse (fp32): diagonal blocks straight from Go,
+// the rest by block doubling.  In bf16 arithmetic Go reads the transposed
+// bf16 copy of Y (both operands K-contiguous).
+static int outer_prepare(hipStream_t s, int math, FoldWs& w, int k2, int64_t pe, int64_t ldt,
+                         int64_t KB) {
   const int64_t B = OUTER_B;
   const bool bf = math == MATH_BF16;
-  const MatRef YoT = bf ? A_t(w.Yob[k2], DT_BF16, B) : A_t(w.Yo[k2], DT_F32, B);
-  const MatRef YoB = bf ? B_n(w.Yob[k2], DT_BF16, B) : B_n(w.Yo[k2], DT_F32, B);
-  RC(gemm(s, math, KB, KB, pe, 1.0f, YoT, YoB, 0.0f, out_f32(w.Go, KB), 1, w.split));
-  RC(launch_ut_tinv(s, w.Go, KB, KB, w.Tio, KB));
-  RC(trinv_core(s, w.Tio, DT_F32, KB, KB, w.To[k2], KB, MATH_F32, 0, w.ttmp, w.tsp));
-  // (Y T)^T = T^T Y^T, K-contiguous in both operands
-  const MatRef YoBt = bf ? B_t(w.Yob[k2], DT_BF16, B) : B_t(w.Yo[k2], DT_F32, B);
-  return gemm(s, math, KB, pe, KB, 1.0f, A_t(w.To[k2], DT_F32, KB, TRI_LOWER), YoBt, 0.0f,
-              bf ? out_bf16(w.Ytob[k2], pe) : out_f32(w.Yto[k2], pe), 1, w.split);
+  const MatRef YA = bf ? A_n(w.YobT[k2], DT_BF16, ldt) : A_t(w.Yo[k2], DT_F32, B);
+  const MatRef YB = bf ? B_t(w.YobT[k2], DT_BF16, ldt) : B_n(w.Yo[k2], DT_F32, B);
+  RC(gemm(s, math, KB, KB, pe, 1.0f, YA, YB, 0.0f, out_f32(w.Go, B), 1, w.split));
+  return trinv_core(s, w.Go, DT_F32, B, KB, w.To[k2], B, MATH_F32, 0, w.ttmp, w.tsp, true);
 }
 
 // Apply outer block k to the columns [c_lo, c_hi) of C, i.e. the rows
 // [c_lo, c_hi) of the transposed working matrix CT (ld ldc):
-//   W^T = CT_cols (Y T) + R_blk^T T,  R_blk -= (W^T)^T,  CT_cols -= W^T Y^T
-// The two large products read K-contiguous operands only.  W^T is nt x KB.
+//   Wp = CT_cols Y + R_blk^T,   W^T = Wp T,   R_blk -= W,   CT_cols -= W^T Y^T
+// Wp does not need T, so it is formed first; t_ready (when given) is waited
+// for before the product with T.  The large products read K-contiguous
+// operands only (CT or its bf16 shadow, the transposed bf16 copy of Y).
+// W^T is nt x KB.
 static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
                        int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1,
-                       int64_t c_lo, int64_t c_hi, float* W, bf16_t* Wb, SplitScratch sp,
-                       int max_wgs) {
+                       int64_t c_lo, int64_t c_hi, float* Wp, float* W, bf16_t* Wb,
+                       SplitScratch sp, int max_wgs, hipEvent_t t_ready) {
   const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
   if (nt <= 0) return IFK_OK;
   const bool bf = math == MATH_BF16;
   float* Rb = R + K0 * ldr + c_lo;
   float* Cr = CT + c_lo * ldc;
   bf16_t* Crb = CTb ? CTb + c_lo * ldc : nullptr;   // bf16 shadow (bf16 arithmetic)
-  const MatRef YtoTB = bf ? B_t(w.Ytob[k2], DT_BF16, pe) : B_t(w.Yto[k2], DT_F32, pe);
+  RC(launch_transpose_to_f32(s, Rb, DT_F32, ldr, KB, nt, Wp, KB));
   const MatRef CA = Crb ? A_n(Crb, DT_BF16, ldc) : A_n(Cr, DT_F32, ldc);
-  RC(gemm(s, math, nt, KB, pe, 1.0f, CA, YtoTB, 0.0f, out_f32(W, KB), 1, sp, max_wgs));
-  RC(gemm(s, math, nt, KB, KB, 1.0f, A_t(Rb, DT_F32, ldr), B_n(w.To[k2], DT_F32, KB, TRI_UPPER),
-          1.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB), 1, sp));
+  const MatRef YB = bf ? B_t(w.YobT[k2], DT_BF16, ldc) : B_n(w.Yo[k2], DT_F32, B);
+  RC(gemm(s, math, nt, KB, pe, 1.0f, CA, YB, 1.0f, out_f32(Wp, KB), 1, sp, max_wgs));
+  if (t_ready) HIPRC(hipStreamWaitEvent(s, t_ready, 0), "tsqr_fold: stream wait failed");
+  RC(gemm(s, math, nt, KB, KB, 1.0f, A_n(Wp, DT_F32, KB), B_n(w.To[k2], DT_F32, B, TRI_UPPER),
+          0.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB), 1, sp, max_wgs));
   RC(launch_sub_transposed(s, Rb, ldr, W, KB, KB, nt));
   const MatRef WA = bf ? A_n(Wb, DT_BF16, KB) : A_n(W, DT_F32, KB);
   const MatRef YoBt = bf ? B_t(w.Yob[k2], DT_BF16, B) : B_t(w.Yo[k2], DT_F32, B);
@@ -235,15 +241,19 @@ static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf
 
 // Core of the fold on the transposed fp32 working copy CT = C^T (n x p, row
 // stride ldc; a panel X_p = C[:, c0:c1] is the contiguous row block
-// CT[c0:c1, :]).  R rows [0, r_new) receive the result.  Two-level blocking: 64-column panels inside 512-column
-// outer blocks; a panel's reflectors update only the rest of its outer block,
-// and each finished outer block is applied to the columns beyond it as one
-// block reflector.  Look-ahead: of that application only the next outer
-// block's columns stay on the critical stream s; the columns beyond run on
-// the device's helper stream and overlap the next block's panels (which are
-// latency-bound on a few CUs).  Buffers a far update still reads are double
-// buffered by block parity, and events order
-//   prepare(k) -> far(k);  far(k-1) -> near(k);  far(last) -> end of fold.
+// CT[c0:c1, :]).  R rows [0, r_new) receive the result.  Two-level blocking:
+// 64-column panels inside 512-column outer blocks; a panel's reflectors
+// update only the rest of its outer block, and each finished outer block is
+// applied to the columns beyond it as one block reflector.  Look-ahead: of
+// that application only the next outer block's columns stay on the critical
+// stream s; the columns beyond run on the device's helper stream and overlap
+// the next block's panels (which are latency-bound on a few CUs).  The
+// application's large product CT_cols Y does not need T, so the helper starts
+// it as soon as the block's reflectors are written, while s forms T.  Buffers
+// a far update still reads are double buffered by block parity, and events
+// order
+//   panels(k) -> far(k) -> [T(k) on s];  far(k-1) -> near(k);
+//   far(last) -> end of fold.
 // With x_tri, C is upper triangular and a panel ending at column c1
 // involves C rows [0, c1).
 static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n, float* R,
@@ -257,11 +267,11 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
   }
   std::unique_lock<std::mutex> lock;
   if (la) lock = std::unique_lock<std::mutex>(la->mu);
+  const bool bf = math == MATH_BF16;
   // bf16 arithmetic: the outer-block products read a bf16 shadow of C (the
   // exact values their operand staging would round to), which the C updates
   // keep current; it is seeded here once
-  bf16_t* Cb = (math == MATH_BF16 && w.Cb && std::min<int64_t>(OUTER_B, r_new) < n) ? w.Cb
-                                                                                   : nullptr;
+  bf16_t* Cb = (bf && w.Cb && std::min<int64_t>(OUTER_B, r_new) < n) ? w.Cb : nullptr;
   if (Cb) RC(launch_cast(s, C, ldc, n, p, Cb, DT_BF16, ldc));
   int far_pending = -1;              // parity of the last far update not yet joined
   bool fall_pending[2] = {false, false};   // a far update still reads parity buffers
@@ -271,7 +281,7 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     const int64_t K1 = std::min<int64_t>(K0 + B, r_new);
     const int64_t KB = K1 - K0;
     const int64_t pe_o = x_tri ? std::min<int64_t>(p, K1) : p;
-    const bool bf = math == MATH_BF16;
+    const bool outer = K1 < n;   // the block is applied to columns beyond it
     // block k - 2's far update reads this parity's reflector store
     if (fall_pending[k2]) {
       HIPRC(hipStreamWaitEvent(s, la->fall[k2], 0), "tsqr_fold: stream wait failed");
@@ -280,6 +290,7 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     if (x_tri) {
       RC(launch_zero(s, w.Yo[k2], B, pe_o, KB));
       if (bf) RC(launch_zero_bf16(s, w.Yob[k2], B, pe_o, KB));
+      if (bf && outer) RC(launch_zero_bf16(s, w.YobT[k2], ldc, KB, pe_o));
     }
     for (int64_t c0 = K0; c0 < K1; c0 += PANEL_B) {
       const int bk = (int)std::min<int64_t>(PANEL_B, K1 - c0);
@@ -301,40 +312,46 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
                           w.flag));
       // C_rest and Y into the outer store
       RC(launch_panel_update(s, w.Q2, pe, bk, w.N, w.Yo[k2] + (c0 - K0), OUTER_B,
-                             bf ? w.Yob[k2] + (c0 - K0) : nullptr, w.NW, OUTER_B, C + c1 * ldc,
-                             ldc, nr));
+                             bf ? w.Yob[k2] + (c0 - K0) : nullptr,
+                             (bf && outer) ? w.YobT[k2] + (c0 - K0) * ldc : nullptr, ldc, w.NW,
+                             OUTER_B, C + c1 * ldc, ldc, nr));
     }
-    if (K1 >= n) continue;
-    RC(outer_prepare(s, math, w, k2, pe_o, KB));
+    if (!outer) continue;
     const int64_t near_hi = std::min<int64_t>(K1 + B, n);
+    const bool far = la && near_hi < n;
+    if (far) {
+      HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
+      HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
+    }
+    RC(outer_prepare(s, math, w, k2, pe_o, ldc, KB));
+    if (far) {
+      // far columns on the helper stream, from the moment the block's
+      // reflectors are written (their product with T waits for T): first the
+      // block after next (the next block's near columns, so its wait below is
+      // short), then everything beyond
+      HIPRC(hipEventRecord(la->tready[k2], s), "tsqr_fold: event record failed");
+      const int64_t mid = std::min<int64_t>(near_hi + B, n);
+      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wpf,
+                     w.Wf, w.Wfb, w.split2, FAR_MAX_WGS, la->tready[k2]));
+      HIPRC(hipEventRecord(la->far[k2], la->s2), "tsqr_fold: event record failed");
+      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wpf, w.Wf,
+                     w.Wfb, w.split2, FAR_MAX_WGS, nullptr));
+      HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
+      fall_pending[k2] = true;
+      HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
+    }
     // near columns wait for the previous block's far update of them
     if (far_pending >= 0) {
       HIPRC(hipStreamWaitEvent(s, la->far[far_pending], 0), "tsqr_fold: stream wait failed");
       far_pending = -1;
     }
-    if (la && near_hi < n) {
-      // far columns on the helper stream, as soon as T and Y T are ready:
-      // first the block after next (the next block's near columns, so its
-      // wait above is short), then everything beyond
-      const int64_t mid = std::min<int64_t>(near_hi + B, n);
-      HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
-      HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
-      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wf,
-                     w.Wfb, w.split2, FAR_MAX_WGS));
-      HIPRC(hipEventRecord(la->far[k2], la->s2), "tsqr_fold: event record failed");
-      far_pending = k2;
-      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wf, w.Wfb,
-                     w.split2, FAR_MAX_WGS));
-      HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
-      fall_pending[k2] = true;
-      HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
-    }
+    if (far) far_pending = k2;
     if (la)
-      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wn, w.Wnb,
-                     w.split, 0));
+      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wpn, w.Wn,
+                     w.Wnb, w.split, 0, nullptr));
     else
-      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wf, w.Wfb, w.split,
-                     0));
+      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf, w.Wf, w.Wfb,
+                     w.split, 0, nullptr));
   }
   if (la) HIPRC(hipStreamWaitEvent(s, la->done, 0), "tsqr_fold: stream wait failed");
   return launch_sign_normalize(s, R, ldr, r_new, n);
@@ -493,33 +510,59 @@ size_t trinv_ws(int64_t n) {
   return a.used;
 }
 
+// Z = R^{-1} for upper-triangular R (n x n): diagonal 64-blocks, then block
+// doubling, Z12 = -Z11 (R12 Z22).  With ut, R holds a reflector Gram matrix G
+// and the inverted matrix is its UT transform striu(G) + diag(1 + diag G) / 2
+// (whose off-diagonal blocks are G's).  fp32 levels up to 256 wide run on the
+// 64-tile kernel, the rest on the GEMM engine.
 static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
-                      int64_t ldz, int math, int safe, float* tmp, SplitScratch sp) {
+                      int64_t ldz, int math, int safe, float* tmp, SplitScratch sp, bool ut) {
   const size_t esz = rdt == DT_F32 ? 4 : 2;
   const char* Rc = (const char*)R;
+  if (ut && rdt != DT_F32) {
+    set_error("tri_inverse: the UT transform takes an fp32 Gram matrix");
+    return IFK_ERR_INVALID;
+  }
   RC(launch_zero(s, Z, ldz, n, n));
-  RC(launch_trinv_diag(s, R, rdt, ldr, n, TRINV_NB, Z, ldz, safe));
+  if (ut) RC(launch_ut_trinv_diag(s, (const float*)R, ldr, n, TRINV_NB, Z, ldz));
+  else RC(launch_trinv_diag(s, R, rdt, ldr, n, TRINV_NB, Z, ldz, safe));
   for (int64_t w = TRINV_NB; w < n; w *= 2) {
     const int64_t step = 2 * w;
     const int64_t nfull = n / step;
+    const bool small = math == MATH_F32 && rdt == DT_F32 && w <= 256;
     if (nfull > 0) {
       const void* R12 = Rc + (size_t)w * esz;  // block (0, w)
-      RC(gemm(s, math, w, w, w, 1.0f, A_n(R12, rdt, ldr, TRI_NONE, step * (ldr + 1)),
-              B_n(Z + w * ldz + w, DT_F32, ldz, TRI_UPPER, step * (ldz + 1)), 0.0f,
-              out_f32(tmp, w, w * w), (int)nfull, sp));
-      RC(gemm(s, math, w, w, w, -1.0f, A_n(Z, DT_F32, ldz, TRI_UPPER, step * (ldz + 1)),
-              B_n(tmp, DT_F32, w, TRI_NONE, w * w), 0.0f, out_f32(Z + w, ldz, step * (ldz + 1)),
-              (int)nfull, sp));
+      if (small) {
+        RC(launch_gemm64(s, w, w, w, 1.0f, (const float*)R12, ldr, step * (ldr + 1), TRI_NONE,
+                         Z + w * ldz + w, ldz, step * (ldz + 1), TRI_UPPER, tmp, w, w * w,
+                         (int)nfull));
+        RC(launch_gemm64(s, w, w, w, -1.0f, Z, ldz, step * (ldz + 1), TRI_UPPER, tmp, w, w * w,
+                         TRI_NONE, Z + w, ldz, step * (ldz + 1), (int)nfull));
+      } else {
+        RC(gemm(s, math, w, w, w, 1.0f, A_n(R12, rdt, ldr, TRI_NONE, step * (ldr + 1)),
+                B_n(Z + w * ldz + w, DT_F32, ldz, TRI_UPPER, step * (ldz + 1)), 0.0f,
+                out_f32(tmp, w, w * w), (int)nfull, sp));
+        RC(gemm(s, math, w, w, w, -1.0f, A_n(Z, DT_F32, ldz, TRI_UPPER, step * (ldz + 1)),
+                B_n(tmp, DT_F32, w, TRI_NONE, w * w), 0.0f, out_f32(Z + w, ldz, step * (ldz + 1)),
+                (int)nfull, sp));
+      }
     }
     const int64_t i0 = nfull * step;
     if (i0 + w < n) {
       const int64_t w2 = n - i0 - w;
       const void* R12 = Rc + ((size_t)i0 * ldr + i0 + w) * esz;
-      RC(gemm(s, math, w, w2, w, 1.0f, A_n(R12, rdt, ldr),
-              B_n(Z + (i0 + w) * ldz + i0 + w, DT_F32, ldz, TRI_UPPER), 0.0f, out_f32(tmp, w2), 1,
-              sp));
-      RC(gemm(s, math, w, w2, w, -1.0f, A_n(Z + i0 * ldz + i0, DT_F32, ldz, TRI_UPPER),
-              B_n(tmp, DT_F32, w2), 0.0f, out_f32(Z + i0 * ldz + i0 + w, ldz), 1, sp));
+      if (small) {
+        RC(launch_gemm64(s, w, w2, w, 1.0f, (const float*)R12, ldr, 0, TRI_NONE,
+                         Z + (i0 + w) * ldz + i0 + w, ldz, 0, TRI_UPPER, tmp, w2, 0, 1));
+        RC(launch_gemm64(s, w, w2, w, -1.0f, Z + i0 * ldz + i0, ldz, 0, TRI_UPPER, tmp, w2, 0,
+                         TRI_NONE, Z + i0 * ldz + i0 + w, ldz, 0, 1));
+      } else {
+        RC(gemm(s, math, w, w2, w, 1.0f, A_n(R12, rdt, ldr),
+                B_n(Z + (i0 + w) * ldz + i0 + w, DT_F32, ldz, TRI_UPPER), 0.0f, out_f32(tmp, w2),
+                1, sp));
+        RC(gemm(s, math, w, w2, w, -1.0f, A_n(Z + i0 * ldz + i0, DT_F32, ldz, TRI_UPPER),
+                B_n(tmp, DT_F32, w2), 0.0f, out_f32(Z + i0 * ldz + i0 + w, ldz), 1, sp));
+      }
     }
   }
   return IFK_OK;

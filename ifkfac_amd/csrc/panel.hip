@@ -210,17 +210,18 @@ __global__ __launch_bounds__(PNT) void apply_m_kernel(const float* XT, int64_t l
 }
 
 // Panel update, one workgroup per (64-row tile, column block cb):
-//   cb == 0:  Y[r][0:b] = Q2[r][:] N           (Y of ld ldy; RNE bf16 copy into
-//                                               Yb, same ld, if given)
+//   cb == 0:  Y[r][0:b] = Q2[r][:] N           (Y of ld ldy; RNE bf16 copies
+//                                               into Yb, same ld, and into YbT
+//                                               transposed, ld ldt, if given)
 //   cb >= 1:  CT[c][r] -= (NW^T Q2^T)[c][r]    for the rows c of block cb - 1
 //                                               of CT_rest (NW 64 x nr, ld ldnw)
 // The transposed product puts consecutive r on consecutive lanes, so the
 // read-modify-write of CT is coalesced.
 __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int64_t pe, int b,
                                                            const float* N, float* Y, int64_t ldy,
-                                                           bf16_t* Yb, const float* NW,
-                                                           int64_t ldnw, float* CT, int64_t ldc,
-                                                           int nr) {
+                                                           bf16_t* Yb, bf16_t* YbT, int64_t ldt,
+                                                           const float* NW, int64_t ldnw,
+                                                           float* CT, int64_t ldc, int nr) {
   __shared__ float sQ[PT * LT];
   __shared__ float sM[PT * TLD];
   const int64_t r0 = (int64_t)blockIdx.x * PT;
@@ -256,6 +257,25 @@ __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int6
         if (gr < pe) {
           Y[gr * ldy + jc] = d[r];
           if (Yb) Yb[gr * ldy + jc] = f32_to_bf16(d[r]);
+        }
+      }
+    }
+    if (YbT) {
+      // the same product transposed, D[j][r] = sum_k N[k][j] Q2[r][k], so
+      // consecutive r go to consecutive lanes and the rows of YbT are
+      // written coalesced
+      zero16(d);
+#pragma unroll 8
+      for (int st = 0; st < 32; ++st) {
+        const int k = 32 * h + st;
+        d = __builtin_amdgcn_mfma_f32_32x32x2f32(sM[k * TLD + mq], sQ[k * LT + nq], d, 0, 0, 0);
+      }
+      const int64_t gr = r0 + jc;
+      if (gr < pe) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = acc_row(r);
+          if (j < w) YbT[(int64_t)j * ldt + gr] = f32_to_bf16(d[r]);
         }
       }
     }
@@ -330,12 +350,16 @@ int launch_apply_m(hipStream_t s, const float* XT, int64_t ldx, int64_t pe, int 
 }
 
 int launch_panel_update(hipStream_t s, const float* Q2, int64_t pe, int b, const float* N,
-                        float* Y, int64_t ldy, bf16_t* Yb, const float* NW, int64_t ldnw,
-                        float* CT, int64_t ldc, int nr) {
+                        float* Y, int64_t ldy, bf16_t* Yb, bf16_t* YbT, int64_t ldt,
+                        const float* NW, int64_t ldnw, float* CT, int64_t ldc, int nr) {
   if (pe <= 0) return IFK_OK;
+  if (YbT && ldt < pe) {
+    set_error("panel_update: transposed copy narrower than the panel");
+    return IFK_ERR_INVALID;
+  }
   const int nblk = nr > 0 ? (int)cdiv((int64_t)nr, (int64_t)PT) : 0;
   hipLaunchKernelGGL(panel_update_kernel, dim3((unsigned)cdiv(pe, (int64_t)PT), 1 + nblk),
-                     dim3(PNT), 0, s, Q2, pe, b, N, Y, ldy, Yb, NW, ldnw, CT, ldc, nr);
+                     dim3(PNT), 0, s, Q2, pe, b, N, Y, ldy, Yb, YbT, ldt, NW, ldnw, CT, ldc, nr);
   return check_launch("panel_update");
 }
 

@@ -655,11 +655,14 @@ __global__ void ut_tinv_kernel(const float* G, int64_t ldg, int64_t n, float* Ti
 // ---------------------------------------------------------------------------
 // Diagonal blocks of a blocked triangular inverse: Z_kk = R_kk^{-1} for every
 // nb x nb block on the diagonal of an upper-triangular R (last block may be
-// ragged).  One workgroup per block.
+// ragged).  One workgroup per block.  With ut, R holds a reflector Gram
+// matrix G and the inverted matrix is its UT transform
+// striu(G) + diag(1 + diag G) / 2.
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t ldr, int64_t n,
-                                                         int nb, float* Z, int64_t ldz, int safe) {
+                                                         int nb, float* Z, int64_t ldz, int safe,
+                                                         int ut) {
   __shared__ float sU[SB * SLD];
   __shared__ float sZ[SB * SLD];
   __shared__ float sT[TRINV_TMP];
@@ -670,12 +673,14 @@ __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t 
 #pragma unroll
     for (int q = 0; q < SB * SB / SNT; ++q) {
       const int e = threadIdx.x + SNT * q, r = e >> 6, c = e & 63;
-      if (r < b && c < b)
+      if (r < b && c < b) {
         v[q] = (r <= c)
                    ? Elem<DT>::load((const typename Elem<DT>::T*)R + (k0 + r) * ldr + k0 + c)
                    : 0.0f;
-      else
+        if (ut && r == c) v[q] = 0.5f * (1.0f + v[q]);
+      } else {
         v[q] = (r == c) ? 1.0f : 0.0f;
+      }
     }
 #pragma unroll
     for (int q = 0; q < SB * SB / SNT; ++q) {
@@ -688,6 +693,80 @@ __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t 
   for (int e = threadIdx.x; e < b * b; e += SNT) {
     const int r = e / b, c = e - r * b;
     Z[(k0 + r) * ldz + k0 + c] = sZ[r * SLD + c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Small fp32 GEMM, C_b = alpha * A_b B_b (row-major, batch b = blockIdx.y),
+// one 64 x 64 output tile per workgroup: the products of a triangular
+// inverse's first doubling levels, whose operands are too small to keep the
+// 128-tile engine's few workgroups busy.  K runs in 64-wide chunks staged in
+// LDS; the structural zeros of a triangular operand (tria / trib, TRI_UPPER
+// or TRI_LOWER) are skipped by K range and masked in the chunks that cross
+// its diagonal, so its stored other triangle is never read.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64_t K, float alpha,
+                                                     const float* A, int64_t lda, int64_t bsa,
+                                                     int tria, const float* B, int64_t ldb,
+                                                     int64_t bsb, int trib, float* C, int64_t ldc,
+                                                     int64_t bsc) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  __shared__ float sA[SB * SLD];
+  __shared__ float sB[SB * SLD];
+  const int64_t tiles_m = (M + SB - 1) / SB;
+  const int64_t m0 = (int64_t)(blockIdx.x % tiles_m) * SB, n0 = (int64_t)(blockIdx.x / tiles_m) * SB;
+  A += (int64_t)blockIdx.y * bsa;
+  B += (int64_t)blockIdx.y * bsb;
+  C += (int64_t)blockIdx.y * bsc;
+  int64_t klo = 0, khi = K;
+  if (tria == TRI_UPPER) klo = max(klo, m0);
+  if (tria == TRI_LOWER) khi = min(khi, m0 + SB);
+  if (trib == TRI_UPPER) khi = min(khi, n0 + SB);
+  if (trib == TRI_LOWER) klo = max(klo, n0);
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int r = (wave >> 1) * 32 + l32;   // row of A this lane supplies
+  const int c = (wave & 1) * 32 + l32;    // column of B this lane supplies
+  f32x16 d;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+  constexpr int PER = SB * SB / SNT;
+  for (int64_t kc = (klo / SB) * SB; kc < khi; kc += SB) {
+    float va[PER], vb[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = t + SNT * q, i = e >> 6, j = e & 63;
+      // A chunk: row m0 + i, column kc + j;  B chunk: row kc + i, column n0 + j
+      const int64_t ar = m0 + i, ak = kc + j, bk = kc + i, bc = n0 + j;
+      bool oka = ar < M && ak < khi && ak >= klo;
+      if (tria == TRI_UPPER) oka = oka && ak >= ar;
+      if (tria == TRI_LOWER) oka = oka && ak <= ar;
+      bool okb = bc < N && bk < khi && bk >= klo;
+      if (trib == TRI_UPPER) okb = okb && bk <= bc;
+      if (trib == TRI_LOWER) okb = okb && bk >= bc;
+      va[q] = oka ? A[ar * lda + ak] : 0.0f;
+      vb[q] = okb ? B[bk * ldb + bc] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = t + SNT * q;
+      sA[(e >> 6) * SLD + (e & 63)] = va[q];
+      sB[(e >> 6) * SLD + (e & 63)] = vb[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < 32; ++st) {
+      const int k = 32 * h + st;
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(sA[r * SLD + k], sB[k * SLD + c], d, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  const int64_t col = n0 + (wave & 1) * 32 + l32;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = m0 + (wave >> 1) * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+    if (row < M && col < N) C[row * ldc + col] = alpha * d[i];
   }
 }
 
@@ -745,11 +824,34 @@ int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
   const unsigned nblk = (unsigned)cdiv(n, nb);
   if (rdt == DT_F32)
     hipLaunchKernelGGL(trinv_diag_kernel<DT_F32>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, nb, Z,
-                       ldz, safe);
+                       ldz, safe, 0);
   else
     hipLaunchKernelGGL(trinv_diag_kernel<DT_BF16>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, nb, Z,
-                       ldz, safe);
+                       ldz, safe, 0);
   return check_launch("trinv_diag");
+}
+
+int launch_ut_trinv_diag(hipStream_t s, const float* G, int64_t ldg, int64_t n, int nb, float* T,
+                         int64_t ldt) {
+  if (int rc = check_b(nb, "ut_trinv_diag")) return rc;
+  if (n <= 0) return IFK_OK;
+  hipLaunchKernelGGL(trinv_diag_kernel<DT_F32>, dim3((unsigned)cdiv(n, (int64_t)nb)), dim3(SNT), 0, s,
+                     G, ldg, n, nb, T, ldt, 0, 1);
+  return check_launch("ut_trinv_diag");
+}
+
+int launch_gemm64(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                  int64_t lda, int64_t bsa, int tria, const float* B, int64_t ldb, int64_t bsb,
+                  int trib, float* C, int64_t ldc, int64_t bsc, int batch) {
+  if (M <= 0 || N <= 0) return IFK_OK;
+  const int64_t tiles = cdiv(M, (int64_t)SB) * cdiv(N, (int64_t)SB);
+  if (tiles > 0x7fffffffLL || batch < 1 || batch > 65535) {
+    set_error("gemm64: grid too large");
+    return IFK_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(gemm64_kernel, dim3((unsigned)tiles, (unsigned)batch), dim3(SNT), 0, s, M, N,
+                     K, alpha, A, lda, bsa, tria, B, ldb, bsb, trib, C, ldc, bsc);
+  return check_launch("gemm64");
 }
 
 }  // namespace ifk

@@ -80,12 +80,15 @@ def test_gemm_engine_large_tiles(hip, adt, ta, tb, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(2048, 2560, 512), (600, 520, 4096), (1000, 700, 2048),
-                                   (512, 512, 8192), (256, 384, 16384)])
+                                   (512, 512, 8192), (256, 384, 16384), (4000, 3700, 256),
+                                   (3840, 3840, 1024)])
 @pytest.mark.parametrize("beta", [0.0, 1.0])
 def test_gemm_direct_lds_kernel(hip, m, n, k, beta):
-    """bf16 operands with K contiguous take the direct-to-LDS kernel: ragged M
-    and N (rows past the operand read as zero through the buffer bounds),
-    split-K for few tiles, alpha / beta, against an fp64 product."""
+    """bf16 operands with K contiguous take the direct-to-LDS kernel (its 128
+    tile below 224 tiles of 256, its 256 tile from there: the last two
+    shapes): ragged M and N (rows past the operand read as zero through the
+    buffer bounds), split-K for few tiles, alpha / beta, against an fp64
+    product."""
     g = torch.Generator(device=DEV).manual_seed(m + 5 * n + 3 * k)
     A = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
     B = torch.randn(n, k, device=DEV, generator=g).to(torch.bfloat16)
@@ -96,14 +99,14 @@ def test_gemm_direct_lds_kernel(hip, m, n, k, beta):
 
 
 @pytest.mark.parametrize("tri", ["upper_a", "lower_b"])
-def test_gemm_direct_lds_triangular(hip, tri):
+@pytest.mark.parametrize("n,rows", [(1280, 1100), (4096, 3600)])
+def test_gemm_direct_lds_triangular(hip, tri, n, rows):
     """Triangular bf16 operands (as in the preconditioner) through the
-    direct-to-LDS kernel: the stored zero triangle is filled with garbage,
-    which the kernel must ignore."""
-    n = 1280
+    direct-to-LDS kernel, both tiles: the stored zero triangle is filled with
+    garbage, which the kernel must ignore."""
     g = torch.Generator(device=DEV).manual_seed(42)
     Z = torch.randn(n, n, device=DEV, generator=g)
-    G = torch.randn(1100, n, device=DEV, generator=g).to(torch.bfloat16)
+    G = torch.randn(rows, n, device=DEV, generator=g).to(torch.bfloat16)
     Zt = torch.triu(Z).to(torch.bfloat16)
     noisy = (Zt.float() + torch.tril(torch.randn(n, n, device=DEV, generator=g), -1)).to(
         torch.bfloat16)
