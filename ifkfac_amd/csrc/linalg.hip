@@ -49,11 +49,12 @@ namespace ifk {
 // of orthogonality is far below its own 1/4 pivot threshold.
 static constexpr float HR_TOL = 1e-4f;
 static constexpr int64_t OUTER_B = 512;
-// Workgroup cap of the far-column products on the helper stream (the large
-// tile kernel fits two workgroups per CU, 512 on the chip): the panel
-// kernels of the next outer block keep CUs (and LDS) of their own.  320
-// measured best between 192 and 448 on the 4096 -> 11008, p = 16384 step.
-static constexpr int FAR_MAX_WGS = 320;
+// Workgroup cap of the far-column products on the helper stream: the far
+// update is bound by HBM and runs beside the next block's panels, whose
+// kernels are bound by memory latency and bandwidth too; capped, it leaves
+// them CUs and bandwidth of their own.  128 measured best between 64 and 320
+// on the 4096 -> 11008, p = 16384 step.
+static constexpr int FAR_MAX_WGS = 128;
 
 static size_t split_floats(int64_t b, int64_t n) {
   size_t f = (size_t)64 * b * n;
