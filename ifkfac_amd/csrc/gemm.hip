@@ -569,6 +569,9 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     const int64_t per_z = std::max<int64_t>(1, max_wgs / std::max<int64_t>(1, batch * splits));
     gx = (unsigned)std::min<int64_t>(gx, per_z);
   }
+  // the direct-to-LDS kernel orders its tiles by XCD when a z slice has a
+  // multiple of eight workgroups (the rest of the tiles go grid-stride)
+  if (bb && gx > 8) gx &= ~7u;
   dim3 grid(gx, 1, (unsigned)(batch * splits));
   const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | ((big ? 1 : 0) << 5) |
                   ((bb ? 1 : 0) << 6) | ((mid ? 1 : 0) << 7);

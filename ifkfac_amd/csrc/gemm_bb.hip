@@ -127,14 +127,13 @@ __device__ __forceinline__ void wait_vm(int ahead) {
 }
 
 template <class CF>
-__device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* smem) {
+__device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf16_t* smem) {
   constexpr int BM = CF::BM, BN = CF::BN, FM = CF::FM, FN = CF::FN;
   constexpr int STAGE = CF::STAGE, SLAB_A = CF::SLAB_A;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave / CF::WAVES_N, wn = wave % CF::WAVES_N;
   const int l32 = lane & 31, h = lane >> 5;
-  const int tm = tile % p.tiles_m, tn = tile / p.tiles_m;
   const int z = blockIdx.z;
   const int bidx = z / p.splits, split = z % p.splits;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -260,14 +259,37 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tile, bf16_t* s
     }
 }
 
-// Tiles visited grid-stride (a launch may use fewer workgroups than tiles).
+// Tile order.  Workgroups go to the eight XCDs round-robin by their linear
+// id, and each XCD has its own L2, so with a multiple of eight workgroups per
+// z slice (workgroup x runs on XCD x % 8) XCD c takes the c-th eighth of the
+// tiles in grouped order -- bands of XCD_GM tile rows, walked down the band
+// first -- and its workgroups step through that range together: the tiles
+// in flight on one XCD share a few row and column operand strips, which stay
+// in its L2 instead of being fetched again for every tile.  Other grids visit
+// tiles grid-stride in column-major order.
+constexpr int XCD_GM = 8;
+
 template <class CF>
 __global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(16))) bf16_t smem_bb[STAGES * CF::STAGE];
-  const int tiles = p.tiles_m * p.tiles_n;
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    bb_tile<CF>(p, tile, smem_bb);
-    __syncthreads();   // the LDS ring is reused by the next tile
+  const int tiles_m = p.tiles_m, tiles_n = p.tiles_n;
+  const int tiles = tiles_m * tiles_n;
+  if ((gridDim.x & 7) == 0) {
+    const int c = blockIdx.x & 7, nl = gridDim.x >> 3;
+    const int per = (tiles + 7) >> 3;
+    const int l1 = min(tiles, (c + 1) * per);
+    for (int l = c * per + (int)(blockIdx.x >> 3); l < l1; l += nl) {
+      const int g = l / (XCD_GM * tiles_n);              // band of tile rows
+      const int rows = min(XCD_GM, tiles_m - g * XCD_GM);
+      const int r = l - g * XCD_GM * tiles_n;
+      bb_tile<CF>(p, g * XCD_GM + r % rows, r / rows, smem_bb);
+      __syncthreads();   // the LDS ring is reused by the next tile
+    }
+  } else {
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+      bb_tile<CF>(p, tile % tiles_m, tile / tiles_m, smem_bb);
+      __syncthreads();
+    }
   }
 }
 
