@@ -265,8 +265,10 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
 // tiles in grouped order -- bands of XCD_GM tile rows, walked down the band
 // first -- and its workgroups step through that range together: the tiles
 // in flight on one XCD share a few row and column operand strips, which stay
-// in its L2 instead of being fetched again for every tile.  Other grids visit
-// tiles grid-stride in column-major order.
+// in its L2 instead of being fetched again for every tile.  Other grids, and
+// products with a triangular operand (whose tiles differ in K range, so
+// contiguous ranges would load some XCDs more than others), visit tiles
+// grid-stride in column-major order.
 constexpr int XCD_GM = 8;
 
 template <class CF>
@@ -274,7 +276,7 @@ __global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p)
   __shared__ __attribute__((aligned(16))) bf16_t smem_bb[STAGES * CF::STAGE];
   const int tiles_m = p.tiles_m, tiles_n = p.tiles_n;
   const int tiles = tiles_m * tiles_n;
-  if ((gridDim.x & 7) == 0) {
+  if ((gridDim.x & 7) == 0 && p.tria == TRI_NONE && p.trib == TRI_NONE) {
     const int c = blockIdx.x & 7, nl = gridDim.x >> 3;
     const int per = (tiles + 7) >> 3;
     const int l1 = min(tiles, (c + 1) * per);

@@ -49,10 +49,12 @@ int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float*
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
 int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
                       float* Z, int64_t ldz, int safe);
-// Diagonal nb x nb blocks of T = (striu(G) + diag(1 + diag G) / 2)^{-1}, the T
-// factor of a block of reflectors [I; Y] from their Gram matrix G = Y^T Y
-int launch_ut_trinv_diag(hipStream_t s, const float* G, int64_t ldg, int64_t n, int nb, float* T,
-                         int64_t ldt);
+// Diagonal 128 x 128 blocks of R^{-1} (R upper triangular, or with ut the UT
+// transform striu(G) + diag(1 + diag G) / 2 of a reflector Gram matrix G =
+// Y^T Y, whose inverse is the T factor of the reflectors [I; Y]); the last
+// block may be ragged
+int launch_trinv_diag128(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
+                         int64_t ldz, int safe, int ut);
 // C_b = alpha A_b B_b, fp32 row-major, 64 x 64 tiles (small products)
 int launch_gemm64(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
                   int64_t lda, int64_t bsa, int tria, const float* B, int64_t ldb, int64_t bsb,

@@ -81,6 +81,8 @@ struct FoldWs {
                     // to bf16 anyway)
   float* Wpn;     // OUTER_B x OUTER_B: CT_cols Y + R_blk^T of the near columns
   float* Wpf;     // n x OUTER_B: ... of the far columns
+  bf16_t* Wpnb;   // bf16 copies of Wpn, Wpf (bf16 arithmetic)
+  bf16_t* Wpfb;
   float* Wn;      // OUTER_B x OUTER_B: W^T of the near columns (critical stream)
   float* Wf;      // n x OUTER_B: W^T of the far columns (helper stream)
   bf16_t* Wnb;
@@ -95,6 +97,7 @@ struct FoldWs {
   float* N;
   float* Go;      // OUTER_B x OUTER_B: Gram of the outer reflectors (upper part)
   float* To[2];   // OUTER_B x OUTER_B: T of an outer block (by block parity)
+  bf16_t* ToTb[2];  // its transpose in bf16 (bf16 arithmetic)
   float* ttmp;    // triangular-inverse scratch for To
   SplitScratch tsp;
   int* flag;
@@ -111,9 +114,12 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
     w.Yob[i] = a.take<bf16_t>((size_t)p * B);
     w.YobT[i] = a.take<bf16_t>((size_t)p * B);
     w.To[i] = a.take<float>(B * B);
+    w.ToTb[i] = a.take<bf16_t>(B * B);
   }
   w.Wpn = a.take<float>((size_t)B * B);
   w.Wpf = a.take<float>((size_t)B * n);
+  w.Wpnb = a.take<bf16_t>((size_t)B * B);
+  w.Wpfb = a.take<bf16_t>((size_t)B * n);
   w.Wn = a.take<float>((size_t)B * B);
   w.Wf = a.take<float>((size_t)B * n);
   w.Wnb = a.take<bf16_t>((size_t)B * B);
@@ -206,7 +212,9 @@ static int outer_prepare(hipStream_t s, int math, FoldWs& w, int k2, int64_t pe,
   const MatRef YA = bf ? A_n(w.YobT[k2], DT_BF16, ldt) : A_t(w.Yo[k2], DT_F32, B);
   const MatRef YB = bf ? B_t(w.YobT[k2], DT_BF16, ldt) : B_n(w.Yo[k2], DT_F32, B);
   RC(gemm(s, math, KB, KB, pe, 1.0f, YA, YB, 0.0f, out_f32(w.Go, B), 1, w.split));
-  return trinv_core(s, w.Go, DT_F32, B, KB, w.To[k2], B, MATH_F32, 0, w.ttmp, w.tsp, true);
+  RC(trinv_core(s, w.Go, DT_F32, B, KB, w.To[k2], B, MATH_F32, 0, w.ttmp, w.tsp, true));
+  // T^T in bf16: the product W^T = Wp T then reads both operands K-contiguous
+  return bf ? launch_transpose_cast(s, w.To[k2], B, KB, KB, w.ToTb[k2], DT_BF16, B) : IFK_OK;
 }
 
 // Apply outer block k to the columns [c_lo, c_hi) of C, i.e. the rows
@@ -218,7 +226,7 @@ static int outer_prepare(hipStream_t s, int math, FoldWs& w, int k2, int64_t pe,
 // W^T is nt x KB.
 static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
                        int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1,
-                       int64_t c_lo, int64_t c_hi, float* Wp, float* W, bf16_t* Wb,
+                       int64_t c_lo, int64_t c_hi, float* Wp, bf16_t* Wpb, float* W, bf16_t* Wb,
                        SplitScratch sp, int max_wgs, hipEvent_t t_ready) {
   const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
   if (nt <= 0) return IFK_OK;
@@ -229,10 +237,13 @@ static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf
   RC(launch_transpose_to_f32(s, Rb, DT_F32, ldr, KB, nt, Wp, KB));
   const MatRef CA = Crb ? A_n(Crb, DT_BF16, ldc) : A_n(Cr, DT_F32, ldc);
   const MatRef YB = bf ? B_t(w.YobT[k2], DT_BF16, ldc) : B_n(w.Yo[k2], DT_F32, B);
-  RC(gemm(s, math, nt, KB, pe, 1.0f, CA, YB, 1.0f, out_f32(Wp, KB), 1, sp, max_wgs));
+  RC(gemm(s, math, nt, KB, pe, 1.0f, CA, YB, 1.0f, bf ? out_both(Wp, KB, Wpb, KB) : out_f32(Wp, KB),
+          1, sp, max_wgs));
   if (t_ready) HIPRC(hipStreamWaitEvent(s, t_ready, 0), "tsqr_fold: stream wait failed");
-  RC(gemm(s, math, nt, KB, KB, 1.0f, A_n(Wp, DT_F32, KB), B_n(w.To[k2], DT_F32, B, TRI_UPPER),
-          0.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB), 1, sp, max_wgs));
+  const MatRef WpA = bf ? A_n(Wpb, DT_BF16, KB) : A_n(Wp, DT_F32, KB);
+  const MatRef TB = bf ? B_t(w.ToTb[k2], DT_BF16, B, TRI_UPPER) : B_n(w.To[k2], DT_F32, B, TRI_UPPER);
+  RC(gemm(s, math, nt, KB, KB, 1.0f, WpA, TB, 0.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB),
+          1, sp, max_wgs));
   RC(launch_sub_transposed(s, Rb, ldr, W, KB, KB, nt));
   const MatRef WA = bf ? A_n(Wb, DT_BF16, KB) : A_n(W, DT_F32, KB);
   const MatRef YoBt = bf ? B_t(w.Yob[k2], DT_BF16, B) : B_t(w.Yo[k2], DT_F32, B);
@@ -333,10 +344,10 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
       HIPRC(hipEventRecord(la->tready[k2], s), "tsqr_fold: event record failed");
       const int64_t mid = std::min<int64_t>(near_hi + B, n);
       RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wpf,
-                     w.Wf, w.Wfb, w.split2, FAR_MAX_WGS, la->tready[k2]));
+                     w.Wpfb, w.Wf, w.Wfb, w.split2, FAR_MAX_WGS, la->tready[k2]));
       HIPRC(hipEventRecord(la->far[k2], la->s2), "tsqr_fold: event record failed");
-      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wpf, w.Wf,
-                     w.Wfb, w.split2, FAR_MAX_WGS, nullptr));
+      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wpf, w.Wpfb,
+                     w.Wf, w.Wfb, w.split2, FAR_MAX_WGS, nullptr));
       HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
       fall_pending[k2] = true;
       HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
@@ -348,11 +359,11 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     }
     if (far) far_pending = k2;
     if (la)
-      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wpn, w.Wn,
-                     w.Wnb, w.split, 0, nullptr));
+      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wpn, w.Wpnb,
+                     w.Wn, w.Wnb, w.split, 0, nullptr));
     else
-      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf, w.Wf, w.Wfb,
-                     w.split, 0, nullptr));
+      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf, w.Wpfb, w.Wf,
+                     w.Wfb, w.split, 0, nullptr));
   }
   if (la) HIPRC(hipStreamWaitEvent(s, la->done, 0), "tsqr_fold: stream wait failed");
   return launch_sign_normalize(s, R, ldr, r_new, n);
@@ -511,10 +522,11 @@ size_t trinv_ws(int64_t n) {
   return a.used;
 }
 
-// Z = R^{-1} for upper-triangular R (n x n): diagonal 64-blocks, then block
-// doubling, Z12 = -Z11 (R12 Z22).  With ut, R holds a reflector Gram matrix G
-// and the inverted matrix is its UT transform striu(G) + diag(1 + diag G) / 2
-// (whose off-diagonal blocks are G's).  fp32 levels up to 256 wide run on the
+// Z = R^{-1} for upper-triangular R (n x n): diagonal 128-blocks (two 64
+// blocks and their coupling, in LDS), then block doubling,
+// Z12 = -Z11 (R12 Z22).  With ut, R holds a reflector Gram matrix G and the
+// inverted matrix is its UT transform striu(G) + diag(1 + diag G) / 2 (whose
+// off-diagonal blocks are G's).  fp32 levels up to 256 wide run on the
 // 64-tile kernel, the rest on the GEMM engine.
 static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
                       int64_t ldz, int math, int safe, float* tmp, SplitScratch sp, bool ut) {
@@ -525,9 +537,8 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
     return IFK_ERR_INVALID;
   }
   RC(launch_zero(s, Z, ldz, n, n));
-  if (ut) RC(launch_ut_trinv_diag(s, (const float*)R, ldr, n, TRINV_NB, Z, ldz));
-  else RC(launch_trinv_diag(s, R, rdt, ldr, n, TRINV_NB, Z, ldz, safe));
-  for (int64_t w = TRINV_NB; w < n; w *= 2) {
+  RC(launch_trinv_diag128(s, R, rdt, ldr, n, Z, ldz, safe, ut ? 1 : 0));
+  for (int64_t w = 2 * TRINV_NB; w < n; w *= 2) {
     const int64_t step = 2 * w;
     const int64_t nfull = n / step;
     const bool small = math == MATH_F32 && rdt == DT_F32 && w <= 256;

@@ -655,14 +655,11 @@ __global__ void ut_tinv_kernel(const float* G, int64_t ldg, int64_t n, float* Ti
 // ---------------------------------------------------------------------------
 // Diagonal blocks of a blocked triangular inverse: Z_kk = R_kk^{-1} for every
 // nb x nb block on the diagonal of an upper-triangular R (last block may be
-// ragged).  One workgroup per block.  With ut, R holds a reflector Gram
-// matrix G and the inverted matrix is its UT transform
-// striu(G) + diag(1 + diag G) / 2.
+// ragged).  One workgroup per block.
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t ldr, int64_t n,
-                                                         int nb, float* Z, int64_t ldz, int safe,
-                                                         int ut) {
+                                                         int nb, float* Z, int64_t ldz, int safe) {
   __shared__ float sU[SB * SLD];
   __shared__ float sZ[SB * SLD];
   __shared__ float sT[TRINV_TMP];
@@ -673,14 +670,12 @@ __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t 
 #pragma unroll
     for (int q = 0; q < SB * SB / SNT; ++q) {
       const int e = threadIdx.x + SNT * q, r = e >> 6, c = e & 63;
-      if (r < b && c < b) {
+      if (r < b && c < b)
         v[q] = (r <= c)
                    ? Elem<DT>::load((const typename Elem<DT>::T*)R + (k0 + r) * ldr + k0 + c)
                    : 0.0f;
-        if (ut && r == c) v[q] = 0.5f * (1.0f + v[q]);
-      } else {
+      else
         v[q] = (r == c) ? 1.0f : 0.0f;
-      }
     }
 #pragma unroll
     for (int q = 0; q < SB * SB / SNT; ++q) {
@@ -693,6 +688,66 @@ __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t 
   for (int e = threadIdx.x; e < b * b; e += SNT) {
     const int r = e / b, c = e - r * b;
     Z[(k0 + r) * ldz + k0 + c] = sZ[r * SLD + c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Diagonal 128 x 128 blocks of a blocked triangular inverse, one workgroup
+// per block (the last may be ragged): the two 64-blocks in LDS, then
+// Z12 = -Z11 (R12 Z22), so the doubling levels of trinv_core start at 128.
+// With ut, R holds a reflector Gram matrix G and the inverted matrix is its
+// UT transform striu(G) + diag(1 + diag G) / 2.
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ void load_blk(float* S, const void* R, int64_t ldr, int64_t r0,
+                                         int64_t c0, int rows, int cols, bool diag, int ut) {
+  float v[SB * SB / SNT];
+#pragma unroll
+  for (int q = 0; q < SB * SB / SNT; ++q) {
+    const int e = threadIdx.x + SNT * q, r = e >> 6, c = e & 63;
+    if (r < rows && c < cols) {
+      v[q] = (!diag || r <= c)
+                 ? Elem<DT>::load((const typename Elem<DT>::T*)R + (r0 + r) * ldr + c0 + c)
+                 : 0.0f;
+      if (diag && ut && r == c) v[q] = 0.5f * (1.0f + v[q]);
+    } else {
+      v[q] = (diag && r == c) ? 1.0f : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < SB * SB / SNT; ++q) {
+    const int e = threadIdx.x + SNT * q;
+    S[(e >> 6) * SLD + (e & 63)] = v[q];
+  }
+  __syncthreads();
+}
+
+template <int DT>
+__global__ __launch_bounds__(SNT) void trinv_diag128_kernel(const void* R, int64_t ldr, int64_t n,
+                                                            float* Z, int64_t ldz, int safe,
+                                                            int ut) {
+  __shared__ float sA[SB * SLD];
+  __shared__ float sZ1[SB * SLD];
+  __shared__ float sZ2[SB * SLD];
+  __shared__ float sX[SB * SLD];
+  __shared__ float sT[TRINV_TMP];
+  const int64_t k0 = (int64_t)blockIdx.x * (2 * SB);
+  const int bt = (int)((n - k0) < 2 * SB ? (n - k0) : 2 * SB);
+  const int b1 = bt < SB ? bt : SB, b2 = bt - b1;
+  load_blk<DT>(sA, R, ldr, k0, k0, b1, b1, true, ut);
+  sm_trinv64(sA, sZ1, sT, safe != 0);
+  if (b2 > 0) {
+    load_blk<DT>(sA, R, ldr, k0 + SB, k0 + SB, b2, b2, true, ut);
+    sm_trinv64(sA, sZ2, sT, safe != 0);
+    load_blk<DT>(sA, R, ldr, k0, k0 + SB, b1, b2, false, 0);   // R12 (b1 x b2)
+    sm_gemm64<false, false>(sA, sZ2, sX, 1.0f, false);          // X = R12 Z22
+    sm_gemm64<false, false>(sZ1, sX, sA, -1.0f, false);         // Z12 = -Z11 X
+  }
+  for (int e = threadIdx.x; e < SB * SB; e += SNT) {
+    const int r = e >> 6, c = e & 63;
+    if (r < b1 && c < b1) Z[(k0 + r) * ldz + k0 + c] = sZ1[r * SLD + c];
+    if (r < b2 && c < b2) Z[(k0 + SB + r) * ldz + k0 + SB + c] = sZ2[r * SLD + c];
+    if (r < b1 && c < b2) Z[(k0 + r) * ldz + k0 + SB + c] = sA[r * SLD + c];
   }
 }
 
@@ -732,12 +787,13 @@ __global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64
 #pragma unroll
   for (int i = 0; i < 16; ++i) d[i] = 0.0f;
   constexpr int PER = SB * SB / SNT;
-  for (int64_t kc = (klo / SB) * SB; kc < khi; kc += SB) {
-    float va[PER], vb[PER];
+  float va[PER], vb[PER];
+  // chunk kc of A (rows m0.., columns kc..) and B (rows kc.., columns n0..)
+  // into registers; the next chunk's loads fly while this one multiplies
+  auto fetch = [&](int64_t kc) {
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int e = t + SNT * q, i = e >> 6, j = e & 63;
-      // A chunk: row m0 + i, column kc + j;  B chunk: row kc + i, column n0 + j
       const int64_t ar = m0 + i, ak = kc + j, bk = kc + i, bc = n0 + j;
       bool oka = ar < M && ak < khi && ak >= klo;
       if (tria == TRI_UPPER) oka = oka && ak >= ar;
@@ -748,6 +804,10 @@ __global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64
       va[q] = oka ? A[ar * lda + ak] : 0.0f;
       vb[q] = okb ? B[bk * ldb + bc] : 0.0f;
     }
+  };
+  int64_t kc = (klo / SB) * SB;
+  if (kc < khi) fetch(kc);
+  for (; kc < khi; kc += SB) {
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int e = t + SNT * q;
@@ -755,6 +815,7 @@ __global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64
       sB[(e >> 6) * SLD + (e & 63)] = vb[q];
     }
     __syncthreads();
+    if (kc + SB < khi) fetch(kc + SB);
 #pragma unroll
     for (int st = 0; st < 32; ++st) {
       const int k = 32 * h + st;
@@ -824,20 +885,24 @@ int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
   const unsigned nblk = (unsigned)cdiv(n, nb);
   if (rdt == DT_F32)
     hipLaunchKernelGGL(trinv_diag_kernel<DT_F32>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, nb, Z,
-                       ldz, safe, 0);
+                       ldz, safe);
   else
     hipLaunchKernelGGL(trinv_diag_kernel<DT_BF16>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, nb, Z,
-                       ldz, safe, 0);
+                       ldz, safe);
   return check_launch("trinv_diag");
 }
 
-int launch_ut_trinv_diag(hipStream_t s, const float* G, int64_t ldg, int64_t n, int nb, float* T,
-                         int64_t ldt) {
-  if (int rc = check_b(nb, "ut_trinv_diag")) return rc;
+int launch_trinv_diag128(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
+                         int64_t ldz, int safe, int ut) {
   if (n <= 0) return IFK_OK;
-  hipLaunchKernelGGL(trinv_diag_kernel<DT_F32>, dim3((unsigned)cdiv(n, (int64_t)nb)), dim3(SNT), 0, s,
-                     G, ldg, n, nb, T, ldt, 0, 1);
-  return check_launch("ut_trinv_diag");
+  const unsigned nblk = (unsigned)cdiv(n, (int64_t)(2 * SB));
+  if (rdt == DT_F32)
+    hipLaunchKernelGGL(trinv_diag128_kernel<DT_F32>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, Z, ldz,
+                       safe, ut);
+  else
+    hipLaunchKernelGGL(trinv_diag128_kernel<DT_BF16>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, Z, ldz,
+                       safe, ut);
+  return check_launch("trinv_diag128");
 }
 
 int launch_gemm64(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const float* A,

@@ -98,7 +98,7 @@ def test_gemm_direct_lds_kernel(hip, m, n, k, beta):
     assert _rel(C, ref.cpu().numpy()) < 2e-6
 
 
-@pytest.mark.parametrize("tri", ["upper_a", "lower_b"])
+@pytest.mark.parametrize("tri", ["upper_a", "lower_b", "upper_b"])
 @pytest.mark.parametrize("n,rows", [(1280, 1100), (4096, 3600)])
 def test_gemm_direct_lds_triangular(hip, tri, n, rows):
     """Triangular bf16 operands (as in the preconditioner) through the
@@ -114,10 +114,17 @@ def test_gemm_direct_lds_triangular(hip, tri, n, rows):
         # C = U G^T: op(A) = U upper triangular, B = G stored (n_rows x K)
         ref = Zt.double() @ G.double().t()
         C = hip.gemm(noisy, G, False, True, 1, tri_a=1)
-    else:
+    elif tri == "lower_b":
         # C = G U^T: op(B) = U^T lower triangular, given as B[n][k] = U
         ref = G.double() @ Zt.double().t()
         C = hip.gemm(G, noisy, False, True, 1, tri_b=2)
+    else:
+        # C = G U: op(B) = U upper triangular, given as B[n][k] = U^T (the
+        # layout of the fold's T^T), garbage above its diagonal
+        ref = G.double() @ Zt.double()
+        noisyT = (Zt.float().t() + torch.triu(torch.randn(n, n, device=DEV, generator=g), 1)).to(
+            torch.bfloat16).contiguous()
+        C = hip.gemm(G, noisyT, False, True, 1, tri_b=1)
     assert _rel(C, ref.cpu().numpy()) < 2e-6
 
 
