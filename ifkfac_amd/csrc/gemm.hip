@@ -426,8 +426,15 @@ __global__ void splitk_reduce_kernel(GemmParams p) {
   bf16_t* Cbp = p.Cb ? p.Cb + (size_t)bidx * p.bscb : nullptr;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < MN;
        e += (int64_t)gridDim.x * blockDim.x) {
+    // eight partials in flight at a time, added in split order
     float s = 0.0f;
-    for (int sp = 0; sp < p.splits; ++sp) s += P[(size_t)sp * MN + e];
+    for (int sp0 = 0; sp0 < p.splits; sp0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = (sp0 + u < p.splits) ? P[(size_t)(sp0 + u) * MN + e] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
     const int64_t row = e / p.N, col = e % p.N;
     float v = p.alpha * s;
     if (p.beta != 0.0f) v += p.beta * Cp[row * p.ldc + col];

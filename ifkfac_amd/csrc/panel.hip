@@ -152,25 +152,43 @@ __global__ __launch_bounds__(PNT) void gram_partial_kernel(const float* A, int64
   for (int r = 0; r < 16; ++r) out[acc_row(r) * PT + jc] = d[r];
 }
 
-// G[cb * 4096 + e] = sum over s < nslab of part[(s * ncb + cb) * 4096 + e],
-// in slab order (deterministic).
+// G[cb * 4096 + e] = sum over s < nslab of part[(s * ncb + cb) * 4096 + e].
+// A workgroup takes 32 consecutive elements; its eight 32-lane groups sum
+// the slabs g, g + 8, g + 16, ... (all loads of a lane issued together), and
+// the eight group sums are added in group order: a fixed association, so the
+// result is deterministic, with one memory latency per element instead of
+// nslab / 8.
+constexpr int GR_E = 32, GR_G = PNT / GR_E;
 __global__ __launch_bounds__(PNT) void gram_reduce_kernel(const float* part, int nslab, int ncb,
                                                           float* G) {
-  const int64_t idx = (int64_t)blockIdx.x * PNT + threadIdx.x;   // over ncb * 4096
-  if (idx >= (int64_t)ncb * PT * PT) return;
-  const int64_t cb = idx / (PT * PT), e = idx % (PT * PT);
-  const float* p0 = part + cb * (PT * PT) + e;
-  const int64_t stride = (int64_t)ncb * PT * PT;
-  float acc[8];
+  __shared__ float acc_s[GR_G][GR_E];
+  const int el = threadIdx.x % GR_E, g = threadIdx.x / GR_E;
+  const int64_t idx = (int64_t)blockIdx.x * GR_E + el;   // over ncb * 4096
+  const int64_t total = (int64_t)ncb * PT * PT;
+  float acc = 0.0f;
+  if (idx < total) {
+    const int64_t cb = idx / (PT * PT), e = idx % (PT * PT);
+    const float* p0 = part + cb * (PT * PT) + e;
+    const int64_t stride = (int64_t)ncb * PT * PT;
+    float v[8];
+    for (int s0 = g; s0 < nslab; s0 += 8 * GR_G) {
 #pragma unroll
-  for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
-  int sl = 0;
-  for (; sl + 8 <= nslab; sl += 8) {
+      for (int u = 0; u < 8; ++u) {
+        const int sl = s0 + u * GR_G;
+        v[u] = sl < nslab ? p0[(int64_t)sl * stride] : 0.0f;
+      }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc[u] += p0[(int64_t)(sl + u) * stride];
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
   }
-  for (int u = 0; sl < nslab; ++sl, ++u) acc[u] += p0[(int64_t)sl * stride];
-  G[idx] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  acc_s[g][el] = acc;
+  __syncthreads();
+  if (g == 0 && idx < total) {
+    float sum = acc_s[0][el];
+#pragma unroll
+    for (int q = 1; q < GR_G; ++q) sum += acc_s[q][el];
+    G[idx] = sum;
+  }
 }
 
 // Q2[r][:] = X_p[r][0:b] M (M b x b in ld b), r < pe, Q2 of ld 64 (columns >=
@@ -332,8 +350,8 @@ int launch_gram(hipStream_t s, const float* A, int64_t lda, int ka, bool a_ts, c
                        ldb0, w0, B1, ldb1, w1, pe, part, ncb);
   if (int rc = check_launch("gram_partial")) return rc;
   const int64_t total = (int64_t)ncb * PT * PT;
-  hipLaunchKernelGGL(gram_reduce_kernel, dim3((unsigned)cdiv(total, (int64_t)PNT)), dim3(PNT), 0, s,
-                     part, ns, ncb, G);
+  hipLaunchKernelGGL(gram_reduce_kernel, dim3((unsigned)cdiv(total, (int64_t)GR_E)), dim3(PNT), 0,
+                     s, part, ns, ncb, G);
   return check_launch("gram_reduce");
 }
 
