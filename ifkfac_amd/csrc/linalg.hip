@@ -151,9 +151,9 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
 struct LookAhead {
   std::mutex mu;
   hipStream_t s2 = nullptr;                 // far updates
-  hipEvent_t ready[2] = {nullptr, nullptr};
-  hipEvent_t far[2] = {nullptr, nullptr};   // the next outer block's columns are done
-  hipEvent_t fall[2] = {nullptr, nullptr};  // all of the block's far update is done
+  hipEvent_t ready[2] = {nullptr, nullptr};   // the outer block's reflectors are written
+  hipEvent_t nearwp[2] = {nullptr, nullptr};  // Wp of the next block's columns is formed
+  hipEvent_t fall[2] = {nullptr, nullptr};    // all of the block's far update is done
   hipEvent_t done = nullptr;                // everything queued on s2 so far
   hipEvent_t tready[2] = {nullptr, nullptr};  // T of the outer block is complete
 };
@@ -177,7 +177,7 @@ static LookAhead* look_ahead(hipStream_t s, int* rc) {
               hipEventCreateWithFlags(&x->done, hipEventDisableTiming) == hipSuccess;
     for (int i = 0; i < 2 && ok; ++i)
       ok = hipEventCreateWithFlags(&x->ready[i], hipEventDisableTiming) == hipSuccess &&
-           hipEventCreateWithFlags(&x->far[i], hipEventDisableTiming) == hipSuccess &&
+           hipEventCreateWithFlags(&x->nearwp[i], hipEventDisableTiming) == hipSuccess &&
            hipEventCreateWithFlags(&x->fall[i], hipEventDisableTiming) == hipSuccess &&
            hipEventCreateWithFlags(&x->tready[i], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
@@ -218,28 +218,37 @@ static int outer_prepare(hipStream_t s, int math, FoldWs& w, int k2, int64_t pe,
 }
 
 // Apply outer block k to the columns [c_lo, c_hi) of C, i.e. the rows
-// [c_lo, c_hi) of the transposed working matrix CT (ld ldc):
-//   Wp = CT_cols Y + R_blk^T,   W^T = Wp T,   R_blk -= W,   CT_cols -= W^T Y^T
-// Wp does not need T, so it is formed first; t_ready (when given) is waited
-// for before the product with T.  The large products read K-contiguous
-// operands only (CT or its bf16 shadow, the transposed bf16 copy of Y).
-// W^T is nt x KB.
-static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
-                       int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1,
-                       int64_t c_lo, int64_t c_hi, float* Wp, bf16_t* Wpb, float* W, bf16_t* Wb,
-                       SplitScratch sp, int max_wgs, hipEvent_t t_ready) {
+// [c_lo, c_hi) of the transposed working matrix CT (ld ldc), in two halves:
+//   outer_wp:     Wp = CT_cols Y + R_blk^T          (does not need T)
+//   outer_finish: W^T = Wp T,  R_blk -= W,  CT_cols -= W^T Y^T
+// The large products read K-contiguous operands only (CT or its bf16
+// shadow, the transposed bf16 copy of Y).  Wp and W^T are nt x KB.
+static int outer_wp(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
+                    int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1,
+                    int64_t c_lo, int64_t c_hi, float* Wp, bf16_t* Wpb, SplitScratch sp,
+                    int max_wgs) {
+  const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
+  if (nt <= 0) return IFK_OK;
+  const bool bf = math == MATH_BF16;
+  float* Cr = CT + c_lo * ldc;
+  bf16_t* Crb = CTb ? CTb + c_lo * ldc : nullptr;   // bf16 shadow (bf16 arithmetic)
+  RC(launch_transpose_to_f32(s, R + K0 * ldr + c_lo, DT_F32, ldr, KB, nt, Wp, KB));
+  const MatRef CA = Crb ? A_n(Crb, DT_BF16, ldc) : A_n(Cr, DT_F32, ldc);
+  const MatRef YB = bf ? B_t(w.YobT[k2], DT_BF16, ldc) : B_n(w.Yo[k2], DT_F32, B);
+  return gemm(s, math, nt, KB, pe, 1.0f, CA, YB, 1.0f,
+              bf ? out_both(Wp, KB, Wpb, KB) : out_f32(Wp, KB), 1, sp, max_wgs);
+}
+
+static int outer_finish(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
+                        int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1,
+                        int64_t c_lo, int64_t c_hi, const float* Wp, const bf16_t* Wpb, float* W,
+                        bf16_t* Wb, SplitScratch sp, int max_wgs) {
   const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
   if (nt <= 0) return IFK_OK;
   const bool bf = math == MATH_BF16;
   float* Rb = R + K0 * ldr + c_lo;
   float* Cr = CT + c_lo * ldc;
-  bf16_t* Crb = CTb ? CTb + c_lo * ldc : nullptr;   // bf16 shadow (bf16 arithmetic)
-  RC(launch_transpose_to_f32(s, Rb, DT_F32, ldr, KB, nt, Wp, KB));
-  const MatRef CA = Crb ? A_n(Crb, DT_BF16, ldc) : A_n(Cr, DT_F32, ldc);
-  const MatRef YB = bf ? B_t(w.YobT[k2], DT_BF16, ldc) : B_n(w.Yo[k2], DT_F32, B);
-  RC(gemm(s, math, nt, KB, pe, 1.0f, CA, YB, 1.0f, bf ? out_both(Wp, KB, Wpb, KB) : out_f32(Wp, KB),
-          1, sp, max_wgs));
-  if (t_ready) HIPRC(hipStreamWaitEvent(s, t_ready, 0), "tsqr_fold: stream wait failed");
+  bf16_t* Crb = CTb ? CTb + c_lo * ldc : nullptr;
   const MatRef WpA = bf ? A_n(Wpb, DT_BF16, KB) : A_n(Wp, DT_F32, KB);
   const MatRef TB = bf ? B_t(w.ToTb[k2], DT_BF16, B, TRI_UPPER) : B_n(w.To[k2], DT_F32, B, TRI_UPPER);
   RC(gemm(s, math, nt, KB, KB, 1.0f, WpA, TB, 0.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB),
@@ -257,15 +266,17 @@ static int outer_apply(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf
 // 64-column panels inside 512-column outer blocks; a panel's reflectors
 // update only the rest of its outer block, and each finished outer block is
 // applied to the columns beyond it as one block reflector.  Look-ahead: of
-// that application only the next outer block's columns stay on the critical
-// stream s; the columns beyond run on the device's helper stream and overlap
-// the next block's panels (which are latency-bound on a few CUs).  The
-// application's large product CT_cols Y does not need T, so the helper starts
-// it as soon as the block's reflectors are written, while s forms T.  Buffers
-// a far update still reads are double buffered by block parity, and events
-// order
-//   panels(k) -> far(k) -> [T(k) on s];  far(k-1) -> near(k);
-//   far(last) -> end of fold.
+// that application only the T-dependent half for the next outer block's
+// columns stays on the critical stream s; the rest runs on the device's
+// helper stream and overlaps the next block's panels (which are latency-bound
+// on a few CUs).  The application's large product CT_cols Y does not need T,
+// so the helper forms it for every column beyond the block (the next block's
+// first) as soon as the block's reflectors are written, while s forms T.
+// Buffers a far update still reads are double buffered by block parity, and
+// events order
+//   panels(k) -> helper Wp(k);  T(k) on s -> helper finish(k);
+//   helper near Wp(k) (after everything earlier on the helper) -> near(k);
+//   far(k - 2) -> panels(k);  far(last) -> end of fold.
 // With x_tri, C is upper triangular and a panel ending at column c1
 // involves C rows [0, c1).
 static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n, float* R,
@@ -285,7 +296,6 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
   // keep current; it is seeded here once
   bf16_t* Cb = (bf && w.Cb && std::min<int64_t>(OUTER_B, r_new) < n) ? w.Cb : nullptr;
   if (Cb) RC(launch_cast(s, C, ldc, n, p, Cb, DT_BF16, ldc));
-  int far_pending = -1;              // parity of the last far update not yet joined
   bool fall_pending[2] = {false, false};   // a far update still reads parity buffers
   int k = 0;
   for (int64_t K0 = 0; K0 < r_new; K0 += B, ++k) {
@@ -331,39 +341,50 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     if (!outer) continue;
     const int64_t near_hi = std::min<int64_t>(K1 + B, n);
     const bool far = la && near_hi < n;
-    if (far) {
+    const int64_t mid = std::min<int64_t>(near_hi + B, n);
+    const int64_t ntA = mid - near_hi;   // far part A: the block after next
+    if (la) {
+      // the T-independent half on the helper stream, from the moment the
+      // block's reflectors are written, while s forms T: the near columns
+      // first (s takes them back), then far part A and the rest beyond
       HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
       HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
+      RC(outer_wp(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wpn,
+                  w.Wpnb, w.split2, 0));
+      HIPRC(hipEventRecord(la->nearwp[k2], la->s2), "tsqr_fold: event record failed");
+      if (far) {
+        RC(outer_wp(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wpf,
+                    w.Wpfb, w.split2, FAR_MAX_WGS));
+        RC(outer_wp(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n,
+                    w.Wpf + ntA * KB, w.Wpfb + ntA * KB, w.split2, FAR_MAX_WGS));
+      }
     }
     RC(outer_prepare(s, math, w, k2, pe_o, ldc, KB));
     if (far) {
-      // far columns on the helper stream, from the moment the block's
-      // reflectors are written (their product with T waits for T): first the
-      // block after next (the next block's near columns, so its wait below is
-      // short), then everything beyond
+      // the T-dependent half of the far columns: part A first (the next
+      // block's near columns wait for it), then the rest
       HIPRC(hipEventRecord(la->tready[k2], s), "tsqr_fold: event record failed");
-      const int64_t mid = std::min<int64_t>(near_hi + B, n);
-      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wpf,
-                     w.Wpfb, w.Wf, w.Wfb, w.split2, FAR_MAX_WGS, la->tready[k2]));
-      HIPRC(hipEventRecord(la->far[k2], la->s2), "tsqr_fold: event record failed");
-      RC(outer_apply(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n, w.Wpf, w.Wpfb,
-                     w.Wf, w.Wfb, w.split2, FAR_MAX_WGS, nullptr));
+      HIPRC(hipStreamWaitEvent(la->s2, la->tready[k2], 0), "tsqr_fold: stream wait failed");
+      RC(outer_finish(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, near_hi, mid, w.Wpf,
+                      w.Wpfb, w.Wf, w.Wfb, w.split2, FAR_MAX_WGS));
+      RC(outer_finish(la->s2, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, mid, n,
+                      w.Wpf + ntA * KB, w.Wpfb + ntA * KB, w.Wf, w.Wfb, w.split2, FAR_MAX_WGS));
       HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
       fall_pending[k2] = true;
       HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
     }
-    // near columns wait for the previous block's far update of them
-    if (far_pending >= 0) {
-      HIPRC(hipStreamWaitEvent(s, la->far[far_pending], 0), "tsqr_fold: stream wait failed");
-      far_pending = -1;
+    if (la) {
+      // the near Wp, and with it every earlier far update (the previous
+      // block's part A covers these columns)
+      HIPRC(hipStreamWaitEvent(s, la->nearwp[k2], 0), "tsqr_fold: stream wait failed");
+      RC(outer_finish(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wpn,
+                      w.Wpnb, w.Wn, w.Wnb, w.split, 0));
+    } else {
+      RC(outer_wp(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf, w.Wpfb, w.split,
+                  0));
+      RC(outer_finish(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf, w.Wpfb, w.Wf,
+                      w.Wfb, w.split, 0));
     }
-    if (far) far_pending = k2;
-    if (la)
-      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi, w.Wpn, w.Wpnb,
-                     w.Wn, w.Wnb, w.split, 0, nullptr));
-    else
-      RC(outer_apply(s, math, w, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf, w.Wpfb, w.Wf,
-                     w.Wfb, w.split, 0, nullptr));
   }
   if (la) HIPRC(hipStreamWaitEvent(s, la->done, 0), "tsqr_fold: stream wait failed");
   return launch_sign_normalize(s, R, ldr, r_new, n);
