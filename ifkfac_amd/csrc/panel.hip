@@ -248,16 +248,24 @@ __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int6
   const int l32 = lane & 31, h = lane >> 5;
   const int mq = (wave >> 1) * 32 + l32, nq = (wave & 1) * 32 + l32;
   const int jc = acc_col();
-  load_cm<false, PT>(sQ, LT, Q2, PT, r0, pe, PT);
-  int w;
-  if (cb == 0) {
-    load_rm(sM, N, b, b, b);
-    w = b;
-  } else {
+  int w = b;
+  // cb >= 1: the C entries this lane updates, loaded first so that their
+  // latency overlaps the operand loads and the product
+  const int64_t gr = r0 + jc;
+  float* Cb = CT + (int64_t)(cb > 0 ? cb - 1 : 0) * PT * ldc + gr;
+  float cur[16];
+  if (cb > 0) {
     w = nr - (cb - 1) * PT;
     if (w > PT) w = PT;
-    load_rm(sM, NW + (cb - 1) * PT, ldnw, PT, w);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = acc_row(r);
+      cur[r] = (gr < pe && c < w) ? Cb[(int64_t)c * ldc] : 0.0f;
+    }
   }
+  load_cm<false, PT>(sQ, LT, Q2, PT, r0, pe, PT);
+  if (cb == 0) load_rm(sM, N, b, b, b);
+  else load_rm(sM, NW + (cb - 1) * PT, ldnw, PT, w);
   __syncthreads();
   f32x16 d;
   zero16(d);
@@ -288,7 +296,6 @@ __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int6
         const int k = 32 * h + st;
         d = __builtin_amdgcn_mfma_f32_32x32x2f32(sM[k * TLD + mq], sQ[k * LT + nq], d, 0, 0, 0);
       }
-      const int64_t gr = r0 + jc;
       if (gr < pe) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -304,15 +311,7 @@ __global__ __launch_bounds__(PNT) void panel_update_kernel(const float* Q2, int6
       const int k = 32 * h + st;
       d = __builtin_amdgcn_mfma_f32_32x32x2f32(sM[k * TLD + mq], sQ[k * LT + nq], d, 0, 0, 0);
     }
-    const int64_t gr = r0 + jc;
     if (gr < pe) {
-      float* Cb = CT + (int64_t)(cb - 1) * PT * ldc + gr;
-      float cur[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int c = acc_row(r);
-        cur[r] = (c < w) ? Cb[(int64_t)c * ldc] : 0.0f;
-      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int c = acc_row(r);
