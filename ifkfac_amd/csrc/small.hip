@@ -45,6 +45,28 @@ __device__ inline float bcast(float v, int lane) {
 // LDS building blocks (all called by the whole 256-thread workgroup)
 // ---------------------------------------------------------------------------
 
+// The two halves of sm_load_pad, for kernels that issue several loads
+// before the first is needed: this thread's 16 entries into registers, and
+// from registers into LDS (no barrier).
+constexpr int PAD_PER = SB * SB / SNT;
+__device__ __forceinline__ void ld_pad(float (&v)[PAD_PER], const float* g, int64_t ld, int b,
+                                       bool upper, float pad) {
+#pragma unroll
+  for (int q = 0; q < PAD_PER; ++q) {
+    const int e = threadIdx.x + SNT * q;
+    const int r = e >> 6, c = e & 63;
+    if (r < b && c < b) v[q] = (upper && r > c) ? 0.0f : g[(int64_t)r * ld + c];
+    else v[q] = (r == c) ? pad : 0.0f;
+  }
+}
+__device__ __forceinline__ void st_pad(float* S, const float (&v)[PAD_PER]) {
+#pragma unroll
+  for (int q = 0; q < PAD_PER; ++q) {
+    const int e = threadIdx.x + SNT * q;
+    S[(e >> 6) * SLD + (e & 63)] = v[q];
+  }
+}
+
 // Load a b x b block (row stride ld) into a padded 64 x 64 LDS matrix.  With
 // upper set, the strict lower part is zeroed.  The pad beyond b is pad * I.
 __device__ __forceinline__ void sm_load_pad(float* S, const float* g, int64_t ld, int b, bool upper,
@@ -473,8 +495,14 @@ __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
   __shared__ float sT[TRINV_TMP];
   __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
-  sm_load_pad(sG, G, SB, b, false);
-  sm_load_pad(sP, Ptop, ldr, b, true, 0.0f);
+  {
+    float vg[PAD_PER], vp[PAD_PER];   // both loads in flight together
+    ld_pad(vg, G, SB, b, false, 1.0f);
+    ld_pad(vp, Ptop, ldr, b, true, 0.0f);
+    st_pad(sG, vg);
+    st_pad(sP, vp);
+    __syncthreads();
+  }
   sm_gemm64<true, false>(sP, sP, sG, 1.0f, true);  // sG = X_p^T X_p + P_top^T P_top
   sm_chol64(sG, tol, &bad, 0);                     // sG = U1
   sm_store(sG, U1, b, b);
@@ -515,9 +543,29 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
   __shared__ int bad;
   const int t = threadIdx.x;
   const int role = blockIdx.x;   // 0: R_new and N; 1 + cb: block cb of the rest
+  const int cb = role - 1;
+  const int c0 = cb * SB;
+  const int w = role > 0 ? ((nr - c0) < SB ? (nr - c0) : SB) : 0;
+  float* Rrest = R + b;
   if (t == 0) bad = 0;
+  // every global operand of this workgroup in flight at once: G2, Q1, and
+  // U1 (role 0) or this block's Q2^T C and R_rest (the others)
+  float vG[PAD_PER], vQ[PAD_PER], vX[PAD_PER], vR[PAD_PER];
+  ld_pad(vG, G, SB, b, false, 1.0f);
+  ld_pad(vQ, Q1, b, b, true, 0.0f);
+  if (role == 0) {
+    ld_pad(vX, U1, b, b, true, 1.0f);
+  } else {
+    ld_pad(vX, G + (size_t)(1 + cb) * SB * SB, SB, SB, false, 1.0f);
+#pragma unroll
+    for (int q = 0; q < PAD_PER; ++q) {
+      const int e = t + SNT * q, i = e >> 6, j = e & 63;
+      vR[q] = (i < b && j < w) ? Rrest[(int64_t)i * ldr + c0 + j] : 0.0f;
+    }
+  }
   const bool flagged = (*flag != 0);
-  sm_load_pad(sG, G, SB, b, false);
+  st_pad(sG, vG);
+  __syncthreads();
   if (flagged) {
     // UT transform: T^{-1} = striu(Y^T Y) + diag(1 + diag(Y^T Y)) / 2
     for (int e = t; e < SB * SB; e += SNT) {
@@ -541,7 +589,8 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
     }
     __syncthreads();
   } else {
-    sm_load_pad(sQ, Q1, b, b, true, 0.0f);
+    st_pad(sQ, vQ);
+    __syncthreads();
     sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
     // after the first pass sG is I + E with E small: a few MFMA sweeps give U2
     // and M2; the general Cholesky / inverse are the fallback
@@ -581,7 +630,8 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
     }
     if (flagged) return;
     const bool ok = (bad == 0);
-    sm_load_pad(sM, U1, b, b, true);
+    st_pad(sM, vX);
+    __syncthreads();
     sm_gemm64<false, false>(sG, sM, sM, 1.0f, false);  // sM = U2 U1
     const float nan = __int_as_float(0x7fc00000);
     for (int e = t; e < b * b; e += SNT) {           // R_new = S U2 U1
@@ -591,25 +641,10 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
     return;
   }
   // block cb of the rest: columns [b + c0, b + c0 + w) of R's block row
-  const int cb = role - 1;
-  const int c0 = cb * SB;
-  const int w = (nr - c0) < SB ? (nr - c0) : SB;
-  float* Rrest = R + b;
-  sm_load_pad(sG, G + (size_t)(1 + cb) * SB * SB, SB, SB, false);  // Q2^T C block
+  st_pad(sG, vX);                                      // Q2^T C block
+  __syncthreads();
   sm_gemm64<true, false>(sQ, sG, sM, 1.0f, false);     // sM = W = NT^T (Q2^T C)
-  {
-    float v[SB * SB / SNT];
-#pragma unroll
-    for (int q = 0; q < SB * SB / SNT; ++q) {
-      const int e = t + SNT * q, i = e >> 6, j = e & 63;
-      v[q] = (i < b && j < w) ? Rrest[(int64_t)i * ldr + c0 + j] : 0.0f;
-    }
-#pragma unroll
-    for (int q = 0; q < SB * SB / SNT; ++q) {
-      const int e = t + SNT * q;
-      sG[(e >> 6) * SLD + (e & 63)] = v[q];
-    }
-  }
+  st_pad(sG, vR);                                      // R_rest
   __syncthreads();
   sm_gemm64<true, false>(sX, sG, sM, 1.0f, true);      // W += T^T R_rest
   for (int e = t; e < SB * SB; e += SNT) {
