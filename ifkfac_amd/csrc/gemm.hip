@@ -504,6 +504,8 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   p.Cb = C.cb; p.ldcb = C.ldcb; p.bscb = C.bstride_b;
   p.vec_a = vec_ok(A);
   p.vec_b = vec_ok(B);
+  p.vec_c = (!C.c || ((uintptr_t)C.c % 16 == 0 && C.ldc % 4 == 0 && C.bstride % 4 == 0)) &&
+            (!C.cb || ((uintptr_t)C.cb % 8 == 0 && C.ldcb % 4 == 0 && C.bstride_b % 4 == 0));
   // The 256 x 256 bf16 kernel takes the large contractions; small or fp32
   // ones stay on the 128 x 128 engine.
   const bool big = math == MATH_BF16 && M >= 192 && N >= 192 &&

@@ -233,6 +233,55 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
   }
   float* Cp = p.C ? p.C + (size_t)bidx * p.bsc : nullptr;
   bf16_t* Cbp = p.Cb ? p.Cb + (size_t)bidx * p.bscb : nullptr;
+  if (p.vec_c) {
+    // Through LDS, one 32-row band of each wave row at a time: the band is
+    // read back row-contiguous, so C is read and written 16 bytes and the bf16
+    // copy 8 bytes per lane.  (The ring is free once every wave is past its
+    // last slab.)
+    constexpr int LDB = BN + 4;                        // band row stride (floats)
+    constexpr int V4 = BN / 4;                         // float4 per band row
+    static_assert(CF::WAVES_M * 32 * LDB * 4 <= STAGES * STAGE * 2, "band fits the ring");
+    float* band = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          band[(wm * 32 + (r >> 2) * 8 + h * 4 + (r & 3)) * LDB + wn * CF::WTN + j * 32 + l32] =
+              acc[i][j][r];
+      __syncthreads();
+      for (int idx = t; idx < CF::WAVES_M * 32 * V4; idx += CF::NTH) {
+        const int rb = idx / V4, c4 = idx - rb * V4;
+        const int64_t row = m0 + (rb >> 5) * CF::WTM + i * 32 + (rb & 31);
+        const int64_t col = n0 + c4 * 4;
+        if (row >= p.M || col >= p.N) continue;
+        const float4 a = *reinterpret_cast<const float4*>(band + rb * LDB + c4 * 4);
+        float v[4] = {p.alpha * a.x, p.alpha * a.y, p.alpha * a.z, p.alpha * a.w};
+        if (col + 3 < p.N) {
+          if (p.beta != 0.0f) {
+            const float4 o = *reinterpret_cast<const float4*>(Cp + row * p.ldc + col);
+            v[0] += p.beta * o.x; v[1] += p.beta * o.y; v[2] += p.beta * o.z; v[3] += p.beta * o.w;
+          }
+          if (Cp) *reinterpret_cast<float4*>(Cp + row * p.ldc + col) = make_float4(v[0], v[1], v[2], v[3]);
+          if (Cbp) {
+            const unsigned lo = (unsigned)f32_to_bf16(v[0]) | ((unsigned)f32_to_bf16(v[1]) << 16);
+            const unsigned hi = (unsigned)f32_to_bf16(v[2]) | ((unsigned)f32_to_bf16(v[3]) << 16);
+            *reinterpret_cast<uint2*>(Cbp + row * p.ldcb + col) = make_uint2(lo, hi);
+          }
+        } else {
+          for (int u = 0; u < 4 && col + u < p.N; ++u) {
+            float x = v[u];
+            if (p.beta != 0.0f) x += p.beta * Cp[row * p.ldc + col + u];
+            if (Cp) Cp[row * p.ldc + col + u] = x;
+            if (Cbp) Cbp[row * p.ldcb + col + u] = f32_to_bf16(x);
+          }
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll

@@ -98,6 +98,26 @@ def test_gemm_direct_lds_kernel(hip, m, n, k, beta):
     assert _rel(C, ref.cpu().numpy()) < 2e-6
 
 
+@pytest.mark.parametrize("m,n,k", [(1000, 701, 2048), (4000, 3701, 256)])
+@pytest.mark.parametrize("ldc_pad", [0, 3])
+def test_gemm_direct_lds_epilogue(hip, m, n, k, ldc_pad):
+    """The direct-to-LDS kernel's output paths: with C rows 16-byte aligned
+    (ld a multiple of 4, here n + 3) the epilogue goes through LDS and writes
+    four columns per lane, the last partial group element by element; with
+    ld = n it writes element by element.  Both tiles, beta = 1."""
+    g = torch.Generator(device=DEV).manual_seed(m + n + k + ldc_pad)
+    A = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    B = torch.randn(n, k, device=DEV, generator=g).to(torch.bfloat16)
+    buf = torch.randn(m, n + ldc_pad, device=DEV, generator=g)
+    pad = buf[:, n:].clone()
+    C0 = buf[:, :n]
+    ref = 0.75 * (A.double() @ B.double().t()) + C0.double()
+    C = hip.gemm(A, B, False, True, 1, 0.75, 1.0, C0)
+    assert C.data_ptr() == buf.data_ptr() and C.stride(0) == n + ldc_pad
+    assert _rel(C, ref.cpu().numpy()) < 2e-6
+    assert torch.equal(buf[:, n:], pad)   # the columns past n are untouched
+
+
 @pytest.mark.parametrize("tri", ["upper_a", "lower_b", "upper_b"])
 @pytest.mark.parametrize("n,rows", [(1280, 1100), (4096, 3600)])
 def test_gemm_direct_lds_triangular(hip, tri, n, rows):
