@@ -53,8 +53,9 @@ inline OutRef out_f32(float* c, int64_t ldc, int64_t bs = 0) {
 inline OutRef out_bf16(bf16_t* cb, int64_t ld, int64_t bs = 0) {
   return OutRef{nullptr, 0, 0, cb, ld, bs};
 }
-inline OutRef out_both(float* c, int64_t ldc, bf16_t* cb, int64_t ldcb) {
-  return OutRef{c, ldc, 0, cb, ldcb, 0};
+inline OutRef out_both(float* c, int64_t ldc, bf16_t* cb, int64_t ldcb, int64_t bstride = 0,
+                       int64_t bstride_b = 0) {
+  return OutRef{c, ldc, bstride, cb, ldcb, bstride_b};
 }
 
 // Scratch the engine may use for split-K partial sums (fp32 elements).  When

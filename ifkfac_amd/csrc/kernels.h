@@ -47,8 +47,11 @@ int launch_sub_transposed(hipStream_t s, float* R, int64_t ldr, const float* WT,
 int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,
                    int64_t ldt);
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
+// (and, when given, RNE bf16 copies of the blocks into Zb row-major and into
+// ZTb transposed, both of row stride ldb)
 int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
-                      float* Z, int64_t ldz, int safe);
+                      float* Z, int64_t ldz, int safe, bf16_t* Zb = nullptr,
+                      bf16_t* ZTb = nullptr, int64_t ldb = 0);
 // Diagonal 128 x 128 blocks of R^{-1} (R upper triangular, or with ut the UT
 // transform striu(G) + diag(1 + diag G) / 2 of a reflector Gram matrix G =
 // Y^T Y, whose inverse is the T factor of the reflectors [I; Y]); the last

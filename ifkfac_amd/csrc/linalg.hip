@@ -528,10 +528,11 @@ static void plan_trinv(Arena& a, int64_t n, float** tmp, SplitScratch* sp) {
   sp->p = a.take<float>(sp->floats);
 }
 
-// ... plus the transposed bf16 copy of Z used by bf16 arithmetic
+// ... plus the bf16 copies of Z used by bf16 arithmetic: transposed, then
+// row-major (2 n^2 elements from zt)
 static void plan_trinv(Arena& a, int64_t n, float** tmp, bf16_t** zt, SplitScratch* sp) {
   plan_trinv(a, n, tmp, sp);
-  *zt = a.take<bf16_t>((size_t)n * n);
+  *zt = a.take<bf16_t>((size_t)n * n * 2);
 }
 
 size_t trinv_ws(int64_t n) {
@@ -601,27 +602,22 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
   return IFK_OK;
 }
 
-// bf16-arithmetic triangular inverse that keeps a transposed bf16 copy ZT of
-// Z (n x n, ld n) next to it, so every product reads K-contiguous operands:
-// per doubling level, for the diagonal pair (Z11, Z22) and the block R12,
-//   TmpT = ZT22 R12^T,   Z12 = -Z11 TmpT^T,   ZT21 = Z12^T.
-// tmpT: n^2 / 2 + 4 * 64^2 bf16 elements.
+// bf16-arithmetic triangular inverse that keeps two bf16 copies of Z
+// (n x n, ld n each, from ZT): ZT = Z^T and Zb = Z, so every product reads
+// K-contiguous bf16 operands: per doubling level, for the diagonal pair
+// (Z11, Z22) and the block R12,
+//   TmpT = ZT22 R12^T,   Z12 = -Zb11 TmpT^T (into Z and Zb),   ZT21 = Z12^T.
+// tmpT: n^2 / 2 + 4 * 64^2 bf16 elements.  The strict lower part of Zb is
+// never written (the products read Zb as upper triangular).
 static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
                         int64_t ldz, int safe, bf16_t* ZT, bf16_t* tmpT, SplitScratch sp) {
   const size_t esz = rdt == DT_F32 ? 4 : 2;
   const char* Rc = (const char*)R;
   const int64_t NB = TRINV_NB;
+  bf16_t* Zb = ZT + (size_t)n * n;
   RC(launch_zero(s, Z, ldz, n, n));
   RC(launch_zero_bf16(s, ZT, n, n, n));
-  RC(launch_trinv_diag(s, R, rdt, ldr, n, NB, Z, ldz, safe));
-  const int64_t nbf = n / NB;
-  if (nbf > 0)
-    RC(launch_transpose_cast(s, Z, ldz, NB, NB, ZT, DT_BF16, n, (int)nbf, NB * (ldz + 1),
-                             NB * (n + 1)));
-  if (nbf * NB < n) {
-    const int64_t i0 = nbf * NB, r = n - i0;
-    RC(launch_transpose_cast(s, Z + i0 * ldz + i0, ldz, r, r, ZT + i0 * n + i0, DT_BF16, n));
-  }
+  RC(launch_trinv_diag(s, R, rdt, ldr, n, NB, Z, ldz, safe, Zb, ZT, n));
   for (int64_t w = NB; w < n; w *= 2) {
     const int64_t step = 2 * w;
     const int64_t nfull = n / step;
@@ -630,9 +626,9 @@ static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int6
       RC(gemm(s, MATH_BF16, w, w, w, 1.0f, A_n(ZT + w * n + w, DT_BF16, n, TRI_LOWER, step * (n + 1)),
               B_t(R12, rdt, ldr, TRI_NONE, step * (ldr + 1)), 0.0f, out_bf16(tmpT, w, w * w),
               (int)nfull, sp));
-      RC(gemm(s, MATH_BF16, w, w, w, -1.0f, A_n(Z, DT_F32, ldz, TRI_UPPER, step * (ldz + 1)),
-              B_t(tmpT, DT_BF16, w, TRI_NONE, w * w), 0.0f, out_f32(Z + w, ldz, step * (ldz + 1)),
-              (int)nfull, sp));
+      RC(gemm(s, MATH_BF16, w, w, w, -1.0f, A_n(Zb, DT_BF16, n, TRI_UPPER, step * (n + 1)),
+              B_t(tmpT, DT_BF16, w, TRI_NONE, w * w), 0.0f,
+              out_both(Z + w, ldz, Zb + w, n, step * (ldz + 1), step * (n + 1)), (int)nfull, sp));
       RC(launch_transpose_cast(s, Z + w, ldz, w, w, ZT + w * n, DT_BF16, n, (int)nfull,
                                step * (ldz + 1), step * (n + 1)));
     }
@@ -643,8 +639,9 @@ static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int6
       RC(gemm(s, MATH_BF16, w2, w, w2, 1.0f,
               A_n(ZT + (i0 + w) * n + i0 + w, DT_BF16, n, TRI_LOWER), B_t(R12, rdt, ldr), 0.0f,
               out_bf16(tmpT, w), 1, sp));
-      RC(gemm(s, MATH_BF16, w, w2, w, -1.0f, A_n(Z + i0 * ldz + i0, DT_F32, ldz, TRI_UPPER),
-              B_t(tmpT, DT_BF16, w), 0.0f, out_f32(Z + i0 * ldz + i0 + w, ldz), 1, sp));
+      RC(gemm(s, MATH_BF16, w, w2, w, -1.0f, A_n(Zb + i0 * n + i0, DT_BF16, n, TRI_UPPER),
+              B_t(tmpT, DT_BF16, w), 0.0f,
+              out_both(Z + i0 * ldz + i0 + w, ldz, Zb + i0 * n + i0 + w, n), 1, sp));
       RC(launch_transpose_cast(s, Z + i0 * ldz + i0 + w, ldz, w, w2, ZT + (i0 + w) * n + i0,
                                DT_BF16, n));
     }

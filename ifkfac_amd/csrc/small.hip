@@ -694,7 +694,8 @@ __global__ void ut_tinv_kernel(const float* G, int64_t ldg, int64_t n, float* Ti
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t ldr, int64_t n,
-                                                         int nb, float* Z, int64_t ldz, int safe) {
+                                                         int nb, float* Z, int64_t ldz, int safe,
+                                                         bf16_t* Zb, bf16_t* ZTb, int64_t ldb) {
   __shared__ float sU[SB * SLD];
   __shared__ float sZ[SB * SLD];
   __shared__ float sT[TRINV_TMP];
@@ -722,7 +723,10 @@ __global__ __launch_bounds__(SNT) void trinv_diag_kernel(const void* R, int64_t 
   sm_trinv64(sU, sZ, sT, safe != 0);
   for (int e = threadIdx.x; e < b * b; e += SNT) {
     const int r = e / b, c = e - r * b;
-    Z[(k0 + r) * ldz + k0 + c] = sZ[r * SLD + c];
+    const float z = sZ[r * SLD + c];
+    Z[(k0 + r) * ldz + k0 + c] = z;
+    if (Zb) Zb[(k0 + r) * ldb + k0 + c] = f32_to_bf16(z);
+    if (ZTb) ZTb[(k0 + c) * ldb + k0 + r] = f32_to_bf16(z);
   }
 }
 
@@ -915,15 +919,15 @@ int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float*
 }
 
 int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
-                      float* Z, int64_t ldz, int safe) {
+                      float* Z, int64_t ldz, int safe, bf16_t* Zb, bf16_t* ZTb, int64_t ldb) {
   if (int rc = check_b(nb, "trinv_diag")) return rc;
   const unsigned nblk = (unsigned)cdiv(n, nb);
   if (rdt == DT_F32)
     hipLaunchKernelGGL(trinv_diag_kernel<DT_F32>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, nb, Z,
-                       ldz, safe);
+                       ldz, safe, Zb, ZTb, ldb);
   else
     hipLaunchKernelGGL(trinv_diag_kernel<DT_BF16>, dim3(nblk), dim3(SNT), 0, s, R, ldr, n, nb, Z,
-                       ldz, safe);
+                       ldz, safe, Zb, ZTb, ldb);
   return check_launch("trinv_diag");
 }
 
