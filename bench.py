@@ -201,10 +201,13 @@ def main() -> int:
         mark()
         (FX, _), (FG, _) = factors(mark)
         mark()
-        ZX, ZG = run_pair(dev, lambda: be.tri_inverse(FX, MATH_BF16),
-                          lambda: be.tri_inverse(FG, MATH_BF16), b_first=n_out > n_in)
+        # IFKFAC._update_factors / _nat_grad in bf16 arithmetic: the inverses
+        # with their bf16 copies, then the apply from the copies
+        (_, ZXb, ZXt), (_, ZGb, ZGt) = run_pair(dev, lambda: be.tri_inverse_bf16(FX),
+                                                lambda: be.tri_inverse_bf16(FG),
+                                                b_first=n_out > n_in)
         mark()
-        nat = be.precondition_apply(grad, ZX, ZG, MATH_BF16)
+        nat = be.precondition_apply_bf16(grad, (ZXb, ZXt), (ZGb, ZGt))
         mark()
         be.momentum_update_(nat, buf, W, lr, mom, 0.0, first)
         mark()

@@ -153,6 +153,53 @@ class HipBackend:
         _lib.check(rc, "ifk_tri_inverse")
         return Z
 
+    def tri_inverse_bf16(self, R: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor,
+                                                          torch.Tensor]:
+        """tri_inverse in bf16 arithmetic, also returning the RNE bf16 copies
+        (Z, Z^T) that precondition_apply_bf16 reads (their other triangle zero)."""
+        R, ldr, rdt = _mat(R, "tri_inverse_bf16")
+        n = R.shape[0]
+        if R.shape[1] != n:
+            raise IFKFACBackendError("tri_inverse_bf16: R must be square")
+        Z = torch.empty((n, n), dtype=torch.float32, device=R.device)
+        Zb = torch.empty((n, n), dtype=torch.bfloat16, device=R.device)
+        ZT = torch.empty((n, n), dtype=torch.bfloat16, device=R.device)
+        ws = self._ws(self.lib.ifk_tri_inverse_bf16_workspace_size(n), R.device)
+        with torch.cuda.device(R.device):
+            rc = self.lib.ifk_tri_inverse_bf16(self._stream(R.device), _ptr(R), rdt, ldr, n,
+                                               _ptr(Z), n, _ptr(Zb), _ptr(ZT), n, _ptr(ws),
+                                               ws.numel())
+        _lib.check(rc, "ifk_tri_inverse_bf16")
+        return Z, Zb, ZT
+
+    def precondition_apply_bf16(self, grad: torch.Tensor, ZX2, ZG2) -> torch.Tensor:
+        """precondition_apply in bf16 arithmetic from (Z_X, Z_X^T), (Z_G, Z_G^T)
+        bf16 copies of tri_inverse_bf16 (views of them, e.g. trimmed, allowed)."""
+        g, ldg, gdt = _mat(grad, "precondition_apply_bf16")
+        if gdt != IFK_F32:
+            g = g.float()
+            ldg = g.stride(0)
+        n_out, n_in = g.shape
+        (ZXb, ZXt), (ZGb, ZGt) = ZX2, ZG2
+        for name, t, n in (("Z_X", ZXb, n_in), ("Z_X^T", ZXt, n_in), ("Z_G", ZGb, n_out),
+                           ("Z_G^T", ZGt, n_out)):
+            _require_device(t, "precondition_apply_bf16")
+            if t.dtype != torch.bfloat16 or t.shape != (n, n) or t.stride(1) != 1:
+                raise IFKFACBackendError(f"precondition_apply_bf16: {name} must be an "
+                                         f"{n} x {n} bf16 row-major matrix")
+        if ZXb.stride(0) != ZXt.stride(0) or ZGb.stride(0) != ZGt.stride(0):
+            raise IFKFACBackendError("precondition_apply_bf16: a side's two copies differ in "
+                                     "row stride")
+        nat = torch.empty((n_out, n_in), dtype=torch.float32, device=g.device)
+        ws = self._ws(self.lib.ifk_precondition_apply_bf16_workspace_size(n_out, n_in), g.device)
+        with torch.cuda.device(g.device):
+            rc = self.lib.ifk_precondition_apply_bf16(
+                self._stream(g.device), _ptr(g), n_out, n_in, ldg, _ptr(ZXb), _ptr(ZXt),
+                ZXb.stride(0), _ptr(ZGb), _ptr(ZGt), ZGb.stride(0), _ptr(nat), n_in, _ptr(ws),
+                ws.numel())
+        _lib.check(rc, "ifk_precondition_apply_bf16")
+        return nat
+
     def precondition(self, grad: torch.Tensor, R_X: torch.Tensor, R_G: torch.Tensor,
                      math: int) -> torch.Tensor:
         g, ldg, gdt = _mat(grad, "precondition")

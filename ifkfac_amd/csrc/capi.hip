@@ -99,6 +99,33 @@ int ifk_tri_inverse(void* stream, const void* R, int r_dtype, int64_t ldr, int64
                workspace_bytes);
 }
 
+size_t ifk_tri_inverse_bf16_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return trinv_copies_ws(n);
+}
+
+int ifk_tri_inverse_bf16(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n,
+                         float* Z, int64_t ldz, void* Zb, void* ZTb, int64_t ldb, void* workspace,
+                         size_t workspace_bytes) {
+  GUARD(dt_ok(r_dtype), "tri_inverse_bf16: bad dtype code");
+  return trinv_copies((hipStream_t)stream, R, r_dtype, ldr, n, Z, ldz, (bf16_t*)Zb, (bf16_t*)ZTb,
+                      ldb, workspace, workspace_bytes);
+}
+
+size_t ifk_precondition_apply_bf16_workspace_size(int64_t n_out, int64_t n_in) {
+  if (n_out < 1 || n_in < 1) return 0;
+  return precondition_apply_b_ws(n_out, n_in);
+}
+
+int ifk_precondition_apply_bf16(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                                int64_t ldg, const void* Z_Xb, const void* Z_Xt, int64_t ldzx,
+                                const void* Z_Gb, const void* Z_Gt, int64_t ldzg, float* nat,
+                                int64_t ldn, void* workspace, size_t workspace_bytes) {
+  return precondition_apply_b((hipStream_t)stream, grad, n_out, n_in, ldg, (const bf16_t*)Z_Xb,
+                              (const bf16_t*)Z_Xt, ldzx, (const bf16_t*)Z_Gb, (const bf16_t*)Z_Gt,
+                              ldzg, nat, ldn, workspace, workspace_bytes);
+}
+
 size_t ifk_precondition_workspace_size(int64_t n_out, int64_t n_in, int math) {
   if (n_out < 1 || n_in < 1 || !math_ok(math)) return 0;
   return precondition_ws(n_out, n_in, math);

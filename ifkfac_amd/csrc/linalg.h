@@ -33,6 +33,20 @@ size_t trinv_ws(int64_t n);
 int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,
           int math, int safe, void* ws, size_t ws_bytes);
 
+// Z = R^{-1} in bf16 arithmetic, plus RNE bf16 copies Zb = Z and ZTb = Z^T
+// (row stride ldb, the other triangle zero) for precondition_apply_b.
+size_t trinv_copies_ws(int64_t n);
+int trinv_copies(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
+                 int64_t ldz, bf16_t* Zb, bf16_t* ZTb, int64_t ldb, void* ws, size_t ws_bytes);
+
+// nat as precondition_apply in bf16 arithmetic, from the copies of
+// trinv_copies (nothing to cast but grad).
+size_t precondition_apply_b_ws(int64_t n_out, int64_t n_in);
+int precondition_apply_b(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                         int64_t ldg, const bf16_t* ZXb, const bf16_t* ZXt, int64_t ldx2,
+                         const bf16_t* ZGb, const bf16_t* ZGt, int64_t ldg2, float* nat,
+                         int64_t ldn, void* ws, size_t ws_bytes);
+
 // nat = Z_G Z_G^T grad Z_X Z_X^T, with Z_X = R_X^{-1}, Z_G = R_G^{-1} given.
 size_t precondition_apply_ws(int64_t n_out, int64_t n_in, int math);
 int precondition_apply(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,

@@ -602,48 +602,51 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
   return IFK_OK;
 }
 
-// bf16-arithmetic triangular inverse that keeps two bf16 copies of Z
-// (n x n, ld n each, from ZT): ZT = Z^T and Zb = Z, so every product reads
+// bf16-arithmetic triangular inverse that keeps two bf16 copies of Z (n x n,
+// row stride ldb each): ZT = Z^T and Zb = Z, so every product reads
 // K-contiguous bf16 operands: per doubling level, for the diagonal pair
 // (Z11, Z22) and the block R12,
 //   TmpT = ZT22 R12^T,   Z12 = -Zb11 TmpT^T (into Z and Zb),   ZT21 = Z12^T.
-// tmpT: n^2 / 2 + 4 * 64^2 bf16 elements.  The strict lower part of Zb is
-// never written (the products read Zb as upper triangular).
+// tmpT: n^2 / 2 + 4 * 64^2 bf16 elements.  The products read Zb as upper
+// triangular only, so its strict lower part is zeroed only on request
+// (zero_zb, when Zb is handed back to the caller).
 static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
-                        int64_t ldz, int safe, bf16_t* ZT, bf16_t* tmpT, SplitScratch sp) {
+                        int64_t ldz, int safe, bf16_t* ZT, bf16_t* Zb, int64_t ldb, bool zero_zb,
+                        bf16_t* tmpT, SplitScratch sp) {
   const size_t esz = rdt == DT_F32 ? 4 : 2;
   const char* Rc = (const char*)R;
   const int64_t NB = TRINV_NB;
-  bf16_t* Zb = ZT + (size_t)n * n;
+  const int64_t n_ = ldb;   // row stride of both bf16 copies
   RC(launch_zero(s, Z, ldz, n, n));
-  RC(launch_zero_bf16(s, ZT, n, n, n));
-  RC(launch_trinv_diag(s, R, rdt, ldr, n, NB, Z, ldz, safe, Zb, ZT, n));
+  RC(launch_zero_bf16(s, ZT, n_, n, n));
+  if (zero_zb) RC(launch_zero_bf16(s, Zb, n_, n, n));
+  RC(launch_trinv_diag(s, R, rdt, ldr, n, NB, Z, ldz, safe, Zb, ZT, n_));
   for (int64_t w = NB; w < n; w *= 2) {
     const int64_t step = 2 * w;
     const int64_t nfull = n / step;
     if (nfull > 0) {
       const void* R12 = Rc + (size_t)w * esz;  // block (0, w) of pair 0
-      RC(gemm(s, MATH_BF16, w, w, w, 1.0f, A_n(ZT + w * n + w, DT_BF16, n, TRI_LOWER, step * (n + 1)),
+      RC(gemm(s, MATH_BF16, w, w, w, 1.0f, A_n(ZT + w * n_ + w, DT_BF16, n_, TRI_LOWER, step * (n_ + 1)),
               B_t(R12, rdt, ldr, TRI_NONE, step * (ldr + 1)), 0.0f, out_bf16(tmpT, w, w * w),
               (int)nfull, sp));
-      RC(gemm(s, MATH_BF16, w, w, w, -1.0f, A_n(Zb, DT_BF16, n, TRI_UPPER, step * (n + 1)),
+      RC(gemm(s, MATH_BF16, w, w, w, -1.0f, A_n(Zb, DT_BF16, n_, TRI_UPPER, step * (n_ + 1)),
               B_t(tmpT, DT_BF16, w, TRI_NONE, w * w), 0.0f,
-              out_both(Z + w, ldz, Zb + w, n, step * (ldz + 1), step * (n + 1)), (int)nfull, sp));
-      RC(launch_transpose_cast(s, Z + w, ldz, w, w, ZT + w * n, DT_BF16, n, (int)nfull,
-                               step * (ldz + 1), step * (n + 1)));
+              out_both(Z + w, ldz, Zb + w, n_, step * (ldz + 1), step * (n_ + 1)), (int)nfull, sp));
+      RC(launch_transpose_cast(s, Z + w, ldz, w, w, ZT + w * n_, DT_BF16, n_, (int)nfull,
+                               step * (ldz + 1), step * (n_ + 1)));
     }
     const int64_t i0 = nfull * step;
     if (i0 + w < n) {
       const int64_t w2 = n - i0 - w;
       const void* R12 = Rc + ((size_t)i0 * ldr + i0 + w) * esz;  // w x w2
       RC(gemm(s, MATH_BF16, w2, w, w2, 1.0f,
-              A_n(ZT + (i0 + w) * n + i0 + w, DT_BF16, n, TRI_LOWER), B_t(R12, rdt, ldr), 0.0f,
+              A_n(ZT + (i0 + w) * n_ + i0 + w, DT_BF16, n_, TRI_LOWER), B_t(R12, rdt, ldr), 0.0f,
               out_bf16(tmpT, w), 1, sp));
-      RC(gemm(s, MATH_BF16, w, w2, w, -1.0f, A_n(Zb + i0 * n + i0, DT_BF16, n, TRI_UPPER),
+      RC(gemm(s, MATH_BF16, w, w2, w, -1.0f, A_n(Zb + i0 * n_ + i0, DT_BF16, n_, TRI_UPPER),
               B_t(tmpT, DT_BF16, w), 0.0f,
-              out_both(Z + i0 * ldz + i0 + w, ldz, Zb + i0 * n + i0 + w, n), 1, sp));
-      RC(launch_transpose_cast(s, Z + i0 * ldz + i0 + w, ldz, w, w2, ZT + (i0 + w) * n + i0,
-                               DT_BF16, n));
+              out_both(Z + i0 * ldz + i0 + w, ldz, Zb + i0 * n_ + i0 + w, n_), 1, sp));
+      RC(launch_transpose_cast(s, Z + i0 * ldz + i0 + w, ldz, w, w2, ZT + (i0 + w) * n_ + i0,
+                               DT_BF16, n_));
     }
   }
   return IFK_OK;
@@ -662,8 +665,32 @@ int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* 
   plan_trinv(a, n, &tmp, &zt, &sp);
   RC(check_ws(a, "tri_inverse"));
   if (math == MATH_BF16)
-    return trinv_core_t(s, R, rdt, ldr, n, Z, ldz, safe, zt, (bf16_t*)tmp, sp);
+    return trinv_core_t(s, R, rdt, ldr, n, Z, ldz, safe, zt, zt + (size_t)n * n, n, false,
+                        (bf16_t*)tmp, sp);
   return trinv_core(s, R, rdt, ldr, n, Z, ldz, math, safe, tmp, sp);
+}
+
+int trinv_copies(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
+                 int64_t ldz, bf16_t* Zb, bf16_t* ZTb, int64_t ldb, void* ws, size_t ws_bytes) {
+  if (n < 1 || ldr < n || ldz < n || ldb < n || !R || !Z || !Zb || !ZTb ||
+      (rdt != DT_F32 && rdt != DT_BF16)) {
+    set_error("tri_inverse_bf16: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  float* tmp;
+  SplitScratch sp;
+  plan_trinv(a, n, &tmp, &sp);
+  RC(check_ws(a, "tri_inverse_bf16"));
+  return trinv_core_t(s, R, rdt, ldr, n, Z, ldz, 0, ZTb, Zb, ldb, true, (bf16_t*)tmp, sp);
+}
+
+size_t trinv_copies_ws(int64_t n) {
+  Arena a(nullptr, 0);
+  float* tmp;
+  SplitScratch sp;
+  plan_trinv(a, n, &tmp, &sp);
+  return a.used;
 }
 
 // ----------------------------------------------------------------------------
@@ -685,6 +712,17 @@ static void plan_apply(Arena& a, int64_t n_out, int64_t n_in, int math, void** T
   sp->p = a.take<float>(sp->floats);
 }
 
+// ... for precondition_apply_b: only grad^T is cast
+static void plan_apply_b(Arena& a, int64_t n_out, int64_t n_in, void** T1, void** T2,
+                         bf16_t** cv, SplitScratch* sp) {
+  const size_t e = (size_t)n_out * n_in;
+  *T1 = a.take<bf16_t>(e);
+  *T2 = a.take<bf16_t>(e);
+  *cv = a.take<bf16_t>(e);
+  sp->floats = split_floats(TRINV_NB, std::max(n_out, n_in));
+  sp->p = a.take<float>(sp->floats);
+}
+
 size_t precondition_apply_ws(int64_t n_out, int64_t n_in, int math) {
   Arena a(nullptr, 0);
   void *T1, *T2;
@@ -694,12 +732,36 @@ size_t precondition_apply_ws(int64_t n_out, int64_t n_in, int math) {
   return a.used;
 }
 
+// The bf16 products of the apply, given bf16 copies (the RNE roundings the
+// MFMA operands get anyway) of grad^T (gT, n_in x n_out), Z_G and Z_G^T (ld
+// ldg2), Z_X and Z_X^T (ld ldx2): every product reads both operands
+// K-contiguous.  Only the upper triangle of ZGb, ZXb and the lower triangle of
+// ZGt, ZXt are read.
+static int apply_core_b(hipStream_t s, const bf16_t* gT, int64_t n_out, int64_t n_in,
+                        const bf16_t* ZXb, const bf16_t* ZXt, int64_t ldx2, const bf16_t* ZGb,
+                        const bf16_t* ZGt, int64_t ldg2, float* nat, int64_t ldn, void* T1,
+                        void* T2, SplitScratch sp) {
+  const int math = MATH_BF16;
+  bf16_t* T1T = (bf16_t*)T1;   // n_in x n_out
+  bf16_t* Tb = (bf16_t*)T2;    // n_out x n_in
+  // T1^T = grad^T Z_G          (T1 = Z_G^T grad: R_G^T T1 = grad, triangular.py:632)
+  RC(gemm(s, math, n_in, n_out, n_out, 1.0f, A_n(gT, DT_BF16, n_out),
+          B_t(ZGt, DT_BF16, ldg2, TRI_UPPER), 0.0f, out_bf16(T1T, n_out), 1, sp));
+  // T2 = Z_G T1                (R_G T2 = T1, triangular.py:636)
+  RC(gemm(s, math, n_out, n_in, n_out, 1.0f, A_n(ZGb, DT_BF16, ldg2, TRI_UPPER),
+          B_t(T1T, DT_BF16, n_out), 0.0f, out_bf16(Tb, n_in), 1, sp));
+  // T3 = T2 Z_X                (R_X^T T3^T = T2^T, triangular.py:645), into T1's buffer
+  RC(gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(Tb, DT_BF16, n_in),
+          B_t(ZXt, DT_BF16, ldx2, TRI_UPPER), 0.0f, out_bf16(T1T, n_in), 1, sp));
+  // nat = T3 Z_X^T             (R_X T4^T = T3^T, triangular.py:649)
+  return gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(T1T, DT_BF16, n_in),
+              B_t(ZXb, DT_BF16, ldx2, TRI_LOWER), 0.0f, out_f32(nat, ldn), 1, sp);
+}
+
 static int apply_core(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,
                       const float* ZX, int64_t ldzx, const float* ZG, int64_t ldzg, float* nat,
                       int64_t ldn, int math, void* T1, void* T2, bf16_t* cv, SplitScratch sp) {
   if (math == MATH_BF16) {
-    // bf16 copies (the RNE roundings the MFMA operands get anyway) of grad^T,
-    // Z_G, Z_G^T, Z_X, Z_X^T make every product K-contiguous in both operands
     bf16_t* gT = cv;                                   // n_in x n_out
     bf16_t* ZGb = gT + (size_t)n_in * n_out;           // n_out x n_out
     bf16_t* ZGt = ZGb + (size_t)n_out * n_out;
@@ -710,20 +772,7 @@ static int apply_core(hipStream_t s, const float* grad, int64_t n_out, int64_t n
     RC(launch_transpose_cast(s, ZG, ldzg, n_out, n_out, ZGt, DT_BF16, n_out));
     RC(launch_cast(s, ZX, ldzx, n_in, n_in, ZXb, DT_BF16, n_in));
     RC(launch_transpose_cast(s, ZX, ldzx, n_in, n_in, ZXt, DT_BF16, n_in));
-    bf16_t* T1T = (bf16_t*)T1;   // n_in x n_out
-    bf16_t* Tb = (bf16_t*)T2;    // n_out x n_in
-    // T1^T = grad^T Z_G          (T1 = Z_G^T grad: R_G^T T1 = grad, triangular.py:632)
-    RC(gemm(s, math, n_in, n_out, n_out, 1.0f, A_n(gT, DT_BF16, n_out),
-            B_t(ZGt, DT_BF16, n_out, TRI_UPPER), 0.0f, out_bf16(T1T, n_out), 1, sp));
-    // T2 = Z_G T1                (R_G T2 = T1, triangular.py:636)
-    RC(gemm(s, math, n_out, n_in, n_out, 1.0f, A_n(ZGb, DT_BF16, n_out, TRI_UPPER),
-            B_t(T1T, DT_BF16, n_out), 0.0f, out_bf16(Tb, n_in), 1, sp));
-    // T3 = T2 Z_X                (R_X^T T3^T = T2^T, triangular.py:645), into T1's buffer
-    RC(gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(Tb, DT_BF16, n_in),
-            B_t(ZXt, DT_BF16, n_in, TRI_UPPER), 0.0f, out_bf16(T1T, n_in), 1, sp));
-    // nat = T3 Z_X^T             (R_X T4^T = T3^T, triangular.py:649)
-    return gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(T1T, DT_BF16, n_in),
-                B_t(ZXb, DT_BF16, n_in, TRI_LOWER), 0.0f, out_f32(nat, ldn), 1, sp);
+    return apply_core_b(s, gT, n_out, n_in, ZXb, ZXt, n_in, ZGb, ZGt, n_out, nat, ldn, T1, T2, sp);
   }
   const int tdt = DT_F32;
   auto out_t = [&](void* p, int64_t ld) {
@@ -761,6 +810,35 @@ int precondition_apply(hipStream_t s, const float* grad, int64_t n_out, int64_t 
   return apply_core(s, grad, n_out, n_in, ldg, ZX, ldzx, ZG, ldzg, nat, ldn, math, T1, T2, cv, sp);
 }
 
+// nat from grad and the bf16 copies written by trinv_copies
+int precondition_apply_b(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                         int64_t ldg, const bf16_t* ZXb, const bf16_t* ZXt, int64_t ldx2,
+                         const bf16_t* ZGb, const bf16_t* ZGt, int64_t ldg2, float* nat,
+                         int64_t ldn, void* ws, size_t ws_bytes) {
+  if (n_out < 1 || n_in < 1 || ldg < n_in || ldn < n_in || ldx2 < n_in || ldg2 < n_out || !grad ||
+      !ZXb || !ZXt || !ZGb || !ZGt || !nat) {
+    set_error("precondition_apply_bf16: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  void *T1, *T2;
+  bf16_t* cv;
+  SplitScratch sp;
+  plan_apply_b(a, n_out, n_in, &T1, &T2, &cv, &sp);
+  RC(check_ws(a, "precondition_apply_bf16"));
+  RC(launch_transpose_cast(s, grad, ldg, n_out, n_in, cv, DT_BF16, n_out));
+  return apply_core_b(s, cv, n_out, n_in, ZXb, ZXt, ldx2, ZGb, ZGt, ldg2, nat, ldn, T1, T2, sp);
+}
+
+size_t precondition_apply_b_ws(int64_t n_out, int64_t n_in) {
+  Arena a(nullptr, 0);
+  void *T1, *T2;
+  bf16_t* cv;
+  SplitScratch sp;
+  plan_apply_b(a, n_out, n_in, &T1, &T2, &cv, &sp);
+  return a.used;
+}
+
 static void plan_prec(Arena& a, int64_t n_out, int64_t n_in, int math, float** ZX, float** ZG,
                       float** tmp, bf16_t** zt, SplitScratch* tsp, void** T1, void** T2,
                       bf16_t** cv, SplitScratch* asp) {
@@ -796,8 +874,10 @@ int precondition(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, 
   plan_prec(a, n_out, n_in, math, &ZX, &ZG, &tmp, &zt, &tsp, &T1, &T2, &cv, &asp);
   RC(check_ws(a, "precondition"));
   if (math == MATH_BF16) {
-    RC(trinv_core_t(s, RX, rdt, ldrx, n_in, ZX, n_in, 0, zt, (bf16_t*)tmp, tsp));
-    RC(trinv_core_t(s, RG, rdt, ldrg, n_out, ZG, n_out, 0, zt, (bf16_t*)tmp, tsp));
+    RC(trinv_core_t(s, RX, rdt, ldrx, n_in, ZX, n_in, 0, zt, zt + (size_t)n_in * n_in, n_in, false,
+                    (bf16_t*)tmp, tsp));
+    RC(trinv_core_t(s, RG, rdt, ldrg, n_out, ZG, n_out, 0, zt, zt + (size_t)n_out * n_out, n_out,
+                    false, (bf16_t*)tmp, tsp));
   } else {
     RC(trinv_core(s, RX, rdt, ldrx, n_in, ZX, n_in, math, 0, tmp, tsp));
     RC(trinv_core(s, RG, rdt, ldrg, n_out, ZG, n_out, math, 0, tmp, tsp));

@@ -92,6 +92,8 @@ class IFKFAC(torch.optim.Optimizer):
 
         self._factors: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._inverses: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        # bf16 arithmetic: RNE bf16 copies ((Z_X, Z_X^T), (Z_G, Z_G^T)) per layer
+        self._inverse_copies: Dict[nn.Module, tuple] = {}
         self._classic_fallback: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._momentum_buffers: Dict[nn.Module, torch.Tensor] = {}
         self._step_count = 0
@@ -159,12 +161,24 @@ class IFKFAC(torch.optim.Optimizer):
         self._factors = clean
         be = get_backend()
         self._inverses = {}
+        self._inverse_copies = {}
+        copies = hasattr(be, "tri_inverse_bf16")
         for module, (R_X, R_G) in clean.items():
             m = solve_math_for(R_X.dtype)
-            self._inverses[module] = run_pair(R_X.device,
-                                              lambda R=R_X: be.tri_inverse(R, m),
-                                              lambda R=R_G: be.tri_inverse(R, m),
-                                              b_first=R_G.shape[0] > R_X.shape[0])
+            b_first = R_G.shape[0] > R_X.shape[0]
+            if m == MATH_BF16 and copies:
+                # bf16 arithmetic: keep the bf16 copies of Z and Z^T next to Z,
+                # so the per-step apply does not cast the inverses again
+                (ZX, ZXb, ZXt), (ZG, ZGb, ZGt) = run_pair(
+                    R_X.device, lambda R=R_X: be.tri_inverse_bf16(R),
+                    lambda R=R_G: be.tri_inverse_bf16(R), b_first=b_first)
+                self._inverses[module] = (ZX, ZG)
+                self._inverse_copies[module] = ((ZXb, ZXt), (ZGb, ZGt))
+            else:
+                self._inverses[module] = run_pair(R_X.device,
+                                                  lambda R=R_X: be.tri_inverse(R, m),
+                                                  lambda R=R_G: be.tri_inverse(R, m),
+                                                  b_first=b_first)
         self.timing["factor_compute"].append(time.perf_counter() - t0)
 
     # ------------------------------------------------------------------ apply
@@ -175,6 +189,12 @@ class IFKFAC(torch.optim.Optimizer):
         return None, None, None
 
     def _nat_grad(self, module: nn.Module, grad_w: torch.Tensor, trim: bool) -> torch.Tensor:
+        copies = self._inverse_copies.get(module)
+        if copies is not None:
+            (ZXb, ZXt), ZG2 = copies
+            if trim:
+                ZXb, ZXt = ZXb[:-1, :-1], ZXt[:-1, :-1]
+            return get_backend().precondition_apply_bf16(grad_w, (ZXb, ZXt), ZG2)
         Z_X, Z_G = self._inverses[module]
         if trim:
             Z_X = Z_X[:-1, :-1]
@@ -338,6 +358,7 @@ class IFKFAC(torch.optim.Optimizer):
         self.hooks.remove()
         self._factors.clear()
         self._inverses.clear()
+        self._inverse_copies.clear()
         self._classic_fallback.clear()
         self._momentum_buffers.clear()
 

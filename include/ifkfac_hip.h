@@ -116,6 +116,18 @@ int ifk_tri_inverse(void* stream, const void* R, int r_dtype, int64_t ldr, int64
                     int64_t ldz, int math, void* workspace, size_t workspace_bytes);
 
 /*
+ * ifk_tri_inverse in bf16 arithmetic that also hands back RNE bf16 copies
+ * Zb = Z and ZTb = Z^T (row stride ldb, the other triangle zero), the
+ * operands ifk_precondition_apply_bf16 reads without casting them again.
+ * No counterpart in the reference (its solves run per step on R); for
+ * callers that keep the inverses between factor updates.
+ */
+size_t ifk_tri_inverse_bf16_workspace_size(int64_t n);
+int ifk_tri_inverse_bf16(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n,
+                         float* Z, int64_t ldz, void* Zb, void* ZTb, int64_t ldb, void* workspace,
+                         size_t workspace_bytes);
+
+/*
  * Four triangular solves -- replaces apply_vered(grad_W, R_X, R_G)
  * (ifkfac/triangular.py:551-656) and the per-entry body of
  * apply_vered_batched (ifkfac/triangular.py:430-451, :506-544):
@@ -134,6 +146,12 @@ int ifk_precondition_apply(void* stream, const float* grad, int64_t n_out, int64
                            int64_t ldg, const float* Z_X, int64_t ldzx, const float* Z_G,
                            int64_t ldzg, float* nat, int64_t ldn, int math, void* workspace,
                            size_t workspace_bytes);
+/* the same in bf16 arithmetic from the copies of ifk_tri_inverse_bf16 */
+size_t ifk_precondition_apply_bf16_workspace_size(int64_t n_out, int64_t n_in);
+int ifk_precondition_apply_bf16(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                                int64_t ldg, const void* Z_Xb, const void* Z_Xt, int64_t ldzx,
+                                const void* Z_Gb, const void* Z_Gt, int64_t ldzg, float* nat,
+                                int64_t ldn, void* workspace, size_t workspace_bytes);
 
 /*
  * Bias preconditioning -- replaces apply_vered_bias(grad_b, R_G)

@@ -441,6 +441,47 @@ def test_tri_inverse_bf16(hip, n):
     assert np.all(np.tril(Z.cpu().numpy(), -1) == 0)
 
 
+@pytest.mark.parametrize("n", [1, 65, 300, 2049])
+def test_tri_inverse_bf16_copies(hip, n):
+    """ifk_tri_inverse_bf16: the same Z as ifk_tri_inverse in bf16 arithmetic,
+    bit for bit, and its bf16 copies are exactly the RNE roundings of Z and
+    Z^T (other triangle zero)."""
+    rng = np.random.default_rng(n + 11)
+    R = np.triu(rng.standard_normal((n, n))) / math.sqrt(n) + 2 * np.eye(n)
+    Rb = torch.tensor(R, dtype=torch.float32, device=DEV).to(torch.bfloat16)
+    Z0 = hip.tri_inverse(Rb, 1)
+    Z, Zb, ZT = hip.tri_inverse_bf16(Rb)
+    assert torch.equal(Z, Z0)
+    assert torch.equal(Zb, Z.bfloat16())
+    assert torch.equal(ZT, Z.t().contiguous().bfloat16())
+
+
+@pytest.mark.parametrize("n_out,n_in,trim", [(256, 128, False), (1100, 700, False),
+                                             (300, 701, True)])
+def test_precondition_apply_bf16_copies(hip, n_out, n_in, trim):
+    """The apply from the bf16 copies equals the bf16 apply from fp32 Z bit for
+    bit (it reads the same RNE values), also for the trimmed views IFKFAC
+    passes with augment_bias."""
+    R_X = O.bf16_round(_factors(4 * n_in, n_in, 1e-2, 1e2, 1).astype(np.float32))
+    R_G = O.bf16_round(_factors(4 * n_out, n_out, 1e-2, 1e1, 2).astype(np.float32))
+    RX = torch.tensor(R_X, device=DEV).to(torch.bfloat16)
+    RG = torch.tensor(R_G, device=DEV).to(torch.bfloat16)
+    ZX, ZXb, ZXt = hip.tri_inverse_bf16(RX)
+    ZG, ZGb, ZGt = hip.tri_inverse_bf16(RG)
+    m = n_in - 1 if trim else n_in
+    if trim:
+        ZX, ZXb, ZXt = ZX[:-1, :-1], ZXb[:-1, :-1], ZXt[:-1, :-1]
+    g = torch.tensor(np.random.default_rng(3).normal(0, 0.1, (n_out, m)), dtype=torch.float32,
+                     device=DEV)
+    want = hip.precondition_apply(g, ZX.contiguous(), ZG, 1)
+    got = hip.precondition_apply_bf16(g, (ZXb, ZXt), (ZGb, ZGt))
+    assert torch.equal(got, want)
+    if not trim:
+        ref = O.apply_vered(g.double().cpu().numpy(), R_X.astype(np.float64),
+                            R_G.astype(np.float64))
+        assert _rel(got, ref) <= 2e-2
+
+
 # --------------------------------------------------------------------------- update
 
 
