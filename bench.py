@@ -183,13 +183,19 @@ def main() -> int:
                             lambda: be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16),
                             lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16),
                             b_first=n_out > n_in)
-        # RawActivationHooks._collect_factors(consume=True) of the update step
-        return run_pair(dev,
-                        lambda: be.fold_finalize(None, 0, X, scale, lam, torch.bfloat16,
-                                                 MATH_BF16),
-                        lambda: be.fold_finalize(None, 0, D, scale, lam, torch.bfloat16,
-                                                 MATH_BF16),
-                        b_first=n_out > n_in)
+        # RawActivationHooks._collect_factors(consume=True) of the update step:
+        # outer blocks by CholeskyQR2, then one host read of the status flags
+        # and the panel path for a side whose blocks were too ill-conditioned
+        ff = [lambda cqr: be.fold_finalize(None, 0, X, scale, lam, torch.bfloat16, MATH_BF16,
+                                           cqr=cqr),
+              lambda cqr: be.fold_finalize(None, 0, D, scale, lam, torch.bfloat16, MATH_BF16,
+                                           cqr=cqr)]
+        out = list(run_pair(dev, lambda: ff[0](True), lambda: ff[1](True), b_first=n_out > n_in))
+        st = torch.cat([out[0][1], out[1][1]]).cpu()
+        for i in range(2):
+            if int(st[i]) == 2:
+                out[i] = ff[i](False)
+        return out
 
     def step(first: bool, events=None):
         k = [0]
@@ -323,7 +329,7 @@ def main() -> int:
         "config": {
             "workload": f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, "
                         f"p={p} rows, bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9",
-            "factor_path": "fold then finalize" if args.unfused else "fused fold + finalize",
+            "factor_path": "fold then finalize" if args.unfused else "fused fold + finalize, 512-column blocks by CholeskyQR2 (panel path if flagged)",
             "n_in": n_in, "n_out": n_out, "p": p, "algorithmic_gflop_per_step": round(flops / 1e9, 1),
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
         },

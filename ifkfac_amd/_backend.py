@@ -109,12 +109,16 @@ class HipBackend:
         return out, flag
 
     def fold_finalize(self, R: Optional[torch.Tensor], r_in: int, X: torch.Tensor, scale: float,
-                      damping: float, out_dtype: torch.dtype,
-                      math: int) -> Tuple[torch.Tensor, torch.Tensor]:
+                      damping: float, out_dtype: torch.dtype, math: int,
+                      cqr: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
         """finalize(fold(R[:r_in], X)) in one factorisation, leaving R untouched.
 
         Returns (R_damped, finite flag int32[1]); R (n x n fp32 buffer whose
         first r_in rows are the running factor) may be None when r_in == 0.
+        With ``cqr`` the outer blocks are factored by CholeskyQR2
+        (ifk_fold_finalize_cqr): the flag is then 1 / 0 as above, or 2 when
+        a block was too ill-conditioned for it -- the caller must then call
+        again without ``cqr``.
         """
         X, ldx, xdt = _mat(X, "fold_finalize")
         p, n = X.shape
@@ -129,14 +133,15 @@ class HipBackend:
             ldr = R.stride(0) if R.shape[0] > 1 else n
         out = torch.empty((n, n), dtype=out_dtype, device=X.device)
         flag = torch.empty(1, dtype=torch.int32, device=X.device)
-        ws = self._ws(self.lib.ifk_fold_finalize_workspace_size(p, n, int(r_in)), X.device)
+        name = "ifk_fold_finalize_cqr" if cqr else "ifk_fold_finalize"
+        ws = self._ws(getattr(self.lib, name + "_workspace_size")(p, n, int(r_in)), X.device)
         with torch.cuda.device(X.device):
-            rc = self.lib.ifk_fold_finalize(self._stream(X.device), _ptr(X), xdt, p, n, ldx,
-                                            _ptr(R) if r_in > 0 else None, ldr, int(r_in),
-                                            float(scale), float(damping), _ptr(out),
-                                            _DT[out_dtype], n, int(math), _ptr(flag), _ptr(ws),
-                                            ws.numel())
-        _lib.check(rc, "ifk_fold_finalize")
+            rc = getattr(self.lib, name)(self._stream(X.device), _ptr(X), xdt, p, n, ldx,
+                                         _ptr(R) if r_in > 0 else None, ldr, int(r_in),
+                                         float(scale), float(damping), _ptr(out),
+                                         _DT[out_dtype], n, int(math), _ptr(flag), _ptr(ws),
+                                         ws.numel())
+        _lib.check(rc, name)
         return out, flag
 
     # -- preconditioning ------------------------------------------------------------

@@ -427,4 +427,79 @@ int launch_transpose_cast(hipStream_t s, const float* src, int64_t lds, int64_t 
   return check_launch("transpose_cast");
 }
 
+// dst[c][r] = src[r][c] for a rows x cols bf16 block, through a 64 x 64 LDS
+// tile; bf16 pairs move as 32-bit words where both ends of the row are even
+// (pair-aligned), element by element otherwise.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16_t* src, int64_t lds,
+                                                             int64_t rows, int64_t cols,
+                                                             bf16_t* dst, int64_t ldd,
+                                                             int pairs_in, int pairs_out) {
+  __shared__ bf16_t tile[64][66];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int e = t + 256 * q, r = e >> 5, cp = (e & 31) * 2;
+    const int64_t gr = r0 + r, gc = c0 + cp;
+    bf16_t a = 0, b = 0;
+    if (gr < rows) {
+      const bf16_t* g = src + gr * lds + gc;
+      if (pairs_in && gc + 1 < cols) {
+        const uint32_t w = *(const uint32_t*)g;
+        a = (bf16_t)(w & 0xffffu);
+        b = (bf16_t)(w >> 16);
+      } else {
+        if (gc < cols) a = g[0];
+        if (gc + 1 < cols) b = g[1];
+      }
+    }
+    tile[r][cp] = a;
+    tile[r][cp + 1] = b;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int e = t + 256 * q, c = e >> 5, rp = (e & 31) * 2;
+    const int64_t gc = c0 + c, gr = r0 + rp;
+    if (gc >= cols) continue;
+    bf16_t* g = dst + gc * ldd + gr;
+    if (pairs_out && gr + 1 < rows) {
+      *(uint32_t*)g = (uint32_t)tile[rp][c] | ((uint32_t)tile[rp + 1][c] << 16);
+    } else {
+      if (gr < rows) g[0] = tile[rp][c];
+      if (gr + 1 < rows) g[1] = tile[rp + 1][c];
+    }
+  }
+}
+
+int launch_transpose_bf16(hipStream_t s, const bf16_t* src, int64_t lds, int64_t rows,
+                          int64_t cols, bf16_t* dst, int64_t ldd) {
+  if (rows * cols == 0) return IFK_OK;
+  if (cdiv(rows, 64) > 65535) {
+    set_error("transpose_bf16: grid too large");
+    return IFK_ERR_INVALID;
+  }
+  // pair access needs every row start 4-byte aligned: an even row stride
+  // and an aligned base
+  const int pin = (lds % 2 == 0) && (((uintptr_t)src & 3) == 0);
+  const int pout = (ldd % 2 == 0) && (((uintptr_t)dst & 3) == 0);
+  const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64));
+  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, s, src, lds, rows, cols, dst, ldd,
+                     pin, pout);
+  return check_launch("transpose_bf16");
+}
+
+// A[i][i] += v for i < n
+__global__ void add_diag_kernel(float* A, int64_t lda, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    A[i * lda + i] += v;
+}
+
+int launch_add_diag(hipStream_t s, float* A, int64_t lda, int64_t n, float v) {
+  if (n <= 0) return IFK_OK;
+  hipLaunchKernelGGL(add_diag_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, A, lda, n, v);
+  return check_launch("add_diag");
+}
+
 }  // namespace ifk

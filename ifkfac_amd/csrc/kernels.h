@@ -47,6 +47,24 @@ int launch_sub_transposed(hipStream_t s, float* R, int64_t ldr, const float* WT,
 int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,
                    int64_t ldt);
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
+// Blocked upper Cholesky A = U^T U of an n x n fp32 matrix, n <= 512 (one
+// launch per 64-column step; A's blocks right of the diagonal are
+// overwritten by the trailing updates).  U (ld ldu) receives the blocks on
+// and above the diagonal, Zd (ceil(n / 64) x 4096 floats) the inverses of the
+// diagonal 64-blocks, dref (n floats) diag(A).  A pivot below tol * diag(A)_i
+// sets *flag.
+int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
+                 float* dref, float tol, int* flag);
+// Householder reconstruction of a block CholeskyQR'd with P_top = c I (upper
+// parts; strict lower parts set to 0): A = c M1 + U2, and R = -P
+int launch_cqr_amat(hipStream_t s, const float* M1, const float* U2, int64_t ld, int n, float c,
+                    float* A, int64_t lda);
+int launch_cqr_rnew(hipStream_t s, const float* P, int64_t ldp, int n, float* R, int64_t ldr);
+// hi = RNE bf16(src), lo = RNE bf16(src - hi); transposed (hi[c][r]) with trans
+int launch_split_bf16(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
+                      bf16_t* hi, bf16_t* lo, int64_t ldo, bool trans = false);
+// *status = 2 if *flag != 0
+int launch_status_merge(hipStream_t s, int* status, const int* flag);
 // (and, when given, RNE bf16 copies of the blocks into Zb row-major and into
 // ZTb transposed, both of row stride ldb)
 int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int nb,
@@ -105,6 +123,11 @@ int launch_transpose_upper(hipStream_t s, const float* src, int64_t lds, int64_t
 int launch_transpose_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
                           void* out, int odt, int64_t ldo, int batch = 1, int64_t bss = 0,
                           int64_t bso = 0);
+// dst[c][r] = src[r][c] for a rows x cols bf16 block
+int launch_transpose_bf16(hipStream_t s, const bf16_t* src, int64_t lds, int64_t rows,
+                          int64_t cols, bf16_t* dst, int64_t ldd);
+// A[i][i] += v, i < n
+int launch_add_diag(hipStream_t s, float* A, int64_t lda, int64_t n, float v);
 // out (dt) = alpha * x (fp32) with optional bf16 output
 int launch_scale_copy_vec(hipStream_t s, const float* x, int64_t n, float alpha, void* out, int odt);
 

@@ -28,6 +28,16 @@ int fold_finalize(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, i
                   void* out, int odt, int64_t ldo, int math, int* finite, void* ws,
                   size_t ws_bytes);
 
+// fold_finalize with each 512-column outer block factored by CholeskyQR2 +
+// Householder reconstruction instead of its 64-column panel chain.  *status:
+// 1 finite, 0 not finite, 2 a block was too ill-conditioned for CholeskyQR
+// (the output is meaningless; fold_finalize computes it).
+size_t fold_finalize_cqr_ws(int64_t p, int64_t n, int64_t r_in);
+int fold_finalize_cqr(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                      const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
+                      void* out, int odt, int64_t ldo, int math, int* status, void* ws,
+                      size_t ws_bytes);
+
 // Z = R^{-1} for upper-triangular R (dtype rdt); Z fp32 upper triangular.
 size_t trinv_ws(int64_t n);
 int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,

@@ -143,6 +143,50 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
   w.split2.p = a.take<float>(w.split2.floats);
 }
 
+// Workspace of the block CholeskyQR path (cqr_block): 512 x 512 factors of
+// the outer block, the Cholesky's diagonal inverses, and the block's tall
+// operands in both layouts (pe x 512 row-major, and transposed 512 x pe with
+// row stride ldq), fp32 or bf16 by the arithmetic.
+struct CqrWs {
+  float* G;       // G1, then G2 (upper parts read)
+  float* U1;
+  float* M1;      // U1^{-1}
+  float* MT;      // M1^T (fp32 arithmetic), or its bf16 split hi | lo
+  float* U2;
+  float* Am;      // c M1 + U2, then U2 U1
+  float* N;       // (c M1 + U2)^{-1}
+  float* NT;      // N^T (fp32 or bf16)
+  float* Zd;      // 8 x 64 x 64
+  float* dref;
+  float* Xc;      // X, pe x 512 (fp32 or bf16)
+  float* Q2f;     // Q2 = X M1, pe x 512 fp32
+  bf16_t* Q2b;    // its bf16 copy (bf16 arithmetic)
+  float* Q2T;     // Q2^T, 512 x pe (ld ldq; fp32 or bf16)
+  int64_t ldq;
+  int* flag;      // set when a block needs the Householder path
+};
+
+static void plan_cqr(Arena& a, int64_t pe, CqrWs& q) {
+  const int64_t B = OUTER_B;
+  const size_t pb = (size_t)(pe > 0 ? pe : 1) * B;
+  q.G = a.take<float>(B * B);
+  q.U1 = a.take<float>(B * B);
+  q.M1 = a.take<float>(B * B);
+  q.MT = a.take<float>(B * B);
+  q.U2 = a.take<float>(B * B);
+  q.Am = a.take<float>(B * B);
+  q.N = a.take<float>(B * B);
+  q.NT = a.take<float>(B * B);
+  q.Zd = a.take<float>((size_t)(B / 64) * 64 * 64);
+  q.dref = a.take<float>(B);
+  q.Xc = a.take<float>(pb);
+  q.Q2f = a.take<float>(pb);
+  q.Q2b = a.take<bf16_t>(pb);
+  q.ldq = (int64_t)align_up((size_t)(pe > 0 ? pe : 1), 8);
+  q.Q2T = a.take<float>((size_t)B * q.ldq);
+  q.flag = a.take<int>(64);
+}
+
 // ----------------------------------------------------------------------------
 // Helper streams and events of the look-ahead (one set per device and
 // calling stream, created on first use; a fold holds the set's lock while it
@@ -260,6 +304,90 @@ static int outer_finish(hipStream_t s, int math, FoldWs& w, int k2, float* CT, b
               Crb ? out_both(Cr, ldc, Crb, ldc) : out_f32(Cr, ldc), 1, sp, max_wgs);
 }
 
+// Outer block [K0, K1) factored as a whole by CholeskyQR2 with Householder
+// reconstruction, in place of its chain of 64-column panels.  P = [c I; X]:
+// the block's rows of R are still the damping diagonal c I of the fused
+// fold + finalize (only a block's own factorisation writes them), and X =
+// C[:, K0:K1] (rows K0:K1 of CT, pe columns):
+//   G1 = X^T X + c^2 I = U1^T U1,   M1 = U1^{-1}
+//   Q = P M1 = [c M1; Q2],  Q2 = X M1            (nearly orthonormal)
+//   G2 = Q2^T Q2 + c^2 M1^T M1 = U2^T U2         (Q_f = Q U2^{-1} orthonormal)
+//   S = -I (Q's top block c M1 has a positive diagonal),
+//   N = (c M1 - S U2)^{-1} = (c M1 + U2)^{-1},  Y = Q2 N,  R_new = S U2 U1
+// Y is the Householder reconstruction Q_f,bot (Q_f,top - S)^{-1} (Q_f,top - S
+// = (c M1 + U2) U2^{-1}), so V = [I; Y] and R_new are the TPQRT factors of P
+// the panel chain produces; the block's T then follows from the UT
+// transform of Y in outer_prepare, as for the panel path.  The block's own
+// columns of C are not needed afterwards and are left as they are.
+// Every tall product reads K-contiguous operands: X and Q2 are kept in both
+// layouts (the transposes are plain copies).
+// bf16 arithmetic: X is read as bf16 (the shadow), Q2 = X (M1_hi + M1_lo)
+// (the bf16 split of M1 keeps Q consistent with its top block and with
+// R_new to about 2^-17) is rounded to bf16, and Y is written as the bf16
+// copies the outer update reads; U1, U2, N and R_new stay fp32.  A Cholesky
+// pivot of pass 1 below HR_TOL, or of pass 2 below 1/4, of its diagonal
+// sets q.flag: the block was too ill-conditioned for CholeskyQR and the
+// factor must be recomputed by the panel path.
+static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
+                     const float* C, const bf16_t* Cb, int64_t ldc, int64_t pe, float* R,
+                     int64_t ldr, int64_t K0, int64_t K1, bool outer) {
+  const int64_t B = OUTER_B, KB = K1 - K0, ldq = q.ldq;
+  const bool bf = math == MATH_BF16;
+  const int tdt = bf ? DT_BF16 : DT_F32;   // dtype of the tall operands
+  const float* Xf = C + K0 * ldc;
+  const bf16_t* Xb = Cb ? Cb + K0 * ldc : nullptr;
+  // pass 1: G1 = X^T X + c^2 I = U1^T U1, M1 = U1^{-1}
+  const MatRef XA = Xb ? A_n(Xb, DT_BF16, ldc) : A_n(Xf, DT_F32, ldc);
+  const MatRef XB = Xb ? B_t(Xb, DT_BF16, ldc) : B_t(Xf, DT_F32, ldc);
+  RC(gemm(s, math, KB, KB, pe, 1.0f, XA, XB, 0.0f, out_f32(q.G, B), 1, w.split));
+  RC(launch_add_diag(s, q.G, B, KB, c * c));
+  RC(launch_cholb(s, q.G, B, (int)KB, q.U1, B, q.Zd, q.dref, HR_TOL, q.flag));
+  RC(trinv_core(s, q.U1, DT_F32, B, KB, q.M1, B, MATH_F32, 0, w.ttmp, w.tsp));
+  // X in its pe x KB layout, then Q2 = X M1 (pe x KB)
+  if (Xb) RC(launch_transpose_bf16(s, Xb, ldc, KB, pe, (bf16_t*)q.Xc, B));
+  else RC(launch_transpose_cast(s, Xf, ldc, KB, pe, q.Xc, tdt, B));
+  if (bf) {
+    bf16_t* MTh = (bf16_t*)q.MT;
+    bf16_t* MTl = MTh + B * B;
+    RC(launch_split_bf16(s, q.M1, B, KB, KB, MTh, MTl, B, true));
+    RC(gemm(s, MATH_BF16, pe, KB, KB, 1.0f, A_n(q.Xc, DT_BF16, B),
+            B_t(MTh, DT_BF16, B, TRI_UPPER), 0.0f, out_f32(q.Q2f, B), 1, w.split));
+    RC(gemm(s, MATH_BF16, pe, KB, KB, 1.0f, A_n(q.Xc, DT_BF16, B),
+            B_t(MTl, DT_BF16, B, TRI_UPPER), 1.0f, out_both(q.Q2f, B, q.Q2b, B), 1, w.split));
+    RC(launch_transpose_bf16(s, q.Q2b, B, pe, KB, (bf16_t*)q.Q2T, ldq));
+  } else {
+    RC(launch_transpose_cast(s, q.M1, B, KB, KB, q.MT, DT_F32, B));
+    RC(gemm(s, MATH_F32, pe, KB, KB, 1.0f, A_n(q.Xc, DT_F32, B),
+            B_t(q.MT, DT_F32, B, TRI_UPPER), 0.0f, out_f32(q.Q2f, B), 1, w.split));
+    RC(launch_transpose_cast(s, q.Q2f, B, pe, KB, q.Q2T, DT_F32, ldq));
+  }
+  // pass 2: G2 = Q2^T Q2 + c^2 M1^T M1 = U2^T U2
+  RC(gemm(s, math, KB, KB, pe, 1.0f, A_n(q.Q2T, tdt, ldq), B_t(q.Q2T, tdt, ldq), 0.0f,
+          out_f32(q.G, B), 1, w.split));
+  if (c > 0.0f)
+    RC(gemm(s, MATH_F32, KB, KB, KB, c * c, A_t(q.M1, DT_F32, B, TRI_LOWER),
+            B_n(q.M1, DT_F32, B, TRI_UPPER), 1.0f, out_f32(q.G, B), 1, w.split));
+  RC(launch_cholb(s, q.G, B, (int)KB, q.U2, B, q.Zd, q.dref, 0.25f, q.flag));
+  // reconstruction: N = (c M1 + U2)^{-1}, Y = Q2 N (and its transpose)
+  if (outer) {
+    RC(launch_cqr_amat(s, q.M1, q.U2, B, (int)KB, c, q.Am, B));
+    RC(trinv_core(s, q.Am, DT_F32, B, KB, q.N, B, MATH_F32, 0, w.ttmp, w.tsp));
+    RC(launch_transpose_cast(s, q.N, B, KB, KB, q.NT, tdt, B));
+    if (bf) {
+      RC(gemm(s, MATH_BF16, pe, KB, KB, 1.0f, A_n(q.Q2b, DT_BF16, B),
+              B_t(q.NT, DT_BF16, B, TRI_UPPER), 0.0f, out_bf16(w.Yob[k2], B), 1, w.split));
+      RC(launch_transpose_bf16(s, w.Yob[k2], B, pe, KB, w.YobT[k2], ldc));
+    } else {
+      RC(gemm(s, MATH_F32, pe, KB, KB, 1.0f, A_n(q.Q2f, DT_F32, B),
+              B_t(q.NT, DT_F32, B, TRI_UPPER), 0.0f, out_f32(w.Yo[k2], B), 1, w.split));
+    }
+  }
+  // R_new = S U2 U1 = -U2 U1
+  RC(gemm(s, MATH_F32, KB, KB, KB, 1.0f, A_n(q.U2, DT_F32, B, TRI_UPPER),
+          B_n(q.U1, DT_F32, B, TRI_UPPER), 0.0f, out_f32(q.Am, B), 1, w.split));
+  return launch_cqr_rnew(s, q.Am, B, (int)KB, R + K0 * ldr + K0, ldr);
+}
+
 // Core of the fold on the transposed fp32 working copy CT = C^T (n x p, row
 // stride ldc; a panel X_p = C[:, c0:c1] is the contiguous row block
 // CT[c0:c1, :]).  R rows [0, r_new) receive the result.  Two-level blocking:
@@ -279,8 +407,15 @@ static int outer_finish(hipStream_t s, int math, FoldWs& w, int k2, float* CT, b
 //   far(k - 2) -> panels(k);  far(last) -> end of fold.
 // With x_tri, C is upper triangular and a panel ending at column c1
 // involves C rows [0, c1).
+static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
+                     const float* C, const bf16_t* Cb, int64_t ldc, int64_t pe, float* R,
+                     int64_t ldr, int64_t K0, int64_t K1, bool outer);
+
+// With cq, every outer block is factored by cqr_block; R's rows are then
+// expected to hold c I on entry (cq_c), as fold_finalize sets them.
 static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n, float* R,
-                     int64_t ldr, int64_t r_new, bool x_tri, int math, FoldWs& w) {
+                     int64_t ldr, int64_t r_new, bool x_tri, int math, FoldWs& w,
+                     CqrWs* cq = nullptr, float cq_c = 0.0f) {
   const int64_t B = OUTER_B;
   int rc = IFK_OK;
   LookAhead* la = nullptr;
@@ -314,7 +449,8 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
       if (bf) RC(launch_zero_bf16(s, w.Yob[k2], B, pe_o, KB));
       if (bf && outer) RC(launch_zero_bf16(s, w.YobT[k2], ldc, KB, pe_o));
     }
-    for (int64_t c0 = K0; c0 < K1; c0 += PANEL_B) {
+    if (cq) RC(cqr_block(s, math, w, *cq, k2, cq_c, C, Cb, ldc, pe_o, R, ldr, K0, K1, outer));
+    for (int64_t c0 = K0; c0 < K1 && !cq; c0 += PANEL_B) {
       const int bk = (int)std::min<int64_t>(PANEL_B, K1 - c0);
       const int64_t c1 = c0 + bk;
       const int nr = (int)(K1 - c1);
@@ -517,6 +653,61 @@ int fold_finalize(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, i
   }
   if (finite) RC(launch_fill_int(s, finite, 1, 1));
   return launch_cast_upper(s, Rw, n, n, out, odt, ldo, finite, scale);
+}
+
+// The same factor with every outer block factored by cqr_block instead of
+// its panel chain.  *status: 1 = the factor is finite, 0 = not finite, 2 =
+// some block was too ill-conditioned for CholeskyQR (the output is then
+// meaningless and the caller recomputes it with fold_finalize).
+static void plan_fold_finalize_cqr(Arena& a, int64_t pe, int64_t n, float** Rw, FoldWs& w,
+                                   CqrWs& q) {
+  plan_fold_finalize(a, pe, n, Rw, w);
+  plan_cqr(a, pe, q);
+}
+
+size_t fold_finalize_cqr_ws(int64_t p, int64_t n, int64_t r_in) {
+  Arena a(nullptr, 0);
+  float* Rw;
+  FoldWs w;
+  CqrWs q;
+  plan_fold_finalize_cqr(a, r_in + p, n, &Rw, w, q);
+  return a.used;
+}
+
+int fold_finalize_cqr(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                      const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
+                      void* out, int odt, int64_t ldo, int math, int* status, void* ws,
+                      size_t ws_bytes) {
+  if (n < 1 || p < 0 || r_in < 0 || r_in > n || (p > 0 && (!X || ldx < n)) ||
+      (r_in > 0 && (!R_in || ldr < n)) || !out || ldo < n || !(scale > 0.0f) ||
+      !(damping >= 0.0f) || (xdt != DT_F32 && xdt != DT_BF16) ||
+      (odt != DT_F32 && odt != DT_BF16) || !status) {
+    set_error("fold_finalize_cqr: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  const int64_t pe = r_in + p;
+  if (!(damping > 0.0f) && pe < n) {
+    set_error("fold_finalize_cqr: fewer rows than columns and no damping (the factor is not square)");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  float* Rw;
+  FoldWs w;
+  CqrWs q;
+  plan_fold_finalize_cqr(a, pe, n, &Rw, w, q);
+  RC(check_ws(a, "fold_finalize_cqr"));
+  RC(launch_fill_int(s, q.flag, 0, 1));
+  RC(launch_set_diag(s, Rw, n, n, std::sqrt(damping) / scale));
+  if (r_in > 0) RC(launch_transpose_to_f32(s, R_in, DT_F32, ldr, r_in, n, w.C, pe, true));
+  if (p > 0) RC(launch_transpose_to_f32(s, X, xdt, ldx, p, n, w.C + r_in, pe));
+  if (pe > 0) {
+    RC(fold_core(s, w.C, pe, pe, n, Rw, n, n, false, math, w, &q, std::sqrt(damping) / scale));
+  } else {
+    RC(launch_sign_normalize(s, Rw, n, n, n));
+  }
+  RC(launch_fill_int(s, status, 1, 1));
+  RC(launch_cast_upper(s, Rw, n, n, out, odt, ldo, status, scale));
+  return launch_status_merge(s, status, q.flag);
 }
 
 // ----------------------------------------------------------------------------

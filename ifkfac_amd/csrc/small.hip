@@ -141,10 +141,10 @@ __device__ inline float safe_divisor(float d) {
 }
 
 // Upper Cholesky in place (A = U^T U, upper triangle read, strict lower
-// zeroed on exit).  mode 0: a pivot below tol * (its diagonal on entry) or not
-// finite raises *bad (the factorisation continues on a clamped pivot so every
-// thread runs the same steps); mode 1: the pivot rule of cholesky_bf16,
-// max(pivot, 1e-7).
+// zeroed on exit).  mode 0: a pivot below tol * (its diagonal on entry, or
+// dref[i] for i < b when dref is given) or not finite raises *bad (the
+// factorisation continues on a clamped pivot so every thread runs the same
+// steps); mode 1: the pivot rule of cholesky_bf16, max(pivot, 1e-7).
 //
 // Right-looking, blocked by CB columns.  Wave 0 factors each CB x CB diagonal
 // block redundantly in every lane's registers (no cross-lane traffic on the
@@ -154,11 +154,12 @@ __device__ inline float safe_divisor(float d) {
 // four waves.  Two barriers per block.  CB = 8 measured fastest (the 16 x 16
 // register leaf costs more than the extra barriers it saves).
 template <int CB = 8>
-__device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode) {
+__device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode,
+                                          const float* dref = nullptr, int b = SB) {
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  __shared__ float dgs[SB];   // diagonal on entry, for the pivot test
-  if (t < SB) dgs[t] = A[t * SLD + t];
+  __shared__ float dgs[SB];   // reference diagonal of the pivot test
+  if (t < SB) dgs[t] = (dref != nullptr && t < b) ? dref[t] : A[t * SLD + t];
   __syncthreads();
   int flag = 0;
 #pragma unroll 1
@@ -674,6 +675,162 @@ __global__ __launch_bounds__(SNT) void chol_block_kernel(float* A, int64_t ld, i
   }
 }
 
+// ---------------------------------------------------------------------------
+// Blocked upper Cholesky of an n x n fp32 matrix (n <= CHOLB_MAX) held in
+// global memory, for the CholeskyQR of a whole outer block of the fold.
+// Right-looking over 64-column steps, one launch per step:
+//   cholb_first:   dref = diag(A) (the reference of the pivot test), then
+//                  U_00 = chol(A_00) and Z_0 = U_00^{-1}
+//   cholb_step k:  workgroup (i, j), k < i <= j: U_ki = Z_k^T A_ki and
+//                  U_kj = Z_k^T A_kj (each workgroup forms the two blocks it
+//                  needs), A_ij -= U_ki^T U_kj; workgroup (j, j) stores U_kj;
+//                  workgroup (k+1, k+1) goes on to factor its updated block,
+//                  U_{k+1,k+1} and Z_{k+1}, which the next step reads.
+// A launch reads block row k of A and writes only blocks (i, j) with i > k,
+// so its workgroups never race.  U (ld ldu) receives the blocks on and above
+// the diagonal (the ones below are not written); Zd holds the 64 x 64
+// inverses of the diagonal blocks (identity beyond n).  A pivot below tol *
+// dref[i] or not finite sets *flag (the factorisation goes on with clamped
+// pivots, so every launch still runs the same steps).
+// ---------------------------------------------------------------------------
+constexpr int CHOLB_MAX = 8 * SB;
+
+// rows x cols block (row stride ld) into registers as a padded 64 x 64 tile:
+// outside the block the tile is pad * I
+__device__ __forceinline__ void ld_blk(float (&v)[PAD_PER], const float* g, int64_t ld, int rows,
+                                       int cols, float pad) {
+#pragma unroll
+  for (int q = 0; q < PAD_PER; ++q) {
+    const int e = threadIdx.x + SNT * q;
+    const int r = e >> 6, c = e & 63;
+    v[q] = (r < rows && c < cols) ? g[(int64_t)r * ld + c] : (r == c ? pad : 0.0f);
+  }
+}
+
+__device__ __forceinline__ void st_blk(const float* S, float* g, int64_t ld, int rows, int cols) {
+  for (int e = threadIdx.x; e < SB * SB; e += SNT) {
+    const int r = e >> 6, c = e & 63;
+    if (r < rows && c < cols) g[(int64_t)r * ld + c] = S[r * SLD + c];
+  }
+}
+
+__global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_t lda, int n,
+                                                          float* U, int64_t ldu, float* Zd,
+                                                          float* dref, float tol, int* flag) {
+  __shared__ float sC[SB * SLD];
+  __shared__ float sZ[SB * SLD];
+  __shared__ float sT[TRINV_TMP];
+  __shared__ int bad;
+  const int t = threadIdx.x;
+  const int b0 = n < SB ? n : SB;
+  if (t == 0) bad = 0;
+  for (int e = t; e < n; e += SNT) dref[e] = A[(int64_t)e * lda + e];
+  float v[PAD_PER];
+  ld_blk(v, A, lda, b0, b0, 1.0f);
+  st_pad(sC, v);
+  __syncthreads();
+  sm_chol64(sC, tol, &bad, 0);   // block 0: its diagonal on entry is A's
+  st_blk(sC, U, ldu, b0, b0);
+  sm_trinv64(sC, sZ, sT);
+  for (int e = t; e < SB * SB; e += SNT) Zd[e] = sZ[(e >> 6) * SLD + (e & 63)];
+  if (t == 0 && bad) *flag = 1;
+}
+
+__global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, int n, float* U,
+                                                         int64_t ldu, float* Zd,
+                                                         const float* dref, float tol, int* flag,
+                                                         int k) {
+  __shared__ float sZ[SB * SLD];
+  __shared__ float sA[SB * SLD];
+  __shared__ float sB[SB * SLD];
+  __shared__ float sC[SB * SLD];
+  __shared__ float sT[TRINV_TMP];
+  __shared__ int bad;
+  const int t = threadIdx.x;
+  const int nb = (n + SB - 1) / SB;
+  // workgroup -> (i, j), k < i <= j < nb, row by row
+  int idx = blockIdx.x, i = k + 1;
+  while (idx >= nb - i) {
+    idx -= nb - i;
+    ++i;
+  }
+  const int j = i + idx;
+  const int bi = (n - SB * i) < SB ? (n - SB * i) : SB;
+  const int bj = (n - SB * j) < SB ? (n - SB * j) : SB;
+  const bool diag = (i == j);
+  if (t == 0) bad = 0;
+  const float* Ak = A + (int64_t)SB * k * lda;   // block row k (full: k < nb - 1)
+  float vz[PAD_PER], va[PAD_PER], vb[PAD_PER], vc[PAD_PER];
+#pragma unroll
+  for (int q = 0; q < PAD_PER; ++q) vz[q] = Zd[(size_t)k * SB * SB + t + SNT * q];
+  ld_blk(va, Ak + SB * i, lda, SB, bi, 0.0f);
+  if (!diag) ld_blk(vb, Ak + SB * j, lda, SB, bj, 0.0f);
+  ld_blk(vc, A + (int64_t)SB * i * lda + SB * j, lda, bi, bj, diag ? 1.0f : 0.0f);
+  st_pad(sZ, vz);
+  st_pad(sA, va);
+  if (!diag) st_pad(sB, vb);
+  st_pad(sC, vc);
+  __syncthreads();
+  sm_gemm64<true, false>(sZ, sA, sA, 1.0f, false);                // U_ki
+  if (!diag) sm_gemm64<true, false>(sZ, sB, sB, 1.0f, false);     // U_kj
+  if (diag) st_blk(sA, U + (int64_t)SB * k * ldu + SB * j, ldu, SB, bj);
+  sm_gemm64<true, false>(sA, diag ? sA : sB, sC, -1.0f, true);    // A_ij -= U_ki^T U_kj
+  if (diag && i == k + 1) {
+    sm_chol64(sC, tol, &bad, 0, dref + SB * i, bi);
+    st_blk(sC, U + (int64_t)SB * i * ldu + SB * i, ldu, bi, bi);
+    sm_trinv64(sC, sZ, sT);
+    for (int e = t; e < SB * SB; e += SNT)
+      Zd[(size_t)i * SB * SB + e] = sZ[(e >> 6) * SLD + (e & 63)];
+    if (t == 0 && bad) *flag = 1;
+  } else {
+    st_blk(sC, A + (int64_t)SB * i * lda + SB * j, lda, bi, bj);
+  }
+}
+
+// Householder reconstruction of a block CholeskyQR'd with P_top = c I (c >=
+// 0, so Q1 = c M1 has a positive diagonal and S = -I):
+//   cqr_amat:  A = Q1 - S U2 = c M1 + U2     (upper part; strict lower 0)
+//   cqr_rnew:  R = S P = -P, P = U2 U1       (upper part; strict lower 0)
+__global__ void cqr_amat_kernel(const float* M1, const float* U2, int64_t ld, int n, float c,
+                                float* A, int64_t lda) {
+  const int64_t total = (int64_t)n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / n, j = e % n;
+    A[i * lda + j] = (i <= j) ? fmaf(c, M1[i * ld + j], U2[i * ld + j]) : 0.0f;
+  }
+}
+
+__global__ void cqr_rnew_kernel(const float* P, int64_t ldp, int n, float* R, int64_t ldr) {
+  const int64_t total = (int64_t)n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / n, j = e % n;
+    R[i * ldr + j] = (i <= j) ? -P[i * ldp + j] : 0.0f;
+  }
+}
+
+// hi = RNE bf16(src), lo = RNE bf16(src - hi) (rows x cols, fp32 src), written
+// transposed (hi[c][r]) when trans is set
+__global__ void split_bf16_kernel(const float* src, int64_t lds, int64_t rows, int64_t cols,
+                                  bf16_t* hi, bf16_t* lo, int64_t ldo, int trans) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e % cols;
+    const float x = src[r * lds + c];
+    const bf16_t h = f32_to_bf16(x);
+    const int64_t o = trans ? c * ldo + r : r * ldo + c;
+    hi[o] = h;
+    lo[o] = f32_to_bf16(x - bf16_to_f32(h));
+  }
+}
+
+// *status = 2 when *flag is set (a single thread)
+__global__ void status_merge_kernel(int* status, const int* flag) {
+  if (threadIdx.x == 0 && blockIdx.x == 0 && *flag != 0) *status = 2;
+}
+
 // UT transform: T^{-1} = striu(G) + diag(1 + diag G) / 2 for a Gram matrix G.
 __global__ void ut_tinv_kernel(const float* G, int64_t ldg, int64_t n, float* Tinv, int64_t ldt) {
   const int64_t total = n * n;
@@ -907,6 +1064,60 @@ int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b) {
   if (int rc = check_b(b, "chol_block")) return rc;
   hipLaunchKernelGGL(chol_block_kernel, dim3(1), dim3(SNT), 0, s, A, ld, b);
   return check_launch("chol_block");
+}
+
+int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
+                 float* dref, float tol, int* flag) {
+  if (n < 1 || n > CHOLB_MAX || lda < n || ldu < n) {
+    set_error("cholb: size out of range");
+    return IFK_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(cholb_first_kernel, dim3(1), dim3(SNT), 0, s, A, lda, n, U, ldu, Zd, dref, tol,
+                     flag);
+  if (int rc = check_launch("cholb_first")) return rc;
+  const int nb = (n + SB - 1) / SB;
+  for (int k = 0; k + 1 < nb; ++k) {
+    const int m = nb - 1 - k;   // blocks right of k; (i, j) pairs: m (m + 1) / 2
+    hipLaunchKernelGGL(cholb_step_kernel, dim3((unsigned)(m * (m + 1) / 2)), dim3(SNT), 0, s, A,
+                       lda, n, U, ldu, Zd, dref, tol, flag, k);
+    if (int rc = check_launch("cholb_step")) return rc;
+  }
+  return IFK_OK;
+}
+
+static unsigned ew_grid(int64_t total) {
+  int64_t g = cdiv(total, 256);
+  if (g < 1) g = 1;
+  if (g > 1024) g = 1024;
+  return (unsigned)g;
+}
+
+int launch_cqr_amat(hipStream_t s, const float* M1, const float* U2, int64_t ld, int n, float c,
+                    float* A, int64_t lda) {
+  if (n <= 0) return IFK_OK;
+  hipLaunchKernelGGL(cqr_amat_kernel, dim3(ew_grid((int64_t)n * n)), dim3(256), 0, s, M1, U2, ld, n,
+                     c, A, lda);
+  return check_launch("cqr_amat");
+}
+
+int launch_cqr_rnew(hipStream_t s, const float* P, int64_t ldp, int n, float* R, int64_t ldr) {
+  if (n <= 0) return IFK_OK;
+  hipLaunchKernelGGL(cqr_rnew_kernel, dim3(ew_grid((int64_t)n * n)), dim3(256), 0, s, P, ldp, n, R,
+                     ldr);
+  return check_launch("cqr_rnew");
+}
+
+int launch_split_bf16(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
+                      bf16_t* hi, bf16_t* lo, int64_t ldo, bool trans) {
+  if (rows <= 0 || cols <= 0) return IFK_OK;
+  hipLaunchKernelGGL(split_bf16_kernel, dim3(ew_grid(rows * cols)), dim3(256), 0, s, src, lds, rows,
+                     cols, hi, lo, ldo, trans ? 1 : 0);
+  return check_launch("split_bf16");
+}
+
+int launch_status_merge(hipStream_t s, int* status, const int* flag) {
+  hipLaunchKernelGGL(status_merge_kernel, dim3(1), dim3(64), 0, s, status, flag);
+  return check_launch("status_merge");
 }
 
 int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,

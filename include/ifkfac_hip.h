@@ -107,6 +107,28 @@ int ifk_fold_finalize(void* stream, const void* X, int x_dtype, int64_t p, int64
                       int32_t* finite, void* workspace, size_t workspace_bytes);
 
 /*
+ * ifk_fold_finalize with each 512-column outer block of the TPQRT fold
+ * factored at once by CholeskyQR2 with Householder reconstruction, instead
+ * of by its chain of 64-column panels: the block's work becomes a few large
+ * MFMA products and 512 x 512 factorisations.  No counterpart in the
+ * reference (its fold is torch.linalg.qr, ifkfac/triangular.py:284-301 and
+ * :411-416); same arguments and result as ifk_fold_finalize, for callers
+ * that can read a status flag before using the factor.  *status (device):
+ *   1  the factor is finite;
+ *   0  it is not (non-finite input);
+ *   2  some block was too ill-conditioned for CholeskyQR (a Cholesky pivot
+ *      below 1e-4 of its diagonal in the first pass, or below 1/4 in the
+ *      second): the output is meaningless and ifk_fold_finalize, on the same
+ *      inputs, computes the factor.
+ * status must not be NULL.
+ */
+size_t ifk_fold_finalize_cqr_workspace_size(int64_t p, int64_t n, int64_t r_in);
+int ifk_fold_finalize_cqr(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
+                          int64_t ldx, const float* R_in, int64_t ldr, int64_t r_in, float scale,
+                          float damping, void* out, int out_dtype, int64_t ldo, int math,
+                          int32_t* status, void* workspace, size_t workspace_bytes);
+
+/*
  * Triangular inverse Z = R^{-1} of an upper-triangular n x n factor (dtype
  * r_dtype) into fp32 Z (ldz).  The four solves of apply_vered are applied as
  * products with Z; this is the factor-side half of them.

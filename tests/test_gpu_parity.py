@@ -335,15 +335,112 @@ def test_fold_finalize_guards_and_flags(hip):
     assert flag.item() == 1
 
 
+# --------------------------------------------------------------------------- block CholeskyQR
+
+
+@pytest.mark.parametrize("prev,p,n,lam", [
+    ([], 500, 300, 1e-2), ([300], 500, 300, 1e-2), ([64], 30, 128, 1e-2),
+    ([], 64, 64, 1e-3), ([], 3000, 1700, 1e-2), ([1200], 1200, 2100, 1e-2), ([], 20, 50, 1e-1),
+    ([], 4000, 1536, 1e-2), ([], 1, 600, 1e-2), ([2000], 100, 1030, 1e-3),
+])
+def test_fold_finalize_cqr_matches_closed_form(hip, prev, p, n, lam):
+    """Outer blocks factored by CholeskyQR2 + Householder reconstruction: the same
+    R_damped as the panel path, within 4 kappa eps_fp32 of the fp64 Cholesky closed
+    form, status 1, positive diagonal, exact zeros below it."""
+    g = torch.Generator(device=DEV).manual_seed(p + n + len(prev))
+    Xs = [torch.randn(q, n, device=DEV, generator=g) for q in prev]
+    X = torch.randn(p, n, device=DEV, generator=g)
+    R, r = _fold_chunks(hip, Xs, n)
+    R_before = R.clone()
+    rows = sum(prev) + p
+    Rd, st = hip.fold_finalize(R, r, X, 1 / math.sqrt(rows), lam, torch.float32, 0, cqr=True)
+    assert st.item() == 1
+    assert torch.equal(R, R_before)
+    want = O.chol_factor([x.double().cpu().numpy() for x in Xs + [X]], rows, lam)
+    assert _gram_rel(Rd, want) <= 4 * _kappa(want) * EPS32
+    Rg = Rd.double().cpu().numpy()
+    assert np.all(np.diag(Rg) > 0) and not np.any(np.tril(Rg, -1))
+    Rp, _ = hip.fold_finalize(R, r, X, 1 / math.sqrt(rows), lam, torch.float32, 0)
+    assert _gram_rel(Rd, Rp.double().cpu().numpy()) <= 4 * _kappa(want) * EPS32
+    Rb, st = hip.fold_finalize(R, r, X, 1 / math.sqrt(rows), lam, torch.bfloat16, 0, cqr=True)
+    assert st.item() == 1 and torch.equal(Rb, Rd.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("p,n,kappa", [(4096, 1024, 1e2), (6000, 2600, 1e1), (2048, 700, 1e2)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_fold_finalize_cqr_bf16_math(hip, p, n, kappa, xdt):
+    """bf16 arithmetic against the fp64 closed form of the same (stored) input.  The
+    block factorisation reads its columns as bf16, so an fp32 input carries the
+    rounding of the data, 2^-9 relative per entry: a Gram error up to about
+    2 * 2^-9 ~ 4e-3 (the panel path reads a block's own columns in fp32).  A bf16
+    input is exact, and the result must then be as close as the panel path's."""
+    rng = np.random.default_rng(p + n)
+    X = torch.from_numpy(O.kappa_matrix(p, n, kappa, rng).astype(np.float32) * math.sqrt(p))
+    X = X.to(xdt).to(DEV)
+    lam = 1e-2
+    want = O.chol_factor([X.double().cpu().numpy()], p, lam)
+    Rd, st = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), lam, torch.float32, 1, cqr=True)
+    assert st.item() == 1
+    e = _gram_rel(Rd, want)
+    Rp, _ = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), lam, torch.float32, 1)
+    ep = _gram_rel(Rp, want)
+    print(f"gram error cqr {e:.3e}, panels {ep:.3e}")
+    assert e <= 4 * _kappa(want) * EPS_BF16
+    if xdt == torch.float32:
+        assert e < 4e-3
+    else:
+        assert e < 1.25 * ep + 1e-5
+
+
+def test_fold_finalize_cqr_flags_ill_conditioned_blocks(hip):
+    """A rank-deficient block (no damping, a zero column) and a non-finite input
+    return status 2 (recompute with the panel path), which then gives the factor or
+    the non-finite flag; a well-posed call after them is unaffected."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    X = torch.randn(900, 600, device=DEV, generator=g)
+    X[:, 37] = 0.0
+    _, st = hip.fold_finalize(None, 0, X, 1 / 30.0, 0.0, torch.float32, 0, cqr=True)
+    assert st.item() == 2
+    X2 = torch.randn(900, 600, device=DEV, generator=g)
+    X2[:, 517] = 3.0 * X2[:, 12] - X2[:, 400]    # dependent columns across two blocks
+    R2, st = hip.fold_finalize(None, 0, X2, 1 / 30.0, 0.0, torch.float32, 0, cqr=True)
+    # the dependent column is rounding noise once the first block is applied:
+    # either flagged, or factored with a backward error at fp32 level
+    assert st.item() in (1, 2)
+    if st.item() == 1:
+        a = R2.double().cpu().numpy()
+        x = X2.double().cpu().numpy() / 30.0
+        assert np.linalg.norm(a.T @ a - x.T @ x) / np.linalg.norm(x.T @ x) < 1e-5
+    X3 = torch.randn(900, 600, device=DEV, generator=g)
+    X3[5, 5] = float("nan")
+    _, st = hip.fold_finalize(None, 0, X3, 1 / 30.0, 1e-2, torch.float32, 0, cqr=True)
+    assert st.item() == 2
+    _, fl = hip.fold_finalize(None, 0, X3, 1 / 30.0, 1e-2, torch.float32, 0)
+    assert fl.item() == 0
+    X3[5, 5] = 0.5
+    Rd, st = hip.fold_finalize(None, 0, X3, 1 / 30.0, 1e-2, torch.float32, 0, cqr=True)
+    want = O.chol_factor([X3.double().cpu().numpy()], 900, 1e-2)
+    assert st.item() == 1 and _gram_rel(Rd, want) <= 4 * _kappa(want) * EPS32
+
+
+def test_fold_finalize_cqr_is_deterministic(hip):
+    g = torch.Generator(device=DEV).manual_seed(11)
+    X = torch.randn(3000, 1300, device=DEV, generator=g)
+    for m in (0, 1):
+        a, _ = hip.fold_finalize(None, 0, X, 1 / math.sqrt(3000), 1e-2, torch.float32, m, cqr=True)
+        b, _ = hip.fold_finalize(None, 0, X, 1 / math.sqrt(3000), 1e-2, torch.float32, m, cqr=True)
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("n_in,n_out,p", [(4096, 11008, 16384)])
 def test_full_size_fold_finalize_bf16(hip, n_in, n_out, p):
     """The benchmarked factor update at full size in bf16 arithmetic: for random
     probes v, ||R_d v||^2 = ||X v||^2 / p + lam ||v||^2, and the natural gradient of
     the fused factors matches that of the two-call factors to the bf16 bound."""
     g = torch.Generator(device=DEV).manual_seed(7)
-    for n in (n_in, n_out):
+    for n, cqr in ((n_in, False), (n_out, False), (n_in, True), (n_out, True)):
         X = torch.randn(p, n, device=DEV, generator=g).to(torch.bfloat16)
-        Rd, flag = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), 1e-2, torch.float32, 1)
+        Rd, flag = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), 1e-2, torch.float32, 1, cqr=cqr)
         assert flag.item() == 1
         V = torch.randn(n, 16, device=DEV, generator=g, dtype=torch.float64)
         l2 = (Rd.double() @ V).norm(dim=0) ** 2
