@@ -55,11 +55,6 @@ int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
 // sets *flag.
 int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
                  float* dref, float tol, int* flag);
-// Householder reconstruction of a block CholeskyQR'd with P_top = c I (upper
-// parts; strict lower parts set to 0): A = c M1 + U2, and R = -P
-int launch_cqr_amat(hipStream_t s, const float* M1, const float* U2, int64_t ld, int n, float c,
-                    float* A, int64_t lda);
-int launch_cqr_rnew(hipStream_t s, const float* P, int64_t ldp, int n, float* R, int64_t ldr);
 // hi = RNE bf16(src), lo = RNE bf16(src - hi); transposed (hi[c][r]) with trans
 int launch_split_bf16(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
                       bf16_t* hi, bf16_t* lo, int64_t ldo, bool trans = false);
@@ -76,6 +71,37 @@ int launch_trinv_diag(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
 // block may be ragged
 int launch_trinv_diag128(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
                          int64_t ldz, int safe, int ut);
+// Small product with a fused epilogue (sqmm_kernel in small.hip):
+//   out = epi(alpha op(A) op(B) + beta1 C1 + beta2 C2 + gamma I)
+enum SqEpi { SQ_PLAIN = 0, SQ_UP = 1, SQ_TRIU = 2 };
+struct SqmmArgs {
+  int64_t M = 0, N = 0, K = 0;
+  const float* A = nullptr;
+  int64_t lda = 0;
+  int ta = 0, tria = TRI_NONE;
+  const float* B = nullptr;
+  int64_t ldb = 0;
+  int tb = 0, trib = TRI_NONE;
+  float alpha = 1.0f;
+  const float* C1 = nullptr;
+  int64_t ld1 = 0;
+  float beta1 = 0.0f;
+  const float* C2 = nullptr;
+  int64_t ld2 = 0;
+  float beta2 = 0.0f;
+  float gamma = 0.0f;
+  int epi = SQ_PLAIN;
+  float* out = nullptr;
+  int64_t ldo = 0;
+  bf16_t* outb = nullptr;
+  int64_t ldob = 0;
+  int outb_t = 0;
+  const float* prev = nullptr;
+  float tol = 0.0f;
+  int* flag = nullptr;
+  int vec_a = 0, vec_b = 0;   // set by launch_sqmm
+};
+int launch_sqmm(hipStream_t s, const SqmmArgs& a);
 // C_b = alpha A_b B_b, fp32 row-major, 64 x 64 tiles (small products)
 int launch_gemm64(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
                   int64_t lda, int64_t bsa, int tria, const float* B, int64_t ldb, int64_t bsb,

@@ -50,11 +50,12 @@ namespace ifk {
 static constexpr float HR_TOL = 1e-4f;
 static constexpr int64_t OUTER_B = 512;
 // Workgroup cap of the far-column products on the helper stream: the far
-// update is bound by HBM and runs beside the next block's panels, whose
-// kernels are bound by memory latency and bandwidth too; capped, it leaves
-// them CUs and bandwidth of their own.  128 measured best between 64 and 320
-// on the 4096 -> 11008, p = 16384 step.
-static constexpr int FAR_MAX_WGS = 128;
+// update is bound by HBM and runs beside the next block's factorisation,
+// whose small kernels are bound by memory latency; capped, it leaves them CUs
+// of their own.  192 measured best between 32 and uncapped on the
+// 4096 -> 11008, p = 16384 step with CholeskyQR outer blocks (32: 69.7 ms,
+// 128: 33.6, 192: 32.6, uncapped: 32.7 for the pair of factor updates).
+static constexpr int FAR_MAX_WGS = 192;
 
 static size_t split_floats(int64_t b, int64_t n) {
   size_t f = (size_t)64 * b * n;
@@ -144,25 +145,31 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
 }
 
 // Workspace of the block CholeskyQR path (cqr_block): 512 x 512 factors of
-// the outer block, the Cholesky's diagonal inverses, and the block's tall
+// the outer block, the Cholesky's diagonal inverses, the block's tall
 // operands in both layouts (pe x 512 row-major, and transposed 512 x pe with
-// row stride ldq), fp32 or bf16 by the arithmetic.
+// row stride ldq), fp32 or bf16 by the arithmetic, and -- by block parity,
+// since a block's far update runs while the next block is factored -- the
+// inverses M2 and N its outer update applies.
 struct CqrWs {
-  float* G;       // G1, then G2 (upper parts read)
+  float* G;       // G1, then G2
   float* U1;
   float* M1;      // U1^{-1}
   float* MT;      // M1^T (fp32 arithmetic), or its bf16 split hi | lo
-  float* U2;
-  float* Am;      // c M1 + U2, then U2 U1
-  float* N;       // (c M1 + U2)^{-1}
-  float* NT;      // N^T (fp32 or bf16)
+  float* E;       // G2 - I (upper part)
+  float* F[2];    // fixed-point iterates of U2 - I
+  float* S;       // F^2, then U2 M2a (Newton step)
+  float* M2a;     // first approximation of U2^{-1}
+  float* Am;      // c M1 + U2
   float* Zd;      // 8 x 64 x 64
   float* dref;
   float* Xc;      // X, pe x 512 (fp32 or bf16)
   float* Q2f;     // Q2 = X M1, pe x 512 fp32
-  bf16_t* Q2b;    // its bf16 copy (bf16 arithmetic)
-  float* Q2T;     // Q2^T, 512 x pe (ld ldq; fp32 or bf16)
+  float* Q2T;     // Q2^T, 512 x pe (ld ldq; fp32 arithmetic)
   int64_t ldq;
+  float* M2[2];   // U2^{-1} (fp32), and its transpose in bf16
+  bf16_t* M2Tb[2];
+  float* N[2];    // (c M1 + U2)^{-1} (fp32), and a row-major bf16 copy
+  bf16_t* Nb[2];
   int* flag;      // set when a block needs the Householder path
 };
 
@@ -173,17 +180,24 @@ static void plan_cqr(Arena& a, int64_t pe, CqrWs& q) {
   q.U1 = a.take<float>(B * B);
   q.M1 = a.take<float>(B * B);
   q.MT = a.take<float>(B * B);
-  q.U2 = a.take<float>(B * B);
+  q.E = a.take<float>(B * B);
+  q.F[0] = a.take<float>(B * B);
+  q.F[1] = a.take<float>(B * B);
+  q.S = a.take<float>(B * B);
+  q.M2a = a.take<float>(B * B);
   q.Am = a.take<float>(B * B);
-  q.N = a.take<float>(B * B);
-  q.NT = a.take<float>(B * B);
   q.Zd = a.take<float>((size_t)(B / 64) * 64 * 64);
   q.dref = a.take<float>(B);
   q.Xc = a.take<float>(pb);
   q.Q2f = a.take<float>(pb);
-  q.Q2b = a.take<bf16_t>(pb);
   q.ldq = (int64_t)align_up((size_t)(pe > 0 ? pe : 1), 8);
   q.Q2T = a.take<float>((size_t)B * q.ldq);
+  for (int i = 0; i < 2; ++i) {
+    q.M2[i] = a.take<float>(B * B);
+    q.M2Tb[i] = a.take<bf16_t>(B * B);
+    q.N[i] = a.take<float>(B * B);
+    q.Nb[i] = a.take<bf16_t>(B * B);
+  }
   q.flag = a.take<int>(64);
 }
 
@@ -304,36 +318,40 @@ static int outer_finish(hipStream_t s, int math, FoldWs& w, int k2, float* CT, b
               Crb ? out_both(Cr, ldc, Crb, ldc) : out_f32(Cr, ldc), 1, sp, max_wgs);
 }
 
-// Outer block [K0, K1) factored as a whole by CholeskyQR2 with Householder
-// reconstruction, in place of its chain of 64-column panels.  P = [c I; X]:
-// the block's rows of R are still the damping diagonal c I of the fused
-// fold + finalize (only a block's own factorisation writes them), and X =
-// C[:, K0:K1] (rows K0:K1 of CT, pe columns):
-//   G1 = X^T X + c^2 I = U1^T U1,   M1 = U1^{-1}
-//   Q = P M1 = [c M1; Q2],  Q2 = X M1            (nearly orthonormal)
-//   G2 = Q2^T Q2 + c^2 M1^T M1 = U2^T U2         (Q_f = Q U2^{-1} orthonormal)
-//   S = -I (Q's top block c M1 has a positive diagonal),
-//   N = (c M1 - S U2)^{-1} = (c M1 + U2)^{-1},  Y = Q2 N,  R_new = S U2 U1
-// Y is the Householder reconstruction Q_f,bot (Q_f,top - S)^{-1} (Q_f,top - S
-// = (c M1 + U2) U2^{-1}), so V = [I; Y] and R_new are the TPQRT factors of P
-// the panel chain produces; the block's T then follows from the UT
-// transform of Y in outer_prepare, as for the panel path.  The block's own
-// columns of C are not needed afterwards and are left as they are.
+// Outer block [K0, K1) factored as a whole by CholeskyQR2, in place of its
+// chain of 64-column panels.  P = [c I; X]: the block's rows of R are still
+// the damping diagonal c I of the fused fold + finalize (only a block's own
+// factorisation writes them) and its rows right of the block are still zero;
+// X = C[:, K0:K1] (rows K0:K1 of CT, pe columns):
+//   G1 = X^T X + c^2 I = U1^T U1,  M1 = U1^{-1},  Q2 = X M1
+//   G2 = Q2^T Q2 + c^2 M1^T M1 = I + E = U2^T U2,  U2 = I + F
+//   R_new = -U2 U1   (the sign the Householder form gives; R is
+//                     sign-normalised at the end of the fold)
+// G2 is close to the identity after the first pass, so U2 comes from the
+// fixed point F = up(E - F^T F) (up = strict upper part + diag / 2; three
+// sweeps from F = up(E)) instead of a second Cholesky, and M2 = U2^{-1} from
+// (I - F)(I + F^2) (plus one Newton step in fp32 arithmetic).  A first-pass
+// pivot below HR_TOL of its diagonal, or a last sweep that still moves F by
+// more than 1e-6, sets q.flag: the block was too ill-conditioned for
+// CholeskyQR and the factor must be recomputed by the panel path.
+// The block reflector of the TPQRT form, Q^T = I - V T^T V^T with V = [I; Y],
+// Y = X (c I - R_new)^{-1} and T = I - c R_new^{-1}, is never formed: applied
+// to the columns right of the block ([0; C_rest], R rows still zero) it is
+//   R_blk = -M2^T Q2^T C_rest,  C_rest -= Q2 N M2^T Q2^T C_rest,
+//   N = (c M1 + U2)^{-1}
+// (Y T = -X R_new^{-1} = Q2 M2 and Y = Q2 N), which outer_wp_q / outer_finish_q
+// compute with Q2 in place of Y and the small factors M2, N in place of T.
 // Every tall product reads K-contiguous operands: X and Q2 are kept in both
 // layouts (the transposes are plain copies).
 // bf16 arithmetic: X is read as bf16 (the shadow), Q2 = X (M1_hi + M1_lo)
-// (the bf16 split of M1 keeps Q consistent with its top block and with
-// R_new to about 2^-17) is rounded to bf16, and Y is written as the bf16
-// copies the outer update reads; U1, U2, N and R_new stay fp32.  A Cholesky
-// pivot of pass 1 below HR_TOL, or of pass 2 below 1/4, of its diagonal
-// sets q.flag: the block was too ill-conditioned for CholeskyQR and the
-// factor must be recomputed by the panel path.
+// (the bf16 split of M1 keeps Q2 consistent with R_new to about 2^-17) is
+// rounded to bf16 into the block's reflector store (row-major and
+// transposed), and M2, N get bf16 copies; the 512 x 512 algebra is fp32.
 static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
                      const float* C, const bf16_t* Cb, int64_t ldc, int64_t pe, float* R,
                      int64_t ldr, int64_t K0, int64_t K1, bool outer) {
   const int64_t B = OUTER_B, KB = K1 - K0, ldq = q.ldq;
   const bool bf = math == MATH_BF16;
-  const int tdt = bf ? DT_BF16 : DT_F32;   // dtype of the tall operands
   const float* Xf = C + K0 * ldc;
   const bf16_t* Xb = Cb ? Cb + K0 * ldc : nullptr;
   // pass 1: G1 = X^T X + c^2 I = U1^T U1, M1 = U1^{-1}
@@ -343,9 +361,9 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
   RC(launch_add_diag(s, q.G, B, KB, c * c));
   RC(launch_cholb(s, q.G, B, (int)KB, q.U1, B, q.Zd, q.dref, HR_TOL, q.flag));
   RC(trinv_core(s, q.U1, DT_F32, B, KB, q.M1, B, MATH_F32, 0, w.ttmp, w.tsp));
-  // X in its pe x KB layout, then Q2 = X M1 (pe x KB)
+  // X in its pe x KB layout, then Q2 = X M1 (pe x KB) into the reflector store
   if (Xb) RC(launch_transpose_bf16(s, Xb, ldc, KB, pe, (bf16_t*)q.Xc, B));
-  else RC(launch_transpose_cast(s, Xf, ldc, KB, pe, q.Xc, tdt, B));
+  else RC(launch_transpose_cast(s, Xf, ldc, KB, pe, q.Xc, DT_F32, B));
   if (bf) {
     bf16_t* MTh = (bf16_t*)q.MT;
     bf16_t* MTl = MTh + B * B;
@@ -353,39 +371,158 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
     RC(gemm(s, MATH_BF16, pe, KB, KB, 1.0f, A_n(q.Xc, DT_BF16, B),
             B_t(MTh, DT_BF16, B, TRI_UPPER), 0.0f, out_f32(q.Q2f, B), 1, w.split));
     RC(gemm(s, MATH_BF16, pe, KB, KB, 1.0f, A_n(q.Xc, DT_BF16, B),
-            B_t(MTl, DT_BF16, B, TRI_UPPER), 1.0f, out_both(q.Q2f, B, q.Q2b, B), 1, w.split));
-    RC(launch_transpose_bf16(s, q.Q2b, B, pe, KB, (bf16_t*)q.Q2T, ldq));
+            B_t(MTl, DT_BF16, B, TRI_UPPER), 1.0f, out_both(q.Q2f, B, w.Yob[k2], B), 1,
+            w.split));
+    RC(launch_transpose_bf16(s, w.Yob[k2], B, pe, KB, w.YobT[k2], ldc));
+    // pass 2: G2 = Q2^T Q2
+    RC(gemm(s, MATH_BF16, KB, KB, pe, 1.0f, A_n(w.YobT[k2], DT_BF16, ldc),
+            B_t(w.YobT[k2], DT_BF16, ldc), 0.0f, out_f32(q.G, B), 1, w.split));
   } else {
     RC(launch_transpose_cast(s, q.M1, B, KB, KB, q.MT, DT_F32, B));
     RC(gemm(s, MATH_F32, pe, KB, KB, 1.0f, A_n(q.Xc, DT_F32, B),
-            B_t(q.MT, DT_F32, B, TRI_UPPER), 0.0f, out_f32(q.Q2f, B), 1, w.split));
-    RC(launch_transpose_cast(s, q.Q2f, B, pe, KB, q.Q2T, DT_F32, ldq));
+            B_t(q.MT, DT_F32, B, TRI_UPPER), 0.0f, out_f32(w.Yo[k2], B), 1, w.split));
+    RC(launch_transpose_cast(s, w.Yo[k2], B, pe, KB, q.Q2T, DT_F32, ldq));
+    RC(gemm(s, MATH_F32, KB, KB, pe, 1.0f, A_n(q.Q2T, DT_F32, ldq), B_t(q.Q2T, DT_F32, ldq), 0.0f,
+            out_f32(q.G, B), 1, w.split));
   }
-  // pass 2: G2 = Q2^T Q2 + c^2 M1^T M1 = U2^T U2
-  RC(gemm(s, math, KB, KB, pe, 1.0f, A_n(q.Q2T, tdt, ldq), B_t(q.Q2T, tdt, ldq), 0.0f,
-          out_f32(q.G, B), 1, w.split));
-  if (c > 0.0f)
-    RC(gemm(s, MATH_F32, KB, KB, KB, c * c, A_t(q.M1, DT_F32, B, TRI_LOWER),
-            B_n(q.M1, DT_F32, B, TRI_UPPER), 1.0f, out_f32(q.G, B), 1, w.split));
-  RC(launch_cholb(s, q.G, B, (int)KB, q.U2, B, q.Zd, q.dref, 0.25f, q.flag));
-  // reconstruction: N = (c M1 + U2)^{-1}, Y = Q2 N (and its transpose)
-  if (outer) {
-    RC(launch_cqr_amat(s, q.M1, q.U2, B, (int)KB, c, q.Am, B));
-    RC(trinv_core(s, q.Am, DT_F32, B, KB, q.N, B, MATH_F32, 0, w.ttmp, w.tsp));
-    RC(launch_transpose_cast(s, q.N, B, KB, KB, q.NT, tdt, B));
-    if (bf) {
-      RC(gemm(s, MATH_BF16, pe, KB, KB, 1.0f, A_n(q.Q2b, DT_BF16, B),
-              B_t(q.NT, DT_BF16, B, TRI_UPPER), 0.0f, out_bf16(w.Yob[k2], B), 1, w.split));
-      RC(launch_transpose_bf16(s, w.Yob[k2], B, pe, KB, w.YobT[k2], ldc));
-    } else {
-      RC(gemm(s, MATH_F32, pe, KB, KB, 1.0f, A_n(q.Q2f, DT_F32, B),
-              B_t(q.NT, DT_F32, B, TRI_UPPER), 0.0f, out_f32(w.Yo[k2], B), 1, w.split));
-    }
+  SqmmArgs a;
+  a.M = a.N = a.K = KB;
+  a.ldo = B;
+  // E = G2 + c^2 M1^T M1 - I (upper part)
+  {
+    SqmmArgs e = a;
+    e.A = q.M1, e.lda = B, e.ta = 1, e.tria = TRI_LOWER;
+    e.B = q.M1, e.ldb = B, e.trib = TRI_UPPER;
+    e.alpha = c * c;
+    e.C1 = q.G, e.ld1 = B, e.beta1 = 1.0f;
+    e.gamma = -1.0f;
+    e.epi = SQ_TRIU;
+    e.out = q.E;
+    RC(launch_sqmm(s, e));
   }
-  // R_new = S U2 U1 = -U2 U1
-  RC(gemm(s, MATH_F32, KB, KB, KB, 1.0f, A_n(q.U2, DT_F32, B, TRI_UPPER),
-          B_n(q.U1, DT_F32, B, TRI_UPPER), 0.0f, out_f32(q.Am, B), 1, w.split));
-  return launch_cqr_rnew(s, q.Am, B, (int)KB, R + K0 * ldr + K0, ldr);
+  // U2 = I + F: F = up(E), then three sweeps F <- up(E - F^T F)
+  {
+    SqmmArgs f = a;
+    f.alpha = 0.0f;
+    f.C1 = q.E, f.ld1 = B, f.beta1 = 1.0f;
+    f.epi = SQ_UP;
+    f.out = q.F[0];
+    RC(launch_sqmm(s, f));
+  }
+  int cur = 0;
+  for (int it = 0; it < 3; ++it, cur ^= 1) {
+    SqmmArgs f = a;
+    f.A = q.F[cur], f.lda = B, f.ta = 1, f.tria = TRI_LOWER;
+    f.B = q.F[cur], f.ldb = B, f.trib = TRI_UPPER;
+    f.alpha = -1.0f;
+    f.C1 = q.E, f.ld1 = B, f.beta1 = 1.0f;
+    f.epi = SQ_UP;
+    f.out = q.F[cur ^ 1];
+    if (it == 2) f.prev = q.F[cur], f.tol = 1e-6f, f.flag = q.flag;
+    RC(launch_sqmm(s, f));
+  }
+  const float* F = q.F[cur];
+  // R_new = -U2 U1 = -(U1 + F U1)
+  {
+    SqmmArgs r = a;
+    r.A = F, r.lda = B, r.tria = TRI_UPPER;
+    r.B = q.U1, r.ldb = B, r.trib = TRI_UPPER;
+    r.alpha = -1.0f;
+    r.C1 = q.U1, r.ld1 = B, r.beta1 = -1.0f;
+    r.epi = SQ_TRIU;
+    r.out = R + K0 * ldr + K0, r.ldo = ldr;
+    RC(launch_sqmm(s, r));
+  }
+  if (!outer) return IFK_OK;
+  // M2 = U2^{-1}: (I - F)(I + F^2) = I + F^2 - F - F F^2, then in fp32
+  // arithmetic one Newton step M2 = M2a (2 I - U2 M2a)
+  {
+    SqmmArgs m = a;
+    m.A = F, m.lda = B, m.tria = TRI_UPPER;
+    m.B = F, m.ldb = B, m.trib = TRI_UPPER;
+    m.epi = SQ_TRIU;
+    m.out = q.S;
+    RC(launch_sqmm(s, m));
+    m.B = q.S;
+    m.alpha = -1.0f;
+    m.C1 = q.S, m.ld1 = B, m.beta1 = 1.0f;
+    m.C2 = F, m.ld2 = B, m.beta2 = -1.0f;
+    m.gamma = 1.0f;
+    m.out = bf ? q.M2[k2] : q.M2a;
+    if (bf) m.outb = q.M2Tb[k2], m.ldob = B, m.outb_t = 1;
+    RC(launch_sqmm(s, m));
+  }
+  if (!bf) {
+    SqmmArgs m = a;
+    m.A = F, m.lda = B, m.tria = TRI_UPPER;
+    m.B = q.M2a, m.ldb = B, m.trib = TRI_UPPER;
+    m.C1 = q.M2a, m.ld1 = B, m.beta1 = 1.0f;
+    m.epi = SQ_TRIU;
+    m.out = q.S;   // U2 M2a
+    RC(launch_sqmm(s, m));
+    m.A = q.M2a;
+    m.B = q.S;
+    m.alpha = -1.0f;
+    m.beta1 = 2.0f;
+    m.out = q.M2[k2];
+    RC(launch_sqmm(s, m));
+  }
+  // N = (c M1 + U2)^{-1}
+  {
+    SqmmArgs m = a;
+    m.alpha = 0.0f;
+    m.C1 = q.M1, m.ld1 = B, m.beta1 = c;
+    m.C2 = F, m.ld2 = B, m.beta2 = 1.0f;
+    m.gamma = 1.0f;
+    m.epi = SQ_TRIU;
+    m.out = q.Am;
+    RC(launch_sqmm(s, m));
+  }
+  RC(trinv_core(s, q.Am, DT_F32, B, KB, q.N[k2], B, MATH_F32, 0, w.ttmp, w.tsp));
+  return bf ? launch_cast(s, q.N[k2], B, KB, KB, q.Nb[k2], DT_BF16, B) : IFK_OK;
+}
+
+// Outer update of a CholeskyQR'd block (see cqr_block) on the columns
+// [c_lo, c_hi) of C, i.e. the rows of CT, in two halves:
+//   outer_wp_q:     S^T = CT_cols Q2
+//   outer_finish_q: S2^T = S^T M2,  R_blk -= S2,  Z^T = S2^T N^T (into Wp),
+//                   CT_cols -= Z^T Q2^T
+static int outer_wp_q(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
+                      int64_t ldc, int64_t pe, int64_t KB, int64_t c_lo, int64_t c_hi, float* Wp,
+                      bf16_t* Wpb, SplitScratch sp, int max_wgs) {
+  const int64_t B = OUTER_B, nt = c_hi - c_lo;
+  if (nt <= 0) return IFK_OK;
+  const bool bf = math == MATH_BF16;
+  const MatRef CA = CTb ? A_n(CTb + c_lo * ldc, DT_BF16, ldc) : A_n(CT + c_lo * ldc, DT_F32, ldc);
+  const MatRef QB = bf ? B_t(w.YobT[k2], DT_BF16, ldc) : B_n(w.Yo[k2], DT_F32, B);
+  return gemm(s, math, nt, KB, pe, 1.0f, CA, QB, 0.0f,
+              bf ? out_both(Wp, KB, Wpb, KB) : out_f32(Wp, KB), 1, sp, max_wgs);
+}
+
+static int outer_finish_q(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float* CT,
+                          bf16_t* CTb, int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0,
+                          int64_t K1, int64_t c_lo, int64_t c_hi, float* Wp, bf16_t* Wpb,
+                          float* W, bf16_t* Wb, SplitScratch sp, int max_wgs) {
+  const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
+  if (nt <= 0) return IFK_OK;
+  const bool bf = math == MATH_BF16;
+  float* Cr = CT + c_lo * ldc;
+  bf16_t* Crb = CTb ? CTb + c_lo * ldc : nullptr;
+  const MatRef SA = bf ? A_n(Wpb, DT_BF16, KB) : A_n(Wp, DT_F32, KB);
+  const MatRef MB = bf ? B_t(q.M2Tb[k2], DT_BF16, B, TRI_UPPER)
+                       : B_n(q.M2[k2], DT_F32, B, TRI_UPPER);
+  RC(gemm(s, math, nt, KB, KB, 1.0f, SA, MB, 0.0f, bf ? out_both(W, KB, Wb, KB) : out_f32(W, KB),
+          1, sp, max_wgs));
+  RC(launch_sub_transposed(s, R + K0 * ldr + c_lo, ldr, W, KB, KB, nt));
+  const MatRef WA = bf ? A_n(Wb, DT_BF16, KB) : A_n(W, DT_F32, KB);
+  const MatRef NB = bf ? B_t(q.Nb[k2], DT_BF16, B, TRI_LOWER)
+                       : B_t(q.N[k2], DT_F32, B, TRI_LOWER);
+  RC(gemm(s, math, nt, KB, KB, 1.0f, WA, NB, 0.0f, bf ? out_bf16(Wpb, KB) : out_f32(Wp, KB), 1, sp,
+          max_wgs));
+  const MatRef ZA = bf ? A_n(Wpb, DT_BF16, KB) : A_n(Wp, DT_F32, KB);
+  const MatRef QBt = bf ? B_t(w.Yob[k2], DT_BF16, B) : B_t(w.Yo[k2], DT_F32, B);
+  return gemm(s, math, nt, pe, KB, -1.0f, ZA, QBt, 1.0f,
+              Crb ? out_both(Cr, ldc, Crb, ldc) : out_f32(Cr, ldc), 1, sp, max_wgs);
 }
 
 // Core of the fold on the transposed fp32 working copy CT = C^T (n x p, row
@@ -407,10 +544,6 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
 //   far(k - 2) -> panels(k);  far(last) -> end of fold.
 // With x_tri, C is upper triangular and a panel ending at column c1
 // involves C rows [0, c1).
-static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
-                     const float* C, const bf16_t* Cb, int64_t ldc, int64_t pe, float* R,
-                     int64_t ldr, int64_t K0, int64_t K1, bool outer);
-
 // With cq, every outer block is factored by cqr_block; R's rows are then
 // expected to hold c I on entry (cq_c), as fold_finalize sets them.
 static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n, float* R,
@@ -479,6 +612,40 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     const bool far = la && near_hi < n;
     const int64_t mid = std::min<int64_t>(near_hi + B, n);
     const int64_t ntA = mid - near_hi;   // far part A: the block after next
+    if (cq) {
+      // no T to wait for: the helper forms the near S^T, then finishes far
+      // part A (the next block's near columns wait for it) and the rest,
+      // while s waits only for the near S^T
+      if (la) {
+        HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
+        HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
+        RC(outer_wp_q(la->s2, math, w, k2, C, Cb, ldc, pe_o, KB, K1, near_hi, w.Wpn, w.Wpnb,
+                      w.split2, 0));
+        HIPRC(hipEventRecord(la->nearwp[k2], la->s2), "tsqr_fold: event record failed");
+        if (far) {
+          const int64_t lo[2] = {near_hi, mid}, hi[2] = {mid, n};
+          for (int part = 0; part < 2; ++part) {
+            float* Wp = w.Wpf + (part ? ntA * KB : 0);
+            bf16_t* Wpb = w.Wpfb + (part ? ntA * KB : 0);
+            RC(outer_wp_q(la->s2, math, w, k2, C, Cb, ldc, pe_o, KB, lo[part], hi[part], Wp, Wpb,
+                          w.split2, FAR_MAX_WGS));
+            RC(outer_finish_q(la->s2, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1,
+                              lo[part], hi[part], Wp, Wpb, w.Wf, w.Wfb, w.split2, FAR_MAX_WGS));
+          }
+          HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
+          fall_pending[k2] = true;
+          HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
+        }
+        HIPRC(hipStreamWaitEvent(s, la->nearwp[k2], 0), "tsqr_fold: stream wait failed");
+        RC(outer_finish_q(s, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi,
+                          w.Wpn, w.Wpnb, w.Wn, w.Wnb, w.split, 0));
+      } else {
+        RC(outer_wp_q(s, math, w, k2, C, Cb, ldc, pe_o, KB, K1, n, w.Wpf, w.Wpfb, w.split, 0));
+        RC(outer_finish_q(s, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf,
+                          w.Wpfb, w.Wf, w.Wfb, w.split, 0));
+      }
+      continue;
+    }
     if (la) {
       // the T-independent half on the helper stream, from the moment the
       // block's reflectors are written, while s forms T: the near columns

@@ -787,29 +787,6 @@ __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, 
   }
 }
 
-// Householder reconstruction of a block CholeskyQR'd with P_top = c I (c >=
-// 0, so Q1 = c M1 has a positive diagonal and S = -I):
-//   cqr_amat:  A = Q1 - S U2 = c M1 + U2     (upper part; strict lower 0)
-//   cqr_rnew:  R = S P = -P, P = U2 U1       (upper part; strict lower 0)
-__global__ void cqr_amat_kernel(const float* M1, const float* U2, int64_t ld, int n, float c,
-                                float* A, int64_t lda) {
-  const int64_t total = (int64_t)n * n;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t i = e / n, j = e % n;
-    A[i * lda + j] = (i <= j) ? fmaf(c, M1[i * ld + j], U2[i * ld + j]) : 0.0f;
-  }
-}
-
-__global__ void cqr_rnew_kernel(const float* P, int64_t ldp, int n, float* R, int64_t ldr) {
-  const int64_t total = (int64_t)n * n;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t i = e / n, j = e % n;
-    R[i * ldr + j] = (i <= j) ? -P[i * ldp + j] : 0.0f;
-  }
-}
-
 // hi = RNE bf16(src), lo = RNE bf16(src - hi) (rows x cols, fp32 src), written
 // transposed (hi[c][r]) when trans is set
 __global__ void split_bf16_kernel(const float* src, int64_t lds, int64_t rows, int64_t cols,
@@ -1028,8 +1005,226 @@ __global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64
 }
 
 // ---------------------------------------------------------------------------
+// Small products with a fused epilogue (the 512 x 512 algebra of a CholeskyQR
+// outer block), on fp32 MFMA:
+//   v = alpha op(A) op(B) + beta1 C1 + beta2 C2 + gamma I
+//   out = epi(v): SQ_PLAIN v, SQ_UP strict upper part + diag / 2, SQ_TRIU upper
+//   part (strict lower zero in both)
+// op(A) = A^T when ta (A stored K x M), op(B) = B^T when tb (B stored N x K);
+// tria / trib describe op(A) / op(B) (their zero triangles are skipped by K
+// range and masked).  alpha = 0 skips the product.  outb receives an RNE
+// bf16 copy, transposed (outb[j][i]) when outb_t.  With prev (same layout as
+// out), any stored entry further than tol from prev's sets *flag = 1 (a
+// convergence test).  K <= SQ_KMAX.
+//
+// These products sit on the critical path of the fold while the far updates
+// keep HBM busy, so the kernel is built for latency: a workgroup owns a
+// 32 x 32 output tile (256 workgroups for 512 x 512), stages the whole K range
+// of both operands into LDS with every load issued before the first store
+// (one memory latency instead of one per K chunk), and its four waves split
+// K, reading k-contiguous fragments four at a time, before one cross-wave
+// reduction.  With SQ_UP / SQ_TRIU, tiles wholly below the diagonal only
+// store zeros and C1 / C2 are read on and above the diagonal only.
+// ---------------------------------------------------------------------------
+constexpr int SQ_T = 32;                 // output tile
+constexpr int SQ_KMAX = 512;
+constexpr int SQ_LD = SQ_KMAX + 4;       // k-contiguous LDS rows; 4 mod 32 keeps
+                                         // 8 rows' 16-byte reads on distinct banks
+constexpr int SQ_PER = SQ_T * SQ_KMAX / 4 / SNT;   // float4 loads per thread and operand
+
+// 32 x kext slice of op(X) (row index = tile row / column, k index) into a
+// k-contiguous LDS tile S[row][k - kbase], k < kbase + kext (kext a multiple
+// of 32, at most SQ_KMAX), zero outside [klo, khi), the matrix and its
+// triangle.  kt: X is stored with k along rows (op(X)[i][k] =
+// X[k * ld + i]); otherwise op(X)[i][k] = X[i * ld + k].  tri is in op(X)
+// terms with i the row index of op(A) or the column index of op(B): for A,
+// TRI_UPPER keeps k >= i; for B (passed as its transpose), TRI_UPPER keeps
+// k <= i.  vec: 16-byte loads are aligned.
+__device__ __forceinline__ void sq_stage(float* S, const float* X, int64_t ld, bool kt, int64_t i0,
+                                         int64_t ilim, int64_t kbase, int kext, int64_t klo,
+                                         int64_t khi, int keep_ge, int keep_le, bool vec) {
+  const int t = threadIdx.x;
+  const int nk4 = kext >> 2;   // float4 groups along k
+  float4 v[SQ_PER];
+  // each thread: SQ_PER groups of 4 consecutive elements along the stored
+  // contiguous index (k when !kt, i when kt)
+#pragma unroll
+  for (int q = 0; q < SQ_PER; ++q) {
+    const int e = t + SNT * q;
+    int ii, kk;   // tile-relative row, k of the group's first element
+    if (!kt) { ii = e / (SQ_KMAX / 4); kk = (e % (SQ_KMAX / 4)) * 4; }
+    else { kk = e / (SQ_T / 4); ii = (e % (SQ_T / 4)) * 4; }
+    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool live = !kt ? (kk >> 2) < nk4 : kk < nk4 * 4;
+    if (live) {
+      const int64_t gi = i0 + ii, gk = kbase + kk;
+      if (!kt) {
+        if (gi < ilim) {
+          const float* g = X + gi * ld + gk;
+          if (vec && gk + 3 < khi && gk >= klo) {
+            const float4 w = *(const float4*)g;
+            x[0] = w.x, x[1] = w.y, x[2] = w.z, x[3] = w.w;
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (gk + u >= klo && gk + u < khi) x[u] = g[u];
+          }
+        }
+      } else {
+        if (gk >= klo && gk < khi) {
+          const float* g = X + gk * ld + gi;
+          if (vec && gi + 3 < ilim) {
+            const float4 w = *(const float4*)g;
+            x[0] = w.x, x[1] = w.y, x[2] = w.z, x[3] = w.w;
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (gi + u < ilim) x[u] = g[u];
+          }
+        }
+      }
+      // triangle masks (element (gi', gk') with its own row / k)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t ri = i0 + ii + (kt ? u : 0), rk = kbase + kk + (kt ? 0 : u);
+        if ((keep_ge && rk < ri) || (keep_le && rk > ri)) x[u] = 0.0f;
+      }
+    }
+    v[q] = make_float4(x[0], x[1], x[2], x[3]);
+  }
+#pragma unroll
+  for (int q = 0; q < SQ_PER; ++q) {
+    const int e = t + SNT * q;
+    if (!kt) {
+      const int ii = e / (SQ_KMAX / 4), kk = (e % (SQ_KMAX / 4)) * 4;
+      if ((kk >> 2) < nk4) *(float4*)&S[ii * SQ_LD + kk] = v[q];
+    } else {
+      const int kk = e / (SQ_T / 4), ii = (e % (SQ_T / 4)) * 4;
+      if (kk < nk4 * 4) {
+        S[(ii + 0) * SQ_LD + kk] = v[q].x;
+        S[(ii + 1) * SQ_LD + kk] = v[q].y;
+        S[(ii + 2) * SQ_LD + kk] = v[q].z;
+        S[(ii + 3) * SQ_LD + kk] = v[q].w;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmArgs a) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  __shared__ __attribute__((aligned(16))) float sA[SQ_T * SQ_LD];
+  __shared__ __attribute__((aligned(16))) float sB[SQ_T * SQ_LD];
+  __shared__ float red[4];
+  const int64_t tiles_m = (a.M + SQ_T - 1) / SQ_T;
+  const int64_t m0 = (int64_t)(blockIdx.x % tiles_m) * SQ_T,
+                n0 = (int64_t)(blockIdx.x / tiles_m) * SQ_T;
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t col = n0 + l32;
+  if (a.epi != SQ_PLAIN && m0 > n0 + SQ_T - 1) {   // strictly below the diagonal
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t row = m0 + (i >> 2) * 8 + h * 4 + (i & 3);
+        if (row < a.M && col < a.N) {
+          a.out[row * a.ldo + col] = 0.0f;
+          if (a.outb) a.outb[a.outb_t ? col * a.ldob + row : row * a.ldob + col] = 0;
+        }
+      }
+    }
+    return;
+  }
+  int64_t klo = 0, khi = a.alpha != 0.0f ? a.K : 0;
+  if (a.tria == TRI_UPPER) klo = max(klo, m0);
+  if (a.tria == TRI_LOWER) khi = min(khi, m0 + SQ_T);
+  if (a.trib == TRI_UPPER) khi = min(khi, n0 + SQ_T);
+  if (a.trib == TRI_LOWER) klo = max(klo, n0);
+  f32x16 d;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) d[i] = 0.0f;
+  if (klo < khi) {
+    const int64_t kbase = klo & ~(int64_t)3;
+    // wave w takes k in [kbase + w kq, kbase + (w + 1) kq); lane half h the
+    // halves of that range, four steps per 16-byte read
+    const int kr = (int)(khi - kbase);
+    const int kq = ((kr + 31) / 32) * 8;
+    sq_stage(sA, a.A, a.lda, a.ta != 0, m0, a.M, kbase, 4 * kq, klo, khi, a.tria == TRI_UPPER,
+             a.tria == TRI_LOWER, a.vec_a != 0);
+    // op(B) staged as its transpose: row = column n of op(B)
+    sq_stage(sB, a.B, a.ldb, a.tb == 0, n0, a.N, kbase, 4 * kq, klo, khi, a.trib == TRI_LOWER,
+             a.trib == TRI_UPPER, a.vec_b != 0);
+    __syncthreads();
+    const int half = kq / 2;
+    const int kw = wave * kq + h * half;
+    for (int st = 0; st < half; st += 4) {
+      const float4 av = *(const float4*)&sA[l32 * SQ_LD + kw + st];
+      const float4 bv = *(const float4*)&sB[l32 * SQ_LD + kw + st];
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, d, 0, 0, 0);
+    }
+    // cross-wave sum into wave 0 (sA is free once every wave is past its reads)
+    __syncthreads();
+    if (wave > 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sA[((wave - 1) * 16 + i) * 64 + lane] = d[i];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        d[i] += sA[i * 64 + lane] + sA[(16 + i) * 64 + lane] + sA[(32 + i) * 64 + lane];
+    }
+  }
+  if (wave != 0) return;
+  float dm = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = m0 + (i >> 2) * 8 + h * 4 + (i & 3);
+    if (row >= a.M || col >= a.N) continue;
+    const bool keep = a.epi == SQ_PLAIN || row <= col;
+    float v = 0.0f;
+    if (keep) {
+      v = a.alpha * d[i];
+      if (a.C1) v += a.beta1 * a.C1[row * a.ld1 + col];
+      if (a.C2) v += a.beta2 * a.C2[row * a.ld2 + col];
+      if (row == col) v += a.gamma;
+      if (a.epi == SQ_UP && row == col) v *= 0.5f;
+    }
+    a.out[row * a.ldo + col] = v;
+    if (a.outb) a.outb[a.outb_t ? col * a.ldob + row : row * a.ldob + col] = f32_to_bf16(v);
+    if (a.prev) dm = fmaxf(dm, fabsf(v - a.prev[row * a.ldo + col]));
+  }
+  if (a.prev) {
+    for (int o = 32; o > 0; o >>= 1) dm = fmaxf(dm, __shfl_xor(dm, o));
+    if (lane == 0 && !(dm <= a.tol)) *a.flag = 1;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
+int launch_sqmm(hipStream_t s, const SqmmArgs& a0) {
+  if (a0.M < 0 || a0.N < 0 || a0.K < 0 || a0.K > SQ_KMAX || !a0.out || (a0.prev && !a0.flag)) {
+    set_error("sqmm: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  if (a0.M == 0 || a0.N == 0) return IFK_OK;
+  const int64_t tiles = cdiv(a0.M, (int64_t)SQ_T) * cdiv(a0.N, (int64_t)SQ_T);
+  if (tiles > 0x7fffffffLL) {
+    set_error("sqmm: grid too large");
+    return IFK_ERR_INVALID;
+  }
+  SqmmArgs a = a0;
+  // 16-byte operand loads need 16-byte aligned rows
+  a.vec_a = a.A && ((uintptr_t)a.A & 15) == 0 && a.lda % 4 == 0;
+  a.vec_b = a.B && ((uintptr_t)a.B & 15) == 0 && a.ldb % 4 == 0;
+  hipLaunchKernelGGL(sqmm_kernel, dim3((unsigned)tiles), dim3(SNT), 0, s, a);
+  return check_launch("sqmm");
+}
+
 static int check_b(int b, const char* what) {
   if (b > SB || b < 1) {
     set_error(std::string(what) + ": block size out of range");
@@ -1090,21 +1285,6 @@ static unsigned ew_grid(int64_t total) {
   if (g < 1) g = 1;
   if (g > 1024) g = 1024;
   return (unsigned)g;
-}
-
-int launch_cqr_amat(hipStream_t s, const float* M1, const float* U2, int64_t ld, int n, float c,
-                    float* A, int64_t lda) {
-  if (n <= 0) return IFK_OK;
-  hipLaunchKernelGGL(cqr_amat_kernel, dim3(ew_grid((int64_t)n * n)), dim3(256), 0, s, M1, U2, ld, n,
-                     c, A, lda);
-  return check_launch("cqr_amat");
-}
-
-int launch_cqr_rnew(hipStream_t s, const float* P, int64_t ldp, int n, float* R, int64_t ldr) {
-  if (n <= 0) return IFK_OK;
-  hipLaunchKernelGGL(cqr_rnew_kernel, dim3(ew_grid((int64_t)n * n)), dim3(256), 0, s, P, ldp, n, R,
-                     ldr);
-  return check_launch("cqr_rnew");
 }
 
 int launch_split_bf16(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
