@@ -47,14 +47,16 @@ int launch_sub_transposed(hipStream_t s, float* R, int64_t ldr, const float* WT,
 int launch_ut_tinv(hipStream_t s, const float* G, int64_t ldg, int64_t n, float* Tinv,
                    int64_t ldt);
 int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
-// Blocked upper Cholesky A = U^T U of an n x n fp32 matrix, n <= 512 (one
+// Blocked upper Cholesky A = U^T U of an n x n fp32 matrix, n <= 1024 (one
 // launch per 64-column step; A's blocks right of the diagonal are
 // overwritten by the trailing updates).  U (ld ldu) receives the blocks on
 // and above the diagonal, Zd (ceil(n / 64) x 4096 floats) the inverses of the
 // diagonal 64-blocks, dref (n floats) diag(A).  A pivot below tol * diag(A)_i
 // sets *flag.
+// With M (ld ldm), M = U^{-1} as well (its blocks on and above the diagonal),
+// formed column block by column block alongside the factorisation.
 int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
-                 float* dref, float tol, int* flag);
+                 float* dref, float tol, int* flag, float* M = nullptr, int64_t ldm = 0);
 // hi = RNE bf16(src), lo = RNE bf16(src - hi); transposed (hi[c][r]) with trans
 int launch_split_bf16(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
                       bf16_t* hi, bf16_t* lo, int64_t ldo, bool trans = false);
@@ -99,9 +101,15 @@ struct SqmmArgs {
   const float* prev = nullptr;
   float tol = 0.0f;
   int* flag = nullptr;
+  float* out2 = nullptr;      // also up(v) (ld ldo), with epi == SQ_TRIU
   int vec_a = 0, vec_b = 0;   // set by launch_sqmm
 };
-int launch_sqmm(hipStream_t s, const SqmmArgs& a);
+constexpr int SQ_BATCH = 3;
+struct SqmmBatch {
+  SqmmArgs a[SQ_BATCH];
+};
+// count independent products of one shape in one launch
+int launch_sqmm(hipStream_t s, const SqmmArgs* a, int count = 1);
 // C_b = alpha A_b B_b, fp32 row-major, 64 x 64 tiles (small products)
 int launch_gemm64(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
                   int64_t lda, int64_t bsa, int tria, const float* B, int64_t ldb, int64_t bsb,

@@ -49,12 +49,21 @@ namespace ifk {
 // of orthogonality is far below its own 1/4 pivot threshold.
 static constexpr float HR_TOL = 1e-4f;
 static constexpr int64_t OUTER_B = 512;
+// Outer block of the CholeskyQR path: a block's factorisation is a chain of
+// latency-bound small kernels whose length grows slower than its width, so
+// wider blocks cut the chain per column (and the far updates' read-modify-
+// write of C per column), up to the 1024 the block Cholesky supports.
+// Measured on the pair of factor updates of the 4096 -> 11008, p = 16384
+// step: 512: 28.0 ms, 768: 26.0, 1024: 23.7.
+static constexpr int64_t CQR_B = 1024;
 // Workgroup cap of the far-column products on the helper stream: the far
 // update is bound by HBM and runs beside the next block's factorisation,
 // whose small kernels are bound by memory latency; capped, it leaves them CUs
 // of their own.  192 measured best between 32 and uncapped on the
-// 4096 -> 11008, p = 16384 step with CholeskyQR outer blocks (32: 69.7 ms,
-// 128: 33.6, 192: 32.6, uncapped: 32.7 for the pair of factor updates).
+// 4096 -> 11008, p = 16384 step with 512-column CholeskyQR outer blocks (32:
+// 69.7 ms, 128: 33.6, 192: 32.6, uncapped: 32.7 for the pair of factor
+// updates) and again with 1024-column ones (64: 29.0, 96: 24.5, 128: 24.0,
+// 192: 24.0, 256: 25.0).
 static constexpr int FAR_MAX_WGS = 192;
 
 static size_t split_floats(int64_t b, int64_t n) {
@@ -73,6 +82,7 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
                       bool ut = false);
 
 struct FoldWs {
+  int64_t B;      // outer block width the buffers are sized for (OUTER_B or CQR_B)
   float* C;       // n x p: the chunk, transposed (CT = C^T; see fold_core)
   bf16_t* Cb;     // n x p: RNE bf16 shadow of C for bf16 arithmetic (the rows of
                   // columns beyond the current outer block are kept current)
@@ -106,8 +116,10 @@ struct FoldWs {
   SplitScratch split2;  // ... and of the helper stream
 };
 
-static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
-  const int64_t b = PANEL_B, B = OUTER_B;
+static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w,
+                      int64_t B = OUTER_B) {
+  const int64_t b = PANEL_B;
+  w.B = B;
   w.C = need_C ? a.take<float>((size_t)p * n) : nullptr;
   w.Cb = need_C ? a.take<bf16_t>((size_t)p * n) : nullptr;
   for (int i = 0; i < 2; ++i) {
@@ -151,6 +163,7 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w) {
 // since a block's far update runs while the next block is factored -- the
 // inverses M2 and N its outer update applies.
 struct CqrWs {
+  int64_t B;      // block width (CQR_B)
   float* G;       // G1, then G2
   float* U1;
   float* M1;      // U1^{-1}
@@ -174,7 +187,8 @@ struct CqrWs {
 };
 
 static void plan_cqr(Arena& a, int64_t pe, CqrWs& q) {
-  const int64_t B = OUTER_B;
+  const int64_t B = CQR_B;
+  q.B = B;
   const size_t pb = (size_t)(pe > 0 ? pe : 1) * B;
   q.G = a.take<float>(B * B);
   q.U1 = a.take<float>(B * B);
@@ -213,7 +227,8 @@ struct LookAhead {
   hipEvent_t nearwp[2] = {nullptr, nullptr};  // Wp of the next block's columns is formed
   hipEvent_t fall[2] = {nullptr, nullptr};    // all of the block's far update is done
   hipEvent_t done = nullptr;                // everything queued on s2 so far
-  hipEvent_t tready[2] = {nullptr, nullptr};  // T of the outer block is complete
+  hipEvent_t tready[2] = {nullptr, nullptr};  // T (or M2, N) of the outer block is complete
+  hipEvent_t aready[2] = {nullptr, nullptr};  // far part A of the outer block is applied
 };
 
 // One helper stream per (device, calling stream): folds issued on different
@@ -237,7 +252,8 @@ static LookAhead* look_ahead(hipStream_t s, int* rc) {
       ok = hipEventCreateWithFlags(&x->ready[i], hipEventDisableTiming) == hipSuccess &&
            hipEventCreateWithFlags(&x->nearwp[i], hipEventDisableTiming) == hipSuccess &&
            hipEventCreateWithFlags(&x->fall[i], hipEventDisableTiming) == hipSuccess &&
-           hipEventCreateWithFlags(&x->tready[i], hipEventDisableTiming) == hipSuccess;
+           hipEventCreateWithFlags(&x->tready[i], hipEventDisableTiming) == hipSuccess &&
+           hipEventCreateWithFlags(&x->aready[i], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
       set_error("tsqr_fold: cannot create the helper stream or its events");
       *rc = IFK_ERR_HIP;
@@ -347,10 +363,12 @@ static int outer_finish(hipStream_t s, int math, FoldWs& w, int k2, float* CT, b
 // (the bf16 split of M1 keeps Q2 consistent with R_new to about 2^-17) is
 // rounded to bf16 into the block's reflector store (row-major and
 // transposed), and M2, N get bf16 copies; the 512 x 512 algebra is fp32.
-static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
-                     const float* C, const bf16_t* Cb, int64_t ldc, int64_t pe, float* R,
-                     int64_t ldr, int64_t K0, int64_t K1, bool outer) {
-  const int64_t B = OUTER_B, KB = K1 - K0, ldq = q.ldq;
+// First pass, up to Q2 in the block's reflector store (all the outer update's
+// S^T = CT_cols Q2 products need).
+static int cqr_pass1(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
+                     const float* C, const bf16_t* Cb, int64_t ldc, int64_t pe, int64_t K0,
+                     int64_t K1) {
+  const int64_t B = q.B, KB = K1 - K0, ldq = q.ldq;
   const bool bf = math == MATH_BF16;
   const float* Xf = C + K0 * ldc;
   const bf16_t* Xb = Cb ? Cb + K0 * ldc : nullptr;
@@ -359,11 +377,10 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
   const MatRef XB = Xb ? B_t(Xb, DT_BF16, ldc) : B_t(Xf, DT_F32, ldc);
   RC(gemm(s, math, KB, KB, pe, 1.0f, XA, XB, 0.0f, out_f32(q.G, B), 1, w.split));
   RC(launch_add_diag(s, q.G, B, KB, c * c));
-  RC(launch_cholb(s, q.G, B, (int)KB, q.U1, B, q.Zd, q.dref, HR_TOL, q.flag));
-  RC(trinv_core(s, q.U1, DT_F32, B, KB, q.M1, B, MATH_F32, 0, w.ttmp, w.tsp));
+  RC(launch_cholb(s, q.G, B, (int)KB, q.U1, B, q.Zd, q.dref, HR_TOL, q.flag, q.M1, B));
   // X in its pe x KB layout, then Q2 = X M1 (pe x KB) into the reflector store
   if (Xb) RC(launch_transpose_bf16(s, Xb, ldc, KB, pe, (bf16_t*)q.Xc, B));
-  else RC(launch_transpose_cast(s, Xf, ldc, KB, pe, q.Xc, DT_F32, B));
+  else RC(launch_transpose_cast(s, Xf, ldc, KB, pe, q.Xc, bf ? DT_BF16 : DT_F32, B));
   if (bf) {
     bf16_t* MTh = (bf16_t*)q.MT;
     bf16_t* MTl = MTh + B * B;
@@ -373,22 +390,32 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
     RC(gemm(s, MATH_BF16, pe, KB, KB, 1.0f, A_n(q.Xc, DT_BF16, B),
             B_t(MTl, DT_BF16, B, TRI_UPPER), 1.0f, out_both(q.Q2f, B, w.Yob[k2], B), 1,
             w.split));
-    RC(launch_transpose_bf16(s, w.Yob[k2], B, pe, KB, w.YobT[k2], ldc));
-    // pass 2: G2 = Q2^T Q2
+    return launch_transpose_bf16(s, w.Yob[k2], B, pe, KB, w.YobT[k2], ldc);
+  }
+  RC(launch_transpose_cast(s, q.M1, B, KB, KB, q.MT, DT_F32, B));
+  RC(gemm(s, MATH_F32, pe, KB, KB, 1.0f, A_n(q.Xc, DT_F32, B), B_t(q.MT, DT_F32, B, TRI_UPPER),
+          0.0f, out_f32(w.Yo[k2], B), 1, w.split));
+  return launch_transpose_cast(s, w.Yo[k2], B, pe, KB, q.Q2T, DT_F32, ldq);
+}
+
+// Second pass from the Q2 of cqr_pass1: R_new into R, and for an outer block
+// the small factors M2 and N of its outer update.
+static int cqr_pass2(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
+                     int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0, int64_t K1,
+                     bool outer) {
+  const int64_t B = q.B, KB = K1 - K0, ldq = q.ldq;
+  const bool bf = math == MATH_BF16;
+  // G2 = Q2^T Q2
+  if (bf)
     RC(gemm(s, MATH_BF16, KB, KB, pe, 1.0f, A_n(w.YobT[k2], DT_BF16, ldc),
             B_t(w.YobT[k2], DT_BF16, ldc), 0.0f, out_f32(q.G, B), 1, w.split));
-  } else {
-    RC(launch_transpose_cast(s, q.M1, B, KB, KB, q.MT, DT_F32, B));
-    RC(gemm(s, MATH_F32, pe, KB, KB, 1.0f, A_n(q.Xc, DT_F32, B),
-            B_t(q.MT, DT_F32, B, TRI_UPPER), 0.0f, out_f32(w.Yo[k2], B), 1, w.split));
-    RC(launch_transpose_cast(s, w.Yo[k2], B, pe, KB, q.Q2T, DT_F32, ldq));
+  else
     RC(gemm(s, MATH_F32, KB, KB, pe, 1.0f, A_n(q.Q2T, DT_F32, ldq), B_t(q.Q2T, DT_F32, ldq), 0.0f,
             out_f32(q.G, B), 1, w.split));
-  }
   SqmmArgs a;
   a.M = a.N = a.K = KB;
   a.ldo = B;
-  // E = G2 + c^2 M1^T M1 - I (upper part)
+  // E = G2 + c^2 M1^T M1 - I (upper part), and F = up(E)
   {
     SqmmArgs e = a;
     e.A = q.M1, e.lda = B, e.ta = 1, e.tria = TRI_LOWER;
@@ -398,19 +425,16 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
     e.gamma = -1.0f;
     e.epi = SQ_TRIU;
     e.out = q.E;
-    RC(launch_sqmm(s, e));
+    e.out2 = q.F[0];
+    RC(launch_sqmm(s, &e));
   }
-  // U2 = I + F: F = up(E), then three sweeps F <- up(E - F^T F)
-  {
-    SqmmArgs f = a;
-    f.alpha = 0.0f;
-    f.C1 = q.E, f.ld1 = B, f.beta1 = 1.0f;
-    f.epi = SQ_UP;
-    f.out = q.F[0];
-    RC(launch_sqmm(s, f));
-  }
+  // U2 = I + F: sweeps F <- up(E - F^T F), the last one tested.  Each sweep
+  // cuts the error by about 2 ||F||; bf16 arithmetic needs F to about 1e-6
+  // (two sweeps, the last moving no entry by more than 1e-4), fp32 arithmetic
+  // to fp32 rounding (three, 1e-6).
+  const int sweeps = bf ? 2 : 3;
   int cur = 0;
-  for (int it = 0; it < 3; ++it, cur ^= 1) {
+  for (int it = 0; it < sweeps; ++it, cur ^= 1) {
     SqmmArgs f = a;
     f.A = q.F[cur], f.lda = B, f.ta = 1, f.tria = TRI_LOWER;
     f.B = q.F[cur], f.ldb = B, f.trib = TRI_UPPER;
@@ -418,39 +442,48 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
     f.C1 = q.E, f.ld1 = B, f.beta1 = 1.0f;
     f.epi = SQ_UP;
     f.out = q.F[cur ^ 1];
-    if (it == 2) f.prev = q.F[cur], f.tol = 1e-6f, f.flag = q.flag;
-    RC(launch_sqmm(s, f));
+    if (it == sweeps - 1) f.prev = q.F[cur], f.tol = bf ? 1e-4f : 1e-6f, f.flag = q.flag;
+    RC(launch_sqmm(s, &f));
   }
   const float* F = q.F[cur];
-  // R_new = -U2 U1 = -(U1 + F U1)
-  {
-    SqmmArgs r = a;
-    r.A = F, r.lda = B, r.tria = TRI_UPPER;
-    r.B = q.U1, r.ldb = B, r.trib = TRI_UPPER;
-    r.alpha = -1.0f;
-    r.C1 = q.U1, r.ld1 = B, r.beta1 = -1.0f;
-    r.epi = SQ_TRIU;
-    r.out = R + K0 * ldr + K0, r.ldo = ldr;
-    RC(launch_sqmm(s, r));
-  }
+  // in one launch: R_new = -U2 U1 = -(U1 + F U1), F^2 (for M2), and
+  // c M1 + U2 (whose inverse is N)
+  SqmmArgs t[3];
+  t[0] = a;
+  t[0].A = F, t[0].lda = B, t[0].tria = TRI_UPPER;
+  t[0].B = q.U1, t[0].ldb = B, t[0].trib = TRI_UPPER;
+  t[0].alpha = -1.0f;
+  t[0].C1 = q.U1, t[0].ld1 = B, t[0].beta1 = -1.0f;
+  t[0].epi = SQ_TRIU;
+  t[0].out = R + K0 * ldr + K0, t[0].ldo = ldr;
+  t[1] = a;
+  t[1].A = F, t[1].lda = B, t[1].tria = TRI_UPPER;
+  t[1].B = F, t[1].ldb = B, t[1].trib = TRI_UPPER;
+  t[1].epi = SQ_TRIU;
+  t[1].out = q.S;
+  t[2] = a;
+  t[2].alpha = 0.0f;
+  t[2].C1 = q.M1, t[2].ld1 = B, t[2].beta1 = c;
+  t[2].C2 = F, t[2].ld2 = B, t[2].beta2 = 1.0f;
+  t[2].gamma = 1.0f;
+  t[2].epi = SQ_TRIU;
+  t[2].out = q.Am;
+  RC(launch_sqmm(s, t, outer ? 3 : 1));
   if (!outer) return IFK_OK;
   // M2 = U2^{-1}: (I - F)(I + F^2) = I + F^2 - F - F F^2, then in fp32
   // arithmetic one Newton step M2 = M2a (2 I - U2 M2a)
   {
     SqmmArgs m = a;
     m.A = F, m.lda = B, m.tria = TRI_UPPER;
-    m.B = F, m.ldb = B, m.trib = TRI_UPPER;
-    m.epi = SQ_TRIU;
-    m.out = q.S;
-    RC(launch_sqmm(s, m));
-    m.B = q.S;
+    m.B = q.S, m.ldb = B, m.trib = TRI_UPPER;
     m.alpha = -1.0f;
     m.C1 = q.S, m.ld1 = B, m.beta1 = 1.0f;
     m.C2 = F, m.ld2 = B, m.beta2 = -1.0f;
     m.gamma = 1.0f;
+    m.epi = SQ_TRIU;
     m.out = bf ? q.M2[k2] : q.M2a;
     if (bf) m.outb = q.M2Tb[k2], m.ldob = B, m.outb_t = 1;
-    RC(launch_sqmm(s, m));
+    RC(launch_sqmm(s, &m));
   }
   if (!bf) {
     SqmmArgs m = a;
@@ -459,30 +492,20 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
     m.C1 = q.M2a, m.ld1 = B, m.beta1 = 1.0f;
     m.epi = SQ_TRIU;
     m.out = q.S;   // U2 M2a
-    RC(launch_sqmm(s, m));
+    RC(launch_sqmm(s, &m));
     m.A = q.M2a;
     m.B = q.S;
     m.alpha = -1.0f;
     m.beta1 = 2.0f;
     m.out = q.M2[k2];
-    RC(launch_sqmm(s, m));
+    RC(launch_sqmm(s, &m));
   }
   // N = (c M1 + U2)^{-1}
-  {
-    SqmmArgs m = a;
-    m.alpha = 0.0f;
-    m.C1 = q.M1, m.ld1 = B, m.beta1 = c;
-    m.C2 = F, m.ld2 = B, m.beta2 = 1.0f;
-    m.gamma = 1.0f;
-    m.epi = SQ_TRIU;
-    m.out = q.Am;
-    RC(launch_sqmm(s, m));
-  }
   RC(trinv_core(s, q.Am, DT_F32, B, KB, q.N[k2], B, MATH_F32, 0, w.ttmp, w.tsp));
   return bf ? launch_cast(s, q.N[k2], B, KB, KB, q.Nb[k2], DT_BF16, B) : IFK_OK;
 }
 
-// Outer update of a CholeskyQR'd block (see cqr_block) on the columns
+// Outer update of a CholeskyQR'd block (see cqr_pass1/2) on the columns
 // [c_lo, c_hi) of C, i.e. the rows of CT, in two halves:
 //   outer_wp_q:     S^T = CT_cols Q2
 //   outer_finish_q: S2^T = S^T M2,  R_blk -= S2,  Z^T = S2^T N^T (into Wp),
@@ -490,7 +513,7 @@ static int cqr_block(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
 static int outer_wp_q(hipStream_t s, int math, FoldWs& w, int k2, float* CT, bf16_t* CTb,
                       int64_t ldc, int64_t pe, int64_t KB, int64_t c_lo, int64_t c_hi, float* Wp,
                       bf16_t* Wpb, SplitScratch sp, int max_wgs) {
-  const int64_t B = OUTER_B, nt = c_hi - c_lo;
+  const int64_t B = w.B, nt = c_hi - c_lo;
   if (nt <= 0) return IFK_OK;
   const bool bf = math == MATH_BF16;
   const MatRef CA = CTb ? A_n(CTb + c_lo * ldc, DT_BF16, ldc) : A_n(CT + c_lo * ldc, DT_F32, ldc);
@@ -503,7 +526,7 @@ static int outer_finish_q(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, 
                           bf16_t* CTb, int64_t ldc, int64_t pe, float* R, int64_t ldr, int64_t K0,
                           int64_t K1, int64_t c_lo, int64_t c_hi, float* Wp, bf16_t* Wpb,
                           float* W, bf16_t* Wb, SplitScratch sp, int max_wgs) {
-  const int64_t B = OUTER_B, KB = K1 - K0, nt = c_hi - c_lo;
+  const int64_t B = w.B, KB = K1 - K0, nt = c_hi - c_lo;
   if (nt <= 0) return IFK_OK;
   const bool bf = math == MATH_BF16;
   float* Cr = CT + c_lo * ldc;
@@ -544,12 +567,12 @@ static int outer_finish_q(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, 
 //   far(k - 2) -> panels(k);  far(last) -> end of fold.
 // With x_tri, C is upper triangular and a panel ending at column c1
 // involves C rows [0, c1).
-// With cq, every outer block is factored by cqr_block; R's rows are then
+// With cq, every outer block is factored by cqr_pass1/2; R's rows are then
 // expected to hold c I on entry (cq_c), as fold_finalize sets them.
 static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n, float* R,
                      int64_t ldr, int64_t r_new, bool x_tri, int math, FoldWs& w,
                      CqrWs* cq = nullptr, float cq_c = 0.0f) {
-  const int64_t B = OUTER_B;
+  const int64_t B = w.B;
   int rc = IFK_OK;
   LookAhead* la = nullptr;
   if (std::min<int64_t>(B, r_new) + B < n) {  // some block has columns beyond the next one
@@ -562,9 +585,10 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
   // bf16 arithmetic: the outer-block products read a bf16 shadow of C (the
   // exact values their operand staging would round to), which the C updates
   // keep current; it is seeded here once
-  bf16_t* Cb = (bf && w.Cb && std::min<int64_t>(OUTER_B, r_new) < n) ? w.Cb : nullptr;
+  bf16_t* Cb = (bf && w.Cb && std::min<int64_t>(B, r_new) < n) ? w.Cb : nullptr;
   if (Cb) RC(launch_cast(s, C, ldc, n, p, Cb, DT_BF16, ldc));
   bool fall_pending[2] = {false, false};   // a far update still reads parity buffers
+  int a_prev = -1;   // parity of the previous block's far part A event, if recorded
   int k = 0;
   for (int64_t K0 = 0; K0 < r_new; K0 += B, ++k) {
     const int k2 = k & 1;
@@ -582,7 +606,10 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
       if (bf) RC(launch_zero_bf16(s, w.Yob[k2], B, pe_o, KB));
       if (bf && outer) RC(launch_zero_bf16(s, w.YobT[k2], ldc, KB, pe_o));
     }
-    if (cq) RC(cqr_block(s, math, w, *cq, k2, cq_c, C, Cb, ldc, pe_o, R, ldr, K0, K1, outer));
+    if (cq) {
+      RC(cqr_pass1(s, math, w, *cq, k2, cq_c, C, Cb, ldc, pe_o, K0, K1));
+      if (!outer) RC(cqr_pass2(s, math, w, *cq, k2, cq_c, ldc, pe_o, R, ldr, K0, K1, false));
+    }
     for (int64_t c0 = K0; c0 < K1 && !cq; c0 += PANEL_B) {
       const int bk = (int)std::min<int64_t>(PANEL_B, K1 - c0);
       const int64_t c1 = c0 + bk;
@@ -613,33 +640,44 @@ static int fold_core(hipStream_t s, float* C, int64_t ldc, int64_t p, int64_t n,
     const int64_t mid = std::min<int64_t>(near_hi + B, n);
     const int64_t ntA = mid - near_hi;   // far part A: the block after next
     if (cq) {
-      // no T to wait for: the helper forms the near S^T, then finishes far
-      // part A (the next block's near columns wait for it) and the rest,
-      // while s waits only for the near S^T
+      // the helper forms S^T = CT_cols Q2 for far part A and the rest while s
+      // runs the second pass; once M2 and N are there it finishes part A (the
+      // next block's near columns), then the rest.  s applies the block to
+      // its near columns itself, after the previous block's part A only (not
+      // behind that block's whole far update on the helper).
       if (la) {
-        HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
-        HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
-        RC(outer_wp_q(la->s2, math, w, k2, C, Cb, ldc, pe_o, KB, K1, near_hi, w.Wpn, w.Wpnb,
-                      w.split2, 0));
-        HIPRC(hipEventRecord(la->nearwp[k2], la->s2), "tsqr_fold: event record failed");
+        const int64_t lo[2] = {near_hi, mid}, hi[2] = {mid, n};
+        float* Wp[2] = {w.Wpf, w.Wpf + ntA * KB};
+        bf16_t* Wpb[2] = {w.Wpfb, w.Wpfb + ntA * KB};
         if (far) {
-          const int64_t lo[2] = {near_hi, mid}, hi[2] = {mid, n};
-          for (int part = 0; part < 2; ++part) {
-            float* Wp = w.Wpf + (part ? ntA * KB : 0);
-            bf16_t* Wpb = w.Wpfb + (part ? ntA * KB : 0);
-            RC(outer_wp_q(la->s2, math, w, k2, C, Cb, ldc, pe_o, KB, lo[part], hi[part], Wp, Wpb,
-                          w.split2, FAR_MAX_WGS));
-            RC(outer_finish_q(la->s2, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1,
-                              lo[part], hi[part], Wp, Wpb, w.Wf, w.Wfb, w.split2, FAR_MAX_WGS));
-          }
+          HIPRC(hipEventRecord(la->ready[k2], s), "tsqr_fold: event record failed");
+          HIPRC(hipStreamWaitEvent(la->s2, la->ready[k2], 0), "tsqr_fold: stream wait failed");
+          for (int part = 0; part < 2; ++part)
+            RC(outer_wp_q(la->s2, math, w, k2, C, Cb, ldc, pe_o, KB, lo[part], hi[part],
+                          Wp[part], Wpb[part], w.split2, FAR_MAX_WGS));
+        }
+        RC(cqr_pass2(s, math, w, *cq, k2, cq_c, ldc, pe_o, R, ldr, K0, K1, true));
+        if (far) {
+          HIPRC(hipEventRecord(la->tready[k2], s), "tsqr_fold: event record failed");
+          HIPRC(hipStreamWaitEvent(la->s2, la->tready[k2], 0), "tsqr_fold: stream wait failed");
+          RC(outer_finish_q(la->s2, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, lo[0],
+                            hi[0], Wp[0], Wpb[0], w.Wf, w.Wfb, w.split2, FAR_MAX_WGS));
+          HIPRC(hipEventRecord(la->aready[k2], la->s2), "tsqr_fold: event record failed");
+          RC(outer_finish_q(la->s2, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, lo[1],
+                            hi[1], Wp[1], Wpb[1], w.Wf, w.Wfb, w.split2, FAR_MAX_WGS));
           HIPRC(hipEventRecord(la->fall[k2], la->s2), "tsqr_fold: event record failed");
           fall_pending[k2] = true;
           HIPRC(hipEventRecord(la->done, la->s2), "tsqr_fold: event record failed");
         }
-        HIPRC(hipStreamWaitEvent(s, la->nearwp[k2], 0), "tsqr_fold: stream wait failed");
+        if (a_prev >= 0)
+          HIPRC(hipStreamWaitEvent(s, la->aready[a_prev], 0), "tsqr_fold: stream wait failed");
+        a_prev = far ? k2 : -1;
+        RC(outer_wp_q(s, math, w, k2, C, Cb, ldc, pe_o, KB, K1, near_hi, w.Wpn, w.Wpnb, w.split,
+                      0));
         RC(outer_finish_q(s, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, near_hi,
                           w.Wpn, w.Wpnb, w.Wn, w.Wnb, w.split, 0));
       } else {
+        RC(cqr_pass2(s, math, w, *cq, k2, cq_c, ldc, pe_o, R, ldr, K0, K1, true));
         RC(outer_wp_q(s, math, w, k2, C, Cb, ldc, pe_o, KB, K1, n, w.Wpf, w.Wpfb, w.split, 0));
         RC(outer_finish_q(s, math, w, *cq, k2, C, Cb, ldc, pe_o, R, ldr, K0, K1, K1, n, w.Wpf,
                           w.Wpfb, w.Wf, w.Wfb, w.split, 0));
@@ -828,7 +866,8 @@ int fold_finalize(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, i
 // meaningless and the caller recomputes it with fold_finalize).
 static void plan_fold_finalize_cqr(Arena& a, int64_t pe, int64_t n, float** Rw, FoldWs& w,
                                    CqrWs& q) {
-  plan_fold_finalize(a, pe, n, Rw, w);
+  *Rw = a.take<float>((size_t)n * n);
+  plan_fold(a, pe, n, true, w, CQR_B);
   plan_cqr(a, pe, q);
 }
 

@@ -693,7 +693,7 @@ __global__ __launch_bounds__(SNT) void chol_block_kernel(float* A, int64_t ld, i
 // dref[i] or not finite sets *flag (the factorisation goes on with clamped
 // pivots, so every launch still runs the same steps).
 // ---------------------------------------------------------------------------
-constexpr int CHOLB_MAX = 8 * SB;
+constexpr int CHOLB_MAX = 16 * SB;
 
 // rows x cols block (row stride ld) into registers as a padded 64 x 64 tile:
 // outside the block the tile is pad * I
@@ -716,7 +716,8 @@ __device__ __forceinline__ void st_blk(const float* S, float* g, int64_t ld, int
 
 __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_t lda, int n,
                                                           float* U, int64_t ldu, float* Zd,
-                                                          float* dref, float tol, int* flag) {
+                                                          float* dref, float tol, int* flag,
+                                                          float* Mo, int64_t ldm) {
   __shared__ float sC[SB * SLD];
   __shared__ float sZ[SB * SLD];
   __shared__ float sT[TRINV_TMP];
@@ -732,14 +733,18 @@ __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_
   sm_chol64(sC, tol, &bad, 0);   // block 0: its diagonal on entry is A's
   st_blk(sC, U, ldu, b0, b0);
   sm_trinv64(sC, sZ, sT);
-  for (int e = t; e < SB * SB; e += SNT) Zd[e] = sZ[(e >> 6) * SLD + (e & 63)];
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int r = e >> 6, c = e & 63;
+    Zd[e] = sZ[r * SLD + c];
+    if (Mo && r < b0 && c < b0) Mo[(int64_t)r * ldm + c] = sZ[r * SLD + c];
+  }
   if (t == 0 && bad) *flag = 1;
 }
 
 __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, int n, float* U,
                                                          int64_t ldu, float* Zd,
                                                          const float* dref, float tol, int* flag,
-                                                         int k) {
+                                                         int k, float* Mo, int64_t ldm) {
   __shared__ float sZ[SB * SLD];
   __shared__ float sA[SB * SLD];
   __shared__ float sB[SB * SLD];
@@ -748,6 +753,43 @@ __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, 
   __shared__ int bad;
   const int t = threadIdx.x;
   const int nb = (n + SB - 1) / SB;
+  const int nupd = (nb - 1 - k) * (nb - k) / 2;
+  if ((int)blockIdx.x >= nupd) {
+    // column block k of M = U^{-1}: M_kk = Z_k, and for i < k
+    //   M_ik = -(sum_{l = i}^{k-1} M_il U_lk) Z_k
+    // from blocks of U and M that earlier launches finished
+    const int i = (int)blockIdx.x - nupd;
+    const int bk = (n - SB * k) < SB ? (n - SB * k) : SB;
+    const float* Zk = Zd + (size_t)k * SB * SB;
+    if (i == k) {
+      for (int e = t; e < SB * SB; e += SNT) {
+        const int r = e >> 6, c = e & 63;
+        if (r < bk && c < bk) Mo[(int64_t)(SB * k + r) * ldm + SB * k + c] = Zk[e];
+      }
+      return;
+    }
+    float va[PAD_PER], vb[PAD_PER];
+    for (int e = t; e < SB * SB; e += SNT) sC[(e >> 6) * SLD + (e & 63)] = 0.0f;
+    ld_blk(va, Mo + (int64_t)SB * i * ldm + SB * i, ldm, SB, SB, 0.0f);
+    ld_blk(vb, U + (int64_t)SB * i * ldu + SB * k, ldu, SB, bk, 0.0f);
+    for (int l = i; l < k; ++l) {
+      st_pad(sA, va);
+      st_pad(sB, vb);
+      __syncthreads();
+      if (l + 1 < k) {   // the next pair's loads fly while this one multiplies
+        ld_blk(va, Mo + (int64_t)SB * i * ldm + SB * (l + 1), ldm, SB, SB, 0.0f);
+        ld_blk(vb, U + (int64_t)SB * (l + 1) * ldu + SB * k, ldu, SB, bk, 0.0f);
+      }
+      sm_gemm64<false, false>(sA, sB, sC, 1.0f, true);
+    }
+#pragma unroll
+    for (int q = 0; q < PAD_PER; ++q) va[q] = Zk[t + SNT * q];
+    st_pad(sZ, va);
+    __syncthreads();
+    sm_gemm64<false, false>(sC, sZ, sA, -1.0f, false);
+    st_blk(sA, Mo + (int64_t)SB * i * ldm + SB * k, ldm, SB, bk);
+    return;
+  }
   // workgroup -> (i, j), k < i <= j < nb, row by row
   int idx = blockIdx.x, i = k + 1;
   while (idx >= nb - i) {
@@ -1012,51 +1054,48 @@ __global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64
 //   part (strict lower zero in both)
 // op(A) = A^T when ta (A stored K x M), op(B) = B^T when tb (B stored N x K);
 // tria / trib describe op(A) / op(B) (their zero triangles are skipped by K
-// range and masked).  alpha = 0 skips the product.  outb receives an RNE
+// range and masked).  alpha = 0 skips the product.  out2 (SQ_TRIU only,
+// same ld as out) receives up(v) as well.  Up to SQ_BATCH products of one
+// shape run in one launch (blockIdx.y selects the product).  outb receives an RNE
 // bf16 copy, transposed (outb[j][i]) when outb_t.  With prev (same layout as
 // out), any stored entry further than tol from prev's sets *flag = 1 (a
-// convergence test).  K <= SQ_KMAX.
+// convergence test).
 //
 // These products sit on the critical path of the fold while the far updates
-// keep HBM busy, so the kernel is built for latency: a workgroup owns a
-// 32 x 32 output tile (256 workgroups for 512 x 512), stages the whole K range
-// of both operands into LDS with every load issued before the first store
-// (one memory latency instead of one per K chunk), and its four waves split
-// K, reading k-contiguous fragments four at a time, before one cross-wave
-// reduction.  With SQ_UP / SQ_TRIU, tiles wholly below the diagonal only
+// occupy most CUs, so the kernel is built for latency and a small footprint:
+// a workgroup owns a 32 x 32 output tile (256 workgroups for 512 x 512),
+// stages K in 128-wide chunks (34 KB of LDS, several workgroups per CU) with
+// the next chunk's loads in flight during the current one, and its four
+// waves split each chunk's K, reading k-contiguous fragments four at a time,
+// before one cross-wave reduction.  With SQ_UP / SQ_TRIU, tiles wholly below the diagonal only
 // store zeros and C1 / C2 are read on and above the diagonal only.
 // ---------------------------------------------------------------------------
 constexpr int SQ_T = 32;                 // output tile
-constexpr int SQ_KMAX = 512;
-constexpr int SQ_LD = SQ_KMAX + 4;       // k-contiguous LDS rows; 4 mod 32 keeps
+constexpr int SQ_KC = 128;               // K chunk staged at a time
+constexpr int SQ_LD = SQ_KC + 4;         // k-contiguous LDS rows; 4 mod 32 keeps
                                          // 8 rows' 16-byte reads on distinct banks
-constexpr int SQ_PER = SQ_T * SQ_KMAX / 4 / SNT;   // float4 loads per thread and operand
+constexpr int SQ_PER = SQ_T * SQ_KC / 4 / SNT;   // float4 loads per thread and operand
 
-// 32 x kext slice of op(X) (row index = tile row / column, k index) into a
-// k-contiguous LDS tile S[row][k - kbase], k < kbase + kext (kext a multiple
-// of 32, at most SQ_KMAX), zero outside [klo, khi), the matrix and its
-// triangle.  kt: X is stored with k along rows (op(X)[i][k] =
-// X[k * ld + i]); otherwise op(X)[i][k] = X[i * ld + k].  tri is in op(X)
-// terms with i the row index of op(A) or the column index of op(B): for A,
-// TRI_UPPER keeps k >= i; for B (passed as its transpose), TRI_UPPER keeps
-// k <= i.  vec: 16-byte loads are aligned.
-__device__ __forceinline__ void sq_stage(float* S, const float* X, int64_t ld, bool kt, int64_t i0,
-                                         int64_t ilim, int64_t kbase, int kext, int64_t klo,
-                                         int64_t khi, int keep_ge, int keep_le, bool vec) {
+// One K chunk of op(X) into registers: rows i0 + [0, 32) (row = tile row of
+// op(A), or column n of op(B) staged as its transpose), k in [kbase, kbase +
+// kext) (kext a multiple of 32, at most SQ_KC), zero outside [klo, khi), the
+// matrix and its triangle.  kt: X is stored with k along rows (op(X)[i][k] =
+// X[k * ld + i]); otherwise op(X)[i][k] = X[i * ld + k].  keep_ge / keep_le
+// keep k >= i / k <= i.  vec: 16-byte loads are aligned.  Each thread loads
+// SQ_PER groups of 4 consecutive elements along the stored contiguous index.
+__device__ __forceinline__ void sq_load(float4 (&v)[SQ_PER], const float* X, int64_t ld, bool kt,
+                                        int64_t i0, int64_t ilim, int64_t kbase, int kext,
+                                        int64_t klo, int64_t khi, int keep_ge, int keep_le,
+                                        bool vec) {
   const int t = threadIdx.x;
-  const int nk4 = kext >> 2;   // float4 groups along k
-  float4 v[SQ_PER];
-  // each thread: SQ_PER groups of 4 consecutive elements along the stored
-  // contiguous index (k when !kt, i when kt)
 #pragma unroll
   for (int q = 0; q < SQ_PER; ++q) {
     const int e = t + SNT * q;
     int ii, kk;   // tile-relative row, k of the group's first element
-    if (!kt) { ii = e / (SQ_KMAX / 4); kk = (e % (SQ_KMAX / 4)) * 4; }
+    if (!kt) { ii = e / (SQ_KC / 4); kk = (e % (SQ_KC / 4)) * 4; }
     else { kk = e / (SQ_T / 4); ii = (e % (SQ_T / 4)) * 4; }
     float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const bool live = !kt ? (kk >> 2) < nk4 : kk < nk4 * 4;
-    if (live) {
+    if (kk < kext) {
       const int64_t gi = i0 + ii, gk = kbase + kk;
       if (!kt) {
         if (gi < ilim) {
@@ -1083,7 +1122,6 @@ __device__ __forceinline__ void sq_stage(float* S, const float* X, int64_t ld, b
           }
         }
       }
-      // triangle masks (element (gi', gk') with its own row / k)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int64_t ri = i0 + ii + (kt ? u : 0), rk = kbase + kk + (kt ? 0 : u);
@@ -1092,15 +1130,20 @@ __device__ __forceinline__ void sq_stage(float* S, const float* X, int64_t ld, b
     }
     v[q] = make_float4(x[0], x[1], x[2], x[3]);
   }
+}
+
+// The registers of sq_load into the k-contiguous LDS tile S[row][k - kbase]
+__device__ __forceinline__ void sq_store(float* S, const float4 (&v)[SQ_PER], bool kt, int kext) {
+  const int t = threadIdx.x;
 #pragma unroll
   for (int q = 0; q < SQ_PER; ++q) {
     const int e = t + SNT * q;
     if (!kt) {
-      const int ii = e / (SQ_KMAX / 4), kk = (e % (SQ_KMAX / 4)) * 4;
-      if ((kk >> 2) < nk4) *(float4*)&S[ii * SQ_LD + kk] = v[q];
+      const int ii = e / (SQ_KC / 4), kk = (e % (SQ_KC / 4)) * 4;
+      if (kk < kext) *(float4*)&S[ii * SQ_LD + kk] = v[q];
     } else {
       const int kk = e / (SQ_T / 4), ii = (e % (SQ_T / 4)) * 4;
-      if (kk < nk4 * 4) {
+      if (kk < kext) {
         S[(ii + 0) * SQ_LD + kk] = v[q].x;
         S[(ii + 1) * SQ_LD + kk] = v[q].y;
         S[(ii + 2) * SQ_LD + kk] = v[q].z;
@@ -1110,8 +1153,9 @@ __device__ __forceinline__ void sq_stage(float* S, const float* X, int64_t ld, b
   }
 }
 
-__global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmArgs a) {
+__global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmBatch batch) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
+  const SqmmArgs& a = batch.a[blockIdx.y];
   __shared__ __attribute__((aligned(16))) float sA[SQ_T * SQ_LD];
   __shared__ __attribute__((aligned(16))) float sB[SQ_T * SQ_LD];
   __shared__ float red[4];
@@ -1129,6 +1173,7 @@ __global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmArgs a) {
         const int64_t row = m0 + (i >> 2) * 8 + h * 4 + (i & 3);
         if (row < a.M && col < a.N) {
           a.out[row * a.ldo + col] = 0.0f;
+          if (a.out2) a.out2[row * a.ldo + col] = 0.0f;
           if (a.outb) a.outb[a.outb_t ? col * a.ldob + row : row * a.ldob + col] = 0;
         }
       }
@@ -1144,26 +1189,43 @@ __global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmArgs a) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) d[i] = 0.0f;
   if (klo < khi) {
-    const int64_t kbase = klo & ~(int64_t)3;
-    // wave w takes k in [kbase + w kq, kbase + (w + 1) kq); lane half h the
-    // halves of that range, four steps per 16-byte read
-    const int kr = (int)(khi - kbase);
-    const int kq = ((kr + 31) / 32) * 8;
-    sq_stage(sA, a.A, a.lda, a.ta != 0, m0, a.M, kbase, 4 * kq, klo, khi, a.tria == TRI_UPPER,
-             a.tria == TRI_LOWER, a.vec_a != 0);
+    // K in chunks of SQ_KC; the next chunk's loads fly while this one
+    // multiplies.  Wave w takes k in [w kq, (w + 1) kq) of the chunk, lane
+    // half h the halves of that range, four steps per 16-byte read.
+    const int64_t k0 = klo & ~(int64_t)3;
+    float4 va[SQ_PER], vb[SQ_PER];
+    auto kext_of = [&](int64_t kb) {
+      const int kr = (int)min((int64_t)SQ_KC, khi - kb);
+      return ((kr + 31) / 32) * 32;
+    };
+    int kext = kext_of(k0);
+    sq_load(va, a.A, a.lda, a.ta != 0, m0, a.M, k0, kext, klo, khi, a.tria == TRI_UPPER,
+            a.tria == TRI_LOWER, a.vec_a != 0);
     // op(B) staged as its transpose: row = column n of op(B)
-    sq_stage(sB, a.B, a.ldb, a.tb == 0, n0, a.N, kbase, 4 * kq, klo, khi, a.trib == TRI_LOWER,
-             a.trib == TRI_UPPER, a.vec_b != 0);
-    __syncthreads();
-    const int half = kq / 2;
-    const int kw = wave * kq + h * half;
-    for (int st = 0; st < half; st += 4) {
-      const float4 av = *(const float4*)&sA[l32 * SQ_LD + kw + st];
-      const float4 bv = *(const float4*)&sB[l32 * SQ_LD + kw + st];
-      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, d, 0, 0, 0);
+    sq_load(vb, a.B, a.ldb, a.tb == 0, n0, a.N, k0, kext, klo, khi, a.trib == TRI_LOWER,
+            a.trib == TRI_UPPER, a.vec_b != 0);
+    for (int64_t kb = k0; kb < khi; kb += SQ_KC) {
+      if (kb != k0) __syncthreads();   // every wave is done with the last chunk
+      sq_store(sA, va, a.ta != 0, kext);
+      sq_store(sB, vb, a.tb == 0, kext);
+      __syncthreads();
+      const int kq = kext / 4, half = kq / 2;
+      if (kb + SQ_KC < khi) {
+        kext = kext_of(kb + SQ_KC);
+        sq_load(va, a.A, a.lda, a.ta != 0, m0, a.M, kb + SQ_KC, kext, klo, khi,
+                a.tria == TRI_UPPER, a.tria == TRI_LOWER, a.vec_a != 0);
+        sq_load(vb, a.B, a.ldb, a.tb == 0, n0, a.N, kb + SQ_KC, kext, klo, khi,
+                a.trib == TRI_LOWER, a.trib == TRI_UPPER, a.vec_b != 0);
+      }
+      const int kw = wave * kq + h * half;
+      for (int st = 0; st < half; st += 4) {
+        const float4 av = *(const float4*)&sA[l32 * SQ_LD + kw + st];
+        const float4 bv = *(const float4*)&sB[l32 * SQ_LD + kw + st];
+        d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, d, 0, 0, 0);
+      }
     }
     // cross-wave sum into wave 0 (sA is free once every wave is past its reads)
     __syncthreads();
@@ -1194,6 +1256,7 @@ __global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmArgs a) {
       if (a.epi == SQ_UP && row == col) v *= 0.5f;
     }
     a.out[row * a.ldo + col] = v;
+    if (a.out2) a.out2[row * a.ldo + col] = (row < col) ? v : (row == col ? 0.5f * v : 0.0f);
     if (a.outb) a.outb[a.outb_t ? col * a.ldob + row : row * a.ldob + col] = f32_to_bf16(v);
     if (a.prev) dm = fmaxf(dm, fabsf(v - a.prev[row * a.ldo + col]));
   }
@@ -1206,22 +1269,31 @@ __global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmArgs a) {
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-int launch_sqmm(hipStream_t s, const SqmmArgs& a0) {
-  if (a0.M < 0 || a0.N < 0 || a0.K < 0 || a0.K > SQ_KMAX || !a0.out || (a0.prev && !a0.flag)) {
-    set_error("sqmm: invalid arguments");
+int launch_sqmm(hipStream_t s, const SqmmArgs* args, int count) {
+  if (count < 1 || count > SQ_BATCH) {
+    set_error("sqmm: batch size out of range");
     return IFK_ERR_INVALID;
   }
-  if (a0.M == 0 || a0.N == 0) return IFK_OK;
-  const int64_t tiles = cdiv(a0.M, (int64_t)SQ_T) * cdiv(a0.N, (int64_t)SQ_T);
+  SqmmBatch b;
+  for (int i = 0; i < count; ++i) {
+    const SqmmArgs& a0 = args[i];
+    if (a0.M < 0 || a0.N < 0 || a0.K < 0 || !a0.out || (a0.prev && !a0.flag) ||
+        a0.M != args[0].M || a0.N != args[0].N || (a0.out2 && a0.epi != SQ_TRIU)) {
+      set_error("sqmm: invalid arguments");
+      return IFK_ERR_INVALID;
+    }
+    b.a[i] = a0;
+    // 16-byte operand loads need 16-byte aligned rows
+    b.a[i].vec_a = a0.A && ((uintptr_t)a0.A & 15) == 0 && a0.lda % 4 == 0;
+    b.a[i].vec_b = a0.B && ((uintptr_t)a0.B & 15) == 0 && a0.ldb % 4 == 0;
+  }
+  if (args[0].M == 0 || args[0].N == 0) return IFK_OK;
+  const int64_t tiles = cdiv(args[0].M, (int64_t)SQ_T) * cdiv(args[0].N, (int64_t)SQ_T);
   if (tiles > 0x7fffffffLL) {
     set_error("sqmm: grid too large");
     return IFK_ERR_INVALID;
   }
-  SqmmArgs a = a0;
-  // 16-byte operand loads need 16-byte aligned rows
-  a.vec_a = a.A && ((uintptr_t)a.A & 15) == 0 && a.lda % 4 == 0;
-  a.vec_b = a.B && ((uintptr_t)a.B & 15) == 0 && a.ldb % 4 == 0;
-  hipLaunchKernelGGL(sqmm_kernel, dim3((unsigned)tiles), dim3(SNT), 0, s, a);
+  hipLaunchKernelGGL(sqmm_kernel, dim3((unsigned)tiles, (unsigned)count), dim3(SNT), 0, s, b);
   return check_launch("sqmm");
 }
 
@@ -1262,19 +1334,24 @@ int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b) {
 }
 
 int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
-                 float* dref, float tol, int* flag) {
-  if (n < 1 || n > CHOLB_MAX || lda < n || ldu < n) {
+                 float* dref, float tol, int* flag, float* M, int64_t ldm) {
+  if (n < 1 || n > CHOLB_MAX || lda < n || ldu < n || (M && ldm < n)) {
     set_error("cholb: size out of range");
     return IFK_ERR_INVALID;
   }
   hipLaunchKernelGGL(cholb_first_kernel, dim3(1), dim3(SNT), 0, s, A, lda, n, U, ldu, Zd, dref, tol,
-                     flag);
+                     flag, M, ldm);
   if (int rc = check_launch("cholb_first")) return rc;
   const int nb = (n + SB - 1) / SB;
-  for (int k = 0; k + 1 < nb; ++k) {
-    const int m = nb - 1 - k;   // blocks right of k; (i, j) pairs: m (m + 1) / 2
-    hipLaunchKernelGGL(cholb_step_kernel, dim3((unsigned)(m * (m + 1) / 2)), dim3(SNT), 0, s, A,
-                       lda, n, U, ldu, Zd, dref, tol, flag, k);
+  // step k: the (i, j) pairs k < i <= j (m (m + 1) / 2 of them, m = nb - 1 - k),
+  // then with M the k + 1 blocks of M's column block k (column block 0 comes
+  // from cholb_first; the last takes one more launch, k = nb - 1, of M blocks only)
+  for (int k = 0; k < nb; ++k) {
+    const int m = nb - 1 - k;
+    const int wgs = m * (m + 1) / 2 + ((M && k > 0) ? k + 1 : 0);
+    if (wgs == 0) continue;
+    hipLaunchKernelGGL(cholb_step_kernel, dim3((unsigned)wgs), dim3(SNT), 0, s, A, lda, n, U, ldu,
+                       Zd, dref, tol, flag, k, M, ldm);
     if (int rc = check_launch("cholb_step")) return rc;
   }
   return IFK_OK;
