@@ -329,7 +329,7 @@ def main() -> int:
         "config": {
             "workload": f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, "
                         f"p={p} rows, bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9",
-            "factor_path": "fold then finalize" if args.unfused else "fused fold + finalize, 512-column blocks by CholeskyQR2 (panel path if flagged)",
+            "factor_path": "fold then finalize" if args.unfused else "fused fold + finalize, 1024-column blocks by CholeskyQR2 (panel path if flagged)",
             "n_in": n_in, "n_out": n_out, "p": p, "algorithmic_gflop_per_step": round(flops / 1e9, 1),
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
         },

@@ -45,6 +45,9 @@ struct OutRef {
   bf16_t* cb;      // optional RNE bf16 copy of the result
   int64_t ldcb;
   int64_t bstride_b;
+  int upper = 0;   // only the upper triangle is wanted (a square Gram matrix):
+                   // tiles wholly below the diagonal are skipped and hold
+                   // unspecified values
 };
 
 inline OutRef out_f32(float* c, int64_t ldc, int64_t bs = 0) {
@@ -56,6 +59,10 @@ inline OutRef out_bf16(bf16_t* cb, int64_t ld, int64_t bs = 0) {
 inline OutRef out_both(float* c, int64_t ldc, bf16_t* cb, int64_t ldcb, int64_t bstride = 0,
                        int64_t bstride_b = 0) {
   return OutRef{c, ldc, bstride, cb, ldcb, bstride_b};
+}
+inline OutRef upper_part(OutRef o) {
+  o.upper = 1;
+  return o;
 }
 
 // Scratch the engine may use for split-K partial sums (fp32 elements).  When

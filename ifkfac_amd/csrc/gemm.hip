@@ -295,6 +295,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   const int z = blockIdx.z;
   const int bidx = z / p.splits, split = z % p.splits;
   const int64_t m0 = (int64_t)tm * GBM, n0 = (int64_t)tn * GBN;
+  if (p.upper_only && m0 >= n0 + GBN) return;   // wholly below the diagonal
 
   const void* Ab = (const char*)p.A + (size_t)bidx * p.bsa * (ADT == DT_F32 ? 4 : 2);
   const void* Bb = (const char*)p.B + (size_t)bidx * p.bsb * (BDT == DT_F32 ? 4 : 2);
@@ -504,6 +505,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   p.Cb = C.cb; p.ldcb = C.ldcb; p.bscb = C.bstride_b;
   p.vec_a = vec_ok(A);
   p.vec_b = vec_ok(B);
+  p.upper_only = C.upper && M == N;
   p.vec_c = (!C.c || ((uintptr_t)C.c % 16 == 0 && C.ldc % 4 == 0 && C.bstride % 4 == 0)) &&
             (!C.cb || ((uintptr_t)C.cb % 8 == 0 && C.ldcb % 4 == 0 && C.bstride_b % 4 == 0));
   // The 256 x 256 bf16 kernel takes the large contractions; small or fp32
@@ -588,7 +590,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   if (pr) {
     // algorithmic work: 2 M N K (M N K when one operand is triangular), and the
     // minimal traffic: each operand read once, C read (beta != 0) and written once
-    const double tri = (A.tri != TRI_NONE || B.tri != TRI_NONE) ? 0.5 : 1.0;
+    const double tri = (A.tri != TRI_NONE || B.tri != TRI_NONE || p.upper_only) ? 0.5 : 1.0;
     pr->variant = vid;
     pr->m = M;
     pr->n = N;

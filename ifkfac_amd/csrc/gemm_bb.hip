@@ -137,6 +137,7 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
   const int z = blockIdx.z;
   const int bidx = z / p.splits, split = z % p.splits;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  if (p.upper_only && m0 >= n0 + BN) return;   // wholly below the diagonal
 
   int64_t klo = 0, khi = p.K;
   if (p.tria == TRI_UPPER) klo = max(klo, m0);

@@ -17,6 +17,7 @@ struct GemmParams {
   int vec_a, vec_b;
   int vec_c;   // C (if any) 16-byte and Cb (if any) 8-byte aligned, with ld and
                // batch strides multiples of 4 elements: vector epilogue
+  int upper_only;   // skip tiles wholly below the diagonal (square Gram output)
 };
 
 // 256 x 256 x 32 bf16 kernel (gemm_big.hip); grid.x = tiles_m * tiles_n of

@@ -104,11 +104,11 @@ struct SqmmArgs {
   float* out2 = nullptr;      // also up(v) (ld ldo), with epi == SQ_TRIU
   int vec_a = 0, vec_b = 0;   // set by launch_sqmm
 };
-constexpr int SQ_BATCH = 3;
+constexpr int SQ_BATCH = 8;
 struct SqmmBatch {
   SqmmArgs a[SQ_BATCH];
 };
-// count independent products of one shape in one launch
+// count independent products (of any shapes) in one launch
 int launch_sqmm(hipStream_t s, const SqmmArgs* a, int count = 1);
 // C_b = alpha A_b B_b, fp32 row-major, 64 x 64 tiles (small products)
 int launch_gemm64(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const float* A,

@@ -375,7 +375,7 @@ static int cqr_pass1(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
   // pass 1: G1 = X^T X + c^2 I = U1^T U1, M1 = U1^{-1}
   const MatRef XA = Xb ? A_n(Xb, DT_BF16, ldc) : A_n(Xf, DT_F32, ldc);
   const MatRef XB = Xb ? B_t(Xb, DT_BF16, ldc) : B_t(Xf, DT_F32, ldc);
-  RC(gemm(s, math, KB, KB, pe, 1.0f, XA, XB, 0.0f, out_f32(q.G, B), 1, w.split));
+  RC(gemm(s, math, KB, KB, pe, 1.0f, XA, XB, 0.0f, upper_part(out_f32(q.G, B)), 1, w.split));
   RC(launch_add_diag(s, q.G, B, KB, c * c));
   RC(launch_cholb(s, q.G, B, (int)KB, q.U1, B, q.Zd, q.dref, HR_TOL, q.flag, q.M1, B));
   // X in its pe x KB layout, then Q2 = X M1 (pe x KB) into the reflector store
@@ -408,10 +408,10 @@ static int cqr_pass2(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
   // G2 = Q2^T Q2
   if (bf)
     RC(gemm(s, MATH_BF16, KB, KB, pe, 1.0f, A_n(w.YobT[k2], DT_BF16, ldc),
-            B_t(w.YobT[k2], DT_BF16, ldc), 0.0f, out_f32(q.G, B), 1, w.split));
+            B_t(w.YobT[k2], DT_BF16, ldc), 0.0f, upper_part(out_f32(q.G, B)), 1, w.split));
   else
     RC(gemm(s, MATH_F32, KB, KB, pe, 1.0f, A_n(q.Q2T, DT_F32, ldq), B_t(q.Q2T, DT_F32, ldq), 0.0f,
-            out_f32(q.G, B), 1, w.split));
+            upper_part(out_f32(q.G, B)), 1, w.split));
   SqmmArgs a;
   a.M = a.N = a.K = KB;
   a.ldo = B;
@@ -446,8 +446,10 @@ static int cqr_pass2(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
     RC(launch_sqmm(s, &f));
   }
   const float* F = q.F[cur];
-  // in one launch: R_new = -U2 U1 = -(U1 + F U1), F^2 (for M2), and
-  // c M1 + U2 (whose inverse is N)
+  // in one launch: R_new = -U2 U1 = -(U1 + F U1); M2 = U2^{-1} = I - F + F^2
+  // (the dropped -F^3 is below 1e-9 for the F of bf16 rounding noise and far
+  // below the bf16 rounding of M2's uses; fp32 arithmetic forms F^2 here and
+  // refines below); and c M1 + U2, whose inverse is N
   SqmmArgs t[3];
   t[0] = a;
   t[0].A = F, t[0].lda = B, t[0].tria = TRI_UPPER;
@@ -460,7 +462,14 @@ static int cqr_pass2(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
   t[1].A = F, t[1].lda = B, t[1].tria = TRI_UPPER;
   t[1].B = F, t[1].ldb = B, t[1].trib = TRI_UPPER;
   t[1].epi = SQ_TRIU;
-  t[1].out = q.S;
+  if (bf) {
+    t[1].C1 = F, t[1].ld1 = B, t[1].beta1 = -1.0f;
+    t[1].gamma = 1.0f;
+    t[1].out = q.M2[k2];
+    t[1].outb = q.M2Tb[k2], t[1].ldob = B, t[1].outb_t = 1;
+  } else {
+    t[1].out = q.S;
+  }
   t[2] = a;
   t[2].alpha = 0.0f;
   t[2].C1 = q.M1, t[2].ld1 = B, t[2].beta1 = c;
@@ -470,22 +479,21 @@ static int cqr_pass2(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float
   t[2].out = q.Am;
   RC(launch_sqmm(s, t, outer ? 3 : 1));
   if (!outer) return IFK_OK;
-  // M2 = U2^{-1}: (I - F)(I + F^2) = I + F^2 - F - F F^2, then in fp32
-  // arithmetic one Newton step M2 = M2a (2 I - U2 M2a)
-  {
-    SqmmArgs m = a;
-    m.A = F, m.lda = B, m.tria = TRI_UPPER;
-    m.B = q.S, m.ldb = B, m.trib = TRI_UPPER;
-    m.alpha = -1.0f;
-    m.C1 = q.S, m.ld1 = B, m.beta1 = 1.0f;
-    m.C2 = F, m.ld2 = B, m.beta2 = -1.0f;
-    m.gamma = 1.0f;
-    m.epi = SQ_TRIU;
-    m.out = bf ? q.M2[k2] : q.M2a;
-    if (bf) m.outb = q.M2Tb[k2], m.ldob = B, m.outb_t = 1;
-    RC(launch_sqmm(s, &m));
-  }
+  // fp32 arithmetic: M2a = (I - F)(I + F^2) = I + F^2 - F - F F^2, then one
+  // Newton step M2 = M2a (2 I - U2 M2a)
   if (!bf) {
+    {
+      SqmmArgs m = a;
+      m.A = F, m.lda = B, m.tria = TRI_UPPER;
+      m.B = q.S, m.ldb = B, m.trib = TRI_UPPER;
+      m.alpha = -1.0f;
+      m.C1 = q.S, m.ld1 = B, m.beta1 = 1.0f;
+      m.C2 = F, m.ld2 = B, m.beta2 = -1.0f;
+      m.gamma = 1.0f;
+      m.epi = SQ_TRIU;
+      m.out = q.M2a;
+      RC(launch_sqmm(s, &m));
+    }
     SqmmArgs m = a;
     m.A = F, m.lda = B, m.tria = TRI_UPPER;
     m.B = q.M2a, m.ldb = B, m.trib = TRI_UPPER;
@@ -960,6 +968,37 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
   for (int64_t w = 2 * TRINV_NB; w < n; w *= 2) {
     const int64_t step = 2 * w;
     const int64_t nfull = n / step;
+    const int64_t i0 = nfull * step;
+    const int64_t w2 = (i0 + w < n) ? n - i0 - w : 0;   // ragged last pair
+    if (math == MATH_F32 && rdt == DT_F32 && nfull + (w2 > 0 ? 1 : 0) <= SQ_BATCH) {
+      // fp32: every pair of the level in one launch per product on the
+      // small-product kernel: T = R12 Z22, then Z12 = -Z11 T
+      const float* Rf = (const float*)R;
+      SqmmArgs t1[SQ_BATCH], t2[SQ_BATCH];
+      int cnt = 0;
+      for (int64_t b = 0; b <= nfull; ++b) {
+        const int64_t r0 = b * step, nw = b < nfull ? w : w2;
+        if (nw <= 0) continue;
+        float* T = tmp + (size_t)b * w * w;
+        SqmmArgs x;
+        x.M = w, x.N = nw, x.K = nw;
+        x.A = Rf + r0 * ldr + r0 + w, x.lda = ldr;
+        x.B = Z + (r0 + w) * ldz + r0 + w, x.ldb = ldz, x.trib = TRI_UPPER;
+        x.out = T, x.ldo = nw;
+        t1[cnt] = x;
+        SqmmArgs y;
+        y.M = w, y.N = nw, y.K = w;
+        y.A = Z + r0 * ldz + r0, y.lda = ldz, y.tria = TRI_UPPER;
+        y.B = T, y.ldb = nw;
+        y.alpha = -1.0f;
+        y.out = Z + r0 * ldz + r0 + w, y.ldo = ldz;
+        t2[cnt] = y;
+        ++cnt;
+      }
+      RC(launch_sqmm(s, t1, cnt));
+      RC(launch_sqmm(s, t2, cnt));
+      continue;
+    }
     const bool small = math == MATH_F32 && rdt == DT_F32 && w <= 256;
     if (nfull > 0) {
       const void* R12 = Rc + (size_t)w * esz;  // block (0, w)
@@ -978,9 +1017,7 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
                 (int)nfull, sp));
       }
     }
-    const int64_t i0 = nfull * step;
-    if (i0 + w < n) {
-      const int64_t w2 = n - i0 - w;
+    if (w2 > 0) {
       const void* R12 = Rc + ((size_t)i0 * ldr + i0 + w) * esz;
       if (small) {
         RC(launch_gemm64(s, w, w2, w, 1.0f, (const float*)R12, ldr, 0, TRI_NONE,

@@ -1055,8 +1055,8 @@ __global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64
 // op(A) = A^T when ta (A stored K x M), op(B) = B^T when tb (B stored N x K);
 // tria / trib describe op(A) / op(B) (their zero triangles are skipped by K
 // range and masked).  alpha = 0 skips the product.  out2 (SQ_TRIU only,
-// same ld as out) receives up(v) as well.  Up to SQ_BATCH products of one
-// shape run in one launch (blockIdx.y selects the product).  outb receives an RNE
+// same ld as out) receives up(v) as well.  Up to SQ_BATCH independent
+// products run in one launch (blockIdx.y selects the product).  outb receives an RNE
 // bf16 copy, transposed (outb[j][i]) when outb_t.  With prev (same layout as
 // out), any stored entry further than tol from prev's sets *flag = 1 (a
 // convergence test).
@@ -1156,6 +1156,7 @@ __device__ __forceinline__ void sq_store(float* S, const float4 (&v)[SQ_PER], bo
 __global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmBatch batch) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
   const SqmmArgs& a = batch.a[blockIdx.y];
+  if ((int64_t)blockIdx.x >= ((a.M + SQ_T - 1) / SQ_T) * ((a.N + SQ_T - 1) / SQ_T)) return;
   __shared__ __attribute__((aligned(16))) float sA[SQ_T * SQ_LD];
   __shared__ __attribute__((aligned(16))) float sB[SQ_T * SQ_LD];
   __shared__ float red[4];
@@ -1275,10 +1276,11 @@ int launch_sqmm(hipStream_t s, const SqmmArgs* args, int count) {
     return IFK_ERR_INVALID;
   }
   SqmmBatch b;
+  int64_t tiles = 0;
   for (int i = 0; i < count; ++i) {
     const SqmmArgs& a0 = args[i];
     if (a0.M < 0 || a0.N < 0 || a0.K < 0 || !a0.out || (a0.prev && !a0.flag) ||
-        a0.M != args[0].M || a0.N != args[0].N || (a0.out2 && a0.epi != SQ_TRIU)) {
+        (a0.out2 && a0.epi != SQ_TRIU)) {
       set_error("sqmm: invalid arguments");
       return IFK_ERR_INVALID;
     }
@@ -1286,9 +1288,9 @@ int launch_sqmm(hipStream_t s, const SqmmArgs* args, int count) {
     // 16-byte operand loads need 16-byte aligned rows
     b.a[i].vec_a = a0.A && ((uintptr_t)a0.A & 15) == 0 && a0.lda % 4 == 0;
     b.a[i].vec_b = a0.B && ((uintptr_t)a0.B & 15) == 0 && a0.ldb % 4 == 0;
+    tiles = std::max<int64_t>(tiles, cdiv(a0.M, (int64_t)SQ_T) * cdiv(a0.N, (int64_t)SQ_T));
   }
-  if (args[0].M == 0 || args[0].N == 0) return IFK_OK;
-  const int64_t tiles = cdiv(args[0].M, (int64_t)SQ_T) * cdiv(args[0].N, (int64_t)SQ_T);
+  if (tiles == 0) return IFK_OK;
   if (tiles > 0x7fffffffLL) {
     set_error("sqmm: grid too large");
     return IFK_ERR_INVALID;
