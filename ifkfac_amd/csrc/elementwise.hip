@@ -108,6 +108,43 @@ int launch_zero_bf16(hipStream_t s, bf16_t* dst, int64_t ldd, int64_t rows, int6
   return check_launch("zero_bf16");
 }
 
+// Zero the 64 x 64 blocks of an n x n matrix (element size es bytes, row
+// stride ldb bytes) strictly below (lower) or above the block diagonal, one
+// row per workgroup, 16-byte stores where the row allows.  The blocked
+// triangular inverses write every block on and above (below, for the
+// transposed copy) the diagonal, so only these need clearing.
+__global__ void zero_tri_blocks_kernel(char* dst, int es, int64_t ldb, int64_t n, int lower,
+                                       int vec) {
+  for (int64_t r = blockIdx.x; r < n; r += gridDim.x) {
+    const int64_t kb = (r / 64) * 64;
+    const int64_t c0 = lower ? 0 : kb + 64, c1 = lower ? kb : n;
+    if (c1 <= c0) continue;
+    char* row = dst + r * ldb;
+    const int64_t b0 = c0 * es, b1 = c1 * es;
+    const int64_t v1 = vec ? b0 + (b1 - b0) / 16 * 16 : b0;
+    for (int64_t b = b0 + (int64_t)threadIdx.x * 16; b < v1; b += (int64_t)blockDim.x * 16)
+      *(uint4*)(row + b) = make_uint4(0, 0, 0, 0);
+    for (int64_t b = v1 + (int64_t)threadIdx.x * es; b < b1; b += (int64_t)blockDim.x * es) {
+      if (es == 4) *(uint32_t*)(row + b) = 0u;
+      else *(uint16_t*)(row + b) = (uint16_t)0;
+    }
+  }
+}
+
+int launch_zero_tri_blocks(hipStream_t s, void* dst, int es, int64_t ld, int64_t n, bool lower) {
+  if (n <= 64) return IFK_OK;
+  if (es != 2 && es != 4) {
+    set_error("zero_tri_blocks: element size");
+    return IFK_ERR_INVALID;
+  }
+  // every block edge is a multiple of 64 elements, so 16-byte stores need
+  // only an aligned base and row stride
+  const int vec = ((uintptr_t)dst % 16 == 0) && ((ld * es) % 16 == 0);
+  hipLaunchKernelGGL(zero_tri_blocks_kernel, dim3((unsigned)std::min<int64_t>(n, 4096)), dim3(256),
+                     0, s, (char*)dst, es, ld * es, n, lower ? 1 : 0, vec);
+  return check_launch("zero_tri_blocks");
+}
+
 // R[i][j] -= WT[j][i] over a rows x cols block, through a 32 x 32 LDS tile so
 // both the read of WT and the update of R are coalesced.
 __global__ void sub_transposed_kernel(float* R, int64_t ldr, const float* WT, int64_t ldw,

@@ -129,6 +129,9 @@ int launch_zero_rows(hipStream_t s, float* dst, int64_t ldd, int64_t r0, int64_t
 // zero a rows x cols block
 int launch_zero(hipStream_t s, float* dst, int64_t ldd, int64_t rows, int64_t cols);
 int launch_zero_bf16(hipStream_t s, bf16_t* dst, int64_t ldd, int64_t rows, int64_t cols);
+// zero the 64 x 64 blocks of an n x n matrix (element size es, ld elements)
+// strictly below (lower) or above the block diagonal
+int launch_zero_tri_blocks(hipStream_t s, void* dst, int es, int64_t ld, int64_t n, bool lower);
 // dst -= src (rows x cols)
 int launch_sub_inplace(hipStream_t s, float* dst, int64_t ldd, const float* src, int64_t lds,
                        int64_t rows, int64_t cols);

@@ -963,7 +963,8 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
     set_error("tri_inverse: the UT transform takes an fp32 Gram matrix");
     return IFK_ERR_INVALID;
   }
-  RC(launch_zero(s, Z, ldz, n, n));
+  // every block on and above the diagonal is written below
+  RC(launch_zero_tri_blocks(s, Z, 4, ldz, n, true));
   RC(launch_trinv_diag128(s, R, rdt, ldr, n, Z, ldz, safe, ut ? 1 : 0));
   for (int64_t w = 2 * TRINV_NB; w < n; w *= 2) {
     const int64_t step = 2 * w;
@@ -1051,9 +1052,11 @@ static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int6
   const char* Rc = (const char*)R;
   const int64_t NB = TRINV_NB;
   const int64_t n_ = ldb;   // row stride of both bf16 copies
-  RC(launch_zero(s, Z, ldz, n, n));
-  RC(launch_zero_bf16(s, ZT, n_, n, n));
-  if (zero_zb) RC(launch_zero_bf16(s, Zb, n_, n, n));
+  // every block on and above the diagonal of Z and Zb, and on and below it
+  // of ZT, is written below: only the other triangle is cleared
+  RC(launch_zero_tri_blocks(s, Z, 4, ldz, n, true));
+  RC(launch_zero_tri_blocks(s, ZT, 2, n_, n, false));
+  if (zero_zb) RC(launch_zero_tri_blocks(s, Zb, 2, n_, n, true));
   RC(launch_trinv_diag(s, R, rdt, ldr, n, NB, Z, ldz, safe, Zb, ZT, n_));
   for (int64_t w = NB; w < n; w *= 2) {
     const int64_t step = 2 * w;
