@@ -1064,14 +1064,17 @@ __global__ __launch_bounds__(SNT) void gemm64_kernel(int64_t M, int64_t N, int64
 // These products sit on the critical path of the fold while the far updates
 // occupy most CUs, so the kernel is built for latency and a small footprint:
 // a workgroup owns a 32 x 32 output tile (256 workgroups for 512 x 512),
-// stages K in 128-wide chunks (34 KB of LDS, several workgroups per CU) with
-// the next chunk's loads in flight during the current one, and its four
+// stages K in 32-wide chunks (12 KB of LDS, so eight workgroups fit a CU)
+// with the next chunk's loads in flight during the current one, and its four
 // waves split each chunk's K, reading k-contiguous fragments four at a time,
-// before one cross-wave reduction.  With SQ_UP / SQ_TRIU, tiles wholly below the diagonal only
+// before one cross-wave reduction.  The chunk width was measured on the
+// 1024-column fold (pair of factor updates of the 4096 -> 11008, p = 16384
+// step): 256: 26.5 ms, 128: 22.9, 64: 21.4, 32: 21.1 -- occupancy beats
+// fewer dependent chunks.  With SQ_UP / SQ_TRIU, tiles wholly below the diagonal only
 // store zeros and C1 / C2 are read on and above the diagonal only.
 // ---------------------------------------------------------------------------
 constexpr int SQ_T = 32;                 // output tile
-constexpr int SQ_KC = 128;               // K chunk staged at a time
+constexpr int SQ_KC = 32;                // K chunk staged at a time
 constexpr int SQ_LD = SQ_KC + 4;         // k-contiguous LDS rows; 4 mod 32 keeps
                                          // 8 rows' 16-byte reads on distinct banks
 constexpr int SQ_PER = SQ_T * SQ_KC / 4 / SNT;   // float4 loads per thread and operand
@@ -1157,9 +1160,12 @@ __global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmBatch batch) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
   const SqmmArgs& a = batch.a[blockIdx.y];
   if ((int64_t)blockIdx.x >= ((a.M + SQ_T - 1) / SQ_T) * ((a.N + SQ_T - 1) / SQ_T)) return;
-  __shared__ __attribute__((aligned(16))) float sA[SQ_T * SQ_LD];
-  __shared__ __attribute__((aligned(16))) float sB[SQ_T * SQ_LD];
-  __shared__ float red[4];
+  // the two staged operands, and after the K loop the cross-wave partial
+  // sums of waves 1..3 (3 x 16 x 64 floats)
+  constexpr int SQ_SMEM = 2 * SQ_T * SQ_LD > 3 * 16 * 64 ? 2 * SQ_T * SQ_LD : 3 * 16 * 64;
+  __shared__ __attribute__((aligned(16))) float smem[SQ_SMEM];
+  float* const sA = smem;
+  float* const sB = smem + SQ_T * SQ_LD;
   const int64_t tiles_m = (a.M + SQ_T - 1) / SQ_T;
   const int64_t m0 = (int64_t)(blockIdx.x % tiles_m) * SQ_T,
                 n0 = (int64_t)(blockIdx.x / tiles_m) * SQ_T;
@@ -1228,17 +1234,17 @@ __global__ __launch_bounds__(SNT) void sqmm_kernel(SqmmBatch batch) {
         d = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, d, 0, 0, 0);
       }
     }
-    // cross-wave sum into wave 0 (sA is free once every wave is past its reads)
+    // cross-wave sum into wave 0 (smem is free once every wave is past its reads)
     __syncthreads();
     if (wave > 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sA[((wave - 1) * 16 + i) * 64 + lane] = d[i];
+      for (int i = 0; i < 16; ++i) smem[((wave - 1) * 16 + i) * 64 + lane] = d[i];
     }
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        d[i] += sA[i * 64 + lane] + sA[(16 + i) * 64 + lane] + sA[(32 + i) * 64 + lane];
+        d[i] += smem[i * 64 + lane] + smem[(16 + i) * 64 + lane] + smem[(32 + i) * 64 + lane];
     }
   }
   if (wave != 0) return;
