@@ -54,7 +54,7 @@ PEAK_HBM_GBS = 8000.0
 # one step of the 4096 -> 11008, p = 16384 workload), from two rocprofv3 --pmc
 # runs (FETCH_SIZE, WRITE_SIZE) scaled by the same counters on a 256 MiB copy
 # (profiles/pmc_traffic_linear4096x11008_p16384.txt).  Other workloads: None.
-TRAFFIC = {("linear_4096x11008_p16384", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1>>"): 799.35e6}
+TRAFFIC = {("linear_4096x11008_p16384", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1>>"): 482.57e6}
 
 WORKLOADS = {
     # name: (n_in, n_out, p)

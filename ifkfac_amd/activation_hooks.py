@@ -232,14 +232,36 @@ class RawActivationHooks(GramMatrixEstimator):
         n = chunk.shape[1]
         return R, r, chunk, min(r + chunk.shape[0], n)
 
-    def _damped(self, side: str, module: nn.Module, rows: int, out_dtype: torch.dtype):
+    def _damped(self, side: str, module: nn.Module, rows: int, out_dtype: torch.dtype,
+                cqr: bool = False):
+        """Damped factor of one side; a held chunk goes into a fused fold +
+        finalize, whose outer blocks are factored by CholeskyQR2 with ``cqr``
+        (its flag may then be 2: see _retry_cholesky_qr)."""
         R, r, chunk, _ = self._side_state(side, module)
         if chunk is None:
             return self._finalize(R, rows, out_dtype)
         bufs = self._buf_X if side == "X" else self._buf_G
         return get_backend().fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
                                            1.0 / math.sqrt(rows), self.damping, out_dtype,
-                                           self.math)
+                                           self.math, cqr=cqr)
+
+    def _retry_cholesky_qr(self, factors, flags, out_dtype: torch.dtype):
+        """One host read of the flags of a consuming factor update: a side whose
+        CholeskyQR2 blocks were too ill-conditioned (flag 2) is recomputed by
+        the panel factorisation, which handles any input."""
+        mods = list(flags)
+        st = torch.cat([torch.cat(flags[m]) for m in mods]).cpu()
+        for i, m in enumerate(mods):
+            for j, side in enumerate(("X", "G")):
+                if int(st[2 * i + j]) != 2:
+                    continue
+                rows = self._n_rows_X[m] if side == "X" else self._n_rows_G[m]
+                logger.debug("get_factors() [%s]: %s factor by the panel path",
+                             _module_tag(m), side)
+                R, f = self._damped(side, m, rows, out_dtype, cqr=False)
+                fac, fl = list(factors[m]), list(flags[m])
+                fac[j], fl[j] = R, f
+                factors[m], flags[m] = tuple(fac), tuple(fl)
 
     # ------------------------------------------------------------------ factors
     def get_factors(self) -> Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]]:
@@ -291,11 +313,13 @@ class RawActivationHooks(GramMatrixEstimator):
             dev = (R_X_raw if R_X_raw is not None else chunk_X).device
             (R_X, fX), (R_G, fG) = run_pair(
                 dev,
-                lambda: self._damped("X", module, rows_X, out_dtype),
-                lambda: self._damped("G", module, rows_G, out_dtype),
+                lambda: self._damped("X", module, rows_X, out_dtype, cqr=consume),
+                lambda: self._damped("G", module, rows_G, out_dtype, cqr=consume),
                 b_first=n_G > n_X)
             factors[module] = (R_X, R_G)
             flags[module] = (fX, fG)
+        if consume and flags:
+            self._retry_cholesky_qr(factors, flags, out_dtype)
         return factors, flags
 
     # ------------------------------------------------------------------ modes

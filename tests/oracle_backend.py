@@ -43,8 +43,19 @@ class OracleBackend:
         flag = torch.tensor([1 if np.all(np.isfinite(Rd)) else 0], dtype=torch.int32)
         return out, flag
 
-    def fold_finalize(self, R, r_in, X, scale, damping, out_dtype, math):
+    # tests set this to make the CholeskyQR2 variant report an ill-conditioned
+    # block (status 2), as ifk_fold_finalize_cqr does, once per call
+    cqr_status2 = 0
+
+    def fold_finalize(self, R, r_in, X, scale, damping, out_dtype, math, cqr=False):
         self.calls["fold_finalize"] += 1
+        if cqr:
+            self.calls["fold_finalize_cqr"] += 1
+            if self.cqr_status2 > 0:
+                self.cqr_status2 -= 1
+                n = X.shape[1]
+                return torch.full((n, n), float("nan")).to(out_dtype), torch.tensor(
+                    [2], dtype=torch.int32)
         old = None if r_in == 0 else _np(R[:r_in])
         new = O.streaming_tsqr_update(old, _np(X))
         assert new.shape[0] == new.shape[1], "fused finalize of a partial-rank factor"

@@ -390,6 +390,30 @@ def test_update_step_consumes_held_chunk_in_fused_call(be):
     assert opt.hooks._held_X[first] is None and opt.hooks._R_X[first] is None
 
 
+def test_update_step_recomputes_ill_conditioned_cqr_side(be):
+    """The fused factor update runs the CholeskyQR2 variant; a side that reports
+    an ill-conditioned block (status 2) is recomputed by the panel path before
+    the factors are used, so they still equal the closed form."""
+    from ifkfac_amd import IFKFAC
+    model = _mlp()
+    lam = 1e-2
+    opt = IFKFAC(model, lr=1e-3, damping=lam, factor_update_freq=1)
+    X = torch.randn(40, 8, generator=torch.Generator().manual_seed(9))
+    acts, grads, hs = _capture(model, X)
+    opt.zero_grad()
+    model(X).pow(2).mean().backward()
+    for h in hs:
+        h.remove()
+    be.cqr_status2 = 1          # the first CholeskyQR2 call reports status 2
+    opt.step()
+    assert be.calls["fold_finalize_cqr"] == 4      # both sides of both layers
+    assert be.calls["fold_finalize"] == 5          # ... and one panel-path retry
+    for m in opt.hooks.linear_layers:
+        R_X, R_G = opt._factors[m]
+        assert np.abs(R_X.double().numpy() - O.chol_factor([acts[m].double().numpy()], 40, lam)).max() < 1e-5
+        assert np.abs(R_G.double().numpy() - O.chol_factor([grads[m].double().numpy()], 40, lam)).max() < 1e-5
+
+
 def test_chunks_fold_eagerly_between_updates(be):
     """factor_update_freq = 3: steps 1 and 2 fold their chunks at once, the chunk
     of step 3 is held for the fused update; get_factors() folds a held chunk
