@@ -558,6 +558,13 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
         return fl / (1.0e15 * rate * util) + part / 4.0e12;
       };
       mid = est(T1, true, 0.55) < est(T2, false, 1.0);
+    } else if ((A.tri != TRI_NONE || B.tri != TRI_NONE) && t256 < 300) {
+      // a triangular operand gives tiles K ranges from 0 to K: with about one
+      // round of 256 tiles the longest tile sets the time, and the 128 tile's
+      // four times as many tiles, taken heaviest first, balance the CUs
+      // (measured: 4096^3 with a triangular operand 160 -> 124 us; at 352
+      // tiles of 256 the 256 tile stays ahead)
+      mid = true;
     }
   }
   const int TM = bb ? gemm_bb_tile(mid) : (big ? gemm_big_tile_m() : GBM);

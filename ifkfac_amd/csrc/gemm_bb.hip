@@ -318,7 +318,7 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
 // in its L2 instead of being fetched again for every tile.  Other grids, and
 // products with a triangular operand (whose tiles differ in K range, so
 // contiguous ranges would load some XCDs more than others), visit tiles
-// grid-stride in column-major order.
+// grid-stride, heaviest first (tile_order).
 constexpr int XCD_GM = 8;
 
 template <class CF>
@@ -339,7 +339,9 @@ __global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p)
     }
   } else {
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-      bb_tile<CF>(p, tile % tiles_m, tile / tiles_m, smem_bb);
+      int tm, tn;
+      tile_order(tile, tiles_m, tiles_n, p.tria, p.trib, &tm, &tn);
+      bb_tile<CF>(p, tm, tn, smem_bb);
       __syncthreads();
     }
   }

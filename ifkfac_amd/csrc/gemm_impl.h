@@ -20,6 +20,27 @@ struct GemmParams {
   int upper_only;   // skip tiles wholly below the diagonal (square Gram output)
 };
 
+// Tile t of a grid-stride walk -> (tile row, tile column), heaviest tiles
+// first when an operand is triangular: a tile's K range shrinks down the rows
+// for an upper op(A) (up the rows for a lower one) and towards the left
+// columns for an upper op(B) (the right ones for a lower one), and
+// workgroups pick up tiles in order, so the longest ones start first.
+// Without a triangular operand: column-major.
+__device__ __forceinline__ void tile_order(int t, int tiles_m, int tiles_n, int tria, int trib,
+                                           int* tm, int* tn) {
+  if (tria == TRI_UPPER || tria == TRI_LOWER) {
+    const int r = t / tiles_n;
+    *tm = tria == TRI_UPPER ? r : tiles_m - 1 - r;
+    *tn = t % tiles_n;
+  } else if (trib == TRI_UPPER) {
+    *tn = tiles_n - 1 - t / tiles_m;
+    *tm = t % tiles_m;
+  } else {
+    *tm = t % tiles_m;
+    *tn = t / tiles_m;
+  }
+}
+
 // 256 x 256 x 32 bf16 kernel (gemm_big.hip); grid.x = tiles_m * tiles_n of
 // its tile, grid.z = batch * splits.
 int gemm_big_tile_m();
