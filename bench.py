@@ -174,7 +174,8 @@ def main() -> int:
     if args.unfused:
         phase_names = ["fold_X", "fold_G", "finalize", "tri_inverse", "precondition", "update"]
     else:
-        phase_names = ["fold_finalize", "tri_inverse", "precondition", "update"]
+        # each side's inverse follows its factor on its stream
+        phase_names = ["fold_finalize_and_inverse", "precondition", "update"]
     nph = len(phase_names)
 
     def factors(mark):
@@ -188,18 +189,21 @@ def main() -> int:
                             lambda: be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16),
                             lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16),
                             b_first=n_out > n_in)
-        # RawActivationHooks._collect_factors(consume=True) of the update step:
-        # outer blocks by CholeskyQR2, then one host read of the status flags
-        # and the panel path for a side whose blocks were too ill-conditioned
-        ff = [lambda cqr: be.fold_finalize(None, 0, X, scale, lam, torch.bfloat16, MATH_BF16,
-                                           cqr=cqr),
-              lambda cqr: be.fold_finalize(None, 0, D, scale, lam, torch.bfloat16, MATH_BF16,
-                                           cqr=cqr)]
-        out = list(run_pair(dev, lambda: ff[0](True), lambda: ff[1](True), b_first=n_out > n_in))
+        # RawActivationHooks._collect_factors(consume=True) of the update step,
+        # as IFKFAC._update_factors calls it: outer blocks by CholeskyQR2, each
+        # side's inverse (with its bf16 copies) right after its factor on its
+        # stream, then one host read of the status flags and the panel path
+        # (and the inverse again) for a side whose blocks were too
+        # ill-conditioned
+        def side(T, cqr):
+            F, st = be.fold_finalize(None, 0, T, scale, lam, torch.bfloat16, MATH_BF16, cqr=cqr)
+            return F, st, be.tri_inverse_bf16(F)
+        out = list(run_pair(dev, lambda: side(X, True), lambda: side(D, True),
+                            b_first=n_out > n_in))
         st = torch.cat([out[0][1], out[1][1]]).cpu()
-        for i in range(2):
+        for i, T in enumerate((X, D)):
             if int(st[i]) == 2:
-                out[i] = ff[i](False)
+                out[i] = side(T, False)
         return out
 
     def step(first: bool, events=None):
@@ -210,14 +214,16 @@ def main() -> int:
                 events[k[0]].record()
             k[0] += 1
         mark()
-        (FX, _), (FG, _) = factors(mark)
+        if args.unfused:
+            (FX, _), (FG, _) = factors(mark)
+            mark()
+            (_, ZXb, ZXt), (_, ZGb, ZGt) = run_pair(dev, lambda: be.tri_inverse_bf16(FX),
+                                                    lambda: be.tri_inverse_bf16(FG),
+                                                    b_first=n_out > n_in)
+        else:
+            (_, _, (_, ZXb, ZXt)), (_, _, (_, ZGb, ZGt)) = factors(mark)
         mark()
-        # IFKFAC._update_factors / _nat_grad in bf16 arithmetic: the inverses
-        # with their bf16 copies, then the apply from the copies
-        (_, ZXb, ZXt), (_, ZGb, ZGt) = run_pair(dev, lambda: be.tri_inverse_bf16(FX),
-                                                lambda: be.tri_inverse_bf16(FG),
-                                                b_first=n_out > n_in)
-        mark()
+        # IFKFAC._nat_grad in bf16 arithmetic: the apply from the inverses' copies
         nat = be.precondition_apply_bf16(grad, (ZXb, ZXt), (ZGb, ZGt))
         mark()
         be.momentum_update_(nat, buf, W, lr, mom, 0.0, first)

@@ -245,10 +245,11 @@ class RawActivationHooks(GramMatrixEstimator):
                                            1.0 / math.sqrt(rows), self.damping, out_dtype,
                                            self.math, cqr=cqr)
 
-    def _retry_cholesky_qr(self, factors, flags, out_dtype: torch.dtype):
+    def _retry_cholesky_qr(self, factors, flags, extras, then, out_dtype: torch.dtype):
         """One host read of the flags of a consuming factor update: a side whose
         CholeskyQR2 blocks were too ill-conditioned (flag 2) is recomputed by
-        the panel factorisation, which handles any input."""
+        the panel factorisation, which handles any input (and ``then`` run on
+        the new factor)."""
         mods = list(flags)
         st = torch.cat([torch.cat(flags[m]) for m in mods]).cpu()
         for i, m in enumerate(mods):
@@ -262,26 +263,39 @@ class RawActivationHooks(GramMatrixEstimator):
                 fac, fl = list(factors[m]), list(flags[m])
                 fac[j], fl[j] = R, f
                 factors[m], flags[m] = tuple(fac), tuple(fl)
+                if then is not None:
+                    ex = list(extras[m])
+                    ex[j] = then(side, m, R)
+                    extras[m] = tuple(ex)
 
     # ------------------------------------------------------------------ factors
     def get_factors(self) -> Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]]:
         """Damped factors (R_X, R_G) of every layer with enough data (fp32)."""
-        factors, _ = self._collect_factors(torch.float32)
+        factors, _, _ = self._collect_factors(torch.float32)
         return factors
 
-    def _collect_factors(self, out_dtype: torch.dtype, consume: bool = False):
+    def _collect_factors(self, out_dtype: torch.dtype, consume: bool = False, then=None):
         """get_factors with the output dtype chosen and the finite flags returned.
 
         With ``consume`` the caller clears the hooks right after, so a held
         chunk goes into a fused fold + finalize and the running factor is
         left as it was (it is about to be dropped); otherwise held chunks are
-        folded first, exactly as get_factors leaves them."""
+        folded first, exactly as get_factors leaves them.  ``then(side,
+        module, R)`` runs on each side's stream right after its factor (work
+        that depends on one side only starts while the other is still being
+        factored); its results come back as the third value, per module as
+        (X side, G side), or None without ``then``."""
         if self.deferred:
             self._drain_deferred()
         if not consume:
             self._fold_held()
         factors: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         flags: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
+        extras: Dict[nn.Module, tuple] = {}
+
+        def side(s, module, rows, cqr):
+            R, f = self._damped(s, module, rows, out_dtype, cqr=cqr)
+            return R, f, (then(s, module, R) if then is not None else None)
         for module in self._linear_layers:
             R_X_raw, _, chunk_X, r_X = self._side_state("X", module)
             R_G_raw, _, chunk_G, r_G = self._side_state("G", module)
@@ -311,16 +325,17 @@ class RawActivationHooks(GramMatrixEstimator):
             # the two sides are independent: finalize them concurrently, the
             # wider (longer) one enqueued first
             dev = (R_X_raw if R_X_raw is not None else chunk_X).device
-            (R_X, fX), (R_G, fG) = run_pair(
+            (R_X, fX, eX), (R_G, fG, eG) = run_pair(
                 dev,
-                lambda: self._damped("X", module, rows_X, out_dtype, cqr=consume),
-                lambda: self._damped("G", module, rows_G, out_dtype, cqr=consume),
+                lambda: side("X", module, rows_X, consume),
+                lambda: side("G", module, rows_G, consume),
                 b_first=n_G > n_X)
             factors[module] = (R_X, R_G)
             flags[module] = (fX, fG)
+            extras[module] = (eX, eG)
         if consume and flags:
-            self._retry_cholesky_qr(factors, flags, out_dtype)
-        return factors, flags
+            self._retry_cholesky_qr(factors, flags, extras, then, out_dtype)
+        return factors, flags, (extras if then is not None else None)
 
     # ------------------------------------------------------------------ modes
     def _drain_deferred(self):

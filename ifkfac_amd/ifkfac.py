@@ -123,9 +123,24 @@ class IFKFAC(torch.optim.Optimizer):
         t0 = time.perf_counter()
         blend = self.gamma > 0.0 and bool(self._factors)
         out_dtype = torch.bfloat16 if (self.use_true_bf16 and not blend) else torch.float32
+        be = get_backend()
+        copies = hasattr(be, "tri_inverse_bf16")
+
+        def inverse(side, module, R):
+            m = solve_math_for(R.dtype)
+            if m == MATH_BF16 and copies:
+                # bf16 arithmetic: keep the bf16 copies of Z and Z^T next to Z,
+                # so the per-step apply does not cast the inverses again
+                return be.tri_inverse_bf16(R)
+            return be.tri_inverse(R, m)
+
         try:
-            # the hooks are cleared right after: a held chunk may be consumed
-            new_factors, flags = self.hooks._collect_factors(out_dtype, consume=True)
+            # the hooks are cleared right after: a held chunk may be consumed.
+            # Without a blend each side's inverse follows its factor on its
+            # stream, so the narrower side's inverse runs while the wider one
+            # is still being factored.
+            new_factors, flags, early = self.hooks._collect_factors(
+                out_dtype, consume=True, then=None if blend else inverse)
         except IFKFACRankError as e:
             logger.warning("IFKFAC: factor update skipped — %s", e)
             self.timing["factor_compute"].append(time.perf_counter() - t0)
@@ -159,26 +174,20 @@ class IFKFAC(torch.optim.Optimizer):
                          for m, (a, b) in clean.items()}
 
         self._factors = clean
-        be = get_backend()
         self._inverses = {}
         self._inverse_copies = {}
-        copies = hasattr(be, "tri_inverse_bf16")
         for module, (R_X, R_G) in clean.items():
-            m = solve_math_for(R_X.dtype)
-            b_first = R_G.shape[0] > R_X.shape[0]
-            if m == MATH_BF16 and copies:
-                # bf16 arithmetic: keep the bf16 copies of Z and Z^T next to Z,
-                # so the per-step apply does not cast the inverses again
-                (ZX, ZXb, ZXt), (ZG, ZGb, ZGt) = run_pair(
-                    R_X.device, lambda R=R_X: be.tri_inverse_bf16(R),
-                    lambda R=R_G: be.tri_inverse_bf16(R), b_first=b_first)
-                self._inverses[module] = (ZX, ZG)
-                self._inverse_copies[module] = ((ZXb, ZXt), (ZGb, ZGt))
+            if early is not None:
+                invX, invG = early[module]
             else:
-                self._inverses[module] = run_pair(R_X.device,
-                                                  lambda R=R_X: be.tri_inverse(R, m),
-                                                  lambda R=R_G: be.tri_inverse(R, m),
-                                                  b_first=b_first)
+                invX, invG = run_pair(R_X.device, lambda R=R_X: inverse("X", module, R),
+                                      lambda R=R_G: inverse("G", module, R),
+                                      b_first=R_G.shape[0] > R_X.shape[0])
+            if isinstance(invX, tuple):
+                self._inverses[module] = (invX[0], invG[0])
+                self._inverse_copies[module] = ((invX[1], invX[2]), (invG[1], invG[2]))
+            else:
+                self._inverses[module] = (invX, invG)
         self.timing["factor_compute"].append(time.perf_counter() - t0)
 
     # ------------------------------------------------------------------ apply
