@@ -146,14 +146,15 @@ __device__ inline float safe_divisor(float d) {
 // factorisation continues on a clamped pivot so every thread runs the same
 // steps); mode 1: the pivot rule of cholesky_bf16, max(pivot, 1e-7).
 //
-// Right-looking, blocked by CB columns.  Wave 0 factors each CB x CB diagonal
-// block redundantly in every lane's registers (no cross-lane traffic on the
-// pivot chain), then lane l solves the block-row column o + CB + l against it
-// by forward substitution, so the whole block row is finished by one wave
-// with no barrier.  The rank-CB trailing update runs on fp32 MFMA across the
-// four waves.  Two barriers per block.  CB = 8 measured fastest (the 16 x 16
-// register leaf costs more than the extra barriers it saves).
-template <int CB = 8>
+// Right-looking, blocked by CB columns.  Wave 0 factors each CB-row panel
+// with lane c holding column c of the panel rows in registers: at step k
+// the pivot and row k's entries come from their lanes by readlane, so the
+// diagonal block's factor and the block row's forward substitution are one
+// sweep with no LDS traffic or barrier on the pivot chain.  The rank-CB
+// trailing update runs on fp32 MFMA across the four waves.  Two barriers per
+// panel.  CB = 32 measured fastest (the pivot chain, not the FMA count,
+// bounds a panel, so fewer panels and barriers win).
+template <int CB = 32>
 __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode,
                                           const float* dref = nullptr, int b = SB) {
   const int t = threadIdx.x;
@@ -166,57 +167,31 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
   for (int kb = 0; kb < SB / CB; ++kb) {
     const int o = kb * CB;
     if (wave == 0) {
-      const int c = o + CB + lane;             // block-row column of this lane
-      float u[CB][CB], x[CB], ri[CB];
+      // a[i] = entry (o + i, lane); only lanes >= o + i hold upper-triangle
+      // entries, and only those are broadcast or stored as results
+      float a[CB];
 #pragma unroll
-      for (int i = 0; i < CB; ++i) {
-#pragma unroll
-        for (int j = i; j < CB; ++j) u[i][j] = A[(o + i) * SLD + o + j];
-        x[i] = (c < SB) ? A[(o + i) * SLD + c] : 0.0f;
-      }
+      for (int i = 0; i < CB; ++i) a[i] = (lane >= o) ? A[(o + i) * SLD + lane] : 0.0f;
 #pragma unroll
       for (int k = 0; k < CB; ++k) {
-        const float piv = u[k][k];
-        float pv, rs;
+        const float piv = bcast(a[k], o + k);
+        float rs, dg;
         if (mode == 0) {
           if (!(piv > tol * dgs[o + k]) || !isfinite(piv)) flag = 1;
-          pv = fmaxf(piv, 1e-30f);
+          const float pv = fmaxf(piv, 1e-30f);
           rs = __builtin_amdgcn_rsqf(pv);
-          u[k][k] = pv * rs;
+          dg = pv * rs;
         } else {
-          pv = fmaxf(piv, 1e-7f);
-          u[k][k] = sqrtf(pv);
-          rs = 1.0f / u[k][k];
+          dg = sqrtf(fmaxf(piv, 1e-7f));
+          rs = 1.0f / dg;
         }
-        ri[k] = rs;
+        a[k] = (lane == o + k) ? dg : a[k] * rs;
 #pragma unroll
-        for (int j = k + 1; j < CB; ++j) u[k][j] *= rs;
-#pragma unroll
-        for (int i = k + 1; i < CB; ++i)
-#pragma unroll
-          for (int j = i; j < CB; ++j) u[i][j] = fmaf(-u[k][i], u[k][j], u[i][j]);
+        for (int i = k + 1; i < CB; ++i) a[i] = fmaf(-bcast(a[k], o + i), a[k], a[i]);
       }
-      // block row: U_kk^T x = a (forward substitution)
+      if (lane >= o) {
 #pragma unroll
-      for (int i = 0; i < CB; ++i) {
-        float acc = x[i];
-#pragma unroll
-        for (int m = 0; m < i; ++m) acc = fmaf(-u[m][i], x[m], acc);
-        x[i] = acc * ri[i];
-      }
-      if (lane < CB) {
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-          float v = 0.0f;
-#pragma unroll
-          for (int j = i; j < CB; ++j)
-            if (j == lane) v = u[i][j];
-          A[(o + i) * SLD + o + lane] = v;
-        }
-      }
-      if (c < SB) {
-#pragma unroll
-        for (int i = 0; i < CB; ++i) A[(o + i) * SLD + c] = x[i];
+        for (int i = 0; i < CB; ++i) A[(o + i) * SLD + lane] = a[i];
       }
     }
     __syncthreads();
