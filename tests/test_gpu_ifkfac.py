@@ -99,3 +99,32 @@ def test_hooks_get_factors_on_gpu(hip):
     again = kfac.hooks.get_factors()
     for m in factors:
         assert torch.equal(factors[m][0], again[m][0])
+
+
+def test_update_step_recomputes_ill_conditioned_side_on_gpu(hip, caplog):
+    """A factor update whose input side has two equal columns of large scale:
+    the CholeskyQR2 pivot test flags it (status 2), the side is refolded by the
+    panel path and its inverse computed again, so the optimizer holds the
+    closed-form damped factor and a matching inverse rather than the flagged
+    block's values.  Tolerance: Gram relative error 1e-5 (fp32 factor,
+    kappa(R) ~ 1.4e4); ||R Z - I||_max 1e-2."""
+    import logging
+    from ifkfac_amd import IFKFAC
+    from oracle import ifk_oracle as O
+    torch.manual_seed(3)
+    model = nn.Linear(96, 64, bias=False).cuda()
+    kfac = IFKFAC(model, lr=0.0, damping=1e-2, factor_update_freq=1, momentum=0.0)
+    x = torch.randn(256, 96, device="cuda")
+    x[:, 10] *= 1e3
+    x[:, 20] = x[:, 10]
+    caplog.set_level(logging.DEBUG, logger="ifkfac_amd.activation_hooks")
+    model(x).square().sum().backward()
+    kfac.step()
+    assert any("X factor by the panel path" in r.getMessage() for r in caplog.records)
+    R_X = kfac._factors[model][0].double().cpu()
+    want = torch.from_numpy(O.chol_factor([x.double().cpu().numpy()], 256, 1e-2))
+    g, gw = R_X.T @ R_X, want.T @ want
+    assert (torch.linalg.norm(g - gw) / torch.linalg.norm(gw)).item() < 1e-5
+    Z_X = kfac._inverses[model][0].double().cpu()
+    assert bool(torch.isfinite(Z_X).all())
+    assert (R_X @ Z_X - torch.eye(96, dtype=torch.float64)).abs().max().item() < 1e-2
