@@ -730,10 +730,37 @@ __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, 
   const int nb = (n + SB - 1) / SB;
   const int nupd = (nb - 1 - k) * (nb - k) / 2;
   if ((int)blockIdx.x >= nupd) {
-    // column block k of M = U^{-1}: M_kk = Z_k, and for i < k
-    //   M_ik = -(sum_{l = i}^{k-1} M_il U_lk) Z_k
-    // from blocks of U and M that earlier launches finished
-    const int i = (int)blockIdx.x - nupd;
+    // M = U^{-1} by column blocks: M_kk = Z_k and, for i < k,
+    //   M_ik = -(sum_{l = i}^{k-1} M_il U_lk) Z_k.
+    // The sum is built up across launches in M_ik's own place: launch k adds
+    // the terms l = k - 1 of the columns kk > k (storing, not adding, the
+    // first term l = i), and finishes column k with its own l = k - 1 term,
+    // so no workgroup multiplies more than two blocks.  Every block read
+    // here was finished by an earlier launch.
+    const int idx = (int)blockIdx.x - nupd;
+    float va[PAD_PER], vb[PAD_PER], vc[PAD_PER];
+    if (idx > k) {
+      const int w = nb - 1 - k, a = idx - (k + 1);
+      const int i = a / w, kk = k + 1 + a % w;   // i < k < kk < nb
+      const int bkk = (n - SB * kk) < SB ? (n - SB * kk) : SB;
+      const bool first = (i == k - 1);
+      ld_blk(va, Mo + (int64_t)SB * i * ldm + SB * (k - 1), ldm, SB, SB, 0.0f);
+      ld_blk(vb, U + (int64_t)SB * (k - 1) * ldu + SB * kk, ldu, SB, bkk, 0.0f);
+      if (first) {
+#pragma unroll
+        for (int q = 0; q < PAD_PER; ++q) vc[q] = 0.0f;
+      } else {
+        ld_blk(vc, Mo + (int64_t)SB * i * ldm + SB * kk, ldm, SB, bkk, 0.0f);
+      }
+      st_pad(sA, va);
+      st_pad(sB, vb);
+      st_pad(sC, vc);
+      __syncthreads();
+      sm_gemm64<false, false>(sA, sB, sC, 1.0f, true);
+      st_blk(sC, Mo + (int64_t)SB * i * ldm + SB * kk, ldm, SB, bkk);
+      return;
+    }
+    const int i = idx;
     const int bk = (n - SB * k) < SB ? (n - SB * k) : SB;
     const float* Zk = Zd + (size_t)k * SB * SB;
     if (i == k) {
@@ -743,25 +770,24 @@ __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, 
       }
       return;
     }
-    float va[PAD_PER], vb[PAD_PER];
-    for (int e = t; e < SB * SB; e += SNT) sC[(e >> 6) * SLD + (e & 63)] = 0.0f;
-    ld_blk(va, Mo + (int64_t)SB * i * ldm + SB * i, ldm, SB, SB, 0.0f);
-    ld_blk(vb, U + (int64_t)SB * i * ldu + SB * k, ldu, SB, bk, 0.0f);
-    for (int l = i; l < k; ++l) {
-      st_pad(sA, va);
-      st_pad(sB, vb);
-      __syncthreads();
-      if (l + 1 < k) {   // the next pair's loads fly while this one multiplies
-        ld_blk(va, Mo + (int64_t)SB * i * ldm + SB * (l + 1), ldm, SB, SB, 0.0f);
-        ld_blk(vb, U + (int64_t)SB * (l + 1) * ldu + SB * k, ldu, SB, bk, 0.0f);
-      }
-      sm_gemm64<false, false>(sA, sB, sC, 1.0f, true);
+    float vz[PAD_PER];
+    ld_blk(va, Mo + (int64_t)SB * i * ldm + SB * (k - 1), ldm, SB, SB, 0.0f);
+    ld_blk(vb, U + (int64_t)SB * (k - 1) * ldu + SB * k, ldu, SB, bk, 0.0f);
+    if (i == k - 1) {
+#pragma unroll
+      for (int q = 0; q < PAD_PER; ++q) vc[q] = 0.0f;
+    } else {
+      ld_blk(vc, Mo + (int64_t)SB * i * ldm + SB * k, ldm, SB, bk, 0.0f);
     }
 #pragma unroll
-    for (int q = 0; q < PAD_PER; ++q) va[q] = Zk[t + SNT * q];
-    st_pad(sZ, va);
+    for (int q = 0; q < PAD_PER; ++q) vz[q] = Zk[t + SNT * q];
+    st_pad(sA, va);
+    st_pad(sB, vb);
+    st_pad(sC, vc);
+    st_pad(sZ, vz);
     __syncthreads();
-    sm_gemm64<false, false>(sC, sZ, sA, -1.0f, false);
+    sm_gemm64<false, false>(sA, sB, sC, 1.0f, true);     // C = P_ik + M_i,k-1 U_k-1,k
+    sm_gemm64<false, false>(sC, sZ, sA, -1.0f, false);   // M_ik = -C Z_k
     st_blk(sA, Mo + (int64_t)SB * i * ldm + SB * k, ldm, SB, bk);
     return;
   }
@@ -1327,11 +1353,12 @@ int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t 
   if (int rc = check_launch("cholb_first")) return rc;
   const int nb = (n + SB - 1) / SB;
   // step k: the (i, j) pairs k < i <= j (m (m + 1) / 2 of them, m = nb - 1 - k),
-  // then with M the k + 1 blocks of M's column block k (column block 0 comes
-  // from cholb_first; the last takes one more launch, k = nb - 1, of M blocks only)
+  // then with M the k + 1 blocks of M's column block k and the k m partial
+  // sums of its later column blocks (column block 0 comes from cholb_first;
+  // the last takes one more launch, k = nb - 1, of M blocks only)
   for (int k = 0; k < nb; ++k) {
     const int m = nb - 1 - k;
-    const int wgs = m * (m + 1) / 2 + ((M && k > 0) ? k + 1 : 0);
+    const int wgs = m * (m + 1) / 2 + ((M && k > 0) ? k + 1 + k * m : 0);
     if (wgs == 0) continue;
     hipLaunchKernelGGL(cholb_step_kernel, dim3((unsigned)wgs), dim3(SNT), 0, s, A, lda, n, U, ldu,
                        Zd, dref, tol, flag, k, M, ldm);
