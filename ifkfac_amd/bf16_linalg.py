@@ -8,10 +8,15 @@ intermediate to bf16, so these results are at least as accurate; parity is at
 the level of the reference's own checks (R against the Cholesky factor of
 A^T A after sign normalisation, L L^T against A, R X against B).
 
-Deliberate differences, both documented: the R factors are returned with a
-positive diagonal (the reference leaves the Householder sign -sign(x0) on
-each diagonal entry), and ``block_size`` is accepted but the panel width is
-the kernel's own (64 columns).
+Deliberate differences: the R factors are returned with a positive
+diagonal (the reference leaves the Householder sign -sign(x0) on each
+diagonal entry); ``block_size`` is accepted but the panel width is the
+kernel's own (64 columns); and a column whose leading entry is exactly 0 is
+reduced as LAPACK's dlarfg does (sign(0) = +1).  The reference takes torch's
+sign(0) = 0 there (bf16_linalg.py:114, :173), so its reflector maps that
+column to its negative instead of onto e1 and leaves the column unreduced.
+The clamps of ``_safe_div`` and of the Cholesky pivot are the reference's,
+NaN pivots included.
 """
 from __future__ import annotations
 

@@ -51,6 +51,11 @@ int trinv_copies(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, 
 
 // nat as precondition_apply in bf16 arithmetic, from the copies of
 // trinv_copies (nothing to cast but grad).
+size_t precondition_apply_b_min_ws(int64_t n_out, int64_t n_in);
+int precondition_apply_b_fit(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                             int64_t ldg, const bf16_t* ZXb, const bf16_t* ZXt, int64_t ldx2,
+                             const bf16_t* ZGb, const bf16_t* ZGt, int64_t ldg2, float* nat,
+                             int64_t ldn, void* ws, size_t ws_bytes);
 size_t precondition_apply_b_ws(int64_t n_out, int64_t n_in);
 int precondition_apply_b(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
                          int64_t ldg, const bf16_t* ZXb, const bf16_t* ZXt, int64_t ldx2,

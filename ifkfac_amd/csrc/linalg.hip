@@ -27,6 +27,7 @@
 //   Z12 = -Z11 R12 Z22 with batched MFMA GEMMs, log2(n/64) levels), then
 //   nat = Z_G (Z_G^T grad) Z_X Z_X^T as four triangular MFMA products.
 #include <algorithm>
+#include <cstdint>
 #include <map>
 #include <mutex>
 #include <cmath>
@@ -156,10 +157,10 @@ static void plan_fold(Arena& a, int64_t p, int64_t n, bool need_C, FoldWs& w,
   w.split2.p = a.take<float>(w.split2.floats);
 }
 
-// Workspace of the block CholeskyQR path (cqr_block): 512 x 512 factors of
-// the outer block, the Cholesky's diagonal inverses, the block's tall
-// operands in both layouts (pe x 512 row-major, and transposed 512 x pe with
-// row stride ldq), fp32 or bf16 by the arithmetic, and -- by block parity,
+// Workspace of the block CholeskyQR path (cqr_pass1/2): CQR_B x CQR_B (1024 x
+// 1024) factors of the outer block, the Cholesky's diagonal inverses, the
+// block's tall operands in both layouts (pe x CQR_B row-major, and transposed
+// CQR_B x pe with row stride ldq), fp32 or bf16 by the arithmetic, and -- by block parity,
 // since a block's far update runs while the next block is factored -- the
 // inverses M2 and N its outer update applies.
 struct CqrWs {
@@ -173,11 +174,11 @@ struct CqrWs {
   float* S;       // F^2, then U2 M2a (Newton step)
   float* M2a;     // first approximation of U2^{-1}
   float* Am;      // c M1 + U2
-  float* Zd;      // 8 x 64 x 64
+  float* Zd;      // CQR_B / 64 (16) x 64 x 64 diagonal-block inverses
   float* dref;
-  float* Xc;      // X, pe x 512 (fp32 or bf16)
-  float* Q2f;     // Q2 = X M1, pe x 512 fp32
-  float* Q2T;     // Q2^T, 512 x pe (ld ldq; fp32 arithmetic)
+  float* Xc;      // X, pe x CQR_B (fp32 or bf16)
+  float* Q2f;     // Q2 = X M1, pe x CQR_B fp32
+  float* Q2T;     // Q2^T, CQR_B x pe (ld ldq; fp32 arithmetic)
   int64_t ldq;
   float* M2[2];   // U2^{-1} (fp32), and its transpose in bf16
   bf16_t* M2Tb[2];
@@ -362,7 +363,7 @@ static int outer_finish(hipStream_t s, int math, FoldWs& w, int k2, float* CT, b
 // bf16 arithmetic: X is read as bf16 (the shadow), Q2 = X (M1_hi + M1_lo)
 // (the bf16 split of M1 keeps Q2 consistent with R_new to about 2^-17) is
 // rounded to bf16 into the block's reflector store (row-major and
-// transposed), and M2, N get bf16 copies; the 512 x 512 algebra is fp32.
+// transposed), and M2, N get bf16 copies; the 1024 x 1024 algebra is fp32.
 // First pass, up to Q2 in the block's reflector store (all the outer update's
 // S^T = CT_cols Q2 products need).
 static int cqr_pass1(hipStream_t s, int math, FoldWs& w, CqrWs& q, int k2, float c,
@@ -1149,14 +1150,16 @@ static void plan_apply(Arena& a, int64_t n_out, int64_t n_in, int math, void** T
   sp->p = a.take<float>(sp->floats);
 }
 
-// ... for precondition_apply_b: only grad^T is cast
+// ... for precondition_apply_b: only grad^T is cast.  The split-K scratch
+// holds at most split_cap floats (the GEMM engine uses fewer splits when it
+// is smaller, never failing for lack of it).
 static void plan_apply_b(Arena& a, int64_t n_out, int64_t n_in, void** T1, void** T2,
-                         bf16_t** cv, SplitScratch* sp) {
+                         bf16_t** cv, SplitScratch* sp, size_t split_cap = SIZE_MAX) {
   const size_t e = (size_t)n_out * n_in;
   *T1 = a.take<bf16_t>(e);
   *T2 = a.take<bf16_t>(e);
   *cv = a.take<bf16_t>(e);
-  sp->floats = split_floats(TRINV_NB, std::max(n_out, n_in));
+  sp->floats = std::min(split_floats(TRINV_NB, std::max(n_out, n_in)), split_cap);
   sp->p = a.take<float>(sp->floats);
 }
 
@@ -1274,6 +1277,40 @@ size_t precondition_apply_b_ws(int64_t n_out, int64_t n_in) {
   SplitScratch sp;
   plan_apply_b(a, n_out, n_in, &T1, &T2, &cv, &sp);
   return a.used;
+}
+
+size_t precondition_apply_b_min_ws(int64_t n_out, int64_t n_in) {
+  Arena a(nullptr, 0);
+  void *T1, *T2;
+  bf16_t* cv;
+  SplitScratch sp;
+  plan_apply_b(a, n_out, n_in, &T1, &T2, &cv, &sp, 0);
+  return a.used;
+}
+
+// precondition_apply_b in a workspace of any size from
+// precondition_apply_b_min_ws up: the split-K scratch gets what is left after
+// the operand buffers, up to what precondition_apply_b would take (with that
+// much room the two run the same launches and give the same bits).
+int precondition_apply_b_fit(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                             int64_t ldg, const bf16_t* ZXb, const bf16_t* ZXt, int64_t ldx2,
+                             const bf16_t* ZGb, const bf16_t* ZGt, int64_t ldg2, float* nat,
+                             int64_t ldn, void* ws, size_t ws_bytes) {
+  if (n_out < 1 || n_in < 1 || ldg < n_in || ldn < n_in || ldx2 < n_in || ldg2 < n_out || !grad ||
+      !ZXb || !ZXt || !ZGb || !ZGt || !nat) {
+    set_error("precondition_apply_bf16: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  const size_t need = precondition_apply_b_min_ws(n_out, n_in);
+  const size_t room = ws_bytes > need + 256 ? (ws_bytes - need - 256) / sizeof(float) : 0;
+  Arena a(ws, ws_bytes);
+  void *T1, *T2;
+  bf16_t* cv;
+  SplitScratch sp;
+  plan_apply_b(a, n_out, n_in, &T1, &T2, &cv, &sp, room);
+  RC(check_ws(a, "precondition_apply_bf16"));
+  RC(launch_transpose_cast(s, grad, ldg, n_out, n_in, cv, DT_BF16, n_out));
+  return apply_core_b(s, cv, n_out, n_in, ZXb, ZXt, ldx2, ZGb, ZGt, ldg2, nat, ldn, T1, T2, sp);
 }
 
 static void plan_prec(Arena& a, int64_t n_out, int64_t n_in, int math, float** ZX, float** ZG,

@@ -144,7 +144,8 @@ __device__ inline float safe_divisor(float d) {
 // zeroed on exit).  mode 0: a pivot below tol * (its diagonal on entry, or
 // dref[i] for i < b when dref is given) or not finite raises *bad (the
 // factorisation continues on a clamped pivot so every thread runs the same
-// steps); mode 1: the pivot rule of cholesky_bf16, max(pivot, 1e-7).
+// steps); mode 1: the pivot rule of cholesky_bf16, clamp_min(pivot, 1e-7)
+// with a NaN pivot kept NaN.
 //
 // Right-looking, blocked by CB columns.  Wave 0 factors each CB-row panel
 // with lane c holding column c of the panel rows in registers: at step k
@@ -182,7 +183,9 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
           rs = __builtin_amdgcn_rsqf(pv);
           dg = pv * rs;
         } else {
-          dg = sqrtf(fmaxf(piv, 1e-7f));
+          // clamp_min(1e-7) of cholesky_bf16 (bf16_linalg.py:258): a NaN
+          // pivot stays NaN (fmaxf would return the bound)
+          dg = sqrtf((piv >= 1e-7f || piv != piv) ? piv : 1e-7f);
           rs = 1.0f / dg;
         }
         a[k] = (lane == o + k) ? dg : a[k] * rs;
@@ -636,7 +639,8 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
 
 // ---------------------------------------------------------------------------
 // Diagonal block of a blocked upper Cholesky (bf16_linalg.cholesky_bf16 pivot
-// rule, bf16_linalg.py:258-260): U_jj = sqrt(max(A_jj - sum_k U_kj^2, 1e-7)).
+// rule, bf16_linalg.py:258-260): U_jj = sqrt(clamp_min(A_jj - sum_k U_kj^2, 1e-7)),
+// a NaN pivot kept NaN.
 // In place on a b x b block at A (ld); only the upper triangle is read; on
 // exit the block holds U (strict lower part zeroed).
 // ---------------------------------------------------------------------------

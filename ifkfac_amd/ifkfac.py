@@ -211,9 +211,12 @@ class IFKFAC(torch.optim.Optimizer):
         return get_backend().precondition_apply(grad_w, Z_X, Z_G, solve_math_for(R_X.dtype))
 
     def _update_param(self, param: torch.Tensor, nat: torch.Tensor, lr: float, wd: float,
-                      mom: float, module: Optional[nn.Module]) -> None:
-        """Clip (if set), momentum (module given and mom > 0), decay, step."""
-        if self.grad_clip is not None:
+                      mom: float, module: Optional[nn.Module], clip: bool = False) -> None:
+        """Clip (``clip`` and grad_clip set), momentum (module given and mom > 0),
+        decay, step.  Only a weight's natural gradient is clipped
+        (ifkfac/ifkfac.py:397-400, 494-497); bias updates (:418-423, :515-519)
+        and the plain-SGD step of a layer without factors (:443-448) are not."""
+        if clip and self.grad_clip is not None:
             gnorm = nat.norm()
             if gnorm > self.grad_clip:
                 nat = nat * (self.grad_clip / gnorm)
@@ -237,7 +240,9 @@ class IFKFAC(torch.optim.Optimizer):
                 nat = buf
             if wd > 0:
                 W.mul_(1.0 - lr * wd)
-            W.add_(nat.to(W.dtype), alpha=-lr)
+            # one rounding to W's dtype, as torch's in-place add does for the
+            # reference's fp32 natural gradient (ifkfac/ifkfac.py:413)
+            W.add_(nat, alpha=-lr)
 
     def _update_bias(self, module: nn.Module, lr: float, wd: float) -> None:
         if module.bias is None or module.bias.grad is None:
@@ -282,7 +287,7 @@ class IFKFAC(torch.optim.Optimizer):
                     self._apply_preconditioner(m, lr=lr, weight_decay=wd, momentum=mom)
                 continue
             for (m, lr, wd, mom), nat in zip(entries, nats):
-                self._update_param(m.weight, nat, lr, wd, mom, m)
+                self._update_param(m.weight, nat, lr, wd, mom, m, clip=True)
                 self._update_bias(m, lr, wd)
 
     def _apply_preconditioner(self, module: nn.Module, lr: float, weight_decay: float,
@@ -306,7 +311,7 @@ class IFKFAC(torch.optim.Optimizer):
                            type(module).__name__, e)
             nat = grad_w
         nat = nat.reshape(orig_shape)
-        self._update_param(weight, nat, lr, weight_decay, momentum, module)
+        self._update_param(weight, nat, lr, weight_decay, momentum, module, clip=True)
         self._update_bias(module, lr, weight_decay)
 
     # ------------------------------------------------------------------ step

@@ -107,10 +107,10 @@ int ifk_fold_finalize(void* stream, const void* X, int x_dtype, int64_t p, int64
                       int32_t* finite, void* workspace, size_t workspace_bytes);
 
 /*
- * ifk_fold_finalize with each 512-column outer block of the TPQRT fold
+ * ifk_fold_finalize with each 1024-column outer block of the TPQRT fold
  * factored at once by CholeskyQR2 with Householder reconstruction, instead
  * of by its chain of 64-column panels: the block's work becomes a few large
- * MFMA products and 512 x 512 factorisations.  No counterpart in the
+ * MFMA products and 1024 x 1024 factorisations.  No counterpart in the
  * reference (its fold is torch.linalg.qr, ifkfac/triangular.py:284-301 and
  * :411-416); same arguments and result as ifk_fold_finalize, for callers
  * that can read a status flag before using the factor.  *status (device):

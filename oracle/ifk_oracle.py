@@ -18,10 +18,17 @@ torch.linalg on CPU).  How each function is pinned (tests/test_oracle.py):
                              and the recipe tests of tests/test_equivalence.py
   bf16_round                 hand-computed RNE ties, NaN/Inf, subnormals
   momentum_step              the recurrence unrolled by hand for 3 steps
-  bf16_linalg restatements   tolerance-level only: R vs chol(A^T A), L L^T vs A,
-                             R X vs B.  Bit-level parity: unpinned (the reference's
-                             bf16 matmul rounding and accumulation order are not
-                             fixed by any fixture the reference holds)
+  bf16_linalg restatements   R vs chol(A^T A), L L^T vs A, R X vs B at tolerance;
+                             the special cases by hand: _safe_div's signed
+                             magnitude clamp (|d| < 1e-7 -> sign(d) 1e-7, sign(0)
+                             = +1, NaN kept), cholesky_bf16's clamp_min(1e-7)
+                             pivot (singular and indefinite inputs, NaN kept),
+                             the zero-norm reflector skip and torch's sign(0) = 0
+                             in the reflector sign, each with a planted mistake
+                             the check rejects.  Bit-level parity of general
+                             inputs: unpinned (the reference's bf16 matmul
+                             rounding and accumulation order are not fixed by
+                             any fixture the reference holds)
 """
 from __future__ import annotations
 
@@ -249,8 +256,9 @@ def cholesky_bf16(A: np.ndarray) -> np.ndarray:
     L = np.zeros_like(A)
     for j in range(n):
         ss = np.float32((L[j, :j].astype(np.float32) ** 2).sum())
-        d = np.float32(max(np.float32(A[j, j]) - ss, np.float32(1e-7)))
-        d = np.float32(d)
+        piv = np.float32(np.float32(A[j, j]) - ss)
+        # torch's clamp_min(1e-7) (bf16_linalg.py:258): NaN stays NaN
+        d = piv if (np.isnan(piv) or piv >= np.float32(1e-7)) else np.float32(1e-7)
         L[j, j] = _b(np.sqrt(d))
         if j + 1 < n:
             below = A[j + 1:, j:j + 1]

@@ -690,6 +690,76 @@ def test_bf16_linalg_guards(hip):
         B.block_householder_qr_bf16(torch.randn(3, 5, device=DEV).bfloat16())
 
 
+@pytest.mark.parametrize("n", [8, 100])
+@pytest.mark.parametrize("upper", [True, False])
+@pytest.mark.parametrize("dv", [5e-8, -5e-8, 0.0, -0.0])
+def test_bf16_trsm_tiny_and_zero_diagonals(hip, n, upper, dv):
+    """solve_triangular_bf16 through the _safe_div clamp (bf16_linalg.py:44-59,
+    :233/:241): a diagonal entry below 1e-7 in magnitude divides by
+    sign(d) 1e-7, with sign(0) = +1 for 0 and -0.0.  One clamped pivot per
+    matrix (two make the solve too ill-conditioned for a forward error to
+    mean anything).  Against the oracle's substitution and against the fp64
+    solve with the clamped diagonal, at the bf16 bound of the general solve
+    test; n = 100 crosses the 64-block doubling of the inverse."""
+    from ifkfac_amd import bf16_linalg as B
+    rng = np.random.default_rng(n + (0 if upper else 1))
+    R = np.triu(rng.standard_normal((n, n)) * 0.1).astype(np.float32)
+    d = rng.choice([2.0, -1.5, 1.0, 3.0], n).astype(np.float32)
+    d[n // 2] = dv
+    np.fill_diagonal(R, d)
+    R = O.bf16_round(R)
+    if not upper:
+        R = np.ascontiguousarray(R.T)
+    Bm = O.bf16_round(rng.standard_normal((n, 3)).astype(np.float32))
+    X = B.solve_triangular_bf16(torch.tensor(R, device=DEV).bfloat16(),
+                                torch.tensor(Bm, device=DEV).bfloat16(), upper=upper)
+    Xo = O.solve_triangular_bf16(R, Bm, upper=upper)
+    Rc = R.astype(np.float64)
+    Rc[n // 2, n // 2] = -1e-7 if dv < 0 else 1e-7       # -0.0 < 0 is False: +1e-7
+    Xt = np.linalg.solve(Rc, Bm.astype(np.float64))
+    assert bool(torch.isfinite(X).all())
+    assert _rel(X, Xt) < 2e-2
+    assert _rel(X, Xo.astype(np.float64)) < 2e-2
+    # the clamped row carries the divisor's sign (1e7 scale): signs as the oracle's
+    Xg = X.double().cpu().numpy()
+    assert np.array_equal(np.sign(Xg[n // 2]), np.sign(Xo[n // 2].astype(np.float64)))
+    assert np.abs(Xg[n // 2]).max() > 1e5
+
+
+def test_bf16_cholesky_pivot_clamp_cases(hip):
+    """cholesky_bf16's pivot rule (bf16_linalg.py:258-260) on the oracle's hand
+    cases: singular (rank 1) and indefinite inputs clamp at 1e-7 and match the
+    oracle bit for bit; a NaN pivot propagates (clamp_min keeps NaN); a larger
+    block-diagonal input with a rank-deficient part (n = 100, two 64-blocks)
+    matches it to the bf16 bound."""
+    from ifkfac_amd import bf16_linalg as B
+    u = np.array([1.0, 2.0, -3.0, 1.0], np.float32)
+    cases = [np.outer(u, u),
+             np.array([[4.0, 2.0, 0.0], [2.0, -3.0, 0.0], [0.0, 0.0, 9.0]], np.float32),
+             np.ones((40, 40), np.float32)]
+    for A in cases:
+        L = B.cholesky_bf16(torch.tensor(A, device=DEV).bfloat16()).float().cpu().numpy()
+        assert np.array_equal(L, O.cholesky_bf16(A)), A.shape
+    A = np.eye(8, dtype=np.float32)
+    A[0, 0] = np.nan
+    L = B.cholesky_bf16(torch.tensor(A, device=DEV).bfloat16()).float().cpu().numpy()
+    assert np.isnan(L[np.tril_indices(8)]).all() and not np.any(np.triu(L, 1))
+    rng = np.random.default_rng(9)
+    n, k = 100, 40
+    A = np.zeros((n, n), np.float32)
+    v = rng.integers(-2, 3, k).astype(np.float32)
+    v[0] = 1.0
+    A[:k, :k] = np.outer(v, v)                      # rank 1: clamped pivots
+    Z = rng.standard_normal((2 * (n - k), n - k)).astype(np.float32)
+    A[k:, k:] = O.bf16_round(Z.T @ Z / (n - k) + np.eye(n - k, dtype=np.float32))
+    L = B.cholesky_bf16(torch.tensor(A, device=DEV).bfloat16()).float().cpu().numpy()
+    Lo = O.cholesky_bf16(A)
+    assert np.all(np.isfinite(L))
+    assert np.linalg.norm(L - Lo) / np.linalg.norm(Lo) < 2e-2
+    r = float(O.bf16_round(np.array([math.sqrt(1e-7)], np.float32))[0])
+    assert np.array_equal(np.diag(L)[1:k], np.full(k - 1, r, np.float32))
+
+
 # --------------------------------------------------------------------------- full sizes
 
 

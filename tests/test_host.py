@@ -162,6 +162,60 @@ def test_grad_clip_scales_natural_gradient(be):
         assert step == pytest.approx(1e-3, rel=1e-4)
 
 
+def test_grad_clip_only_clips_the_weight_natural_gradient(be):
+    """grad_clip scales a weight's natural gradient only (ifkfac/ifkfac.py:397-400,
+    494-497); bias updates (:418-423, :515-519) and the plain-SGD step of a layer
+    without factors (:443-448) are never clipped.  With factor_update_freq=2,
+    step 1 has no factors (plain SGD on the weight, bias untouched) and step 2
+    builds them from both steps' rows: its weight step has norm lr * grad_clip and
+    its bias step is the oracle's unclipped G^-1 g_b."""
+    from ifkfac_amd import IFKFAC
+    torch.manual_seed(0)
+    layer = nn.Linear(8, 4, bias=True)
+    model = nn.Sequential(layer)
+    lr, lam, clip = 0.5, 1e-2, 1e-3
+    opt = IFKFAC(model, lr=lr, damping=lam, factor_update_freq=2, momentum=0.0, grad_clip=clip)
+    g = torch.Generator().manual_seed(1)
+    deltas = []
+    for step, X in enumerate([torch.randn(64, 8, generator=g), torch.randn(64, 8, generator=g)]):
+        acts, grads, hs = _capture(model, X)
+        W, b = layer.weight.detach().clone(), layer.bias.detach().clone()
+        opt.zero_grad()
+        model(X).pow(2).mean().backward()
+        gW, gb = layer.weight.grad.clone(), layer.bias.grad.clone()
+        for h in hs:
+            h.remove()
+        deltas.append(grads[layer].double().numpy())
+        opt.step()
+        if step == 0:   # no factors: plain SGD, unclipped, bias untouched
+            assert torch.allclose(layer.weight.detach(), W - lr * gW, atol=1e-7)
+            assert (lr * gW).norm().item() > 10 * clip
+            assert torch.equal(layer.bias.detach(), b)
+    step_w = (layer.weight.detach() - W).norm().item()
+    assert step_w == pytest.approx(lr * clip, rel=1e-4)       # the weight step is clipped
+    d = np.vstack(deltas)
+    R_G = O.get_factor(O.streaming_tsqr_update(None, d), d.shape[0], lam)
+    want_b = b.double().numpy() - lr * O.apply_vered_bias(gb.double().numpy(), R_G)
+    assert np.abs(layer.bias.detach().double().numpy() - want_b).max() < 1e-6
+    assert (layer.bias.detach() - b).norm().item() > 10 * clip  # and the bias step is not
+
+
+def test_weight_step_rounds_once_for_bf16_parameters(be):
+    """A non-fp32 weight takes W.add_(nat, alpha=-lr) with the fp32 natural
+    gradient: one rounding to bf16, as torch does for the reference's update
+    (ifkfac/ifkfac.py:413), not a cast of nat to bf16 first."""
+    from ifkfac_amd import IFKFAC
+    layer = nn.Linear(8, 4, bias=False)
+    opt = IFKFAC(nn.Sequential(layer), lr=0.3, factor_update_freq=1, momentum=0.0)
+    layer.weight.data = torch.zeros(4, 8, dtype=torch.bfloat16)
+    nat = torch.full((4, 8), 1.0 + 3 * 2 ** -9)        # not a bf16 value
+    opt._update_param(layer.weight, nat, 0.3, 0.0, 0.0, None)
+    want = torch.zeros(4, 8, dtype=torch.bfloat16).add_(nat, alpha=-0.3)
+    twice = torch.zeros(4, 8, dtype=torch.bfloat16).add_(nat.bfloat16(), alpha=-0.3)
+    assert torch.equal(layer.weight.detach(), want)
+    assert not torch.equal(want, twice)                  # the check tells the two apart
+
+
 def test_capture_controls(be):
     from ifkfac_amd import IFKFAC
     model = _mlp()

@@ -259,3 +259,154 @@ def test_kappa_matrix_condition():
     X = O.kappa_matrix(512, 256, 100.0, rng)
     s = np.linalg.svd(X, compute_uv=False)
     assert abs(s[0] - 1.0) < 1e-10 and abs(s[-1] - 0.01) < 1e-12
+
+
+# --------------------------------------------------------------------------- bf16_linalg special cases
+#
+# The clamps and skips of bf16_linalg.py (_safe_div :44-59, cholesky_bf16's
+# clamp_min(1e-7) pivot :258-260, the zero-norm reflector of the Householder
+# QRs :117-121 / :175-176) computed by hand, each with a planted mistake the
+# same check must reject.
+
+EPS_DIV = np.float32(1e-7)
+
+
+def _bad_div_unsigned(num, denom, eps=1e-7):
+    """Planted mistake: a value clamp |d| -> eps that loses the sign."""
+    d = np.float32(np.asarray(denom).reshape(()))
+    safe = np.float32(eps) if abs(d) < eps else d
+    return O._b(np.asarray(num, np.float32) / np.float32(safe))
+
+
+def _bad_div_sign0(num, denom, eps=1e-7):
+    """Planted mistake: sign(0) = 0, so a zero divisor stays zero."""
+    d = np.float32(np.asarray(denom).reshape(()))
+    safe = np.sign(d) * np.float32(eps) if abs(d) < eps else d
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return O._b(np.asarray(num, np.float32) / np.float32(safe))
+
+
+def test_safe_div_hand_cases():
+    one = np.array([1.0], np.float32)
+    cases = [
+        (5e-8, 1e7),          # |d| < eps, positive: divide by +eps
+        (-5e-8, -1e7),        # |d| < eps, negative: divide by -eps (sign kept)
+        (0.0, 1e7),           # sign(0) -> +1: divide by +eps
+        (-0.0, 1e7),          # -0.0 == 0 as well: +eps
+        (1e-7, 1e7),          # |d| == eps is not clamped (and divides alike)
+        (2.0, 0.5),           # ordinary divisor
+        (-4.0, -0.25),
+    ]
+    for d, want in cases:
+        got = float(O._safe_div(one, np.float32(d))[0])
+        assert got == float(O.bf16_round(np.array([want], np.float32))[0]), (d, got)
+    assert np.isnan(O._safe_div(one, np.float32(np.nan))[0])   # NaN divisor propagates
+    # the checks reject an unsigned clamp and a sign(0) = 0 clamp
+    assert float(_bad_div_unsigned(one, np.float32(-5e-8))[0]) > 0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        assert not np.isfinite(_bad_div_sign0(one, np.float32(0.0))[0])
+
+
+def _bad_chol_clamp0(A):
+    """Planted mistake: the pivot clamped at 0 instead of 1e-7."""
+    A = O._b(A)
+    n = A.shape[0]
+    L = np.zeros_like(A)
+    for j in range(n):
+        ss = np.float32((L[j, :j].astype(np.float32) ** 2).sum())
+        L[j, j] = O._b(np.sqrt(np.float32(max(np.float32(A[j, j]) - ss, np.float32(0.0)))))
+        if j + 1 < n:
+            head = O._mm(L[j + 1:, :j], L[j:j + 1, :j].T)
+            with np.errstate(divide="ignore", invalid="ignore"):
+                L[j + 1:, j:j + 1] = O._b((O._b(A[j + 1:, j:j + 1] - head)) / L[j, j])
+    return L
+
+
+def test_cholesky_bf16_pivot_clamp_hand_cases():
+    r = float(O.bf16_round(np.array([math.sqrt(1e-7)], np.float32))[0])   # bf16(sqrt(1e-7))
+    # singular (rank 1): every pivot after the first is 0 -> sqrt(1e-7), and the
+    # columns below them are exactly 0
+    u = np.array([1.0, 2.0, -3.0, 1.0], np.float32)
+    L = O.cholesky_bf16(np.outer(u, u))
+    want = np.diag([1.0, r, r, r]).astype(np.float32)
+    want[:, 0] = u
+    assert np.array_equal(L, want)
+    # indefinite: a negative pivot is clamped, later pivots are exact
+    L = O.cholesky_bf16(np.array([[4.0, 2.0, 0.0], [2.0, -3.0, 0.0], [0.0, 0.0, 9.0]], np.float32))
+    assert np.array_equal(L, np.array([[2.0, 0, 0], [1.0, r, 0], [0, 0, 3.0]], np.float32))
+    # a NaN pivot propagates (torch's clamp_min keeps NaN) through everything below it
+    A = np.eye(3, dtype=np.float32)
+    A[0, 0] = np.nan
+    L = O.cholesky_bf16(A)
+    assert np.isnan(L[np.tril_indices(3)]).all()
+    # the planted clamp-at-zero gives a zero pivot, which the hand case rejects
+    with np.errstate(divide="ignore", invalid="ignore"):
+        bad = _bad_chol_clamp0(np.outer(u, u))
+    assert not np.array_equal(bad, want)
+
+
+def test_householder_qr_bf16_zero_and_sign_cases():
+    # a column that is zero from the diagonal down: zero-norm reflector, skipped
+    A = np.array([[1.0, 0.0], [0.0, 0.0], [0.0, 0.0]], np.float32)
+    R = O.householder_qr_bf16(A)
+    assert np.array_equal(R, np.array([[-1.0, 0.0], [0.0, 0.0]], np.float32))
+    # the reflector sign is -sign(x0) with torch's sign(0) = 0: a column whose
+    # leading entry is exactly 0 gets alpha = 0, and v = x / ||x|| reflects x to
+    # -x instead of onto e1, so R's diagonal entry stays 0
+    A = np.array([[0.0, 1.0], [3.0, 1.0], [4.0, 1.0]], np.float32)
+    R = O.householder_qr_bf16(A)
+    assert R[0, 0] == 0.0 and R[0, 1] == 1.0
+    assert abs(abs(float(R[1, 1])) - math.sqrt(0.68 ** 2 + 1.24 ** 2)) < 2e-2
+
+    # planted mistake: sign(0) taken as +1 (the LAPACK convention) gives -5 there
+    def qr_sign_plus(A):
+        A = O._b(A).copy()
+        m, n = A.shape
+        for i in range(n):
+            x = A[i:, i:i + 1]
+            s = 1.0 if x[0, 0] >= 0 else -1.0
+            alpha = -s * O._safe_norm(x)
+            v = x.copy()
+            v[0, 0] = O._b(v[0, 0] - alpha)
+            vn = O._safe_norm(v)
+            if vn == 0.0:
+                continue
+            v = O._safe_div(v, vn)
+            blk = A[i:, i:]
+            A[i:, i:] = O._b(blk - O._b(2.0 * O._mm(v, O._mm(v.T, blk))))
+        return np.triu(A[:n, :n])
+    assert qr_sign_plus(A)[0, 0] == -5.0
+
+    # planted mistake: no zero-norm skip (v / 0) poisons the factor
+    def qr_no_skip(A):
+        A = O._b(A).copy()
+        m, n = A.shape
+        for i in range(n):
+            x = A[i:, i:i + 1]
+            alpha = -np.sign(x[0, 0]) * O._safe_norm(x)
+            v = x.copy()
+            v[0, 0] = O._b(v[0, 0] - alpha)
+            with np.errstate(divide="ignore", invalid="ignore"):
+                v = O._b(v / O._safe_norm(v))
+                blk = A[i:, i:]
+                A[i:, i:] = O._b(blk - O._b(2.0 * O._mm(v, O._mm(v.T, blk))))
+        return np.triu(A[:n, :n])
+    with np.errstate(invalid="ignore"):
+        assert not np.isfinite(qr_no_skip(np.array([[1.0, 0.0], [0.0, 0.0], [0.0, 0.0]],
+                                                  np.float32))).all()
+
+
+def test_solve_triangular_bf16_tiny_and_zero_diagonals():
+    """Back and forward substitution through the _safe_div clamp, by hand."""
+    R = np.array([[2.0, 1.0], [0.0, 5e-8]], np.float32)
+    X = O.solve_triangular_bf16(R, np.array([[1.0], [1.0]], np.float32), upper=True)
+    x1 = float(O.bf16_round(np.array([1e7], np.float32))[0])
+    assert X[1, 0] == x1
+    assert X[0, 0] == float(O.bf16_round(np.array([(1.0 - x1) / 2.0], np.float32))[0])
+    Rn = np.array([[2.0, 1.0], [0.0, -5e-8]], np.float32)   # sign kept
+    assert O.solve_triangular_bf16(Rn, np.array([[1.0], [1.0]], np.float32))[1, 0] == -x1
+    Rz = np.array([[0.0, 0.0], [3.0, 4.0]], np.float32)     # lower, zero pivot -> +1e-7
+    X = O.solve_triangular_bf16(Rz, np.array([[1.0], [2.0]], np.float32), upper=False)
+    assert X[0, 0] == x1
+    # the unsigned-clamp mistake flips the sign of the negative case
+    assert float(_bad_div_unsigned(np.array([1.0], np.float32), np.float32(-5e-8))[0]) == x1
