@@ -64,6 +64,9 @@ SIGNATURES = {
     "ifk_precondition_apply_bf16": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
                                              _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp,
                                              _c_sz]),
+    "ifk_precondition_apply_bf16_noalloc": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp,
+                                                     _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp,
+                                                     _c_i64]),
     "ifk_precondition_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_int]),
     "ifk_precondition": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                   _c_i64, _c_int, _c_vp, _c_i64, _c_int, _c_vp, _c_sz]),

@@ -176,6 +176,24 @@ int ifk_precondition_apply_bf16(void* stream, const float* grad, int64_t n_out, 
                                 int64_t ldn, void* workspace, size_t workspace_bytes);
 
 /*
+ * ifk_precondition_apply_bf16 without a workspace argument: its scratch is a
+ * 64 MiB device array inside this library (one per GPU, held until the
+ * process ends), so the call allocates nothing.  No counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and result as ifk_precondition_apply_bf16, bit for bit while the
+ * array also has room for that entry's split-K scratch.  Limit: the three bf16
+ * n_out x n_in intermediates must fit in the array (n_out * n_in up to about
+ * 11.18 million; larger calls return IFK_ERR_INVALID).  The stream's device
+ * must be the current device.  All calls on one GPU share the array: calls
+ * that overlap on one GPU (other streams, other threads) race.
+ */
+int ifk_precondition_apply_bf16_noalloc(void* stream, const float* grad, int64_t n_out,
+                                        int64_t n_in, int64_t ldg, const void* Z_Xb,
+                                        const void* Z_Xt, int64_t ldzx, const void* Z_Gb,
+                                        const void* Z_Gt, int64_t ldzg, float* nat, int64_t ldn);
+
+/*
  * Bias preconditioning -- replaces apply_vered_bias(grad_b, R_G)
  * (ifkfac/triangular.py:659-705): out = (R_G^T R_G)^{-1} g, given Z_G.
  */
