@@ -177,6 +177,22 @@ class HipBackend:
         _lib.check(rc, "ifk_tri_inverse_bf16")
         return Z, Zb, ZT
 
+    def cond_estimate(self, R: torch.Tensor, Z: torch.Tensor) -> torch.Tensor:
+        """kappa_2(R) estimate from R and its fp32 inverse Z, as a device float[1]
+        (read it with the factor flags, after the stream has progressed)."""
+        R, ldr, rdt = _mat(R, "cond_estimate")
+        Zc, ldz, zdt = _mat(Z, "cond_estimate")
+        n = R.shape[0]
+        if R.shape != (n, n) or Zc.shape != (n, n) or zdt != IFK_F32:
+            raise IFKFACBackendError("cond_estimate: R and Z must be n x n, Z fp32")
+        out = torch.empty(1, dtype=torch.float32, device=R.device)
+        ws = self._ws(self.lib.ifk_cond_estimate_workspace_size(n), R.device)
+        with torch.cuda.device(R.device):
+            rc = self.lib.ifk_cond_estimate(self._stream(R.device), _ptr(R), rdt, ldr, _ptr(Zc),
+                                            ldz, n, _ptr(out), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_cond_estimate")
+        return out
+
     def precondition_apply_bf16(self, grad: torch.Tensor, ZX2, ZG2) -> torch.Tensor:
         """precondition_apply in bf16 arithmetic from (Z_X, Z_X^T), (Z_G, Z_G^T)
         bf16 copies of tri_inverse_bf16 (views of them, e.g. trimmed, allowed)."""

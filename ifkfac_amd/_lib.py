@@ -60,6 +60,9 @@ SIGNATURES = {
     "ifk_tri_inverse_bf16_workspace_size": (_c_sz, [_c_i64]),
     "ifk_tri_inverse_bf16": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                       _c_vp, _c_i64, _c_vp, _c_sz]),
+    "ifk_cond_estimate_workspace_size": (_c_sz, [_c_i64]),
+    "ifk_cond_estimate": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp,
+                                   _c_vp, _c_sz]),
     "ifk_precondition_apply_bf16_workspace_size": (_c_sz, [_c_i64, _c_i64]),
     "ifk_precondition_apply_bf16": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
                                              _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp,

@@ -128,6 +128,19 @@ int ifk_tri_inverse_bf16(void* stream, const void* R, int r_dtype, int64_t ldr, 
                       ldb, workspace, workspace_bytes);
 }
 
+size_t ifk_cond_estimate_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return cond_est_ws(n);
+}
+
+int ifk_cond_estimate(void* stream, const void* R, int r_dtype, int64_t ldr, const float* Z,
+                      int64_t ldz, int64_t n, float* kappa, void* workspace,
+                      size_t workspace_bytes) {
+  GUARD(dt_ok(r_dtype), "cond_estimate: bad dtype code");
+  return cond_est((hipStream_t)stream, R, r_dtype, ldr, Z, ldz, n, kappa, workspace,
+                  workspace_bytes);
+}
+
 size_t ifk_precondition_apply_bf16_workspace_size(int64_t n_out, int64_t n_in) {
   if (n_out < 1 || n_in < 1) return 0;
   return precondition_apply_b_ws(n_out, n_in);

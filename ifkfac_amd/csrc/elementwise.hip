@@ -539,4 +539,77 @@ int launch_add_diag(hipStream_t s, float* A, int64_t lda, int64_t n, float v) {
   return check_launch("add_diag");
 }
 
+
+// ---------------------------------------------------------------------------
+// Power-iteration helpers of the condition estimate (linalg.hip: cond_est).
+// ---------------------------------------------------------------------------
+
+// V (n x k, row-major) <- deterministic probe vectors: hashed values in
+// [-1, 1), column 0 shifted by +1 so that it overlaps a dominant direction
+// with all-positive weights (the mean of a layer's activations).
+__global__ void probe_init_kernel(float* V, int64_t n, int k) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n * k;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t h = (uint32_t)e * 2654435761u + 0x9e3779b9u;
+    h ^= h >> 16;
+    h *= 0x85ebca6bu;
+    h ^= h >> 13;
+    h *= 0xc2b2ae35u;
+    h ^= h >> 16;
+    const float u = (float)(h >> 8) * (1.0f / 8388608.0f) - 1.0f;
+    V[e] = u + ((e % k) == 0 ? 1.0f : 0.0f);
+  }
+}
+
+// Column j of V (n x k) scaled to unit norm (left alone if zero or not
+// finite); its sum of squares before scaling into ss[j].  One workgroup per
+// column.
+__global__ __launch_bounds__(256) void colnorm_kernel(float* V, int64_t n, int k, float* ss) {
+  __shared__ float red[256];
+  const int j = blockIdx.x;
+  float acc = 0.0f;
+  for (int64_t i = threadIdx.x; i < n; i += 256) {
+    const float v = V[i * k + j];
+    acc = fmaf(v, v, acc);
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  const float tot = red[0];
+  if (threadIdx.x == 0) ss[j] = tot;
+  if (!(tot > 0.0f) || !isfinite(tot)) return;
+  const float sc = 1.0f / sqrtf(tot);
+  for (int64_t i = threadIdx.x; i < n; i += 256) V[i * k + j] *= sc;
+}
+
+// kappa = (max_j ssa[j] * max_j ssb[j])^(1/4): each max is the squared norm
+// of M^T M v for a unit v, about sigma_max(M)^4.
+__global__ void cond_final_kernel(const float* ssa, const float* ssb, int k, float* kappa) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float a = 0.0f, b = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    a = fmaxf(a, ssa[j]);
+    b = fmaxf(b, ssb[j]);
+  }
+  *kappa = sqrtf(sqrtf(a) * sqrtf(b));
+}
+
+int launch_probe_init(hipStream_t s, float* V, int64_t n, int k) {
+  hipLaunchKernelGGL(probe_init_kernel, dim3(grid_for(n * k)), dim3(256), 0, s, V, n, k);
+  return check_launch("probe_init");
+}
+
+int launch_colnorm(hipStream_t s, float* V, int64_t n, int k, float* ss) {
+  hipLaunchKernelGGL(colnorm_kernel, dim3((unsigned)k), dim3(256), 0, s, V, n, k, ss);
+  return check_launch("colnorm");
+}
+
+int launch_cond_final(hipStream_t s, const float* ssa, const float* ssb, int k, float* kappa) {
+  hipLaunchKernelGGL(cond_final_kernel, dim3(1), dim3(64), 0, s, ssa, ssb, k, kappa);
+  return check_launch("cond_final");
+}
+
 }  // namespace ifk

@@ -165,6 +165,10 @@ int launch_transpose_bf16(hipStream_t s, const bf16_t* src, int64_t lds, int64_t
                           int64_t cols, bf16_t* dst, int64_t ldd);
 // A[i][i] += v, i < n
 int launch_add_diag(hipStream_t s, float* A, int64_t lda, int64_t n, float v);
+// condition-estimate helpers (elementwise.hip)
+int launch_probe_init(hipStream_t s, float* V, int64_t n, int k);
+int launch_colnorm(hipStream_t s, float* V, int64_t n, int k, float* ss);
+int launch_cond_final(hipStream_t s, const float* ssa, const float* ssb, int k, float* kappa);
 // out (dt) = alpha * x (fp32) with optional bf16 output
 int launch_scale_copy_vec(hipStream_t s, const float* x, int64_t n, float alpha, void* out, int odt);
 

@@ -49,6 +49,12 @@ size_t trinv_copies_ws(int64_t n);
 int trinv_copies(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
                  int64_t ldz, bf16_t* Zb, bf16_t* ZTb, int64_t ldb, void* ws, size_t ws_bytes);
 
+// kappa_2 estimate of an upper-triangular R from R and Z = R^{-1} (device
+// float out).
+size_t cond_est_ws(int64_t n);
+int cond_est(hipStream_t s, const void* R, int rdt, int64_t ldr, const float* Z, int64_t ldz,
+             int64_t n, float* kappa, void* ws, size_t ws_bytes);
+
 // nat as precondition_apply in bf16 arithmetic, from the copies of
 // trinv_copies (nothing to cast but grad).
 size_t precondition_apply_b_min_ws(int64_t n_out, int64_t n_in);

@@ -155,7 +155,7 @@ __device__ inline float safe_divisor(float d) {
 // trailing update runs on fp32 MFMA across the four waves.  Two barriers per
 // panel.  CB = 32 measured fastest (the pivot chain, not the FMA count,
 // bounds a panel, so fewer panels and barriers win).
-template <int CB = 32>
+template <int CB = 32, bool EXACT = false>
 __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode,
                                           const float* dref = nullptr, int b = SB) {
   const int t = threadIdx.x;
@@ -180,8 +180,16 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
         if (mode == 0) {
           if (!(piv > tol * dgs[o + k]) || !isfinite(piv)) flag = 1;
           const float pv = fmaxf(piv, 1e-30f);
-          rs = __builtin_amdgcn_rsqf(pv);
-          dg = pv * rs;
+          if (EXACT) {
+            // correctly rounded: a first pass whose second pass cannot carry
+            // a sub-ulp correction must not add a biased one (v_rsq_f32's
+            // error is systematic, and a stream of folds compounds it)
+            dg = sqrtf(pv);
+            rs = 1.0f / dg;
+          } else {
+            rs = __builtin_amdgcn_rsqf(pv);
+            dg = pv * rs;
+          }
         } else {
           // clamp_min(1e-7) of cholesky_bf16 (bf16_linalg.py:258): a NaN
           // pivot stays NaN (fmaxf would return the bound)
@@ -483,7 +491,7 @@ __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
     __syncthreads();
   }
   sm_gemm64<true, false>(sP, sP, sG, 1.0f, true);  // sG = X_p^T X_p + P_top^T P_top
-  sm_chol64(sG, tol, &bad, 0);                     // sG = U1
+  sm_chol64<32, true>(sG, tol, &bad, 0);           // sG = U1
   sm_store(sG, U1, b, b);
   sm_trinv64(sG, sM, sT);                          // sM = M1
   sm_store(sM, M1, b, b);
@@ -543,6 +551,8 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
     }
   }
   const bool flagged = (*flag != 0);
+  bool near = false;
+  float vF[PAD_PER];
   st_pad(sG, vG);
   __syncthreads();
   if (flagged) {
@@ -573,8 +583,18 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
     sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
     // after the first pass sG is I + E with E small: a few MFMA sweeps give U2
     // and M2; the general Cholesky / inverse are the fallback
-    const bool near = sm_chol_near_id(sG, sX, sM, sgn, 8);   // sG = U2
-    if (!near) sm_chol64(sG, 0.25f, &bad, 0);
+    near = sm_chol_near_id(sG, sX, sM, sgn, 8);   // sG = U2
+    if (near) {
+      // F = U2 - I exactly as the sweeps left it: U2 itself, rounded next to
+      // 1, drops corrections below half an ulp of 1
+#pragma unroll
+      for (int q = 0; q < PAD_PER; ++q) {
+        const int e = t + SNT * q;
+        vF[q] = sX[(e >> 6) * SLD + (e & 63)];
+      }
+    } else {
+      sm_chol64(sG, 0.25f, &bad, 0);
+    }
     if (!(near && sm_inv_near_id(sG, sM, sX, sN, sgn, 8)))   // sM = M2
       sm_trinv64(sG, sM, sTmp);
     sm_gemm64<false, false>(sQ, sM, sX, 1.0f, false);  // sX = Q1f = Q1 M2
@@ -610,9 +630,21 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
     if (flagged) return;
     const bool ok = (bad == 0);
     st_pad(sM, vX);
+    const float nan = __int_as_float(0x7fc00000);
+    if (near) {
+      // R_new = S (U1 + F U1), with U2 = I + F
+      st_pad(sG, vF);
+      __syncthreads();
+      sm_gemm64<false, false>(sG, sM, sX, 1.0f, false);  // sX = F U1
+      for (int e = t; e < b * b; e += SNT) {
+        const int i = e / b, j = e - i * b;
+        R[(int64_t)i * ldr + j] =
+            !ok ? nan : ((i <= j) ? sgn[i] * (sM[i * SLD + j] + sX[i * SLD + j]) : 0.0f);
+      }
+      return;
+    }
     __syncthreads();
     sm_gemm64<false, false>(sG, sM, sM, 1.0f, false);  // sM = U2 U1
-    const float nan = __int_as_float(0x7fc00000);
     for (int e = t; e < b * b; e += SNT) {           // R_new = S U2 U1
       const int i = e / b, j = e - i * b;
       R[(int64_t)i * ldr + j] = !ok ? nan : ((i <= j) ? sgn[i] * sM[i * SLD + j] : 0.0f);

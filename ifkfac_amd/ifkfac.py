@@ -12,6 +12,10 @@ the G factor only).  What changes is where the arithmetic happens:
 * after each refresh the factor inverses ``Z = R^{-1}`` are formed once
   (``ifk_tri_inverse``) and every step applies the four solves as MFMA
   products with them (``ifk_precondition_apply``);
+* bf16 mode runs a layer's inverses and solves in bf16 arithmetic while both
+  of its factors are near-isotropic (kappa_2 estimate from
+  ``ifk_cond_estimate`` at most KAPPA_BF16_MAX), and in fp32 arithmetic on the
+  bf16-valued factors, the reference's regime, otherwise;
 * momentum, decay and the weight step are one fused pass
   (``ifk_momentum_update``).
 """
@@ -33,6 +37,16 @@ from .activation_hooks import IFKFACRankError, RawActivationHooks
 from .triangular import solve_math_for
 
 logger = logging.getLogger(__name__)
+
+# bf16 mode: a layer keeps bf16 arithmetic for its solves while both of its
+# factors have kappa_2(R) <= KAPPA_BF16_MAX; otherwise its inverses and applies
+# run in fp32 arithmetic on the bf16-valued factors, as the reference's bf16
+# mode does (ifkfac/triangular.py:621-628).  The bf16 products' rounding is
+# amplified by kappa(A) kappa(G) = kappa(R_X)^2 kappa(R_G)^2 for a gradient
+# aligned with the factors' dominant directions (as a layer's gradient is):
+# measured 5e-3 against fp64 solves of the same factors at kappa 1, 1.4e-2 to
+# 3e-2 at kappa 3.1-3.2, while the fp32 arithmetic stays near 6e-6.
+KAPPA_BF16_MAX = 1.5
 
 
 class IFKFAC(torch.optim.Optimizer):
@@ -94,6 +108,10 @@ class IFKFAC(torch.optim.Optimizer):
         self._inverses: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         # bf16 arithmetic: RNE bf16 copies ((Z_X, Z_X^T), (Z_G, Z_G^T)) per layer
         self._inverse_copies: Dict[nn.Module, tuple] = {}
+        # per layer: MFMA arithmetic of its solves, and the kappa_2 estimates
+        # (R_X, R_G) that chose it (bf16 mode)
+        self._solve_math: Dict[nn.Module, int] = {}
+        self._kappas: Dict[nn.Module, Tuple[float, float]] = {}
         self._classic_fallback: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._momentum_buffers: Dict[nn.Module, torch.Tensor] = {}
         self._step_count = 0
@@ -130,8 +148,10 @@ class IFKFAC(torch.optim.Optimizer):
             m = solve_math_for(R.dtype)
             if m == MATH_BF16 and copies:
                 # bf16 arithmetic: keep the bf16 copies of Z and Z^T next to Z,
-                # so the per-step apply does not cast the inverses again
-                return be.tri_inverse_bf16(R)
+                # so the per-step apply does not cast the inverses again, and
+                # estimate kappa_2(R) for the choice of arithmetic
+                Z, Zb, ZT = be.tri_inverse_bf16(R)
+                return Z, Zb, ZT, be.cond_estimate(R, Z)
             return be.tri_inverse(R, m)
 
         try:
@@ -176,18 +196,41 @@ class IFKFAC(torch.optim.Optimizer):
         self._factors = clean
         self._inverses = {}
         self._inverse_copies = {}
+        self._solve_math = {}
+        self._kappas = {}
+        invs = {}
         for module, (R_X, R_G) in clean.items():
             if early is not None:
-                invX, invG = early[module]
+                invs[module] = early[module]
             else:
-                invX, invG = run_pair(R_X.device, lambda R=R_X: inverse("X", module, R),
-                                      lambda R=R_G: inverse("G", module, R),
-                                      b_first=R_G.shape[0] > R_X.shape[0])
-            if isinstance(invX, tuple):
+                invs[module] = run_pair(R_X.device, lambda R=R_X: inverse("X", module, R),
+                                        lambda R=R_G: inverse("G", module, R),
+                                        b_first=R_G.shape[0] > R_X.shape[0])
+        # one host read of every kappa estimate (the flags were read above)
+        bf = [m for m, (iX, _) in invs.items() if isinstance(iX, tuple)]
+        kap = torch.cat([torch.cat([invs[m][0][3], invs[m][1][3]]) for m in bf]).view(-1, 2).cpu() \
+            if bf else None
+        for module, (invX, invG) in invs.items():
+            R_X, R_G = clean[module]
+            if not isinstance(invX, tuple):
+                self._inverses[module] = (invX, invG)
+                self._solve_math[module] = solve_math_for(R_X.dtype)
+                continue
+            kx, kg = (float(v) for v in kap[bf.index(module)])
+            self._kappas[module] = (kx, kg)
+            if kx <= KAPPA_BF16_MAX and kg <= KAPPA_BF16_MAX:
                 self._inverses[module] = (invX[0], invG[0])
                 self._inverse_copies[module] = ((invX[1], invX[2]), (invG[1], invG[2]))
+                self._solve_math[module] = MATH_BF16
             else:
-                self._inverses[module] = (invX, invG)
+                # fp32 arithmetic on the bf16-valued factors (the reference's regime)
+                logger.debug("IFKFAC: kappa(R_X) %.3g, kappa(R_G) %.3g: fp32 solves for %s",
+                             kx, kg, type(module).__name__)
+                self._inverses[module] = run_pair(
+                    R_X.device, lambda R=R_X: be.tri_inverse(R, MATH_F32),
+                    lambda R=R_G: be.tri_inverse(R, MATH_F32),
+                    b_first=R_G.shape[0] > R_X.shape[0])
+                self._solve_math[module] = MATH_F32
         self.timing["factor_compute"].append(time.perf_counter() - t0)
 
     # ------------------------------------------------------------------ apply
@@ -208,7 +251,8 @@ class IFKFAC(torch.optim.Optimizer):
         if trim:
             Z_X = Z_X[:-1, :-1]
         R_X = self._factors[module][0]
-        return get_backend().precondition_apply(grad_w, Z_X, Z_G, solve_math_for(R_X.dtype))
+        m = self._solve_math.get(module, solve_math_for(R_X.dtype))
+        return get_backend().precondition_apply(grad_w, Z_X, Z_G, m)
 
     def _update_param(self, param: torch.Tensor, nat: torch.Tensor, lr: float, wd: float,
                       mom: float, module: Optional[nn.Module], clip: bool = False) -> None:
@@ -373,6 +417,8 @@ class IFKFAC(torch.optim.Optimizer):
         self._factors.clear()
         self._inverses.clear()
         self._inverse_copies.clear()
+        self._solve_math.clear()
+        self._kappas.clear()
         self._classic_fallback.clear()
         self._momentum_buffers.clear()
 

@@ -150,6 +150,23 @@ int ifk_tri_inverse_bf16(void* stream, const void* R, int r_dtype, int64_t ldr, 
                          size_t workspace_bytes);
 
 /*
+ * Condition estimate kappa_2(R) ~ sigma_max(R) sigma_max(Z) of an upper-
+ * triangular n x n factor R (dtype r_dtype, ldr) from R and its inverse Z
+ * (fp32, ldz, e.g. from ifk_tri_inverse_bf16), each sigma_max by four steps
+ * of block power iteration with four deterministic probe vectors; the result
+ * (a lower bound, within a few percent when the extreme singular values are
+ * spread, about 10 % when they cluster) is written on the stream to the
+ * device float *kappa.  No
+ * counterpart in the reference; IFKFAC uses it to choose the arithmetic of a
+ * layer's solves in bf16 mode (bf16 where the factors are near-isotropic,
+ * fp32 as the reference's triangular.py:621-628 otherwise).
+ */
+size_t ifk_cond_estimate_workspace_size(int64_t n);
+int ifk_cond_estimate(void* stream, const void* R, int r_dtype, int64_t ldr, const float* Z,
+                      int64_t ldz, int64_t n, float* kappa, void* workspace,
+                      size_t workspace_bytes);
+
+/*
  * Four triangular solves -- replaces apply_vered(grad_W, R_X, R_G)
  * (ifkfac/triangular.py:551-656) and the per-entry body of
  * apply_vered_batched (ifkfac/triangular.py:430-451, :506-544):

@@ -68,6 +68,22 @@ class OracleBackend:
         self.calls["tri_inverse"] += 1
         return torch.from_numpy(np.linalg.inv(_np(R))).float()
 
+    def tri_inverse_bf16(self, R):
+        """Z (fp32) and its RNE bf16 copies (Z, Z^T), as ifk_tri_inverse_bf16."""
+        self.calls["tri_inverse_bf16"] += 1
+        Z = torch.from_numpy(np.linalg.inv(_np(R))).float()
+        return Z, Z.bfloat16(), Z.t().contiguous().bfloat16()
+
+    def cond_estimate(self, R, Z):
+        """kappa_2(R) (exact, by SVD) as a float[1] tensor."""
+        self.calls["cond_estimate"] += 1
+        return torch.tensor([float(np.linalg.cond(_np(R)))], dtype=torch.float32)
+
+    def precondition_apply_bf16(self, grad, ZX2, ZG2):
+        self.calls["precondition_apply_bf16"] += 1
+        zx, zg = _np(ZX2[0]), _np(ZG2[0])
+        return torch.from_numpy(zg @ (zg.T @ _np(grad)) @ zx @ zx.T).float()
+
     def precondition(self, grad, R_X, R_G, math):
         self.calls["precondition"] += 1
         return torch.from_numpy(O.apply_vered(_np(grad), _np(R_X), _np(R_G))).float()

@@ -579,6 +579,27 @@ def test_precondition_apply_bf16_copies(hip, n_out, n_in, trim):
         assert _rel(got, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("n,kappa", [(64, 1.0), (300, 3.0), (1100, 50.0), (2049, 1e3)])
+@pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
+def test_cond_estimate(hip, n, kappa, rdt):
+    """ifk_cond_estimate against kappa_2(R) from the singular values (fp64, torch
+    on the GPU as the checker): a lower bound within 10 % for factors of
+    matrices with log-spaced singular values and a mean component, the
+    inverse Z from the bf16-arithmetic triangular inverse IFKFAC uses.  The
+    bound is 10 %: a factor's smallest singular values cluster when its input
+    has a mean component, which slows the power iteration on Z."""
+    rng = np.random.default_rng(n)
+    X = O.kappa_matrix(4 * n, n, kappa, rng) + (0.5 if kappa > 1 else 0.0)
+    R = O.get_factor(O.streaming_tsqr_update(None, X), 4 * n, 0.0 if kappa > 1 else 1.0)
+    Rt = torch.tensor(R, dtype=torch.float32, device=DEV).to(rdt)
+    Z = hip.tri_inverse_bf16(Rt)[0] if rdt == torch.bfloat16 else hip.tri_inverse(Rt, 0)
+    got = hip.cond_estimate(Rt, Z).item()
+    sv = torch.linalg.svdvals(Rt.double())
+    want = (sv[0] / sv[-1]).item()
+    assert got <= want * 1.001 + 1e-6
+    assert got >= 0.9 * want
+
+
 # --------------------------------------------------------------------------- update
 
 

@@ -216,6 +216,42 @@ def test_weight_step_rounds_once_for_bf16_parameters(be):
     assert not torch.equal(want, twice)                  # the check tells the two apart
 
 
+def test_bf16_mode_chooses_solve_arithmetic_by_kappa(be):
+    """use_true_bf16: a layer whose factors are near-isotropic (kappa_2 <= 1.5,
+    the damping dominating its Grams) keeps the bf16 inverse copies and apply; a
+    layer whose input carries a large mean (kappa(R_X) far above 1.5) gets fp32
+    inverses and fp32 applies, the reference's bf16-mode arithmetic
+    (triangular.py:621-628).  Both updates match the oracle's closed form."""
+    from ifkfac_amd import IFKFAC
+    from ifkfac_amd._backend import MATH_BF16, MATH_F32
+    torch.manual_seed(0)
+    iso, skew = nn.Linear(8, 4, bias=False), nn.Linear(8, 4, bias=False)
+    lam = 1.0
+    opt_iso = IFKFAC(nn.Sequential(iso), lr=1.0, damping=lam, factor_update_freq=1, momentum=0.0,
+                     use_true_bf16=True)
+    g = torch.Generator().manual_seed(3)
+    X = torch.randn(64, 8, generator=g) * 0.1
+    iso(X).pow(2).mean().backward()
+    opt_iso.step()
+    assert opt_iso._solve_math[iso] == MATH_BF16 and iso in opt_iso._inverse_copies
+    assert max(opt_iso._kappas[iso]) <= 1.5
+    opt_sk = IFKFAC(nn.Sequential(skew), lr=1.0, damping=1e-2, factor_update_freq=1,
+                    momentum=0.0, use_true_bf16=True)
+    Xs = torch.randn(64, 8, generator=g) + 5.0
+    acts, grads, hs = _capture(nn.Sequential(skew), Xs)
+    W0 = skew.weight.detach().clone()
+    skew(Xs).pow(2).mean().backward()
+    gW = skew.weight.grad.double().numpy()
+    for h in hs:
+        h.remove()
+    opt_sk.step()
+    assert opt_sk._solve_math[skew] == MATH_F32 and skew not in opt_sk._inverse_copies
+    assert opt_sk._kappas[skew][0] > 1.5
+    RX, RG = (f.float().double().numpy() for f in opt_sk._factors[skew])
+    want = W0.double().numpy() - O.apply_vered(gW, RX, RG)
+    assert np.abs(skew.weight.detach().double().numpy() - want).max() < 1e-5 * np.abs(want).max()
+
+
 def test_capture_controls(be):
     from ifkfac_amd import IFKFAC
     model = _mlp()
