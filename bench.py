@@ -129,6 +129,10 @@ def main() -> int:
     ap.add_argument("--workload", default="linear_4096x11008_p16384", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", default="linear_4096x4096_p8192", choices=sorted(WORKLOADS))
+    ap.add_argument("--factor-path", default="gram", choices=["gram", "cqr", "panel"],
+                    help="the consuming factor update: Gram matrix + blocked Cholesky, "
+                         "CholeskyQR2 outer blocks, or the panel TPQRT fold (a side "
+                         "flagged by the first two is recomputed by the panel path)")
     ap.add_argument("--unfused", action="store_true",
                     help="fold, then finalize (two factorisations per side) instead of the "
                          "fused fold + finalize of IFKFAC's factor update")
@@ -195,15 +199,16 @@ def main() -> int:
         # stream, then one host read of the status flags and the panel path
         # (and the inverse again) for a side whose blocks were too
         # ill-conditioned
-        def side(T, cqr):
-            F, st = be.fold_finalize(None, 0, T, scale, lam, torch.bfloat16, MATH_BF16, cqr=cqr)
+        def side(T, how):
+            F, st = be.fold_finalize(None, 0, T, scale, lam, torch.bfloat16, MATH_BF16,
+                                     cqr=how == "cqr", gram=how == "gram")
             return F, st, be.tri_inverse_bf16(F)
-        out = list(run_pair(dev, lambda: side(X, True), lambda: side(D, True),
-                            b_first=n_out > n_in))
+        out = list(run_pair(dev, lambda: side(X, args.factor_path),
+                            lambda: side(D, args.factor_path), b_first=n_out > n_in))
         st = torch.cat([out[0][1], out[1][1]]).cpu()
         for i, T in enumerate((X, D)):
             if int(st[i]) == 2:
-                out[i] = side(T, False)
+                out[i] = side(T, "panel")
         return out
 
     def step(first: bool, events=None):
@@ -348,7 +353,12 @@ def main() -> int:
         "config": {
             "workload": f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, "
                         f"p={p} rows, bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9",
-            "factor_path": "fold then finalize" if args.unfused else "fused fold + finalize, 1024-column blocks by CholeskyQR2 (panel path if flagged)",
+            "factor_path": "fold then finalize" if args.unfused else {
+                "gram": "fused fold + finalize: Gram matrix + 1024-block Cholesky with split-bf16 "
+                        "updates (panel path if flagged)",
+                "cqr": "fused fold + finalize, 1024-column blocks by CholeskyQR2 (panel path if "
+                       "flagged)",
+                "panel": "fused fold + finalize, panel TPQRT fold"}[args.factor_path],
             "n_in": n_in, "n_out": n_out, "p": p, "algorithmic_gflop_per_step": round(flops / 1e9, 1),
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
         },

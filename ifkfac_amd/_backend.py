@@ -110,15 +110,17 @@ class HipBackend:
 
     def fold_finalize(self, R: Optional[torch.Tensor], r_in: int, X: torch.Tensor, scale: float,
                       damping: float, out_dtype: torch.dtype, math: int,
-                      cqr: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+                      cqr: bool = False, gram: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
         """finalize(fold(R[:r_in], X)) in one factorisation, leaving R untouched.
 
         Returns (R_damped, finite flag int32[1]); R (n x n fp32 buffer whose
         first r_in rows are the running factor) may be None when r_in == 0.
         With ``cqr`` the outer blocks are factored by CholeskyQR2
-        (ifk_fold_finalize_cqr): the flag is then 1 / 0 as above, or 2 when
-        a block was too ill-conditioned for it -- the caller must then call
-        again without ``cqr``.
+        (ifk_fold_finalize_cqr); with ``gram`` (bf16 arithmetic only) the
+        factor is the Cholesky factor of the Gram matrix
+        (ifk_fold_finalize_gram).  Either way the flag is then 1 / 0 as
+        above, or 2 when the input was too ill-conditioned for that method --
+        the caller must then call again with neither.
         """
         X, ldx, xdt = _mat(X, "fold_finalize")
         p, n = X.shape
@@ -133,7 +135,10 @@ class HipBackend:
             ldr = R.stride(0) if R.shape[0] > 1 else n
         out = torch.empty((n, n), dtype=out_dtype, device=X.device)
         flag = torch.empty(1, dtype=torch.int32, device=X.device)
-        name = "ifk_fold_finalize_cqr" if cqr else "ifk_fold_finalize"
+        if gram and math != MATH_BF16:
+            raise IFKFACBackendError("fold_finalize: the Gram path is bf16 arithmetic only")
+        name = ("ifk_fold_finalize_gram" if gram else
+                "ifk_fold_finalize_cqr" if cqr else "ifk_fold_finalize")
         ws = self._ws(getattr(self.lib, name + "_workspace_size")(p, n, int(r_in)), X.device)
         with torch.cuda.device(X.device):
             rc = getattr(self.lib, name)(self._stream(X.device), _ptr(X), xdt, p, n, ldx,

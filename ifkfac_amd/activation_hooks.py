@@ -20,7 +20,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ._backend import MATH_F32, get_backend, run_pair
+from ._backend import MATH_BF16, MATH_F32, get_backend, run_pair
 from .gram_estimator import GramMatrixEstimator
 
 logger = logging.getLogger(__name__)
@@ -233,23 +233,25 @@ class RawActivationHooks(GramMatrixEstimator):
         return R, r, chunk, min(r + chunk.shape[0], n)
 
     def _damped(self, side: str, module: nn.Module, rows: int, out_dtype: torch.dtype,
-                cqr: bool = False):
+                fast: bool = False):
         """Damped factor of one side; a held chunk goes into a fused fold +
-        finalize, whose outer blocks are factored by CholeskyQR2 with ``cqr``
-        (its flag may then be 2: see _retry_cholesky_qr)."""
+        finalize.  With ``fast`` that factorisation is the Gram matrix +
+        blocked Cholesky in bf16 arithmetic, CholeskyQR2 outer blocks in fp32
+        arithmetic; its flag may then be 2 (see _retry_cholesky_qr)."""
         R, r, chunk, _ = self._side_state(side, module)
         if chunk is None:
             return self._finalize(R, rows, out_dtype)
         bufs = self._buf_X if side == "X" else self._buf_G
         return get_backend().fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
                                            1.0 / math.sqrt(rows), self.damping, out_dtype,
-                                           self.math, cqr=cqr)
+                                           self.math, cqr=fast and self.math != MATH_BF16,
+                                           gram=fast and self.math == MATH_BF16)
 
     def _retry_cholesky_qr(self, factors, flags, extras, then, out_dtype: torch.dtype):
-        """One host read of the flags of a consuming factor update: a side whose
-        CholeskyQR2 blocks were too ill-conditioned (flag 2) is recomputed by
-        the panel factorisation, which handles any input (and ``then`` run on
-        the new factor)."""
+        """One host read of the flags of a consuming factor update: a side too
+        ill-conditioned for its Gram / CholeskyQR2 factorisation (flag 2) is
+        recomputed by the panel factorisation, which handles any input (and
+        ``then`` run on the new factor)."""
         mods = list(flags)
         st = torch.cat([torch.cat(flags[m]) for m in mods]).cpu()
         for i, m in enumerate(mods):
@@ -259,7 +261,7 @@ class RawActivationHooks(GramMatrixEstimator):
                 rows = self._n_rows_X[m] if side == "X" else self._n_rows_G[m]
                 logger.debug("get_factors() [%s]: %s factor by the panel path",
                              _module_tag(m), side)
-                R, f = self._damped(side, m, rows, out_dtype, cqr=False)
+                R, f = self._damped(side, m, rows, out_dtype, fast=False)
                 fac, fl = list(factors[m]), list(flags[m])
                 fac[j], fl[j] = R, f
                 factors[m], flags[m] = tuple(fac), tuple(fl)
@@ -293,8 +295,8 @@ class RawActivationHooks(GramMatrixEstimator):
         flags: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         extras: Dict[nn.Module, tuple] = {}
 
-        def side(s, module, rows, cqr):
-            R, f = self._damped(s, module, rows, out_dtype, cqr=cqr)
+        def side(s, module, rows, fast):
+            R, f = self._damped(s, module, rows, out_dtype, fast=fast)
             return R, f, (then(s, module, R) if then is not None else None)
         for module in self._linear_layers:
             R_X_raw, _, chunk_X, r_X = self._side_state("X", module)

@@ -48,6 +48,9 @@ struct OutRef {
   int upper = 0;   // only the upper triangle is wanted (a square Gram matrix):
                    // tiles wholly below the diagonal are skipped and hold
                    // unspecified values
+  int lower = 0;   // only the lower triangle is wanted: tiles wholly above
+                   // the diagonal (row index < column index throughout) are
+                   // skipped and hold unspecified values
 };
 
 inline OutRef out_f32(float* c, int64_t ldc, int64_t bs = 0) {
@@ -62,6 +65,10 @@ inline OutRef out_both(float* c, int64_t ldc, bf16_t* cb, int64_t ldcb, int64_t 
 }
 inline OutRef upper_part(OutRef o) {
   o.upper = 1;
+  return o;
+}
+inline OutRef lower_part(OutRef o) {
+  o.lower = 1;
   return o;
 }
 

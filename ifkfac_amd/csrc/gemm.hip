@@ -296,6 +296,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
   const int bidx = z / p.splits, split = z % p.splits;
   const int64_t m0 = (int64_t)tm * GBM, n0 = (int64_t)tn * GBN;
   if (p.upper_only && m0 >= n0 + GBN) return;   // wholly below the diagonal
+  if (p.lower_only && n0 >= m0 + GBM) return;   // wholly above the diagonal
 
   const void* Ab = (const char*)p.A + (size_t)bidx * p.bsa * (ADT == DT_F32 ? 4 : 2);
   const void* Bb = (const char*)p.B + (size_t)bidx * p.bsb * (BDT == DT_F32 ? 4 : 2);
@@ -506,6 +507,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   p.vec_a = vec_ok(A);
   p.vec_b = vec_ok(B);
   p.upper_only = C.upper && M == N;
+  p.lower_only = C.lower && !C.upper;
   p.vec_c = (!C.c || ((uintptr_t)C.c % 16 == 0 && C.ldc % 4 == 0 && C.bstride % 4 == 0)) &&
             (!C.cb || ((uintptr_t)C.cb % 8 == 0 && C.ldcb % 4 == 0 && C.bstride_b % 4 == 0));
   // The 256 x 256 bf16 kernel takes the large contractions; small or fp32
@@ -583,6 +585,10 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
     return IFK_ERR_INVALID;
   }
   unsigned gx = (unsigned)(p.tiles_m * p.tiles_n);
+  // a square output of which one triangle is wanted: the direct-to-LDS
+  // kernel enumerates the live tiles only
+  if (bb && (p.upper_only || p.lower_only) && M == N && p.tiles_m == p.tiles_n)
+    gx = (unsigned)(p.tiles_m * (p.tiles_m + 1) / 2);
   if (big && max_wgs > 0) {
     const int64_t per_z = std::max<int64_t>(1, max_wgs / std::max<int64_t>(1, batch * splits));
     gx = (unsigned)std::min<int64_t>(gx, per_z);
@@ -597,7 +603,10 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   if (pr) {
     // algorithmic work: 2 M N K (M N K when one operand is triangular), and the
     // minimal traffic: each operand read once, C read (beta != 0) and written once
-    const double tri = (A.tri != TRI_NONE || B.tri != TRI_NONE || p.upper_only) ? 0.5 : 1.0;
+    const double tri =
+        (A.tri != TRI_NONE || B.tri != TRI_NONE || p.upper_only || (p.lower_only && M == N))
+            ? 0.5
+            : 1.0;
     pr->variant = vid;
     pr->m = M;
     pr->n = N;

@@ -51,7 +51,7 @@ struct BbCfg {
   static constexpr int LOADS_A = SLAB_A * 2 / 16 / NTH;          // 16-byte loads per thread
   static constexpr int LOADS_B = SLAB_B * 2 / 16 / NTH;
   static constexpr int LOADS = LOADS_A + LOADS_B;                // per thread per slab pair
-  static_assert(LOADS == 4, "wait_vm immediates assume four loads per slab pair");
+  static_assert(2 * LOADS <= 63, "vmcnt holds at most 63 loads in flight");
   static_assert(SLAB_A * 2 % (16 * NTH) == 0 && SLAB_B * 2 % (16 * NTH) == 0, "slab split");
 };
 using BigCfg = BbCfg<256, 256, 2, 4, 1>;   // 512 threads, 128 KB ring, one workgroup per CU
@@ -118,12 +118,17 @@ __device__ __forceinline__ bool slab_crosses(int tri, int64_t mn0, int ext, int6
   return k0 < mn0 + ext && k0 + BK > mn0;
 }
 
+// s_waitcnt immediate for vmcnt(n) with expcnt and lgkmcnt left alone
+// (vmcnt bits 3:0 and 15:14, expcnt 6:4 = 7, lgkmcnt 11:8 = 15)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0f70; }
+
 // Wait until the loads of this slab have landed, leaving those of the
-// `ahead` later slabs already issued (0, 1 or 2: four loads each) in flight.
+// `ahead` later slabs already issued (0, 1 or 2: L loads each) in flight.
+template <int L>
 __device__ __forceinline__ void wait_vm(int ahead) {
-  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x0f78);     // vmcnt(8)
-  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0f74); // vmcnt(4)
-  else __builtin_amdgcn_s_waitcnt(0x0f70);                // vmcnt(0)
+  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * L));
+  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(L));
+  else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
 
 template <class CF>
@@ -138,6 +143,7 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
   const int bidx = z / p.splits, split = z % p.splits;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   if (p.upper_only && m0 >= n0 + BN) return;   // wholly below the diagonal
+  if (p.lower_only && n0 >= m0 + BM) return;   // wholly above the diagonal
 
   int64_t klo = 0, khi = p.K;
   if (p.tria == TRI_UPPER) klo = max(klo, m0);
@@ -173,7 +179,7 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
     }
   }
   for (int it = 0; it < n_it; ++it) {
-    wait_vm(min(n_it - 1 - it, STAGES - 2));    // this slab landed (later ones may fly)
+    wait_vm<CF::LOADS>(min(n_it - 1 - it, STAGES - 2));   // this slab landed (later ones may fly)
     // every wave's loads of this slab are in LDS and slab it - 1 is free
     // again.  A bare s_barrier: __syncthreads() would also wait for the next
     // slab's loads (its fence drains vmcnt).
@@ -318,15 +324,41 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
 // in its L2 instead of being fetched again for every tile.  Other grids, and
 // products with a triangular operand (whose tiles differ in K range, so
 // contiguous ranges would load some XCDs more than others), visit tiles
-// grid-stride, heaviest first (tile_order).
+// grid-stride, heaviest first (tile_order).  A square output of which only
+// one triangle is wanted enumerates the live tiles only (row by row of the
+// wanted triangle), so that the skipped ones do not leave some XCDs idle.
 constexpr int XCD_GM = 8;
+
+// Live tile l (0 .. T (T + 1) / 2 - 1) of a T x T tile grid of which only the
+// lower triangle (upper = false) or the upper one is wanted: row r of the
+// triangle holds tiles (r, 0 .. r).
+__device__ __forceinline__ void tri_tile(int l, bool upper, int* tm, int* tn) {
+  int r = (int)((sqrtf(8.0f * (float)l + 1.0f) - 1.0f) * 0.5f);
+  while (r > 0 && r * (r + 1) / 2 > l) --r;
+  while ((r + 1) * (r + 2) / 2 <= l) ++r;
+  const int c = l - r * (r + 1) / 2;
+  *tm = upper ? c : r;
+  *tn = upper ? r : c;
+}
 
 template <class CF>
 __global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(16))) bf16_t smem_bb[STAGES * CF::STAGE];
   const int tiles_m = p.tiles_m, tiles_n = p.tiles_n;
   const int tiles = tiles_m * tiles_n;
-  if ((gridDim.x & 7) == 0 && p.tria == TRI_NONE && p.trib == TRI_NONE) {
+  if ((p.upper_only || p.lower_only) && tiles_m == tiles_n && p.M == p.N) {
+    const int live = tiles_m * (tiles_m + 1) / 2;
+    const bool xcd = (gridDim.x & 7) == 0;
+    const int c = xcd ? (int)(blockIdx.x & 7) : 0, nl = xcd ? (int)(gridDim.x >> 3) : gridDim.x;
+    const int per = xcd ? (live + 7) >> 3 : live;
+    const int l1 = min(live, (c + 1) * per);
+    for (int l = c * per + (int)(xcd ? blockIdx.x >> 3 : blockIdx.x); l < l1; l += nl) {
+      int tm, tn;
+      tri_tile(l, p.upper_only != 0, &tm, &tn);
+      bb_tile<CF>(p, tm, tn, smem_bb);
+      __syncthreads();
+    }
+  } else if ((gridDim.x & 7) == 0 && p.tria == TRI_NONE && p.trib == TRI_NONE) {
     const int c = blockIdx.x & 7, nl = gridDim.x >> 3;
     const int per = (tiles + 7) >> 3;
     const int l1 = min(tiles, (c + 1) * per);

@@ -223,6 +223,7 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int tile, bf1
   const int bidx = z / p.splits, split = z % p.splits;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   if (p.upper_only && m0 >= n0 + BN) return;   // wholly below the diagonal
+  if (p.lower_only && n0 >= m0 + BM) return;   // wholly above the diagonal
   const void* Ab = (const char*)p.A + (size_t)bidx * p.bsa * (ADT == DT_F32 ? 4 : 2);
   const void* Bb = (const char*)p.B + (size_t)bidx * p.bsb * (BDT == DT_F32 ? 4 : 2);
 

@@ -18,6 +18,7 @@ struct GemmParams {
   int vec_c;   // C (if any) 16-byte and Cb (if any) 8-byte aligned, with ld and
                // batch strides multiples of 4 elements: vector epilogue
   int upper_only;   // skip tiles wholly below the diagonal (square Gram output)
+  int lower_only;   // skip tiles wholly above the diagonal
 };
 
 // Tile t of a grid-stride walk -> (tile row, tile column), heaviest tiles

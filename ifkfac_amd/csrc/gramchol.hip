@@ -1,0 +1,519 @@
+// Fused fold + finalize by Gram matrix and blocked Cholesky (bf16 arithmetic).
+//
+// The damped factor of a factor update is the upper-triangular R with
+//   R^T R = scale^2 (R_in^T R_in + X^T X) + damping I
+// (activation_hooks.py:328-332 with triangular.py:246-307, 386-421: the QR of
+// [scale R_in; scale X; sqrt(damping) I] with a positive diagonal, which is
+// unique).  So R = scale * chol(A) with
+//   A = P^T P + c^2 I,  P = [R_in; X],  c = sqrt(damping) / scale,
+// and Q is never needed.  In bf16 arithmetic P is read as its RNE bf16
+// rounding (what every MFMA operand of the fold gets), so the products of the
+// Gram matrix are exact and only its fp32 accumulation rounds.
+//
+// Layout: the working matrix Aw (n x n fp32, row stride lda) keeps A's LOWER
+// triangle, so that a column block below the diagonal (the panel of a
+// Cholesky step and both operands of its Schur update) is a stack of
+// contiguous rows: every large product reads K-contiguous operands on the
+// direct-to-LDS kernel, with no transposes.  The factor is built as
+// L = R^T / scale in place of A's lower triangle and cast to R at the end.
+//
+// Left-looking over GB-column blocks (1024; cholb factors one block).  Column
+// block c (rows >= c0, the lower part) is
+//   A_c = (P^T P)_c + c^2 I_cc - sum_{l < c} L_l L_{c,l}^T
+// and step c factors it:
+//   U_cc = chol(A_cc), M = U_cc^{-1}        (cholb, with M alongside)
+//   L_cc = U_cc^T                            (into Aw)
+//   L_rc = A_rc M                            (panel, rows below block c)
+// The panel and the updates need fp32 accuracy from bf16 MFMA: operands are
+// split as x = x_hi + x_lo (both RNE bf16), and a product is
+// a_hi b_hi + a_hi b_lo + a_lo b_hi, formed as ONE product with K tripled by
+// concatenating the halves along K:
+//   panel:   [A_hi | A_lo | A_hi] . [M_hi | M_hi | M_lo]  (M given transposed)
+//   updates: panel l is kept as LA = [L_hi | L_lo | L_hi] and LB = [L_lo |
+//            L_hi | L_hi] at columns 3 GB l of two buffers, so the update of a
+//            column by panels 0 .. m is one product over K = 3 GB (m + 1).
+// The dropped lo.lo term and the roundings leave each product within about
+// 2^-17 of |a||b|, far below the bf16 rounding of the stored factor.
+//
+// Look-ahead: the calling stream runs the chain of steps (latency-bound:
+// cholb is a chain of 64-column launches); the helper stream prepares column
+// c + 2 -- its Gram columns, the damping, and the updates by panels 0 .. c --
+// while step c + 1 runs, so the Gram matrix (p n^2 flops for its lower part)
+// and most of the updates (n^3 in all, split) are done beside the chain.
+// Step c itself applies only the update by panel c - 1.
+//
+// Pivot test: a pivot below GRAM_TOL times the Gram diagonal of its column
+// (A's diagonal before any update) means that column is nearly a combination
+// of the ones before it (cancellation of more than 1 - GRAM_TOL in the Schur
+// complement): the rounding of the Gram matrix and of the updates, about
+// 2^-17 of that diagonal, would then be a visible part of the pivot.  The
+// call then reports status 2, and the caller recomputes the factor by the
+// TPQRT fold (linalg.hip), which never forms A.  Non-finite input raises the
+// same flag (NaN pivots fail the test).
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <mutex>
+
+#include "gemm.h"
+#include "kernels.h"
+#include "linalg.h"
+#include "lookahead.h"
+
+namespace ifk {
+
+#define RC(x)                 \
+  do {                        \
+    int _rc = (x);            \
+    if (_rc) return _rc;      \
+  } while (0)
+
+namespace {
+
+constexpr int64_t GB = 1024;          // Cholesky block (cholb supports up to 1024)
+constexpr float GRAM_TOL = 1e-3f;     // relative pivot threshold (see above)
+
+// ---------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------
+
+// dst (cols x rows, bf16, row stride ldd) = src^T for a rows x cols block of
+// fp32 or bf16 src; with upper set, entries of src below its diagonal are
+// taken as zero.  32 x 32 LDS tile: reads and writes coalesced.
+template <int DT>
+__global__ __launch_bounds__(256) void transpose_to_bf16_kernel(const void* src, int64_t lds,
+                                                                int64_t rows, int64_t cols,
+                                                                bf16_t* dst, int64_t ldd,
+                                                                int upper) {
+  __shared__ float tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = r0 + k, c = c0 + tx;
+    tile[k][tx] = (r < rows && c < cols && !(upper && r > c))
+                      ? Elem<DT>::load((const typename Elem<DT>::T*)src + r * lds + c)
+                      : 0.0f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t c = c0 + k, r = r0 + tx;
+    if (c < cols && r < rows) dst[c * ldd + r] = f32_to_bf16(tile[tx][k]);
+  }
+}
+
+// Split rows x cols fp32 into nseg consecutive bf16 segments per row,
+// dst[r][s cols + c] = lo(x) if bit s of lo_mask else hi(x), hi = RNE(x),
+// lo = RNE(x - hi), and the same into dst2 (ldd2, lo_mask2) when given.
+// Four columns per thread (cols % 4 == 0, 16-byte rows).
+__global__ __launch_bounds__(256) void split_seg_kernel(const float* src, int64_t lds,
+                                                        int64_t rows, int64_t cols, bf16_t* dst,
+                                                        int64_t ldd, int nseg, int lo_mask,
+                                                        bf16_t* dst2, int64_t ldd2,
+                                                        int lo_mask2) {
+  const int64_t c4 = cols >> 2;
+  const int64_t total = rows * c4;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / c4, c = (e - r * c4) * 4;
+    const float4 x = *reinterpret_cast<const float4*>(src + r * lds + c);
+    const float v[4] = {x.x, x.y, x.z, x.w};
+    bf16_t h[4], l[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      h[u] = f32_to_bf16(v[u]);
+      l[u] = f32_to_bf16(v[u] - bf16_to_f32(h[u]));
+    }
+    const uint2 hw = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+    const uint2 lw = make_uint2((uint32_t)l[0] | ((uint32_t)l[1] << 16),
+                                (uint32_t)l[2] | ((uint32_t)l[3] << 16));
+    bf16_t* d = dst + r * ldd + c;
+    for (int s = 0; s < nseg; ++s)
+      *reinterpret_cast<uint2*>(d + s * cols) = ((lo_mask >> s) & 1) ? lw : hw;
+    if (dst2) {
+      bf16_t* d2 = dst2 + r * ldd2 + c;
+      for (int s = 0; s < nseg; ++s)
+        *reinterpret_cast<uint2*>(d2 + s * cols) = ((lo_mask2 >> s) & 1) ? lw : hw;
+    }
+  }
+}
+
+// G (n x n, ldg) = the symmetric matrix whose lower triangle is A's (lda):
+// G_ij = A_max(i,j),min(i,j).  Tile (tr, tc) of G reads A's tile
+// (max, min) once through LDS.
+__global__ __launch_bounds__(256) void sym_from_lower_kernel(const float* A, int64_t lda,
+                                                             int64_t n, float* G, int64_t ldg) {
+  __shared__ float tile[32][33];
+  const int tr = blockIdx.y, tc = blockIdx.x;
+  const int ar = tr > tc ? tr : tc, ac = tr > tc ? tc : tr;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)ar * 32 + k, c = (int64_t)ac * 32 + tx;
+    tile[k][tx] = (r < n && c < n) ? A[r * lda + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)tr * 32 + k, c = (int64_t)tc * 32 + tx;
+    if (r >= n || c >= n) continue;
+    float v;
+    if (tr > tc) v = tile[k][tx];
+    else if (tr < tc) v = tile[tx][k];
+    else v = (k >= tx) ? tile[k][tx] : tile[tx][k];
+    G[r * ldg + c] = v;
+  }
+}
+
+// out (odt, n x n, ldo) = scale * L^T for the lower-triangular L (ldl):
+// out_ij = scale L_ji for j >= i, 0 below the diagonal; *finite = 0 when any
+// stored value is not finite.
+template <int ODT>
+__global__ __launch_bounds__(256) void cast_lower_t_kernel(const float* L, int64_t ldl, int64_t n,
+                                                           float scale, void* out, int64_t ldo,
+                                                           int* finite) {
+  __shared__ float tile[32][33];
+  const int tr = blockIdx.y, tc = blockIdx.x;   // output tile
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  typedef typename Elem<ODT>::T OT;
+  OT* O = (OT*)out;
+  if (tr > tc) {
+    for (int k = ty; k < 32; k += 8) {
+      const int64_t r = (int64_t)tr * 32 + k, c = (int64_t)tc * 32 + tx;
+      if (r < n && c < n) Elem<ODT>::store(O + r * ldo + c, 0.0f);
+    }
+    return;
+  }
+  // L's tile (tc, tr) holds the output tile transposed
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)tc * 32 + k, c = (int64_t)tr * 32 + tx;
+    tile[k][tx] = (r < n && c < n) ? L[r * ldl + c] : 0.0f;
+  }
+  __syncthreads();
+  bool bad = false;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)tr * 32 + k, c = (int64_t)tc * 32 + tx;
+    if (r >= n || c >= n) continue;
+    const float v = (c >= r) ? scale * tile[tx][k] : 0.0f;
+    if (!isfinite(v)) bad = true;
+    Elem<ODT>::store(O + r * ldo + c, v);
+  }
+  if (bad) *finite = 0;
+}
+
+// A_ii += v and dref_i = A_ii (after the addition), i < n
+__global__ void add_diag_ref_kernel(float* A, int64_t lda, int64_t n, float v, float* dref) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float d = A[i * lda + i] + v;
+    A[i * lda + i] = d;
+    dref[i] = d;
+  }
+}
+
+unsigned grid_of(int64_t work, int64_t cap = 2048) {
+  int64_t g = cdiv(work, 256);
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+int transpose_to_bf16(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
+                      int64_t cols, bf16_t* dst, int64_t ldd, bool upper) {
+  if (rows * cols == 0) return IFK_OK;
+  if (cdiv(rows, 32) > 65535) {
+    set_error("fold_finalize_gram: too many rows to transpose");
+    return IFK_ERR_INVALID;
+  }
+  const dim3 grid((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32));
+  if (sdt == DT_F32)
+    hipLaunchKernelGGL(transpose_to_bf16_kernel<DT_F32>, grid, dim3(256), 0, s, src, lds, rows,
+                       cols, dst, ldd, upper ? 1 : 0);
+  else
+    hipLaunchKernelGGL(transpose_to_bf16_kernel<DT_BF16>, grid, dim3(256), 0, s, src, lds, rows,
+                       cols, dst, ldd, upper ? 1 : 0);
+  return check_launch("transpose_to_bf16");
+}
+
+int split_seg(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
+              bf16_t* dst, int64_t ldd, int nseg, int lo_mask, bf16_t* dst2 = nullptr,
+              int64_t ldd2 = 0, int lo_mask2 = 0) {
+  if (rows * cols == 0) return IFK_OK;
+  hipLaunchKernelGGL(split_seg_kernel, dim3(grid_of(rows * cols / 4)), dim3(256), 0, s, src, lds,
+                     rows, cols, dst, ldd, nseg, lo_mask, dst2, ldd2, lo_mask2);
+  return check_launch("split_seg");
+}
+
+int sym_from_lower(hipStream_t s, const float* A, int64_t lda, int64_t n, float* G, int64_t ldg) {
+  const dim3 grid((unsigned)cdiv(n, 32), (unsigned)cdiv(n, 32));
+  hipLaunchKernelGGL(sym_from_lower_kernel, grid, dim3(256), 0, s, A, lda, n, G, ldg);
+  return check_launch("sym_from_lower");
+}
+
+int cast_lower_t(hipStream_t s, const float* L, int64_t ldl, int64_t n, float scale, void* out,
+                 int odt, int64_t ldo, int* finite) {
+  if (cdiv(n, 32) > 65535) {
+    set_error("fold_finalize_gram: factor too large");
+    return IFK_ERR_INVALID;
+  }
+  const dim3 grid((unsigned)cdiv(n, 32), (unsigned)cdiv(n, 32));
+  if (odt == DT_F32)
+    hipLaunchKernelGGL(cast_lower_t_kernel<DT_F32>, grid, dim3(256), 0, s, L, ldl, n, scale, out,
+                       ldo, finite);
+  else
+    hipLaunchKernelGGL(cast_lower_t_kernel<DT_BF16>, grid, dim3(256), 0, s, L, ldl, n, scale, out,
+                       ldo, finite);
+  return check_launch("cast_lower_t");
+}
+
+// ---------------------------------------------------------------------------
+// Workspace
+// ---------------------------------------------------------------------------
+struct GramWs {
+  int64_t ldk;        // row stride of PT (pe rounded up to 8; the pad is zero)
+  int64_t lda;        // row stride of Aw
+  int64_t ldl;        // row stride of LA / LB: 3 GB per panel
+  bf16_t* PT;         // P^T in bf16, n x ldk
+  float* Aw;          // working matrix / factor (lower), n x lda
+  float* dref;        // Gram diagonal (+ c^2), n
+  float* G;           // symmetrised diagonal block, GB x GB; then M^T
+  float* U;           // U_kk, GB x GB
+  float* M;           // U_kk^{-1}, GB x GB
+  float* Zd;          // cholb's 64 x 64 diagonal inverses
+  bf16_t* MT3[2];     // [M^T_hi | M^T_hi | M^T_lo], GB x 3 GB, by step parity
+  bf16_t* ASb;        // [A_hi | A_lo | A_hi] of the band block, GB x 3 GB
+  bf16_t* LSb;        // [L_hi | L_lo | L_hi | L_hi] of the band block, GB x 4 GB
+  bf16_t* AS2;        // [A_hi | A_lo | A_hi] of the rest of a panel, n x 3 GB
+  bf16_t* LA;         // panel l at columns 3 GB l: [L_hi | L_lo | L_hi], n x ldl
+  bf16_t* LB;         // panel l at columns 3 GB l: [L_lo | L_hi | L_hi], n x ldl
+  int* flag;
+  SplitScratch sp, sp2, sp3;   // split-K partials of the three streams
+};
+
+void plan_gram(Arena& a, int64_t pe, int64_t n, GramWs& w) {
+  const int64_t nb = cdiv(n, GB);
+  w.ldk = (int64_t)align_up((size_t)std::max<int64_t>(pe, 1), 8);
+  w.lda = (int64_t)align_up((size_t)n, 64);
+  w.ldl = 3 * GB * std::max<int64_t>(nb - 1, 1);
+  const bool multi = nb > 1;
+  const size_t big = multi ? (size_t)n : 1;
+  w.PT = a.take<bf16_t>((size_t)n * w.ldk);
+  w.Aw = a.take<float>((size_t)n * w.lda);
+  w.dref = a.take<float>((size_t)n);
+  w.G = a.take<float>((size_t)GB * GB);
+  w.U = a.take<float>((size_t)GB * GB);
+  w.M = a.take<float>((size_t)GB * GB);
+  w.Zd = a.take<float>((size_t)(GB / 64) * 64 * 64);
+  for (int i = 0; i < 2; ++i) w.MT3[i] = a.take<bf16_t>(multi ? (size_t)GB * 3 * GB : 1);
+  w.ASb = a.take<bf16_t>(multi ? (size_t)GB * 3 * GB : 1);
+  w.LSb = a.take<bf16_t>(multi ? (size_t)GB * 4 * GB : 1);
+  w.AS2 = a.take<bf16_t>(big * 3 * GB);
+  w.LA = a.take<bf16_t>(big * w.ldl);
+  w.LB = a.take<bf16_t>(big * w.ldl);
+  w.flag = a.take<int>(64);
+  // split-K partials for the products with one block column of output
+  w.sp.floats = (size_t)std::min<int64_t>(n, 8 * GB) * GB * 2;
+  w.sp.p = a.take<float>(w.sp.floats);
+  w.sp2.floats = (size_t)std::min<int64_t>(n, 16 * GB) * GB * 2;
+  w.sp2.p = a.take<float>(w.sp2.floats);
+  w.sp3.floats = w.sp2.floats;
+  w.sp3.p = a.take<float>(w.sp3.floats);
+}
+
+// Workgroup caps of the helper streams' products: the chain's launches
+// (cholb's diagonal workgroup, the band products) must find CUs free while
+// the Gram columns and the panel work run beside them.
+constexpr int GRAM_MAX_WGS = 192;
+constexpr int REST_MAX_WGS = 128;
+
+struct Blk {
+  int64_t r0, r1;   // rows / columns of block k
+};
+inline Blk blk(int64_t k, int64_t n) { return Blk{k * GB, std::min<int64_t>(k * GB + GB, n)}; }
+
+// Gram column c of A (rows >= c0, lower part) with c^2 on its diagonal and
+// the pivot test's reference diagonal taken there.
+int gram_column(hipStream_t s, GramWs& w, int64_t n, int64_t c, float c2, bool have_rows,
+                int max_wgs) {
+  const Blk b = blk(c, n);
+  const int64_t W = b.r1 - b.r0, rows = n - b.r0;
+  float* Ac = w.Aw + b.r0 * w.lda + b.r0;
+  if (have_rows) {
+    RC(gemm(s, MATH_BF16, rows, W, w.ldk, 1.0f, A_n(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk),
+            B_t(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk), 0.0f, lower_part(out_f32(Ac, w.lda)), 1,
+            w.sp3, max_wgs));
+  } else {
+    RC(launch_zero(s, Ac, w.lda, rows, W));
+  }
+  hipLaunchKernelGGL(add_diag_ref_kernel, dim3(grid_of(W, 64)), dim3(256), 0, s, Ac, w.lda, W, c2,
+                     w.dref + b.r0);
+  return check_launch("add_diag_ref");
+}
+
+// Chain, part 1 of step k: L_kk = chol(A_kk)^T and M = U_kk^{-1}.
+int chain_factor(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
+  const Blk b = blk(k, n);
+  const int64_t W = b.r1 - b.r0;
+  float* Akk = w.Aw + b.r0 * w.lda + b.r0;
+  RC(sym_from_lower(s, Akk, w.lda, W, w.G, GB));
+  RC(launch_cholb(s, w.G, GB, (int)W, w.U, GB, w.Zd, w.dref + b.r0, GRAM_TOL, w.flag, w.M, GB,
+                  true));
+  return launch_transpose_cast(s, w.U, GB, W, W, Akk, DT_F32, w.lda);
+}
+
+// Chain, part 2 of step k (block k + 1 exists): M^T split into MT3[k % 2];
+// the band L_{k+1,k} = A_{k+1,k} M; the next diagonal block's update
+// A_{k+1,k+1} -= L_{k+1,k} L_{k+1,k}^T.
+int chain_band(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
+  const Blk b = blk(k, n), b1 = blk(k + 1, n);
+  const int64_t W = b.r1 - b.r0, W1 = b1.r1 - b1.r0;   // W == GB here
+  bf16_t* MT3 = w.MT3[k & 1];
+  RC(launch_zero_tri_blocks(s, w.M, 4, GB, W, true));   // cholb leaves M's lower blocks unset
+  RC(launch_transpose_cast(s, w.M, GB, W, W, w.G, DT_F32, GB));
+  RC(split_seg(s, w.G, GB, W, W, MT3, 3 * GB, 3, 0b100));
+  float* Ab = w.Aw + b1.r0 * w.lda + b.r0;   // block (k + 1, k)
+  RC(split_seg(s, Ab, w.lda, W1, W, w.ASb, 3 * GB, 3, 0b010));
+  RC(gemm(s, MATH_BF16, W1, W, 3 * W, 1.0f, A_n(w.ASb, DT_BF16, 3 * GB),
+          B_t(MT3, DT_BF16, 3 * GB), 0.0f, out_f32(Ab, w.lda), 1, w.sp));
+  RC(split_seg(s, Ab, w.lda, W1, W, w.LSb, 4 * GB, 4, 0b0010));
+  float* A11 = w.Aw + b1.r0 * w.lda + b1.r0;
+  return gemm(s, MATH_BF16, W1, W1, 3 * W, -1.0f, A_n(w.LSb, DT_BF16, 4 * GB),
+              B_t(w.LSb + GB, DT_BF16, 4 * GB), 1.0f, lower_part(out_f32(A11, w.lda)), 1, w.sp);
+}
+
+// Helper work of step k (blocks k + 2 .. exist): the rest of panel k,
+// L_{>k+1,k} = A_{>k+1,k} M (in place); panel k's split copies (rows > k);
+// column k + 1's rows > k + 1 updated by panel k; column k + 2 updated by
+// panels 0 .. k (after its Gram column, event gev).
+int helper_step(hipStream_t s, GramWs& w, int64_t n, int64_t k, hipEvent_t gev_k2,
+                hipEvent_t gev_k1, int max_wgs) {
+  const Blk b = blk(k, n), b1 = blk(k + 1, n), b2 = blk(k + 2, n);
+  const int64_t W = b.r1 - b.r0;
+  const int64_t lda = w.lda, ldl = w.ldl;
+  const int64_t rest = n - b2.r0;   // rows > k + 1
+  float* Arest = w.Aw + b2.r0 * lda + b.r0;
+  RC(split_seg(s, Arest, lda, rest, W, w.AS2, 3 * GB, 3, 0b010));
+  RC(gemm(s, MATH_BF16, rest, W, 3 * W, 1.0f, A_n(w.AS2, DT_BF16, 3 * GB),
+          B_t(w.MT3[k & 1], DT_BF16, 3 * GB), 0.0f, out_f32(Arest, lda), 1, w.sp2, max_wgs));
+  const int64_t k0 = 3 * GB * k;
+  RC(split_seg(s, w.Aw + b1.r0 * lda + b.r0, lda, n - b1.r0, W, w.LA + b1.r0 * ldl + k0, ldl, 3,
+               0b010, w.LB + b1.r0 * ldl + k0, ldl, 0b001));
+  // column k + 1, rows > k + 1, by panel k
+  if (gev_k1) HIPRC(hipStreamWaitEvent(s, gev_k1, 0), "fold_finalize_gram: stream wait failed");
+  const int64_t W1 = b1.r1 - b1.r0;
+  RC(gemm(s, MATH_BF16, rest, W1, 3 * GB, -1.0f, A_n(w.LA + b2.r0 * ldl + k0, DT_BF16, ldl),
+          B_t(w.LB + b1.r0 * ldl + k0, DT_BF16, ldl), 1.0f,
+          out_f32(w.Aw + b2.r0 * lda + b1.r0, lda), 1, w.sp2, max_wgs));
+  // column k + 2 by panels 0 .. k
+  if (gev_k2) HIPRC(hipStreamWaitEvent(s, gev_k2, 0), "fold_finalize_gram: stream wait failed");
+  const int64_t W2 = b2.r1 - b2.r0;
+  return gemm(s, MATH_BF16, rest, W2, 3 * GB * (k + 1), -1.0f,
+              A_n(w.LA + b2.r0 * ldl, DT_BF16, ldl), B_t(w.LB + b2.r0 * ldl, DT_BF16, ldl), 1.0f,
+              lower_part(out_f32(w.Aw + b2.r0 * lda + b2.r0, lda)), 1, w.sp2, max_wgs);
+}
+
+}  // namespace
+
+size_t fold_finalize_gram_ws(int64_t p, int64_t n, int64_t r_in) {
+  Arena a(nullptr, 0);
+  GramWs w;
+  plan_gram(a, r_in + p, n, w);
+  return a.used;
+}
+
+int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                       const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
+                       void* out, int odt, int64_t ldo, int math, int* status, void* ws,
+                       size_t ws_bytes) {
+  if (n < 1 || p < 0 || r_in < 0 || r_in > n || (p > 0 && (!X || ldx < n)) ||
+      (r_in > 0 && (!R_in || ldr < n)) || !out || ldo < n || !(scale > 0.0f) ||
+      !(damping >= 0.0f) || (xdt != DT_F32 && xdt != DT_BF16) ||
+      (odt != DT_F32 && odt != DT_BF16) || !status) {
+    set_error("fold_finalize_gram: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  if (math != MATH_BF16) {
+    set_error("fold_finalize_gram: bf16 arithmetic only (fp32 arithmetic folds by "
+              "ifk_fold_finalize_cqr / ifk_fold_finalize)");
+    return IFK_ERR_INVALID;
+  }
+  const int64_t pe = r_in + p;
+  if (!(damping > 0.0f) && pe < n) {
+    set_error("fold_finalize_gram: fewer rows than columns and no damping (the factor is not "
+              "square)");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  GramWs w;
+  plan_gram(a, pe, n, w);
+  if (a.overflow) {
+    set_error("fold_finalize_gram: workspace too small");
+    return IFK_ERR_WORKSPACE;
+  }
+  const int64_t nb = cdiv(n, GB);
+  LookAhead* la = nullptr;
+  int rc = IFK_OK;
+  if (nb > 2) {   // helper streams: the Gram columns, and the panel work beside the chain
+    la = look_ahead(s, &rc);
+    if (!la) return rc;
+  }
+  std::unique_lock<std::mutex> lock;
+  if (la) {
+    lock = std::unique_lock<std::mutex>(la->mu);
+    RC(look_ahead_events(la, (size_t)nb));
+  }
+  hipStream_t s2 = la ? la->s2 : s, s3 = la ? la->s3 : s;
+  const int wg2 = la ? REST_MAX_WGS : 0, wg3 = la ? GRAM_MAX_WGS : 0;
+  const float c2 = damping / (scale * scale);
+  const bool have_rows = pe > 0;
+  RC(launch_fill_int(s, w.flag, 0, 1));
+  // P^T (bf16, K-padded with zeros)
+  if (w.ldk > pe) RC(launch_zero_bf16(s, w.PT + pe, w.ldk, n, w.ldk - pe));
+  if (r_in > 0) RC(transpose_to_bf16(s, R_in, DT_F32, ldr, r_in, n, w.PT, w.ldk, true));
+  if (p > 0) RC(transpose_to_bf16(s, X, xdt, ldx, p, n, w.PT + r_in, w.ldk, false));
+  // Gram columns in order on s3, each with its event (they depend on P^T only)
+  if (la) {
+    HIPRC(hipEventRecord(la->ready[0], s), "fold_finalize_gram: event record failed");
+    HIPRC(hipStreamWaitEvent(s3, la->ready[0], 0), "fold_finalize_gram: stream wait failed");
+  }
+  for (int64_t c = 0; c < nb; ++c) {
+    RC(gram_column(s3, w, n, c, c2, have_rows, wg3));
+    if (la) HIPRC(hipEventRecord(la->col[c], s3), "fold_finalize_gram: event record failed");
+  }
+  // The chain on s; the helper s2 works one step behind it.  Events (each
+  // recorded again only after the wait on its previous record is enqueued):
+  //   col[c]:        Gram column c done (s3)
+  //   ready[k % 2]:  step k's band and diagonal update done (s -> s2)
+  //   aready[k % 2]: helper step k done (s2 -> s, before step k + 1's band)
+  if (la) HIPRC(hipStreamWaitEvent(s, la->col[0], 0), "fold_finalize_gram: stream wait failed");
+  for (int64_t k = 0; k < nb; ++k) {
+    const int kp = (int)(k & 1);
+    RC(chain_factor(s, w, n, k));
+    if (k + 1 >= nb) break;
+    // the band of step k needs helper step k - 1 (column k's rows > k, and
+    // column k + 1 updated by panels < k), which also frees MT3[k % 2]
+    if (la && k >= 1 && k + 1 < nb && (k - 1) + 2 < nb)
+      HIPRC(hipStreamWaitEvent(s, la->aready[kp ^ 1], 0), "fold_finalize_gram: stream wait failed");
+    if (la && k == 0)
+      HIPRC(hipStreamWaitEvent(s, la->col[1], 0), "fold_finalize_gram: stream wait failed");
+    RC(chain_band(s, w, n, k));
+    if (k + 2 < nb) {
+      if (la) {
+        HIPRC(hipEventRecord(la->ready[kp], s), "fold_finalize_gram: event record failed");
+        HIPRC(hipStreamWaitEvent(s2, la->ready[kp], 0), "fold_finalize_gram: stream wait failed");
+      }
+      RC(helper_step(s2, w, n, k, la ? la->col[k + 2] : nullptr,
+                     (la && k == 0) ? la->col[1] : nullptr, wg2));
+      if (la) HIPRC(hipEventRecord(la->aready[kp], s2), "fold_finalize_gram: event record failed");
+    }
+  }
+  if (la) {
+    HIPRC(hipEventRecord(la->done, s2), "fold_finalize_gram: event record failed");
+    HIPRC(hipStreamWaitEvent(s, la->done, 0), "fold_finalize_gram: stream wait failed");
+    HIPRC(hipEventRecord(la->fall[0], s3), "fold_finalize_gram: event record failed");
+    HIPRC(hipStreamWaitEvent(s, la->fall[0], 0), "fold_finalize_gram: stream wait failed");
+  }
+  RC(launch_fill_int(s, status, 1, 1));
+  RC(cast_lower_t(s, w.Aw, w.lda, n, scale, out, odt, ldo, status));
+  return launch_status_merge(s, status, w.flag);
+}
+
+}  // namespace ifk

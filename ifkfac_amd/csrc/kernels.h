@@ -54,9 +54,12 @@ int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
 // diagonal 64-blocks, dref (n floats) diag(A).  A pivot below tol * diag(A)_i
 // sets *flag.
 // With M (ld ldm), M = U^{-1} as well (its blocks on and above the diagonal),
-// formed column block by column block alongside the factorisation.
+// formed column block by column block alongside the factorisation.  With
+// dref_in, dref holds the reference diagonal on entry instead (e.g. a Gram
+// matrix's diagonal before the updates that produced A).
 int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
-                 float* dref, float tol, int* flag, float* M = nullptr, int64_t ldm = 0);
+                 float* dref, float tol, int* flag, float* M = nullptr, int64_t ldm = 0,
+                 bool dref_in = false);
 // hi = RNE bf16(src), lo = RNE bf16(src - hi); transposed (hi[c][r]) with trans
 int launch_split_bf16(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
                       bf16_t* hi, bf16_t* lo, int64_t ldo, bool trans = false);

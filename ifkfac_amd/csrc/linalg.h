@@ -38,6 +38,15 @@ int fold_finalize_cqr(hipStream_t s, const void* X, int xdt, int64_t p, int64_t 
                       void* out, int odt, int64_t ldo, int math, int* status, void* ws,
                       size_t ws_bytes);
 
+// The same factor as fold_finalize from the Gram matrix of [R_in; X] and a
+// blocked Cholesky (gramchol.hip; bf16 arithmetic only).  *status as for
+// fold_finalize_cqr (2: a pivot below 1e-3 of its Gram diagonal).
+size_t fold_finalize_gram_ws(int64_t p, int64_t n, int64_t r_in);
+int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                       const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
+                       void* out, int odt, int64_t ldo, int math, int* status, void* ws,
+                       size_t ws_bytes);
+
 // Z = R^{-1} for upper-triangular R (dtype rdt); Z fp32 upper triangular.
 size_t trinv_ws(int64_t n);
 int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,

@@ -35,6 +35,7 @@
 #include "gemm.h"
 #include "kernels.h"
 #include "linalg.h"
+#include "lookahead.h"
 
 namespace ifk {
 
@@ -216,25 +217,9 @@ static void plan_cqr(Arena& a, int64_t pe, CqrWs& q) {
   q.flag = a.take<int>(64);
 }
 
-// ----------------------------------------------------------------------------
-// Helper streams and events of the look-ahead (one set per device and
-// calling stream, created on first use; a fold holds the set's lock while it
-// enqueues).
-// ----------------------------------------------------------------------------
-struct LookAhead {
-  std::mutex mu;
-  hipStream_t s2 = nullptr;                 // far updates
-  hipEvent_t ready[2] = {nullptr, nullptr};   // the outer block's reflectors are written
-  hipEvent_t nearwp[2] = {nullptr, nullptr};  // Wp of the next block's columns is formed
-  hipEvent_t fall[2] = {nullptr, nullptr};    // all of the block's far update is done
-  hipEvent_t done = nullptr;                // everything queued on s2 so far
-  hipEvent_t tready[2] = {nullptr, nullptr};  // T (or M2, N) of the outer block is complete
-  hipEvent_t aready[2] = {nullptr, nullptr};  // far part A of the outer block is applied
-};
-
 // One helper stream per (device, calling stream): folds issued on different
 // streams (the two sides of a layer) keep independent far updates.
-static LookAhead* look_ahead(hipStream_t s, int* rc) {
+LookAhead* look_ahead(hipStream_t s, int* rc) {
   static std::mutex g_mu;
   static std::map<std::pair<int, hipStream_t>, LookAhead*> g_la;
   int dev = 0;
@@ -248,6 +233,7 @@ static LookAhead* look_ahead(hipStream_t s, int* rc) {
   if (!la) {
     LookAhead* x = new LookAhead();
     bool ok = hipStreamCreateWithFlags(&x->s2, hipStreamNonBlocking) == hipSuccess &&
+              hipStreamCreateWithFlags(&x->s3, hipStreamNonBlocking) == hipSuccess &&
               hipEventCreateWithFlags(&x->done, hipEventDisableTiming) == hipSuccess;
     for (int i = 0; i < 2 && ok; ++i)
       ok = hipEventCreateWithFlags(&x->ready[i], hipEventDisableTiming) == hipSuccess &&
@@ -266,13 +252,18 @@ static LookAhead* look_ahead(hipStream_t s, int* rc) {
   return la;
 }
 
-#define HIPRC(x, what)              \
-  do {                              \
-    if ((x) != hipSuccess) {        \
-      set_error(what);              \
-      return IFK_ERR_HIP;           \
-    }                               \
-  } while (0)
+int look_ahead_events(LookAhead* la, size_t n) {
+  while (la->col.size() < n) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      set_error("look-ahead: cannot create an event");
+      return IFK_ERR_HIP;
+    }
+    la->col.push_back(e);
+  }
+  return IFK_OK;
+}
+
 
 // T of outer block k (reflectors V = [I; Y] of columns [K0, K1), pe rows,
 // buffers of parity k2).  The UT transform gives

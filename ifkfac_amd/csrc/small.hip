@@ -728,7 +728,7 @@ __device__ __forceinline__ void st_blk(const float* S, float* g, int64_t ld, int
 __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_t lda, int n,
                                                           float* U, int64_t ldu, float* Zd,
                                                           float* dref, float tol, int* flag,
-                                                          float* Mo, int64_t ldm) {
+                                                          float* Mo, int64_t ldm, int dref_in) {
   __shared__ float sC[SB * SLD];
   __shared__ float sZ[SB * SLD];
   __shared__ float sT[TRINV_TMP];
@@ -736,12 +736,14 @@ __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_
   const int t = threadIdx.x;
   const int b0 = n < SB ? n : SB;
   if (t == 0) bad = 0;
-  for (int e = t; e < n; e += SNT) dref[e] = A[(int64_t)e * lda + e];
+  if (!dref_in)
+    for (int e = t; e < n; e += SNT) dref[e] = A[(int64_t)e * lda + e];
   float v[PAD_PER];
   ld_blk(v, A, lda, b0, b0, 1.0f);
   st_pad(sC, v);
   __syncthreads();
-  sm_chol64(sC, tol, &bad, 0);   // block 0: its diagonal on entry is A's
+  // block 0: its diagonal on entry is A's (or the given reference)
+  sm_chol64(sC, tol, &bad, 0, dref_in ? dref : nullptr, b0);
   st_blk(sC, U, ldu, b0, b0);
   sm_trinv64(sC, sZ, sT);
   for (int e = t; e < SB * SB; e += SNT) {
@@ -1379,13 +1381,13 @@ int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b) {
 }
 
 int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
-                 float* dref, float tol, int* flag, float* M, int64_t ldm) {
+                 float* dref, float tol, int* flag, float* M, int64_t ldm, bool dref_in) {
   if (n < 1 || n > CHOLB_MAX || lda < n || ldu < n || (M && ldm < n)) {
     set_error("cholb: size out of range");
     return IFK_ERR_INVALID;
   }
   hipLaunchKernelGGL(cholb_first_kernel, dim3(1), dim3(SNT), 0, s, A, lda, n, U, ldu, Zd, dref, tol,
-                     flag, M, ldm);
+                     flag, M, ldm, dref_in ? 1 : 0);
   if (int rc = check_launch("cholb_first")) return rc;
   const int nb = (n + SB - 1) / SB;
   // step k: the (i, j) pairs k < i <= j (m (m + 1) / 2 of them, m = nb - 1 - k),

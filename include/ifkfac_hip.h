@@ -129,6 +129,27 @@ int ifk_fold_finalize_cqr(void* stream, const void* X, int x_dtype, int64_t p, i
                           int32_t* status, void* workspace, size_t workspace_bytes);
 
 /*
+ * ifk_fold_finalize from the Gram matrix instead of a TPQRT fold, in bf16
+ * arithmetic (math must be IFK_MATH_BF16): A = P^T P + (damping / scale^2) I
+ * with P = [R_in; X] rounded to bf16 (exact products, fp32 accumulation), the
+ * factor R = scale * chol(A) by a right-looking Cholesky over 1024-column
+ * blocks whose panel and Schur-update products keep fp32 accuracy by
+ * splitting each operand into two bf16 halves.  No counterpart in the
+ * reference (its fold is torch.linalg.qr, ifkfac/triangular.py:284-301 and
+ * :411-416, whose R is the same unique factor); same arguments and result as
+ * ifk_fold_finalize_cqr.  *status (device): 1 finite, 0 not finite, 2 some
+ * pivot fell below 1e-3 of its column's Gram diagonal (more cancellation
+ * than the Gram matrix's rounding leaves room for): the output is then
+ * meaningless and ifk_fold_finalize, on the same inputs, computes the
+ * factor.  status must not be NULL.
+ */
+size_t ifk_fold_finalize_gram_workspace_size(int64_t p, int64_t n, int64_t r_in);
+int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
+                           int64_t ldx, const float* R_in, int64_t ldr, int64_t r_in, float scale,
+                           float damping, void* out, int out_dtype, int64_t ldo, int math,
+                           int32_t* status, void* workspace, size_t workspace_bytes);
+
+/*
  * Triangular inverse Z = R^{-1} of an upper-triangular n x n factor (dtype
  * r_dtype) into fp32 Z (ldz).  The four solves of apply_vered are applied as
  * products with Z; this is the factor-side half of them.

@@ -5,8 +5,9 @@ Linear 4096 <-> 11008 at p = 16384 (bf16): for kappa(X) in {1e1, 1e2, 1e3},
 literal (singular values log-spaced in [1/kappa, 1], damping 1e-2, where the
 damping dominates X^T X / p) and kappa-exposed (X scaled by sqrt(p) and
 damping 0.1 / kappa^2, so kappa(R_damped) ~ kappa), both orientations, the
-factor update IFKFAC times: fold_finalize with CholeskyQR2 blocks (the panel
-path for a side whose status is 2) -> tri_inverse_bf16 -> the bf16 apply.
+factor update IFKFAC times: fold_finalize by the Gram matrix + blocked
+Cholesky (the panel path for a side whose status is 2) -> tri_inverse_bf16 ->
+the bf16 apply.
 Bounds, each on its own part of the error:
   factor    ||R^T R - (X^T X / p + lam I)||_F / ||.||_F <= 4 kappa(R) eps_bf16
             (vacuous) and <= 5e-3 (measured at most 2.2e-3): the bf16 rounding
@@ -69,10 +70,12 @@ def damped_gram(T, lam):
 
 
 def factor_update(hip, T, lam, out_dtype=torch.bfloat16, math_=1):
-    """RawActivationHooks' consuming factor update for one side: CholeskyQR2 blocks,
-    the panel path if they report status 2."""
+    """RawActivationHooks' consuming factor update for one side: the Gram matrix +
+    blocked Cholesky in bf16 arithmetic (CholeskyQR2 blocks in fp32), the panel
+    path if that reports status 2."""
     p = T.shape[0]
-    F_, st = hip.fold_finalize(None, 0, T, 1 / math.sqrt(p), lam, out_dtype, math_, cqr=True)
+    F_, st = hip.fold_finalize(None, 0, T, 1 / math.sqrt(p), lam, out_dtype, math_,
+                               cqr=math_ == 0, gram=math_ == 1)
     first = int(st.item())
     if first == 2:
         F_, st = hip.fold_finalize(None, 0, T, 1 / math.sqrt(p), lam, out_dtype, math_, cqr=False)
@@ -155,9 +158,9 @@ def test_linear_4096_11008_kappa_sweep_timed_chain(hip, n_in, n_out, kappa, expo
 
 @pytest.mark.parametrize("side", ["X", "G"])
 def test_linear_4096_11008_flagged_block_takes_the_panel_path(hip, side):
-    """A side whose CholeskyQR2 pass-1 pivot test fails at full size (two equal
-    columns of large scale: the Gram's pivot falls to the damping, 1e-6 of its
-    diagonal) reports status 2, and the panel path (ifk_fold_finalize) gives the
+    """A side whose Cholesky pivot test fails at full size (two equal columns of
+    large scale: the Gram's pivot falls to the damping, 1e-6 of its diagonal)
+    reports status 2, and the panel path (ifk_fold_finalize) gives the
     factor, which then runs through the bf16 inverse and apply: factor and
     solves within the bounds of the sweep."""
     p, n_in, n_out, lam = 16384, 4096, 11008, 1e-2
