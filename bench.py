@@ -5,65 +5,69 @@ One step = one factor update plus one preconditioned weight update for a
 single Linear layer, exactly the work IFKFAC.step does for that layer with
 factor_update_freq=1 in bf16 mode:
 
-  fold X (p x n_in) and delta (p x n_out) into fresh R factors and finalize
-  them (scale 1/sqrt(p), damping, positive diagonal, bf16): the hooks hold
-  the chunk of an update step back and the factor update runs fold and
-  finalize as one factorisation per side, the two sides concurrently
-  triangular inverses of both bf16 factors                       (solve setup)
-  nat = (R_G^T R_G)^-1 grad (R_X^T R_X)^-1                       (four solves)
+  the damped bf16 factors of X (p x n_in) and delta (p x n_out), each side by
+  the Gram matrix + blocked Cholesky (the panel TPQRT fold for a side it
+  flags), the two sides concurrently, each side's triangular inverse (with
+  its bf16 copies) right behind its factor                     (factor update)
+  nat = (R_G^T R_G)^-1 grad (R_X^T R_X)^-1 from the inverses    (four solves)
   heavy-ball momentum + weight step                              (update)
 
---unfused times the two-call path instead (fold into the running factor,
-then finalize), which is what get_factors() outside a factor update does.
-
-Default workload: Linear 4096 -> 11008 at p = 16384 rows, inputs resident in
+Headline workload: Linear 4096 -> 11008 at p = 16384 rows, inputs resident in
 HBM.  value = algorithmic TFLOP/s of the step, with the algorithmic count
 2 p (n_in^2 + n_out^2) + 2 n_out n_in (n_in + n_out).
 
+Extra keys on the same JSON line (unless --no-extras): the other benchmark
+layers (Linear 1024 -> 1024 streamed over 8 chunks, 4096 -> 4096 at p = 8192,
+11008 -> 4096 at p = 16384, one ViT-B block's capture folds), IFKFAC.step()
+itself on a Linear(4096, 11008) model and on the 4 x (Linear(4096, 4096) +
+GELU) stack, the same step in fp32 arithmetic (the reference's regime),
+the step under the default hardware-queue count (child process), kappa of
+the damped factors, and a roofline per phase.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       [--no-extras] [--factor-path gram|cqr|panel]
 Prints one JSON line.
 """
 from __future__ import annotations
 
 import argparse
+import contextlib
+import io
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 
 # HIP maps streams onto a pool of hardware queues (GPU_MAX_HW_QUEUES, 4 by
-# default), and streams that share a queue run in submission order.  The step
-# runs on five streams: the main one, one per factor side, and one look-ahead
-# helper per side; with 4 queues the two helpers share one and the output
-# side's far updates wait behind the input side's.  HIP reads the variable
-# when it initialises, so it is raised here, before torch touches the GPU
-# (a larger setting is kept).
-try:
-    _queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "0"))
-except ValueError:
-    _queues = 0
-if _queues < 8:
-    os.environ["GPU_MAX_HW_QUEUES"] = "8"
+# default), and streams that share a queue run in submission order.  A layer's
+# factor update runs each side on its own stream with two helper streams
+# (Gram columns; panel work beside the Cholesky chain), so with 4 queues some
+# of them share one.  HIP reads the variable when it initialises, so it is
+# raised here, before torch touches the GPU (a larger setting is kept); with
+# --hw-queues-default it is left alone (the drop-in user's default).
+if "--hw-queues-default" not in sys.argv:
+    try:
+        _queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "0"))
+    except ValueError:
+        _queues = 0
+    if _queues < 8:
+        os.environ["GPU_MAX_HW_QUEUES"] = "8"
 
 METRIC = "ms per factor-update + precond step per layer; bf16 TFLOP/s vs MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_F32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per launch of the dominant kernel (average over its launches in
-# one step of the 4096 -> 11008, p = 16384 workload), from two rocprofv3 --pmc
-# runs (FETCH_SIZE, WRITE_SIZE) scaled by the same counters on a 256 MiB copy
-# (profiles/pmc_traffic_linear4096x11008_p16384.txt).  Other workloads: None.
-TRAFFIC = {("linear_4096x11008_p16384", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1>>"): 629.73e6,
-           ("linear_4096x11008_p16384", "gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2>>"): 139.69e6}
-
-# Dominant GEMM family by rocprofv3 kernel time over the timed steps, where
-# the per-launch events are skewed (see main): 2 = gemm_bb_kernel 256 tile.
-DOMINANT_FAMILY = {"linear_4096x11008_p16384": 2}
+# HBM bytes per launch of the dominant kernel on the headline workload, from
+# two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same
+# counters on a 256 MiB copy; None until measured for this factor path.
+TRAFFIC = {}
 
 WORKLOADS = {
     # name: (n_in, n_out, p)
     "linear_4096x11008_p16384": (4096, 11008, 16384),
+    "linear_11008x4096_p16384": (11008, 4096, 16384),
     "linear_4096x4096_p8192": (4096, 4096, 8192),
     "linear_1024x1024_p4096": (1024, 1024, 4096),
 }
@@ -71,6 +75,14 @@ WORKLOADS = {
 
 def algorithmic_flops(n_in: int, n_out: int, p: int) -> float:
     return 2.0 * p * (n_in ** 2 + n_out ** 2) + 2.0 * n_out * n_in * (n_in + n_out)
+
+
+def update_flops(n_in: int, n_out: int, p: int) -> float:
+    return 2.0 * p * (n_in ** 2 + n_out ** 2)
+
+
+def precond_flops(n_in: int, n_out: int) -> float:
+    return 2.0 * n_out * n_in * (n_in + n_out)
 
 
 def kappa_matrix(p: int, n: int, kappa: float, seed: int, dtype):
@@ -93,32 +105,287 @@ def kappa_matrix(p: int, n: int, kappa: float, seed: int, dtype):
     return X.to(dtype).contiguous()
 
 
-def cpu_baseline(sample: str, threads: int):
-    """The reference's CPU call sequence (oracle/ref_recipe.py) timed on host cores."""
+def cpu_info(threads: int) -> dict:
+    import torch
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cfg = torch.__config__.show()
+    lapack = "unknown"
+    for key in ("LAPACK is enabled", "BLAS_INFO", "LAPACK_INFO"):
+        for line in cfg.splitlines():
+            if key in line:
+                lapack = line.strip()
+                break
+        if lapack != "unknown":
+            break
+    mkl = [l.strip() for l in cfg.splitlines() if "Math Kernel Library" in l or "MKL" in l[:12]]
+    return {"cpu_model": model, "threads": threads,
+            "lapack": (mkl[0] if mkl else lapack)[:120]}
+
+
+def cpu_baseline(threads: int):
+    """The reference's CPU call sequence (oracle/ref_recipe.py) timed on host cores:
+    one step of the headline layer (a single rep: about half a minute of CPU work),
+    and the median of three steps of Linear 4096 -> 4096 at p = 8192 after a warm-up."""
     import torch
     from oracle import ref_recipe
-    n_in, n_out, p = WORKLOADS[sample]
     torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(0)
-    X = torch.randn(p, n_in, generator=g)
-    D = torch.randn(p, n_out, generator=g)
-    grad = torch.randn(n_out, n_in, generator=g) * 0.1
-    W = torch.randn(n_out, n_in, generator=g) * 0.01
-    t0 = time.perf_counter()
-    ref_recipe.factor_update_precond_step([X], [D], grad, W, None, 1e-3, 0.9, 1e-2, True)
-    dt = time.perf_counter() - t0
+
+    def one(n_in, n_out, p, seed):
+        g = torch.Generator().manual_seed(seed)
+        X = torch.randn(p, n_in, generator=g)
+        D = torch.randn(p, n_out, generator=g)
+        grad = torch.randn(n_out, n_in, generator=g) * 0.1
+        W = torch.randn(n_out, n_in, generator=g) * 0.01
+        t0 = time.perf_counter()
+        ref_recipe.factor_update_precond_step([X], [D], grad, W, None, 1e-3, 0.9, 1e-2, True)
+        return time.perf_counter() - t0
+
+    n_in, n_out, p = WORKLOADS["linear_4096x11008_p16384"]
+    dt = one(n_in, n_out, p, 0)
     fl = algorithmic_flops(n_in, n_out, p)
-    return {
+    s_in, s_out, s_p = WORKLOADS["linear_4096x4096_p8192"]
+    one(s_in, s_out, s_p, 1)   # warm-up
+    reps = sorted(one(s_in, s_out, s_p, 2 + i) for i in range(3))
+    med = reps[1]
+    out = {
         "value": round(fl / dt / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
         "ms_per_step": round(dt * 1e3, 1),
-        "sample": (f"one factor-update + precondition step of Linear {n_in}->{n_out} at "
-                   f"p={p} (bf16 factors) through the reference's torch-CPU call sequence "
-                   f"(LAPACK qr/solve_triangular), {threads} threads, "
-                   f"torch {torch.__version__}"),
+        "sample": (f"one factor-update + precondition step of Linear {n_in}->{n_out} at p={p} "
+                   f"(bf16 factors) through the reference's torch-CPU call sequence (LAPACK "
+                   f"qr/solve_triangular), a single rep, {threads} threads, torch "
+                   f"{torch.__version__}"),
+        "small_sample": {"workload": f"Linear {s_in}->{s_out} p={s_p}",
+                         "ms_per_step_median_of_3": round(med * 1e3, 1),
+                         "tflops": round(algorithmic_flops(s_in, s_out, s_p) / med / 1e12, 4)},
     }
+    out.update(cpu_info(threads))
+    return out
+
+
+def default_queue_child(args) -> dict:
+    """The headline step in a child process left at the default hardware-queue
+    count (HIP reads it at start-up, so it takes a process of its own)."""
+    env = dict(os.environ)
+    env.pop("GPU_MAX_HW_QUEUES", None)
+    cmd = [sys.executable, os.path.abspath(__file__), "--hw-queues-default", "--no-extras",
+           "--no-cpu-baseline", "--steps", str(max(3, args.steps // 2)), "--warmup", "2",
+           "--factor-path", args.factor_path]
+    try:
+        r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+        line = [l for l in r.stdout.strip().splitlines() if l.startswith("{")][-1]
+        d = json.loads(line)
+        return {"ms_per_step": d["ms_per_step"], "value": d["value"],
+                "GPU_MAX_HW_QUEUES": "default (unset)"}
+    except Exception as e:   # reported, never fatal: the headline does not depend on it
+        return {"error": f"{type(e).__name__}: {e}"[:200]}
+
+
+# ----------------------------------------------------------------------------
+# the per-layer chain
+# ----------------------------------------------------------------------------
+class LayerChain:
+    """The backend calls of one IFKFAC step for one Linear layer (factor update
+    with freq 1, bf16 factors), on resident synthetic inputs."""
+
+    def __init__(self, be, n_in, n_out, p, factor_path="gram", math_=1, chunks=1,
+                 kappa_x=1e2, kappa_d=1e1, lam=1e-2, seed=1):
+        import torch
+        self.be, self.n_in, self.n_out, self.p = be, n_in, n_out, p
+        self.path, self.math, self.lam = factor_path, math_, lam
+        self.X = kappa_matrix(p, n_in, kappa_x, seed, torch.bfloat16)
+        self.D = kappa_matrix(p, n_out, kappa_d, seed + 1, torch.bfloat16)
+        self.chunks = chunks
+        gg = torch.Generator(device="cuda").manual_seed(seed + 2)
+        self.grad = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.1
+        self.W = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.01
+        self.buf = torch.zeros_like(self.W)
+        self.dev = torch.device("cuda", 0)
+        self.factors = None
+        if chunks > 1:
+            self.RX = torch.zeros(n_in, n_in, device=self.dev)
+            self.RG = torch.zeros(n_out, n_out, device=self.dev)
+
+    def _side(self, T, R, how):
+        import torch
+        from ifkfac_amd._backend import MATH_BF16
+        be, p = self.be, self.p
+        r = 0
+        last = T
+        if self.chunks > 1:
+            # the hooks fold every chunk but the held one into the running factor
+            q = p // self.chunks
+            for c in range(self.chunks - 1):
+                r = be.fold_(R, r, T[c * q:(c + 1) * q], self.math)
+            last = T[(self.chunks - 1) * q:]
+        out_dtype = torch.bfloat16
+        # as IFKFAC's factor update: the Gram path in bf16 arithmetic,
+        # CholeskyQR2 blocks in fp32 arithmetic
+        gram = how == "gram" and self.math == MATH_BF16
+        cqr = how == "cqr" or (how == "gram" and not gram)
+        F, st = be.fold_finalize(R if r > 0 else None, r, last, 1 / math.sqrt(p), self.lam,
+                                 out_dtype, self.math, cqr=cqr, gram=gram)
+        return F, st, (be.tri_inverse_bf16(F) if self.math == MATH_BF16
+                       else be.tri_inverse(F, 0))
+
+    def factor_update(self):
+        import torch
+        from ifkfac_amd._backend import run_pair
+        RX = getattr(self, "RX", None)
+        RG = getattr(self, "RG", None)
+        out = list(run_pair(self.dev, lambda: self._side(self.X, RX, self.path),
+                            lambda: self._side(self.D, RG, self.path),
+                            b_first=self.n_out > self.n_in))
+        st = torch.cat([out[0][1], out[1][1]]).cpu()
+        for i, (T, R) in enumerate(((self.X, RX), (self.D, RG))):
+            if int(st[i]) == 2:
+                out[i] = self._side(T, R, "panel")
+        self.factors = out
+        return out
+
+    def step(self, first, mark=lambda: None):
+        mark()
+        (_, _, ix), (_, _, ig) = self.factor_update()
+        mark()
+        if self.math == 1:
+            nat = self.be.precondition_apply_bf16(self.grad, (ix[1], ix[2]), (ig[1], ig[2]))
+        else:
+            nat = self.be.precondition_apply(self.grad, ix, ig, 0)
+        mark()
+        self.be.momentum_update_(nat, self.buf, self.W, 1e-3, 0.9, 0.0, first)
+        mark()
+
+
+def timed(fn, steps, warmup):
+    import torch
+    for i in range(warmup):
+        fn(i == 0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn(False)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def extras(be, args, head_kappa):
+    """The other benchmark layers and IFKFAC.step() itself (see the module doc)."""
+    import torch
+    import torch.nn as nn
+    from ifkfac_amd import IFKFAC
+    from ifkfac_amd._backend import MATH_BF16
+    res = {}
+    steps, warm = max(3, args.steps // 2), 2
+
+    def layer(name, n_in, n_out, p, chunks=1, math_=1):
+        c = LayerChain(be, n_in, n_out, p, args.factor_path, math_=math_, chunks=chunks)
+        ms = timed(c.step, steps, warm)
+        del c
+        torch.cuda.empty_cache()
+        return {"ms_per_step": round(ms, 3),
+                "tflops": round(algorithmic_flops(n_in, n_out, p) / ms / 1e9, 1)}
+
+    res["layers"] = {
+        "linear_1024x1024_p4096_8_chunks": layer("c2", 1024, 1024, 4096, chunks=8),
+        "linear_4096x4096_p8192": layer("c3", 4096, 4096, 8192),
+        "linear_11008x4096_p16384": layer("c4b", 11008, 4096, 16384),
+    }
+    h_in, h_out, h_p = WORKLOADS["linear_4096x11008_p16384"]
+    res["fp32_arithmetic"] = dict(layer("fp32", h_in, h_out, h_p, math_=0), **{
+        "note": "the headline step in fp32 arithmetic (CholeskyQR2 fp32 factor update, fp32 "
+                "inverses and solves): the reference's regime"})
+
+    quiet = contextlib.redirect_stdout(io.StringIO())
+
+    # IFKFAC.step() on a Linear(4096, 11008) model: forward and backward outside the timer
+    def ifkfac_model(model, x, target, steps_, warm_):
+        opt = IFKFAC(model, lr=1e-3, damping=1e-2, factor_update_freq=1, momentum=0.9,
+                     use_true_bf16=True)
+        times = []
+        with quiet:
+            for i in range(warm_ + steps_):
+                model.zero_grad(set_to_none=True)
+                loss = ((model(x) - target) ** 2).mean()
+                loss.backward()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                opt.step()
+                torch.cuda.synchronize()
+                if i >= warm_:
+                    times.append((time.perf_counter() - t0) * 1e3)
+        opt.cleanup() if hasattr(opt, "cleanup") else None
+        return sorted(times)[len(times) // 2]
+
+    torch.manual_seed(0)
+    lin = nn.Linear(h_in, h_out, bias=False).cuda()
+    x = kappa_matrix(h_p, h_in, 1e2, 11, torch.float32)
+    tgt = torch.randn(h_p, h_out, device="cuda") * 0.1
+    ms = ifkfac_model(lin, x, tgt, 3, 2)
+    res["ifkfac_step_linear_4096x11008_p16384"] = {
+        "ms_per_step_median": round(ms, 3),
+        "note": "IFKFAC(use_true_bf16=True, factor_update_freq=1, momentum=0.9).step() with "
+                "fp32 activations captured by the hooks; forward and backward untimed"}
+    del lin, x, tgt
+    torch.cuda.empty_cache()
+
+    n, p = 4096, 8192
+    layers = [nn.Linear(n, n) for _ in range(4)]
+    mlp = nn.Sequential(*[m for l in layers for m in (l, nn.GELU())]).cuda()
+    x = kappa_matrix(p, n, 1e2, 12, torch.float32)
+    tgt = torch.randn(p, n, device="cuda") * 0.1
+    ms = ifkfac_model(mlp, x, tgt, 3, 2)
+    res["ifkfac_step_mlp_4x4096_gelu_p8192"] = {
+        "ms_per_step_median": round(ms, 3),
+        "tflops": round(4 * algorithmic_flops(n, n, p) / ms / 1e9, 1),
+        "note": "4 x (Linear(4096, 4096) + GELU), one same-shape bucket, IFKFAC.step() "
+                "end to end; forward and backward untimed"}
+    del mlp, layers, x, tgt
+    torch.cuda.empty_cache()
+
+    # one ViT-B block's factor capture: the folds of one 4096-row batch (both
+    # sides of qkv 768->2304, proj 768->768, fc1 768->3072, fc2 3072->768) into
+    # running factors, then get_factors() once
+    shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+    rows = 4096
+    g = torch.Generator(device="cuda").manual_seed(13)
+    Rs, chunks = [], []
+    for (a, b) in shapes:
+        for nn_ in (a, b):
+            R = torch.zeros(nn_, nn_, device="cuda")
+            T = torch.randn(rows, nn_, device="cuda", generator=g)
+            be.fold_(R, 0, T, MATH_BF16)
+            Rs.append(R)
+            chunks.append(T)
+
+    def batch(_first):
+        for R, T in zip(Rs, chunks):
+            be.fold_(R, R.shape[0], T, MATH_BF16)
+    ms_b = timed(batch, steps, warm)
+    fl_b = sum(2.0 * rows * nn_ ** 2 for (a, b) in shapes for nn_ in (a, b))
+
+    def finalize_all(_first):
+        for R in Rs:
+            be.finalize(R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16, MATH_BF16)
+    ms_f = timed(finalize_all, 3, 1)
+    res["vit_b_block_capture_p4096"] = {
+        "ms_per_batch": round(ms_b, 3), "tflops_per_batch": round(fl_b / ms_b / 1e9, 1),
+        "ms_get_factors": round(ms_f, 3),
+        "note": "8 folds of 4096 rows per batch into running factors (bf16 arithmetic); "
+                "200 batches x 12 blocks take 2400 x ms_per_batch"}
+    del Rs, chunks
+    torch.cuda.empty_cache()
+    res["kappa_R_damped_headline"] = head_kappa
+    return res
 
 
 def main() -> int:
@@ -128,14 +395,14 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="linear_4096x11008_p16384", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", default="linear_4096x4096_p8192", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--hw-queues-default", action="store_true",
+                    help="leave GPU_MAX_HW_QUEUES at HIP's default (used by the child that "
+                         "reports the step under the default)")
     ap.add_argument("--factor-path", default="gram", choices=["gram", "cqr", "panel"],
                     help="the consuming factor update: Gram matrix + blocked Cholesky, "
                          "CholeskyQR2 outer blocks, or the panel TPQRT fold (a side "
                          "flagged by the first two is recomputed by the panel path)")
-    ap.add_argument("--unfused", action="store_true",
-                    help="fold, then finalize (two factorisations per side) instead of the "
-                         "fused fold + finalize of IFKFAC's factor update")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the warmup, copy a device buffer of this many MiB three "
                          "times (a kernel of known HBM traffic for counter calibration)")
@@ -145,15 +412,17 @@ def main() -> int:
               "benchmarked on a single MI355X); run with --gpus 1", file=sys.stderr)
         return 2
 
+    child = None
+    if not args.no_extras and not args.hw_queues_default:
+        child = default_queue_child(args)   # before this process initialises HIP
+
     import torch
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from ifkfac_amd import _backend, _lib
-    from ifkfac_amd._backend import MATH_BF16, run_pair
 
     be = _backend.get_backend()
     lib = be.lib
     n_in, n_out, p = WORKLOADS[args.workload]
-    lam, lr, mom = 1e-2, 1e-3, 0.9
     torch.cuda.set_device(0)
 
     if args.calib_copy_mib > 0:
@@ -164,85 +433,24 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    X = kappa_matrix(p, n_in, 1e2, 1, torch.bfloat16)
-    D = kappa_matrix(p, n_out, 1e1, 2, torch.bfloat16)
-    gg = torch.Generator(device="cuda").manual_seed(3)
-    grad = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.1
-    W = torch.randn(n_out, n_in, device="cuda", generator=gg) * 0.01
-    buf = torch.zeros_like(W)
-    dev = torch.device("cuda", 0)
-    if args.unfused:
-        R_X = torch.zeros(n_in, n_in, device=dev)
-        R_G = torch.zeros(n_out, n_out, device=dev)
-    scale = 1.0 / math.sqrt(p)
-    if args.unfused:
-        phase_names = ["fold_X", "fold_G", "finalize", "tri_inverse", "precondition", "update"]
-    else:
-        # each side's inverse follows its factor on its stream
-        phase_names = ["fold_finalize_and_inverse", "precondition", "update"]
+    chain = LayerChain(be, n_in, n_out, p, args.factor_path)
+    phase_names = ["factor_update_and_inverse", "precondition", "update"]
     nph = len(phase_names)
 
-    def factors(mark):
-        if args.unfused:
-            be.fold_(R_X, 0, X, MATH_BF16)
-            mark()
-            be.fold_(R_G, 0, D, MATH_BF16)
-            mark()
-            # input and output sides are independent, as in IFKFAC._update_factors
-            return run_pair(dev,
-                            lambda: be.finalize(R_X, scale, lam, torch.bfloat16, MATH_BF16),
-                            lambda: be.finalize(R_G, scale, lam, torch.bfloat16, MATH_BF16),
-                            b_first=n_out > n_in)
-        # RawActivationHooks._collect_factors(consume=True) of the update step,
-        # as IFKFAC._update_factors calls it: outer blocks by CholeskyQR2, each
-        # side's inverse (with its bf16 copies) right after its factor on its
-        # stream, then one host read of the status flags and the panel path
-        # (and the inverse again) for a side whose blocks were too
-        # ill-conditioned
-        def side(T, how):
-            F, st = be.fold_finalize(None, 0, T, scale, lam, torch.bfloat16, MATH_BF16,
-                                     cqr=how == "cqr", gram=how == "gram")
-            return F, st, be.tri_inverse_bf16(F)
-        out = list(run_pair(dev, lambda: side(X, args.factor_path),
-                            lambda: side(D, args.factor_path), b_first=n_out > n_in))
-        st = torch.cat([out[0][1], out[1][1]]).cpu()
-        for i, T in enumerate((X, D)):
-            if int(st[i]) == 2:
-                out[i] = side(T, "panel")
-        return out
-
-    def step(first: bool, events=None):
-        k = [0]
-
-        def mark():
-            if events is not None:
-                events[k[0]].record()
-            k[0] += 1
-        mark()
-        if args.unfused:
-            (FX, _), (FG, _) = factors(mark)
-            mark()
-            (_, ZXb, ZXt), (_, ZGb, ZGt) = run_pair(dev, lambda: be.tri_inverse_bf16(FX),
-                                                    lambda: be.tri_inverse_bf16(FG),
-                                                    b_first=n_out > n_in)
-        else:
-            (_, _, (_, ZXb, ZXt)), (_, _, (_, ZGb, ZGt)) = factors(mark)
-        mark()
-        # IFKFAC._nat_grad in bf16 arithmetic: the apply from the inverses' copies
-        nat = be.precondition_apply_bf16(grad, (ZXb, ZXt), (ZGb, ZGt))
-        mark()
-        be.momentum_update_(nat, buf, W, lr, mom, 0.0, first)
-        mark()
-
     for i in range(args.warmup):
-        step(i == 0)
+        chain.step(i == 0)
     torch.cuda.synchronize()
 
-    # one untimed step with every GEMM launch bracketed by events: find the
-    # dominant GEMM variant and the per-phase split
+    # one untimed step with every GEMM launch bracketed by events: the GEMM
+    # variants and the per-phase split
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(nph + 1)]
+    k = [0]
+
+    def mark():
+        ev[k[0]].record()
+        k[0] += 1
     _lib.check(lib.ifk_profile_begin(-2), "profile_begin")
-    step(False, ev)
+    chain.step(False, mark)
     n = _lib.ctypes.c_int64(0)
     _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
     torch.cuda.synchronize()
@@ -271,25 +479,18 @@ def main() -> int:
         a[1] += 1
         a[2] += fl
         a[3] += by
-    # dominant GEMM kernel (family as rocprofv3 reports kernels: 0 gemm_kernel,
-    # 1 gemm_big_kernel, 2 / 3 gemm_bb_kernel with its 256 / 128 tile), timed
-    # over all of its launches
+
+    # the dominant GEMM kernel family (as rocprofv3 names kernels: 0
+    # gemm_kernel, 1 gemm_big_kernel, 2 / 3 gemm_bb_kernel with its 256 / 128
+    # tile) by algorithmic flops in the survey step, timed over the timed steps
     def family(vid):
         if (vid >> 6) & 1:
             return 3 if (vid >> 7) & 1 else 2
         return (vid >> 5) & 1
-    fam_ms = {0: 0.0, 1: 0.0, 2: 0.0, 3: 0.0}
+    fam_fl = {0: 0.0, 1: 0.0, 2: 0.0, 3: 0.0}
     for vid, a in per_variant.items():
-        fam_ms[family(vid)] += a[0]
-    fam = max(fam_ms, key=fam_ms.get)
-    # The events bracket each launch on its stream, so they also count the
-    # time a launch waits for CUs held by the other streams' kernels: that
-    # inflates the many short 128-tile launches of the block factorisations.
-    # On the named workload the rocprofv3 kernel trace of the timed steps
-    # puts the 256-tile kernel first (10.8 ms per step against 9.0), and its
-    # event durations agree with the trace to within 7 %, so it is the one
-    # reported there.
-    fam = DOMINANT_FAMILY.get(args.workload, fam)
+        fam_fl[family(vid)] += a[2]
+    fam = max(fam_fl, key=fam_fl.get)
     arm = {0: -4, 1: -3, 2: -5, 3: -6}[fam]
     kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1>>",
              3: "gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2>>"}[fam]
@@ -298,7 +499,7 @@ def main() -> int:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(False)
+        chain.step(False)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
@@ -324,7 +525,7 @@ def main() -> int:
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak_flops,
                 "unit": "TFLOP/s", "frac": round(achieved / peak_flops, 4)}
     roof.update({
-        "traffic": TRAFFIC.get((args.workload, kname)),
+        "traffic": TRAFFIC.get((args.workload, args.factor_path, kname)),
         "kernel": kname + {0: " (128x128 MFMA)", 1: " (256x128x32 bf16 MFMA, register staged)",
                            2: " (256x256x32 bf16 MFMA, direct-to-LDS ring)",
                            3: " (128x128x32 bf16 MFMA, direct-to-LDS ring)"}[fam],
@@ -335,6 +536,33 @@ def main() -> int:
         "algorithmic_flops_per_launch": round(tot_fl / max(len(recs), 1)),
         "algorithmic_bytes_per_launch": round(tot_by / max(len(recs), 1)),
     })
+    # a roofline per phase: algorithmic work over the phase's time in the
+    # survey step (the whole GPU, all streams)
+    ph_upd = phases["factor_update_and_inverse"]
+    ph_pre = phases["precondition"]
+    ph_mom = phases["update"]
+    upd_fl = update_flops(n_in, n_out, p)
+    pre_fl = precond_flops(n_in, n_out)
+    mom_by = 20.0 * n_in * n_out   # read nat, read/write buf, read/write W (fp32)
+    phase_roofs = {
+        "factor_update_and_inverse": {"bound": "mfma", "achieved": round(upd_fl / ph_upd / 1e9, 1),
+                                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                      "frac": round(upd_fl / ph_upd / 1e9 / PEAK_BF16_TFLOPS, 4),
+                                      "algorithmic": "2 p (n_in^2 + n_out^2)"},
+        "precondition": {"bound": "mfma", "achieved": round(pre_fl / ph_pre / 1e9, 1),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pre_fl / ph_pre / 1e9 / PEAK_BF16_TFLOPS, 4),
+                         "algorithmic": "2 n_out n_in (n_in + n_out)"},
+        "update": {"bound": "hbm", "achieved": round(mom_by / ph_mom / 1e6, 1),
+                   "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                   "frac": round(mom_by / ph_mom / 1e6 / PEAK_HBM_GBS, 4),
+                   "algorithmic": "20 n_out n_in bytes"},
+    }
+    # kappa_2 of the damped factors of the timed step
+    (FX, _, ix), (FG, _, ig) = chain.factors
+    kx = float(be.cond_estimate(FX, ix[0]).item())
+    kg = float(be.cond_estimate(FG, ig[0]).item())
+    head_kappa = {"R_X": round(kx, 4), "R_G": round(kg, 4)}
 
     out = {
         "metric": METRIC,
@@ -353,23 +581,31 @@ def main() -> int:
         "config": {
             "workload": f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, "
                         f"p={p} rows, bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9",
-            "factor_path": "fold then finalize" if args.unfused else {
-                "gram": "fused fold + finalize: Gram matrix + 1024-block Cholesky with split-bf16 "
-                        "updates (panel path if flagged)",
-                "cqr": "fused fold + finalize, 1024-column blocks by CholeskyQR2 (panel path if "
-                       "flagged)",
-                "panel": "fused fold + finalize, panel TPQRT fold"}[args.factor_path],
+            "factor_path": {
+                "gram": "Gram matrix + 1024-block Cholesky with split-bf16 updates (panel path "
+                        "if flagged)",
+                "cqr": "1024-column blocks by CholeskyQR2 (panel path if flagged)",
+                "panel": "panel TPQRT fold"}[args.factor_path],
             "n_in": n_in, "n_out": n_out, "p": p, "algorithmic_gflop_per_step": round(flops / 1e9, 1),
             "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
+            "GPU_MAX_HW_QUEUES": os.environ.get("GPU_MAX_HW_QUEUES", "default (unset)"),
         },
         "phases_ms": phases,
         "roofline": roof,
-        "gemm_variants_ms_per_step": {str(k): round(v[0], 3) for k, v in
+        "phase_rooflines": phase_roofs,
+        "kappa_R_damped": head_kappa,
+        "gemm_variants_ms_per_step": {str(kk): round(v[0], 3) for kk, v in
                                       sorted(per_variant.items(), key=lambda kv: -kv[1][0])},
     }
+    if child is not None:
+        out["default_hw_queues"] = child
+    if not args.no_extras:
+        del chain
+        torch.cuda.empty_cache()
+        out["extras"] = extras(be, args, head_kappa)
     if not args.no_cpu_baseline:
-        threads = min(os.cpu_count() or 1, 16)
-        out["cpu_baseline"] = cpu_baseline(args.cpu_sample, threads)
+        # the cores this process may run on (a container's share, not the host's count)
+        out["cpu_baseline"] = cpu_baseline(len(os.sched_getaffinity(0)) or 1)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
