@@ -110,7 +110,7 @@ class HipBackend:
 
     def fold_finalize(self, R: Optional[torch.Tensor], r_in: int, X: torch.Tensor, scale: float,
                       damping: float, out_dtype: torch.dtype, math: int,
-                      cqr: bool = False, gram: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+                      cqr: bool = False, gram: bool = False, with_kappa: bool = False):
         """finalize(fold(R[:r_in], X)) in one factorisation, leaving R untouched.
 
         Returns (R_damped, finite flag int32[1]); R (n x n fp32 buffer whose
@@ -120,7 +120,9 @@ class HipBackend:
         factor is the Cholesky factor of the Gram matrix
         (ifk_fold_finalize_gram).  Either way the flag is then 1 / 0 as
         above, or 2 when the input was too ill-conditioned for that method --
-        the caller must then call again with neither.
+        the caller must then call again with neither.  With ``with_kappa``
+        (Gram path) a third value is returned: a device float[1] upper bound
+        of kappa_2 of the factor.
         """
         X, ldx, xdt = _mat(X, "fold_finalize")
         p, n = X.shape
@@ -135,19 +137,21 @@ class HipBackend:
             ldr = R.stride(0) if R.shape[0] > 1 else n
         out = torch.empty((n, n), dtype=out_dtype, device=X.device)
         flag = torch.empty(1, dtype=torch.int32, device=X.device)
+        kb = torch.empty(1, dtype=torch.float32, device=X.device) if (gram and with_kappa) else None
         if gram and math != MATH_BF16:
             raise IFKFACBackendError("fold_finalize: the Gram path is bf16 arithmetic only")
         name = ("ifk_fold_finalize_gram" if gram else
                 "ifk_fold_finalize_cqr" if cqr else "ifk_fold_finalize")
         ws = self._ws(getattr(self.lib, name + "_workspace_size")(p, n, int(r_in)), X.device)
+        extra = (_ptr(kb),) if gram else ()
         with torch.cuda.device(X.device):
             rc = getattr(self.lib, name)(self._stream(X.device), _ptr(X), xdt, p, n, ldx,
                                          _ptr(R) if r_in > 0 else None, ldr, int(r_in),
                                          float(scale), float(damping), _ptr(out),
-                                         _DT[out_dtype], n, int(math), _ptr(flag), _ptr(ws),
-                                         ws.numel())
+                                         _DT[out_dtype], n, int(math), _ptr(flag), *extra,
+                                         _ptr(ws), ws.numel())
         _lib.check(rc, name)
-        return out, flag
+        return (out, flag, kb) if kb is not None else (out, flag)
 
     # -- preconditioning ------------------------------------------------------------
     def tri_inverse(self, R: torch.Tensor, math: int) -> torch.Tensor:

@@ -234,18 +234,21 @@ class RawActivationHooks(GramMatrixEstimator):
 
     def _damped(self, side: str, module: nn.Module, rows: int, out_dtype: torch.dtype,
                 fast: bool = False):
-        """Damped factor of one side; a held chunk goes into a fused fold +
-        finalize.  With ``fast`` that factorisation is the Gram matrix +
-        blocked Cholesky in bf16 arithmetic, CholeskyQR2 outer blocks in fp32
-        arithmetic; its flag may then be 2 (see _retry_cholesky_qr)."""
+        """(R_damped, flag, kappa bound or None) of one side; a held chunk goes
+        into a fused fold + finalize.  With ``fast`` that factorisation is the
+        Gram matrix + blocked Cholesky in bf16 arithmetic (which also bounds
+        kappa_2 of the factor), CholeskyQR2 outer blocks in fp32 arithmetic;
+        its flag may then be 2 (see _retry_cholesky_qr)."""
         R, r, chunk, _ = self._side_state(side, module)
         if chunk is None:
-            return self._finalize(R, rows, out_dtype)
+            return self._finalize(R, rows, out_dtype) + (None,)
         bufs = self._buf_X if side == "X" else self._buf_G
-        return get_backend().fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
-                                           1.0 / math.sqrt(rows), self.damping, out_dtype,
-                                           self.math, cqr=fast and self.math != MATH_BF16,
-                                           gram=fast and self.math == MATH_BF16)
+        gram = fast and self.math == MATH_BF16
+        res = get_backend().fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
+                                          1.0 / math.sqrt(rows), self.damping, out_dtype,
+                                          self.math, cqr=fast and not gram, gram=gram,
+                                          with_kappa=gram)
+        return res if gram else res + (None,)
 
     def _retry_cholesky_qr(self, factors, flags, extras, then, out_dtype: torch.dtype):
         """One host read of the flags of a consuming factor update: a side too
@@ -261,13 +264,13 @@ class RawActivationHooks(GramMatrixEstimator):
                 rows = self._n_rows_X[m] if side == "X" else self._n_rows_G[m]
                 logger.debug("get_factors() [%s]: %s factor by the panel path",
                              _module_tag(m), side)
-                R, f = self._damped(side, m, rows, out_dtype, fast=False)
+                R, f, kb = self._damped(side, m, rows, out_dtype, fast=False)
                 fac, fl = list(factors[m]), list(flags[m])
                 fac[j], fl[j] = R, f
                 factors[m], flags[m] = tuple(fac), tuple(fl)
                 if then is not None:
                     ex = list(extras[m])
-                    ex[j] = then(side, m, R)
+                    ex[j] = then(side, m, R, kb)
                     extras[m] = tuple(ex)
 
     # ------------------------------------------------------------------ factors
@@ -283,7 +286,9 @@ class RawActivationHooks(GramMatrixEstimator):
         chunk goes into a fused fold + finalize and the running factor is
         left as it was (it is about to be dropped); otherwise held chunks are
         folded first, exactly as get_factors leaves them.  ``then(side,
-        module, R)`` runs on each side's stream right after its factor (work
+        module, R, kappa_bound)`` runs on each side's stream right after its
+        factor (kappa_bound: the Gram path's device bound of kappa_2(R), or
+        None) (work
         that depends on one side only starts while the other is still being
         factored); its results come back as the third value, per module as
         (X side, G side), or None without ``then``."""
@@ -296,8 +301,8 @@ class RawActivationHooks(GramMatrixEstimator):
         extras: Dict[nn.Module, tuple] = {}
 
         def side(s, module, rows, fast):
-            R, f = self._damped(s, module, rows, out_dtype, fast=fast)
-            return R, f, (then(s, module, R) if then is not None else None)
+            R, f, kb = self._damped(s, module, rows, out_dtype, fast=fast)
+            return R, f, (then(s, module, R, kb) if then is not None else None)
         for module in self._linear_layers:
             R_X_raw, _, chunk_X, r_X = self._side_state("X", module)
             R_G_raw, _, chunk_G, r_G = self._side_state("G", module)

@@ -111,11 +111,12 @@ size_t ifk_fold_finalize_gram_workspace_size(int64_t p, int64_t n, int64_t r_in)
 int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
                            int64_t ldx, const float* R_in, int64_t ldr, int64_t r_in, float scale,
                            float damping, void* out, int out_dtype, int64_t ldo, int math,
-                           int32_t* status, void* workspace, size_t workspace_bytes) {
+                           int32_t* status, float* kappa_bound, void* workspace,
+                           size_t workspace_bytes) {
   GUARD(dt_ok(x_dtype) && dt_ok(out_dtype) && math_ok(math),
         "fold_finalize_gram: bad dtype or math code");
   return fold_finalize_gram((hipStream_t)stream, X, x_dtype, p, n, ldx, R_in, ldr, r_in, scale,
-                            damping, out, out_dtype, ldo, math, status, workspace,
+                            damping, out, out_dtype, ldo, math, status, kappa_bound, workspace,
                             workspace_bytes);
 }
 

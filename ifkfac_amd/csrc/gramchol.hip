@@ -209,6 +209,41 @@ __global__ void add_diag_ref_kernel(float* A, int64_t lda, int64_t n, float v, f
   }
 }
 
+// Sum of squares of a Gram column block's lower part (rows x W at A, row
+// stride lda; the block's diagonal at its top, entries above it ignored),
+// off-diagonal entries counted twice (they stand for both triangles): one
+// partial per workgroup into part[blockIdx.x], in a fixed order, so the
+// result does not depend on scheduling.
+constexpr int FROB_WG = 64;
+__global__ __launch_bounds__(256) void gram_frob_kernel(const float* A, int64_t lda, int64_t rows,
+                                                        int64_t W, float* part) {
+  __shared__ float red[4];
+  float acc = 0.0f;
+  const int64_t total = rows * W;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)FROB_WG * 256) {
+    const int64_t r = e / W, c = e - r * W;
+    if (r < c) continue;
+    const float v = A[r * lda + c];
+    acc = fmaf(r == c ? v : 2.0f * v, v, acc);
+  }
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// *kb = sqrt(1 + scale^2 sqrt(sum of the count partials) / damping): with
+// E = scale^2 P^T P, kappa_2(R)^2 = kappa(E + damping I)
+// <= 1 + ||E||_2 / damping <= 1 + ||E||_F / damping.  Infinite without damping.
+__global__ void kappa_bound_kernel(const float* part, int count, float scale, float damping,
+                                   float* kb) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  double ss = 0.0;
+  for (int i = 0; i < count; ++i) ss += (double)part[i];
+  const double e = (double)scale * (double)scale * sqrt(ss);
+  *kb = damping > 0.0f ? (float)sqrt(1.0 + e / (double)damping) : INFINITY;
+}
+
 unsigned grid_of(int64_t work, int64_t cap = 2048) {
   int64_t g = cdiv(work, 256);
   if (g < 1) g = 1;
@@ -285,6 +320,7 @@ struct GramWs {
   bf16_t* LA;         // panel l at columns 3 GB l: [L_hi | L_lo | L_hi], n x ldl
   bf16_t* LB;         // panel l at columns 3 GB l: [L_lo | L_hi | L_hi], n x ldl
   int* flag;
+  float* frob;        // per Gram column, FROB_WG partial sums of squares
   SplitScratch sp, sp2, sp3;   // split-K partials of the three streams
 };
 
@@ -309,6 +345,7 @@ void plan_gram(Arena& a, int64_t pe, int64_t n, GramWs& w) {
   w.LA = a.take<bf16_t>(big * w.ldl);
   w.LB = a.take<bf16_t>(big * w.ldl);
   w.flag = a.take<int>(64);
+  w.frob = a.take<float>((size_t)nb * FROB_WG);
   // split-K partials for the products with one block column of output
   w.sp.floats = (size_t)std::min<int64_t>(n, 8 * GB) * GB * 2;
   w.sp.p = a.take<float>(w.sp.floats);
@@ -343,6 +380,9 @@ int gram_column(hipStream_t s, GramWs& w, int64_t n, int64_t c, float c2, bool h
   } else {
     RC(launch_zero(s, Ac, w.lda, rows, W));
   }
+  hipLaunchKernelGGL(gram_frob_kernel, dim3(FROB_WG), dim3(256), 0, s, Ac, w.lda, rows, W,
+                     w.frob + c * FROB_WG);
+  RC(check_launch("gram_frob"));
   hipLaunchKernelGGL(add_diag_ref_kernel, dim3(grid_of(W, 64)), dim3(256), 0, s, Ac, w.lda, W, c2,
                      w.dref + b.r0);
   return check_launch("add_diag_ref");
@@ -421,8 +461,8 @@ size_t fold_finalize_gram_ws(int64_t p, int64_t n, int64_t r_in) {
 
 int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
                        const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
-                       void* out, int odt, int64_t ldo, int math, int* status, void* ws,
-                       size_t ws_bytes) {
+                       void* out, int odt, int64_t ldo, int math, int* status, float* kappa_bound,
+                       void* ws, size_t ws_bytes) {
   if (n < 1 || p < 0 || r_in < 0 || r_in > n || (p > 0 && (!X || ldx < n)) ||
       (r_in > 0 && (!R_in || ldr < n)) || !out || ldo < n || !(scale > 0.0f) ||
       !(damping >= 0.0f) || (xdt != DT_F32 && xdt != DT_BF16) ||
@@ -513,6 +553,11 @@ int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t
   }
   RC(launch_fill_int(s, status, 1, 1));
   RC(cast_lower_t(s, w.Aw, w.lda, n, scale, out, odt, ldo, status));
+  if (kappa_bound) {
+    hipLaunchKernelGGL(kappa_bound_kernel, dim3(1), dim3(64), 0, s, w.frob, (int)(nb * FROB_WG),
+                       scale, damping, kappa_bound);
+    RC(check_launch("kappa_bound"));
+  }
   return launch_status_merge(s, status, w.flag);
 }
 

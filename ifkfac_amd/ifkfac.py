@@ -144,14 +144,16 @@ class IFKFAC(torch.optim.Optimizer):
         be = get_backend()
         copies = hasattr(be, "tri_inverse_bf16")
 
-        def inverse(side, module, R):
+        def inverse(side, module, R, kappa_bound=None):
             m = solve_math_for(R.dtype)
             if m == MATH_BF16 and copies:
                 # bf16 arithmetic: keep the bf16 copies of Z and Z^T next to Z,
-                # so the per-step apply does not cast the inverses again, and
-                # estimate kappa_2(R) for the choice of arithmetic
+                # so the per-step apply does not cast the inverses again.  The
+                # choice of arithmetic needs kappa_2(R): the Gram path's upper
+                # bound when the factor came from it, else an estimate
                 Z, Zb, ZT = be.tri_inverse_bf16(R)
-                return Z, Zb, ZT, be.cond_estimate(R, Z)
+                k = kappa_bound if kappa_bound is not None else be.cond_estimate(R, Z)
+                return Z, Zb, ZT, k
             return be.tri_inverse(R, m)
 
         try:

@@ -141,13 +141,17 @@ int ifk_fold_finalize_cqr(void* stream, const void* X, int x_dtype, int64_t p, i
  * pivot fell below 1e-3 of its column's Gram diagonal (more cancellation
  * than the Gram matrix's rounding leaves room for): the output is then
  * meaningless and ifk_fold_finalize, on the same inputs, computes the
- * factor.  status must not be NULL.
+ * factor.  status must not be NULL.  kappa_bound (device float, may be
+ * NULL) receives an upper bound of kappa_2(R) from the Gram matrix,
+ * sqrt(1 + ||scale^2 P^T P||_F / damping) (infinite without damping): the
+ * choice between bf16 and fp32-accurate solves needs no power iteration.
  */
 size_t ifk_fold_finalize_gram_workspace_size(int64_t p, int64_t n, int64_t r_in);
 int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
                            int64_t ldx, const float* R_in, int64_t ldr, int64_t r_in, float scale,
                            float damping, void* out, int out_dtype, int64_t ldo, int math,
-                           int32_t* status, void* workspace, size_t workspace_bytes);
+                           int32_t* status, float* kappa_bound, void* workspace,
+                           size_t workspace_bytes);
 
 /*
  * Triangular inverse Z = R^{-1} of an upper-triangular n x n factor (dtype

@@ -47,21 +47,30 @@ class OracleBackend:
     # block (status 2), as ifk_fold_finalize_cqr does, once per call
     cqr_status2 = 0
 
-    def fold_finalize(self, R, r_in, X, scale, damping, out_dtype, math, cqr=False):
+    def fold_finalize(self, R, r_in, X, scale, damping, out_dtype, math, cqr=False, gram=False,
+                      with_kappa=False):
+        """The fused fold + finalize; with cqr or gram the fast variants' status 2 can
+        be injected (cqr_status2), and with_kappa returns the Gram path's kappa bound
+        sqrt(1 + ||scale^2 P^T P||_F / damping) as a third value."""
         self.calls["fold_finalize"] += 1
-        if cqr:
-            self.calls["fold_finalize_cqr"] += 1
+        if cqr or gram:
+            self.calls["fold_finalize_cqr" if cqr else "fold_finalize_gram"] += 1
             if self.cqr_status2 > 0:
                 self.cqr_status2 -= 1
                 n = X.shape[1]
-                return torch.full((n, n), float("nan")).to(out_dtype), torch.tensor(
-                    [2], dtype=torch.int32)
+                out = (torch.full((n, n), float("nan")).to(out_dtype),
+                       torch.tensor([2], dtype=torch.int32))
+                return out + (torch.tensor([float("inf")]),) if (gram and with_kappa) else out
         old = None if r_in == 0 else _np(R[:r_in])
         new = O.streaming_tsqr_update(old, _np(X))
         assert new.shape[0] == new.shape[1], "fused finalize of a partial-rank factor"
         Rd = O.finalize_R(new * scale, damping)
         out = torch.from_numpy(Rd).float().to(out_dtype)
         flag = torch.tensor([1 if np.all(np.isfinite(Rd)) else 0], dtype=torch.int32)
+        if gram and with_kappa:
+            E = scale * scale * (new.T @ new)
+            kb = float(np.sqrt(1.0 + np.linalg.norm(E) / damping)) if damping > 0 else float("inf")
+            return out, flag, torch.tensor([kb], dtype=torch.float32)
         return out, flag
 
     def tri_inverse(self, R, math):

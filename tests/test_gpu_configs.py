@@ -200,7 +200,8 @@ def test_mlp_4x4096_gelu_ifkfac_step_bf16(hip):
     """4 x (Linear(4096, 4096) + GELU), p = 8192 tokens with kappa(X) = 1e2 input,
     IFKFAC(use_true_bf16=True, factor_update_freq=1, momentum=0.9).step(): all
     four layers go through one same-shape bucket; each layer's solves run in bf16
-    arithmetic when both its factors have kappa_2 <= 1.5 and in fp32 otherwise
+    arithmetic when the Gram path's upper bound of kappa_2 of both its factors
+    is at most 1.5, and in fp32 otherwise
     (the first layer's input is near-isotropic after damping, the GELU inputs
     of layers 2-4 are not); every layer's bf16 factors
     against its captured activations and deltas (the sweep's Gram bound); each
@@ -236,7 +237,11 @@ def test_mlp_4x4096_gelu_ifkfac_step_bf16(hip):
         bf16_solves = max(kx, kg) <= KAPPA_BF16_MAX
         assert (l in opt._inverse_copies) == bf16_solves
         kx_true = kappa_of_gram(RX.double().t() @ RX.double())
-        assert 0.9 * kx_true <= kx <= 1.001 * kx_true   # a lower bound within 10 %
+        # the Gram path's bound sqrt(1 + ||X^T X / p||_F / lam) bounds kappa_2 of
+        # the exact factor; the bf16 rounding of the stored one moves its kappa by
+        # up to about 2^-8 relative (measured 0.17 % above a tight bound: the
+        # GELU inputs' Gram matrix is dominated by one mean direction)
+        assert kx >= 0.99 * kx_true
         assert RX.dtype == torch.bfloat16 and RG.dtype == torch.bfloat16
         A, G = damped_gram(acts[l], lam), damped_gram(grads[l], lam)
         for Fm, M in ((RX, A), (RG, G)):

@@ -9,6 +9,8 @@ bf16(X)^T bf16(X)) / rows + lambda I), computed in fp64.  Bounds:
                 product) and the fp32 accumulation; a forgotten lo term
                 (2^-9 per entry) or a dropped Schur update fails it.
   bf16 output   exactly the RNE cast of the fp32 output.
+  kappa bound   sqrt(1 + ||P^T P / rows||_F / lambda) to 1e-4 (fp64 formula on the
+                same rows), and never below kappa_2 of the fp64 factor.
   status        1 for well-posed input; 2 when a pivot falls below 1e-3 of its
                 Gram diagonal (rank deficiency without damping) or the input is
                 not finite; the panel path then gives the factor or flag 0.
@@ -77,8 +79,15 @@ def test_fold_finalize_gram_matches_closed_form(hip, prev, p, n, lam):
     assert e <= 3e-5
     Rg = Rd.double().cpu().numpy()
     assert np.all(np.diag(Rg) > 0) and not np.any(np.tril(Rg, -1))
-    Rb, st = hip.fold_finalize(R, r, X, 1 / math.sqrt(rows), lam, torch.bfloat16, 1, gram=True)
+    Rb, st, kb = hip.fold_finalize(R, r, X, 1 / math.sqrt(rows), lam, torch.bfloat16, 1,
+                                   gram=True, with_kappa=True)
     assert st.item() == 1 and torch.equal(Rb, Rd.to(torch.bfloat16))
+    # kappa bound: sqrt(1 + ||P^T P / rows||_F / lam) of the same rows, never below
+    # kappa_2 of the factor
+    P = np.concatenate(parts, axis=0)
+    want_kb = math.sqrt(1.0 + np.linalg.norm(P.T @ P / rows) / lam)
+    assert abs(kb.item() - want_kb) <= 1e-4 * want_kb
+    assert kb.item() >= (1 - 1e-4) * _kappa(want)
 
 
 @pytest.mark.parametrize("p,n,kappa", [(4096, 1024, 1e2), (6000, 2600, 1e1), (8192, 3072, 1e2),
