@@ -210,21 +210,33 @@ __global__ void add_diag_ref_kernel(float* A, int64_t lda, int64_t n, float v, f
 }
 
 // Sum of squares of a Gram column block's lower part (rows x W at A, row
-// stride lda; the block's diagonal at its top, entries above it ignored),
-// off-diagonal entries counted twice (they stand for both triangles): one
-// partial per workgroup into part[blockIdx.x], in a fixed order, so the
+// stride lda a multiple of 4, A 16-byte aligned, W <= 1024; the block's
+// diagonal at its top, entries above it ignored), off-diagonal entries
+// counted twice (they stand for both triangles): workgroup g takes rows g,
+// g + FROB_WG, ... with four consecutive columns per thread (one float4 when
+// all four lie in the block) and writes one partial to part[g], so the
 // result does not depend on scheduling.
-constexpr int FROB_WG = 64;
+constexpr int FROB_WG = 1024;
 __global__ __launch_bounds__(256) void gram_frob_kernel(const float* A, int64_t lda, int64_t rows,
                                                         int64_t W, float* part) {
   __shared__ float red[4];
   float acc = 0.0f;
-  const int64_t total = rows * W;
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)FROB_WG * 256) {
-    const int64_t r = e / W, c = e - r * W;
-    if (r < c) continue;
-    const float v = A[r * lda + c];
-    acc = fmaf(r == c ? v : 2.0f * v, v, acc);
+  const int64_t c = (int64_t)threadIdx.x * 4;
+  if (c < W) {
+    for (int64_t r = blockIdx.x; r < rows; r += FROB_WG) {
+      float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (c + 3 < W) {
+        const float4 v = *reinterpret_cast<const float4*>(A + r * lda + c);
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+      } else {
+        for (int u = 0; c + u < W; ++u) x[u] = A[r * lda + c + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t cc = c + u;
+        if (cc < W && cc <= r) acc = fmaf(cc == r ? x[u] : 2.0f * x[u], x[u], acc);
+      }
+    }
   }
   for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
@@ -234,14 +246,23 @@ __global__ __launch_bounds__(256) void gram_frob_kernel(const float* A, int64_t 
 
 // *kb = sqrt(1 + scale^2 sqrt(sum of the count partials) / damping): with
 // E = scale^2 P^T P, kappa_2(R)^2 = kappa(E + damping I)
-// <= 1 + ||E||_2 / damping <= 1 + ||E||_F / damping.  Infinite without damping.
-__global__ void kappa_bound_kernel(const float* part, int count, float scale, float damping,
-                                   float* kb) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// <= 1 + ||E||_2 / damping <= 1 + ||E||_F / damping.  Infinite without
+// damping.  256 threads: strided sums in a fixed order, then a fixed tree.
+__global__ __launch_bounds__(256) void kappa_bound_kernel(const float* part, int count,
+                                                          float scale, float damping, float* kb) {
+  __shared__ double red[256];
   double ss = 0.0;
-  for (int i = 0; i < count; ++i) ss += (double)part[i];
-  const double e = (double)scale * (double)scale * sqrt(ss);
-  *kb = damping > 0.0f ? (float)sqrt(1.0 + e / (double)damping) : INFINITY;
+  for (int i = threadIdx.x; i < count; i += 256) ss += (double)part[i];
+  red[threadIdx.x] = ss;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double e = (double)scale * (double)scale * sqrt(red[0]);
+    *kb = damping > 0.0f ? (float)sqrt(1.0 + e / (double)damping) : INFINITY;
+  }
 }
 
 unsigned grid_of(int64_t work, int64_t cap = 2048) {
@@ -554,7 +575,7 @@ int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t
   RC(launch_fill_int(s, status, 1, 1));
   RC(cast_lower_t(s, w.Aw, w.lda, n, scale, out, odt, ldo, status));
   if (kappa_bound) {
-    hipLaunchKernelGGL(kappa_bound_kernel, dim3(1), dim3(64), 0, s, w.frob, (int)(nb * FROB_WG),
+    hipLaunchKernelGGL(kappa_bound_kernel, dim3(1), dim3(256), 0, s, w.frob, (int)(nb * FROB_WG),
                        scale, damping, kappa_bound);
     RC(check_launch("kappa_bound"));
   }
