@@ -79,25 +79,53 @@ constexpr float GRAM_TOL = 1e-3f;     // relative pivot threshold (see above)
 
 // dst (cols x rows, bf16, row stride ldd) = src^T for a rows x cols block of
 // fp32 or bf16 src; with upper set, entries of src below its diagonal are
-// taken as zero.  32 x 32 LDS tile: reads and writes coalesced.
+// taken as zero.  64 x 64 LDS tile: fp32 rows read as float4 (vec_in: src
+// 16-byte aligned, lds a multiple of 4), the output written as bf16 pairs
+// (pairs_out: dst 4-byte aligned, ldd even); element-wise otherwise.
 template <int DT>
 __global__ __launch_bounds__(256) void transpose_to_bf16_kernel(const void* src, int64_t lds,
                                                                 int64_t rows, int64_t cols,
                                                                 bf16_t* dst, int64_t ldd,
-                                                                int upper) {
-  __shared__ float tile[32][33];
-  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  for (int k = ty; k < 32; k += 8) {
-    const int64_t r = r0 + k, c = c0 + tx;
-    tile[k][tx] = (r < rows && c < cols && !(upper && r > c))
-                      ? Elem<DT>::load((const typename Elem<DT>::T*)src + r * lds + c)
-                      : 0.0f;
+                                                                int upper, int vec_in,
+                                                                int pairs_out) {
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+  typedef typename Elem<DT>::T ST;
+  const ST* S = (const ST*)src;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rl = (t >> 4) + 16 * q, cl = (t & 15) * 4;
+    const int64_t r = r0 + rl, c = c0 + cl;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (r < rows) {
+      if (DT == DT_F32 && vec_in && c + 3 < cols) {
+        const float4 x = *reinterpret_cast<const float4*>((const float*)src + r * lds + c);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      } else {
+        for (int u = 0; u < 4; ++u)
+          if (c + u < cols) v[u] = Elem<DT>::load(S + r * lds + c + u);
+      }
+      if (upper)
+        for (int u = 0; u < 4; ++u)
+          if (r > c + u) v[u] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) tile[rl][cl + u] = v[u];
   }
   __syncthreads();
-  for (int k = ty; k < 32; k += 8) {
-    const int64_t c = c0 + k, r = r0 + tx;
-    if (c < cols && r < rows) dst[c * ldd + r] = f32_to_bf16(tile[tx][k]);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int idx = t + 256 * q, cl = idx >> 5, rp = (idx & 31) * 2;
+    const int64_t c = c0 + cl, r = r0 + rp;
+    if (c >= cols || r >= rows) continue;
+    bf16_t* g = dst + c * ldd + r;
+    if (pairs_out && r + 1 < rows) {
+      *reinterpret_cast<uint32_t*>(g) = pack_bf16x2(tile[rp][cl], tile[rp + 1][cl]);
+    } else {
+      g[0] = f32_to_bf16(tile[rp][cl]);
+      if (r + 1 < rows) g[1] = f32_to_bf16(tile[rp + 1][cl]);
+    }
   }
 }
 
@@ -275,17 +303,19 @@ unsigned grid_of(int64_t work, int64_t cap = 2048) {
 int transpose_to_bf16(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
                       int64_t cols, bf16_t* dst, int64_t ldd, bool upper) {
   if (rows * cols == 0) return IFK_OK;
-  if (cdiv(rows, 32) > 65535) {
+  if (cdiv(rows, 64) > 65535) {
     set_error("fold_finalize_gram: too many rows to transpose");
     return IFK_ERR_INVALID;
   }
-  const dim3 grid((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32));
+  const int vec_in = (((uintptr_t)src & 15) == 0) && (lds % 4 == 0);
+  const int pairs_out = (((uintptr_t)dst & 3) == 0) && (ldd % 2 == 0);
+  const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64));
   if (sdt == DT_F32)
     hipLaunchKernelGGL(transpose_to_bf16_kernel<DT_F32>, grid, dim3(256), 0, s, src, lds, rows,
-                       cols, dst, ldd, upper ? 1 : 0);
+                       cols, dst, ldd, upper ? 1 : 0, vec_in, pairs_out);
   else
     hipLaunchKernelGGL(transpose_to_bf16_kernel<DT_BF16>, grid, dim3(256), 0, s, src, lds, rows,
-                       cols, dst, ldd, upper ? 1 : 0);
+                       cols, dst, ldd, upper ? 1 : 0, 0, pairs_out);
   return check_launch("transpose_to_bf16");
 }
 
@@ -529,7 +559,13 @@ int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t
   // P^T (bf16, K-padded with zeros)
   if (w.ldk > pe) RC(launch_zero_bf16(s, w.PT + pe, w.ldk, n, w.ldk - pe));
   if (r_in > 0) RC(transpose_to_bf16(s, R_in, DT_F32, ldr, r_in, n, w.PT, w.ldk, true));
-  if (p > 0) RC(transpose_to_bf16(s, X, xdt, ldx, p, n, w.PT + r_in, w.ldk, false));
+  if (p > 0) {
+    // a bf16 chunk moves as 32-bit pairs through a 64 x 64 tile
+    if (xdt == DT_BF16)
+      RC(launch_transpose_bf16(s, (const bf16_t*)X, ldx, p, n, w.PT + r_in, w.ldk));
+    else
+      RC(transpose_to_bf16(s, X, xdt, ldx, p, n, w.PT + r_in, w.ldk, false));
+  }
   // Gram columns in order on s3, each with its event (they depend on P^T only)
   if (la) {
     HIPRC(hipEventRecord(la->ready[0], s), "fold_finalize_gram: event record failed");
