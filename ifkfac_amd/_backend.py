@@ -11,6 +11,7 @@ installed a double with ``set_backend``).
 """
 from __future__ import annotations
 
+import ctypes
 import math as _math
 from typing import Optional, Tuple
 
@@ -152,6 +153,48 @@ class HipBackend:
                                          _ptr(ws), ws.numel())
         _lib.check(rc, name)
         return (out, flag, kb) if kb is not None else (out, flag)
+
+    def fold_finalize_gram_batched(self, Rs, r_in: int, Xs, scale: float, damping: float,
+                                   out_dtype: torch.dtype):
+        """fold_finalize(..., gram=True, with_kappa=True) for B same-shape sides in
+        the same launches (ifk_fold_finalize_gram_batched).  Xs: B chunks (p x n,
+        one dtype); Rs: B running-factor buffers or None when r_in == 0.
+        Returns (factors (B, n, n), status int32[B], kappa bound float32[B]); entry
+        b is bitwise the single-side result."""
+        B = len(Xs)
+        mats = [_mat(X, "fold_finalize_gram_batched") for X in Xs]
+        X0, ldx, xdt = mats[0]
+        p, n = X0.shape
+        if any(m[0].shape != (p, n) or m[1] != ldx or m[2] != xdt for m in mats):
+            raise IFKFACBackendError("fold_finalize_gram_batched: chunks differ in shape or dtype")
+        ldr = n
+        rptrs = None
+        if r_in > 0:
+            Rs = [R if R.stride(1) == 1 else R.contiguous() for R in Rs]
+            for R in Rs:
+                if R.dtype != torch.float32 or R.shape[1] != n or R.shape[0] < r_in:
+                    raise IFKFACBackendError("fold_finalize_gram_batched: bad running factor")
+                _require_device(R, "fold_finalize_gram_batched")
+            ldr = Rs[0].stride(0) if Rs[0].shape[0] > 1 else n
+            if any((R.stride(0) if R.shape[0] > 1 else n) != ldr for R in Rs):
+                raise IFKFACBackendError("fold_finalize_gram_batched: running factors differ "
+                                         "in row stride")
+            rptrs = (ctypes.c_void_p * B)(*[R.data_ptr() for R in Rs])
+        xptrs = (ctypes.c_void_p * B)(*[m[0].data_ptr() for m in mats])
+        dev = X0.device
+        out = torch.empty((B, n, n), dtype=out_dtype, device=dev)
+        st = torch.empty(B, dtype=torch.int32, device=dev)
+        kb = torch.empty(B, dtype=torch.float32, device=dev)
+        ws = self._ws(self.lib.ifk_fold_finalize_gram_batched_workspace_size(B, p, n, int(r_in)),
+                      dev)
+        with torch.cuda.device(dev):
+            rc = self.lib.ifk_fold_finalize_gram_batched(
+                self._stream(dev), B, ctypes.cast(xptrs, ctypes.c_void_p), xdt, p, n, ldx,
+                ctypes.cast(rptrs, ctypes.c_void_p) if rptrs is not None else None, ldr,
+                int(r_in), float(scale), float(damping), _ptr(out), _DT[out_dtype], n, n * n,
+                MATH_BF16, _ptr(st), _ptr(kb), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_fold_finalize_gram_batched")
+        return out, st, kb
 
     # -- preconditioning ------------------------------------------------------------
     def tri_inverse(self, R: torch.Tensor, math: int) -> torch.Tensor:

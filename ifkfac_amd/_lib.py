@@ -58,6 +58,11 @@ SIGNATURES = {
     "ifk_fold_finalize_gram": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_vp,
                                         _c_i64, _c_i64, _c_f, _c_f, _c_vp, _c_int, _c_i64, _c_int,
                                         _c_vp, _c_vp, _c_vp, _c_sz]),
+    "ifk_fold_finalize_gram_batched_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ifk_fold_finalize_gram_batched": (_c_int, [_c_vp, _c_i64, _c_vp, _c_int, _c_i64, _c_i64,
+                                                _c_i64, _c_vp, _c_i64, _c_i64, _c_f, _c_f, _c_vp,
+                                                _c_int, _c_i64, _c_i64, _c_int, _c_vp, _c_vp,
+                                                _c_vp, _c_sz]),
     "ifk_tri_inverse_workspace_size": (_c_sz, [_c_i64]),
     "ifk_tri_inverse": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_int,
                                  _c_vp, _c_sz]),

@@ -273,6 +273,48 @@ class RawActivationHooks(GramMatrixEstimator):
                     ex[j] = then(side, m, R, kb)
                     extras[m] = tuple(ex)
 
+    # ------------------------------------------------------------------ batches
+    def _side_signature(self, side: str, module: nn.Module, rows: int):
+        """What must agree for two layers' sides to share a batched factor update:
+        the held chunk's shape, dtype and layout, the running factor's row count,
+        and the row count behind the scale."""
+        R, r, chunk, _ = self._side_state(side, module)
+        if chunk is None:
+            return None
+        return (tuple(chunk.shape), chunk.dtype, chunk.stride(), r, rows, chunk.device)
+
+    def _batch_groups(self, eligible):
+        """Groups (lists of modules, two or more) whose X sides and G sides each
+        have one signature; the backend must offer the batched factor update."""
+        if not hasattr(get_backend(), "fold_finalize_gram_batched"):
+            return []
+        by_key: Dict[tuple, list] = {}
+        for module, rows_X, rows_G, _, _, _ in eligible:
+            sx = self._side_signature("X", module, rows_X)
+            sg = self._side_signature("G", module, rows_G)
+            if sx is None or sg is None:
+                continue
+            by_key.setdefault((sx, sg), []).append(module)
+        return [mods for mods in by_key.values() if len(mods) >= 2]
+
+    def _damped_batch(self, side: str, mods, rows: int, out_dtype: torch.dtype, then):
+        """_damped(fast=True) for a group of same-signature sides in one batched
+        call; per module (R_damped, flag, then's result or None).  The factors are
+        views of one (B, n, n) buffer."""
+        chunks, bufs = [], []
+        r = 0
+        for m in mods:
+            R, r, chunk, _ = self._side_state(side, m)
+            chunks.append(chunk)
+            bufs.append((self._buf_X if side == "X" else self._buf_G).get(m))
+        out, st, kb = get_backend().fold_finalize_gram_batched(
+            bufs if r > 0 else None, r, chunks, 1.0 / math.sqrt(rows), self.damping, out_dtype)
+        res = []
+        for e, m in enumerate(mods):
+            R, f, k = out[e], st[e:e + 1], kb[e:e + 1]
+            res.append((R, f, then(side, m, R, k) if then is not None else None))
+        return res
+
     # ------------------------------------------------------------------ factors
     def get_factors(self) -> Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]]:
         """Damped factors (R_X, R_G) of every layer with enough data (fp32)."""
@@ -303,6 +345,7 @@ class RawActivationHooks(GramMatrixEstimator):
         def side(s, module, rows, fast):
             R, f, kb = self._damped(s, module, rows, out_dtype, fast=fast)
             return R, f, (then(s, module, R, kb) if then is not None else None)
+        eligible = []
         for module in self._linear_layers:
             R_X_raw, _, chunk_X, r_X = self._side_state("X", module)
             R_G_raw, _, chunk_G, r_G = self._side_state("G", module)
@@ -329,9 +372,28 @@ class RawActivationHooks(GramMatrixEstimator):
                     raise IFKFACRankError(
                         f"Layer {module}: accumulated {rows_G} rows for δ, "
                         f"but need >= n_out={R_G_raw.shape[1]} (batched mode).")
+            dev = (R_X_raw if R_X_raw is not None else chunk_X).device
+            eligible.append((module, rows_X, rows_G, n_X, n_G, dev))
+        # a consuming bf16 factor update runs same-shape layers as one batch per
+        # side (ifk_fold_finalize_gram_batched: one chain of launches for all)
+        groups = self._batch_groups(eligible) if (consume and self.math == MATH_BF16) else []
+        batched = {m for g in groups for m in g}
+        for mods in groups:
+            module0, rows_X, rows_G, n_X, n_G, dev = next(e for e in eligible if e[0] is mods[0])
+            resX, resG = run_pair(
+                dev,
+                lambda: self._damped_batch("X", mods, rows_X, out_dtype, then),
+                lambda: self._damped_batch("G", mods, rows_G, out_dtype, then),
+                b_first=n_G > n_X)
+            for m, (R_X, fX, eX), (R_G, fG, eG) in zip(mods, resX, resG):
+                factors[m] = (R_X, R_G)
+                flags[m] = (fX, fG)
+                extras[m] = (eX, eG)
+        for module, rows_X, rows_G, n_X, n_G, dev in eligible:
+            if module in batched:
+                continue
             # the two sides are independent: finalize them concurrently, the
             # wider (longer) one enqueued first
-            dev = (R_X_raw if R_X_raw is not None else chunk_X).device
             (R_X, fX, eX), (R_G, fG, eG) = run_pair(
                 dev,
                 lambda: side("X", module, rows_X, consume),

@@ -105,7 +105,7 @@ int ifk_fold_finalize_cqr(void* stream, const void* X, int x_dtype, int64_t p, i
 
 size_t ifk_fold_finalize_gram_workspace_size(int64_t p, int64_t n, int64_t r_in) {
   if (p < 0 || n < 1 || r_in < 0 || r_in > n) return 0;
-  return fold_finalize_gram_ws(p, n, r_in);
+  return fold_finalize_gram_ws(1, p, n, r_in);
 }
 
 int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
@@ -115,9 +115,30 @@ int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, 
                            size_t workspace_bytes) {
   GUARD(dt_ok(x_dtype) && dt_ok(out_dtype) && math_ok(math),
         "fold_finalize_gram: bad dtype or math code");
-  return fold_finalize_gram((hipStream_t)stream, X, x_dtype, p, n, ldx, R_in, ldr, r_in, scale,
-                            damping, out, out_dtype, ldo, math, status, kappa_bound, workspace,
-                            workspace_bytes);
+  const void* xs[1] = {X};
+  const float* rs[1] = {R_in};
+  return fold_finalize_gram((hipStream_t)stream, 1, xs, x_dtype, p, n, ldx, rs, ldr, r_in, scale,
+                            damping, out, out_dtype, ldo, n * ldo, math, status, kappa_bound,
+                            workspace, workspace_bytes);
+}
+
+size_t ifk_fold_finalize_gram_batched_workspace_size(int64_t batch, int64_t p, int64_t n,
+                                                     int64_t r_in) {
+  if (batch < 1 || p < 0 || n < 1 || r_in < 0 || r_in > n) return 0;
+  return fold_finalize_gram_ws(batch, p, n, r_in);
+}
+
+int ifk_fold_finalize_gram_batched(void* stream, int64_t batch, const void* const* X, int x_dtype,
+                                   int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
+                                   int64_t ldr, int64_t r_in, float scale, float damping,
+                                   void* out, int out_dtype, int64_t ldo, int64_t out_stride,
+                                   int math, int32_t* status, float* kappa_bound, void* workspace,
+                                   size_t workspace_bytes) {
+  GUARD(dt_ok(x_dtype) && dt_ok(out_dtype) && math_ok(math),
+        "fold_finalize_gram_batched: bad dtype or math code");
+  return fold_finalize_gram((hipStream_t)stream, batch, X, x_dtype, p, n, ldx, R_in, ldr, r_in,
+                            scale, damping, out, out_dtype, ldo, out_stride, math, status,
+                            kappa_bound, workspace, workspace_bytes);
 }
 
 size_t ifk_tri_inverse_workspace_size(int64_t n) {

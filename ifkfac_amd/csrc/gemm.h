@@ -51,6 +51,8 @@ struct OutRef {
   int lower = 0;   // only the lower triangle is wanted: tiles wholly above
                    // the diagonal (row index < column index throughout) are
                    // skipped and hold unspecified values
+  int per_entry = 0;   // choose tile and split-K as for a single batch entry, so
+                       // every entry of a batch gets the bits a batch of one gets
 };
 
 inline OutRef out_f32(float* c, int64_t ldc, int64_t bs = 0) {
@@ -69,6 +71,10 @@ inline OutRef upper_part(OutRef o) {
 }
 inline OutRef lower_part(OutRef o) {
   o.lower = 1;
+  return o;
+}
+inline OutRef per_entry(OutRef o) {
+  o.per_entry = 1;
   return o;
 }
 

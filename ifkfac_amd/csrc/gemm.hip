@@ -521,9 +521,11 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   const bool bb = big && A.dt == DT_BF16 && A.kc && B.dt == DT_BF16 && B.kc && p.vec_a &&
                   p.vec_b && K % 8 == 0 && A.ld < ((int64_t)1 << 21) &&
                   B.ld < ((int64_t)1 << 21);
+  // batch entries the tile and split-K choices are made for
+  const int64_t bdec = C.per_entry ? 1 : batch;
   // split-K factor for a tile of TM x TN with BK-deep slabs
   auto split_for = [&](int TM, int TN, int BK, bool mid_tile) -> int {
-    const int64_t tiles = cdiv(M, (int64_t)TM) * cdiv(N, (int64_t)TN) * batch;
+    const int64_t tiles = cdiv(M, (int64_t)TM) * cdiv(N, (int64_t)TN) * bdec;
     const int64_t nkt = cdiv(K, (int64_t)BK);
     int64_t want = 1;
     if (mid_tile) {
@@ -549,14 +551,14 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   bool mid = false;
   if (bb) {
     const int T2 = gemm_bb_tile(false), T1 = gemm_bb_tile(true), bk = gemm_bb_bk();
-    const int64_t t256 = cdiv(M, (int64_t)T2) * cdiv(N, (int64_t)T2) * batch;
+    const int64_t t256 = cdiv(M, (int64_t)T2) * cdiv(N, (int64_t)T2) * bdec;
     if (t256 < 224) {
-      const double fl = 2.0 * (double)M * (double)N * (double)K * batch;
+      const double fl = 2.0 * (double)M * (double)N * (double)K * bdec;
       auto est = [&](int T, bool mt, double rate) {
         const int sp = split_for(T, T, bk, mt);
-        const double wgs = (double)(cdiv(M, (int64_t)T) * cdiv(N, (int64_t)T) * batch) * sp;
+        const double wgs = (double)(cdiv(M, (int64_t)T) * cdiv(N, (int64_t)T) * bdec) * sp;
         const double util = std::min(1.0, wgs / 256.0);
-        const double part = sp > 1 ? (double)sp * (double)M * (double)N * batch * 8.0 : 0.0;
+        const double part = sp > 1 ? (double)sp * (double)M * (double)N * bdec * 8.0 : 0.0;
         return fl / (1.0e15 * rate * util) + part / 4.0e12;
       };
       mid = est(T1, true, 0.55) < est(T2, false, 1.0);

@@ -74,7 +74,9 @@ constexpr int64_t GB = 1024;          // Cholesky block (cholb supports up to 10
 constexpr float GRAM_TOL = 1e-3f;     // relative pivot threshold (see above)
 
 // ---------------------------------------------------------------------------
-// Kernels
+// Kernels.  Every one takes a batch of same-shaped problems: entry b of a
+// launch is blockIdx.y (blockIdx.z for the 2-D tiled ones), at the given
+// element strides from each pointer.
 // ---------------------------------------------------------------------------
 
 // dst (cols x rows, bf16, row stride ldd) = src^T for a rows x cols block of
@@ -133,11 +135,20 @@ __global__ __launch_bounds__(256) void transpose_to_bf16_kernel(const void* src,
 // dst[r][s cols + c] = lo(x) if bit s of lo_mask else hi(x), hi = RNE(x),
 // lo = RNE(x - hi), and the same into dst2 (ldd2, lo_mask2) when given.
 // Four columns per thread (cols % 4 == 0, 16-byte rows).
+struct SegStrides {
+  int64_t src = 0, dst = 0, dst2 = 0;
+};
 __global__ __launch_bounds__(256) void split_seg_kernel(const float* src, int64_t lds,
                                                         int64_t rows, int64_t cols, bf16_t* dst,
                                                         int64_t ldd, int nseg, int lo_mask,
-                                                        bf16_t* dst2, int64_t ldd2,
-                                                        int lo_mask2) {
+                                                        bf16_t* dst2, int64_t ldd2, int lo_mask2,
+                                                        SegStrides bs) {
+  {
+    const int64_t b = blockIdx.y;
+    src += b * bs.src;
+    dst += b * bs.dst;
+    if (dst2) dst2 += b * bs.dst2;
+  }
   const int64_t c4 = cols >> 2;
   const int64_t total = rows * c4;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
@@ -170,8 +181,11 @@ __global__ __launch_bounds__(256) void split_seg_kernel(const float* src, int64_
 // G_ij = A_max(i,j),min(i,j).  Tile (tr, tc) of G reads A's tile
 // (max, min) once through LDS.
 __global__ __launch_bounds__(256) void sym_from_lower_kernel(const float* A, int64_t lda,
-                                                             int64_t n, float* G, int64_t ldg) {
+                                                             int64_t n, float* G, int64_t ldg,
+                                                             int64_t sa, int64_t sg) {
   __shared__ float tile[32][33];
+  A += (int64_t)blockIdx.z * sa;
+  G += (int64_t)blockIdx.z * sg;
   const int tr = blockIdx.y, tc = blockIdx.x;
   const int ar = tr > tc ? tr : tc, ac = tr > tc ? tc : tr;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
@@ -192,17 +206,21 @@ __global__ __launch_bounds__(256) void sym_from_lower_kernel(const float* A, int
 }
 
 // out (odt, n x n, ldo) = scale * L^T for the lower-triangular L (ldl):
-// out_ij = scale L_ji for j >= i, 0 below the diagonal; *finite = 0 when any
-// stored value is not finite.
+// out_ij = scale L_ji for j >= i, 0 below the diagonal; finite[b] = 0 when
+// any stored value is not finite.
 template <int ODT>
 __global__ __launch_bounds__(256) void cast_lower_t_kernel(const float* L, int64_t ldl, int64_t n,
                                                            float scale, void* out, int64_t ldo,
-                                                           int* finite) {
+                                                           int* finite, int64_t sl,
+                                                           int64_t so) {
   __shared__ float tile[32][33];
+  const int64_t b = blockIdx.z;
+  L += b * sl;
+  finite += b;
   const int tr = blockIdx.y, tc = blockIdx.x;   // output tile
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
   typedef typename Elem<ODT>::T OT;
-  OT* O = (OT*)out;
+  OT* O = (OT*)out + b * so;
   if (tr > tc) {
     for (int k = ty; k < 32; k += 8) {
       const int64_t r = (int64_t)tr * 32 + k, c = (int64_t)tc * 32 + tx;
@@ -228,7 +246,10 @@ __global__ __launch_bounds__(256) void cast_lower_t_kernel(const float* L, int64
 }
 
 // A_ii += v and dref_i = A_ii (after the addition), i < n
-__global__ void add_diag_ref_kernel(float* A, int64_t lda, int64_t n, float v, float* dref) {
+__global__ void add_diag_ref_kernel(float* A, int64_t lda, int64_t n, float v, float* dref,
+                                    int64_t sa, int64_t sd) {
+  A += (int64_t)blockIdx.y * sa;
+  dref += (int64_t)blockIdx.y * sd;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const float d = A[i * lda + i] + v;
@@ -246,8 +267,11 @@ __global__ void add_diag_ref_kernel(float* A, int64_t lda, int64_t n, float v, f
 // result does not depend on scheduling.
 constexpr int FROB_WG = 1024;
 __global__ __launch_bounds__(256) void gram_frob_kernel(const float* A, int64_t lda, int64_t rows,
-                                                        int64_t W, float* part) {
+                                                        int64_t W, float* part, int64_t sa,
+                                                        int64_t sp) {
   __shared__ float red[4];
+  A += (int64_t)blockIdx.y * sa;
+  part += (int64_t)blockIdx.y * sp;
   float acc = 0.0f;
   const int64_t c = (int64_t)threadIdx.x * 4;
   if (c < W) {
@@ -272,13 +296,15 @@ __global__ __launch_bounds__(256) void gram_frob_kernel(const float* A, int64_t 
   if (threadIdx.x == 0) part[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// *kb = sqrt(1 + scale^2 sqrt(sum of the count partials) / damping): with
-// E = scale^2 P^T P, kappa_2(R)^2 = kappa(E + damping I)
+// kb[b] = sqrt(1 + scale^2 sqrt(sum of entry b's count partials) / damping):
+// with E = scale^2 P^T P, kappa_2(R)^2 = kappa(E + damping I)
 // <= 1 + ||E||_2 / damping <= 1 + ||E||_F / damping.  Infinite without
-// damping.  256 threads: strided sums in a fixed order, then a fixed tree.
+// damping.  256 threads per entry: strided sums in a fixed order, then a
+// fixed tree.
 __global__ __launch_bounds__(256) void kappa_bound_kernel(const float* part, int count,
                                                           float scale, float damping, float* kb) {
   __shared__ double red[256];
+  part += (int64_t)blockIdx.x * count;
   double ss = 0.0;
   for (int i = threadIdx.x; i < count; i += 256) ss += (double)part[i];
   red[threadIdx.x] = ss;
@@ -289,8 +315,14 @@ __global__ __launch_bounds__(256) void kappa_bound_kernel(const float* part, int
   }
   if (threadIdx.x == 0) {
     const double e = (double)scale * (double)scale * sqrt(red[0]);
-    *kb = damping > 0.0f ? (float)sqrt(1.0 + e / (double)damping) : INFINITY;
+    kb[blockIdx.x] = damping > 0.0f ? (float)sqrt(1.0 + e / (double)damping) : INFINITY;
   }
+}
+
+// status[b] = 2 where flag[b] is set (flags at int stride fs)
+__global__ void status_merge_batch_kernel(int* status, const int* flag, int64_t fs, int batch) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < batch && flag[b * fs] != 0) status[b] = 2;
 }
 
 unsigned grid_of(int64_t work, int64_t cap = 2048) {
@@ -319,41 +351,44 @@ int transpose_to_bf16(hipStream_t s, const void* src, int sdt, int64_t lds, int6
   return check_launch("transpose_to_bf16");
 }
 
-int split_seg(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
-              bf16_t* dst, int64_t ldd, int nseg, int lo_mask, bf16_t* dst2 = nullptr,
-              int64_t ldd2 = 0, int lo_mask2 = 0) {
+int split_seg(hipStream_t s, int batch, const float* src, int64_t lds, int64_t rows, int64_t cols,
+              bf16_t* dst, int64_t ldd, int nseg, int lo_mask, SegStrides bs,
+              bf16_t* dst2 = nullptr, int64_t ldd2 = 0, int lo_mask2 = 0) {
   if (rows * cols == 0) return IFK_OK;
-  hipLaunchKernelGGL(split_seg_kernel, dim3(grid_of(rows * cols / 4)), dim3(256), 0, s, src, lds,
-                     rows, cols, dst, ldd, nseg, lo_mask, dst2, ldd2, lo_mask2);
+  hipLaunchKernelGGL(split_seg_kernel, dim3(grid_of(rows * cols / 4, 1024), (unsigned)batch),
+                     dim3(256), 0, s, src, lds, rows, cols, dst, ldd, nseg, lo_mask, dst2, ldd2,
+                     lo_mask2, bs);
   return check_launch("split_seg");
 }
 
-int sym_from_lower(hipStream_t s, const float* A, int64_t lda, int64_t n, float* G, int64_t ldg) {
-  const dim3 grid((unsigned)cdiv(n, 32), (unsigned)cdiv(n, 32));
-  hipLaunchKernelGGL(sym_from_lower_kernel, grid, dim3(256), 0, s, A, lda, n, G, ldg);
+int sym_from_lower(hipStream_t s, int batch, const float* A, int64_t lda, int64_t n, float* G,
+                   int64_t ldg, int64_t sa, int64_t sg) {
+  const dim3 grid((unsigned)cdiv(n, 32), (unsigned)cdiv(n, 32), (unsigned)batch);
+  hipLaunchKernelGGL(sym_from_lower_kernel, grid, dim3(256), 0, s, A, lda, n, G, ldg, sa, sg);
   return check_launch("sym_from_lower");
 }
 
-int cast_lower_t(hipStream_t s, const float* L, int64_t ldl, int64_t n, float scale, void* out,
-                 int odt, int64_t ldo, int* finite) {
+int cast_lower_t(hipStream_t s, int batch, const float* L, int64_t ldl, int64_t n, float scale,
+                 void* out, int odt, int64_t ldo, int* finite, int64_t sl, int64_t so) {
   if (cdiv(n, 32) > 65535) {
     set_error("fold_finalize_gram: factor too large");
     return IFK_ERR_INVALID;
   }
-  const dim3 grid((unsigned)cdiv(n, 32), (unsigned)cdiv(n, 32));
+  const dim3 grid((unsigned)cdiv(n, 32), (unsigned)cdiv(n, 32), (unsigned)batch);
   if (odt == DT_F32)
     hipLaunchKernelGGL(cast_lower_t_kernel<DT_F32>, grid, dim3(256), 0, s, L, ldl, n, scale, out,
-                       ldo, finite);
+                       ldo, finite, sl, so);
   else
     hipLaunchKernelGGL(cast_lower_t_kernel<DT_BF16>, grid, dim3(256), 0, s, L, ldl, n, scale, out,
-                       ldo, finite);
+                       ldo, finite, sl, so);
   return check_launch("cast_lower_t");
 }
 
 // ---------------------------------------------------------------------------
-// Workspace
+// Workspace (every buffer once per batch entry, at the stride s*)
 // ---------------------------------------------------------------------------
 struct GramWs {
+  int64_t B;          // batch entries
   int64_t ldk;        // row stride of PT (pe rounded up to 8; the pad is zero)
   int64_t lda;        // row stride of Aw
   int64_t ldl;        // row stride of LA / LB: 3 GB per panel
@@ -363,44 +398,59 @@ struct GramWs {
   float* G;           // symmetrised diagonal block, GB x GB; then M^T
   float* U;           // U_kk, GB x GB
   float* M;           // U_kk^{-1}, GB x GB
-  float* Zd;          // cholb's 64 x 64 diagonal inverses
+  float* Zd;          // cholb's 64 x 64 diagonal inverses, GB x 64
   bf16_t* MT3[2];     // [M^T_hi | M^T_hi | M^T_lo], GB x 3 GB, by step parity
   bf16_t* ASb;        // [A_hi | A_lo | A_hi] of the band block, GB x 3 GB
   bf16_t* LSb;        // [L_hi | L_lo | L_hi | L_hi] of the band block, GB x 4 GB
   bf16_t* AS2;        // [A_hi | A_lo | A_hi] of the rest of a panel, n x 3 GB
   bf16_t* LA;         // panel l at columns 3 GB l: [L_hi | L_lo | L_hi], n x ldl
   bf16_t* LB;         // panel l at columns 3 GB l: [L_lo | L_hi | L_hi], n x ldl
-  int* flag;
-  float* frob;        // per Gram column, FROB_WG partial sums of squares
+  int* flag;          // one per entry, at int stride FLAG_S
+  float* frob;        // per entry and Gram column, FROB_WG partial sums of squares
+  int64_t sPT, sAw, sdref, sGB, sZd, sMT3, sLSb, sAS2, sL, sfrob;
   SplitScratch sp, sp2, sp3;   // split-K partials of the three streams
 };
+constexpr int64_t FLAG_S = 64;   // ints between two entries' flags (separate cache lines)
 
-void plan_gram(Arena& a, int64_t pe, int64_t n, GramWs& w) {
+void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w) {
   const int64_t nb = cdiv(n, GB);
+  w.B = B;
   w.ldk = (int64_t)align_up((size_t)std::max<int64_t>(pe, 1), 8);
   w.lda = (int64_t)align_up((size_t)n, 64);
   w.ldl = 3 * GB * std::max<int64_t>(nb - 1, 1);
   const bool multi = nb > 1;
-  const size_t big = multi ? (size_t)n : 1;
-  w.PT = a.take<bf16_t>((size_t)n * w.ldk);
-  w.Aw = a.take<float>((size_t)n * w.lda);
-  w.dref = a.take<float>((size_t)n);
-  w.G = a.take<float>((size_t)GB * GB);
-  w.U = a.take<float>((size_t)GB * GB);
-  w.M = a.take<float>((size_t)GB * GB);
-  w.Zd = a.take<float>((size_t)(GB / 64) * 64 * 64);
-  for (int i = 0; i < 2; ++i) w.MT3[i] = a.take<bf16_t>(multi ? (size_t)GB * 3 * GB : 1);
-  w.ASb = a.take<bf16_t>(multi ? (size_t)GB * 3 * GB : 1);
-  w.LSb = a.take<bf16_t>(multi ? (size_t)GB * 4 * GB : 1);
-  w.AS2 = a.take<bf16_t>(big * 3 * GB);
-  w.LA = a.take<bf16_t>(big * w.ldl);
-  w.LB = a.take<bf16_t>(big * w.ldl);
-  w.flag = a.take<int>(64);
-  w.frob = a.take<float>((size_t)nb * FROB_WG);
+  const int64_t big = multi ? n : 1;
+  // strides rounded to 64 elements: every entry's buffers stay 256-byte aligned
+  auto al = [](int64_t e) { return (int64_t)align_up((size_t)e, 64); };
+  w.sPT = al(n * w.ldk);
+  w.sAw = al(n * w.lda);
+  w.sdref = al(n);
+  w.sGB = GB * GB;
+  w.sZd = (GB / 64) * 64 * 64;
+  w.sMT3 = multi ? GB * 3 * GB : 64;
+  w.sLSb = multi ? GB * 4 * GB : 64;
+  w.sAS2 = al(big * 3 * GB);
+  w.sL = al(big * w.ldl);
+  w.sfrob = nb * FROB_WG;
+  w.PT = a.take<bf16_t>((size_t)(B * w.sPT));
+  w.Aw = a.take<float>((size_t)(B * w.sAw));
+  w.dref = a.take<float>((size_t)(B * w.sdref));
+  w.G = a.take<float>((size_t)(B * w.sGB));
+  w.U = a.take<float>((size_t)(B * w.sGB));
+  w.M = a.take<float>((size_t)(B * w.sGB));
+  w.Zd = a.take<float>((size_t)(B * w.sZd));
+  for (int i = 0; i < 2; ++i) w.MT3[i] = a.take<bf16_t>((size_t)(B * w.sMT3));
+  w.ASb = a.take<bf16_t>((size_t)(B * w.sMT3));
+  w.LSb = a.take<bf16_t>((size_t)(B * w.sLSb));
+  w.AS2 = a.take<bf16_t>((size_t)(B * w.sAS2));
+  w.LA = a.take<bf16_t>((size_t)(B * w.sL));
+  w.LB = a.take<bf16_t>((size_t)(B * w.sL));
+  w.flag = a.take<int>((size_t)(B * FLAG_S));
+  w.frob = a.take<float>((size_t)(B * w.sfrob));
   // split-K partials for the products with one block column of output
-  w.sp.floats = (size_t)std::min<int64_t>(n, 8 * GB) * GB * 2;
+  w.sp.floats = (size_t)(B * std::min<int64_t>(n, 8 * GB) * GB * 2);
   w.sp.p = a.take<float>(w.sp.floats);
-  w.sp2.floats = (size_t)std::min<int64_t>(n, 16 * GB) * GB * 2;
+  w.sp2.floats = (size_t)(B * std::min<int64_t>(n, 16 * GB) * GB * 2);
   w.sp2.p = a.take<float>(w.sp2.floats);
   w.sp3.floats = w.sp2.floats;
   w.sp3.p = a.take<float>(w.sp3.floats);
@@ -418,24 +468,26 @@ struct Blk {
 inline Blk blk(int64_t k, int64_t n) { return Blk{k * GB, std::min<int64_t>(k * GB + GB, n)}; }
 
 // Gram column c of A (rows >= c0, lower part) with c^2 on its diagonal and
-// the pivot test's reference diagonal taken there.
+// the pivot test's reference diagonal taken there, for every entry.
 int gram_column(hipStream_t s, GramWs& w, int64_t n, int64_t c, float c2, bool have_rows,
                 int max_wgs) {
   const Blk b = blk(c, n);
   const int64_t W = b.r1 - b.r0, rows = n - b.r0;
+  const int B = (int)w.B;
   float* Ac = w.Aw + b.r0 * w.lda + b.r0;
   if (have_rows) {
-    RC(gemm(s, MATH_BF16, rows, W, w.ldk, 1.0f, A_n(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk),
-            B_t(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk), 0.0f, lower_part(out_f32(Ac, w.lda)), 1,
-            w.sp3, max_wgs));
+    RC(gemm(s, MATH_BF16, rows, W, w.ldk, 1.0f,
+            A_n(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk, TRI_NONE, w.sPT),
+            B_t(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
+            per_entry(lower_part(out_f32(Ac, w.lda, w.sAw))), B, w.sp3, max_wgs));
   } else {
-    RC(launch_zero(s, Ac, w.lda, rows, W));
+    for (int e = 0; e < B; ++e) RC(launch_zero(s, Ac + e * w.sAw, w.lda, rows, W));
   }
-  hipLaunchKernelGGL(gram_frob_kernel, dim3(FROB_WG), dim3(256), 0, s, Ac, w.lda, rows, W,
-                     w.frob + c * FROB_WG);
+  hipLaunchKernelGGL(gram_frob_kernel, dim3(FROB_WG, (unsigned)B), dim3(256), 0, s, Ac, w.lda,
+                     rows, W, w.frob + c * FROB_WG, w.sAw, w.sfrob);
   RC(check_launch("gram_frob"));
-  hipLaunchKernelGGL(add_diag_ref_kernel, dim3(grid_of(W, 64)), dim3(256), 0, s, Ac, w.lda, W, c2,
-                     w.dref + b.r0);
+  hipLaunchKernelGGL(add_diag_ref_kernel, dim3(grid_of(W, 64), (unsigned)B), dim3(256), 0, s, Ac,
+                     w.lda, W, c2, w.dref + b.r0, w.sAw, w.sdref);
   return check_launch("add_diag_ref");
 }
 
@@ -443,11 +495,14 @@ int gram_column(hipStream_t s, GramWs& w, int64_t n, int64_t c, float c2, bool h
 int chain_factor(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
   const Blk b = blk(k, n);
   const int64_t W = b.r1 - b.r0;
+  const int B = (int)w.B;
   float* Akk = w.Aw + b.r0 * w.lda + b.r0;
-  RC(sym_from_lower(s, Akk, w.lda, W, w.G, GB));
+  RC(sym_from_lower(s, B, Akk, w.lda, W, w.G, GB, w.sAw, w.sGB));
+  CholbStrides cs;
+  cs.a = w.sGB; cs.u = w.sGB; cs.zd = w.sZd; cs.dref = w.sdref; cs.m = w.sGB; cs.flag = FLAG_S;
   RC(launch_cholb(s, w.G, GB, (int)W, w.U, GB, w.Zd, w.dref + b.r0, GRAM_TOL, w.flag, w.M, GB,
-                  true));
-  return launch_transpose_cast(s, w.U, GB, W, W, Akk, DT_F32, w.lda);
+                  true, B, cs));
+  return launch_transpose_cast(s, w.U, GB, W, W, Akk, DT_F32, w.lda, B, w.sGB, w.sAw);
 }
 
 // Chain, part 2 of step k (block k + 1 exists): M^T split into MT3[k % 2];
@@ -456,68 +511,91 @@ int chain_factor(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
 int chain_band(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
   const Blk b = blk(k, n), b1 = blk(k + 1, n);
   const int64_t W = b.r1 - b.r0, W1 = b1.r1 - b1.r0;   // W == GB here
+  const int B = (int)w.B;
   bf16_t* MT3 = w.MT3[k & 1];
-  RC(launch_zero_tri_blocks(s, w.M, 4, GB, W, true));   // cholb leaves M's lower blocks unset
-  RC(launch_transpose_cast(s, w.M, GB, W, W, w.G, DT_F32, GB));
-  RC(split_seg(s, w.G, GB, W, W, MT3, 3 * GB, 3, 0b100));
+  // cholb leaves M's blocks below the diagonal unset
+  for (int e = 0; e < B; ++e)
+    RC(launch_zero_tri_blocks(s, w.M + e * w.sGB, 4, GB, W, true));
+  RC(launch_transpose_cast(s, w.M, GB, W, W, w.G, DT_F32, GB, B, w.sGB, w.sGB));
+  SegStrides g3;
+  g3.src = w.sGB; g3.dst = w.sMT3;
+  RC(split_seg(s, B, w.G, GB, W, W, MT3, 3 * GB, 3, 0b100, g3));
   float* Ab = w.Aw + b1.r0 * w.lda + b.r0;   // block (k + 1, k)
-  RC(split_seg(s, Ab, w.lda, W1, W, w.ASb, 3 * GB, 3, 0b010));
-  RC(gemm(s, MATH_BF16, W1, W, 3 * W, 1.0f, A_n(w.ASb, DT_BF16, 3 * GB),
-          B_t(MT3, DT_BF16, 3 * GB), 0.0f, out_f32(Ab, w.lda), 1, w.sp));
-  RC(split_seg(s, Ab, w.lda, W1, W, w.LSb, 4 * GB, 4, 0b0010));
+  SegStrides a3;
+  a3.src = w.sAw; a3.dst = w.sMT3;
+  RC(split_seg(s, B, Ab, w.lda, W1, W, w.ASb, 3 * GB, 3, 0b010, a3));
+  RC(gemm(s, MATH_BF16, W1, W, 3 * W, 1.0f, A_n(w.ASb, DT_BF16, 3 * GB, TRI_NONE, w.sMT3),
+          B_t(MT3, DT_BF16, 3 * GB, TRI_NONE, w.sMT3), 0.0f, per_entry(out_f32(Ab, w.lda, w.sAw)), B,
+          w.sp));
+  SegStrides l4;
+  l4.src = w.sAw; l4.dst = w.sLSb;
+  RC(split_seg(s, B, Ab, w.lda, W1, W, w.LSb, 4 * GB, 4, 0b0010, l4));
   float* A11 = w.Aw + b1.r0 * w.lda + b1.r0;
-  return gemm(s, MATH_BF16, W1, W1, 3 * W, -1.0f, A_n(w.LSb, DT_BF16, 4 * GB),
-              B_t(w.LSb + GB, DT_BF16, 4 * GB), 1.0f, lower_part(out_f32(A11, w.lda)), 1, w.sp);
+  return gemm(s, MATH_BF16, W1, W1, 3 * W, -1.0f, A_n(w.LSb, DT_BF16, 4 * GB, TRI_NONE, w.sLSb),
+              B_t(w.LSb + GB, DT_BF16, 4 * GB, TRI_NONE, w.sLSb), 1.0f,
+              per_entry(lower_part(out_f32(A11, w.lda, w.sAw))), B, w.sp);
 }
 
 // Helper work of step k (blocks k + 2 .. exist): the rest of panel k,
 // L_{>k+1,k} = A_{>k+1,k} M (in place); panel k's split copies (rows > k);
 // column k + 1's rows > k + 1 updated by panel k; column k + 2 updated by
-// panels 0 .. k (after its Gram column, event gev).
+// panels 0 .. k (after its Gram column, event gev_k2).
 int helper_step(hipStream_t s, GramWs& w, int64_t n, int64_t k, hipEvent_t gev_k2,
                 hipEvent_t gev_k1, int max_wgs) {
   const Blk b = blk(k, n), b1 = blk(k + 1, n), b2 = blk(k + 2, n);
   const int64_t W = b.r1 - b.r0;
   const int64_t lda = w.lda, ldl = w.ldl;
+  const int B = (int)w.B;
   const int64_t rest = n - b2.r0;   // rows > k + 1
   float* Arest = w.Aw + b2.r0 * lda + b.r0;
-  RC(split_seg(s, Arest, lda, rest, W, w.AS2, 3 * GB, 3, 0b010));
-  RC(gemm(s, MATH_BF16, rest, W, 3 * W, 1.0f, A_n(w.AS2, DT_BF16, 3 * GB),
-          B_t(w.MT3[k & 1], DT_BF16, 3 * GB), 0.0f, out_f32(Arest, lda), 1, w.sp2, max_wgs));
+  SegStrides a3;
+  a3.src = w.sAw; a3.dst = w.sAS2;
+  RC(split_seg(s, B, Arest, lda, rest, W, w.AS2, 3 * GB, 3, 0b010, a3));
+  RC(gemm(s, MATH_BF16, rest, W, 3 * W, 1.0f, A_n(w.AS2, DT_BF16, 3 * GB, TRI_NONE, w.sAS2),
+          B_t(w.MT3[k & 1], DT_BF16, 3 * GB, TRI_NONE, w.sMT3), 0.0f,
+          per_entry(out_f32(Arest, lda, w.sAw)), B, w.sp2, max_wgs));
   const int64_t k0 = 3 * GB * k;
-  RC(split_seg(s, w.Aw + b1.r0 * lda + b.r0, lda, n - b1.r0, W, w.LA + b1.r0 * ldl + k0, ldl, 3,
-               0b010, w.LB + b1.r0 * ldl + k0, ldl, 0b001));
+  SegStrides l2;
+  l2.src = w.sAw; l2.dst = w.sL; l2.dst2 = w.sL;
+  RC(split_seg(s, B, w.Aw + b1.r0 * lda + b.r0, lda, n - b1.r0, W, w.LA + b1.r0 * ldl + k0, ldl,
+               3, 0b010, l2, w.LB + b1.r0 * ldl + k0, ldl, 0b001));
   // column k + 1, rows > k + 1, by panel k
   if (gev_k1) HIPRC(hipStreamWaitEvent(s, gev_k1, 0), "fold_finalize_gram: stream wait failed");
   const int64_t W1 = b1.r1 - b1.r0;
-  RC(gemm(s, MATH_BF16, rest, W1, 3 * GB, -1.0f, A_n(w.LA + b2.r0 * ldl + k0, DT_BF16, ldl),
-          B_t(w.LB + b1.r0 * ldl + k0, DT_BF16, ldl), 1.0f,
-          out_f32(w.Aw + b2.r0 * lda + b1.r0, lda), 1, w.sp2, max_wgs));
+  RC(gemm(s, MATH_BF16, rest, W1, 3 * GB, -1.0f,
+          A_n(w.LA + b2.r0 * ldl + k0, DT_BF16, ldl, TRI_NONE, w.sL),
+          B_t(w.LB + b1.r0 * ldl + k0, DT_BF16, ldl, TRI_NONE, w.sL), 1.0f,
+          per_entry(out_f32(w.Aw + b2.r0 * lda + b1.r0, lda, w.sAw)), B, w.sp2, max_wgs));
   // column k + 2 by panels 0 .. k
   if (gev_k2) HIPRC(hipStreamWaitEvent(s, gev_k2, 0), "fold_finalize_gram: stream wait failed");
   const int64_t W2 = b2.r1 - b2.r0;
   return gemm(s, MATH_BF16, rest, W2, 3 * GB * (k + 1), -1.0f,
-              A_n(w.LA + b2.r0 * ldl, DT_BF16, ldl), B_t(w.LB + b2.r0 * ldl, DT_BF16, ldl), 1.0f,
-              lower_part(out_f32(w.Aw + b2.r0 * lda + b2.r0, lda)), 1, w.sp2, max_wgs);
+              A_n(w.LA + b2.r0 * ldl, DT_BF16, ldl, TRI_NONE, w.sL),
+              B_t(w.LB + b2.r0 * ldl, DT_BF16, ldl, TRI_NONE, w.sL), 1.0f,
+              per_entry(lower_part(out_f32(w.Aw + b2.r0 * lda + b2.r0, lda, w.sAw))), B, w.sp2, max_wgs);
 }
 
 }  // namespace
 
-size_t fold_finalize_gram_ws(int64_t p, int64_t n, int64_t r_in) {
+size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in) {
   Arena a(nullptr, 0);
   GramWs w;
-  plan_gram(a, r_in + p, n, w);
+  plan_gram(a, batch, r_in + p, n, w);
   return a.used;
 }
 
-int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
-                       const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
-                       void* out, int odt, int64_t ldo, int math, int* status, float* kappa_bound,
-                       void* ws, size_t ws_bytes) {
-  if (n < 1 || p < 0 || r_in < 0 || r_in > n || (p > 0 && (!X || ldx < n)) ||
-      (r_in > 0 && (!R_in || ldr < n)) || !out || ldo < n || !(scale > 0.0f) ||
-      !(damping >= 0.0f) || (xdt != DT_F32 && xdt != DT_BF16) ||
-      (odt != DT_F32 && odt != DT_BF16) || !status) {
+int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int xdt, int64_t p,
+                       int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
+                       int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
+                       int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
+                       size_t ws_bytes) {
+  bool ok = n >= 1 && p >= 0 && r_in >= 0 && r_in <= n && batch >= 1 && batch <= 65535 &&
+            (p == 0 || (X && ldx >= n)) && (r_in == 0 || (R_in && ldr >= n)) && out &&
+            ldo >= n && out_stride >= n * ldo && scale > 0.0f && damping >= 0.0f &&
+            (xdt == DT_F32 || xdt == DT_BF16) && (odt == DT_F32 || odt == DT_BF16) && status;
+  for (int64_t e = 0; ok && e < batch; ++e)
+    ok = (p == 0 || X[e]) && (r_in == 0 || R_in[e]);
+  if (!ok) {
     set_error("fold_finalize_gram: invalid arguments");
     return IFK_ERR_INVALID;
   }
@@ -534,11 +612,12 @@ int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t
   }
   Arena a(ws, ws_bytes);
   GramWs w;
-  plan_gram(a, pe, n, w);
+  plan_gram(a, batch, pe, n, w);
   if (a.overflow) {
     set_error("fold_finalize_gram: workspace too small");
     return IFK_ERR_WORKSPACE;
   }
+  const int B = (int)batch;
   const int64_t nb = cdiv(n, GB);
   LookAhead* la = nullptr;
   int rc = IFK_OK;
@@ -555,16 +634,19 @@ int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t
   const int wg2 = la ? REST_MAX_WGS : 0, wg3 = la ? GRAM_MAX_WGS : 0;
   const float c2 = damping / (scale * scale);
   const bool have_rows = pe > 0;
-  RC(launch_fill_int(s, w.flag, 0, 1));
-  // P^T (bf16, K-padded with zeros)
-  if (w.ldk > pe) RC(launch_zero_bf16(s, w.PT + pe, w.ldk, n, w.ldk - pe));
-  if (r_in > 0) RC(transpose_to_bf16(s, R_in, DT_F32, ldr, r_in, n, w.PT, w.ldk, true));
-  if (p > 0) {
-    // a bf16 chunk moves as 32-bit pairs through a 64 x 64 tile
-    if (xdt == DT_BF16)
-      RC(launch_transpose_bf16(s, (const bf16_t*)X, ldx, p, n, w.PT + r_in, w.ldk));
-    else
-      RC(transpose_to_bf16(s, X, xdt, ldx, p, n, w.PT + r_in, w.ldk, false));
+  for (int e = 0; e < B; ++e) RC(launch_fill_int(s, w.flag + e * FLAG_S, 0, 1));
+  // P^T of each entry (bf16, K-padded with zeros)
+  for (int e = 0; e < B; ++e) {
+    bf16_t* PT = w.PT + e * w.sPT;
+    if (w.ldk > pe) RC(launch_zero_bf16(s, PT + pe, w.ldk, n, w.ldk - pe));
+    if (r_in > 0) RC(transpose_to_bf16(s, R_in[e], DT_F32, ldr, r_in, n, PT, w.ldk, true));
+    if (p > 0) {
+      // a bf16 chunk moves as 32-bit pairs through a 64 x 64 tile
+      if (xdt == DT_BF16)
+        RC(launch_transpose_bf16(s, (const bf16_t*)X[e], ldx, p, n, PT + r_in, w.ldk));
+      else
+        RC(transpose_to_bf16(s, X[e], xdt, ldx, p, n, PT + r_in, w.ldk, false));
+    }
   }
   // Gram columns in order on s3, each with its event (they depend on P^T only)
   if (la) {
@@ -587,7 +669,7 @@ int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t
     if (k + 1 >= nb) break;
     // the band of step k needs helper step k - 1 (column k's rows > k, and
     // column k + 1 updated by panels < k), which also frees MT3[k % 2]
-    if (la && k >= 1 && k + 1 < nb && (k - 1) + 2 < nb)
+    if (la && k >= 1 && k + 1 < nb)
       HIPRC(hipStreamWaitEvent(s, la->aready[kp ^ 1], 0), "fold_finalize_gram: stream wait failed");
     if (la && k == 0)
       HIPRC(hipStreamWaitEvent(s, la->col[1], 0), "fold_finalize_gram: stream wait failed");
@@ -608,14 +690,16 @@ int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t
     HIPRC(hipEventRecord(la->fall[0], s3), "fold_finalize_gram: event record failed");
     HIPRC(hipStreamWaitEvent(s, la->fall[0], 0), "fold_finalize_gram: stream wait failed");
   }
-  RC(launch_fill_int(s, status, 1, 1));
-  RC(cast_lower_t(s, w.Aw, w.lda, n, scale, out, odt, ldo, status));
+  RC(launch_fill_int(s, status, 1, B));
+  RC(cast_lower_t(s, B, w.Aw, w.lda, n, scale, out, odt, ldo, status, w.sAw, out_stride));
   if (kappa_bound) {
-    hipLaunchKernelGGL(kappa_bound_kernel, dim3(1), dim3(256), 0, s, w.frob, (int)(nb * FROB_WG),
-                       scale, damping, kappa_bound);
+    hipLaunchKernelGGL(kappa_bound_kernel, dim3((unsigned)B), dim3(256), 0, s, w.frob,
+                       (int)w.sfrob, scale, damping, kappa_bound);
     RC(check_launch("kappa_bound"));
   }
-  return launch_status_merge(s, status, w.flag);
+  hipLaunchKernelGGL(status_merge_batch_kernel, dim3((unsigned)cdiv(B, 64)), dim3(64), 0, s,
+                     status, w.flag, FLAG_S, B);
+  return check_launch("status_merge");
 }
 
 }  // namespace ifk

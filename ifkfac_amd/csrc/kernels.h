@@ -56,10 +56,15 @@ int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b);
 // With M (ld ldm), M = U^{-1} as well (its blocks on and above the diagonal),
 // formed column block by column block alongside the factorisation.  With
 // dref_in, dref holds the reference diagonal on entry instead (e.g. a Gram
-// matrix's diagonal before the updates that produced A).
+// matrix's diagonal before the updates that produced A).  batch independent
+// factorisations of the same size run in the same launches, entry b at the
+// given element strides from each pointer (flag: int strides).
+struct CholbStrides {
+  int64_t a = 0, u = 0, zd = 0, dref = 0, m = 0, flag = 0;
+};
 int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
                  float* dref, float tol, int* flag, float* M = nullptr, int64_t ldm = 0,
-                 bool dref_in = false);
+                 bool dref_in = false, int batch = 1, CholbStrides bs = CholbStrides());
 // hi = RNE bf16(src), lo = RNE bf16(src - hi); transposed (hi[c][r]) with trans
 int launch_split_bf16(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
                       bf16_t* hi, bf16_t* lo, int64_t ldo, bool trans = false);

@@ -42,12 +42,16 @@ int fold_finalize_cqr(hipStream_t s, const void* X, int xdt, int64_t p, int64_t 
 // blocked Cholesky (gramchol.hip; bf16 arithmetic only).  *status as for
 // fold_finalize_cqr (2: a pivot below 1e-3 of its Gram diagonal).  With
 // kappa_bound, an upper bound of kappa_2 of the factor from the Gram
-// matrix's Frobenius norm (device float).
-size_t fold_finalize_gram_ws(int64_t p, int64_t n, int64_t r_in);
-int fold_finalize_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
-                       const float* R_in, int64_t ldr, int64_t r_in, float scale, float damping,
-                       void* out, int odt, int64_t ldo, int math, int* status, float* kappa_bound,
-                       void* ws, size_t ws_bytes);
+// matrix's Frobenius norm (device float).  batch factors of the same shape
+// at once: X and R_in are host arrays of batch device pointers, entry b's
+// factor goes to out + b * out_stride, its status to status[b] and its bound
+// to kappa_bound[b].
+size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in);
+int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int xdt, int64_t p,
+                       int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
+                       int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
+                       int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
+                       size_t ws_bytes);
 
 // Z = R^{-1} for upper-triangular R (dtype rdt); Z fp32 upper triangular.
 size_t trinv_ws(int64_t n);

@@ -728,7 +728,14 @@ __device__ __forceinline__ void st_blk(const float* S, float* g, int64_t ld, int
 __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_t lda, int n,
                                                           float* U, int64_t ldu, float* Zd,
                                                           float* dref, float tol, int* flag,
-                                                          float* Mo, int64_t ldm, int dref_in) {
+                                                          float* Mo, int64_t ldm, int dref_in,
+                                                          CholbStrides bs) {
+  // batch entry blockIdx.y
+  {
+    const int64_t b = blockIdx.y;
+    A += b * bs.a; U += b * bs.u; Zd += b * bs.zd; dref += b * bs.dref; flag += b * bs.flag;
+    if (Mo) Mo += b * bs.m;
+  }
   __shared__ float sC[SB * SLD];
   __shared__ float sZ[SB * SLD];
   __shared__ float sT[TRINV_TMP];
@@ -757,7 +764,13 @@ __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_
 __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, int n, float* U,
                                                          int64_t ldu, float* Zd,
                                                          const float* dref, float tol, int* flag,
-                                                         int k, float* Mo, int64_t ldm) {
+                                                         int k, float* Mo, int64_t ldm,
+                                                         CholbStrides bs) {
+  {
+    const int64_t b = blockIdx.y;
+    A += b * bs.a; U += b * bs.u; Zd += b * bs.zd; dref += b * bs.dref; flag += b * bs.flag;
+    if (Mo) Mo += b * bs.m;
+  }
   __shared__ float sZ[SB * SLD];
   __shared__ float sA[SB * SLD];
   __shared__ float sB[SB * SLD];
@@ -1381,13 +1394,15 @@ int launch_chol_block(hipStream_t s, float* A, int64_t ld, int b) {
 }
 
 int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t ldu, float* Zd,
-                 float* dref, float tol, int* flag, float* M, int64_t ldm, bool dref_in) {
-  if (n < 1 || n > CHOLB_MAX || lda < n || ldu < n || (M && ldm < n)) {
+                 float* dref, float tol, int* flag, float* M, int64_t ldm, bool dref_in,
+                 int batch, CholbStrides bs) {
+  if (n < 1 || n > CHOLB_MAX || lda < n || ldu < n || (M && ldm < n) || batch < 1 ||
+      batch > 65535) {
     set_error("cholb: size out of range");
     return IFK_ERR_INVALID;
   }
-  hipLaunchKernelGGL(cholb_first_kernel, dim3(1), dim3(SNT), 0, s, A, lda, n, U, ldu, Zd, dref, tol,
-                     flag, M, ldm, dref_in ? 1 : 0);
+  hipLaunchKernelGGL(cholb_first_kernel, dim3(1, (unsigned)batch), dim3(SNT), 0, s, A, lda, n, U,
+                     ldu, Zd, dref, tol, flag, M, ldm, dref_in ? 1 : 0, bs);
   if (int rc = check_launch("cholb_first")) return rc;
   const int nb = (n + SB - 1) / SB;
   // step k: the (i, j) pairs k < i <= j (m (m + 1) / 2 of them, m = nb - 1 - k),
@@ -1398,8 +1413,8 @@ int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t 
     const int m = nb - 1 - k;
     const int wgs = m * (m + 1) / 2 + ((M && k > 0) ? k + 1 + k * m : 0);
     if (wgs == 0) continue;
-    hipLaunchKernelGGL(cholb_step_kernel, dim3((unsigned)wgs), dim3(SNT), 0, s, A, lda, n, U, ldu,
-                       Zd, dref, tol, flag, k, M, ldm);
+    hipLaunchKernelGGL(cholb_step_kernel, dim3((unsigned)wgs, (unsigned)batch), dim3(SNT), 0, s, A,
+                       lda, n, U, ldu, Zd, dref, tol, flag, k, M, ldm, bs);
     if (int rc = check_launch("cholb_step")) return rc;
   }
   return IFK_OK;

@@ -154,6 +154,26 @@ int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, 
                            size_t workspace_bytes);
 
 /*
+ * ifk_fold_finalize_gram for `batch` layers of the same shape in the same
+ * launches (replaces the per-layer loop of batched_streaming_tsqr_update /
+ * flush, ifkfac/triangular.py:331-379, ifkfac/activation_hooks.py:370-457,
+ * for the factor update of a bucket of same-shape layers): every launch of
+ * the latency-bound Cholesky chain serves all of them.  X and R_in are HOST
+ * arrays of `batch` device pointers (R_in may be NULL when r_in == 0); entry
+ * b's factor is written at out + b * out_stride elements (out_stride >= n *
+ * ldo), its status to status[b] and its kappa bound to kappa_bound[b] (may be
+ * NULL).  Every entry's result is the one ifk_fold_finalize_gram gives it.
+ */
+size_t ifk_fold_finalize_gram_batched_workspace_size(int64_t batch, int64_t p, int64_t n,
+                                                     int64_t r_in);
+int ifk_fold_finalize_gram_batched(void* stream, int64_t batch, const void* const* X, int x_dtype,
+                                   int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
+                                   int64_t ldr, int64_t r_in, float scale, float damping,
+                                   void* out, int out_dtype, int64_t ldo, int64_t out_stride,
+                                   int math, int32_t* status, float* kappa_bound, void* workspace,
+                                   size_t workspace_bytes);
+
+/*
  * Triangular inverse Z = R^{-1} of an upper-triangular n x n factor (dtype
  * r_dtype) into fp32 Z (ldz).  The four solves of apply_vered are applied as
  * products with Z; this is the factor-side half of them.

@@ -73,6 +73,19 @@ class OracleBackend:
             return out, flag, torch.tensor([kb], dtype=torch.float32)
         return out, flag
 
+    def fold_finalize_gram_batched(self, Rs, r_in, Xs, scale, damping, out_dtype):
+        """The batched Gram factor update, entry by entry (the batched launch gives
+        every entry the single call's bits)."""
+        self.calls["fold_finalize_gram_batched"] += 1
+        outs, sts, kbs = [], [], []
+        for e, X in enumerate(Xs):
+            o, s, k = self.fold_finalize(Rs[e] if Rs is not None else None, r_in, X, scale, damping,
+                                         out_dtype, 1, gram=True, with_kappa=True)
+            outs.append(o)
+            sts.append(s)
+            kbs.append(k)
+        return torch.stack(outs), torch.cat(sts), torch.cat(kbs)
+
     def tri_inverse(self, R, math):
         self.calls["tri_inverse"] += 1
         return torch.from_numpy(np.linalg.inv(_np(R))).float()

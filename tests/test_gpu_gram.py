@@ -162,3 +162,29 @@ def test_fold_finalize_gram_is_deterministic(hip):
     a, _ = hip.fold_finalize(None, 0, X, 1 / math.sqrt(3000), 1e-2, torch.bfloat16, 1, gram=True)
     b, _ = hip.fold_finalize(None, 0, X, 1 / math.sqrt(3000), 1e-2, torch.bfloat16, 1, gram=True)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B,prev,p,n", [(3, 0, 900, 600), (4, 0, 4096, 3100), (2, 1200, 1200, 2100),
+                                        (4, 0, 8192, 4096)])
+def test_fold_finalize_gram_batched_matches_single(hip, B, prev, p, n):
+    """The batched entry (one chain of launches for B same-shape sides) gives every
+    entry exactly the bits of the single-side entry, status and kappa bound included."""
+    g = torch.Generator(device=DEV).manual_seed(B * 7 + n)
+    Xs = [(torch.randn(p, n, device=DEV, generator=g) * (1 + e)).to(torch.bfloat16)
+          for e in range(B)]
+    Rs = None
+    r = 0
+    if prev:
+        Rs = []
+        for e in range(B):
+            R, r = _fold_chunks(hip, [torch.randn(prev, n, device=DEV, generator=g)], n)
+            Rs.append(R)
+    rows = prev + p
+    out, st, kb = hip.fold_finalize_gram_batched(Rs, r, Xs, 1 / math.sqrt(rows), 1e-2,
+                                                 torch.bfloat16)
+    for e in range(B):
+        one, s1, k1 = hip.fold_finalize(Rs[e] if Rs else None, r, Xs[e], 1 / math.sqrt(rows), 1e-2,
+                                        torch.bfloat16, 1, gram=True, with_kappa=True)
+        assert torch.equal(out[e], one), e
+        assert st[e].item() == s1.item() == 1
+        assert kb[e].item() == k1.item()

@@ -528,3 +528,35 @@ def test_chunks_fold_eagerly_between_updates(be):
     assert np.abs(f[first][0].double().numpy() - want).max() < 1e-5
     opt.step()
     assert first in opt._factors
+
+
+def test_bf16_update_batches_same_shape_layers(be):
+    """A consuming bf16 factor update sends the layers whose X sides and G sides
+    share a shape through one batched Gram call per side (three 12 -> 12 layers
+    here; the 12 -> 5 head goes alone), and every layer's factors are its own
+    closed form, as the per-layer path gives them."""
+    from ifkfac_amd import IFKFAC
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(12, 12), nn.Tanh(), nn.Linear(12, 12), nn.Tanh(),
+                          nn.Linear(12, 12), nn.Tanh(), nn.Linear(12, 5))
+    lam = 1e-2
+    opt = IFKFAC(model, lr=1e-3, damping=lam, factor_update_freq=1, use_true_bf16=True)
+    X = torch.randn(48, 12, generator=torch.Generator().manual_seed(3))
+    acts, grads, hs = _capture(model, X)
+    opt.zero_grad()
+    model(X).pow(2).mean().backward()
+    for h in hs:
+        h.remove()
+    import contextlib
+    import io
+    with contextlib.redirect_stdout(io.StringIO()):
+        opt.step()
+    assert be.calls["fold_finalize_gram_batched"] == 2      # the X group and the G group
+    assert be.calls["fold_finalize_gram"] == 2 * 3 + 2      # three batched entries per side + the head
+    for m in opt._factors:
+        R_X, R_G = opt._factors[m]
+        want_X = O.chol_factor([acts[m].double().numpy()], 48, lam)
+        want_G = O.chol_factor([grads[m].double().numpy()], 48, lam)
+        assert np.abs(R_X.double().numpy() - want_X).max() <= 4e-3 * np.abs(want_X).max()
+        assert np.abs(R_G.double().numpy() - want_G).max() <= 4e-3 * np.abs(want_G).max()
+    assert len(opt._factors) == 4
