@@ -273,6 +273,48 @@ class HipBackend:
         _lib.check(rc, "ifk_precondition_apply_bf16")
         return nat
 
+    def inverse_split_copies(self, Z: torch.Tensor) -> Tuple[torch.Tensor, ...]:
+        """bf16 halves of an fp32 inverse for precondition_apply_x3:
+        (Z_hi, Z_lo, Z^T_hi, Z^T_lo), Z = Z_hi + Z_lo, each n x n row-major."""
+        Zc, ldz, zdt = _mat(Z, "inverse_split_copies")
+        n = Zc.shape[0]
+        if Zc.shape != (n, n) or zdt != IFK_F32:
+            raise IFKFACBackendError("inverse_split_copies: Z must be n x n fp32")
+        out = torch.empty((4, n, n), dtype=torch.bfloat16, device=Zc.device)
+        with torch.cuda.device(Zc.device):
+            rc = self.lib.ifk_inverse_split_copies(self._stream(Zc.device), _ptr(Zc), ldz, n,
+                                                   _ptr(out[0]), _ptr(out[1]), _ptr(out[2]),
+                                                   _ptr(out[3]), n)
+        _lib.check(rc, "ifk_inverse_split_copies")
+        return tuple(out.unbind(0))
+
+    def precondition_apply_x3(self, grad: torch.Tensor, ZX4, ZG4) -> torch.Tensor:
+        """precondition_apply at fp32 accuracy from the split copies of
+        inverse_split_copies (views of them, e.g. trimmed, allowed)."""
+        g, ldg, gdt = _mat(grad, "precondition_apply_x3")
+        if gdt != IFK_F32:
+            g = g.float()
+            ldg = g.stride(0)
+        n_out, n_in = g.shape
+        for name, side, n in (("Z_X", ZX4, n_in), ("Z_G", ZG4, n_out)):
+            if len(side) != 4:
+                raise IFKFACBackendError(f"precondition_apply_x3: {name} needs four copies")
+            for t in side:
+                _require_device(t, "precondition_apply_x3")
+                if t.dtype != torch.bfloat16 or t.shape != (n, n) or t.stride(1) != 1 or \
+                        t.stride(0) != side[0].stride(0):
+                    raise IFKFACBackendError(f"precondition_apply_x3: {name} copies must be "
+                                             f"{n} x {n} bf16 row-major with one row stride")
+        nat = torch.empty((n_out, n_in), dtype=torch.float32, device=g.device)
+        ws = self._ws(self.lib.ifk_precondition_apply_x3_workspace_size(n_out, n_in), g.device)
+        with torch.cuda.device(g.device):
+            rc = self.lib.ifk_precondition_apply_x3(
+                self._stream(g.device), _ptr(g), n_out, n_in, ldg, *[_ptr(t) for t in ZX4],
+                ZX4[0].stride(0), *[_ptr(t) for t in ZG4], ZG4[0].stride(0), _ptr(nat), n_in,
+                _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_precondition_apply_x3")
+        return nat
+
     def precondition(self, grad: torch.Tensor, R_X: torch.Tensor, R_G: torch.Tensor,
                      math: int) -> torch.Tensor:
         g, ldg, gdt = _mat(grad, "precondition")

@@ -63,6 +63,12 @@ SIGNATURES = {
                                                 _c_i64, _c_vp, _c_i64, _c_i64, _c_f, _c_f, _c_vp,
                                                 _c_int, _c_i64, _c_i64, _c_int, _c_vp, _c_vp,
                                                 _c_vp, _c_sz]),
+    "ifk_inverse_split_copies": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp,
+                                          _c_i64]),
+    "ifk_precondition_apply_x3_workspace_size": (_c_sz, [_c_i64, _c_i64]),
+    "ifk_precondition_apply_x3": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
+                                           _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp,
+                                           _c_i64, _c_vp, _c_i64, _c_vp, _c_sz]),
     "ifk_tri_inverse_workspace_size": (_c_sz, [_c_i64]),
     "ifk_tri_inverse": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_int,
                                  _c_vp, _c_sz]),

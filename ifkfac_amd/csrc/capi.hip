@@ -193,6 +193,31 @@ int ifk_precondition_apply_bf16(void* stream, const float* grad, int64_t n_out, 
                               ldzg, nat, ldn, workspace, workspace_bytes);
 }
 
+int ifk_inverse_split_copies(void* stream, const float* Z, int64_t ldz, int64_t n, void* Z_hi,
+                             void* Z_lo, void* ZT_hi, void* ZT_lo, int64_t ldb) {
+  return split_inverse((hipStream_t)stream, Z, ldz, n, (bf16_t*)Z_hi, (bf16_t*)Z_lo,
+                       (bf16_t*)ZT_hi, (bf16_t*)ZT_lo, ldb);
+}
+
+size_t ifk_precondition_apply_x3_workspace_size(int64_t n_out, int64_t n_in) {
+  if (n_out < 1 || n_in < 1) return 0;
+  return precondition_apply_x3_ws(n_out, n_in);
+}
+
+int ifk_precondition_apply_x3(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                              int64_t ldg, const void* Z_X_hi, const void* Z_X_lo,
+                              const void* Z_XT_hi, const void* Z_XT_lo, int64_t ldzx,
+                              const void* Z_G_hi, const void* Z_G_lo, const void* Z_GT_hi,
+                              const void* Z_GT_lo, int64_t ldzg, float* nat, int64_t ldn,
+                              void* workspace, size_t workspace_bytes) {
+  const bf16_t* zx[4] = {(const bf16_t*)Z_X_hi, (const bf16_t*)Z_X_lo, (const bf16_t*)Z_XT_hi,
+                         (const bf16_t*)Z_XT_lo};
+  const bf16_t* zg[4] = {(const bf16_t*)Z_G_hi, (const bf16_t*)Z_G_lo, (const bf16_t*)Z_GT_hi,
+                         (const bf16_t*)Z_GT_lo};
+  return precondition_apply_x3((hipStream_t)stream, grad, n_out, n_in, ldg, zx, ldzx, zg, ldzg, nat,
+                               ldn, workspace, workspace_bytes);
+}
+
 size_t ifk_precondition_workspace_size(int64_t n_out, int64_t n_in, int math) {
   if (n_out < 1 || n_in < 1 || !math_ok(math)) return 0;
   return precondition_ws(n_out, n_in, math);

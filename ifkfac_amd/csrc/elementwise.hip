@@ -464,6 +464,75 @@ int launch_transpose_cast(hipStream_t s, const float* src, int64_t lds, int64_t 
   return check_launch("transpose_cast");
 }
 
+// hi[c][r] = RNE bf16(x), lo[c][r] = RNE bf16(x - hi) for x = src[r][c] of a
+// rows x cols fp32 block (the bf16 halves of src^T, row stride ldo), through
+// a 64 x 64 LDS tile: rows read as float4 when src is 16-byte aligned with
+// lds a multiple of 4 (vec_in), the halves written as bf16 pairs when both
+// outputs are 4-byte aligned with ldo even (pairs_out).
+__global__ __launch_bounds__(256) void split_transpose_kernel(const float* src, int64_t lds,
+                                                              int64_t rows, int64_t cols,
+                                                              bf16_t* hi, bf16_t* lo, int64_t ldo,
+                                                              int vec_in, int pairs_out) {
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rl = (t >> 4) + 16 * q, cl = (t & 15) * 4;
+    const int64_t r = r0 + rl, c = c0 + cl;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (r < rows) {
+      if (vec_in && c + 3 < cols) {
+        const float4 x = *reinterpret_cast<const float4*>(src + r * lds + c);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      } else {
+        for (int u = 0; u < 4; ++u)
+          if (c + u < cols) v[u] = src[r * lds + c + u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) tile[rl][cl + u] = v[u];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int idx = t + 256 * q, cl = idx >> 5, rp = (idx & 31) * 2;
+    const int64_t c = c0 + cl, r = r0 + rp;
+    if (c >= cols || r >= rows) continue;
+    const float a = tile[rp][cl], b = tile[rp + 1][cl];
+    const bf16_t ah = f32_to_bf16(a), bh = f32_to_bf16(b);
+    const bf16_t al = f32_to_bf16(a - bf16_to_f32(ah)), bl = f32_to_bf16(b - bf16_to_f32(bh));
+    bf16_t* gh = hi + c * ldo + r;
+    bf16_t* gl = lo + c * ldo + r;
+    if (pairs_out && r + 1 < rows) {
+      *reinterpret_cast<uint32_t*>(gh) = (uint32_t)ah | ((uint32_t)bh << 16);
+      *reinterpret_cast<uint32_t*>(gl) = (uint32_t)al | ((uint32_t)bl << 16);
+    } else {
+      gh[0] = ah;
+      gl[0] = al;
+      if (r + 1 < rows) {
+        gh[1] = bh;
+        gl[1] = bl;
+      }
+    }
+  }
+}
+
+int launch_split_transpose(hipStream_t s, const float* src, int64_t lds, int64_t rows,
+                           int64_t cols, bf16_t* hi, bf16_t* lo, int64_t ldo) {
+  if (rows * cols == 0) return IFK_OK;
+  if (cdiv(rows, 64) > 65535) {
+    set_error("split_transpose: grid too large");
+    return IFK_ERR_INVALID;
+  }
+  const int vec_in = (((uintptr_t)src & 15) == 0) && (lds % 4 == 0);
+  const int pairs_out = (((uintptr_t)hi & 3) == 0) && (((uintptr_t)lo & 3) == 0) && (ldo % 2 == 0);
+  const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64));
+  hipLaunchKernelGGL(split_transpose_kernel, grid, dim3(256), 0, s, src, lds, rows, cols, hi, lo, ldo,
+                     vec_in, pairs_out);
+  return check_launch("split_transpose");
+}
+
 // dst[c][r] = src[r][c] for a rows x cols bf16 block, through a 64 x 64 LDS
 // tile; bf16 pairs move as 32-bit words where both ends of the row are even
 // (pair-aligned), element by element otherwise.

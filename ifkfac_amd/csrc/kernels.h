@@ -168,6 +168,10 @@ int launch_transpose_upper(hipStream_t s, const float* src, int64_t lds, int64_t
 int launch_transpose_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int64_t cols,
                           void* out, int odt, int64_t ldo, int batch = 1, int64_t bss = 0,
                           int64_t bso = 0);
+// hi, lo (cols x rows, ldo) = the bf16 halves of src^T (src rows x cols fp32):
+// hi = RNE(x), lo = RNE(x - hi)
+int launch_split_transpose(hipStream_t s, const float* src, int64_t lds, int64_t rows,
+                           int64_t cols, bf16_t* hi, bf16_t* lo, int64_t ldo);
 // dst[c][r] = src[r][c] for a rows x cols bf16 block
 int launch_transpose_bf16(hipStream_t s, const bf16_t* src, int64_t lds, int64_t rows,
                           int64_t cols, bf16_t* dst, int64_t ldd);

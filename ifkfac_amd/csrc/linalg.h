@@ -83,6 +83,18 @@ int precondition_apply_b(hipStream_t s, const float* grad, int64_t n_out, int64_
                          const bf16_t* ZGb, const bf16_t* ZGt, int64_t ldg2, float* nat,
                          int64_t ldn, void* ws, size_t ws_bytes);
 
+// bf16 halves of an fp32 inverse for precondition_apply_x3: Z = Zh + Zl and
+// Z^T = ZTh + ZTl (row stride ldb).
+int split_inverse(hipStream_t s, const float* Z, int64_t ldz, int64_t n, bf16_t* Zh, bf16_t* Zl,
+                  bf16_t* ZTh, bf16_t* ZTl, int64_t ldb);
+// nat = Z_G Z_G^T grad Z_X Z_X^T at fp32 accuracy from split bf16 operands:
+// ZX, ZG = {Z_hi, Z_lo, Z^T_hi, Z^T_lo}, row strides ldx, ldg2.
+size_t precondition_apply_x3_ws(int64_t n_out, int64_t n_in);
+int precondition_apply_x3(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                          int64_t ldg, const bf16_t* const* ZX, int64_t ldx,
+                          const bf16_t* const* ZG, int64_t ldg2, float* nat, int64_t ldn, void* ws,
+                          size_t ws_bytes);
+
 // nat = Z_G Z_G^T grad Z_X Z_X^T, with Z_X = R_X^{-1}, Z_G = R_G^{-1} given.
 size_t precondition_apply_ws(int64_t n_out, int64_t n_in, int math);
 int precondition_apply(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,

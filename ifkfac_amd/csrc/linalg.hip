@@ -1246,6 +1246,92 @@ static int apply_core_b(hipStream_t s, const bf16_t* gT, int64_t n_out, int64_t 
               B_t(ZXb, DT_BF16, ldx2, TRI_LOWER), 0.0f, out_f32(nat, ldn), 1, sp);
 }
 
+// ----------------------------------------------------------------------------
+// The apply at fp32 accuracy on bf16 MFMA: every operand x = x_hi + x_lo (RNE
+// bf16 halves) and every product a b as a_hi b_hi + a_hi b_lo + a_lo b_hi --
+// three launches into one fp32 result, each keeping the triangular operand's
+// K trimming; the dropped lo.lo term and the roundings leave about 2^-17 of
+// |a||b| per product.  This is the arithmetic for factors whose kappa makes the
+// bf16 apply's rounding visible (the reference's regime, fp32 solves on the
+// bf16-valued factors, triangular.py:621-628, to the same order).
+// ----------------------------------------------------------------------------
+int split_inverse(hipStream_t s, const float* Z, int64_t ldz, int64_t n, bf16_t* Zh, bf16_t* Zl,
+                  bf16_t* ZTh, bf16_t* ZTl, int64_t ldb) {
+  if (n < 1 || ldz < n || ldb < n || !Z || !Zh || !Zl || !ZTh || !ZTl) {
+    set_error("inverse_split_copies: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  RC(launch_split_bf16(s, Z, ldz, n, n, Zh, Zl, ldb, false));
+  return launch_split_transpose(s, Z, ldz, n, n, ZTh, ZTl, ldb);
+}
+
+static void plan_apply_x3(Arena& a, int64_t n_out, int64_t n_in, float** T, bf16_t** Sh,
+                          bf16_t** Sl, bf16_t** gTh, bf16_t** gTl, SplitScratch* sp) {
+  const size_t e = (size_t)n_out * n_in;
+  *T = a.take<float>(e);
+  *Sh = a.take<bf16_t>(e);
+  *Sl = a.take<bf16_t>(e);
+  *gTh = a.take<bf16_t>(e);
+  *gTl = a.take<bf16_t>(e);
+  sp->floats = split_floats(TRINV_NB, std::max(n_out, n_in));
+  sp->p = a.take<float>(sp->floats);
+}
+
+size_t precondition_apply_x3_ws(int64_t n_out, int64_t n_in) {
+  Arena a(nullptr, 0);
+  float* T;
+  bf16_t *Sh, *Sl, *gTh, *gTl;
+  SplitScratch sp;
+  plan_apply_x3(a, n_out, n_in, &T, &Sh, &Sl, &gTh, &gTl, &sp);
+  return a.used;
+}
+
+// C (fp32, ldc) = op(A) op(B) from the halves (A_hi, A_lo) and (B_hi, B_lo)
+static int gemm_x3(hipStream_t s, int64_t M, int64_t N, int64_t K, const MatRef& Ah,
+                   const MatRef& Al, const MatRef& Bh, const MatRef& Bl, float* C, int64_t ldc,
+                   SplitScratch sp) {
+  RC(gemm(s, MATH_BF16, M, N, K, 1.0f, Ah, Bh, 0.0f, out_f32(C, ldc), 1, sp));
+  RC(gemm(s, MATH_BF16, M, N, K, 1.0f, Ah, Bl, 1.0f, out_f32(C, ldc), 1, sp));
+  return gemm(s, MATH_BF16, M, N, K, 1.0f, Al, Bh, 1.0f, out_f32(C, ldc), 1, sp);
+}
+
+int precondition_apply_x3(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                          int64_t ldg, const bf16_t* const* ZX, int64_t ldx,
+                          const bf16_t* const* ZG, int64_t ldg2, float* nat, int64_t ldn, void* ws,
+                          size_t ws_bytes) {
+  if (n_out < 1 || n_in < 1 || ldg < n_in || ldn < n_in || ldx < n_in || ldg2 < n_out || !grad ||
+      !nat || !ZX || !ZG || !ZX[0] || !ZX[1] || !ZX[2] || !ZX[3] || !ZG[0] || !ZG[1] || !ZG[2] ||
+      !ZG[3]) {
+    set_error("precondition_apply_x3: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  float* T;
+  bf16_t *Sh, *Sl, *gTh, *gTl;
+  SplitScratch sp;
+  plan_apply_x3(a, n_out, n_in, &T, &Sh, &Sl, &gTh, &gTl, &sp);
+  RC(check_ws(a, "precondition_apply_x3"));
+  const int B16 = DT_BF16;
+  // ZX / ZG: [Z_hi, Z_lo, Z^T_hi, Z^T_lo]
+  RC(launch_split_transpose(s, grad, ldg, n_out, n_in, gTh, gTl, n_out));
+  // T1^T = grad^T Z_G (n_in x n_out)
+  RC(gemm_x3(s, n_in, n_out, n_out, A_n(gTh, B16, n_out), A_n(gTl, B16, n_out),
+             B_t(ZG[2], B16, ldg2, TRI_UPPER), B_t(ZG[3], B16, ldg2, TRI_UPPER), T, n_out, sp));
+  RC(launch_split_bf16(s, T, n_out, n_in, n_out, Sh, Sl, n_out, false));
+  // T2 = Z_G T1 (n_out x n_in)
+  RC(gemm_x3(s, n_out, n_in, n_out, A_n(ZG[0], B16, ldg2, TRI_UPPER),
+             A_n(ZG[1], B16, ldg2, TRI_UPPER), B_t(Sh, B16, n_out), B_t(Sl, B16, n_out), T, n_in,
+             sp));
+  RC(launch_split_bf16(s, T, n_in, n_out, n_in, Sh, Sl, n_in, false));
+  // T3 = T2 Z_X
+  RC(gemm_x3(s, n_out, n_in, n_in, A_n(Sh, B16, n_in), A_n(Sl, B16, n_in),
+             B_t(ZX[2], B16, ldx, TRI_UPPER), B_t(ZX[3], B16, ldx, TRI_UPPER), T, n_in, sp));
+  RC(launch_split_bf16(s, T, n_in, n_out, n_in, Sh, Sl, n_in, false));
+  // nat = T3 Z_X^T
+  return gemm_x3(s, n_out, n_in, n_in, A_n(Sh, B16, n_in), A_n(Sl, B16, n_in),
+                 B_t(ZX[0], B16, ldx, TRI_LOWER), B_t(ZX[1], B16, ldx, TRI_LOWER), nat, ldn, sp);
+}
+
 static int apply_core(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in, int64_t ldg,
                       const float* ZX, int64_t ldzx, const float* ZG, int64_t ldzg, float* nat,
                       int64_t ldn, int math, void* T1, void* T2, bf16_t* cv, SplitScratch sp) {

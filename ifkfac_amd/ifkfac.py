@@ -14,8 +14,10 @@ the G factor only).  What changes is where the arithmetic happens:
   products with them (``ifk_precondition_apply``);
 * bf16 mode runs a layer's inverses and solves in bf16 arithmetic while both
   of its factors are near-isotropic (kappa_2 estimate from
-  ``ifk_cond_estimate`` at most KAPPA_BF16_MAX), and in fp32 arithmetic on the
-  bf16-valued factors, the reference's regime, otherwise;
+  ``ifk_cond_estimate`` at most KAPPA_BF16_MAX), and at fp32 accuracy on the
+  bf16-valued factors, the reference's regime, otherwise: fp32 inverses whose
+  split bf16 halves every step applies by three MFMA products per product
+  (``ifk_precondition_apply_x3``);
 * momentum, decay and the weight step are one fused pass
   (``ifk_momentum_update``).
 """
@@ -108,6 +110,8 @@ class IFKFAC(torch.optim.Optimizer):
         self._inverses: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         # bf16 arithmetic: RNE bf16 copies ((Z_X, Z_X^T), (Z_G, Z_G^T)) per layer
         self._inverse_copies: Dict[nn.Module, tuple] = {}
+        # fp32 accuracy: split bf16 halves (Z_hi, Z_lo, Z^T_hi, Z^T_lo) per side
+        self._split_copies: Dict[nn.Module, tuple] = {}
         # per layer: MFMA arithmetic of its solves, and the kappa_2 estimates
         # (R_X, R_G) that chose it (bf16 mode)
         self._solve_math: Dict[nn.Module, int] = {}
@@ -143,6 +147,7 @@ class IFKFAC(torch.optim.Optimizer):
         out_dtype = torch.bfloat16 if (self.use_true_bf16 and not blend) else torch.float32
         be = get_backend()
         copies = hasattr(be, "tri_inverse_bf16")
+        split = hasattr(be, "precondition_apply_x3")
 
         def inverse(side, module, R, kappa_bound=None):
             m = solve_math_for(R.dtype)
@@ -198,6 +203,7 @@ class IFKFAC(torch.optim.Optimizer):
         self._factors = clean
         self._inverses = {}
         self._inverse_copies = {}
+        self._split_copies = {}
         self._solve_math = {}
         self._kappas = {}
         invs = {}
@@ -225,13 +231,23 @@ class IFKFAC(torch.optim.Optimizer):
                 self._inverse_copies[module] = ((invX[1], invX[2]), (invG[1], invG[2]))
                 self._solve_math[module] = MATH_BF16
             else:
-                # fp32 arithmetic on the bf16-valued factors (the reference's regime)
+                # fp32 accuracy on the bf16-valued factors (the reference's
+                # regime): fp32 inverses, applied through their split bf16
+                # halves (three MFMA products per solve product) when the
+                # backend has that apply, else by fp32 arithmetic
                 logger.debug("IFKFAC: kappa(R_X) %.3g, kappa(R_G) %.3g: fp32 solves for %s",
                              kx, kg, type(module).__name__)
-                self._inverses[module] = run_pair(
-                    R_X.device, lambda R=R_X: be.tri_inverse(R, MATH_F32),
-                    lambda R=R_G: be.tri_inverse(R, MATH_F32),
-                    b_first=R_G.shape[0] > R_X.shape[0])
+
+                def inv32(R):
+                    Z = be.tri_inverse(R, MATH_F32)
+                    return (Z, be.inverse_split_copies(Z)) if split else (Z, None)
+
+                (ZX, sx), (ZG, sg) = run_pair(R_X.device, lambda R=R_X: inv32(R),
+                                              lambda R=R_G: inv32(R),
+                                              b_first=R_G.shape[0] > R_X.shape[0])
+                self._inverses[module] = (ZX, ZG)
+                if split:
+                    self._split_copies[module] = (sx, sg)
                 self._solve_math[module] = MATH_F32
         self.timing["factor_compute"].append(time.perf_counter() - t0)
 
@@ -249,6 +265,12 @@ class IFKFAC(torch.optim.Optimizer):
             if trim:
                 ZXb, ZXt = ZXb[:-1, :-1], ZXt[:-1, :-1]
             return get_backend().precondition_apply_bf16(grad_w, (ZXb, ZXt), ZG2)
+        split = self._split_copies.get(module)
+        if split is not None:
+            sx, sg = split
+            if trim:
+                sx = tuple(t[:-1, :-1] for t in sx)
+            return get_backend().precondition_apply_x3(grad_w, sx, sg)
         Z_X, Z_G = self._inverses[module]
         if trim:
             Z_X = Z_X[:-1, :-1]
@@ -419,6 +441,7 @@ class IFKFAC(torch.optim.Optimizer):
         self._factors.clear()
         self._inverses.clear()
         self._inverse_copies.clear()
+        self._split_copies.clear()
         self._solve_math.clear()
         self._kappas.clear()
         self._classic_fallback.clear()

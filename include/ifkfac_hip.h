@@ -238,6 +238,27 @@ int ifk_precondition_apply_bf16(void* stream, const float* grad, int64_t n_out, 
                                 int64_t ldn, void* workspace, size_t workspace_bytes);
 
 /*
+ * The apply at fp32 accuracy on bf16 MFMA, for factors whose kappa_2 makes the
+ * bf16 apply's rounding visible (IFKFAC's bf16 mode takes it when the factor
+ * update's kappa bound exceeds 1.5; the reference's bf16 mode solves in fp32
+ * on the bf16-valued factors, ifkfac/triangular.py:621-628).  Every product of
+ * nat = Z_G Z_G^T grad Z_X Z_X^T is formed from bf16 halves x = x_hi + x_lo as
+ * a_hi b_hi + a_hi b_lo + a_lo b_hi (three MFMA launches into one fp32 result,
+ * about 2^-17 of |a||b| per product).  ifk_inverse_split_copies makes a side's
+ * halves from its fp32 inverse Z (tri_inverse): Z_hi, Z_lo (row-major) and
+ * ZT_hi, ZT_lo (Z^T), all n x n bf16 with row stride ldb.
+ */
+int ifk_inverse_split_copies(void* stream, const float* Z, int64_t ldz, int64_t n, void* Z_hi,
+                             void* Z_lo, void* ZT_hi, void* ZT_lo, int64_t ldb);
+size_t ifk_precondition_apply_x3_workspace_size(int64_t n_out, int64_t n_in);
+int ifk_precondition_apply_x3(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                              int64_t ldg, const void* Z_X_hi, const void* Z_X_lo,
+                              const void* Z_XT_hi, const void* Z_XT_lo, int64_t ldzx,
+                              const void* Z_G_hi, const void* Z_G_lo, const void* Z_GT_hi,
+                              const void* Z_GT_lo, int64_t ldzg, float* nat, int64_t ldn,
+                              void* workspace, size_t workspace_bytes);
+
+/*
  * ifk_precondition_apply_bf16 without a workspace argument: its scratch is a
  * 64 MiB device array inside this library (one per GPU, held until the
  * process ends), so the call allocates nothing.  No counterpart in the

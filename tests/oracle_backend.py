@@ -106,6 +106,20 @@ class OracleBackend:
         zx, zg = _np(ZX2[0]), _np(ZG2[0])
         return torch.from_numpy(zg @ (zg.T @ _np(grad)) @ zx @ zx.T).float()
 
+    def inverse_split_copies(self, Z):
+        """RNE bf16 halves (Z_hi, Z_lo, Z^T_hi, Z^T_lo), as ifk_inverse_split_copies."""
+        self.calls["inverse_split_copies"] += 1
+        Z = Z.float()
+        hi = Z.bfloat16()
+        lo = (Z - hi.float()).bfloat16()
+        return hi, lo, hi.t().contiguous(), lo.t().contiguous()
+
+    def precondition_apply_x3(self, grad, ZX4, ZG4):
+        self.calls["precondition_apply_x3"] += 1
+        zx = _np(ZX4[0]) + _np(ZX4[1])
+        zg = _np(ZG4[0]) + _np(ZG4[1])
+        return torch.from_numpy(zg @ (zg.T @ _np(grad)) @ zx @ zx.T).float()
+
     def precondition(self, grad, R_X, R_G, math):
         self.calls["precondition"] += 1
         return torch.from_numpy(O.apply_vered(_np(grad), _np(R_X), _np(R_G))).float()

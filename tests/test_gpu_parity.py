@@ -579,6 +579,71 @@ def test_precondition_apply_bf16_copies(hip, n_out, n_in, trim):
         assert _rel(got, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("n", [1, 65, 300, 2049])
+def test_inverse_split_copies(hip, n):
+    """ifk_inverse_split_copies: Z_hi = RNE(Z), Z_lo = RNE(Z - Z_hi) and the same
+    halves of Z^T, exactly."""
+    rng = np.random.default_rng(n + 13)
+    R = np.triu(rng.standard_normal((n, n))) / math.sqrt(n) + 2 * np.eye(n)
+    Z = hip.tri_inverse(torch.tensor(R, dtype=torch.float32, device=DEV), 0)
+    hi, lo, thi, tlo = hip.inverse_split_copies(Z)
+    assert torch.equal(hi, Z.bfloat16())
+    assert torch.equal(lo, (Z - hi.float()).bfloat16())
+    assert torch.equal(thi, hi.t().contiguous()) and torch.equal(tlo, lo.t().contiguous())
+
+
+def _exposed_factor(p, n, kappa, seed):
+    """kappa(R_damped) ~ kappa: X scaled by sqrt(p), lambda far below sigma_min^2."""
+    rng = np.random.default_rng(seed)
+    X = O.kappa_matrix(p, n, kappa, rng) * math.sqrt(p)
+    return O.bf16_round(O.get_factor(O.streaming_tsqr_update(None, X), p, 1e-5).astype(np.float32))
+
+
+@pytest.mark.parametrize("n_out,n_in,trim,exposed", [
+    (256, 128, False, False), (1100, 700, False, False), (300, 701, True, False),
+    (2100, 1500, False, False), (512, 256, False, True), (1300, 1024, False, True)])
+def test_precondition_apply_x3(hip, n_out, n_in, trim, exposed):
+    """The split-bf16 apply (three MFMA products per product from the hi/lo
+    halves of the fp32 inverses) against fp64 solves on the same bf16 factors:
+    within 4 * 2^-17 kappa(R_X) kappa(R_G), the accuracy of the split products
+    through the kappa-amplifying solves, and far below the bf16 apply's error
+    (a dropped lo half fails it); also for the trimmed views IFKFAC passes with
+    augment_bias."""
+    if exposed:
+        R_X = _exposed_factor(4 * n_in, n_in, 1e2, 1)
+        R_G = _exposed_factor(4 * n_out, n_out, 1e1, 2)
+    else:
+        R_X = O.bf16_round(_factors(4 * n_in, n_in, 1e-2, 1e2, 1).astype(np.float32))
+        R_G = O.bf16_round(_factors(4 * n_out, n_out, 1e-2, 1e1, 2).astype(np.float32))
+    RX = torch.tensor(R_X, device=DEV).to(torch.bfloat16)
+    RG = torch.tensor(R_G, device=DEV).to(torch.bfloat16)
+    ZX = hip.tri_inverse(RX, 0)
+    ZG = hip.tri_inverse(RG, 0)
+    sx, sg = hip.inverse_split_copies(ZX), hip.inverse_split_copies(ZG)
+    m = n_in - 1 if trim else n_in
+    if trim:
+        sx = tuple(t[:-1, :-1] for t in sx)
+    g = torch.tensor(np.random.default_rng(3).normal(0, 0.1, (n_out, m)), dtype=torch.float32,
+                     device=DEV)
+    got = hip.precondition_apply_x3(g, sx, sg)
+    rx = R_X.astype(np.float64)[:m, :m] if trim else R_X.astype(np.float64)
+    # trimming Z_X = R_X^{-1} to its leading block is the inverse of R_X's leading block
+    ref = O.apply_vered(g.double().cpu().numpy(), rx, R_G.astype(np.float64))
+    kx, kg = _kappa(rx), _kappa(R_G.astype(np.float64))
+    e = _rel(got, ref)
+    print(f"x3 apply {n_out}x{m}: rel {e:.3e}, kappa(R_X) {kx:.3g}, kappa(R_G) {kg:.3g}")
+    assert e <= 4 * 2.0 ** -17 * kx * kg
+    assert e <= 1e-3 * max(1.0, kx * kg / 100)
+    if exposed:
+        # the fp32-arithmetic apply on the same inverses, for scale
+        e32 = _rel(hip.precondition_apply(g, ZX, ZG, 0), ref)
+        print(f"  fp32 apply: rel {e32:.3e}")
+    if not trim:
+        ZXb, ZXt = sx[0], sx[2]
+        eb = _rel(hip.precondition_apply_bf16(g, (ZXb, ZXt), (sg[0], sg[2])), ref)
+        assert e <= eb / 10
+
+
 @pytest.mark.parametrize("n,kappa", [(64, 1.0), (300, 3.0), (1100, 50.0), (2049, 1e3)])
 @pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
 def test_cond_estimate(hip, n, kappa, rdt):
