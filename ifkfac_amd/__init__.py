@@ -12,12 +12,16 @@ All curvature arithmetic runs in ``libifkfac_hip.so`` (include/ifkfac_hip.h);
 tensors must live on a ROCm device.
 """
 from .activation_hooks import IFKFACRankError, RawActivationHooks
+from .classic_kfac import ClassicKFAC
 from .ifkfac import IFKFAC
+from .kfac_hooks import KFACHooks
 from ._lib import IFKFACBackendError
 
 __version__ = "0.1.0"
 __all__ = [
     "IFKFAC",
+    "ClassicKFAC",
+    "KFACHooks",
     "RawActivationHooks",
     "IFKFACRankError",
     "IFKFACBackendError",

@@ -315,6 +315,75 @@ class HipBackend:
         _lib.check(rc, "ifk_precondition_apply_x3")
         return nat
 
+    # -- Classic K-FAC control ------------------------------------------------------
+    def gram_accumulate_(self, S: torch.Tensor, X: torch.Tensor, beta: float) -> None:
+        """S = beta S + X^T X in place (S fp32 n x n contiguous, X p x n)."""
+        Xc, ldx, xdt = _mat(X, "gram_accumulate")
+        p, n = Xc.shape
+        _require_device(S, "gram_accumulate")
+        if S.dtype != torch.float32 or S.shape != (n, n) or S.stride(1) != 1:
+            raise IFKFACBackendError("gram_accumulate: S must be an n x n fp32 row-major matrix")
+        ws = self._ws(self.lib.ifk_gram_accumulate_workspace_size(n), Xc.device)
+        with torch.cuda.device(Xc.device):
+            rc = self.lib.ifk_gram_accumulate(self._stream(Xc.device), _ptr(Xc), xdt, p, n, ldx,
+                                              _ptr(S), S.stride(0), float(beta), _ptr(ws),
+                                              ws.numel())
+        _lib.check(rc, "ifk_gram_accumulate")
+
+    def axpby(self, alpha: float, X: torch.Tensor, beta: float,
+              Y: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """alpha X + beta Y (fp32; a new tensor when Y is None, else Y in place)."""
+        Xc, ldx, xdt = _mat(X, "axpby")
+        if xdt != IFK_F32:
+            raise IFKFACBackendError("axpby: X must be fp32")
+        rows, cols = Xc.shape
+        if Y is None:
+            Y = torch.empty((rows, cols), dtype=torch.float32, device=Xc.device)
+            beta = 0.0
+        elif Y.dtype != torch.float32 or Y.shape != Xc.shape or Y.stride(1) != 1:
+            raise IFKFACBackendError("axpby: Y must match X (fp32, row-major)")
+        with torch.cuda.device(Xc.device):
+            rc = self.lib.ifk_axpby(self._stream(Xc.device), float(alpha), _ptr(Xc), ldx,
+                                    float(beta), _ptr(Y), Y.stride(0), rows, cols)
+        _lib.check(rc, "ifk_axpby")
+        return Y
+
+    def inv_spd_damped(self, A: torch.Tensor, damping: float) -> torch.Tensor:
+        """(A + damping I)^{-1} in fp32 (Cholesky and triangular inverse)."""
+        Ac, lda, adt = _mat(A, "inv_spd_damped")
+        n = Ac.shape[0]
+        if Ac.shape != (n, n):
+            raise IFKFACBackendError("inv_spd_damped: A must be square")
+        X = torch.empty((n, n), dtype=torch.float32, device=Ac.device)
+        ws = self._ws(self.lib.ifk_inv_spd_damped_workspace_size(n), Ac.device)
+        with torch.cuda.device(Ac.device):
+            rc = self.lib.ifk_inv_spd_damped(self._stream(Ac.device), _ptr(Ac), adt, n, lda,
+                                             float(damping), _ptr(X), n, _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_inv_spd_damped")
+        return X
+
+    def classic_precondition(self, grad: torch.Tensor, A_inv: torch.Tensor,
+                             G_inv: torch.Tensor) -> torch.Tensor:
+        """G_inv grad A_inv in fp32."""
+        g, ldg, gdt = _mat(grad, "classic_precondition")
+        if gdt != IFK_F32:
+            g = g.float()
+            ldg = g.stride(0)
+        n_out, n_in = g.shape
+        Ai, ldai, adt = _mat(A_inv, "classic_precondition")
+        Gi, ldgi, gidt = _mat(G_inv, "classic_precondition")
+        if adt != IFK_F32 or gidt != IFK_F32 or Ai.shape != (n_in, n_in) or \
+                Gi.shape != (n_out, n_out):
+            raise IFKFACBackendError("classic_precondition: inverses must be fp32 and match grad")
+        nat = torch.empty((n_out, n_in), dtype=torch.float32, device=g.device)
+        ws = self._ws(self.lib.ifk_classic_precondition_workspace_size(n_out, n_in), g.device)
+        with torch.cuda.device(g.device):
+            rc = self.lib.ifk_classic_precondition(self._stream(g.device), _ptr(g), n_out, n_in,
+                                                   ldg, _ptr(Ai), ldai, _ptr(Gi), ldgi, _ptr(nat),
+                                                   n_in, _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_classic_precondition")
+        return nat
+
     def precondition(self, grad: torch.Tensor, R_X: torch.Tensor, R_G: torch.Tensor,
                      math: int) -> torch.Tensor:
         g, ldg, gdt = _mat(grad, "precondition")

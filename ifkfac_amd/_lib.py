@@ -104,6 +104,16 @@ SIGNATURES = {
     "ifk_potrf_workspace_size": (_c_sz, [_c_i64]),
     "ifk_potrf": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_int, _c_i64, _c_int,
                            _c_vp, _c_sz]),
+    "ifk_gram_accumulate_workspace_size": (_c_sz, [_c_i64]),
+    "ifk_gram_accumulate": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64,
+                                     _c_f, _c_vp, _c_sz]),
+    "ifk_axpby": (_c_int, [_c_vp, _c_f, _c_vp, _c_i64, _c_f, _c_vp, _c_i64, _c_i64, _c_i64]),
+    "ifk_inv_spd_damped_workspace_size": (_c_sz, [_c_i64]),
+    "ifk_inv_spd_damped": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_f, _c_vp, _c_i64,
+                                    _c_vp, _c_sz]),
+    "ifk_classic_precondition_workspace_size": (_c_sz, [_c_i64, _c_i64]),
+    "ifk_classic_precondition": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64,
+                                          _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_sz]),
     "ifk_inv_spd_workspace_size": (_c_sz, [_c_i64]),
     "ifk_inv_spd": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_int, _c_i64, _c_int,
                              _c_vp, _c_sz]),

@@ -315,6 +315,52 @@ int ifk_inv_spd(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda
                  workspace_bytes);
 }
 
+size_t ifk_gram_accumulate_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return gram_accumulate_ws(n);
+}
+
+int ifk_gram_accumulate(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
+                        int64_t ldx, float* S, int64_t lds, float beta, void* workspace,
+                        size_t workspace_bytes) {
+  GUARD(dt_ok(x_dtype), "gram_accumulate: bad dtype");
+  return gram_accumulate((hipStream_t)stream, X, x_dtype, p, n, ldx, S, lds, beta, workspace,
+                         workspace_bytes);
+}
+
+int ifk_axpby(void* stream, float alpha, const float* X, int64_t ldx, float beta, float* Y,
+              int64_t ldy, int64_t rows, int64_t cols) {
+  GUARD(rows >= 0 && cols >= 0 && ldx >= cols && ldy >= cols && (rows * cols == 0 || (X && Y)),
+        "axpby: invalid arguments");
+  return launch_axpby((hipStream_t)stream, alpha, X, ldx, beta, Y, ldy, rows, cols);
+}
+
+size_t ifk_inv_spd_damped_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return inv_spd_damped_ws(n);
+}
+
+int ifk_inv_spd_damped(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda,
+                       float damping, float* X, int64_t ldx, void* workspace,
+                       size_t workspace_bytes) {
+  GUARD(dt_ok(a_dtype), "inv_spd_damped: bad dtype");
+  return inv_spd_damped((hipStream_t)stream, A, a_dtype, n, lda, damping, X, ldx, workspace,
+                        workspace_bytes);
+}
+
+size_t ifk_classic_precondition_workspace_size(int64_t n_out, int64_t n_in) {
+  if (n_out < 1 || n_in < 1) return 0;
+  return classic_precondition_ws(n_out, n_in);
+}
+
+int ifk_classic_precondition(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                             int64_t ldg, const float* A_inv, int64_t ldai, const float* G_inv,
+                             int64_t ldgi, float* nat, int64_t ldn, void* workspace,
+                             size_t workspace_bytes) {
+  return classic_precondition((hipStream_t)stream, grad, n_out, n_in, ldg, A_inv, ldai, G_inv,
+                              ldgi, nat, ldn, workspace, workspace_bytes);
+}
+
 size_t ifk_gemm_workspace_size(int64_t m, int64_t n) {
   if (m < 1 || n < 1) return 0;
   size_t f = (size_t)m * n * 64;

@@ -608,6 +608,62 @@ int launch_add_diag(hipStream_t s, float* A, int64_t lda, int64_t n, float v) {
   return check_launch("add_diag");
 }
 
+// S[c][r] = S[r][c] for r > c (the upper triangle from the lower), one 64 x 64
+// tile pair per workgroup through LDS: tile (by, bx) with by >= bx is read and
+// written transposed into tile (bx, by).  Workgroups of upper tiles exit.
+__global__ __launch_bounds__(256) void mirror_lower_kernel(float* S, int64_t ld, int64_t n) {
+  if (blockIdx.y < blockIdx.x) return;
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int e = t + 256 * q, rl = e >> 6, cl = e & 63;
+    const int64_t r = r0 + rl, c = c0 + cl;
+    tile[rl][cl] = (r < n && c < n) ? S[r * ld + c] : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int e = t + 256 * q, rl = e >> 6, cl = e & 63;
+    // destination (c0 + rl, r0 + cl) holds source (r0 + cl, c0 + rl)
+    const int64_t dr = c0 + rl, dc = r0 + cl;
+    if (dr < n && dc < n && dc > dr) S[dr * ld + dc] = tile[cl][rl];
+  }
+}
+
+// Y = alpha X + beta Y (fp32, rows x cols); beta == 0 does not read Y.
+__global__ void axpby_kernel(float alpha, const float* X, int64_t ldx, float beta, float* Y,
+                             int64_t ldy, int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / cols, c = e - r * cols;
+    const float x = alpha * X[r * ldx + c];
+    Y[r * ldy + c] = beta == 0.0f ? x : x + beta * Y[r * ldy + c];
+  }
+}
+
+int launch_axpby(hipStream_t s, float alpha, const float* X, int64_t ldx, float beta, float* Y,
+                 int64_t ldy, int64_t rows, int64_t cols) {
+  if (rows * cols <= 0) return IFK_OK;
+  const int64_t blocks = std::min<int64_t>(cdiv(rows * cols, 256), 65536);
+  hipLaunchKernelGGL(axpby_kernel, dim3((unsigned)blocks), dim3(256), 0, s, alpha, X, ldx, beta,
+                     Y, ldy, rows, cols);
+  return check_launch("axpby");
+}
+
+int launch_mirror_lower(hipStream_t s, float* S, int64_t ld, int64_t n) {
+  if (n <= 0) return IFK_OK;
+  if (cdiv(n, 64) > 65535) {
+    set_error("mirror_lower: matrix too large");
+    return IFK_ERR_INVALID;
+  }
+  const dim3 grid((unsigned)cdiv(n, 64), (unsigned)cdiv(n, 64));
+  hipLaunchKernelGGL(mirror_lower_kernel, grid, dim3(256), 0, s, S, ld, n);
+  return check_launch("mirror_lower");
+}
+
 
 // ---------------------------------------------------------------------------
 // Power-iteration helpers of the condition estimate (linalg.hip: cond_est).

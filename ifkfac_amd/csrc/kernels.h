@@ -177,6 +177,11 @@ int launch_transpose_bf16(hipStream_t s, const bf16_t* src, int64_t lds, int64_t
                           int64_t cols, bf16_t* dst, int64_t ldd);
 // A[i][i] += v, i < n
 int launch_add_diag(hipStream_t s, float* A, int64_t lda, int64_t n, float v);
+// Y = alpha X + beta Y (fp32); beta == 0 does not read Y
+int launch_axpby(hipStream_t s, float alpha, const float* X, int64_t ldx, float beta, float* Y,
+                 int64_t ldy, int64_t rows, int64_t cols);
+// S[c][r] = S[r][c] for r > c: a symmetric matrix from its lower triangle
+int launch_mirror_lower(hipStream_t s, float* S, int64_t ld, int64_t n);
 // condition-estimate helpers (elementwise.hip)
 int launch_probe_init(hipStream_t s, float* V, int64_t n, int k);
 int launch_colnorm(hipStream_t s, float* V, int64_t n, int k, float* ss);

@@ -83,6 +83,19 @@ int precondition_apply_b(hipStream_t s, const float* grad, int64_t n_out, int64_
                          const bf16_t* ZGb, const bf16_t* ZGt, int64_t ldg2, float* nat,
                          int64_t ldn, void* ws, size_t ws_bytes);
 
+// Classic K-FAC control: S = beta S + X^T X (full symmetric, fp32), the damped
+// SPD inverse (A + damping I)^{-1} by Cholesky, and nat = G^{-1} grad A^{-1}.
+size_t gram_accumulate_ws(int64_t n);
+int gram_accumulate(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                    float* S, int64_t lds, float beta, void* ws, size_t ws_bytes);
+size_t inv_spd_damped_ws(int64_t n);
+int inv_spd_damped(hipStream_t s, const void* A, int adt, int64_t n, int64_t lda, float damping,
+                   float* X, int64_t ldx, void* ws, size_t ws_bytes);
+size_t classic_precondition_ws(int64_t n_out, int64_t n_in);
+int classic_precondition(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                         int64_t ldg, const float* A_inv, int64_t ldai, const float* G_inv,
+                         int64_t ldgi, float* nat, int64_t ldn, void* ws, size_t ws_bytes);
+
 // bf16 halves of an fp32 inverse for precondition_apply_x3: Z = Zh + Zl and
 // Z^T = ZTh + ZTl (row stride ldb).
 int split_inverse(hipStream_t s, const float* Z, int64_t ldz, int64_t n, bf16_t* Zh, bf16_t* Zl,

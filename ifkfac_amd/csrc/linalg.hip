@@ -1679,4 +1679,80 @@ int inv_spd(hipStream_t s, const void* A, int adt, int64_t n, int64_t lda, void*
               0.0f, o, 1, tsp);
 }
 
+// ----------------------------------------------------------------------------
+// Classic K-FAC control: explicit Gram factors and their damped inverses
+// (ifkfac/kfac_hooks.py:208-258, ifkfac/classic_kfac.py:119-141, :218).
+// ----------------------------------------------------------------------------
+size_t gram_accumulate_ws(int64_t n) { return split_floats(TRINV_NB, n) * sizeof(float) + 256; }
+
+int gram_accumulate(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                    float* S, int64_t lds, float beta, void* ws, size_t ws_bytes) {
+  if (p < 1 || n < 1 || ldx < n || lds < n || !X || !S || (xdt != DT_F32 && xdt != DT_BF16)) {
+    set_error("gram_accumulate: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  SplitScratch sp;
+  sp.floats = split_floats(TRINV_NB, n);
+  sp.p = a.take<float>(sp.floats);
+  RC(check_ws(a, "gram_accumulate"));
+  // the arithmetic of the activations' own product (torch mm in their dtype)
+  const int math = xdt == DT_F32 ? MATH_F32 : MATH_BF16;
+  RC(gemm(s, math, n, n, p, 1.0f, A_t(X, xdt, ldx), B_n(X, xdt, ldx), beta,
+          lower_part(out_f32(S, lds)), 1, sp));
+  return launch_mirror_lower(s, S, lds, n);
+}
+
+size_t inv_spd_damped_ws(int64_t n) { return inv_spd_ws(n); }
+
+int inv_spd_damped(hipStream_t s, const void* A, int adt, int64_t n, int64_t lda, float damping,
+                   float* X, int64_t ldx, void* ws, size_t ws_bytes) {
+  if (n < 1 || lda < n || ldx < n || !A || !X || !(damping >= 0.0f)) {
+    set_error("inv_spd_damped: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  float *W, *Zk, *tmp;
+  SplitScratch sp;
+  plan_potrf(a, n, &W, &Zk, &tmp, &sp);
+  float* Z = a.take<float>((size_t)n * n);
+  float* ttmp;
+  SplitScratch tsp;
+  plan_trinv(a, n, &ttmp, &tsp);
+  RC(check_ws(a, "inv_spd_damped"));
+  RC(launch_copy_to_f32(s, A, adt, lda, n, n, 1.0f, W, n));
+  RC(launch_add_diag(s, W, n, n, damping));
+  RC(potrf_core(s, W, n, MATH_F32, Zk, tmp, sp));
+  // (A + damping I)^{-1} = U^{-1} U^{-T} with A + damping I = U^T U
+  RC(trinv_core(s, W, DT_F32, n, n, Z, n, MATH_F32, 1, ttmp, tsp));
+  return gemm(s, MATH_F32, n, n, n, 1.0f, A_n(Z, DT_F32, n, TRI_UPPER),
+              B_t(Z, DT_F32, n, TRI_LOWER), 0.0f, out_f32(X, ldx), 1, tsp);
+}
+
+size_t classic_precondition_ws(int64_t n_out, int64_t n_in) {
+  return ((size_t)n_out * n_in + split_floats(TRINV_NB, std::max(n_out, n_in))) * sizeof(float) +
+         512;
+}
+
+int classic_precondition(hipStream_t s, const float* grad, int64_t n_out, int64_t n_in,
+                         int64_t ldg, const float* A_inv, int64_t ldai, const float* G_inv,
+                         int64_t ldgi, float* nat, int64_t ldn, void* ws, size_t ws_bytes) {
+  if (n_out < 1 || n_in < 1 || ldg < n_in || ldai < n_in || ldgi < n_out || ldn < n_in || !grad ||
+      !A_inv || !G_inv || !nat) {
+    set_error("classic_precondition: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  float* T = a.take<float>((size_t)n_out * n_in);
+  SplitScratch sp;
+  sp.floats = split_floats(TRINV_NB, std::max(n_out, n_in));
+  sp.p = a.take<float>(sp.floats);
+  RC(check_ws(a, "classic_precondition"));
+  // nat = G^{-1} grad A^{-1} (classic_kfac.py:218), fp32 arithmetic
+  RC(gemm(s, MATH_F32, n_out, n_in, n_in, 1.0f, A_n(grad, DT_F32, ldg), B_n(A_inv, DT_F32, ldai),
+          0.0f, out_f32(T, n_in), 1, sp));
+  return gemm(s, MATH_F32, n_out, n_in, n_out, 1.0f, A_n(G_inv, DT_F32, ldgi),
+              B_n(T, DT_F32, n_in), 0.0f, out_f32(nat, ldn), 1, sp);
+}
+
 }  // namespace ifk

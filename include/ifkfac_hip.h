@@ -334,6 +334,39 @@ int ifk_inv_spd(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda
                 int x_dtype, int64_t ldx, int math, void* workspace, size_t workspace_bytes);
 
 /*
+ * Classic K-FAC control (the reference's explicit-Gram baseline, kept to
+ * contrast the kappa^2 of forming X^T X with the factor path's kappa):
+ *   ifk_gram_accumulate   S = beta S + X^T X, full symmetric fp32 n x n, in the
+ *                         arithmetic of the activations' dtype -- replaces
+ *                         `x.t().mm(x)` + `A_sum.add_` of KFACHooks' hooks
+ *                         (ifkfac/kfac_hooks.py:208-214, :239-245);
+ *   ifk_inv_spd_damped    X = (A + damping I)^{-1} in fp32 by Cholesky (pivots
+ *                         clamped at 1e-7) and the triangular inverse --
+ *                         replaces `A + damping * eye` + `torch.linalg.inv`
+ *                         (ifkfac/classic_kfac.py:131-138);
+ *   ifk_classic_precondition  nat = G_inv grad A_inv in fp32 -- replaces
+ *                         `G_inv @ grad_w @ A_inv` (ifkfac/classic_kfac.py:218).
+ */
+size_t ifk_gram_accumulate_workspace_size(int64_t n);
+int ifk_gram_accumulate(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
+                        int64_t ldx, float* S, int64_t lds, float beta, void* workspace,
+                        size_t workspace_bytes);
+/* Y = alpha X + beta Y (fp32 rows x cols; beta == 0 does not read Y): the
+ * Gram averages A_sum / n_A (kfac_hooks.py:263-264) and the EMA blend
+ * gamma A_old + (1 - gamma) A_new (classic_kfac.py:113-120). */
+int ifk_axpby(void* stream, float alpha, const float* X, int64_t ldx, float beta, float* Y,
+              int64_t ldy, int64_t rows, int64_t cols);
+size_t ifk_inv_spd_damped_workspace_size(int64_t n);
+int ifk_inv_spd_damped(void* stream, const void* A, int a_dtype, int64_t n, int64_t lda,
+                       float damping, float* X, int64_t ldx, void* workspace,
+                       size_t workspace_bytes);
+size_t ifk_classic_precondition_workspace_size(int64_t n_out, int64_t n_in);
+int ifk_classic_precondition(void* stream, const float* grad, int64_t n_out, int64_t n_in,
+                             int64_t ldg, const float* A_inv, int64_t ldai, const float* G_inv,
+                             int64_t ldgi, float* nat, int64_t ldn, void* workspace,
+                             size_t workspace_bytes);
+
+/*
  * General MFMA matrix product C = alpha op(A) op(B) + beta C, exposed for
  * tests and for callers that compose the path themselves.  Bit 0 of
  * trans_a/trans_b selects op(X) = X^T; bits 1-2 declare op(X) upper (1) or

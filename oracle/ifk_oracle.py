@@ -18,6 +18,12 @@ torch.linalg on CPU).  How each function is pinned (tests/test_oracle.py):
                              and the recipe tests of tests/test_equivalence.py
   bf16_round                 hand-computed RNE ties, NaN/Inf, subnormals
   momentum_step              the recurrence unrolled by hand for 3 steps
+  gram_average               brute-force sum of row outer products; chunking
+                             invariance; a planted 1/chunks average fails
+  classic_inverse            (A + lambda I) X = I; 1x1 and diagonal closed
+                             forms; a planted undamped inverse fails
+  classic_nat                diagonal closed form g_ij / ((a_j + l)(g_i + l))
+  classic_updates_at         the schedule listed by hand for freq 1, 3, 10
   bf16_linalg restatements   R vs chol(A^T A), L L^T vs A, R X vs B at tolerance;
                              the special cases by hand: _safe_div's signed
                              magnitude clamp (|d| < 1e-7 -> sign(d) 1e-7, sign(0)
@@ -184,6 +190,42 @@ def should_update_factors(step: int, freq: int) -> bool:
     if freq == 1:
         return True
     return step >= freq and step % freq == 0
+
+
+# ----------------------------------------------------------------------------
+# kfac_hooks.py / classic_kfac.py restatements (the Classic K-FAC control)
+# ----------------------------------------------------------------------------
+
+
+def gram_average(chunks) -> np.ndarray:
+    """A = sum_i x_i^T x_i / sum_i rows_i over the captured chunks
+    (kfac_hooks.py:208-214 accumulate, :262-264 average), in fp64."""
+    S = None
+    rows = 0
+    for x in chunks:
+        x = np.asarray(x, dtype=np.float64)
+        g = x.T @ x
+        S = g if S is None else S + g
+        rows += x.shape[0]
+    return S / rows
+
+
+def classic_inverse(A: np.ndarray, damping: float) -> np.ndarray:
+    """(A + damping I)^{-1} by LU, torch.linalg.inv's method (classic_kfac.py:131-138)."""
+    A = np.asarray(A, dtype=np.float64)
+    return np.linalg.inv(A + damping * np.eye(A.shape[0]))
+
+
+def classic_nat(grad_W: np.ndarray, A_inv: np.ndarray, G_inv: np.ndarray) -> np.ndarray:
+    """G^{-1} grad A^{-1} (classic_kfac.py:218)."""
+    return np.asarray(G_inv, np.float64) @ np.asarray(grad_W, np.float64) @ \
+        np.asarray(A_inv, np.float64)
+
+
+def classic_updates_at(step: int, freq: int) -> bool:
+    """ClassicKFAC's schedule (classic_kfac.py:154,158): step % freq == 1, or every
+    step when freq == 1 -- one step after IFKFAC's step % freq == 0."""
+    return freq == 1 or step % freq == 1
 
 
 # ----------------------------------------------------------------------------

@@ -120,6 +120,37 @@ class OracleBackend:
         zg = _np(ZG4[0]) + _np(ZG4[1])
         return torch.from_numpy(zg @ (zg.T @ _np(grad)) @ zx @ zx.T).float()
 
+    def gram_accumulate_(self, S, X, beta):
+        self.calls["gram_accumulate"] += 1
+        x = _np(X)
+        prev = _np(S) if beta != 0.0 else 0.0
+        S.copy_(torch.from_numpy(beta * prev + x.T @ x).float())
+
+    def axpby(self, alpha, X, beta, Y=None):
+        self.calls["axpby"] += 1
+        out = alpha * _np(X) + (beta * _np(Y) if Y is not None and beta != 0.0 else 0.0)
+        out = torch.from_numpy(np.asarray(out)).float()
+        if Y is None:
+            return out
+        Y.copy_(out)
+        return Y
+
+    def gemm(self, A, B, trans_a=False, trans_b=False, math=0, alpha=1.0, beta=0.0, C=None,
+             tri_a=0, tri_b=0):
+        self.calls["gemm"] += 1
+        a = _np(A).T if trans_a else _np(A)
+        b = _np(B).T if trans_b else _np(B)
+        out = alpha * (a @ b) + (beta * _np(C) if C is not None and beta != 0.0 else 0.0)
+        return torch.from_numpy(np.asarray(out)).float()
+
+    def inv_spd_damped(self, A, damping):
+        self.calls["inv_spd_damped"] += 1
+        return torch.from_numpy(O.classic_inverse(_np(A), damping)).float()
+
+    def classic_precondition(self, grad, A_inv, G_inv):
+        self.calls["classic_precondition"] += 1
+        return torch.from_numpy(O.classic_nat(_np(grad), _np(A_inv), _np(G_inv))).float()
+
     def precondition(self, grad, R_X, R_G, math):
         self.calls["precondition"] += 1
         return torch.from_numpy(O.apply_vered(_np(grad), _np(R_X), _np(R_G))).float()

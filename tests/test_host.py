@@ -571,3 +571,108 @@ def test_bf16_update_batches_same_shape_layers(be):
         assert np.abs(R_X.double().numpy() - want_X).max() <= 4e-3 * np.abs(want_X).max()
         assert np.abs(R_G.double().numpy() - want_G).max() <= 4e-3 * np.abs(want_G).max()
     assert len(opt._factors) == 4
+
+
+# ---------------------------------------------------------------------------
+# Classic K-FAC control (kfac_hooks.py / classic_kfac.py)
+# ---------------------------------------------------------------------------
+def test_kfac_hooks_average_grams_over_passes(be):
+    """KFACHooks: A = sum x^T x / rows and G = sum delta^T delta / rows over every
+    captured pass (kfac_hooks.py:208-266); clear() starts a new window."""
+    from ifkfac_amd import KFACHooks
+    model = _mlp()
+    hooks = KFACHooks(model)
+    hooks.enable()
+    xs, ds = {m: [] for m in hooks.linear_layers}, {m: [] for m in hooks.linear_layers}
+    g = torch.Generator().manual_seed(5)
+    for rows in (32, 48):
+        X = torch.randn(rows, 8, generator=g)
+        acts, grads, hs = _capture(model, X)
+        model(X).pow(2).mean().backward()
+        for h in hs:
+            h.remove()
+        for m in hooks.linear_layers:
+            xs[m].append(acts[m].double().numpy())
+            ds[m].append(grads[m].double().numpy())
+    f = hooks.get_factors()
+    assert hooks.n_samples_accumulated() == 80
+    for m in hooks.linear_layers:
+        A, G = f[m]
+        assert np.allclose(A.double().numpy(), O.gram_average(xs[m]), rtol=1e-5, atol=1e-6)
+        assert np.allclose(G.double().numpy(), O.gram_average(ds[m]), rtol=1e-5, atol=1e-9)
+    hooks.clear()
+    assert hooks.get_factors() == {} and hooks.n_samples_accumulated() == 0
+    hooks.remove()
+
+
+def test_kfac_hooks_max_gram_dim_and_capture(be):
+    from ifkfac_amd import KFACHooks
+    model = nn.Sequential(nn.Linear(8, 16), nn.ReLU(), nn.Linear(16, 40))
+    hooks = KFACHooks(model, max_gram_dim=32)
+    assert hooks.linear_layers == [model[0]]
+    hooks.enable()
+    hooks.pause()
+    model(torch.randn(4, 8)).sum().backward()
+    assert hooks.get_factors() == {}
+    with hooks.capture():
+        model(torch.randn(4, 8)).sum().backward()
+    assert set(hooks.get_factors()) == {model[0]}
+
+
+@pytest.mark.parametrize("freq,gamma", [(1, 0.0), (3, 0.0), (1, 0.5)])
+def test_classic_kfac_matches_closed_form(be, freq, gamma):
+    """ClassicKFAC over 5 steps against the restated reference: the schedule
+    (step % freq == 1), the Gram averages of the window, the EMA blend, damped
+    inverses, G^-1 g A^-1, momentum and decoupled decay, the bias through G^-1
+    without momentum, and plain SGD before the first inverses."""
+    from ifkfac_amd import ClassicKFAC
+    model = _mlp(seed=3)
+    lr, lam, mu, wd = 1e-2, 1e-2, 0.9, 0.01
+    opt = ClassicKFAC(model, lr=lr, damping=lam, factor_update_freq=freq, decomp_update_freq=freq,
+                      momentum=mu, weight_decay=wd, gamma=gamma)
+    layers = opt.hooks.linear_layers
+    W = {m: m.weight.detach().double().numpy().copy() for m in layers}
+    b = {m: m.bias.detach().double().numpy().copy() for m in layers}
+    buf = {m: None for m in layers}
+    window = {m: ([], []) for m in layers}
+    facs, invs = {}, {}
+    g = torch.Generator().manual_seed(9)
+    for step in range(1, 6):
+        X = torch.randn(64, 8, generator=g)
+        acts, grads, hs = _capture(model, X)
+        opt.zero_grad()
+        model(X).pow(2).mean().backward()
+        for h in hs:
+            h.remove()
+        gW = {m: m.weight.grad.double().numpy() for m in layers}
+        gb = {m: m.bias.grad.double().numpy() for m in layers}
+        opt.step()
+        for m in layers:
+            window[m][0].append(acts[m].double().numpy())
+            window[m][1].append(grads[m].double().numpy())
+        if O.classic_updates_at(step, freq):
+            for m in layers:
+                A, G = O.gram_average(window[m][0]), O.gram_average(window[m][1])
+                if gamma > 0 and m in facs:
+                    A = gamma * facs[m][0] + (1 - gamma) * A
+                    G = gamma * facs[m][1] + (1 - gamma) * G
+                facs[m] = (A, G)
+                window[m] = ([], [])
+                invs[m] = (O.classic_inverse(A, lam), O.classic_inverse(G, lam))
+        for m in layers:
+            if m not in invs:
+                W[m] = W[m] * (1 - lr * wd) - lr * gW[m]
+                b[m] = b[m] * (1 - lr * wd) - lr * gb[m]
+                continue
+            nat = O.classic_nat(gW[m], *invs[m])
+            buf[m] = nat if buf[m] is None else mu * buf[m] + nat
+            W[m] = W[m] * (1 - lr * wd) - lr * buf[m]
+            b[m] = b[m] * (1 - lr * wd) - lr * (invs[m][1] @ gb[m])
+        # every seam hands fp32 values on (factors, inverses, natural gradients):
+        # fp32 accuracy relative to the weights' scale
+        for m in layers:
+            tw = 1e-5 * max(1.0, np.abs(W[m]).max())
+            tb = 1e-5 * max(1.0, np.abs(b[m]).max())
+            assert np.abs(m.weight.detach().double().numpy() - W[m]).max() < tw, step
+            assert np.abs(m.bias.detach().double().numpy() - b[m]).max() < tb, step
+    assert be.calls["gram_accumulate"] == 5 * 2 * len(layers)

@@ -410,3 +410,59 @@ def test_solve_triangular_bf16_tiny_and_zero_diagonals():
     assert X[0, 0] == x1
     # the unsigned-clamp mistake flips the sign of the negative case
     assert float(_bad_div_unsigned(np.array([1.0], np.float32), np.float32(-5e-8))[0]) == x1
+
+
+# ---------------------------------------------------------------------------
+# Classic K-FAC control (kfac_hooks.py / classic_kfac.py)
+# ---------------------------------------------------------------------------
+def test_gram_average_brute_force_and_chunking():
+    rng = np.random.default_rng(41)
+    chunks = [rng.standard_normal((r, 5)) for r in (3, 7, 1)]
+    want = np.zeros((5, 5))
+    for x in chunks:
+        for row in x:
+            for i in range(5):
+                for j in range(5):
+                    want[i, j] += row[i] * row[j]
+    want /= 11
+    got = O.gram_average(chunks)
+    assert np.allclose(got, want, rtol=1e-13, atol=1e-14)
+    # one chunk of all rows gives the same average
+    assert np.allclose(O.gram_average([np.concatenate(chunks)]), want, rtol=1e-13)
+    # planted mistake: averaging per chunk (1 / number of chunks) is rejected
+    bad = sum(x.T @ x / x.shape[0] for x in chunks) / len(chunks)
+    assert not np.allclose(bad, want, rtol=1e-3)
+
+
+def test_classic_inverse_closed_forms():
+    A = np.array([[4.0]])
+    assert np.allclose(O.classic_inverse(A, 1.0), [[0.2]], rtol=1e-15)
+    d = np.array([1.0, 3.0, 0.5])
+    assert np.allclose(O.classic_inverse(np.diag(d), 0.5), np.diag(1 / (d + 0.5)), rtol=1e-15)
+    rng = np.random.default_rng(2)
+    X = rng.standard_normal((30, 6))
+    A = X.T @ X / 30
+    Xi = O.classic_inverse(A, 1e-2)
+    assert np.allclose((A + 1e-2 * np.eye(6)) @ Xi, np.eye(6), atol=1e-12)
+    # planted mistake: the undamped inverse fails the damped identity
+    assert not np.allclose((A + 1e-2 * np.eye(6)) @ np.linalg.inv(A), np.eye(6), atol=1e-6)
+
+
+def test_classic_nat_diagonal_closed_form():
+    a = np.array([1.0, 2.0, 4.0])
+    g = np.array([0.5, 3.0])
+    lam = 0.1
+    grad = np.arange(6.0).reshape(2, 3) + 1
+    got = O.classic_nat(grad, O.classic_inverse(np.diag(a), lam), O.classic_inverse(np.diag(g), lam))
+    want = grad / np.outer(g + lam, a + lam)
+    assert np.allclose(got, want, rtol=1e-14)
+    # the transposed product (A^{-1} on the left) would not even conform
+    assert got.shape == (2, 3)
+
+
+def test_classic_schedule_by_hand():
+    assert [s for s in range(1, 8) if O.classic_updates_at(s, 1)] == list(range(1, 8))
+    assert [s for s in range(1, 12) if O.classic_updates_at(s, 3)] == [1, 4, 7, 10]
+    assert [s for s in range(1, 32) if O.classic_updates_at(s, 10)] == [1, 11, 21, 31]
+    # IFKFAC's schedule differs: step % freq == 0 once step >= freq
+    assert [s for s in range(1, 32) if O.should_update_factors(s, 10)] == [10, 20, 30]
