@@ -15,6 +15,7 @@ from .activation_hooks import IFKFACRankError, RawActivationHooks
 from .classic_kfac import ClassicKFAC
 from .ifkfac import IFKFAC
 from .kfac_hooks import KFACHooks
+from .laplace import LaplacePosterior, factors_to_evd
 from ._lib import IFKFACBackendError
 
 __version__ = "0.1.0"
@@ -22,6 +23,8 @@ __all__ = [
     "IFKFAC",
     "ClassicKFAC",
     "KFACHooks",
+    "LaplacePosterior",
+    "factors_to_evd",
     "RawActivationHooks",
     "IFKFACRankError",
     "IFKFACBackendError",

@@ -315,6 +315,60 @@ class HipBackend:
         _lib.check(rc, "ifk_precondition_apply_x3")
         return nat
 
+    # -- Laplace consumer -------------------------------------------------------------
+    def factor_evd(self, R: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(V, eig, sweeps): R^T R = V diag(eig) V^T from the upper triangle of R,
+        eig descending (fp32); sweeps a device int32[1] (negative: not converged)."""
+        Rc, ldr, rdt = _mat(R, "factor_evd")
+        n = Rc.shape[0]
+        if Rc.shape != (n, n):
+            raise IFKFACBackendError("factor_evd: R must be square")
+        V = torch.empty((n, n), dtype=torch.float32, device=Rc.device)
+        eig = torch.empty(n, dtype=torch.float32, device=Rc.device)
+        sweeps = torch.empty(1, dtype=torch.int32, device=Rc.device)
+        ws = self._ws(self.lib.ifk_factor_evd_workspace_size(n), Rc.device)
+        with torch.cuda.device(Rc.device):
+            rc = self.lib.ifk_factor_evd(self._stream(Rc.device), _ptr(Rc), rdt, ldr, n, _ptr(V), n,
+                                         _ptr(eig), _ptr(sweeps), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_factor_evd")
+        return V, eig, sweeps
+
+    def laplace_scales(self, d: torch.Tensor, sqrt_n: float, sqrt_lam: float) -> torch.Tensor:
+        """1 / sqrt(sqrt_n d + sqrt_lam), fp32."""
+        _require_device(d, "laplace_scales")
+        dc = d.reshape(-1).float().contiguous()
+        out = torch.empty_like(dc)
+        with torch.cuda.device(dc.device):
+            rc = self.lib.ifk_laplace_scales(self._stream(dc.device), _ptr(dc), dc.numel(),
+                                             float(sqrt_n), float(sqrt_lam), _ptr(out))
+        _lib.check(rc, "ifk_laplace_scales")
+        return out
+
+    def laplace_sample_(self, W_map: torch.Tensor, W: torch.Tensor, U_G: torch.Tensor,
+                        s_G: torch.Tensor, U_A: torch.Tensor, s_A: torch.Tensor,
+                        Xi: torch.Tensor) -> None:
+        """W (fp32 n_out x n_in, row-major, in place) = W_map + U_G diag(s_G) Xi
+        diag(s_A) U_A^T."""
+        n_out, n_in = Xi.shape
+        mats = {}
+        for name, t, shape in (("W_map", W_map, (n_out, n_in)), ("W", W, (n_out, n_in)),
+                               ("U_G", U_G, (n_out, n_out)), ("U_A", U_A, (n_in, n_in)),
+                               ("Xi", Xi, (n_out, n_in))):
+            _require_device(t, "laplace_sample")
+            if t.dtype != torch.float32 or t.shape != shape or t.stride(1) != 1:
+                raise IFKFACBackendError(f"laplace_sample: {name} must be fp32 {shape} row-major")
+            mats[name] = t
+        for name, t, n in (("s_G", s_G, n_out), ("s_A", s_A, n_in)):
+            if t.dtype != torch.float32 or t.numel() != n or not t.is_contiguous():
+                raise IFKFACBackendError(f"laplace_sample: {name} must be fp32 of length {n}")
+        ws = self._ws(self.lib.ifk_laplace_sample_workspace_size(n_out, n_in), W.device)
+        with torch.cuda.device(W.device):
+            rc = self.lib.ifk_laplace_sample(
+                self._stream(W.device), _ptr(W_map), W_map.stride(0), _ptr(W), W.stride(0), n_out,
+                n_in, _ptr(U_G), U_G.stride(0), _ptr(s_G), _ptr(U_A), U_A.stride(0), _ptr(s_A),
+                _ptr(Xi), Xi.stride(0), _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_laplace_sample")
+
     # -- Classic K-FAC control ------------------------------------------------------
     def gram_accumulate_(self, S: torch.Tensor, X: torch.Tensor, beta: float) -> None:
         """S = beta S + X^T X in place (S fp32 n x n contiguous, X p x n)."""

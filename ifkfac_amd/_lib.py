@@ -114,6 +114,14 @@ SIGNATURES = {
     "ifk_classic_precondition_workspace_size": (_c_sz, [_c_i64, _c_i64]),
     "ifk_classic_precondition": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64,
                                           _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_sz]),
+    "ifk_factor_evd_workspace_size": (_c_sz, [_c_i64]),
+    "ifk_factor_evd": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp,
+                                _c_vp, _c_sz]),
+    "ifk_laplace_scales": (_c_int, [_c_vp, _c_vp, _c_i64, _c_f, _c_f, _c_vp]),
+    "ifk_laplace_sample_workspace_size": (_c_sz, [_c_i64, _c_i64]),
+    "ifk_laplace_sample": (_c_int, [_c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp,
+                                    _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp,
+                                    _c_sz]),
     "ifk_inv_spd_workspace_size": (_c_sz, [_c_i64]),
     "ifk_inv_spd": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_int, _c_i64, _c_int,
                              _c_vp, _c_sz]),

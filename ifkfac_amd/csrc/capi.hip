@@ -361,6 +361,37 @@ int ifk_classic_precondition(void* stream, const float* grad, int64_t n_out, int
                               ldgi, nat, ldn, workspace, workspace_bytes);
 }
 
+size_t ifk_factor_evd_workspace_size(int64_t n) {
+  if (n < 1) return 0;
+  return factor_evd_ws(n);
+}
+
+int ifk_factor_evd(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n, float* V,
+                   int64_t ldv, float* eigvals, int* sweeps, void* workspace,
+                   size_t workspace_bytes) {
+  GUARD(dt_ok(r_dtype), "factor_evd: bad dtype");
+  return factor_evd((hipStream_t)stream, R, r_dtype, ldr, n, V, ldv, eigvals, sweeps, workspace,
+                    workspace_bytes);
+}
+
+int ifk_laplace_scales(void* stream, const float* d, int64_t n, float sqrt_n, float sqrt_lam,
+                       float* out) {
+  return laplace_scales((hipStream_t)stream, d, n, sqrt_n, sqrt_lam, out);
+}
+
+size_t ifk_laplace_sample_workspace_size(int64_t n_out, int64_t n_in) {
+  if (n_out < 1 || n_in < 1) return 0;
+  return laplace_sample_ws(n_out, n_in);
+}
+
+int ifk_laplace_sample(void* stream, const float* W_map, int64_t ldm, float* W, int64_t ldw,
+                       int64_t n_out, int64_t n_in, const float* U_G, int64_t ldug,
+                       const float* s_G, const float* U_A, int64_t ldua, const float* s_A,
+                       const float* Xi, int64_t ldxi, void* workspace, size_t workspace_bytes) {
+  return laplace_sample((hipStream_t)stream, W_map, ldm, W, ldw, n_out, n_in, U_G, ldug, s_G, U_A,
+                        ldua, s_A, Xi, ldxi, workspace, workspace_bytes);
+}
+
 size_t ifk_gemm_workspace_size(int64_t m, int64_t n) {
   if (m < 1 || n < 1) return 0;
   size_t f = (size_t)m * n * 64;

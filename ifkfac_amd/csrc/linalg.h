@@ -96,6 +96,21 @@ int classic_precondition(hipStream_t s, const float* grad, int64_t n_out, int64_
                          int64_t ldg, const float* A_inv, int64_t ldai, const float* G_inv,
                          int64_t ldgi, float* nat, int64_t ldn, void* ws, size_t ws_bytes);
 
+// Laplace consumer: R^T R = V diag(eig) V^T from R (one-sided block Jacobi SVD
+// of R, eig = sigma^2 descending, *sweeps = sweeps to convergence, negative if
+// not converged); the posterior scales 1 / sqrt(sqrt_n d + sqrt_lam); one
+// weight sample W = W_map + U_G diag(s_G) Xi diag(s_A) U_A^T.
+size_t factor_evd_ws(int64_t n);
+int factor_evd(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* V,
+               int64_t ldv, float* eig, int* sweeps, void* ws, size_t ws_bytes);
+int laplace_scales(hipStream_t s, const float* d, int64_t n, float sqrt_n, float sqrt_lam,
+                   float* out);
+size_t laplace_sample_ws(int64_t n_out, int64_t n_in);
+int laplace_sample(hipStream_t s, const float* W_map, int64_t ldm, float* W, int64_t ldw,
+                   int64_t n_out, int64_t n_in, const float* U_G, int64_t ldug, const float* s_G,
+                   const float* U_A, int64_t ldua, const float* s_A, const float* Xi,
+                   int64_t ldxi, void* ws, size_t ws_bytes);
+
 // bf16 halves of an fp32 inverse for precondition_apply_x3: Z = Zh + Zl and
 // Z^T = ZTh + ZTl (row stride ldb).
 int split_inverse(hipStream_t s, const float* Z, int64_t ldz, int64_t n, bf16_t* Zh, bf16_t* Zl,

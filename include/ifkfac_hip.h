@@ -367,6 +367,34 @@ int ifk_classic_precondition(void* stream, const float* grad, int64_t n_out, int
                              size_t workspace_bytes);
 
 /*
+ * Laplace consumer of the factors (the K-FAC Laplace posterior of
+ * ifkfac/laplace.py, fed by hooks.get_factors() as README.md:146-171 shows):
+ *   ifk_factor_evd      R^T R = V diag(eigvals) V^T from the n x n factor R (its
+ *                       upper triangle), by one-sided block Jacobi SVD of R:
+ *                       V (n x n fp32, columns = right singular vectors of R),
+ *                       eigvals = sigma(R)^2 descending; *sweeps = Jacobi sweeps
+ *                       to convergence (negative: not converged).  This is the
+ *                       `factors_to_evd` the reference's README names
+ *                       (README.md:167) and never defines: svd(R) per factor
+ *                       (laplace.py:26-30);
+ *   ifk_laplace_scales  out = 1 / sqrt(sqrt_n d + sqrt_lam) -- replaces
+ *                       laplace.py:95-96;
+ *   ifk_laplace_sample  W = W_map + U_G diag(s_G) Xi diag(s_A) U_A^T (fp32) --
+ *                       replaces laplace.py:138-154 (Xi drawn by the caller).
+ */
+size_t ifk_factor_evd_workspace_size(int64_t n);
+int ifk_factor_evd(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n, float* V,
+                   int64_t ldv, float* eigvals, int* sweeps, void* workspace,
+                   size_t workspace_bytes);
+int ifk_laplace_scales(void* stream, const float* d, int64_t n, float sqrt_n, float sqrt_lam,
+                       float* out);
+size_t ifk_laplace_sample_workspace_size(int64_t n_out, int64_t n_in);
+int ifk_laplace_sample(void* stream, const float* W_map, int64_t ldm, float* W, int64_t ldw,
+                       int64_t n_out, int64_t n_in, const float* U_G, int64_t ldug,
+                       const float* s_G, const float* U_A, int64_t ldua, const float* s_A,
+                       const float* Xi, int64_t ldxi, void* workspace, size_t workspace_bytes);
+
+/*
  * General MFMA matrix product C = alpha op(A) op(B) + beta C, exposed for
  * tests and for callers that compose the path themselves.  Bit 0 of
  * trans_a/trans_b selects op(X) = X^T; bits 1-2 declare op(X) upper (1) or

@@ -24,6 +24,13 @@ torch.linalg on CPU).  How each function is pinned (tests/test_oracle.py):
                              forms; a planted undamped inverse fails
   classic_nat                diagonal closed form g_ij / ((a_j + l)(g_i + l))
   classic_updates_at         the schedule listed by hand for freq 1, 3, 10
+  factor_evd                 diagonal and 2 x 2 closed forms; V diag(d) V^T =
+                             R^T R; the lower triangle ignored; d descending;
+                             a planted left-vector mistake fails
+  laplace_scales             by hand
+  laplace_sample             identity bases: elementwise by hand; the sample
+                             covariance of many draws matches the Kronecker
+                             covariance and rejects swapped sides
   bf16_linalg restatements   R vs chol(A^T A), L L^T vs A, R X vs B at tolerance;
                              the special cases by hand: _safe_div's signed
                              magnitude clamp (|d| < 1e-7 -> sign(d) 1e-7, sign(0)
@@ -226,6 +233,35 @@ def classic_updates_at(step: int, freq: int) -> bool:
     """ClassicKFAC's schedule (classic_kfac.py:154,158): step % freq == 1, or every
     step when freq == 1 -- one step after IFKFAC's step % freq == 0."""
     return freq == 1 or step % freq == 1
+
+
+# ----------------------------------------------------------------------------
+# laplace.py restatements (the Laplace consumer of the factors)
+# ----------------------------------------------------------------------------
+
+
+def factor_evd(R: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """(V, d) with R^T R = V diag(d) V^T, d descending: the right singular vectors
+    and squared singular values of the upper triangle of R -- svd(R), the
+    IFKFAC route of laplace.py:26-30 (README.md:167 names it factors_to_evd)."""
+    R = np.triu(np.asarray(R, dtype=np.float64))
+    _, s, Vh = np.linalg.svd(R)
+    return Vh.T, s * s
+
+
+def laplace_scales(d: np.ndarray, dataset_size: int, prior_precision: float) -> np.ndarray:
+    """1 / sqrt(sqrt(N) d + sqrt(lambda)) (laplace.py:92-101)."""
+    return 1.0 / np.sqrt(math.sqrt(dataset_size) * np.asarray(d, np.float64) +
+                         math.sqrt(prior_precision))
+
+
+def laplace_sample(W_map: np.ndarray, U_A: np.ndarray, s_A: np.ndarray, U_G: np.ndarray,
+                   s_G: np.ndarray, Xi: np.ndarray) -> np.ndarray:
+    """W_map + U_G diag(s_G) Xi diag(s_A) U_A^T (laplace.py:138-154)."""
+    xs = np.asarray(Xi, np.float64) * np.asarray(s_G, np.float64)[:, None] * \
+        np.asarray(s_A, np.float64)[None, :]
+    return np.asarray(W_map, np.float64) + np.asarray(U_G, np.float64) @ xs @ \
+        np.asarray(U_A, np.float64).T
 
 
 # ----------------------------------------------------------------------------

@@ -120,6 +120,21 @@ class OracleBackend:
         zg = _np(ZG4[0]) + _np(ZG4[1])
         return torch.from_numpy(zg @ (zg.T @ _np(grad)) @ zx @ zx.T).float()
 
+    def factor_evd(self, R):
+        self.calls["factor_evd"] += 1
+        V, d = O.factor_evd(_np(R))
+        return (torch.from_numpy(V).float(), torch.from_numpy(d).float(),
+                torch.tensor([1], dtype=torch.int32))
+
+    def laplace_scales(self, d, sqrt_n, sqrt_lam):
+        self.calls["laplace_scales"] += 1
+        return torch.from_numpy(1.0 / np.sqrt(sqrt_n * _np(d) + sqrt_lam)).float()
+
+    def laplace_sample_(self, W_map, W, U_G, s_G, U_A, s_A, Xi):
+        self.calls["laplace_sample"] += 1
+        out = O.laplace_sample(_np(W_map), _np(U_A), _np(s_A), _np(U_G), _np(s_G), _np(Xi))
+        W.copy_(torch.from_numpy(out).float())
+
     def gram_accumulate_(self, S, X, beta):
         self.calls["gram_accumulate"] += 1
         x = _np(X)

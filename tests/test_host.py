@@ -676,3 +676,44 @@ def test_classic_kfac_matches_closed_form(be, freq, gamma):
             assert np.abs(m.weight.detach().double().numpy() - W[m]).max() < tw, step
             assert np.abs(m.bias.detach().double().numpy() - b[m]).max() < tb, step
     assert be.calls["gram_accumulate"] == 5 * 2 * len(layers)
+
+
+# ---------------------------------------------------------------------------
+# Laplace consumer (laplace.py)
+# ---------------------------------------------------------------------------
+def test_laplace_posterior_from_ifkfac_factors(be):
+    """README.md:146-171's flow: IFKFAC captures, get_factors(), factors_to_evd,
+    LaplacePosterior; a seeded draw equals the restated sample on the same Xi,
+    restore_map returns the MAP weights, predictive averages softmaxes."""
+    from ifkfac_amd import IFKFAC, LaplacePosterior, factors_to_evd
+    model = _mlp(seed=4)
+    opt = IFKFAC(model, lr=0.0, damping=1e-3, factor_update_freq=1000)
+    X = torch.randn(128, 8, generator=torch.Generator().manual_seed(6))
+    model(X).pow(2).mean().backward()
+    factors = opt.hooks.get_factors()
+    evd = factors_to_evd(factors)
+    for m, (R_X, R_G) in factors.items():
+        U_A, d_A, U_G, d_G = evd[m]
+        for R, U, d in ((R_X, U_A, d_A), (R_G, U_G, d_G)):
+            Rn = R.double().numpy()
+            assert np.allclose(U.double().numpy() @ np.diag(d.double().numpy()) @ U.double().numpy().T,
+                               Rn.T @ Rn, rtol=1e-5, atol=1e-6)
+    W0 = {m: m.weight.detach().clone() for m in factors}
+    post = LaplacePosterior(model, evd, prior_precision=10.0, dataset_size=500)
+    post.sample_in_place(generator=torch.Generator().manual_seed(1))
+    g = torch.Generator().manual_seed(1)
+    for m in factors:
+        U_A, d_A, U_G, d_G = evd[m]
+        xi = torch.randn(U_G.shape[0], U_A.shape[0], generator=g).double().numpy()
+        sA = O.laplace_scales(d_A.double().numpy(), 500, 10.0)
+        sG = O.laplace_scales(d_G.double().numpy(), 500, 10.0)
+        want = O.laplace_sample(W0[m].double().numpy(), U_A.double().numpy(), sA,
+                                U_G.double().numpy(), sG, xi)
+        assert np.allclose(m.weight.detach().double().numpy(), want, rtol=1e-5, atol=1e-6)
+    post.restore_map()
+    for m in factors:
+        assert torch.equal(m.weight.detach(), W0[m])
+    probs = post.predictive(X[:16], n_samples=3, generator=torch.Generator().manual_seed(2))
+    assert probs.shape == (16, 4) and torch.allclose(probs.sum(-1), torch.ones(16))
+    for m in factors:
+        assert torch.equal(m.weight.detach(), W0[m])

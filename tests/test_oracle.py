@@ -466,3 +466,61 @@ def test_classic_schedule_by_hand():
     assert [s for s in range(1, 32) if O.classic_updates_at(s, 10)] == [1, 11, 21, 31]
     # IFKFAC's schedule differs: step % freq == 0 once step >= freq
     assert [s for s in range(1, 32) if O.should_update_factors(s, 10)] == [10, 20, 30]
+
+
+# ---------------------------------------------------------------------------
+# Laplace consumer (laplace.py)
+# ---------------------------------------------------------------------------
+def test_factor_evd_closed_forms():
+    # diagonal R: eigenvalues r_ii^2 descending, eigenvectors the unit vectors
+    V, d = O.factor_evd(np.diag([1.0, 3.0, 2.0]))
+    assert np.allclose(d, [9.0, 4.0, 1.0], rtol=1e-14)
+    assert np.allclose(np.abs(V), np.eye(3)[:, [1, 2, 0]], atol=1e-14)
+    # 2 x 2: R = [[a, b], [0, c]], R^T R = [[a^2, ab], [ab, b^2 + c^2]]
+    a, b, c = 2.0, 1.0, 1.0
+    A = np.array([[a * a, a * b], [a * b, b * b + c * c]])
+    tr, det = np.trace(A), np.linalg.det(A)
+    lam = np.array([tr / 2 + math.sqrt(tr * tr / 4 - det), tr / 2 - math.sqrt(tr * tr / 4 - det)])
+    V, d = O.factor_evd(np.array([[a, b], [0.0, c]]))
+    assert np.allclose(d, lam, rtol=1e-14)
+    # reconstruction, lower triangle ignored
+    rng = np.random.default_rng(3)
+    R = np.triu(rng.standard_normal((6, 6))) + 3 * np.eye(6)
+    Rg = R + np.tril(rng.standard_normal((6, 6)), -1)
+    V, d = O.factor_evd(Rg)
+    assert np.allclose(V @ np.diag(d) @ V.T, R.T @ R, atol=1e-12)
+    assert np.all(np.diff(d) <= 0)
+    # planted mistake: the left singular vectors do not diagonalise R^T R
+    U = np.linalg.svd(R)[0]
+    assert not np.allclose(U @ np.diag(d) @ U.T, R.T @ R, atol=1e-6)
+
+
+def test_laplace_scales_and_identity_basis_sample():
+    s = O.laplace_scales(np.array([0.0, 1.0, 3.0]), 4, 9.0)
+    assert np.allclose(s, [1 / math.sqrt(3.0), 1 / math.sqrt(5.0), 1 / 3.0], rtol=1e-15)
+    Xi = np.arange(6.0).reshape(2, 3) - 2
+    W0 = np.ones((2, 3))
+    sG, sA = np.array([2.0, 0.5]), np.array([1.0, 3.0, 0.25])
+    got = O.laplace_sample(W0, np.eye(3), sA, np.eye(2), sG, Xi)
+    want = np.ones((2, 3)) + Xi * np.outer(sG, sA)
+    assert np.allclose(got, want, rtol=1e-15)
+
+
+def test_laplace_sample_kronecker_covariance():
+    """Draws of vec(dW) (row-major) have covariance Sigma_G (x) Sigma_A with
+    Sigma = U diag(s^2) U^T; swapping the two sides is rejected."""
+    rng = np.random.default_rng(11)
+    n_out, n_in, N = 2, 3, 60000
+    U_G = np.linalg.qr(rng.standard_normal((n_out, n_out)))[0]
+    U_A = np.linalg.qr(rng.standard_normal((n_in, n_in)))[0]
+    s_G, s_A = np.array([1.5, 0.5]), np.array([1.0, 0.7, 0.2])
+    W0 = np.zeros((n_out, n_in))
+    Xi = rng.standard_normal((N, n_out, n_in))
+    D = np.einsum("ij,njk,lk->nil", U_G * s_G, Xi, U_A * s_A).reshape(N, -1)
+    cov = D.T @ D / N
+    want = np.kron(U_G @ np.diag(s_G ** 2) @ U_G.T, U_A @ np.diag(s_A ** 2) @ U_A.T)
+    assert np.abs(cov - want).max() < 0.03
+    one = O.laplace_sample(W0, U_A, s_A, U_G, s_G, Xi[0]).reshape(-1)
+    assert np.allclose(one, D[0], atol=1e-12)
+    swapped = np.kron(U_A @ np.diag(s_A ** 2) @ U_A.T, U_G @ np.diag(s_G ** 2) @ U_G.T)
+    assert np.abs(cov - swapped).max() > 0.1
