@@ -128,3 +128,48 @@ def test_update_step_recomputes_ill_conditioned_side_on_gpu(hip, caplog):
     Z_X = kfac._inverses[model][0].double().cpu()
     assert bool(torch.isfinite(Z_X).all())
     assert (R_X @ Z_X - torch.eye(96, dtype=torch.float64)).abs().max().item() < 1e-2
+
+
+@pytest.mark.parametrize("use_bf16", [False, True])
+def test_gamma_blend_on_gpu(hip, use_bf16):
+    """The exact EMA blend (gamma > 0, ifkfac/ifkfac.py:261-285) on the GPU: after
+    each update R_b^T R_b = gamma R_old^T R_old + (1 - gamma) R_new^T R_new, with
+    R_new the fresh damped factor of the window (the oracle's closed form of its
+    rows); the fold of [sqrt(gamma) R_old; sqrt(1 - gamma) R_new] is exact up to
+    fp32 (1e-5 relative), and bf16 mode stores the RNE bf16 cast of the blend."""
+    from oracle import ifk_oracle as O
+    from ifkfac_amd import IFKFAC
+    torch.manual_seed(0)
+    layer = nn.Linear(256, 384, bias=False).cuda()
+    model = nn.Sequential(layer)
+    gamma, lam = 0.7, 1e-2
+    opt = IFKFAC(model, lr=0.0, damping=lam, factor_update_freq=1, gamma=gamma,
+                 use_true_bf16=use_bf16)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    old = None
+    for step in range(3):
+        X = torch.randn(1024, 256, device="cuda", generator=g) * (1 + step)
+        acts = []
+        h1 = layer.register_forward_hook(lambda m, i, o: acts.append(i[0].detach().clone()))
+        grads = []
+        h2 = layer.register_full_backward_hook(lambda m, gi, go: grads.append(go[0].detach().clone()))
+        opt.zero_grad()
+        model(X).pow(2).mean().backward()
+        h1.remove()
+        h2.remove()
+        opt.step()
+        R_X, R_G = opt._factors[layer]
+        fresh = [O.chol_factor([acts[0].double().cpu().numpy()], 1024, lam),
+                 O.chol_factor([grads[0].double().cpu().numpy()], 1024, lam)]
+        for side, R in enumerate((R_X, R_G)):
+            Rb = R.double().cpu().numpy()
+            if old is None:
+                want = fresh[side].T @ fresh[side]
+            else:
+                want = gamma * old[side].T @ old[side] + (1 - gamma) * fresh[side].T @ fresh[side]
+            e = np.linalg.norm(Rb.T @ Rb - want) / np.linalg.norm(want)
+            assert e <= (2e-2 if use_bf16 else 1e-5), (step, side, e)
+            assert np.all(np.diag(Rb) > 0) and not np.any(np.tril(Rb, -1))
+        old = [R_X.double().cpu().numpy(), R_G.double().cpu().numpy()]
+        if use_bf16:
+            assert R_X.dtype == torch.bfloat16 and R_G.dtype == torch.bfloat16
