@@ -8,8 +8,7 @@ include/ifkfac_hip.h:
 * ``finalize_R``            (triangular.py:386-421) -> ``ifk_finalize``
 * ``apply_vered``           (triangular.py:551-656) -> ``ifk_precondition``
 * ``apply_vered_batched``   (triangular.py:506-544) -> per entry, same kernels
-* ``apply_vered_bias``      (triangular.py:659-705) -> ``ifk_tri_inverse`` +
-  ``ifk_precondition_bias``
+* ``apply_vered_bias``      (triangular.py:659-705) -> two ``ifk_trsm``
 * ``batched_streaming_tsqr_update`` (triangular.py:331-379) and ``tsqr``
   (triangular.py:150-227) -> ``ifk_tsqr_fold``
 
@@ -135,6 +134,10 @@ def apply_vered_bias(grad_b: torch.Tensor, R_G: torch.Tensor) -> torch.Tensor:
         print(f"[apply_vered_bias bf16] SKIP — R_G non-square: "
               f"shape={tuple(R_G.shape)}.  Returning raw bias gradient.", flush=True)
         return grad_b
+    # two triangular solves, R_G^T y = g then R_G x = y (triangular.py:695-701),
+    # in fp32 arithmetic on the (upcast) factor
     be = get_backend()
-    Z_G = be.tri_inverse(R_G, MATH_F32)
-    return be.precondition_bias(grad_b, Z_G).to(grad_b.dtype)
+    g = grad_b.reshape(-1, 1).float()
+    y = be.trsm(R_G.t(), g, False, torch.float32, MATH_F32)
+    x = be.trsm(R_G, y, True, torch.float32, MATH_F32)
+    return x.reshape(grad_b.shape).to(grad_b.dtype)

@@ -11,6 +11,7 @@ from __future__ import annotations
 import collections
 
 import numpy as np
+import scipy.linalg as sla
 import torch
 
 from oracle import ifk_oracle as O
@@ -165,6 +166,11 @@ class OracleBackend:
     def classic_precondition(self, grad, A_inv, G_inv):
         self.calls["classic_precondition"] += 1
         return torch.from_numpy(O.classic_nat(_np(grad), _np(A_inv), _np(G_inv))).float()
+
+    def trsm(self, R, B, upper, out_dtype, math):
+        self.calls["trsm"] += 1
+        r = np.triu(_np(R)) if upper else np.tril(_np(R))
+        return torch.from_numpy(sla.solve_triangular(r, _np(B), lower=not upper)).to(out_dtype)
 
     def precondition(self, grad, R_X, R_G, math):
         self.calls["precondition"] += 1

@@ -899,3 +899,39 @@ def test_full_size_precondition_residual(hip):
         rxd, rgd = rx.double(), rg.double()
         back = rgd.t() @ (rgd @ nat.double() @ rxd.t()) @ rxd
         assert ((back - grad.double()).norm() / grad.double().norm()).item() < tol
+
+
+def test_triangular_mirrors_on_gpu(hip):
+    """The function-level mirrors of ifkfac/triangular.py on the GPU against the
+    oracle: streaming update (trapezoid, then square), tsqr, the bucket fold,
+    finalize_R, apply_vered (fp32 and bf16 factors), apply_vered_batched and
+    apply_vered_bias (two triangular solves)."""
+    from ifkfac_amd import triangular as T
+    rng = np.random.default_rng(33)
+    X1, X2 = rng.standard_normal((100, 300)), rng.standard_normal((700, 300))
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=DEV)
+    R = T.streaming_tsqr_update(T.streaming_tsqr_update(None, t(X1)), t(X2))
+    want = O.streaming_tsqr_update(O.streaming_tsqr_update(None, X1), X2)
+    assert _gram_rel(R.double().cpu().numpy(), want) <= 4 * _kappa(want) * EPS32
+    Rt = T.tsqr(t(X2)).double().cpu().numpy()
+    assert _gram_rel(Rt, O.streaming_tsqr_update(None, X2)) <= 1e-5
+    Rb = T.batched_streaming_tsqr_update(torch.zeros(2, 300, 300, device=DEV),
+                                         t(np.stack([X2, 0.5 * X2])))
+    assert _gram_rel(Rb[1].double().cpu().numpy(),
+                        O.streaming_tsqr_update(None, 0.5 * X2)) <= 1e-5
+    Rd = T.finalize_R(t(want), 1e-2).double().cpu().numpy()
+    assert np.linalg.norm(Rd.T @ Rd - want.T @ want - 1e-2 * np.eye(300)) <= \
+        1e-5 * np.linalg.norm(want.T @ want)
+    R_X = O.get_factor(O.streaming_tsqr_update(None, X2), 700, 1e-2)
+    R_G = O.get_factor(O.streaming_tsqr_update(None, rng.standard_normal((900, 200))), 900, 1e-2)
+    g = rng.standard_normal((200, 300))
+    ref = O.apply_vered(g, R_X, R_G)
+    assert _rel(T.apply_vered(t(g), t(R_X), t(R_G)), ref) <= 1e-5
+    Rxb, Rgb = O.bf16_round(R_X.astype(np.float32)), O.bf16_round(R_G.astype(np.float32))
+    nat_b = T.apply_vered(t(g), t(Rxb).bfloat16(), t(Rgb).bfloat16())
+    assert _rel(nat_b, O.apply_vered(g, Rxb.astype(np.float64), Rgb.astype(np.float64))) <= 2e-2
+    natb = T.apply_vered_batched(t(np.stack([g, 2 * g])), t(np.stack([R_X, R_X])),
+                                 t(np.stack([R_G, R_G])))
+    assert _rel(natb[1], 2 * ref) <= 1e-5
+    gb = rng.standard_normal(200)
+    assert _rel(T.apply_vered_bias(t(gb), t(R_G)), O.apply_vered_bias(gb, R_G)) <= 1e-5

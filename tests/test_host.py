@@ -717,3 +717,52 @@ def test_laplace_posterior_from_ifkfac_factors(be):
     assert probs.shape == (16, 4) and torch.allclose(probs.sum(-1), torch.ones(16))
     for m in factors:
         assert torch.equal(m.weight.detach(), W0[m])
+
+
+# ---------------------------------------------------------------------------
+# the function-level mirrors of ifkfac/triangular.py
+# ---------------------------------------------------------------------------
+def test_triangular_mirrors_match_oracle(be):
+    """Each public function of ifkfac_amd.triangular against the oracle's restatement
+    of the reference function it mirrors (triangular.py:150-227, 246-307, 331-379,
+    386-421, 506-544, 551-656, 659-705)."""
+    from ifkfac_amd import triangular as T
+    rng = np.random.default_rng(21)
+    X1, X2 = rng.standard_normal((5, 12)), rng.standard_normal((30, 12))
+    t = lambda a: torch.tensor(a, dtype=torch.float32)
+    # streaming update: trapezoid first, then square; R^T R = sum X^T X
+    R = T.streaming_tsqr_update(None, t(X1))
+    assert R.shape == (5, 12)
+    R = T.streaming_tsqr_update(R, t(X2))
+    want = O.streaming_tsqr_update(O.streaming_tsqr_update(None, X1), X2)
+    assert R.shape == (12, 12)
+    assert np.allclose(R.double().numpy(), want, atol=1e-5)
+    # tsqr of a tall matrix, p < n rejected
+    assert np.allclose(T.tsqr(t(X2)).double().numpy(), O.streaming_tsqr_update(None, X2), atol=1e-5)
+    with pytest.raises(ValueError):
+        T.tsqr(t(X1))
+    # batched fold over a bucket (zero running factors, zero-padded chunks)
+    B = np.stack([X2, 2 * X2])
+    Rb = T.batched_streaming_tsqr_update(torch.zeros(2, 12, 12), t(B))
+    for i in range(2):
+        assert np.allclose(Rb[i].double().numpy(), O.streaming_tsqr_update(None, B[i]), atol=1e-5)
+    # finalize: R_d^T R_d = R^T R + lambda I
+    Rd = T.finalize_R(R, 1e-2).double().numpy()
+    Rn = R.double().numpy()
+    assert np.allclose(Rd.T @ Rd, Rn.T @ Rn + 1e-2 * np.eye(12), atol=1e-5)
+    # four solves, batched, bias
+    R_X = O.get_factor(O.streaming_tsqr_update(None, X2), 30, 1e-2)
+    R_G = O.get_factor(O.streaming_tsqr_update(None, rng.standard_normal((40, 6))), 40, 1e-2)
+    g = rng.standard_normal((6, 12))
+    nat = T.apply_vered(t(g), t(R_X), t(R_G))
+    assert np.allclose(nat.double().numpy(), O.apply_vered(g, R_X, R_G), rtol=1e-5, atol=1e-6)
+    natb = T.apply_vered_batched(t(np.stack([g, -g])), t(np.stack([R_X, R_X])),
+                                 t(np.stack([R_G, R_G])))
+    assert np.allclose(natb[1].double().numpy(), -O.apply_vered(g, R_X, R_G), rtol=1e-5, atol=1e-6)
+    gb = rng.standard_normal(6)
+    nb = T.apply_vered_bias(t(gb), t(R_G))
+    assert np.allclose(nb.double().numpy(), O.apply_vered_bias(gb, R_G), rtol=1e-5, atol=1e-6)
+    # bf16 branch: non-square factors give the raw gradient back (triangular.py:608-617)
+    raw = t(g)
+    assert T.apply_vered(raw, t(R_X[:5]).bfloat16(), t(R_G).bfloat16()) is raw
+    assert T.apply_vered_bias(t(gb), t(R_G[:3]).bfloat16()).shape == (6,)
