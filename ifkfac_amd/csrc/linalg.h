@@ -28,7 +28,7 @@ int fold_finalize(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, i
                   void* out, int odt, int64_t ldo, int math, int* finite, void* ws,
                   size_t ws_bytes);
 
-// fold_finalize with each 512-column outer block factored by CholeskyQR2 +
+// fold_finalize with each 1024-column outer block factored by CholeskyQR2 +
 // Householder reconstruction instead of its 64-column panel chain.  *status:
 // 1 finite, 0 not finite, 2 a block was too ill-conditioned for CholeskyQR
 // (the output is meaningless; fold_finalize computes it).
