@@ -267,8 +267,8 @@ __global__ void add_diag_ref_kernel(float* A, int64_t lda, int64_t n, float v, f
 // result does not depend on scheduling.
 constexpr int FROB_WG = 1024;
 __global__ __launch_bounds__(256) void gram_frob_kernel(const float* A, int64_t lda, int64_t rows,
-                                                        int64_t W, float* part, int64_t sa,
-                                                        int64_t sp) {
+                                                        int64_t W, int64_t r_off, float* part,
+                                                        int64_t sa, int64_t sp) {
   __shared__ float red[4];
   A += (int64_t)blockIdx.y * sa;
   part += (int64_t)blockIdx.y * sp;
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(256) void gram_frob_kernel(const float* A, int64_t 
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int64_t cc = c + u;
-        if (cc < W && cc <= r) acc = fmaf(cc == r ? x[u] : 2.0f * x[u], x[u], acc);
+        if (cc < W && cc <= r + r_off) acc = fmaf(cc == r + r_off ? x[u] : 2.0f * x[u], x[u], acc);
       }
     }
   }
@@ -406,7 +406,8 @@ struct GramWs {
   bf16_t* LA;         // panel l at columns 3 GB l: [L_hi | L_lo | L_hi], n x ldl
   bf16_t* LB;         // panel l at columns 3 GB l: [L_lo | L_hi | L_hi], n x ldl
   int* flag;          // one per entry, at int stride FLAG_S
-  float* frob;        // per entry and Gram column, FROB_WG partial sums of squares
+  float* frob;        // per entry and Gram column, FROB_WG partial sums of squares (column 0's
+                      // diagonal block in the extra set nb, its rows below in set 0)
   int64_t sPT, sAw, sdref, sGB, sZd, sMT3, sLSb, sAS2, sL, sfrob;
   SplitScratch sp, sp2, sp3;   // split-K partials of the three streams
 };
@@ -431,7 +432,7 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w) {
   w.sLSb = multi ? GB * 4 * GB : 64;
   w.sAS2 = al(big * 3 * GB);
   w.sL = al(big * w.ldl);
-  w.sfrob = nb * FROB_WG;
+  w.sfrob = (nb + 1) * FROB_WG;   // + the diagonal block of column 0, kept apart
   w.PT = a.take<bf16_t>((size_t)(B * w.sPT));
   w.Aw = a.take<float>((size_t)(B * w.sAw));
   w.dref = a.take<float>((size_t)(B * w.sdref));
@@ -484,11 +485,59 @@ int gram_column(hipStream_t s, GramWs& w, int64_t n, int64_t c, float c2, bool h
     for (int e = 0; e < B; ++e) RC(launch_zero(s, Ac + e * w.sAw, w.lda, rows, W));
   }
   hipLaunchKernelGGL(gram_frob_kernel, dim3(FROB_WG, (unsigned)B), dim3(256), 0, s, Ac, w.lda,
-                     rows, W, w.frob + c * FROB_WG, w.sAw, w.sfrob);
+                     rows, W, (int64_t)0, w.frob + c * FROB_WG, w.sAw, w.sfrob);
   RC(check_launch("gram_frob"));
   hipLaunchKernelGGL(add_diag_ref_kernel, dim3(grid_of(W, 64), (unsigned)B), dim3(256), 0, s, Ac,
                      w.lda, W, c2, w.dref + b.r0, w.sAw, w.sdref);
   return check_launch("add_diag_ref");
+}
+
+// Gram column 0 in two parts, so that the chain can start on the first: its
+// diagonal block (with c^2 and the reference diagonal), and its rows below.
+int gram_column0_diag(hipStream_t s, GramWs& w, int64_t n, float c2, bool have_rows,
+                      int max_wgs) {
+  const Blk b = blk(0, n);
+  const int64_t W = b.r1 - b.r0;
+  const int B = (int)w.B;
+  float* Ac = w.Aw;
+  if (have_rows) {
+    RC(gemm(s, MATH_BF16, W, W, w.ldk, 1.0f, A_n(w.PT, DT_BF16, w.ldk, TRI_NONE, w.sPT),
+            B_t(w.PT, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
+            per_entry(lower_part(out_f32(Ac, w.lda, w.sAw))), B, w.sp3, max_wgs));
+  } else {
+    for (int e = 0; e < B; ++e) RC(launch_zero(s, Ac + e * w.sAw, w.lda, W, W));
+  }
+  const int64_t nb = cdiv(n, GB);
+  hipLaunchKernelGGL(gram_frob_kernel, dim3(FROB_WG, (unsigned)B), dim3(256), 0, s, Ac, w.lda, W,
+                     W, (int64_t)0, w.frob + nb * FROB_WG, w.sAw, w.sfrob);
+  RC(check_launch("gram_frob"));
+  hipLaunchKernelGGL(add_diag_ref_kernel, dim3(grid_of(W, 64), (unsigned)B), dim3(256), 0, s, Ac,
+                     w.lda, W, c2, w.dref, w.sAw, w.sdref);
+  return check_launch("add_diag_ref");
+}
+
+int gram_column0_rest(hipStream_t s, GramWs& w, int64_t n, bool have_rows, int max_wgs) {
+  const Blk b = blk(0, n);
+  const int64_t W = b.r1 - b.r0, rows = n - W;
+  const int B = (int)w.B;
+  float* Ac = w.Aw + W * w.lda;
+  if (rows <= 0) {
+    // one block: the set of the rows below stays empty
+    hipLaunchKernelGGL(gram_frob_kernel, dim3(FROB_WG, (unsigned)B), dim3(256), 0, s, w.Aw, w.lda,
+                       (int64_t)0, W, W, w.frob, w.sAw, w.sfrob);
+    return check_launch("gram_frob");
+  }
+  if (have_rows) {
+    RC(gemm(s, MATH_BF16, rows, W, w.ldk, 1.0f,
+            A_n(w.PT + W * w.ldk, DT_BF16, w.ldk, TRI_NONE, w.sPT),
+            B_t(w.PT, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
+            per_entry(out_f32(Ac, w.lda, w.sAw)), B, w.sp3, max_wgs));
+  } else {
+    for (int e = 0; e < B; ++e) RC(launch_zero(s, Ac + e * w.sAw, w.lda, rows, W));
+  }
+  hipLaunchKernelGGL(gram_frob_kernel, dim3(FROB_WG, (unsigned)B), dim3(256), 0, s, Ac, w.lda,
+                     rows, W, W, w.frob, w.sAw, w.sfrob);
+  return check_launch("gram_frob");
 }
 
 // Chain, part 1 of step k: L_kk = chol(A_kk)^T and M = U_kk^{-1}.
@@ -635,34 +684,50 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   const float c2 = damping / (scale * scale);
   const bool have_rows = pe > 0;
   for (int e = 0; e < B; ++e) RC(launch_fill_int(s, w.flag + e * FLAG_S, 0, 1));
-  // P^T of each entry (bf16, K-padded with zeros)
+  // P^T of each entry (bf16, K-padded with zeros): the running factor's rows
+  // and the chunk's first column block on s, so that column 0's diagonal
+  // block (all the chain's first step needs) can start; the chunk's other
+  // column blocks go on s3 ahead of the rest of the Gram columns.
+  const Blk b0 = blk(0, n);
+  auto x_cols = [&](hipStream_t st, int64_t c0, int64_t c1) -> int {
+    for (int e = 0; e < B; ++e) {
+      bf16_t* PT = w.PT + e * w.sPT + c0 * w.ldk + r_in;
+      const char* Xe = (const char*)X[e] + c0 * (xdt == DT_BF16 ? 2 : 4);
+      // a bf16 chunk moves as 32-bit pairs through a 64 x 64 tile
+      if (xdt == DT_BF16)
+        RC(launch_transpose_bf16(st, (const bf16_t*)Xe, ldx, p, c1 - c0, PT, w.ldk));
+      else
+        RC(transpose_to_bf16(st, Xe, xdt, ldx, p, c1 - c0, PT, w.ldk, false));
+    }
+    return IFK_OK;
+  };
   for (int e = 0; e < B; ++e) {
     bf16_t* PT = w.PT + e * w.sPT;
     if (w.ldk > pe) RC(launch_zero_bf16(s, PT + pe, w.ldk, n, w.ldk - pe));
     if (r_in > 0) RC(transpose_to_bf16(s, R_in[e], DT_F32, ldr, r_in, n, PT, w.ldk, true));
-    if (p > 0) {
-      // a bf16 chunk moves as 32-bit pairs through a 64 x 64 tile
-      if (xdt == DT_BF16)
-        RC(launch_transpose_bf16(s, (const bf16_t*)X[e], ldx, p, n, PT + r_in, w.ldk));
-      else
-        RC(transpose_to_bf16(s, X[e], xdt, ldx, p, n, PT + r_in, w.ldk, false));
-    }
   }
-  // Gram columns in order on s3, each with its event (they depend on P^T only)
+  if (p > 0) RC(x_cols(s, b0.r0, b0.r1));
   if (la) {
     HIPRC(hipEventRecord(la->ready[0], s), "fold_finalize_gram: event record failed");
     HIPRC(hipStreamWaitEvent(s3, la->ready[0], 0), "fold_finalize_gram: stream wait failed");
   }
-  for (int64_t c = 0; c < nb; ++c) {
+  // Gram columns in order on s3, each with its event (they depend on P^T only)
+  RC(gram_column0_diag(s3, w, n, c2, have_rows, wg3));
+  if (la) HIPRC(hipEventRecord(la->tready[0], s3), "fold_finalize_gram: event record failed");
+  if (p > 0 && n > b0.r1) RC(x_cols(s3, b0.r1, n));
+  RC(gram_column0_rest(s3, w, n, have_rows, wg3));
+  if (la) HIPRC(hipEventRecord(la->col[0], s3), "fold_finalize_gram: event record failed");
+  for (int64_t c = 1; c < nb; ++c) {
     RC(gram_column(s3, w, n, c, c2, have_rows, wg3));
     if (la) HIPRC(hipEventRecord(la->col[c], s3), "fold_finalize_gram: event record failed");
   }
   // The chain on s; the helper s2 works one step behind it.  Events (each
   // recorded again only after the wait on its previous record is enqueued):
+  //   tready[0]:     column 0's diagonal block done (s3)
   //   col[c]:        Gram column c done (s3)
   //   ready[k % 2]:  step k's band and diagonal update done (s -> s2)
   //   aready[k % 2]: helper step k done (s2 -> s, before step k + 1's band)
-  if (la) HIPRC(hipStreamWaitEvent(s, la->col[0], 0), "fold_finalize_gram: stream wait failed");
+  if (la) HIPRC(hipStreamWaitEvent(s, la->tready[0], 0), "fold_finalize_gram: stream wait failed");
   for (int64_t k = 0; k < nb; ++k) {
     const int kp = (int)(k & 1);
     RC(chain_factor(s, w, n, k));
@@ -671,8 +736,10 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
     // column k + 1 updated by panels < k), which also frees MT3[k % 2]
     if (la && k >= 1 && k + 1 < nb)
       HIPRC(hipStreamWaitEvent(s, la->aready[kp ^ 1], 0), "fold_finalize_gram: stream wait failed");
-    if (la && k == 0)
+    if (la && k == 0) {
+      HIPRC(hipStreamWaitEvent(s, la->col[0], 0), "fold_finalize_gram: stream wait failed");
       HIPRC(hipStreamWaitEvent(s, la->col[1], 0), "fold_finalize_gram: stream wait failed");
+    }
     RC(chain_band(s, w, n, k));
     if (k + 2 < nb) {
       if (la) {
