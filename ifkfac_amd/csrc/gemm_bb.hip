@@ -40,9 +40,10 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int BK = 32, STAGES = 4;
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int OCC_>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int OCC_, bool PIPE_ = false>
 struct BbCfg {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, OCC = OCC_;
+  static constexpr bool PIPE = PIPE_;   // fragment reads one half-slab ahead (see bb_tile)
   static constexpr int NWAVE = WAVES_M * WAVES_N, NTH = NWAVE * 64;
   static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;   // wave tile
   static constexpr int FM = WTM / 32, FN = WTN / 32;             // 32 x 32 MFMA tiles per wave
@@ -54,7 +55,7 @@ struct BbCfg {
   static_assert(2 * LOADS <= 63, "vmcnt holds at most 63 loads in flight");
   static_assert(SLAB_A * 2 % (16 * NTH) == 0 && SLAB_B * 2 % (16 * NTH) == 0, "slab split");
 };
-using BigCfg = BbCfg<256, 256, 2, 4, 1>;   // 512 threads, 128 KB ring, one workgroup per CU
+using BigCfg = BbCfg<256, 256, 2, 4, 1, true>;   // 512 threads, 128 KB ring, one WG per CU
 using MidCfg = BbCfg<128, 128, 2, 2, 2>;   // 256 threads, 64 KB ring, two workgroups per CU
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -64,27 +65,44 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nrec, 0x00020000);
 }
 
-// Issue the loads of one operand slab (NL * NWAVE * 16 rows from row r0 of
-// the operand view whose buffer descriptor starts at row r0, K chunk kt) into
-// LDS S.  Wave w, instruction i fills slots (NWAVE i + w) * 64 .. + 63; lane
-// l's slot s = (row, q) holds the logical chunk q ^ ((row >> 2) & 3) of that
-// row.
+// Per-thread addressing of the slab loads, fixed for a tile: wave w,
+// instruction i fills slots (NWAVE i + w) * 64 .. + 63; lane l's slot
+// s = (row, q) holds the logical chunk c = q ^ ((row >> 2) & 3) of that row,
+// i.e. byte offset row * ld * 2 + 16 c of the operand view plus 64 per K
+// slab (row < 256 and ld < 2^21 keep it in 32 bits), and K index 8 c plus
+// 32 per slab.
 template <int NWAVE, int NL>
-__device__ __forceinline__ void issue_slab(__amdgpu_buffer_rsrc_t rs, bf16_t* S, int64_t ld,
-                                           int64_t kt, int64_t kmax) {
+struct SlabAddr {
+  unsigned base[NL];
+  int kc[NL];
+  __device__ __forceinline__ void init(int64_t ld) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int slot = (i * NWAVE + wave) * 64 + lane;
+      const int row = slot >> 2, q = slot & 3;
+      const int c = q ^ ((row >> 2) & 3);
+      base[i] = (unsigned)((int64_t)row * ld * 2) + 16u * (unsigned)c;
+      kc[i] = 8 * c;
+    }
+  }
+};
+
+// Issue the loads of one operand slab (K chunk kt) into LDS S.  Chunks at or
+// past K read as zero (the offset is beyond the buffer).
+template <int NWAVE, int NL>
+__device__ __forceinline__ void issue_slab(__amdgpu_buffer_rsrc_t rs, bf16_t* S,
+                                           const SlabAddr<NWAVE, NL>& a, int kt, int kmax) {
   // the LDS destination (M0) must be wave-uniform: take the wave index from
   // a scalar register so the compiler knows it
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int k0 = kt * BK;
+  const unsigned koff = (unsigned)k0 * 2u;
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     const int slot0 = (i * NWAVE + wave) * 64;
-    const int slot = slot0 + lane;
-    const int row = slot >> 2, q = slot & 3;
-    const int c = q ^ ((row >> 2) & 3);
-    const int64_t k = kt * BK + 8 * c;
-    // chunks at or past K read as zero (the offset is beyond the buffer)
-    const unsigned off = (k < kmax) ? (unsigned)(((int64_t)row * ld + k) * 2) : 0x80000000u;
+    const unsigned off = (k0 + a.kc[i] < kmax) ? a.base[i] + koff : 0x80000000u;
     lds_void* dst = (lds_void*)(uintptr_t)(S + slot0 * 8);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, off, 0, 0, 0);
   }
@@ -131,7 +149,103 @@ __device__ __forceinline__ void wait_vm(int ahead) {
   else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
 
+// The fragments of one K half (16) of a slab: FM rows of A, FN rows of B,
+// masked where a triangular operand's slab crosses the diagonal.
+template <class CF, bool TRI>
+struct Frags {
+  bf16x8_t a[CF::FM], b[CF::FN];
+  __device__ __forceinline__ void read(const bf16_t* As, const bf16_t* Bs, int ks, int wm, int wn,
+                                       int l32, int h) {
+#pragma unroll
+    for (int i = 0; i < CF::FM; ++i) a[i] = frag(As, wm * CF::WTM + i * 32 + l32, 2 * ks + h);
+#pragma unroll
+    for (int j = 0; j < CF::FN; ++j) b[j] = frag(Bs, wn * CF::WTN + j * 32 + l32, 2 * ks + h);
+  }
+  __device__ __forceinline__ void mask(const GemmParams& p, int64_t m0, int64_t n0, int64_t kbase,
+                                       int ks, int wm, int wn, int l32, int h) {
+    if (!TRI) return;
+    if (slab_crosses(p.tria, m0, CF::BM, kbase)) {
+#pragma unroll
+      for (int i = 0; i < CF::FM; ++i)
+        a[i] = mask_frag<true>(a[i], p.tria, m0 + wm * CF::WTM + i * 32 + l32,
+                               kbase + ks * 16 + h * 8);
+    }
+    if (slab_crosses(p.trib, n0, CF::BN, kbase)) {
+#pragma unroll
+      for (int j = 0; j < CF::FN; ++j)
+        b[j] = mask_frag<false>(b[j], p.trib, n0 + wn * CF::WTN + j * 32 + l32,
+                                kbase + ks * 16 + h * 8);
+    }
+  }
+};
+
 template <class CF>
+__device__ __forceinline__ void mfma_all(f32x16_t (&acc)[CF::FM][CF::FN], const bf16x8_t* a,
+                                         const bf16x8_t* b) {
+#pragma unroll
+  for (int i = 0; i < CF::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < CF::FN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+
+// Main loop with the fragment reads one K half ahead of the products that
+// use them, for configurations of one wave per SIMD (no second wave to cover
+// the LDS latency).  Per slab: read the second half's fragments, multiply
+// the first half's, then wait for the next slab's loads and meet at the
+// barrier (after it every wave is past its reads of the previous slab, whose
+// ring slot then takes the slab STAGES - 1 ahead), read the next slab's first
+// half, multiply this slab's second half.  So the barrier and the LDS
+// latency fall under a half slab of products.
+template <class CF, bool TRI>
+__device__ __forceinline__ void pipe_loop(const GemmParams& p, f32x16_t (&acc)[CF::FM][CF::FN],
+                                          bf16_t* smem, __amdgpu_buffer_rsrc_t ra,
+                                          __amdgpu_buffer_rsrc_t rb,
+                                          const SlabAddr<CF::NWAVE, CF::LOADS_A>& aa,
+                                          const SlabAddr<CF::NWAVE, CF::LOADS_B>& ab, int kmax,
+                                          int64_t kt0, int n_it, int64_t m0, int64_t n0, int wm,
+                                          int wn, int l32, int h) {
+  constexpr int STAGE = CF::STAGE, SLAB_A = CF::SLAB_A;
+  if (n_it <= 0) return;
+  // prologue: slabs 0 .. STAGES - 2 in flight, slab 0 landed everywhere
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) {
+    if (s < n_it) {
+      issue_slab(ra, smem + s * STAGE, aa, (int)(kt0 + s), kmax);
+      issue_slab(rb, smem + s * STAGE + SLAB_A, ab, (int)(kt0 + s), kmax);
+    }
+  }
+  wait_vm<CF::LOADS>(min(n_it - 1, STAGES - 2));
+  __builtin_amdgcn_s_barrier();
+  Frags<CF, TRI> f0, f1;
+  f0.read(smem, smem + SLAB_A, 0, wm, wn, l32, h);
+  f0.mask(p, m0, n0, kt0 * BK, 0, wm, wn, l32, h);
+  for (int it = 0; it < n_it; ++it) {
+    const bf16_t* As = smem + (it % STAGES) * STAGE;
+    const int64_t kbase = (kt0 + it) * BK;
+    f1.read(As, As + SLAB_A, 1, wm, wn, l32, h);
+    f1.mask(p, m0, n0, kbase, 1, wm, wn, l32, h);
+    mfma_all<CF>(acc, f0.a, f0.b);
+    if (it + 1 < n_it) {
+      // slab it + 1 landed (the slabs issued after it may fly), every wave
+      // past its reads of slab it - 1
+      wait_vm<CF::LOADS>(min(STAGES - 3, n_it - 2 - it));
+      __builtin_amdgcn_s_barrier();
+      if (it + STAGES - 1 < n_it) {
+        const int sn = (it + STAGES - 1) % STAGES;
+        issue_slab(ra, smem + sn * STAGE, aa, (int)(kt0 + it + STAGES - 1), kmax);
+        issue_slab(rb, smem + sn * STAGE + SLAB_A, ab, (int)(kt0 + it + STAGES - 1), kmax);
+      }
+      const bf16_t* An = smem + ((it + 1) % STAGES) * STAGE;
+      f0.read(An, An + SLAB_A, 0, wm, wn, l32, h);
+      f0.mask(p, m0, n0, kbase + BK, 0, wm, wn, l32, h);
+    }
+    mfma_all<CF>(acc, f1.a, f1.b);
+  }
+}
+
+// TRI: a triangular operand (K range trimmed, slabs across the diagonal masked)
+template <class CF, bool TRI>
 __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf16_t* smem) {
   constexpr int BM = CF::BM, BN = CF::BN, FM = CF::FM, FN = CF::FN;
   constexpr int STAGE = CF::STAGE, SLAB_A = CF::SLAB_A;
@@ -161,6 +275,11 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
   const bf16_t* Bb = (const bf16_t*)p.B + (size_t)bidx * p.bsb + n0 * p.ldb;
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ab, (p.M - m0) * p.lda * 2);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bb, (p.N - n0) * p.ldb * 2);
+  SlabAddr<CF::NWAVE, CF::LOADS_A> aa;
+  SlabAddr<CF::NWAVE, CF::LOADS_B> ab;
+  aa.init(p.lda);
+  ab.init(p.ldb);
+  const int kmax = (int)p.K;
 
   f32x16_t acc[FM][FN];
 #pragma unroll
@@ -170,56 +289,58 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // prologue: slabs 0 .. STAGES - 2
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) {
-    if (s < n_it) {
-      issue_slab<CF::NWAVE, CF::LOADS_A>(ra, smem + s * STAGE, p.lda, kt0 + s, p.K);
-      issue_slab<CF::NWAVE, CF::LOADS_B>(rb, smem + s * STAGE + SLAB_A, p.ldb, kt0 + s, p.K);
-    }
-  }
-  for (int it = 0; it < n_it; ++it) {
-    wait_vm<CF::LOADS>(min(n_it - 1 - it, STAGES - 2));   // this slab landed (later ones may fly)
-    // every wave's loads of this slab are in LDS and slab it - 1 is free
-    // again.  A bare s_barrier: __syncthreads() would also wait for the next
-    // slab's loads (its fence drains vmcnt).
-    __builtin_amdgcn_s_barrier();
-    if (it + STAGES - 1 < n_it) {
-      const int sn = (it + STAGES - 1) % STAGES;
-      issue_slab<CF::NWAVE, CF::LOADS_A>(ra, smem + sn * STAGE, p.lda, kt0 + it + STAGES - 1,
-                                         p.K);
-      issue_slab<CF::NWAVE, CF::LOADS_B>(rb, smem + sn * STAGE + SLAB_A, p.ldb,
-                                         kt0 + it + STAGES - 1, p.K);
-    }
-    const bf16_t* As = smem + (it % STAGES) * STAGE;
-    const bf16_t* Bs = As + SLAB_A;
-    const int64_t kbase = (kt0 + it) * BK;
-    const bool xa = slab_crosses(p.tria, m0, BM, kbase);
-    const bool xb = slab_crosses(p.trib, n0, BN, kbase);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8_t af[FM], bfr[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = frag(As, wm * CF::WTM + i * 32 + l32, 2 * ks + h);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[j] = frag(Bs, wn * CF::WTN + j * 32 + l32, 2 * ks + h);
-      if (xa) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          af[i] = mask_frag<true>(af[i], p.tria, m0 + wm * CF::WTM + i * 32 + l32,
-                                  kbase + ks * 16 + h * 8);
+  if constexpr (CF::PIPE) {
+    pipe_loop<CF, TRI>(p, acc, smem, ra, rb, aa, ab, kmax, kt0, n_it, m0, n0, wm, wn, l32, h);
+  } else {
+    // prologue: slabs 0 .. STAGES - 2
+  #pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) {
+      if (s < n_it) {
+        issue_slab(ra, smem + s * STAGE, aa, (int)(kt0 + s), kmax);
+        issue_slab(rb, smem + s * STAGE + SLAB_A, ab, (int)(kt0 + s), kmax);
       }
-      if (xb) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          bfr[j] = mask_frag<false>(bfr[j], p.trib, n0 + wn * CF::WTN + j * 32 + l32,
+    }
+    for (int it = 0; it < n_it; ++it) {
+      wait_vm<CF::LOADS>(min(n_it - 1 - it, STAGES - 2));   // this slab landed (later ones may fly)
+      // every wave's loads of this slab are in LDS and slab it - 1 is free
+      // again.  A bare s_barrier: __syncthreads() would also wait for the next
+      // slab's loads (its fence drains vmcnt).
+      __builtin_amdgcn_s_barrier();
+      if (it + STAGES - 1 < n_it) {
+        const int sn = (it + STAGES - 1) % STAGES;
+        issue_slab(ra, smem + sn * STAGE, aa, (int)(kt0 + it + STAGES - 1), kmax);
+        issue_slab(rb, smem + sn * STAGE + SLAB_A, ab, (int)(kt0 + it + STAGES - 1), kmax);
+      }
+      const bf16_t* As = smem + (it % STAGES) * STAGE;
+      const bf16_t* Bs = As + SLAB_A;
+      const int64_t kbase = (kt0 + it) * BK;
+      const bool xa = TRI && slab_crosses(p.tria, m0, BM, kbase);
+      const bool xb = TRI && slab_crosses(p.trib, n0, BN, kbase);
+  #pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8_t af[FM], bfr[FN];
+  #pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = frag(As, wm * CF::WTM + i * 32 + l32, 2 * ks + h);
+  #pragma unroll
+        for (int j = 0; j < FN; ++j) bfr[j] = frag(Bs, wn * CF::WTN + j * 32 + l32, 2 * ks + h);
+        if (xa) {
+  #pragma unroll
+          for (int i = 0; i < FM; ++i)
+            af[i] = mask_frag<true>(af[i], p.tria, m0 + wm * CF::WTM + i * 32 + l32,
                                     kbase + ks * 16 + h * 8);
+        }
+        if (xb) {
+  #pragma unroll
+          for (int j = 0; j < FN; ++j)
+            bfr[j] = mask_frag<false>(bfr[j], p.trib, n0 + wn * CF::WTN + j * 32 + l32,
+                                      kbase + ks * 16 + h * 8);
+        }
+  #pragma unroll
+        for (int i = 0; i < FM; ++i)
+  #pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
   }
 
@@ -355,7 +476,8 @@ __global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p)
     for (int l = c * per + (int)(xcd ? blockIdx.x >> 3 : blockIdx.x); l < l1; l += nl) {
       int tm, tn;
       tri_tile(l, p.upper_only != 0, &tm, &tn);
-      bb_tile<CF>(p, tm, tn, smem_bb);
+      if (p.tria == TRI_NONE && p.trib == TRI_NONE) bb_tile<CF, false>(p, tm, tn, smem_bb);
+      else bb_tile<CF, true>(p, tm, tn, smem_bb);
       __syncthreads();
     }
   } else if ((gridDim.x & 7) == 0 && p.tria == TRI_NONE && p.trib == TRI_NONE) {
@@ -366,14 +488,15 @@ __global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p)
       const int g = l / (XCD_GM * tiles_n);              // band of tile rows
       const int rows = min(XCD_GM, tiles_m - g * XCD_GM);
       const int r = l - g * XCD_GM * tiles_n;
-      bb_tile<CF>(p, g * XCD_GM + r % rows, r / rows, smem_bb);
+      bb_tile<CF, false>(p, g * XCD_GM + r % rows, r / rows, smem_bb);
       __syncthreads();   // the LDS ring is reused by the next tile
     }
   } else {
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
       int tm, tn;
       tile_order(tile, tiles_m, tiles_n, p.tria, p.trib, &tm, &tn);
-      bb_tile<CF>(p, tm, tn, smem_bb);
+      if (p.tria == TRI_NONE && p.trib == TRI_NONE) bb_tile<CF, false>(p, tm, tn, smem_bb);
+      else bb_tile<CF, true>(p, tm, tn, smem_bb);
       __syncthreads();
     }
   }
