@@ -88,6 +88,32 @@ class HipBackend:
         _lib.check(rc, "ifk_tsqr_fold")
         return int(r_out.value)
 
+    def fold_gram_(self, R: torch.Tensor, r_in: int, X: torch.Tensor,
+                   pivot_tol: float) -> torch.Tensor:
+        """Fold chunk X into R by the Gram route (bf16 arithmetic, r_in + p >= n).
+
+        Returns the device int32[1] status: 1 R holds the factor of
+        [R[:r_in]; X] (n rows); 2 a pivot fell below ``pivot_tol`` of its Gram
+        diagonal or the input is not finite -- R is then unchanged and the
+        caller folds by ``fold_``.
+        """
+        _require_device(R, "tsqr_fold_gram")
+        n = R.shape[1]
+        if R.dtype != torch.float32 or R.shape[0] != n or not R.is_contiguous():
+            raise IFKFACBackendError("tsqr_fold_gram: R must be a contiguous n x n fp32 buffer")
+        X, ldx, xdt = _mat(X, "tsqr_fold_gram")
+        if X.shape[1] != n:
+            raise IFKFACBackendError(f"tsqr_fold_gram: chunk has {X.shape[1]} columns, R has {n}")
+        p = X.shape[0]
+        st = torch.empty(1, dtype=torch.int32, device=R.device)
+        ws = self._ws(self.lib.ifk_tsqr_fold_gram_workspace_size(p, n, int(r_in)), R.device)
+        with torch.cuda.device(R.device):
+            rc = self.lib.ifk_tsqr_fold_gram(self._stream(R.device), _ptr(X), xdt, p, n, ldx,
+                                             _ptr(R), n, int(r_in), float(pivot_tol), _ptr(st),
+                                             _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_tsqr_fold_gram")
+        return st
+
     # -- damping / finalisation -------------------------------------------------
     def finalize(self, R: torch.Tensor, scale: float, damping: float, out_dtype: torch.dtype,
                  math: int) -> Tuple[torch.Tensor, torch.Tensor]:

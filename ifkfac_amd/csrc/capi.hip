@@ -122,6 +122,19 @@ int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, 
                             workspace, workspace_bytes);
 }
 
+size_t ifk_tsqr_fold_gram_workspace_size(int64_t p, int64_t n, int64_t r_in) {
+  if (p < 0 || n < 1 || r_in < 0 || r_in > n) return 0;
+  return tsqr_fold_gram_ws(p, n, r_in);
+}
+
+int ifk_tsqr_fold_gram(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
+                       int64_t ldx, float* R, int64_t ldr, int64_t r_in, float pivot_tol,
+                       int32_t* status, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(x_dtype), "tsqr_fold_gram: bad dtype");
+  return tsqr_fold_gram((hipStream_t)stream, X, x_dtype, p, n, ldx, R, ldr, r_in, pivot_tol,
+                        status, workspace, workspace_bytes);
+}
+
 size_t ifk_fold_finalize_gram_batched_workspace_size(int64_t batch, int64_t p, int64_t n,
                                                      int64_t r_in) {
   if (batch < 1 || p < 0 || n < 1 || r_in < 0 || r_in > n) return 0;

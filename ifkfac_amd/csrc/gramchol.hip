@@ -42,7 +42,8 @@
 // and most of the updates (n^3 in all, split) are done beside the chain.
 // Step c itself applies only the update by panel c - 1.
 //
-// Pivot test: a pivot below GRAM_TOL times the Gram diagonal of its column
+// Pivot test: a pivot below the tolerance (GRAM_TOL for the factor update,
+// the caller's for the streaming fold) times the Gram diagonal of its column
 // (A's diagonal before any update) means that column is nearly a combination
 // of the ones before it (cancellation of more than 1 - GRAM_TOL in the Schur
 // complement): the rounding of the Gram matrix and of the updates, about
@@ -410,6 +411,7 @@ struct GramWs {
                       // diagonal block in the extra set nb, its rows below in set 0)
   int64_t sPT, sAw, sdref, sGB, sZd, sMT3, sLSb, sAS2, sL, sfrob;
   SplitScratch sp, sp2, sp3;   // split-K partials of the three streams
+  float tol;                   // relative pivot threshold of the pivot test
 };
 constexpr int64_t FLAG_S = 64;   // ints between two entries' flags (separate cache lines)
 
@@ -549,7 +551,7 @@ int chain_factor(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
   RC(sym_from_lower(s, B, Akk, w.lda, W, w.G, GB, w.sAw, w.sGB));
   CholbStrides cs;
   cs.a = w.sGB; cs.u = w.sGB; cs.zd = w.sZd; cs.dref = w.sdref; cs.m = w.sGB; cs.flag = FLAG_S;
-  RC(launch_cholb(s, w.G, GB, (int)W, w.U, GB, w.Zd, w.dref + b.r0, GRAM_TOL, w.flag, w.M, GB,
+  RC(launch_cholb(s, w.G, GB, (int)W, w.U, GB, w.Zd, w.dref + b.r0, w.tol, w.flag, w.M, GB,
                   true, B, cs));
   return launch_transpose_cast(s, w.U, GB, W, W, Akk, DT_F32, w.lda, B, w.sGB, w.sAw);
 }
@@ -637,7 +639,7 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
                        int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
                        int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
                        int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
-                       size_t ws_bytes) {
+                       size_t ws_bytes, float pivot_tol) {
   bool ok = n >= 1 && p >= 0 && r_in >= 0 && r_in <= n && batch >= 1 && batch <= 65535 &&
             (p == 0 || (X && ldx >= n)) && (r_in == 0 || (R_in && ldr >= n)) && out &&
             ldo >= n && out_stride >= n * ldo && scale > 0.0f && damping >= 0.0f &&
@@ -666,6 +668,11 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
     set_error("fold_finalize_gram: workspace too small");
     return IFK_ERR_WORKSPACE;
   }
+  if (!(pivot_tol > 0.0f && pivot_tol < 1.0f)) {
+    set_error("fold_finalize_gram: pivot tolerance outside (0, 1)");
+    return IFK_ERR_INVALID;
+  }
+  w.tol = pivot_tol;
   const int B = (int)batch;
   const int64_t nb = cdiv(n, GB);
   LookAhead* la = nullptr;
@@ -767,6 +774,57 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   hipLaunchKernelGGL(status_merge_batch_kernel, dim3((unsigned)cdiv(B, 64)), dim3(64), 0, s,
                      status, w.flag, FLAG_S, B);
   return check_launch("status_merge");
+}
+
+// ---------------------------------------------------------------------------
+// The streaming fold by the Gram route (bf16 arithmetic): R (n x n, rows
+// [0, r_in) valid) becomes the factor of [R[0:r_in]; X] when that is square
+// (r_in + p >= n).  The factor goes to the workspace first and is copied into
+// R only where the status is 1, so a fold that fails the pivot test or meets
+// non-finite input (status 2) leaves R as it was for the caller's panel fold.
+// ---------------------------------------------------------------------------
+namespace {
+
+__global__ void cond_copy_kernel(const float* src, int64_t n, float* R, int64_t ldr,
+                                 const int* status) {
+  if (*status != 1) return;
+  const int64_t total = n * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / n, j = e - i * n;
+    R[i * ldr + j] = src[e];
+  }
+}
+
+}  // namespace
+
+size_t tsqr_fold_gram_ws(int64_t p, int64_t n, int64_t r_in) {
+  return align_up((size_t)n * n * sizeof(float), 256) + fold_finalize_gram_ws(1, p, n, r_in);
+}
+
+int tsqr_fold_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                   float* R, int64_t ldr, int64_t r_in, float pivot_tol, int* status, void* ws,
+                   size_t ws_bytes) {
+  if (n < 1 || p < 0 || r_in < 0 || r_in > n || r_in + p < n || !R || ldr < n || !status ||
+      (p > 0 && (!X || ldx < n))) {
+    set_error("tsqr_fold_gram: invalid arguments (the folded factor must be square: "
+              "r_in + p >= n)");
+    return IFK_ERR_INVALID;
+  }
+  const size_t head = align_up((size_t)n * n * sizeof(float), 256);
+  if (!ws || ws_bytes < head) {
+    set_error("tsqr_fold_gram: workspace too small");
+    return IFK_ERR_WORKSPACE;
+  }
+  float* tmp = (float*)ws;
+  const void* xs[1] = {X};
+  const float* rs[1] = {R};
+  RC(fold_finalize_gram(s, 1, xs, xdt, p, n, ldx, rs, ldr, r_in, 1.0f, 0.0f, tmp, DT_F32, n,
+                        n * n, MATH_BF16, status, nullptr, (char*)ws + head, ws_bytes - head,
+                        pivot_tol));
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(n * n, 256), 4096);
+  hipLaunchKernelGGL(cond_copy_kernel, dim3(blocks), dim3(256), 0, s, tmp, n, R, ldr, status);
+  return check_launch("tsqr_fold_gram copy");
 }
 
 }  // namespace ifk

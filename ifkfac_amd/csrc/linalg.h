@@ -51,7 +51,16 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
                        int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
                        int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
                        int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
-                       size_t ws_bytes);
+                       size_t ws_bytes, float pivot_tol = 1e-3f);
+
+// The streaming fold by the Gram route (bf16 arithmetic): R (rows [0, r_in)
+// valid) <- the factor of [R[0:r_in]; X] when r_in + p >= n; *status 1 (R
+// written) or 2 (a pivot below pivot_tol of its Gram diagonal, or input not
+// finite), R unchanged unless 1.
+size_t tsqr_fold_gram_ws(int64_t p, int64_t n, int64_t r_in);
+int tsqr_fold_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
+                   float* R, int64_t ldr, int64_t r_in, float pivot_tol, int* status, void* ws,
+                   size_t ws_bytes);
 
 // Z = R^{-1} for upper-triangular R (dtype rdt); Z fp32 upper triangular.
 size_t trinv_ws(int64_t n);

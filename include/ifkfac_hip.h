@@ -154,6 +154,23 @@ int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, 
                            size_t workspace_bytes);
 
 /*
+ * The streaming fold by the Gram route -- replaces streaming_tsqr_update
+ * (ifkfac/triangular.py:246-307) in bf16 arithmetic when the folded factor is
+ * square (r_in + p >= n): R (n x n fp32, rows [0, r_in) valid) becomes the
+ * upper factor with positive diagonal of [R[0:r_in]; X] from the Gram matrix
+ * of the bf16-rounded rows and the blocked Cholesky of ifk_fold_finalize_gram.
+ * *status: 1 R written; 2 a pivot fell below pivot_tol times its Gram
+ * diagonal (too ill-conditioned for the Gram route at that tolerance) or the
+ * input is not finite.  R is left unchanged unless *status is 1, so the caller
+ * folds by ifk_tsqr_fold instead (the host reads the status).  pivot_tol in
+ * (0, 1).
+ */
+size_t ifk_tsqr_fold_gram_workspace_size(int64_t p, int64_t n, int64_t r_in);
+int ifk_tsqr_fold_gram(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
+                       int64_t ldx, float* R, int64_t ldr, int64_t r_in, float pivot_tol,
+                       int32_t* status, void* workspace, size_t workspace_bytes);
+
+/*
  * ifk_fold_finalize_gram for `batch` layers of the same shape in the same
  * launches (replaces the per-layer loop of batched_streaming_tsqr_update /
  * flush, ifkfac/triangular.py:331-379, ifkfac/activation_hooks.py:370-457,

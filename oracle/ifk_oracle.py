@@ -10,6 +10,8 @@ scipy LAPACK (the same routine family the reference reaches through
 torch.linalg on CPU).  How each function is pinned (tests/test_oracle.py):
 
   positive_diagonal          closed form; sign(0) = +1 special case
+  gram_pivot_ratio           two columns at angle t: (1, sin^2 t) by hand;
+                             orthogonal columns all 1; a repeated column 0
   streaming_tsqr_update      uniqueness: R^T R = sum X_i^T X_i with positive
                              diagonal == Cholesky factor of the Gram matrix;
                              exact-rational Gram-Schmidt on tiny integer inputs
@@ -112,6 +114,19 @@ def streaming_tsqr_update(running_R: Optional[np.ndarray], new_chunk: np.ndarray
     if running_R is None:
         return positive_diagonal(R_new)
     return positive_diagonal(_qr_r(np.vstack([running_R, R_new])))
+
+
+def gram_pivot_ratio(P: np.ndarray) -> np.ndarray:
+    """Pivot ratios of the Cholesky of A = P^T P: R_kk^2 / A_kk for each column,
+    the squared sine of the angle between column k and the span of the columns
+    before it.  No counterpart in the reference: it is the rule by which the
+    Gram-route fold (ifk_tsqr_fold_gram) refuses a chunk and the panel fold
+    (triangular.py:246-307) takes it instead.  Computed from the QR of P (fp64),
+    so the checker itself does not lose the small ratios to the Gram matrix."""
+    R = _qr_r(np.asarray(P, dtype=np.float64))
+    d = np.sum(np.asarray(P, dtype=np.float64) ** 2, axis=0)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return np.where(d > 0, np.diag(R) ** 2 / np.where(d > 0, d, 1.0), 0.0)
 
 
 def finalize_R(running_R: np.ndarray, damping: float) -> np.ndarray:

@@ -37,6 +37,30 @@ class OracleBackend:
         R[:r_new] = torch.from_numpy(new).to(R.dtype)
         return r_new
 
+    # tests set this to make the Gram-route fold refuse (status 2) once per call
+    gram_fold_status2 = 0
+
+    def fold_gram_(self, R, r_in, X, pivot_tol):
+        """The Gram-route fold: status 2 (R untouched) when the Cholesky of the
+        Gram matrix of [R[:r_in]; X] meets a pivot below pivot_tol of its column's
+        diagonal (O.gram_pivot_ratio), else the fold's factor and status 1."""
+        self.calls["fold_gram"] += 1
+        n = R.shape[1]
+        assert r_in + X.shape[0] >= n, "Gram-route fold of a partial-rank factor"
+        old = None if r_in == 0 else _np(R[:r_in])
+        P = _np(X) if old is None else np.vstack([old, _np(X)])
+        if self.gram_fold_status2 > 0:
+            self.gram_fold_status2 -= 1
+            return torch.tensor([2], dtype=torch.int32)
+        if not np.all(np.isfinite(P)):
+            return torch.tensor([2], dtype=torch.int32)
+        if O.gram_pivot_ratio(P).min() < pivot_tol:
+            return torch.tensor([2], dtype=torch.int32)
+        new = O.streaming_tsqr_update(old, _np(X))
+        R.zero_()
+        R[:n] = torch.from_numpy(new).to(R.dtype)
+        return torch.tensor([1], dtype=torch.int32)
+
     def finalize(self, R, scale, damping, out_dtype, math):
         self.calls["finalize"] += 1
         Rd = O.finalize_R(_np(R) * scale, damping)

@@ -188,3 +188,92 @@ def test_fold_finalize_gram_batched_matches_single(hip, B, prev, p, n):
         assert torch.equal(out[e], one), e
         assert st[e].item() == s1.item() == 1
         assert kb[e].item() == k1.item()
+
+
+# ---------------------------------------------------------------------------
+# the streaming fold by the Gram route (ifk_tsqr_fold_gram)
+# ---------------------------------------------------------------------------
+FOLD_TOL = 1e-4
+
+
+@pytest.mark.parametrize("prev,p,n,xdt", [
+    ([], 600, 500, torch.float32), ([300], 400, 600, torch.bfloat16), ([600], 600, 600, torch.float32),
+    ([1200], 1200, 2100, torch.float32), ([512, 512], 512, 1024, torch.bfloat16),
+    ([2048], 4096, 3072, torch.float32),
+])
+def test_tsqr_fold_gram_matches_closed_form(hip, prev, p, n, xdt):
+    """R <- the undamped factor of [bf16(R_in); bf16(X)]: ||R^T R - P^T P||_F /
+    ||P^T P||_F <= 3e-5 (Cholesky's backward error with 2^-17 products), upper
+    triangular with a positive diagonal, and no worse than the bf16 panel fold of the
+    same chunk against the same closed form."""
+    g = torch.Generator(device=DEV).manual_seed(p + n + len(prev))
+    R, r = _fold_chunks(hip, [torch.randn(q, n, device=DEV, generator=g) for q in prev], n)
+    X = torch.randn(p, n, device=DEV, generator=g).to(xdt)
+    R_before = R.clone()
+    st = hip.fold_gram_(R, r, X, FOLD_TOL)
+    assert st.item() == 1
+    parts = ([_bf16_np(R_before[:r])] if r > 0 else []) + [_bf16_np(X)]
+    want = O.chol_factor(parts, 1, 0.0)
+    e = _gram_rel(R, want)
+    Rp = R_before.clone()
+    assert hip.fold_(Rp, r, X, 1) == n
+    ep = _gram_rel(Rp, want)
+    print(f"tsqr_fold_gram n={n} p={p} r_in={r}: gram rel {e:.3e} (panel fold {ep:.3e})")
+    assert e <= 3e-5 and e <= ep
+    Rg = R.double().cpu().numpy()
+    assert np.all(np.diag(Rg) > 0) and not np.any(np.tril(Rg, -1))
+
+
+def test_tsqr_fold_gram_refusals_leave_R(hip):
+    """A dependent column (pivot ratio 0), a NaN, and a nearly square running
+    factor whose last pivot ratio is below the threshold: status 2 and R bit for bit
+    as it was; the panel fold then takes the chunk."""
+    from ifkfac_amd.activation_hooks import fold_chunk
+    g = torch.Generator(device=DEV).manual_seed(21)
+    R, r = _fold_chunks(hip, [torch.randn(700, 640, device=DEV, generator=g)], 640)
+    X = torch.randn(300, 640, device=DEV, generator=g)
+    for case in ("dependent", "nan"):
+        Rz = torch.zeros(640, 640, device=DEV)
+        Y = X.clone()
+        if case == "dependent":
+            Y = torch.randn(900, 640, device=DEV, generator=g)
+            Y[:, 600] = 2.0 * Y[:, 3] - Y[:, 500]
+            before = Rz.clone()
+            assert hip.fold_gram_(Rz, 0, Y, FOLD_TOL).item() == 2
+            assert torch.equal(Rz, before)
+        else:
+            Y[17, 33] = float("nan")
+            before = R.clone()
+            assert hip.fold_gram_(R, r, Y, FOLD_TOL).item() == 2
+            assert torch.equal(R, before)
+    # kappa 1e2 chunks of 512 rows into a 1024-column factor: the second fold is
+    # square with a pivot ratio near 3e-6 (refused), the later ones near 3e-3
+    rng = np.random.default_rng(1)
+    Xk = torch.from_numpy(O.kappa_matrix(4096, 1024, 1e2, rng).astype(np.float32))
+    Xk = Xk.to(torch.bfloat16).to(DEV)
+    Rg = torch.zeros(1024, 1024, device=DEV)
+    Rp = torch.zeros(1024, 1024, device=DEV)
+    rg = rp = 0
+    statuses = []
+    for c in range(8):
+        chunk = Xk[512 * c:512 * (c + 1)]
+        if rg + 512 >= 1024:
+            Rb = Rg.clone()
+            s = hip.fold_gram_(Rb, rg, chunk, FOLD_TOL).item()
+            statuses.append(s)
+        rg = fold_chunk(Rg, rg, chunk, 1)
+        rp = hip.fold_(Rp, rp, chunk, 1)
+    print(f"kappa 1e2 chunk statuses {statuses}")
+    assert statuses[0] == 2 and all(s == 1 for s in statuses[1:])
+    want = O.chol_factor([_bf16_np(Xk)], 1, 0.0)
+    eg, ep = _gram_rel(Rg, want), _gram_rel(Rp, want)
+    print(f"8 folds: gram route {eg:.3e}, panel folds {ep:.3e}")
+    assert rg == rp == 1024 and eg <= ep
+
+
+def test_tsqr_fold_gram_guards(hip):
+    R = torch.zeros(64, 64, device=DEV)
+    with pytest.raises(Exception):   # the folded factor would not be square
+        hip.fold_gram_(R, 10, torch.randn(50, 64, device=DEV), FOLD_TOL)
+    with pytest.raises(Exception):   # tolerance outside (0, 1)
+        hip.fold_gram_(R, 0, torch.randn(80, 64, device=DEV), 0.0)

@@ -173,3 +173,42 @@ def test_gamma_blend_on_gpu(hip, use_bf16):
         old = [R_X.double().cpu().numpy(), R_G.double().cpu().numpy()]
         if use_bf16:
             assert R_X.dtype == torch.bfloat16 and R_G.dtype == torch.bfloat16
+
+
+def test_bf16_capture_takes_gram_route_on_gpu(hip, caplog):
+    """bf16 arithmetic (use_true_bf16): square folds and get_factors() go by the
+    Gram route; an input side with a repeated column of large scale is refused by
+    both (pivot tests) and taken by the panel fold and finalize.  Every factor is
+    upper triangular with a positive diagonal and within 1e-2 (Gram relative
+    error: bf16 rounding of the data and of the running factor at each fold) of
+    the fp64 closed form chol(sum X^T X / rows + lambda I)."""
+    import logging
+    from ifkfac_amd import IFKFAC
+    from oracle import ifk_oracle as O
+    torch.manual_seed(4)
+    model = nn.Sequential(nn.Linear(256, 512), nn.Tanh(), nn.Linear(512, 64)).cuda()
+    kfac = IFKFAC(model, lr=0.0, damping=1e-3, use_true_bf16=True, factor_update_freq=1000)
+    caplog.set_level(logging.DEBUG, logger="ifkfac_amd.activation_hooks")
+    acts = {m: [] for m in (model[0], model[2])}
+    hs = [m.register_forward_hook(lambda mod, i, o: acts[mod].append(i[0].detach().double()))
+          for m in acts]
+    for b in range(4):
+        x = torch.randn(384, 256, device="cuda")
+        x[:, 7] = 30.0 * x[:, 5]                     # the first layer's input side is singular
+        model(x).logsumexp(-1).sum().backward()
+    for h in hs:
+        h.remove()
+    factors = kfac.hooks.get_factors()
+    msgs = [r.getMessage() for r in caplog.records]
+    assert any("Gram route refused" in m and "256-column" in m for m in msgs)
+    assert any("X factor by the panel path" in m for m in msgs)
+    for m, (R_X, _) in factors.items():
+        R = R_X.double()
+        assert torch.count_nonzero(torch.tril(R, -1)).item() == 0
+        assert bool((torch.diagonal(R) > 0).all())
+        X = torch.cat(acts[m]).cpu().numpy()
+        want = O.chol_factor([X], X.shape[0], 1e-3)
+        a, b = R.cpu().numpy(), want
+        e = np.linalg.norm(a.T @ a - b.T @ b) / np.linalg.norm(b.T @ b)
+        print(f"{tuple(R.shape)}: gram rel {e:.3e}")
+        assert e <= 1e-2

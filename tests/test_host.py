@@ -766,3 +766,39 @@ def test_triangular_mirrors_match_oracle(be):
     raw = t(g)
     assert T.apply_vered(raw, t(R_X[:5]).bfloat16(), t(R_G).bfloat16()) is raw
     assert T.apply_vered_bias(t(gb), t(R_G[:3]).bfloat16()).shape == (6,)
+
+
+def test_bf16_fold_takes_gram_route_when_square(be):
+    """bf16 arithmetic: a fold whose result is square goes to the Gram-route fold;
+    the first (partial-rank) chunk, a refused fold (status 2, injected or from a
+    repeated column) and fp32 arithmetic go to the panel fold.  Every path leaves
+    the oracle's running factor."""
+    from ifkfac_amd._backend import MATH_BF16, MATH_F32
+    from ifkfac_amd.activation_hooks import GRAM_FOLD_TOL, RawActivationHooks
+    model = nn.Sequential(nn.Linear(8, 4))
+    lin = model[0]
+    rng = np.random.default_rng(3)
+    chunks = [rng.standard_normal((p, 8)) for p in (5, 6, 8, 8)]
+    chunks[3][:, 7] = chunks[3][:, 0]            # a column repeated within the chunk
+    for math_, calls in ((MATH_BF16, (0, 1, 1, 1)), (MATH_F32, (0, 0, 0, 0))):
+        be.calls.clear()
+        hooks = RawActivationHooks(model, math=math_)
+        old = None
+        for i, c in enumerate(chunks):
+            if i == 2 and math_ == MATH_BF16:
+                be.gram_fold_status2 = 1          # the device reports an ill-conditioned fold
+            before = be.calls["fold_gram"]
+            hooks._fold("X", lin, torch.tensor(c, dtype=torch.float32))
+            assert be.calls["fold_gram"] - before == calls[i], (math_, i)
+            old = O.streaming_tsqr_update(old, c.astype(np.float32).astype(np.float64))
+            got = hooks._R_X[lin].double().numpy()
+            assert got.shape == old.shape
+            assert np.abs(got - old).max() <= 1e-5 * np.abs(old).max(), (math_, i)
+        hooks.remove()
+    assert be.gram_fold_status2 == 0
+    # the repeated column is refused by the pivot rule itself
+    P = np.vstack([O.streaming_tsqr_update(None, np.vstack(chunks[:3])), chunks[3]])
+    assert O.gram_pivot_ratio(P).min() > GRAM_FOLD_TOL   # earlier rows keep it independent
+    R0 = torch.zeros(8, 8)
+    st = be.fold_gram_(R0, 0, torch.tensor(chunks[3], dtype=torch.float32), GRAM_FOLD_TOL)
+    assert int(st.item()) == 2 and torch.count_nonzero(R0) == 0

@@ -59,6 +59,23 @@ def test_positive_diagonal_hand_case():
     assert np.array_equal(O.positive_diagonal(R), want)
 
 
+def test_gram_pivot_ratio_closed_forms():
+    """Two unit columns at angle t: ratios (1, sin^2 t); orthogonal columns of any
+    length: all 1; a repeated column: 0.  A planted variant that divides by the
+    pivot's own column norm after the update (always 1) fails the angle case."""
+    for t in (0.7, 1e-2, 1e-3):
+        P = np.array([[1.0, math.cos(t)], [0.0, math.sin(t)], [0.0, 0.0]])
+        r = O.gram_pivot_ratio(P)
+        assert abs(r[0] - 1.0) < 1e-15 and abs(r[1] - math.sin(t) ** 2) <= 1e-12 * math.sin(t) ** 2
+        planted = np.diag(np.linalg.qr(P, mode="r")) ** 2 / np.diag(np.linalg.qr(P, mode="r")) ** 2
+        assert abs(planted[1] - math.sin(t) ** 2) > 1e-3
+    Q = np.linalg.qr(np.random.default_rng(0).standard_normal((9, 4)))[0] * np.array([3, .1, 7, 1])
+    assert np.allclose(O.gram_pivot_ratio(Q), 1.0, rtol=1e-12)
+    P = np.random.default_rng(1).standard_normal((6, 3))
+    P[:, 2] = P[:, 0]
+    assert O.gram_pivot_ratio(P)[2] < 1e-25
+
+
 def _gs_exact(A):
     """R of Gram-Schmidt in exact rationals, returned as R^T R (sqrt-free form):
     the Gram matrix A^T A itself, built from Fractions."""
