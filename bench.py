@@ -63,7 +63,7 @@ PEAK_HBM_GBS = 8000.0
 # two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same
 # counters on a 256 MiB copy (profiles/pmc_traffic_linear4096x11008_p16384.txt);
 # None for other workloads and factor paths.
-TRAFFIC = {("linear_4096x11008_p16384", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1>>"): 881.40e6}
+TRAFFIC = {("linear_4096x11008_p16384", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"): 892.36e6}
 
 WORKLOADS = {
     # name: (n_in, n_out, p)
@@ -220,6 +220,7 @@ class LayerChain:
     def _side(self, T, R, how):
         import torch
         from ifkfac_amd._backend import MATH_BF16
+        from ifkfac_amd.activation_hooks import fold_chunk
         be, p = self.be, self.p
         r = 0
         last = T
@@ -227,7 +228,7 @@ class LayerChain:
             # the hooks fold every chunk but the held one into the running factor
             q = p // self.chunks
             for c in range(self.chunks - 1):
-                r = be.fold_(R, r, T[c * q:(c + 1) * q], self.math)
+                r = fold_chunk(R, r, T[c * q:(c + 1) * q], self.math)
             last = T[(self.chunks - 1) * q:]
         out_dtype = torch.bfloat16
         # as IFKFAC's factor update: the Gram path in bf16 arithmetic,
@@ -285,6 +286,7 @@ def extras(be, args, head_kappa):
     import torch.nn as nn
     from ifkfac_amd import IFKFAC
     from ifkfac_amd._backend import MATH_BF16
+    from ifkfac_amd.activation_hooks import fold_chunk
     res = {}
     steps, warm = max(3, args.steps // 2), 2
 
@@ -370,19 +372,27 @@ def extras(be, args, head_kappa):
 
     def batch(_first):
         for R, T in zip(Rs, chunks):
-            be.fold_(R, R.shape[0], T, MATH_BF16)
+            fold_chunk(R, R.shape[0], T, MATH_BF16)
     ms_b = timed(batch, steps, warm)
     fl_b = sum(2.0 * rows * nn_ ** 2 for (a, b) in shapes for nn_ in (a, b))
 
     def finalize_all(_first):
-        for R in Rs:
-            be.finalize(R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16, MATH_BF16)
+        # as get_factors() in bf16 arithmetic: every side by the Gram route,
+        # one host read of the flags, the panel finalize for a side flagged 2
+        out = [be.fold_finalize(None, 0, R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16,
+                                MATH_BF16, gram=True) for R in Rs]
+        st = torch.cat([f for _, f in out]).cpu()
+        for i, R in enumerate(Rs):
+            if int(st[i]) == 2:
+                be.finalize(R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16, MATH_BF16)
     ms_f = timed(finalize_all, 3, 1)
     res["vit_b_block_capture_p4096"] = {
         "ms_per_batch": round(ms_b, 3), "tflops_per_batch": round(fl_b / ms_b / 1e9, 1),
         "ms_get_factors": round(ms_f, 3),
-        "note": "8 folds of 4096 rows per batch into running factors (bf16 arithmetic); "
-                "200 batches x 12 blocks take 2400 x ms_per_batch"}
+        "note": "8 folds of 4096 rows per batch into running factors (bf16 arithmetic, "
+                "the Gram route with the panel fold for a refused fold); 200 batches x 12 "
+                "blocks take 2400 x ms_per_batch; get_factors() of the 8 sides by the Gram "
+                "route"}
     del Rs, chunks
     torch.cuda.empty_cache()
     res["kappa_R_damped_headline"] = head_kappa
@@ -493,8 +503,8 @@ def main() -> int:
         fam_fl[family(vid)] += a[2]
     fam = max(fam_fl, key=fam_fl.get)
     arm = {0: -4, 1: -3, 2: -5, 3: -6}[fam]
-    kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1>>",
-             3: "gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2>>"}[fam]
+    kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>",
+             3: "gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2, false>>"}[fam]
     torch.cuda.synchronize()
     _lib.check(lib.ifk_profile_begin(arm), "profile_begin")
     torch.cuda.synchronize()
