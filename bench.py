@@ -231,9 +231,15 @@ class LayerChain:
                 r = fold_chunk(R, r, T[c * q:(c + 1) * q], self.math)
             last = T[(self.chunks - 1) * q:]
         out_dtype = torch.bfloat16
-        # as IFKFAC's factor update: the Gram path in bf16 arithmetic,
-        # CholeskyQR2 blocks in fp32 arithmetic
+        # as IFKFAC's factor update: the Gram path in bf16 arithmetic (the
+        # factor's inverse formed in the same call), CholeskyQR2 blocks in fp32
+        # arithmetic
         gram = how == "gram" and self.math == MATH_BF16
+        if gram:
+            F, st, _, (Z, Zb, ZT) = be.fold_finalize_gram_batched(
+                [R] if r > 0 else None, r, [last], 1 / math.sqrt(p), self.lam, out_dtype,
+                with_inverse=True)
+            return F[0], st, (Z[0], Zb[0], ZT[0])
         cqr = how == "cqr" or (how == "gram" and not gram)
         F, st = be.fold_finalize(R if r > 0 else None, r, last, 1 / math.sqrt(p), self.lam,
                                  out_dtype, self.math, cqr=cqr, gram=gram)

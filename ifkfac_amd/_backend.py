@@ -181,12 +181,15 @@ class HipBackend:
         return (out, flag, kb) if kb is not None else (out, flag)
 
     def fold_finalize_gram_batched(self, Rs, r_in: int, Xs, scale: float, damping: float,
-                                   out_dtype: torch.dtype):
+                                   out_dtype: torch.dtype, with_inverse: bool = False):
         """fold_finalize(..., gram=True, with_kappa=True) for B same-shape sides in
         the same launches (ifk_fold_finalize_gram_batched).  Xs: B chunks (p x n,
         one dtype); Rs: B running-factor buffers or None when r_in == 0.
         Returns (factors (B, n, n), status int32[B], kappa bound float32[B]); entry
-        b is bitwise the single-side result."""
+        b is bitwise the single-side result.  With ``with_inverse``
+        (ifk_fold_finalize_gram_inverse) a fourth value (Z fp32, Zb, ZT bf16, each
+        (B, n, n)): the inverse of each fp32 factor and its bf16 copies, formed
+        beside the factorisation (meaningless where the status is 2)."""
         B = len(Xs)
         mats = [_mat(X, "fold_finalize_gram_batched") for X in Xs]
         X0, ldx, xdt = mats[0]
@@ -211,6 +214,21 @@ class HipBackend:
         out = torch.empty((B, n, n), dtype=out_dtype, device=dev)
         st = torch.empty(B, dtype=torch.int32, device=dev)
         kb = torch.empty(B, dtype=torch.float32, device=dev)
+        if with_inverse:
+            Z = torch.empty((B, n, n), dtype=torch.float32, device=dev)
+            Zb = torch.empty((B, n, n), dtype=torch.bfloat16, device=dev)
+            ZT = torch.empty((B, n, n), dtype=torch.bfloat16, device=dev)
+            ws = self._ws(self.lib.ifk_fold_finalize_gram_inverse_workspace_size(
+                B, p, n, int(r_in)), dev)
+            with torch.cuda.device(dev):
+                rc = self.lib.ifk_fold_finalize_gram_inverse(
+                    self._stream(dev), B, ctypes.cast(xptrs, ctypes.c_void_p), xdt, p, n, ldx,
+                    ctypes.cast(rptrs, ctypes.c_void_p) if rptrs is not None else None, ldr,
+                    int(r_in), float(scale), float(damping), _ptr(out), _DT[out_dtype], n, n * n,
+                    _ptr(st), _ptr(kb), _ptr(Z), n, n * n, _ptr(Zb), _ptr(ZT), n, n * n,
+                    _ptr(ws), ws.numel())
+            _lib.check(rc, "ifk_fold_finalize_gram_inverse")
+            return out, st, kb, (Z, Zb, ZT)
         ws = self._ws(self.lib.ifk_fold_finalize_gram_batched_workspace_size(B, p, n, int(r_in)),
                       dev)
         with torch.cuda.device(dev):

@@ -122,6 +122,12 @@ SIGNATURES = {
     "ifk_laplace_sample": (_c_int, [_c_vp, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp,
                                     _c_i64, _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_i64, _c_vp,
                                     _c_sz]),
+    "ifk_fold_finalize_gram_inverse_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ifk_fold_finalize_gram_inverse": (_c_int, [_c_vp, _c_i64, _c_vp, _c_int, _c_i64, _c_i64,
+                                                _c_i64, _c_vp, _c_i64, _c_i64, _c_f, _c_f, _c_vp,
+                                                _c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp,
+                                                _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
+                                                _c_vp, _c_sz]),
     "ifk_tsqr_fold_gram_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64]),
     "ifk_tsqr_fold_gram": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64,
                                     _c_i64, _c_f, _c_vp, _c_vp, _c_sz]),

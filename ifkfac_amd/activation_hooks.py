@@ -257,28 +257,37 @@ class RawActivationHooks(GramMatrixEstimator):
         return R, r, chunk, min(r + chunk.shape[0], n)
 
     def _damped(self, side: str, module: nn.Module, rows: int, out_dtype: torch.dtype,
-                fast: bool = False):
+                fast: bool = False, with_inverse: bool = False):
         """(R_damped, flag, kappa bound or None) of one side; a held chunk goes
         into a fused fold + finalize.  With ``fast`` that factorisation is the
         Gram matrix + blocked Cholesky in bf16 arithmetic (which also bounds
         kappa_2 of the factor; without a held chunk its input is the running
         factor), CholeskyQR2 outer blocks in fp32 arithmetic; its flag may
-        then be 2 (see _retry_cholesky_qr)."""
+        then be 2 (see _retry_cholesky_qr).  With ``with_inverse`` the Gram
+        route also forms the factor's inverse and its bf16 copies beside the
+        factorisation (a fourth value (Z, Zb, ZT), else None)."""
         R, r, chunk, _ = self._side_state(side, module)
-        if chunk is None:
-            if fast and self.math == MATH_BF16:
-                # the running factor itself is the Gram route's input (p = n rows)
-                return get_backend().fold_finalize(None, 0, R, 1.0 / math.sqrt(rows),
-                                                   self.damping, out_dtype, self.math,
-                                                   gram=True, with_kappa=True)
-            return self._finalize(R, rows, out_dtype) + (None,)
-        bufs = self._buf_X if side == "X" else self._buf_G
+        be = get_backend()
         gram = fast and self.math == MATH_BF16
-        res = get_backend().fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
-                                          1.0 / math.sqrt(rows), self.damping, out_dtype,
-                                          self.math, cqr=fast and not gram, gram=gram,
-                                          with_kappa=gram)
-        return res if gram else res + (None,)
+        if gram and with_inverse:
+            bufs = self._buf_X if side == "X" else self._buf_G
+            Rs, X, r_in = ([bufs.get(module)], chunk, r) if chunk is not None else (None, R, 0)
+            out, st, kb, (Z, Zb, ZT) = be.fold_finalize_gram_batched(
+                Rs if r_in > 0 else None, r_in, [X], 1.0 / math.sqrt(rows), self.damping,
+                out_dtype, with_inverse=True)
+            return out[0], st, kb, (Z[0], Zb[0], ZT[0])
+        if chunk is None:
+            if gram:
+                # the running factor itself is the Gram route's input (p = n rows)
+                return be.fold_finalize(None, 0, R, 1.0 / math.sqrt(rows), self.damping,
+                                        out_dtype, self.math, gram=True,
+                                        with_kappa=True) + (None,)
+            return self._finalize(R, rows, out_dtype) + (None, None)
+        bufs = self._buf_X if side == "X" else self._buf_G
+        res = be.fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
+                               1.0 / math.sqrt(rows), self.damping, out_dtype, self.math,
+                               cqr=fast and not gram, gram=gram, with_kappa=gram)
+        return res + (None,) if gram else res + (None, None)
 
     def _retry_cholesky_qr(self, factors, flags, extras, then, out_dtype: torch.dtype):
         """One host read of the flags of a consuming factor update (or of
@@ -295,7 +304,7 @@ class RawActivationHooks(GramMatrixEstimator):
                 rows = self._n_rows_X[m] if side == "X" else self._n_rows_G[m]
                 logger.debug("get_factors() [%s]: %s factor by the panel path",
                              _module_tag(m), side)
-                R, f, kb = self._damped(side, m, rows, out_dtype, fast=False)
+                R, f, kb, _ = self._damped(side, m, rows, out_dtype, fast=False)
                 fac, fl = list(factors[m]), list(flags[m])
                 fac[j], fl[j] = R, f
                 factors[m], flags[m] = tuple(fac), tuple(fl)
@@ -328,7 +337,8 @@ class RawActivationHooks(GramMatrixEstimator):
             by_key.setdefault((sx, sg), []).append(module)
         return [mods for mods in by_key.values() if len(mods) >= 2]
 
-    def _damped_batch(self, side: str, mods, rows: int, out_dtype: torch.dtype, then):
+    def _damped_batch(self, side: str, mods, rows: int, out_dtype: torch.dtype, then,
+                      with_inverse: bool = False):
         """_damped(fast=True) for a group of same-signature sides in one batched
         call; per module (R_damped, flag, then's result or None).  The factors are
         views of one (B, n, n) buffer."""
@@ -338,12 +348,20 @@ class RawActivationHooks(GramMatrixEstimator):
             R, r, chunk, _ = self._side_state(side, m)
             chunks.append(chunk)
             bufs.append((self._buf_X if side == "X" else self._buf_G).get(m))
-        out, st, kb = get_backend().fold_finalize_gram_batched(
-            bufs if r > 0 else None, r, chunks, 1.0 / math.sqrt(rows), self.damping, out_dtype)
+        got = get_backend().fold_finalize_gram_batched(
+            bufs if r > 0 else None, r, chunks, 1.0 / math.sqrt(rows), self.damping, out_dtype,
+            with_inverse=with_inverse)
+        out, st, kb = got[:3]
         res = []
         for e, m in enumerate(mods):
             R, f, k = out[e], st[e:e + 1], kb[e:e + 1]
-            res.append((R, f, then(side, m, R, k) if then is not None else None))
+            if then is None:
+                res.append((R, f, None))
+            elif with_inverse:
+                Z, Zb, ZT = got[3]
+                res.append((R, f, then(side, m, R, k, inv=(Z[e], Zb[e], ZT[e]))))
+            else:
+                res.append((R, f, then(side, m, R, k)))
         return res
 
     # ------------------------------------------------------------------ factors
@@ -352,7 +370,8 @@ class RawActivationHooks(GramMatrixEstimator):
         factors, _, _ = self._collect_factors(torch.float32)
         return factors
 
-    def _collect_factors(self, out_dtype: torch.dtype, consume: bool = False, then=None):
+    def _collect_factors(self, out_dtype: torch.dtype, consume: bool = False, then=None,
+                         with_inverse: bool = False):
         """get_factors with the output dtype chosen and the finite flags returned.
 
         With ``consume`` the caller clears the hooks right after, so a held
@@ -364,7 +383,9 @@ class RawActivationHooks(GramMatrixEstimator):
         None) (work
         that depends on one side only starts while the other is still being
         factored); its results come back as the third value, per module as
-        (X side, G side), or None without ``then``."""
+        (X side, G side), or None without ``then``.  With ``with_inverse`` a
+        side factored by the Gram route comes with its inverse, formed beside
+        the factorisation: ``then`` is then called with ``inv=(Z, Zb, ZT)``."""
         if self.deferred:
             self._drain_deferred()
         if not consume:
@@ -377,9 +398,15 @@ class RawActivationHooks(GramMatrixEstimator):
         flags: Dict[nn.Module, Tuple[torch.Tensor, torch.Tensor]] = {}
         extras: Dict[nn.Module, tuple] = {}
 
+        want_inv = with_inverse and then is not None
+
         def side(s, module, rows, fast):
-            R, f, kb = self._damped(s, module, rows, out_dtype, fast=fast)
-            return R, f, (then(s, module, R, kb) if then is not None else None)
+            R, f, kb, inv = self._damped(s, module, rows, out_dtype, fast=fast,
+                                         with_inverse=want_inv)
+            if then is None:
+                return R, f, None
+            return R, f, (then(s, module, R, kb) if inv is None
+                          else then(s, module, R, kb, inv=inv))
         eligible = []
         for module in self._linear_layers:
             R_X_raw, _, chunk_X, r_X = self._side_state("X", module)
@@ -417,8 +444,8 @@ class RawActivationHooks(GramMatrixEstimator):
             module0, rows_X, rows_G, n_X, n_G, dev = next(e for e in eligible if e[0] is mods[0])
             resX, resG = run_pair(
                 dev,
-                lambda: self._damped_batch("X", mods, rows_X, out_dtype, then),
-                lambda: self._damped_batch("G", mods, rows_G, out_dtype, then),
+                lambda: self._damped_batch("X", mods, rows_X, out_dtype, then, want_inv),
+                lambda: self._damped_batch("G", mods, rows_G, out_dtype, then, want_inv),
                 b_first=n_G > n_X)
             for m, (R_X, fX, eX), (R_G, fG, eG) in zip(mods, resX, resG):
                 factors[m] = (R_X, R_G)

@@ -154,6 +154,26 @@ int ifk_fold_finalize_gram_batched(void* stream, int64_t batch, const void* cons
                             kappa_bound, workspace, workspace_bytes);
 }
 
+size_t ifk_fold_finalize_gram_inverse_workspace_size(int64_t batch, int64_t p, int64_t n,
+                                                     int64_t r_in) {
+  if (batch < 1 || p < 0 || n < 1 || r_in < 0 || r_in > n) return 0;
+  return fold_finalize_gram_inv_ws(batch, p, n, r_in);
+}
+
+int ifk_fold_finalize_gram_inverse(void* stream, int64_t batch, const void* const* X, int x_dtype,
+                                   int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
+                                   int64_t ldr, int64_t r_in, float scale, float damping,
+                                   void* out, int out_dtype, int64_t ldo, int64_t out_stride,
+                                   int32_t* status, float* kappa_bound, float* Z, int64_t ldz,
+                                   int64_t z_stride, void* Zb, void* ZTb, int64_t ldb,
+                                   int64_t b_stride, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(x_dtype) && dt_ok(out_dtype), "fold_finalize_gram_inverse: bad dtype");
+  GramInverse inv{Z, ldz, z_stride, (bf16_t*)Zb, (bf16_t*)ZTb, ldb, b_stride};
+  return fold_finalize_gram((hipStream_t)stream, batch, X, x_dtype, p, n, ldx, R_in, ldr, r_in,
+                            scale, damping, out, out_dtype, ldo, out_stride, MATH_BF16, status,
+                            kappa_bound, workspace, workspace_bytes, 1e-3f, &inv);
+}
+
 size_t ifk_tri_inverse_workspace_size(int64_t n) {
   if (n < 1) return 0;
   return trinv_ws(n);

@@ -326,6 +326,40 @@ __global__ void status_merge_batch_kernel(int* status, const int* flag, int64_t 
   if (b < batch && flag[b * fs] != 0) status[b] = 2;
 }
 
+// Diagonal block of the inverse: Z = alpha M on and above the diagonal (zero
+// below), its RNE bf16 copy Zb and the transposed copy ZT (zero above), a W x
+// W block of each; batch entry blockIdx.z at the element strides sm, sz, sb.
+// 32 x 32 tiles through LDS, so the transposed copy is written by rows too.
+__global__ __launch_bounds__(256) void diag_inverse_kernel(const float* M, int64_t ldm, int64_t W,
+                                                           float alpha, float* Z, int64_t ldz,
+                                                           bf16_t* Zb, bf16_t* ZT, int64_t ldb,
+                                                           int64_t sm, int64_t sz, int64_t sb) {
+  __shared__ float tile[32][33];
+  const int64_t e = blockIdx.z;
+  M += e * sm;
+  Z += e * sz;
+  Zb += e * sb;
+  ZT += e * sb;
+  const int tr = blockIdx.y, tc = blockIdx.x;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)tr * 32 + k, c = (int64_t)tc * 32 + tx;
+    float v = 0.0f;
+    if (r < W && c < W) {
+      if (c >= r) v = alpha * M[r * ldm + c];
+      Z[r * ldz + c] = v;
+      Zb[r * ldb + c] = f32_to_bf16(v);
+    }
+    tile[k][tx] = v;
+  }
+  __syncthreads();
+  // ZT's tile (tc, tr): ZT[r][c] = Z[c][r]
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)tc * 32 + k, c = (int64_t)tr * 32 + tx;
+    if (r < W && c < W) ZT[r * ldb + c] = f32_to_bf16(tile[tx][k]);
+  }
+}
+
 unsigned grid_of(int64_t work, int64_t cap = 2048) {
   int64_t g = cdiv(work, 256);
   if (g < 1) g = 1;
@@ -398,7 +432,7 @@ struct GramWs {
   float* dref;        // Gram diagonal (+ c^2), n
   float* G;           // symmetrised diagonal block, GB x GB; then M^T
   float* U;           // U_kk, GB x GB
-  float* M;           // U_kk^{-1}, GB x GB
+  float* Mh;          // U_kk^{-1} of every block k, at k GB^2 (nb GB x GB blocks)
   float* Zd;          // cholb's 64 x 64 diagonal inverses, GB x 64
   bf16_t* MT3[2];     // [M^T_hi | M^T_hi | M^T_lo], GB x 3 GB, by step parity
   bf16_t* ASb;        // [A_hi | A_lo | A_hi] of the band block, GB x 3 GB
@@ -409,13 +443,14 @@ struct GramWs {
   int* flag;          // one per entry, at int stride FLAG_S
   float* frob;        // per entry and Gram column, FROB_WG partial sums of squares (column 0's
                       // diagonal block in the extra set nb, its rows below in set 0)
-  int64_t sPT, sAw, sdref, sGB, sZd, sMT3, sLSb, sAS2, sL, sfrob;
+  bf16_t* Tinv;       // the inverse's doubling levels: n^2 / 4 bf16 (one entry at a time)
+  int64_t sPT, sAw, sdref, sGB, sMh, sZd, sMT3, sLSb, sAS2, sL, sfrob;
   SplitScratch sp, sp2, sp3;   // split-K partials of the three streams
   float tol;                   // relative pivot threshold of the pivot test
 };
 constexpr int64_t FLAG_S = 64;   // ints between two entries' flags (separate cache lines)
 
-void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w) {
+void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w, bool inv = false) {
   const int64_t nb = cdiv(n, GB);
   w.B = B;
   w.ldk = (int64_t)align_up((size_t)std::max<int64_t>(pe, 1), 8);
@@ -429,6 +464,7 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w) {
   w.sAw = al(n * w.lda);
   w.sdref = al(n);
   w.sGB = GB * GB;
+  w.sMh = nb * GB * GB;
   w.sZd = (GB / 64) * 64 * 64;
   w.sMT3 = multi ? GB * 3 * GB : 64;
   w.sLSb = multi ? GB * 4 * GB : 64;
@@ -440,7 +476,8 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w) {
   w.dref = a.take<float>((size_t)(B * w.sdref));
   w.G = a.take<float>((size_t)(B * w.sGB));
   w.U = a.take<float>((size_t)(B * w.sGB));
-  w.M = a.take<float>((size_t)(B * w.sGB));
+  w.Mh = a.take<float>((size_t)(B * w.sMh));
+  w.Tinv = inv ? a.take<bf16_t>((size_t)(n * n / 4 + 64)) : nullptr;
   w.Zd = a.take<float>((size_t)(B * w.sZd));
   for (int i = 0; i < 2; ++i) w.MT3[i] = a.take<bf16_t>((size_t)(B * w.sMT3));
   w.ASb = a.take<bf16_t>((size_t)(B * w.sMT3));
@@ -463,7 +500,7 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w) {
 // (cholb's diagonal workgroup, the band products) must find CUs free while
 // the Gram columns and the panel work run beside them.
 constexpr int GRAM_MAX_WGS = 192;
-constexpr int REST_MAX_WGS = 128;
+constexpr int REST_MAX_WGS = 192;
 
 struct Blk {
   int64_t r0, r1;   // rows / columns of block k
@@ -550,9 +587,12 @@ int chain_factor(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
   float* Akk = w.Aw + b.r0 * w.lda + b.r0;
   RC(sym_from_lower(s, B, Akk, w.lda, W, w.G, GB, w.sAw, w.sGB));
   CholbStrides cs;
-  cs.a = w.sGB; cs.u = w.sGB; cs.zd = w.sZd; cs.dref = w.sdref; cs.m = w.sGB; cs.flag = FLAG_S;
-  RC(launch_cholb(s, w.G, GB, (int)W, w.U, GB, w.Zd, w.dref + b.r0, w.tol, w.flag, w.M, GB,
+  cs.a = w.sGB; cs.u = w.sGB; cs.zd = w.sZd; cs.dref = w.sdref; cs.m = w.sMh; cs.flag = FLAG_S;
+  float* Mk = w.Mh + k * GB * GB;
+  RC(launch_cholb(s, w.G, GB, (int)W, w.U, GB, w.Zd, w.dref + b.r0, w.tol, w.flag, Mk, GB,
                   true, B, cs));
+  // cholb leaves M's blocks below the diagonal unset
+  for (int e = 0; e < B; ++e) RC(launch_zero_tri_blocks(s, Mk + e * w.sMh, 4, GB, W, true));
   return launch_transpose_cast(s, w.U, GB, W, W, Akk, DT_F32, w.lda, B, w.sGB, w.sAw);
 }
 
@@ -564,10 +604,7 @@ int chain_band(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
   const int64_t W = b.r1 - b.r0, W1 = b1.r1 - b1.r0;   // W == GB here
   const int B = (int)w.B;
   bf16_t* MT3 = w.MT3[k & 1];
-  // cholb leaves M's blocks below the diagonal unset
-  for (int e = 0; e < B; ++e)
-    RC(launch_zero_tri_blocks(s, w.M + e * w.sGB, 4, GB, W, true));
-  RC(launch_transpose_cast(s, w.M, GB, W, W, w.G, DT_F32, GB, B, w.sGB, w.sGB));
+  RC(launch_transpose_cast(s, w.Mh + k * GB * GB, GB, W, W, w.G, DT_F32, GB, B, w.sMh, w.sGB));
   SegStrides g3;
   g3.src = w.sGB; g3.dst = w.sMT3;
   RC(split_seg(s, B, w.G, GB, W, W, MT3, 3 * GB, 3, 0b100, g3));
@@ -626,7 +663,50 @@ int helper_step(hipStream_t s, GramWs& w, int64_t n, int64_t k, hipEvent_t gev_k
               per_entry(lower_part(out_f32(w.Aw + b2.r0 * lda + b2.r0, lda, w.sAw))), B, w.sp2, max_wgs);
 }
 
+// The inverse of the factor, Z = R^{-1}, and its bf16 copies, after the
+// factorisation: the diagonal blocks are Z_jj = M_j / scale from the chain's
+// M_j = U_jj^{-1} (U = L^T; the output R is scale U), and the block-doubling
+// levels Z12 = -Z11 (R12 Z22) of the bf16 triangular inverse start at width
+// GB instead of at its 64-column leaves.
+int inverse_clear(hipStream_t s, const GramInverse& o, int64_t n, int B) {
+  for (int e = 0; e < B; ++e) {
+    RC(launch_zero_tri_blocks(s, o.Z + e * o.sz, 4, o.ldz, n, true));
+    RC(launch_zero_tri_blocks(s, o.Zb + e * o.sb, 2, o.ldb, n, true));
+    RC(launch_zero_tri_blocks(s, o.ZT + e * o.sb, 2, o.ldb, n, false));
+  }
+  return IFK_OK;
+}
+
+int inverse_from_blocks(hipStream_t s, GramWs& w, int64_t n, float scale, const void* out,
+                        int odt, int64_t ldo, int64_t out_stride, const GramInverse& o) {
+  const int B = (int)w.B;
+  const int64_t nb = cdiv(n, GB);
+  RC(inverse_clear(s, o, n, B));
+  for (int64_t j = 0; j < nb; ++j) {
+    const Blk b = blk(j, n);
+    const int64_t W = b.r1 - b.r0, r = b.r0;
+    const dim3 grid((unsigned)cdiv(W, 32), (unsigned)cdiv(W, 32), (unsigned)B);
+    hipLaunchKernelGGL(diag_inverse_kernel, grid, dim3(256), 0, s, w.Mh + j * GB * GB, GB, W,
+                       1.0f / scale, o.Z + r * o.ldz + r, o.ldz, o.Zb + r * o.ldb + r,
+                       o.ZT + r * o.ldb + r, o.ldb, w.sMh, o.sz, o.sb);
+    RC(check_launch("diag_inverse"));
+  }
+  const size_t esz = odt == DT_F32 ? 4 : 2;
+  for (int e = 0; e < B; ++e)
+    RC(trinv_levels_t(s, (const char*)out + (size_t)e * out_stride * esz, odt, ldo, n, GB,
+                      o.Z + e * o.sz, o.ldz, o.ZT + e * o.sb, o.Zb + e * o.sb, o.ldb, w.Tinv,
+                      w.sp2));
+  return IFK_OK;
+}
+
 }  // namespace
+
+size_t fold_finalize_gram_inv_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in) {
+  Arena a(nullptr, 0);
+  GramWs w;
+  plan_gram(a, batch, r_in + p, n, w, true);
+  return a.used;
+}
 
 size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in) {
   Arena a(nullptr, 0);
@@ -639,13 +719,16 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
                        int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
                        int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
                        int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
-                       size_t ws_bytes, float pivot_tol) {
+                       size_t ws_bytes, float pivot_tol, const GramInverse* inv) {
   bool ok = n >= 1 && p >= 0 && r_in >= 0 && r_in <= n && batch >= 1 && batch <= 65535 &&
             (p == 0 || (X && ldx >= n)) && (r_in == 0 || (R_in && ldr >= n)) && out &&
             ldo >= n && out_stride >= n * ldo && scale > 0.0f && damping >= 0.0f &&
             (xdt == DT_F32 || xdt == DT_BF16) && (odt == DT_F32 || odt == DT_BF16) && status;
   for (int64_t e = 0; ok && e < batch; ++e)
     ok = (p == 0 || X[e]) && (r_in == 0 || R_in[e]);
+  if (ok && inv)
+    ok = inv->Z && inv->Zb && inv->ZT && inv->ldz >= n && inv->ldb >= n &&
+         (batch == 1 || (inv->sz >= n * inv->ldz && inv->sb >= n * inv->ldb));
   if (!ok) {
     set_error("fold_finalize_gram: invalid arguments");
     return IFK_ERR_INVALID;
@@ -663,7 +746,7 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   }
   Arena a(ws, ws_bytes);
   GramWs w;
-  plan_gram(a, batch, pe, n, w);
+  plan_gram(a, batch, pe, n, w, inv != nullptr);
   if (a.overflow) {
     set_error("fold_finalize_gram: workspace too small");
     return IFK_ERR_WORKSPACE;
@@ -718,9 +801,16 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
     HIPRC(hipEventRecord(la->ready[0], s), "fold_finalize_gram: event record failed");
     HIPRC(hipStreamWaitEvent(s3, la->ready[0], 0), "fold_finalize_gram: stream wait failed");
   }
-  // Gram columns in order on s3, each with its event (they depend on P^T only)
+  // Gram columns in order on s3, each with its event (they depend on P^T
+  // only).  The chain's first step goes right behind column 0's diagonal
+  // block: enqueued before the other columns, it does not wait for the host
+  // to launch them.
   RC(gram_column0_diag(s3, w, n, c2, have_rows, wg3));
-  if (la) HIPRC(hipEventRecord(la->tready[0], s3), "fold_finalize_gram: event record failed");
+  if (la) {
+    HIPRC(hipEventRecord(la->tready[0], s3), "fold_finalize_gram: event record failed");
+    HIPRC(hipStreamWaitEvent(s, la->tready[0], 0), "fold_finalize_gram: stream wait failed");
+  }
+  RC(chain_factor(s, w, n, 0));
   if (p > 0 && n > b0.r1) RC(x_cols(s3, b0.r1, n));
   RC(gram_column0_rest(s3, w, n, have_rows, wg3));
   if (la) HIPRC(hipEventRecord(la->col[0], s3), "fold_finalize_gram: event record failed");
@@ -734,10 +824,9 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   //   col[c]:        Gram column c done (s3)
   //   ready[k % 2]:  step k's band and diagonal update done (s -> s2)
   //   aready[k % 2]: helper step k done (s2 -> s, before step k + 1's band)
-  if (la) HIPRC(hipStreamWaitEvent(s, la->tready[0], 0), "fold_finalize_gram: stream wait failed");
   for (int64_t k = 0; k < nb; ++k) {
     const int kp = (int)(k & 1);
-    RC(chain_factor(s, w, n, k));
+    if (k > 0) RC(chain_factor(s, w, n, k));
     if (k + 1 >= nb) break;
     // the band of step k needs helper step k - 1 (column k's rows > k, and
     // column k + 1 updated by panels < k), which also frees MT3[k % 2]
@@ -766,6 +855,7 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   }
   RC(launch_fill_int(s, status, 1, B));
   RC(cast_lower_t(s, B, w.Aw, w.lda, n, scale, out, odt, ldo, status, w.sAw, out_stride));
+  if (inv) RC(inverse_from_blocks(s, w, n, scale, out, odt, ldo, out_stride, *inv));
   if (kappa_bound) {
     hipLaunchKernelGGL(kappa_bound_kernel, dim3((unsigned)B), dim3(256), 0, s, w.frob,
                        (int)w.sfrob, scale, damping, kappa_bound);

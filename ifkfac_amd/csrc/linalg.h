@@ -3,6 +3,7 @@
 // returns IFK_OK or a negative status with the message in get_error().
 #pragma once
 #include "common.h"
+#include "gemm.h"
 
 namespace ifk {
 
@@ -46,12 +47,25 @@ int fold_finalize_cqr(hipStream_t s, const void* X, int xdt, int64_t p, int64_t 
 // at once: X and R_in are host arrays of batch device pointers, entry b's
 // factor goes to out + b * out_stride, its status to status[b] and its bound
 // to kappa_bound[b].
+// With inv, also Z = R^{-1} and its RNE bf16 copies Zb = Z (upper) and
+// ZTb = Z^T (lower): diagonal GB-blocks from the chain's block inverses (of
+// the fp32 factor), the rest by the bf16 block-doubling levels on the output
+// factor (fold_finalize_gram_inv_ws workspace); entry b's at the element
+// strides sz, sb.
+struct GramInverse {
+  float* Z;
+  int64_t ldz, sz;
+  bf16_t *Zb, *ZT;
+  int64_t ldb, sb;
+};
 size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in);
+size_t fold_finalize_gram_inv_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in);
 int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int xdt, int64_t p,
                        int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
                        int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
                        int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
-                       size_t ws_bytes, float pivot_tol = 1e-3f);
+                       size_t ws_bytes, float pivot_tol = 1e-3f,
+                       const GramInverse* inv = nullptr);
 
 // The streaming fold by the Gram route (bf16 arithmetic): R (rows [0, r_in)
 // valid) <- the factor of [R[0:r_in]; X] when r_in + p >= n; *status 1 (R
@@ -66,6 +80,13 @@ int tsqr_fold_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, 
 size_t trinv_ws(int64_t n);
 int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,
           int math, int safe, void* ws, size_t ws_bytes);
+
+// The block-doubling levels of the bf16-arithmetic triangular inverse from
+// width w0 on, Z12 = -Z11 (R12 Z22): Z's (and Zb's, ZT's) diagonal w0-blocks
+// are given, the rest of their triangles is formed (tmpT: n^2 / 4 bf16).
+int trinv_levels_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int64_t w0,
+                   float* Z, int64_t ldz, bf16_t* ZT, bf16_t* Zb, int64_t ldb, bf16_t* tmpT,
+                   SplitScratch sp);
 
 // Z = R^{-1} in bf16 arithmetic, plus RNE bf16 copies Zb = Z and ZTb = Z^T
 // (row stride ldb, the other triangle zero) for precondition_apply_b.

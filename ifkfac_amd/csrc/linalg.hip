@@ -253,13 +253,15 @@ LookAhead* look_ahead(hipStream_t s, int* rc) {
 }
 
 int look_ahead_events(LookAhead* la, size_t n) {
-  while (la->col.size() < n) {
-    hipEvent_t e = nullptr;
-    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
-      set_error("look-ahead: cannot create an event");
-      return IFK_ERR_HIP;
+  for (std::vector<hipEvent_t>* v : {&la->col}) {
+    while (v->size() < n) {
+      hipEvent_t e = nullptr;
+      if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+        set_error("look-ahead: cannot create an event");
+        return IFK_ERR_HIP;
+      }
+      v->push_back(e);
     }
-    la->col.push_back(e);
   }
   return IFK_OK;
 }
@@ -1040,8 +1042,6 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
 static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
                         int64_t ldz, int safe, bf16_t* ZT, bf16_t* Zb, int64_t ldb, bool zero_zb,
                         bf16_t* tmpT, SplitScratch sp) {
-  const size_t esz = rdt == DT_F32 ? 4 : 2;
-  const char* Rc = (const char*)R;
   const int64_t NB = TRINV_NB;
   const int64_t n_ = ldb;   // row stride of both bf16 copies
   // every block on and above the diagonal of Z and Zb, and on and below it
@@ -1050,7 +1050,16 @@ static int trinv_core_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int6
   RC(launch_zero_tri_blocks(s, ZT, 2, n_, n, false));
   if (zero_zb) RC(launch_zero_tri_blocks(s, Zb, 2, n_, n, true));
   RC(launch_trinv_diag(s, R, rdt, ldr, n, NB, Z, ldz, safe, Zb, ZT, n_));
-  for (int64_t w = NB; w < n; w *= 2) {
+  return trinv_levels_t(s, R, rdt, ldr, n, NB, Z, ldz, ZT, Zb, ldb, tmpT, sp);
+}
+
+int trinv_levels_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, int64_t w0,
+                   float* Z, int64_t ldz, bf16_t* ZT, bf16_t* Zb, int64_t ldb, bf16_t* tmpT,
+                   SplitScratch sp) {
+  const size_t esz = rdt == DT_F32 ? 4 : 2;
+  const char* Rc = (const char*)R;
+  const int64_t n_ = ldb;   // row stride of both bf16 copies
+  for (int64_t w = w0; w < n; w *= 2) {
     const int64_t step = 2 * w;
     const int64_t nfull = n / step;
     if (nfull > 0) {

@@ -148,9 +148,17 @@ class IFKFAC(torch.optim.Optimizer):
         be = get_backend()
         copies = hasattr(be, "tri_inverse_bf16")
         split = hasattr(be, "precondition_apply_x3")
+        # bf16 factors in bf16 arithmetic: the Gram route forms each side's
+        # inverse beside its factorisation
+        fused_inverse = (copies and out_dtype == torch.bfloat16
+                         and solve_math_for(torch.bfloat16) == MATH_BF16)
 
-        def inverse(side, module, R, kappa_bound=None):
+        def inverse(side, module, R, kappa_bound=None, inv=None):
             m = solve_math_for(R.dtype)
+            if inv is not None and m == MATH_BF16:
+                # formed beside the Gram route's factorisation: the inverse of
+                # the fp32 factor before its bf16 rounding, and its bf16 copies
+                return inv[0], inv[1], inv[2], kappa_bound
             if m == MATH_BF16 and copies:
                 # bf16 arithmetic: keep the bf16 copies of Z and Z^T next to Z,
                 # so the per-step apply does not cast the inverses again.  The
@@ -167,7 +175,8 @@ class IFKFAC(torch.optim.Optimizer):
             # stream, so the narrower side's inverse runs while the wider one
             # is still being factored.
             new_factors, flags, early = self.hooks._collect_factors(
-                out_dtype, consume=True, then=None if blend else inverse)
+                out_dtype, consume=True, then=None if blend else inverse,
+                with_inverse=fused_inverse)
         except IFKFACRankError as e:
             logger.warning("IFKFAC: factor update skipped — %s", e)
             self.timing["factor_compute"].append(time.perf_counter() - t0)

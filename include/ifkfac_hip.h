@@ -191,6 +191,33 @@ int ifk_fold_finalize_gram_batched(void* stream, int64_t batch, const void* cons
                                    size_t workspace_bytes);
 
 /*
+ * ifk_fold_finalize_gram_batched together with the triangular inverse of each
+ * factor and its bf16 copies (replaces finalize_R, ifkfac/triangular.py:
+ * 386-421, and the solves of apply_vered on bf16 factors, triangular.py:
+ * 608-628, whose inverse ifk_tri_inverse_bf16 would otherwise form after the
+ * factor): Z = R^{-1} (fp32, upper, zero below) of the fp32 factor before the
+ * RNE rounding of `out`, Zb = bf16(Z) (upper, zero below) and ZTb = bf16(Z^T)
+ * (lower, zero above), the copies ifk_precondition_apply_bf16 reads.  Z's
+ * column blocks are formed beside the Cholesky chain from the diagonal
+ * blocks' inverses the chain forms anyway, in bf16 arithmetic with fp32
+ * accumulation as ifk_tri_inverse_bf16.  Entry b's Z at Z + b * z_stride
+ * (ld ldz), its copies at Zb / ZTb + b * b_stride (ld ldb, bf16 elements).
+ * The factor, status and kappa bound are bit for bit those of
+ * ifk_fold_finalize_gram_batched; where an entry's status is 2 its inverse
+ * is meaningless (the caller refactors that side and inverts it by
+ * ifk_tri_inverse_bf16).  bf16 arithmetic only (no math argument).
+ */
+size_t ifk_fold_finalize_gram_inverse_workspace_size(int64_t batch, int64_t p, int64_t n,
+                                                     int64_t r_in);
+int ifk_fold_finalize_gram_inverse(void* stream, int64_t batch, const void* const* X, int x_dtype,
+                                   int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
+                                   int64_t ldr, int64_t r_in, float scale, float damping,
+                                   void* out, int out_dtype, int64_t ldo, int64_t out_stride,
+                                   int32_t* status, float* kappa_bound, float* Z, int64_t ldz,
+                                   int64_t z_stride, void* Zb, void* ZTb, int64_t ldb,
+                                   int64_t b_stride, void* workspace, size_t workspace_bytes);
+
+/*
  * Triangular inverse Z = R^{-1} of an upper-triangular n x n factor (dtype
  * r_dtype) into fp32 Z (ldz).  The four solves of apply_vered are applied as
  * products with Z; this is the factor-side half of them.

@@ -98,18 +98,35 @@ class OracleBackend:
             return out, flag, torch.tensor([kb], dtype=torch.float32)
         return out, flag
 
-    def fold_finalize_gram_batched(self, Rs, r_in, Xs, scale, damping, out_dtype):
+    def fold_finalize_gram_batched(self, Rs, r_in, Xs, scale, damping, out_dtype,
+                                   with_inverse=False):
         """The batched Gram factor update, entry by entry (the batched launch gives
-        every entry the single call's bits)."""
+        every entry the single call's bits).  With ``with_inverse`` also the
+        inverse of each damped factor before its output rounding (fp64 here) and
+        its bf16 copies, as ifk_fold_finalize_gram_inverse."""
         self.calls["fold_finalize_gram_batched"] += 1
-        outs, sts, kbs = [], [], []
+        if with_inverse:
+            self.calls["fold_finalize_gram_inverse"] += 1
+        outs, sts, kbs, invs = [], [], [], []
         for e, X in enumerate(Xs):
-            o, s, k = self.fold_finalize(Rs[e] if Rs is not None else None, r_in, X, scale, damping,
-                                         out_dtype, 1, gram=True, with_kappa=True)
+            R = Rs[e] if Rs is not None else None
+            o, s, k = self.fold_finalize(R, r_in, X, scale, damping, out_dtype, 1, gram=True,
+                                         with_kappa=True)
             outs.append(o)
             sts.append(s)
             kbs.append(k)
-        return torch.stack(outs), torch.cat(sts), torch.cat(kbs)
+            if with_inverse:
+                old = None if r_in == 0 else _np(R[:r_in])
+                Rd = O.finalize_R(O.streaming_tsqr_update(old, _np(X)) * scale, damping)
+                Z = torch.from_numpy(np.linalg.inv(Rd)).float()
+                if int(s.item()) == 2:
+                    Z = torch.full_like(Z, float("nan"))
+                invs.append(Z)
+        if not with_inverse:
+            return torch.stack(outs), torch.cat(sts), torch.cat(kbs)
+        Z = torch.stack(invs)
+        return (torch.stack(outs), torch.cat(sts), torch.cat(kbs),
+                (Z, Z.bfloat16(), Z.transpose(1, 2).contiguous().bfloat16()))
 
     def tri_inverse(self, R, math):
         self.calls["tri_inverse"] += 1

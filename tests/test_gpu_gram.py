@@ -277,3 +277,47 @@ def test_tsqr_fold_gram_guards(hip):
         hip.fold_gram_(R, 10, torch.randn(50, 64, device=DEV), FOLD_TOL)
     with pytest.raises(Exception):   # tolerance outside (0, 1)
         hip.fold_gram_(R, 0, torch.randn(80, 64, device=DEV), 0.0)
+
+
+# ---------------------------------------------------------------------------
+# the inverse formed beside the factorisation (ifk_fold_finalize_gram_inverse)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,prev,p,n,odt", [
+    (1, 0, 500, 300, torch.bfloat16), (1, 0, 2000, 1500, torch.float32),
+    (1, 1200, 1200, 2100, torch.bfloat16), (1, 0, 4000, 3100, torch.bfloat16),
+    (1, 0, 6000, 5000, torch.float32), (3, 0, 2600, 2100, torch.bfloat16),
+    (2, 0, 4096, 4096, torch.bfloat16),
+])
+def test_fold_finalize_gram_inverse(hip, B, prev, p, n, odt):
+    """Factor, status and kappa bound bit for bit those of the call without the
+    inverse; Zb = bf16(Z) and ZT = bf16(Z^T) exactly with the other triangle zero;
+    ||R Z - I||_max, R the fp32 factor, at most twice that of ifk_tri_inverse_bf16
+    on the same R (both bf16 arithmetic) plus 1e-3."""
+    g = torch.Generator(device=DEV).manual_seed(B * 13 + n)
+    Xs = [(torch.randn(p, n, device=DEV, generator=g) * (1 + e)).to(torch.bfloat16)
+          for e in range(B)]
+    Rs, r = None, 0
+    if prev:
+        Rs = []
+        for e in range(B):
+            R, r = _fold_chunks(hip, [torch.randn(prev, n, device=DEV, generator=g)], n)
+            Rs.append(R)
+    rows = prev + p
+    out, st, kb, (Z, Zb, ZT) = hip.fold_finalize_gram_batched(Rs, r, Xs, 1 / math.sqrt(rows),
+                                                             1e-2, odt, with_inverse=True)
+    out0, st0, kb0 = hip.fold_finalize_gram_batched(Rs, r, Xs, 1 / math.sqrt(rows), 1e-2, odt)
+    assert torch.equal(out, out0) and torch.equal(st, st0) and torch.equal(kb, kb0)
+    R32, _, _ = hip.fold_finalize_gram_batched(Rs, r, Xs, 1 / math.sqrt(rows), 1e-2,
+                                               torch.float32)
+    eye = torch.eye(n, device=DEV, dtype=torch.float64)
+    for e in range(B):
+        assert st[e].item() == 1
+        assert torch.equal(Zb[e], Z[e].to(torch.bfloat16))
+        assert torch.equal(ZT[e], Z[e].t().contiguous().to(torch.bfloat16))
+        assert torch.count_nonzero(torch.tril(Z[e], -1)).item() == 0
+        Rd = R32[e].double()
+        err = (Rd @ Z[e].double() - eye).abs().max().item()
+        Zt, _, _ = hip.tri_inverse_bf16(R32[e])
+        err_t = (Rd @ Zt.double() - eye).abs().max().item()
+        print(f"B={B} n={n} entry {e}: ||R Z - I||_max {err:.3e} (tri_inverse_bf16 {err_t:.3e})")
+        assert err <= 2 * err_t + 1e-3

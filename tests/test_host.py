@@ -544,8 +544,9 @@ def test_chunks_fold_eagerly_between_updates(be):
 def test_bf16_update_batches_same_shape_layers(be):
     """A consuming bf16 factor update sends the layers whose X sides and G sides
     share a shape through one batched Gram call per side (three 12 -> 12 layers
-    here; the 12 -> 5 head goes alone), and every layer's factors are its own
-    closed form, as the per-layer path gives them."""
+    here; the 12 -> 5 head's sides go alone, as batches of one), every layer's
+    factors are its own closed form, as the per-layer path gives them, and each
+    side's inverse comes from the factor call (no separate triangular inverse)."""
     from ifkfac_amd import IFKFAC
     torch.manual_seed(0)
     model = nn.Sequential(nn.Linear(12, 12), nn.Tanh(), nn.Linear(12, 12), nn.Tanh(),
@@ -562,14 +563,22 @@ def test_bf16_update_batches_same_shape_layers(be):
     import io
     with contextlib.redirect_stdout(io.StringIO()):
         opt.step()
-    assert be.calls["fold_finalize_gram_batched"] == 2      # the X group and the G group
+    # the X group, the G group and the head's two sides
+    assert be.calls["fold_finalize_gram_batched"] == be.calls["fold_finalize_gram_inverse"] == 4
     assert be.calls["fold_finalize_gram"] == 2 * 3 + 2      # three batched entries per side + the head
+    assert be.calls["tri_inverse_bf16"] == 0
     for m in opt._factors:
         R_X, R_G = opt._factors[m]
         want_X = O.chol_factor([acts[m].double().numpy()], 48, lam)
         want_G = O.chol_factor([grads[m].double().numpy()], 48, lam)
         assert np.abs(R_X.double().numpy() - want_X).max() <= 4e-3 * np.abs(want_X).max()
         assert np.abs(R_G.double().numpy() - want_G).max() <= 4e-3 * np.abs(want_G).max()
+        # the fused inverse is that of the unrounded factor; a side whose kappa
+        # bound exceeds 1.5 is inverted again in fp32 from the stored bf16 factor
+        fused = max(opt._kappas[m]) <= 1.5
+        for Z, R, want in ((opt._inverses[m][0], R_X, want_X), (opt._inverses[m][1], R_G, want_G)):
+            ref = np.linalg.inv(want if fused else R.double().numpy())
+            assert np.abs(Z.double().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
     assert len(opt._factors) == 4
 
 
