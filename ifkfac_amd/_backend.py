@@ -188,8 +188,8 @@ class HipBackend:
         Returns (factors (B, n, n), status int32[B], kappa bound float32[B]); entry
         b is bitwise the single-side result.  With ``with_inverse``
         (ifk_fold_finalize_gram_inverse) a fourth value (Z fp32, Zb, ZT bf16, each
-        (B, n, n)): the inverse of each fp32 factor and its bf16 copies, formed
-        beside the factorisation (meaningless where the status is 2)."""
+        (B, n, n)): each factor's inverse and its bf16 copies, from the Cholesky's
+        1024-block inverses (meaningless where the status is 2)."""
         B = len(Xs)
         mats = [_mat(X, "fold_finalize_gram_batched") for X in Xs]
         X0, ldx, xdt = mats[0]

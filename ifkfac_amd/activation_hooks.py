@@ -264,8 +264,8 @@ class RawActivationHooks(GramMatrixEstimator):
         kappa_2 of the factor; without a held chunk its input is the running
         factor), CholeskyQR2 outer blocks in fp32 arithmetic; its flag may
         then be 2 (see _retry_cholesky_qr).  With ``with_inverse`` the Gram
-        route also forms the factor's inverse and its bf16 copies beside the
-        factorisation (a fourth value (Z, Zb, ZT), else None)."""
+        route also forms the factor's inverse and its bf16 copies in the same
+        call (a fourth value (Z, Zb, ZT), else None)."""
         R, r, chunk, _ = self._side_state(side, module)
         be = get_backend()
         gram = fast and self.math == MATH_BF16
@@ -384,8 +384,8 @@ class RawActivationHooks(GramMatrixEstimator):
         that depends on one side only starts while the other is still being
         factored); its results come back as the third value, per module as
         (X side, G side), or None without ``then``.  With ``with_inverse`` a
-        side factored by the Gram route comes with its inverse, formed beside
-        the factorisation: ``then`` is then called with ``inv=(Z, Zb, ZT)``."""
+        side factored by the Gram route comes with its inverse, formed by
+        the same call: ``then`` is then called with ``inv=(Z, Zb, ZT)``."""
         if self.deferred:
             self._drain_deferred()
         if not consume:

@@ -148,16 +148,16 @@ class IFKFAC(torch.optim.Optimizer):
         be = get_backend()
         copies = hasattr(be, "tri_inverse_bf16")
         split = hasattr(be, "precondition_apply_x3")
-        # bf16 factors in bf16 arithmetic: the Gram route forms each side's
-        # inverse beside its factorisation
+        # bf16 factors in bf16 arithmetic: the Gram route's call forms each
+        # side's inverse as well
         fused_inverse = (copies and out_dtype == torch.bfloat16
                          and solve_math_for(torch.bfloat16) == MATH_BF16)
 
         def inverse(side, module, R, kappa_bound=None, inv=None):
             m = solve_math_for(R.dtype)
             if inv is not None and m == MATH_BF16:
-                # formed beside the Gram route's factorisation: the inverse of
-                # the fp32 factor before its bf16 rounding, and its bf16 copies
+                # formed by the Gram route's call from the Cholesky's 1024-block
+                # inverses, with its bf16 copies
                 return inv[0], inv[1], inv[2], kappa_bound
             if m == MATH_BF16 and copies:
                 # bf16 arithmetic: keep the bf16 copies of Z and Z^T next to Z,

@@ -195,12 +195,13 @@ int ifk_fold_finalize_gram_batched(void* stream, int64_t batch, const void* cons
  * factor and its bf16 copies (replaces finalize_R, ifkfac/triangular.py:
  * 386-421, and the solves of apply_vered on bf16 factors, triangular.py:
  * 608-628, whose inverse ifk_tri_inverse_bf16 would otherwise form after the
- * factor): Z = R^{-1} (fp32, upper, zero below) of the fp32 factor before the
- * RNE rounding of `out`, Zb = bf16(Z) (upper, zero below) and ZTb = bf16(Z^T)
- * (lower, zero above), the copies ifk_precondition_apply_bf16 reads.  Z's
- * column blocks are formed beside the Cholesky chain from the diagonal
- * blocks' inverses the chain forms anyway, in bf16 arithmetic with fp32
- * accumulation as ifk_tri_inverse_bf16.  Entry b's Z at Z + b * z_stride
+ * factor): Z = R^{-1} (fp32, upper, zero below), Zb = bf16(Z) (upper, zero
+ * below) and ZTb = bf16(Z^T) (lower, zero above), the copies
+ * ifk_precondition_apply_bf16 reads.  Z's diagonal 1024-blocks are the
+ * inverses of the fp32 factor's diagonal blocks, which the blocked Cholesky
+ * forms anyway; the rest comes from the block-doubling levels of
+ * ifk_tri_inverse_bf16 on `out` (bf16 arithmetic, fp32 accumulation), which
+ * start at width 1024 instead of at its 64-column leaves.  Entry b's Z at Z + b * z_stride
  * (ld ldz), its copies at Zb / ZTb + b * b_stride (ld ldb, bf16 elements).
  * The factor, status and kappa bound are bit for bit those of
  * ifk_fold_finalize_gram_batched; where an entry's status is 2 its inverse
