@@ -549,6 +549,15 @@ class HipBackend:
         _lib.check(rc, "ifk_precondition_bias")
         return out
 
+    def release_stream_state(self, device, stream=None) -> None:
+        """Free the helper streams and events the library keeps for (device,
+        stream) -- the current stream by default (ifk_release_stream_state)."""
+        dev = torch.device(device)
+        with torch.cuda.device(dev):
+            st = stream if stream is not None else torch.cuda.current_stream(dev)
+            rc = self.lib.ifk_release_stream_state(ctypes.c_void_p(st.cuda_stream))
+        _lib.check(rc, "ifk_release_stream_state")
+
     def momentum_update_(self, nat: torch.Tensor, buf: Optional[torch.Tensor], W: torch.Tensor,
                          lr: float, momentum: float, weight_decay: float, buf_init: bool) -> None:
         _require_device(W, "momentum_update")

@@ -8,6 +8,7 @@
 #include "gemm.h"
 #include "kernels.h"
 #include "linalg.h"
+#include "lookahead.h"
 
 namespace ifk {
 
@@ -172,6 +173,10 @@ int ifk_fold_finalize_gram_inverse(void* stream, int64_t batch, const void* cons
   return fold_finalize_gram((hipStream_t)stream, batch, X, x_dtype, p, n, ldx, R_in, ldr, r_in,
                             scale, damping, out, out_dtype, ldo, out_stride, MATH_BF16, status,
                             kappa_bound, workspace, workspace_bytes, 1e-3f, &inv);
+}
+
+int ifk_release_stream_state(void* stream) {
+  return look_ahead_release((hipStream_t)stream);
 }
 
 size_t ifk_tri_inverse_workspace_size(int64_t n) {

@@ -219,9 +219,10 @@ static void plan_cqr(Arena& a, int64_t pe, CqrWs& q) {
 
 // One helper stream per (device, calling stream): folds issued on different
 // streams (the two sides of a layer) keep independent far updates.
+static std::mutex g_mu;
+static std::map<std::pair<int, hipStream_t>, LookAhead*> g_la;
+
 LookAhead* look_ahead(hipStream_t s, int* rc) {
-  static std::mutex g_mu;
-  static std::map<std::pair<int, hipStream_t>, LookAhead*> g_la;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     set_error("tsqr_fold: hipGetDevice failed");
@@ -250,6 +251,42 @@ LookAhead* look_ahead(hipStream_t s, int* rc) {
   }
   *rc = IFK_OK;
   return la;
+}
+
+int look_ahead_release(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("release_stream_state: hipGetDevice failed");
+    return IFK_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> g(g_mu);
+  auto it = g_la.find(std::make_pair(dev, s));
+  if (it == g_la.end()) return IFK_OK;
+  LookAhead* la = it->second;
+  g_la.erase(it);
+  if (!la) return IFK_OK;
+  bool ok = true;
+  {
+    std::lock_guard<std::mutex> l(la->mu);
+    // the helpers' queued work, and the calling stream's waits on their
+    // events, must finish before the streams and events go
+    for (hipStream_t h : {la->s2, la->s3, s})
+      if (h) ok = hipStreamSynchronize(h) == hipSuccess && ok;
+    for (hipEvent_t e : la->col)
+      if (e) ok = hipEventDestroy(e) == hipSuccess && ok;
+    for (hipEvent_t e : {la->done, la->ready[0], la->ready[1], la->nearwp[0], la->nearwp[1],
+                         la->fall[0], la->fall[1], la->tready[0], la->tready[1], la->aready[0],
+                         la->aready[1]})
+      if (e) ok = hipEventDestroy(e) == hipSuccess && ok;
+    for (hipStream_t h : {la->s2, la->s3})
+      if (h) ok = hipStreamDestroy(h) == hipSuccess && ok;
+  }
+  delete la;
+  if (!ok) {
+    set_error("release_stream_state: a helper stream or event could not be released");
+    return IFK_ERR_HIP;
+  }
+  return IFK_OK;
 }
 
 int look_ahead_events(LookAhead* la, size_t n) {

@@ -28,6 +28,11 @@ struct LookAhead {
 // failure).  Sets live until the process ends.
 LookAhead* look_ahead(hipStream_t s, int* rc);
 
+// Destroy the set of the current device and calling stream s, after the
+// queued work of s and of its helper streams (no set: nothing to do).  Not concurrently with
+// a factorisation on s.
+int look_ahead_release(hipStream_t s);
+
 // At least n per-column events in la->col (the caller holds la->mu).
 int look_ahead_events(LookAhead* la, size_t n);
 

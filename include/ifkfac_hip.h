@@ -49,6 +49,18 @@ int ifk_abi_version(void);
 const char* ifk_last_error(void);
 
 /*
+ * Release the helper streams and events that the factorisations of more than
+ * 1024 columns create for (current device, calling stream) on first use and
+ * otherwise keep until the process ends.  No counterpart in the reference
+ * (torch manages its own streams): it is for callers that create many
+ * calling streams over a process's life.  Waits for the stream's and its
+ * helpers' queued work; a later factorisation on the stream creates them
+ * again.  Not to be called while another host thread issues a factorisation
+ * on the same stream.  A stream with no such state: nothing to do, 0.
+ */
+int ifk_release_stream_state(void* stream);
+
+/*
  * Streaming TSQR fold -- replaces streaming_tsqr_update(running_R, new_chunk)
  * (ifkfac/triangular.py:246-307) as called from the hooks
  * (ifkfac/activation_hooks.py:579, :642).

@@ -321,3 +321,24 @@ def test_fold_finalize_gram_inverse(hip, B, prev, p, n, odt):
         err_t = (Rd @ Zt.double() - eye).abs().max().item()
         print(f"B={B} n={n} entry {e}: ||R Z - I||_max {err:.3e} (tri_inverse_bf16 {err_t:.3e})")
         assert err <= 2 * err_t + 1e-3
+
+
+def test_release_stream_state(hip):
+    """ifk_release_stream_state: a stream's helper set released between two
+    factorisations of more than 1024 columns (three streams and their events)
+    gives the second the same bits; releasing a stream with no set, or twice,
+    is a no-op."""
+    g = torch.Generator(device=DEV).manual_seed(41)
+    X = torch.randn(4000, 3100, device=DEV, generator=g).to(torch.bfloat16)
+    st_ = torch.cuda.Stream()
+    with torch.cuda.stream(st_):
+        a, s1 = hip.fold_finalize(None, 0, X, 1 / math.sqrt(4000), 1e-2, torch.bfloat16, 1,
+                                  gram=True)
+        hip.release_stream_state(DEV, st_)
+        hip.release_stream_state(DEV, st_)
+        b, s2 = hip.fold_finalize(None, 0, X, 1 / math.sqrt(4000), 1e-2, torch.bfloat16, 1,
+                                  gram=True)
+        hip.release_stream_state(DEV, st_)
+    torch.cuda.synchronize()
+    assert s1.item() == s2.item() == 1 and torch.equal(a, b)
+    hip.release_stream_state(DEV, torch.cuda.Stream())
