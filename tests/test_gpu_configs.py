@@ -7,7 +7,9 @@ damping dominates X^T X / p) and kappa-exposed (X scaled by sqrt(p) and
 damping 0.1 / kappa^2, so kappa(R_damped) ~ kappa), both orientations, the
 factor update IFKFAC times: fold_finalize by the Gram matrix + blocked
 Cholesky (the panel path for a side whose status is 2) -> tri_inverse_bf16 ->
-the bf16 apply.
+the bf16 apply, and the chain IFKFAC runs where both sides take the Gram
+route: the factor with its inverse from ifk_fold_finalize_gram_inverse ->
+the bf16 apply, held to the same bounds.
 Bounds, each on its own part of the error:
   factor    ||R^T R - (X^T X / p + lam I)||_F / ||.||_F <= 4 kappa(R) eps_bf16
             (vacuous) and <= 5e-3 (measured at most 2.2e-3): the bf16 rounding
@@ -154,6 +156,19 @@ def test_linear_4096_11008_kappa_sweep_timed_chain(hip, n_in, n_out, kappa, expo
         assert e_truth <= 2e-2
     else:
         assert e_truth <= e_ref + 2e-2
+    if sx0 == 1 and sg0 == 1:
+        # the factor and its inverse from one call, as IFKFAC takes them
+        inv = []
+        for T, Fm in ((Xb, FX), (Db, FG)):
+            out, st, _, (Z, Zb, ZT) = hip.fold_finalize_gram_batched(
+                None, 0, [T], 1 / math.sqrt(p), lam, torch.bfloat16, with_inverse=True)
+            assert st.item() == 1 and torch.equal(out[0], Fm)
+            inv.append((Zb[0], ZT[0]))
+        nat_f = hip.precondition_apply_bf16(grad, inv[0], inv[1])
+        e_fs, e_ft = rel(nat_f, stored), rel(nat_f, truth)
+        print(f"  with the inverse from the factor call: solve {e_fs:.2e}, vs closed form {e_ft:.2e}")
+        assert e_fs <= 2e-2
+        assert e_ft <= (2e-2 if not exposed else e_ref + 2e-2)
 
 
 @pytest.mark.parametrize("side", ["X", "G"])
