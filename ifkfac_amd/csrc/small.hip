@@ -147,38 +147,50 @@ __device__ inline float safe_divisor(float d) {
 // steps); mode 1: the pivot rule of cholesky_bf16, clamp_min(pivot, 1e-7)
 // with a NaN pivot kept NaN.
 //
-// Right-looking, blocked by CB columns.  Wave 0 factors each CB-row panel
-// with lane c holding column c of the panel rows in registers: at step k
-// the pivot and row k's entries come from their lanes by readlane, so the
-// diagonal block's factor and the block row's forward substitution are one
-// sweep with no LDS traffic or barrier on the pivot chain.  The rank-CB
-// trailing update runs on fp32 MFMA across the four waves.  Two barriers per
-// panel.  CB = 32 measured fastest (the pivot chain, not the FMA count,
-// bounds a panel, so fewer panels and barriers win).
+// One wave holds the upper triangle in registers, as three 32 x 32 blocks
+// (00, 01, 11) in the fp32 MFMA 32x32 result layout: lane l holds column
+// l % 32 of a block, register j its row 8 (j / 4) + 4 (l / 32) + j % 4.  So
+// the four rows 4p .. 4p + 3 of a panel sit in four consecutive registers of
+// one half of the lanes, across every block of their block row.  Each panel
+// is factored on the VALU (its pivots come by readlane, its rows are scaled
+// and the later panel rows updated lane = column), then applied to the
+// trailing blocks as two rank-2 products on fp32 MFMA, whose operands are the
+// panel rows with one row moved to the other half of the lanes
+// (v_permlane32_swap) and everything left of the panel's end masked to zero.
+// The other waves only meet the two barriers.  (CB is kept for the callers'
+// spelling; the panel is four rows.)
 template <int CB = 32, bool EXACT = false>
 __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode,
                                           const float* dref = nullptr, int b = SB) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
+  const int lane = t & 63, wave = t >> 6, l32 = lane & 31, h = lane >> 5;
   __shared__ float dgs[SB];   // reference diagonal of the pivot test
   if (t < SB) dgs[t] = (dref != nullptr && t < b) ? dref[t] : A[t * SLD + t];
   __syncthreads();
-  int flag = 0;
-#pragma unroll 1
-  for (int kb = 0; kb < SB / CB; ++kb) {
-    const int o = kb * CB;
-    if (wave == 0) {
-      // a[i] = entry (o + i, lane); only lanes >= o + i hold upper-triangle
-      // entries, and only those are broadcast or stored as results
-      float a[CB];
+  if (wave == 0) {
+    f32x16 b00, b01, b11;
 #pragma unroll
-      for (int i = 0; i < CB; ++i) a[i] = (lane >= o) ? A[(o + i) * SLD + lane] : 0.0f;
+    for (int j = 0; j < 16; ++j) {
+      const int r = (j >> 2) * 8 + h * 4 + (j & 3);
+      b00[j] = (r <= l32) ? A[r * SLD + l32] : 0.0f;
+      b01[j] = A[r * SLD + 32 + l32];
+      b11[j] = (r <= l32) ? A[(32 + r) * SLD + 32 + l32] : 0.0f;
+    }
+    int flag = 0;
 #pragma unroll
-      for (int k = 0; k < CB; ++k) {
-        const float piv = bcast(a[k], o + k);
+    for (int p = 0; p < 16; ++p) {
+      const int K = p >> 3;                 // block row of the panel
+      const int hk = p & 1;                 // the half of the lanes holding its rows
+      const int jb = ((p & 7) >> 1) * 4;    // and their registers jb .. jb + 3
+      const bool mine = h == hk;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int k = 4 * p + q, kk = k & 31, reg = jb + q;
+        const float piv = bcast(K == 0 ? b00[reg] : b11[reg], kk + 32 * hk);
         float rs, dg;
         if (mode == 0) {
-          if (!(piv > tol * dgs[o + k]) || !isfinite(piv)) flag = 1;
+          if (!(piv > tol * dgs[k]) || !isfinite(piv)) flag = 1;
           const float pv = fmaxf(piv, 1e-30f);
           if (EXACT) {
             // correctly rounded: a first pass whose second pass cannot carry
@@ -196,53 +208,68 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
           dg = sqrtf((piv >= 1e-7f || piv != piv) ? piv : 1e-7f);
           rs = 1.0f / dg;
         }
-        a[k] = (lane == o + k) ? dg : a[k] * rs;
-#pragma unroll
-        for (int i = k + 1; i < CB; ++i) a[i] = fmaf(-bcast(a[k], o + i), a[k], a[i]);
-      }
-      if (lane >= o) {
-#pragma unroll
-        for (int i = 0; i < CB; ++i) A[(o + i) * SLD + lane] = a[i];
-      }
-    }
-    __syncthreads();
-    const int lo = o + CB;
-    if (lo < SB) {
-      typedef float f32x16 __attribute__((ext_vector_type(16)));
-      const int q0 = (wave >> 1) * 32, q1 = (wave & 1) * 32;
-      if (wave != 2 && q0 + 31 >= lo && q1 + 31 >= lo) {
-        const int l32 = lane & 31, h = lane >> 5;
-        const int r = q0 + l32, cc = q1 + l32;
-        float av[CB / 2], bv[CB / 2];
-#pragma unroll
-        for (int s2 = 0; s2 < CB / 2; ++s2) {
-          const int k = o + (CB / 2) * h + s2;
-          av[s2] = (r >= lo) ? A[k * SLD + r] : 0.0f;
-          bv[s2] = (cc >= lo) ? A[k * SLD + cc] : 0.0f;
+        // row k of U: its half's lanes of every block in block row K
+        if (K == 0) {
+          b00[reg] = mine ? ((l32 == kk) ? dg : b00[reg] * rs) : b00[reg];
+          b01[reg] = mine ? b01[reg] * rs : b01[reg];
+        } else {
+          b11[reg] = mine ? ((l32 == kk) ? dg : b11[reg] * rs) : b11[reg];
         }
-        float cur[16];
+        // the panel's later rows
 #pragma unroll
-        for (int i = 0; i < 16; ++i) cur[i] = A[(q0 + (i >> 2) * 8 + h * 4 + (i & 3)) * SLD + cc];
-        f32x16 dd;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) dd[i] = 0.0f;
-#pragma unroll
-        for (int s2 = 0; s2 < CB / 2; ++s2)
-          dd = __builtin_amdgcn_mfma_f32_32x32x2f32(av[s2], bv[s2], dd, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int row = q0 + (i >> 2) * 8 + h * 4 + (i & 3);
-          if (row >= lo && cc >= row) A[row * SLD + cc] = cur[i] - dd[i];
+        for (int q2 = q + 1; q2 < 4; ++q2) {
+          const int r2 = jb + q2;
+          const float c = bcast(K == 0 ? b00[reg] : b11[reg], ((4 * p + q2) & 31) + 32 * hk);
+          if (K == 0) {
+            b00[r2] = mine ? fmaf(-c, b00[reg], b00[r2]) : b00[r2];
+            b01[r2] = mine ? fmaf(-c, b01[reg], b01[r2]) : b01[r2];
+          } else {
+            b11[r2] = mine ? fmaf(-c, b11[reg], b11[r2]) : b11[r2];
+          }
         }
       }
-      __syncthreads();
+      if (p == 15) break;
+      // the panel applied to rows and columns from pend on: two rank-2 products
+      const int pend = 4 * p + 4;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int r0 = jb + 2 * s2, r1 = r0 + 1;
+        // lane l: row 4p + 2 s2 (l < 32) or the next row (l >= 32) of the
+        // panel at column colbase + l % 32, zero left of pend
+        auto opnd = [&](float x0, float x1, int colbase) -> float {
+          float v;
+          if (hk == 0) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x1),
+                                                             __float_as_uint(x1), false, false);
+            v = h == 0 ? x0 : __uint_as_float(sw[0]);
+          } else {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0),
+                                                             __float_as_uint(x0), false, false);
+            v = h == 0 ? __uint_as_float(sw[1]) : x1;
+          }
+          return (colbase + l32 >= pend) ? v : 0.0f;
+        };
+        if (K == 0) {
+          const float u0 = opnd(b00[r0], b00[r1], 0), u1 = opnd(b01[r0], b01[r1], 32);
+          if (pend < 32) b00 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, u0, b00, 0, 0, 0);
+          b01 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, u1, b01, 0, 0, 0);
+          b11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, u1, b11, 0, 0, 0);
+        } else {
+          const float u1 = opnd(b11[r0], b11[r1], 32);
+          b11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, u1, b11, 0, 0, 0);
+        }
+      }
     }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = (j >> 2) * 8 + h * 4 + (j & 3);
+      A[r * SLD + l32] = (r <= l32) ? b00[j] : 0.0f;
+      A[r * SLD + 32 + l32] = b01[j];
+      A[(32 + r) * SLD + l32] = 0.0f;
+      A[(32 + r) * SLD + 32 + l32] = (r <= l32) ? b11[j] : 0.0f;
+    }
+    if (flag && bad) *bad = 1;
   }
-  for (int e = t; e < SB * SB; e += SNT) {
-    const int r = e >> 6, cc = e & 63;
-    if (r > cc) A[r * SLD + cc] = 0.0f;
-  }
-  if (wave == 0 && flag && bad) *bad = 1;
   __syncthreads();
 }
 
