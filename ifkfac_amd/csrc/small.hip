@@ -178,6 +178,7 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
       b11[j] = (r <= l32) ? A[(32 + r) * SLD + 32 + l32] : 0.0f;
     }
     int flag = 0;
+    const float dgv = dgs[lane];            // the reference diagonal, lane k holding k's
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
       const int K = p >> 3;                 // block row of the panel
@@ -190,7 +191,7 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
         const float piv = bcast(K == 0 ? b00[reg] : b11[reg], kk + 32 * hk);
         float rs, dg;
         if (mode == 0) {
-          if (!(piv > tol * dgs[k]) || !isfinite(piv)) flag = 1;
+          if (!(piv > tol * bcast(dgv, k)) || !isfinite(piv)) flag = 1;
           const float pv = fmaxf(piv, 1e-30f);
           if (EXACT) {
             // correctly rounded: a first pass whose second pass cannot carry
