@@ -159,9 +159,15 @@ __device__ inline float safe_divisor(float d) {
 // (v_permlane32_swap) and everything left of the panel's end masked to zero.
 // The other waves only meet the two barriers.  (CB is kept for the callers'
 // spelling; the panel is four rows.)
-template <int CB = 32, bool EXACT = false>
+//
+// With INV, Z (LDS, stride SLD) also receives U^{-1}: the same row operations
+// applied to the identity give W = U^{-T} (lower triangular; blocks 00, 10,
+// 11 in the same layout, updated by the same pivots, scalings and rank-2
+// products), stored transposed.
+template <int CB = 32, bool EXACT = false, bool INV = false>
 __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode,
-                                          const float* dref = nullptr, int b = SB) {
+                                          const float* dref = nullptr, int b = SB,
+                                          float* Z = nullptr) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6, l32 = lane & 31, h = lane >> 5;
@@ -176,6 +182,16 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
       b00[j] = (r <= l32) ? A[r * SLD + l32] : 0.0f;
       b01[j] = A[r * SLD + 32 + l32];
       b11[j] = (r <= l32) ? A[(32 + r) * SLD + 32 + l32] : 0.0f;
+    }
+    f32x16 w00, w10, w11;   // W = U^{-T}, from the identity
+    if (INV) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = (j >> 2) * 8 + h * 4 + (j & 3);
+        w00[j] = (r == l32) ? 1.0f : 0.0f;
+        w10[j] = 0.0f;
+        w11[j] = (r == l32) ? 1.0f : 0.0f;
+      }
     }
     int flag = 0;
     const float dgv = dgs[lane];            // the reference diagonal, lane k holding k's
@@ -213,8 +229,13 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
         if (K == 0) {
           b00[reg] = mine ? ((l32 == kk) ? dg : b00[reg] * rs) : b00[reg];
           b01[reg] = mine ? b01[reg] * rs : b01[reg];
+          if (INV) w00[reg] = mine ? w00[reg] * rs : w00[reg];
         } else {
           b11[reg] = mine ? ((l32 == kk) ? dg : b11[reg] * rs) : b11[reg];
+          if (INV) {
+            w10[reg] = mine ? w10[reg] * rs : w10[reg];
+            w11[reg] = mine ? w11[reg] * rs : w11[reg];
+          }
         }
         // the panel's later rows
 #pragma unroll
@@ -224,8 +245,13 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
           if (K == 0) {
             b00[r2] = mine ? fmaf(-c, b00[reg], b00[r2]) : b00[r2];
             b01[r2] = mine ? fmaf(-c, b01[reg], b01[r2]) : b01[r2];
+            if (INV) w00[r2] = mine ? fmaf(-c, w00[reg], w00[r2]) : w00[r2];
           } else {
             b11[r2] = mine ? fmaf(-c, b11[reg], b11[r2]) : b11[r2];
+            if (INV) {
+              w10[r2] = mine ? fmaf(-c, w10[reg], w10[r2]) : w10[r2];
+              w11[r2] = mine ? fmaf(-c, w11[reg], w11[r2]) : w11[r2];
+            }
           }
         }
       }
@@ -237,17 +263,18 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
         const int r0 = jb + 2 * s2, r1 = r0 + 1;
         // lane l: row 4p + 2 s2 (l < 32) or the next row (l >= 32) of the
         // panel at column colbase + l % 32, zero left of pend
-        auto opnd = [&](float x0, float x1, int colbase) -> float {
-          float v;
+        auto pair = [&](float x0, float x1) -> float {
           if (hk == 0) {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x1),
                                                              __float_as_uint(x1), false, false);
-            v = h == 0 ? x0 : __uint_as_float(sw[0]);
-          } else {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0),
-                                                             __float_as_uint(x0), false, false);
-            v = h == 0 ? __uint_as_float(sw[1]) : x1;
+            return h == 0 ? x0 : __uint_as_float(sw[0]);
           }
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0),
+                                                           __float_as_uint(x0), false, false);
+          return h == 0 ? __uint_as_float(sw[1]) : x1;
+        };
+        auto opnd = [&](float x0, float x1, int colbase) -> float {
+          const float v = pair(x0, x1);
           return (colbase + l32 >= pend) ? v : 0.0f;
         };
         if (K == 0) {
@@ -255,9 +282,20 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
           if (pend < 32) b00 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, u0, b00, 0, 0, 0);
           b01 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, u1, b01, 0, 0, 0);
           b11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, u1, b11, 0, 0, 0);
+          if (INV) {
+            // rows >= pend of W take the panel's rows of W (columns <= k)
+            const float v0 = pair(w00[r0], w00[r1]);
+            if (pend < 32) w00 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, v0, w00, 0, 0, 0);
+            w10 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v0, w10, 0, 0, 0);
+          }
         } else {
           const float u1 = opnd(b11[r0], b11[r1], 32);
           b11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, u1, b11, 0, 0, 0);
+          if (INV) {
+            const float v0 = pair(w10[r0], w10[r1]), v1 = pair(w11[r0], w11[r1]);
+            w10 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v0, w10, 0, 0, 0);
+            w11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v1, w11, 0, 0, 0);
+          }
         }
       }
     }
@@ -268,6 +306,13 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
       A[r * SLD + 32 + l32] = b01[j];
       A[(32 + r) * SLD + l32] = 0.0f;
       A[(32 + r) * SLD + 32 + l32] = (r <= l32) ? b11[j] : 0.0f;
+      if (INV) {
+        // Z = W^T: W's element (row, col) goes to Z[col][row]
+        Z[l32 * SLD + r] = (r >= l32) ? w00[j] : 0.0f;
+        Z[l32 * SLD + 32 + r] = w10[j];
+        Z[(32 + l32) * SLD + r] = 0.0f;
+        Z[(32 + l32) * SLD + 32 + r] = (r >= l32) ? w11[j] : 0.0f;
+      }
     }
     if (flag && bad) *bad = 1;
   }
@@ -766,7 +811,6 @@ __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_
   }
   __shared__ float sC[SB * SLD];
   __shared__ float sZ[SB * SLD];
-  __shared__ float sT[TRINV_TMP];
   __shared__ int bad;
   const int t = threadIdx.x;
   const int b0 = n < SB ? n : SB;
@@ -777,10 +821,10 @@ __global__ __launch_bounds__(SNT) void cholb_first_kernel(const float* A, int64_
   ld_blk(v, A, lda, b0, b0, 1.0f);
   st_pad(sC, v);
   __syncthreads();
-  // block 0: its diagonal on entry is A's (or the given reference)
-  sm_chol64(sC, tol, &bad, 0, dref_in ? dref : nullptr, b0);
+  // block 0: its diagonal on entry is A's (or the given reference); its
+  // inverse alongside
+  sm_chol64<32, false, true>(sC, tol, &bad, 0, dref_in ? dref : nullptr, b0, sZ);
   st_blk(sC, U, ldu, b0, b0);
-  sm_trinv64(sC, sZ, sT);
   for (int e = t; e < SB * SB; e += SNT) {
     const int r = e >> 6, c = e & 63;
     Zd[e] = sZ[r * SLD + c];
@@ -803,7 +847,6 @@ __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, 
   __shared__ float sA[SB * SLD];
   __shared__ float sB[SB * SLD];
   __shared__ float sC[SB * SLD];
-  __shared__ float sT[TRINV_TMP];
   __shared__ int bad;
   const int t = threadIdx.x;
   const int nb = (n + SB - 1) / SB;
@@ -898,9 +941,8 @@ __global__ __launch_bounds__(SNT) void cholb_step_kernel(float* A, int64_t lda, 
   if (diag) st_blk(sA, U + (int64_t)SB * k * ldu + SB * j, ldu, SB, bj);
   sm_gemm64<true, false>(sA, diag ? sA : sB, sC, -1.0f, true);    // A_ij -= U_ki^T U_kj
   if (diag && i == k + 1) {
-    sm_chol64(sC, tol, &bad, 0, dref + SB * i, bi);
+    sm_chol64<32, false, true>(sC, tol, &bad, 0, dref + SB * i, bi, sZ);
     st_blk(sC, U + (int64_t)SB * i * ldu + SB * i, ldu, bi, bi);
-    sm_trinv64(sC, sZ, sT);
     for (int e = t; e < SB * SB; e += SNT)
       Zd[(size_t)i * SB * SB + e] = sZ[(e >> 6) * SLD + (e & 63)];
     if (t == 0 && bad) *flag = 1;
