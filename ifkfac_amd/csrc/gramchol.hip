@@ -326,6 +326,36 @@ __global__ void status_merge_batch_kernel(int* status, const int* flag, int64_t 
   if (b < batch && flag[b * fs] != 0) status[b] = 2;
 }
 
+// MT3 (W x 3 GB bf16, row stride ld3) = [hi(M^T) | hi(M^T) | lo(M^T)] for the
+// upper-triangular M (W x W, ldm; entries below its diagonal read as zero),
+// hi = RNE(x), lo = RNE(x - hi); batch entry blockIdx.z at the strides sm,
+// s3.  32 x 32 tiles through LDS.
+__global__ __launch_bounds__(256) void mt3_kernel(const float* M, int64_t ldm, int64_t W,
+                                                  bf16_t* MT3, int64_t ld3, int64_t sm,
+                                                  int64_t s3) {
+  __shared__ float tile[32][33];
+  M += (int64_t)blockIdx.z * sm;
+  MT3 += (int64_t)blockIdx.z * s3;
+  const int tr = blockIdx.y, tc = blockIdx.x;   // output tile (row block of M^T)
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  // M's tile (tc, tr) is the output tile transposed
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)tc * 32 + k, c = (int64_t)tr * 32 + tx;
+    tile[k][tx] = (r < W && c < W && r <= c) ? M[r * ldm + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int64_t r = (int64_t)tr * 32 + k, c = (int64_t)tc * 32 + tx;
+    if (r >= W || c >= W) continue;
+    const float x = tile[tx][k];
+    const bf16_t hi = f32_to_bf16(x), lo = f32_to_bf16(x - bf16_to_f32(hi));
+    bf16_t* o = MT3 + r * ld3 + c;
+    o[0] = hi;
+    o[GB] = hi;
+    o[2 * GB] = lo;
+  }
+}
+
 // Diagonal block of the inverse: Z = alpha M on and above the diagonal (zero
 // below), its RNE bf16 copy Zb and the transposed copy ZT (zero above), a W x
 // W block of each; batch entry blockIdx.z at the element strides sm, sz, sb.
@@ -589,11 +619,20 @@ int chain_factor(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
   CholbStrides cs;
   cs.a = w.sGB; cs.u = w.sGB; cs.zd = w.sZd; cs.dref = w.sdref; cs.m = w.sMh; cs.flag = FLAG_S;
   float* Mk = w.Mh + k * GB * GB;
+  // (cholb leaves M's blocks below the diagonal unset; their readers take
+  // the upper triangle only)
   RC(launch_cholb(s, w.G, GB, (int)W, w.U, GB, w.Zd, w.dref + b.r0, w.tol, w.flag, Mk, GB,
                   true, B, cs));
-  // cholb leaves M's blocks below the diagonal unset
-  for (int e = 0; e < B; ++e) RC(launch_zero_tri_blocks(s, Mk + e * w.sMh, 4, GB, W, true));
   return launch_transpose_cast(s, w.U, GB, W, W, Akk, DT_F32, w.lda, B, w.sGB, w.sAw);
+}
+
+// ASb = [A_hi | A_lo | A_hi] of block (k + 1, k), the band product's operand.
+int split_band(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
+  const Blk b = blk(k, n), b1 = blk(k + 1, n);
+  SegStrides a3;
+  a3.src = w.sAw; a3.dst = w.sMT3;
+  return split_seg(s, (int)w.B, w.Aw + b1.r0 * w.lda + b.r0, w.lda, b1.r1 - b1.r0, b.r1 - b.r0,
+                   w.ASb, 3 * GB, 3, 0b010, a3);
 }
 
 // Chain, part 2 of step k (block k + 1 exists): M^T split into MT3[k % 2];
@@ -604,14 +643,14 @@ int chain_band(hipStream_t s, GramWs& w, int64_t n, int64_t k) {
   const int64_t W = b.r1 - b.r0, W1 = b1.r1 - b1.r0;   // W == GB here
   const int B = (int)w.B;
   bf16_t* MT3 = w.MT3[k & 1];
-  RC(launch_transpose_cast(s, w.Mh + k * GB * GB, GB, W, W, w.G, DT_F32, GB, B, w.sMh, w.sGB));
-  SegStrides g3;
-  g3.src = w.sGB; g3.dst = w.sMT3;
-  RC(split_seg(s, B, w.G, GB, W, W, MT3, 3 * GB, 3, 0b100, g3));
+  const dim3 tg((unsigned)cdiv(W, 32), (unsigned)cdiv(W, 32), (unsigned)B);
+  hipLaunchKernelGGL(mt3_kernel, tg, dim3(256), 0, s, w.Mh + k * GB * GB, GB, W, MT3, 3 * GB,
+                     w.sMh, w.sMT3);
+  RC(check_launch("mt3"));
   float* Ab = w.Aw + b1.r0 * w.lda + b.r0;   // block (k + 1, k)
-  SegStrides a3;
-  a3.src = w.sAw; a3.dst = w.sMT3;
-  RC(split_seg(s, B, Ab, w.lda, W1, W, w.ASb, 3 * GB, 3, 0b010, a3));
+  // the band's split copy: helper step k - 1 made it (as soon as the block
+  // was final), step 0 makes its own
+  if (k == 0) RC(split_band(s, w, n, 0));
   RC(gemm(s, MATH_BF16, W1, W, 3 * W, 1.0f, A_n(w.ASb, DT_BF16, 3 * GB, TRI_NONE, w.sMT3),
           B_t(MT3, DT_BF16, 3 * GB, TRI_NONE, w.sMT3), 0.0f, per_entry(out_f32(Ab, w.lda, w.sAw)), B,
           w.sp));
@@ -654,6 +693,8 @@ int helper_step(hipStream_t s, GramWs& w, int64_t n, int64_t k, hipEvent_t gev_k
           A_n(w.LA + b2.r0 * ldl + k0, DT_BF16, ldl, TRI_NONE, w.sL),
           B_t(w.LB + b1.r0 * ldl + k0, DT_BF16, ldl, TRI_NONE, w.sL), 1.0f,
           per_entry(out_f32(w.Aw + b2.r0 * lda + b1.r0, lda, w.sAw)), B, w.sp2, max_wgs));
+  // block (k + 2, k + 1) is final: the next band's split copy, off the chain
+  RC(split_band(s, w, n, k + 1));
   // column k + 2 by panels 0 .. k
   if (gev_k2) HIPRC(hipStreamWaitEvent(s, gev_k2, 0), "fold_finalize_gram: stream wait failed");
   const int64_t W2 = b2.r1 - b2.r0;
