@@ -87,9 +87,10 @@ struct SplitScratch {
 
 // Launch profiler (see gemm.hip).  variant: gemm_variant_id() (bit 5 set for
 // the large-tile bf16 kernels, bit 6 as well for the direct-to-LDS one, bit 7
-// for its 128 x 128 tile), -2 all, -3 all of the register-staged 256 x 128
-// kernel, -4 all of the 128 x 128 kernel, -5 / -6 all of the direct-to-LDS
-// kernel with its 256 / 128 tile, -1 off.
+// for its 128 x 128 tile, bit 8 for a product run by hipBLASLt), -2 all, -3
+// all of the register-staged 256 x 128 kernel, -4 all of the 128 x 128
+// kernel, -5 / -6 all of the direct-to-LDS kernel with its 256 / 128 tile, -7
+// all hipBLASLt products, -1 off.
 int gemm_variant_id(int math, int adt, bool akc, int bdt, bool bkc);
 int profile_begin(int variant);
 int profile_end(int64_t* n_launches);
@@ -98,8 +99,21 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
 
 // max_wgs > 0 caps the number of workgroups of a large-tile launch (tiles are
 // then visited grid-stride), leaving CUs free for work on other streams.
+// Plain large bf16 products (both operands K-contiguous, neither triangular,
+// an fp32 result only) go to hipBLASLt (libgemm.hip), one call per batch
+// entry, uncapped; the environment variable IFK_GEMM_LIB=0 keeps them on the
+// engine's kernels.
 int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
          const MatRef& A, const MatRef& B, float beta, const OutRef& C, int batch,
          SplitScratch scratch, int max_wgs = 0);
+
+// hipBLASLt (libgemm.hip): C (fp32, M x N, ldc) = alpha A B^T + beta C for
+// bf16 A (M x K, lda) and B (N x K, ldb), row-major, one entry.
+bool lib_gemm_enabled();
+int lib_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                  bool beta_nz, size_t ws_bytes);
+int lib_gemm_bf16_nt(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha,
+                     const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, float beta,
+                     float* C, int64_t ldc, void* ws, size_t ws_bytes);
 
 }  // namespace ifk

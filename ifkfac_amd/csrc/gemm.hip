@@ -83,19 +83,20 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
 // register-staged kernel (bit 5), 2 / 3 the direct-to-LDS kernel with its 256
 // / 128 tile (bits 5 and 6, and bit 7 for the 128 tile).
 static int gemm_family(int vid) {
+  if ((vid >> 8) & 1) return 4;
   if ((vid >> 6) & 1) return ((vid >> 7) & 1) ? 3 : 2;
   return (vid >> 5) & 1;
 }
 
-// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 / -6
-// every launch of family 1 / 0 / 2 / 3.
+// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 / -6 /
+// -7 every launch of family 1 / 0 / 2 / 3 / 4 (hipBLASLt).
 static ProfRec* prof_slot(int vid) {
   const int a = g_prof_variant;
   if (a == -1) return nullptr;
   if (a >= 0 && a != vid) return nullptr;
   const int fam = gemm_family(vid);
   if ((a == -3 && fam != 1) || (a == -4 && fam != 0) || (a == -5 && fam != 2) ||
-      (a == -6 && fam != 3))
+      (a == -6 && fam != 3) || (a == -7 && fam != 4))
     return nullptr;
   std::lock_guard<std::mutex> g(g_prof_mu);
   if (g_prof_used == g_prof.size()) {
@@ -521,6 +522,34 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   const bool bb = big && A.dt == DT_BF16 && A.kc && B.dt == DT_BF16 && B.kc && p.vec_a &&
                   p.vec_b && K % 8 == 0 && A.ld < ((int64_t)1 << 21) &&
                   B.ld < ((int64_t)1 << 21);
+  // plain products: hipBLASLt, entry by entry (every entry gets the bits a
+  // batch of one gets)
+  if (bb && A.tri == TRI_NONE && B.tri == TRI_NONE && C.c && !C.cb && lib_gemm_enabled()) {
+    const size_t wsb = scratch.p ? scratch.floats * sizeof(float) : 0;
+    if (lib_gemm_plan(M, N, K, A.ld, B.ld, C.ldc, beta != 0.0f, wsb)) {
+      const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | (1 << 8);
+      ProfRec* pr = prof_slot(vid);
+      if (pr) {
+        pr->variant = vid;
+        pr->m = M;
+        pr->n = N;
+        pr->k = K;
+        pr->flops = 2.0 * (double)M * (double)N * (double)K * batch;
+        pr->bytes = ((double)M * K * 2 + (double)K * N * 2 +
+                     (double)M * N * (beta != 0.0f ? 8.0 : 4.0)) * batch;
+        hipEventRecord(pr->beg, s);
+      }
+      for (int e = 0; e < batch; ++e) {
+        const int rc = lib_gemm_bf16_nt(
+            s, M, N, K, alpha, (const bf16_t*)A.p + (size_t)e * A.bstride, A.ld,
+            (const bf16_t*)B.p + (size_t)e * B.bstride, B.ld, beta, C.c + (size_t)e * C.bstride,
+            C.ldc, scratch.p, wsb);
+        if (rc) return rc;
+      }
+      if (pr) hipEventRecord(pr->end, s);
+      return IFK_OK;
+    }
+  }
   // batch entries the tile and split-K choices are made for
   const int64_t bdec = C.per_entry ? 1 : batch;
   // split-K factor for a tile of TM x TN with BK-deep slabs

@@ -531,6 +531,14 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w, bool inv =
 // the Gram columns and the panel work run beside them.
 constexpr int GRAM_MAX_WGS = 192;
 constexpr int REST_MAX_WGS = 192;
+// Gram column c >= GRAM_LEAD starts only when helper step c - GRAM_LEAD is
+// done.  Unthrottled, the Gram stream runs far ahead of the chain and holds
+// its CUs for the whole first half of the factorisation, while the helper's
+// panel work -- which the chain waits for -- gets what is left; throttled,
+// the Gram columns stay a few blocks ahead of where the helper needs them
+// (helper step k waits for column k + 2, so the lead must be at least 3).
+constexpr int64_t GRAM_LEAD = 4;
+static_assert(GRAM_LEAD >= 3, "helper step k must find column k + 2 enqueued");
 
 struct Blk {
   int64_t r0, r1;   // rows / columns of block k
@@ -855,7 +863,10 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   if (p > 0 && n > b0.r1) RC(x_cols(s3, b0.r1, n));
   RC(gram_column0_rest(s3, w, n, have_rows, wg3));
   if (la) HIPRC(hipEventRecord(la->col[0], s3), "fold_finalize_gram: event record failed");
-  for (int64_t c = 1; c < nb; ++c) {
+  // the columns before the lead (all of them without helper streams); the
+  // rest are enqueued in the loop below, each behind its helper step
+  const int64_t c_pre = la ? std::min<int64_t>(nb, GRAM_LEAD) : nb;
+  for (int64_t c = 1; c < c_pre; ++c) {
     RC(gram_column(s3, w, n, c, c2, have_rows, wg3));
     if (la) HIPRC(hipEventRecord(la->col[c], s3), "fold_finalize_gram: event record failed");
   }
@@ -886,6 +897,14 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
       RC(helper_step(s2, w, n, k, la ? la->col[k + 2] : nullptr,
                      (la && k == 0) ? la->col[1] : nullptr, wg2));
       if (la) HIPRC(hipEventRecord(la->aready[kp], s2), "fold_finalize_gram: event record failed");
+      // Gram column k + GRAM_LEAD behind helper step k (every column >=
+      // GRAM_LEAD comes here: k + 2 < nb holds for k = c - GRAM_LEAD)
+      const int64_t c = k + GRAM_LEAD;
+      if (la && c < nb) {
+        HIPRC(hipStreamWaitEvent(s3, la->aready[kp], 0), "fold_finalize_gram: stream wait failed");
+        RC(gram_column(s3, w, n, c, c2, have_rows, wg3));
+        HIPRC(hipEventRecord(la->col[c], s3), "fold_finalize_gram: event record failed");
+      }
     }
   }
   if (la) {

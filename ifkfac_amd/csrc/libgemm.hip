@@ -1,0 +1,150 @@
+// Plain bf16 products through hipBLASLt, the vendor GEMM library:
+//   C (fp32, row-major M x N, ldc) = alpha * A B^T + beta * C,
+//   A (bf16, M x K, lda) and B (bf16, N x K, ldb) with K contiguous.
+// The engine's dispatcher (gemm.hip) sends here the products that are plain
+// in this sense -- no triangular operand, no bf16 copy of the result -- which
+// are the Gram columns of a factor update and its panel and band updates:
+// for those narrow, long-K shapes (an 11008 x 1024 output at K = 16384) the
+// library's tuned kernels run at over twice the rate of the direct-to-LDS
+// kernel.  Products with a triangular operand keep the engine's kernels,
+// which skip the zero half.
+//
+// Row-major C = A B^T is the column-major product C^T = B^T-op(B_cm) A_cm:
+// the library's "A" is our B viewed column-major (K x N, ld ldb) used
+// transposed, its "B" is our A (K x M, ld lda) used as is, and C^T is N x M
+// with ld ldc.  One plan per (device, shape, strides, beta != 0, workspace):
+// the descriptors and the heuristic's first algorithm, made once under a
+// lock and kept for the process (each a few hundred bytes of host memory).
+// The workspace is the caller's split-K scratch of the same stream.
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "common.h"
+#include "gemm.h"
+
+namespace ifk {
+
+namespace {
+
+struct LtKey {
+  int dev;
+  int64_t m, n, k, lda, ldb, ldc;
+  int beta_nz;
+  size_t ws;
+  bool operator<(const LtKey& o) const {
+    return std::tie(dev, m, n, k, lda, ldb, ldc, beta_nz, ws) <
+           std::tie(o.dev, o.m, o.n, o.k, o.lda, o.ldb, o.ldc, o.beta_nz, o.ws);
+  }
+};
+
+struct LtPlan {
+  bool ok = false;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo;
+  size_t ws = 0;
+};
+
+std::mutex g_lt_mu;
+std::map<int, hipblasLtHandle_t> g_lt_handle;
+std::map<LtKey, LtPlan> g_lt_plan;
+
+// the plan for a key (made on first use); null handle when the library
+// cannot be initialised on this device
+const LtPlan* lt_plan(const LtKey& key, hipblasLtHandle_t* h) {
+  std::lock_guard<std::mutex> lock(g_lt_mu);
+  auto hi = g_lt_handle.find(key.dev);
+  if (hi == g_lt_handle.end()) {
+    hipblasLtHandle_t nh = nullptr;
+    if (hipblasLtCreate(&nh) != HIPBLAS_STATUS_SUCCESS) nh = nullptr;
+    hi = g_lt_handle.emplace(key.dev, nh).first;
+  }
+  *h = hi->second;
+  if (!*h) return nullptr;
+  auto it = g_lt_plan.find(key);
+  if (it != g_lt_plan.end()) return &it->second;
+  LtPlan pl;
+  bool ok = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) ==
+            HIPBLAS_STATUS_SUCCESS;
+  const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+  ok = ok && hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT,
+                                             sizeof(opT)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN,
+                                             sizeof(opN)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&pl.la, HIP_R_16BF, (uint64_t)key.k, (uint64_t)key.n,
+                                         key.ldb) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&pl.lb, HIP_R_16BF, (uint64_t)key.k, (uint64_t)key.m,
+                                         key.lda) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&pl.lc, HIP_R_32F, (uint64_t)key.n, (uint64_t)key.m,
+                                         key.ldc) == HIPBLAS_STATUS_SUCCESS;
+  if (ok) {
+    hipblasLtMatmulPreference_t pref = nullptr;
+    ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+    const uint64_t wsb = key.ws;
+    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
+                                                     &wsb, sizeof(wsb)) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int count = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(*h, pl.desc, pl.la, pl.lb, pl.lc, pl.lc, pref, 1,
+                                               res, &count) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && count >= 1 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= key.ws;
+    if (ok) {
+      pl.algo = res[0].algo;
+      pl.ws = res[0].workspaceSize;
+    }
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  }
+  pl.ok = ok;
+  return &g_lt_plan.emplace(key, pl).first->second;
+}
+
+}  // namespace
+
+bool lib_gemm_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("IFK_GEMM_LIB");
+    return !(e && std::strcmp(e, "0") == 0);
+  }();
+  return on;
+}
+
+int lib_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                  bool beta_nz, size_t ws_bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  hipblasLtHandle_t h = nullptr;
+  const LtPlan* pl = lt_plan(LtKey{dev, M, N, K, lda, ldb, ldc, beta_nz ? 1 : 0, ws_bytes}, &h);
+  return (pl && pl->ok) ? 1 : 0;
+}
+
+int lib_gemm_bf16_nt(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha,
+                     const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, float beta,
+                     float* C, int64_t ldc, void* ws, size_t ws_bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("gemm: no current device");
+    return IFK_ERR_HIP;
+  }
+  hipblasLtHandle_t h = nullptr;
+  const LtPlan* pl =
+      lt_plan(LtKey{dev, M, N, K, lda, ldb, ldc, beta != 0.0f ? 1 : 0, ws_bytes}, &h);
+  if (!pl || !pl->ok) {
+    set_error("gemm: hipBLASLt has no algorithm for this product");
+    return IFK_ERR_INVALID;
+  }
+  const hipblasStatus_t st = hipblasLtMatmul(h, pl->desc, &alpha, B, pl->la, A, pl->lb, &beta, C,
+                                             pl->lc, C, pl->lc, &pl->algo, pl->ws ? ws : nullptr,
+                                             pl->ws, s);
+  if (st != HIPBLAS_STATUS_SUCCESS) {
+    set_error("gemm: hipblasLtMatmul failed");
+    return IFK_ERR_HIP;
+  }
+  return IFK_OK;
+}
+
+}  // namespace ifk

@@ -466,14 +466,15 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
 /*
  * Measurement support (no counterpart in the reference; used by bench.py).
  * ifk_profile_begin(v) arms the GEMM launch profiler for GEMM variant v
- * (v = (mid << 7) | (direct << 6) | (large_tile << 5) | (math << 4) |
+ * (v = (lib << 8) | (mid << 7) | (direct << 6) | (large_tile << 5) | (math << 4) |
  * (a_dtype << 3) | (a_k_contiguous << 2) | (b_dtype << 1) | b_k_contiguous;
  * large_tile marks the bf16 kernels with the large tiles, direct the one that
  * loads operands straight into LDS, gemm_bb_kernel, and mid its 128 x 128
- * tile; large_tile alone gemm_big_kernel, neither gemm_kernel), for every
- * variant with v = -2, for every launch of gemm_big_kernel with v = -3, of
- * gemm_kernel with v = -4, of gemm_bb_kernel with its 256 x 256 tile with
- * v = -5 and with its 128 x 128 tile with v = -6; v = -1 disarms.
+ * tile; large_tile alone gemm_big_kernel, neither gemm_kernel; lib a plain
+ * bf16 product run by hipBLASLt), for every variant with v = -2, for every
+ * launch of gemm_big_kernel with v = -3, of gemm_kernel with v = -4, of
+ * gemm_bb_kernel with its 256 x 256 tile with v = -5 and with its 128 x 128
+ * tile with v = -6, of hipBLASLt with v = -7; v = -1 disarms.
  * Each armed launch is bracketed by two HIP events on its own stream.
  * ifk_profile_end() disarms, waits for the events and returns the number of
  * launches recorded; ifk_profile_get(i, ...) returns launch i's variant,
