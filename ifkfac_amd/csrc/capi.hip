@@ -462,6 +462,8 @@ int ifk_profile_begin(int variant) { return profile_begin(variant); }
 
 int ifk_profile_end(int64_t* n_launches) { return profile_end(n_launches); }
 
+int ifk_set_gemm_library(int on) { return lib_gemm_set(on); }
+
 int ifk_profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
                     int64_t* n, int64_t* k) {
   GUARD(variant && ms && flops && bytes && m && n && k, "profile_get: null pointer");

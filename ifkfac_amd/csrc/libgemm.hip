@@ -18,6 +18,7 @@
 // The workspace is the caller's split-K scratch of the same stream.
 #include <hipblaslt/hipblaslt.h>
 
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -105,12 +106,24 @@ const LtPlan* lt_plan(const LtKey& key, hipblasLtHandle_t* h) {
 
 }  // namespace
 
+// -1: not yet read from the environment; then 0 / 1
+static std::atomic<int> g_lib_on{-1};
+
 bool lib_gemm_enabled() {
-  static const bool on = [] {
+  int v = g_lib_on.load(std::memory_order_relaxed);
+  if (v < 0) {
     const char* e = std::getenv("IFK_GEMM_LIB");
-    return !(e && std::strcmp(e, "0") == 0);
-  }();
-  return on;
+    int want = (e && std::strcmp(e, "0") == 0) ? 0 : 1;
+    g_lib_on.compare_exchange_strong(v, want);
+    v = g_lib_on.load(std::memory_order_relaxed);
+  }
+  return v != 0;
+}
+
+int lib_gemm_set(int on) {
+  const int prev = lib_gemm_enabled() ? 1 : 0;
+  g_lib_on.store(on ? 1 : 0, std::memory_order_relaxed);
+  return prev;
 }
 
 int lib_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,

@@ -482,6 +482,18 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
  */
 int ifk_profile_begin(int variant);
 int ifk_profile_end(int64_t* n_launches);
+
+/*
+ * No counterpart in the reference (measurement and test support).
+ * ifk_set_gemm_library(on) chooses where the plain bf16 products (both
+ * operands K-contiguous, neither triangular, an fp32 result: the Gram route's
+ * Gram columns and panel and band updates) run for the calls enqueued after
+ * it: on = 1 hipBLASLt (the default; the environment variable IFK_GEMM_LIB=0
+ * makes 0 the default), on = 0 this library's own kernels.  Returns the
+ * previous setting.  Process-wide; results agree within rounding (the
+ * summation order differs), not bit for bit.
+ */
+int ifk_set_gemm_library(int on);
 int ifk_profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
                     int64_t* n, int64_t* k);
 

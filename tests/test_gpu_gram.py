@@ -342,3 +342,41 @@ def test_release_stream_state(hip):
     torch.cuda.synchronize()
     assert s1.item() == s2.item() == 1 and torch.equal(a, b)
     hip.release_stream_state(DEV, torch.cuda.Stream())
+
+
+def test_gram_route_plain_products_library_and_own_kernels(hip):
+    """The Gram route's plain products (Gram columns, band and panel updates) run on
+    hipBLASLt by default and on this library's kernels after
+    ifk_set_gemm_library(0): both factors meet the closed-form bound, agree with
+    each other to the same bound (the summation order differs, so not bit for bit),
+    and the launch profiler sees hipBLASLt calls only in the first run."""
+    import ctypes
+    from ifkfac_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=DEV).manual_seed(29)
+    p, n = 4000, 3100
+    X = torch.randn(p, n, device=DEV, generator=g).to(torch.bfloat16)
+    Xd = _bf16_np(X)
+    Ro = np.linalg.cholesky(Xd.T @ Xd / p + 1e-2 * np.eye(n)).T
+    out, calls = {}, {}
+    prev = lib.ifk_set_gemm_library(1)
+    try:
+        for on in (1, 0):
+            lib.ifk_set_gemm_library(on)
+            torch.cuda.synchronize()
+            _lib.check(lib.ifk_profile_begin(-7), "profile_begin")
+            R, st = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), 1e-2, torch.float32, 1,
+                                      gram=True)
+            torch.cuda.synchronize()
+            cnt = ctypes.c_int64(0)
+            _lib.check(lib.ifk_profile_end(ctypes.byref(cnt)), "profile_end")
+            assert int(st.reshape(-1)[0].item()) == 1
+            out[on], calls[on] = R.double().cpu().numpy(), cnt.value
+    finally:
+        lib.ifk_set_gemm_library(prev)
+    print(f"hipBLASLt calls {calls[1]} / {calls[0]}; closed form {_gram_rel(out[1], Ro):.2e} / "
+          f"{_gram_rel(out[0], Ro):.2e}; mutual {_gram_rel(out[1], out[0]):.2e}")
+    assert calls[1] > 0 and calls[0] == 0
+    for on in (1, 0):
+        assert _gram_rel(out[on], Ro) <= 3e-5
+    assert _gram_rel(out[1], out[0]) <= 6e-5
