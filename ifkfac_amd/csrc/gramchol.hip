@@ -528,7 +528,10 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w, bool inv =
 
 // Workgroup caps of the helper streams' products: the chain's launches
 // (cholb's diagonal workgroup, the band products) must find CUs free while
-// the Gram columns and the panel work run beside them.
+// the Gram columns and the panel work run beside them.  They bind the
+// engine's own kernels only: the plain products that the GEMM dispatcher
+// sends to hipBLASLt (all of this file's large products, unless that is
+// switched off) launch their own grids.
 constexpr int GRAM_MAX_WGS = 192;
 constexpr int REST_MAX_WGS = 192;
 // Gram column c >= GRAM_LEAD starts only when helper step c - GRAM_LEAD is
