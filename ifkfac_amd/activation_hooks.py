@@ -42,28 +42,14 @@ def fold_chunk(buf: torch.Tensor, r_in: int, chunk: torch.Tensor, math_: int) ->
     the Gram matrix and the blocked Cholesky (about 3x faster than the panel
     fold); the status read waits for that fold only, and a fold the Gram route
     refuses left buf as it was for the panel fold."""
-    return fold_chunk_route(buf, r_in, chunk, math_)[0]
-
-
-def fold_chunk_route(buf: torch.Tensor, r_in: int, chunk: torch.Tensor, math_: int,
-                     try_gram: bool = True):
-    """fold_chunk, also returning whether the Gram route refused the fold;
-    ``try_gram=False`` goes to the panel fold at once (same factor)."""
     be = get_backend()
     n = buf.shape[1]
-    if try_gram and math_ == MATH_BF16 and r_in + chunk.shape[0] >= n:
+    if math_ == MATH_BF16 and r_in + chunk.shape[0] >= n:
         if int(be.fold_gram_(buf, r_in, chunk, GRAM_FOLD_TOL).item()) == 1:
-            return n, False
+            return n
         logger.debug("fold of %d rows into a %d-column factor: Gram route refused, panel fold",
                      chunk.shape[0], n)
-        return be.fold_(buf, r_in, chunk, math_), True
-    return be.fold_(buf, r_in, chunk, math_), False
-
-
-# After the Gram route refuses a side's fold, that side's next folds go to the
-# panel fold at once (their data are likely as ill-conditioned): the refused
-# attempt costs a Gram matrix and a Cholesky on top of the panel fold.
-GRAM_RETRY_AFTER = 4
+    return be.fold_(buf, r_in, chunk, math_)
 
 
 class IFKFACRankError(RuntimeError):
@@ -119,8 +105,6 @@ class RawActivationHooks(GramMatrixEstimator):
         self._enabled = False
         self._R_X: Dict[nn.Module, Optional[torch.Tensor]] = {}
         self._R_G: Dict[nn.Module, Optional[torch.Tensor]] = {}
-        # folds left before a side refused by the Gram route tries it again
-        self._gram_skip: Dict[Tuple[str, nn.Module], int] = {}
         self._n_rows_X: Dict[nn.Module, int] = {}
         self._n_rows_G: Dict[nn.Module, int] = {}
         self._pending_X: Dict[nn.Module, List[torch.Tensor]] = {}
@@ -225,10 +209,7 @@ class RawActivationHooks(GramMatrixEstimator):
             r_in = cur.shape[0]
             if cur.data_ptr() != buf.data_ptr():
                 buf[:r_in].copy_(cur)
-        key = (side, module)
-        skip = self._gram_skip.get(key, 0)
-        r_new, refused = fold_chunk_route(buf, r_in, chunk, self.math, try_gram=skip == 0)
-        self._gram_skip[key] = GRAM_RETRY_AFTER if refused else max(skip - 1, 0)
+        r_new = fold_chunk(buf, r_in, chunk, self.math)
         Rd[module] = buf[:r_new]
 
     def _finalize(self, R_raw: torch.Tensor, rows: int, out_dtype: torch.dtype):

@@ -780,21 +780,16 @@ def test_triangular_mirrors_match_oracle(be):
 def test_bf16_fold_takes_gram_route_when_square(be):
     """bf16 arithmetic: a fold whose result is square goes to the Gram-route fold;
     the first (partial-rank) chunk, a refused fold (status 2, injected or from a
-    repeated column) and fp32 arithmetic go to the panel fold; after a refusal the
-    side's next GRAM_RETRY_AFTER folds go to the panel fold at once, and the one
-    after tries the Gram route again.  Every path leaves the oracle's running
-    factor."""
+    repeated column) and fp32 arithmetic go to the panel fold.  Every path leaves
+    the oracle's running factor."""
     from ifkfac_amd._backend import MATH_BF16, MATH_F32
-    from ifkfac_amd.activation_hooks import GRAM_FOLD_TOL, GRAM_RETRY_AFTER, RawActivationHooks
+    from ifkfac_amd.activation_hooks import GRAM_FOLD_TOL, RawActivationHooks
     model = nn.Sequential(nn.Linear(8, 4))
     lin = model[0]
     rng = np.random.default_rng(3)
     chunks = [rng.standard_normal((p, 8)) for p in (5, 6, 8, 8)]
     chunks[3][:, 7] = chunks[3][:, 0]            # a column repeated within the chunk
-    extra = [rng.standard_normal((6, 8)) for _ in range(GRAM_RETRY_AFTER)]
-    chunks = chunks + extra
-    bf16_calls = (0, 1, 1) + (0,) * GRAM_RETRY_AFTER + (1,)   # refusal at 2, backoff, retry
-    for math_, calls in ((MATH_BF16, bf16_calls), (MATH_F32, (0,) * len(chunks))):
+    for math_, calls in ((MATH_BF16, (0, 1, 1, 1)), (MATH_F32, (0, 0, 0, 0))):
         be.calls.clear()
         hooks = RawActivationHooks(model, math=math_)
         old = None
@@ -811,7 +806,6 @@ def test_bf16_fold_takes_gram_route_when_square(be):
         hooks.remove()
     assert be.gram_fold_status2 == 0
     # the repeated column is refused by the pivot rule itself
-    chunks = chunks[:4]
     P = np.vstack([O.streaming_tsqr_update(None, np.vstack(chunks[:3])), chunks[3]])
     assert O.gram_pivot_ratio(P).min() > GRAM_FOLD_TOL   # earlier rows keep it independent
     R0 = torch.zeros(8, 8)
