@@ -111,8 +111,8 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
 // bf16 A (M x K, lda) and B (N x K, ldb), row-major, one entry.
 bool lib_gemm_enabled();
 int lib_gemm_set(int on);   // returns the previous setting
-int lib_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                  bool beta_nz, size_t ws_bytes);
+int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                  int64_t ldc, bool beta_nz, size_t ws_bytes);
 int lib_gemm_bf16_nt(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha,
                      const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, float beta,
                      float* C, int64_t ldc, void* ws, size_t ws_bytes);

@@ -526,7 +526,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   // batch of one gets)
   if (bb && A.tri == TRI_NONE && B.tri == TRI_NONE && C.c && !C.cb && lib_gemm_enabled()) {
     const size_t wsb = scratch.p ? scratch.floats * sizeof(float) : 0;
-    if (lib_gemm_plan(M, N, K, A.ld, B.ld, C.ldc, beta != 0.0f, wsb)) {
+    if (lib_gemm_plan(s, M, N, K, A.ld, B.ld, C.ldc, beta != 0.0f, wsb)) {
       const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | (1 << 8);
       ProfRec* pr = prof_slot(vid);
       if (pr) {

@@ -12,10 +12,12 @@
 // Row-major C = A B^T is the column-major product C^T = B^T-op(B_cm) A_cm:
 // the library's "A" is our B viewed column-major (K x N, ld ldb) used
 // transposed, its "B" is our A (K x M, ld lda) used as is, and C^T is N x M
-// with ld ldc.  One plan per (device, shape, strides, beta != 0, workspace):
-// the descriptors and the heuristic's first algorithm, made once under a
-// lock and kept for the process (each a few hundred bytes of host memory).
-// The workspace is the caller's split-K scratch of the same stream.
+// with ld ldc.  One handle per (device, stream), so that products enqueued on
+// different streams never share a handle's state, and one plan per (handle,
+// shape, strides, beta != 0, workspace): the descriptors and the heuristic's
+// first algorithm, made once under a lock and kept for the process (each a
+// few hundred bytes of host memory).  Every call gets the caller's split-K
+// scratch of the same stream as its workspace, whatever the algorithm asks.
 #include <hipblaslt/hipblaslt.h>
 
 #include <atomic>
@@ -34,12 +36,13 @@ namespace {
 
 struct LtKey {
   int dev;
+  uintptr_t stream;
   int64_t m, n, k, lda, ldb, ldc;
   int beta_nz;
   size_t ws;
   bool operator<(const LtKey& o) const {
-    return std::tie(dev, m, n, k, lda, ldb, ldc, beta_nz, ws) <
-           std::tie(o.dev, o.m, o.n, o.k, o.lda, o.ldb, o.ldc, o.beta_nz, o.ws);
+    return std::tie(dev, stream, m, n, k, lda, ldb, ldc, beta_nz, ws) <
+           std::tie(o.dev, o.stream, o.m, o.n, o.k, o.lda, o.ldb, o.ldc, o.beta_nz, o.ws);
   }
 };
 
@@ -52,18 +55,19 @@ struct LtPlan {
 };
 
 std::mutex g_lt_mu;
-std::map<int, hipblasLtHandle_t> g_lt_handle;
+std::map<std::pair<int, uintptr_t>, hipblasLtHandle_t> g_lt_handle;
 std::map<LtKey, LtPlan> g_lt_plan;
 
 // the plan for a key (made on first use); null handle when the library
 // cannot be initialised on this device
 const LtPlan* lt_plan(const LtKey& key, hipblasLtHandle_t* h) {
   std::lock_guard<std::mutex> lock(g_lt_mu);
-  auto hi = g_lt_handle.find(key.dev);
+  const auto hk = std::make_pair(key.dev, key.stream);
+  auto hi = g_lt_handle.find(hk);
   if (hi == g_lt_handle.end()) {
     hipblasLtHandle_t nh = nullptr;
     if (hipblasLtCreate(&nh) != HIPBLAS_STATUS_SUCCESS) nh = nullptr;
-    hi = g_lt_handle.emplace(key.dev, nh).first;
+    hi = g_lt_handle.emplace(hk, nh).first;
   }
   *h = hi->second;
   if (!*h) return nullptr;
@@ -126,12 +130,13 @@ int lib_gemm_set(int on) {
   return prev;
 }
 
-int lib_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-                  bool beta_nz, size_t ws_bytes) {
+int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                  int64_t ldc, bool beta_nz, size_t ws_bytes) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   hipblasLtHandle_t h = nullptr;
-  const LtPlan* pl = lt_plan(LtKey{dev, M, N, K, lda, ldb, ldc, beta_nz ? 1 : 0, ws_bytes}, &h);
+  const LtPlan* pl = lt_plan(
+      LtKey{dev, (uintptr_t)s, M, N, K, lda, ldb, ldc, beta_nz ? 1 : 0, ws_bytes}, &h);
   return (pl && pl->ok) ? 1 : 0;
 }
 
@@ -144,15 +149,14 @@ int lib_gemm_bf16_nt(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha
     return IFK_ERR_HIP;
   }
   hipblasLtHandle_t h = nullptr;
-  const LtPlan* pl =
-      lt_plan(LtKey{dev, M, N, K, lda, ldb, ldc, beta != 0.0f ? 1 : 0, ws_bytes}, &h);
+  const LtPlan* pl = lt_plan(
+      LtKey{dev, (uintptr_t)s, M, N, K, lda, ldb, ldc, beta != 0.0f ? 1 : 0, ws_bytes}, &h);
   if (!pl || !pl->ok) {
     set_error("gemm: hipBLASLt has no algorithm for this product");
     return IFK_ERR_INVALID;
   }
   const hipblasStatus_t st = hipblasLtMatmul(h, pl->desc, &alpha, B, pl->la, A, pl->lb, &beta, C,
-                                             pl->lc, C, pl->lc, &pl->algo, pl->ws ? ws : nullptr,
-                                             pl->ws, s);
+                                             pl->lc, C, pl->lc, &pl->algo, ws, ws_bytes, s);
   if (st != HIPBLAS_STATUS_SUCCESS) {
     set_error("gemm: hipblasLtMatmul failed");
     return IFK_ERR_HIP;

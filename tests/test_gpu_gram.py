@@ -380,3 +380,23 @@ def test_gram_route_plain_products_library_and_own_kernels(hip):
     for on in (1, 0):
         assert _gram_rel(out[on], Ro) <= 3e-5
     assert _gram_rel(out[1], out[0]) <= 6e-5
+
+
+def test_gram_route_repeated_folds_identical(hip):
+    """Ten folds of the same chunk into the same square factor, each a Gram-route
+    factorisation on three streams (n = 3072: the helper and Gram streams run
+    hipBLASLt products beside the chain), give identical bits: the streams'
+    library calls share no handle state and no workspace."""
+    g = torch.Generator(device=DEV).manual_seed(31)
+    n, p = 3072, 4096
+    R0 = torch.zeros(n, n, device=DEV)
+    assert hip.fold_gram_(R0, 0, torch.randn(p, n, device=DEV, generator=g), 1e-4).item() == 1
+    X = torch.randn(p, n, device=DEV, generator=g)
+    outs = []
+    for _ in range(10):
+        R = R0.clone()
+        st = hip.fold_gram_(R, n, X, 1e-4)
+        outs.append((st.item(), R))
+    assert all(s == 1 for s, _ in outs)
+    for _, R in outs[1:]:
+        assert torch.equal(R, outs[0][1])
