@@ -11,7 +11,10 @@
 // into a kernel argument.  Every call on one GPU shares the array, so calls
 // that overlap on one GPU (on different streams, or from different threads)
 // race.  Nothing in the array has to start at zero: the apply writes each
-// intermediate before reading it.
+// intermediate before reading it.  Its four products each have a triangular
+// operand, so the GEMM dispatcher keeps them on this library's kernels
+// (hipBLASLt, which allocates when it makes a handle, takes only plain
+// products).
 #include "../../include/ifkfac_hip.h"
 
 #include <mutex>
