@@ -111,6 +111,9 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
 // bf16 A (M x K, lda) and B (N x K, ldb), row-major, one entry.
 bool lib_gemm_enabled();
 int lib_gemm_set(int on);   // returns the previous setting
+// frees the handle and plans kept for stream s on the current device (the
+// caller has drained s)
+int lib_gemm_release(hipStream_t s);
 int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                   int64_t ldc, bool beta_nz, size_t ws_bytes);
 int lib_gemm_bf16_nt(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha,

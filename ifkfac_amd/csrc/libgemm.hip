@@ -130,6 +130,37 @@ int lib_gemm_set(int on) {
   return prev;
 }
 
+int lib_gemm_release(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("release_stream_state: hipGetDevice failed");
+    return IFK_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_lt_mu);
+  bool ok = true;
+  for (auto it = g_lt_plan.begin(); it != g_lt_plan.end();) {
+    if (it->first.dev == dev && it->first.stream == (uintptr_t)s) {
+      LtPlan& pl = it->second;
+      for (hipblasLtMatrixLayout_t l : {pl.la, pl.lb, pl.lc})
+        if (l) ok = hipblasLtMatrixLayoutDestroy(l) == HIPBLAS_STATUS_SUCCESS && ok;
+      if (pl.desc) ok = hipblasLtMatmulDescDestroy(pl.desc) == HIPBLAS_STATUS_SUCCESS && ok;
+      it = g_lt_plan.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  auto hi = g_lt_handle.find(std::make_pair(dev, (uintptr_t)s));
+  if (hi != g_lt_handle.end()) {
+    if (hi->second) ok = hipblasLtDestroy(hi->second) == HIPBLAS_STATUS_SUCCESS && ok;
+    g_lt_handle.erase(hi);
+  }
+  if (!ok) {
+    set_error("release_stream_state: a hipBLASLt handle or plan could not be released");
+    return IFK_ERR_HIP;
+  }
+  return IFK_OK;
+}
+
 int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                   int64_t ldc, bool beta_nz, size_t ws_bytes) {
   int dev = 0;

@@ -51,12 +51,13 @@ const char* ifk_last_error(void);
 /*
  * Release the helper streams and events that the factorisations of more than
  * 1024 columns create for (current device, calling stream) on first use and
- * otherwise keep until the process ends.  No counterpart in the reference
- * (torch manages its own streams): it is for callers that create many
- * calling streams over a process's life.  Waits for the stream's and its
- * helpers' queued work; a later factorisation on the stream creates them
- * again.  Not to be called while another host thread issues a factorisation
- * on the same stream.  A stream with no such state: nothing to do, 0.
+ * otherwise keep until the process ends, and the hipBLASLt handles and plans
+ * kept for the calling stream and those helpers.  No counterpart in the
+ * reference (torch manages its own streams): it is for callers that create
+ * many calling streams over a process's life.  Waits for the stream's and its
+ * helpers' queued work; a later call on the stream creates them again.  Not
+ * to be called while another host thread issues work of this library on the
+ * same stream.  A stream with no such state: nothing to do, 0.
  */
 int ifk_release_stream_state(void* stream);
 

@@ -324,10 +324,10 @@ def test_fold_finalize_gram_inverse(hip, B, prev, p, n, odt):
 
 
 def test_release_stream_state(hip):
-    """ifk_release_stream_state: a stream's helper set released between two
-    factorisations of more than 1024 columns (three streams and their events)
-    gives the second the same bits; releasing a stream with no set, or twice,
-    is a no-op."""
+    """ifk_release_stream_state: a stream's helper set (three streams and their
+    events) and the hipBLASLt handles and plans of those streams released between
+    two factorisations of more than 1024 columns give the second the same bits;
+    releasing a stream with no set, or twice, is a no-op."""
     g = torch.Generator(device=DEV).manual_seed(41)
     X = torch.randn(4000, 3100, device=DEV, generator=g).to(torch.bfloat16)
     st_ = torch.cuda.Stream()
