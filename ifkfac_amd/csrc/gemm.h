@@ -99,25 +99,27 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
 
 // max_wgs > 0 caps the number of workgroups of a large-tile launch (tiles are
 // then visited grid-stride), leaving CUs free for work on other streams.
-// Plain large bf16 products (both operands K-contiguous, neither triangular,
-// an fp32 result only) go to hipBLASLt (libgemm.hip), one call per batch
-// entry, uncapped; the environment variable IFK_GEMM_LIB=0 keeps them on the
+// Plain large products (neither operand triangular, an fp32 result only:
+// bf16 operands with K contiguous in bf16 arithmetic, fp32 operands in fp32
+// arithmetic) go to hipBLASLt (libgemm.hip), one call per batch entry,
+// uncapped; the environment variable IFK_GEMM_LIB=0 keeps them on the
 // engine's kernels.
 int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
          const MatRef& A, const MatRef& B, float beta, const OutRef& C, int batch,
          SplitScratch scratch, int max_wgs = 0);
 
-// hipBLASLt (libgemm.hip): C (fp32, M x N, ldc) = alpha A B^T + beta C for
-// bf16 A (M x K, lda) and B (N x K, ldb), row-major, one entry.
+// hipBLASLt (libgemm.hip): C (fp32, M x N, ldc) = alpha op(A) op(B) + beta C,
+// one entry; operands as MatRef describes them (type, ld, K-contiguity).
 bool lib_gemm_enabled();
 int lib_gemm_set(int on);   // returns the previous setting
 // frees the handle and plans kept for stream s on the current device (the
 // caller has drained s)
 int lib_gemm_release(hipStream_t s);
-int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                  int64_t ldc, bool beta_nz, size_t ws_bytes);
-int lib_gemm_bf16_nt(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha,
-                     const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, float beta,
-                     float* C, int64_t ldc, void* ws, size_t ws_bytes);
+int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int adt, int64_t lda,
+                  bool akc, int bdt, int64_t ldb, bool bkc, int64_t ldc, bool beta_nz,
+                  size_t ws_bytes);
+int lib_gemm_run(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
+                 int adt, int64_t lda, bool akc, const void* B, int bdt, int64_t ldb, bool bkc,
+                 float beta, float* C, int64_t ldc, void* ws, size_t ws_bytes);
 
 }  // namespace ifk

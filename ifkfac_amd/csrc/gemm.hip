@@ -523,10 +523,15 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
                   p.vec_b && K % 8 == 0 && A.ld < ((int64_t)1 << 21) &&
                   B.ld < ((int64_t)1 << 21);
   // plain products: hipBLASLt, entry by entry (every entry gets the bits a
-  // batch of one gets)
-  if (bb && A.tri == TRI_NONE && B.tri == TRI_NONE && C.c && !C.cb && lib_gemm_enabled()) {
+  // batch of one gets): bf16 operands with K contiguous in bf16 arithmetic,
+  // fp32 operands in fp32 arithmetic, both large
+  const bool lib_f32 = math == MATH_F32 && A.dt == DT_F32 && B.dt == DT_F32 && M >= 192 &&
+                       N >= 192 && (double)M * (double)N * (double)K * batch >= 1e9;
+  if ((bb || lib_f32) && A.tri == TRI_NONE && B.tri == TRI_NONE && C.c && !C.cb &&
+      lib_gemm_enabled()) {
     const size_t wsb = scratch.p ? scratch.floats * sizeof(float) : 0;
-    if (lib_gemm_plan(s, M, N, K, A.ld, B.ld, C.ldc, beta != 0.0f, wsb)) {
+    if (lib_gemm_plan(s, M, N, K, A.dt, A.ld, A.kc, B.dt, B.ld, B.kc, C.ldc, beta != 0.0f,
+                      wsb)) {
       const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | (1 << 8);
       ProfRec* pr = prof_slot(vid);
       if (pr) {
@@ -535,15 +540,17 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
         pr->n = N;
         pr->k = K;
         pr->flops = 2.0 * (double)M * (double)N * (double)K * batch;
-        pr->bytes = ((double)M * K * 2 + (double)K * N * 2 +
+        pr->bytes = ((double)M * K * (A.dt == DT_BF16 ? 2 : 4) +
+                     (double)K * N * (B.dt == DT_BF16 ? 2 : 4) +
                      (double)M * N * (beta != 0.0f ? 8.0 : 4.0)) * batch;
         hipEventRecord(pr->beg, s);
       }
+      const size_t ea = A.dt == DT_BF16 ? 2 : 4, eb = B.dt == DT_BF16 ? 2 : 4;
       for (int e = 0; e < batch; ++e) {
-        const int rc = lib_gemm_bf16_nt(
-            s, M, N, K, alpha, (const bf16_t*)A.p + (size_t)e * A.bstride, A.ld,
-            (const bf16_t*)B.p + (size_t)e * B.bstride, B.ld, beta, C.c + (size_t)e * C.bstride,
-            C.ldc, scratch.p, wsb);
+        const int rc = lib_gemm_run(
+            s, M, N, K, alpha, (const char*)A.p + (size_t)e * A.bstride * ea, A.dt, A.ld, A.kc,
+            (const char*)B.p + (size_t)e * B.bstride * eb, B.dt, B.ld, B.kc, beta,
+            C.c + (size_t)e * C.bstride, C.ldc, scratch.p, wsb);
         if (rc) return rc;
       }
       if (pr) hipEventRecord(pr->end, s);

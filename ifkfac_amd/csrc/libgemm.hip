@@ -1,6 +1,7 @@
-// Plain bf16 products through hipBLASLt, the vendor GEMM library:
-//   C (fp32, row-major M x N, ldc) = alpha * A B^T + beta * C,
-//   A (bf16, M x K, lda) and B (bf16, N x K, ldb) with K contiguous.
+// Plain products through hipBLASLt, the vendor GEMM library:
+//   C (fp32, row-major M x N, ldc) = alpha * op(A) op(B) + beta * C,
+// bf16 operands with K contiguous (A M x K, B N x K) in bf16 arithmetic, and
+// fp32 operands stored either way (gemm.h's kc flags) in fp32 arithmetic.
 // The engine's dispatcher (gemm.hip) sends here the products that are plain
 // in this sense -- no triangular operand, no bf16 copy of the result -- which
 // are the Gram columns of a factor update and its panel and band updates:
@@ -40,9 +41,11 @@ struct LtKey {
   int64_t m, n, k, lda, ldb, ldc;
   int beta_nz;
   size_t ws;
+  int adt, akc, bdt, bkc;   // operand types (DT_F32 / DT_BF16) and K-contiguity
   bool operator<(const LtKey& o) const {
-    return std::tie(dev, stream, m, n, k, lda, ldb, ldc, beta_nz, ws) <
-           std::tie(o.dev, o.stream, o.m, o.n, o.k, o.lda, o.ldb, o.ldc, o.beta_nz, o.ws);
+    return std::tie(dev, stream, m, n, k, lda, ldb, ldc, beta_nz, ws, adt, akc, bdt, bkc) <
+           std::tie(o.dev, o.stream, o.m, o.n, o.k, o.lda, o.ldb, o.ldc, o.beta_nz, o.ws, o.adt,
+                    o.akc, o.bdt, o.bkc);
   }
 };
 
@@ -76,14 +79,23 @@ const LtPlan* lt_plan(const LtKey& key, hipblasLtHandle_t* h) {
   LtPlan pl;
   bool ok = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) ==
             HIPBLAS_STATUS_SUCCESS;
-  const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
-  ok = ok && hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT,
-                                             sizeof(opT)) == HIPBLAS_STATUS_SUCCESS;
-  ok = ok && hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN,
-                                             sizeof(opN)) == HIPBLAS_STATUS_SUCCESS;
-  ok = ok && hipblasLtMatrixLayoutCreate(&pl.la, HIP_R_16BF, (uint64_t)key.k, (uint64_t)key.n,
+  // the library's A is our B: K-contiguous B (N x K row-major) is a K x N
+  // column-major matrix used transposed, else (K x N row-major) an N x K one
+  // used as is; its B is our A: K-contiguous A (M x K row-major) is K x M
+  // column-major used as is, else (K x M row-major) M x K used transposed
+  const int32_t opA = key.bkc ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  const int32_t opB = key.akc ? HIPBLAS_OP_N : HIPBLAS_OP_T;
+  const hipDataType ta = key.bdt == DT_BF16 ? HIP_R_16BF : HIP_R_32F;
+  const hipDataType tb = key.adt == DT_BF16 ? HIP_R_16BF : HIP_R_32F;
+  ok = ok && hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opA,
+                                             sizeof(opA)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opB,
+                                             sizeof(opB)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&pl.la, ta, (uint64_t)(key.bkc ? key.k : key.n),
+                                         (uint64_t)(key.bkc ? key.n : key.k),
                                          key.ldb) == HIPBLAS_STATUS_SUCCESS;
-  ok = ok && hipblasLtMatrixLayoutCreate(&pl.lb, HIP_R_16BF, (uint64_t)key.k, (uint64_t)key.m,
+  ok = ok && hipblasLtMatrixLayoutCreate(&pl.lb, tb, (uint64_t)(key.akc ? key.k : key.m),
+                                         (uint64_t)(key.akc ? key.m : key.k),
                                          key.lda) == HIPBLAS_STATUS_SUCCESS;
   ok = ok && hipblasLtMatrixLayoutCreate(&pl.lc, HIP_R_32F, (uint64_t)key.n, (uint64_t)key.m,
                                          key.ldc) == HIPBLAS_STATUS_SUCCESS;
@@ -161,27 +173,31 @@ int lib_gemm_release(hipStream_t s) {
   return IFK_OK;
 }
 
-int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                  int64_t ldc, bool beta_nz, size_t ws_bytes) {
+int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int adt, int64_t lda,
+                  bool akc, int bdt, int64_t ldb, bool bkc, int64_t ldc, bool beta_nz,
+                  size_t ws_bytes) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   hipblasLtHandle_t h = nullptr;
-  const LtPlan* pl = lt_plan(
-      LtKey{dev, (uintptr_t)s, M, N, K, lda, ldb, ldc, beta_nz ? 1 : 0, ws_bytes}, &h);
+  const LtPlan* pl = lt_plan(LtKey{dev, (uintptr_t)s, M, N, K, lda, ldb, ldc, beta_nz ? 1 : 0,
+                                   ws_bytes, adt, akc ? 1 : 0, bdt, bkc ? 1 : 0},
+                             &h);
   return (pl && pl->ok) ? 1 : 0;
 }
 
-int lib_gemm_bf16_nt(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha,
-                     const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, float beta,
-                     float* C, int64_t ldc, void* ws, size_t ws_bytes) {
+int lib_gemm_run(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
+                 int adt, int64_t lda, bool akc, const void* B, int bdt, int64_t ldb, bool bkc,
+                 float beta, float* C, int64_t ldc, void* ws, size_t ws_bytes) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     set_error("gemm: no current device");
     return IFK_ERR_HIP;
   }
   hipblasLtHandle_t h = nullptr;
-  const LtPlan* pl = lt_plan(
-      LtKey{dev, (uintptr_t)s, M, N, K, lda, ldb, ldc, beta != 0.0f ? 1 : 0, ws_bytes}, &h);
+  const LtPlan* pl = lt_plan(LtKey{dev, (uintptr_t)s, M, N, K, lda, ldb, ldc,
+                                   beta != 0.0f ? 1 : 0, ws_bytes, adt, akc ? 1 : 0, bdt,
+                                   bkc ? 1 : 0},
+                             &h);
   if (!pl || !pl->ok) {
     set_error("gemm: hipBLASLt has no algorithm for this product");
     return IFK_ERR_INVALID;

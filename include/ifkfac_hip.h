@@ -486,10 +486,11 @@ int ifk_profile_end(int64_t* n_launches);
 
 /*
  * No counterpart in the reference (measurement and test support).
- * ifk_set_gemm_library(on) chooses where the plain bf16 products (both
- * operands K-contiguous, neither triangular, an fp32 result: the Gram route's
- * Gram columns and panel and band updates) run for the calls enqueued after
- * it: on = 1 hipBLASLt (the default; the environment variable IFK_GEMM_LIB=0
+ * ifk_set_gemm_library(on) chooses where the plain products (neither operand
+ * triangular, an fp32 result only; bf16 operands with K contiguous in bf16
+ * arithmetic -- the Gram route's Gram columns and panel and band updates --
+ * and large fp32 products in fp32 arithmetic) run for the calls enqueued
+ * after it: on = 1 hipBLASLt (the default; the environment variable IFK_GEMM_LIB=0
  * makes 0 the default), on = 0 this library's own kernels.  Returns the
  * previous setting.  Process-wide; results agree within rounding (the
  * summation order differs), not bit for bit.
