@@ -63,7 +63,7 @@ PEAK_HBM_GBS = 8000.0
 # two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same
 # counters on a 256 MiB copy (profiles/pmc_traffic_linear4096x11008_p16384.txt);
 # None for other workloads and factor paths.
-TRAFFIC = {("linear_4096x11008_p16384", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"): 1266.30e6}
+TRAFFIC = {("linear_4096x11008_p16384", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"): 1263.74e6}
 
 WORKLOADS = {
     # name: (n_in, n_out, p)
