@@ -500,23 +500,15 @@ def main() -> int:
     # the dominant GEMM kernel family of this library's own kernels (as
     # rocprofv3 names them: 0 gemm_kernel, 1 gemm_big_kernel, 2 / 3
     # gemm_bb_kernel with its 256 / 128 tile) by algorithmic flops in the
-    # survey step, timed over the timed steps; the plain products that run on
-    # hipBLASLt (family 4) are reported beside it, from the survey step
+    # survey step, timed over the timed steps
     def family(vid):
-        if (vid >> 8) & 1:
-            return 4
         if (vid >> 6) & 1:
             return 3 if (vid >> 7) & 1 else 2
         return (vid >> 5) & 1
-    fam_fl = {0: 0.0, 1: 0.0, 2: 0.0, 3: 0.0, 4: 0.0}
-    lib_rec = [0.0, 0, 0.0]
+    fam_fl = {0: 0.0, 1: 0.0, 2: 0.0, 3: 0.0}
     for vid, a in per_variant.items():
         fam_fl[family(vid)] += a[2]
-        if family(vid) == 4:
-            lib_rec[0] += a[0]
-            lib_rec[1] += a[1]
-            lib_rec[2] += a[2]
-    fam = max((f for f in fam_fl if f != 4), key=fam_fl.get)
+    fam = max(fam_fl, key=fam_fl.get)
     arm = {0: -4, 1: -3, 2: -5, 3: -6}[fam]
     kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>",
              3: "gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2, false>>"}[fam]
@@ -562,16 +554,6 @@ def main() -> int:
         "algorithmic_flops_per_launch": round(tot_fl / max(len(recs), 1)),
         "algorithmic_bytes_per_launch": round(tot_by / max(len(recs), 1)),
     })
-    if lib_rec[1]:
-        # plain bf16 products on hipBLASLt (Gram columns, panel and band
-        # updates), events around each call in the survey step
-        roof["hipblaslt_products"] = {
-            "launches_per_step": lib_rec[1],
-            "achieved_tflops": round(lib_rec[2] / (lib_rec[0] * 1e-3) / 1e12, 1),
-            "frac": round(lib_rec[2] / (lib_rec[0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "ms_per_step_summed": round(lib_rec[0], 3),
-            "share_of_flops": round(lib_rec[2] / max(sum(fam_fl.values()), 1.0), 3),
-        }
     # a roofline per phase: algorithmic work over the phase's time in the
     # survey step (the whole GPU, all streams)
     ph_upd = phases["factor_update_and_inverse"]

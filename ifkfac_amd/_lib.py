@@ -141,7 +141,6 @@ SIGNATURES = {
                           _c_sz]),
     "ifk_profile_begin": (_c_int, [_c_int]),
     "ifk_profile_end": (_c_int, [_c_i64p]),
-    "ifk_set_gemm_library": (_c_int, [_c_int]),
     "ifk_profile_get": (_c_int, [_c_i64, ctypes.POINTER(_c_int), ctypes.POINTER(_c_f),
                                  ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                  _c_i64p, _c_i64p, _c_i64p]),

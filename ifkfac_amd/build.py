@@ -64,10 +64,7 @@ def build(verbose: bool = False) -> str:
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, sources))
     tmp = LIB_PATH + ".tmp"
-    # hipBLASLt takes the plain bf16 products (csrc/libgemm.hip)
-    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-           f"-L{os.path.join(rocm, 'lib')}", "-lhipblaslt"]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -3,6 +3,7 @@
 // every failure to a status code plus a thread-local message.
 #include "../../include/ifkfac_hip.h"
 
+#include <algorithm>
 #include <string>
 
 #include "gemm.h"
@@ -434,6 +435,8 @@ size_t ifk_gemm_workspace_size(int64_t m, int64_t n) {
   if (m < 1 || n < 1) return 0;
   size_t f = (size_t)m * n * 64;
   if (f > ((size_t)16 << 20)) f = (size_t)16 << 20;
+  // and the stream-K partial tiles of a product with K up to 2^20
+  f = std::max(f, gemm_scratch_floats(m, n, (int64_t)1 << 20, 1));
   return f * sizeof(float);
 }
 
@@ -461,8 +464,6 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
 int ifk_profile_begin(int variant) { return profile_begin(variant); }
 
 int ifk_profile_end(int64_t* n_launches) { return profile_end(n_launches); }
-
-int ifk_set_gemm_library(int on) { return lib_gemm_set(on); }
 
 int ifk_profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
                     int64_t* n, int64_t* k) {

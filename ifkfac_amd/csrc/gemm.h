@@ -87,10 +87,9 @@ struct SplitScratch {
 
 // Launch profiler (see gemm.hip).  variant: gemm_variant_id() (bit 5 set for
 // the large-tile bf16 kernels, bit 6 as well for the direct-to-LDS one, bit 7
-// for its 128 x 128 tile, bit 8 for a product run by hipBLASLt), -2 all, -3
-// all of the register-staged 256 x 128 kernel, -4 all of the 128 x 128
-// kernel, -5 / -6 all of the direct-to-LDS kernel with its 256 / 128 tile, -7
-// all hipBLASLt products, -1 off.
+// for its 128 x 128 tile, bit 9 for a stream-K launch), -2 all, -3 all of the
+// register-staged 256 x 128 kernel, -4 all of the 128 x 128 kernel, -5 / -6
+// all of the direct-to-LDS kernel with its 256 / 128 tile, -1 off.
 int gemm_variant_id(int math, int adt, bool akc, int bdt, bool bkc);
 int profile_begin(int variant);
 int profile_end(int64_t* n_launches);
@@ -98,28 +97,16 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
                 int64_t* n, int64_t* k);
 
 // max_wgs > 0 caps the number of workgroups of a large-tile launch (tiles are
-// then visited grid-stride), leaving CUs free for work on other streams.
-// Plain large products (neither operand triangular, an fp32 result only:
-// bf16 operands with K contiguous in bf16 arithmetic, fp32 operands in fp32
-// arithmetic) go to hipBLASLt (libgemm.hip), one call per batch entry,
-// uncapped; the environment variable IFK_GEMM_LIB=0 keeps them on the
-// engine's kernels.
+// then visited grid-stride, or a stream-K grid is sized within it), leaving
+// CUs free for work on other streams.  Every product runs on this library's
+// own kernels.
 int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha,
          const MatRef& A, const MatRef& B, float beta, const OutRef& C, int batch,
          SplitScratch scratch, int max_wgs = 0);
 
-// hipBLASLt (libgemm.hip): C (fp32, M x N, ldc) = alpha op(A) op(B) + beta C,
-// one entry; operands as MatRef describes them (type, ld, K-contiguity).
-bool lib_gemm_enabled();
-int lib_gemm_set(int on);   // returns the previous setting
-// frees the handle and plans kept for stream s on the current device (the
-// caller has drained s)
-int lib_gemm_release(hipStream_t s);
-int lib_gemm_plan(hipStream_t s, int64_t M, int64_t N, int64_t K, int adt, int64_t lda,
-                  bool akc, int bdt, int64_t ldb, bool bkc, int64_t ldc, bool beta_nz,
-                  size_t ws_bytes);
-int lib_gemm_run(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
-                 int adt, int64_t lda, bool akc, const void* B, int bdt, int64_t ldb, bool bkc,
-                 float beta, float* C, int64_t ldc, void* ws, size_t ws_bytes);
+// Scratch (fp32 elements) that lets the GEMM of an M x N output with K deep
+// operands take its fastest grid, stream-K included, for `batch` entries
+// within max_wgs workgroups (0: uncapped).
+size_t gemm_scratch_floats(int64_t M, int64_t N, int64_t K, int batch, int max_wgs = 0);
 
 }  // namespace ifk

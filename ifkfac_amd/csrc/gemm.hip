@@ -8,6 +8,7 @@
 // MFMA fragment with 128-bit loads; operands that are K-strided in memory are
 // transposed in registers on the way in (8 k x 4 mn micro-blocks per thread).
 #include "gemm_impl.h"
+#include "kernels.h"
 
 #include <mutex>
 #include <vector>
@@ -81,22 +82,22 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
 
 // Kernel family of a variant id: 0 the 128 x 128 kernel, 1 the 256 x 128
 // register-staged kernel (bit 5), 2 / 3 the direct-to-LDS kernel with its 256
-// / 128 tile (bits 5 and 6, and bit 7 for the 128 tile).
+// / 128 tile (bits 5 and 6, and bit 7 for the 128 tile; bit 9 marks a
+// stream-K launch of either).
 static int gemm_family(int vid) {
-  if ((vid >> 8) & 1) return 4;
   if ((vid >> 6) & 1) return ((vid >> 7) & 1) ? 3 : 2;
   return (vid >> 5) & 1;
 }
 
-// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 / -6 /
-// -7 every launch of family 1 / 0 / 2 / 3 / 4 (hipBLASLt).
+// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 / -6
+// every launch of family 1 / 0 / 2 / 3.
 static ProfRec* prof_slot(int vid) {
   const int a = g_prof_variant;
   if (a == -1) return nullptr;
   if (a >= 0 && a != vid) return nullptr;
   const int fam = gemm_family(vid);
   if ((a == -3 && fam != 1) || (a == -4 && fam != 0) || (a == -5 && fam != 2) ||
-      (a == -6 && fam != 3) || (a == -7 && fam != 4))
+      (a == -6 && fam != 3))
     return nullptr;
   std::lock_guard<std::mutex> g(g_prof_mu);
   if (g_prof_used == g_prof.size()) {
@@ -479,6 +480,113 @@ static bool vec_ok(const MatRef& X) {
   return (a % 16 == 0) && (X.ld % 8 == 0) && (X.bstride % 8 == 0);
 }
 
+// Stream-K plan of a plain product on the direct-to-LDS kernel (gemm_impl.h):
+// lanes > 0 when it is estimated faster than the data-parallel grid (tile
+// dp_mid, dp_splits split-K shares).  The estimates count slabs per
+// workgroup in the slowest round: a 256-tile slab takes about 1.1 us (one
+// workgroup per CU), a 128-tile slab 0.98 us with two workgroups on a CU and
+// 0.75 us with one.  Split-K partials cost their fp32 traffic at 4 TB/s and
+// a launch.  A stream-K walk pays for its share exchange, measured on
+// MI355X at about 12 + 11 s us for 256 tiles and 10 + 4 s us for 128 tiles,
+// s the number of lanes sharing a tile row: every lane's last share ends at
+// the same moment, so the exchange is a burst at the end of the launch.
+// Every lane count (a multiple of eight) up to the cap is tried.  So
+// stream-K takes the long-K products with few output tiles (the Gram
+// route's Gram columns: 1024 columns, K = p rows, whose 150-odd 256-tiles
+// leave a second round of workgroups two-thirds empty), not the short-K ones.
+// Stream-K is considered for K >= SK_MIN_K only.  Beside the factorisation's
+// chain of small launches, short-K products did better data-parallel with
+// split-K than stream-K (the Linear 4096 -> 11008 step, 13.06 against
+// 13.20 ms with every plain product eligible): their workgroups are short-
+// lived, so the chain finds CUs sooner, and their share exchange is a larger
+// part of the launch.
+constexpr int64_t SK_MIN_K = 8192;
+
+struct SkPlan {
+  int lanes = 0;
+  bool mid = false;
+  int iters = 0;
+  size_t cnt_floats = 0;   // counter region (ints) at the head of the scratch
+  size_t floats = 0;       // counters + partial tiles
+};
+
+static double slab_us(bool mid, int64_t wgs) {
+  if (!mid) return 1.1;
+  return wgs > 256 ? 0.98 : 0.75;
+}
+
+// lanes_max of the stream-K walk with tile `mid` (0 when not eligible)
+static int64_t sk_lanes_max(int64_t M, int64_t N, int64_t K, bool mid, int max_wgs) {
+  const int T = gemm_bb_tile(mid);
+  const int64_t tn = cdiv(N, (int64_t)T), tm = cdiv(M, (int64_t)T);
+  if (tn > 8) return 0;
+  const int64_t U = tm * cdiv(K, (int64_t)gemm_bb_bk());
+  int64_t G = mid ? 512 : 256;
+  if (max_wgs > 0) G = std::min<int64_t>(G, max_wgs);
+  int64_t L = std::min<int64_t>(G / tn, U / 8);
+  return L - L % 8;
+}
+
+static size_t sk_floats(int64_t M, int64_t N, bool mid, int batch, int64_t L) {
+  const int T = gemm_bb_tile(mid);
+  const int64_t tn = cdiv(N, (int64_t)T), tm = cdiv(M, (int64_t)T);
+  const size_t cntf = align_up((size_t)(batch * tm * tn), 64);
+  return cntf + (size_t)batch * L * 2 * tn * T * T;
+}
+
+size_t gemm_scratch_floats(int64_t M, int64_t N, int64_t K, int batch, int max_wgs) {
+  if (M < 1 || N < 1 || K < 1 || batch < 1) return 0;
+  size_t f = 0;
+  for (int c = 0; c < 2; ++c) {
+    const int64_t L = sk_lanes_max(M, N, K, c == 1, max_wgs);
+    if (L >= 8) f = std::max(f, sk_floats(M, N, c == 1, batch, L));
+  }
+  return f;
+}
+
+static SkPlan sk_choose(int64_t M, int64_t N, int64_t K, int batch, int max_wgs, bool dp_mid,
+                        int dp_splits, size_t scratch_floats) {
+  SkPlan best;
+  const int bk = gemm_bb_bk();
+  const int64_t I = cdiv(K, (int64_t)bk);
+  // the data-parallel estimate
+  double t_dp;
+  {
+    const int T = gemm_bb_tile(dp_mid);
+    const int64_t wgs = cdiv(M, (int64_t)T) * cdiv(N, (int64_t)T) * dp_splits;
+    int64_t G = dp_mid ? 512 : 256;
+    if (max_wgs > 0) G = std::min<int64_t>(G, max_wgs);
+    const int64_t rounds = cdiv(wgs, G);
+    t_dp = (double)rounds * (double)cdiv(I, (int64_t)dp_splits) *
+           slab_us(dp_mid, std::min<int64_t>(wgs, G));
+    if (dp_splits > 1) t_dp += (double)dp_splits * (double)M * (double)N * 8.0 / 4.0e6 + 4.0;
+  }
+  double t_best = 0.9 * t_dp;   // stream-K only for a clear gain
+  for (int c = 0; c < 2; ++c) {
+    const bool mid = c == 1;
+    const int T = gemm_bb_tile(mid);
+    const int64_t tn = cdiv(N, (int64_t)T), tm = cdiv(M, (int64_t)T);
+    const int64_t U = tm * I;
+    for (int64_t L = sk_lanes_max(M, N, K, mid, max_wgs); L >= 8; L -= 8) {
+      const size_t need = sk_floats(M, N, mid, batch, L);
+      if (need > scratch_floats) continue;
+      const int64_t s = cdiv(U, L);   // slabs per lane
+      const double shares = s >= I ? 2.0 : (double)I / (double)s + 1.0;
+      const double t = (double)s * slab_us(mid, L * tn) +
+                       (mid ? 10.0 + 4.0 * shares : 12.0 + 11.0 * shares);
+      if (t < t_best) {
+        t_best = t;
+        best.lanes = (int)L;
+        best.mid = mid;
+        best.iters = (int)I;
+        best.cnt_floats = align_up((size_t)(batch * tm * tn), 64);
+        best.floats = need;
+      }
+    }
+  }
+  return best;
+}
+
 int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, const MatRef& A,
          const MatRef& B, float beta, const OutRef& C, int batch, SplitScratch scratch,
          int max_wgs) {
@@ -522,41 +630,6 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   const bool bb = big && A.dt == DT_BF16 && A.kc && B.dt == DT_BF16 && B.kc && p.vec_a &&
                   p.vec_b && K % 8 == 0 && A.ld < ((int64_t)1 << 21) &&
                   B.ld < ((int64_t)1 << 21);
-  // plain products: hipBLASLt, entry by entry (every entry gets the bits a
-  // batch of one gets): bf16 operands with K contiguous in bf16 arithmetic,
-  // fp32 operands in fp32 arithmetic, both large
-  const bool lib_f32 = math == MATH_F32 && A.dt == DT_F32 && B.dt == DT_F32 && M >= 192 &&
-                       N >= 192 && (double)M * (double)N * (double)K * batch >= 1e9;
-  if ((bb || lib_f32) && A.tri == TRI_NONE && B.tri == TRI_NONE && C.c && !C.cb &&
-      lib_gemm_enabled()) {
-    const size_t wsb = scratch.p ? scratch.floats * sizeof(float) : 0;
-    if (lib_gemm_plan(s, M, N, K, A.dt, A.ld, A.kc, B.dt, B.ld, B.kc, C.ldc, beta != 0.0f,
-                      wsb)) {
-      const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | (1 << 8);
-      ProfRec* pr = prof_slot(vid);
-      if (pr) {
-        pr->variant = vid;
-        pr->m = M;
-        pr->n = N;
-        pr->k = K;
-        pr->flops = 2.0 * (double)M * (double)N * (double)K * batch;
-        pr->bytes = ((double)M * K * (A.dt == DT_BF16 ? 2 : 4) +
-                     (double)K * N * (B.dt == DT_BF16 ? 2 : 4) +
-                     (double)M * N * (beta != 0.0f ? 8.0 : 4.0)) * batch;
-        hipEventRecord(pr->beg, s);
-      }
-      const size_t ea = A.dt == DT_BF16 ? 2 : 4, eb = B.dt == DT_BF16 ? 2 : 4;
-      for (int e = 0; e < batch; ++e) {
-        const int rc = lib_gemm_run(
-            s, M, N, K, alpha, (const char*)A.p + (size_t)e * A.bstride * ea, A.dt, A.ld, A.kc,
-            (const char*)B.p + (size_t)e * B.bstride * eb, B.dt, B.ld, B.kc, beta,
-            C.c + (size_t)e * C.bstride, C.ldc, scratch.p, wsb);
-        if (rc) return rc;
-      }
-      if (pr) hipEventRecord(pr->end, s);
-      return IFK_OK;
-    }
-  }
   // batch entries the tile and split-K choices are made for
   const int64_t bdec = C.per_entry ? 1 : batch;
   // split-K factor for a tile of TM x TN with BK-deep slabs
@@ -607,6 +680,23 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
       mid = true;
     }
   }
+  p.sk_lanes = 0;
+  p.sk_iters = 0;
+  p.sk_cnt = nullptr;
+  p.sk_part = nullptr;
+  if (bb && A.tri == TRI_NONE && B.tri == TRI_NONE && !p.upper_only &&
+      !(p.lower_only && M == N) && K >= SK_MIN_K && scratch.p && (C.per_entry || batch == 1)) {
+    const int T = gemm_bb_tile(mid);
+    const int dp_splits = split_for(T, T, gemm_bb_bk(), mid);
+    const SkPlan sk = sk_choose(M, N, K, batch, max_wgs, mid, dp_splits, scratch.floats);
+    if (sk.lanes > 0) {
+      mid = sk.mid;
+      p.sk_lanes = sk.lanes;
+      p.sk_iters = sk.iters;
+      p.sk_cnt = reinterpret_cast<int*>(scratch.p);
+      p.sk_part = scratch.p + sk.cnt_floats;
+    }
+  }
   const int TM = bb ? gemm_bb_tile(mid) : (big ? gemm_big_tile_m() : GBM);
   const int TN = bb ? gemm_bb_tile(mid) : (big ? gemm_big_tile_n() : GBN);
   p.tiles_m = (int)cdiv(M, TM);
@@ -615,7 +705,7 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
                     : big ? gemm_big_bk()
                           : (math == MATH_BF16 ? GCfg<MATH_BF16>::BK : GCfg<MATH_F32>::BK);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n * batch;
-  const int splits = split_for(TM, TN, BK, mid);
+  const int splits = p.sk_lanes > 0 ? 1 : split_for(TM, TN, BK, mid);
   p.splits = splits;
   p.part = splits > 1 ? scratch.p : nullptr;
   if (tiles * splits > 0x7fffffffLL || (int64_t)batch * splits > 65535) {
@@ -634,22 +724,33 @@ int gemm(hipStream_t s, int math, int64_t M, int64_t N, int64_t K, float alpha, 
   // the direct-to-LDS kernel orders its tiles by XCD when a z slice has a
   // multiple of eight workgroups (the rest of the tiles go grid-stride)
   if (bb && gx > 8) gx &= ~7u;
+  // stream-K: one workgroup per lane and tile column (the lanes were chosen
+  // for one entry within the cap), the arrival counters zeroed first
+  if (p.sk_lanes > 0) {
+    gx = (unsigned)(p.sk_lanes * p.tiles_n);
+    const int rc0 = launch_fill_int(s, p.sk_cnt, 0, (int)(batch * p.tiles_m * p.tiles_n));
+    if (rc0) return rc0;
+  }
   dim3 grid(gx, 1, (unsigned)(batch * splits));
   const int vid = gemm_variant_id(math, A.dt, A.kc, B.dt, B.kc) | ((big ? 1 : 0) << 5) |
-                  ((bb ? 1 : 0) << 6) | ((mid ? 1 : 0) << 7);
+                  ((bb ? 1 : 0) << 6) | ((mid ? 1 : 0) << 7) |
+                  ((p.sk_lanes > 0 ? 1 : 0) << 9);
   ProfRec* pr = prof_slot(vid);
   if (pr) {
-    // algorithmic work: 2 M N K (M N K when one operand is triangular), and the
-    // minimal traffic: each operand read once, C read (beta != 0) and written once
-    const double tri =
-        (A.tri != TRI_NONE || B.tri != TRI_NONE || p.upper_only || (p.lower_only && M == N))
-            ? 0.5
-            : 1.0;
+    // algorithmic work: 2 K times the wanted outputs (M N, or one triangle of
+    // them), halved when one operand is triangular; and the minimal traffic:
+    // each operand read once, C read (beta != 0) and written once
+    const double tri = (A.tri != TRI_NONE || B.tri != TRI_NONE) ? 0.5 : 1.0;
+    double live = (double)M * (double)N;
+    if (p.upper_only) live = (double)N * (double)(N + 1) / 2.0;
+    else if (p.lower_only)
+      live = M >= N ? (double)M * (double)N - (double)N * (double)(N - 1) / 2.0
+                    : (double)M * (double)(M + 1) / 2.0;
     pr->variant = vid;
     pr->m = M;
     pr->n = N;
     pr->k = K;
-    pr->flops = 2.0 * tri * (double)M * (double)N * (double)K * batch;
+    pr->flops = 2.0 * tri * live * (double)K * batch;
     const double sa = A.dt == DT_F32 ? 4 : 2, sb = B.dt == DT_F32 ? 4 : 2;
     double cb = (C.c ? 4.0 : 0.0) + (C.cb ? 2.0 : 0.0) + (beta != 0.0f ? 4.0 : 0.0);
     pr->bytes = ((double)M * K * sa + (double)K * N * sb + (double)M * N * cb) * batch;

@@ -244,32 +244,19 @@ __device__ __forceinline__ void pipe_loop(const GemmParams& p, f32x16_t (&acc)[C
   }
 }
 
-// TRI: a triangular operand (K range trimmed, slabs across the diagonal masked)
+// Products of tile (m0, n0) of entry bidx over K slabs [kt0, kt0 + n_it):
+// acc = A_tile B_tile^T (zero when n_it <= 0).  TRI: a triangular operand
+// (slabs across the diagonal masked).
 template <class CF, bool TRI>
-__device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf16_t* smem) {
+__device__ __forceinline__ void bb_acc(const GemmParams& p, int bidx, int64_t m0, int64_t n0,
+                                       int64_t kt0, int n_it, f32x16_t (&acc)[CF::FM][CF::FN],
+                                       bf16_t* smem) {
   constexpr int BM = CF::BM, BN = CF::BN, FM = CF::FM, FN = CF::FN;
   constexpr int STAGE = CF::STAGE, SLAB_A = CF::SLAB_A;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave / CF::WAVES_N, wn = wave % CF::WAVES_N;
   const int l32 = lane & 31, h = lane >> 5;
-  const int z = blockIdx.z;
-  const int bidx = z / p.splits, split = z % p.splits;
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  if (p.upper_only && m0 >= n0 + BN) return;   // wholly below the diagonal
-  if (p.lower_only && n0 >= m0 + BM) return;   // wholly above the diagonal
-
-  int64_t klo = 0, khi = p.K;
-  if (p.tria == TRI_UPPER) klo = max(klo, m0);
-  if (p.tria == TRI_LOWER) khi = min(khi, m0 + BM);
-  if (p.trib == TRI_UPPER) khi = min(khi, n0 + BN);
-  if (p.trib == TRI_LOWER) klo = max(klo, n0);
-  const int64_t kt_lo = klo / BK;
-  const int64_t nkt = khi > kt_lo * BK ? (khi - kt_lo * BK + BK - 1) / BK : 0;
-  const int64_t per = (nkt + p.splits - 1) / p.splits;
-  const int64_t kt0 = kt_lo + (int64_t)split * per;
-  const int64_t kt1 = min(kt_lo + nkt, kt0 + per);
-  const int n_it = (int)max((int64_t)0, kt1 - kt0);
 
   const bf16_t* Ab = (const bf16_t*)p.A + (size_t)bidx * p.bsa + m0 * p.lda;
   const bf16_t* Bb = (const bf16_t*)p.B + (size_t)bidx * p.bsb + n0 * p.ldb;
@@ -281,7 +268,6 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
   ab.init(p.ldb);
   const int kmax = (int)p.K;
 
-  f32x16_t acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -343,32 +329,29 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
       }
     }
   }
+}
 
-  // acc[i][j][r]: row (r / 4) * 8 + h * 4 + r % 4, column l32 of 32 x 32 tile (i, j)
-  if (p.splits > 1) {
-    float* P = p.part + ((size_t)(bidx * p.splits + split)) * (size_t)p.M * (size_t)p.N;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm * CF::WTM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-          const int64_t col = n0 + wn * CF::WTN + j * 32 + l32;
-          if (row < p.M && col < p.N) P[row * p.N + col] = acc[i][j][r];
-        }
-    return;
-  }
+// Tile (m0, n0) of entry bidx: C = alpha acc + beta C, and the bf16 copy.
+// acc[i][j][r] holds row (r / 4) * 8 + h * 4 + r % 4, column l32 of 32 x 32
+// tile (i, j) of the wave.  Uses the LDS ring (every wave must be past its
+// last fragment reads; the first barrier below sees to that).
+template <class CF>
+__device__ __forceinline__ void bb_store(const GemmParams& p, int bidx, int64_t m0, int64_t n0,
+                                         const f32x16_t (&acc)[CF::FM][CF::FN], bf16_t* smem) {
+  constexpr int BN = CF::BN, FM = CF::FM, FN = CF::FN;
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave / CF::WAVES_N, wn = wave % CF::WAVES_N;
+  const int l32 = lane & 31, h = lane >> 5;
   float* Cp = p.C ? p.C + (size_t)bidx * p.bsc : nullptr;
   bf16_t* Cbp = p.Cb ? p.Cb + (size_t)bidx * p.bscb : nullptr;
   if (p.vec_c) {
     // Through LDS, one 32-row band of each wave row at a time: the band is
     // read back row-contiguous, so C is read and written 16 bytes and the bf16
-    // copy 8 bytes per lane.  (The ring is free once every wave is past its
-    // last slab.)
+    // copy 8 bytes per lane.
     constexpr int LDB = BN + 4;                        // band row stride (floats)
     constexpr int V4 = BN / 4;                         // float4 per band row
-    static_assert(CF::WAVES_M * 32 * LDB * 4 <= STAGES * STAGE * 2, "band fits the ring");
+    static_assert(CF::WAVES_M * 32 * LDB * 4 <= STAGES * CF::STAGE * 2, "band fits the ring");
     float* band = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -436,6 +419,180 @@ __device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf1
     }
 }
 
+// One output tile, or one split-K share of it (grid.z = batch * splits).
+// TRI: a triangular operand (K range trimmed to the structural non-zeros).
+template <class CF, bool TRI>
+__device__ __forceinline__ void bb_tile(const GemmParams& p, int tm, int tn, bf16_t* smem) {
+  constexpr int BM = CF::BM, BN = CF::BN, FM = CF::FM, FN = CF::FN;
+  const int z = blockIdx.z;
+  const int bidx = z / p.splits, split = z % p.splits;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  if (p.upper_only && m0 >= n0 + BN) return;   // wholly below the diagonal
+  if (p.lower_only && n0 >= m0 + BM) return;   // wholly above the diagonal
+
+  int64_t klo = 0, khi = p.K;
+  if (p.tria == TRI_UPPER) klo = max(klo, m0);
+  if (p.tria == TRI_LOWER) khi = min(khi, m0 + BM);
+  if (p.trib == TRI_UPPER) khi = min(khi, n0 + BN);
+  if (p.trib == TRI_LOWER) klo = max(klo, n0);
+  const int64_t kt_lo = klo / BK;
+  const int64_t nkt = khi > kt_lo * BK ? (khi - kt_lo * BK + BK - 1) / BK : 0;
+  const int64_t per = (nkt + p.splits - 1) / p.splits;
+  const int64_t kt0 = kt_lo + (int64_t)split * per;
+  const int64_t kt1 = min(kt_lo + nkt, kt0 + per);
+  const int n_it = (int)max((int64_t)0, kt1 - kt0);
+
+  f32x16_t acc[FM][FN];
+  bb_acc<CF, TRI>(p, bidx, m0, n0, kt0, n_it, acc, smem);
+
+  if (p.splits > 1) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int wm = wave / CF::WAVES_N, wn = wave % CF::WAVES_N;
+    const int l32 = lane & 31, h = lane >> 5;
+    float* P = p.part + ((size_t)(bidx * p.splits + split)) * (size_t)p.M * (size_t)p.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm * CF::WTM + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+          const int64_t col = n0 + wn * CF::WTN + j * 32 + l32;
+          if (row < p.M && col < p.N) P[row * p.N + col] = acc[i][j][r];
+        }
+    return;
+  }
+  bb_store<CF>(p, bidx, m0, n0, acc, smem);
+}
+
+// Partial tile slot of a stream-K lane: slot `which` (0: the first tile row
+// the lane touches, 1: its last) of tile column col, entry bidx.  A slot holds
+// the workgroup's accumulators in register order, 16 bytes per thread.
+template <class CF>
+__device__ __forceinline__ float* sk_slot(const GemmParams& p, int bidx, int lane, int which,
+                                          int col) {
+  const size_t idx = (((size_t)bidx * p.sk_lanes + lane) * 2 + which) * p.tiles_n + col;
+  return p.sk_part + idx * (size_t)(CF::BM * CF::BN);
+}
+
+// A partial tile's buffer descriptor.  The shares move between workgroups
+// (on any XCD, each with its own L2) by device-scope stores and loads
+// (cache policy SC1, what relaxed agent-scope atomic stores and loads of the
+// memory model use): coherent without the L2 write-back and invalidation of
+// a device-scope fence.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int CPOL_SC1 = 16;
+template <class CF>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(float* S) {
+  return make_rsrc(S, (int64_t)CF::BM * CF::BN * 4);
+}
+
+// Stream-K walk of one workgroup (lane, tile column col): tile rows
+// u0 / I .. (u1 - 1) / I of its share [u0, u1) of the U = tiles_m * I
+// (row, slab) steps.  A tile whose K range lies wholly in the share is
+// stored directly.  Otherwise every lane that holds part of it stores its
+// partial tile by device-scope stores, waits for them to complete, and counts
+// itself in on the tile's counter (a device-scope atomic); the one that
+// arrives last reads the partials by device-scope loads, adds them in lane
+// order and stores the tile.  (The first lane of a row, which usually
+// arrives last, first looks at the counter and skips its own store when the
+// others are all in.)  Nobody waits for anybody, so the walk ends
+// whatever order the workgroups run in, and the sum's order does not depend
+// on the arrival order: the result is deterministic.
+template <class CF>
+__device__ __forceinline__ void bb_streamk(const GemmParams& p, bf16_t* smem, int* s_old) {
+  constexpr int BM = CF::BM, BN = CF::BN, FM = CF::FM, FN = CF::FN, NTH = CF::NTH;
+  const int tn_ = p.tiles_n, L = p.sk_lanes, I = p.sk_iters;
+  const int bidx = blockIdx.z;
+  // workgroup x runs on XCD x % 8: the lanes of one XCD take consecutive
+  // shares, so most shared tiles are summed within one L2
+  const int per_xcd = (int)(gridDim.x >> 3);
+  const int pos = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  const int lane = pos / tn_, col = pos - lane * tn_;
+  const int64_t U = (int64_t)p.tiles_m * I;
+  const int64_t u0 = (int64_t)lane * U / L, u1 = (int64_t)(lane + 1) * U / L;
+  const int64_t r_first = u0 / I;
+  const int t = threadIdx.x;
+  for (int64_t r = r_first; r * I < u1; ++r) {
+    const int64_t s0 = max(u0, r * I) - r * I, s1 = min(u1, (r + 1) * I) - r * I;
+    const int64_t m0 = r * BM, n0 = (int64_t)col * BN;
+    if (p.upper_only && m0 >= n0 + BN) continue;   // every lane skips the same tiles
+    if (p.lower_only && n0 >= m0 + BM) continue;
+    f32x16_t acc[FM][FN];
+    bb_acc<CF, false>(p, bidx, m0, n0, s0, (int)(s1 - s0), acc, smem);
+    // a tile wholly in this share is stored directly; a shared one by the
+    // last lane to arrive
+    bool store = true;
+    if (!(s0 == 0 && s1 == I)) {
+      const int lf = sk_lane_of(r * I, U, L), ll = sk_lane_of((r + 1) * I - 1, U, L);
+      int* cnt = p.sk_cnt + ((int64_t)bidx * p.tiles_m + r) * tn_ + col;
+      // The row's first lane usually arrives last: its share of the row ends
+      // its walk, the other lanes' shares begin (or make up) theirs.  When a
+      // look at the counter shows every other share in, it adds them to its
+      // own accumulators, which hold the first term of the sum, and stores
+      // nothing of its own.
+      int seen = -1;
+      if (lane == lf) {
+        if (t == 0) *s_old = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        seen = *s_old;
+        __syncthreads();
+      }
+      int first_mem = lf + 1;   // the first share read from memory
+      if (seen != ll - lf) {
+        first_mem = lf;
+        const __amdgpu_buffer_rsrc_t rs =
+            slot_rsrc<CF>(sk_slot<CF>(p, bidx, lane, r == r_first ? 0 : 1, col));
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              u32x4_t v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = __float_as_uint(acc[i][j][4 * q + e]);
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  v, rs, (unsigned)((((i * FN + j) * 4 + q) * NTH + t) * 16), 0, CPOL_SC1);
+            }
+        // the device-scope stores have completed (so every other lane sees
+        // them) before the count
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();
+        if (t == 0) *s_old = atomicAdd(cnt, 1);
+        __syncthreads();
+        store = *s_old == ll - lf;
+      }
+      if (store) {
+        // the shares in lane order by device-scope loads (the first lane's
+        // from its registers when it never stored it), summed into the
+        // accumulators: the same additions in the same order either way
+        for (int l = first_mem; l <= ll; ++l) {
+          const int wh = (r == ((int64_t)l * U / L) / I) ? 0 : 1;
+          const __amdgpu_buffer_rsrc_t rs = slot_rsrc<CF>(sk_slot<CF>(p, bidx, l, wh, col));
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(
+                    rs, (unsigned)((((i * FN + j) * 4 + q) * NTH + t) * 16), 0, CPOL_SC1);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  if (l == lf) acc[i][j][4 * q + e] = __uint_as_float(x[e]);
+                  else acc[i][j][4 * q + e] += __uint_as_float(x[e]);
+                }
+              }
+        }
+      }
+    }
+    if (store) bb_store<CF>(p, bidx, m0, n0, acc, smem);
+    __syncthreads();   // the ring and *s_old are reused by the next tile
+  }
+}
+
 // Tile order.  Workgroups go to the eight XCDs round-robin by their linear
 // id, and each XCD has its own L2, so with a multiple of eight workgroups per
 // z slice (workgroup x runs on XCD x % 8) XCD c takes the c-th eighth of the
@@ -465,9 +622,12 @@ __device__ __forceinline__ void tri_tile(int l, bool upper, int* tm, int* tn) {
 template <class CF>
 __global__ __launch_bounds__(CF::NTH, CF::OCC) void gemm_bb_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(16))) bf16_t smem_bb[STAGES * CF::STAGE];
+  __shared__ int s_old;
   const int tiles_m = p.tiles_m, tiles_n = p.tiles_n;
   const int tiles = tiles_m * tiles_n;
-  if ((p.upper_only || p.lower_only) && tiles_m == tiles_n && p.M == p.N) {
+  if (p.sk_lanes > 0) {
+    bb_streamk<CF>(p, smem_bb, &s_old);
+  } else if ((p.upper_only || p.lower_only) && tiles_m == tiles_n && p.M == p.N) {
     const int live = tiles_m * (tiles_m + 1) / 2;
     const bool xcd = (gridDim.x & 7) == 0;
     const int c = xcd ? (int)(blockIdx.x & 7) : 0, nl = xcd ? (int)(gridDim.x >> 3) : gridDim.x;

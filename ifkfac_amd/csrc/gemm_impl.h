@@ -19,7 +19,23 @@ struct GemmParams {
                // batch strides multiples of 4 elements: vector epilogue
   int upper_only;   // skip tiles wholly below the diagonal (square Gram output)
   int lower_only;   // skip tiles wholly above the diagonal
+  // Stream-K (direct-to-LDS kernel, neither operand triangular; splits == 1):
+  // sk_lanes > 0 lanes of tiles_n workgroups each (one per tile column) walk
+  // an equal contiguous share of the (tile row, K slab) space of a batch
+  // entry (grid.z), so every workgroup gets the same number of slabs however
+  // few tiles there are.  A tile shared by several lanes is summed by the
+  // last of them to arrive, in lane order, from the others' partial tiles.
+  int sk_lanes;
+  int sk_iters;     // K slabs per tile
+  int* sk_cnt;      // arrival counter per tile and entry, zero at launch
+  float* sk_part;   // partial tiles: two per lane, tile column and entry
 };
+
+// Lane of a stream-K walk over U (tile row, slab) steps with L lanes that
+// holds step u: lane l covers [l U / L, (l + 1) U / L).
+__host__ __device__ inline int sk_lane_of(int64_t u, int64_t U, int L) {
+  return (int)(((u + 1) * (int64_t)L - 1) / U);
+}
 
 // Tile t of a grid-stride walk -> (tile row, tile column), heaviest tiles
 // first when an operand is triangular: a tile's K range shrinks down the rows
@@ -52,7 +68,9 @@ void launch_gemm_big(hipStream_t s, dim3 grid, const GemmParams& p, int adt, boo
 
 // bf16 x bf16 kernel for K-contiguous operands with a four-slab
 // direct-to-LDS ring (gemm_bb.hip), square tile 256 (mid = false) or 128
-// (mid = true), BK 32; grid.x = tiles, grid.z = batch * splits.
+// (mid = true), BK 32; grid.x = tiles, grid.z = batch * splits; in
+// stream-K mode grid.x = sk_lanes * tiles_n (sk_lanes a multiple of 8) and
+// grid.z = batch.
 int gemm_bb_tile(bool mid);
 int gemm_bb_bk();
 void launch_gemm_bb(hipStream_t s, dim3 grid, const GemmParams& p, bool mid);

@@ -452,6 +452,12 @@ int cast_lower_t(hipStream_t s, int batch, const float* L, int64_t ldl, int64_t 
 // ---------------------------------------------------------------------------
 // Workspace (every buffer once per batch entry, at the stride s*)
 // ---------------------------------------------------------------------------
+// Workgroup caps of the helper streams' products: the chain's launches
+// (cholb's diagonal workgroup, the band products) must find CUs free while
+// the Gram columns and the panel work run beside them.
+constexpr int GRAM_MAX_WGS = 192;
+constexpr int REST_MAX_WGS = 192;
+
 struct GramWs {
   int64_t B;          // batch entries
   int64_t ldk;        // row stride of PT (pe rounded up to 8; the pad is zero)
@@ -517,23 +523,24 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w, bool inv =
   w.LB = a.take<bf16_t>((size_t)(B * w.sL));
   w.flag = a.take<int>((size_t)(B * FLAG_S));
   w.frob = a.take<float>((size_t)(B * w.sfrob));
-  // split-K partials for the products with one block column of output
-  w.sp.floats = (size_t)(B * std::min<int64_t>(n, 8 * GB) * GB * 2);
+  // split-K and stream-K partials of the products with one block column of
+  // output: the chain's band products (GB x GB, K = 3 GB), the helper's
+  // panel and column updates (up to n x GB, K up to 3 GB (nb - 1)) and the
+  // Gram columns (n x GB, K = pe).  Stream-K needs are per entry times B, so
+  // a batch takes the grid a batch of one takes (the same bits).
+  const int64_t kmax2 = 3 * GB * std::max<int64_t>(nb - 1, 1);
+  w.sp.floats = std::max((size_t)(B * std::min<int64_t>(n, 8 * GB) * GB * 2),
+                         (size_t)B * gemm_scratch_floats(GB, GB, 3 * GB, 1));
   w.sp.p = a.take<float>(w.sp.floats);
-  w.sp2.floats = (size_t)(B * std::min<int64_t>(n, 16 * GB) * GB * 2);
+  w.sp2.floats = std::max((size_t)(B * std::min<int64_t>(n, 16 * GB) * GB * 2),
+                          (size_t)B * gemm_scratch_floats(n, GB, kmax2, 1, REST_MAX_WGS));
   w.sp2.p = a.take<float>(w.sp2.floats);
-  w.sp3.floats = w.sp2.floats;
+  w.sp3.floats = std::max((size_t)(B * std::min<int64_t>(n, 16 * GB) * GB * 2),
+                          (size_t)B * gemm_scratch_floats(n, GB, std::max<int64_t>(pe, 1), 1,
+                                                          GRAM_MAX_WGS));
   w.sp3.p = a.take<float>(w.sp3.floats);
 }
 
-// Workgroup caps of the helper streams' products: the chain's launches
-// (cholb's diagonal workgroup, the band products) must find CUs free while
-// the Gram columns and the panel work run beside them.  They bind the
-// engine's own kernels only: the plain products that the GEMM dispatcher
-// sends to hipBLASLt (all of this file's large products, unless that is
-// switched off) launch their own grids.
-constexpr int GRAM_MAX_WGS = 192;
-constexpr int REST_MAX_WGS = 192;
 // Gram column c >= GRAM_LEAD starts only when helper step c - GRAM_LEAD is
 // done.  Unthrottled, the Gram stream runs far ahead of the chain and holds
 // its CUs for the whole first half of the factorisation, while the helper's

@@ -266,14 +266,7 @@ int look_ahead_release(hipStream_t s) {
     la = it->second;
     g_la.erase(it);
   }
-  if (!la) {
-    // no helper streams: the calling stream's own hipBLASLt state only
-    if (hipStreamSynchronize(s) != hipSuccess) {
-      set_error("release_stream_state: stream synchronize failed");
-      return IFK_ERR_HIP;
-    }
-    return lib_gemm_release(s);
-  }
+  if (!la) return IFK_OK;   // no helper streams were made for this stream
   bool ok = true;
   {
     std::lock_guard<std::mutex> l(la->mu);
@@ -281,9 +274,6 @@ int look_ahead_release(hipStream_t s) {
     // events, must finish before the streams and events go
     for (hipStream_t h : {la->s2, la->s3, s})
       if (h) ok = hipStreamSynchronize(h) == hipSuccess && ok;
-    // the hipBLASLt handles and plans of the three streams
-    for (hipStream_t h : {la->s2, la->s3, s})
-      if (h) ok = lib_gemm_release(h) == IFK_OK && ok;
     for (hipEvent_t e : la->col)
       if (e) ok = hipEventDestroy(e) == hipSuccess && ok;
     for (hipEvent_t e : {la->done, la->ready[0], la->ready[1], la->nearwp[0], la->nearwp[1],

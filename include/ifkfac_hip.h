@@ -51,8 +51,7 @@ const char* ifk_last_error(void);
 /*
  * Release the helper streams and events that the factorisations of more than
  * 1024 columns create for (current device, calling stream) on first use and
- * otherwise keep until the process ends, and the hipBLASLt handles and plans
- * kept for the calling stream and those helpers.  No counterpart in the
+ * otherwise keep until the process ends.  No counterpart in the
  * reference (torch manages its own streams): it is for callers that create
  * many calling streams over a process's life.  Waits for the stream's and its
  * helpers' queued work; a later call on the stream creates them again.  Not
@@ -467,15 +466,15 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
 /*
  * Measurement support (no counterpart in the reference; used by bench.py).
  * ifk_profile_begin(v) arms the GEMM launch profiler for GEMM variant v
- * (v = (lib << 8) | (mid << 7) | (direct << 6) | (large_tile << 5) | (math << 4) |
- * (a_dtype << 3) | (a_k_contiguous << 2) | (b_dtype << 1) | b_k_contiguous;
- * large_tile marks the bf16 kernels with the large tiles, direct the one that
- * loads operands straight into LDS, gemm_bb_kernel, and mid its 128 x 128
- * tile; large_tile alone gemm_big_kernel, neither gemm_kernel; lib a plain
- * bf16 product run by hipBLASLt), for every variant with v = -2, for every
- * launch of gemm_big_kernel with v = -3, of gemm_kernel with v = -4, of
- * gemm_bb_kernel with its 256 x 256 tile with v = -5 and with its 128 x 128
- * tile with v = -6, of hipBLASLt with v = -7; v = -1 disarms.
+ * (v = (streamk << 9) | (mid << 7) | (direct << 6) | (large_tile << 5) |
+ * (math << 4) | (a_dtype << 3) | (a_k_contiguous << 2) | (b_dtype << 1) |
+ * b_k_contiguous; large_tile marks the bf16 kernels with the large tiles,
+ * direct the one that loads operands straight into LDS, gemm_bb_kernel, mid
+ * its 128 x 128 tile and streamk a launch of it that walks the tiles
+ * stream-K; large_tile alone gemm_big_kernel, neither gemm_kernel), for
+ * every variant with v = -2, for every launch of gemm_big_kernel with v = -3,
+ * of gemm_kernel with v = -4, of gemm_bb_kernel with its 256 x 256 tile with
+ * v = -5 and with its 128 x 128 tile with v = -6; v = -1 disarms.
  * Each armed launch is bracketed by two HIP events on its own stream.
  * ifk_profile_end() disarms, waits for the events and returns the number of
  * launches recorded; ifk_profile_get(i, ...) returns launch i's variant,
@@ -484,18 +483,6 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
 int ifk_profile_begin(int variant);
 int ifk_profile_end(int64_t* n_launches);
 
-/*
- * No counterpart in the reference (measurement and test support).
- * ifk_set_gemm_library(on) chooses where the plain products (neither operand
- * triangular, an fp32 result only; bf16 operands with K contiguous in bf16
- * arithmetic -- the Gram route's Gram columns and panel and band updates --
- * and large fp32 products in fp32 arithmetic) run for the calls enqueued
- * after it: on = 1 hipBLASLt (the default; the environment variable IFK_GEMM_LIB=0
- * makes 0 the default), on = 0 this library's own kernels.  Returns the
- * previous setting.  Process-wide; results agree within rounding (the
- * summation order differs), not bit for bit.
- */
-int ifk_set_gemm_library(int on);
 int ifk_profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,
                     int64_t* n, int64_t* k);
 

@@ -325,8 +325,8 @@ def test_fold_finalize_gram_inverse(hip, B, prev, p, n, odt):
 
 def test_release_stream_state(hip):
     """ifk_release_stream_state: a stream's helper set (three streams and their
-    events) and the hipBLASLt handles and plans of those streams released between
-    two factorisations of more than 1024 columns give the second the same bits;
+    events) released between two factorisations of more than 1024 columns gives
+    the second the same bits;
     releasing a stream with no set, or twice, is a no-op."""
     g = torch.Generator(device=DEV).manual_seed(41)
     X = torch.randn(4000, 3100, device=DEV, generator=g).to(torch.bfloat16)
@@ -344,12 +344,12 @@ def test_release_stream_state(hip):
     hip.release_stream_state(DEV, torch.cuda.Stream())
 
 
-def test_gram_route_plain_products_library_and_own_kernels(hip):
-    """The Gram route's plain products (Gram columns, band and panel updates) run on
-    hipBLASLt by default and on this library's kernels after
-    ifk_set_gemm_library(0): both factors meet the closed-form bound, agree with
-    each other to the same bound (the summation order differs, so not bit for bit),
-    and the launch profiler sees hipBLASLt calls only in the first run."""
+def test_gram_route_products_own_kernel(hip):
+    """The Gram route's large products (Gram columns, band and panel updates: N =
+    1024 column blocks) run on this library's direct-to-LDS kernel (variant bit
+    6), data-parallel or stream-K (bit 9) as the dispatcher estimates faster
+    (at n = 3100, p = 4000 every one is short enough for data-parallel), and
+    the factor meets the fp64 closed form at 3e-5."""
     import ctypes
     from ifkfac_amd import _lib
     lib = _lib.load()
@@ -358,35 +358,38 @@ def test_gram_route_plain_products_library_and_own_kernels(hip):
     X = torch.randn(p, n, device=DEV, generator=g).to(torch.bfloat16)
     Xd = _bf16_np(X)
     Ro = np.linalg.cholesky(Xd.T @ Xd / p + 1e-2 * np.eye(n)).T
-    out, calls = {}, {}
-    prev = lib.ifk_set_gemm_library(1)
-    try:
-        for on in (1, 0):
-            lib.ifk_set_gemm_library(on)
-            torch.cuda.synchronize()
-            _lib.check(lib.ifk_profile_begin(-7), "profile_begin")
-            R, st = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), 1e-2, torch.float32, 1,
-                                      gram=True)
-            torch.cuda.synchronize()
-            cnt = ctypes.c_int64(0)
-            _lib.check(lib.ifk_profile_end(ctypes.byref(cnt)), "profile_end")
-            assert int(st.reshape(-1)[0].item()) == 1
-            out[on], calls[on] = R.double().cpu().numpy(), cnt.value
-    finally:
-        lib.ifk_set_gemm_library(prev)
-    print(f"hipBLASLt calls {calls[1]} / {calls[0]}; closed form {_gram_rel(out[1], Ro):.2e} / "
-          f"{_gram_rel(out[0], Ro):.2e}; mutual {_gram_rel(out[1], out[0]):.2e}")
-    assert calls[1] > 0 and calls[0] == 0
-    for on in (1, 0):
-        assert _gram_rel(out[on], Ro) <= 3e-5
-    assert _gram_rel(out[1], out[0]) <= 6e-5
+    torch.cuda.synchronize()
+    _lib.check(lib.ifk_profile_begin(-2), "profile_begin")
+    R, st = hip.fold_finalize(None, 0, X, 1 / math.sqrt(p), 1e-2, torch.float32, 1, gram=True)
+    torch.cuda.synchronize()
+    cnt = ctypes.c_int64(0)
+    _lib.check(lib.ifk_profile_end(ctypes.byref(cnt)), "profile_end")
+    v, ms, fl, by = ctypes.c_int(), ctypes.c_float(), ctypes.c_double(), ctypes.c_double()
+    m_, n_, k_ = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    variants = []
+    for i in range(cnt.value):
+        _lib.check(lib.ifk_profile_get(i, *(ctypes.byref(x) for x in (v, ms, fl, by, m_, n_, k_))),
+                   "profile_get")
+        variants.append((v.value, m_.value, n_.value, k_.value))
+    assert int(st.reshape(-1)[0].item()) == 1
+    sk = [x for x in variants if (x[0] >> 9) & 1]
+    print(f"{len(variants)} GEMM launches, {len(sk)} stream-K; closed form "
+          f"{_gram_rel(R.double().cpu().numpy(), Ro):.2e}")
+    assert len(variants) >= 10
+    # the dispatcher's rule: products of 1e9 multiply-adds or more on the
+    # direct-to-LDS kernel (the ragged last block's smaller ones on the
+    # 128 x 128 engine)
+    big = [x for x in variants if x[1] * x[2] * x[3] >= 1e9]
+    assert len(big) >= 8 and all((x[0] >> 6) & 1 for x in big)
+    assert _gram_rel(R.double().cpu().numpy(), Ro) <= 3e-5
 
 
 def test_gram_route_repeated_folds_identical(hip):
     """Ten folds of the same chunk into the same square factor, each a Gram-route
     factorisation on three streams (n = 3072: the helper and Gram streams run
-    hipBLASLt products beside the chain), give identical bits: the streams'
-    library calls share no handle state and no workspace."""
+    stream-K products beside the chain), give identical bits: each stream has
+    its own counters and partial tiles, and a stream-K tile's sum does not
+    depend on the order its shares arrive in."""
     g = torch.Generator(device=DEV).manual_seed(31)
     n, p = 3072, 4096
     R0 = torch.zeros(n, n, device=DEV)

@@ -118,6 +118,52 @@ def test_gemm_direct_lds_epilogue(hip, m, n, k, ldc_pad):
     assert torch.equal(buf[:, n:], pad)   # the columns past n are untouched
 
 
+def _gemm_variants(fn):
+    """Run fn with the GEMM launch profiler armed for every variant; returns
+    (fn's result, [(variant, m, n, k), ...])."""
+    import ctypes
+    from ifkfac_amd import _lib
+    lib = _lib.load()
+    torch.cuda.synchronize()
+    _lib.check(lib.ifk_profile_begin(-2), "profile_begin")
+    try:
+        out = fn()
+        torch.cuda.synchronize()
+    finally:
+        cnt = ctypes.c_int64(0)
+        _lib.check(lib.ifk_profile_end(ctypes.byref(cnt)), "profile_end")
+    v, ms, fl, by = ctypes.c_int(), ctypes.c_float(), ctypes.c_double(), ctypes.c_double()
+    m_, n_, k_ = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    res = []
+    for i in range(cnt.value):
+        _lib.check(lib.ifk_profile_get(i, *(ctypes.byref(x) for x in (v, ms, fl, by, m_, n_, k_))),
+                   "profile_get")
+        res.append((v.value, m_.value, n_.value, k_.value))
+    return out, res
+
+
+@pytest.mark.parametrize("m,n,k", [(9984, 1024, 16384), (10000, 1000, 16000), (9000, 777, 12000),
+                                   (3000, 1000, 9000)])
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_gemm_stream_k(hip, m, n, k, beta):
+    """Plain bf16 products with few output tiles and a long K (the Gram
+    route's Gram columns: N = 1024, K = p; ragged edges; the last on the 128
+    tile) take the stream-K walk of the direct-to-LDS kernel: against an
+    fp64 product of the same bf16 operands at 2e-6, and bit for bit equal on
+    a second call (a shared tile's shares are summed in lane order, whatever
+    order they arrive in)."""
+    g = torch.Generator(device=DEV).manual_seed(m + 11 * n + 3 * k)
+    A = torch.randn(m, k, device=DEV, generator=g).to(torch.bfloat16)
+    B = torch.randn(n, k, device=DEV, generator=g).to(torch.bfloat16)
+    C0 = torch.randn(m, n, device=DEV, generator=g)
+    ref = 0.5 * (A.double() @ B.double().t()) + beta * C0.double()
+    C1, var = _gemm_variants(lambda: hip.gemm(A, B, False, True, 1, 0.5, beta, C0.clone()))
+    C2 = hip.gemm(A, B, False, True, 1, 0.5, beta, C0.clone())
+    assert len(var) == 1 and (var[0][0] >> 9) & 1 and (var[0][0] >> 6) & 1
+    assert _rel(C1, ref.cpu().numpy()) < 2e-6
+    assert torch.equal(C1, C2)
+
+
 @pytest.mark.parametrize("tri", ["upper_a", "lower_b", "upper_b"])
 @pytest.mark.parametrize("n,rows", [(1280, 1100), (4096, 3600)])
 def test_gemm_direct_lds_triangular(hip, tri, n, rows):
