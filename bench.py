@@ -16,13 +16,21 @@ Headline workload: Linear 4096 -> 11008 at p = 16384 rows, inputs resident in
 HBM.  value = algorithmic TFLOP/s of the step, with the algorithmic count
 2 p (n_in^2 + n_out^2) + 2 n_out n_in (n_in + n_out).
 
+roofline: the dominant kernel of the workload -- the family with the largest
+summed launch time in a survey step with every GEMM launch and every
+block-Cholesky step bracketed by HIP events on its own stream -- timed over
+the timed steps: algorithmic work per launch over its average launch time,
+against the bf16 MFMA, fp32 MFMA or HBM peak as its intensity says.
+
 Extra keys on the same JSON line (unless --no-extras): the other benchmark
 layers (Linear 1024 -> 1024 streamed over 8 chunks, 4096 -> 4096 at p = 8192,
-11008 -> 4096 at p = 16384, one ViT-B block's capture folds), IFKFAC.step()
-itself on a Linear(4096, 11008) model and on the 4 x (Linear(4096, 4096) +
-GELU) stack, the same step in fp32 arithmetic (the reference's regime),
-the step under the default hardware-queue count (child process), kappa of
-the damped factors, and a roofline per phase.
+11008 -> 4096 at p = 16384, one ViT-B block's capture folds), each with the
+roofline of its own dominant kernel, IFKFAC.step() itself on a
+Linear(4096, 11008) model and on the 4 x (Linear(4096, 4096) + GELU) stack,
+the same step in fp32 arithmetic (the reference's regime), the step under the
+default hardware-queue count (child process), kappa of the damped factors,
+and a roofline per phase.  --workload measures one of the other layers as the
+line's own workload (for its kernel-trace and counter runs).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        [--no-extras] [--factor-path gram|cqr|panel]
@@ -59,18 +67,21 @@ METRIC = "ms per factor-update + precond step per layer; bf16 TFLOP/s vs MFMA pe
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_F32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per launch of the dominant kernel on the headline workload, from
-# two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same
-# counters on a 256 MiB copy (profiles/pmc_traffic_linear4096x11008_p16384.txt);
-# None for other workloads and factor paths.
-TRAFFIC = {("linear_4096x11008_p16384", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"): 1263.74e6}
+# HBM bytes per launch of a workload's dominant kernel, from two rocprofv3
+# --pmc runs (FETCH_SIZE, WRITE_SIZE) of that workload, scaled by the same
+# counters on a 256 MiB copy (profiles/pmc_traffic_*.txt), keyed by
+# (workload, factor path, kernel); None where no counter run was made.
+TRAFFIC = {}
 
 WORKLOADS = {
-    # name: (n_in, n_out, p)
-    "linear_4096x11008_p16384": (4096, 11008, 16384),
-    "linear_11008x4096_p16384": (11008, 4096, 16384),
-    "linear_4096x4096_p8192": (4096, 4096, 8192),
-    "linear_1024x1024_p4096": (1024, 1024, 4096),
+    # name: (n_in, n_out, p, chunks) of a Linear layer's step, or ("vit",) for
+    # one ViT-B block's capture folds
+    "linear_4096x11008_p16384": (4096, 11008, 16384, 1),
+    "linear_11008x4096_p16384": (11008, 4096, 16384, 1),
+    "linear_4096x4096_p8192": (4096, 4096, 8192, 1),
+    "linear_1024x1024_p4096": (1024, 1024, 4096, 1),
+    "linear_1024x1024_p4096_8_chunks": (1024, 1024, 4096, 8),
+    "vit_b_block_capture_p4096": ("vit",),
 }
 
 
@@ -149,10 +160,10 @@ def cpu_baseline(threads: int):
         ref_recipe.factor_update_precond_step([X], [D], grad, W, None, 1e-3, 0.9, 1e-2, True)
         return time.perf_counter() - t0
 
-    n_in, n_out, p = WORKLOADS["linear_4096x11008_p16384"]
+    n_in, n_out, p = WORKLOADS["linear_4096x11008_p16384"][:3]
     dt = one(n_in, n_out, p, 0)
     fl = algorithmic_flops(n_in, n_out, p)
-    s_in, s_out, s_p = WORKLOADS["linear_4096x4096_p8192"]
+    s_in, s_out, s_p = WORKLOADS["linear_4096x4096_p8192"][:3]
     one(s_in, s_out, s_p, 1)   # warm-up
     reps = sorted(one(s_in, s_out, s_p, 2 + i) for i in range(3))
     med = reps[1]
@@ -286,30 +297,207 @@ def timed(fn, steps, warmup):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+# ----------------------------------------------------------------------------
+# launch profiler: every GEMM launch and every block-Cholesky step of the
+# library bracketed by HIP events on its own stream (ifk_profile_*)
+# ----------------------------------------------------------------------------
+# family -> (kernel name as rocprofv3 prints it, what it is, bound)
+FAMILIES = {
+    0: ("gemm_kernel", "128x128 MFMA GEMM engine", "mfma"),
+    1: ("gemm_big_kernel", "256x128x32 bf16 MFMA GEMM, register staged", "mfma"),
+    2: ("gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>",
+        "256x256x32 bf16 MFMA GEMM, direct-to-LDS ring (data-parallel or stream-K)", "mfma"),
+    3: ("gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2, false>>",
+        "128x128x32 bf16 MFMA GEMM, direct-to-LDS ring (data-parallel or stream-K)", "mfma"),
+    5: ("cholb_first_kernel", "first launch of the 1024-block Cholesky (fp32 MFMA)", "mfma_f32"),
+    6: ("cholb_step_kernel",
+        "one 64-column step of the 1024-block Cholesky with its inverse (fp32 MFMA)", "mfma_f32"),
+}
+ARM = {0: -4, 1: -3, 2: -5, 3: -6, 5: -7, 6: -8}
+KVID = 1 << 12
+
+
+def family(vid: int) -> int:
+    if vid >= KVID:
+        return 5 + (vid - KVID)
+    if (vid >> 6) & 1:
+        return 3 if (vid >> 7) & 1 else 2
+    return (vid >> 5) & 1
+
+
+def read_profile(lib, count: int) -> list:
+    """(variant, ms, algorithmic flops, algorithmic bytes) of each recorded launch."""
+    from ifkfac_amd import _lib
+    C = _lib.ctypes
+    v, ms, fl, by = C.c_int(0), C.c_float(0), C.c_double(0), C.c_double(0)
+    m_, n_, k_ = C.c_int64(0), C.c_int64(0), C.c_int64(0)
+    recs = []
+    for i in range(count):
+        _lib.check(lib.ifk_profile_get(i, *(C.byref(x) for x in (v, ms, fl, by, m_, n_, k_))),
+                   "profile_get")
+        recs.append((v.value, ms.value, fl.value, by.value))
+    return recs
+
+
+def profiled(lib, arm: int, fn) -> list:
+    """Run fn with the launch profiler armed (arm as ifk_profile_begin takes it)."""
+    import torch
+    from ifkfac_amd import _lib
+    torch.cuda.synchronize()
+    _lib.check(lib.ifk_profile_begin(arm), "profile_begin")
+    try:
+        fn()
+        torch.cuda.synchronize()
+    finally:
+        n = _lib.ctypes.c_int64(0)
+        _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
+    return read_profile(lib, n.value)
+
+
+def per_family(recs: list, steps: int) -> dict:
+    out = {}
+    for vid, ms, fl, by in recs:
+        a = out.setdefault(family(vid), [0.0, 0, 0.0, 0.0])
+        a[0] += ms / steps
+        a[1] += 1.0 / steps
+        a[2] += fl
+        a[3] += by
+    return out
+
+
+def roofline(fam: int, recs: list, steps: int, ms_per_step: float, traffic_key=None) -> dict:
+    """Roofline of one kernel family over the given launches: algorithmic work per
+    launch over the launches' average event-measured duration."""
+    name, desc, bound = FAMILIES[fam]
+    tot_ms = sum(r[1] for r in recs)
+    tot_fl = sum(r[2] for r in recs)
+    tot_by = sum(r[3] for r in recs)
+    n = max(len(recs), 1)
+    if bound == "mfma_f32":
+        peak, bf16_share = PEAK_F32_TFLOPS, 0.0
+    else:
+        bf16_share = sum(r[2] for r in recs if (r[0] >> 4) & 1) / max(tot_fl, 1.0)
+        peak = PEAK_BF16_TFLOPS if bf16_share >= 0.5 else PEAK_F32_TFLOPS
+    intensity = tot_fl / max(tot_by, 1.0)
+    ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if intensity < ridge:
+        ach = tot_by / (tot_ms * 1e-3) / 1e9
+        r = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+             "frac": round(ach / PEAK_HBM_GBS, 4)}
+    else:
+        ach = tot_fl / (tot_ms * 1e-3) / 1e12
+        r = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+             "frac": round(ach / peak, 4)}
+    r.update({
+        "traffic": TRAFFIC.get(traffic_key + (name,)) if traffic_key else None,
+        "kernel": f"{name} ({desc})",
+        "bf16_share_of_flops": round(bf16_share, 3),
+        "launches_per_step": round(len(recs) / steps, 1),
+        "avg_launch_ms": round(tot_ms / n, 4),
+        "share_of_step": round(tot_ms / steps / ms_per_step, 3),
+        "algorithmic_flops_per_launch": round(tot_fl / n),
+        "algorithmic_bytes_per_launch": round(tot_by / n),
+    })
+    return r
+
+
+def measure(lib, step, steps: int, warmup: int, traffic_key=None, marks=None):
+    """warmup steps; one survey step with every family armed (the dominant
+    family: the largest summed launch time per step, as a kernel-trace summary
+    ranks kernels); then the timed steps with that family armed.  Returns
+    (ms_per_step, roofline of the dominant family, survey table, phases)."""
+    import torch
+    for i in range(warmup):
+        step(i == 0)
+    torch.cuda.synchronize()
+    ev = []
+
+    def mark():
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        ev.append(e)
+    survey = per_family(profiled(lib, -2, lambda: step(False, mark)), 1)
+    phases = None
+    if marks:
+        torch.cuda.synchronize()
+        phases = {marks[i]: round(ev[i].elapsed_time(ev[i + 1]), 3) for i in range(len(marks))}
+    fam = max(survey, key=lambda f: survey[f][0])
+    timing = {}
+
+    def run():
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(False)
+        torch.cuda.synchronize()
+        timing["ms"] = (time.perf_counter() - t0) * 1e3 / steps
+    recs = profiled(lib, ARM[fam], run)
+    ms = timing["ms"]
+    table = {FAMILIES[f][0]: {"ms_per_step": round(a[0], 3), "launches": round(a[1], 1),
+                              "tflops": round(a[2] / (a[0] * 1e-3) / 1e12, 2) if a[0] else None}
+             for f, a in sorted(survey.items(), key=lambda kv: -kv[1][0])}
+    return ms, roofline(fam, recs, steps, ms, traffic_key), table, phases
+
+
+class VitCapture:
+    """One ViT-B block's factor capture per step: the folds of one 4096-row batch
+    into the running factors of both sides of qkv 768->2304, proj 768->768,
+    fc1 768->3072 and fc2 3072->768 (bf16 arithmetic, the Gram route with the
+    panel fold for a refused fold), as the hooks issue them."""
+
+    shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
+    rows = 4096
+
+    def __init__(self, be, seed=13):
+        import torch
+        from ifkfac_amd._backend import MATH_BF16
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        self.be = be
+        self.Rs, self.chunks = [], []
+        for (a, b) in self.shapes:
+            for nn_ in (a, b):
+                R = torch.zeros(nn_, nn_, device="cuda")
+                T = torch.randn(self.rows, nn_, device="cuda", generator=g)
+                be.fold_(R, 0, T, MATH_BF16)
+                self.Rs.append(R)
+                self.chunks.append(T)
+        self.flops = sum(2.0 * self.rows * nn_ ** 2 for (a, b) in self.shapes for nn_ in (a, b))
+
+    def step(self, first, mark=lambda: None):
+        from ifkfac_amd._backend import MATH_BF16
+        from ifkfac_amd.activation_hooks import fold_chunk
+        mark()
+        for R, T in zip(self.Rs, self.chunks):
+            fold_chunk(R, R.shape[0], T, MATH_BF16)
+        mark()
+
+
 def extras(be, args, head_kappa):
-    """The other benchmark layers and IFKFAC.step() itself (see the module doc)."""
+    """The other benchmark layers, each with the roofline of its dominant kernel,
+    and IFKFAC.step() itself (see the module doc)."""
     import torch
     import torch.nn as nn
     from ifkfac_amd import IFKFAC
     from ifkfac_amd._backend import MATH_BF16
-    from ifkfac_amd.activation_hooks import fold_chunk
+    lib = be.lib
     res = {}
     steps, warm = max(3, args.steps // 2), 2
 
     def layer(name, n_in, n_out, p, chunks=1, math_=1):
         c = LayerChain(be, n_in, n_out, p, args.factor_path, math_=math_, chunks=chunks)
-        ms = timed(c.step, steps, warm)
+        ms, roof, table, _ = measure(lib, c.step, steps, warm, (name, args.factor_path))
         del c
         torch.cuda.empty_cache()
         return {"ms_per_step": round(ms, 3),
-                "tflops": round(algorithmic_flops(n_in, n_out, p) / ms / 1e9, 1)}
+                "tflops": round(algorithmic_flops(n_in, n_out, p) / ms / 1e9, 1),
+                "roofline": roof, "kernels": table}
 
     res["layers"] = {
-        "linear_1024x1024_p4096_8_chunks": layer("c2", 1024, 1024, 4096, chunks=8),
-        "linear_4096x4096_p8192": layer("c3", 4096, 4096, 8192),
-        "linear_11008x4096_p16384": layer("c4b", 11008, 4096, 16384),
+        "linear_1024x1024_p4096_8_chunks": layer("linear_1024x1024_p4096_8_chunks", 1024, 1024,
+                                                 4096, chunks=8),
+        "linear_4096x4096_p8192": layer("linear_4096x4096_p8192", 4096, 4096, 8192),
+        "linear_11008x4096_p16384": layer("linear_11008x4096_p16384", 11008, 4096, 16384),
     }
-    h_in, h_out, h_p = WORKLOADS["linear_4096x11008_p16384"]
+    h_in, h_out, h_p = WORKLOADS["linear_4096x11008_p16384"][:3]
     res["fp32_arithmetic"] = dict(layer("fp32", h_in, h_out, h_p, math_=0), **{
         "note": "the headline step in fp32 arithmetic (CholeskyQR2 fp32 factor update, fp32 "
                 "inverses and solves): the reference's regime"})
@@ -361,45 +549,31 @@ def extras(be, args, head_kappa):
     del mlp, layers, x, tgt
     torch.cuda.empty_cache()
 
-    # one ViT-B block's factor capture: the folds of one 4096-row batch (both
-    # sides of qkv 768->2304, proj 768->768, fc1 768->3072, fc2 3072->768) into
-    # running factors, then get_factors() once
-    shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
-    rows = 4096
-    g = torch.Generator(device="cuda").manual_seed(13)
-    Rs, chunks = [], []
-    for (a, b) in shapes:
-        for nn_ in (a, b):
-            R = torch.zeros(nn_, nn_, device="cuda")
-            T = torch.randn(rows, nn_, device="cuda", generator=g)
-            be.fold_(R, 0, T, MATH_BF16)
-            Rs.append(R)
-            chunks.append(T)
-
-    def batch(_first):
-        for R, T in zip(Rs, chunks):
-            fold_chunk(R, R.shape[0], T, MATH_BF16)
-    ms_b = timed(batch, steps, warm)
-    fl_b = sum(2.0 * rows * nn_ ** 2 for (a, b) in shapes for nn_ in (a, b))
+    # one ViT-B block's factor capture per batch, then get_factors() once
+    cap = VitCapture(be)
+    ms_b, roof_b, table_b, _ = measure(lib, cap.step, steps, warm,
+                                       ("vit_b_block_capture_p4096", args.factor_path))
+    rows = cap.rows
 
     def finalize_all(_first):
         # as get_factors() in bf16 arithmetic: every side by the Gram route,
         # one host read of the flags, the panel finalize for a side flagged 2
         out = [be.fold_finalize(None, 0, R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16,
-                                MATH_BF16, gram=True) for R in Rs]
+                                MATH_BF16, gram=True) for R in cap.Rs]
         st = torch.cat([f for _, f in out]).cpu()
-        for i, R in enumerate(Rs):
+        for i, R in enumerate(cap.Rs):
             if int(st[i]) == 2:
                 be.finalize(R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16, MATH_BF16)
     ms_f = timed(finalize_all, 3, 1)
     res["vit_b_block_capture_p4096"] = {
-        "ms_per_batch": round(ms_b, 3), "tflops_per_batch": round(fl_b / ms_b / 1e9, 1),
+        "ms_per_batch": round(ms_b, 3), "tflops_per_batch": round(cap.flops / ms_b / 1e9, 1),
+        "roofline": roof_b, "kernels": table_b,
         "ms_get_factors": round(ms_f, 3),
         "note": "8 folds of 4096 rows per batch into running factors (bf16 arithmetic, "
                 "the Gram route with the panel fold for a refused fold); 200 batches x 12 "
                 "blocks take 2400 x ms_per_batch; get_factors() of the 8 sides by the Gram "
                 "route"}
-    del Rs, chunks
+    del cap
     torch.cuda.empty_cache()
     res["kappa_R_damped_headline"] = head_kappa
     return res
@@ -430,7 +604,8 @@ def main() -> int:
         return 2
 
     child = None
-    if not args.no_extras and not args.hw_queues_default:
+    if (not args.no_extras and not args.hw_queues_default and
+            args.workload == "linear_4096x11008_p16384"):
         child = default_queue_child(args)   # before this process initialises HIP
 
     import torch
@@ -439,7 +614,6 @@ def main() -> int:
 
     be = _backend.get_backend()
     lib = be.lib
-    n_in, n_out, p = WORKLOADS[args.workload]
     torch.cuda.set_device(0)
 
     if args.calib_copy_mib > 0:
@@ -450,138 +624,72 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    chain = LayerChain(be, n_in, n_out, p, args.factor_path)
-    phase_names = ["factor_update_and_inverse", "precondition", "update"]
-    nph = len(phase_names)
+    wl = WORKLOADS[args.workload]
+    if wl[0] == "vit":
+        runner = VitCapture(be)
+        flops = runner.flops
+        marks = ["folds"]
+        desc = ("ViT-B block factor capture: the folds of one 4096-row batch into the running "
+                "factors of qkv 768->2304, proj 768->768, fc1 768->3072, fc2 3072->768 (both "
+                "sides, bf16 arithmetic)")
+        cfg = {"rows_per_batch": VitCapture.rows, "sides": 8}
+    else:
+        n_in, n_out, p, chunks = wl
+        runner = LayerChain(be, n_in, n_out, p, args.factor_path, chunks=chunks)
+        flops = algorithmic_flops(n_in, n_out, p)
+        marks = ["factor_update_and_inverse", "precondition", "update"]
+        desc = (f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, p={p} rows"
+                + (f" in {chunks} streamed chunks" if chunks > 1 else "")
+                + ", bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9")
+        cfg = {"n_in": n_in, "n_out": n_out, "p": p, "chunks": chunks}
 
-    for i in range(args.warmup):
-        chain.step(i == 0)
-    torch.cuda.synchronize()
-
-    # one untimed step with every GEMM launch bracketed by events: the GEMM
-    # variants and the per-phase split
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(nph + 1)]
-    k = [0]
-
-    def mark():
-        ev[k[0]].record()
-        k[0] += 1
-    _lib.check(lib.ifk_profile_begin(-2), "profile_begin")
-    chain.step(False, mark)
-    n = _lib.ctypes.c_int64(0)
-    _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
-    torch.cuda.synchronize()
-    phases = {phase_names[i]: round(ev[i].elapsed_time(ev[i + 1]), 3) for i in range(nph)}
-
-    def read_profile(count):
-        recs = []
-        v = _lib.ctypes.c_int(0)
-        ms = _lib.ctypes.c_float(0)
-        fl = _lib.ctypes.c_double(0)
-        by = _lib.ctypes.c_double(0)
-        m_ = _lib.ctypes.c_int64(0)
-        n_ = _lib.ctypes.c_int64(0)
-        k_ = _lib.ctypes.c_int64(0)
-        for i in range(count):
-            _lib.check(lib.ifk_profile_get(i, *(_lib.ctypes.byref(x) for x in
-                                                 (v, ms, fl, by, m_, n_, k_))), "profile_get")
-            recs.append((v.value, ms.value, fl.value, by.value))
-        return recs
-
-    survey = read_profile(n.value)
-    per_variant = {}
-    for vid, ms, fl, by in survey:
-        a = per_variant.setdefault(vid, [0.0, 0, 0.0, 0.0])
-        a[0] += ms
-        a[1] += 1
-        a[2] += fl
-        a[3] += by
-
-    # the dominant GEMM kernel family of this library's own kernels (as
-    # rocprofv3 names them: 0 gemm_kernel, 1 gemm_big_kernel, 2 / 3
-    # gemm_bb_kernel with its 256 / 128 tile) by algorithmic flops in the
-    # survey step, timed over the timed steps
-    def family(vid):
-        if (vid >> 6) & 1:
-            return 3 if (vid >> 7) & 1 else 2
-        return (vid >> 5) & 1
-    fam_fl = {0: 0.0, 1: 0.0, 2: 0.0, 3: 0.0}
-    for vid, a in per_variant.items():
-        fam_fl[family(vid)] += a[2]
-    fam = max(fam_fl, key=fam_fl.get)
-    arm = {0: -4, 1: -3, 2: -5, 3: -6}[fam]
-    kname = {0: "gemm_kernel", 1: "gemm_big_kernel", 2: "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>",
-             3: "gemm_bb_kernel<BbCfg<128, 128, 2, 2, 2, false>>"}[fam]
-    torch.cuda.synchronize()
-    _lib.check(lib.ifk_profile_begin(arm), "profile_begin")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        chain.step(False)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    _lib.check(lib.ifk_profile_end(_lib.ctypes.byref(n)), "profile_end")
-    recs = read_profile(n.value)
-
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    flops = algorithmic_flops(n_in, n_out, p)
+    ms_per_step, roof, table, phases = measure(lib, runner.step, args.steps, args.warmup,
+                                               (args.workload, args.factor_path), marks)
     value = flops / (ms_per_step * 1e-3) / 1e12
 
-    tot_ms = sum(r[1] for r in recs)
-    tot_fl = sum(r[2] for r in recs)
-    tot_by = sum(r[3] for r in recs)
-    bf16_share = sum(r[2] for r in recs if (r[0] >> 4) & 1) / max(tot_fl, 1.0)
-    peak_flops = PEAK_BF16_TFLOPS if bf16_share >= 0.5 else PEAK_F32_TFLOPS
-    intensity = tot_fl / max(tot_by, 1.0)
-    ridge = peak_flops * 1e12 / (PEAK_HBM_GBS * 1e9)
-    if intensity < ridge:
-        achieved = tot_by / (tot_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
-    else:
-        achieved = tot_fl / (tot_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak_flops,
-                "unit": "TFLOP/s", "frac": round(achieved / peak_flops, 4)}
-    roof.update({
-        "traffic": TRAFFIC.get((args.workload, args.factor_path, kname)),
-        "kernel": kname + {0: " (128x128 MFMA)", 1: " (256x128x32 bf16 MFMA, register staged)",
-                           2: " (256x256x32 bf16 MFMA, direct-to-LDS ring)",
-                           3: " (128x128x32 bf16 MFMA, direct-to-LDS ring)"}[fam],
-        "bf16_share_of_flops": round(bf16_share, 3),
-        "launches_per_step": round(len(recs) / args.steps, 1),
-        "avg_launch_ms": round(tot_ms / max(len(recs), 1), 4),
-        "share_of_step": round(tot_ms / args.steps / ms_per_step, 3),
-        "algorithmic_flops_per_launch": round(tot_fl / max(len(recs), 1)),
-        "algorithmic_bytes_per_launch": round(tot_by / max(len(recs), 1)),
-    })
-    # a roofline per phase: algorithmic work over the phase's time in the
-    # survey step (the whole GPU, all streams)
-    ph_upd = phases["factor_update_and_inverse"]
-    ph_pre = phases["precondition"]
-    ph_mom = phases["update"]
-    upd_fl = update_flops(n_in, n_out, p)
-    pre_fl = precond_flops(n_in, n_out)
-    mom_by = 20.0 * n_in * n_out   # read nat, read/write buf, read/write W (fp32)
-    phase_roofs = {
-        "factor_update_and_inverse": {"bound": "mfma", "achieved": round(upd_fl / ph_upd / 1e9, 1),
-                                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                                      "frac": round(upd_fl / ph_upd / 1e9 / PEAK_BF16_TFLOPS, 4),
-                                      "algorithmic": "2 p (n_in^2 + n_out^2)"},
-        "precondition": {"bound": "mfma", "achieved": round(pre_fl / ph_pre / 1e9, 1),
-                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(pre_fl / ph_pre / 1e9 / PEAK_BF16_TFLOPS, 4),
-                         "algorithmic": "2 n_out n_in (n_in + n_out)"},
-        "update": {"bound": "hbm", "achieved": round(mom_by / ph_mom / 1e6, 1),
-                   "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                   "frac": round(mom_by / ph_mom / 1e6 / PEAK_HBM_GBS, 4),
-                   "algorithmic": "20 n_out n_in bytes"},
-    }
-    # kappa_2 of the damped factors of the timed step
-    (FX, _, ix), (FG, _, ig) = chain.factors
-    kx = float(be.cond_estimate(FX, ix[0]).item())
-    kg = float(be.cond_estimate(FG, ig[0]).item())
-    head_kappa = {"R_X": round(kx, 4), "R_G": round(kg, 4)}
+    out_extra = {}
+    if wl[0] != "vit":
+        # a roofline per phase: algorithmic work over the phase's time in the
+        # survey step (the whole GPU, all streams)
+        ph_upd = phases["factor_update_and_inverse"]
+        ph_pre = phases["precondition"]
+        ph_mom = phases["update"]
+        upd_fl = update_flops(n_in, n_out, p)
+        pre_fl = precond_flops(n_in, n_out)
+        mom_by = 20.0 * n_in * n_out   # read nat, read/write buf, read/write W (fp32)
+        out_extra["phase_rooflines"] = {
+            "factor_update_and_inverse": {
+                "bound": "mfma", "achieved": round(upd_fl / ph_upd / 1e9, 1),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(upd_fl / ph_upd / 1e9 / PEAK_BF16_TFLOPS, 4),
+                "algorithmic": "2 p (n_in^2 + n_out^2)"},
+            "precondition": {
+                "bound": "mfma", "achieved": round(pre_fl / ph_pre / 1e9, 1),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(pre_fl / ph_pre / 1e9 / PEAK_BF16_TFLOPS, 4),
+                "algorithmic": "2 n_out n_in (n_in + n_out)"},
+            "update": {
+                "bound": "hbm", "achieved": round(mom_by / ph_mom / 1e6, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(mom_by / ph_mom / 1e6 / PEAK_HBM_GBS, 4),
+                "algorithmic": "20 n_out n_in bytes"},
+        }
+        # kappa_2 of the damped factors of the timed step
+        (FX, _, ix), (FG, _, ig) = runner.factors
+        kx = float(be.cond_estimate(FX, ix[0]).item())
+        kg = float(be.cond_estimate(FG, ig[0]).item())
+        out_extra["kappa_R_damped"] = {"R_X": round(kx, 4), "R_G": round(kg, 4)}
+    head_kappa = out_extra.get("kappa_R_damped")
 
+    cfg.update({"workload": desc,
+                "factor_path": {
+                    "gram": "Gram matrix + 1024-block Cholesky with split-bf16 updates (panel "
+                            "path if flagged)",
+                    "cqr": "1024-column blocks by CholeskyQR2 (panel path if flagged)",
+                    "panel": "panel TPQRT fold"}[args.factor_path],
+                "algorithmic_gflop_per_step": round(flops / 1e9, 1),
+                "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
+                "GPU_MAX_HW_QUEUES": os.environ.get("GPU_MAX_HW_QUEUES", "default (unset)")})
     out = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -596,29 +704,16 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded; X kappa=1e2 and delta kappa=1e1 log-spaced singular values, "
                 "grad ~ N(0, 0.01))",
-        "config": {
-            "workload": f"IFKFAC factor update + precondition, Linear {n_in}->{n_out}, "
-                        f"p={p} rows, bf16 factors (use_true_bf16), damping 1e-2, momentum 0.9",
-            "factor_path": {
-                "gram": "Gram matrix + 1024-block Cholesky with split-bf16 updates (panel path "
-                        "if flagged)",
-                "cqr": "1024-column blocks by CholeskyQR2 (panel path if flagged)",
-                "panel": "panel TPQRT fold"}[args.factor_path],
-            "n_in": n_in, "n_out": n_out, "p": p, "algorithmic_gflop_per_step": round(flops / 1e9, 1),
-            "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
-            "GPU_MAX_HW_QUEUES": os.environ.get("GPU_MAX_HW_QUEUES", "default (unset)"),
-        },
+        "config": cfg,
         "phases_ms": phases,
         "roofline": roof,
-        "phase_rooflines": phase_roofs,
-        "kappa_R_damped": head_kappa,
-        "gemm_variants_ms_per_step": {str(kk): round(v[0], 3) for kk, v in
-                                      sorted(per_variant.items(), key=lambda kv: -kv[1][0])},
+        "kernels": table,
     }
+    out.update(out_extra)
     if child is not None:
         out["default_hw_queues"] = child
-    if not args.no_extras:
-        del chain
+    if not args.no_extras and args.workload == "linear_4096x11008_p16384":
+        del runner
         torch.cuda.empty_cache()
         out["extras"] = extras(be, args, head_kappa)
     if not args.no_cpu_baseline:

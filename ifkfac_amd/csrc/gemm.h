@@ -89,8 +89,18 @@ struct SplitScratch {
 // the large-tile bf16 kernels, bit 6 as well for the direct-to-LDS one, bit 7
 // for its 128 x 128 tile, bit 9 for a stream-K launch), -2 all, -3 all of the
 // register-staged 256 x 128 kernel, -4 all of the 128 x 128 kernel, -5 / -6
-// all of the direct-to-LDS kernel with its 256 / 128 tile, -1 off.
+// all of the direct-to-LDS kernel with its 256 / 128 tile, -7 / -8 all
+// cholb_first / cholb_step launches, -1 off.
 int gemm_variant_id(int math, int adt, bool akc, int bdt, bool bkc);
+// The same profiler for other kernels: variant KVID + kind (families 5, 6:
+// cholb_first_kernel, cholb_step_kernel; armed by -7 / -8).  A launcher
+// brackets one launch with prof_kernel_begin / prof_kernel_end (no-ops when
+// the profiler is not armed for it).
+constexpr int KVID = 1 << 12;
+constexpr int KVID_CHOLB_FIRST = KVID + 0, KVID_CHOLB_STEP = KVID + 1;
+void* prof_kernel_begin(hipStream_t s, int vid, double flops, double bytes, int64_t m, int64_t n,
+                        int64_t k);
+void prof_kernel_end(void* rec, hipStream_t s);
 int profile_begin(int variant);
 int profile_end(int64_t* n_launches);
 int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes, int64_t* m,

@@ -85,19 +85,20 @@ int profile_get(int64_t i, int* variant, float* ms, double* flops, double* bytes
 // / 128 tile (bits 5 and 6, and bit 7 for the 128 tile; bit 9 marks a
 // stream-K launch of either).
 static int gemm_family(int vid) {
+  if (vid >= KVID) return 5 + (vid - KVID);   // 5 cholb_first, 6 cholb_step
   if ((vid >> 6) & 1) return ((vid >> 7) & 1) ? 3 : 2;
   return (vid >> 5) & 1;
 }
 
-// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 / -6
-// every launch of family 1 / 0 / 2 / 3.
+// Armed variant: >= 0 one variant id, -2 every launch, -3 / -4 / -5 / -6 /
+// -7 / -8 every launch of family 1 / 0 / 2 / 3 / 5 / 6.
 static ProfRec* prof_slot(int vid) {
   const int a = g_prof_variant;
   if (a == -1) return nullptr;
   if (a >= 0 && a != vid) return nullptr;
   const int fam = gemm_family(vid);
   if ((a == -3 && fam != 1) || (a == -4 && fam != 0) || (a == -5 && fam != 2) ||
-      (a == -6 && fam != 3))
+      (a == -6 && fam != 3) || (a == -7 && fam != 5) || (a == -8 && fam != 6))
     return nullptr;
   std::lock_guard<std::mutex> g(g_prof_mu);
   if (g_prof_used == g_prof.size()) {
@@ -107,6 +108,24 @@ static ProfRec* prof_slot(int vid) {
     g_prof.push_back(r);
   }
   return &g_prof[g_prof_used++];
+}
+
+void* prof_kernel_begin(hipStream_t s, int vid, double flops, double bytes, int64_t m, int64_t n,
+                        int64_t k) {
+  ProfRec* pr = prof_slot(vid);
+  if (!pr) return nullptr;
+  pr->variant = vid;
+  pr->m = m;
+  pr->n = n;
+  pr->k = k;
+  pr->flops = flops;
+  pr->bytes = bytes;
+  hipEventRecord(pr->beg, s);
+  return pr;
+}
+
+void prof_kernel_end(void* rec, hipStream_t s) {
+  if (rec) hipEventRecord(static_cast<ProfRec*>(rec)->end, s);
 }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));

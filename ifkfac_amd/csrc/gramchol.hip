@@ -455,7 +455,7 @@ int cast_lower_t(hipStream_t s, int batch, const float* L, int64_t ldl, int64_t 
 // Workgroup caps of the helper streams' products: the chain's launches
 // (cholb's diagonal workgroup, the band products) must find CUs free while
 // the Gram columns and the panel work run beside them.
-constexpr int GRAM_MAX_WGS = 192;
+constexpr int GRAM_MAX_WGS = 128;
 constexpr int REST_MAX_WGS = 192;
 
 struct GramWs {

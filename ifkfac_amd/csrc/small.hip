@@ -27,6 +27,7 @@
 //   T^{-1} = striu(V^T V) + diag(V^T V) / 2,  V^T V = I + Y^T Y.
 // The partial Gram matrices over row slabs come from panel.hip.
 #include "common.h"
+#include "gemm.h"
 #include "kernels.h"
 
 namespace ifk {
@@ -1471,10 +1472,19 @@ int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t 
     set_error("cholb: size out of range");
     return IFK_ERR_INVALID;
   }
+  const int nb = (n + SB - 1) / SB;
+  // launch profiler: the algorithmic work of the factor (n^3 / 3) and, with M,
+  // its inverse (n^3 / 3 more) spread evenly over the launches, the bytes of
+  // A's upper triangle read and of U (and M) written
+  const int launches = M ? nb + 1 : nb;
+  const double nn = (double)n;
+  const double fl = (M ? 2.0 : 1.0) * nn * nn * nn / 3.0 * batch / launches;
+  const double by = (M ? 3.0 : 2.0) * nn * nn / 2.0 * 4.0 * batch / launches;
+  void* pr = prof_kernel_begin(s, KVID_CHOLB_FIRST, fl, by, n, n, 0);
   hipLaunchKernelGGL(cholb_first_kernel, dim3(1, (unsigned)batch), dim3(SNT), 0, s, A, lda, n, U,
                      ldu, Zd, dref, tol, flag, M, ldm, dref_in ? 1 : 0, bs);
+  prof_kernel_end(pr, s);
   if (int rc = check_launch("cholb_first")) return rc;
-  const int nb = (n + SB - 1) / SB;
   // step k: the (i, j) pairs k < i <= j (m (m + 1) / 2 of them, m = nb - 1 - k),
   // then with M the k + 1 blocks of M's column block k and the k m partial
   // sums of its later column blocks (column block 0 comes from cholb_first;
@@ -1483,8 +1493,10 @@ int launch_cholb(hipStream_t s, float* A, int64_t lda, int n, float* U, int64_t 
     const int m = nb - 1 - k;
     const int wgs = m * (m + 1) / 2 + ((M && k > 0) ? k + 1 + k * m : 0);
     if (wgs == 0) continue;
+    void* ps = prof_kernel_begin(s, KVID_CHOLB_STEP, fl, by, n, n, k);
     hipLaunchKernelGGL(cholb_step_kernel, dim3((unsigned)wgs, (unsigned)batch), dim3(SNT), 0, s, A,
                        lda, n, U, ldu, Zd, dref, tol, flag, k, M, ldm, bs);
+    prof_kernel_end(ps, s);
     if (int rc = check_launch("cholb_step")) return rc;
   }
   return IFK_OK;

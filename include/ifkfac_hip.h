@@ -471,10 +471,14 @@ int ifk_gemm(void* stream, int math, int64_t m, int64_t n, int64_t k, float alph
  * b_k_contiguous; large_tile marks the bf16 kernels with the large tiles,
  * direct the one that loads operands straight into LDS, gemm_bb_kernel, mid
  * its 128 x 128 tile and streamk a launch of it that walks the tiles
- * stream-K; large_tile alone gemm_big_kernel, neither gemm_kernel), for
- * every variant with v = -2, for every launch of gemm_big_kernel with v = -3,
- * of gemm_kernel with v = -4, of gemm_bb_kernel with its 256 x 256 tile with
- * v = -5 and with its 128 x 128 tile with v = -6; v = -1 disarms.
+ * stream-K; large_tile alone gemm_big_kernel, neither gemm_kernel; the
+ * block Cholesky's launches have v = 4096 (cholb_first_kernel) and 4097
+ * (cholb_step_kernel)), for every variant with v = -2, for every launch of
+ * gemm_big_kernel with v = -3, of gemm_kernel with v = -4, of gemm_bb_kernel
+ * with its 256 x 256 tile with v = -5 and with its 128 x 128 tile with v = -6,
+ * of cholb_first_kernel with v = -7 and of cholb_step_kernel with v = -8;
+ * v = -1 disarms.  A block-Cholesky launch's algorithmic flops are its even
+ * share of n^3 / 3 for the factor plus n^3 / 3 for its inverse.
  * Each armed launch is bracketed by two HIP events on its own stream.
  * ifk_profile_end() disarms, waits for the events and returns the number of
  * launches recorded; ifk_profile_get(i, ...) returns launch i's variant,
