@@ -180,6 +180,37 @@ class HipBackend:
         _lib.check(rc, name)
         return (out, flag, kb) if kb is not None else (out, flag)
 
+    def fold_gram_batched_(self, Rs, r_in: int, Xs, pivot_tol: float) -> torch.Tensor:
+        """fold_gram_ for B running factors of one shape, each folding its own
+        chunk, in one chain of launches (ifk_tsqr_fold_gram_batched).  Rs:
+        contiguous n x n fp32 buffers; Xs: B chunks (p x n, one dtype).
+        Returns the device int32[B] statuses; entry e's R and status are bitwise
+        what fold_gram_ gives it alone (R untouched where the status is 2)."""
+        B = len(Xs)
+        mats = [_mat(X, "tsqr_fold_gram_batched") for X in Xs]
+        X0, ldx, xdt = mats[0]
+        p, n = X0.shape
+        if any(m[0].shape != (p, n) or m[1] != ldx or m[2] != xdt for m in mats):
+            raise IFKFACBackendError("tsqr_fold_gram_batched: chunks differ in shape or dtype")
+        for R in Rs:
+            _require_device(R, "tsqr_fold_gram_batched")
+            if R.dtype != torch.float32 or R.shape != (n, n) or not R.is_contiguous():
+                raise IFKFACBackendError("tsqr_fold_gram_batched: each R must be a contiguous "
+                                         "n x n fp32 buffer")
+        dev = X0.device
+        xptrs = (ctypes.c_void_p * B)(*[m[0].data_ptr() for m in mats])
+        rptrs = (ctypes.c_void_p * B)(*[R.data_ptr() for R in Rs])
+        st = torch.empty(B, dtype=torch.int32, device=dev)
+        ws = self._ws(self.lib.ifk_tsqr_fold_gram_batched_workspace_size(B, p, n, int(r_in)),
+                      dev)
+        with torch.cuda.device(dev):
+            rc = self.lib.ifk_tsqr_fold_gram_batched(
+                self._stream(dev), B, ctypes.cast(xptrs, ctypes.c_void_p), xdt, p, n, ldx,
+                ctypes.cast(rptrs, ctypes.c_void_p), n, int(r_in), float(pivot_tol), _ptr(st),
+                _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_tsqr_fold_gram_batched")
+        return st
+
     def fold_finalize_gram_batched(self, Rs, r_in: int, Xs, scale: float, damping: float,
                                    out_dtype: torch.dtype, with_inverse: bool = False):
         """fold_finalize(..., gram=True, with_kappa=True) for B same-shape sides in
@@ -331,6 +362,134 @@ class HipBackend:
                                                    _ptr(out[3]), n)
         _lib.check(rc, "ifk_inverse_split_copies")
         return tuple(out.unbind(0))
+
+    def inverse_split_copies_batched(self, Zs) -> list:
+        """inverse_split_copies for B inverses of one size, the halves of all of
+        them in one (4, B, n, n) buffer: entry e gets the views
+        (Z_hi, Z_lo, Z^T_hi, Z^T_lo) at a fixed stride from entry to entry, as
+        precondition_apply_x3_batched takes them."""
+        n = Zs[0].shape[0]
+        dev = Zs[0].device
+        out = torch.empty((4, len(Zs), n, n), dtype=torch.bfloat16, device=dev)
+        for e, Z in enumerate(Zs):
+            Zc, ldz, zdt = _mat(Z, "inverse_split_copies")
+            if Zc.shape != (n, n) or zdt != IFK_F32:
+                raise IFKFACBackendError("inverse_split_copies: Z must be n x n fp32")
+            with torch.cuda.device(dev):
+                rc = self.lib.ifk_inverse_split_copies(self._stream(dev), _ptr(Zc), ldz, n,
+                                                       _ptr(out[0, e]), _ptr(out[1, e]),
+                                                       _ptr(out[2, e]), _ptr(out[3, e]), n)
+            _lib.check(rc, "ifk_inverse_split_copies")
+        return [tuple(out[i, e] for i in range(4)) for e in range(len(Zs))]
+
+    @staticmethod
+    def entry_stride(ts) -> Optional[int]:
+        """The element stride at which the same-shape tensors ts sit one after
+        another in memory (one stride between every two consecutive ones, row
+        stride and dtype alike), or None (len(ts) == 1: 0)."""
+        if len(ts) == 1:
+            return 0
+        es = ts[0].element_size()
+        d = ts[1].data_ptr() - ts[0].data_ptr()
+        if d <= 0 or d % es:
+            return None
+        for a, b in zip(ts, ts[1:]):
+            if (b.data_ptr() - a.data_ptr() != d or b.shape != a.shape or b.stride() != a.stride()
+                    or b.dtype != a.dtype or b.device != a.device):
+                return None
+        return d // es
+
+    def _batch_grads(self, grads, name):
+        gs = []
+        for g in grads:
+            g, ldg, gdt = _mat(g, name)
+            if gdt != IFK_F32:
+                g = g.float()
+                ldg = g.stride(0)
+            gs.append((g, ldg))
+        n_out, n_in = gs[0][0].shape
+        ldg = gs[0][1]
+        if any(g.shape != (n_out, n_in) or l != ldg or g.device != gs[0][0].device
+               for g, l in gs):
+            raise IFKFACBackendError(f"{name}: gradients differ in shape or row stride")
+        ptrs = (ctypes.c_void_p * len(gs))(*[g.data_ptr() for g, _ in gs])
+        return gs, ptrs, n_out, n_in, ldg
+
+    def precondition_apply_bf16_batched(self, grads, ZX2s, ZG2s) -> torch.Tensor:
+        """precondition_apply_bf16 for B layers of one shape in grouped launches
+        (ifk_precondition_apply_bf16_batched): every layer's (Z_X, Z_X^T) and
+        (Z_G, Z_G^T) copies at one fixed stride from layer to layer (views of
+        one (B, n, n) buffer each, as the batched factor update returns them).
+        Returns nat (B, n_out, n_in); entry e is bitwise the single-layer result."""
+        name = "precondition_apply_bf16_batched"
+        gs, ptrs, n_out, n_in, ldg = self._batch_grads(grads, name)
+        B = len(gs)
+        strides = []
+        for side, n in ((ZX2s, n_in), (ZG2s, n_out)):
+            for j in (0, 1):
+                ts = [c[j] for c in side]
+                for t in ts:
+                    _require_device(t, name)
+                    if t.dtype != torch.bfloat16 or t.shape != (n, n) or t.stride(1) != 1:
+                        raise IFKFACBackendError(f"{name}: copies must be {n} x {n} bf16")
+                st = self.entry_stride(ts)
+                if st is None:
+                    raise IFKFACBackendError(f"{name}: a side's copies are not at one stride")
+                strides.append(st)
+        if strides[0] != strides[1] or strides[2] != strides[3] or \
+                ZX2s[0][0].stride(0) != ZX2s[0][1].stride(0) or \
+                ZG2s[0][0].stride(0) != ZG2s[0][1].stride(0):
+            raise IFKFACBackendError(f"{name}: a side's two copies differ in stride")
+        dev = gs[0][0].device
+        nat = torch.empty((B, n_out, n_in), dtype=torch.float32, device=dev)
+        ws = self._ws(self.lib.ifk_precondition_apply_bf16_batched_workspace_size(B, n_out, n_in),
+                      dev)
+        (ZXb, ZXt), (ZGb, ZGt) = ZX2s[0], ZG2s[0]
+        with torch.cuda.device(dev):
+            rc = self.lib.ifk_precondition_apply_bf16_batched(
+                self._stream(dev), B, ctypes.cast(ptrs, ctypes.c_void_p), n_out, n_in, ldg,
+                _ptr(ZXb), _ptr(ZXt), ZXb.stride(0), strides[0], _ptr(ZGb), _ptr(ZGt),
+                ZGb.stride(0), strides[2], _ptr(nat), n_in, n_out * n_in, _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_precondition_apply_bf16_batched")
+        return nat
+
+    def precondition_apply_x3_batched(self, grads, ZX4s, ZG4s) -> torch.Tensor:
+        """precondition_apply_x3 for B layers of one shape in grouped launches
+        (ifk_precondition_apply_x3_batched): each of the four halves of every
+        side at one fixed stride from layer to layer (inverse_split_copies_batched
+        makes them so).  Returns nat (B, n_out, n_in), bitwise the per-layer
+        results."""
+        name = "precondition_apply_x3_batched"
+        gs, ptrs, n_out, n_in, ldg = self._batch_grads(grads, name)
+        B = len(gs)
+        sides = []
+        for side, n in ((ZX4s, n_in), (ZG4s, n_out)):
+            st = None
+            for j in range(4):
+                ts = [c[j] for c in side]
+                for t in ts:
+                    _require_device(t, name)
+                    if t.dtype != torch.bfloat16 or t.shape != (n, n) or t.stride(1) != 1 or \
+                            t.stride(0) != side[0][0].stride(0):
+                        raise IFKFACBackendError(f"{name}: halves must be {n} x {n} bf16 with "
+                                                 f"one row stride")
+                sj = self.entry_stride(ts)
+                if sj is None or (st is not None and sj != st):
+                    raise IFKFACBackendError(f"{name}: a side's halves are not at one stride")
+                st = sj
+            sides.append(st)
+        dev = gs[0][0].device
+        nat = torch.empty((B, n_out, n_in), dtype=torch.float32, device=dev)
+        ws = self._ws(self.lib.ifk_precondition_apply_x3_batched_workspace_size(B, n_out, n_in),
+                      dev)
+        with torch.cuda.device(dev):
+            rc = self.lib.ifk_precondition_apply_x3_batched(
+                self._stream(dev), B, ctypes.cast(ptrs, ctypes.c_void_p), n_out, n_in, ldg,
+                *[_ptr(t) for t in ZX4s[0]], ZX4s[0][0].stride(0), sides[0],
+                *[_ptr(t) for t in ZG4s[0]], ZG4s[0][0].stride(0), sides[1], _ptr(nat), n_in,
+                n_out * n_in, _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_precondition_apply_x3_batched")
+        return nat
 
     def precondition_apply_x3(self, grad: torch.Tensor, ZX4, ZG4) -> torch.Tensor:
         """precondition_apply at fp32 accuracy from the split copies of

@@ -70,6 +70,19 @@ SIGNATURES = {
     "ifk_precondition_apply_x3": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
                                            _c_vp, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp,
                                            _c_i64, _c_vp, _c_i64, _c_vp, _c_sz]),
+    "ifk_tsqr_fold_gram_batched_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "ifk_tsqr_fold_gram_batched": (_c_int, [_c_vp, _c_i64, _c_vp, _c_int, _c_i64, _c_i64, _c_i64,
+                                            _c_vp, _c_i64, _c_i64, _c_f, _c_vp, _c_vp, _c_sz]),
+    "ifk_precondition_apply_bf16_batched_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64]),
+    "ifk_precondition_apply_bf16_batched": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64,
+                                                     _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
+                                                     _c_vp, _c_vp, _c_i64, _c_i64, _c_vp,
+                                                     _c_i64, _c_i64, _c_vp, _c_sz]),
+    "ifk_precondition_apply_x3_batched_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64]),
+    "ifk_precondition_apply_x3_batched": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64,
+                                                   _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                                                   _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                                                   _c_vp, _c_i64, _c_i64, _c_vp, _c_sz]),
     "ifk_tri_inverse_workspace_size": (_c_sz, [_c_i64]),
     "ifk_tri_inverse": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_int,
                                  _c_vp, _c_sz]),

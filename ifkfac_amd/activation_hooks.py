@@ -490,13 +490,63 @@ class RawActivationHooks(GramMatrixEstimator):
         if not self.batched:
             return
         for side, pending in (("X", self._pending_X), ("G", self._pending_G)):
+            work = []
             for module in list(pending.keys()):
                 chunks = pending[module]
                 if not chunks:
                     continue
                 X = chunks[0] if len(chunks) == 1 else torch.cat(chunks, dim=0)
-                self._fold(side, module, X, full_rank_shape=True)
+                work.append((module, X))
                 pending[module] = []
+            # same-shape layers fold together (the reference's batched_qr over
+            # a bucket, triangular.py:331-379): in bf16 arithmetic a square
+            # fold by the batched Gram route, one status read for the group
+            groups: Dict[tuple, list] = {}
+            for module, X in work:
+                key = (X.shape[0], X.shape[1], X.dtype, X.device, self._rows_in(side, module, X))
+                groups.setdefault(key, []).append((module, X))
+            for (p, n, _, _, r_in), items in groups.items():
+                if (len(items) > 1 and self.math == MATH_BF16 and r_in + p >= n and
+                        hasattr(get_backend(), "fold_gram_batched_")):
+                    self._fold_group(side, items, r_in)
+                else:
+                    for module, X in items:
+                        self._fold(side, module, X, full_rank_shape=True)
+
+    def _rows_in(self, side: str, module: nn.Module, X: torch.Tensor) -> int:
+        """The rows a flush fold of X starts from (as _fold with full_rank_shape)."""
+        cur = (self._R_X if side == "X" else self._R_G).get(module)
+        return X.shape[1] if cur is None else cur.shape[0]
+
+    def _fold_group(self, side: str, items, r_in: int) -> None:
+        """_fold(full_rank_shape=True) of same-shape chunks into their layers'
+        running factors by one batched Gram-route fold; a layer the Gram route
+        refuses (status 2, its buffer untouched) folds by the panel path."""
+        Rd = self._R_X if side == "X" else self._R_G
+        bufs_d = self._buf_X if side == "X" else self._buf_G
+        bufs = []
+        for module, X in items:
+            n = X.shape[1]
+            cur = Rd.get(module)
+            buf = bufs_d.get(module)
+            if buf is None or buf.shape[0] != n or buf.device != X.device:
+                buf = torch.zeros((n, n), dtype=torch.float32, device=X.device)
+                bufs_d[module] = buf
+            if cur is None:
+                buf.zero_()
+            elif cur.data_ptr() != buf.data_ptr():
+                buf[:r_in].copy_(cur)
+            bufs.append(buf)
+        st = get_backend().fold_gram_batched_(bufs, r_in, [X for _, X in items],
+                                              GRAM_FOLD_TOL).cpu()
+        for e, (module, X) in enumerate(items):
+            n = X.shape[1]
+            r_new = n
+            if int(st[e]) != 1:
+                logger.debug("flush fold of %d rows into a %d-column factor: Gram route "
+                             "refused, panel fold", X.shape[0], n)
+                r_new = get_backend().fold_(bufs[e], r_in, X, self.math)
+            Rd[module] = bufs[e][:r_new]
 
     # ------------------------------------------------------------------ conv helpers
     @staticmethod

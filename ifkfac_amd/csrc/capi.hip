@@ -137,6 +137,21 @@ int ifk_tsqr_fold_gram(void* stream, const void* X, int x_dtype, int64_t p, int6
                         status, workspace, workspace_bytes);
 }
 
+size_t ifk_tsqr_fold_gram_batched_workspace_size(int64_t batch, int64_t p, int64_t n,
+                                                  int64_t r_in) {
+  if (batch < 1 || p < 0 || n < 1 || r_in < 0 || r_in > n) return 0;
+  return tsqr_fold_gram_batched_ws(batch, p, n, r_in);
+}
+
+int ifk_tsqr_fold_gram_batched(void* stream, int64_t batch, const void* const* X, int x_dtype,
+                               int64_t p, int64_t n, int64_t ldx, float* const* R, int64_t ldr,
+                               int64_t r_in, float pivot_tol, int32_t* status, void* workspace,
+                               size_t workspace_bytes) {
+  GUARD(dt_ok(x_dtype), "tsqr_fold_gram_batched: bad dtype");
+  return tsqr_fold_gram_batched((hipStream_t)stream, batch, X, x_dtype, p, n, ldx, R, ldr, r_in,
+                                pivot_tol, status, workspace, workspace_bytes);
+}
+
 size_t ifk_fold_finalize_gram_batched_workspace_size(int64_t batch, int64_t p, int64_t n,
                                                      int64_t r_in) {
   if (batch < 1 || p < 0 || n < 1 || r_in < 0 || r_in > n) return 0;
@@ -255,6 +270,48 @@ int ifk_precondition_apply_x3(void* stream, const float* grad, int64_t n_out, in
                          (const bf16_t*)Z_GT_lo};
   return precondition_apply_x3((hipStream_t)stream, grad, n_out, n_in, ldg, zx, ldzx, zg, ldzg, nat,
                                ldn, workspace, workspace_bytes);
+}
+
+size_t ifk_precondition_apply_bf16_batched_workspace_size(int64_t batch, int64_t n_out,
+                                                          int64_t n_in) {
+  if (batch < 1 || n_out < 1 || n_in < 1) return 0;
+  return precondition_apply_b_batched_ws(batch, n_out, n_in);
+}
+
+int ifk_precondition_apply_bf16_batched(void* stream, int64_t batch, const float* const* grad,
+                                        int64_t n_out, int64_t n_in, int64_t ldg,
+                                        const void* Z_Xb, const void* Z_Xt, int64_t ldzx,
+                                        int64_t stride_zx, const void* Z_Gb, const void* Z_Gt,
+                                        int64_t ldzg, int64_t stride_zg, float* nat, int64_t ldn,
+                                        int64_t stride_nat, void* workspace,
+                                        size_t workspace_bytes) {
+  return precondition_apply_b_batched((hipStream_t)stream, batch, grad, n_out, n_in, ldg,
+                                      (const bf16_t*)Z_Xb, (const bf16_t*)Z_Xt, ldzx, stride_zx,
+                                      (const bf16_t*)Z_Gb, (const bf16_t*)Z_Gt, ldzg, stride_zg,
+                                      nat, ldn, stride_nat, workspace, workspace_bytes);
+}
+
+size_t ifk_precondition_apply_x3_batched_workspace_size(int64_t batch, int64_t n_out,
+                                                        int64_t n_in) {
+  if (batch < 1 || n_out < 1 || n_in < 1) return 0;
+  return precondition_apply_x3_batched_ws(batch, n_out, n_in);
+}
+
+int ifk_precondition_apply_x3_batched(void* stream, int64_t batch, const float* const* grad,
+                                      int64_t n_out, int64_t n_in, int64_t ldg,
+                                      const void* Z_X_hi, const void* Z_X_lo, const void* Z_XT_hi,
+                                      const void* Z_XT_lo, int64_t ldzx, int64_t stride_zx,
+                                      const void* Z_G_hi, const void* Z_G_lo, const void* Z_GT_hi,
+                                      const void* Z_GT_lo, int64_t ldzg, int64_t stride_zg,
+                                      float* nat, int64_t ldn, int64_t stride_nat,
+                                      void* workspace, size_t workspace_bytes) {
+  const bf16_t* zx[4] = {(const bf16_t*)Z_X_hi, (const bf16_t*)Z_X_lo, (const bf16_t*)Z_XT_hi,
+                         (const bf16_t*)Z_XT_lo};
+  const bf16_t* zg[4] = {(const bf16_t*)Z_G_hi, (const bf16_t*)Z_G_lo, (const bf16_t*)Z_GT_hi,
+                         (const bf16_t*)Z_GT_lo};
+  return precondition_apply_x3_batched((hipStream_t)stream, batch, grad, n_out, n_in, ldg, zx,
+                                       ldzx, stride_zx, zg, ldzg, stride_zg, nat, ldn, stride_nat,
+                                       workspace, workspace_bytes);
 }
 
 size_t ifk_precondition_workspace_size(int64_t n_out, int64_t n_in, int math) {

@@ -84,13 +84,17 @@ constexpr float GRAM_TOL = 1e-3f;     // relative pivot threshold (see above)
 // fp32 or bf16 src; with upper set, entries of src below its diagonal are
 // taken as zero.  64 x 64 LDS tile: fp32 rows read as float4 (vec_in: src
 // 16-byte aligned, lds a multiple of 4), the output written as bf16 pairs
-// (pairs_out: dst 4-byte aligned, ldd even); element-wise otherwise.
+// (pairs_out: dst 4-byte aligned, ldd even); element-wise otherwise.  With
+// dst2 set, each value x is split as x = hi + lo (both RNE bf16) and the rows
+// of dst get three segments of rows elements [hi | lo | hi], those of dst2
+// [hi | hi | lo]: K-concatenated operands whose product is
+// hi hi^T + lo hi^T + hi lo^T, x x^T to about 2^-17.
 template <int DT>
 __global__ __launch_bounds__(256) void transpose_to_bf16_kernel(const void* src, int64_t lds,
                                                                 int64_t rows, int64_t cols,
                                                                 bf16_t* dst, int64_t ldd,
                                                                 int upper, int vec_in,
-                                                                int pairs_out) {
+                                                                int pairs_out, bf16_t* dst2) {
   __shared__ float tile[64][65];
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const int t = threadIdx.x;
@@ -123,7 +127,22 @@ __global__ __launch_bounds__(256) void transpose_to_bf16_kernel(const void* src,
     const int64_t c = c0 + cl, r = r0 + rp;
     if (c >= cols || r >= rows) continue;
     bf16_t* g = dst + c * ldd + r;
-    if (pairs_out && r + 1 < rows) {
+    if (dst2) {
+      // split: x = hi + lo (both RNE bf16); dst gets [hi | lo | hi] and
+      // dst2 [hi | hi | lo] in three segments of rows elements along its rows
+      bf16_t* g2 = dst2 + c * ldd + r;
+      for (int u = 0; u < 2 && r + u < rows; ++u) {
+        const float x = tile[rp + u][cl];
+        const bf16_t hi = f32_to_bf16(x);
+        const bf16_t lo = f32_to_bf16(x - bf16_to_f32(hi));
+        g[u] = hi;
+        g[rows + u] = lo;
+        g[2 * rows + u] = hi;
+        g2[u] = hi;
+        g2[rows + u] = hi;
+        g2[2 * rows + u] = lo;
+      }
+    } else if (pairs_out && r + 1 < rows) {
       *reinterpret_cast<uint32_t*>(g) = pack_bf16x2(tile[rp][cl], tile[rp + 1][cl]);
     } else {
       g[0] = f32_to_bf16(tile[rp][cl]);
@@ -398,7 +417,8 @@ unsigned grid_of(int64_t work, int64_t cap = 2048) {
 }
 
 int transpose_to_bf16(hipStream_t s, const void* src, int sdt, int64_t lds, int64_t rows,
-                      int64_t cols, bf16_t* dst, int64_t ldd, bool upper) {
+                      int64_t cols, bf16_t* dst, int64_t ldd, bool upper,
+                      bf16_t* dst2 = nullptr) {
   if (rows * cols == 0) return IFK_OK;
   if (cdiv(rows, 64) > 65535) {
     set_error("fold_finalize_gram: too many rows to transpose");
@@ -409,10 +429,10 @@ int transpose_to_bf16(hipStream_t s, const void* src, int sdt, int64_t lds, int6
   const dim3 grid((unsigned)cdiv(cols, 64), (unsigned)cdiv(rows, 64));
   if (sdt == DT_F32)
     hipLaunchKernelGGL(transpose_to_bf16_kernel<DT_F32>, grid, dim3(256), 0, s, src, lds, rows,
-                       cols, dst, ldd, upper ? 1 : 0, vec_in, pairs_out);
+                       cols, dst, ldd, upper ? 1 : 0, vec_in, pairs_out, dst2);
   else
     hipLaunchKernelGGL(transpose_to_bf16_kernel<DT_BF16>, grid, dim3(256), 0, s, src, lds, rows,
-                       cols, dst, ldd, upper ? 1 : 0, 0, pairs_out);
+                       cols, dst, ldd, upper ? 1 : 0, 0, pairs_out, dst2);
   return check_launch("transpose_to_bf16");
 }
 
@@ -460,10 +480,14 @@ constexpr int REST_MAX_WGS = 192;
 
 struct GramWs {
   int64_t B;          // batch entries
-  int64_t ldk;        // row stride of PT (pe rounded up to 8; the pad is zero)
+  int64_t ldk;        // row stride of PT and PB (K rows rounded up to 8; the pad is zero)
+  int64_t kr;         // K offset of the chunk's rows: r_in, or 3 r_in with the split
   int64_t lda;        // row stride of Aw
   int64_t ldl;        // row stride of LA / LB: 3 GB per panel
-  bf16_t* PT;         // P^T in bf16, n x ldk
+  bf16_t* PT;         // P^T in bf16, n x ldk: the A operand of the Gram products
+  bf16_t* PB;         // their B operand: PT itself, or with the split running
+                      // factor the K segments [R_hi | R_hi | R_lo | X] against
+                      // PT's [R_hi | R_lo | R_hi | X]
   float* Aw;          // working matrix / factor (lower), n x lda
   float* dref;        // Gram diagonal (+ c^2), n
   float* G;           // symmetrised diagonal block, GB x GB; then M^T
@@ -486,9 +510,13 @@ struct GramWs {
 };
 constexpr int64_t FLAG_S = 64;   // ints between two entries' flags (separate cache lines)
 
-void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w, bool inv = false) {
+void plan_gram(Arena& a, int64_t B, int64_t p, int64_t r_in, int64_t n, GramWs& w,
+               bool inv = false, bool split_r = false) {
   const int64_t nb = cdiv(n, GB);
+  const bool two = split_r && r_in > 0;
+  const int64_t pe = (two ? 3 * r_in : r_in) + p;   // K extent of the Gram products
   w.B = B;
+  w.kr = two ? 3 * r_in : r_in;
   w.ldk = (int64_t)align_up((size_t)std::max<int64_t>(pe, 1), 8);
   w.lda = (int64_t)align_up((size_t)n, 64);
   w.ldl = 3 * GB * std::max<int64_t>(nb - 1, 1);
@@ -508,6 +536,7 @@ void plan_gram(Arena& a, int64_t B, int64_t pe, int64_t n, GramWs& w, bool inv =
   w.sL = al(big * w.ldl);
   w.sfrob = (nb + 1) * FROB_WG;   // + the diagonal block of column 0, kept apart
   w.PT = a.take<bf16_t>((size_t)(B * w.sPT));
+  w.PB = two ? a.take<bf16_t>((size_t)(B * w.sPT)) : w.PT;
   w.Aw = a.take<float>((size_t)(B * w.sAw));
   w.dref = a.take<float>((size_t)(B * w.sdref));
   w.G = a.take<float>((size_t)(B * w.sGB));
@@ -566,7 +595,7 @@ int gram_column(hipStream_t s, GramWs& w, int64_t n, int64_t c, float c2, bool h
   if (have_rows) {
     RC(gemm(s, MATH_BF16, rows, W, w.ldk, 1.0f,
             A_n(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk, TRI_NONE, w.sPT),
-            B_t(w.PT + b.r0 * w.ldk, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
+            B_t(w.PB + b.r0 * w.ldk, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
             per_entry(lower_part(out_f32(Ac, w.lda, w.sAw))), B, w.sp3, max_wgs));
   } else {
     for (int e = 0; e < B; ++e) RC(launch_zero(s, Ac + e * w.sAw, w.lda, rows, W));
@@ -589,7 +618,7 @@ int gram_column0_diag(hipStream_t s, GramWs& w, int64_t n, float c2, bool have_r
   float* Ac = w.Aw;
   if (have_rows) {
     RC(gemm(s, MATH_BF16, W, W, w.ldk, 1.0f, A_n(w.PT, DT_BF16, w.ldk, TRI_NONE, w.sPT),
-            B_t(w.PT, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
+            B_t(w.PB, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
             per_entry(lower_part(out_f32(Ac, w.lda, w.sAw))), B, w.sp3, max_wgs));
   } else {
     for (int e = 0; e < B; ++e) RC(launch_zero(s, Ac + e * w.sAw, w.lda, W, W));
@@ -617,7 +646,7 @@ int gram_column0_rest(hipStream_t s, GramWs& w, int64_t n, bool have_rows, int m
   if (have_rows) {
     RC(gemm(s, MATH_BF16, rows, W, w.ldk, 1.0f,
             A_n(w.PT + W * w.ldk, DT_BF16, w.ldk, TRI_NONE, w.sPT),
-            B_t(w.PT, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
+            B_t(w.PB, DT_BF16, w.ldk, TRI_NONE, w.sPT), 0.0f,
             per_entry(out_f32(Ac, w.lda, w.sAw)), B, w.sp3, max_wgs));
   } else {
     for (int e = 0; e < B; ++e) RC(launch_zero(s, Ac + e * w.sAw, w.lda, rows, W));
@@ -763,14 +792,14 @@ int inverse_from_blocks(hipStream_t s, GramWs& w, int64_t n, float scale, const 
 size_t fold_finalize_gram_inv_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in) {
   Arena a(nullptr, 0);
   GramWs w;
-  plan_gram(a, batch, r_in + p, n, w, true);
+  plan_gram(a, batch, p, r_in, n, w, true);
   return a.used;
 }
 
-size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in) {
+size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in, bool split_r) {
   Arena a(nullptr, 0);
   GramWs w;
-  plan_gram(a, batch, r_in + p, n, w);
+  plan_gram(a, batch, p, r_in, n, w, false, split_r);
   return a.used;
 }
 
@@ -778,7 +807,8 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
                        int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
                        int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
                        int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
-                       size_t ws_bytes, float pivot_tol, const GramInverse* inv) {
+                       size_t ws_bytes, float pivot_tol, const GramInverse* inv,
+                       bool split_r) {
   bool ok = n >= 1 && p >= 0 && r_in >= 0 && r_in <= n && batch >= 1 && batch <= 65535 &&
             (p == 0 || (X && ldx >= n)) && (r_in == 0 || (R_in && ldr >= n)) && out &&
             ldo >= n && out_stride >= n * ldo && scale > 0.0f && damping >= 0.0f &&
@@ -805,7 +835,8 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   }
   Arena a(ws, ws_bytes);
   GramWs w;
-  plan_gram(a, batch, pe, n, w, inv != nullptr);
+  plan_gram(a, batch, p, r_in, n, w, inv != nullptr, split_r);
+  const int64_t ke = w.kr + p;   // K extent of the Gram products
   if (a.overflow) {
     set_error("fold_finalize_gram: workspace too small");
     return IFK_ERR_WORKSPACE;
@@ -840,20 +871,30 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
   const Blk b0 = blk(0, n);
   auto x_cols = [&](hipStream_t st, int64_t c0, int64_t c1) -> int {
     for (int e = 0; e < B; ++e) {
-      bf16_t* PT = w.PT + e * w.sPT + c0 * w.ldk + r_in;
       const char* Xe = (const char*)X[e] + c0 * (xdt == DT_BF16 ? 2 : 4);
-      // a bf16 chunk moves as 32-bit pairs through a 64 x 64 tile
-      if (xdt == DT_BF16)
-        RC(launch_transpose_bf16(st, (const bf16_t*)Xe, ldx, p, c1 - c0, PT, w.ldk));
-      else
-        RC(transpose_to_bf16(st, Xe, xdt, ldx, p, c1 - c0, PT, w.ldk, false));
+      for (bf16_t* base : {w.PT, w.PB}) {
+        bf16_t* PT = base + e * w.sPT + c0 * w.ldk + w.kr;
+        // a bf16 chunk moves as 32-bit pairs through a 64 x 64 tile
+        if (xdt == DT_BF16)
+          RC(launch_transpose_bf16(st, (const bf16_t*)Xe, ldx, p, c1 - c0, PT, w.ldk));
+        else
+          RC(transpose_to_bf16(st, Xe, xdt, ldx, p, c1 - c0, PT, w.ldk, false));
+        if (w.PB == w.PT) break;
+      }
     }
     return IFK_OK;
   };
+  const bool two = w.PB != w.PT;
   for (int e = 0; e < B; ++e) {
     bf16_t* PT = w.PT + e * w.sPT;
-    if (w.ldk > pe) RC(launch_zero_bf16(s, PT + pe, w.ldk, n, w.ldk - pe));
-    if (r_in > 0) RC(transpose_to_bf16(s, R_in[e], DT_F32, ldr, r_in, n, PT, w.ldk, true));
+    bf16_t* PB = w.PB + e * w.sPT;
+    if (w.ldk > ke) {
+      RC(launch_zero_bf16(s, PT + ke, w.ldk, n, w.ldk - ke));
+      if (two) RC(launch_zero_bf16(s, PB + ke, w.ldk, n, w.ldk - ke));
+    }
+    if (r_in > 0)
+      RC(transpose_to_bf16(s, R_in[e], DT_F32, ldr, r_in, n, PT, w.ldk, true,
+                           two ? PB : nullptr));
   }
   if (p > 0) RC(x_cols(s, b0.r0, b0.r1));
   if (la) {
@@ -959,7 +1000,8 @@ __global__ void cond_copy_kernel(const float* src, int64_t n, float* R, int64_t 
 }  // namespace
 
 size_t tsqr_fold_gram_ws(int64_t p, int64_t n, int64_t r_in) {
-  return align_up((size_t)n * n * sizeof(float), 256) + fold_finalize_gram_ws(1, p, n, r_in);
+  return align_up((size_t)n * n * sizeof(float), 256) +
+         fold_finalize_gram_ws(1, p, n, r_in, true);
 }
 
 int tsqr_fold_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
@@ -981,10 +1023,45 @@ int tsqr_fold_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, 
   const float* rs[1] = {R};
   RC(fold_finalize_gram(s, 1, xs, xdt, p, n, ldx, rs, ldr, r_in, 1.0f, 0.0f, tmp, DT_F32, n,
                         n * n, MATH_BF16, status, nullptr, (char*)ws + head, ws_bytes - head,
-                        pivot_tol));
+                        pivot_tol, nullptr, true));
   const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(n * n, 256), 4096);
   hipLaunchKernelGGL(cond_copy_kernel, dim3(blocks), dim3(256), 0, s, tmp, n, R, ldr, status);
   return check_launch("tsqr_fold_gram copy");
+}
+
+size_t tsqr_fold_gram_batched_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in) {
+  return align_up((size_t)batch * n * n * sizeof(float), 256) +
+         fold_finalize_gram_ws(batch, p, n, r_in, true);
+}
+
+int tsqr_fold_gram_batched(hipStream_t s, int64_t batch, const void* const* X, int xdt,
+                           int64_t p, int64_t n, int64_t ldx, float* const* R, int64_t ldr,
+                           int64_t r_in, float pivot_tol, int* status, void* ws,
+                           size_t ws_bytes) {
+  bool ok = batch >= 1 && batch <= 65535 && n >= 1 && p >= 0 && r_in >= 0 && r_in <= n &&
+            r_in + p >= n && R && X && ldr >= n && status && (p == 0 || ldx >= n);
+  for (int64_t e = 0; ok && e < batch; ++e) ok = R[e] && (p == 0 || X[e]);
+  if (!ok) {
+    set_error("tsqr_fold_gram_batched: invalid arguments (the folded factors must be square: "
+              "r_in + p >= n)");
+    return IFK_ERR_INVALID;
+  }
+  const size_t head = align_up((size_t)batch * n * n * sizeof(float), 256);
+  if (!ws || ws_bytes < head) {
+    set_error("tsqr_fold_gram_batched: workspace too small");
+    return IFK_ERR_WORKSPACE;
+  }
+  float* tmp = (float*)ws;
+  RC(fold_finalize_gram(s, batch, X, xdt, p, n, ldx, (const float* const*)R, ldr, r_in, 1.0f,
+                        0.0f, tmp, DT_F32, n, n * n, MATH_BF16, status, nullptr,
+                        (char*)ws + head, ws_bytes - head, pivot_tol, nullptr, true));
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(n * n, 256), 4096);
+  for (int64_t e = 0; e < batch; ++e) {
+    hipLaunchKernelGGL(cond_copy_kernel, dim3(blocks), dim3(256), 0, s, tmp + e * n * n, n, R[e],
+                       ldr, status + e);
+    RC(check_launch("tsqr_fold_gram_batched copy"));
+  }
+  return IFK_OK;
 }
 
 }  // namespace ifk

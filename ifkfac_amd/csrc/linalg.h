@@ -58,23 +58,38 @@ struct GramInverse {
   bf16_t *Zb, *ZT;
   int64_t ldb, sb;
 };
-size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in);
+// With split_r, R_in enters the Gram matrix as R_in = hi + lo (both RNE
+// bf16; R_in^T R_in to about 2^-17 by three products, K = 3 r_in) instead of
+// its bf16 rounding: the streaming fold's running factor is fp32 state, and a
+// 2^-9 rounding of it at every fold would add up along a stream.
+size_t fold_finalize_gram_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in,
+                             bool split_r = false);
 size_t fold_finalize_gram_inv_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in);
 int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int xdt, int64_t p,
                        int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
                        int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
                        int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
                        size_t ws_bytes, float pivot_tol = 1e-3f,
-                       const GramInverse* inv = nullptr);
+                       const GramInverse* inv = nullptr, bool split_r = false);
 
 // The streaming fold by the Gram route (bf16 arithmetic): R (rows [0, r_in)
 // valid) <- the factor of [R[0:r_in]; X] when r_in + p >= n; *status 1 (R
 // written) or 2 (a pivot below pivot_tol of its Gram diagonal, or input not
-// finite), R unchanged unless 1.
+// finite), R unchanged unless 1.  The running factor R enters split (hi + lo
+// bf16), the chunk X as its RNE bf16 rounding.
 size_t tsqr_fold_gram_ws(int64_t p, int64_t n, int64_t r_in);
 int tsqr_fold_gram(hipStream_t s, const void* X, int xdt, int64_t p, int64_t n, int64_t ldx,
                    float* R, int64_t ldr, int64_t r_in, float pivot_tol, int* status, void* ws,
                    size_t ws_bytes);
+
+// The same for B running factors of one shape, each folding its own chunk,
+// in one chain of launches (fold_finalize_gram's batch): R[e] and status[e]
+// exactly as tsqr_fold_gram gives them for that entry alone.
+size_t tsqr_fold_gram_batched_ws(int64_t batch, int64_t p, int64_t n, int64_t r_in);
+int tsqr_fold_gram_batched(hipStream_t s, int64_t batch, const void* const* X, int xdt,
+                           int64_t p, int64_t n, int64_t ldx, float* const* R, int64_t ldr,
+                           int64_t r_in, float pivot_tol, int* status, void* ws,
+                           size_t ws_bytes);
 
 // Z = R^{-1} for upper-triangular R (dtype rdt); Z fp32 upper triangular.
 size_t trinv_ws(int64_t n);
@@ -152,6 +167,24 @@ int precondition_apply_x3(hipStream_t s, const float* grad, int64_t n_out, int64
                           int64_t ldg, const bf16_t* const* ZX, int64_t ldx,
                           const bf16_t* const* ZG, int64_t ldg2, float* nat, int64_t ldn, void* ws,
                           size_t ws_bytes);
+
+// The two applies for B layers of one shape in grouped launches: each
+// product is one launch over the batch, every entry getting the bits the
+// single-layer call gives it.  Inverse copies (and their halves) sit at a
+// fixed element stride from entry to entry (sx, sg), the results at snat; the
+// gradients are given by pointer (ldg each).
+size_t precondition_apply_b_batched_ws(int64_t batch, int64_t n_out, int64_t n_in);
+int precondition_apply_b_batched(hipStream_t s, int64_t batch, const float* const* grad,
+                                 int64_t n_out, int64_t n_in, int64_t ldg, const bf16_t* ZXb,
+                                 const bf16_t* ZXt, int64_t ldx2, int64_t sx, const bf16_t* ZGb,
+                                 const bf16_t* ZGt, int64_t ldg2, int64_t sg, float* nat,
+                                 int64_t ldn, int64_t snat, void* ws, size_t ws_bytes);
+size_t precondition_apply_x3_batched_ws(int64_t batch, int64_t n_out, int64_t n_in);
+int precondition_apply_x3_batched(hipStream_t s, int64_t batch, const float* const* grad,
+                                  int64_t n_out, int64_t n_in, int64_t ldg,
+                                  const bf16_t* const* ZX, int64_t ldx, int64_t sx,
+                                  const bf16_t* const* ZG, int64_t ldg2, int64_t sg, float* nat,
+                                  int64_t ldn, int64_t snat, void* ws, size_t ws_bytes);
 
 // nat = Z_G Z_G^T grad Z_X Z_X^T, with Z_X = R_X^{-1}, Z_G = R_G^{-1} given.
 size_t precondition_apply_ws(int64_t n_out, int64_t n_in, int math);

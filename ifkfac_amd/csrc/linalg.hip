@@ -1470,6 +1470,150 @@ size_t precondition_apply_b_min_ws(int64_t n_out, int64_t n_in) {
   return a.used;
 }
 
+// ---------------------------------------------------------------------------
+// The applies for B layers of one shape (grouped launches).  Every product is
+// one launch over the batch with per-entry tile and split-K choices, and the
+// split-K scratch is B times a single call's, so each entry gets exactly the
+// bits precondition_apply_b / precondition_apply_x3 give it alone.  The
+// intermediate buffers are B-strided (E = n_out n_in elements per entry).
+// ---------------------------------------------------------------------------
+static void plan_apply_b_batched(Arena& a, int64_t B, int64_t n_out, int64_t n_in, bf16_t** T1,
+                                 bf16_t** T2, bf16_t** cv, SplitScratch* sp) {
+  const size_t e = (size_t)B * n_out * n_in;
+  *T1 = a.take<bf16_t>(e);
+  *T2 = a.take<bf16_t>(e);
+  *cv = a.take<bf16_t>(e);
+  sp->floats = (size_t)B * split_floats(TRINV_NB, std::max(n_out, n_in));
+  sp->p = a.take<float>(sp->floats);
+}
+
+size_t precondition_apply_b_batched_ws(int64_t batch, int64_t n_out, int64_t n_in) {
+  Arena a(nullptr, 0);
+  bf16_t *T1, *T2, *cv;
+  SplitScratch sp;
+  plan_apply_b_batched(a, batch, n_out, n_in, &T1, &T2, &cv, &sp);
+  return a.used;
+}
+
+static bool batch_args_ok(int64_t B, const float* const* grad, int64_t n_out, int64_t n_in,
+                          int64_t ldg, int64_t ldn, int64_t snat, const float* nat) {
+  if (B < 1 || B > 65535 || n_out < 1 || n_in < 1 || ldg < n_in || ldn < n_in || !grad || !nat ||
+      (B > 1 && snat < n_out * ldn))
+    return false;
+  for (int64_t e = 0; e < B; ++e)
+    if (!grad[e]) return false;
+  return true;
+}
+
+int precondition_apply_b_batched(hipStream_t s, int64_t B, const float* const* grad,
+                                 int64_t n_out, int64_t n_in, int64_t ldg, const bf16_t* ZXb,
+                                 const bf16_t* ZXt, int64_t ldx2, int64_t sx, const bf16_t* ZGb,
+                                 const bf16_t* ZGt, int64_t ldg2, int64_t sg, float* nat,
+                                 int64_t ldn, int64_t snat, void* ws, size_t ws_bytes) {
+  if (!batch_args_ok(B, grad, n_out, n_in, ldg, ldn, snat, nat) || ldx2 < n_in ||
+      ldg2 < n_out || !ZXb || !ZXt || !ZGb || !ZGt ||
+      (B > 1 && (sx < n_in * ldx2 || sg < n_out * ldg2))) {
+    set_error("precondition_apply_bf16_batched: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  bf16_t *T1T, *Tb, *cv;
+  SplitScratch sp;
+  plan_apply_b_batched(a, B, n_out, n_in, &T1T, &Tb, &cv, &sp);
+  RC(check_ws(a, "precondition_apply_bf16_batched"));
+  const int64_t E = n_out * n_in;
+  const int math = MATH_BF16, nb = (int)B;
+  for (int64_t e = 0; e < B; ++e)
+    RC(launch_transpose_cast(s, grad[e], ldg, n_out, n_in, cv + e * E, DT_BF16, n_out));
+  // the four products of apply_core_b, each over the batch
+  RC(gemm(s, math, n_in, n_out, n_out, 1.0f, A_n(cv, DT_BF16, n_out, TRI_NONE, E),
+          B_t(ZGt, DT_BF16, ldg2, TRI_UPPER, sg), 0.0f, per_entry(out_bf16(T1T, n_out, E)), nb,
+          sp));
+  RC(gemm(s, math, n_out, n_in, n_out, 1.0f, A_n(ZGb, DT_BF16, ldg2, TRI_UPPER, sg),
+          B_t(T1T, DT_BF16, n_out, TRI_NONE, E), 0.0f, per_entry(out_bf16(Tb, n_in, E)), nb, sp));
+  RC(gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(Tb, DT_BF16, n_in, TRI_NONE, E),
+          B_t(ZXt, DT_BF16, ldx2, TRI_UPPER, sx), 0.0f, per_entry(out_bf16(T1T, n_in, E)), nb,
+          sp));
+  return gemm(s, math, n_out, n_in, n_in, 1.0f, A_n(T1T, DT_BF16, n_in, TRI_NONE, E),
+              B_t(ZXb, DT_BF16, ldx2, TRI_LOWER, sx), 0.0f, per_entry(out_f32(nat, ldn, snat)),
+              nb, sp);
+}
+
+static void plan_apply_x3_batched(Arena& a, int64_t B, int64_t n_out, int64_t n_in, float** T,
+                                  bf16_t** Sh, bf16_t** Sl, bf16_t** gTh, bf16_t** gTl,
+                                  SplitScratch* sp) {
+  const size_t e = (size_t)B * n_out * n_in;
+  *T = a.take<float>(e);
+  *Sh = a.take<bf16_t>(e);
+  *Sl = a.take<bf16_t>(e);
+  *gTh = a.take<bf16_t>(e);
+  *gTl = a.take<bf16_t>(e);
+  sp->floats = (size_t)B * split_floats(TRINV_NB, std::max(n_out, n_in));
+  sp->p = a.take<float>(sp->floats);
+}
+
+size_t precondition_apply_x3_batched_ws(int64_t batch, int64_t n_out, int64_t n_in) {
+  Arena a(nullptr, 0);
+  float* T;
+  bf16_t *Sh, *Sl, *gTh, *gTl;
+  SplitScratch sp;
+  plan_apply_x3_batched(a, batch, n_out, n_in, &T, &Sh, &Sl, &gTh, &gTl, &sp);
+  return a.used;
+}
+
+// C (fp32, ldc, entry stride sc) = op(A) op(B) from the halves, B entries
+static int gemm_x3_batched(hipStream_t s, int B, int64_t M, int64_t N, int64_t K,
+                           const MatRef& Ah, const MatRef& Al, const MatRef& Bh,
+                           const MatRef& Bl, float* C, int64_t ldc, int64_t sc, SplitScratch sp) {
+  RC(gemm(s, MATH_BF16, M, N, K, 1.0f, Ah, Bh, 0.0f, per_entry(out_f32(C, ldc, sc)), B, sp));
+  RC(gemm(s, MATH_BF16, M, N, K, 1.0f, Ah, Bl, 1.0f, per_entry(out_f32(C, ldc, sc)), B, sp));
+  return gemm(s, MATH_BF16, M, N, K, 1.0f, Al, Bh, 1.0f, per_entry(out_f32(C, ldc, sc)), B, sp);
+}
+
+int precondition_apply_x3_batched(hipStream_t s, int64_t B, const float* const* grad,
+                                  int64_t n_out, int64_t n_in, int64_t ldg,
+                                  const bf16_t* const* ZX, int64_t ldx, int64_t sx,
+                                  const bf16_t* const* ZG, int64_t ldg2, int64_t sg, float* nat,
+                                  int64_t ldn, int64_t snat, void* ws, size_t ws_bytes) {
+  bool ok = batch_args_ok(B, grad, n_out, n_in, ldg, ldn, snat, nat) && ldx >= n_in &&
+            ldg2 >= n_out && ZX && ZG && (B == 1 || (sx >= n_in * ldx && sg >= n_out * ldg2));
+  for (int i = 0; ok && i < 4; ++i) ok = ZX[i] && ZG[i];
+  if (!ok) {
+    set_error("precondition_apply_x3_batched: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  float* T;
+  bf16_t *Sh, *Sl, *gTh, *gTl;
+  SplitScratch sp;
+  plan_apply_x3_batched(a, B, n_out, n_in, &T, &Sh, &Sl, &gTh, &gTl, &sp);
+  RC(check_ws(a, "precondition_apply_x3_batched"));
+  const int B16 = DT_BF16, nb = (int)B;
+  const int64_t E = n_out * n_in;
+  for (int64_t e = 0; e < B; ++e)
+    RC(launch_split_transpose(s, grad[e], ldg, n_out, n_in, gTh + e * E, gTl + e * E, n_out));
+  // T1^T = grad^T Z_G (n_in x n_out per entry)
+  RC(gemm_x3_batched(s, nb, n_in, n_out, n_out, A_n(gTh, B16, n_out, TRI_NONE, E),
+                     A_n(gTl, B16, n_out, TRI_NONE, E), B_t(ZG[2], B16, ldg2, TRI_UPPER, sg),
+                     B_t(ZG[3], B16, ldg2, TRI_UPPER, sg), T, n_out, E, sp));
+  // the batch's entries are consecutive rows of the same width: one split each
+  RC(launch_split_bf16(s, T, n_out, B * n_in, n_out, Sh, Sl, n_out, false));
+  // T2 = Z_G T1 (n_out x n_in)
+  RC(gemm_x3_batched(s, nb, n_out, n_in, n_out, A_n(ZG[0], B16, ldg2, TRI_UPPER, sg),
+                     A_n(ZG[1], B16, ldg2, TRI_UPPER, sg), B_t(Sh, B16, n_out, TRI_NONE, E),
+                     B_t(Sl, B16, n_out, TRI_NONE, E), T, n_in, E, sp));
+  RC(launch_split_bf16(s, T, n_in, B * n_out, n_in, Sh, Sl, n_in, false));
+  // T3 = T2 Z_X
+  RC(gemm_x3_batched(s, nb, n_out, n_in, n_in, A_n(Sh, B16, n_in, TRI_NONE, E),
+                     A_n(Sl, B16, n_in, TRI_NONE, E), B_t(ZX[2], B16, ldx, TRI_UPPER, sx),
+                     B_t(ZX[3], B16, ldx, TRI_UPPER, sx), T, n_in, E, sp));
+  RC(launch_split_bf16(s, T, n_in, B * n_out, n_in, Sh, Sl, n_in, false));
+  // nat = T3 Z_X^T
+  return gemm_x3_batched(s, nb, n_out, n_in, n_in, A_n(Sh, B16, n_in, TRI_NONE, E),
+                         A_n(Sl, B16, n_in, TRI_NONE, E), B_t(ZX[0], B16, ldx, TRI_LOWER, sx),
+                         B_t(ZX[1], B16, ldx, TRI_LOWER, sx), nat, ldn, snat, sp);
+}
+
 // precondition_apply_b in a workspace of any size from
 // precondition_apply_b_min_ws up: the split-K scratch gets what is left after
 // the operand buffers, up to what precondition_apply_b would take (with that

@@ -468,16 +468,18 @@ __device__ __forceinline__ float sm_maxabs(const float* A, float d, float* red) 
 // F upper triangular, U^T U = A is the fixed point
 //   F = up(E - F^T F),  up(X) = strict upper part of X + diag(X) / 2,
 // which contracts at a rate of about 2 ||F|| from F_0 = up(E); each sweep is
-// one 64 x 64 MFMA product.  On success A holds U (strict lower part zero)
-// and the function returns true; when the sweeps have not settled below
-// 2^-26 after maxit (E not small enough) A is left unchanged and it returns
-// false.  F, P: LDS scratch (padded 64 x 64), red: 4 floats.
+// one 64 x 64 MFMA product.  On success A holds U (strict lower part zero),
+// F holds U - I unrounded, and the function returns true; when the sweeps
+// have not settled below 2^-26 after maxit (E not small enough) A is left
+// unchanged and it returns false.  With one = 0, A holds E itself on entry
+// (for callers that form E without rounding I + E).  F, P: LDS scratch
+// (padded 64 x 64), red: 4 floats.
 __device__ __forceinline__ bool sm_chol_near_id(float* A, float* F, float* P, float* red,
-                                                int maxit) {
+                                                int maxit, float one = 1.0f) {
   const int t = threadIdx.x;
   for (int e = t; e < SB * SB; e += SNT) {
     const int i = e >> 6, j = e & 63;
-    const float x = A[i * SLD + j] - (i == j ? 1.0f : 0.0f);
+    const float x = A[i * SLD + j] - (i == j ? one : 0.0f);
     F[i * SLD + j] = (i < j) ? x : (i == j ? 0.5f * x : 0.0f);
   }
   __syncthreads();
@@ -489,7 +491,7 @@ __device__ __forceinline__ bool sm_chol_near_id(float* A, float* F, float* P, fl
     for (int q = 0; q < SB * SB / SNT; ++q) {
       const int e = t + SNT * q, i = e >> 6, j = e & 63;
       if (i <= j) {
-        const float x = A[i * SLD + j] - (i == j ? 1.0f : 0.0f) - P[i * SLD + j];
+        const float x = A[i * SLD + j] - (i == j ? one : 0.0f) - P[i * SLD + j];
         const float f = (i < j) ? x : 0.5f * x;
         dmax = fmaxf(dmax, fabsf(f - F[i * SLD + j]));
         F[i * SLD + j] = f;
@@ -546,6 +548,14 @@ __device__ __forceinline__ bool sm_inv_near_id(const float* U, float* Z, float* 
 // Out: U1 (Cholesky factor of P^T P), M1 = U1^{-1}, Q1 = P_top M1 (b x b,
 // ld b); *flag = 1 when a pivot falls below tol times its diagonal (the
 // panel then goes to the Householder fallback), else 0.
+//
+// P^T P = X_p^T X_p + P_top^T P_top is summed in fp64 before its one
+// rounding to fp32: along a stream the running factor's block P_top grows
+// with the rows folded so far and dominates the sum, and the fp32 rounding of
+// its 64-term products, repeated fold after fold, would add up (200 folds of
+// 4096 rows into a 512-column factor: 2e-6 relative Gram error where fp32
+// Householder QR keeps 1.4e-7; with the sum in fp64 the fold keeps the
+// latter).
 __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
                                                           const float* Ptop, int64_t ldr, int b,
                                                           float tol, float* U1, float* M1,
@@ -554,8 +564,10 @@ __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
   __shared__ float sP[SB * SLD];
   __shared__ float sM[SB * SLD];
   __shared__ float sT[TRINV_TMP];
+  __shared__ double sG64[SB * SB];
   __shared__ int bad;
-  if (threadIdx.x == 0) bad = 0;
+  const int t = threadIdx.x;
+  if (t == 0) bad = 0;
   {
     float vg[PAD_PER], vp[PAD_PER];   // both loads in flight together
     ld_pad(vg, G, SB, b, false, 1.0f);
@@ -564,7 +576,18 @@ __global__ __launch_bounds__(SNT) void panel_hr_a_kernel(const float* G,
     st_pad(sP, vp);
     __syncthreads();
   }
-  sm_gemm64<true, false>(sP, sP, sG, 1.0f, true);  // sG = X_p^T X_p + P_top^T P_top
+  // sG64 = X_p^T X_p + P_top^T P_top (P_top upper triangular: k <= min(i, j));
+  // beyond b the identity of the pad
+  for (int e = t; e < SB * SB; e += SNT) {
+    const int i = e >> 6, j = e & 63;
+    double v = (double)sG[i * SLD + j];
+    const int km = min(i, j);
+    for (int k = 0; k <= km; ++k) v += (double)sP[k * SLD + i] * (double)sP[k * SLD + j];
+    sG64[e] = v;
+  }
+  __syncthreads();
+  for (int e = t; e < SB * SB; e += SNT) sG[(e >> 6) * SLD + (e & 63)] = (float)sG64[e];
+  __syncthreads();
   sm_chol64<32, true>(sG, tol, &bad, 0);           // sG = U1
   sm_store(sG, U1, b, b);
   sm_trinv64(sG, sM, sT);                          // sM = M1
@@ -654,10 +677,26 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
   } else {
     st_pad(sQ, vQ);
     __syncthreads();
-    sm_gemm64<true, false>(sQ, sQ, sG, 1.0f, true);  // sG = Q2^T Q2 + Q1^T Q1
-    // after the first pass sG is I + E with E small: a few MFMA sweeps give U2
-    // and M2; the general Cholesky / inverse are the fallback
-    near = sm_chol_near_id(sG, sX, sM, sgn, 8);   // sG = U2
+    // after the first pass G2 = Q^T Q is I + E with E small.  E is formed
+    // without rounding I + E to fp32 -- near 1 that rounding is as large as
+    // E, and along a stream the lost correction adds up fold after fold --
+    // from D = Q1 - I (exact):  E = Q2^T Q2 + D + D^T + D^T D  (zero in the
+    // pad, where sG holds the identity).
+    for (int e = t; e < SB * SB; e += SNT) {
+      const int i = e >> 6, j = e & 63;
+      sM[i * SLD + j] = (i < b && j < b) ? sQ[i * SLD + j] - (i == j ? 1.0f : 0.0f) : 0.0f;
+    }
+    __syncthreads();
+    for (int e = t; e < SB * SB; e += SNT) {
+      const int i = e >> 6, j = e & 63;
+      const float g = sG[i * SLD + j];
+      sG[i * SLD + j] = (i < b && j < b) ? g + sM[i * SLD + j] + sM[j * SLD + i] : 0.0f;
+    }
+    __syncthreads();
+    sm_gemm64<true, false>(sM, sM, sG, 1.0f, true);  // sG = E
+    // a few MFMA sweeps give U2 (and F = U2 - I) and M2; the general
+    // Cholesky / inverse of I + E are the fallback
+    near = sm_chol_near_id(sG, sX, sM, sgn, 8, 0.0f);   // sG = U2
     if (near) {
       // F = U2 - I exactly as the sweeps left it: U2 itself, rounded next to
       // 1, drops corrections below half an ulp of 1
@@ -667,6 +706,8 @@ __global__ __launch_bounds__(SNT) void panel_hrw_kernel(const float* G, const fl
         vF[q] = sX[(e >> 6) * SLD + (e & 63)];
       }
     } else {
+      for (int j = t; j < SB; j += SNT) sG[j * SLD + j] += 1.0f;   // I + E
+      __syncthreads();
       sm_chol64(sG, 0.25f, &bad, 0);
     }
     if (!(near && sm_inv_near_id(sG, sM, sX, sN, sgn, 8)))   // sM = M2

@@ -227,6 +227,7 @@ class IFKFAC(torch.optim.Optimizer):
         bf = [m for m, (iX, _) in invs.items() if isinstance(iX, tuple)]
         kap = torch.cat([torch.cat([invs[m][0][3], invs[m][1][3]]) for m in bf]).view(-1, 2).cpu() \
             if bf else None
+        fp32_solves = []
         for module, (invX, invG) in invs.items():
             R_X, R_G = clean[module]
             if not isinstance(invX, tuple):
@@ -247,17 +248,29 @@ class IFKFAC(torch.optim.Optimizer):
                 logger.debug("IFKFAC: kappa(R_X) %.3g, kappa(R_G) %.3g: fp32 solves for %s",
                              kx, kg, type(module).__name__)
 
-                def inv32(R):
-                    Z = be.tri_inverse(R, MATH_F32)
-                    return (Z, be.inverse_split_copies(Z)) if split else (Z, None)
-
-                (ZX, sx), (ZG, sg) = run_pair(R_X.device, lambda R=R_X: inv32(R),
-                                              lambda R=R_G: inv32(R),
-                                              b_first=R_G.shape[0] > R_X.shape[0])
+                ZX, ZG = run_pair(R_X.device, lambda R=R_X: be.tri_inverse(R, MATH_F32),
+                                  lambda R=R_G: be.tri_inverse(R, MATH_F32),
+                                  b_first=R_G.shape[0] > R_X.shape[0])
                 self._inverses[module] = (ZX, ZG)
-                if split:
-                    self._split_copies[module] = (sx, sg)
                 self._solve_math[module] = MATH_F32
+                fp32_solves.append(module)
+        if split and fp32_solves:
+            # the split halves of same-shape layers in one buffer per side, at
+            # one stride from layer to layer, so their apply can be grouped
+            groups: Dict[tuple, list] = {}
+            for module in fp32_solves:
+                ZX, ZG = self._inverses[module]
+                groups.setdefault((ZX.shape[0], ZG.shape[0], ZX.device), []).append(module)
+            batched = hasattr(be, "inverse_split_copies_batched")
+            for mods in groups.values():
+                if batched and len(mods) > 1:
+                    sxs = be.inverse_split_copies_batched([self._inverses[m][0] for m in mods])
+                    sgs = be.inverse_split_copies_batched([self._inverses[m][1] for m in mods])
+                else:
+                    sxs = [be.inverse_split_copies(self._inverses[m][0]) for m in mods]
+                    sgs = [be.inverse_split_copies(self._inverses[m][1]) for m in mods]
+                for m, sx, sg in zip(mods, sxs, sgs):
+                    self._split_copies[m] = (sx, sg)
         self.timing["factor_compute"].append(time.perf_counter() - t0)
 
     # ------------------------------------------------------------------ apply
@@ -286,6 +299,33 @@ class IFKFAC(torch.optim.Optimizer):
         R_X = self._factors[module][0]
         m = self._solve_math.get(module, solve_math_for(R_X.dtype))
         return get_backend().precondition_apply(grad_w, Z_X, Z_G, m)
+
+    def _nat_grads_grouped(self, mods) -> list:
+        """_nat_grad for a bucket of same-shape layers (apply_vered_batched,
+        ifkfac/triangular.py:506-544): the layers that take the same apply and
+        whose inverse copies sit at one stride from layer to layer (as the
+        batched factor update and inverse_split_copies_batched leave them) go
+        through one grouped call, each product one launch over the group; the
+        others layer by layer.  Every layer gets the bits its own call gives."""
+        be = get_backend()
+        out = {}
+        bf = [m for m in mods if m in self._inverse_copies]
+        x3 = [m for m in mods if m not in self._inverse_copies and m in self._split_copies]
+        if len(bf) > 1 and hasattr(be, "precondition_apply_bf16_batched"):
+            ZX2s = [self._inverse_copies[m][0] for m in bf]
+            ZG2s = [self._inverse_copies[m][1] for m in bf]
+            if all(be.entry_stride(list(ts)) is not None
+                   for side in (ZX2s, ZG2s) for ts in zip(*side)):
+                nat = be.precondition_apply_bf16_batched([m.weight.grad for m in bf], ZX2s, ZG2s)
+                out.update({m: nat[e] for e, m in enumerate(bf)})
+        if len(x3) > 1 and hasattr(be, "precondition_apply_x3_batched"):
+            sxs = [self._split_copies[m][0] for m in x3]
+            sgs = [self._split_copies[m][1] for m in x3]
+            if all(be.entry_stride(list(ts)) is not None
+                   for side in (sxs, sgs) for ts in zip(*side)):
+                nat = be.precondition_apply_x3_batched([m.weight.grad for m in x3], sxs, sgs)
+                out.update({m: nat[e] for e, m in enumerate(x3)})
+        return [out[m] if m in out else self._nat_grad(m, m.weight.grad, False) for m in mods]
 
     def _update_param(self, param: torch.Tensor, nat: torch.Tensor, lr: float, wd: float,
                       mom: float, module: Optional[nn.Module], clip: bool = False) -> None:
@@ -355,7 +395,7 @@ class IFKFAC(torch.optim.Optimizer):
 
         for (n_in, n_out, _, _), entries in fast.items():
             try:
-                nats = [self._nat_grad(m, m.weight.grad, False) for m, _, _, _ in entries]
+                nats = self._nat_grads_grouped([m for m, _, _, _ in entries])
             except Exception as e:  # same recovery as the reference's bucket failure
                 logger.warning(
                     "IFKFAC: apply_vered_batched failed for bucket (n_in=%d, n_out=%d, B=%d): "

@@ -169,8 +169,13 @@ int ifk_fold_finalize_gram(void* stream, const void* X, int x_dtype, int64_t p, 
  * The streaming fold by the Gram route -- replaces streaming_tsqr_update
  * (ifkfac/triangular.py:246-307) in bf16 arithmetic when the folded factor is
  * square (r_in + p >= n): R (n x n fp32, rows [0, r_in) valid) becomes the
- * upper factor with positive diagonal of [R[0:r_in]; X] from the Gram matrix
- * of the bf16-rounded rows and the blocked Cholesky of ifk_fold_finalize_gram.
+ * upper factor with positive diagonal of [R[0:r_in]; X] from its Gram matrix
+ * and the blocked Cholesky of ifk_fold_finalize_gram.  The chunk enters as its
+ * RNE bf16 rounding; the running factor, fp32 state that every fold of a
+ * stream reads again, enters split as hi + lo (two bf16 halves: R^T R to
+ * about 2^-17, three products over its rows) -- rounded to bf16 at every
+ * fold, it would drift (0.28 relative Gram error after 200 folds of 4096 x
+ * 768 chunks, against 2.5e-4 split).
  * *status: 1 R written; 2 a pivot fell below pivot_tol times its Gram
  * diagonal (too ill-conditioned for the Gram route at that tolerance) or the
  * input is not finite.  R is left unchanged unless *status is 1, so the caller
@@ -181,6 +186,23 @@ size_t ifk_tsqr_fold_gram_workspace_size(int64_t p, int64_t n, int64_t r_in);
 int ifk_tsqr_fold_gram(void* stream, const void* X, int x_dtype, int64_t p, int64_t n,
                        int64_t ldx, float* R, int64_t ldr, int64_t r_in, float pivot_tol,
                        int32_t* status, void* workspace, size_t workspace_bytes);
+
+/*
+ * ifk_tsqr_fold_gram for `batch` running factors of one shape, each folding
+ * its own chunk (X[e], p x n), in one chain of launches -- replaces the
+ * per-layer folds of the bucketed flush (ifkfac/activation_hooks.py:370-457,
+ * its batched_qr over same-shape layers, triangular.py:331-379).  R[e]
+ * (n x n fp32, ldr, rows [0, r_in) valid) and status[e] (device) are exactly
+ * what ifk_tsqr_fold_gram gives that entry alone: 1 and R[e] the factor of
+ * [R[e][0:r_in]; X[e]], or 2 and R[e] untouched (the caller folds that entry
+ * by ifk_tsqr_fold).  X and R are host arrays of device pointers.
+ */
+size_t ifk_tsqr_fold_gram_batched_workspace_size(int64_t batch, int64_t p, int64_t n,
+                                                 int64_t r_in);
+int ifk_tsqr_fold_gram_batched(void* stream, int64_t batch, const void* const* X, int x_dtype,
+                               int64_t p, int64_t n, int64_t ldx, float* const* R, int64_t ldr,
+                               int64_t r_in, float pivot_tol, int32_t* status, void* workspace,
+                               size_t workspace_bytes);
 
 /*
  * ifk_fold_finalize_gram for `batch` layers of the same shape in the same
@@ -337,6 +359,37 @@ int ifk_precondition_apply_bf16_noalloc(void* stream, const float* grad, int64_t
  * Bias preconditioning -- replaces apply_vered_bias(grad_b, R_G)
  * (ifkfac/triangular.py:659-705): out = (R_G^T R_G)^{-1} g, given Z_G.
  */
+/*
+ * The two per-step applies for `batch` layers of one shape in grouped
+ * launches -- replaces apply_vered_batched (ifkfac/triangular.py:506-544, the
+ * bucketed apply of ifkfac/ifkfac.py:371-380): each of the four products (in
+ * the _x3 form each split product) is one launch over the batch, and every
+ * entry's nat is bit for bit what ifk_precondition_apply_bf16 /
+ * ifk_precondition_apply_x3 give that layer alone.  grad is a host array of
+ * `batch` device pointers (n_out x n_in fp32, ldg each); the inverse copies
+ * (and their halves) of entry e sit at e * stride_zx / e * stride_zg elements
+ * from the given ones, and nat of entry e at e * stride_nat.
+ */
+size_t ifk_precondition_apply_bf16_batched_workspace_size(int64_t batch, int64_t n_out,
+                                                         int64_t n_in);
+int ifk_precondition_apply_bf16_batched(void* stream, int64_t batch, const float* const* grad,
+                                        int64_t n_out, int64_t n_in, int64_t ldg,
+                                        const void* Z_Xb, const void* Z_Xt, int64_t ldzx,
+                                        int64_t stride_zx, const void* Z_Gb, const void* Z_Gt,
+                                        int64_t ldzg, int64_t stride_zg, float* nat, int64_t ldn,
+                                        int64_t stride_nat, void* workspace,
+                                        size_t workspace_bytes);
+size_t ifk_precondition_apply_x3_batched_workspace_size(int64_t batch, int64_t n_out,
+                                                       int64_t n_in);
+int ifk_precondition_apply_x3_batched(void* stream, int64_t batch, const float* const* grad,
+                                      int64_t n_out, int64_t n_in, int64_t ldg,
+                                      const void* Z_X_hi, const void* Z_X_lo, const void* Z_XT_hi,
+                                      const void* Z_XT_lo, int64_t ldzx, int64_t stride_zx,
+                                      const void* Z_G_hi, const void* Z_G_lo, const void* Z_GT_hi,
+                                      const void* Z_GT_lo, int64_t ldzg, int64_t stride_zg,
+                                      float* nat, int64_t ldn, int64_t stride_nat,
+                                      void* workspace, size_t workspace_bytes);
+
 size_t ifk_precondition_bias_workspace_size(int64_t n_out);
 int ifk_precondition_bias(void* stream, const float* g, int64_t n_out, const float* Z_G,
                           int64_t ldzg, float* out, void* workspace, size_t workspace_bytes);

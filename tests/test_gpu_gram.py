@@ -202,17 +202,18 @@ FOLD_TOL = 1e-4
     ([2048], 4096, 3072, torch.float32),
 ])
 def test_tsqr_fold_gram_matches_closed_form(hip, prev, p, n, xdt):
-    """R <- the undamped factor of [bf16(R_in); bf16(X)]: ||R^T R - P^T P||_F /
-    ||P^T P||_F <= 3e-5 (Cholesky's backward error with 2^-17 products), upper
-    triangular with a positive diagonal, and no worse than the bf16 panel fold of the
-    same chunk against the same closed form."""
+    """R <- the undamped factor of [R_in; bf16(X)] (the running factor enters as
+    fp32 state, split hi + lo; the chunk as the bf16 operand it is):
+    ||R^T R - P^T P||_F / ||P^T P||_F <= 3e-5 (Cholesky's backward error with
+    2^-17 products), upper triangular with a positive diagonal, and no worse than
+    the bf16 panel fold of the same chunk against the same closed form."""
     g = torch.Generator(device=DEV).manual_seed(p + n + len(prev))
     R, r = _fold_chunks(hip, [torch.randn(q, n, device=DEV, generator=g) for q in prev], n)
     X = torch.randn(p, n, device=DEV, generator=g).to(xdt)
     R_before = R.clone()
     st = hip.fold_gram_(R, r, X, FOLD_TOL)
     assert st.item() == 1
-    parts = ([_bf16_np(R_before[:r])] if r > 0 else []) + [_bf16_np(X)]
+    parts = ([R_before[:r].double().cpu().numpy()] if r > 0 else []) + [_bf16_np(X)]
     want = O.chol_factor(parts, 1, 0.0)
     e = _gram_rel(R, want)
     Rp = R_before.clone()

@@ -1,0 +1,199 @@
+"""Grouped launches for same-shape layers (the reference's bucketed apply and
+flush: ifkfac/triangular.py:331-379, 506-544; ifkfac/activation_hooks.py:370-457;
+ifkfac/ifkfac.py:371-380).
+
+Each grouped call runs every product once over the group and must give every
+layer exactly the bits of its own per-layer call (torch.equal), for the bf16
+apply, the split (x3) apply, and the Gram-route streaming fold of a flush,
+including an entry the Gram route refuses.  End to end, IFKFAC's bucketed
+apply and RawActivationHooks' batched flush with the grouped calls give the
+same weights and factors as with the grouped calls hidden from them.
+"""
+import math
+
+import pytest
+import torch
+import torch.nn as nn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _upper_inverse(n, g, scale=1.0):
+    R = torch.triu(torch.randn(n, n, device=DEV, generator=g)) * 0.05 * scale
+    R += torch.eye(n, device=DEV)
+    return torch.linalg.inv(R.double()).float().triu().contiguous()
+
+
+@pytest.mark.parametrize("n_out,n_in", [(1024, 1024), (1536, 512)])
+def test_apply_bf16_batched_bit_equal(hip, n_out, n_in):
+    """B = 4 layers: the bf16 apply from copies stacked in one (B, n, n) buffer
+    per side against the per-layer ifk_precondition_apply_bf16."""
+    g = torch.Generator(device=DEV).manual_seed(n_out + n_in)
+    B = 4
+    ZX = torch.stack([_upper_inverse(n_in, g) for _ in range(B)])
+    ZG = torch.stack([_upper_inverse(n_out, g) for _ in range(B)])
+    ZXb, ZXt = ZX.bfloat16(), ZX.transpose(1, 2).contiguous().bfloat16()
+    ZGb, ZGt = ZG.bfloat16(), ZG.transpose(1, 2).contiguous().bfloat16()
+    grads = [torch.randn(n_out, n_in, device=DEV, generator=g) * 0.1 for _ in range(B)]
+    nat = hip.precondition_apply_bf16_batched(grads, [(ZXb[e], ZXt[e]) for e in range(B)],
+                                              [(ZGb[e], ZGt[e]) for e in range(B)])
+    for e in range(B):
+        one = hip.precondition_apply_bf16(grads[e], (ZXb[e], ZXt[e]), (ZGb[e], ZGt[e]))
+        assert torch.equal(nat[e], one), e
+
+
+@pytest.mark.parametrize("n_out,n_in", [(1024, 1024), (512, 1536)])
+def test_apply_x3_batched_bit_equal(hip, n_out, n_in):
+    """B = 3 layers: the split apply from halves made by
+    inverse_split_copies_batched against the per-layer ifk_precondition_apply_x3
+    on the per-layer halves (which are bit-equal too)."""
+    g = torch.Generator(device=DEV).manual_seed(7 + n_out)
+    B = 3
+    ZXs = [_upper_inverse(n_in, g, 3.0) for _ in range(B)]
+    ZGs = [_upper_inverse(n_out, g, 3.0) for _ in range(B)]
+    sx = hip.inverse_split_copies_batched(ZXs)
+    sg = hip.inverse_split_copies_batched(ZGs)
+    grads = [torch.randn(n_out, n_in, device=DEV, generator=g) * 0.1 for _ in range(B)]
+    nat = hip.precondition_apply_x3_batched(grads, sx, sg)
+    for e in range(B):
+        sx1, sg1 = hip.inverse_split_copies(ZXs[e]), hip.inverse_split_copies(ZGs[e])
+        assert all(torch.equal(a, b) for a, b in zip(sx[e], sx1))
+        one = hip.precondition_apply_x3(grads[e], sx1, sg1)
+        assert torch.equal(nat[e], one), e
+
+
+@pytest.mark.parametrize("n,p", [(768, 4096), (2304, 4096)])
+def test_fold_gram_batched_bit_equal(hip, n, p):
+    """B = 4 running factors of one shape, each folding its own chunk: the
+    batched Gram-route fold against the per-layer fold_gram_, factors and
+    statuses bit-equal; entry 2's chunk repeats a column of large scale, so the
+    Gram route refuses it (status 2) and its buffer stays untouched."""
+    from ifkfac_amd.activation_hooks import GRAM_FOLD_TOL
+    g = torch.Generator(device=DEV).manual_seed(n)
+    B = 4
+    Rs0 = []
+    for e in range(B):
+        R = torch.zeros(n, n, device=DEV)
+        assert hip.fold_gram_(R, 0, torch.randn(p, n, device=DEV, generator=g),
+                              GRAM_FOLD_TOL).item() == 1
+        Rs0.append(R)
+    Xs = [torch.randn(p, n, device=DEV, generator=g) for _ in range(B)]
+    Xs[2][:, 5] *= 1e3
+    Xs[2][:, 17] = Xs[2][:, 5]
+    Rb = [R.clone() for R in Rs0]
+    st = hip.fold_gram_batched_(Rb, n, Xs, GRAM_FOLD_TOL)
+    for e in range(B):
+        R1 = Rs0[e].clone()
+        s1 = hip.fold_gram_(R1, n, Xs[e], GRAM_FOLD_TOL)
+        assert int(st[e].item()) == int(s1.item())
+        assert torch.equal(Rb[e], R1), e
+    assert int(st[2].item()) == 2 and torch.equal(Rb[2], Rs0[2])
+    assert all(int(st[e].item()) == 1 for e in (0, 1, 3))
+
+
+class _Hide:
+    """Hide attributes of the backend object for the duration (the callers take
+    the per-layer path when a grouped method is missing)."""
+
+    def __init__(self, be, names):
+        self.be, self.names, self.saved = be, names, {}
+
+    def __enter__(self):
+        cls = type(self.be)
+        for nm in self.names:
+            self.saved[nm] = getattr(cls, nm)
+            delattr(cls, nm)
+
+    def __exit__(self, *a):
+        cls = type(self.be)
+        for nm, f in self.saved.items():
+            setattr(cls, nm, f)
+
+
+def _mlp(seed, n=1024, layers=4):
+    torch.manual_seed(seed)
+    mods = []
+    for _ in range(layers):
+        mods += [nn.Linear(n, n), nn.GELU()]
+    return nn.Sequential(*mods).to(DEV)
+
+
+def test_ifkfac_grouped_apply_matches_per_layer(hip):
+    """4 x (Linear(1024, 1024) + GELU), bf16 factors: the first layer's input is
+    near-isotropic (bf16 apply), the GELU inputs are not (split apply), so the
+    bucket holds a group of each kind.  Two optimizer steps with the grouped
+    applies give bit for bit the weights of the same steps with the grouped
+    methods hidden, and the grouped calls were made."""
+    from ifkfac_amd import IFKFAC
+    import contextlib, io
+    calls = {"bf16": 0, "x3": 0}
+    cls = type(hip)
+    real_b, real_x = cls.precondition_apply_bf16_batched, cls.precondition_apply_x3_batched
+
+    def wrap_b(self, *a):
+        calls["bf16"] += 1
+        return real_b(self, *a)
+
+    def wrap_x(self, *a):
+        calls["x3"] += 1
+        return real_x(self, *a)
+
+    def run(grouped):
+        model = _mlp(0)
+        opt = IFKFAC(model, lr=1e-2, damping=1e-2, factor_update_freq=1, momentum=0.9,
+                     use_true_bf16=True)
+        g = torch.Generator(device=DEV).manual_seed(1)
+        x = torch.randn(2048, 1024, device=DEV, generator=g)
+        tgt = torch.randn(2048, 1024, device=DEV, generator=g) * 0.1
+        for _ in range(2):
+            opt.zero_grad()
+            ((model(x) - tgt) ** 2).mean().backward()
+            with contextlib.redirect_stdout(io.StringIO()):
+                opt.step()
+        torch.cuda.synchronize()
+        return [p.detach().clone() for p in model.parameters()], opt
+
+    cls.precondition_apply_bf16_batched, cls.precondition_apply_x3_batched = wrap_b, wrap_x
+    try:
+        Wg, opt = run(True)
+    finally:
+        cls.precondition_apply_bf16_batched, cls.precondition_apply_x3_batched = real_b, real_x
+    modes = ["bf16" if m in opt._inverse_copies else "x3" for m in opt._factors]
+    print(f"apply modes {modes}; grouped calls {calls}")
+    with _Hide(hip, ["precondition_apply_bf16_batched", "precondition_apply_x3_batched",
+                     "inverse_split_copies_batched"]):
+        Wp, _ = run(False)
+    assert sum(c > 0 for c in calls.values()) >= 1
+    if modes.count("x3") > 1:
+        assert calls["x3"] == 2
+    for a, b in zip(Wg, Wp):
+        assert torch.equal(a, b)
+
+
+def test_hooks_batched_flush_grouped_matches_per_layer(hip):
+    """RawActivationHooks(batched=True) in bf16 arithmetic over three same-shape
+    layers: the flush folds each side's buffered chunks of the three layers by
+    one batched Gram-route fold; the factors are bit for bit those of the
+    per-layer flush."""
+    from ifkfac_amd import RawActivationHooks
+    from ifkfac_amd._backend import MATH_BF16
+
+    def run():
+        model = _mlp(3, n=768, layers=3)
+        hooks = RawActivationHooks(model, damping=1e-3, batched=True, math=MATH_BF16)
+        hooks.enable()
+        g = torch.Generator(device=DEV).manual_seed(4)
+        for _ in range(2):
+            x = torch.randn(1024, 768, device=DEV, generator=g)
+            model(x).square().mean().backward()
+            hooks.flush()
+        f = hooks.get_factors()
+        return [tuple(t.clone() for t in f[m]) for m in model if isinstance(m, nn.Linear)]
+
+    grouped = run()
+    with _Hide(hip, ["fold_gram_batched_"]):
+        single = run()
+    for a, b in zip(grouped, single):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
