@@ -228,24 +228,25 @@ class LayerChain:
             self.RX = torch.zeros(n_in, n_in, device=self.dev)
             self.RG = torch.zeros(n_out, n_out, device=self.dev)
 
-    def _side(self, T, R, how):
+    def _side(self, T, R, how, math_=None):
         import torch
         from ifkfac_amd._backend import MATH_BF16
         from ifkfac_amd.activation_hooks import fold_chunk
         be, p = self.be, self.p
+        am = self.math if math_ is None else math_
         r = 0
         last = T
         if self.chunks > 1:
             # the hooks fold every chunk but the held one into the running factor
             q = p // self.chunks
             for c in range(self.chunks - 1):
-                r = fold_chunk(R, r, T[c * q:(c + 1) * q], self.math)
+                r = fold_chunk(R, r, T[c * q:(c + 1) * q], am)
             last = T[(self.chunks - 1) * q:]
         out_dtype = torch.bfloat16
         # as IFKFAC's factor update: the Gram path in bf16 arithmetic (the
         # factor's inverse formed in the same call), CholeskyQR2 blocks in fp32
         # arithmetic
-        gram = how == "gram" and self.math == MATH_BF16
+        gram = how == "gram" and am == MATH_BF16
         if gram:
             F, st, _, (Z, Zb, ZT) = be.fold_finalize_gram_batched(
                 [R] if r > 0 else None, r, [last], 1 / math.sqrt(p), self.lam, out_dtype,
@@ -253,8 +254,8 @@ class LayerChain:
             return F[0], st, (Z[0], Zb[0], ZT[0])
         cqr = how == "cqr" or (how == "gram" and not gram)
         F, st = be.fold_finalize(R if r > 0 else None, r, last, 1 / math.sqrt(p), self.lam,
-                                 out_dtype, self.math, cqr=cqr, gram=gram)
-        return F, st, (be.tri_inverse_bf16(F) if self.math == MATH_BF16
+                                 out_dtype, am, cqr=cqr, gram=gram)
+        return F, st, (be.tri_inverse_bf16(F) if am == MATH_BF16
                        else be.tri_inverse(F, 0))
 
     def factor_update(self):
@@ -268,7 +269,8 @@ class LayerChain:
         st = torch.cat([out[0][1], out[1][1]]).cpu()
         for i, (T, R) in enumerate(((self.X, RX), (self.D, RG))):
             if int(st[i]) == 2:
-                out[i] = self._side(T, R, "panel")
+                # as the hooks: a flagged side is refactored in fp32 arithmetic
+                out[i] = self._side(T, R, "panel", math_=0)
         self.factors = out
         return out
 

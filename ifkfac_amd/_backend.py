@@ -22,6 +22,9 @@ from ._lib import IFK_BF16, IFK_F32, IFK_MATH_BF16, IFK_MATH_F32, IFKFACBackendE
 
 MATH_F32 = IFK_MATH_F32
 MATH_BF16 = IFK_MATH_BF16
+# Relative pivot threshold of the Gram route's factor update (status 2 below
+# it: the side is refactored by the panel path); the library's default too.
+GRAM_PIVOT_TOL = 1e-3
 
 _DT = {torch.float32: IFK_F32, torch.bfloat16: IFK_BF16}
 _TORCH_DT = {IFK_F32: torch.float32, IFK_BF16: torch.bfloat16}
@@ -212,7 +215,8 @@ class HipBackend:
         return st
 
     def fold_finalize_gram_batched(self, Rs, r_in: int, Xs, scale: float, damping: float,
-                                   out_dtype: torch.dtype, with_inverse: bool = False):
+                                   out_dtype: torch.dtype, with_inverse: bool = False,
+                                   pivot_tol: float = GRAM_PIVOT_TOL):
         """fold_finalize(..., gram=True, with_kappa=True) for B same-shape sides in
         the same launches (ifk_fold_finalize_gram_batched).  Xs: B chunks (p x n,
         one dtype); Rs: B running-factor buffers or None when r_in == 0.
@@ -220,7 +224,8 @@ class HipBackend:
         b is bitwise the single-side result.  With ``with_inverse``
         (ifk_fold_finalize_gram_inverse) a fourth value (Z fp32, Zb, ZT bf16, each
         (B, n, n)): each factor's inverse and its bf16 copies, from the Cholesky's
-        1024-block inverses (meaningless where the status is 2)."""
+        1024-block inverses (meaningless where the status is 2).  ``pivot_tol``: the
+        relative pivot threshold of the status."""
         B = len(Xs)
         mats = [_mat(X, "fold_finalize_gram_batched") for X in Xs]
         X0, ldx, xdt = mats[0]
@@ -256,7 +261,8 @@ class HipBackend:
                     self._stream(dev), B, ctypes.cast(xptrs, ctypes.c_void_p), xdt, p, n, ldx,
                     ctypes.cast(rptrs, ctypes.c_void_p) if rptrs is not None else None, ldr,
                     int(r_in), float(scale), float(damping), _ptr(out), _DT[out_dtype], n, n * n,
-                    _ptr(st), _ptr(kb), _ptr(Z), n, n * n, _ptr(Zb), _ptr(ZT), n, n * n,
+                    float(pivot_tol), _ptr(st), _ptr(kb), _ptr(Z), n, n * n, _ptr(Zb), _ptr(ZT),
+                    n, n * n,
                     _ptr(ws), ws.numel())
             _lib.check(rc, "ifk_fold_finalize_gram_inverse")
             return out, st, kb, (Z, Zb, ZT)
@@ -267,7 +273,7 @@ class HipBackend:
                 self._stream(dev), B, ctypes.cast(xptrs, ctypes.c_void_p), xdt, p, n, ldx,
                 ctypes.cast(rptrs, ctypes.c_void_p) if rptrs is not None else None, ldr,
                 int(r_in), float(scale), float(damping), _ptr(out), _DT[out_dtype], n, n * n,
-                MATH_BF16, _ptr(st), _ptr(kb), _ptr(ws), ws.numel())
+                MATH_BF16, float(pivot_tol), _ptr(st), _ptr(kb), _ptr(ws), ws.numel())
         _lib.check(rc, "ifk_fold_finalize_gram_batched")
         return out, st, kb
 

@@ -22,7 +22,7 @@ IFK_BF16 = 1
 IFK_MATH_F32 = 0
 IFK_MATH_BF16 = 1
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class IFKFACBackendError(RuntimeError):
@@ -62,8 +62,8 @@ SIGNATURES = {
     "ifk_fold_finalize_gram_batched_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "ifk_fold_finalize_gram_batched": (_c_int, [_c_vp, _c_i64, _c_vp, _c_int, _c_i64, _c_i64,
                                                 _c_i64, _c_vp, _c_i64, _c_i64, _c_f, _c_f, _c_vp,
-                                                _c_int, _c_i64, _c_i64, _c_int, _c_vp, _c_vp,
-                                                _c_vp, _c_sz]),
+                                                _c_int, _c_i64, _c_i64, _c_int, _c_f, _c_vp,
+                                                _c_vp, _c_vp, _c_sz]),
     "ifk_inverse_split_copies": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp,
                                           _c_i64]),
     "ifk_precondition_apply_x3_workspace_size": (_c_sz, [_c_i64, _c_i64]),
@@ -139,7 +139,7 @@ SIGNATURES = {
     "ifk_fold_finalize_gram_inverse_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "ifk_fold_finalize_gram_inverse": (_c_int, [_c_vp, _c_i64, _c_vp, _c_int, _c_i64, _c_i64,
                                                 _c_i64, _c_vp, _c_i64, _c_i64, _c_f, _c_f, _c_vp,
-                                                _c_int, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp,
+                                                _c_int, _c_i64, _c_i64, _c_f, _c_vp, _c_vp, _c_vp,
                                                 _c_i64, _c_i64, _c_vp, _c_vp, _c_i64, _c_i64,
                                                 _c_vp, _c_sz]),
     "ifk_tsqr_fold_gram_workspace_size": (_c_sz, [_c_i64, _c_i64, _c_i64]),

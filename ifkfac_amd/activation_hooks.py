@@ -212,9 +212,10 @@ class RawActivationHooks(GramMatrixEstimator):
         r_new = fold_chunk(buf, r_in, chunk, self.math)
         Rd[module] = buf[:r_new]
 
-    def _finalize(self, R_raw: torch.Tensor, rows: int, out_dtype: torch.dtype):
+    def _finalize(self, R_raw: torch.Tensor, rows: int, out_dtype: torch.dtype,
+                  math_: Optional[int] = None):
         return get_backend().finalize(R_raw, 1.0 / math.sqrt(rows), self.damping, out_dtype,
-                                      self.math)
+                                      self.math if math_ is None else math_)
 
     def _take(self, side: str, module: nn.Module, chunk: torch.Tensor) -> None:
         """Fold ``chunk``, or hold it back when the next reader is a fused finalize."""
@@ -257,7 +258,7 @@ class RawActivationHooks(GramMatrixEstimator):
         return R, r, chunk, min(r + chunk.shape[0], n)
 
     def _damped(self, side: str, module: nn.Module, rows: int, out_dtype: torch.dtype,
-                fast: bool = False, with_inverse: bool = False):
+                fast: bool = False, with_inverse: bool = False, math_: Optional[int] = None):
         """(R_damped, flag, kappa bound or None) of one side; a held chunk goes
         into a fused fold + finalize.  With ``fast`` that factorisation is the
         Gram matrix + blocked Cholesky in bf16 arithmetic (which also bounds
@@ -265,10 +266,12 @@ class RawActivationHooks(GramMatrixEstimator):
         factor), CholeskyQR2 outer blocks in fp32 arithmetic; its flag may
         then be 2 (see _retry_cholesky_qr).  With ``with_inverse`` the Gram
         route also forms the factor's inverse and its bf16 copies in the same
-        call (a fourth value (Z, Zb, ZT), else None)."""
+        call (a fourth value (Z, Zb, ZT), else None).  ``math_`` overrides the
+        hooks' arithmetic for this factorisation."""
         R, r, chunk, _ = self._side_state(side, module)
         be = get_backend()
-        gram = fast and self.math == MATH_BF16
+        am = self.math if math_ is None else math_
+        gram = fast and am == MATH_BF16
         if gram and with_inverse:
             bufs = self._buf_X if side == "X" else self._buf_G
             Rs, X, r_in = ([bufs.get(module)], chunk, r) if chunk is not None else (None, R, 0)
@@ -280,12 +283,12 @@ class RawActivationHooks(GramMatrixEstimator):
             if gram:
                 # the running factor itself is the Gram route's input (p = n rows)
                 return be.fold_finalize(None, 0, R, 1.0 / math.sqrt(rows), self.damping,
-                                        out_dtype, self.math, gram=True,
+                                        out_dtype, am, gram=True,
                                         with_kappa=True) + (None,)
-            return self._finalize(R, rows, out_dtype) + (None, None)
+            return self._finalize(R, rows, out_dtype, am) + (None, None)
         bufs = self._buf_X if side == "X" else self._buf_G
         res = be.fold_finalize(bufs.get(module) if r > 0 else None, r, chunk,
-                               1.0 / math.sqrt(rows), self.damping, out_dtype, self.math,
+                               1.0 / math.sqrt(rows), self.damping, out_dtype, am,
                                cqr=fast and not gram, gram=gram, with_kappa=gram)
         return res + (None,) if gram else res + (None, None)
 
@@ -294,7 +297,13 @@ class RawActivationHooks(GramMatrixEstimator):
         get_factors in bf16 arithmetic): a side too
         ill-conditioned for its Gram / CholeskyQR2 factorisation (flag 2) is
         recomputed by the panel factorisation, which handles any input (and
-        ``then`` run on the new factor)."""
+        ``then`` run on the new factor).  That refactorisation runs in fp32
+        arithmetic whatever the hooks' arithmetic: flag 2 means kappa is large,
+        where the bf16 panel factor's normwise error (about 2e-3), amplified
+        by kappa^2 in the solves, would leave the reference's bf16-mode result
+        (an fp32 Householder factor cast to bf16, triangular.py:284,299-301,
+        411-416 with ifkfac.py:292-294) far behind: measured 1.6e-1 against
+        its 1.3e-2 at kappa(R) = 950."""
         mods = list(flags)
         st = torch.cat([torch.cat(flags[m]) for m in mods]).cpu()
         for i, m in enumerate(mods):
@@ -304,7 +313,7 @@ class RawActivationHooks(GramMatrixEstimator):
                 rows = self._n_rows_X[m] if side == "X" else self._n_rows_G[m]
                 logger.debug("get_factors() [%s]: %s factor by the panel path",
                              _module_tag(m), side)
-                R, f, kb, _ = self._damped(side, m, rows, out_dtype, fast=False)
+                R, f, kb, _ = self._damped(side, m, rows, out_dtype, fast=False, math_=MATH_F32)
                 fac, fl = list(factors[m]), list(flags[m])
                 fac[j], fl[j] = R, f
                 factors[m], flags[m] = tuple(fac), tuple(fl)

@@ -44,7 +44,7 @@ using namespace ifk;
 
 extern "C" {
 
-int ifk_abi_version(void) { return 1; }
+int ifk_abi_version(void) { return 2; }
 
 const char* ifk_last_error(void) { return get_error(); }
 
@@ -162,13 +162,13 @@ int ifk_fold_finalize_gram_batched(void* stream, int64_t batch, const void* cons
                                    int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
                                    int64_t ldr, int64_t r_in, float scale, float damping,
                                    void* out, int out_dtype, int64_t ldo, int64_t out_stride,
-                                   int math, int32_t* status, float* kappa_bound, void* workspace,
-                                   size_t workspace_bytes) {
+                                   int math, float pivot_tol, int32_t* status, float* kappa_bound,
+                                   void* workspace, size_t workspace_bytes) {
   GUARD(dt_ok(x_dtype) && dt_ok(out_dtype) && math_ok(math),
         "fold_finalize_gram_batched: bad dtype or math code");
   return fold_finalize_gram((hipStream_t)stream, batch, X, x_dtype, p, n, ldx, R_in, ldr, r_in,
                             scale, damping, out, out_dtype, ldo, out_stride, math, status,
-                            kappa_bound, workspace, workspace_bytes);
+                            kappa_bound, workspace, workspace_bytes, pivot_tol);
 }
 
 size_t ifk_fold_finalize_gram_inverse_workspace_size(int64_t batch, int64_t p, int64_t n,
@@ -181,14 +181,14 @@ int ifk_fold_finalize_gram_inverse(void* stream, int64_t batch, const void* cons
                                    int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
                                    int64_t ldr, int64_t r_in, float scale, float damping,
                                    void* out, int out_dtype, int64_t ldo, int64_t out_stride,
-                                   int32_t* status, float* kappa_bound, float* Z, int64_t ldz,
-                                   int64_t z_stride, void* Zb, void* ZTb, int64_t ldb,
+                                   float pivot_tol, int32_t* status, float* kappa_bound, float* Z,
+                                   int64_t ldz, int64_t z_stride, void* Zb, void* ZTb, int64_t ldb,
                                    int64_t b_stride, void* workspace, size_t workspace_bytes) {
   GUARD(dt_ok(x_dtype) && dt_ok(out_dtype), "fold_finalize_gram_inverse: bad dtype");
   GramInverse inv{Z, ldz, z_stride, (bf16_t*)Zb, (bf16_t*)ZTb, ldb, b_stride};
   return fold_finalize_gram((hipStream_t)stream, batch, X, x_dtype, p, n, ldx, R_in, ldr, r_in,
                             scale, damping, out, out_dtype, ldo, out_stride, MATH_BF16, status,
-                            kappa_bound, workspace, workspace_bytes, 1e-3f, &inv);
+                            kappa_bound, workspace, workspace_bytes, pivot_tol, &inv);
 }
 
 int ifk_release_stream_state(void* stream) {

@@ -42,10 +42,11 @@
 // and most of the updates (n^3 in all, split) are done beside the chain.
 // Step c itself applies only the update by panel c - 1.
 //
-// Pivot test: a pivot below the tolerance (GRAM_TOL for the factor update,
-// the caller's for the streaming fold) times the Gram diagonal of its column
+// Pivot test: a pivot below the tolerance pivot_tol (GRAM_PIVOT_TOL, 1e-3, by
+// default for the factor update; the streaming fold's caller passes its own)
+// times the Gram diagonal of its column
 // (A's diagonal before any update) means that column is nearly a combination
-// of the ones before it (cancellation of more than 1 - GRAM_TOL in the Schur
+// of the ones before it (cancellation of more than 1 - pivot_tol in the Schur
 // complement): the rounding of the Gram matrix and of the updates, about
 // 2^-17 of that diagonal, would then be a visible part of the pivot.  The
 // call then reports status 2, and the caller recomputes the factor by the
@@ -72,7 +73,6 @@ namespace ifk {
 namespace {
 
 constexpr int64_t GB = 1024;          // Cholesky block (cholb supports up to 1024)
-constexpr float GRAM_TOL = 1e-3f;     // relative pivot threshold (see above)
 
 // ---------------------------------------------------------------------------
 // Kernels.  Every one takes a batch of same-shaped problems: entry b of a

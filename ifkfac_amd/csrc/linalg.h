@@ -41,7 +41,7 @@ int fold_finalize_cqr(hipStream_t s, const void* X, int xdt, int64_t p, int64_t 
 
 // The same factor as fold_finalize from the Gram matrix of [R_in; X] and a
 // blocked Cholesky (gramchol.hip; bf16 arithmetic only).  *status as for
-// fold_finalize_cqr (2: a pivot below 1e-3 of its Gram diagonal).  With
+// fold_finalize_cqr (2: a pivot below pivot_tol of its Gram diagonal).  With
 // kappa_bound, an upper bound of kappa_2 of the factor from the Gram
 // matrix's Frobenius norm (device float).  batch factors of the same shape
 // at once: X and R_in are host arrays of batch device pointers, entry b's
@@ -58,6 +58,9 @@ struct GramInverse {
   bf16_t *Zb, *ZT;
   int64_t ldb, sb;
 };
+// The factor update's default relative pivot threshold of the Gram route
+// (the streaming fold's caller passes its own).
+constexpr float GRAM_PIVOT_TOL = 1e-3f;
 // With split_r, R_in enters the Gram matrix as R_in = hi + lo (both RNE
 // bf16; R_in^T R_in to about 2^-17 by three products, K = 3 r_in) instead of
 // its bf16 rounding: the streaming fold's running factor is fp32 state, and a
@@ -69,7 +72,7 @@ int fold_finalize_gram(hipStream_t s, int64_t batch, const void* const* X, int x
                        int64_t n, int64_t ldx, const float* const* R_in, int64_t ldr,
                        int64_t r_in, float scale, float damping, void* out, int odt, int64_t ldo,
                        int64_t out_stride, int math, int* status, float* kappa_bound, void* ws,
-                       size_t ws_bytes, float pivot_tol = 1e-3f,
+                       size_t ws_bytes, float pivot_tol = GRAM_PIVOT_TOL,
                        const GramInverse* inv = nullptr, bool split_r = false);
 
 // The streaming fold by the Gram route (bf16 arithmetic): R (rows [0, r_in)

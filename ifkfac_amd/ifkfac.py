@@ -49,6 +49,11 @@ logger = logging.getLogger(__name__)
 # measured 5e-3 against fp64 solves of the same factors at kappa 1, 1.4e-2 to
 # 3e-2 at kappa 3.1-3.2, while the fp32 arithmetic stays near 6e-6.
 KAPPA_BF16_MAX = 1.5
+# ifk_cond_estimate is a power-iteration lower bound of kappa_2 (up to about
+# 10 % low); it is raised by this factor before the comparison, so that the
+# gate errs towards fp32 arithmetic (the Gram route's bound is an upper bound
+# and is taken as is).
+COND_ESTIMATE_MARGIN = 1.1
 
 
 class IFKFAC(torch.optim.Optimizer):
@@ -165,7 +170,8 @@ class IFKFAC(torch.optim.Optimizer):
                 # choice of arithmetic needs kappa_2(R): the Gram path's upper
                 # bound when the factor came from it, else an estimate
                 Z, Zb, ZT = be.tri_inverse_bf16(R)
-                k = kappa_bound if kappa_bound is not None else be.cond_estimate(R, Z)
+                k = (kappa_bound if kappa_bound is not None
+                     else COND_ESTIMATE_MARGIN * be.cond_estimate(R, Z))
                 return Z, Zb, ZT, k
             return be.tri_inverse(R, m)
 

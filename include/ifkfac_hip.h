@@ -213,7 +213,9 @@ int ifk_tsqr_fold_gram_batched(void* stream, int64_t batch, const void* const* X
  * arrays of `batch` device pointers (R_in may be NULL when r_in == 0); entry
  * b's factor is written at out + b * out_stride elements (out_stride >= n *
  * ldo), its status to status[b] and its kappa bound to kappa_bound[b] (may be
- * NULL).  Every entry's result is the one ifk_fold_finalize_gram gives it.
+ * NULL).  pivot_tol in (0, 1) is the relative pivot threshold of the
+ * status (ifk_fold_finalize_gram uses 1e-3).  Every entry's result is the one
+ * ifk_fold_finalize_gram gives it at that threshold.
  */
 size_t ifk_fold_finalize_gram_batched_workspace_size(int64_t batch, int64_t p, int64_t n,
                                                      int64_t r_in);
@@ -221,8 +223,8 @@ int ifk_fold_finalize_gram_batched(void* stream, int64_t batch, const void* cons
                                    int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
                                    int64_t ldr, int64_t r_in, float scale, float damping,
                                    void* out, int out_dtype, int64_t ldo, int64_t out_stride,
-                                   int math, int32_t* status, float* kappa_bound, void* workspace,
-                                   size_t workspace_bytes);
+                                   int math, float pivot_tol, int32_t* status, float* kappa_bound,
+                                   void* workspace, size_t workspace_bytes);
 
 /*
  * ifk_fold_finalize_gram_batched together with the triangular inverse of each
@@ -248,8 +250,8 @@ int ifk_fold_finalize_gram_inverse(void* stream, int64_t batch, const void* cons
                                    int64_t p, int64_t n, int64_t ldx, const float* const* R_in,
                                    int64_t ldr, int64_t r_in, float scale, float damping,
                                    void* out, int out_dtype, int64_t ldo, int64_t out_stride,
-                                   int32_t* status, float* kappa_bound, float* Z, int64_t ldz,
-                                   int64_t z_stride, void* Zb, void* ZTb, int64_t ldb,
+                                   float pivot_tol, int32_t* status, float* kappa_bound, float* Z,
+                                   int64_t ldz, int64_t z_stride, void* Zb, void* ZTb, int64_t ldb,
                                    int64_t b_stride, void* workspace, size_t workspace_bytes);
 
 /*

@@ -152,12 +152,6 @@ def apply_vered(grad_W: np.ndarray, R_X: np.ndarray, R_G: np.ndarray) -> np.ndar
     return T4_T.T
 
 
-def apply_vered_bf16(grad_W: np.ndarray, R_X_bf16: np.ndarray, R_G_bf16: np.ndarray) -> np.ndarray:
-    """triangular.py:607-628: bf16-valued factors upcast, fp32 solves."""
-    return apply_vered(grad_W.astype(np.float32), R_X_bf16.astype(np.float32),
-                       R_G_bf16.astype(np.float32)).astype(np.float32)
-
-
 def apply_vered_bias(grad_b: np.ndarray, R_G: np.ndarray) -> np.ndarray:
     """triangular.py:699-702: G^-1 g_b by two solves."""
     t = sla.solve_triangular(R_G.T, grad_b, lower=True)

@@ -46,7 +46,8 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_version_and_sizes(lib):
-    assert lib.ifk_abi_version() == 1
+    from ifkfac_amd import _lib
+    assert lib.ifk_abi_version() == _lib.ABI_VERSION == 2
     assert lib.ifk_tsqr_fold_workspace_size(512, 1024) > 512 * 1024 * 4
     assert lib.ifk_finalize_workspace_size(1024) > 1024 * 1024 * 4
     assert lib.ifk_tri_inverse_workspace_size(11008) > 0

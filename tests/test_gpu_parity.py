@@ -480,9 +480,10 @@ def test_fold_finalize_cqr_is_deterministic(hip):
 
 @pytest.mark.parametrize("n_in,n_out,p", [(4096, 11008, 16384)])
 def test_full_size_fold_finalize_bf16(hip, n_in, n_out, p):
-    """The benchmarked factor update at full size in bf16 arithmetic: for random
-    probes v, ||R_d v||^2 = ||X v||^2 / p + lam ||v||^2, and the natural gradient of
-    the fused factors matches that of the two-call factors to the bf16 bound."""
+    """The benchmarked factor update at full size in bf16 arithmetic, by the
+    panel path and by CholeskyQR2 blocks: for 16 random probes v,
+    ||R_d v||^2 = ||X v||^2 / p + lam ||v||^2 within 2e-3, and R_d upper
+    triangular with a positive diagonal."""
     g = torch.Generator(device=DEV).manual_seed(7)
     for n, cqr in ((n_in, False), (n_out, False), (n_in, True), (n_out, True)):
         X = torch.randn(p, n, device=DEV, generator=g).to(torch.bfloat16)
@@ -535,21 +536,33 @@ def test_precondition_bf16(hip, n_out, n_in):
 
 
 def test_precondition_kappa_exposed(hip):
-    """kappa(R_damped) ~ kappa(X): X scaled by sqrt(p), lambda below sigma_min^2 / 10."""
+    """kappa(R_damped) ~ kappa(X) ~ 95: X scaled by sqrt(p), lambda below
+    sigma_min^2 / 10.  The kernel gets the factors in fp32, and their rounding
+    alone moves the four solves' result by up to kappa^2 eps32 (1e-3 here), for
+    the reference as for this path; so the comparison is with fp64 solves on the
+    same fp32 factors.  There the reference's own fp32 solves (four trsm,
+    triangular.py:630-651, by LAPACK's strtrs) have their forward error, about
+    kappa eps32 per solve; the HIP path (triangular inverses, then products)
+    is held to 1e-5, or to twice the reference's error where that is larger."""
     n, p = 256, 1024
     rng = np.random.default_rng(7)
     X = O.kappa_matrix(p, n, 1e2, rng) * math.sqrt(p)
     R_X = O.get_factor(O.streaming_tsqr_update(None, X), p, 1e-5)
-    R_G = R_X.copy()
     kap = _kappa(R_X)
     assert kap > 50
-    g = rng.normal(0, 0.1, (n, n))
-    want = O.apply_vered(g, R_X, R_G)
-    nat = hip.precondition(torch.tensor(g, dtype=torch.float32, device=DEV),
-                           torch.tensor(R_X, dtype=torch.float32, device=DEV),
-                           torch.tensor(R_G, dtype=torch.float32, device=DEV), 0)
-    # forward error of four solves scales with kappa(R)^4 eps in the worst case
-    assert _rel(nat, want) <= 4 * kap ** 2 * EPS32
+    Rx32 = R_X.astype(np.float32)
+    Rg32 = Rx32.copy()
+    g32 = rng.normal(0, 0.1, (n, n)).astype(np.float32)
+    exact = O.apply_vered(g32.astype(np.float64), Rx32.astype(np.float64),
+                          Rg32.astype(np.float64))
+    ref32 = O.apply_vered(g32, Rx32, Rg32)
+    assert ref32.dtype == np.float32
+    nat = hip.precondition(torch.tensor(g32, device=DEV), torch.tensor(Rx32, device=DEV),
+                           torch.tensor(Rg32, device=DEV), 0)
+    e, e_ref = _rel(nat, exact), _rel(ref32, exact)
+    print(f"kappa {kap:.1f}: fp32 HIP {e:.2e}, reference fp32 solves {e_ref:.2e} "
+          f"(against fp64 solves on the same fp32 factors)")
+    assert e <= max(1e-5, 2 * e_ref)
 
 
 def test_precondition_bias(hip):

@@ -2,7 +2,8 @@
 workspace entry point it varies (ifk_precondition_apply_bf16), called through
 the C ABI: two calls in a row, the second with a smaller input, each bit for
 bit equal to the workspace entry's result (the library's scratch array has
-room for the same split-K partials at these sizes), and the size limit
+room for the same split-K partials at these sizes); a warm call leaves the
+device's free memory unchanged (it allocates nothing); and the size limit
 rejected before any launch."""
 import ctypes
 
@@ -22,8 +23,12 @@ def _inverse_copies(hip, n, seed):
 
 
 def _noalloc(lib, g, ZX, ZG):
+    nat = torch.empty(g.shape[0], g.shape[1], device="cuda")
+    return _noalloc_into(lib, g, ZX, ZG, nat)
+
+
+def _noalloc_into(lib, g, ZX, ZG, nat):
     n_out, n_in = g.shape
-    nat = torch.empty(n_out, n_in, device="cuda")
     rc = lib.ifk_precondition_apply_bf16_noalloc(
         torch.cuda.current_stream().cuda_stream, g.data_ptr(), n_out, n_in, g.stride(0),
         ZX[0].data_ptr(), ZX[1].data_ptr(), ZX[0].stride(0), ZG[0].data_ptr(), ZG[1].data_ptr(),
@@ -48,14 +53,25 @@ def test_noalloc_apply_matches_workspace_entry(hip):
         out.append(nat)
     # the first result is unchanged by the second call (outputs are the caller's)
     assert out[0].shape == (1100, 700) and bool(torch.isfinite(out[0]).all())
+    # a warm call allocates no device memory: the free memory the driver
+    # reports (torch's cache aside, which this call does not touch) is the same
+    # before and after
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    rc, _ = _noalloc_into(lib, g, ZX, ZG, nat)
+    torch.cuda.synchronize()
+    assert rc == 0, lib.ifk_last_error()
+    assert torch.cuda.mem_get_info()[0] == free0
 
 
 def test_noalloc_apply_rejects_sizes_beyond_the_scratch(hip):
     from ifkfac_amd import _lib
     lib = _lib.load()
-    # 4096 x 4096 needs three 32 MiB bf16 buffers: more than the 64 MiB array
+    # 4096 x 4096 needs three 32 MiB bf16 buffers: more than the 64 MiB array.
+    # Null pointers: the size check answers first, and the argument check
+    # behind it would reject them too
     rc = lib.ifk_precondition_apply_bf16_noalloc(
-        torch.cuda.current_stream().cuda_stream, 1, 4096, 4096, 4096, 1, 1, 4096, 1, 1, 4096, 1,
-        4096)
+        torch.cuda.current_stream().cuda_stream, None, 4096, 4096, 4096, None, None, 4096, None,
+        None, 4096, None, 4096)
     assert rc == -1
     assert b"too large" in lib.ifk_last_error()
