@@ -18,9 +18,12 @@ HBM.  value = algorithmic TFLOP/s of the step, with the algorithmic count
 
 roofline: the dominant kernel of the workload -- the family with the largest
 summed launch time in a survey step with every GEMM launch and every
-block-Cholesky step bracketed by HIP events on its own stream -- timed over
-the timed steps: algorithmic work per launch over its average launch time,
-against the bf16 MFMA, fp32 MFMA or HBM peak as its intensity says.
+block-Cholesky step bracketed by HIP events on its own stream -- timed by
+such event pairs over as many steps again, run right after the timed steps
+(which run with no events armed: an event pair per launch costs host time,
+which a launch-bound chain would add to the step): algorithmic work per
+launch over its average launch time, against the bf16 MFMA, fp32 MFMA or
+HBM peak as its intensity says.
 
 Extra keys on the same JSON line (unless --no-extras): the other benchmark
 layers (Linear 1024 -> 1024 streamed over 8 chunks, 4096 -> 4096 at p = 8192,
@@ -231,16 +234,19 @@ class LayerChain:
     def _side(self, T, R, how, math_=None):
         import torch
         from ifkfac_amd._backend import MATH_BF16
-        from ifkfac_amd.activation_hooks import fold_chunk
+        from ifkfac_amd.activation_hooks import FoldStatusQueue, fold_chunk
         be, p = self.be, self.p
         am = self.math if math_ is None else math_
         r = 0
         last = T
         if self.chunks > 1:
-            # the hooks fold every chunk but the held one into the running factor
+            # the hooks fold every chunk but the held one into the running
+            # factor without reading a status; the factor update reads them
             q = p // self.chunks
+            fq = FoldStatusQueue()
             for c in range(self.chunks - 1):
-                r = fold_chunk(R, r, T[c * q:(c + 1) * q], am)
+                r = fold_chunk(R, r, T[c * q:(c + 1) * q], am, fq)
+            fq.drain()
             last = T[(self.chunks - 1) * q:]
         out_dtype = torch.bfloat16
         # as IFKFAC's factor update: the Gram path in bf16 arithmetic (the
@@ -406,7 +412,10 @@ def roofline(fam: int, recs: list, steps: int, ms_per_step: float, traffic_key=N
 def measure(lib, step, steps: int, warmup: int, traffic_key=None, marks=None):
     """warmup steps; one survey step with every family armed (the dominant
     family: the largest summed launch time per step, as a kernel-trace summary
-    ranks kernels); then the timed steps with that family armed.  Returns
+    ranks kernels); then the timed steps, with nothing armed; then the same
+    number of steps again with the dominant family armed, whose launches give
+    the roofline (an event pair per launch costs host time, which a
+    launch-bound chain would otherwise add to the timed steps).  Returns
     (ms_per_step, roofline of the dominant family, survey table, phases)."""
     import torch
     for i in range(warmup):
@@ -432,8 +441,9 @@ def measure(lib, step, steps: int, warmup: int, traffic_key=None, marks=None):
             step(False)
         torch.cuda.synchronize()
         timing["ms"] = (time.perf_counter() - t0) * 1e3 / steps
-    recs = profiled(lib, ARM[fam], run)
+    run()
     ms = timing["ms"]
+    recs = profiled(lib, ARM[fam], run)
     table = {FAMILIES[f][0]: {"ms_per_step": round(a[0], 3), "launches": round(a[1], 1),
                               "tflops": round(a[2] / (a[0] * 1e-3) / 1e12, 2) if a[0] else None}
              for f, a in sorted(survey.items(), key=lambda kv: -kv[1][0])}
@@ -444,7 +454,8 @@ class VitCapture:
     """One ViT-B block's factor capture per step: the folds of one 4096-row batch
     into the running factors of both sides of qkv 768->2304, proj 768->768,
     fc1 768->3072 and fc2 3072->768 (bf16 arithmetic, the Gram route with the
-    panel fold for a refused fold), as the hooks issue them."""
+    panel fold for a refused fold, the statuses read without blocking), as the
+    hooks issue them."""
 
     shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
     rows = 4096
@@ -452,8 +463,10 @@ class VitCapture:
     def __init__(self, be, seed=13):
         import torch
         from ifkfac_amd._backend import MATH_BF16
+        from ifkfac_amd.activation_hooks import FoldStatusQueue
         g = torch.Generator(device="cuda").manual_seed(seed)
         self.be = be
+        self.queue = FoldStatusQueue()
         self.Rs, self.chunks = [], []
         for (a, b) in self.shapes:
             for nn_ in (a, b):
@@ -468,8 +481,9 @@ class VitCapture:
         from ifkfac_amd._backend import MATH_BF16
         from ifkfac_amd.activation_hooks import fold_chunk
         mark()
+        self.queue.poll()
         for R, T in zip(self.Rs, self.chunks):
-            fold_chunk(R, R.shape[0], T, MATH_BF16)
+            fold_chunk(R, R.shape[0], T, MATH_BF16, self.queue)
         mark()
 
 

@@ -183,6 +183,18 @@ class HipBackend:
         _lib.check(rc, name)
         return (out, flag, kb) if kb is not None else (out, flag)
 
+    def status_to_host(self, st: torch.Tensor, host: torch.Tensor) -> None:
+        """host[:n] <- st[:n] (int32; host pinned) by a kernel on the current
+        stream (ifk_status_to_host); read it after an event recorded behind."""
+        _require_device(st, "status_to_host")
+        if (st.dtype != torch.int32 or host.dtype != torch.int32 or not host.is_pinned()
+                or host.numel() < st.numel() or not st.is_contiguous()):
+            raise IFKFACBackendError("status_to_host: int32 device status, pinned int32 host")
+        with torch.cuda.device(st.device):
+            rc = self.lib.ifk_status_to_host(self._stream(st.device), _ptr(st), host.data_ptr(),
+                                             st.numel())
+        _lib.check(rc, "ifk_status_to_host")
+
     def fold_gram_batched_(self, Rs, r_in: int, Xs, pivot_tol: float) -> torch.Tensor:
         """fold_gram_ for B running factors of one shape, each folding its own
         chunk, in one chain of launches (ifk_tsqr_fold_gram_batched).  Rs:

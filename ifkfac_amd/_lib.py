@@ -39,6 +39,7 @@ _c_i64p = ctypes.POINTER(ctypes.c_int64)
 # name -> (restype, argtypes); mirrors include/ifkfac_hip.h exactly.
 SIGNATURES = {
     "ifk_abi_version": (_c_int, []),
+    "ifk_status_to_host": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64]),
     "ifk_last_error": (ctypes.c_char_p, []),
     "ifk_release_stream_state": (_c_int, [_c_vp]),
     "ifk_tsqr_fold_workspace_size": (_c_sz, [_c_i64, _c_i64]),

@@ -11,6 +11,7 @@ running factors are.
 """
 from __future__ import annotations
 
+import collections
 import logging
 import math
 import warnings
@@ -34,21 +35,139 @@ warnings.filterwarnings("ignore", message="Full backward hook is firing", catego
 # keeps, and its factor's backward error (R^T R against the Gram matrix of
 # the bf16-rounded rows) stays far below the bf16 panel fold's.
 GRAM_FOLD_TOL = 1e-4
+# A fold the Gram route refuses (its pivot test found the rows ill-conditioned
+# or rank-deficient) is redone by the panel fold in fp32 arithmetic: on such
+# rows the bf16 panel fold drifts along a stream (the output-gradient side of
+# a ViT-B qkv projection, columns 768.. zero: 6.3e-2 relative Gram error after
+# 120 folds of 4096 rows, against 7e-5 in fp32 arithmetic), while the
+# reference keeps its running factor in fp32 (triangular.py:246-307).
+REFUSED_FOLD_MATH = MATH_F32
 
 
-def fold_chunk(buf: torch.Tensor, r_in: int, chunk: torch.Tensor, math_: int) -> int:
+class FoldStatusQueue:
+    """Gram-route folds whose status is read without blocking the host.
+
+    A fold by the Gram route either writes the factor of [R; X] (status 1) or
+    leaves R as it was (status 2: a pivot below GRAM_FOLD_TOL of its Gram
+    diagonal).  Instead of reading the status at once -- a blocking device
+    read inside a forward or backward hook, which the reference's hooks never
+    make (activation_hooks.py:579-580, 642-643) -- ``push`` copies it to
+    pinned host memory behind the fold on the same stream, records an event,
+    and keeps a copy of the chunk (the caller's tensor may be changed in
+    place once the hook returns -- autograd reuses gradient buffers -- while a
+    refused chunk is read again later).  ``poll`` resolves, without blocking,
+    the folds whose
+    event has completed: a refused chunk is then folded by the panel path
+    into the running factor as it is at that point (R^T R is the sum of the
+    folded chunks' Gram matrices, so the order of the folds does not change
+    the factor).  ``drain`` resolves the rest, blocking; readers of the
+    factors call it first.  At most ``cap`` folds wait (the kept chunks hold
+    memory); beyond that the oldest is resolved blocking.  The pinned status
+    words and their events come from one process-wide pool (a pinned
+    allocation costs far more than a fold's launches)."""
+
+    # (pinned int32[1], event) pairs per device, shared by all queues
+    _pool: Dict[int, List[tuple]] = {}
+
+    def __init__(self, cap: int = 32):
+        self.cap = cap
+        self._q: collections.deque = collections.deque()
+        self.refused = 0               # refused folds resolved so far
+
+    def __len__(self) -> int:
+        return len(self._q)
+
+    def push(self, st: torch.Tensor, buf: torch.Tensor, chunk: torch.Tensor,
+             math_: int) -> None:
+        if st.device.type != "cuda":
+            # a host backend: the status is on the host already
+            self._resolve(int(st.reshape(-1)[0].item()), buf, chunk, math_)
+            return
+        if len(self._q) >= self.cap:
+            self._pop(block=True)
+        free = FoldStatusQueue._pool.setdefault(st.device.index, [])
+        if not free:
+            with torch.cuda.device(st.device):
+                block = torch.empty(64, dtype=torch.int32, pin_memory=True)
+                free.extend((block[i:i + 1], torch.cuda.Event()) for i in range(64))
+        slot, ev = free.pop()
+        chunk = chunk.clone()   # on the stream, behind the fold that read it
+        be = get_backend()
+        if hasattr(be, "status_to_host"):
+            # a kernel store: a copy-engine transfer between two folds' kernels
+            # would stall the stream for far longer than the folds take
+            be.status_to_host(st.reshape(-1)[:1], slot)
+        else:
+            slot.copy_(st.reshape(-1)[:1], non_blocking=True)
+        ev.record()
+        self._q.append((slot, ev, st.device.index, buf, chunk, math_))
+
+    def poll(self) -> None:
+        while self._q and self._q[0][1].query():
+            self._pop(block=False)
+
+    def drain(self) -> None:
+        while self._q:
+            self._pop(block=True)
+
+    def discard(self) -> None:
+        """Forget the waiting folds (their factors are being dropped)."""
+        while self._q:
+            slot, ev, dev, _, _, _ = self._q.popleft()
+            ev.synchronize()     # the slot is reused only once its copy is done
+            FoldStatusQueue._pool[dev].append((slot, ev))
+
+    def _pop(self, block: bool) -> None:
+        slot, ev, dev, buf, chunk, math_ = self._q.popleft()
+        if block:
+            ev.synchronize()
+        st = int(slot[0])
+        FoldStatusQueue._pool[dev].append((slot, ev))
+        self._resolve(st, buf, chunk, math_)
+
+    def _resolve(self, st: int, buf: torch.Tensor, chunk: torch.Tensor, math_: int) -> None:
+        if st == 1:
+            return
+        self.refused += 1
+        n = buf.shape[1]
+        logger.debug("fold of %d rows into a %d-column factor: Gram route refused, panel fold",
+                     chunk.shape[0], n)
+        get_backend().fold_(buf, n, chunk, REFUSED_FOLD_MATH)
+
+
+def fold_chunk(buf: torch.Tensor, r_in: int, chunk: torch.Tensor, math_: int,
+               queue: Optional[FoldStatusQueue] = None) -> int:
     """Fold ``chunk`` into ``buf`` (n x n fp32, rows [0, r_in) valid); returns
     the new row count.  In bf16 arithmetic a fold whose result is square goes by
     the Gram matrix and the blocked Cholesky (about 3x faster than the panel
-    fold); the status read waits for that fold only, and a fold the Gram route
-    refuses left buf as it was for the panel fold."""
+    fold), and a fold the Gram route refuses leaves buf as it was for the
+    panel fold (in fp32 arithmetic: REFUSED_FOLD_MATH).  Without ``queue`` the
+    status is read at once (the host waits for that fold).  With it the
+    status is read later (FoldStatusQueue), so
+    the next folds run before a refusal is known: the Gram route is then
+    taken where the folded rows stay well spread whatever happens -- into a
+    square running factor (r_in = n), or with at least 2n rows in all -- and
+    rows [r_in, n) are zeroed first, so that a refused fold leaves an n-row
+    factor whose extra rows contribute nothing.  A nearly square first fold
+    (n <= r_in + p < 2n: its Gram matrix is often too ill-conditioned, and a
+    refusal would leave the following folds a rank-deficient factor, which
+    they would refuse in turn) takes the panel fold directly."""
     be = get_backend()
     n = buf.shape[1]
-    if math_ == MATH_BF16 and r_in + chunk.shape[0] >= n:
+    p = chunk.shape[0]
+    if math_ == MATH_BF16 and r_in + p >= n:
+        if queue is not None:
+            if r_in < n and r_in + p < 2 * n:
+                return be.fold_(buf, r_in, chunk, math_)
+            if r_in < n:
+                buf[r_in:].zero_()
+            queue.push(be.fold_gram_(buf, r_in, chunk, GRAM_FOLD_TOL), buf, chunk, math_)
+            return n
         if int(be.fold_gram_(buf, r_in, chunk, GRAM_FOLD_TOL).item()) == 1:
             return n
         logger.debug("fold of %d rows into a %d-column factor: Gram route refused, panel fold",
                      chunk.shape[0], n)
+        return be.fold_(buf, r_in, chunk, REFUSED_FOLD_MATH)
     return be.fold_(buf, r_in, chunk, math_)
 
 
@@ -122,6 +241,8 @@ class RawActivationHooks(GramMatrixEstimator):
         self._defer_last = False
         self._held_X: Dict[nn.Module, Optional[torch.Tensor]] = {}
         self._held_G: Dict[nn.Module, Optional[torch.Tensor]] = {}
+        # Gram-route folds (bf16 arithmetic) whose status the host has not read
+        self._fold_queue = FoldStatusQueue()
         self._linear_layers: List[nn.Module] = []
 
         for module in model.modules():
@@ -162,6 +283,7 @@ class RawActivationHooks(GramMatrixEstimator):
         self._enabled = True
 
     def clear(self):
+        self._fold_queue.discard()
         for module in self._linear_layers:
             self._R_X[module] = None
             self._R_G[module] = None
@@ -209,7 +331,8 @@ class RawActivationHooks(GramMatrixEstimator):
             r_in = cur.shape[0]
             if cur.data_ptr() != buf.data_ptr():
                 buf[:r_in].copy_(cur)
-        r_new = fold_chunk(buf, r_in, chunk, self.math)
+        self._fold_queue.poll()
+        r_new = fold_chunk(buf, r_in, chunk, self.math, self._fold_queue)
         Rd[module] = buf[:r_new]
 
     def _finalize(self, R_raw: torch.Tensor, rows: int, out_dtype: torch.dtype,
@@ -245,6 +368,7 @@ class RawActivationHooks(GramMatrixEstimator):
         if chunk is not None:
             self._fold(side, module, chunk)
             held[module] = None
+        self._fold_queue.drain()
         return (self._R_X if side == "X" else self._R_G).get(module)
 
     def _side_state(self, side: str, module: nn.Module):
@@ -399,6 +523,9 @@ class RawActivationHooks(GramMatrixEstimator):
             self._drain_deferred()
         if not consume:
             self._fold_held()
+        # the Gram-route folds whose status is still on its way: a refused
+        # chunk goes into its running factor by the panel path now
+        self._fold_queue.drain()
         # bf16 arithmetic factors every side by the Gram route (flag 2 -> panel
         # path after one host read of the flags); fp32 arithmetic takes
         # CholeskyQR2 blocks for a consumed held chunk only
@@ -530,7 +657,8 @@ class RawActivationHooks(GramMatrixEstimator):
     def _fold_group(self, side: str, items, r_in: int) -> None:
         """_fold(full_rank_shape=True) of same-shape chunks into their layers'
         running factors by one batched Gram-route fold; a layer the Gram route
-        refuses (status 2, its buffer untouched) folds by the panel path."""
+        refuses (status 2, its buffer untouched) folds by the panel path once
+        its status has been read (FoldStatusQueue: no host read here)."""
         Rd = self._R_X if side == "X" else self._R_G
         bufs_d = self._buf_X if side == "X" else self._buf_G
         bufs = []
@@ -545,17 +673,14 @@ class RawActivationHooks(GramMatrixEstimator):
                 buf.zero_()
             elif cur.data_ptr() != buf.data_ptr():
                 buf[:r_in].copy_(cur)
+            if r_in < n:
+                buf[r_in:].zero_()
             bufs.append(buf)
-        st = get_backend().fold_gram_batched_(bufs, r_in, [X for _, X in items],
-                                              GRAM_FOLD_TOL).cpu()
+        self._fold_queue.poll()
+        st = get_backend().fold_gram_batched_(bufs, r_in, [X for _, X in items], GRAM_FOLD_TOL)
         for e, (module, X) in enumerate(items):
-            n = X.shape[1]
-            r_new = n
-            if int(st[e]) != 1:
-                logger.debug("flush fold of %d rows into a %d-column factor: Gram route "
-                             "refused, panel fold", X.shape[0], n)
-                r_new = get_backend().fold_(bufs[e], r_in, X, self.math)
-            Rd[module] = bufs[e][:r_new]
+            self._fold_queue.push(st[e:e + 1], bufs[e], X, self.math)
+            Rd[module] = bufs[e][:X.shape[1]]
 
     # ------------------------------------------------------------------ conv helpers
     @staticmethod

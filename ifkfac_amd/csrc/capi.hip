@@ -191,6 +191,20 @@ int ifk_fold_finalize_gram_inverse(void* stream, int64_t batch, const void* cons
                             kappa_bound, workspace, workspace_bytes, pivot_tol, &inv);
 }
 
+int ifk_status_to_host(void* stream, const int32_t* status, int32_t* host_status, int64_t n) {
+  if (n < 1 || n > (1 << 20) || !status || !host_status) {
+    set_error("status_to_host: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  void* dev = nullptr;
+  if (hipHostGetDevicePointer(&dev, host_status, 0) != hipSuccess || !dev) {
+    (void)hipGetLastError();
+    set_error("status_to_host: host_status is not pinned host memory (hipHostMalloc)");
+    return IFK_ERR_INVALID;
+  }
+  return launch_status_to_host((hipStream_t)stream, status, (int*)dev, (int)n);
+}
+
 int ifk_release_stream_state(void* stream) {
   return look_ahead_release((hipStream_t)stream);
 }

@@ -274,6 +274,20 @@ int launch_fill_int(hipStream_t s, int* p, int value, int count) {
   return check_launch("fill_int");
 }
 
+// dst[i] = src[i] for status words, dst in pinned host memory (its device
+// address): one store per word at system scope, so the value is in host
+// memory once the kernel has completed.
+__global__ void status_to_host_kernel(const int* __restrict__ src, int* dst, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x)
+    __hip_atomic_store(dst + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+int launch_status_to_host(hipStream_t s, const int* src, int* dst_dev, int n) {
+  if (n <= 0) return IFK_OK;
+  hipLaunchKernelGGL(status_to_host_kernel, dim3(1), dim3(64), 0, s, src, dst_dev, n);
+  return check_launch("status_to_host");
+}
+
 // buf <- (buf_init ? nat : momentum * buf + nat)   [ifkfac.py:404-406]
 // W   <- W * (1 - lr * wd) - lr * buf               [ifkfac.py:411-413]
 // momentum == 0 uses nat directly and leaves buf untouched (buf may be null).

@@ -153,6 +153,9 @@ int launch_cast(hipStream_t s, const float* src, int64_t lds, int64_t rows, int6
                 int odt, int64_t ldo);
 // *flag = 1 (a one-thread fill, safe to capture in a graph)
 int launch_fill_int(hipStream_t s, int* p, int value, int count);
+// n status words from device memory to pinned host memory, by a kernel
+// (dst_dev: the host buffer's device address)
+int launch_status_to_host(hipStream_t s, const int* src, int* dst_dev, int n);
 // heavy-ball momentum + decoupled weight decay + SGD step
 int launch_momentum_update(hipStream_t s, const float* nat, float* buf, float* W, int64_t numel,
                            float lr, float momentum, float weight_decay, int buf_init);

@@ -61,6 +61,18 @@ const char* ifk_last_error(void);
 int ifk_release_stream_state(void* stream);
 
 /*
+ * Copy n int32 status words (device memory) into pinned host memory
+ * (hipHostMalloc, or torch's pin_memory) by a kernel on the stream: the host
+ * reads them once an event recorded behind this call has completed, with no
+ * blocking read and no copy-engine transfer between the kernels around it.
+ * No counterpart in the reference (its hooks read no device status,
+ * activation_hooks.py:579-580, 642-643): it is for callers that decide a
+ * status-dependent fallback later, such as the hooks' streaming folds in bf16
+ * arithmetic.  n in [1, 2^20].
+ */
+int ifk_status_to_host(void* stream, const int32_t* status, int32_t* host_status, int64_t n);
+
+/*
  * Streaming TSQR fold -- replaces streaming_tsqr_update(running_R, new_chunk)
  * (ifkfac/triangular.py:246-307) as called from the hooks
  * (ifkfac/activation_hooks.py:579, :642).

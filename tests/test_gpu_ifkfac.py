@@ -180,8 +180,8 @@ def test_bf16_capture_takes_gram_route_on_gpu(hip, caplog):
     Gram route; an input side with a repeated column of large scale is refused by
     both (pivot tests) and taken by the panel fold and finalize.  Every factor is
     upper triangular with a positive diagonal and within 1e-2 (Gram relative
-    error: bf16 rounding of the data and of the running factor at each fold) of
-    the fp64 closed form chol(sum X^T X / rows + lambda I)."""
+    error: bf16 rounding of the data and the bf16 panel folds) of the fp64
+    closed form chol(sum X^T X / rows + lambda I)."""
     import logging
     from ifkfac_amd import IFKFAC
     from oracle import ifk_oracle as O
@@ -212,3 +212,41 @@ def test_bf16_capture_takes_gram_route_on_gpu(hip, caplog):
         e = np.linalg.norm(a.T @ a - b.T @ b) / np.linalg.norm(b.T @ b)
         print(f"{tuple(R.shape)}: gram rel {e:.3e}")
         assert e <= 1e-2
+
+
+def test_hooks_read_no_fold_status_on_gpu(hip):
+    """bf16 arithmetic: the hooks fold every chunk by the Gram route without
+    reading its status (it waits in the hooks' FoldStatusQueue: after the last
+    backward hook at least that fold's status is unread), and a chunk the Gram
+    route refused -- batches 1 and 3 repeat a column at 1e3 times the others'
+    scale, a pivot ratio near 0 -- goes into the running factor by the panel
+    fold once its status is read, after later chunks (the factor does not
+    depend on the order of the folds).  get_factors() reads the rest.  The
+    factor is within 5e-3 of the fp64 closed form of the bf16-rounded rows (the
+    bf16 panel fold's 2e-3 to 4e-3), and refused folds were resolved."""
+    from ifkfac_amd import RawActivationHooks
+    from ifkfac_amd._backend import MATH_BF16
+    from oracle import ifk_oracle as O
+    torch.manual_seed(9)
+    model = nn.Sequential(nn.Linear(192, 96), nn.Tanh(), nn.Linear(96, 32)).cuda()
+    hooks = RawActivationHooks(model, damping=1e-3, math=MATH_BF16)
+    hooks.enable()
+    rows = []
+    g = torch.Generator(device="cuda").manual_seed(10)
+    for b in range(6):
+        x = torch.randn(512, 192, device="cuda", generator=g)
+        if b in (1, 3):
+            x[:, 11] = 1e3 * torch.randn(512, device="cuda", generator=g)
+            x[:, 40] = x[:, 11]
+        rows.append(x.bfloat16().double().cpu().numpy())
+        model(x).square().mean().backward()
+    assert len(hooks._fold_queue) >= 1
+    factors = hooks.get_factors()
+    assert len(hooks._fold_queue) == 0
+    assert hooks._fold_queue.refused >= 2
+    R = factors[model[0]][0].double().cpu().numpy()
+    want = O.chol_factor(rows, 6 * 512, 1e-3)
+    e = np.linalg.norm(R.T @ R - want.T @ want) / np.linalg.norm(want.T @ want)
+    print(f"refused folds {hooks._fold_queue.refused}: gram rel {e:.3e}")
+    assert e <= 5e-3
+    hooks.remove()

@@ -778,10 +778,12 @@ def test_triangular_mirrors_match_oracle(be):
 
 
 def test_bf16_fold_takes_gram_route_when_square(be):
-    """bf16 arithmetic: a fold whose result is square goes to the Gram-route fold;
-    the first (partial-rank) chunk, a refused fold (status 2, injected or from a
-    repeated column) and fp32 arithmetic go to the panel fold.  Every path leaves
-    the oracle's running factor."""
+    """bf16 arithmetic: a fold into a square running factor goes to the
+    Gram-route fold; the first (partial-rank) chunk, a nearly square fold into
+    a partial-rank factor (r_in < n <= r_in + p < 2n: its status is read only
+    later, so it takes the panel fold directly), a refused fold (status 2,
+    injected or from a repeated column) and fp32 arithmetic go to the panel
+    fold.  Every path leaves the oracle's running factor."""
     from ifkfac_amd._backend import MATH_BF16, MATH_F32
     from ifkfac_amd.activation_hooks import GRAM_FOLD_TOL, RawActivationHooks
     model = nn.Sequential(nn.Linear(8, 4))
@@ -789,7 +791,7 @@ def test_bf16_fold_takes_gram_route_when_square(be):
     rng = np.random.default_rng(3)
     chunks = [rng.standard_normal((p, 8)) for p in (5, 6, 8, 8)]
     chunks[3][:, 7] = chunks[3][:, 0]            # a column repeated within the chunk
-    for math_, calls in ((MATH_BF16, (0, 1, 1, 1)), (MATH_F32, (0, 0, 0, 0))):
+    for math_, calls in ((MATH_BF16, (0, 0, 1, 1)), (MATH_F32, (0, 0, 0, 0))):
         be.calls.clear()
         hooks = RawActivationHooks(model, math=math_)
         old = None
