@@ -72,9 +72,19 @@ PEAK_F32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of a workload's dominant kernel, from two rocprofv3
 # --pmc runs (FETCH_SIZE, WRITE_SIZE) of that workload, scaled by the same
-# counters on a 256 MiB copy (profiles/pmc_traffic_*.txt), keyed by
-# (workload, factor path, kernel); None where no counter run was made.
-TRAFFIC = {}
+# counters on a 256 MiB copy (profiles/pmc_traffic_*.txt: fetch factor 2.0,
+# write factor 1.0), averaged over the kernel's dispatches in the run, keyed
+# by (workload, factor path, kernel); None where no counter run was made.
+# (The dominant kernel of a run is the one with the largest summed launch time
+# in its survey step; for these workloads that is either of two kernels.)
+TRAFFIC = {
+    ("linear_4096x11008_p16384", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"):
+        861.81e6,
+    ("linear_4096x11008_p16384", "gram", "cholb_step_kernel"): 5.12e6,
+    ("vit_b_block_capture_p4096", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"):
+        313.09e6,
+    ("vit_b_block_capture_p4096", "gram", "cholb_step_kernel"): 4.52e6,
+}
 
 WORKLOADS = {
     # name: (n_in, n_out, p, chunks) of a Linear layer's step, or ("vit",) for
