@@ -244,20 +244,26 @@ class LayerChain:
     def _side(self, T, R, how, math_=None):
         import torch
         from ifkfac_amd._backend import MATH_BF16
-        from ifkfac_amd.activation_hooks import FoldStatusQueue, fold_chunk
+        from ifkfac_amd.activation_hooks import FoldStatusQueue, RowAccumulator
         be, p = self.be, self.p
         am = self.math if math_ is None else math_
         r = 0
         last = T
         if self.chunks > 1:
-            # the hooks fold every chunk but the held one into the running
-            # factor without reading a status; the factor update reads them
+            # as the hooks: every chunk but the held one goes into the running
+            # factor (small ones held until a fold of them pays), no status
+            # read; the factor update takes the rows still held in front of
+            # the held chunk, after reading the statuses
             q = p // self.chunks
             fq = FoldStatusQueue()
+            acc = RowAccumulator()
             for c in range(self.chunks - 1):
-                r = fold_chunk(R, r, T[c * q:(c + 1) * q], am, fq)
+                r = acc.add(R, r, T[c * q:(c + 1) * q], am, fq)
             fq.drain()
             last = T[(self.chunks - 1) * q:]
+            rows = acc.take()
+            if rows is not None:
+                last = torch.cat([rows, last], dim=0)
         out_dtype = torch.bfloat16
         # as IFKFAC's factor update: the Gram path in bf16 arithmetic (the
         # factor's inverse formed in the same call), CholeskyQR2 blocks in fp32

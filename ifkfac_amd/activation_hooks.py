@@ -171,6 +171,51 @@ def fold_chunk(buf: torch.Tensor, r_in: int, chunk: torch.Tensor, math_: int,
     return be.fold_(buf, r_in, chunk, math_)
 
 
+class RowAccumulator:
+    """Small chunks of one running factor, held until one fold of them pays.
+
+    A fold's cost at a given width is mostly its chain of latency-bound
+    launches, whatever the rows; and a fold whose result is not a square
+    factor, or barely one, cannot take the Gram route.  In bf16 arithmetic a
+    chunk that would make such a fold -- fewer than 2n rows in all into a
+    partial factor, or fewer than n into a square one -- is kept (a copy)
+    and folded with the chunks after it once they reach that many rows.
+    RᵀR is the sum of the folded rows' Gram matrices, so the factor does not
+    depend on how the rows are grouped.  fp32 arithmetic folds every chunk
+    as it comes.  Readers of the factor drain the rows held."""
+
+    def __init__(self) -> None:
+        self.chunks: List[torch.Tensor] = []
+        self.rows = 0
+
+    def _due(self, r_in: int, n: int, rows: int) -> bool:
+        return r_in + rows >= 2 * n or (r_in >= n and rows >= n)
+
+    def add(self, buf: torch.Tensor, r_in: int, chunk: torch.Tensor, math_: int,
+            queue: Optional["FoldStatusQueue"] = None) -> int:
+        n = buf.shape[1]
+        if not self.chunks and (math_ != MATH_BF16 or self._due(r_in, n, chunk.shape[0])):
+            return fold_chunk(buf, r_in, chunk, math_, queue)
+        self.chunks.append(chunk.detach().clone(memory_format=torch.contiguous_format))
+        self.rows += chunk.shape[0]
+        if self._due(r_in, n, self.rows):
+            return self.drain(buf, r_in, math_, queue)
+        return r_in
+
+    def take(self) -> Optional[torch.Tensor]:
+        """The rows held, as one chunk (None if none), and forget them."""
+        if not self.chunks:
+            return None
+        X = self.chunks[0] if len(self.chunks) == 1 else torch.cat(self.chunks, dim=0)
+        self.chunks, self.rows = [], 0
+        return X
+
+    def drain(self, buf: torch.Tensor, r_in: int, math_: int,
+              queue: Optional["FoldStatusQueue"] = None) -> int:
+        X = self.take()
+        return r_in if X is None else fold_chunk(buf, r_in, X, math_, queue)
+
+
 class IFKFACRankError(RuntimeError):
     """Raised when a layer has fewer accumulated rows than columns (p < n)."""
 
@@ -243,6 +288,9 @@ class RawActivationHooks(GramMatrixEstimator):
         self._held_G: Dict[nn.Module, Optional[torch.Tensor]] = {}
         # Gram-route folds (bf16 arithmetic) whose status the host has not read
         self._fold_queue = FoldStatusQueue()
+        # small chunks held for one larger fold (bf16 arithmetic)
+        self._acc_X: Dict[nn.Module, RowAccumulator] = {}
+        self._acc_G: Dict[nn.Module, RowAccumulator] = {}
         self._linear_layers: List[nn.Module] = []
 
         for module in model.modules():
@@ -284,6 +332,8 @@ class RawActivationHooks(GramMatrixEstimator):
 
     def clear(self):
         self._fold_queue.discard()
+        self._acc_X.clear()
+        self._acc_G.clear()
         for module in self._linear_layers:
             self._R_X[module] = None
             self._R_G[module] = None
@@ -332,8 +382,35 @@ class RawActivationHooks(GramMatrixEstimator):
             if cur.data_ptr() != buf.data_ptr():
                 buf[:r_in].copy_(cur)
         self._fold_queue.poll()
-        r_new = fold_chunk(buf, r_in, chunk, self.math, self._fold_queue)
+        if full_rank_shape:
+            r_new = fold_chunk(buf, r_in, chunk, self.math, self._fold_queue)
+        else:
+            acc = (self._acc_X if side == "X" else self._acc_G).setdefault(module,
+                                                                            RowAccumulator())
+            r_new = acc.add(buf, r_in, chunk, self.math, self._fold_queue)
         Rd[module] = buf[:r_new]
+
+    def _drain_rows(self, consume: bool, only: Optional[Tuple[str, nn.Module]] = None) -> None:
+        """Fold the rows the accumulators hold -- or, with ``consume``, put them
+        in front of the side's held chunk, which the fused fold + finalize
+        then takes in one factorisation."""
+        for side, accs, held in (("X", self._acc_X, self._held_X),
+                                 ("G", self._acc_G, self._held_G)):
+            for module, acc in list(accs.items()):
+                if only is not None and (side, module) != only:
+                    continue
+                if not acc.chunks:
+                    continue
+                if consume and held.get(module) is not None:
+                    held[module] = torch.cat([acc.take(), held[module]], dim=0)
+                    continue
+                X = acc.take()
+                Rd = self._R_X if side == "X" else self._R_G
+                cur = Rd.get(module)
+                buf = (self._buf_X if side == "X" else self._buf_G)[module]
+                r_in = 0 if cur is None else cur.shape[0]
+                r_new = fold_chunk(buf, r_in, X, self.math, self._fold_queue)
+                Rd[module] = buf[:r_new]
 
     def _finalize(self, R_raw: torch.Tensor, rows: int, out_dtype: torch.dtype,
                   math_: Optional[int] = None):
@@ -368,6 +445,7 @@ class RawActivationHooks(GramMatrixEstimator):
         if chunk is not None:
             self._fold(side, module, chunk)
             held[module] = None
+        self._drain_rows(False, (side, module))
         self._fold_queue.drain()
         return (self._R_X if side == "X" else self._R_G).get(module)
 
@@ -523,6 +601,7 @@ class RawActivationHooks(GramMatrixEstimator):
             self._drain_deferred()
         if not consume:
             self._fold_held()
+        self._drain_rows(consume)
         # the Gram-route folds whose status is still on its way: a refused
         # chunk goes into its running factor by the panel path now
         self._fold_queue.drain()

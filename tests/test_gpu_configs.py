@@ -385,6 +385,7 @@ def test_vit_b_block_capture_200_batches(hip, math_):
         if b % 25 == 24:
             # every running factor against the fp64 Gram of its rows so far (a
             # fold that went wrong shows as a jump at its checkpoint)
+            hooks._drain_rows(False)
             hooks._fold_queue.drain()
             errs = []
             for m in block:

@@ -778,12 +778,14 @@ def test_triangular_mirrors_match_oracle(be):
 
 
 def test_bf16_fold_takes_gram_route_when_square(be):
-    """bf16 arithmetic: a fold into a square running factor goes to the
-    Gram-route fold; the first (partial-rank) chunk, a nearly square fold into
-    a partial-rank factor (r_in < n <= r_in + p < 2n: its status is read only
-    later, so it takes the panel fold directly), a refused fold (status 2,
-    injected or from a repeated column) and fp32 arithmetic go to the panel
-    fold.  Every path leaves the oracle's running factor."""
+    """bf16 arithmetic: chunks too small for a fold that pays (fewer than 2n
+    rows into a partial factor) are held and folded together once they
+    reach it -- by the Gram route, whose refusal (status 2, injected) sends
+    the rows to the panel fold -- and a chunk of n rows into the square
+    factor goes to the Gram route at once; fp32 arithmetic folds every chunk
+    by the panel fold as it comes.  Whatever the grouping, the running
+    factor is the oracle's of the rows folded; ``_running_factor`` folds the
+    rows still held."""
     from ifkfac_amd._backend import MATH_BF16, MATH_F32
     from ifkfac_amd.activation_hooks import GRAM_FOLD_TOL, RawActivationHooks
     model = nn.Sequential(nn.Linear(8, 4))
@@ -791,21 +793,37 @@ def test_bf16_fold_takes_gram_route_when_square(be):
     rng = np.random.default_rng(3)
     chunks = [rng.standard_normal((p, 8)) for p in (5, 6, 8, 8)]
     chunks[3][:, 7] = chunks[3][:, 0]            # a column repeated within the chunk
-    for math_, calls in ((MATH_BF16, (0, 0, 1, 1)), (MATH_F32, (0, 0, 0, 0))):
+    for math_, calls, folded in ((MATH_BF16, (0, 0, 1, 1), (0, 0, 3, 4)),
+                                 (MATH_F32, (0, 0, 0, 0), (1, 2, 3, 4))):
         be.calls.clear()
         hooks = RawActivationHooks(model, math=math_)
-        old = None
         for i, c in enumerate(chunks):
             if i == 2 and math_ == MATH_BF16:
                 be.gram_fold_status2 = 1          # the device reports an ill-conditioned fold
             before = be.calls["fold_gram"]
             hooks._fold("X", lin, torch.tensor(c, dtype=torch.float32))
             assert be.calls["fold_gram"] - before == calls[i], (math_, i)
-            old = O.streaming_tsqr_update(old, c.astype(np.float32).astype(np.float64))
-            got = hooks._R_X[lin].double().numpy()
+            R = hooks._R_X[lin]
+            k = folded[i]
+            if k == 0:
+                assert R is None or R.shape[0] == 0
+                continue
+            old = None
+            for c2 in chunks[:k]:
+                old = O.streaming_tsqr_update(old, c2.astype(np.float32).astype(np.float64))
+            got = R.double().numpy()
             assert got.shape == old.shape
-            assert np.abs(got - old).max() <= 1e-5 * np.abs(old).max(), (math_, i)
+            assert np.abs(got.T @ got - old.T @ old).max() <= 1e-5 * np.abs(old.T @ old).max(), \
+                (math_, i)
         hooks.remove()
+    # rows held are folded by the readers of the factor
+    hooks = RawActivationHooks(model, math=MATH_BF16)
+    hooks._fold("X", lin, torch.tensor(chunks[0], dtype=torch.float32))
+    assert hooks._R_X[lin] is None or hooks._R_X[lin].shape[0] == 0
+    R = hooks._running_factor(lin, "X").double().numpy()
+    want = O.streaming_tsqr_update(None, chunks[0].astype(np.float32).astype(np.float64))
+    assert np.abs(R.T @ R - want.T @ want).max() <= 1e-5 * np.abs(want.T @ want).max()
+    hooks.remove()
     assert be.gram_fold_status2 == 0
     # the repeated column is refused by the pivot rule itself
     P = np.vstack([O.streaming_tsqr_update(None, np.vstack(chunks[:3])), chunks[3]])
