@@ -289,21 +289,27 @@ class LayerChain:
                             lambda: self._side(self.D, RG, self.path),
                             b_first=self.n_out > self.n_in))
         st = torch.cat([out[0][1], out[1][1]]).cpu()
+        self.flagged = False
         for i, (T, R) in enumerate(((self.X, RX), (self.D, RG))):
             if int(st[i]) == 2:
                 # as the hooks: a flagged side is refactored in fp32 arithmetic
                 out[i] = self._side(T, R, "panel", math_=0)
+                self.flagged = True
         self.factors = out
         return out
 
     def step(self, first, mark=lambda: None):
+        import torch
         mark()
         (_, _, ix), (_, _, ig) = self.factor_update()
         mark()
-        if self.math == 1:
-            nat = self.be.precondition_apply_bf16(self.grad, (ix[1], ix[2]), (ig[1], ig[2]))
+        if self.math == 1 and not self.flagged:
+            nat = self.be.precondition_apply_bf16(self.grad, ix[1:], ig[1:])
         else:
-            nat = self.be.precondition_apply(self.grad, ix, ig, 0)
+            # fp32 arithmetic, or a side refactored in fp32: the fp32 apply on
+            # both sides' fp32 inverses
+            zx, zg = (z if isinstance(z, torch.Tensor) else z[0] for z in (ix, ig))
+            nat = self.be.precondition_apply(self.grad, zx, zg, 0)
         mark()
         self.be.momentum_update_(nat, self.buf, self.W, 1e-3, 0.9, 0.0, first)
         mark()
@@ -708,8 +714,9 @@ def main() -> int:
         }
         # kappa_2 of the damped factors of the timed step
         (FX, _, ix), (FG, _, ig) = runner.factors
-        kx = float(be.cond_estimate(FX, ix[0]).item())
-        kg = float(be.cond_estimate(FG, ig[0]).item())
+        zx, zg = (z if isinstance(z, torch.Tensor) else z[0] for z in (ix, ig))
+        kx = float(be.cond_estimate(FX, zx).item())
+        kg = float(be.cond_estimate(FG, zg).item())
         out_extra["kappa_R_damped"] = {"R_X": round(kx, 4), "R_G": round(kg, 4)}
     head_kappa = out_extra.get("kappa_R_damped")
 
