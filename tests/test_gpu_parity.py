@@ -164,12 +164,13 @@ def test_gemm_stream_k(hip, m, n, k, beta):
     assert torch.equal(C1, C2)
 
 
-@pytest.mark.parametrize("tri", ["upper_a", "lower_b", "upper_b"])
-@pytest.mark.parametrize("n,rows", [(1280, 1100), (4096, 3600)])
+@pytest.mark.parametrize("tri", ["upper_a", "lower_a", "lower_b", "upper_b"])
+@pytest.mark.parametrize("n,rows", [(1280, 1100), (4096, 3600), (2900, 5000), (11008, 300)])
 def test_gemm_direct_lds_triangular(hip, tri, n, rows):
     """Triangular bf16 operands (as in the preconditioner) through the
-    direct-to-LDS kernel, both tiles: the stored zero triangle is filled with
-    garbage, which the kernel must ignore."""
+    direct-to-LDS kernel, both tiles and the XCD walks over ragged tile
+    counts: the stored zero triangle is filled with garbage, which the kernel
+    must ignore."""
     g = torch.Generator(device=DEV).manual_seed(42)
     Z = torch.randn(n, n, device=DEV, generator=g)
     G = torch.randn(rows, n, device=DEV, generator=g).to(torch.bfloat16)
@@ -180,6 +181,13 @@ def test_gemm_direct_lds_triangular(hip, tri, n, rows):
         # C = U G^T: op(A) = U upper triangular, B = G stored (n_rows x K)
         ref = Zt.double() @ G.double().t()
         C = hip.gemm(noisy, G, False, True, 1, tri_a=1)
+    elif tri == "lower_a":
+        # C = L G^T: op(A) = L = U^T lower triangular, given row-major,
+        # garbage above its diagonal
+        ref = Zt.double().t() @ G.double().t()
+        noisyT = (Zt.float().t() + torch.triu(torch.randn(n, n, device=DEV, generator=g), 1)).to(
+            torch.bfloat16).contiguous()
+        C = hip.gemm(noisyT, G, False, True, 1, tri_a=2)
     elif tri == "lower_b":
         # C = G U^T: op(B) = U^T lower triangular, given as B[n][k] = U
         ref = G.double() @ Zt.double().t()
