@@ -477,7 +477,7 @@ class VitCapture:
     into the running factors of both sides of qkv 768->2304, proj 768->768,
     fc1 768->3072 and fc2 3072->768 (bf16 arithmetic, the Gram route with the
     panel fold for a refused fold, the statuses read without blocking), as the
-    hooks issue them."""
+    hooks issue them: held, then one batched fold per shape)."""
 
     shapes = [(768, 2304), (768, 768), (768, 3072), (3072, 768)]
     rows = 4096
@@ -501,11 +501,15 @@ class VitCapture:
 
     def step(self, first, mark=lambda: None):
         from ifkfac_amd._backend import MATH_BF16
-        from ifkfac_amd.activation_hooks import fold_chunk
+        from ifkfac_amd.activation_hooks import FoldGroups
         mark()
         self.queue.poll()
-        for R, T in zip(self.Rs, self.chunks):
-            fold_chunk(R, R.shape[0], T, MATH_BF16, self.queue)
+        # as the hooks: each fold held (a copy of its chunk), then one batched
+        # Gram-route fold per shape
+        groups = FoldGroups()
+        for i, (R, T) in enumerate(zip(self.Rs, self.chunks)):
+            groups.hold(i, R, R.shape[0], T)
+        groups.flush(MATH_BF16, self.queue)
         mark()
 
 
@@ -608,7 +612,8 @@ def extras(be, args, head_kappa):
         "roofline": roof_b, "kernels": table_b,
         "ms_get_factors": round(ms_f, 3),
         "note": "8 folds of 4096 rows per batch into running factors (bf16 arithmetic, "
-                "the Gram route with the panel fold for a refused fold); 200 batches x 12 "
+                "held as the hooks hold them and folded by one batched Gram-route fold per "
+                "shape, the panel fold for a refused fold); 200 batches x 12 "
                 "blocks take 2400 x ms_per_batch; get_factors() of the 8 sides by the Gram "
                 "route"}
     del cap

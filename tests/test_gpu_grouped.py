@@ -197,3 +197,43 @@ def test_hooks_batched_flush_grouped_matches_per_layer(hip):
         single = run()
     for a, b in zip(grouped, single):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_hooks_grouped_folds_match_per_layer(hip):
+    """RawActivationHooks (per-batch folds) in bf16 arithmetic over three
+    same-shape layers, 2048-row batches: each batch's Gram-route folds of the
+    three layers are held and go through one batched fold per side (the first
+    batch's trapezoid folds included); after three batches the factors are bit
+    for bit those of the per-layer folds, and the batched fold was called."""
+    from ifkfac_amd import RawActivationHooks
+    from ifkfac_amd._backend import MATH_BF16
+    calls = [0]
+    cls = type(hip)
+    real = cls.fold_gram_batched_
+
+    def wrap(self, *a):
+        calls[0] += 1
+        return real(self, *a)
+
+    def run():
+        model = _mlp(5, n=768, layers=3)
+        hooks = RawActivationHooks(model, damping=1e-3, math=MATH_BF16)
+        hooks.enable()
+        g = torch.Generator(device=DEV).manual_seed(6)
+        for _ in range(3):
+            x = torch.randn(2048, 768, device=DEV, generator=g)
+            model(x).square().mean().backward()
+        f = hooks.get_factors()
+        return [tuple(t.clone() for t in f[m]) for m in model if isinstance(m, nn.Linear)]
+
+    cls.fold_gram_batched_ = wrap
+    try:
+        grouped = run()
+    finally:
+        cls.fold_gram_batched_ = real
+    with _Hide(hip, ["fold_gram_batched_"]):
+        single = run()
+    print(f"batched folds {calls[0]}")
+    assert calls[0] >= 2
+    for a, b in zip(grouped, single):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
