@@ -164,7 +164,13 @@ __device__ inline float safe_divisor(float d) {
 // With INV, Z (LDS, stride SLD) also receives U^{-1}: the same row operations
 // applied to the identity give W = U^{-T} (lower triangular; blocks 00, 10,
 // 11 in the same layout, updated by the same pivots, scalings and rank-2
-// products), stored transposed.
+// products), stored transposed.  Wave 1 carries W alongside wave 0: as soon
+// as wave 0 has factored a panel it writes the panel's four rows of U (final
+// from then on) into A and their pivots' reciprocal square roots into LDS and
+// bumps a panel counter; wave 1 takes the row operations' coefficients and
+// the rank-2 operands from there, so the inverse costs the factorisation no
+// time (the same operations on the same values: W bit for bit as when one
+// wave did both).
 template <int CB = 32, bool EXACT = false, bool INV = false>
 __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mode,
                                           const float* dref = nullptr, int b = SB,
@@ -173,8 +179,23 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6, l32 = lane & 31, h = lane >> 5;
   __shared__ float dgs[SB];   // reference diagonal of the pivot test
+  __shared__ float rsv[SB];   // INV: each pivot's reciprocal square root (wave 0 -> 1)
+  __shared__ int panels;      // INV: panels whose rows of U are in A (wave 0 -> 1)
   if (t < SB) dgs[t] = (dref != nullptr && t < b) ? dref[t] : A[t * SLD + t];
+  if (INV && t == 0) panels = 0;
   __syncthreads();
+  // lane l: row 4p + 2 s2 (l < 32) or the next row (l >= 32) of a panel whose
+  // rows sit in the lanes of half hk, from the registers of its two rows
+  auto pair = [&](float x0, float x1, int hk) -> float {
+    if (hk == 0) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x1), __float_as_uint(x1),
+                                                       false, false);
+      return h == 0 ? x0 : __uint_as_float(sw[0]);
+    }
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0), __float_as_uint(x0),
+                                                     false, false);
+    return h == 0 ? __uint_as_float(sw[1]) : x1;
+  };
   if (wave == 0) {
     f32x16 b00, b01, b11;
 #pragma unroll
@@ -183,16 +204,6 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
       b00[j] = (r <= l32) ? A[r * SLD + l32] : 0.0f;
       b01[j] = A[r * SLD + 32 + l32];
       b11[j] = (r <= l32) ? A[(32 + r) * SLD + 32 + l32] : 0.0f;
-    }
-    f32x16 w00, w10, w11;   // W = U^{-T}, from the identity
-    if (INV) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = (j >> 2) * 8 + h * 4 + (j & 3);
-        w00[j] = (r == l32) ? 1.0f : 0.0f;
-        w10[j] = 0.0f;
-        w11[j] = (r == l32) ? 1.0f : 0.0f;
-      }
     }
     int flag = 0;
     const float dgv = dgs[lane];            // the reference diagonal, lane k holding k's
@@ -226,17 +237,13 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
           dg = sqrtf((piv >= 1e-7f || piv != piv) ? piv : 1e-7f);
           rs = 1.0f / dg;
         }
+        if (INV && lane == 0) rsv[k] = rs;
         // row k of U: its half's lanes of every block in block row K
         if (K == 0) {
           b00[reg] = mine ? ((l32 == kk) ? dg : b00[reg] * rs) : b00[reg];
           b01[reg] = mine ? b01[reg] * rs : b01[reg];
-          if (INV) w00[reg] = mine ? w00[reg] * rs : w00[reg];
         } else {
           b11[reg] = mine ? ((l32 == kk) ? dg : b11[reg] * rs) : b11[reg];
-          if (INV) {
-            w10[reg] = mine ? w10[reg] * rs : w10[reg];
-            w11[reg] = mine ? w11[reg] * rs : w11[reg];
-          }
         }
         // the panel's later rows
 #pragma unroll
@@ -246,36 +253,40 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
           if (K == 0) {
             b00[r2] = mine ? fmaf(-c, b00[reg], b00[r2]) : b00[r2];
             b01[r2] = mine ? fmaf(-c, b01[reg], b01[r2]) : b01[r2];
-            if (INV) w00[r2] = mine ? fmaf(-c, w00[reg], w00[r2]) : w00[r2];
           } else {
             b11[r2] = mine ? fmaf(-c, b11[reg], b11[r2]) : b11[r2];
-            if (INV) {
-              w10[r2] = mine ? fmaf(-c, w10[reg], w10[r2]) : w10[r2];
-              w11[r2] = mine ? fmaf(-c, w11[reg], w11[r2]) : w11[r2];
+          }
+        }
+      }
+      if (INV) {
+        // the panel's rows of U are final: into A (zero left of the
+        // diagonal) for wave 1
+        if (mine) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int k = 4 * p + q, reg = jb + q;
+            if (K == 0) {
+              A[k * SLD + l32] = (k <= l32) ? b00[reg] : 0.0f;
+              A[k * SLD + 32 + l32] = b01[reg];
+            } else {
+              A[k * SLD + l32] = 0.0f;
+              A[k * SLD + 32 + l32] = (k - 32 <= l32) ? b11[reg] : 0.0f;
             }
           }
         }
       }
-      if (p == 15) break;
+      if (p == 15) {
+        if (INV && lane == 0)
+          __hip_atomic_store(&panels, 16, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        break;
+      }
       // the panel applied to rows and columns from pend on: two rank-2 products
       const int pend = 4 * p + 4;
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         const int r0 = jb + 2 * s2, r1 = r0 + 1;
-        // lane l: row 4p + 2 s2 (l < 32) or the next row (l >= 32) of the
-        // panel at column colbase + l % 32, zero left of pend
-        auto pair = [&](float x0, float x1) -> float {
-          if (hk == 0) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x1),
-                                                             __float_as_uint(x1), false, false);
-            return h == 0 ? x0 : __uint_as_float(sw[0]);
-          }
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0),
-                                                           __float_as_uint(x0), false, false);
-          return h == 0 ? __uint_as_float(sw[1]) : x1;
-        };
         auto opnd = [&](float x0, float x1, int colbase) -> float {
-          const float v = pair(x0, x1);
+          const float v = pair(x0, x1, hk);
           return (colbase + l32 >= pend) ? v : 0.0f;
         };
         if (K == 0) {
@@ -283,39 +294,103 @@ __device__ __forceinline__ void sm_chol64(float* A, float tol, int* bad, int mod
           if (pend < 32) b00 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, u0, b00, 0, 0, 0);
           b01 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, u1, b01, 0, 0, 0);
           b11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, u1, b11, 0, 0, 0);
-          if (INV) {
-            // rows >= pend of W take the panel's rows of W (columns <= k)
-            const float v0 = pair(w00[r0], w00[r1]);
-            if (pend < 32) w00 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, v0, w00, 0, 0, 0);
-            w10 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v0, w10, 0, 0, 0);
-          }
         } else {
           const float u1 = opnd(b11[r0], b11[r1], 32);
           b11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, u1, b11, 0, 0, 0);
-          if (INV) {
-            const float v0 = pair(w10[r0], w10[r1]), v1 = pair(w11[r0], w11[r1]);
-            w10 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v0, w10, 0, 0, 0);
-            w11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v1, w11, 0, 0, 0);
+        }
+      }
+      // the count behind the rank-2 products: the row writes have landed by
+      // now, so its wait for them costs nothing
+      if (INV && lane == 0)
+        __hip_atomic_store(&panels, p + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (!INV) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = (j >> 2) * 8 + h * 4 + (j & 3);
+        A[r * SLD + l32] = (r <= l32) ? b00[j] : 0.0f;
+        A[r * SLD + 32 + l32] = b01[j];
+        A[(32 + r) * SLD + l32] = 0.0f;
+        A[(32 + r) * SLD + 32 + l32] = (r <= l32) ? b11[j] : 0.0f;
+      }
+    }
+    if (flag && bad) *bad = 1;
+  } else if (INV && wave == 1) {
+    f32x16 w00, w10, w11;   // W = U^{-T}, from the identity
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = (j >> 2) * 8 + h * 4 + (j & 3);
+      w00[j] = (r == l32) ? 1.0f : 0.0f;
+      w10[j] = 0.0f;
+      w11[j] = (r == l32) ? 1.0f : 0.0f;
+    }
+    bool late = false;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const int K = p >> 3, hk = p & 1, jb = ((p & 7) >> 1) * 4;
+      const bool mine = h == hk;
+      // wave 0 runs ahead and never waits for this wave, so the wait ends;
+      // the bound only keeps a broken count from spinning forever
+      for (int it = 0; __hip_atomic_load(&panels, __ATOMIC_ACQUIRE,
+                                         __HIP_MEMORY_SCOPE_WORKGROUP) < p + 1; ++it) {
+        if (it > (1 << 22)) {
+          late = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int k = 4 * p + q, reg = jb + q;
+        const float rs = rsv[k];
+        if (K == 0) {
+          w00[reg] = mine ? w00[reg] * rs : w00[reg];
+        } else {
+          w10[reg] = mine ? w10[reg] * rs : w10[reg];
+          w11[reg] = mine ? w11[reg] * rs : w11[reg];
+        }
+#pragma unroll
+        for (int q2 = q + 1; q2 < 4; ++q2) {
+          const int r2 = jb + q2;
+          const float c = A[k * SLD + 4 * p + q2];   // U[k][4p + q2]
+          if (K == 0) {
+            w00[r2] = mine ? fmaf(-c, w00[reg], w00[r2]) : w00[r2];
+          } else {
+            w10[r2] = mine ? fmaf(-c, w10[reg], w10[r2]) : w10[r2];
+            w11[r2] = mine ? fmaf(-c, w11[reg], w11[r2]) : w11[r2];
           }
+        }
+      }
+      if (p == 15) break;
+      const int pend = 4 * p + 4;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int r0 = jb + 2 * s2, r1 = r0 + 1;
+        // the rank-2 operands wave 0 uses, from the rows of U in A
+        const int row = 4 * p + 2 * s2 + h;
+        const float u1 = (32 + l32 >= pend) ? A[row * SLD + 32 + l32] : 0.0f;
+        if (K == 0) {
+          const float u0 = (l32 >= pend) ? A[row * SLD + l32] : 0.0f;
+          const float v0 = pair(w00[r0], w00[r1], hk);
+          if (pend < 32) w00 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u0, v0, w00, 0, 0, 0);
+          w10 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v0, w10, 0, 0, 0);
+        } else {
+          const float v0 = pair(w10[r0], w10[r1], hk), v1 = pair(w11[r0], w11[r1], hk);
+          w10 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v0, w10, 0, 0, 0);
+          w11 = __builtin_amdgcn_mfma_f32_32x32x2f32(-u1, v1, w11, 0, 0, 0);
         }
       }
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int r = (j >> 2) * 8 + h * 4 + (j & 3);
-      A[r * SLD + l32] = (r <= l32) ? b00[j] : 0.0f;
-      A[r * SLD + 32 + l32] = b01[j];
-      A[(32 + r) * SLD + l32] = 0.0f;
-      A[(32 + r) * SLD + 32 + l32] = (r <= l32) ? b11[j] : 0.0f;
-      if (INV) {
-        // Z = W^T: W's element (row, col) goes to Z[col][row]
-        Z[l32 * SLD + r] = (r >= l32) ? w00[j] : 0.0f;
-        Z[l32 * SLD + 32 + r] = w10[j];
-        Z[(32 + l32) * SLD + r] = 0.0f;
-        Z[(32 + l32) * SLD + 32 + r] = (r >= l32) ? w11[j] : 0.0f;
-      }
+      // Z = W^T: W's element (row, col) goes to Z[col][row]
+      Z[l32 * SLD + r] = (r >= l32) ? w00[j] : 0.0f;
+      Z[l32 * SLD + 32 + r] = w10[j];
+      Z[(32 + l32) * SLD + r] = 0.0f;
+      Z[(32 + l32) * SLD + 32 + r] = (r >= l32) ? w11[j] : 0.0f;
     }
-    if (flag && bad) *bad = 1;
+    if (late && bad) *bad = 1;
   }
   __syncthreads();
 }
