@@ -1002,3 +1002,81 @@ def test_triangular_mirrors_on_gpu(hip):
     assert _rel(natb[1], 2 * ref) <= 1e-5
     gb = rng.standard_normal(200)
     assert _rel(T.apply_vered_bias(t(gb), t(R_G)), O.apply_vered_bias(gb, R_G)) <= 1e-5
+
+
+def test_triangular_api_helpers_on_gpu(hip):
+    """The reference module's off-path helpers (triangular.py:89-143, 150-227,
+    331-379, 506-544) on the GPU: tsqr honours tile_size (700 rows in tiles of
+    128: the same R as one fold, against the oracle); sgso's Q has orthonormal
+    columns and Q R = M, R the oracle's; the bucket fold in bf16 arithmetic
+    takes one batched Gram-route fold (each entry's factor that of its
+    bf16-rounded rows within 1e-4) and folds an entry the Gram route
+    refuses -- a repeated column at 1e3 times the others' scale -- by the
+    panel path; apply_vered_batched with bf16 factors runs the batched apply,
+    each entry bit for bit tri_inverse_bf16 + precondition_apply_bf16, within
+    2e-2 of fp64 solves on the same factors."""
+    from ifkfac_amd import triangular as T
+    from ifkfac_amd._backend import MATH_BF16
+    rng = np.random.default_rng(34)
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=DEV)
+    X = rng.standard_normal((700, 300))
+    want = O.streaming_tsqr_update(None, X)
+    Rt = T.tsqr(t(X), tile_size=128).double().cpu().numpy()
+    assert _gram_rel(Rt, want) <= 1e-5
+    with pytest.raises(ValueError):
+        T.tsqr(t(X), tile_size=0)
+    Q, R = T.sgso(t(X))
+    Qd, Rd = Q.double().cpu().numpy(), R.double().cpu().numpy()
+    assert _gram_rel(Rd, want) <= 1e-5 and bool((np.diag(Rd) > 0).all())
+    assert np.linalg.norm(Qd.T @ Qd - np.eye(300)) <= 1e-4 * np.sqrt(300)
+    assert np.linalg.norm(Qd @ Rd - X) <= 1e-5 * np.linalg.norm(X)
+    with pytest.raises(ValueError):
+        T.sgso(t(X[:100]))
+    # bucket fold, bf16 arithmetic: entries 0 and 2 by the Gram route, entry 1 refused
+    n, p = 256, 1024
+    R0 = torch.stack([t(O.streaming_tsqr_update(None, rng.standard_normal((p, n))))
+                      for _ in range(3)])
+    chunks = np.stack([rng.standard_normal((p, n)) for _ in range(3)])
+    chunks[1][:, 5] *= 1e3
+    chunks[1][:, 9] = chunks[1][:, 5]
+    calls = [0]
+    real = type(hip).fold_gram_batched_
+
+    def wrap(self, *a):
+        calls[0] += 1
+        return real(self, *a)
+
+    type(hip).fold_gram_batched_ = wrap
+    try:
+        Rb = T.batched_streaming_tsqr_update(R0, t(chunks), math=MATH_BF16)
+    finally:
+        type(hip).fold_gram_batched_ = real
+    assert calls[0] == 1
+    for i in range(3):
+        r0 = R0[i].double().cpu().numpy()
+        rows = O.bf16_round(chunks[i].astype(np.float32)).astype(np.float64)
+        got = Rb[i].double().cpu().numpy()
+        if i == 1:
+            # the panel path in fp32 arithmetic on the rows as given
+            ref_i = O.streaming_tsqr_update(r0, chunks[i])
+            assert _gram_rel(got, ref_i) <= 4 * _kappa(ref_i) * EPS32
+        else:
+            # the chunk's rows as bf16 (their RNE rounding), the running
+            # factor split hi + lo (fp32 to about 2^-16)
+            ref_i = O.streaming_tsqr_update(r0, rows)
+            assert _gram_rel(got, ref_i) <= 1e-4, i
+    # bucket apply, bf16 factors
+    R_X = O.get_factor(O.streaming_tsqr_update(None, rng.standard_normal((900, 256))), 900, 1e-2)
+    R_G = O.get_factor(O.streaming_tsqr_update(None, rng.standard_normal((900, 192))), 900, 1e-2)
+    Rxb = torch.stack([t(R_X), t(2 * R_X)]).bfloat16()
+    Rgb = torch.stack([t(R_G), t(R_G)]).bfloat16()
+    G = t(rng.standard_normal((2, 192, 256)))
+    natb = T.apply_vered_batched(G, Rxb, Rgb)
+    for i in range(2):
+        _, zxb, zxt = hip.tri_inverse_bf16(Rxb[i])
+        _, zgb, zgt = hip.tri_inverse_bf16(Rgb[i])
+        one = hip.precondition_apply_bf16(G[i], (zxb, zxt), (zgb, zgt))
+        assert torch.equal(natb[i], one), i
+        ref = O.apply_vered(G[i].double().cpu().numpy(), Rxb[i].double().cpu().numpy(),
+                            Rgb[i].double().cpu().numpy())
+        assert _rel(natb[i], ref) <= 2e-2
