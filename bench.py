@@ -241,29 +241,51 @@ class LayerChain:
             self.RX = torch.zeros(n_in, n_in, device=self.dev)
             self.RG = torch.zeros(n_out, n_out, device=self.dev)
 
-    def _side(self, T, R, how, math_=None):
+    def _chunk_folds(self, fq, accs):
+        """As the hooks: the chunks of a streamed step but the last, both
+        sides in arrival order (a batch's input chunk in the forward pass, its
+        output-gradient chunk in the backward pass), small ones held until a
+        fold of them pays, and in bf16 arithmetic each fold that pays held for
+        one batched fold with the other side's (a factor's next fold first
+        folds everything held), with no status read.  Returns each side's row
+        count."""
+        from ifkfac_amd._backend import MATH_BF16
+        from ifkfac_amd.activation_hooks import FoldGroups, RowAccumulator
+        q = self.p // self.chunks
+        r = {"X": 0, "G": 0}
+        groups = FoldGroups()
+        grouping = self.math == MATH_BF16 and hasattr(self.be, "fold_gram_batched_")
+        for c in range(self.chunks - 1):
+            for side, T, R in (("X", self.X, self.RX), ("G", self.D, self.RG)):
+                if side in groups:
+                    groups.flush(self.math, fq)
+                acc = accs.setdefault(side, RowAccumulator())
+                chunk = T[c * q:(c + 1) * q]
+                if grouping:
+                    rows, private = acc.offer(r[side], R.shape[1], chunk)
+                    if rows is not None:
+                        groups.hold(side, R, r[side], rows, private)
+                        r[side] = R.shape[1]
+                else:
+                    r[side] = acc.add(R, r[side], chunk, self.math, fq)
+        groups.flush(self.math, fq)
+        return r
+
+    def _last_rows(self, T, acc):
+        """The rows the factor update folds: the whole input, or with chunks the
+        last chunk with the rows still held in front of it."""
+        import torch
+        if self.chunks == 1:
+            return T
+        last = T[(self.chunks - 1) * (self.p // self.chunks):]
+        rows = acc.take() if acc is not None else None
+        return last if rows is None else torch.cat([rows, last], dim=0)
+
+    def _side(self, last, R, how, math_=None, r=0):
         import torch
         from ifkfac_amd._backend import MATH_BF16
-        from ifkfac_amd.activation_hooks import FoldStatusQueue, RowAccumulator
         be, p = self.be, self.p
         am = self.math if math_ is None else math_
-        r = 0
-        last = T
-        if self.chunks > 1:
-            # as the hooks: every chunk but the held one goes into the running
-            # factor (small ones held until a fold of them pays), no status
-            # read; the factor update takes the rows still held in front of
-            # the held chunk, after reading the statuses
-            q = p // self.chunks
-            fq = FoldStatusQueue()
-            acc = RowAccumulator()
-            for c in range(self.chunks - 1):
-                r = acc.add(R, r, T[c * q:(c + 1) * q], am, fq)
-            fq.drain()
-            last = T[(self.chunks - 1) * q:]
-            rows = acc.take()
-            if rows is not None:
-                last = torch.cat([rows, last], dim=0)
         out_dtype = torch.bfloat16
         # as IFKFAC's factor update: the Gram path in bf16 arithmetic (the
         # factor's inverse formed in the same call), CholeskyQR2 blocks in fp32
@@ -283,17 +305,29 @@ class LayerChain:
     def factor_update(self):
         import torch
         from ifkfac_amd._backend import run_pair
+        from ifkfac_amd.activation_hooks import FoldStatusQueue
         RX = getattr(self, "RX", None)
         RG = getattr(self, "RG", None)
-        out = list(run_pair(self.dev, lambda: self._side(self.X, RX, self.path),
-                            lambda: self._side(self.D, RG, self.path),
+        r = {"X": 0, "G": 0}
+        accs = {}
+        if self.chunks > 1:
+            fq = FoldStatusQueue()
+            r = self._chunk_folds(fq, accs)
+            # the factor update reads the folds' statuses first (a refused
+            # fold goes into its factor by the panel path)
+            fq.drain()
+        lx = self._last_rows(self.X, accs.get("X"))
+        lg = self._last_rows(self.D, accs.get("G"))
+        out = list(run_pair(self.dev,
+                            lambda: self._side(lx, RX, self.path, r=r["X"]),
+                            lambda: self._side(lg, RG, self.path, r=r["G"]),
                             b_first=self.n_out > self.n_in))
         st = torch.cat([out[0][1], out[1][1]]).cpu()
         self.flagged = False
-        for i, (T, R) in enumerate(((self.X, RX), (self.D, RG))):
+        for i, (last, R, side) in enumerate(((lx, RX, "X"), (lg, RG, "G"))):
             if int(st[i]) == 2:
                 # as the hooks: a flagged side is refactored in fp32 arithmetic
-                out[i] = self._side(T, R, "panel", math_=0)
+                out[i] = self._side(last, R, "panel", math_=0, r=r[side])
                 self.flagged = True
         self.factors = out
         return out

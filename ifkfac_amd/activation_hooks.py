@@ -186,7 +186,9 @@ class RowAccumulator:
     and folded with the chunks after it once they reach that many rows.
     RᵀR is the sum of the folded rows' Gram matrices, so the factor does not
     depend on how the rows are grouped.  fp32 arithmetic folds every chunk
-    as it comes.  Readers of the factor drain the rows held."""
+    as it comes.  Readers of the factor drain the rows held.  ``add`` folds
+    the rows once due; ``offer`` hands them to a caller that folds them with
+    other factors' (FoldGroups)."""
 
     def __init__(self) -> None:
         self.chunks: List[torch.Tensor] = []
@@ -205,6 +207,21 @@ class RowAccumulator:
         if self._due(r_in, n, self.rows):
             return self.drain(buf, r_in, math_, queue)
         return r_in
+
+    def offer(self, r_in: int, n: int, chunk: torch.Tensor,
+              owned: bool = False) -> Tuple[Optional[torch.Tensor], bool]:
+        """Hold ``chunk`` (a copy unless ``owned``) unless the rows held with it
+        make a fold that pays; then return them as one chunk, forgetting them:
+        (rows, whether they are a private copy), or (None, False) while held.
+        For a caller that folds them itself (a grouped fold)."""
+        if not self.chunks and self._due(r_in, n, chunk.shape[0]):
+            return chunk, owned
+        self.chunks.append(chunk if owned else
+                           chunk.detach().clone(memory_format=torch.contiguous_format))
+        self.rows += chunk.shape[0]
+        if self._due(r_in, n, self.rows):
+            return self.take(), True
+        return None, False
 
     def take(self) -> Optional[torch.Tensor]:
         """The rows held, as one chunk (None if none), and forget them."""
@@ -248,12 +265,6 @@ class FoldGroups:
 
     def __len__(self) -> int:
         return len(self._items)
-
-    @staticmethod
-    def due(r_in: int, n: int, p: int) -> bool:
-        """Whether fold_chunk (with a queue) would fold p rows into a factor of
-        r_in rows and n columns by the Gram route."""
-        return r_in >= n or r_in + p >= 2 * n
 
     def hold(self, key, buf: torch.Tensor, r_in: int, chunk: torch.Tensor,
              owned: bool = False) -> bool:
@@ -485,11 +496,16 @@ class RawActivationHooks(GramMatrixEstimator):
         else:
             acc = (self._acc_X if side == "X" else self._acc_G).setdefault(module,
                                                                             RowAccumulator())
-            if (not acc.chunks and self._grouping() and
-                    FoldGroups.due(r_in, n, chunk.shape[0])):
-                if self._groups.hold((side, module), buf, r_in, chunk, owned):
-                    self._flush_groups()
-                r_new = n
+            if self._grouping():
+                # small chunks held until a fold of them pays, as the
+                # accumulator does; that fold held for the grouped fold
+                rows, private = acc.offer(r_in, n, chunk, owned)
+                if rows is None:
+                    r_new = r_in
+                else:
+                    if self._groups.hold((side, module), buf, r_in, rows, private):
+                        self._flush_groups()
+                    r_new = n
             else:
                 r_new = acc.add(buf, r_in, chunk, self.math, self._fold_queue)
         Rd[module] = buf[:r_new]
