@@ -281,6 +281,15 @@ class FoldGroups:
         self._items.clear()
         self._bytes = 0
 
+    # A square group of width n joins a wider square group of width N (same
+    # rows per chunk) when n >= MERGE_RATIO * N: its entries ride the wider
+    # group's chain of launches, embedded as [[R, 0], [0, I]] with the chunk
+    # padded by zero columns, whose factor is [[R', 0], [0, I]] with R' the
+    # entry's own.  That costs the entry (N / n)^2 of its Gram flops and saves
+    # its own chain (a ViT-B block's 2304-wide side with its two 3072-wide
+    # ones).
+    MERGE_RATIO = 0.7
+
     def flush(self, math_: int, queue: FoldStatusQueue) -> None:
         items = list(self._items.values())
         self.discard()
@@ -290,20 +299,53 @@ class FoldGroups:
         groups: Dict[tuple, list] = {}
         for buf, r_in, X in items:
             groups.setdefault((tuple(X.shape), X.dtype, X.device, r_in), []).append((buf, X))
-        for (shape, _, _, r_in), ent in groups.items():
+        batched = hasattr(be, "fold_gram_batched_")
+        # narrower square groups into the widest square group of their rows
+        pads: Dict[tuple, list] = {}
+        if batched:
+            square = [k for k in groups if k[3] == k[0][1]]
+            for k in sorted(square, key=lambda k: k[0][1]):
+                if k in pads:   # it takes narrower ones itself
+                    continue
+                p, n = k[0]
+                wide = [w for w in square if w[0][0] == p and w[1:3] == k[1:3] and
+                        w[0][1] > n and n >= self.MERGE_RATIO * w[0][1] and w in groups]
+                if wide:
+                    w = max(wide, key=lambda w: w[0][1])
+                    pads.setdefault(w, []).extend(groups.pop(k))
+        for key, ent in groups.items():
+            shape, r_in = key[0], key[3]
             n = shape[1]
-            if len(ent) == 1 or not hasattr(be, "fold_gram_batched_"):
+            extra = pads.get(key, [])
+            if len(ent) + len(extra) == 1 or not batched:
                 for buf, X in ent:
                     fold_chunk(buf, r_in, X, math_, queue, owned=True)
                 continue
             bufs = [b for b, _ in ent]
+            chunks = [X for _, X in ent]
             if r_in < n:
                 # as fold_chunk: a refused fold then leaves n rows whose extra
                 # rows contribute nothing
                 for b in bufs:
                     b[r_in:].zero_()
-            st = be.fold_gram_batched_(bufs, r_in, [X for _, X in ent], GRAM_FOLD_TOL)
+            embedded = []
+            for buf, X in extra:
+                m = buf.shape[0]
+                P = torch.zeros((n, n), dtype=torch.float32, device=buf.device)
+                P[:m, :m].copy_(buf)
+                d = torch.arange(m, n, device=buf.device)
+                P[d, d] = 1.0
+                Xp = torch.zeros((X.shape[0], n), dtype=X.dtype, device=X.device)
+                Xp[:, :m].copy_(X)
+                bufs.append(P)
+                chunks.append(Xp)
+                embedded.append((buf, X, P, m))
+            st = be.fold_gram_batched_(bufs, r_in, chunks, GRAM_FOLD_TOL)
             for e, (buf, X) in enumerate(ent):
+                queue.push(st[e:e + 1], buf, X, math_, owned=True)
+            for e, (buf, X, P, m) in enumerate(embedded, start=len(ent)):
+                # a refused entry's P is as it was: the copy back changes nothing
+                buf.copy_(P[:m, :m])
                 queue.push(st[e:e + 1], buf, X, math_, owned=True)
 
 

@@ -11,6 +11,7 @@ same weights and factors as with the grouped calls hidden from them.
 """
 import math
 
+import numpy as np
 import pytest
 import torch
 import torch.nn as nn
@@ -237,3 +238,62 @@ def test_hooks_grouped_folds_match_per_layer(hip):
     assert calls[0] >= 2
     for a, b in zip(grouped, single):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_fold_groups_merge_narrower_square_group(hip):
+    """FoldGroups.flush with square factors of widths 2304 and 3072 (4096-row
+    chunks, a ViT-B block's qkv and fc1/fc2 sides): the 2304-wide entries ride
+    the 3072-wide group's batched fold embedded as [[R, 0], [0, I]], so one
+    batched call takes all of them; every factor is that of its rows (the
+    chunk's bf16 rounding, the running factor to fp32 accuracy) within 1e-4,
+    and a 2304-wide entry the Gram route refuses (a repeated column at 1e3
+    times the others' scale) is folded by the panel path once its status is
+    read, its factor untouched by the merged fold."""
+    from ifkfac_amd.activation_hooks import FoldGroups, FoldStatusQueue
+    from ifkfac_amd._backend import MATH_BF16
+    from oracle import ifk_oracle as O
+    rng = np.random.default_rng(11)
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=DEV)
+    widths = [2304, 3072, 3072, 2304]
+    Rs, chunks, R0 = [], [], []
+    for n in widths:
+        R = t(O.streaming_tsqr_update(None, rng.standard_normal((n + 512, n)) * 0.5))
+        Rs.append(R)
+        R0.append(R.double().cpu().numpy())
+        chunks.append(rng.standard_normal((4096, n)))
+    chunks[3][:, 7] *= 1e3
+    chunks[3][:, 11] = chunks[3][:, 7]
+    calls = []
+    cls = type(hip)
+    real = cls.fold_gram_batched_
+
+    def wrap(self, Rs_, r_in, Xs, tol):
+        calls.append((len(Rs_), r_in, Xs[0].shape[1]))
+        return real(self, Rs_, r_in, Xs, tol)
+
+    q = FoldStatusQueue()
+    g = FoldGroups()
+    for i, (R, X) in enumerate(zip(Rs, chunks)):
+        g.hold(i, R, R.shape[0], t(X))
+    cls.fold_gram_batched_ = wrap
+    try:
+        g.flush(MATH_BF16, q)
+    finally:
+        cls.fold_gram_batched_ = real
+    q.drain()
+    print(f"batched calls {calls}, refused {q.refused}")
+    assert calls == [(4, 3072, 3072)]
+    assert q.refused == 1
+    for i, n in enumerate(widths):
+        got = Rs[i].double().cpu().numpy()
+        if i == 3:
+            ref = O.streaming_tsqr_update(R0[i], chunks[i])
+            tol = 4 * np.linalg.cond(ref) * 1.1920929e-07
+        else:
+            rows = O.bf16_round(chunks[i].astype(np.float32)).astype(np.float64)
+            ref = O.streaming_tsqr_update(R0[i], rows)
+            tol = 1e-4
+        a, w = got.T @ got, ref.T @ ref
+        e = np.linalg.norm(a - w) / np.linalg.norm(w)
+        print(f"entry {i} n={n}: {e:.2e}")
+        assert e <= tol, (i, e)
