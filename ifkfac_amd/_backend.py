@@ -303,6 +303,21 @@ class HipBackend:
         _lib.check(rc, "ifk_tri_inverse")
         return Z
 
+    def tri_inverse_x3(self, R: torch.Tensor) -> torch.Tensor:
+        """tri_inverse at about fp32 accuracy on bf16 MFMA (split halves on
+        the wide levels; ifk_tri_inverse_x3)."""
+        R, ldr, rdt = _mat(R, "tri_inverse_x3")
+        n = R.shape[0]
+        if R.shape[1] != n:
+            raise IFKFACBackendError("tri_inverse_x3: R must be square")
+        Z = torch.empty((n, n), dtype=torch.float32, device=R.device)
+        ws = self._ws(self.lib.ifk_tri_inverse_x3_workspace_size(n, rdt), R.device)
+        with torch.cuda.device(R.device):
+            rc = self.lib.ifk_tri_inverse_x3(self._stream(R.device), _ptr(R), rdt, ldr, n, _ptr(Z),
+                                             n, _ptr(ws), ws.numel())
+        _lib.check(rc, "ifk_tri_inverse_x3")
+        return Z
+
     def tri_inverse_bf16(self, R: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor,
                                                           torch.Tensor]:
         """tri_inverse in bf16 arithmetic, also returning the RNE bf16 copies

@@ -87,6 +87,9 @@ SIGNATURES = {
     "ifk_tri_inverse_workspace_size": (_c_sz, [_c_i64]),
     "ifk_tri_inverse": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_int,
                                  _c_vp, _c_sz]),
+    "ifk_tri_inverse_x3_workspace_size": (_c_sz, [_c_i64, _c_int]),
+    "ifk_tri_inverse_x3": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
+                                    _c_sz]),
     "ifk_tri_inverse_bf16_workspace_size": (_c_sz, [_c_i64]),
     "ifk_tri_inverse_bf16": (_c_int, [_c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                       _c_vp, _c_i64, _c_vp, _c_sz]),

@@ -234,6 +234,17 @@ int ifk_tri_inverse_bf16(void* stream, const void* R, int r_dtype, int64_t ldr, 
                       ldb, workspace, workspace_bytes);
 }
 
+size_t ifk_tri_inverse_x3_workspace_size(int64_t n, int r_dtype) {
+  if (n < 1 || !dt_ok(r_dtype)) return 0;
+  return trinv_x3_ws(n, r_dtype);
+}
+
+int ifk_tri_inverse_x3(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n, float* Z,
+                       int64_t ldz, void* workspace, size_t workspace_bytes) {
+  GUARD(dt_ok(r_dtype), "tri_inverse_x3: bad dtype code");
+  return trinv_x3((hipStream_t)stream, R, r_dtype, ldr, n, Z, ldz, workspace, workspace_bytes);
+}
+
 size_t ifk_cond_estimate_workspace_size(int64_t n) {
   if (n < 1) return 0;
   return cond_est_ws(n);

@@ -109,6 +109,10 @@ int trinv_levels_t(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n
 // Z = R^{-1} in bf16 arithmetic, plus RNE bf16 copies Zb = Z and ZTb = Z^T
 // (row stride ldb, the other triangle zero) for precondition_apply_b.
 size_t trinv_copies_ws(int64_t n);
+// fp32-accurate inverse on bf16 MFMA (split halves for the wide levels)
+size_t trinv_x3_ws(int64_t n, int rdt);
+int trinv_x3(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,
+             void* ws, size_t ws_bytes);
 int trinv_copies(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
                  int64_t ldz, bf16_t* Zb, bf16_t* ZTb, int64_t ldb, void* ws, size_t ws_bytes);
 

@@ -81,7 +81,7 @@ static size_t split_floats(int64_t b, int64_t n) {
 // ----------------------------------------------------------------------------
 static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
                       int64_t ldz, int math, int safe, float* tmp, SplitScratch sp,
-                      bool ut = false);
+                      bool ut = false, int64_t w_stop = INT64_MAX);
 
 struct FoldWs {
   int64_t B;      // outer block width the buffers are sized for (OUTER_B or CQR_B)
@@ -989,7 +989,8 @@ size_t trinv_ws(int64_t n) {
 // off-diagonal blocks are G's).  fp32 levels up to 256 wide run on the
 // 64-tile kernel, the rest on the GEMM engine.
 static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,
-                      int64_t ldz, int math, int safe, float* tmp, SplitScratch sp, bool ut) {
+                      int64_t ldz, int math, int safe, float* tmp, SplitScratch sp, bool ut,
+                      int64_t w_stop) {
   const size_t esz = rdt == DT_F32 ? 4 : 2;
   const char* Rc = (const char*)R;
   if (ut && rdt != DT_F32) {
@@ -999,7 +1000,7 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
   // every block on and above the diagonal is written below
   RC(launch_zero_tri_blocks(s, Z, 4, ldz, n, true));
   RC(launch_trinv_diag128(s, R, rdt, ldr, n, Z, ldz, safe, ut ? 1 : 0));
-  for (int64_t w = 2 * TRINV_NB; w < n; w *= 2) {
+  for (int64_t w = 2 * TRINV_NB; w < n && w < w_stop; w *= 2) {
     const int64_t step = 2 * w;
     const int64_t nfull = n / step;
     const int64_t i0 = nfull * step;
@@ -1145,6 +1146,132 @@ int trinv(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* 
     return trinv_core_t(s, R, rdt, ldr, n, Z, ldz, safe, zt, zt + (size_t)n * n, n, false,
                         (bf16_t*)tmp, sp);
   return trinv_core(s, R, rdt, ldr, n, Z, ldz, math, safe, tmp, sp);
+}
+
+// Z = R^{-1} (R upper triangular, fp32 or bf16) at about fp32 accuracy on
+// bf16 MFMA.  The 128-blocks and the doubling levels up to X3_W0 / 2 wide run
+// in fp32 arithmetic as in trinv_core (in LDS and on the small-product
+// kernels, which are quick at those sizes); the wider levels, where the fp32
+// GEMMs would cost the most, multiply split bf16 halves x = x_hi + x_lo (both
+// RNE bf16) as a_hi b_hi + a_hi b_lo + a_lo b_hi (the lo.lo term dropped,
+// about 2^-17 of |a||b| per product; a bf16 R has no lo half, so its products
+// take two terms).  The halves of Z are kept in both layouts next to it (Zh,
+// Zl row-major; ZTh, ZTl transposed, row stride n) so every product reads
+// K-contiguous operands: per pair (Z11, Z22, R12) of a level
+//   TmpT = ZT22 R12^T,   Z12 = -Z11 TmpT^T,
+// and each new block's halves go into both copies for the wider levels.
+static constexpr int64_t X3_W0 = 512;   // the first level on split bf16
+
+struct TrinvX3Ws {
+  float* tmp;
+  SplitScratch sp;
+  bf16_t *Zh, *Zl, *ZTh, *ZTl;   // n x n each
+  bf16_t *Rh, *Rl;               // fp32 R's halves (n x n), or null
+  float* T;                      // a level's TmpT blocks: n^2 / 2
+  bf16_t *Th, *Tl;
+};
+
+static void plan_trinv_x3(Arena& a, int64_t n, int rdt, TrinvX3Ws& x) {
+  plan_trinv(a, n, &x.tmp, &x.sp);
+  const size_t nn = (size_t)n * n;
+  x.Zh = a.take<bf16_t>(nn);
+  x.Zl = a.take<bf16_t>(nn);
+  x.ZTh = a.take<bf16_t>(nn);
+  x.ZTl = a.take<bf16_t>(nn);
+  x.Rh = rdt == DT_F32 ? a.take<bf16_t>(nn) : nullptr;
+  x.Rl = rdt == DT_F32 ? a.take<bf16_t>(nn) : nullptr;
+  x.T = a.take<float>(nn / 2 + 64);
+  x.Th = a.take<bf16_t>(nn / 2 + 64);
+  x.Tl = a.take<bf16_t>(nn / 2 + 64);
+}
+
+size_t trinv_x3_ws(int64_t n, int rdt) {
+  Arena a(nullptr, 0);
+  TrinvX3Ws x;
+  plan_trinv_x3(a, n, rdt, x);
+  return a.used;
+}
+
+// C (= or +=) alpha A B^T from split operands: the terms (hi, hi), (hi, lo),
+// (lo, hi), each a null operand half skipped
+static int gemm_split(hipStream_t s, int64_t M, int64_t N, int64_t K, float alpha,
+                      const MatRef& Ah, const MatRef* Al, const MatRef& Bh, const MatRef* Bl,
+                      const OutRef& out, int batch, SplitScratch sp) {
+  RC(gemm(s, MATH_BF16, M, N, K, alpha, Ah, Bh, 0.0f, out, batch, sp));
+  if (Bl) RC(gemm(s, MATH_BF16, M, N, K, alpha, Ah, *Bl, 1.0f, out, batch, sp));
+  if (Al) RC(gemm(s, MATH_BF16, M, N, K, alpha, *Al, Bh, 1.0f, out, batch, sp));
+  return IFK_OK;
+}
+
+int trinv_x3(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z, int64_t ldz,
+             void* ws, size_t ws_bytes) {
+  if (n < 1 || ldr < n || ldz < n || !R || !Z || (rdt != DT_F32 && rdt != DT_BF16)) {
+    set_error("tri_inverse_x3: invalid arguments");
+    return IFK_ERR_INVALID;
+  }
+  Arena a(ws, ws_bytes);
+  TrinvX3Ws x;
+  plan_trinv_x3(a, n, rdt, x);
+  RC(check_ws(a, "tri_inverse_x3"));
+  RC(trinv_core(s, R, rdt, ldr, n, Z, ldz, MATH_F32, 0, x.tmp, x.sp, false, X3_W0));
+  if (X3_W0 >= n) return IFK_OK;
+  const int B16 = DT_BF16;
+  // the halves of Z (its diagonal X3_W0-blocks are final; the rest is
+  // written level by level below) and of an fp32 R
+  RC(launch_split_bf16(s, Z, ldz, n, n, x.Zh, x.Zl, n, false));
+  RC(launch_split_transpose(s, Z, ldz, n, n, x.ZTh, x.ZTl, n));
+  if (rdt == DT_F32) RC(launch_split_bf16(s, (const float*)R, ldr, n, n, x.Rh, x.Rl, n, false));
+  const bf16_t* Rb = rdt == DT_F32 ? x.Rh : (const bf16_t*)R;
+  const int64_t ldrb = rdt == DT_F32 ? n : ldr;
+  for (int64_t w = X3_W0; w < n; w *= 2) {
+    const int64_t step = 2 * w;
+    const int64_t nfull = n / step;
+    if (nfull > 0) {
+      const int64_t sa = step * (n + 1), sr = step * (ldrb + 1), sz = step * (ldz + 1);
+      // TmpT = ZT22 R12^T for every full pair, batched
+      const MatRef Rh12 = B_t(Rb + w, B16, ldrb, TRI_NONE, sr);
+      const MatRef Rl12 = B_t(x.Rl ? x.Rl + w : nullptr, B16, ldrb, TRI_NONE, sr);
+      const MatRef ZTh22 = A_n(x.ZTh + w * n + w, B16, n, TRI_LOWER, sa);
+      const MatRef ZTl22 = A_n(x.ZTl + w * n + w, B16, n, TRI_LOWER, sa);
+      RC(gemm_split(s, w, w, w, 1.0f, ZTh22, &ZTl22, Rh12, x.Rl ? &Rl12 : nullptr,
+                    out_f32(x.T, w, w * w), (int)nfull, x.sp));
+      RC(launch_split_bf16(s, x.T, w, nfull * w, w, x.Th, x.Tl, w, false));
+      // Z12 = -Z11 TmpT^T
+      const MatRef Zh11 = A_n(x.Zh, B16, n, TRI_UPPER, sa), Zl11 = A_n(x.Zl, B16, n, TRI_UPPER, sa);
+      const MatRef Th = B_t(x.Th, B16, w, TRI_NONE, w * w), Tl = B_t(x.Tl, B16, w, TRI_NONE, w * w);
+      RC(gemm_split(s, w, w, w, -1.0f, Zh11, &Zl11, Th, &Tl, out_f32(Z + w, ldz, sz), (int)nfull,
+                    x.sp));
+      for (int64_t b = 0; b < nfull; ++b) {
+        const int64_t r0 = b * step;
+        const float* Z12 = Z + r0 * ldz + r0 + w;
+        RC(launch_split_bf16(s, Z12, ldz, w, w, x.Zh + r0 * n + r0 + w, x.Zl + r0 * n + r0 + w, n,
+                             false));
+        RC(launch_split_transpose(s, Z12, ldz, w, w, x.ZTh + (r0 + w) * n + r0,
+                                  x.ZTl + (r0 + w) * n + r0, n));
+      }
+    }
+    const int64_t i0 = nfull * step;
+    if (i0 + w < n) {
+      const int64_t w2 = n - i0 - w;   // ragged pair: Z22 is w2 x w2, R12 w x w2
+      const MatRef Rh12 = B_t(Rb + i0 * ldrb + i0 + w, B16, ldrb);
+      const MatRef Rl12 = B_t(x.Rl ? x.Rl + i0 * ldrb + i0 + w : nullptr, B16, ldrb);
+      const MatRef ZTh22 = A_n(x.ZTh + (i0 + w) * n + i0 + w, B16, n, TRI_LOWER);
+      const MatRef ZTl22 = A_n(x.ZTl + (i0 + w) * n + i0 + w, B16, n, TRI_LOWER);
+      RC(gemm_split(s, w2, w, w2, 1.0f, ZTh22, &ZTl22, Rh12, x.Rl ? &Rl12 : nullptr,
+                    out_f32(x.T, w), 1, x.sp));
+      RC(launch_split_bf16(s, x.T, w, w2, w, x.Th, x.Tl, w, false));
+      const MatRef Zh11 = A_n(x.Zh + i0 * n + i0, B16, n, TRI_UPPER);
+      const MatRef Zl11 = A_n(x.Zl + i0 * n + i0, B16, n, TRI_UPPER);
+      const MatRef Th = B_t(x.Th, B16, w), Tl = B_t(x.Tl, B16, w);
+      float* Z12 = Z + i0 * ldz + i0 + w;
+      RC(gemm_split(s, w, w2, w, -1.0f, Zh11, &Zl11, Th, &Tl, out_f32(Z12, ldz), 1, x.sp));
+      RC(launch_split_bf16(s, Z12, ldz, w, w2, x.Zh + i0 * n + i0 + w, x.Zl + i0 * n + i0 + w, n,
+                           false));
+      RC(launch_split_transpose(s, Z12, ldz, w, w2, x.ZTh + (i0 + w) * n + i0,
+                                x.ZTl + (i0 + w) * n + i0, n));
+    }
+  }
+  return IFK_OK;
 }
 
 int trinv_copies(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_t n, float* Z,

@@ -153,6 +153,7 @@ class IFKFAC(torch.optim.Optimizer):
         be = get_backend()
         copies = hasattr(be, "tri_inverse_bf16")
         split = hasattr(be, "precondition_apply_x3")
+        x3_inverse = hasattr(be, "tri_inverse_x3")
         # bf16 factors in bf16 arithmetic: the Gram route's call forms each
         # side's inverse as well
         fused_inverse = (copies and out_dtype == torch.bfloat16
@@ -248,14 +249,16 @@ class IFKFAC(torch.optim.Optimizer):
                 self._solve_math[module] = MATH_BF16
             else:
                 # fp32 accuracy on the bf16-valued factors (the reference's
-                # regime): fp32 inverses, applied through their split bf16
-                # halves (three MFMA products per solve product) when the
-                # backend has that apply, else by fp32 arithmetic
+                # regime): inverses at fp32 accuracy -- from split bf16
+                # halves on the wide levels when the backend has them, the
+                # same accuracy class as the apply -- applied through their
+                # split bf16 halves (three MFMA products per solve product)
+                # when the backend has that apply, else by fp32 arithmetic
                 logger.debug("IFKFAC: kappa(R_X) %.3g, kappa(R_G) %.3g: fp32 solves for %s",
                              kx, kg, type(module).__name__)
-
-                ZX, ZG = run_pair(R_X.device, lambda R=R_X: be.tri_inverse(R, MATH_F32),
-                                  lambda R=R_G: be.tri_inverse(R, MATH_F32),
+                inv32 = ((lambda R: be.tri_inverse_x3(R)) if split and x3_inverse
+                         else (lambda R: be.tri_inverse(R, MATH_F32)))
+                ZX, ZG = run_pair(R_X.device, lambda R=R_X: inv32(R), lambda R=R_G: inv32(R),
                                   b_first=R_G.shape[0] > R_X.shape[0])
                 self._inverses[module] = (ZX, ZG)
                 self._solve_math[module] = MATH_F32

@@ -288,6 +288,20 @@ int ifk_tri_inverse_bf16(void* stream, const void* R, int r_dtype, int64_t ldr, 
                          size_t workspace_bytes);
 
 /*
+ * ifk_tri_inverse at about fp32 accuracy on bf16 MFMA: the wide doubling
+ * levels multiply split bf16 halves (x = x_hi + x_lo; three products per
+ * product, about 2^-17 of |a||b| each, two when R is bf16-valued), the
+ * 128-blocks and the levels up to 256 wide run in fp32 arithmetic.  The
+ * fp32 solves on bf16-valued factors of triangular.py:607-628 use this
+ * inverse with ifk_precondition_apply_x3 (same accuracy class); about 4x
+ * faster than ifk_tri_inverse in fp32 arithmetic at n = 4096.  Workspace
+ * about 8 n^2 bytes plus 4 n^2 more for an fp32 R.
+ */
+size_t ifk_tri_inverse_x3_workspace_size(int64_t n, int r_dtype);
+int ifk_tri_inverse_x3(void* stream, const void* R, int r_dtype, int64_t ldr, int64_t n, float* Z,
+                       int64_t ldz, void* workspace, size_t workspace_bytes);
+
+/*
  * Condition estimate kappa_2(R) ~ sigma_max(R) sigma_max(Z) of an upper-
  * triangular n x n factor R (dtype r_dtype, ldr) from R and its inverse Z
  * (fp32, ldz, e.g. from ifk_tri_inverse_bf16), each sigma_max by four steps

@@ -968,6 +968,32 @@ def test_full_size_precondition_residual(hip):
         assert ((back - grad.double()).norm() / grad.double().norm()).item() < tol
 
 
+@pytest.mark.parametrize("n", [300, 700, 3000, 4096])
+@pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16])
+def test_tri_inverse_x3(hip, n, rdt):
+    """ifk_tri_inverse_x3 against the fp64 inverse of the same (fp32 or
+    bf16-valued) factor: the split levels (512 wide and up; ragged pairs at
+    700 and 3000, none at 300) keep the error within 8 kappa 2^-17 and within
+    four times the fp32-arithmetic inverse's own error plus 2^-17."""
+    g = torch.Generator(device=DEV).manual_seed(n)
+    X = torch.randn(2 * n, n, device=DEV, generator=g, dtype=torch.float64)
+    X[:, : n // 3] *= 10.0
+    R = torch.linalg.qr(X, mode="r")[1]
+    R = R * torch.sign(torch.diagonal(R)).unsqueeze(1)
+    Rt = R.to(rdt)
+    R64 = Rt.double()
+    Z64 = torch.linalg.inv(R64)
+    kap = float(torch.linalg.cond(R64))
+    Zx = hip.tri_inverse_x3(Rt).double()
+    Zf = hip.tri_inverse(Rt, 0).double()
+    ex = float((Zx - Z64).norm() / Z64.norm())
+    ef = float((Zf - Z64).norm() / Z64.norm())
+    print(f"n {n} {rdt}: kappa {kap:.1f}, x3 {ex:.2e}, fp32 {ef:.2e}")
+    assert ex <= 8 * kap * 2.0 ** -17
+    assert ex <= 4 * ef + 2.0 ** -17
+    assert bool(torch.isfinite(Zx).all()) and float(torch.tril(Zx, -1).abs().max()) == 0.0
+
+
 def test_triangular_mirrors_on_gpu(hip):
     """The function-level mirrors of ifkfac/triangular.py on the GPU against the
     oracle: streaming update (trapezoid, then square), tsqr, the bucket fold,
