@@ -79,11 +79,11 @@ PEAK_HBM_GBS = 8000.0
 # in its survey step; for these workloads that is either of two kernels.)
 TRAFFIC = {
     ("linear_4096x11008_p16384", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"):
-        861.81e6,
-    ("linear_4096x11008_p16384", "gram", "cholb_step_kernel"): 5.12e6,
+        864.75e6,
+    ("linear_4096x11008_p16384", "gram", "cholb_step_kernel"): 5.14e6,
     ("vit_b_block_capture_p4096", "gram", "gemm_bb_kernel<BbCfg<256, 256, 2, 4, 1, true>>"):
-        313.09e6,
-    ("vit_b_block_capture_p4096", "gram", "cholb_step_kernel"): 4.52e6,
+        1221.33e6,
+    ("vit_b_block_capture_p4096", "gram", "cholb_step_kernel"): 15.14e6,
 }
 
 WORKLOADS = {
@@ -204,8 +204,8 @@ def default_queue_child(args) -> dict:
     env = dict(os.environ)
     env.pop("GPU_MAX_HW_QUEUES", None)
     cmd = [sys.executable, os.path.abspath(__file__), "--hw-queues-default", "--no-extras",
-           "--no-cpu-baseline", "--steps", str(max(3, args.steps // 2)), "--warmup", "2",
-           "--factor-path", args.factor_path]
+           "--no-cpu-baseline", "--steps", str(max(5, args.steps)), "--warmup",
+           str(max(3, args.warmup)), "--factor-path", args.factor_path]
     try:
         r = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
         line = [l for l in r.stdout.strip().splitlines() if l.startswith("{")][-1]
