@@ -633,13 +633,15 @@ def extras(be, args, head_kappa):
 
     def finalize_all(_first):
         # as get_factors() in bf16 arithmetic: every side by the Gram route,
-        # one host read of the flags, the panel finalize for a side flagged 2
-        out = [be.fold_finalize(None, 0, R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16,
-                                MATH_BF16, gram=True) for R in cap.Rs]
-        st = torch.cat([f for _, f in out]).cpu()
+        # grouped by width (grouped_gram_finalize), one host read of the
+        # flags, the panel finalize for a side flagged 2
+        from ifkfac_amd.activation_hooks import grouped_gram_finalize
+        got = grouped_gram_finalize([(i, R, rows * 200) for i, R in enumerate(cap.Rs)], 1e-3,
+                                    torch.float32)
+        st = torch.cat([got[i][1] for i in range(len(cap.Rs))]).cpu()
         for i, R in enumerate(cap.Rs):
             if int(st[i]) == 2:
-                be.finalize(R, 1 / math.sqrt(rows * 200), 1e-3, torch.bfloat16, MATH_BF16)
+                be.finalize(R, 1 / math.sqrt(rows * 200), 1e-3, torch.float32, MATH_BF16)
     ms_f = timed(finalize_all, 3, 1)
     res["vit_b_block_capture_p4096"] = {
         "ms_per_batch": round(ms_b, 3), "tflops_per_batch": round(cap.flops / ms_b / 1e9, 1),
@@ -649,7 +651,7 @@ def extras(be, args, head_kappa):
                 "held as the hooks hold them and folded by one batched Gram-route fold per "
                 "shape, the panel fold for a refused fold); 200 batches x 12 "
                 "blocks take 2400 x ms_per_batch; get_factors() of the 8 sides by the Gram "
-                "route"}
+                "route, grouped by width"}
     del cap
     torch.cuda.empty_cache()
     res["kappa_R_damped_headline"] = head_kappa

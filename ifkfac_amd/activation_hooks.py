@@ -349,6 +349,52 @@ class FoldGroups:
                 queue.push(st[e:e + 1], buf, X, math_, owned=True)
 
 
+def grouped_gram_finalize(items, damping: float, out_dtype: torch.dtype,
+                          merge_ratio: float = FoldGroups.MERGE_RATIO) -> dict:
+    """The damped factors of square running factors by the Gram route, one
+    batched call per (width, rows folded, device) group instead of one call
+    each; a narrower group rides a wider one (same rows, width n >=
+    merge_ratio * N) embedded as [[R, 0], [0, I]], whose damped factor has
+    the entry's own in its leading n x n block.  items: (key, R (n x n fp32),
+    rows).  Returns key -> (R_damped, status int32[1], kappa bound float32[1])
+    with the status of ``fold_finalize`` (2: redo by the panel path)."""
+    be = get_backend()
+    groups: Dict[tuple, list] = {}
+    for key, R, rows in items:
+        groups.setdefault((R.shape[1], rows, R.device), []).append((key, R))
+    pads: Dict[tuple, list] = {}
+    for k in sorted(groups, key=lambda k: k[0]):
+        if k in pads:
+            continue
+        n = k[0]
+        wide = [w for w in groups if w[1:] == k[1:] and w[0] > n and n >= merge_ratio * w[0]
+                and w is not k]
+        if wide:
+            w = max(wide, key=lambda w: w[0])
+            pads.setdefault(w, []).extend(groups.pop(k))
+    out: dict = {}
+    for (N, rows, dev), ent in groups.items():
+        ent = ent + pads.get((N, rows, dev), [])
+        Xs = []
+        for _, R in ent:
+            m = R.shape[1]
+            if m == N:
+                Xs.append(R)
+                continue
+            P = torch.zeros((N, N), dtype=torch.float32, device=dev)
+            P[:m, :m].copy_(R)
+            d = torch.arange(m, N, device=dev)
+            P[d, d] = 1.0
+            Xs.append(P)
+        F, st, kb = be.fold_finalize_gram_batched(None, 0, Xs, 1.0 / math.sqrt(rows), damping,
+                                                  out_dtype)
+        for e, (key, R) in enumerate(ent):
+            m = R.shape[1]
+            Fe = F[e] if m == N else F[e][:m, :m].contiguous()
+            out[key] = (Fe, st[e:e + 1], kb[e:e + 1])
+    return out
+
+
 class IFKFACRankError(RuntimeError):
     """Raised when a layer has fewer accumulated rows than columns (p < n)."""
 
@@ -829,6 +875,27 @@ class RawActivationHooks(GramMatrixEstimator):
                 factors[m] = (R_X, R_G)
                 flags[m] = (fX, fG)
                 extras[m] = (eX, eG)
+        if (not consume and then is None and fast and self.math == MATH_BF16 and
+                hasattr(get_backend(), "fold_finalize_gram_batched")):
+            # get_factors of the running factors (no chunk held): every side
+            # of every layer grouped by width (grouped_gram_finalize)
+            items = []
+            for module, rows_X, rows_G, _, _, _ in eligible:
+                if module in batched:
+                    continue
+                for side, rows in (("X", rows_X), ("G", rows_G)):
+                    R, _, chunk, _ = self._side_state(side, module)
+                    if chunk is None and R is not None and R.shape[0] == R.shape[1]:
+                        items.append(((module, side), R, rows))
+            if len(items) > 1:
+                got = grouped_gram_finalize(items, self.damping, out_dtype)
+                for module, _, _, _, _, _ in eligible:
+                    if (module, "X") in got and (module, "G") in got:
+                        (R_X, fX, _), (R_G, fG, _) = got[(module, "X")], got[(module, "G")]
+                        factors[module] = (R_X, R_G)
+                        flags[module] = (fX, fG)
+                        extras[module] = (None, None)
+                        batched.add(module)
         for module, rows_X, rows_G, n_X, n_G, dev in eligible:
             if module in batched:
                 continue

@@ -297,3 +297,55 @@ def test_fold_groups_merge_narrower_square_group(hip):
         e = np.linalg.norm(a - w) / np.linalg.norm(w)
         print(f"entry {i} n={n}: {e:.2e}")
         assert e <= tol, (i, e)
+
+
+def test_get_factors_grouped_by_width(hip):
+    """get_factors() in bf16 arithmetic (the Laplace use, no factor update):
+    the running factors of every layer and side go through one batched
+    Gram-route finalize per width -- widths 384 (five sides), 1536 (two) and
+    1152, which rides the 1536 group embedded as [[R, 0], [0, I]] -- with the
+    factors of the per-side finalizes: bit for bit where the width has its
+    own group, within 1e-5 (relative Gram error of the damped factor) where it
+    rides a wider one."""
+    from ifkfac_amd import RawActivationHooks
+    from ifkfac_amd._backend import MATH_BF16
+    calls = []
+    cls = type(hip)
+    real = cls.fold_finalize_gram_batched
+
+    def wrap(self, Rs, r_in, Xs, *a, **k):
+        calls.append((len(Xs), Xs[0].shape[1]))
+        return real(self, Rs, r_in, Xs, *a, **k)
+
+    def run():
+        torch.manual_seed(8)
+        layers = nn.ModuleList([nn.Linear(384, 1152), nn.Linear(384, 384), nn.Linear(384, 1536),
+                                nn.Linear(1536, 384)]).to(DEV)
+        hooks = RawActivationHooks(layers, damping=1e-3, math=MATH_BF16)
+        hooks.enable()
+        g = torch.Generator(device=DEV).manual_seed(9)
+        for _ in range(2):
+            x = torch.randn(2048, 384, device=DEV, generator=g)
+            h = layers[0](x)[:, :384] + layers[1](x) + layers[3](torch.tanh(layers[2](x)))
+            h.square().mean().backward()
+            layers.zero_grad()
+        f = hooks.get_factors()
+        return [tuple(t.clone() for t in f[m]) for m in layers]
+
+    cls.fold_finalize_gram_batched = wrap
+    try:
+        grouped = run()
+    finally:
+        cls.fold_finalize_gram_batched = real
+    print(f"batched finalize calls {sorted(calls)}")
+    assert sorted(calls) == [(2 + 1, 1536), (5, 384)]
+    with _Hide(hip, ["fold_finalize_gram_batched"]):
+        single = run()
+    for li, (a, b) in enumerate(zip(grouped, single)):
+        for side, (x, y) in enumerate(zip(a, b)):
+            if x.shape[0] == 1152:
+                xd, yd = x.double(), y.double()
+                e = float((xd.t() @ xd - yd.t() @ yd).norm() / (yd.t() @ yd).norm())
+                assert e <= 1e-5, (li, side, e)
+            else:
+                assert torch.equal(x, y), (li, side)
