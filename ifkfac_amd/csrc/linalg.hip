@@ -1053,14 +1053,16 @@ static int trinv_core(hipStream_t s, const void* R, int rdt, int64_t ldr, int64_
       }
     }
     if (w2 > 0) {
+      // ragged pair: R12 is w x w2 and Z22 w2 x w2, so T = R12 Z22 sums over
+      // w2 terms (Z22's rows end at row n - 1; a longer K would read past it)
       const void* R12 = Rc + ((size_t)i0 * ldr + i0 + w) * esz;
       if (small) {
-        RC(launch_gemm64(s, w, w2, w, 1.0f, (const float*)R12, ldr, 0, TRI_NONE,
+        RC(launch_gemm64(s, w, w2, w2, 1.0f, (const float*)R12, ldr, 0, TRI_NONE,
                          Z + (i0 + w) * ldz + i0 + w, ldz, 0, TRI_UPPER, tmp, w2, 0, 1));
         RC(launch_gemm64(s, w, w2, w, -1.0f, Z + i0 * ldz + i0, ldz, 0, TRI_UPPER, tmp, w2, 0,
                          TRI_NONE, Z + i0 * ldz + i0 + w, ldz, 0, 1));
       } else {
-        RC(gemm(s, math, w, w2, w, 1.0f, A_n(R12, rdt, ldr),
+        RC(gemm(s, math, w, w2, w2, 1.0f, A_n(R12, rdt, ldr),
                 B_n(Z + (i0 + w) * ldz + i0 + w, DT_F32, ldz, TRI_UPPER), 0.0f, out_f32(tmp, w2),
                 1, sp));
         RC(gemm(s, math, w, w2, w, -1.0f, A_n(Z + i0 * ldz + i0, DT_F32, ldz, TRI_UPPER),
