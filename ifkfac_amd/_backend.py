@@ -886,7 +886,13 @@ def run_pair(device: torch.device, fa, fb, b_first: bool = False):
     Used for the independent input-side and output-side factor work (fold +
     finalize, triangular inverse).  b_first enqueues fb() before fa() (the
     longer call first, so its GPU work starts while the host enqueues the
-    other).  On a CPU device the two calls simply run in order."""
+    other).  The call enqueued first always runs on the same side stream,
+    whichever of fa and fb it is: the library keeps its helper streams per
+    calling stream, and a layer's longer factorisation ran about 3 ms slower
+    per step (Linear 11008 -> 4096, p = 16384: 15.4 against 12.5 ms) on the
+    side stream whose helpers had carried the shorter side of another layer
+    (4096 -> 11008) than on the one whose helpers had carried the longer.
+    On a CPU device the two calls simply run in order."""
     if device.type != "cuda":
         return fa(), fb()
     main = torch.cuda.current_stream(device)
@@ -899,9 +905,9 @@ def run_pair(device: torch.device, fa, fb, b_first: bool = False):
         with torch.cuda.stream(s1):
             ra = fa()
     else:
-        with torch.cuda.stream(s1):
-            ra = fa()
         with torch.cuda.stream(s2):
+            ra = fa()
+        with torch.cuda.stream(s1):
             rb = fb()
     main.wait_stream(s1)
     main.wait_stream(s2)
