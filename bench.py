@@ -30,7 +30,9 @@ layers (Linear 1024 -> 1024 streamed over 8 chunks, 4096 -> 4096 at p = 8192,
 11008 -> 4096 at p = 16384, one ViT-B block's capture folds), each with the
 roofline of its own dominant kernel, IFKFAC.step() itself on a
 Linear(4096, 11008) model and on the 4 x (Linear(4096, 4096) + GELU) stack,
-the same step in fp32 arithmetic (the reference's regime), the step under the
+the same step in fp32 arithmetic (the reference's regime), the same step with
+its factors by the other two factor paths (CholeskyQR2 blocks, the panel
+TPQRT fold), the step under the
 default hardware-queue count (child process), kappa of the damped factors,
 and a roofline per phase.  --workload measures one of the other layers as the
 line's own workload (for its kernel-trace and counter runs).
@@ -558,9 +560,10 @@ def extras(be, args, head_kappa):
     res = {}
     steps, warm = max(3, args.steps // 2), 2
 
-    def layer(name, n_in, n_out, p, chunks=1, math_=1):
-        c = LayerChain(be, n_in, n_out, p, args.factor_path, math_=math_, chunks=chunks)
-        ms, roof, table, _ = measure(lib, c.step, steps, warm, (name, args.factor_path))
+    def layer(name, n_in, n_out, p, chunks=1, math_=1, path=None):
+        path = path or args.factor_path
+        c = LayerChain(be, n_in, n_out, p, path, math_=math_, chunks=chunks)
+        ms, roof, table, _ = measure(lib, c.step, steps, warm, (name, path))
         del c
         torch.cuda.empty_cache()
         return {"ms_per_step": round(ms, 3),
@@ -577,6 +580,18 @@ def extras(be, args, head_kappa):
     res["fp32_arithmetic"] = dict(layer("fp32", h_in, h_out, h_p, math_=0), **{
         "note": "the headline step in fp32 arithmetic (CholeskyQR2 fp32 factor update, fp32 "
                 "inverses and solves): the reference's regime"})
+
+    # the headline step on the other factor paths: the north star's streaming
+    # TSQR and Householder pieces, which the Gram route runs only as its
+    # fallback
+    res["other_factor_paths"] = {
+        path: dict(layer(f"path_{path}", h_in, h_out, h_p, path=path), **{"note": note})
+        for path, note in (
+            ("cqr", "the headline step with each side factored by 1024-column CholeskyQR2 "
+                    "blocks (bf16 arithmetic)"),
+            ("panel", "the headline step with each side factored by the panel TPQRT fold "
+                      "(blocked Householder, bf16 arithmetic)"))
+        if path != args.factor_path}
 
     quiet = contextlib.redirect_stdout(io.StringIO())
 
