@@ -526,6 +526,7 @@ class VitCapture:
         self.be = be
         self.queue = FoldStatusQueue()
         self.Rs, self.chunks = [], []
+        self.accs = None
         for (a, b) in self.shapes:
             for nn_ in (a, b):
                 R = torch.zeros(nn_, nn_, device="cuda")
@@ -537,14 +538,20 @@ class VitCapture:
 
     def step(self, first, mark=lambda: None):
         from ifkfac_amd._backend import MATH_BF16
-        from ifkfac_amd.activation_hooks import FoldGroups
+        from ifkfac_amd.activation_hooks import FoldGroups, RowAccumulator
         mark()
         self.queue.poll()
-        # as the hooks: each fold held (a copy of its chunk), then one batched
-        # Gram-route fold per shape
+        # as the hooks: each factor's chunk offered to its row accumulator
+        # (a square factor folds two widths' worth of rows at a time, so the
+        # 2304- and 3072-wide factors fold every other batch), each fold that
+        # pays held, then one batched Gram-route fold per shape
+        if self.accs is None:
+            self.accs = [RowAccumulator() for _ in self.Rs]
         groups = FoldGroups()
         for i, (R, T) in enumerate(zip(self.Rs, self.chunks)):
-            groups.hold(i, R, R.shape[0], T)
+            rows, private = self.accs[i].offer(R.shape[0], R.shape[1], T)
+            if rows is not None:
+                groups.hold(i, R, R.shape[0], rows, private)
         groups.flush(MATH_BF16, self.queue)
         mark()
 
@@ -642,7 +649,9 @@ def extras(be, args, head_kappa):
 
     # one ViT-B block's factor capture per batch, then get_factors() once
     cap = VitCapture(be)
-    ms_b, roof_b, table_b, _ = measure(lib, cap.step, steps, warm,
+    # an even number of batches: the 2304- and 3072-wide factors fold every
+    # other batch
+    ms_b, roof_b, table_b, _ = measure(lib, cap.step, 2 * ((steps + 1) // 2), warm,
                                        ("vit_b_block_capture_p4096", args.factor_path))
     rows = cap.rows
 
@@ -662,9 +671,11 @@ def extras(be, args, head_kappa):
         "ms_per_batch": round(ms_b, 3), "tflops_per_batch": round(cap.flops / ms_b / 1e9, 1),
         "roofline": roof_b, "kernels": table_b,
         "ms_get_factors": round(ms_f, 3),
-        "note": "8 folds of 4096 rows per batch into running factors (bf16 arithmetic, "
-                "held as the hooks hold them and folded by one batched Gram-route fold per "
-                "shape, the panel fold for a refused fold); 200 batches x 12 "
+        "note": "one 4096-row batch per step into the 8 running factors (bf16 arithmetic, "
+                "held as the hooks hold them -- a square factor folds two widths' worth of "
+                "rows, so the 2304- and 3072-wide ones every other batch -- and folded by "
+                "one batched Gram-route fold per shape, the panel fold for a refused fold), "
+                "averaged over an even number of batches; 200 batches x 12 "
                 "blocks take 2400 x ms_per_batch; get_factors() of the 8 sides by the Gram "
                 "route, grouped by width"}
     del cap

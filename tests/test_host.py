@@ -779,22 +779,22 @@ def test_triangular_mirrors_match_oracle(be):
 
 def test_bf16_fold_takes_gram_route_when_square(be):
     """bf16 arithmetic: chunks too small for a fold that pays (fewer than 2n
-    rows into a partial factor) are held and folded together once they
-    reach it -- by the Gram route, whose refusal (status 2, injected) sends
-    the rows to the panel fold -- and a chunk of n rows into the square
-    factor goes to the Gram route at once; fp32 arithmetic folds every chunk
-    by the panel fold as it comes.  Whatever the grouping, the running
-    factor is the oracle's of the rows folded; ``_running_factor`` folds the
-    rows still held."""
+    rows into a partial factor, or into the square factor) are held and
+    folded together once they reach it -- by the Gram route, whose refusal
+    (status 2, injected) sends the rows to the panel fold -- so a chunk of n
+    rows into the square factor waits for the next one; fp32 arithmetic
+    folds every chunk by the panel fold as it comes.  Whatever the grouping,
+    the running factor is the oracle's of the rows folded;
+    ``_running_factor`` folds the rows still held."""
     from ifkfac_amd._backend import MATH_BF16, MATH_F32
     from ifkfac_amd.activation_hooks import GRAM_FOLD_TOL, RawActivationHooks
     model = nn.Sequential(nn.Linear(8, 4))
     lin = model[0]
     rng = np.random.default_rng(3)
-    chunks = [rng.standard_normal((p, 8)) for p in (5, 6, 8, 8)]
+    chunks = [rng.standard_normal((p, 8)) for p in (5, 6, 8, 8, 8)]
     chunks[3][:, 7] = chunks[3][:, 0]            # a column repeated within the chunk
-    for math_, calls, folded in ((MATH_BF16, (0, 0, 1, 1), (0, 0, 3, 4)),
-                                 (MATH_F32, (0, 0, 0, 0), (1, 2, 3, 4))):
+    for math_, calls, folded in ((MATH_BF16, (0, 0, 1, 0, 1), (0, 0, 3, 3, 5)),
+                                 (MATH_F32, (0, 0, 0, 0, 0), (1, 2, 3, 4, 5))):
         be.calls.clear()
         hooks = RawActivationHooks(model, math=math_)
         for i, c in enumerate(chunks):
