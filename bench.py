@@ -306,7 +306,7 @@ class LayerChain:
 
     def factor_update(self):
         import torch
-        from ifkfac_amd._backend import run_pair
+        from ifkfac_amd._backend import MATH_BF16, run_pair
         from ifkfac_amd.activation_hooks import FoldStatusQueue
         RX = getattr(self, "RX", None)
         RG = getattr(self, "RG", None)
@@ -320,10 +320,18 @@ class LayerChain:
             fq.drain()
         lx = self._last_rows(self.X, accs.get("X"))
         lg = self._last_rows(self.D, accs.get("G"))
-        out = list(run_pair(self.dev,
-                            lambda: self._side(lx, RX, self.path, r=r["X"]),
-                            lambda: self._side(lg, RG, self.path, r=r["G"]),
-                            b_first=self.n_out > self.n_in))
+        if (self.path == "gram" and self.math == MATH_BF16 and r["X"] == r["G"] and
+                lx.shape == lg.shape and lx.dtype == lg.dtype and lx.stride() == lg.stride()):
+            # as the hooks: a square layer's two sides in one batched call
+            F, st, _, (Z, Zb, ZT) = self.be.fold_finalize_gram_batched(
+                [RX, RG] if r["X"] > 0 else None, r["X"], [lx, lg], 1 / math.sqrt(self.p),
+                self.lam, torch.bfloat16, with_inverse=True)
+            out = [(F[i], st[i:i + 1], (Z[i], Zb[i], ZT[i])) for i in range(2)]
+        else:
+            out = list(run_pair(self.dev,
+                                lambda: self._side(lx, RX, self.path, r=r["X"]),
+                                lambda: self._side(lg, RG, self.path, r=r["G"]),
+                                b_first=self.n_out > self.n_in))
         st = torch.cat([out[0][1], out[1][1]]).cpu()
         self.flagged = False
         for i, (last, R, side) in enumerate(((lx, RX, "X"), (lg, RG, "G"))):

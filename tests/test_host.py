@@ -543,10 +543,12 @@ def test_chunks_fold_eagerly_between_updates(be):
 
 def test_bf16_update_batches_same_shape_layers(be):
     """A consuming bf16 factor update sends the layers whose X sides and G sides
-    share a shape through one batched Gram call per side (three 12 -> 12 layers
-    here; the 12 -> 5 head's sides go alone, as batches of one), every layer's
-    factors are its own closed form, as the per-layer path gives them, and each
-    side's inverse comes from the factor call (no separate triangular inverse)."""
+    share a shape through one batched Gram call -- one for all six sides of the
+    three 12 -> 12 layers here, whose X and G sides share one signature (one
+    call per side otherwise); the 12 -> 5 head's sides go alone, as batches of
+    one -- every layer's factors are its own closed form, as the per-layer path
+    gives them, and each side's inverse comes from the factor call (no
+    separate triangular inverse)."""
     from ifkfac_amd import IFKFAC
     torch.manual_seed(0)
     model = nn.Sequential(nn.Linear(12, 12), nn.Tanh(), nn.Linear(12, 12), nn.Tanh(),
@@ -563,9 +565,9 @@ def test_bf16_update_batches_same_shape_layers(be):
     import io
     with contextlib.redirect_stdout(io.StringIO()):
         opt.step()
-    # the X group, the G group and the head's two sides
-    assert be.calls["fold_finalize_gram_batched"] == be.calls["fold_finalize_gram_inverse"] == 4
-    assert be.calls["fold_finalize_gram"] == 2 * 3 + 2      # three batched entries per side + the head
+    # the square layers' six sides in one call, and the head's two sides
+    assert be.calls["fold_finalize_gram_batched"] == be.calls["fold_finalize_gram_inverse"] == 3
+    assert be.calls["fold_finalize_gram"] == 2 * 3 + 2      # six batched entries + the head
     assert be.calls["tri_inverse_bf16"] == 0
     for m in opt._factors:
         R_X, R_G = opt._factors[m]
