@@ -797,16 +797,31 @@ class RawActivationHooks(GramMatrixEstimator):
             bufs if r > 0 else None, r, chunks, 1.0 / math.sqrt(rows), self.damping, out_dtype,
             with_inverse=with_inverse)
         out, st, kb = got[:3]
-        res = []
-        for e, (side, m) in enumerate(entries):
-            R, f, k = out[e], st[e:e + 1], kb[e:e + 1]
-            if then is None:
-                res.append((R, f, None))
-            elif with_inverse:
-                Z, Zb, ZT = got[3]
-                res.append((R, f, then(side, m, R, k, inv=(Z[e], Zb[e], ZT[e]))))
-            else:
-                res.append((R, f, then(side, m, R, k)))
+
+        def follow(idx):
+            res = []
+            for e in idx:
+                side, m = entries[e]
+                R, f, k = out[e], st[e:e + 1], kb[e:e + 1]
+                if then is None:
+                    res.append((R, f, None))
+                elif with_inverse:
+                    Z, Zb, ZT = got[3]
+                    res.append((R, f, then(side, m, R, k, inv=(Z[e], Zb[e], ZT[e]))))
+                else:
+                    res.append((R, f, then(side, m, R, k)))
+            return res
+
+        ix = [e for e, (side, _) in enumerate(entries) if side == "X"]
+        ig = [e for e, (side, _) in enumerate(entries) if side == "G"]
+        if then is None or not ix or not ig:
+            return follow(range(len(entries)))
+        # both sides in the call: each side's follow-up work (its inverse in
+        # fp32 accuracy where kappa asks for it) on its own side stream
+        rx, rg = run_pair(out.device, lambda: follow(ix), lambda: follow(ig))
+        res = [None] * len(entries)
+        for e, r_ in zip(ix + ig, rx + rg):
+            res[e] = r_
         return res
 
     # ------------------------------------------------------------------ factors
